@@ -1,0 +1,363 @@
+/*
+ * yuuka_hip.h — C ABI of the MI355X (gfx950) speculative-verify library.
+ *
+ * This is a drop-in replacement for the reference bridge header
+ * backend/hip/bridge/yuuka_hip.h (ABI version 10). Every v10 type, enum value
+ * and entry point keeps its exact name, signature and numeric value so the
+ * unchanged Go binding (backend/hip/hip.go, RequiredABI = 10 at hip.go:49)
+ * links and runs against libyuuka_hip.so. Citations name the reference
+ * declaration each entry replaces (paths relative to the reference tree).
+ *
+ * Entry points outside the verify hot path (decode GEMVs, rocBLAS/WMMA
+ * prefill GEMMs, MoE plan ops, ...) are exported and fail with
+ * YUUKA_ERR_UNSUPPORTED and a message, which the Go side maps to
+ * hip.ErrUnsupported (hip.go:26,348-363) and already falls back from.
+ *
+ * The extension block at the end (YUUKA_EXT_*) is additive: new symbols, new
+ * op codes >= 64, and no change to any v10 layout.
+ *
+ * Conventions kept from the reference:
+ *  - every call returns yuuka_status; the message of the last failure on the
+ *    calling thread is yuuka_last_error() (reference :51-52);
+ *  - no C++ exception crosses the ABI;
+ *  - the caller owns every handle and frees it exactly once (reference :54-63);
+ *  - a rejected plan op is not appended (reference :330-334).
+ */
+#ifndef YUUKA_HIP_H
+#define YUUKA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* reference yuuka_hip.h:11 */
+#define YUUKA_HIP_ABI_VERSION 10
+
+#if defined(__GNUC__)
+#define YUUKA_API __attribute__((visibility("default")))
+#else
+#define YUUKA_API
+#endif
+
+/* Opaque handles (reference :22-25). */
+typedef struct yuuka_device yuuka_device;
+typedef struct yuuka_buffer yuuka_buffer;
+typedef struct yuuka_stream yuuka_stream;
+typedef struct yuuka_event yuuka_event;
+
+/* reference :27-34 */
+typedef enum yuuka_status {
+    YUUKA_OK = 0,
+    YUUKA_ERR_INVALID_ARGUMENT = 1,
+    YUUKA_ERR_UNSUPPORTED = 2,
+    YUUKA_ERR_DEVICE = 3,
+    YUUKA_ERR_ALLOCATION = 4,
+    YUUKA_ERR_INTERNAL = 5
+} yuuka_status;
+
+/* reference :36-46 */
+typedef struct yuuka_device_info {
+    char name[256];
+    char gcn_arch[64];
+    char hip_version[64];
+    uint64_t total_memory;
+    uint32_t compute_units;
+    uint32_t clock_mhz;
+    int32_t pci_domain;
+    int32_t pci_bus;
+    int32_t pci_device;
+} yuuka_device_info;
+
+/* reference :48-49. Returns 10: the v10 contract is honoured in full. */
+YUUKA_API uint32_t yuuka_abi_version(void);
+/* reference :51-52. Thread-local; valid until the next failing call. */
+YUUKA_API const char * yuuka_last_error(void);
+
+/* reference :54-57 */
+YUUKA_API yuuka_status yuuka_device_open(int32_t index, yuuka_device ** out);
+YUUKA_API void yuuka_device_close(yuuka_device * dev);
+YUUKA_API yuuka_status yuuka_device_info_get(const yuuka_device * dev, yuuka_device_info * info);
+
+/* reference :59-63 */
+YUUKA_API yuuka_status yuuka_buffer_alloc(yuuka_device * dev, uint64_t bytes, yuuka_buffer ** out);
+YUUKA_API void yuuka_buffer_free(yuuka_buffer * buf);
+YUUKA_API uint64_t yuuka_buffer_size(const yuuka_buffer * buf);
+YUUKA_API void * yuuka_buffer_ptr(const yuuka_buffer * buf);
+
+/* reference :65-71 */
+YUUKA_API yuuka_status yuuka_stream_create(yuuka_device * dev, yuuka_stream ** out);
+YUUKA_API void yuuka_stream_destroy(yuuka_stream * stream);
+YUUKA_API yuuka_status yuuka_stream_synchronize(yuuka_stream * stream);
+YUUKA_API yuuka_status yuuka_event_create(yuuka_device * dev, yuuka_event ** out);
+YUUKA_API void yuuka_event_destroy(yuuka_event * event);
+YUUKA_API yuuka_status yuuka_event_wait(yuuka_event * event);
+
+/* reference :73-85 */
+YUUKA_API yuuka_status yuuka_memcpy_h2d(yuuka_buffer * dst, const void * src, uint64_t bytes);
+YUUKA_API yuuka_status yuuka_memcpy_d2h(void * dst, const yuuka_buffer * src, uint64_t bytes);
+YUUKA_API yuuka_status yuuka_memcpy_d2h_at(void * dst, const yuuka_buffer * src,
+                                           uint64_t offset, uint64_t bytes);
+YUUKA_API yuuka_status yuuka_memset(yuuka_stream * stream, yuuka_buffer * dst, int value, uint64_t bytes);
+
+/* reference :87-90 */
+YUUKA_API yuuka_status yuuka_buffer_copy(yuuka_stream * stream,
+                                yuuka_buffer * dst, uint64_t dst_offset,
+                                const yuuka_buffer * src, uint64_t src_offset,
+                                uint64_t bytes, yuuka_event * completion);
+
+/* reference :92-95 */
+YUUKA_API yuuka_status yuuka_dynamic_set(yuuka_stream * stream, yuuka_buffer * dynamic,
+                                int32_t token, uint32_t position);
+
+/* reference :97-100 */
+YUUKA_API yuuka_status yuuka_add_f32(yuuka_stream * stream, yuuka_buffer * dst,
+                           const yuuka_buffer * a, const yuuka_buffer * b,
+                           uint64_t n, yuuka_event * completion);
+
+/* Operation codes of the plan API (reference :104-149). */
+typedef enum yuuka_op_code {
+    YUUKA_OP_GEMV = 1,
+    YUUKA_OP_RMSNORM = 2,
+    YUUKA_OP_L2NORM = 3,
+    YUUKA_OP_GATED_RMSNORM = 4,
+    YUUKA_OP_ROPE = 5,
+    YUUKA_OP_ATTENTION = 6,
+    YUUKA_OP_CONV1D = 7,
+    YUUKA_OP_GDN = 8,
+    YUUKA_OP_SILU_MUL = 9,
+    YUUKA_OP_ADD = 10,
+    YUUKA_OP_COPY = 11,
+    YUUKA_OP_SCALE = 12,
+    YUUKA_OP_EMBEDDING = 13,
+    YUUKA_OP_KV_WRITE = 14,
+    YUUKA_OP_RMSNORM_HEADS = 15,
+    YUUKA_OP_GEMM = 16,
+    YUUKA_OP_GEMV_BATCH = 17,
+    YUUKA_OP_RMSNORM_BATCH = 18,
+    YUUKA_OP_RMSNORM_HEADS_BATCH = 19,
+    YUUKA_OP_ROPE_BATCH = 20,
+    YUUKA_OP_KV_WRITE_BATCH = 21,
+    YUUKA_OP_ATTENTION_PREFILL = 22,
+    YUUKA_OP_RECURRENT_CHUNK = 23,
+    YUUKA_OP_EMBEDDING_BATCH = 24,
+    YUUKA_OP_CAST_F16 = 25,
+    YUUKA_OP_KV_WRITE_PAGED = 26,
+    YUUKA_OP_ATTENTION_PAGED = 27,
+    YUUKA_OP_KV_WRITE_BATCH_PAGED = 28,
+    YUUKA_OP_ATTENTION_PREFILL_PAGED = 29,
+    YUUKA_OP_MOE_ROUTE = 30,
+    YUUKA_OP_MOE_GATE_UP = 31,
+    YUUKA_OP_MOE_DOWN = 32,
+    YUUKA_OP_MOE_REDUCE_ADD = 33,
+    YUUKA_OP_GEMM_SWIGLU = 34,
+    YUUKA_OP_DEQUANT_F16 = 35,
+    YUUKA_OP_QUANT_Q8_1 = 36,
+    YUUKA_OP_LM_HEAD = 37,
+    YUUKA_OP_GEMV_Q8_1 = 38,
+    YUUKA_OP_RECURRENT_TOKEN = 39,
+    YUUKA_OP_CONV_L2NORM = 40,
+    YUUKA_OP_GEMV_RESIDUAL = 41,
+    YUUKA_OP_GEMV_PAIR = 42,
+    YUUKA_OP_SILU_MUL_QUANT_Q8_1 = 43,
+    YUUKA_OP_PREFILL_Q8_0_PAIR = 44
+} yuuka_op_code;
+
+/* reference :151-161 */
+#define YUUKA_OP_FLAG_TAIL 0x1u
+#define YUUKA_OP_FLAG_PREFILL_BLAS 0x2u
+#define YUUKA_OP_FLAG_PREFILL_ATTENTION_TILED 0x4u
+#define YUUKA_OP_FLAG_PREFILL_SPLIT_MASK 0x18u
+#define YUUKA_OP_FLAG_PREFILL_SPLIT_1 0x08u
+#define YUUKA_OP_FLAG_PREFILL_SPLIT_2 0x10u
+#define YUUKA_OP_FLAG_PREFILL_SPLIT_4 0x18u
+
+/* reference :171-174 */
+#define YUUKA_GEMM_PATH_AUTO 0u
+#define YUUKA_GEMM_PATH_BLAS 1u
+#define YUUKA_GEMM_PATH_WMMA 2u
+#define YUUKA_GEMM_PATH_MMQ 3u
+
+/* Plan operation descriptor (reference :185-193). yuuka_plan_add copies it. */
+typedef struct yuuka_op {
+    uint32_t code;
+    uint32_t flags;
+    yuuka_buffer * buf[16];
+    uint64_t off[16];
+    uint64_t n[6];
+    uint32_t u[4];
+    float f[4];
+} yuuka_op;
+
+typedef struct yuuka_plan yuuka_plan;
+typedef struct yuuka_graph yuuka_graph;
+
+/* GGUF dtype codes (reference :198-207). */
+typedef enum yuuka_dtype {
+    YUUKA_DTYPE_F32 = 0,
+    YUUKA_DTYPE_F16 = 1,
+    YUUKA_DTYPE_Q4_0 = 2,
+    YUUKA_DTYPE_Q5_0 = 6,
+    YUUKA_DTYPE_Q8_0 = 8,
+    YUUKA_DTYPE_Q4_K = 12,
+    YUUKA_DTYPE_Q5_K = 13,
+    YUUKA_DTYPE_Q6_K = 14
+} yuuka_dtype;
+
+/* reference :209-212. Single-row decode GEMV: served by the verify GEMM with
+ * one row (Q4_K / Q6_K), else UNSUPPORTED. */
+YUUKA_API yuuka_status yuuka_gemv(yuuka_stream * stream, yuuka_buffer * out,
+                        const yuuka_buffer * x, const yuuka_buffer * w,
+                        uint64_t n_in, uint64_t n_out, uint32_t dtype,
+                        yuuka_event * completion);
+
+/* reference :221-224, :235-238, :250-256, :266-270: prefill GEMM routes of
+ * the reference (rocBLAS/rocWMMA/MMQ). Out of scope: UNSUPPORTED. */
+YUUKA_API yuuka_status yuuka_gemm(yuuka_stream * stream, yuuka_buffer * out,
+                        const yuuka_buffer * x, const yuuka_buffer * w,
+                        uint64_t n_in, uint64_t n_out, uint64_t batch,
+                        uint32_t dtype, yuuka_event * completion);
+YUUKA_API yuuka_status yuuka_gemm_wmma(yuuka_stream * stream, yuuka_buffer * out,
+                        const yuuka_buffer * x, const yuuka_buffer * w,
+                        uint64_t n_in, uint64_t n_out, uint64_t batch,
+                        uint32_t dtype, yuuka_event * completion);
+YUUKA_API yuuka_status yuuka_quantize_q8_1(yuuka_stream * stream, yuuka_buffer * qs,
+                        yuuka_buffer * ds, const yuuka_buffer * x,
+                        uint64_t n, uint64_t batch, yuuka_event * completion);
+YUUKA_API yuuka_status yuuka_gemm_mmq(yuuka_stream * stream, yuuka_buffer * out,
+                        const yuuka_buffer * qs, const yuuka_buffer * ds,
+                        const yuuka_buffer * w, uint64_t n_in, uint64_t n_out,
+                        uint64_t batch, uint32_t dtype, yuuka_event * completion);
+YUUKA_API yuuka_status yuuka_gemm_blas(yuuka_stream * stream, yuuka_buffer * out,
+                        yuuka_buffer * out16, const yuuka_buffer * x16,
+                        const yuuka_buffer * w, uint64_t n_in, uint64_t n_out,
+                        uint64_t batch, yuuka_event * completion);
+
+/* The verify GEMM (reference :286-289, kernels/hip/gemm/lm_head.hip:61-173):
+ *
+ *   out[rows, n_out] = W[n_out, n_in] * x[rows, n_in]
+ *
+ * x and out are FP32 row-major; W is packed GGUF Q4_K or Q6_K (n_in a
+ * multiple of 256). rows is 1..16 as in the reference. Submitted on stream,
+ * completion recorded after the last kernel, no host synchronization.
+ * Implementation: x is quantized to a 16-bit fixed-point split into two int8
+ * planes, and the weights are decoded to int8 in registers and contracted on
+ * the gfx950 int8 MFMA units with exact int32 sums per quant sub-block;
+ * the K-quant scales are applied in FP32. */
+YUUKA_API yuuka_status yuuka_lm_head(yuuka_stream * stream, yuuka_buffer * out,
+                        const yuuka_buffer * x, const yuuka_buffer * w,
+                        uint64_t n_in, uint64_t n_out, uint64_t rows,
+                        uint32_t dtype, yuuka_event * completion);
+
+/* reference :301-304, :308-309: FP16 staging helpers of the rocBLAS route.
+ * yuuka_dequant_f16 is served for Q4_K/Q6_K (values rounded to FP16 from the
+ * exact FP32 dequantization); the cast is served. */
+YUUKA_API yuuka_status yuuka_dequant_f16(yuuka_stream * stream, yuuka_buffer * dst,
+                        const yuuka_buffer * src, uint64_t n_in, uint64_t n_out,
+                        uint32_t dtype, yuuka_event * completion);
+YUUKA_API yuuka_status yuuka_cast_f32_to_f16(yuuka_stream * stream, yuuka_buffer * dst,
+                        const yuuka_buffer * src, uint64_t n, yuuka_event * completion);
+
+/* reference :318-321: batched GEMV (batch <= 16). Served by the verify GEMM
+ * for Q4_K/Q6_K. */
+YUUKA_API yuuka_status yuuka_gemv_batch(yuuka_stream * stream, yuuka_buffer * out,
+                        const yuuka_buffer * x, const yuuka_buffer * w,
+                        uint64_t n_in, uint64_t n_out, uint64_t batch,
+                        uint32_t dtype, yuuka_event * completion);
+
+/* Plan and graph API (reference :477-496). Supported op codes: LM_HEAD,
+ * GEMV_BATCH (Q4_K/Q6_K), RMSNORM_BATCH, RMSNORM_HEADS_BATCH, ROPE_BATCH,
+ * EMBEDDING_BATCH, KV_WRITE_BATCH_PAGED, ATTENTION_PREFILL_PAGED,
+ * RECURRENT_CHUNK, ADD, SILU_MUL, COPY, plus the YUUKA_EXT_OP_* codes. The
+ * v10 buffer layouts of the reference header (:336-476) are honoured.
+ * Other codes are rejected with YUUKA_ERR_UNSUPPORTED and not appended. */
+YUUKA_API yuuka_status yuuka_graph_create(yuuka_plan * plan, yuuka_stream * stream,
+                                          yuuka_buffer * dynamic, int run_tail,
+                                          yuuka_graph ** out);
+YUUKA_API yuuka_status yuuka_graph_replay(yuuka_graph * graph, yuuka_stream * stream,
+                                          yuuka_event * completion);
+YUUKA_API void yuuka_graph_destroy(yuuka_graph * graph);
+YUUKA_API yuuka_status yuuka_plan_create(yuuka_device * dev, yuuka_plan ** out);
+YUUKA_API void yuuka_plan_destroy(yuuka_plan * plan);
+YUUKA_API yuuka_status yuuka_plan_add(yuuka_plan * plan, const yuuka_op * op);
+YUUKA_API yuuka_status yuuka_plan_execute(yuuka_plan * plan, yuuka_stream * stream,
+                                          int32_t token, uint32_t position,
+                                          int run_tail, yuuka_event * completion);
+/* reference :493-496 */
+YUUKA_API yuuka_status yuuka_plan_execute_profiled(
+    yuuka_plan * plan, yuuka_stream * stream, int32_t token, uint32_t position,
+    int run_tail, uint32_t * op_codes, uint64_t * op_times_ns,
+    uint64_t capacity, uint64_t * op_count, yuuka_event * completion);
+
+/* ======================================================================
+ * Extension block. No counterpart in the reference v10 header unless a
+ * citation says otherwise; additive only.
+ * ====================================================================== */
+
+#define YUUKA_EXT_VERSION 1
+
+/* Version of the extension block compiled into the library. */
+YUUKA_API uint32_t yuuka_ext_version(void);
+
+/* Bit-exact FP32 dequantization of a packed matrix:
+ *   dst[n_out, n_in] = dequant(W[n_out, n_in])
+ * Same values as the reference CPU decoder tensor/quant.go:15-62
+ * (DequantizeRow): every multiply and subtract separately rounded. Used to
+ * prove the device decoder bit-exact. Q4_K, Q5_K, Q6_K, Q8_0, F16, F32. */
+YUUKA_API yuuka_status yuuka_dequant_f32(yuuka_stream * stream, yuuka_buffer * dst,
+                        const yuuka_buffer * src, uint64_t n_in, uint64_t n_out,
+                        uint32_t dtype, yuuka_event * completion);
+
+/* Acceptance modes of yuuka_verify_accept. */
+#define YUUKA_ACCEPT_GREEDY 0u
+#define YUUKA_ACCEPT_STOCHASTIC 1u
+
+/* Parameters of one fused verify-accept call (host struct, copied). */
+typedef struct yuuka_accept_params {
+    uint32_t mode;        /* YUUKA_ACCEPT_* */
+    uint32_t batch;       /* requests B >= 1 */
+    uint32_t drafts;      /* k >= 0; every request holds k+1 logits rows */
+    uint32_t vocab;       /* V */
+    float temperature;    /* stochastic: T > 0; <= 0 means greedy target */
+    uint32_t top_k;       /* 0 = off */
+    float top_p;          /* >= 1 = off */
+    uint32_t request_base;/* request index of batch entry 0 (Philox counter) */
+    uint64_t seed;        /* Philox4x32-10 key */
+    uint64_t step;        /* Philox counter word (verify step) */
+    uint64_t row_stride;  /* floats between consecutive logits rows; 0 = V */
+} yuuka_accept_params;
+
+/* Fused verify-accept over the logits of one verify step (replaces the host
+ * loop of engine/speculative.go:191-208 plus argmaxLogit :263-271; the
+ * stochastic mode has no reference counterpart).
+ *
+ * logits: FP32 [B][k+1][V] (row stride params->row_stride), row i of request
+ *         b is the target distribution for draft i, row k the bonus row.
+ * drafts: int32 [B][k].
+ * result: int32 [B][4] = {accepted in 0..k, next token, argmax of row 0,
+ *         reserved}.
+ * debug:  optional (may be NULL) FP64 [B][k+1][4] = {p(draft), u, row total,
+ *         row max logit}.
+ * Greedy: accept draft i iff argmax(row i) == draft i (lowest index among
+ * equal maxima; a NaN at index 0 wins, later NaNs never do); next = argmax
+ * of the first rejected row, or of row k when every draft is accepted.
+ * Stochastic: target p = softmax(logit/T) over finite logits (float64 sums);
+ * draft i is accepted iff u_i < p(d_i) with u_i = Philox(seed; step, i,
+ * request, 0); on the first rejection next is drawn from p with d_i removed,
+ * and after full acceptance from row k, by inverse CDF in index order with
+ * u = Philox(seed; step, i, request, 1).
+ * top_k > 1 or top_p < 1 currently returns YUUKA_ERR_UNSUPPORTED. */
+YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
+                        const yuuka_buffer * logits, uint64_t logits_offset,
+                        const yuuka_buffer * drafts, uint64_t drafts_offset,
+                        yuuka_buffer * result, uint64_t result_offset,
+                        yuuka_buffer * debug, const yuuka_accept_params * params,
+                        yuuka_event * completion);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

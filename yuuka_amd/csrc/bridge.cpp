@@ -1,0 +1,519 @@
+// bridge.cpp — implementation of the yuuka_hip.h C ABI on HIP for gfx950.
+//
+// Mirrors the contract of the reference bridge (backend/hip/bridge/bridge.cpp):
+// opaque handles, thread-local error text (:47-57), an exception guard on every
+// entry (:1893-1906), per-op validation before a plan op is appended
+// (reject-without-append, yuuka_hip.h:330-334), asynchronous submission with a
+// completion event (:3837-3870). Kernels live in k_*.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+#include "plan.h"
+
+namespace yk {
+
+static thread_local std::string g_last_error;
+
+yuuka_status fail(yuuka_status status, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+const char *hip_error(hipError_t err) { return hipGetErrorString(err); }
+
+yuuka_status ensure_scratch(yuuka_stream *stream, yk_scratch *area, uint64_t bytes) {
+    if (area->bytes >= bytes) return YUUKA_OK;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream->stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return fail(YUUKA_ERR_UNSUPPORTED, "workspace must be sized before graph capture");
+    // Outstanding work may still use the old area.
+    hipError_t err = hipStreamSynchronize(stream->stream);
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "stream synchronize: %s", hip_error(err));
+    if (area->ptr) (void)hipFree(area->ptr);
+    area->ptr = nullptr;
+    area->bytes = 0;
+    const uint64_t want = (bytes + 0xfffffull) & ~0xfffffull;
+    err = hipMalloc(&area->ptr, want);
+    if (err != hipSuccess) {
+        area->ptr = nullptr;
+        return fail(YUUKA_ERR_ALLOCATION, "workspace of %llu bytes: %s", (unsigned long long)want,
+                    hip_error(err));
+    }
+    err = hipMemset(area->ptr, 0, want);
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "workspace clear: %s", hip_error(err));
+    area->bytes = want;
+    return YUUKA_OK;
+}
+
+template <typename F>
+static yuuka_status guard(const char *what, F &&f) {
+    try {
+        return f();
+    } catch (const std::bad_alloc &) {
+        return fail(YUUKA_ERR_ALLOCATION, "%s: host allocation failed", what);
+    } catch (const std::exception &e) {
+        return fail(YUUKA_ERR_INTERNAL, "%s: %s", what, e.what());
+    } catch (...) {
+        return fail(YUUKA_ERR_INTERNAL, "%s: unknown exception", what);
+    }
+}
+
+static bool range_ok(const yuuka_buffer *b, uint64_t off, uint64_t bytes) {
+    return b != nullptr && off <= b->bytes && bytes <= b->bytes - off;
+}
+
+static yuuka_status record(yuuka_stream *stream, yuuka_event *completion) {
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "kernel launch: %s", hip_error(err));
+    if (completion) {
+        err = hipEventRecord(completion->event, stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "event record: %s", hip_error(err));
+    }
+    return YUUKA_OK;
+}
+
+// Shared validation of the verify GEMM shape (reference bridge.cpp:303-349).
+yuuka_status check_verify_gemm(uint64_t n_in, uint64_t n_out, uint64_t rows, uint32_t dtype,
+                               uint64_t max_rows) {
+    if (dtype != YUUKA_DTYPE_Q4_K && dtype != YUUKA_DTYPE_Q6_K)
+        return fail(YUUKA_ERR_UNSUPPORTED, "verify GEMM dtype %u is not Q4_K or Q6_K", dtype);
+    if (n_in == 0 || n_in % 256 != 0)
+        return fail(YUUKA_ERR_UNSUPPORTED, "verify GEMM input width %llu is not a multiple of 256",
+                    (unsigned long long)n_in);
+    if (n_out == 0 || rows == 0 || rows > max_rows)
+        return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid output width %llu or row block %llu",
+                    (unsigned long long)n_out, (unsigned long long)rows);
+    if (n_in > (1ull << 24) || n_out > (1ull << 26))
+        return fail(YUUKA_ERR_UNSUPPORTED, "verify GEMM shape %llux%llu too large",
+                    (unsigned long long)n_out, (unsigned long long)n_in);
+    const uint64_t wb = row_bytes(dtype, n_in) * n_out;
+    if (wb >= (1ull << 32) - 16)
+        return fail(YUUKA_ERR_UNSUPPORTED, "weight matrix of %llu bytes exceeds 4 GiB",
+                    (unsigned long long)wb);
+    return YUUKA_OK;
+}
+
+// Runs quantize + GEMM using `ws` (>= xq + partials) and `tickets`.
+yuuka_status run_verify_gemm(hipStream_t stream, const void *w, uint32_t dtype, const float *x,
+                             float *out, uint64_t n_in, uint64_t n_out, uint64_t rows, void *ws,
+                             uint32_t *tickets) {
+    const GemmPlan plan = gemm_plan(n_in, n_out, rows);
+    uint8_t *xq = static_cast<uint8_t *>(ws);
+    void *partials = xq + ((plan.xq_bytes + 255) & ~255ull);
+    hipError_t err = launch_quantize_x(x, n_in, rows, xq, stream);
+    if (err == hipSuccess)
+        err = launch_gemm_q(w, dtype, xq, out, n_in, n_out, rows, plan, partials, tickets, stream);
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "verify GEMM launch: %s", hip_error(err));
+    return YUUKA_OK;
+}
+
+uint64_t verify_gemm_ws_bytes(uint64_t n_in, uint64_t n_out, uint64_t rows) {
+    const GemmPlan plan = gemm_plan(n_in, n_out, rows);
+    return ((plan.xq_bytes + 255) & ~255ull) + plan.part_bytes + 256;
+}
+
+uint32_t verify_gemm_tickets(uint64_t n_in, uint64_t n_out, uint64_t rows) {
+    return gemm_plan(n_in, n_out, rows).tickets;
+}
+
+}  // namespace yk
+
+using namespace yk;
+
+#define UNSUPPORTED_ENTRY(name) \
+    return fail(YUUKA_ERR_UNSUPPORTED, "%s is outside the verify path served by this library", name)
+
+extern "C" {
+
+uint32_t yuuka_abi_version(void) { return YUUKA_HIP_ABI_VERSION; }
+uint32_t yuuka_ext_version(void) { return YUUKA_EXT_VERSION; }
+const char *yuuka_last_error(void) { return g_last_error.c_str(); }
+
+yuuka_status yuuka_device_open(int32_t index, yuuka_device **out) {
+    return guard("device_open", [&]() -> yuuka_status {
+        if (!out) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null output handle");
+        *out = nullptr;
+        int count = 0;
+        hipError_t err = hipGetDeviceCount(&count);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "device count: %s", hip_error(err));
+        if (index < 0 || index >= count)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "device index %d outside 0..%d", index, count - 1);
+        err = hipSetDevice(index);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "set device: %s", hip_error(err));
+        auto *dev = new yuuka_device();
+        dev->index = index;
+        err = hipGetDeviceProperties(&dev->props, index);
+        if (err != hipSuccess) {
+            delete dev;
+            return fail(YUUKA_ERR_DEVICE, "device properties: %s", hip_error(err));
+        }
+        *out = dev;
+        return YUUKA_OK;
+    });
+}
+
+void yuuka_device_close(yuuka_device *dev) { delete dev; }
+
+yuuka_status yuuka_device_info_get(const yuuka_device *dev, yuuka_device_info *info) {
+    return guard("device_info", [&]() -> yuuka_status {
+        if (!dev || !info) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null device or info");
+        std::memset(info, 0, sizeof(*info));
+        std::snprintf(info->name, sizeof(info->name), "%s", dev->props.name);
+        std::snprintf(info->gcn_arch, sizeof(info->gcn_arch), "%s", dev->props.gcnArchName);
+        int rt = 0;
+        (void)hipRuntimeGetVersion(&rt);
+        std::snprintf(info->hip_version, sizeof(info->hip_version), "%d", rt);
+        info->total_memory = dev->props.totalGlobalMem;
+        info->compute_units = (uint32_t)dev->props.multiProcessorCount;
+        info->clock_mhz = (uint32_t)(dev->props.clockRate / 1000);
+        info->pci_domain = dev->props.pciDomainID;
+        info->pci_bus = dev->props.pciBusID;
+        info->pci_device = dev->props.pciDeviceID;
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_buffer_alloc(yuuka_device *dev, uint64_t bytes, yuuka_buffer **out) {
+    return guard("buffer_alloc", [&]() -> yuuka_status {
+        if (!dev || !out) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null device or output");
+        *out = nullptr;
+        if (bytes == 0) return fail(YUUKA_ERR_INVALID_ARGUMENT, "zero-byte allocation");
+        hipError_t err = hipSetDevice(dev->index);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "set device: %s", hip_error(err));
+        void *ptr = nullptr;
+        err = hipMalloc(&ptr, bytes);
+        if (err != hipSuccess)
+            return fail(YUUKA_ERR_ALLOCATION, "hipMalloc(%llu): %s", (unsigned long long)bytes,
+                        hip_error(err));
+        auto *b = new yuuka_buffer();
+        b->dev = dev;
+        b->ptr = ptr;
+        b->bytes = bytes;
+        *out = b;
+        return YUUKA_OK;
+    });
+}
+
+void yuuka_buffer_free(yuuka_buffer *buf) {
+    if (!buf) return;
+    if (buf->ptr) (void)hipFree(buf->ptr);
+    delete buf;
+}
+
+uint64_t yuuka_buffer_size(const yuuka_buffer *buf) { return buf ? buf->bytes : 0; }
+void *yuuka_buffer_ptr(const yuuka_buffer *buf) { return buf ? buf->ptr : nullptr; }
+
+yuuka_status yuuka_stream_create(yuuka_device *dev, yuuka_stream **out) {
+    return guard("stream_create", [&]() -> yuuka_status {
+        if (!dev || !out) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null device or output");
+        *out = nullptr;
+        hipError_t err = hipSetDevice(dev->index);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "set device: %s", hip_error(err));
+        auto *s = new yuuka_stream();
+        s->dev = dev;
+        err = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
+        if (err != hipSuccess) {
+            delete s;
+            return fail(YUUKA_ERR_DEVICE, "stream create: %s", hip_error(err));
+        }
+        *out = s;
+        return YUUKA_OK;
+    });
+}
+
+void yuuka_stream_destroy(yuuka_stream *stream) {
+    if (!stream) return;
+    (void)hipStreamSynchronize(stream->stream);
+    if (stream->scratch.ptr) (void)hipFree(stream->scratch.ptr);
+    if (stream->tickets.ptr) (void)hipFree(stream->tickets.ptr);
+    (void)hipStreamDestroy(stream->stream);
+    delete stream;
+}
+
+yuuka_status yuuka_stream_synchronize(yuuka_stream *stream) {
+    return guard("stream_synchronize", [&]() -> yuuka_status {
+        if (!stream) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null stream");
+        hipError_t err = hipStreamSynchronize(stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "stream synchronize: %s", hip_error(err));
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_event_create(yuuka_device *dev, yuuka_event **out) {
+    return guard("event_create", [&]() -> yuuka_status {
+        if (!dev || !out) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null device or output");
+        *out = nullptr;
+        auto *e = new yuuka_event();
+        hipError_t err = hipEventCreateWithFlags(&e->event, hipEventDisableTiming);
+        if (err != hipSuccess) {
+            delete e;
+            return fail(YUUKA_ERR_DEVICE, "event create: %s", hip_error(err));
+        }
+        *out = e;
+        return YUUKA_OK;
+    });
+}
+
+void yuuka_event_destroy(yuuka_event *event) {
+    if (!event) return;
+    (void)hipEventDestroy(event->event);
+    delete event;
+}
+
+yuuka_status yuuka_event_wait(yuuka_event *event) {
+    return guard("event_wait", [&]() -> yuuka_status {
+        if (!event) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null event");
+        hipError_t err = hipEventSynchronize(event->event);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "event wait: %s", hip_error(err));
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_memcpy_h2d(yuuka_buffer *dst, const void *src, uint64_t bytes) {
+    return guard("memcpy_h2d", [&]() -> yuuka_status {
+        if (!dst || (!src && bytes)) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null buffer or source");
+        if (bytes > dst->bytes) return fail(YUUKA_ERR_INVALID_ARGUMENT, "copy exceeds buffer");
+        if (!bytes) return YUUKA_OK;
+        hipError_t err = hipMemcpy(dst->ptr, src, bytes, hipMemcpyHostToDevice);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "memcpy h2d: %s", hip_error(err));
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_memcpy_d2h(void *dst, const yuuka_buffer *src, uint64_t bytes) {
+    return yuuka_memcpy_d2h_at(dst, src, 0, bytes);
+}
+
+yuuka_status yuuka_memcpy_d2h_at(void *dst, const yuuka_buffer *src, uint64_t offset, uint64_t bytes) {
+    return guard("memcpy_d2h", [&]() -> yuuka_status {
+        if (!src || (!dst && bytes)) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null buffer or destination");
+        if (!range_ok(src, offset, bytes)) return fail(YUUKA_ERR_INVALID_ARGUMENT, "copy exceeds buffer");
+        if (!bytes) return YUUKA_OK;
+        hipError_t err = hipMemcpy(dst, static_cast<const uint8_t *>(src->ptr) + offset, bytes,
+                                   hipMemcpyDeviceToHost);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "memcpy d2h: %s", hip_error(err));
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_memset(yuuka_stream *stream, yuuka_buffer *dst, int value, uint64_t bytes) {
+    return guard("memset", [&]() -> yuuka_status {
+        if (!stream || !dst) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null stream or buffer");
+        if (bytes > dst->bytes) return fail(YUUKA_ERR_INVALID_ARGUMENT, "memset exceeds buffer");
+        hipError_t err = hipMemsetAsync(dst->ptr, value, bytes, stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "memset: %s", hip_error(err));
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_buffer_copy(yuuka_stream *stream, yuuka_buffer *dst, uint64_t dst_offset,
+                               const yuuka_buffer *src, uint64_t src_offset, uint64_t bytes,
+                               yuuka_event *completion) {
+    return guard("buffer_copy", [&]() -> yuuka_status {
+        if (!stream || !dst || !src) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        if (!range_ok(dst, dst_offset, bytes) || !range_ok(src, src_offset, bytes))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "copy range exceeds a buffer");
+        if (bytes) {
+            hipError_t err = hipMemcpyAsync(static_cast<uint8_t *>(dst->ptr) + dst_offset,
+                                            static_cast<const uint8_t *>(src->ptr) + src_offset, bytes,
+                                            hipMemcpyDeviceToDevice, stream->stream);
+            if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "buffer copy: %s", hip_error(err));
+        }
+        return record(stream, completion);
+    });
+}
+
+yuuka_status yuuka_dynamic_set(yuuka_stream *stream, yuuka_buffer *dynamic, int32_t token,
+                               uint32_t position) {
+    return guard("dynamic_set", [&]() -> yuuka_status {
+        if (!stream || !dynamic) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        if (dynamic->bytes < 8) return fail(YUUKA_ERR_INVALID_ARGUMENT, "dynamic buffer under 8 bytes");
+        const int32_t v[2] = {token, (int32_t)position};
+        hipError_t err = hipMemcpyAsync(dynamic->ptr, v, 8, hipMemcpyHostToDevice, stream->stream);
+        if (err == hipSuccess) err = hipStreamSynchronize(stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "dynamic set: %s", hip_error(err));
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_add_f32(yuuka_stream *stream, yuuka_buffer *dst, const yuuka_buffer *a,
+                           const yuuka_buffer *b, uint64_t n, yuuka_event *completion) {
+    return guard("add_f32", [&]() -> yuuka_status {
+        if (!stream || !dst || !a || !b) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        if (!range_ok(dst, 0, n * 4) || !range_ok(a, 0, n * 4) || !range_ok(b, 0, n * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "add exceeds a buffer");
+        hipError_t err = launch_add_f32(static_cast<float *>(dst->ptr), static_cast<const float *>(a->ptr),
+                                        static_cast<const float *>(b->ptr), n, stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "add launch: %s", hip_error(err));
+        return record(stream, completion);
+    });
+}
+
+static yuuka_status direct_gemm(const char *what, yuuka_stream *stream, yuuka_buffer *out,
+                                const yuuka_buffer *x, const yuuka_buffer *w, uint64_t n_in,
+                                uint64_t n_out, uint64_t rows, uint32_t dtype,
+                                yuuka_event *completion) {
+    return guard(what, [&]() -> yuuka_status {
+        if (!stream || !out || !x || !w) return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s: null argument", what);
+        yuuka_status st = check_verify_gemm(n_in, n_out, rows, dtype, 16);
+        if (st != YUUKA_OK) return st;
+        if (!range_ok(w, 0, row_bytes(dtype, n_in) * n_out))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s weight buffer is too small", what);
+        if (!range_ok(x, 0, n_in * rows * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s input buffer is too small", what);
+        if (!range_ok(out, 0, n_out * rows * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s output buffer is too small", what);
+        st = ensure_scratch(stream, &stream->scratch, verify_gemm_ws_bytes(n_in, n_out, rows));
+        if (st != YUUKA_OK) return st;
+        st = ensure_scratch(stream, &stream->tickets, (uint64_t)verify_gemm_tickets(n_in, n_out, rows) * 4 + 4);
+        if (st != YUUKA_OK) return st;
+        st = run_verify_gemm(stream->stream, w->ptr, dtype, static_cast<const float *>(x->ptr),
+                             static_cast<float *>(out->ptr), n_in, n_out, rows, stream->scratch.ptr,
+                             static_cast<uint32_t *>(stream->tickets.ptr));
+        if (st != YUUKA_OK) return st;
+        return record(stream, completion);
+    });
+}
+
+yuuka_status yuuka_lm_head(yuuka_stream *stream, yuuka_buffer *out, const yuuka_buffer *x,
+                           const yuuka_buffer *w, uint64_t n_in, uint64_t n_out, uint64_t rows,
+                           uint32_t dtype, yuuka_event *completion) {
+    return direct_gemm("lm_head", stream, out, x, w, n_in, n_out, rows, dtype, completion);
+}
+
+yuuka_status yuuka_gemv(yuuka_stream *stream, yuuka_buffer *out, const yuuka_buffer *x,
+                        const yuuka_buffer *w, uint64_t n_in, uint64_t n_out, uint32_t dtype,
+                        yuuka_event *completion) {
+    return direct_gemm("gemv", stream, out, x, w, n_in, n_out, 1, dtype, completion);
+}
+
+yuuka_status yuuka_gemv_batch(yuuka_stream *stream, yuuka_buffer *out, const yuuka_buffer *x,
+                              const yuuka_buffer *w, uint64_t n_in, uint64_t n_out, uint64_t batch,
+                              uint32_t dtype, yuuka_event *completion) {
+    return direct_gemm("gemv_batch", stream, out, x, w, n_in, n_out, batch, dtype, completion);
+}
+
+yuuka_status yuuka_gemm(yuuka_stream *, yuuka_buffer *, const yuuka_buffer *, const yuuka_buffer *,
+                        uint64_t, uint64_t, uint64_t, uint32_t, yuuka_event *) {
+    UNSUPPORTED_ENTRY("yuuka_gemm (prefill GEMM)");
+}
+yuuka_status yuuka_gemm_wmma(yuuka_stream *, yuuka_buffer *, const yuuka_buffer *, const yuuka_buffer *,
+                             uint64_t, uint64_t, uint64_t, uint32_t, yuuka_event *) {
+    UNSUPPORTED_ENTRY("yuuka_gemm_wmma (rocWMMA prefill GEMM)");
+}
+yuuka_status yuuka_quantize_q8_1(yuuka_stream *, yuuka_buffer *, yuuka_buffer *, const yuuka_buffer *,
+                                 uint64_t, uint64_t, yuuka_event *) {
+    UNSUPPORTED_ENTRY("yuuka_quantize_q8_1 (MMQ prefill route)");
+}
+yuuka_status yuuka_gemm_mmq(yuuka_stream *, yuuka_buffer *, const yuuka_buffer *, const yuuka_buffer *,
+                            const yuuka_buffer *, uint64_t, uint64_t, uint64_t, uint32_t, yuuka_event *) {
+    UNSUPPORTED_ENTRY("yuuka_gemm_mmq (MMQ prefill route)");
+}
+yuuka_status yuuka_gemm_blas(yuuka_stream *, yuuka_buffer *, yuuka_buffer *, const yuuka_buffer *,
+                             const yuuka_buffer *, uint64_t, uint64_t, uint64_t, yuuka_event *) {
+    UNSUPPORTED_ENTRY("yuuka_gemm_blas (rocBLAS prefill route)");
+}
+
+static yuuka_status dequant_entry(const char *what, yuuka_stream *stream, yuuka_buffer *dst,
+                                  const yuuka_buffer *src, uint64_t n_in, uint64_t n_out,
+                                  uint32_t dtype, uint64_t elem_bytes, yuuka_event *completion) {
+    return guard(what, [&]() -> yuuka_status {
+        if (!stream || !dst || !src) return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s: null argument", what);
+        const uint64_t rb = row_bytes(dtype, n_in);
+        if (rb == 0 || dtype == YUUKA_DTYPE_Q4_0 || dtype == YUUKA_DTYPE_Q5_0)
+            return fail(YUUKA_ERR_UNSUPPORTED, "%s: dtype %u / width %llu unsupported", what, dtype,
+                        (unsigned long long)n_in);
+        if (n_out == 0) return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s: zero rows", what);
+        if (!range_ok(src, 0, rb * n_out)) return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s: source too small", what);
+        if (!range_ok(dst, 0, n_in * n_out * elem_bytes))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s: destination too small", what);
+        hipError_t err = elem_bytes == 4
+                             ? launch_dequant_f32(src->ptr, dtype, static_cast<float *>(dst->ptr), n_in, n_out, stream->stream)
+                             : launch_dequant_f16(src->ptr, dtype, static_cast<uint16_t *>(dst->ptr), n_in, n_out, stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "%s launch: %s", what, hip_error(err));
+        return record(stream, completion);
+    });
+}
+
+yuuka_status yuuka_dequant_f32(yuuka_stream *stream, yuuka_buffer *dst, const yuuka_buffer *src,
+                               uint64_t n_in, uint64_t n_out, uint32_t dtype, yuuka_event *completion) {
+    return dequant_entry("dequant_f32", stream, dst, src, n_in, n_out, dtype, 4, completion);
+}
+
+yuuka_status yuuka_dequant_f16(yuuka_stream *stream, yuuka_buffer *dst, const yuuka_buffer *src,
+                               uint64_t n_in, uint64_t n_out, uint32_t dtype, yuuka_event *completion) {
+    return dequant_entry("dequant_f16", stream, dst, src, n_in, n_out, dtype, 2, completion);
+}
+
+yuuka_status yuuka_cast_f32_to_f16(yuuka_stream *stream, yuuka_buffer *dst, const yuuka_buffer *src,
+                                   uint64_t n, yuuka_event *completion) {
+    return guard("cast_f16", [&]() -> yuuka_status {
+        if (!stream || !dst || !src) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        if (!range_ok(src, 0, n * 4) || !range_ok(dst, 0, n * 2))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "cast exceeds a buffer");
+        hipError_t err = launch_cast_f16(static_cast<const float *>(src->ptr),
+                                         static_cast<uint16_t *>(dst->ptr), n, stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "cast launch: %s", hip_error(err));
+        return record(stream, completion);
+    });
+}
+
+yuuka_status yuuka_verify_accept(yuuka_stream *stream, const yuuka_buffer *logits,
+                                 uint64_t logits_offset, const yuuka_buffer *drafts,
+                                 uint64_t drafts_offset, yuuka_buffer *result,
+                                 uint64_t result_offset, yuuka_buffer *debug,
+                                 const yuuka_accept_params *params, yuuka_event *completion) {
+    return guard("verify_accept", [&]() -> yuuka_status {
+        if (!stream || !logits || !result || !params)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        const yuuka_accept_params &p = *params;
+        if (p.mode != YUUKA_ACCEPT_GREEDY && p.mode != YUUKA_ACCEPT_STOCHASTIC)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "unknown accept mode %u", p.mode);
+        if (p.batch == 0 || p.vocab == 0 || p.vocab > (1u << 30) || p.drafts > 255)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid batch %u, drafts %u or vocab %u", p.batch,
+                        p.drafts, p.vocab);
+        if (p.mode == YUUKA_ACCEPT_STOCHASTIC && p.temperature > 0.0f && p.top_k != 1 &&
+            (p.top_k > 1 || p.top_p < 1.0f))
+            return fail(YUUKA_ERR_UNSUPPORTED, "top-k/top-p truncation is not implemented");
+        if (p.mode == YUUKA_ACCEPT_STOCHASTIC && !(p.top_p >= 0.0f && p.top_p <= 1.0f) && p.top_p != 0.0f)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "top-p must be in (0,1]");
+        const uint64_t stride = p.row_stride ? p.row_stride : p.vocab;
+        if (stride < p.vocab) return fail(YUUKA_ERR_INVALID_ARGUMENT, "row stride below vocab");
+        const uint64_t rows = (uint64_t)p.batch * (p.drafts + 1);
+        if (logits_offset % 4 || !range_ok(logits, logits_offset, ((rows - 1) * stride + p.vocab) * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "logits buffer too small or misaligned");
+        if (p.drafts > 0 && (!drafts || drafts_offset % 4 ||
+                             !range_ok(drafts, drafts_offset, (uint64_t)p.batch * p.drafts * 4)))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "drafts buffer too small or misaligned");
+        if (result_offset % 4 || !range_ok(result, result_offset, (uint64_t)p.batch * 16))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "result buffer too small or misaligned");
+        if (debug && !range_ok(debug, 0, rows * 32))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "debug buffer too small");
+        yuuka_status st = ensure_scratch(stream, &stream->scratch, accept_scratch_bytes(p));
+        if (st != YUUKA_OK) return st;
+        const int32_t *dp = p.drafts > 0
+                                ? reinterpret_cast<const int32_t *>(static_cast<const uint8_t *>(drafts->ptr) + drafts_offset)
+                                : nullptr;
+        hipError_t err = launch_verify_accept(
+            reinterpret_cast<const float *>(static_cast<const uint8_t *>(logits->ptr) + logits_offset), dp,
+            reinterpret_cast<int32_t *>(static_cast<uint8_t *>(result->ptr) + result_offset),
+            debug ? static_cast<double *>(debug->ptr) : nullptr, p, stream->scratch.ptr, stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "accept launch: %s", hip_error(err));
+        return record(stream, completion);
+    });
+}
+
+}  // extern "C"

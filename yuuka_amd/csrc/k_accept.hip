@@ -1,0 +1,359 @@
+// k_accept.hip — fused verify-accept over the k+1 logits rows of one verify
+// step, batched over requests.
+//
+// Greedy mode restates the accept loop of engine/speculative.go:191-208 with
+// argmaxLogit (:263-271): draft i is accepted iff the first maximum of row i
+// equals it. Stochastic mode is speculative sampling with a one-hot draft
+// (no reference counterpart): accept iff u < p(d), else resample from p with
+// d removed; the target p follows engine/sampling.go:94-100 (weights
+// exp(float64(logit - max) / T) over finite logits).
+//
+// Three kernels (the two passes over a row are separate launches so that the
+// exact row maximum is known before any exponential is taken):
+//   1. stats:    per (request, row, chunk): maximum and its first index.
+//   2. weights:  (stochastic) per chunk: float64 sum of the weights with the
+//                draft removed, and the draft's own weight.
+//   3. finalize: one workgroup per request walks the rows in order, decides,
+//                and for a rejection or the bonus row draws by inverse CDF
+//                in index order (chunk prefix, then a scan inside the chunk).
+#include <hip/hip_runtime.h>
+
+#include <climits>
+
+#include "internal.h"
+
+namespace yk {
+namespace {
+
+struct Stat {
+    float v;
+    int i;
+};
+
+// a beats b: larger value, or equal value and lower index. NaN never wins.
+__device__ __forceinline__ bool beats(float av, int ai, float bv, int bi) {
+    return av > bv || (av == bv && ai < bi);
+}
+
+struct Geo {
+    int B, R, k, V, C, L;
+    uint64_t stride;
+};
+
+__device__ __forceinline__ const float *row_ptr(const float *logits, const Geo &g, int b, int row) {
+    return logits + ((uint64_t)b * g.R + row) * g.stride;
+}
+
+__global__ __launch_bounds__(256) void accept_stats_kernel(const float *__restrict__ logits, Geo g,
+                                                           Stat *__restrict__ stats) {
+    const int c = blockIdx.x, row = blockIdx.y, b = blockIdx.z;
+    const float *p = row_ptr(logits, g, b, row);
+    const int begin = c * g.L;
+    const int end = min(begin + g.L, g.V);
+    float bv = -INFINITY;
+    int bi = INT_MAX;
+    for (int j = begin + threadIdx.x; j < end; j += 256) {
+        const float v = p[j];
+        if (beats(v, j, bv, bi)) {
+            bv = v;
+            bi = j;
+        }
+    }
+    // wave reduction, then across the four waves
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off);
+        if (beats(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    __shared__ Stat ws[4];
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = Stat{bv, bi};
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Stat s = ws[0];
+        for (int w = 1; w < 4; w++)
+            if (beats(ws[w].v, ws[w].i, s.v, s.i)) s = ws[w];
+        stats[((uint64_t)b * g.R + row) * g.C + c] = s;
+    }
+}
+
+__device__ __forceinline__ Stat row_best(const Stat *stats, const Geo &g, int b, int row) {
+    const Stat *s = stats + ((uint64_t)b * g.R + row) * g.C;
+    Stat best{-INFINITY, INT_MAX};
+    for (int c = 0; c < g.C; c++)
+        if (beats(s[c].v, s[c].i, best.v, best.i)) best = s[c];
+    return best;
+}
+
+__device__ __forceinline__ double weight_of(float l, float mx, double inv_t) {
+    if (!(l == l) || l == -INFINITY) return 0.0;  // NaN and -Inf are dropped
+    return exp((double)(l - mx) * inv_t);
+}
+
+__global__ __launch_bounds__(256) void accept_weights_kernel(const float *__restrict__ logits, Geo g,
+                                                             const int32_t *__restrict__ drafts,
+                                                             const Stat *__restrict__ stats,
+                                                             double inv_t, double *__restrict__ sums,
+                                                             double *__restrict__ wdraft) {
+    const int c = blockIdx.x, row = blockIdx.y, b = blockIdx.z;
+    const float *p = row_ptr(logits, g, b, row);
+    __shared__ float mx_s;
+    if (threadIdx.x == 0) mx_s = row_best(stats, g, b, row).v;
+    __syncthreads();
+    const float mx = mx_s;
+    const int d = row < g.k ? drafts[(uint64_t)b * g.k + row] : -1;
+    const int begin = c * g.L;
+    const int end = min(begin + g.L, g.V);
+    double acc = 0.0;
+    for (int j = begin + threadIdx.x; j < end; j += 256) {
+        const double w = weight_of(p[j], mx, inv_t);
+        if (j == d)
+            wdraft[(uint64_t)b * g.R + row] = w;
+        else
+            acc += w;
+    }
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+    __shared__ double ws[4];
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) sums[((uint64_t)b * g.R + row) * g.C + c] = ws[0] + ws[1] + ws[2] + ws[3];
+}
+
+// Philox4x32-10 (Salmon et al., SC'11).
+__device__ __forceinline__ void philox(uint32_t c[4], uint32_t k0, uint32_t k1) {
+    for (int r = 0; r < 10; r++) {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c[0];
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c[2];
+        const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0;
+        const uint32_t n1 = (uint32_t)p1;
+        const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+        const uint32_t n3 = (uint32_t)p0;
+        c[0] = n0; c[1] = n1; c[2] = n2; c[3] = n3;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+}
+
+__device__ __forceinline__ double draw(uint64_t seed, uint64_t step, uint32_t row, uint32_t request,
+                                       uint32_t purpose) {
+    uint32_t c[4] = {(uint32_t)step, (uint32_t)(step >> 32), request, (row << 8) | (purpose & 0xffu)};
+    philox(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    const uint64_t v = ((((uint64_t)c[0]) << 32) | c[1]) >> 11;
+    return (double)v * (1.0 / 9007199254740992.0);
+}
+
+// Block-wide inverse CDF inside chunk `c` of a row: the first index j (j != d,
+// weight > 0) whose running weight sum exceeds `target`. Returns -1 when the
+// target lies beyond the chunk's own sum (rounding), with *last the last
+// positive-weight index of the chunk.
+__device__ int scan_chunk(const float *p, const Geo &g, int c, int d, float mx, double inv_t,
+                          double target, double *shared_prefix, int *shared_pick) {
+    const int begin = c * g.L;
+    const int end = min(begin + g.L, g.V);
+    const int len = end - begin;
+    const int per = (len + 255) / 256;
+    const int lo = begin + threadIdx.x * per;
+    const int hi = min(lo + per, end);
+    double local = 0.0;
+    for (int j = lo; j < hi; j++)
+        if (j != d) local += weight_of(p[j], mx, inv_t);
+    shared_prefix[threadIdx.x] = local;
+    if (threadIdx.x == 0) *shared_pick = -1;
+    __syncthreads();
+    if (threadIdx.x == 0) {  // exclusive prefix in thread order
+        double run = 0.0;
+        for (int t = 0; t < 256; t++) {
+            const double v = shared_prefix[t];
+            shared_prefix[t] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    double run = shared_prefix[threadIdx.x];
+    if (run <= target && target < run + local) {
+        for (int j = lo; j < hi; j++) {
+            if (j == d) continue;
+            const double w = weight_of(p[j], mx, inv_t);
+            if (w <= 0.0) continue;
+            run += w;
+            if (target < run) {
+                *shared_pick = j;
+                break;
+            }
+        }
+        if (*shared_pick < 0) {  // rounding at the boundary: last positive weight
+            for (int j = hi - 1; j >= lo; j--)
+                if (j != d && weight_of(p[j], mx, inv_t) > 0.0) {
+                    *shared_pick = j;
+                    break;
+                }
+        }
+    }
+    __syncthreads();
+    return *shared_pick;
+}
+
+__global__ __launch_bounds__(256) void accept_finalize_kernel(
+    const float *__restrict__ logits, Geo g, const int32_t *__restrict__ drafts,
+    const Stat *__restrict__ stats, const double *__restrict__ sums,
+    const double *__restrict__ wdraft, int stochastic, double inv_t, uint64_t seed, uint64_t step,
+    uint32_t request_base, int32_t *__restrict__ result, double *__restrict__ debug) {
+    const int b = blockIdx.x;
+    const uint32_t request = request_base + (uint32_t)b;
+    __shared__ double prefix[256];
+    __shared__ int pick;
+    __shared__ int decided_next;
+    __shared__ int accepted_s;
+    __shared__ int argmax0;
+    if (threadIdx.x == 0) {
+        decided_next = -1;
+        accepted_s = 0;
+    }
+    __syncthreads();
+    for (int row = 0; row <= g.k; row++) {
+        const float *p = row_ptr(logits, g, b, row);
+        __shared__ Stat best_s;
+        __shared__ int action;  // 0 accept, 1 done (next decided), 2 resample
+        __shared__ double target_s;
+        __shared__ int cstar;
+        __shared__ float mx_s;
+        if (threadIdx.x == 0) {
+            Stat best = row_best(stats, g, b, row);
+            if (p[0] != p[0]) best = Stat{p[0], 0};  // argmaxLogit keeps a NaN at index 0
+            best_s = best;
+            if (row == 0) argmax0 = best.i;
+            const int d = row < g.k ? drafts[(uint64_t)b * g.k + row] : -1;
+            double dbg[4] = {0.0, 0.0, 0.0, (double)best.v};
+            action = 1;
+            if (!stochastic) {
+                if (row < g.k && best.i == d) {
+                    action = 0;
+                } else {
+                    decided_next = best.i;
+                }
+            } else {
+                const double *cs = sums + ((uint64_t)b * g.R + row) * g.C;
+                double rest = 0.0;
+                for (int c = 0; c < g.C; c++) rest += cs[c];
+                const double wd = (row < g.k && d >= 0 && d < g.V) ? wdraft[(uint64_t)b * g.R + row] : 0.0;
+                double total = rest + wd;
+                const bool onehot = !(total > 0.0) || isinf(total);
+                dbg[2] = total;
+                if (row < g.k) {
+                    const double pd = onehot ? (d == best.i ? 1.0 : 0.0) : wd / total;
+                    const double u = draw(seed, step, (uint32_t)row, request, 0);
+                    dbg[0] = pd;
+                    dbg[1] = u;
+                    if (u < pd) {
+                        action = 0;
+                    } else if (onehot || !(rest > 0.0)) {
+                        decided_next = best.i;
+                    } else {
+                        const double u2 = draw(seed, step, (uint32_t)row, request, 1);
+                        const double target = u2 * rest;
+                        double run = 0.0;
+                        int c = 0;
+                        for (; c < g.C - 1; c++) {
+                            if (target < run + cs[c]) break;
+                            run += cs[c];
+                        }
+                        target_s = target - run;
+                        cstar = c;
+                        mx_s = best.v;
+                        action = 2;
+                    }
+                } else {
+                    if (onehot) {
+                        decided_next = best.i;
+                    } else {
+                        const double u2 = draw(seed, step, (uint32_t)row, request, 1);
+                        const double target = u2 * total;
+                        double run = 0.0;
+                        int c = 0;
+                        for (; c < g.C - 1; c++) {
+                            if (target < run + cs[c]) break;
+                            run += cs[c];
+                        }
+                        target_s = target - run;
+                        cstar = c;
+                        mx_s = best.v;
+                        action = 2;
+                    }
+                }
+            }
+            if (debug) {
+                double *o = debug + (((uint64_t)b * g.R) + row) * 4;
+                for (int i = 0; i < 4; i++) o[i] = dbg[i];
+            }
+        }
+        __syncthreads();
+        if (action == 0) {
+            if (threadIdx.x == 0) accepted_s++;
+            __syncthreads();
+            continue;
+        }
+        if (action == 2) {
+            const int d = row < g.k ? drafts[(uint64_t)b * g.k + row] : -1;
+            const int j = scan_chunk(p, g, cstar, d, mx_s, inv_t, target_s, prefix, &pick);
+            if (threadIdx.x == 0) decided_next = j >= 0 ? j : best_s.i;
+        }
+        break;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t *o = result + (uint64_t)b * 4;
+        o[0] = accepted_s;
+        o[1] = decided_next;
+        o[2] = argmax0;
+        o[3] = 0;
+    }
+}
+
+Geo make_geo(const yuuka_accept_params &p) {
+    Geo g;
+    g.B = (int)p.batch;
+    g.k = (int)p.drafts;
+    g.R = g.k + 1;
+    g.V = (int)p.vocab;
+    g.stride = p.row_stride ? p.row_stride : p.vocab;
+    int c = (2048 + g.B * g.R - 1) / (g.B * g.R);
+    c = c < 1 ? 1 : (c > 256 ? 256 : c);
+    int L = (g.V + c - 1) / c;
+    L = (L + 3) & ~3;
+    g.L = L;
+    g.C = (g.V + L - 1) / L;
+    return g;
+}
+
+}  // namespace
+
+uint64_t accept_scratch_bytes(const yuuka_accept_params &p) {
+    const Geo g = make_geo(p);
+    const uint64_t n = (uint64_t)g.B * g.R * g.C;
+    return n * sizeof(Stat) + n * sizeof(double) + (uint64_t)g.B * g.R * sizeof(double) + 256;
+}
+
+hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int32_t *result,
+                                double *debug, const yuuka_accept_params &p, void *scratch,
+                                hipStream_t stream) {
+    const Geo g = make_geo(p);
+    const uint64_t n = (uint64_t)g.B * g.R * g.C;
+    auto *base = static_cast<uint8_t *>(scratch);
+    Stat *stats = reinterpret_cast<Stat *>(base);
+    double *sums = reinterpret_cast<double *>(base + ((n * sizeof(Stat) + 255) & ~255ull));
+    double *wdraft = sums + n;
+    const bool stochastic = p.mode == YUUKA_ACCEPT_STOCHASTIC && p.temperature > 0.0f && p.top_k != 1;
+    const double inv_t = stochastic ? 1.0 / (double)p.temperature : 0.0;
+    const dim3 grid((unsigned)g.C, (unsigned)g.R, (unsigned)g.B);
+    accept_stats_kernel<<<grid, 256, 0, stream>>>(logits, g, stats);
+    if (stochastic)
+        accept_weights_kernel<<<grid, 256, 0, stream>>>(logits, g, drafts, stats, inv_t, sums, wdraft);
+    accept_finalize_kernel<<<(unsigned)g.B, 256, 0, stream>>>(logits, g, drafts, stats, sums, wdraft,
+                                                             stochastic ? 1 : 0, inv_t, p.seed, p.step,
+                                                             p.request_base, result, debug);
+    return hipGetLastError();
+}
+
+}  // namespace yk

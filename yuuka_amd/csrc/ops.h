@@ -1,0 +1,22 @@
+// ops.h — validation and execution of the non-GEMM plan ops (norms, RoPE,
+// embedding, paged KV write, paged attention, recurrent chunk, elementwise).
+#pragma once
+
+#include "plan.h"
+
+namespace yk {
+
+// Validates a plan op other than LM_HEAD/GEMV_BATCH; *ws receives the
+// workspace bytes it needs. Unknown codes fail with YUUKA_ERR_UNSUPPORTED.
+yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws);
+yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx);
+// True when the op reads the execution position (graph capture then needs
+// the dynamic-parameter buffer).
+bool op_uses_position(const yuuka_op &op);
+
+// Elementwise launchers (k_ops.hip).
+hipError_t launch_copy_f32(float *dst, const float *src, uint64_t n, hipStream_t stream);
+hipError_t launch_silu_mul(const float *gate, const float *up, float *out, uint64_t n,
+                           hipStream_t stream);
+
+}  // namespace yk

@@ -1,0 +1,282 @@
+// plan.cpp — yuuka_plan_* and yuuka_graph_* (reference yuuka_hip.h:477-496,
+// bridge.cpp:3453-3870). Ops are validated and copied at add time; a rejected
+// op is not appended. Execution submits every op on the caller's stream.
+#include "plan.h"
+
+#include <algorithm>
+#include <cstring>
+#include <exception>
+#include <new>
+
+#include "ops.h"
+
+namespace yk {
+
+static bool buf_ok(const yuuka_buffer *b, uint64_t off, uint64_t bytes) {
+    return b != nullptr && off <= b->bytes && bytes <= b->bytes - off;
+}
+
+template <typename T>
+static T *at(const yuuka_op &op, int i) {
+    return reinterpret_cast<T *>(static_cast<uint8_t *>(op.buf[i]->ptr) + op.off[i]);
+}
+
+// ------------------------------------------------------------ validation
+
+struct Need {
+    uint64_t ws = 0;
+    uint32_t tickets = 0;
+};
+
+static yuuka_status validate(const yuuka_op &op, Need *need) {
+    switch (op.code) {
+    case YUUKA_OP_LM_HEAD:
+    case YUUKA_OP_GEMV_BATCH: {
+        // LM_HEAD: buf0 W, buf1 x, buf2 out; n={K,N,rows}; u0 dtype (reference :385-387).
+        // GEMV_BATCH (hip.go:492-520): buf0 W, buf1 x, buf2 out; n={K,N,batch}; u0 dtype.
+        for (int i = 0; i < 3; i++)
+            if (!op.buf[i]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify GEMM buffer %d is null", i);
+        const uint64_t K = op.n[0], N = op.n[1], rows = op.n[2];
+        yuuka_status st = check_verify_gemm(K, N, rows, op.u[0], 16);
+        if (st != YUUKA_OK) return st;
+        if (op.off[0] % 16 || op.off[1] % 16 || op.off[2] % 4)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify GEMM offsets must be 16-byte aligned");
+        if (!buf_ok(op.buf[0], op.off[0], row_bytes(op.u[0], K) * N))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify GEMM weight buffer is too small");
+        if (!buf_ok(op.buf[1], op.off[1], K * rows * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify GEMM input buffer is too small");
+        if (!buf_ok(op.buf[2], op.off[2], N * rows * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify GEMM output buffer is too small");
+        need->ws = verify_gemm_ws_bytes(K, N, rows);
+        need->tickets = verify_gemm_tickets(K, N, rows);
+        return YUUKA_OK;
+    }
+    default:
+        return validate_model_op(op, &need->ws);
+    }
+}
+
+static yuuka_status execute(const yuuka_op &op, const ExecCtx &ctx) {
+    switch (op.code) {
+    case YUUKA_OP_LM_HEAD:
+    case YUUKA_OP_GEMV_BATCH:
+        return run_verify_gemm(ctx.stream, at<const uint8_t>(op, 0), op.u[0], at<const float>(op, 1),
+                               at<float>(op, 2), op.n[0], op.n[1], op.n[2], ctx.ws, ctx.tickets);
+    default:
+        return execute_model_op(op, ctx);
+    }
+}
+
+static yuuka_status prepare(yuuka_plan *plan) {
+    if (plan->ws_bytes < plan->ws_need) {
+        if (plan->ws) (void)hipFree(plan->ws);
+        plan->ws = nullptr;
+        plan->ws_bytes = 0;
+        const uint64_t want = (plan->ws_need + 0xffffull) & ~0xffffull;
+        hipError_t err = hipMalloc(&plan->ws, want);
+        if (err != hipSuccess) return fail(YUUKA_ERR_ALLOCATION, "plan workspace: %s", hip_error(err));
+        plan->ws_bytes = want;
+    }
+    if (plan->tickets_len < plan->ticket_need + 1) {
+        if (plan->tickets) (void)hipFree(plan->tickets);
+        plan->tickets = nullptr;
+        const uint32_t want = plan->ticket_need + 64;
+        hipError_t err = hipMalloc(reinterpret_cast<void **>(&plan->tickets), (size_t)want * 4);
+        if (err == hipSuccess) err = hipMemset(plan->tickets, 0, (size_t)want * 4);
+        if (err != hipSuccess) return fail(YUUKA_ERR_ALLOCATION, "plan tickets: %s", hip_error(err));
+        plan->tickets_len = want;
+    }
+    return YUUKA_OK;
+}
+
+template <typename F>
+static yuuka_status guard(F &&f) {
+    try {
+        return f();
+    } catch (const std::bad_alloc &) {
+        return fail(YUUKA_ERR_ALLOCATION, "host allocation failed");
+    } catch (const std::exception &e) {
+        return fail(YUUKA_ERR_INTERNAL, "%s", e.what());
+    } catch (...) {
+        return fail(YUUKA_ERR_INTERNAL, "unknown exception");
+    }
+}
+
+static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token, uint32_t position,
+                            const int32_t *dyn, int run_tail, uint32_t *codes, uint64_t *times,
+                            uint64_t capacity, uint64_t *count) {
+    ExecCtx ctx{stream, token, position, dyn, plan->ws, plan->tickets};
+    uint64_t n = 0;
+    hipEvent_t a = nullptr, b = nullptr;
+    if (times) {
+        if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)
+            return fail(YUUKA_ERR_DEVICE, "profiling events");
+    }
+    yuuka_status st = YUUKA_OK;
+    for (const yuuka_op &op : plan->ops) {
+        if ((op.flags & YUUKA_OP_FLAG_TAIL) && !run_tail) continue;
+        for (int i = 0; i < 16; i++)
+            if (op.buf[i] && !op.buf[i]->ptr) {
+                st = fail(YUUKA_ERR_INVALID_ARGUMENT, "plan op %u has a freed buffer", op.code);
+                break;
+            }
+        if (st != YUUKA_OK) break;
+        if (times) (void)hipEventRecord(a, stream);
+        st = execute(op, ctx);
+        if (st != YUUKA_OK) break;
+        if (times) {
+            (void)hipEventRecord(b, stream);
+            (void)hipEventSynchronize(b);
+            float ms = 0.0f;
+            (void)hipEventElapsedTime(&ms, a, b);
+            if (n < capacity) {
+                codes[n] = op.code;
+                times[n] = (uint64_t)((double)ms * 1e6);
+            }
+        }
+        n++;
+    }
+    if (times) {
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+    }
+    if (count) *count = n;
+    return st;
+}
+
+}  // namespace yk
+
+using namespace yk;
+
+extern "C" {
+
+yuuka_status yuuka_plan_create(yuuka_device *dev, yuuka_plan **out) {
+    return guard([&]() -> yuuka_status {
+        if (!dev || !out) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null device or output");
+        auto *p = new yuuka_plan();
+        p->dev = dev;
+        *out = p;
+        return YUUKA_OK;
+    });
+}
+
+void yuuka_plan_destroy(yuuka_plan *plan) {
+    if (!plan) return;
+    (void)hipDeviceSynchronize();
+    if (plan->ws) (void)hipFree(plan->ws);
+    if (plan->tickets) (void)hipFree(plan->tickets);
+    delete plan;
+}
+
+yuuka_status yuuka_plan_add(yuuka_plan *plan, const yuuka_op *op) {
+    return guard([&]() -> yuuka_status {
+        if (!plan || !op) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null plan or op");
+        Need need;
+        yuuka_status st = validate(*op, &need);
+        if (st != YUUKA_OK) return st;
+        plan->ops.push_back(*op);
+        plan->ws_need = std::max(plan->ws_need, need.ws);
+        plan->ticket_need = std::max(plan->ticket_need, need.tickets);
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_plan_execute(yuuka_plan *plan, yuuka_stream *stream, int32_t token,
+                                uint32_t position, int run_tail, yuuka_event *completion) {
+    return guard([&]() -> yuuka_status {
+        if (!plan || !stream) return fail(YUUKA_ERR_INVALID_ARGUMENT, "plan or stream is null");
+        yuuka_status st = prepare(plan);
+        if (st != YUUKA_OK) return st;
+        st = run_ops(plan, stream->stream, token, position, nullptr, run_tail, nullptr, nullptr, 0, nullptr);
+        if (st != YUUKA_OK) return st;
+        hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "plan execute: %s", hip_error(err));
+        if (completion) {
+            err = hipEventRecord(completion->event, stream->stream);
+            if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "event record: %s", hip_error(err));
+        }
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_plan_execute_profiled(yuuka_plan *plan, yuuka_stream *stream, int32_t token,
+                                         uint32_t position, int run_tail, uint32_t *op_codes,
+                                         uint64_t *op_times_ns, uint64_t capacity,
+                                         uint64_t *op_count, yuuka_event *completion) {
+    return guard([&]() -> yuuka_status {
+        if (!plan || !stream || !op_codes || !op_times_ns || !op_count)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        yuuka_status st = prepare(plan);
+        if (st != YUUKA_OK) return st;
+        st = run_ops(plan, stream->stream, token, position, nullptr, run_tail, op_codes, op_times_ns,
+                     capacity, op_count);
+        if (st != YUUKA_OK) return st;
+        if (completion) {
+            hipError_t err = hipEventRecord(completion->event, stream->stream);
+            if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "event record: %s", hip_error(err));
+        }
+        return YUUKA_OK;
+    });
+}
+
+// Captures the plan into a HIP graph. Position-dependent ops read {token,
+// position} from `dynamic` (written by yuuka_dynamic_set) at replay time.
+yuuka_status yuuka_graph_create(yuuka_plan *plan, yuuka_stream *stream, yuuka_buffer *dynamic,
+                                int run_tail, yuuka_graph **out) {
+    return guard([&]() -> yuuka_status {
+        if (!plan || !stream || !out) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        *out = nullptr;
+        if (dynamic && dynamic->bytes < 8) return fail(YUUKA_ERR_INVALID_ARGUMENT, "dynamic buffer under 8 bytes");
+        for (const yuuka_op &op : plan->ops)
+            if (op_uses_position(op) && !dynamic)
+                return fail(YUUKA_ERR_UNSUPPORTED, "plan op %u needs a dynamic-parameter buffer", op.code);
+        yuuka_status st = prepare(plan);
+        if (st != YUUKA_OK) return st;
+        hipError_t err = hipStreamSynchronize(stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "pre-capture sync: %s", hip_error(err));
+        err = hipStreamBeginCapture(stream->stream, hipStreamCaptureModeThreadLocal);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "begin capture: %s", hip_error(err));
+        const int32_t *dyn = dynamic ? static_cast<const int32_t *>(dynamic->ptr) : nullptr;
+        st = run_ops(plan, stream->stream, 0, 0, dyn, run_tail, nullptr, nullptr, 0, nullptr);
+        hipGraph_t graph = nullptr;
+        err = hipStreamEndCapture(stream->stream, &graph);
+        if (st != YUUKA_OK) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return st;
+        }
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "end capture: %s", hip_error(err));
+        hipGraphExec_t exec = nullptr;
+        err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (err != hipSuccess) {
+            (void)hipGraphDestroy(graph);
+            return fail(YUUKA_ERR_DEVICE, "graph instantiate: %s", hip_error(err));
+        }
+        auto *g = new yuuka_graph();
+        g->graph = graph;
+        g->exec = exec;
+        *out = g;
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_graph_replay(yuuka_graph *graph, yuuka_stream *stream, yuuka_event *completion) {
+    return guard([&]() -> yuuka_status {
+        if (!graph || !stream) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        hipError_t err = hipGraphLaunch(graph->exec, stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "graph launch: %s", hip_error(err));
+        if (completion) {
+            err = hipEventRecord(completion->event, stream->stream);
+            if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "event record: %s", hip_error(err));
+        }
+        return YUUKA_OK;
+    });
+}
+
+void yuuka_graph_destroy(yuuka_graph *graph) {
+    if (!graph) return;
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
+}
+
+}  // extern "C"

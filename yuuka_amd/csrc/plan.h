@@ -1,0 +1,44 @@
+// plan.h — recorded op lists (yuuka_plan) and captured graphs (yuuka_graph).
+#pragma once
+
+#include <vector>
+
+#include "internal.h"
+
+struct yuuka_plan {
+    yuuka_device *dev = nullptr;
+    std::vector<yuuka_op> ops;
+    uint64_t ws_need = 0;      // bytes of op workspace (max over ops)
+    uint32_t ticket_need = 0;  // split-K tickets (max over ops)
+    void *ws = nullptr;
+    uint64_t ws_bytes = 0;
+    uint32_t *tickets = nullptr;
+    uint32_t tickets_len = 0;
+};
+
+struct yuuka_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace yk {
+
+yuuka_status check_verify_gemm(uint64_t n_in, uint64_t n_out, uint64_t rows, uint32_t dtype,
+                               uint64_t max_rows);
+yuuka_status run_verify_gemm(hipStream_t stream, const void *w, uint32_t dtype, const float *x,
+                             float *out, uint64_t n_in, uint64_t n_out, uint64_t rows, void *ws,
+                             uint32_t *tickets);
+uint64_t verify_gemm_ws_bytes(uint64_t n_in, uint64_t n_out, uint64_t rows);
+uint32_t verify_gemm_tickets(uint64_t n_in, uint64_t n_out, uint64_t rows);
+
+// Execution context handed to op executors.
+struct ExecCtx {
+    hipStream_t stream;
+    int32_t token;
+    uint32_t position;
+    const int32_t *dyn;  // device {token, position} for graph replay, or null
+    void *ws;
+    uint32_t *tickets;
+};
+
+}  // namespace yk
