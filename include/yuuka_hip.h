@@ -356,6 +356,27 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
                         yuuka_buffer * debug, const yuuka_accept_params * params,
                         yuuka_event * completion);
 
+/* Timing events (extension): an event created with timing enabled, recorded
+ * on a stream, and the elapsed milliseconds between two recorded events. */
+YUUKA_API yuuka_status yuuka_event_create_timed(yuuka_device * dev, yuuka_event ** out);
+YUUKA_API yuuka_status yuuka_event_record(yuuka_event * event, yuuka_stream * stream);
+YUUKA_API yuuka_status yuuka_event_elapsed_ms(yuuka_event * start, yuuka_event * end, float * ms);
+
+/* Split form of the verify GEMM. yuuka_quantize_activations writes the int8
+ * planes of x[rows, n_in] (rows <= 16) into xq, which must hold
+ * yuuka_quantized_bytes(n_in, rows) bytes; yuuka_gemm_quantized then computes
+ * out[rows, n_out] = W * x from them. One quantization can feed every GEMM
+ * that reads the same activation (q/k/v, gate/up). Workspace for split-K
+ * partial sums comes from the stream. */
+YUUKA_API uint64_t yuuka_quantized_bytes(uint64_t n_in, uint64_t rows);
+YUUKA_API yuuka_status yuuka_quantize_activations(yuuka_stream * stream, yuuka_buffer * xq,
+                        const yuuka_buffer * x, uint64_t n_in, uint64_t rows,
+                        yuuka_event * completion);
+YUUKA_API yuuka_status yuuka_gemm_quantized(yuuka_stream * stream, yuuka_buffer * out,
+                        const yuuka_buffer * xq, const yuuka_buffer * w, uint64_t n_in,
+                        uint64_t n_out, uint64_t rows, uint32_t dtype,
+                        yuuka_event * completion);
+
 #ifdef __cplusplus
 }
 #endif

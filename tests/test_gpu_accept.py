@@ -1,0 +1,120 @@
+"""GPU parity of the fused verify-accept kernel against the oracle restatement
+of engine/speculative.go:191-208 (greedy) and the repository's stochastic
+speculative-sampling definition. Every call goes through the C ABI."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from yuuka_amd import hip, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(dev, stream, logits, drafts, params):
+    B = params.batch
+    lb = dev.upload(logits.astype(np.float32))
+    db = dev.upload(np.asarray(drafts, np.int32).reshape(-1)) if params.drafts else None
+    rb = dev.alloc(B * 16)
+    dbg = dev.alloc(B * (params.drafts + 1) * 32)
+    hip.verify_accept(stream, lb, db, rb, params, debug=dbg)
+    stream.sync()
+    return rb.read(np.int32).reshape(B, 4), dbg.read(np.float64).reshape(B, params.drafts + 1, 4)
+
+
+def test_greedy_config1(dev, stream):
+    c = synth.config1(0)
+    p = hip.accept_params(hip.ACCEPT_GREEDY, 1, c["k"], c["V"])
+    res, _ = _run(dev, stream, c["logits"], c["drafts"], p)
+    a, nxt, rows = O.accept_greedy(c["logits"], c["drafts"])
+    assert (res[0, 0], res[0, 1], res[0, 2]) == (a, nxt, rows[0])
+
+
+@pytest.mark.parametrize("accept_len", [0, 1, 2, 3, 4])
+def test_greedy_forced_acceptance_lengths(dev, stream, accept_len):
+    rng = np.random.default_rng(accept_len)
+    k, V = 4, 151936
+    logits = rng.normal(0, 3, (k + 1, V)).astype(np.float32)
+    am = logits.argmax(axis=1)
+    drafts = [int(am[i]) if i < accept_len else int((am[i] + 1) % V) for i in range(k)]
+    p = hip.accept_params(hip.ACCEPT_GREEDY, 1, k, V)
+    res, _ = _run(dev, stream, logits, drafts, p)
+    a, nxt, _ = O.accept_greedy(logits, drafts)
+    assert a == accept_len and (res[0, 0], res[0, 1]) == (a, nxt)
+
+
+def test_greedy_ties_nan_inf(dev, stream):
+    V, k = 5000, 3
+    logits = np.zeros((k + 1, V), np.float32)
+    logits[0, [10, 4000, 4999]] = 7.0          # tie: lowest index wins
+    logits[1, 0] = np.nan                       # NaN at index 0 wins
+    logits[1, 5] = 100.0
+    logits[2, :] = -np.inf                      # all -inf: index 0
+    logits[2, 3] = np.nan
+    logits[3, 17] = np.inf
+    logits[3, 12] = np.nan
+    for drafts in ([10, 0, 0], [10, 5, 0], [4000, 0, 0], [10, 0, 1]):
+        p = hip.accept_params(hip.ACCEPT_GREEDY, 1, k, V)
+        res, _ = _run(dev, stream, logits, drafts, p)
+        a, nxt, rows = O.accept_greedy(logits, drafts)
+        assert (res[0, 0], res[0, 1]) == (a, nxt), drafts
+
+
+def test_greedy_batched_with_stride(dev, stream):
+    rng = np.random.default_rng(9)
+    B, k, V, stride = 3, 8, 32000, 32064
+    logits = rng.normal(0, 3, (B, k + 1, stride)).astype(np.float32)
+    drafts = np.zeros((B, k), np.int32)
+    for b in range(B):
+        am = logits[b, :, :V].argmax(axis=1)
+        drafts[b] = [am[i] if i < 2 * b + 1 else (am[i] + 3) % V for i in range(k)]
+    p = hip.accept_params(hip.ACCEPT_GREEDY, B, k, V, row_stride=stride)
+    res, _ = _run(dev, stream, logits, drafts, p)
+    for b in range(B):
+        a, nxt, _ = O.accept_greedy(np.ascontiguousarray(logits[b, :, :V]), drafts[b])
+        assert (res[b, 0], res[b, 1]) == (a, nxt)
+
+
+def test_stochastic_matches_oracle_decisions(dev, stream):
+    """Identical accept/reject decisions and resampled tokens whenever the
+    probabilities agree to tolerance; a mismatch is tolerated only at a
+    documented near-tie (|u - p| or the inverse-CDF boundary within 1e-9)."""
+    rng = np.random.default_rng(21)
+    k, V, T = 4, 151936, 0.8
+    mismatches = 0
+    for trial in range(24):
+        logits = rng.normal(0, 3, (k + 1, V)).astype(np.float32)
+        # make acceptance likely for a few rows: sharpen the draft's logit
+        drafts = rng.integers(0, V, k).astype(np.int32)
+        for i in range(k):
+            if rng.random() < 0.6:
+                logits[i, drafts[i]] = logits[i].max() + rng.uniform(-1, 3)
+        p = hip.accept_params(hip.ACCEPT_STOCHASTIC, 1, k, V, temperature=T, seed=1234, step=trial)
+        res, dbg = _run(dev, stream, logits, drafts, p)
+        a, nxt, pd, ua = O.accept_stochastic(logits, drafts, T, 1234, trial, 0)
+        for i in range(min(a, int(res[0, 0])) + 1):
+            if i < k:
+                assert dbg[0, i, 1] == ua[i]                    # same Philox draw, bit for bit
+                assert abs(dbg[0, i, 0] - pd[i]) <= 1e-9 * max(pd[i], 1e-300) + 1e-15
+        if (int(res[0, 0]), int(res[0, 1])) != (a, nxt):
+            i = min(a, int(res[0, 0]))
+            near = i < k and abs(ua[i] - pd[i]) < 1e-9
+            assert near, (trial, res[0], a, nxt)
+            mismatches += 1
+    assert mismatches <= 1
+
+
+def test_stochastic_zero_temperature_is_greedy(dev, stream):
+    c = synth.config1(3)
+    p = hip.accept_params(hip.ACCEPT_STOCHASTIC, 1, c["k"], c["V"], temperature=0.0)
+    res, _ = _run(dev, stream, c["logits"], c["drafts"], p)
+    a, nxt, _ = O.accept_greedy(c["logits"], c["drafts"])
+    assert (res[0, 0], res[0, 1]) == (a, nxt)
+
+
+def test_top_p_is_reported_unsupported(dev, stream):
+    c = synth.config1(0)
+    p = hip.accept_params(hip.ACCEPT_STOCHASTIC, 1, c["k"], c["V"], temperature=0.7, top_p=0.9)
+    with pytest.raises(hip.Unsupported):
+        _run(dev, stream, c["logits"], c["drafts"], p)

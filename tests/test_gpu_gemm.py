@@ -1,0 +1,128 @@
+"""GPU parity of the verify GEMM and the bit-exact dequantizer against the
+oracle (tensor/quant.go restatement). Every call goes through the C ABI."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from yuuka_amd import hip, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _dequant_gpu(dev, stream, dtype, w, rows, cols):
+    src = dev.upload(w)
+    dst = dev.alloc(rows * cols * 4)
+    hip.dequant_f32(stream, dst, src, cols, rows, dtype)
+    stream.sync()
+    return dst.read(np.float32).reshape(rows, cols)
+
+
+@pytest.mark.parametrize("dtype", [O.Q4_K, O.Q6_K])
+def test_dequant_bit_exact(dev, stream, dtype):
+    rng = np.random.default_rng(100 + dtype)
+    rows, cols = 37, 1024
+    w = synth.quant_matrix(rng, dtype, rows, cols)
+    got = _dequant_gpu(dev, stream, dtype, w, rows, cols)
+    want = O.dequantize(dtype, w, rows, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_bit_exact_subnormal_and_extreme_scales(dev, stream):
+    rng = np.random.default_rng(5)
+    rows, cols = 8, 512
+    w = synth.quant_matrix(rng, O.Q4_K, rows, cols).reshape(-1, 144)
+    w[0, 0:2] = [0x01, 0x00]          # smallest subnormal d
+    w[1, 0:4] = [0xFF, 0x7B, 0xFF, 0x7B]  # 65504 for d and dmin
+    w[2, 2:4] = [0x00, 0x80]          # dmin = -0
+    got = _dequant_gpu(dev, stream, O.Q4_K, w.reshape(-1), rows, cols)
+    want = O.dequantize(O.Q4_K, w.reshape(-1), rows, cols)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def _gemm(dev, stream, dtype, w, x, n, k, m):
+    wb = dev.upload(w)
+    xb = dev.upload(x.astype(np.float32))
+    ob = dev.alloc(m * n * 4)
+    hip.lm_head(stream, ob, xb, wb, k, n, m, dtype)
+    stream.sync()
+    return ob.read(np.float32).reshape(m, n)
+
+
+def _check(got, want):
+    # Error budget of the 16-bit activation quantization: well inside the
+    # north-star bar of 1e-2 relative, asserted separately below.
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2))) + 1e-30
+    err = np.abs(got.astype(np.float64) - want)
+    assert float(err.max()) <= 2e-4 * rms, (float(err.max()), rms)
+    assert np.all(err <= 1e-2 * (np.abs(want) + rms))
+
+
+CASES = [
+    (O.Q4_K, 9216, 2560, 5),   # configuration 1
+    (O.Q4_K, 1000, 512, 1),
+    (O.Q4_K, 100, 256, 3),
+    (O.Q4_K, 17, 9216, 8),
+    (O.Q4_K, 2560, 9216, 5),   # down projection shape (split K)
+    (O.Q4_K, 300, 1024, 9),
+    (O.Q4_K, 64, 2560, 16),
+    (O.Q6_K, 2000, 2560, 5),
+    (O.Q6_K, 77, 512, 1),
+    (O.Q6_K, 130, 1536, 12),
+    (O.Q6_K, 1024, 2048, 8),
+]
+
+
+@pytest.mark.parametrize("dtype,n,k,m", CASES)
+def test_verify_gemm_matches_oracle(dev, stream, dtype, n, k, m):
+    rng = np.random.default_rng(n * 7 + k + m + dtype)
+    w = synth.quant_matrix(rng, dtype, n, k)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    got = _gemm(dev, stream, dtype, w, x, n, k, m)
+    want = O.matmul(dtype, w, x, n, k)
+    _check(got, want)
+
+
+def test_verify_gemm_is_bitwise_repeatable(dev, stream):
+    rng = np.random.default_rng(1)
+    n, k, m = 2560, 9216, 5
+    w = synth.quant_matrix(rng, O.Q4_K, n, k)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    a = _gemm(dev, stream, O.Q4_K, w, x, n, k, m)
+    b = _gemm(dev, stream, O.Q4_K, w, x, n, k, m)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_verify_gemm_zero_and_outlier_rows(dev, stream):
+    rng = np.random.default_rng(2)
+    n, k, m = 256, 1024, 4
+    w = synth.quant_matrix(rng, O.Q4_K, n, k)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    x[1] = 0.0
+    x[2, 17] = 1.0e4
+    got = _gemm(dev, stream, O.Q4_K, w, x, n, k, m)
+    want = O.matmul(O.Q4_K, w, x, n, k)
+    assert np.all(got[1] == 0.0)
+    for r in (0, 2, 3):
+        _check(got[r:r + 1], want[r:r + 1])
+
+
+def test_plan_lm_head_matches_direct_and_rejects_bad_ops(dev, stream):
+    rng = np.random.default_rng(3)
+    n, k, m = 500, 2560, 5
+    w = synth.quant_matrix(rng, O.Q6_K, n, k)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    direct = _gemm(dev, stream, O.Q6_K, w, x, n, k, m)
+    wb, xb, ob = dev.upload(w), dev.upload(x), dev.alloc(m * n * 4)
+    plan = hip.Plan(dev)
+    plan.add(hip.OP["LM_HEAD"], bufs=[wb, xb, ob], n=[k, n, m], u=[O.Q6_K])
+    with pytest.raises(hip.Unsupported):
+        plan.add(hip.OP["LM_HEAD"], bufs=[wb, xb, ob], n=[k, n, m], u=[hip.Q8_0])
+    with pytest.raises(hip.HipError):
+        plan.add(hip.OP["LM_HEAD"], bufs=[wb, xb, ob], n=[k, n, 17], u=[O.Q6_K])
+    plan.execute(stream)
+    stream.sync()
+    got = ob.read(np.float32).reshape(m, n)
+    assert np.array_equal(got.view(np.uint32), direct.view(np.uint32))
+    plan.destroy()

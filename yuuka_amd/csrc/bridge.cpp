@@ -516,4 +516,80 @@ yuuka_status yuuka_verify_accept(yuuka_stream *stream, const yuuka_buffer *logit
     });
 }
 
+yuuka_status yuuka_event_create_timed(yuuka_device *dev, yuuka_event **out) {
+    return guard("event_create_timed", [&]() -> yuuka_status {
+        if (!dev || !out) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null device or output");
+        *out = nullptr;
+        auto *e = new yuuka_event();
+        hipError_t err = hipEventCreate(&e->event);
+        if (err != hipSuccess) {
+            delete e;
+            return fail(YUUKA_ERR_DEVICE, "event create: %s", hip_error(err));
+        }
+        *out = e;
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_event_record(yuuka_event *event, yuuka_stream *stream) {
+    return guard("event_record", [&]() -> yuuka_status {
+        if (!event || !stream) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null event or stream");
+        hipError_t err = hipEventRecord(event->event, stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "event record: %s", hip_error(err));
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_event_elapsed_ms(yuuka_event *start, yuuka_event *end, float *ms) {
+    return guard("event_elapsed", [&]() -> yuuka_status {
+        if (!start || !end || !ms) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        hipError_t err = hipEventElapsedTime(ms, start->event, end->event);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "event elapsed: %s", hip_error(err));
+        return YUUKA_OK;
+    });
+}
+
+uint64_t yuuka_quantized_bytes(uint64_t n_in, uint64_t rows) {
+    if (n_in == 0 || n_in % 256 || rows == 0 || rows > 16) return 0;
+    return gemm_plan(n_in, 1, rows).xq_bytes;
+}
+
+yuuka_status yuuka_quantize_activations(yuuka_stream *stream, yuuka_buffer *xq, const yuuka_buffer *x,
+                                        uint64_t n_in, uint64_t rows, yuuka_event *completion) {
+    return guard("quantize_activations", [&]() -> yuuka_status {
+        if (!stream || !xq || !x) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        const uint64_t need = yuuka_quantized_bytes(n_in, rows);
+        if (!need) return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid width %llu or rows %llu",
+                               (unsigned long long)n_in, (unsigned long long)rows);
+        if (!range_ok(xq, 0, need) || !range_ok(x, 0, n_in * rows * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "quantize buffers too small");
+        hipError_t err = launch_quantize_x(static_cast<const float *>(x->ptr), n_in, rows, xq->ptr, stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "quantize launch: %s", hip_error(err));
+        return record(stream, completion);
+    });
+}
+
+yuuka_status yuuka_gemm_quantized(yuuka_stream *stream, yuuka_buffer *out, const yuuka_buffer *xq,
+                                  const yuuka_buffer *w, uint64_t n_in, uint64_t n_out, uint64_t rows,
+                                  uint32_t dtype, yuuka_event *completion) {
+    return guard("gemm_quantized", [&]() -> yuuka_status {
+        if (!stream || !out || !xq || !w) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        yuuka_status st = check_verify_gemm(n_in, n_out, rows, dtype, 16);
+        if (st != YUUKA_OK) return st;
+        const GemmPlan plan = gemm_plan(n_in, n_out, rows);
+        if (!range_ok(w, 0, row_bytes(dtype, n_in) * n_out) || !range_ok(xq, 0, plan.xq_bytes) ||
+            !range_ok(out, 0, n_out * rows * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "gemm buffers too small");
+        st = ensure_scratch(stream, &stream->scratch, plan.part_bytes + 256);
+        if (st != YUUKA_OK) return st;
+        st = ensure_scratch(stream, &stream->tickets, (uint64_t)plan.tickets * 4 + 4);
+        if (st != YUUKA_OK) return st;
+        hipError_t err = launch_gemm_q(w->ptr, dtype, xq->ptr, static_cast<float *>(out->ptr), n_in, n_out,
+                                       rows, plan, stream->scratch.ptr,
+                                       static_cast<uint32_t *>(stream->tickets.ptr), stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "gemm launch: %s", hip_error(err));
+        return record(stream, completion);
+    });
+}
+
 }  // extern "C"

@@ -132,6 +132,12 @@ def _declare(L: C.CDLL) -> None:
         "yuuka_dequant_f16": (C.c_int, [vp, vp, vp, u64, u64, u32, vp]),
         "yuuka_verify_accept": (C.c_int, [vp, vp, u64, vp, u64, vp, u64, vp,
                                           C.POINTER(yuuka_accept_params), vp]),
+        "yuuka_event_create_timed": (C.c_int, [vp, C.POINTER(vp)]),
+        "yuuka_event_record": (C.c_int, [vp, vp]),
+        "yuuka_event_elapsed_ms": (C.c_int, [vp, vp, C.POINTER(C.c_float)]),
+        "yuuka_quantized_bytes": (u64, [u64, u64]),
+        "yuuka_quantize_activations": (C.c_int, [vp, vp, vp, u64, u64, vp]),
+        "yuuka_gemm_quantized": (C.c_int, [vp, vp, vp, vp, u64, u64, u64, u32, vp]),
         "yuuka_plan_create": (C.c_int, [vp, C.POINTER(vp)]),
         "yuuka_plan_destroy": (None, [vp]),
         "yuuka_plan_add": (C.c_int, [vp, C.POINTER(yuuka_op)]),
@@ -241,10 +247,19 @@ class Stream:
 
 
 class Event:
-    def __init__(self, dev: Device):
+    def __init__(self, dev: Device, timed: bool = False):
         p = C.c_void_p()
-        check(lib().yuuka_event_create(dev.ptr, C.byref(p)), "event_create")
+        fn = lib().yuuka_event_create_timed if timed else lib().yuuka_event_create
+        check(fn(dev.ptr, C.byref(p)), "event_create")
         self.ptr = p
+
+    def record(self, stream: "Stream") -> None:
+        check(lib().yuuka_event_record(self.ptr, stream.ptr), "event_record")
+
+    def elapsed_ms(self, start: "Event") -> float:
+        ms = C.c_float()
+        check(lib().yuuka_event_elapsed_ms(start.ptr, self.ptr, C.byref(ms)), "event_elapsed")
+        return float(ms.value)
 
     def wait(self) -> None:
         check(lib().yuuka_event_wait(self.ptr), "event_wait")
@@ -263,6 +278,21 @@ def lm_head(stream: Stream, out: Buffer, x: Buffer, w: Buffer, n_in: int, n_out:
             dtype: int, event: Event | None = None) -> None:
     check(lib().yuuka_lm_head(stream.ptr, out.ptr, x.ptr, w.ptr, n_in, n_out, rows, dtype, _p(event)),
           "lm_head")
+
+
+def quantized_bytes(n_in: int, rows: int) -> int:
+    return int(lib().yuuka_quantized_bytes(n_in, rows))
+
+
+def quantize_activations(stream: Stream, xq: Buffer, x: Buffer, n_in: int, rows: int) -> None:
+    check(lib().yuuka_quantize_activations(stream.ptr, xq.ptr, x.ptr, n_in, rows, None),
+          "quantize_activations")
+
+
+def gemm_quantized(stream: Stream, out: Buffer, xq: Buffer, w: Buffer, n_in: int, n_out: int,
+                   rows: int, dtype: int) -> None:
+    check(lib().yuuka_gemm_quantized(stream.ptr, out.ptr, xq.ptr, w.ptr, n_in, n_out, rows, dtype, None),
+          "gemm_quantized")
 
 
 def dequant_f32(stream: Stream, dst: Buffer, src: Buffer, n_in: int, n_out: int, dtype: int) -> None:
