@@ -25,6 +25,6 @@ def test_abi_versions_and_empty_error():
 
 
 def test_quantized_bytes_rules():
-    assert hip.quantized_bytes(2560, 5) == 64 + 2560 * 16 + (2560 // 32) * 64
-    assert hip.quantized_bytes(2560, 9) == 64 + 2 * (2560 * 16 + (2560 // 32) * 64)
+    assert hip.quantized_bytes(2560, 5) == 64 + 2560 * 17
+    assert hip.quantized_bytes(2560, 9) == 64 + 2 * 2560 * 17
     assert hip.quantized_bytes(100, 5) == 0 and hip.quantized_bytes(256, 17) == 0

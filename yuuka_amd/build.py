@@ -30,6 +30,8 @@ CFLAGS = [
     "-Wno-unused-function",
     "-fvisibility=hidden",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the GEMM epilogues read every result lane once.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

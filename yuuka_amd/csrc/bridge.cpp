@@ -110,7 +110,7 @@ yuuka_status check_verify_gemm(uint64_t n_in, uint64_t n_out, uint64_t rows, uin
 yuuka_status run_verify_gemm(hipStream_t stream, const void *w, uint32_t dtype, const float *x,
                              float *out, uint64_t n_in, uint64_t n_out, uint64_t rows, void *ws,
                              uint32_t *tickets) {
-    const GemmPlan plan = gemm_plan(n_in, n_out, rows);
+    const GemmPlan plan = gemm_plan(n_in, n_out, rows, dtype);
     uint8_t *xq = static_cast<uint8_t *>(ws);
     void *partials = xq + ((plan.xq_bytes + 255) & ~255ull);
     hipError_t err = launch_quantize_x(x, n_in, rows, xq, stream);
@@ -120,13 +120,13 @@ yuuka_status run_verify_gemm(hipStream_t stream, const void *w, uint32_t dtype, 
     return YUUKA_OK;
 }
 
-uint64_t verify_gemm_ws_bytes(uint64_t n_in, uint64_t n_out, uint64_t rows) {
-    const GemmPlan plan = gemm_plan(n_in, n_out, rows);
+uint64_t verify_gemm_ws_bytes(uint64_t n_in, uint64_t n_out, uint64_t rows, uint32_t dtype) {
+    const GemmPlan plan = gemm_plan(n_in, n_out, rows, dtype);
     return ((plan.xq_bytes + 255) & ~255ull) + plan.part_bytes + 256;
 }
 
-uint32_t verify_gemm_tickets(uint64_t n_in, uint64_t n_out, uint64_t rows) {
-    return gemm_plan(n_in, n_out, rows).tickets;
+uint32_t verify_gemm_tickets(uint64_t n_in, uint64_t n_out, uint64_t rows, uint32_t dtype) {
+    return gemm_plan(n_in, n_out, rows, dtype).tickets;
 }
 
 }  // namespace yk
@@ -376,9 +376,9 @@ static yuuka_status direct_gemm(const char *what, yuuka_stream *stream, yuuka_bu
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s input buffer is too small", what);
         if (!range_ok(out, 0, n_out * rows * 4))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s output buffer is too small", what);
-        st = ensure_scratch(stream, &stream->scratch, verify_gemm_ws_bytes(n_in, n_out, rows));
+        st = ensure_scratch(stream, &stream->scratch, verify_gemm_ws_bytes(n_in, n_out, rows, dtype));
         if (st != YUUKA_OK) return st;
-        st = ensure_scratch(stream, &stream->tickets, (uint64_t)verify_gemm_tickets(n_in, n_out, rows) * 4 + 4);
+        st = ensure_scratch(stream, &stream->tickets, (uint64_t)verify_gemm_tickets(n_in, n_out, rows, dtype) * 4 + 4);
         if (st != YUUKA_OK) return st;
         st = run_verify_gemm(stream->stream, w->ptr, dtype, static_cast<const float *>(x->ptr),
                              static_cast<float *>(out->ptr), n_in, n_out, rows, stream->scratch.ptr,
@@ -551,7 +551,7 @@ yuuka_status yuuka_event_elapsed_ms(yuuka_event *start, yuuka_event *end, float 
 
 uint64_t yuuka_quantized_bytes(uint64_t n_in, uint64_t rows) {
     if (n_in == 0 || n_in % 256 || rows == 0 || rows > 16) return 0;
-    return gemm_plan(n_in, 1, rows).xq_bytes;
+    return gemm_plan(n_in, 1, rows, YUUKA_DTYPE_Q4_K).xq_bytes;
 }
 
 yuuka_status yuuka_quantize_activations(yuuka_stream *stream, yuuka_buffer *xq, const yuuka_buffer *x,
@@ -576,7 +576,7 @@ yuuka_status yuuka_gemm_quantized(yuuka_stream *stream, yuuka_buffer *out, const
         if (!stream || !out || !xq || !w) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
         yuuka_status st = check_verify_gemm(n_in, n_out, rows, dtype, 16);
         if (st != YUUKA_OK) return st;
-        const GemmPlan plan = gemm_plan(n_in, n_out, rows);
+        const GemmPlan plan = gemm_plan(n_in, n_out, rows, dtype);
         if (!range_ok(w, 0, row_bytes(dtype, n_in) * n_out) || !range_ok(xq, 0, plan.xq_bytes) ||
             !range_ok(out, 0, n_out * rows * 4))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "gemm buffers too small");

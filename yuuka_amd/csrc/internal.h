@@ -63,7 +63,7 @@ struct GemmPlan {
     uint64_t part_bytes = 0;
     uint32_t tickets = 0;
 };
-GemmPlan gemm_plan(uint64_t n_in, uint64_t n_out, uint64_t rows);
+GemmPlan gemm_plan(uint64_t n_in, uint64_t n_out, uint64_t rows, uint32_t dtype);
 
 // Quantizes x[rows, n_in] (FP32) into the int8 hi/lo planes the GEMM reads.
 hipError_t launch_quantize_x(const float *x, uint64_t n_in, uint64_t rows, void *xq,

@@ -79,14 +79,6 @@ __global__ __launch_bounds__(256) void accept_stats_kernel(const float *__restri
     }
 }
 
-__device__ __forceinline__ Stat row_best(const Stat *stats, const Geo &g, int b, int row) {
-    const Stat *s = stats + ((uint64_t)b * g.R + row) * g.C;
-    Stat best{-INFINITY, INT_MAX};
-    for (int c = 0; c < g.C; c++)
-        if (beats(s[c].v, s[c].i, best.v, best.i)) best = s[c];
-    return best;
-}
-
 __device__ __forceinline__ double weight_of(float l, float mx, double inv_t) {
     if (!(l == l) || l == -INFINITY) return 0.0;  // NaN and -Inf are dropped
     return exp((double)(l - mx) * inv_t);
@@ -100,7 +92,19 @@ __global__ __launch_bounds__(256) void accept_weights_kernel(const float *__rest
     const int c = blockIdx.x, row = blockIdx.y, b = blockIdx.z;
     const float *p = row_ptr(logits, g, b, row);
     __shared__ float mx_s;
-    if (threadIdx.x == 0) mx_s = row_best(stats, g, b, row).v;
+    if (threadIdx.x < 64) {  // wave 0 reduces the row's chunk maxima
+        const Stat *st = stats + ((uint64_t)b * g.R + row) * g.C;
+        float bv = -INFINITY;
+        int bi = INT_MAX;
+        for (int cc = threadIdx.x; cc < g.C; cc += 64)
+            if (beats(st[cc].v, st[cc].i, bv, bi)) { bv = st[cc].v; bi = st[cc].i; }
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+        }
+        if (threadIdx.x == 0) mx_s = bv;
+    }
     __syncthreads();
     const float mx = mx_s;
     const int d = row < g.k ? drafts[(uint64_t)b * g.k + row] : -1;
@@ -207,9 +211,34 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
     __shared__ int decided_next;
     __shared__ int accepted_s;
     __shared__ int argmax0;
+    __shared__ Stat row_best_s[256];
+    __shared__ double row_rest_s[256];
     if (threadIdx.x == 0) {
         decided_next = -1;
         accepted_s = 0;
+    }
+    // Per-row maxima and weight sums: one wave per row, lanes over chunks.
+    {
+        const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+        for (int row = wave; row <= g.k; row += 4) {
+            const Stat *st = stats + ((uint64_t)b * g.R + row) * g.C;
+            Stat best{-INFINITY, INT_MAX};
+            double rest = 0.0;
+            for (int c = lane; c < g.C; c += 64) {
+                if (beats(st[c].v, st[c].i, best.v, best.i)) best = st[c];
+                if (stochastic) rest += sums[((uint64_t)b * g.R + row) * g.C + c];
+            }
+            for (int off = 32; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(best.v, off);
+                const int oi = __shfl_xor(best.i, off);
+                if (beats(ov, oi, best.v, best.i)) best = Stat{ov, oi};
+                rest += __shfl_xor(rest, off);
+            }
+            if (lane == 0) {
+                row_best_s[row] = best;
+                row_rest_s[row] = rest;
+            }
+        }
     }
     __syncthreads();
     for (int row = 0; row <= g.k; row++) {
@@ -220,7 +249,7 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
         __shared__ int cstar;
         __shared__ float mx_s;
         if (threadIdx.x == 0) {
-            Stat best = row_best(stats, g, b, row);
+            Stat best = row_best_s[row];
             if (p[0] != p[0]) best = Stat{p[0], 0};  // argmaxLogit keeps a NaN at index 0
             best_s = best;
             if (row == 0) argmax0 = best.i;
@@ -235,8 +264,7 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
                 }
             } else {
                 const double *cs = sums + ((uint64_t)b * g.R + row) * g.C;
-                double rest = 0.0;
-                for (int c = 0; c < g.C; c++) rest += cs[c];
+                const double rest = row_rest_s[row];
                 const double wd = (row < g.k && d >= 0 && d < g.V) ? wdraft[(uint64_t)b * g.R + row] : 0.0;
                 double total = rest + wd;
                 const bool onehot = !(total > 0.0) || isinf(total);

@@ -47,8 +47,8 @@ static yuuka_status validate(const yuuka_op &op, Need *need) {
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify GEMM input buffer is too small");
         if (!buf_ok(op.buf[2], op.off[2], N * rows * 4))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify GEMM output buffer is too small");
-        need->ws = verify_gemm_ws_bytes(K, N, rows);
-        need->tickets = verify_gemm_tickets(K, N, rows);
+        need->ws = verify_gemm_ws_bytes(K, N, rows, op.u[0]);
+        need->tickets = verify_gemm_tickets(K, N, rows, op.u[0]);
         return YUUKA_OK;
     }
     default:

@@ -28,8 +28,8 @@ yuuka_status check_verify_gemm(uint64_t n_in, uint64_t n_out, uint64_t rows, uin
 yuuka_status run_verify_gemm(hipStream_t stream, const void *w, uint32_t dtype, const float *x,
                              float *out, uint64_t n_in, uint64_t n_out, uint64_t rows, void *ws,
                              uint32_t *tickets);
-uint64_t verify_gemm_ws_bytes(uint64_t n_in, uint64_t n_out, uint64_t rows);
-uint32_t verify_gemm_tickets(uint64_t n_in, uint64_t n_out, uint64_t rows);
+uint64_t verify_gemm_ws_bytes(uint64_t n_in, uint64_t n_out, uint64_t rows, uint32_t dtype);
+uint32_t verify_gemm_tickets(uint64_t n_in, uint64_t n_out, uint64_t rows, uint32_t dtype);
 
 // Execution context handed to op executors.
 struct ExecCtx {
