@@ -356,6 +356,35 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
                         yuuka_buffer * debug, const yuuka_accept_params * params,
                         yuuka_event * completion);
 
+/* Extension plan ops (codes >= 64; layouts below).
+ *   QUANTIZE_X: buf0 FP32 x, buf1 quantized block (yuuka_quantized_bytes);
+ *               n={n_in, rows}
+ *   GEMM_Q:     buf0 packed W, buf1 quantized x, buf2 FP32 out, optional
+ *               buf3 FP32 residual (out = W x + residual; may alias out);
+ *               n={n_in, n_out, rows}; u0 = dtype (Q4_K / Q6_K)
+ *   ACCEPT:     buf0 logits, buf1 int32 drafts, buf2 int32 result [batch][4],
+ *               optional buf3 FP64 debug, optional buf4 uint64 step counter
+ *               (else n[5] is the step); n={batch, drafts, vocab, row_stride,
+ *               seed, step}; u0 mode, u1 top_k, u2 request_base;
+ *               f0 temperature, f1 top_p (yuuka_verify_accept semantics)
+ *   GDN_COMMIT: buf0 conv_state, buf1 matrix state, buf2 raw qkv rows,
+ *               buf3 conv outputs (RECURRENT_CHUNK buf11), buf4 alpha,
+ *               buf5 beta, buf6 dt, buf7 a, buf8 int32 acceptance result;
+ *               n={rows, groups, heads, state, conv_dim, inner}; u0 kernel.
+ *               Advances both states by result[0] + 1 rows (the accepted
+ *               prefix of a RECURRENT_CHUNK run with YUUKA_EXT_FLAG_DEFER).
+ *   ADVANCE:    buf0 dynamic buffer {token, position}, buf1 int32 result,
+ *               optional buf2 uint64 step counter; n0 = rows. position +=
+ *               result[0] + 1; step += 1.
+ * YUUKA_EXT_FLAG_DEFER on RECURRENT_CHUNK: compute the outputs of every row
+ * but leave both states untouched (verify mode; see GDN_COMMIT). */
+#define YUUKA_EXT_OP_QUANTIZE_X 64u
+#define YUUKA_EXT_OP_GEMM_Q 65u
+#define YUUKA_EXT_OP_ACCEPT 66u
+#define YUUKA_EXT_OP_GDN_COMMIT 67u
+#define YUUKA_EXT_OP_ADVANCE 68u
+#define YUUKA_EXT_FLAG_DEFER 0x100u
+
 /* Timing events (extension): an event created with timing enabled, recorded
  * on a stream, and the elapsed milliseconds between two recorded events. */
 YUUKA_API yuuka_status yuuka_event_create_timed(yuuka_device * dev, yuuka_event ** out);
@@ -376,6 +405,115 @@ YUUKA_API yuuka_status yuuka_gemm_quantized(yuuka_stream * stream, yuuka_buffer 
                         const yuuka_buffer * xq, const yuuka_buffer * w, uint64_t n_in,
                         uint64_t n_out, uint64_t rows, uint32_t dtype,
                         yuuka_event * completion);
+
+/* ----------------------------------------------------------------------
+ * qwen35 verify engine (extension). Host side of the speculative verify
+ * path in C++ over the plan API above: the counterpart of the reference's
+ * engine/gpu (runtime.go, session.go, plan.go) and engine/speculative.go.
+ * Every step is one captured HIP graph: embedding, 32 layers, LM head,
+ * fused acceptance, on-device GDN commit of the accepted prefix and
+ * position advance; the host only uploads k+1 token ids and reads 16 bytes.
+ * ---------------------------------------------------------------------- */
+typedef struct yuuka_q35 yuuka_q35;
+
+/* model/qwen35/config.go:18-45 plus session geometry. */
+typedef struct yuuka_q35_config {
+    int32_t n_layers, hidden, ffn, heads, kv_heads, head_dim, rope_dim, vocab;
+    int32_t conv_kernel, state_size, groups, rank, inner, full_interval;
+    double rope_base;
+    float eps;
+    int32_t capacity;    /* tokens of context */
+    int32_t block_size;  /* paged KV block (16) */
+    uint32_t kv_dtype;   /* YUUKA_DTYPE_F16 (reference default) or F32 */
+    int32_t max_rows;    /* largest row block of one step (<= 16) */
+} yuuka_q35_config;
+
+typedef struct yuuka_q35_tensor {
+    const void * data;   /* host bytes in GGUF packing */
+    uint64_t rows, cols;
+    uint32_t dtype;
+    uint32_t pad;
+} yuuka_q35_tensor;
+
+/* model/qwen35/load.go:104-212 tensor set of one layer (host pointers). */
+typedef struct yuuka_q35_layer_weights {
+    const float * attn_norm;
+    const float * post_norm;
+    yuuka_q35_tensor qkv, gate, out, beta, alpha;
+    const float * conv;      /* [conv_dim, kernel] */
+    const float * dt;
+    const float * a;
+    const float * ssm_norm;  /* [state_size] */
+    yuuka_q35_tensor q, k, v, o;
+    const float * q_norm;
+    const float * k_norm;
+    yuuka_q35_tensor ffn_gate, ffn_up, ffn_down;
+} yuuka_q35_layer_weights;
+
+typedef struct yuuka_q35_weights {
+    yuuka_q35_tensor embedding, output;
+    const float * output_norm;
+    const yuuka_q35_layer_weights * layers;
+} yuuka_q35_weights;
+
+/* Acceptance settings of one engine (yuuka_accept_params semantics). */
+typedef struct yuuka_q35_accept {
+    uint32_t mode;
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    uint64_t seed;
+} yuuka_q35_accept;
+
+YUUKA_API yuuka_status yuuka_q35_create(yuuka_device * dev, const yuuka_q35_config * cfg,
+                                        const yuuka_q35_weights * weights, yuuka_q35 ** out);
+YUUKA_API void yuuka_q35_destroy(yuuka_q35 * q);
+/* state.go:174-189: recurrent state cleared, position 0, step counter 0. */
+YUUKA_API yuuka_status yuuka_q35_reset(yuuka_q35 * q);
+YUUKA_API int32_t yuuka_q35_position(const yuuka_q35 * q);
+/* Processes n tokens (session.go:195-242 Prefill); *last_logits (may be
+ * NULL) receives the logits of the final token [vocab]. */
+YUUKA_API yuuka_status yuuka_q35_prefill(yuuka_q35 * q, const int32_t * tokens, int32_t n,
+                                         float * last_logits);
+/* One verify step over rows = k+1 tokens {pending, d1..dk}: logits of every
+ * row, acceptance on device, commit of the accepted prefix. result[4] =
+ * {accepted, next token, argmax row 0, 0}. Graph-captured per row count. */
+YUUKA_API yuuka_status yuuka_q35_verify(yuuka_q35 * q, const int32_t * tokens, int32_t rows,
+                                        const yuuka_q35_accept * accept, int32_t * result);
+/* Copies the logits rows of the last verify or prefill step [rows][vocab]. */
+YUUKA_API yuuka_status yuuka_q35_logits(yuuka_q35 * q, float * out, int32_t rows);
+/* state.go:211-263 Snapshot/Restore: all recurrent state (conv then matrix,
+ * per recurrent layer, little-endian FP32) and the position. */
+YUUKA_API uint64_t yuuka_q35_snapshot_bytes(const yuuka_q35 * q);
+YUUKA_API yuuka_status yuuka_q35_snapshot(yuuka_q35 * q, void * out, int32_t * position);
+YUUKA_API yuuka_status yuuka_q35_restore(yuuka_q35 * q, const void * data, uint64_t bytes, int32_t position);
+
+/* engine/speculative.go:13-34 options and :48-49 counters. */
+typedef struct yuuka_q35_generate_opts {
+    int32_t max_tokens;
+    int32_t max_draft;   /* k: drafts verified per step (<= max_rows - 1) */
+    int32_t min_match;   /* prompt-lookup suffix length (lookupDraft) */
+    int32_t stop_token;  /* < 0: none */
+    yuuka_q35_accept accept;
+} yuuka_q35_generate_opts;
+
+typedef struct yuuka_q35_generate_stats {
+    int32_t output_tokens;
+    int32_t steps;
+    int32_t draft_tokens;
+    int32_t accepted_draft;
+    double prefill_ms;
+    double decode_ms;
+} yuuka_q35_generate_stats;
+
+/* engine/speculative.go:68-261 generateSpeculative over this engine: prompt
+ * prefill, then per step prompt-lookup drafts (lookupDraft, padded to k with
+ * the pending token so every step verifies k+1 rows), one yuuka_q35_verify,
+ * emit accepted drafts and the correction/bonus token. out_tokens holds at
+ * least max_tokens entries. */
+YUUKA_API yuuka_status yuuka_q35_generate(yuuka_q35 * q, const int32_t * prompt, int32_t n_prompt,
+                                          const yuuka_q35_generate_opts * opts, int32_t * out_tokens,
+                                          yuuka_q35_generate_stats * stats);
 
 #ifdef __cplusplus
 }

@@ -163,3 +163,190 @@ def accept_stochastic(logits: np.ndarray, drafts, temperature: float, seed: int,
     lib().orc_accept_stochastic(_ptr(logits), V, k, _ptr(d), temperature, top_k, top_p, seed, step,
                                 request, C.byref(a), C.byref(nxt), _ptr(pd), _ptr(ua))
     return a.value, nxt.value, pd[:k].tolist(), ua[:k].tolist()
+
+
+# ------------------------------------------------------------ qwen35 model
+
+class orc_q35_config(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in (
+        "n_layers", "hidden", "ffn", "heads", "kv_heads", "head_dim", "rope_dim", "vocab", "conv_kernel",
+        "state_size", "groups", "rank", "inner", "full_interval", "n_experts", "n_experts_used", "expert_ffn",
+        "shared_ffn")] + [("rope_base", C.c_double), ("eps", C.c_float), ("matmul_workers", C.c_int32)]
+
+
+class orc_q35_matrix(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("rows", C.c_int64), ("cols", C.c_int64), ("dtype", C.c_uint32),
+                ("pad", C.c_uint32)]
+
+
+_FP = C.POINTER(C.c_float)
+
+
+class orc_q35_layer(C.Structure):
+    _fields_ = [("attn_norm", _FP), ("post_norm", _FP)] + \
+        [(n, orc_q35_matrix) for n in ("qkv", "gate", "out", "beta", "alpha")] + \
+        [(n, _FP) for n in ("conv", "dt", "a", "ssm_norm")] + \
+        [(n, orc_q35_matrix) for n in ("q", "k", "v", "o")] + \
+        [("q_norm", _FP), ("k_norm", _FP)] + \
+        [(n, orc_q35_matrix) for n in ("ffn_gate", "ffn_up", "ffn_down", "router")] + \
+        [("shared_gate_vec", _FP)] + \
+        [(n, orc_q35_matrix) for n in ("shared_gate", "shared_up", "shared_down", "gate_exps", "up_exps",
+                                       "down_exps")]
+
+
+class orc_q35_model(C.Structure):
+    _fields_ = [("cfg", orc_q35_config), ("embedding", orc_q35_matrix), ("output", orc_q35_matrix),
+                ("output_norm", _FP), ("layers", C.POINTER(orc_q35_layer))]
+
+
+def _declare_q35(L):
+    vp, i32 = C.c_void_p, C.c_int32
+    sig = {
+        "orc_q35_pool_new": (vp, [C.POINTER(orc_q35_config), i32, i32, i32]),
+        "orc_q35_pool_free": (None, [vp]),
+        "orc_q35_pool_data": (vp, [vp, i32, i32, C.POINTER(C.c_uint64)]),
+        "orc_q35_state_new": (vp, [C.POINTER(orc_q35_config), vp, vp, i32, i32]),
+        "orc_q35_state_free": (None, [vp]),
+        "orc_q35_state_reset": (None, [vp]),
+        "orc_q35_state_pos": (i32, [vp]),
+        "orc_q35_state_set_pos": (C.c_int, [vp, i32]),
+        "orc_q35_state_conv": (vp, [vp, i32]),
+        "orc_q35_state_matrix": (vp, [vp, i32]),
+        "orc_q35_snapshot_bytes": (C.c_uint64, [vp]),
+        "orc_q35_snapshot": (None, [vp, vp]),
+        "orc_q35_restore": (C.c_int, [vp, vp, C.c_uint64]),
+        "orc_q35_forward": (C.c_int, [C.POINTER(orc_q35_model), vp, vp, i32, i32, vp, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype, fn.argtypes = res, args
+
+
+def _mat(t):
+    if t is None:
+        return orc_q35_matrix()
+    return orc_q35_matrix(t["data"].ctypes.data_as(C.c_void_p), t["rows"], t["cols"], t["dtype"], 0)
+
+
+class Q35:
+    """The CPU reference decoder (model/qwen35 restatement) over host weights
+    from yuuka_amd.model.make_weights. format: 0 F32, 1 F16 KV rows."""
+
+    def __init__(self, cfg, weights, kv_format: int = 1, workers: int = 0):
+        L = lib()
+        if not hasattr(L, "_q35_declared"):
+            _declare_q35(L)
+            L._q35_declared = True
+        self.cfg = cfg
+        c = orc_q35_config()
+        for n in ("n_layers", "hidden", "ffn", "heads", "kv_heads", "head_dim", "rope_dim", "vocab",
+                  "conv_kernel", "state_size", "groups", "rank", "full_interval"):
+            setattr(c, n, getattr(cfg, n))
+        c.inner = cfg.inner
+        c.rope_base = cfg.rope_base
+        c.eps = cfg.eps
+        c.matmul_workers = workers
+        self.layers = (orc_q35_layer * cfg.n_layers)()
+        for i, Lw in enumerate(weights["layers"]):
+            s = self.layers[i]
+            s.attn_norm = Lw["attn_norm"].ctypes.data_as(_FP)
+            s.post_norm = Lw["post_norm"].ctypes.data_as(_FP)
+            for n in ("qkv", "gate", "out", "beta", "alpha", "q", "k", "v", "o", "ffn_gate", "ffn_up", "ffn_down"):
+                setattr(s, n, _mat(Lw.get(n)))
+            for n in ("conv", "dt", "a", "ssm_norm", "q_norm", "k_norm"):
+                if n in Lw:
+                    setattr(s, n, Lw[n].ctypes.data_as(_FP))
+        self.model = orc_q35_model(c, _mat(weights["embedding"]), _mat(weights["output"]),
+                                   weights["output_norm"].ctypes.data_as(_FP), self.layers)
+        self.weights = weights
+        blocks = (cfg.capacity + cfg.block_size - 1) // cfg.block_size
+        self.pool = L.orc_q35_pool_new(C.byref(self.model.cfg), blocks, cfg.block_size, kv_format)
+        self.table = np.arange(blocks, dtype=np.int32)
+        self.state = L.orc_q35_state_new(C.byref(self.model.cfg), self.pool, _ptr(self.table), blocks,
+                                         cfg.capacity)
+
+    def reset(self):
+        lib().orc_q35_state_reset(self.state)
+
+    @property
+    def position(self) -> int:
+        return int(lib().orc_q35_state_pos(self.state))
+
+    def forward(self, tokens, all_logits: bool = False) -> np.ndarray:
+        """Forward (last-token logits) or PrefillLogits (every row)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.zeros((t.size if all_logits else 1, self.cfg.vocab), np.float32)
+        rc = lib().orc_q35_forward(C.byref(self.model), self.state, _ptr(t), t.size, int(all_logits), _ptr(out),
+                                   None)
+        if rc != 0:
+            raise RuntimeError(f"orc_q35_forward failed ({rc})")
+        return out if all_logits else out[0]
+
+    def snapshot(self):
+        n = lib().orc_q35_snapshot_bytes(self.state)
+        buf = np.zeros(n, np.uint8)
+        lib().orc_q35_snapshot(self.state, _ptr(buf))
+        return buf, self.position
+
+    def restore(self, data, position):
+        if lib().orc_q35_restore(self.state, _ptr(data), data.nbytes) != 0:
+            raise ValueError("snapshot length mismatch")
+        lib().orc_q35_state_set_pos(self.state, position)
+
+    def close(self):
+        if self.state:
+            lib().orc_q35_state_free(self.state)
+            lib().orc_q35_pool_free(self.pool)
+            self.state = self.pool = None
+
+
+def generate_greedy_speculative(oracle: Q35, prompt, max_tokens: int, max_draft: int = 4, min_match: int = 2):
+    """engine/speculative.go:68-261 over the CPU decoder (greedy, no stop
+    tokens): prompt-lookup drafts, PrefillLogits verify, snapshot/restore and
+    replay on partial acceptance. Returns (tokens, draft_tokens, accepted)."""
+    oracle.reset()
+    logits = oracle.forward(prompt)
+    history = list(prompt)
+    out, drafts_n, acc_n = [], 0, 0
+    while len(out) < max_tokens:
+        limit = min(max_draft, max_tokens - len(out), oracle.cfg.capacity - len(history))
+        if limit <= 0:
+            break
+        draft = lookup_draft(history, limit, min_match)
+        if not draft:
+            tok = argmax(logits)
+            out.append(tok)
+            history.append(tok)
+            if len(out) >= max_tokens:
+                break
+            logits = oracle.forward([tok])
+            continue
+        snap, pos = oracle.snapshot()
+        cand = oracle.forward(draft, all_logits=True)
+        drafts_n += len(draft)
+        accepted, before, correction = 0, logits, -1
+        for i, d in enumerate(draft):
+            want = argmax(before)
+            if want == d:
+                accepted += 1
+                before = cand[i]
+                continue
+            correction = want
+            break
+        acc_n += accepted
+        if accepted == len(draft):
+            emitted, nxt = list(draft), cand[-1]
+        else:
+            oracle.restore(snap, pos)
+            replay = list(draft[:accepted]) + [correction]
+            nxt = oracle.forward(replay)
+            emitted = replay
+        for t in emitted:
+            out.append(t)
+            history.append(t)
+            if len(out) >= max_tokens:
+                break
+        if len(out) >= max_tokens:
+            break
+        logits = nxt
+    return out, drafts_n, acc_n

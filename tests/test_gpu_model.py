@@ -1,0 +1,158 @@
+"""GPU verify engine (yuuka_q35_*) against the CPU reference decoder (oracle
+restatement of model/qwen35 + engine/speculative.go) on the same seeded
+weights. Logit tolerance: |gpu - cpu| <= 1e-2 * (|cpu| + rms(row)) per
+element, the north-star bar; greedy tokens must be identical (a mismatch is
+only tolerated at a logged near-tie of the top two logits)."""
+from __future__ import annotations
+
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from yuuka_amd import model as Mdl
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    cfg = Mdl.TINY
+    w = Mdl.make_weights(cfg, seed=7)
+    return cfg, w
+
+
+def _close(got, want, what=""):
+    want = np.atleast_2d(want)
+    got = np.atleast_2d(got)
+    for r in range(want.shape[0]):
+        rms = float(np.sqrt(np.mean(want[r].astype(np.float64) ** 2)))
+        err = np.abs(got[r].astype(np.float64) - want[r])
+        assert np.all(err <= 1e-2 * (np.abs(want[r]) + rms)), (what, r, float(err.max()), rms)
+
+
+def _top2_gap(row):
+    s = np.sort(row)
+    return float(s[-1] - s[-2])
+
+
+def test_prefill_logits_match_oracle(dev, tiny):
+    cfg, w = tiny
+    eng = Mdl.Engine(dev, cfg, w)
+    orc = O.Q35(cfg, w)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, 37).astype(np.int32)
+    got = eng.prefill(prompt)
+    want = orc.forward(prompt)
+    _close(got, want, "prefill")
+    assert eng.position == orc.position == 37
+    eng.close()
+    orc.close()
+
+
+@pytest.mark.parametrize("kv", [Mdl.F16, Mdl.F32])
+def test_verify_rows_match_prefill_logits(dev, tiny, kv):
+    cfg, w = tiny
+    cfg = replace(cfg, kv_dtype=kv)
+    eng = Mdl.Engine(dev, cfg, w)
+    orc = O.Q35(cfg, w, kv_format=1 if kv == Mdl.F16 else 0)
+    rng = np.random.default_rng(2)
+    prompt = rng.integers(0, cfg.vocab, 20).astype(np.int32)
+    eng.prefill(prompt[:-1])
+    orc.forward(prompt[:-1])
+    rows = np.concatenate([prompt[-1:], rng.integers(0, cfg.vocab, 4)]).astype(np.int32)
+    res = eng.verify(rows)
+    got = eng.logits(5)
+    want = orc.forward(rows, all_logits=True)
+    _close(got, want, "verify")
+    a, nxt, am = O.accept_greedy(got, rows[1:])
+    assert (res[0], res[1]) == (a, nxt)
+    a_ref, nxt_ref, _ = O.accept_greedy(want, rows[1:])
+    if (a, nxt) != (a_ref, nxt_ref):
+        assert _top2_gap(want[min(a, a_ref)]) < 1e-2
+    eng.close()
+    orc.close()
+
+
+def test_partial_acceptance_commits_exact_prefix(dev, tiny):
+    """Drafts chosen so that exactly two are accepted: the device commit must
+    leave the state the oracle has after the accepted prefix, and the next
+    step's logits must agree."""
+    cfg, w = tiny
+    eng = Mdl.Engine(dev, cfg, w)
+    orc = O.Q35(cfg, w)
+    rng = np.random.default_rng(3)
+    prompt = rng.integers(0, cfg.vocab, 12).astype(np.int32)
+    eng.prefill(prompt[:-1])
+    orc.forward(prompt[:-1])
+    # true greedy continuation from the oracle (on a snapshot)
+    snap, pos = orc.snapshot()
+    seq = [int(prompt[-1])]
+    for _ in range(3):
+        lg = orc.forward([seq[-1]])
+        seq.append(O.argmax(lg))
+    orc.restore(snap, pos)
+    drafts = [seq[1], seq[2], (seq[3] + 1) % cfg.vocab, 5]
+    res = eng.verify(np.array([prompt[-1]] + drafts, np.int32))
+    assert res[0] == 2 and res[1] == seq[3]
+    orc.forward([prompt[-1], seq[1], seq[2]])
+    assert eng.position == orc.position
+    gs, gp = eng.snapshot()
+    cs, cp = orc.snapshot()
+    assert gp == cp
+    g32, c32 = gs.view(np.float32), cs.view(np.float32)
+    assert np.max(np.abs(g32 - c32)) <= 1e-3 * (np.max(np.abs(c32)) + 1e-6)
+    # next step continues from the committed state
+    nxt = [res[1], 1, 2, 3, 4]
+    eng.verify(np.array(nxt, np.int32))
+    _close(eng.logits(5), orc.forward(nxt, all_logits=True), "after commit")
+    eng.close()
+    orc.close()
+
+
+def test_snapshot_restore_roundtrip(dev, tiny):
+    cfg, w = tiny
+    eng = Mdl.Engine(dev, cfg, w)
+    prompt = np.arange(1, 30, dtype=np.int32)
+    eng.prefill(prompt)
+    snap, pos = eng.snapshot()
+    a = eng.verify(np.array([7, 8, 9], np.int32))
+    la = eng.logits(3)
+    eng.restore(snap, pos)
+    b = eng.verify(np.array([7, 8, 9], np.int32))
+    assert np.array_equal(a, b)
+    assert np.array_equal(la, eng.logits(3))
+    eng.close()
+
+
+def test_speculative_generate_equals_greedy(dev, tiny):
+    """engine/speculative_test.go:180-215 TestSpeculativeMatchesGreedy on the
+    device engine: speculative output equals plain greedy decoding."""
+    cfg, w = tiny
+    eng = Mdl.Engine(dev, cfg, w)
+    orc = O.Q35(cfg, w)
+    prompt = [5, 6, 7, 5, 6, 7, 5, 6, 9, 5, 6, 7]
+    toks, stats = eng.generate(prompt, 40, max_draft=4, min_match=2)
+    ref, _, _ = O.generate_greedy_speculative(orc, prompt, 40, 4, 2)
+    if toks != ref:
+        # only acceptable at a near-tie: find the first difference
+        i = next(j for j in range(min(len(toks), len(ref))) if toks[j] != ref[j])
+        orc.reset()
+        lg = orc.forward(prompt + ref[:i])
+        assert _top2_gap(lg) < 1e-2, (i, toks[i], ref[i])
+    assert stats.output_tokens == 40 and stats.steps <= 40
+    eng.close()
+    orc.close()
+
+
+def test_stochastic_generate_is_deterministic(dev, tiny):
+    cfg, w = tiny
+    eng = Mdl.Engine(dev, cfg, w)
+    acc = Mdl.accept_struct(mode=1, temperature=0.8, seed=11)
+    prompt = [3, 4, 5, 3, 4, 5, 3, 4]
+    a, _ = eng.generate(prompt, 24, accept=acc)
+    b, _ = eng.generate(prompt, 24, accept=acc)
+    assert a == b and len(a) == 24
+    c, _ = eng.generate(prompt, 24, accept=Mdl.accept_struct(mode=1, temperature=0.8, seed=12))
+    assert len(c) == 24
+    eng.close()

@@ -71,7 +71,8 @@ hipError_t launch_quantize_x(const float *x, uint64_t n_in, uint64_t rows, void 
 // out[rows, n_out] = W * x using the planes written by launch_quantize_x.
 hipError_t launch_gemm_q(const void *w, uint32_t dtype, const void *xq, float *out,
                          uint64_t n_in, uint64_t n_out, uint64_t rows, const GemmPlan &plan,
-                         void *partials, uint32_t *tickets, hipStream_t stream);
+                         void *partials, uint32_t *tickets, hipStream_t stream,
+                         const float *residual = nullptr);
 hipError_t launch_dequant_f32(const void *src, uint32_t dtype, float *dst, uint64_t n_in,
                               uint64_t n_out, hipStream_t stream);
 hipError_t launch_dequant_f16(const void *src, uint32_t dtype, uint16_t *dst, uint64_t n_in,
@@ -82,7 +83,7 @@ hipError_t launch_cast_f16(const float *src, uint16_t *dst, uint64_t n, hipStrea
 uint64_t accept_scratch_bytes(const yuuka_accept_params &p);
 hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int32_t *result,
                                 double *debug, const yuuka_accept_params &p, void *scratch,
-                                hipStream_t stream);
+                                hipStream_t stream, const uint64_t *step_dev = nullptr);
 
 // ----------------------------------------------------------- small ops
 hipError_t launch_add_f32(float *dst, const float *a, const float *b, uint64_t n,

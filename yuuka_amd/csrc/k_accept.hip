@@ -203,8 +203,10 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
     const float *__restrict__ logits, Geo g, const int32_t *__restrict__ drafts,
     const Stat *__restrict__ stats, const double *__restrict__ sums,
     const double *__restrict__ wdraft, int stochastic, double inv_t, uint64_t seed, uint64_t step,
-    uint32_t request_base, int32_t *__restrict__ result, double *__restrict__ debug) {
+    uint32_t request_base, int32_t *__restrict__ result, double *__restrict__ debug,
+    const uint64_t *__restrict__ step_dev) {
     const int b = blockIdx.x;
+    if (step_dev) step = *step_dev;
     const uint32_t request = request_base + (uint32_t)b;
     __shared__ double prefix[256];
     __shared__ int pick;
@@ -365,7 +367,7 @@ uint64_t accept_scratch_bytes(const yuuka_accept_params &p) {
 
 hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int32_t *result,
                                 double *debug, const yuuka_accept_params &p, void *scratch,
-                                hipStream_t stream) {
+                                hipStream_t stream, const uint64_t *step_dev) {
     const Geo g = make_geo(p);
     const uint64_t n = (uint64_t)g.B * g.R * g.C;
     auto *base = static_cast<uint8_t *>(scratch);
@@ -380,7 +382,7 @@ hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int3
         accept_weights_kernel<<<grid, 256, 0, stream>>>(logits, g, drafts, stats, inv_t, sums, wdraft);
     accept_finalize_kernel<<<(unsigned)g.B, 256, 0, stream>>>(logits, g, drafts, stats, sums, wdraft,
                                                              stochastic ? 1 : 0, inv_t, p.seed, p.step,
-                                                             p.request_base, result, debug);
+                                                             p.request_base, result, debug, step_dev);
     return hipGetLastError();
 }
 

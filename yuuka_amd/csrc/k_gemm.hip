@@ -169,9 +169,9 @@ template <int DT, int NA>
 __global__ __launch_bounds__(256) void gemm_kq_kernel(const uint8_t *__restrict__ w,
                                                       uint32_t w_bytes, uint32_t row_bytes,
                                                       const uint8_t *__restrict__ xq,
-                                                      float *__restrict__ out, int N, int K,
+                                                      float *out, int N, int K,
                                                       int M, int splits, int spw,
-                                                      float *__restrict__ partials) {
+                                                      float *__restrict__ partials, const float *residual) {
     using L = Layout<DT, NA>;
     constexpr int BB = Fmt<DT>::block;
     constexpr int CH = Fmt<DT>::chunks;
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(const uint8_t *__restrict_
         v *= xs[m];
         if (n < N) {
             if (splits == 1)
-                out[(size_t)m * N + n] = v;
+                out[(size_t)m * N + n] = residual ? v + residual[(size_t)m * N + n] : v;
             else
                 partials[((size_t)split * M + m) * N + n] = v;
         }
@@ -442,8 +442,9 @@ __device__ __forceinline__ int dot2(uint32_t a, uint32_t b, int c) {
 template <int NA>
 __global__ __launch_bounds__(256) void gemm_q4k_kernel(const uint8_t *__restrict__ w, uint32_t w_bytes,
                                                        uint32_t row_bytes, const uint8_t *__restrict__ xq,
-                                                       float *__restrict__ out, int N, int K, int M,
-                                                       int splits, int spw, float *__restrict__ partials) {
+                                                       float *out, int N, int K, int M,
+                                                       int splits, int spw, float *__restrict__ partials,
+                                                       const float *residual) {
     using L = L4<NA>;
     extern __shared__ __align__(16) uint8_t lds[];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -602,7 +603,7 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(const uint8_t *__restrict
     if (n < N) {
         for (int m = 0; m < M; m++) {
             const float v = (256.0f * red[m * 64 + lane] + red[(M + m) * 64 + lane]) * xs[m];
-            if (splits == 1) out[(size_t)m * N + n] = v;
+            if (splits == 1) out[(size_t)m * N + n] = residual ? v + residual[(size_t)m * N + n] : v;
             else partials[((size_t)split * M + m) * N + n] = v;
         }
     }
@@ -611,13 +612,13 @@ __global__ __launch_bounds__(256) void gemm_q4k_kernel(const uint8_t *__restrict
 
 // Sums the split-K partials in a fixed order (deterministic).
 __global__ __launch_bounds__(256) void reduce_splits_kernel(const float *__restrict__ partials,
-                                                            float *__restrict__ out, int splits,
-                                                            uint64_t count) {
+                                                            float *out, int splits,
+                                                            uint64_t count, const float *residual) {
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= count) return;
     float v = 0.0f;
     for (int s = 0; s < splits; s++) v += partials[(uint64_t)s * count + i];
-    out[i] = v;
+    out[i] = residual ? v + residual[i] : v;
 }
 
 // --------------------------------------------------------------------------
@@ -794,15 +795,16 @@ hipError_t launch_quantize_x(const float *x, uint64_t n_in, uint64_t rows, void 
 
 template <int DT, int NA>
 static void launch_one(dim3 grid, hipStream_t stream, const uint8_t *wp, uint64_t wbytes, uint64_t rb,
-                       const uint8_t *xp, float *dst, int N, int K, int M, const GemmPlan &plan, float *pp) {
+                       const uint8_t *xp, float *dst, int N, int K, int M, const GemmPlan &plan, float *pp,
+                       const float *res) {
     const size_t lds = 4 * Layout<DT, NA>::WAVE_BYTES + 16;
     gemm_kq_kernel<DT, NA><<<grid, 256, lds, stream>>>(wp, (uint32_t)wbytes, (uint32_t)rb, xp, dst, N, K, M,
-                                                       plan.splits, plan.sb_per_wave, pp);
+                                                       plan.splits, plan.sb_per_wave, pp, res);
 }
 
 hipError_t launch_gemm_q(const void *w, uint32_t dtype, const void *xq, float *out, uint64_t n_in,
                          uint64_t n_out, uint64_t rows, const GemmPlan &plan, void *partials,
-                         uint32_t *tickets, hipStream_t stream) {
+                         uint32_t *tickets, hipStream_t stream, const float *residual) {
     (void)tickets;
     const uint64_t rb = row_bytes(dtype, n_in);
     const uint64_t wbytes = rb * n_out;
@@ -815,16 +817,16 @@ hipError_t launch_gemm_q(const void *w, uint32_t dtype, const void *xq, float *o
     if (dtype == YUUKA_DTYPE_Q4_K) {
         const dim3 grid((unsigned)(((n_out + 255) / 256) * plan.splits));
         if (rows <= 8)
-            gemm_q4k_kernel<1><<<grid, 256, L4<1>::TOTAL, stream>>>(wp, (uint32_t)wbytes, (uint32_t)rb, xp, out, N, K, M, plan.splits, plan.sb_per_wave, pp);
+            gemm_q4k_kernel<1><<<grid, 256, L4<1>::TOTAL, stream>>>(wp, (uint32_t)wbytes, (uint32_t)rb, xp, out, N, K, M, plan.splits, plan.sb_per_wave, pp, residual);
         else
-            gemm_q4k_kernel<2><<<grid, 256, L4<2>::TOTAL, stream>>>(wp, (uint32_t)wbytes, (uint32_t)rb, xp, out, N, K, M, plan.splits, plan.sb_per_wave, pp);
+            gemm_q4k_kernel<2><<<grid, 256, L4<2>::TOTAL, stream>>>(wp, (uint32_t)wbytes, (uint32_t)rb, xp, out, N, K, M, plan.splits, plan.sb_per_wave, pp, residual);
     } else {
-        if (rows <= 8) launch_one<kQ6K, 1>(grid, stream, wp, wbytes, rb, xp, out, N, K, M, plan, pp);
-        else launch_one<kQ6K, 2>(grid, stream, wp, wbytes, rb, xp, out, N, K, M, plan, pp);
+        if (rows <= 8) launch_one<kQ6K, 1>(grid, stream, wp, wbytes, rb, xp, out, N, K, M, plan, pp, residual);
+        else launch_one<kQ6K, 2>(grid, stream, wp, wbytes, rb, xp, out, N, K, M, plan, pp, residual);
     }
     if (plan.splits > 1) {
         const uint64_t count = rows * n_out;
-        reduce_splits_kernel<<<(unsigned)((count + 255) / 256), 256, 0, stream>>>(pp, out, plan.splits, count);
+        reduce_splits_kernel<<<(unsigned)((count + 255) / 256), 256, 0, stream>>>(pp, out, plan.splits, count, residual);
     }
     return hipGetLastError();
 }

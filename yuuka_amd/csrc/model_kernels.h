@@ -1,0 +1,60 @@
+// model_kernels.h — argument blocks and launchers of k_model.hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+
+#include "../../include/yuuka_hip.h"
+
+namespace yk {
+
+// Position source: a device int (graph replay / on-device advance) or the
+// host value passed at submission.
+struct ModelDyn {
+    int32_t *pos_dev;
+    int32_t pos;
+};
+
+struct AttnArgs {
+    int kv_heads, heads, head_dim, kv_dim, rows, displacement, block_size, capacity;
+    uint32_t fmt;  // 0 F32, 1 F16 KV rows
+    int gated;     // 1: query rows hold [q | gate] per head (qwen35)
+    float scale;
+};
+
+struct GdnArgs {
+    int rows, groups, rank, state, conv_dim, inner, kernel;
+    float eps, q_scale;
+};
+
+hipError_t launch_embedding(const void *table, uint32_t dtype, uint64_t row_bytes, const int32_t *tokens, int vocab,
+                            int cols, int rows, float *out, hipStream_t s);
+hipError_t launch_rmsnorm_rows(const float *src, const float *w, float *dst, int cols, int rows, uint64_t src_stride,
+                               uint64_t dst_stride, float eps, hipStream_t s);
+hipError_t launch_rmsnorm_heads(const float *src, const float *w, float *dst, int size, int heads, int stride, int rows,
+                                float eps, hipStream_t s);
+hipError_t launch_rope(float *data, int heads, int stride, int rot_dim, int rows, uint64_t row_stride, double base,
+                       const ModelDyn &dyn, int displacement, hipStream_t s);
+hipError_t launch_kv_write(const float *k, const float *v, void *kpool, void *vpool, const int32_t *table, int kv_dim,
+                           int rows, int block_size, uint32_t fmt, const ModelDyn &dyn, int displacement,
+                           hipStream_t s);
+uint64_t attention_scratch_bytes(const AttnArgs &a);
+// max_pos_hint: largest row position the call can see (host-known), or -1.
+hipError_t launch_attention(const float *q, const void *kpool, const void *vpool, const int32_t *table, float *out,
+                            const AttnArgs &a, void *scratch, const ModelDyn &dyn, int max_pos_hint, hipStream_t s);
+hipError_t launch_gdn_conv(const float *conv_state, const float *qkv, const float *w, float *out, const GdnArgs &g,
+                           hipStream_t s);
+// mode 0: verify (outputs, state untouched); mode 1: commit accepted rows.
+hipError_t launch_gdn_scan(float *state, const float *conv, const float *alpha, const float *beta, const float *dt,
+                           const float *a, float *out, const GdnArgs &g, int mode, const int32_t *accept_result,
+                           hipStream_t s);
+hipError_t launch_gdn_norm_gate(const float *raw, const float *z, const float *norm, float *out, const GdnArgs &g,
+                                hipStream_t s);
+hipError_t launch_gdn_conv_commit(float *conv_state, const float *qkv, const GdnArgs &g, const int32_t *accept_result,
+                                  hipStream_t s);
+hipError_t launch_advance(const ModelDyn &dyn, const int32_t *accept_result, int rows, uint64_t *step,
+                          hipStream_t s);
+
+}  // namespace yk

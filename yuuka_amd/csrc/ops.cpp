@@ -1,7 +1,10 @@
-// ops.cpp — plan-op validation and dispatch for the non-GEMM ops. Buffer
+// ops.cpp — plan-op validation and dispatch for the non-LM_HEAD ops. Buffer
 // layouts follow the reference header comments (yuuka_hip.h:336-476) and the
-// Go builders (backend/hip/hip.go).
+// Go builders in backend/hip/hip.go (cited per op); extension ops are
+// documented in include/yuuka_hip.h.
 #include "ops.h"
+
+#include "model_kernels.h"
 
 namespace yk {
 
@@ -11,7 +14,57 @@ static bool buf_ok(const yuuka_buffer *b, uint64_t off, uint64_t bytes) {
 
 template <typename T>
 static T *at(const yuuka_op &op, int i) {
-    return reinterpret_cast<T *>(static_cast<uint8_t *>(op.buf[i]->ptr) + op.off[i]);
+    return op.buf[i] ? reinterpret_cast<T *>(static_cast<uint8_t *>(op.buf[i]->ptr) + op.off[i]) : nullptr;
+}
+
+static ModelDyn dyn_of(const ExecCtx &ctx) {
+    return ModelDyn{ctx.dyn ? const_cast<int32_t *>(ctx.dyn) + 1 : nullptr, (int32_t)ctx.position};
+}
+
+static uint32_t kv_fmt(uint32_t dtype, bool *ok) {
+    *ok = dtype == YUUKA_DTYPE_F32 || dtype == YUUKA_DTYPE_F16;
+    return dtype == YUUKA_DTYPE_F16 ? 1u : 0u;
+}
+
+static AttnArgs attn_args(const yuuka_op &op) {
+    AttnArgs a;
+    a.kv_heads = (int)op.n[0];
+    a.heads = (int)op.n[1];
+    a.head_dim = (int)op.n[2];
+    a.kv_dim = (int)op.n[3];
+    a.rows = (int)op.n[4];
+    a.displacement = (int)op.n[5];
+    a.block_size = (int)op.u[0];
+    a.capacity = (int)op.u[1];
+    bool ok;
+    a.fmt = kv_fmt(op.u[2], &ok);
+    a.gated = op.u[3] == 0;
+    a.scale = op.f[0];
+    return a;
+}
+
+static GdnArgs gdn_args(const yuuka_op &op) {
+    GdnArgs g;
+    g.rows = (int)op.n[0];
+    g.groups = (int)op.n[1];
+    g.rank = (int)op.n[2];
+    g.state = (int)op.n[3];
+    g.conv_dim = (int)op.n[4];
+    g.inner = (int)op.n[5];
+    g.kernel = (int)op.u[0];
+    g.eps = op.f[0];
+    g.q_scale = op.f[1];
+    return g;
+}
+
+static yuuka_status check_gdn(const GdnArgs &g, const char *what) {
+    if (g.rows <= 0 || g.rows > 64 || g.groups <= 0 || g.rank <= 0 || g.kernel < 2 || g.kernel > 8)
+        return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s: invalid rows/groups/heads/kernel", what);
+    if (g.state != 128)
+        return fail(YUUKA_ERR_UNSUPPORTED, "%s: state size %d (only 128 is served)", what, g.state);
+    if (g.conv_dim != 2 * g.groups * g.state + g.inner || g.inner != g.rank * g.state || g.conv_dim % 128)
+        return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s: inconsistent conv/inner widths", what);
+    return YUUKA_OK;
 }
 
 bool op_uses_position(const yuuka_op &op) {
@@ -48,6 +101,149 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid SILU_MUL buffers or count");
         return YUUKA_OK;
     }
+    case YUUKA_OP_EMBEDDING_BATCH: {  // hip.go:1936-1960
+        const uint64_t cols = op.n[0], rows = op.n[1], rb = op.n[2], vocab = op.n[3];
+        const uint32_t dt = op.u[0];
+        if (dt != YUUKA_DTYPE_F32 && dt != YUUKA_DTYPE_F16 && dt != YUUKA_DTYPE_Q8_0 && dt != YUUKA_DTYPE_Q4_K &&
+            dt != YUUKA_DTYPE_Q6_K)
+            return fail(YUUKA_ERR_UNSUPPORTED, "embedding dtype %u", dt);
+        if (!cols || !rows || !vocab || row_bytes(dt, cols) != rb)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid embedding shape");
+        if (!buf_ok(op.buf[0], op.off[0], rb * vocab) || !buf_ok(op.buf[1], op.off[1], cols * rows * 4) ||
+            !buf_ok(op.buf[2], op.off[2], rows * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "embedding buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_RMSNORM_BATCH: {  // hip.go:1320-1340
+        const uint64_t cols = op.n[0], rows = op.n[1], ss = op.n[2], ds = op.n[3];
+        if (!cols || !rows || ss < cols || ds < cols)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid batch RMSNorm dimensions");
+        if (!buf_ok(op.buf[0], op.off[0], ((rows - 1) * ss + cols) * 4) || !buf_ok(op.buf[1], op.off[1], cols * 4) ||
+            !buf_ok(op.buf[2], op.off[2], ((rows - 1) * ds + cols) * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "batch RMSNorm buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_RMSNORM_HEADS_BATCH: {  // hip.go:1343-1366
+        const uint64_t size = op.n[0], heads = op.n[1], stride = op.n[2], rows = op.n[3];
+        if (!size || !heads || !rows || stride < size)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid batch head RMSNorm dimensions");
+        const uint64_t span = (rows * heads - 1) * stride + size;
+        if (!buf_ok(op.buf[0], op.off[0], span * 4) || !buf_ok(op.buf[1], op.off[1], size * 4) ||
+            !buf_ok(op.buf[2], op.off[2], span * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "batch head RMSNorm buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_ROPE_BATCH: {  // hip.go:1376-1399
+        const uint64_t heads = op.n[0], stride = op.n[1], hd = op.n[2], rot = op.n[3], rows = op.n[4],
+                       rs = op.n[5];
+        if (!rows || !heads || !rot || rot % 2 || rot > hd || stride < hd || rs < heads * stride)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid batch RoPE dimensions");
+        if (!buf_ok(op.buf[0], op.off[0], ((rows - 1) * rs + (heads - 1) * stride + hd) * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "batch RoPE buffer too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_KV_WRITE_BATCH_PAGED: {  // hip.go:1488-1520
+        const uint64_t kv_dim = op.n[0], rows = op.n[1];
+        const uint32_t bs = op.u[0], cap = op.u[1];
+        bool ok;
+        kv_fmt(op.u[2], &ok);
+        if (!ok) return fail(YUUKA_ERR_UNSUPPORTED, "KV pool dtype %u (F32 and F16 are served)", op.u[2]);
+        if (!kv_dim || !rows || !bs || cap < rows || bs > cap)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid paged KV write dimensions");
+        const uint64_t blocks = (cap + bs - 1) / bs;
+        if (!buf_ok(op.buf[0], op.off[0], rows * kv_dim * 4) || !buf_ok(op.buf[1], op.off[1], rows * kv_dim * 4) ||
+            !op.buf[2] || !op.buf[3] || !buf_ok(op.buf[4], op.off[4], blocks * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "paged KV write buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_ATTENTION_PREFILL_PAGED: {  // hip.go:1787-1835
+        const AttnArgs a = attn_args(op);
+        bool ok;
+        kv_fmt(op.u[2], &ok);
+        if (!ok) return fail(YUUKA_ERR_UNSUPPORTED, "KV pool dtype %u (F32 and F16 are served)", op.u[2]);
+        if (a.rows <= 0 || a.rows > 16 || a.heads <= 0 || a.kv_heads <= 0 || a.heads % a.kv_heads ||
+            a.kv_dim != a.kv_heads * a.head_dim || a.block_size <= 0 || a.capacity < a.rows)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid paged attention dimensions");
+        if (a.head_dim % 64 || a.head_dim > 256)
+            return fail(YUUKA_ERR_UNSUPPORTED, "attention head dimension %d", a.head_dim);
+        const int qs = a.gated ? 2 * a.head_dim : a.head_dim;
+        const uint64_t blocks = ((uint64_t)a.capacity + a.block_size - 1) / a.block_size;
+        if (!buf_ok(op.buf[0], op.off[0], (uint64_t)a.rows * a.heads * qs * 4) || !op.buf[1] || !op.buf[2] ||
+            !buf_ok(op.buf[3], op.off[3], (uint64_t)a.rows * a.heads * a.head_dim * 4) ||
+            !buf_ok(op.buf[4], op.off[4], blocks * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "paged attention buffers too small");
+        *ws = attention_scratch_bytes(a);
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_RECURRENT_CHUNK: {  // hip.go:1874-1934
+        const GdnArgs g = gdn_args(op);
+        yuuka_status st = check_gdn(g, "recurrent chunk");
+        if (st != YUUKA_OK) return st;
+        for (int i = 0; i < 12; i++)
+            if (!op.buf[i]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "recurrent chunk buffer %d is null", i);
+        const uint64_t R = (uint64_t)g.rows;
+        if (!buf_ok(op.buf[0], op.off[0], (uint64_t)(g.kernel - 1) * g.conv_dim * 4) ||
+            !buf_ok(op.buf[1], op.off[1], (uint64_t)g.rank * g.state * g.state * 4) ||
+            !buf_ok(op.buf[2], op.off[2], R * g.conv_dim * 4) || !buf_ok(op.buf[3], op.off[3], R * g.inner * 4) ||
+            !buf_ok(op.buf[4], op.off[4], R * g.rank * 4) || !buf_ok(op.buf[5], op.off[5], R * g.rank * 4) ||
+            !buf_ok(op.buf[10], op.off[10], R * g.inner * 4) || !buf_ok(op.buf[11], op.off[11], R * g.conv_dim * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "recurrent chunk buffers too small");
+        *ws = R * g.inner * 4;  // raw per-head outputs before the gated norm
+        return YUUKA_OK;
+    }
+    case YUUKA_EXT_OP_QUANTIZE_X: {
+        const uint64_t K = op.n[0], rows = op.n[1];
+        const uint64_t need = rows >= 1 && rows <= 16 && K && K % 256 == 0 ? gemm_plan(K, 1, rows, YUUKA_DTYPE_Q4_K).xq_bytes : 0;
+        if (!need || op.off[0] % 16 || op.off[1] % 16 || !buf_ok(op.buf[0], op.off[0], K * rows * 4) ||
+            !buf_ok(op.buf[1], op.off[1], need))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid QUANTIZE_X shape or buffers");
+        return YUUKA_OK;
+    }
+    case YUUKA_EXT_OP_GEMM_Q: {
+        const uint64_t K = op.n[0], N = op.n[1], rows = op.n[2];
+        yuuka_status st = check_verify_gemm(K, N, rows, op.u[0], 16);
+        if (st != YUUKA_OK) return st;
+        const GemmPlan p = gemm_plan(K, N, rows, op.u[0]);
+        if (op.off[0] % 16 || op.off[1] % 16 || !buf_ok(op.buf[0], op.off[0], row_bytes(op.u[0], K) * N) ||
+            !buf_ok(op.buf[1], op.off[1], p.xq_bytes) || !buf_ok(op.buf[2], op.off[2], N * rows * 4) ||
+            (op.buf[3] && !buf_ok(op.buf[3], op.off[3], N * rows * 4)))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid GEMM_Q buffers");
+        *ws = p.part_bytes + 256;
+        return YUUKA_OK;
+    }
+    case YUUKA_EXT_OP_ACCEPT: {
+        yuuka_accept_params p{};
+        p.mode = op.u[0];
+        p.batch = (uint32_t)op.n[0];
+        p.drafts = (uint32_t)op.n[1];
+        p.vocab = (uint32_t)op.n[2];
+        p.row_stride = op.n[3];
+        if ((p.mode != YUUKA_ACCEPT_GREEDY && p.mode != YUUKA_ACCEPT_STOCHASTIC) || !p.batch || !p.vocab ||
+            p.drafts > 255)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid ACCEPT parameters");
+        if (p.mode == YUUKA_ACCEPT_STOCHASTIC && op.f[0] > 0.0f && op.u[1] != 1 && (op.u[1] > 1 || op.f[1] < 1.0f))
+            return fail(YUUKA_ERR_UNSUPPORTED, "top-k/top-p truncation is not implemented");
+        const uint64_t stride = p.row_stride ? p.row_stride : p.vocab;
+        const uint64_t rows = (uint64_t)p.batch * (p.drafts + 1);
+        if (!buf_ok(op.buf[0], op.off[0], ((rows - 1) * stride + p.vocab) * 4) ||
+            (p.drafts && !buf_ok(op.buf[1], op.off[1], (uint64_t)p.batch * p.drafts * 4)) ||
+            !buf_ok(op.buf[2], op.off[2], (uint64_t)p.batch * 16))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "ACCEPT buffers too small");
+        *ws = accept_scratch_bytes(p);
+        return YUUKA_OK;
+    }
+    case YUUKA_EXT_OP_GDN_COMMIT: {
+        const GdnArgs g = gdn_args(op);
+        yuuka_status st = check_gdn(g, "GDN commit");
+        if (st != YUUKA_OK) return st;
+        for (int i = 0; i < 9; i++)
+            if (!op.buf[i]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "GDN commit buffer %d is null", i);
+        return YUUKA_OK;
+    }
+    case YUUKA_EXT_OP_ADVANCE:
+        if (!op.buf[0] || op.buf[0]->bytes < 8 || !op.buf[1] || op.n[0] == 0)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid ADVANCE buffers");
+        return YUUKA_OK;
     default:
         return fail(YUUKA_ERR_UNSUPPORTED, "plan op code %u is not served by this library", op.code);
     }
@@ -55,16 +251,101 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
 
 yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
     hipError_t err = hipSuccess;
+    const hipStream_t s = ctx.stream;
     switch (op.code) {
     case YUUKA_OP_ADD:
-        err = launch_add_f32(at<float>(op, 0), at<const float>(op, 0), at<const float>(op, 1), op.n[0], ctx.stream);
+        err = launch_add_f32(at<float>(op, 0), at<const float>(op, 0), at<const float>(op, 1), op.n[0], s);
         break;
     case YUUKA_OP_COPY:
-        err = launch_copy_f32(at<float>(op, 0), at<const float>(op, 1), op.n[0], ctx.stream);
+        err = launch_copy_f32(at<float>(op, 0), at<const float>(op, 1), op.n[0], s);
         break;
     case YUUKA_OP_SILU_MUL:
-        err = launch_silu_mul(at<const float>(op, 0), at<const float>(op, 1), at<float>(op, 2), op.n[0], ctx.stream);
+        err = launch_silu_mul(at<const float>(op, 0), at<const float>(op, 1), at<float>(op, 2), op.n[0], s);
         break;
+    case YUUKA_OP_EMBEDDING_BATCH:
+        err = launch_embedding(at<const uint8_t>(op, 0), op.u[0], op.n[2], at<const int32_t>(op, 2), (int)op.n[3],
+                               (int)op.n[0], (int)op.n[1], at<float>(op, 1), s);
+        break;
+    case YUUKA_OP_RMSNORM_BATCH:
+        err = launch_rmsnorm_rows(at<const float>(op, 0), at<const float>(op, 1), at<float>(op, 2), (int)op.n[0],
+                                  (int)op.n[1], op.n[2], op.n[3], op.f[0], s);
+        break;
+    case YUUKA_OP_RMSNORM_HEADS_BATCH:
+        err = launch_rmsnorm_heads(at<const float>(op, 0), at<const float>(op, 1), at<float>(op, 2), (int)op.n[0],
+                                   (int)op.n[1], (int)op.n[2], (int)op.n[3], op.f[0], s);
+        break;
+    case YUUKA_OP_ROPE_BATCH:
+        err = launch_rope(at<float>(op, 0), (int)op.n[0], (int)op.n[1], (int)op.n[3], (int)op.n[4], op.n[5],
+                          (double)op.f[0], dyn_of(ctx), (int)op.u[0], s);
+        break;
+    case YUUKA_OP_KV_WRITE_BATCH_PAGED: {
+        bool ok;
+        err = launch_kv_write(at<const float>(op, 0), at<const float>(op, 1), at<uint8_t>(op, 2), at<uint8_t>(op, 3),
+                              at<const int32_t>(op, 4), (int)op.n[0], (int)op.n[1], (int)op.u[0], kv_fmt(op.u[2], &ok),
+                              dyn_of(ctx), 0, s);
+        break;
+    }
+    case YUUKA_OP_ATTENTION_PREFILL_PAGED: {
+        const AttnArgs a = attn_args(op);
+        const int hint = ctx.dyn ? -1 : (int)ctx.position + a.displacement + a.rows - 1;
+        err = launch_attention(at<const float>(op, 0), at<const uint8_t>(op, 1), at<const uint8_t>(op, 2),
+                               at<const int32_t>(op, 4), at<float>(op, 3), a, ctx.ws, dyn_of(ctx), hint, s);
+        break;
+    }
+    case YUUKA_OP_RECURRENT_CHUNK: {
+        const GdnArgs g = gdn_args(op);
+        const bool defer = (op.flags & YUUKA_EXT_FLAG_DEFER) != 0;
+        float *conv = at<float>(op, 11);
+        float *raw = static_cast<float *>(ctx.ws);
+        err = launch_gdn_conv(at<const float>(op, 0), at<const float>(op, 2), at<const float>(op, 6), conv, g, s);
+        if (err == hipSuccess)
+            err = launch_gdn_scan(at<float>(op, 1), conv, at<const float>(op, 4), at<const float>(op, 5),
+                                  at<const float>(op, 7), at<const float>(op, 8), raw, g, defer ? 0 : 2, nullptr, s);
+        if (err == hipSuccess && !defer)
+            err = launch_gdn_conv_commit(at<float>(op, 0), at<const float>(op, 2), g, nullptr, s);
+        if (err == hipSuccess)
+            err = launch_gdn_norm_gate(raw, at<const float>(op, 3), at<const float>(op, 9), at<float>(op, 10), g, s);
+        break;
+    }
+    case YUUKA_EXT_OP_QUANTIZE_X:
+        err = launch_quantize_x(at<const float>(op, 0), op.n[0], op.n[1], at<uint8_t>(op, 1), s);
+        break;
+    case YUUKA_EXT_OP_GEMM_Q: {
+        const GemmPlan p = gemm_plan(op.n[0], op.n[1], op.n[2], op.u[0]);
+        err = launch_gemm_q(at<const uint8_t>(op, 0), op.u[0], at<const uint8_t>(op, 1), at<float>(op, 2), op.n[0],
+                            op.n[1], op.n[2], p, ctx.ws, nullptr, s, at<const float>(op, 3));
+        break;
+    }
+    case YUUKA_EXT_OP_ACCEPT: {
+        yuuka_accept_params p{};
+        p.mode = op.u[0];
+        p.batch = (uint32_t)op.n[0];
+        p.drafts = (uint32_t)op.n[1];
+        p.vocab = (uint32_t)op.n[2];
+        p.row_stride = op.n[3];
+        p.seed = op.n[4];
+        p.step = op.n[5];
+        p.top_k = op.u[1];
+        p.request_base = op.u[2];
+        p.temperature = op.f[0];
+        p.top_p = op.f[1];
+        err = launch_verify_accept(at<const float>(op, 0), at<const int32_t>(op, 1), at<int32_t>(op, 2),
+                                   at<double>(op, 3), p, ctx.ws, s, at<const uint64_t>(op, 4));
+        break;
+    }
+    case YUUKA_EXT_OP_GDN_COMMIT: {
+        const GdnArgs g = gdn_args(op);
+        const int32_t *res = at<const int32_t>(op, 8);
+        err = launch_gdn_scan(at<float>(op, 1), at<const float>(op, 3), at<const float>(op, 4), at<const float>(op, 5),
+                              at<const float>(op, 6), at<const float>(op, 7), nullptr, g, 1, res, s);
+        if (err == hipSuccess) err = launch_gdn_conv_commit(at<float>(op, 0), at<const float>(op, 2), g, res, s);
+        break;
+    }
+    case YUUKA_EXT_OP_ADVANCE: {
+        ModelDyn d{static_cast<int32_t *>(op.buf[0]->ptr) + 1, 0};
+        err = launch_advance(d, at<const int32_t>(op, 1), (int)op.n[0], at<uint64_t>(op, 2), s);
+        break;
+    }
     default:
         return fail(YUUKA_ERR_UNSUPPORTED, "plan op code %u is not served by this library", op.code);
     }
