@@ -5,9 +5,15 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1]
 
 A step is one pass of the hot path over one synthetic batch, with every input
 already resident in HBM:
-  config 1: activation quantization + one Q4_K 9216x2560 verify GEMM (M = 5
-            rows: 1 accepted token + k = 4 drafts) + fused greedy acceptance
-            over 5 x 151936 logits.
+  config 2 (default): one speculative verify step
+            of the Qwen3.5-4B-like hybrid decoder — k+1 = 5 rows through 32
+            layers (24 Gated DeltaNet + 8 gated attention), LM head over
+            151936 tokens, fused greedy acceptance, on-device commit of the
+            accepted prefix — as one captured HIP graph; drafts from prompt
+            lookup over the history (engine/speculative.go lookupDraft).
+  config 1: activation quantization + one Q4_K
+            9216x2560 verify GEMM (M = 5) + fused greedy acceptance over
+            5 x 151936 logits.
 To defeat the 256 MB Infinity Cache, steps rotate through >= 512 MB of
 distinct weight copies.
 
@@ -32,10 +38,11 @@ HBM_PEAK_GBS = 8000.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=1)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--drafts", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     return ap.parse_args()
 
@@ -167,6 +174,181 @@ def cpu_baseline_config1(c, budget_s):
             "ms_per_step": step_s * 1e3}
 
 
+def lookup_draft(history, max_draft, min_match=2):
+    """engine/speculative.go:39-66 (prompt-lookup drafts), host side."""
+    n = len(history)
+    if max_draft <= 0 or n <= min_match:
+        return []
+    for ln in range(min(8, n - 1), min_match - 1, -1):
+        suffix = history[n - ln:]
+        for start in range(n - ln - 1, -1, -1):
+            if history[start:start + ln] == suffix:
+                follow = start + ln
+                take = min(max_draft, n - follow)
+                if take > 0:
+                    return history[follow:follow + take]
+    return []
+
+
+def bench_config2(args):
+    """full verify step on the Qwen3.5-4B-like hybrid
+    decoder (random init, Q4_K_M mix), 512-token prompt in paged F16 KV,
+    k drafts per step, greedy acceptance."""
+    from yuuka_amd import hip, model as Mdl, synth
+
+    k = args.drafts
+    steps, warmup = args.steps or 256, args.warmup if args.warmup is not None else 8
+    cfg = Mdl.replace(Mdl.QWEN35_4B_LIKE, capacity=512 + (steps + warmup + 4) * (k + 1))
+    t0 = time.perf_counter()
+    w = Mdl.make_weights(cfg, seed=0)
+    gen_s = time.perf_counter() - t0
+    wbytes = Mdl.weight_bytes(w)
+    dev = hip.Device(0)
+    info = dev.info()
+    eng = Mdl.Engine(dev, cfg, w)
+    rng = np.random.default_rng(2)
+    prompt = rng.integers(0, cfg.vocab, 512).astype(np.int32).tolist()
+    t0 = time.perf_counter()
+    eng.prefill(prompt[:-1], want_logits=False)
+    prefill_s = time.perf_counter() - t0
+    history = list(prompt)
+    pending = prompt[-1]
+    acc = Mdl.accept_struct()
+
+    def step():
+        nonlocal pending
+        d = lookup_draft(history, k)
+        d = d + [pending] * (k - len(d))
+        res = eng.verify(np.array([pending] + d, np.int32), acc)
+        emitted = d[:res[0]] + [int(res[1])]
+        history.extend(emitted)
+        pending = int(res[1])
+        return len(emitted), eng.last_step_ms
+
+    for _ in range(warmup):
+        step()
+    tokens, gpu_ms = 0, []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        n, ms = step()
+        tokens += n
+        gpu_ms.append(ms)
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / steps
+    step_gpu_ms = float(np.median(gpu_ms))
+    ctx = eng.position
+    rows = k + 1
+    kvdim = cfg.kv_heads * cfg.head_dim
+    n_attn = sum(1 for i in range(cfg.n_layers) if not cfg.is_recurrent(i))
+    n_rec = cfg.n_layers - n_attn
+    kv_bytes = n_attn * ctx * kvdim * 2 * 2            # K and V rows read once (F16)
+    state_bytes = 2 * n_rec * (cfg.rank * cfg.state_size ** 2 + 3 * cfg.conv_dim) * 4  # read + write once
+    logit_bytes = 2 * rows * cfg.vocab * 4              # written by the LM head, read by the acceptance
+    step_bytes = wbytes + kv_bytes + state_bytes + logit_bytes
+    step_ach = step_bytes / (step_gpu_ms * 1e-3) / 1e9
+
+    # Dominant kernel (Q4_K verify GEMM at the FFN gate/up shape, the most
+    # frequent weight stream of the step), timed live on one stream.
+    N, K = cfg.ffn, cfg.hidden
+    wq = synth.quant_matrix(rng, synth.Q4_K, N, K)
+    copies = max(1, -(-512 * 2**20 // wq.nbytes))
+    wbufs = [dev.upload(wq)] + [dev.upload(synth.quant_matrix(rng, synth.Q4_K, N, K)) for _ in range(copies - 1)]
+    st = hip.Stream(dev)
+    xb = dev.upload(rng.normal(0, 1, (rows, K)).astype(np.float32))
+    xq = dev.alloc(hip.quantized_bytes(K, rows))
+    ob = dev.alloc(rows * N * 4)
+    hip.quantize_activations(st, xq, xb, K, rows)
+    for i in range(10):
+        hip.gemm_quantized(st, ob, xq, wbufs[i % copies], K, N, rows, synth.Q4_K)
+    st.sync()
+    e0, e1 = hip.Event(dev, timed=True), hip.Event(dev, timed=True)
+    reps = 200
+    e0.record(st)
+    for i in range(reps):
+        hip.gemm_quantized(st, ob, xq, wbufs[i % copies], K, N, rows, synth.Q4_K)
+    e1.record(st)
+    st.sync()
+    gemm_us = e1.elapsed_ms(e0) * 1e3 / reps
+    gemm_bytes = wq.nbytes + rows * K * 4 + rows * N * 4
+    gemm_ach = gemm_bytes / (gemm_us * 1e-6) / 1e9
+
+    line = {
+        "metric": "accepted tokens/s on 1 MI355X; verify-step HBM GB/s vs peak",
+        "value": tokens / wall,
+        "unit": "accepted tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k/q6_k weights x int16-split activations (int32 MFMA), fp32 norms/attention/GDN",
+        "data": "synthetic: random-init Q4_K_M-mix weights (dequantized std ~0.02), random 512-token prompt, "
+                "prompt-lookup drafts padded to k",
+        "config": {"workload": "config2: Qwen3.5-4B-like hybrid decoder verify step, batch 1",
+                   "hidden": cfg.hidden, "ffn": cfg.ffn, "layers": cfg.n_layers, "gdn_heads": cfg.rank,
+                   "attn_heads": f"{cfg.heads}q/{cfg.kv_heads}kv x {cfg.head_dim}", "vocab": cfg.vocab,
+                   "prompt": 512, "drafts": k, "rows": rows, "acceptance": "greedy", "kv": "paged F16, 16-token blocks",
+                   "parallelism": "single GPU"},
+        "verify_step_gpu_us": step_gpu_ms * 1e3,
+        "accepted_tokens_per_step": tokens / steps,
+        "step_roofline": {"bound": "hbm", "achieved": step_ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": step_ach / HBM_PEAK_GBS, "alg_bytes_per_step": step_bytes,
+                          "weights": wbytes, "kv": kv_bytes, "gdn_state": state_bytes, "logits": logit_bytes},
+        "roofline": {"bound": "hbm", "achieved": gemm_ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gemm_ach / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": f"gemm_q4k_kernel<1> {N}x{K} M={rows}", "alg_bytes_per_launch": gemm_bytes,
+                     "avg_us": gemm_us},
+        "context_end": ctx,
+        "prefill_s": prefill_s,
+        "weight_gen_s": gen_s,
+        "device": info,
+    }
+    eng.close()
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_config2(cfg, w, k, args.cpu_seconds)
+    return line
+
+
+def cpu_baseline_config2(cfg, w, k, budget_s):
+    """The oracle decoder (restatement of model/qwen35 forwardOne, every weight
+    re-read per token, matmul rows split over all host cores) running the
+    same verify steps: k+1 rows of PrefillLogits + greedy accept per step."""
+    from oracle import oracle as O
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    orc = O.Q35(cfg, w, kv_format=1, workers=cores)
+    rng = np.random.default_rng(3)
+    prompt = rng.integers(0, cfg.vocab, 4).astype(np.int32).tolist()
+    orc.forward(prompt[:-1])
+    history, pending = list(prompt), prompt[-1]
+    n, tokens = 0, 0
+    t0 = time.perf_counter()
+    while True:
+        d = lookup_draft(history, k)
+        d = d + [pending] * (k - len(d))
+        rows = [pending] + d
+        snap, pos = orc.snapshot()
+        logits = orc.forward(rows, all_logits=True)
+        a, nxt, _ = O.accept_greedy(logits, d)
+        if a < k:  # reference rollback: restore and replay the accepted prefix
+            orc.restore(snap, pos)
+            orc.forward(rows[:a + 1])
+        emitted = d[:a] + [nxt]
+        history.extend(emitted)
+        pending = nxt
+        tokens += len(emitted)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 1000:
+            break
+    orc.close()
+    return {"value": tokens / el, "unit": "accepted tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{n} verify steps (k={k}, {k + 1} rows of the full 32-layer model each, greedy, "
+                      f"snapshot/replay rollback) after a 4-token prompt, {el:.1f} s",
+            "ms_per_step": el * 1e3 / n}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -175,7 +357,11 @@ def main():
         sys.exit(2)
     ensure_built()
     if args.config == 1:
+        args.steps = args.steps or 200
+        args.warmup = args.warmup if args.warmup is not None else 20
         line = bench_config1(args)
+    elif args.config == 2:
+        line = bench_config2(args)
     else:
         print(json.dumps({"error": f"config {args.config} not available yet"}))
         sys.exit(2)

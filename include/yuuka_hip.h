@@ -471,6 +471,8 @@ YUUKA_API void yuuka_q35_destroy(yuuka_q35 * q);
 /* state.go:174-189: recurrent state cleared, position 0, step counter 0. */
 YUUKA_API yuuka_status yuuka_q35_reset(yuuka_q35 * q);
 YUUKA_API int32_t yuuka_q35_position(const yuuka_q35 * q);
+/* GPU time of the last step's graph (HIP events on the engine stream). */
+YUUKA_API float yuuka_q35_last_step_ms(const yuuka_q35 * q);
 /* Processes n tokens (session.go:195-242 Prefill); *last_logits (may be
  * NULL) receives the logits of the final token [vocab]. */
 YUUKA_API yuuka_status yuuka_q35_prefill(yuuka_q35 * q, const int32_t * tokens, int32_t n,

@@ -72,6 +72,8 @@ struct yuuka_q35 {
                  *attn = nullptr, *z = nullptr, *gdn_out = nullptr, *fg = nullptr, *fu = nullptr, *logits = nullptr,
                  *tokens = nullptr, *result = nullptr, *dyn = nullptr, *step = nullptr, *table = nullptr;
     int32_t *pinned = nullptr;  // tokens staging {tokens[16], result[4]}
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;  // around the last graph replay
+    float last_ms = 0.0f;
     // plans keyed by (rows, mode): mode 0 verify greedy/stochastic, 1 commit-all
     std::map<std::pair<int, int>, Graphs> plans;
     yuuka_q35_accept accept_cfg{};
@@ -272,11 +274,14 @@ yuuka_status run_step(yuuka_q35 *q, int rows, int mode, int32_t *result_out) {
         err = hipMemcpyAsync(q->result->ptr, q->pinned + 16, 8, hipMemcpyHostToDevice, s);
     }
     if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "token upload: %s", yk::hip_error(err));
+    (void)hipEventRecord(q->ev0, s);
     st = yuuka_graph_replay(g->graph, q->stream, nullptr);
     if (st != YUUKA_OK) return st;
+    (void)hipEventRecord(q->ev1, s);
     err = hipMemcpyAsync(q->pinned + 16, q->result->ptr, 16, hipMemcpyDeviceToHost, s);
     if (err == hipSuccess) err = hipStreamSynchronize(s);
     if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "verify step: %s", yk::hip_error(err));
+    (void)hipEventElapsedTime(&q->last_ms, q->ev0, q->ev1);
     q->last_rows = rows;
     if (result_out) std::memcpy(result_out, q->pinned + 16, 16);
     return YUUKA_OK;
@@ -349,6 +354,8 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
         if (st != YUUKA_OK) return st;
         hipError_t err = hipHostMalloc(reinterpret_cast<void **>(&q->pinned), 32 * 4, hipHostMallocDefault);
         if (err != hipSuccess) return fail(YUUKA_ERR_ALLOCATION, "pinned staging: %s", yk::hip_error(err));
+        if (hipEventCreate(&q->ev0) != hipSuccess || hipEventCreate(&q->ev1) != hipSuccess)
+            return fail(YUUKA_ERR_DEVICE, "timing events");
         const uint64_t H = c.hidden, M = c.max_rows, hd = c.head_dim;
         const uint64_t qdim = (uint64_t)c.heads * hd * 2, kvdim = (uint64_t)c.kv_heads * hd;
         const uint64_t cd = (uint64_t)q->conv_dim;
@@ -435,6 +442,8 @@ void yuuka_q35_destroy(yuuka_q35 *q) {
     drop_graphs(q);
     for (auto *b : q->owned) yuuka_buffer_free(b);
     if (q->pinned) (void)hipHostFree(q->pinned);
+    if (q->ev0) (void)hipEventDestroy(q->ev0);
+    if (q->ev1) (void)hipEventDestroy(q->ev1);
     yuuka_stream_destroy(q->stream);
     delete q;
 }
@@ -455,6 +464,8 @@ yuuka_status yuuka_q35_reset(yuuka_q35 *q) {
         return YUUKA_OK;
     });
 }
+
+float yuuka_q35_last_step_ms(const yuuka_q35 *q) { return q ? q->last_ms : 0.0f; }
 
 int32_t yuuka_q35_position(const yuuka_q35 *q) { return q ? read_pos(const_cast<yuuka_q35 *>(q)) : -1; }
 

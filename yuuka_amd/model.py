@@ -7,7 +7,7 @@ the CPU baseline) to the oracle, so both run the identical model.
 from __future__ import annotations
 
 import ctypes as C
-from dataclasses import dataclass, fields, replace
+from dataclasses import dataclass, fields, replace  # noqa: F401 (replace re-exported)
 
 import numpy as np
 
@@ -195,6 +195,7 @@ def _declare(L):
         "yuuka_q35_destroy": (None, [vp]),
         "yuuka_q35_reset": (C.c_int, [vp]),
         "yuuka_q35_position": (C.c_int32, [vp]),
+        "yuuka_q35_last_step_ms": (C.c_float, [vp]),
         "yuuka_q35_prefill": (C.c_int, [vp, vp, C.c_int32, vp]),
         "yuuka_q35_verify": (C.c_int, [vp, vp, C.c_int32, C.POINTER(yuuka_q35_accept), vp]),
         "yuuka_q35_logits": (C.c_int, [vp, vp, C.c_int32]),
@@ -236,6 +237,10 @@ class Engine:
     @property
     def position(self) -> int:
         return int(hip.lib().yuuka_q35_position(self.ptr))
+
+    @property
+    def last_step_ms(self) -> float:
+        return float(hip.lib().yuuka_q35_last_step_ms(self.ptr))
 
     def prefill(self, tokens, want_logits=True):
         t = np.ascontiguousarray(tokens, np.int32)
