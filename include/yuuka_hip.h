@@ -376,6 +376,15 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
  *   ADVANCE:    buf0 dynamic buffer {token, position}, buf1 int32 result,
  *               optional buf2 uint64 step counter; n0 = rows. position +=
  *               result[0] + 1; step += 1.
+ *   GEMM_FUSED: buf0 FP32 x [rows][n_in], optional buf1 FP32 RMSNorm weight
+ *               [n_in] (y = RMSNorm(x) * w, eps f0; else y = x); segments
+ *               i = 0..3 (the leading non-null weights): buf2+i packed W_i
+ *               (Q4_K or Q6_K, dtype in byte i of u0), buf6+i FP32 out_i
+ *               [rows][N_i], buf10+i FP32 residual_i (epilogue 1, may alias
+ *               out_i); n={n_in, rows, N_0, N_1, N_2, N_3}; u1 epilogue:
+ *               0 out = y W^T, 1 out = y W^T + residual, 2 SwiGLU
+ *               out_0 = SiLU(y W_0^T) * (y W_1^T) (two segments, same shape).
+ *               rows <= 16. One launch, no workspace.
  * YUUKA_EXT_FLAG_DEFER on RECURRENT_CHUNK: compute the outputs of every row
  * but leave both states untouched (verify mode; see GDN_COMMIT). */
 #define YUUKA_EXT_OP_QUANTIZE_X 64u
@@ -383,6 +392,7 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
 #define YUUKA_EXT_OP_ACCEPT 66u
 #define YUUKA_EXT_OP_GDN_COMMIT 67u
 #define YUUKA_EXT_OP_ADVANCE 68u
+#define YUUKA_EXT_OP_GEMM_FUSED 69u
 #define YUUKA_EXT_FLAG_DEFER 0x100u
 
 /* Timing events (extension): an event created with timing enabled, recorded

@@ -104,6 +104,22 @@ def matmul(dtype: int, w: np.ndarray, x: np.ndarray, rows: int, cols: int, worke
     return out
 
 
+def rmsnorm_rows(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """forward.go:460-470 rmsNorm applied to every row of x."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    for r in range(x.shape[0]):
+        lib().orc_rmsnorm(_ptr(out[r]), _ptr(x[r]), _ptr(w), x.shape[1], eps)
+    return out
+
+
+def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
+    """forward.go SwiGLU: silu(g) * u per element (float32)."""
+    f = lib().orc_silu
+    return np.array([f(float(a)) for a in g.ravel()], np.float32).reshape(g.shape) * u.astype(np.float32)
+
+
 def argmax(logits: np.ndarray) -> int:
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     return int(lib().orc_argmax(_ptr(logits), logits.size))

@@ -1,0 +1,136 @@
+"""GPU parity of the fused verify GEMM (plan op GEMM_FUSED) against the oracle
+restatement of tensor/quant.go MatMul on the same seeded inputs, with the
+fused RMSNorm prologue (forward.go:460-470) and the residual / SwiGLU
+epilogues. Tolerance: the 16-bit activation quantization error budget
+relative to the output rms, plus the north-star 1e-2 relative bar."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from yuuka_amd import hip, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(got, want, budget=5e-4):
+    want = want.astype(np.float64)
+    rms = float(np.sqrt(np.mean(want ** 2))) + 1e-30
+    err = np.abs(got.astype(np.float64) - want)
+    assert float(err.max()) <= budget * rms, (float(err.max()), rms)
+    assert np.all(err <= 1e-2 * (np.abs(want) + rms))
+
+
+def _run(dev, stream, x, segs, k, rows, epilogue=hip.EPI_STORE, norm=None, eps=1e-6, residuals=None):
+    """segs: [(dtype, w_bytes_array, n_out)] -> list of outputs."""
+    plan = hip.Plan(dev)
+    xb = dev.upload(x.astype(np.float32))
+    nb = dev.upload(norm.astype(np.float32)) if norm is not None else None
+    outs, spec = [], []
+    for i, (dt, w, n) in enumerate(segs):
+        ob = dev.alloc(rows * n * 4)
+        rb = None
+        if residuals is not None:
+            ob.write(residuals[i].astype(np.float32))
+            rb = ob   # in-place residual: out = W y + out
+        outs.append(ob)
+        spec.append((dev.upload(w), dt, n, ob, rb))
+    hip.gemm_fused_op(plan, xb, k, rows, spec, epilogue, nb, eps)
+    plan.execute(stream)
+    stream.sync()
+    res = [o.read(np.float32).reshape(rows, n) for o, (_, _, n) in zip(outs, segs)]
+    plan.destroy()
+    return res
+
+
+def _want(dt, w, n, k, y):
+    return O.matmul(dt, w, y, n, k)
+
+
+CASES = [
+    # (segments [(dtype, n)], K, rows, norm)
+    ([(O.Q4_K, 9216)], 2560, 5, False),             # configuration-1 shape
+    ([(O.Q4_K, 6144), (O.Q4_K, 2048), (O.Q4_K, 16), (O.Q4_K, 16)], 2560, 5, True),  # GDN projections
+    ([(O.Q4_K, 8192), (O.Q4_K, 1024), (O.Q6_K, 1024)], 2560, 5, True),              # attention q/k/v
+    ([(O.Q4_K, 2560)], 9216, 5, False),             # down projection
+    ([(O.Q4_K, 2560)], 2048, 5, False),             # GDN out projection
+    ([(O.Q6_K, 3000)], 2560, 5, True),              # LM head shape (fewer rows)
+    ([(O.Q4_K, 100)], 256, 1, False),
+    ([(O.Q4_K, 333)], 1024, 8, True),
+    ([(O.Q4_K, 300), (O.Q6_K, 77)], 1536, 12, False),
+    ([(O.Q4_K, 64)], 9216, 16, False),              # K split into LDS chunks
+    ([(O.Q6_K, 130)], 2560, 16, True),
+]
+
+
+@pytest.mark.parametrize("segs,k,rows,norm", CASES)
+def test_fused_gemm_matches_oracle(dev, stream, segs, k, rows, norm):
+    rng = np.random.default_rng(k * 7 + rows + len(segs))
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    g = rng.normal(1, 0.1, k).astype(np.float32) if norm else None
+    ws = [synth.quant_matrix(rng, dt, n, k) for dt, n in segs]
+    got = _run(dev, stream, x, [(dt, w, n) for (dt, n), w in zip(segs, ws)], k, rows, norm=g)
+    y = O.rmsnorm_rows(x, g, 1e-6) if norm else x
+    for (dt, n), w, gv in zip(segs, ws, got):
+        _check(gv, _want(dt, w, n, k, y))
+
+
+def test_fused_gemm_residual_epilogue(dev, stream):
+    rng = np.random.default_rng(11)
+    k, n, rows = 9216, 2560, 5
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    w = synth.quant_matrix(rng, O.Q4_K, n, k)
+    res = rng.normal(0, 3, (rows, n)).astype(np.float32)
+    got = _run(dev, stream, x, [(O.Q4_K, w, n)], k, rows, hip.EPI_RESIDUAL, residuals=[res])[0]
+    prod = _want(O.Q4_K, w, n, k, x)
+    _check(got - res, prod)
+
+
+def test_fused_gemm_swiglu_epilogue(dev, stream):
+    rng = np.random.default_rng(12)
+    k, n, rows = 2560, 1000, 5
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    g = rng.normal(1, 0.1, k).astype(np.float32)
+    wg = synth.quant_matrix(rng, O.Q4_K, n, k)
+    wu = synth.quant_matrix(rng, O.Q4_K, n, k)
+    got = _run(dev, stream, x, [(O.Q4_K, wg, n), (O.Q4_K, wu, n)], k, rows, hip.EPI_SWIGLU, norm=g)[0]
+    y = O.rmsnorm_rows(x, g, 1e-6)
+    want = O.silu_mul(_want(O.Q4_K, wg, n, k, y), _want(O.Q4_K, wu, n, k, y))
+    _check(got, want, budget=1e-3)
+
+
+def test_fused_gemm_repeatable_and_outliers(dev, stream):
+    """Bitwise repeatable; a row of zeros stays zero; a 1e4 outlier in one
+    super-block only costs that super-block's resolution."""
+    rng = np.random.default_rng(13)
+    k, n, rows = 2560, 700, 4
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    x[1] = 0.0
+    x[2, 5] = 1e4
+    w = synth.quant_matrix(rng, O.Q4_K, n, k)
+    a = _run(dev, stream, x, [(O.Q4_K, w, n)], k, rows)[0]
+    b = _run(dev, stream, x, [(O.Q4_K, w, n)], k, rows)[0]
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert not np.any(a[1])
+    want = _want(O.Q4_K, w, n, k, x)
+    for r in (0, 2, 3):
+        _check(a[r:r + 1], want[r:r + 1], budget=2e-3)
+
+
+def test_fused_gemm_rejects_bad_ops(dev):
+    plan = hip.Plan(dev)
+    xb = dev.alloc(5 * 2560 * 4)
+    wb = dev.alloc(synth.BLOCK_BYTES[O.Q4_K] * 10 * 64)
+    ob = dev.alloc(5 * 64 * 4)
+    with pytest.raises(hip.HipError):   # K not a multiple of 256
+        hip.gemm_fused_op(plan, xb, 2500, 5, [(wb, O.Q4_K, 64, ob, None)])
+    with pytest.raises(hip.HipError):   # 17 rows
+        hip.gemm_fused_op(plan, xb, 2560, 17, [(wb, O.Q4_K, 64, ob, None)])
+    with pytest.raises(hip.HipError):   # weight buffer too small for 65 rows
+        hip.gemm_fused_op(plan, xb, 2560, 5, [(wb, O.Q4_K, 65, ob, None)])
+    with pytest.raises(hip.HipError):   # Q8_0 weights
+        hip.gemm_fused_op(plan, xb, 2560, 5, [(wb, O.Q8_0, 64, ob, None)])
+    with pytest.raises(hip.HipError):   # residual epilogue without residual
+        hip.gemm_fused_op(plan, xb, 2560, 5, [(wb, O.Q4_K, 64, ob, None)], hip.EPI_RESIDUAL)
+    plan.destroy()

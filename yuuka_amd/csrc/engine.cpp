@@ -73,6 +73,7 @@ struct yuuka_q35 {
                  *tokens = nullptr, *result = nullptr, *dyn = nullptr, *step = nullptr, *table = nullptr;
     int32_t *pinned = nullptr;  // tokens staging {tokens[16], result[4]}
     hipEvent_t ev0 = nullptr, ev1 = nullptr;  // around the last graph replay
+    bool eager = false;  // YUUKA_Q35_EAGER=1: launch plans op by op (profilers), no graphs
     float last_ms = 0.0f;
     // plans keyed by (rows, mode): mode 0 verify greedy/stochastic, 1 commit-all
     std::map<std::pair<int, int>, Graphs> plans;
@@ -145,7 +146,49 @@ struct Builder {
     void quant(yuuka_buffer *x, uint64_t K, uint64_t rows, yuuka_buffer *xq) {
         add(YUUKA_EXT_OP_QUANTIZE_X, {x, xq}, {K, rows});
     }
+    struct Seg {
+        const Tensor *w;
+        yuuka_buffer *out, *res;
+    };
+    // One GEMM_FUSED op: every segment reads the same activation rows x
+    // (optionally RMS-normalised with `norm`).
+    void fused(yuuka_buffer *x, yuuka_buffer *norm, float eps, uint64_t rows, std::initializer_list<Seg> segs,
+               uint32_t epilogue) {
+        if (st != YUUKA_OK) return;
+        yuuka_op op{};
+        op.code = YUUKA_EXT_OP_GEMM_FUSED;
+        op.buf[0] = x;
+        op.buf[1] = norm;
+        op.n[1] = rows;
+        op.u[1] = epilogue;
+        op.f[0] = eps;
+        int i = 0;
+        for (const Seg &g : segs) {
+            op.buf[2 + i] = g.w->b;
+            op.buf[6 + i] = g.out;
+            op.buf[10 + i] = g.res;
+            op.n[0] = g.w->cols;
+            op.n[2 + i] = g.w->rows;
+            op.u[0] |= g.w->dtype << (8 * i);
+            i++;
+        }
+        st = yuuka_plan_add(plan, &op);
+    }
 };
+
+// Fused projections need Q4_K / Q6_K weights; YUUKA_Q35_FUSED=0 selects the
+// separate quantize / GEMM / reduce ops (comparison and fallback).
+bool use_fused(const yuuka_q35 *q) {
+    if (const char *e = getenv("YUUKA_Q35_FUSED"))
+        if (e[0] == '0') return false;
+    auto ok = [](const Tensor &t) { return !t.b || t.dtype == YUUKA_DTYPE_Q4_K || t.dtype == YUUKA_DTYPE_Q6_K; };
+    if (!ok(q->output)) return false;
+    for (const Layer &L : q->layers)
+        for (const Tensor *t : {&L.qkv, &L.gate, &L.beta, &L.alpha, &L.out, &L.q, &L.k, &L.v, &L.o, &L.ffn_gate,
+                                &L.ffn_up, &L.ffn_down})
+            if (!ok(*t)) return false;
+    return true;
+}
 
 // mode 0: verify (acceptance on device), mode 1: commit every row (prefill).
 yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
@@ -159,44 +202,68 @@ yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
     // plan.go:585-588 EMBEDDING_BATCH
     b.add(YUUKA_OP_EMBEDDING_BATCH, {q->embedding.b, q->x, q->tokens},
           {H, R, yk::row_bytes(q->embedding.dtype, H), (uint64_t)c.vocab}, {q->embedding.dtype});
+    const bool fused = use_fused(q);
+    const float qscale = (float)(1.0 / std::sqrt((double)c.state_size));
+    auto recurrent_chunk = [&](Layer &L) {
+        b.add(YUUKA_OP_RECURRENT_CHUNK,
+              {L.conv_state, L.mat_state, L.qkv_rows, q->z, L.alpha_rows, L.beta_rows, L.conv, L.dt, L.a, L.ssm_norm,
+               q->gdn_out, L.conv_rows},
+              {R, (uint64_t)c.groups, (uint64_t)c.rank, (uint64_t)c.state_size, (uint64_t)q->conv_dim,
+               (uint64_t)c.inner},
+              {(uint32_t)c.conv_kernel}, {c.eps, qscale}, YUUKA_EXT_FLAG_DEFER);
+    };
+    auto attention = [&](Layer &L) {
+        b.add(YUUKA_OP_RMSNORM_HEADS_BATCH, {q->k, L.k_norm, q->k}, {hd, (uint64_t)c.kv_heads, hd, R}, {}, {c.eps});
+        b.add(YUUKA_OP_ROPE_BATCH, {q->k}, {(uint64_t)c.kv_heads, hd, hd, (uint64_t)c.rope_dim, R, kvdim}, {0},
+              {(float)c.rope_base});
+        b.add(YUUKA_OP_KV_WRITE_BATCH_PAGED, {q->k, q->v, L.kpool, L.vpool, q->table}, {kvdim, R},
+              {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype});
+        b.add(YUUKA_OP_RMSNORM_HEADS_BATCH, {q->q, L.q_norm, q->q}, {hd, (uint64_t)c.heads, 2 * hd, R}, {}, {c.eps});
+        b.add(YUUKA_OP_ROPE_BATCH, {q->q}, {(uint64_t)c.heads, 2 * hd, hd, (uint64_t)c.rope_dim, R, qdim}, {0},
+              {(float)c.rope_base});
+        b.add(YUUKA_OP_ATTENTION_PREFILL_PAGED, {q->q, L.kpool, L.vpool, q->attn, q->table},
+              {(uint64_t)c.kv_heads, (uint64_t)c.heads, hd, kvdim, R, 0},
+              {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype, 0}, {(float)(1.0 / std::sqrt((double)hd))});
+    };
     for (int i = 0; i < c.n_layers; i++) {
         Layer &L = q->layers[i];
+        if (fused) {
+            if (L.recurrent) {  // plan.go:806-913
+                b.fused(q->x, L.attn_norm, c.eps, R,
+                        {{&L.qkv, L.qkv_rows, nullptr}, {&L.gate, q->z, nullptr}, {&L.beta, L.beta_rows, nullptr},
+                         {&L.alpha, L.alpha_rows, nullptr}},
+                        0);
+                recurrent_chunk(L);
+                b.fused(q->gdn_out, nullptr, 0.0f, R, {{&L.out, q->x, q->x}}, 1);
+            } else {  // plan.go:684-804
+                b.fused(q->x, L.attn_norm, c.eps, R,
+                        {{&L.q, q->q, nullptr}, {&L.k, q->k, nullptr}, {&L.v, q->v, nullptr}}, 0);
+                attention(L);
+                b.fused(q->attn, nullptr, 0.0f, R, {{&L.o, q->x, q->x}}, 1);
+            }
+            // plan.go:915-988 FFN: norm + gate/up + SwiGLU in one op, down + residual
+            b.fused(q->x, L.post_norm, c.eps, R, {{&L.ffn_gate, q->fg, nullptr}, {&L.ffn_up, nullptr, nullptr}}, 2);
+            b.fused(q->fg, nullptr, 0.0f, R, {{&L.ffn_down, q->x, q->x}}, 1);
+            continue;
+        }
         b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, L.attn_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
         b.quant(q->xn, H, R, q->xq);
-        if (L.recurrent) {  // plan.go:806-913
+        if (L.recurrent) {
             b.gemm(L.qkv, q->xq, L.qkv_rows, R);
             b.gemm(L.gate, q->xq, q->z, R);
             b.gemm(L.beta, q->xq, L.beta_rows, R);
             b.gemm(L.alpha, q->xq, L.alpha_rows, R);
-            const float qscale = (float)(1.0 / std::sqrt((double)c.state_size));
-            b.add(YUUKA_OP_RECURRENT_CHUNK,
-                  {L.conv_state, L.mat_state, L.qkv_rows, q->z, L.alpha_rows, L.beta_rows, L.conv, L.dt, L.a,
-                   L.ssm_norm, q->gdn_out, L.conv_rows},
-                  {R, (uint64_t)c.groups, (uint64_t)c.rank, (uint64_t)c.state_size, (uint64_t)q->conv_dim,
-                   (uint64_t)c.inner},
-                  {(uint32_t)c.conv_kernel}, {c.eps, qscale}, YUUKA_EXT_FLAG_DEFER);
+            recurrent_chunk(L);
             b.quant(q->gdn_out, (uint64_t)c.inner, R, q->xq);
             b.gemm(L.out, q->xq, q->x, R, q->x);
-        } else {  // plan.go:684-804
+        } else {
             b.gemm(L.q, q->xq, q->q, R);
             b.gemm(L.k, q->xq, q->k, R);
             b.gemm(L.v, q->xq, q->v, R);
-            b.add(YUUKA_OP_RMSNORM_HEADS_BATCH, {q->k, L.k_norm, q->k}, {hd, (uint64_t)c.kv_heads, hd, R}, {}, {c.eps});
-            b.add(YUUKA_OP_ROPE_BATCH, {q->k}, {(uint64_t)c.kv_heads, hd, hd, (uint64_t)c.rope_dim, R, kvdim}, {0},
-                  {(float)c.rope_base});
-            b.add(YUUKA_OP_KV_WRITE_BATCH_PAGED, {q->k, q->v, L.kpool, L.vpool, q->table}, {kvdim, R},
-                  {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype});
-            b.add(YUUKA_OP_RMSNORM_HEADS_BATCH, {q->q, L.q_norm, q->q}, {hd, (uint64_t)c.heads, 2 * hd, R}, {}, {c.eps});
-            b.add(YUUKA_OP_ROPE_BATCH, {q->q}, {(uint64_t)c.heads, 2 * hd, hd, (uint64_t)c.rope_dim, R, qdim}, {0},
-                  {(float)c.rope_base});
-            b.add(YUUKA_OP_ATTENTION_PREFILL_PAGED, {q->q, L.kpool, L.vpool, q->attn, q->table},
-                  {(uint64_t)c.kv_heads, (uint64_t)c.heads, hd, kvdim, R, 0},
-                  {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype, 0},
-                  {(float)(1.0 / std::sqrt((double)hd))});
+            attention(L);
             b.quant(q->attn, odim, R, q->xq);
             b.gemm(L.o, q->xq, q->x, R, q->x);
         }
-        // plan.go:915-988 FFN
         b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, L.post_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
         b.quant(q->xn, H, R, q->xq);
         b.gemm(L.ffn_gate, q->xq, q->fg, R);
@@ -206,9 +273,13 @@ yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
         b.gemm(L.ffn_down, q->xq, q->x, R, q->x);
     }
     // plan.go:635-662 all-logits tail
-    b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, q->output_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
-    b.quant(q->xn, H, R, q->xq);
-    b.gemm(q->output, q->xq, q->logits, R);
+    if (fused) {
+        b.fused(q->x, q->output_norm, c.eps, R, {{&q->output, q->logits, nullptr}}, 0);
+    } else {
+        b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, q->output_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
+        b.quant(q->xn, H, R, q->xq);
+        b.gemm(q->output, q->xq, q->logits, R);
+    }
     if (mode == 0) {
         const yuuka_q35_accept &a = q->accept_cfg;
         // drafts are tokens[1..k]
@@ -241,7 +312,7 @@ yuuka_status get_graph(yuuka_q35 *q, int rows, int mode, Graphs **out) {
         Graphs g;
         yuuka_status st = build_plan(q, rows, mode, &g.plan);
         if (st != YUUKA_OK) return st;
-        st = yuuka_graph_create(g.plan, q->stream, q->dyn, 1, &g.graph);
+        if (!q->eager) st = yuuka_graph_create(g.plan, q->stream, q->dyn, 1, &g.graph);
         if (st != YUUKA_OK) {
             yuuka_plan_destroy(g.plan);
             return st;
@@ -275,7 +346,10 @@ yuuka_status run_step(yuuka_q35 *q, int rows, int mode, int32_t *result_out) {
     }
     if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "token upload: %s", yk::hip_error(err));
     (void)hipEventRecord(q->ev0, s);
-    st = yuuka_graph_replay(g->graph, q->stream, nullptr);
+    if (g->graph)
+        st = yuuka_graph_replay(g->graph, q->stream, nullptr);
+    else
+        st = yk::plan_run_dynamic(g->plan, s, static_cast<const int32_t *>(q->dyn->ptr));
     if (st != YUUKA_OK) return st;
     (void)hipEventRecord(q->ev1, s);
     err = hipMemcpyAsync(q->pinned + 16, q->result->ptr, 16, hipMemcpyDeviceToHost, s);
@@ -354,6 +428,7 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
         if (st != YUUKA_OK) return st;
         hipError_t err = hipHostMalloc(reinterpret_cast<void **>(&q->pinned), 32 * 4, hipHostMallocDefault);
         if (err != hipSuccess) return fail(YUUKA_ERR_ALLOCATION, "pinned staging: %s", yk::hip_error(err));
+        q->eager = getenv("YUUKA_Q35_EAGER") && getenv("YUUKA_Q35_EAGER")[0] == '1';
         if (hipEventCreate(&q->ev0) != hipSuccess || hipEventCreate(&q->ev1) != hipSuccess)
             return fail(YUUKA_ERR_DEVICE, "timing events");
         const uint64_t H = c.hidden, M = c.max_rows, hd = c.head_dim;

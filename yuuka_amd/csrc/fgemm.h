@@ -1,0 +1,53 @@
+// fgemm.h — fused verify GEMM (k_fgemm.hip): argument block and launcher.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/yuuka_hip.h"
+
+namespace yk {
+
+constexpr int kFusedMaxSeg = 4;
+constexpr int kFusedWaves = 8;                   // waves per workgroup (they split K)
+constexpr uint32_t kFusedLds = 160 * 1024;       // LDS per workgroup on gfx950
+constexpr int kFusedMaxGrid = 512;               // workgroups of a persistent (one-chunk) launch
+
+enum FusedEpilogue : int {
+    kEpiStore = 0,     // out = y W^T
+    kEpiResidual = 1,  // out = y W^T + res (res may alias out)
+    kEpiSwiglu = 2,    // seg0.out = SiLU(y W0^T) * (y W1^T); segments 0, 1 same shape
+};
+
+struct FusedSeg {
+    const void *w;       // packed rows (Q4_K or Q6_K)
+    uint32_t w_bytes;    // bytes of the packed matrix (loads past it read 0)
+    uint32_t row_bytes;  // bytes of one packed row
+    int n;               // output rows
+    int dtype;
+    float *out;          // [rows][n]
+    const float *res;    // [rows][n] (kEpiResidual)
+    int wg_begin;        // first workgroup (set by the launcher)
+};
+
+struct FusedGemmArgs {
+    const float *x;     // [rows][K] activations
+    const float *norm;  // optional RMSNorm weight [K]
+    float eps;
+    int K, rows;
+    int chunk_sb;       // super-blocks of K quantized into LDS at a time
+    int epilogue;       // FusedEpilogue
+    int nseg;
+    int groups;         // tile groups over all segments (set by the launcher)
+    FusedSeg seg[kFusedMaxSeg];
+};
+
+// Largest K chunk (in 256-element super-blocks) whose activations fit LDS
+// next to the partial-sum area of a tt-tile launch (0 if none fits).
+int fused_gemm_chunk_sb(int rows, int K, int tt);
+uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt);
+// tt: 16-row tiles per workgroup (1, 2 or 4; even for kEpiSwiglu).
+hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s);
+
+}  // namespace yk

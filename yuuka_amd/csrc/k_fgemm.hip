@@ -1,0 +1,667 @@
+// k_fgemm.hip — fused verify GEMM on gfx950 (wave64, int8 MFMA).
+//
+//   out_s[m, n] = epi( sum_k y[m, k] * dequant(W_s)[n, k] ),  m < rows <= 16
+//
+// One launch covers up to four weight matrices ("segments") that read the
+// same activation rows — the q/k/v/z/alpha/beta projections of a layer, or
+// the FFN gate/up pair — so a layer's projections cost one launch instead of
+// one per matrix plus a quantization pass and a split-K reduction.
+//
+// y is x, or RMSNorm(x) * g when a norm weight is given
+// (model/qwen35/forward.go:460-482 rmsNorm). The norm is applied as
+//   y @ W^T = inv_rms(x) * ((x * g) @ W^T)
+// so the activations are quantized without waiting for the row sum of
+// squares; inv_rms (float64 sum, the reference's formula) scales the result.
+//
+// Per workgroup (512 threads = 8 waves):
+//  * Prologue: x * g is quantized into LDS — one int16 value per element,
+//    split into two int8 planes (q = 256 h + l), one scale per row and
+//    256-element super-block (max |x| over it), and the exact int16 sums of
+//    every 32-element sub-block (Q4_K min term). A lane quantizes one
+//    8-element slice; a wave does two (row, super-block) units at a time.
+//  * Main loop: the workgroup owns 16*TT output rows; its eight waves split
+//    the super-blocks of K. Weights are read straight from HBM into registers
+//    in MFMA operand order — lane (r, g) loads bytes [8g, 8g + 8) of each
+//    32-byte quant group of row r — with later super-blocks' loads in flight
+//    while the current one is multiplied. No LDS staging of weights and no
+//    barriers inside the loop.
+//  * Per 32-element sub-block the int32 MFMA result is scaled by the integer
+//    sub-block scale in int32 (exact); per super-block d, dmin and the
+//    activation scale are applied in FP32.
+//  * Epilogue: the eight waves' partial sums are added in a fixed order
+//    through LDS (deterministic), then stored, added to a residual, or
+//    combined as SiLU(gate) * up.
+//  * Launches whose activations fit LDS in one piece are persistent: each
+//    workgroup quantizes once and then walks several row groups.
+//
+// Replaces, for the verify shapes, the reference's per-matrix quantized GEMV
+// launches (kernels/hip/gemm/lm_head.hip:61-173 via bridge.cpp:3348-3371 and
+// the qwen35 plan's per-projection ops, engine/gpu/plan.go).
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+
+#include "fgemm.h"
+#include "refmath.h"
+
+namespace yk {
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+typedef short __attribute__((ext_vector_type(2))) s16x2;
+
+constexpr int kQ4K = YUUKA_DTYPE_Q4_K;
+constexpr int kQ6K = YUUKA_DTYPE_Q6_K;
+constexpr int kQMax = 32639;  // |q| bound that keeps the high plane in int8
+constexpr int kWaves = kFusedWaves;
+constexpr int kThreads = 64 * kWaves;
+
+#ifdef YK_FG_TIMING
+// Phase timestamps per wave (builds with YK_FG_TIMING only; s_memrealtime,
+// 100 MHz): kernel start, prologue done, main loop done, group done.
+__device__ uint64_t *yk_fg_dbg;
+#define YK_FG_STAMP(v) (v) = __builtin_amdgcn_s_memrealtime()
+#else
+#define YK_FG_STAMP(v) (void)0
+#endif
+
+__device__ __forceinline__ i32x4 mfma_i8(int64_t a, int64_t b) {
+    const i32x4 zero = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero, 0, 0, 0);
+}
+
+// Plain 24-bit multiply-add. (Inline v_mad_i32_i24 asm reading MFMA results
+// skips the compiler's MFMA-to-VALU wait states; keep this in C.)
+__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+
+__device__ __forceinline__ int dot2(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(s16x2, a), __builtin_bit_cast(s16x2, b), c, false);
+}
+
+__device__ __forceinline__ float half_lo(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)(h & 0xffffu))); }
+
+// 8 bytes at an even byte offset of the buffer (Q6_K blocks are only 2-byte
+// aligned): one dword-aligned 12-byte load, then a byte shift.
+__device__ __forceinline__ uint64_t load8_a2(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    typedef __attribute__((ext_vector_type(3))) int i32x3;
+    const i32x3 v = __builtin_bit_cast(i32x3, __builtin_amdgcn_raw_buffer_load_b96(rs, off & ~3u, 0, 0));
+    const uint32_t sh = off & 3u;
+    const uint32_t lo = __builtin_amdgcn_alignbyte((uint32_t)v[1], (uint32_t)v[0], sh);
+    const uint32_t hi = __builtin_amdgcn_alignbyte((uint32_t)v[2], (uint32_t)v[1], sh);
+    return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
+// Signed q - 32 for eight packed unsigned 6-bit values (one per byte).
+__device__ __forceinline__ uint64_t q6_to_i8(uint64_t q6) {
+    const uint64_t t = q6 ^ 0x2020202020202020ull;
+    const uint64_t s = t & 0x2020202020202020ull;
+    return t | (s << 1) | (s << 2);
+}
+
+// Cross-lane steps on the DPP path (no LDS round trip): quad_perm [1,0,3,2]
+// and [2,3,0,1] pair lanes at distance 1 and 2, row_ror 4 / 8 rotate inside
+// a 16-lane row.
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true); }
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) { return __int_as_float(dpp<CTRL>(__float_as_int(v))); }
+__device__ __forceinline__ float rdl(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+
+// Maximum / sum over each 16-lane row, in every lane of the row.
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dppf<0xb1>(v));
+    v = fmaxf(v, dppf<0x4e>(v));
+    v = fmaxf(v, dppf<0x124>(v));
+    return fmaxf(v, dppf<0x128>(v));
+}
+__device__ __forceinline__ float row_sum(float v) {
+    v += dppf<0xb1>(v);
+    v += dppf<0x4e>(v);
+    v += dppf<0x124>(v);
+    return v + dppf<0x128>(v);
+}
+// Sum over each quad, in every lane of the quad.
+__device__ __forceinline__ int quad_sum(int v) {
+    v += dpp<0xb1>(v);
+    return v + dpp<0x4e>(v);
+}
+
+// LDS layout of one K chunk, RHO = 2 * rows live A rows (h plane rows
+// 0..rows-1, l plane rows rows..2rows-1), RHOP = 16 * NA:
+//   planes [cap * 8 sub-blocks][4 slices][RHO][8 B]
+//   sums   [cap][RHOP][8] int16      (sub-block sums of each plane row)
+//   xs     [cap][RHOP] float         (activation scale of each plane row)
+//   nsq    [rows][nsb] float         (per super-block sums of x^2, norm)
+//   junk   16 B                      (stores of units past the end)
+// The tables hold `cap` super-blocks (the chunk capacity); `cnt` of them are
+// live in the current chunk.
+struct ActLayout {
+    int rho, rhop, cap, cnt;
+    uint32_t planes, sums, xs, nsq, junk, total;
+    __host__ __device__ ActLayout(int rows, int na, int cap_, int nsb, int cnt_ = -1)
+        : rho(2 * rows), rhop(16 * na), cap(cap_), cnt(cnt_ < 0 ? cap_ : cnt_) {
+        planes = 0;
+        sums = planes + (uint32_t)cap * 8 * 4 * rho * 8;
+        xs = sums + (uint32_t)cap * rhop * 16;
+        nsq = xs + (uint32_t)cap * rhop * 4;
+        junk = nsq + (uint32_t)rows * nsb * 4;
+        total = (junk + 16 + 15) & ~15u;
+    }
+};
+
+// Quantizes super-blocks [c0, c0 + cnt) of every row into LDS. Wave w owns
+// the chunk's super-blocks w, w + kWaves, ...; its (row, super-block) units
+// are taken two at a time, one per half wave, where lane s of the half
+// quantizes elements [8s, 8s + 8) (sub-block s/4, MFMA slice s%4). All loads
+// of a batch are issued before any is used; stores are branch-free (a unit
+// past the end writes to a scratch slot).
+__device__ void act_prologue(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, int c0, int nsb) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int half = lane >> 5, s = lane & 31;
+    const int M = A.rows, K = A.K;
+    const int mine = wave < L.cnt ? (L.cnt - wave + kWaves - 1) / kWaves : 0;
+    const int units = mine * M;  // row-major: unit u = (row u / mine, my super-block u % mine)
+    constexpr int kPairs = 4;    // unit pairs per batch
+    float *nsq = reinterpret_cast<float *>(lds + L.nsq);
+    float *xsv = reinterpret_cast<float *>(lds + L.xs);
+    int16_t *sums = reinterpret_cast<int16_t *>(lds + L.sums);
+    uint8_t *junk = lds + L.junk;
+    const int jl = s >> 2, g = s & 3;
+    int m_run = 0, ii_run = 0;   // unit q0 as (row, super-block), wave-uniform
+    for (int q0 = 0; q0 < units; q0 += 2 * kPairs) {
+        // (row, super-block) of the batch's units: a scalar walk, no division
+        int um[2 * kPairs], uii[2 * kPairs];
+#pragma unroll
+        for (int q = 0; q < 2 * kPairs; q++) {
+            um[q] = min(m_run, M - 1);
+            uii[q] = ii_run;
+            if (++ii_run == mine) {
+                ii_run = 0;
+                ++m_run;
+            }
+        }
+        float4 xa[kPairs], xb[kPairs], ga[kPairs], gb[kPairs];
+#pragma unroll
+        for (int p = 0; p < kPairs; p++) {
+            const int m = half ? um[2 * p + 1] : um[2 * p];
+            const int ii = half ? uii[2 * p + 1] : uii[2 * p];
+            const int k = (c0 + wave + kWaves * ii) * 256 + s * 8;
+            const float *src = A.x + (size_t)m * K + k;
+            xa[p] = *reinterpret_cast<const float4 *>(src);
+            xb[p] = *reinterpret_cast<const float4 *>(src + 4);
+            if (A.norm) {
+                ga[p] = *reinterpret_cast<const float4 *>(A.norm + k);
+                gb[p] = *reinterpret_cast<const float4 *>(A.norm + k + 4);
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < kPairs; p++) {
+            const bool valid = q0 + 2 * p + half < units;
+            const int m = half ? um[2 * p + 1] : um[2 * p];
+            const int ii = half ? uii[2 * p + 1] : uii[2 * p];
+            const int sbl = wave + kWaves * ii;
+            float v[8] = {xa[p].x, xa[p].y, xa[p].z, xa[p].w, xb[p].x, xb[p].y, xb[p].z, xb[p].w};
+            if (A.norm) {
+                float t = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) t = fmaf(v[i], v[i], t);
+                t = row_sum(t);
+                const float tot = half ? rdl(t, 32) + rdl(t, 48) : rdl(t, 0) + rdl(t, 16);
+                float *dst = valid ? nsq + m * nsb + c0 + sbl : reinterpret_cast<float *>(junk);
+                *dst = tot;
+                const float gg[8] = {ga[p].x, ga[p].y, ga[p].z, ga[p].w, gb[p].x, gb[p].y, gb[p].z, gb[p].w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = __fmul_rn(v[i], gg[i]);
+            }
+            float a = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
+                            fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
+            a = row_max(a);
+            const float amax = half ? fmaxf(rdl(a, 32), rdl(a, 48)) : fmaxf(rdl(a, 0), rdl(a, 16));
+            // xs * inv ~ 1 keeps every value exact to the quantization step;
+            // the reciprocal keeps |v * inv| <= kQMax + 2^-10, so no clamp.
+            const float xs = amax * (1.0f / (float)kQMax);
+            const float inv = amax > 0.0f ? (float)kQMax * __builtin_amdgcn_rcpf(amax) : 0.0f;
+            int q[8], hsum = 0, qsum = 0;
+            uint32_t hb[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                q[i] = (int)rintf(v[i] * inv);
+                hb[i] = (uint32_t)(q[i] + 128);  // high plane h = (q + 128) >> 8 sits in byte 1
+                hsum += (int)hb[i] >> 8;
+                qsum += q[i];
+            }
+            // l = q - 256 h has the low byte of q; h the second byte of q + 128
+            const uint32_t l0 = __builtin_amdgcn_perm((uint32_t)q[1], (uint32_t)q[0], 0x0c0c0400u) |
+                                (__builtin_amdgcn_perm((uint32_t)q[3], (uint32_t)q[2], 0x0c0c0400u) << 16);
+            const uint32_t l1 = __builtin_amdgcn_perm((uint32_t)q[5], (uint32_t)q[4], 0x0c0c0400u) |
+                                (__builtin_amdgcn_perm((uint32_t)q[7], (uint32_t)q[6], 0x0c0c0400u) << 16);
+            const uint32_t h0 = __builtin_amdgcn_perm(hb[1], hb[0], 0x0c0c0501u) |
+                                (__builtin_amdgcn_perm(hb[3], hb[2], 0x0c0c0501u) << 16);
+            const uint32_t h1 = __builtin_amdgcn_perm(hb[5], hb[4], 0x0c0c0501u) |
+                                (__builtin_amdgcn_perm(hb[7], hb[6], 0x0c0c0501u) << 16);
+            const int j = sbl * 8 + jl;
+            uint8_t *hp = valid ? lds + L.planes + ((uint32_t)(j * 4 + g) * L.rho + m) * 8 : junk;
+            uint8_t *lp = valid ? lds + L.planes + ((uint32_t)(j * 4 + g) * L.rho + M + m) * 8 : junk;
+            *reinterpret_cast<uint2 *>(hp) = make_uint2(h0, h1);
+            *reinterpret_cast<uint2 *>(lp) = make_uint2(l0, l1);
+            // sub-block (4 lanes) sums of both planes: sum l = sum q - 256 sum h
+            hsum = quad_sum(hsum);
+            qsum = quad_sum(qsum);
+            int16_t *sh = valid ? sums + ((uint32_t)sbl * L.rhop + m) * 8 + jl : reinterpret_cast<int16_t *>(junk);
+            int16_t *sl = valid ? sums + ((uint32_t)sbl * L.rhop + M + m) * 8 + jl : reinterpret_cast<int16_t *>(junk);
+            *sh = (int16_t)hsum;
+            *sl = (int16_t)(qsum - 256 * hsum);
+            float *xh = valid ? xsv + (uint32_t)sbl * L.rhop + m : reinterpret_cast<float *>(junk);
+            float *xl = valid ? xsv + (uint32_t)sbl * L.rhop + M + m : reinterpret_cast<float *>(junk);
+            *xh = xs;
+            *xl = xs;
+        }
+    }
+    // rows past 2M of the padded tables read as zero
+    for (int idx = threadIdx.x; idx < L.cnt * L.rhop; idx += kThreads) {
+        const int rho = idx % L.rhop;
+        if (rho >= L.rho) {
+            xsv[idx] = 0.0f;
+            *reinterpret_cast<uint4 *>(lds + L.sums + (uint32_t)idx * 16) = make_uint4(0, 0, 0, 0);
+        }
+    }
+}
+
+// Staged weight bytes of one 16-row tile for one super-block.
+struct Q4Stage {
+    i32x4 hdr;      // d | dmin, 12 scale bytes
+    uint64_t qs[4]; // bytes [16 + 32p + 8g, +8) for p = 0..3
+};
+struct Q6Stage {
+    uint64_t ql[4]; // [n][half]: bytes n*64 + half*32 + 8g
+    uint64_t qh[2]; // bytes 128 + n*32 + 8g
+    i32x4 sc;       // 16 int8 scales
+    uint32_t d;     // f16 bits
+};
+
+template <int DT> struct StageOf;
+template <> struct StageOf<kQ4K> { using T = Q4Stage; };
+template <> struct StageOf<kQ6K> { using T = Q6Stage; };
+
+__device__ __forceinline__ void issue(Q4Stage &S, __amdgpu_buffer_rsrc_t rs, uint32_t row_off, int g) {
+    S.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, row_off, 0, 0);
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+        S.qs[p] = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rs, row_off + 16 + 32 * p + 8 * g, 0, 0));
+}
+
+__device__ __forceinline__ void issue(Q6Stage &S, __amdgpu_buffer_rsrc_t rs, uint32_t row_off, int g) {
+#pragma unroll
+    for (int n = 0; n < 2; n++) {
+        S.ql[2 * n] = load8_a2(rs, row_off + n * 64 + 8 * g);
+        S.ql[2 * n + 1] = load8_a2(rs, row_off + n * 64 + 32 + 8 * g);
+        S.qh[n] = load8_a2(rs, row_off + 128 + n * 32 + 8 * g);
+    }
+    const uint32_t a = row_off + 192;
+    typedef __attribute__((ext_vector_type(4))) int v4;
+    if ((a & 3u) == 0) {
+        S.sc = __builtin_amdgcn_raw_buffer_load_b128(rs, a, 0, 0);
+        S.d = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, a + 16, 0, 0) & 0xffffu;
+    } else {  // a = 2 mod 4
+        const v4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, a - 2, 0, 0);
+        const uint32_t w4 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, a + 14, 0, 0);
+        S.sc[0] = (int)__builtin_amdgcn_alignbyte((uint32_t)w[1], (uint32_t)w[0], 2);
+        S.sc[1] = (int)__builtin_amdgcn_alignbyte((uint32_t)w[2], (uint32_t)w[1], 2);
+        S.sc[2] = (int)__builtin_amdgcn_alignbyte((uint32_t)w[3], (uint32_t)w[2], 2);
+        S.sc[3] = (int)__builtin_amdgcn_alignbyte(w4, (uint32_t)w[3], 2);
+        S.d = w4 >> 16;
+    }
+}
+
+// One tile, one super-block: int32 sums per plane row, then the FP32 update
+// acc += xs * (d * sum(sc * dot) - dmin * sum(min * xsum)).
+template <int NA>
+__device__ __forceinline__ void compute(const Q4Stage &S, const int64_t (&xa)[NA][8], const uint32_t (&sxp)[NA][4][4],
+                                        const float (&xsr)[NA][4], float (&acc)[NA][4]) {
+    const uint32_t h0 = (uint32_t)S.hdr[0], q0 = (uint32_t)S.hdr[1], q1 = (uint32_t)S.hdr[2], q2 = (uint32_t)S.hdr[3];
+    const float d = half_lo(h0), dmin = half_lo(h0 >> 16);
+    // getScaleMinK4 (tensor/quant.go:96-103) for all eight sub-blocks
+    const uint32_t sc_lo = q0 & 0x3f3f3f3fu;
+    const uint32_t sc_hi = (q2 & 0x0f0f0f0fu) | ((q0 >> 2) & 0x30303030u);
+    const uint32_t mn_lo = q1 & 0x3f3f3f3fu;
+    const uint32_t mn_hi = ((q2 >> 4) & 0x0f0f0f0fu) | ((q1 >> 2) & 0x30303030u);
+    const uint32_t mp[4] = {__builtin_amdgcn_perm(0u, mn_lo, 0x0c010c00u), __builtin_amdgcn_perm(0u, mn_lo, 0x0c030c02u),
+                            __builtin_amdgcn_perm(0u, mn_hi, 0x0c010c00u), __builtin_amdgcn_perm(0u, mn_hi, 0x0c030c02u)};
+    int acci[NA][4];
+#pragma unroll
+    for (int a = 0; a < NA; a++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acci[a][i] = 0;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const int64_t blo = (int64_t)(S.qs[p] & 0x0f0f0f0f0f0f0f0full);
+        const int64_t bhi = (int64_t)((S.qs[p] >> 4) & 0x0f0f0f0f0f0f0f0full);
+        const uint32_t scw = p < 2 ? sc_lo : sc_hi;
+        const int s0 = (int)__builtin_amdgcn_ubfe(scw, 16 * (p & 1), 8);
+        const int s1 = (int)__builtin_amdgcn_ubfe(scw, 16 * (p & 1) + 8, 8);
+#pragma unroll
+        for (int a = 0; a < NA; a++) {
+            const i32x4 c0 = mfma_i8(xa[a][2 * p], blo);
+            const i32x4 c1 = mfma_i8(xa[a][2 * p + 1], bhi);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acci[a][i] = mad24(s1, c1[i], mad24(s0, c0[i], acci[a][i]));
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < NA; a++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int mm = 0;
+#pragma unroll
+            for (int p = 0; p < 4; p++) mm = dot2(mp[p], sxp[a][i][p], mm);
+            acc[a][i] += xsr[a][i] * (d * (float)acci[a][i] - dmin * (float)mm);
+        }
+}
+
+template <int NA>
+__device__ __forceinline__ void compute(const Q6Stage &S, const int64_t (&xa)[NA][8], const uint32_t (&)[NA][4][4],
+                                        const float (&xsr)[NA][4], float (&acc)[NA][4], int g) {
+    const float d = half_lo(S.d);
+    int acci[NA][4];
+#pragma unroll
+    for (int a = 0; a < NA; a++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acci[a][i] = 0;
+    const bool first = g < 2;  // lanes holding elements 0..15 of each 32
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        const int n = c >> 2, qd = c & 3;
+        const uint64_t lo = (S.ql[2 * n + (qd & 1)] >> (4 * (qd >> 1))) & 0x0f0f0f0f0f0f0f0full;
+        const uint64_t hi = ((S.qh[n] >> (2 * qd)) & 0x0303030303030303ull) << 4;
+        const int64_t q = (int64_t)q6_to_i8(lo | hi);
+        const int64_t b0 = first ? q : 0, b1 = first ? 0 : q;
+        const uint32_t scw = (uint32_t)S.sc[c >> 1];
+        const int s0 = (int)(int8_t)__builtin_amdgcn_ubfe(scw, 16 * (c & 1), 8);
+        const int s1 = (int)(int8_t)__builtin_amdgcn_ubfe(scw, 16 * (c & 1) + 8, 8);
+#pragma unroll
+        for (int a = 0; a < NA; a++) {
+            const i32x4 c0 = mfma_i8(xa[a][c], b0);
+            const i32x4 c1 = mfma_i8(xa[a][c], b1);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acci[a][i] = mad24(s1, c1[i], mad24(s0, c0[i], acci[a][i]));
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < NA; a++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[a][i] += xsr[a][i] * (d * (float)acci[a][i]);
+}
+
+template <int NA>
+__device__ __forceinline__ void load_act(const uint8_t *lds, const ActLayout &L, int sbl, int r, int g,
+                                         int64_t (&xa)[NA][8], uint32_t (&sxp)[NA][4][4], float (&xsr)[NA][4],
+                                         bool want_sums) {
+#pragma unroll
+    for (int a = 0; a < NA; a++) {
+        const int rho = 16 * a + r;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            int64_t v = 0;
+            if (rho < L.rho) v = *reinterpret_cast<const int64_t *>(lds + L.planes + ((uint32_t)((sbl * 8 + j) * 4 + g) * L.rho + rho) * 8);
+            xa[a][j] = v;
+        }
+        const float4 xv = *reinterpret_cast<const float4 *>(lds + L.xs + ((uint32_t)sbl * L.rhop + 16 * a + 4 * g) * 4);
+        xsr[a][0] = xv.x;
+        xsr[a][1] = xv.y;
+        xsr[a][2] = xv.z;
+        xsr[a][3] = xv.w;
+        if (want_sums) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint4 sv = *reinterpret_cast<const uint4 *>(lds + L.sums + ((uint32_t)sbl * L.rhop + 16 * a + 4 * g + i) * 16);
+                sxp[a][i][0] = sv.x;
+                sxp[a][i][1] = sv.y;
+                sxp[a][i][2] = sv.z;
+                sxp[a][i][3] = sv.w;
+            }
+        }
+    }
+}
+
+// Prefetch depth (super-blocks in flight per wave).
+template <int DT, int TT> struct Depth { static constexpr int value = DT == kQ4K ? (TT == 1 ? 3 : 2) : 2; };
+
+// One K chunk: the wave's first super-blocks are requested before the
+// activation prologue runs, so HBM latency overlaps the quantization; the
+// rest stream through a ring of Depth register stages. Wave w owns the
+// chunk's super-blocks w, w + kWaves, ...
+template <int DT, int TT, int NA>
+__device__ __forceinline__ void chunk_pass(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, int c0, int nsb,
+                                           const __amdgpu_buffer_rsrc_t (&rs)[TT], const uint32_t (&row_off)[TT],
+                                           float (&acc)[TT][NA][4], bool prologue, uint64_t &t_pro) {
+    using Stage = typename StageOf<DT>::T;
+    constexpr int D = Depth<DT, TT>::value;
+    constexpr uint32_t blk = DT == kQ4K ? 144u : 210u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15, g = lane >> 4;
+    const int mine = wave < L.cnt ? (L.cnt - wave + kWaves - 1) / kWaves : 0;
+    Stage st[D][TT];
+#pragma unroll
+    for (int d = 0; d < D; d++)
+        if (d < mine) {
+#pragma unroll
+            for (int t = 0; t < TT; t++) issue(st[d][t], rs[t], row_off[t] + (uint32_t)(c0 + wave + kWaves * d) * blk, g);
+        }
+    if (prologue) {
+        act_prologue(A, L, lds, c0, nsb);
+        __syncthreads();
+        YK_FG_STAMP(t_pro);
+    }
+    for (int base = 0; base < mine; base += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int i = base + d;
+            if (i < mine) {
+                int64_t xa[NA][8];
+                uint32_t sxp[NA][4][4];
+                float xsr[NA][4];
+                load_act<NA>(lds, L, wave + kWaves * i, r, g, xa, sxp, xsr, DT == kQ4K);
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    if constexpr (DT == kQ4K) compute<NA>(st[d][t], xa, sxp, xsr, acc[t]);
+                    else compute<NA>(st[d][t], xa, sxp, xsr, acc[t], g);
+                }
+                if (i + D < mine) {
+#pragma unroll
+                    for (int t = 0; t < TT; t++)
+                        issue(st[d][t], rs[t], row_off[t] + (uint32_t)(c0 + wave + kWaves * (i + D)) * blk, g);
+                }
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return __fmul_rn(__fmul_rn(g, sigmoid_ref(g)), u); }
+
+// TT: 16-row tiles per group (for SwiGLU, TT/2 gate tiles then TT/2 up tiles
+// over the same rows). NA: 16-row A tiles (rows <= 8: 1, <= 16: 2).
+// DTM: kQ4K or kQ6K for single-dtype launches, 0 for a per-segment switch.
+template <int DTM, int TT, int NA>
+__global__ __launch_bounds__(kThreads) void fgemm_kernel(const FusedGemmArgs A) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15;
+    const bool swiglu = A.epilogue == kEpiSwiglu;
+    const int rows_out = swiglu ? 8 * TT : 16 * TT;  // output rows of one group
+    const int nsb = A.K / 256;
+    const int M = A.rows;
+    const ActLayout L0(M, NA, min(A.chunk_sb, nsb), nsb);
+    const bool one_chunk = A.chunk_sb >= nsb;  // activations stay in LDS across groups
+    float *inv_rms = reinterpret_cast<float *>(lds + L0.total);
+    float *red = reinterpret_cast<float *>(lds + L0.total + 64);
+    uint64_t t_start = 0, t_pro = 0, t_loop = 0, t_end = 0;
+    YK_FG_STAMP(t_start);
+
+    for (int grp = blockIdx.x; grp < A.groups; grp += gridDim.x) {
+        int s = 0;
+#pragma unroll
+        for (int i = 1; i < kFusedMaxSeg; i++)
+            if (i < A.nseg && grp >= A.seg[i].wg_begin) s = i;
+        const int n0 = (grp - A.seg[s].wg_begin) * rows_out;
+        const int N = A.seg[s].n;
+        __amdgpu_buffer_rsrc_t rs[TT];
+        uint32_t row_off[TT];
+        const int dt = A.seg[s].dtype;
+#pragma unroll
+        for (int t = 0; t < TT; t++) {
+            const FusedSeg &S = A.seg[swiglu && t >= TT / 2 ? 1 : s];
+            const int tile_row = swiglu ? (t % (TT / 2)) * 16 : t * 16;
+            const int n = min(n0 + tile_row + r, N - 1);
+            rs[t] = __builtin_amdgcn_make_buffer_rsrc((void *)S.w, (short)0, (int)S.w_bytes, 0x00020000);
+            row_off[t] = (uint32_t)n * S.row_bytes;
+        }
+
+        float acc[TT][NA][4];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int a = 0; a < NA; a++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[t][a][i] = 0.0f;
+
+        const bool first = grp == (int)blockIdx.x;
+        for (int c0 = 0; c0 < nsb; c0 += A.chunk_sb) {
+            const ActLayout L(M, NA, min(A.chunk_sb, nsb), nsb, min(A.chunk_sb, nsb - c0));
+            const bool pro = first || !one_chunk;
+            if (c0 && pro) __syncthreads();  // previous chunk's LDS reads are done
+            if constexpr (DTM != 0) chunk_pass<DTM, TT, NA>(A, L, lds, c0, nsb, rs, row_off, acc, pro, t_pro);
+            else if (dt == kQ4K) chunk_pass<kQ4K, TT, NA>(A, L, lds, c0, nsb, rs, row_off, acc, pro, t_pro);
+            else chunk_pass<kQ6K, TT, NA>(A, L, lds, c0, nsb, rs, row_off, acc, pro, t_pro);
+        }
+
+        // ---- epilogue: fixed-order sum of the waves' partials
+        if (first) YK_FG_STAMP(t_loop);
+        __syncthreads();  // previous group's partials consumed; this group's LDS reads done
+        if (A.norm && first && threadIdx.x < M) {
+            const float *nsq = reinterpret_cast<const float *>(lds + L0.nsq);
+            double sum = 0.0;
+            for (int sb = 0; sb < nsb; sb++) sum += (double)nsq[threadIdx.x * nsb + sb];
+            const float mean = (float)(sum / (double)A.K);
+            inv_rms[threadIdx.x] = (float)(1.0 / sqrt((double)(mean + A.eps)));
+        }
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int a = 0; a < NA; a++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) red[(((wave * TT + t) * NA + a) * 4 + i) * 64 + lane] = acc[t][a][i];
+        __syncthreads();
+        auto partial = [&](int t, int rho, int col) {
+            const int a = rho >> 4, g = (rho & 15) >> 2, i = rho & 3;
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) v += red[(((w * TT + t) * NA + a) * 4 + i) * 64 + g * 16 + col];
+            return v;
+        };
+        auto value = [&](int t, int m, int col) {
+            float v = 256.0f * partial(t, m, col) + partial(t, M + m, col);
+            if (A.norm) v *= inv_rms[m];
+            return v;
+        };
+        for (int idx = threadIdx.x; idx < rows_out * M; idx += kThreads) {
+            const int m = idx / rows_out, rr = idx % rows_out;
+            const int n = n0 + rr;
+            if (n >= N) continue;
+            const int t = rr >> 4, col = rr & 15;
+            const size_t o = (size_t)m * N + n;
+            if (swiglu) {
+                const float gv = value(t, m, col), uv = value(t + TT / 2, m, col);
+                A.seg[0].out[o] = silu_mul(gv, uv);
+            } else {
+                float v = value(t, m, col);
+                if (A.epilogue == kEpiResidual) v += A.seg[s].res[o];
+                A.seg[s].out[o] = v;
+            }
+        }
+        if (first) YK_FG_STAMP(t_end);
+    }
+#ifdef YK_FG_TIMING
+    if (yk_fg_dbg && lane == 0) {
+        uint64_t *d = yk_fg_dbg + ((size_t)blockIdx.x * kWaves + wave) * 4;
+        d[0] = t_start;
+        d[1] = t_pro;
+        d[2] = t_loop;
+        d[3] = t_end;
+    }
+#else
+    (void)t_start; (void)t_pro; (void)t_loop; (void)t_end;
+#endif
+}
+
+}  // namespace
+
+uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt) {
+    const int na = rows <= 8 ? 1 : 2;
+    const int nsb = K / 256;
+    const ActLayout L(rows, na, std::min(chunk_sb, nsb), nsb);
+    return L.total + 64 + (uint32_t)kWaves * tt * na * 4 * 64 * 4;
+}
+
+int fused_gemm_chunk_sb(int rows, int K, int tt) {
+    const int nsb = K / 256;
+    for (int c = nsb; c >= 1; c--)
+        if (fused_gemm_lds_bytes(rows, K, c, tt) <= kFusedLds) return c;
+    return 0;
+}
+
+template <int DTM, int TT, int NA>
+static hipError_t launch_tt(const FusedGemmArgs &a, unsigned grid, uint32_t lds, hipStream_t s) {
+    auto k = fgemm_kernel<DTM, TT, NA>;
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr = true;
+    }
+    k<<<grid, kThreads, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+template <int DTM>
+static hipError_t launch_dt(const FusedGemmArgs &a, int tt, unsigned grid, uint32_t lds, hipStream_t s) {
+    const bool na1 = a.rows <= 8;
+    switch (tt) {
+    case 1: return na1 ? launch_tt<DTM, 1, 1>(a, grid, lds, s) : launch_tt<DTM, 1, 2>(a, grid, lds, s);
+    case 2: return na1 ? launch_tt<DTM, 2, 1>(a, grid, lds, s) : launch_tt<DTM, 2, 2>(a, grid, lds, s);
+    case 4:
+        if constexpr (DTM == kQ4K) return na1 ? launch_tt<DTM, 4, 1>(a, grid, lds, s) : launch_tt<DTM, 4, 2>(a, grid, lds, s);
+        return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s) {
+    const int rows_out = a.epilogue == kEpiSwiglu ? 8 * tt : 16 * tt;
+    FusedGemmArgs b = a;
+    unsigned grid = 0;
+    for (int i = 0; i < b.nseg; i++) {
+        b.seg[i].wg_begin = (int)grid;
+        if (b.epilogue == kEpiSwiglu && i == 1) {  // the up matrix shares the gate's groups
+            b.seg[i].wg_begin = 1 << 30;
+            continue;
+        }
+        grid += (unsigned)((b.seg[i].n + rows_out - 1) / rows_out);
+    }
+    b.groups = (int)grid;
+    const int nsb = b.K / 256;
+    // One-chunk launches run persistent group loops: the activations are
+    // quantized once per workgroup, then every further group only streams
+    // weights.
+    if (b.chunk_sb >= nsb && grid > (unsigned)kFusedMaxGrid) grid = kFusedMaxGrid;
+    const uint32_t lds = fused_gemm_lds_bytes(b.rows, b.K, b.chunk_sb, tt);
+    bool mixed = false;
+    for (int i = 1; i < b.nseg; i++) mixed |= b.seg[i].dtype != b.seg[0].dtype;
+    if (mixed) return launch_dt<0>(b, tt, grid, lds, s);
+    if (b.seg[0].dtype == kQ4K) return launch_dt<kQ4K>(b, tt, grid, lds, s);
+    return launch_dt<kQ6K>(b, tt, grid, lds, s);
+}
+
+}  // namespace yk

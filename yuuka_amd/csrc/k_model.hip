@@ -12,6 +12,7 @@
 #include <hip/hip_fp16.h>
 
 #include "model_kernels.h"
+#include "refmath.h"
 
 namespace yk {
 namespace {
@@ -43,9 +44,6 @@ __device__ __forceinline__ uint16_t ref_f32_to_f16(float f) {
     return (uint16_t)(sign | (uint16_t)((exp + 15) << 10) | (uint16_t)(rounded >> 13));
 }
 
-__device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + (float)exp((double)(-x))); }
-__device__ __forceinline__ float silu_ref(float x) { return __fmul_rn(x, sigmoid_ref(x)); }
-__device__ __forceinline__ float softplus_ref(float x) { return x > 20.0f ? x : (float)log1p(exp((double)x)); }
 
 __device__ __forceinline__ int cur_pos(const ModelDyn &dyn) { return dyn.pos_dev ? *dyn.pos_dev : dyn.pos; }
 

@@ -4,14 +4,10 @@
 #include <hip/hip_runtime.h>
 
 #include "ops.h"
+#include "refmath.h"
 
 namespace yk {
 namespace {
-
-__device__ __forceinline__ float sigmoid_ref(float x) {
-    // 1/(1+float32(exp(float64(-x)))) as model/qwen35/forward.go:552-554.
-    return 1.0f / (1.0f + (float)exp((double)(-x)));
-}
 
 __global__ __launch_bounds__(256) void add_kernel(float *__restrict__ dst, const float *__restrict__ a,
                                                   const float *__restrict__ b, uint64_t n) {

@@ -4,6 +4,7 @@
 // documented in include/yuuka_hip.h.
 #include "ops.h"
 
+#include "fgemm.h"
 #include "model_kernels.h"
 
 namespace yk {
@@ -55,6 +56,58 @@ static GdnArgs gdn_args(const yuuka_op &op) {
     g.eps = op.f[0];
     g.q_scale = op.f[1];
     return g;
+}
+
+// GEMM_FUSED: leading non-null weight buffers (2..5) are the segments.
+static int fused_segments(const yuuka_op &op) {
+    int n = 0;
+    while (n < kFusedMaxSeg && op.buf[2 + n]) n++;
+    return n;
+}
+
+// Tiles per workgroup: the largest of 4, 2, 1 that still gives every CU
+// work (about 2 workgroups per CU); Q6_K holds more staging registers and
+// stops at 2. YUUKA_FGEMM_TT overrides (tuning).
+static int fused_tiles(const yuuka_op &op, int nseg) {
+    uint64_t tiles = 0;
+    bool q6 = false;
+    for (int i = 0; i < nseg; i++) {
+        tiles += (op.n[2 + i] + 15) / 16;
+        q6 |= ((op.u[0] >> (8 * i)) & 0xff) == YUUKA_DTYPE_Q6_K;
+    }
+    int tt = 1;
+    if (!q6 && tiles >= 4 * 1024) tt = 4;
+    else if (tiles >= 2 * 256) tt = 2;
+    if (const char *e = getenv("YUUKA_FGEMM_TT")) {
+        const int v = atoi(e);
+        if (v == 1 || v == 2 || v == 4) tt = v;
+    }
+    if (q6 && tt > 2) tt = 2;
+    if (op.u[1] == kEpiSwiglu && tt < 2) tt = 2;
+    return tt;
+}
+
+static FusedGemmArgs fused_args(const yuuka_op &op) {
+    FusedGemmArgs a{};
+    a.x = at<const float>(op, 0);
+    a.norm = at<const float>(op, 1);
+    a.eps = op.f[0];
+    a.K = (int)op.n[0];
+    a.rows = (int)op.n[1];
+    a.chunk_sb = 0;  // set with the tile count
+    a.epilogue = (int)op.u[1];
+    a.nseg = fused_segments(op);
+    for (int i = 0; i < a.nseg; i++) {
+        FusedSeg &g = a.seg[i];
+        g.dtype = (int)((op.u[0] >> (8 * i)) & 0xff);
+        g.n = (int)op.n[2 + i];
+        g.row_bytes = (uint32_t)row_bytes((uint32_t)g.dtype, op.n[0]);
+        g.w = at<const uint8_t>(op, 2 + i);
+        g.w_bytes = (uint32_t)(g.row_bytes * (uint64_t)g.n);
+        g.out = at<float>(op, 6 + i);
+        g.res = at<const float>(op, 10 + i);
+    }
+    return a;
 }
 
 static yuuka_status check_gdn(const GdnArgs &g, const char *what) {
@@ -211,6 +264,35 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         *ws = p.part_bytes + 256;
         return YUUKA_OK;
     }
+    case YUUKA_EXT_OP_GEMM_FUSED: {
+        const uint64_t K = op.n[0], rows = op.n[1];
+        const int nseg = fused_segments(op);
+        const uint32_t epi = op.u[1];
+        if (!K || K % 256 || K > 65536 || rows < 1 || rows > 16 || nseg == 0 || epi > kEpiSwiglu ||
+            (epi == kEpiSwiglu && nseg != 2) || op.off[0] % 16 || op.off[1] % 16 ||
+            !buf_ok(op.buf[0], op.off[0], K * rows * 4) || (op.buf[1] && !buf_ok(op.buf[1], op.off[1], K * 4)))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid GEMM_FUSED shape or activation buffers");
+        for (int i = 0; i < nseg; i++) {
+            const uint32_t dt = (op.u[0] >> (8 * i)) & 0xff;
+            const uint64_t N = op.n[2 + i];
+            if (dt != YUUKA_DTYPE_Q4_K && dt != YUUKA_DTYPE_Q6_K)
+                return fail(YUUKA_ERR_UNSUPPORTED, "GEMM_FUSED segment %d: dtype %u (Q4_K and Q6_K only)", i, dt);
+            const uint64_t wb = row_bytes(dt, K) * N;
+            if (!N || N > (1u << 24) || wb >= (1ull << 32) || !buf_ok(op.buf[2 + i], op.off[2 + i], wb) ||
+                (dt == YUUKA_DTYPE_Q4_K && op.off[2 + i] % 16) || op.off[2 + i] % 4)
+                return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED segment %d: weight buffer", i);
+            const bool writes = epi != kEpiSwiglu || i == 0;
+            if (writes && !buf_ok(op.buf[6 + i], op.off[6 + i], N * rows * 4))
+                return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED segment %d: output buffer", i);
+            if (epi == kEpiResidual && !buf_ok(op.buf[10 + i], op.off[10 + i], N * rows * 4))
+                return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED segment %d: residual buffer", i);
+        }
+        if (epi == kEpiSwiglu && (op.n[2] != op.n[3] || (op.u[0] & 0xff) != ((op.u[0] >> 8) & 0xff)))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED SwiGLU: gate and up must match");
+        if (fused_gemm_chunk_sb((int)rows, (int)K, fused_tiles(op, nseg)) < 1)
+            return fail(YUUKA_ERR_UNSUPPORTED, "GEMM_FUSED: activations do not fit LDS");
+        return YUUKA_OK;
+    }
     case YUUKA_EXT_OP_ACCEPT: {
         yuuka_accept_params p{};
         p.mode = op.u[0];
@@ -314,6 +396,13 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
         const GemmPlan p = gemm_plan(op.n[0], op.n[1], op.n[2], op.u[0]);
         err = launch_gemm_q(at<const uint8_t>(op, 0), op.u[0], at<const uint8_t>(op, 1), at<float>(op, 2), op.n[0],
                             op.n[1], op.n[2], p, ctx.ws, nullptr, s, at<const float>(op, 3));
+        break;
+    }
+    case YUUKA_EXT_OP_GEMM_FUSED: {
+        FusedGemmArgs a = fused_args(op);
+        const int tt = fused_tiles(op, a.nseg);
+        a.chunk_sb = fused_gemm_chunk_sb(a.rows, a.K, tt);
+        err = launch_fused_gemm(a, tt, s);
         break;
     }
     case YUUKA_EXT_OP_ACCEPT: {

@@ -2,6 +2,8 @@
 // embedding, paged KV write, paged attention, recurrent chunk, elementwise).
 #pragma once
 
+#include <cstdlib>
+
 #include "plan.h"
 
 namespace yk {

@@ -148,6 +148,14 @@ static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token,
 
 using namespace yk;
 
+namespace yk {
+yuuka_status plan_run_dynamic(yuuka_plan *plan, hipStream_t stream, const int32_t *dyn) {
+    yuuka_status st = prepare(plan);
+    if (st != YUUKA_OK) return st;
+    return run_ops(plan, stream, 0, 0, dyn, 1, nullptr, nullptr, 0, nullptr);
+}
+}  // namespace yk
+
 extern "C" {
 
 yuuka_status yuuka_plan_create(yuuka_device *dev, yuuka_plan **out) {

@@ -31,6 +31,10 @@ yuuka_status run_verify_gemm(hipStream_t stream, const void *w, uint32_t dtype, 
 uint64_t verify_gemm_ws_bytes(uint64_t n_in, uint64_t n_out, uint64_t rows, uint32_t dtype);
 uint32_t verify_gemm_tickets(uint64_t n_in, uint64_t n_out, uint64_t rows, uint32_t dtype);
 
+// Runs the plan's ops directly on `stream` (no graph), reading {token,
+// position} from the device buffer `dyn` exactly as a captured graph would.
+yuuka_status plan_run_dynamic(yuuka_plan *plan, hipStream_t stream, const int32_t *dyn);
+
 // Execution context handed to op executors.
 struct ExecCtx {
     hipStream_t stream;

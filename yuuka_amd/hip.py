@@ -25,8 +25,9 @@ F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 6, 8, 12, 13, 14
 OP = dict(
     SILU_MUL=9, ADD=10, COPY=11, GEMV_BATCH=17, RMSNORM_BATCH=18, RMSNORM_HEADS_BATCH=19,
     ROPE_BATCH=20, RECURRENT_CHUNK=23, EMBEDDING_BATCH=24, KV_WRITE_BATCH_PAGED=28,
-    ATTENTION_PREFILL_PAGED=29, LM_HEAD=37,
+    ATTENTION_PREFILL_PAGED=29, LM_HEAD=37, GEMM_FUSED=69,
 )
+EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
 FLAG_TAIL = 0x1
 
 ACCEPT_GREEDY, ACCEPT_STOCHASTIC = 0, 1
@@ -312,6 +313,21 @@ def accept_params(mode: int, batch: int, drafts: int, vocab: int, temperature: f
                   request_base: int = 0, row_stride: int = 0) -> yuuka_accept_params:
     return yuuka_accept_params(mode, batch, drafts, vocab, temperature, top_k, top_p, request_base,
                                seed, step, row_stride)
+
+
+def gemm_fused_op(plan: "Plan", x: Buffer, n_in: int, rows: int, segments, epilogue: int = 0,
+                  norm: Buffer | None = None, eps: float = 1e-6) -> None:
+    """Appends one GEMM_FUSED op. segments: [(w, dtype, n_out, out, residual)]
+    (out / residual may be None where the epilogue does not use them)."""
+    bufs = [None] * 14
+    bufs[0], bufs[1] = x, norm
+    n = [n_in, rows, 0, 0, 0, 0]
+    dt = 0
+    for i, (w, dtype, n_out, out, res) in enumerate(segments):
+        bufs[2 + i], bufs[6 + i], bufs[10 + i] = w, out, res
+        n[2 + i] = n_out
+        dt |= dtype << (8 * i)
+    plan.add(OP["GEMM_FUSED"], bufs, n=n, u=[dt, epilogue], f=[eps])
 
 
 class Plan:
