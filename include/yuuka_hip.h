@@ -385,6 +385,19 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
  *               0 out = y W^T, 1 out = y W^T + residual, 2 SwiGLU
  *               out_0 = SiLU(y W_0^T) * (y W_1^T) (two segments, same shape).
  *               rows <= 16. One launch, no workspace.
+ *   ROPE_TABLE: buf0 FP32 {cos, sin} [rows][rot_dim/2] of positions
+ *               position + n2 + row; n={rows, rot_dim, displacement};
+ *               f0 base (float64 angles as forward.go:495-514).
+ *   ATTN_VERIFY: gated paged attention of the verify rows with the per-head
+ *               q/k RMSNorm, RoPE and the KV write folded in: buf0 FP32 raw
+ *               q rows [rows][heads][2*head_dim] (q | gate), buf1 raw k rows
+ *               [rows][kv_dim], buf2 raw v rows, buf3 K pool, buf4 V pool,
+ *               buf5 FP32 out [rows][heads][head_dim], buf6 int32 block
+ *               table, buf7 q_norm [head_dim], buf8 k_norm [head_dim],
+ *               buf9 ROPE_TABLE output; n={kv_heads, heads, head_dim, kv_dim,
+ *               rows, displacement}; u={block_size, capacity, kv dtype (F32 or
+ *               F16), rot_dim}; f={scale, eps}. Writes the rows' K/V to the
+ *               pool at position + displacement + row.
  * YUUKA_EXT_FLAG_DEFER on RECURRENT_CHUNK: compute the outputs of every row
  * but leave both states untouched (verify mode; see GDN_COMMIT). */
 #define YUUKA_EXT_OP_QUANTIZE_X 64u
@@ -393,6 +406,8 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
 #define YUUKA_EXT_OP_GDN_COMMIT 67u
 #define YUUKA_EXT_OP_ADVANCE 68u
 #define YUUKA_EXT_OP_GEMM_FUSED 69u
+#define YUUKA_EXT_OP_ROPE_TABLE 70u
+#define YUUKA_EXT_OP_ATTN_VERIFY 71u
 #define YUUKA_EXT_FLAG_DEFER 0x100u
 
 /* Timing events (extension): an event created with timing enabled, recorded

@@ -70,7 +70,8 @@ struct yuuka_q35 {
     // activations [max_rows][...]
     yuuka_buffer *x = nullptr, *xn = nullptr, *xq = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
                  *attn = nullptr, *z = nullptr, *gdn_out = nullptr, *fg = nullptr, *fu = nullptr, *logits = nullptr,
-                 *tokens = nullptr, *result = nullptr, *dyn = nullptr, *step = nullptr, *table = nullptr;
+                 *tokens = nullptr, *result = nullptr, *dyn = nullptr, *step = nullptr, *table = nullptr,
+                 *rope = nullptr;
     int32_t *pinned = nullptr;  // tokens staging {tokens[16], result[4]}
     hipEvent_t ev0 = nullptr, ev1 = nullptr;  // around the last graph replay
     bool eager = false;  // YUUKA_Q35_EAGER=1: launch plans op by op (profilers), no graphs
@@ -212,7 +213,23 @@ yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
                (uint64_t)c.inner},
               {(uint32_t)c.conv_kernel}, {c.eps, qscale}, YUUKA_EXT_FLAG_DEFER);
     };
+    // YUUKA_Q35_ATTN=0 selects the separate norm / RoPE / KV-write /
+    // attention ops (comparison); by default one ATTN_VERIFY op per layer.
+    const char *attn_env = getenv("YUUKA_Q35_ATTN");
+    const bool attn_fused = !(attn_env && attn_env[0] == '0');
+    bool any_attn = false;
+    for (const Layer &L : q->layers) any_attn |= !L.recurrent;
+    if (attn_fused && any_attn)
+        b.add(YUUKA_EXT_OP_ROPE_TABLE, {q->rope}, {R, (uint64_t)c.rope_dim, 0}, {}, {(float)c.rope_base});
     auto attention = [&](Layer &L) {
+        if (attn_fused) {
+            b.add(YUUKA_EXT_OP_ATTN_VERIFY,
+                  {q->q, q->k, q->v, L.kpool, L.vpool, q->attn, q->table, L.q_norm, L.k_norm, q->rope},
+                  {(uint64_t)c.kv_heads, (uint64_t)c.heads, hd, kvdim, R, 0},
+                  {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype, (uint32_t)c.rope_dim},
+                  {(float)(1.0 / std::sqrt((double)hd)), c.eps});
+            return;
+        }
         b.add(YUUKA_OP_RMSNORM_HEADS_BATCH, {q->k, L.k_norm, q->k}, {hd, (uint64_t)c.kv_heads, hd, R}, {}, {c.eps});
         b.add(YUUKA_OP_ROPE_BATCH, {q->k}, {(uint64_t)c.kv_heads, hd, hd, (uint64_t)c.rope_dim, R, kvdim}, {0},
               {(float)c.rope_base});
@@ -492,6 +509,7 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
         CHK(alloc(q.get(), M * kvdim * 4, &q->k));
         CHK(alloc(q.get(), M * kvdim * 4, &q->v));
         CHK(alloc(q.get(), M * c.heads * hd * 4, &q->attn));
+        CHK(alloc(q.get(), M * (uint64_t)(c.rope_dim / 2) * 8, &q->rope));
         CHK(alloc(q.get(), M * c.inner * 4, &q->z));
         CHK(alloc(q.get(), M * c.inner * 4, &q->gdn_out));
         CHK(alloc(q.get(), M * c.ffn * 4, &q->fg));

@@ -24,6 +24,15 @@ struct AttnArgs {
     float scale;
 };
 
+// Verify attention (k_attn.hip): one gated-attention layer's verify rows.
+struct AttnVArgs {
+    int kv_heads, heads, head_dim, kv_dim, rows, displacement, block_size, capacity;
+    uint32_t fmt;  // 0 F32, 1 F16 KV rows
+    int gated;     // 1: query rows hold [q | gate] per head (qwen35)
+    int rope_dim;  // rotated dimensions per head (pairs i, i + rope_dim/2)
+    float scale, eps;
+};
+
 struct GdnArgs {
     int rows, groups, rank, state, conv_dim, inner, kernel;
     float eps, q_scale;
@@ -42,6 +51,15 @@ hipError_t launch_kv_write(const float *k, const float *v, void *kpool, void *vp
                            hipStream_t s);
 uint64_t attention_scratch_bytes(const AttnArgs &a);
 // max_pos_hint: largest row position the call can see (host-known), or -1.
+int attn_verify_chunk(uint32_t fmt);
+uint64_t attn_verify_scratch_bytes(const AttnVArgs &a);
+uint32_t attn_verify_lds_bytes(const AttnVArgs &a);
+hipError_t launch_rope_table(float2 *tab, int rows, int rot_dim, double base, const ModelDyn &dyn, int displacement,
+                             hipStream_t s);
+hipError_t launch_attn_verify(const float *q, const float *k, const float *v, void *kpool, void *vpool,
+                              const int32_t *table, const float *q_norm, const float *k_norm, const float2 *rope,
+                              float *out, const AttnVArgs &a, void *scratch, const ModelDyn &dyn, int max_pos_hint,
+                              hipStream_t s);
 hipError_t launch_attention(const float *q, const void *kpool, const void *vpool, const int32_t *table, float *out,
                             const AttnArgs &a, void *scratch, const ModelDyn &dyn, int max_pos_hint, hipStream_t s);
 hipError_t launch_gdn_conv(const float *conv_state, const float *qkv, const float *w, float *out, const GdnArgs &g,

@@ -44,6 +44,25 @@ static AttnArgs attn_args(const yuuka_op &op) {
     return a;
 }
 
+static AttnVArgs attnv_args(const yuuka_op &op) {
+    AttnVArgs a{};
+    a.kv_heads = (int)op.n[0];
+    a.heads = (int)op.n[1];
+    a.head_dim = (int)op.n[2];
+    a.kv_dim = (int)op.n[3];
+    a.rows = (int)op.n[4];
+    a.displacement = (int)op.n[5];
+    a.block_size = (int)op.u[0];
+    a.capacity = (int)op.u[1];
+    bool ok;
+    a.fmt = kv_fmt(op.u[2], &ok);
+    a.gated = 1;
+    a.rope_dim = (int)op.u[3];
+    a.scale = op.f[0];
+    a.eps = op.f[1];
+    return a;
+}
+
 static GdnArgs gdn_args(const yuuka_op &op) {
     GdnArgs g;
     g.rows = (int)op.n[0];
@@ -125,6 +144,8 @@ bool op_uses_position(const yuuka_op &op) {
     case YUUKA_OP_ROPE_BATCH:
     case YUUKA_OP_KV_WRITE_BATCH_PAGED:
     case YUUKA_OP_ATTENTION_PREFILL_PAGED:
+    case YUUKA_EXT_OP_ROPE_TABLE:
+    case YUUKA_EXT_OP_ATTN_VERIFY:
         return true;
     default:
         return false;
@@ -226,6 +247,43 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
             !buf_ok(op.buf[4], op.off[4], blocks * 4))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "paged attention buffers too small");
         *ws = attention_scratch_bytes(a);
+        return YUUKA_OK;
+    }
+    case YUUKA_EXT_OP_ROPE_TABLE: {
+        const uint64_t rows = op.n[0], rot = op.n[1];
+        if (!rows || rows > 4096 || !rot || rot % 2 || rot > 128 || op.off[0] % 8 ||
+            !buf_ok(op.buf[0], op.off[0], rows * (rot / 2) * 8))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid ROPE_TABLE shape or buffer");
+        return YUUKA_OK;
+    }
+    case YUUKA_EXT_OP_ATTN_VERIFY: {
+        const AttnVArgs a = attnv_args(op);
+        bool ok;
+        kv_fmt(op.u[2], &ok);
+        if (!ok) return fail(YUUKA_ERR_UNSUPPORTED, "KV pool dtype %u (F32 and F16 are served)", op.u[2]);
+        if (a.rows <= 0 || a.rows > 16 || a.heads <= 0 || a.kv_heads <= 0 || a.heads % a.kv_heads ||
+            a.kv_dim != a.kv_heads * a.head_dim || a.block_size <= 0 || a.capacity < a.rows)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid verify attention dimensions");
+        if (a.head_dim % 64 || a.head_dim > 256 || a.rope_dim <= 0 || a.rope_dim % 2 || a.rope_dim > a.head_dim ||
+            a.rope_dim > 128)
+            return fail(YUUKA_ERR_UNSUPPORTED, "attention head dimension %d / rotation %d", a.head_dim, a.rope_dim);
+        if (attn_verify_lds_bytes(a) > 160 * 1024)
+            return fail(YUUKA_ERR_UNSUPPORTED, "verify attention: %d query rows per kv head do not fit LDS",
+                        a.rows * a.heads / a.kv_heads);
+        const uint64_t blocks = ((uint64_t)a.capacity + a.block_size - 1) / a.block_size;
+        const uint64_t R = (uint64_t)a.rows;
+        if (!buf_ok(op.buf[0], op.off[0], R * a.heads * 2 * a.head_dim * 4) ||
+            !buf_ok(op.buf[1], op.off[1], R * a.kv_dim * 4) || !buf_ok(op.buf[2], op.off[2], R * a.kv_dim * 4) ||
+            !op.buf[3] || !op.buf[4] || !buf_ok(op.buf[5], op.off[5], R * a.heads * a.head_dim * 4) ||
+            !buf_ok(op.buf[6], op.off[6], blocks * 4) || !buf_ok(op.buf[7], op.off[7], (uint64_t)a.head_dim * 4) ||
+            !buf_ok(op.buf[8], op.off[8], (uint64_t)a.head_dim * 4) ||
+            !buf_ok(op.buf[9], op.off[9], R * (a.rope_dim / 2) * 8))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify attention buffers too small");
+        const uint64_t esz = a.fmt == 1 ? 2 : 4;
+        const uint64_t pool = (uint64_t)blocks * a.block_size * a.kv_dim * esz;
+        if (op.buf[3]->bytes < pool || op.buf[4]->bytes < pool)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify attention: KV pool smaller than capacity");
+        *ws = attn_verify_scratch_bytes(a);
         return YUUKA_OK;
     }
     case YUUKA_OP_RECURRENT_CHUNK: {  // hip.go:1874-1934
@@ -372,6 +430,19 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
         const int hint = ctx.dyn ? -1 : (int)ctx.position + a.displacement + a.rows - 1;
         err = launch_attention(at<const float>(op, 0), at<const uint8_t>(op, 1), at<const uint8_t>(op, 2),
                                at<const int32_t>(op, 4), at<float>(op, 3), a, ctx.ws, dyn_of(ctx), hint, s);
+        break;
+    }
+    case YUUKA_EXT_OP_ROPE_TABLE:
+        err = launch_rope_table(at<float2>(op, 0), (int)op.n[0], (int)op.n[1], (double)op.f[0], dyn_of(ctx),
+                                (int)op.n[2], s);
+        break;
+    case YUUKA_EXT_OP_ATTN_VERIFY: {
+        const AttnVArgs a = attnv_args(op);
+        const int hint = ctx.dyn ? -1 : (int)ctx.position + a.displacement + a.rows - 1;
+        err = launch_attn_verify(at<const float>(op, 0), at<const float>(op, 1), at<const float>(op, 2),
+                                 at<uint8_t>(op, 3), at<uint8_t>(op, 4), at<const int32_t>(op, 6),
+                                 at<const float>(op, 7), at<const float>(op, 8), at<const float2>(op, 9),
+                                 at<float>(op, 5), a, ctx.ws, dyn_of(ctx), hint, s);
         break;
     }
     case YUUKA_OP_RECURRENT_CHUNK: {
