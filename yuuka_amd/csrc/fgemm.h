@@ -12,7 +12,6 @@ namespace yk {
 constexpr int kFusedMaxSeg = 4;
 constexpr int kFusedWaves = 8;                   // waves per workgroup (they split K)
 constexpr uint32_t kFusedLds = 160 * 1024;       // LDS per workgroup on gfx950
-constexpr int kFusedMaxGrid = 512;               // workgroups of a persistent (one-chunk) launch
 
 enum FusedEpilogue : int {
     kEpiStore = 0,     // out = y W^T
@@ -39,14 +38,15 @@ struct FusedGemmArgs {
     int chunk_sb;       // super-blocks of K quantized into LDS at a time
     int epilogue;       // FusedEpilogue
     int nseg;
-    int groups;         // tile groups over all segments (set by the launcher)
+    int groups;         // row tiles (16*tt rows) over all segments (set by the launcher)
+    int wk;             // waves splitting K in the streaming path (1, 2, 4 or 8; set by the launcher)
     FusedSeg seg[kFusedMaxSeg];
 };
 
 // Largest K chunk (in 256-element super-blocks) whose activations fit LDS
 // next to the partial-sum area of a tt-tile launch (0 if none fits).
-int fused_gemm_chunk_sb(int rows, int K, int tt);
-uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt);
+int fused_gemm_chunk_sb(int rows, int K, int tt, bool norm);
+uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt, bool norm);
 // tt: 16-row tiles per workgroup (1, 2 or 4; even for kEpiSwiglu).
 hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s);
 

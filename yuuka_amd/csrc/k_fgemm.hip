@@ -57,6 +57,18 @@ constexpr int kQMax = 32639;  // |q| bound that keeps the high plane in int8
 constexpr int kWaves = kFusedWaves;
 constexpr int kThreads = 64 * kWaves;
 
+// Keeps one ring stage's activation reads from being hoisted into the
+// previous stage (that multiplies live registers).
+#ifndef YK_FG_STAGE_FENCE
+#define YK_FG_STAGE_FENCE() __builtin_amdgcn_sched_barrier(0)
+#endif
+#ifndef YK_FG_PAIRS
+#define YK_FG_PAIRS 4
+#endif
+#ifndef YK_FG_DEPTH1
+#define YK_FG_DEPTH1 2
+#endif
+
 #ifdef YK_FG_TIMING
 // Phase timestamps per wave (builds with YK_FG_TIMING only; s_memrealtime,
 // 100 MHz): kernel start, prologue done, main loop done, group done.
@@ -129,6 +141,8 @@ __device__ __forceinline__ int quad_sum(int v) {
 
 // LDS layout of one K chunk, RHO = 2 * rows live A rows (h plane rows
 // 0..rows-1, l plane rows rows..2rows-1), RHOP = 16 * NA:
+//   raw    [cap][rows][256] float    (the chunk's x, copied straight from HBM)
+//   graw   [cap][256] float          (the chunk's norm weights)
 //   planes [cap * 8 sub-blocks][4 slices][RHO][8 B]
 //   sums   [cap][RHOP][8] int16      (sub-block sums of each plane row)
 //   xs     [cap][RHOP] float         (activation scale of each plane row)
@@ -138,10 +152,12 @@ __device__ __forceinline__ int quad_sum(int v) {
 // live in the current chunk.
 struct ActLayout {
     int rho, rhop, cap, cnt;
-    uint32_t planes, sums, xs, nsq, junk, total;
-    __host__ __device__ ActLayout(int rows, int na, int cap_, int nsb, int cnt_ = -1)
+    uint32_t raw, graw, planes, sums, xs, nsq, junk, total;
+    __host__ __device__ ActLayout(int rows, int na, int cap_, int nsb, bool norm, int cnt_ = -1)
         : rho(2 * rows), rhop(16 * na), cap(cap_), cnt(cnt_ < 0 ? cap_ : cnt_) {
-        planes = 0;
+        raw = 0;
+        graw = raw + (uint32_t)cap * rows * 1024;
+        planes = graw + (norm ? (uint32_t)cap * 1024 : 0u);
         sums = planes + (uint32_t)cap * 8 * 4 * rho * 8;
         xs = sums + (uint32_t)cap * rhop * 16;
         nsq = xs + (uint32_t)cap * rhop * 4;
@@ -150,58 +166,78 @@ struct ActLayout {
     }
 };
 
-// Quantizes super-blocks [c0, c0 + cnt) of every row into LDS. Wave w owns
-// the chunk's super-blocks w, w + kWaves, ...; its (row, super-block) units
-// are taken two at a time, one per half wave, where lane s of the half
-// quantizes elements [8s, 8s + 8) (sub-block s/4, MFMA slice s%4). All loads
-// of a batch are issued before any is used; stores are branch-free (a unit
-// past the end writes to a scratch slot).
-__device__ void act_prologue(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, int c0, int nsb) {
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+// Issues the chunk's activation (and norm weight) copies into LDS: one
+// 1 KB wave load per (row, super-block), no registers held.
+__device__ __forceinline__ void act_fetch(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, int c0) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int M = A.rows;
+    const int xunits = M * L.cnt, gunits = A.norm ? L.cnt : 0;
+    for (int u = wave; u < xunits + gunits; u += kWaves) {
+        const float *src;
+        uint32_t dst;
+        if (u < xunits) {
+            const int m = u / L.cnt, sbl = u - m * L.cnt;
+            src = A.x + (size_t)m * A.K + (size_t)(c0 + sbl) * 256 + lane * 4;
+            dst = L.raw + (uint32_t)(sbl * M + m) * 1024;
+        } else {
+            const int sbl = u - xunits;
+            src = A.norm + (size_t)(c0 + sbl) * 256 + lane * 4;
+            dst = L.graw + (uint32_t)sbl * 1024;
+        }
+        __builtin_amdgcn_global_load_lds((const void *)src, (lds_ptr_t)(lds + dst), 16, 0, 0);
+    }
+}
+
+// Quantizes super-blocks [c0, c0 + cnt) of every row from the LDS copy made
+// by act_fetch. Wave w owns the chunk's super-blocks w, w + kWaves, ...; its
+// (row, super-block) units are taken two at a time, one per half wave, where
+// lane s of the half quantizes elements [8s, 8s + 8) (sub-block s/4, MFMA
+// slice s%4). Stores are branch-free (a unit past the end writes to a
+// scratch slot).
+__device__ __forceinline__ void act_prologue(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, int c0,
+                                             int nsb) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int half = lane >> 5, s = lane & 31;
-    const int M = A.rows, K = A.K;
-    const int mine = wave < L.cnt ? (L.cnt - wave + kWaves - 1) / kWaves : 0;
-    const int units = mine * M;  // row-major: unit u = (row u / mine, my super-block u % mine)
-    constexpr int kPairs = 4;    // unit pairs per batch
+    const int M = A.rows;
+    const int total = M * L.cnt;                              // (row, super-block) units of the chunk
+    const int units = wave < total ? (total - wave + kWaves - 1) / kWaves : 0;  // mine: wave + kWaves*i
+    constexpr int kPairs = YK_FG_PAIRS;  // unit pairs per batch
     float *nsq = reinterpret_cast<float *>(lds + L.nsq);
     float *xsv = reinterpret_cast<float *>(lds + L.xs);
     int16_t *sums = reinterpret_cast<int16_t *>(lds + L.sums);
     uint8_t *junk = lds + L.junk;
+    const float *raw = reinterpret_cast<const float *>(lds + L.raw);
+    const float *graw = reinterpret_cast<const float *>(lds + L.graw);
     const int jl = s >> 2, g = s & 3;
-    int m_run = 0, ii_run = 0;   // unit q0 as (row, super-block), wave-uniform
+    // unit index -> (row, super-block): row-major over the chunk, u = m * cnt + sbl
     for (int q0 = 0; q0 < units; q0 += 2 * kPairs) {
-        // (row, super-block) of the batch's units: a scalar walk, no division
-        int um[2 * kPairs], uii[2 * kPairs];
-#pragma unroll
-        for (int q = 0; q < 2 * kPairs; q++) {
-            um[q] = min(m_run, M - 1);
-            uii[q] = ii_run;
-            if (++ii_run == mine) {
-                ii_run = 0;
-                ++m_run;
-            }
-        }
         float4 xa[kPairs], xb[kPairs], ga[kPairs], gb[kPairs];
+        int mq[kPairs], sq[kPairs];
 #pragma unroll
         for (int p = 0; p < kPairs; p++) {
-            const int m = half ? um[2 * p + 1] : um[2 * p];
-            const int ii = half ? uii[2 * p + 1] : uii[2 * p];
-            const int k = (c0 + wave + kWaves * ii) * 256 + s * 8;
-            const float *src = A.x + (size_t)m * K + k;
+            // this half's unit, from wave-uniform pieces (no per-lane array index)
+            const int ua = min(wave + kWaves * (q0 + 2 * p), total - 1);
+            const int ub = min(wave + kWaves * (q0 + 2 * p + 1), total - 1);
+            const int ma = ua / L.cnt, mb = ub / L.cnt;
+            const int sa = ua - ma * L.cnt, sbb = ub - mb * L.cnt;
+            mq[p] = ma + half * (mb - ma);
+            sq[p] = sa + half * (sbb - sa);
+            const float *src = raw + (sq[p] * M + mq[p]) * 256 + s * 8;
             xa[p] = *reinterpret_cast<const float4 *>(src);
             xb[p] = *reinterpret_cast<const float4 *>(src + 4);
             if (A.norm) {
-                ga[p] = *reinterpret_cast<const float4 *>(A.norm + k);
-                gb[p] = *reinterpret_cast<const float4 *>(A.norm + k + 4);
+                ga[p] = *reinterpret_cast<const float4 *>(graw + sq[p] * 256 + s * 8);
+                gb[p] = *reinterpret_cast<const float4 *>(graw + sq[p] * 256 + s * 8 + 4);
             }
         }
 #pragma unroll
         for (int p = 0; p < kPairs; p++) {
             const bool valid = q0 + 2 * p + half < units;
-            const int m = half ? um[2 * p + 1] : um[2 * p];
-            const int ii = half ? uii[2 * p + 1] : uii[2 * p];
-            const int sbl = wave + kWaves * ii;
+            const int m = mq[p], sbl = sq[p];
             float v[8] = {xa[p].x, xa[p].y, xa[p].z, xa[p].w, xb[p].x, xb[p].y, xb[p].z, xb[p].w};
             if (A.norm) {
                 float t = 0.0f;
@@ -426,7 +462,7 @@ __device__ __forceinline__ void load_act(const uint8_t *lds, const ActLayout &L,
 }
 
 // Prefetch depth (super-blocks in flight per wave).
-template <int DT, int TT> struct Depth { static constexpr int value = DT == kQ4K ? (TT == 1 ? 3 : 2) : 2; };
+template <int DT, int TT> struct Depth { static constexpr int value = DT == kQ4K && TT == 1 ? YK_FG_DEPTH1 : 2; };
 
 // One K chunk: the wave's first super-blocks are requested before the
 // activation prologue runs, so HBM latency overlaps the quantization; the
@@ -435,7 +471,8 @@ template <int DT, int TT> struct Depth { static constexpr int value = DT == kQ4K
 template <int DT, int TT, int NA>
 __device__ __forceinline__ void chunk_pass(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, int c0, int nsb,
                                            const __amdgpu_buffer_rsrc_t (&rs)[TT], const uint32_t (&row_off)[TT],
-                                           float (&acc)[TT][NA][4], bool prologue, uint64_t &t_pro) {
+                                           float (&acc)[TT][NA][4], bool prologue, uint64_t &t_pro,
+                                           uint64_t &t_wait) {
     using Stage = typename StageOf<DT>::T;
     constexpr int D = Depth<DT, TT>::value;
     constexpr uint32_t blk = DT == kQ4K ? 144u : 210u;
@@ -444,6 +481,7 @@ __device__ __forceinline__ void chunk_pass(const FusedGemmArgs &A, const ActLayo
     const int r = lane & 15, g = lane >> 4;
     const int mine = wave < L.cnt ? (L.cnt - wave + kWaves - 1) / kWaves : 0;
     Stage st[D][TT];
+    if (prologue) act_fetch(A, L, lds, c0);
 #pragma unroll
     for (int d = 0; d < D; d++)
         if (d < mine) {
@@ -451,6 +489,11 @@ __device__ __forceinline__ void chunk_pass(const FusedGemmArgs &A, const ActLayo
             for (int t = 0; t < TT; t++) issue(st[d][t], rs[t], row_off[t] + (uint32_t)(c0 + wave + kWaves * d) * blk, g);
         }
     if (prologue) {
+        // the LDS copies (issued before the weights) are complete once the
+        // counter drains; the weights are already in flight behind them
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        YK_FG_STAMP(t_wait);
         act_prologue(A, L, lds, c0, nsb);
         __syncthreads();
         YK_FG_STAMP(t_pro);
@@ -459,6 +502,7 @@ __device__ __forceinline__ void chunk_pass(const FusedGemmArgs &A, const ActLayo
 #pragma unroll
         for (int d = 0; d < D; d++) {
             const int i = base + d;
+            YK_FG_STAGE_FENCE();
             if (i < mine) {
                 int64_t xa[NA][8];
                 uint32_t sxp[NA][4][4];
@@ -484,33 +528,21 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return __fmul_rn(_
 // TT: 16-row tiles per group (for SwiGLU, TT/2 gate tiles then TT/2 up tiles
 // over the same rows). NA: 16-row A tiles (rows <= 8: 1, <= 16: 2).
 // DTM: kQ4K or kQ6K for single-dtype launches, 0 for a per-segment switch.
-template <int DTM, int TT, int NA>
-__global__ __launch_bounds__(kThreads) void fgemm_kernel(const FusedGemmArgs A) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int r = lane & 15;
-    const bool swiglu = A.epilogue == kEpiSwiglu;
-    const int rows_out = swiglu ? 8 * TT : 16 * TT;  // output rows of one group
-    const int nsb = A.K / 256;
-    const int M = A.rows;
-    const ActLayout L0(M, NA, min(A.chunk_sb, nsb), nsb);
-    const bool one_chunk = A.chunk_sb >= nsb;  // activations stay in LDS across groups
-    float *inv_rms = reinterpret_cast<float *>(lds + L0.total);
-    float *red = reinterpret_cast<float *>(lds + L0.total + 64);
-    uint64_t t_start = 0, t_pro = 0, t_loop = 0, t_end = 0;
-    YK_FG_STAMP(t_start);
-
-    for (int grp = blockIdx.x; grp < A.groups; grp += gridDim.x) {
-        int s = 0;
+// Row group `grp`: segment, first output row and the weight rows of its
+// tiles (uniform per workgroup).
+template <int TT>
+struct GroupRows {
+    int s, n0, N, dt;
+    __amdgpu_buffer_rsrc_t rs[TT];
+    uint32_t row_off[TT];
+    __device__ __forceinline__ GroupRows(const FusedGemmArgs &A, int grp, int rows_out, bool swiglu, int r) {
+        s = 0;
 #pragma unroll
         for (int i = 1; i < kFusedMaxSeg; i++)
             if (i < A.nseg && grp >= A.seg[i].wg_begin) s = i;
-        const int n0 = (grp - A.seg[s].wg_begin) * rows_out;
-        const int N = A.seg[s].n;
-        __amdgpu_buffer_rsrc_t rs[TT];
-        uint32_t row_off[TT];
-        const int dt = A.seg[s].dtype;
+        n0 = (grp - A.seg[s].wg_begin) * rows_out;
+        N = A.seg[s].n;
+        dt = A.seg[s].dtype;
 #pragma unroll
         for (int t = 0; t < TT; t++) {
             const FusedSeg &S = A.seg[swiglu && t >= TT / 2 ? 1 : s];
@@ -519,47 +551,165 @@ __global__ __launch_bounds__(kThreads) void fgemm_kernel(const FusedGemmArgs A) 
             rs[t] = __builtin_amdgcn_make_buffer_rsrc((void *)S.w, (short)0, (int)S.w_bytes, 0x00020000);
             row_off[t] = (uint32_t)n * S.row_bytes;
         }
+    }
+};
 
+// inv_rms of every row from the per super-block sums of squares (float64
+// sum in super-block order, the reference's formula).
+__device__ __forceinline__ void compute_inv_rms(const FusedGemmArgs &A, const ActLayout &L0, const uint8_t *lds,
+                                                float *inv_rms, int nsb) {
+    if (A.norm && threadIdx.x < (unsigned)A.rows) {
+        const float *nsq = reinterpret_cast<const float *>(lds + L0.nsq);
+        double sum = 0.0;
+        for (int sb = 0; sb < nsb; sb++) sum += (double)nsq[threadIdx.x * nsb + sb];
+        const float mean = (float)(sum / (double)A.K);
+        inv_rms[threadIdx.x] = (float)(1.0 / sqrt((double)(mean + A.eps)));
+    }
+}
+
+// Fixed-order sum of the waves' partials of one group, then the epilogue.
+template <int TT, int NA>
+__device__ __forceinline__ void group_epilogue(const FusedGemmArgs &A, float *red, const float *inv_rms,
+                                               const float (&acc)[TT][NA][4], int n0, int N, int s, int rows_out,
+                                               bool swiglu) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int M = A.rows;
+    __syncthreads();  // the previous group's partials are consumed
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int a = 0; a < NA; a++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) red[(((wave * TT + t) * NA + a) * 4 + i) * 64 + lane] = acc[t][a][i];
+    __syncthreads();
+    auto partial = [&](int t, int rho, int col) {
+        const int a = rho >> 4, g = (rho & 15) >> 2, i = rho & 3;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) v += red[(((w * TT + t) * NA + a) * 4 + i) * 64 + g * 16 + col];
+        return v;
+    };
+    auto value = [&](int t, int m, int col) {
+        float v = 256.0f * partial(t, m, col) + partial(t, M + m, col);
+        if (A.norm) v *= inv_rms[m];
+        return v;
+    };
+    for (int idx = threadIdx.x; idx < rows_out * M; idx += kThreads) {
+        const int m = idx / rows_out, rr = idx % rows_out;
+        const int n = n0 + rr;
+        if (n >= N) continue;
+        const int t = rr >> 4, col = rr & 15;
+        const size_t o = (size_t)m * N + n;
+        if (swiglu) {
+            const float gv = value(t, m, col), uv = value(t + TT / 2, m, col);
+            A.seg[0].out[o] = silu_mul(gv, uv);
+        } else {
+            float v = value(t, m, col);
+            if (A.epilogue == kEpiResidual) v += A.seg[s].res[o];
+            A.seg[s].out[o] = v;
+        }
+    }
+}
+
+// Single-dtype launch whose activations fit LDS in one piece. The eight
+// waves form A.wr row groups x A.wk K groups: a workgroup iteration covers
+// wr row tiles (16*TT rows each); wave (rg, kg) owns tile rg of the
+// iteration and super-blocks kg, kg + wk, ... of K. A wave's work is one
+// sequence of (iteration, super-block) items; its two register stages run
+// across iterations, so the next tile's weights are in flight while the
+// current one is stored. With wk = 1 (large launches such as the LM head) a
+// wave owns whole rows: no barrier after the prologue, each wave stores its
+// own results.
+template <int DT, int TT, int NA>
+__device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *lds, float *inv_rms, float *red,
+                                              int rows_out, bool swiglu) {
+    using Stage = typename StageOf<DT>::T;
+    constexpr uint32_t blk = DT == kQ4K ? 144u : 210u;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15, g = lane >> 4;
+    const int nsb = A.K / 256;
+    const int wk = A.wk, wr = kWaves / wk;
+    const int rg = wave / wk, kg = wave - rg * wk;
+    const ActLayout L(A.rows, NA, nsb, nsb, A.norm != nullptr);
+    const int mine = kg < nsb ? (nsb - kg + wk - 1) / wk : 0;  // super-blocks per tile
+    const int per_iter = (int)gridDim.x * wr;                   // row tiles per grid iteration
+    const int niter = (A.groups - (int)blockIdx.x * wr + per_iter - 1) / per_iter;
+    auto tile_of = [&](int k) { return ((int)blockIdx.x + k * (int)gridDim.x) * wr + rg; };
+    // my items: iterations whose tile exists, times my super-blocks
+    int ntile = 0;
+    for (int k = 0; k < niter; k++) ntile += tile_of(k) < A.groups ? 1 : 0;
+    const int total = ntile * mine;
+    int kq = 0, jq = 0;  // issue cursor (iteration, super-block index)
+    auto issue_next = [&](Stage (&S)[TT]) {
+        const GroupRows<TT> G(A, tile_of(kq), rows_out, swiglu, r);
+#pragma unroll
+        for (int t = 0; t < TT; t++) issue(S[t], G.rs[t], G.row_off[t] + (uint32_t)(kg + wk * jq) * blk, g);
+        if (++jq == mine) {
+            jq = 0;
+            ++kq;
+        }
+    };
+    Stage st[2][TT];
+    act_fetch(A, L, lds, 0);
+    if (total > 0) issue_next(st[0]);
+    if (total > 1) issue_next(st[1]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    act_prologue(A, L, lds, 0, nsb);
+    __syncthreads();
+    compute_inv_rms(A, L, lds, inv_rms, nsb);
+    __syncthreads();
+    int i = 0;
+    for (int k = 0; k < niter; k++) {
+        const int tile = tile_of(k);
+        const bool live = tile < A.groups;
         float acc[TT][NA][4];
 #pragma unroll
         for (int t = 0; t < TT; t++)
 #pragma unroll
             for (int a = 0; a < NA; a++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) acc[t][a][i] = 0.0f;
-
-        const bool first = grp == (int)blockIdx.x;
-        for (int c0 = 0; c0 < nsb; c0 += A.chunk_sb) {
-            const ActLayout L(M, NA, min(A.chunk_sb, nsb), nsb, min(A.chunk_sb, nsb - c0));
-            const bool pro = first || !one_chunk;
-            if (c0 && pro) __syncthreads();  // previous chunk's LDS reads are done
-            if constexpr (DTM != 0) chunk_pass<DTM, TT, NA>(A, L, lds, c0, nsb, rs, row_off, acc, pro, t_pro);
-            else if (dt == kQ4K) chunk_pass<kQ4K, TT, NA>(A, L, lds, c0, nsb, rs, row_off, acc, pro, t_pro);
-            else chunk_pass<kQ6K, TT, NA>(A, L, lds, c0, nsb, rs, row_off, acc, pro, t_pro);
+                for (int e = 0; e < 4; e++) acc[t][a][e] = 0.0f;
+        for (int j = 0; live && j < mine; j++, i++) {
+            int64_t xa[NA][8];
+            uint32_t sxp[NA][4][4];
+            float xsr[NA][4];
+            load_act<NA>(lds, L, kg + wk * j, r, g, xa, sxp, xsr, DT == kQ4K);
+            if ((i & 1) == 0) {
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    if constexpr (DT == kQ4K) compute<NA>(st[0][t], xa, sxp, xsr, acc[t]);
+                    else compute<NA>(st[0][t], xa, sxp, xsr, acc[t], g);
+                }
+                if (i + 2 < total) issue_next(st[0]);
+            } else {
+#pragma unroll
+                for (int t = 0; t < TT; t++) {
+                    if constexpr (DT == kQ4K) compute<NA>(st[1][t], xa, sxp, xsr, acc[t]);
+                    else compute<NA>(st[1][t], xa, sxp, xsr, acc[t], g);
+                }
+                if (i + 2 < total) issue_next(st[1]);
+            }
         }
-
-        // ---- epilogue: fixed-order sum of the waves' partials
-        if (first) YK_FG_STAMP(t_loop);
-        __syncthreads();  // previous group's partials consumed; this group's LDS reads done
-        if (A.norm && first && threadIdx.x < M) {
-            const float *nsq = reinterpret_cast<const float *>(lds + L0.nsq);
-            double sum = 0.0;
-            for (int sb = 0; sb < nsb; sb++) sum += (double)nsq[threadIdx.x * nsb + sb];
-            const float mean = (float)(sum / (double)A.K);
-            inv_rms[threadIdx.x] = (float)(1.0 / sqrt((double)(mean + A.eps)));
-        }
+        // ---- epilogue: sum the wk waves of this row group in a fixed order
+        const GroupRows<TT> G(A, live ? tile : 0, rows_out, swiglu, r);
+        float *myred = red + (size_t)rg * wk * TT * NA * 4 * 64;  // this row group's partials
+        if (wk > 1) __syncthreads();  // previous iteration's partials are consumed
 #pragma unroll
         for (int t = 0; t < TT; t++)
 #pragma unroll
             for (int a = 0; a < NA; a++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) red[(((wave * TT + t) * NA + a) * 4 + i) * 64 + lane] = acc[t][a][i];
-        __syncthreads();
+                for (int e = 0; e < 4; e++) myred[(((kg * TT + t) * NA + a) * 4 + e) * 64 + lane] = acc[t][a][e];
+        if (wk > 1) __syncthreads();
+        if (!live) continue;
+        const int M = A.rows;
         auto partial = [&](int t, int rho, int col) {
-            const int a = rho >> 4, g = (rho & 15) >> 2, i = rho & 3;
+            const int a = rho >> 4, gg = (rho & 15) >> 2, e = rho & 3;
             float v = 0.0f;
-#pragma unroll
-            for (int w = 0; w < kWaves; w++) v += red[(((w * TT + t) * NA + a) * 4 + i) * 64 + g * 16 + col];
+            for (int w = 0; w < wk; w++) v += myred[(((w * TT + t) * NA + a) * 4 + e) * 64 + gg * 16 + col];
             return v;
         };
         auto value = [&](int t, int m, int col) {
@@ -567,50 +717,102 @@ __global__ __launch_bounds__(kThreads) void fgemm_kernel(const FusedGemmArgs A) 
             if (A.norm) v *= inv_rms[m];
             return v;
         };
-        for (int idx = threadIdx.x; idx < rows_out * M; idx += kThreads) {
+        // the row group's wk waves share the stores
+        for (int idx = kg * 64 + lane; idx < rows_out * M; idx += wk * 64) {
             const int m = idx / rows_out, rr = idx % rows_out;
-            const int n = n0 + rr;
-            if (n >= N) continue;
+            const int n = G.n0 + rr;
+            if (n >= G.N) continue;
             const int t = rr >> 4, col = rr & 15;
-            const size_t o = (size_t)m * N + n;
+            const size_t o = (size_t)m * G.N + n;
             if (swiglu) {
                 const float gv = value(t, m, col), uv = value(t + TT / 2, m, col);
                 A.seg[0].out[o] = silu_mul(gv, uv);
             } else {
                 float v = value(t, m, col);
-                if (A.epilogue == kEpiResidual) v += A.seg[s].res[o];
-                A.seg[s].out[o] = v;
+                if (A.epilogue == kEpiResidual) v += A.seg[G.s].res[o];
+                A.seg[G.s].out[o] = v;
             }
         }
-        if (first) YK_FG_STAMP(t_end);
     }
-#ifdef YK_FG_TIMING
-    if (yk_fg_dbg && lane == 0) {
-        uint64_t *d = yk_fg_dbg + ((size_t)blockIdx.x * kWaves + wave) * 4;
-        d[0] = t_start;
-        d[1] = t_pro;
-        d[2] = t_loop;
-        d[3] = t_end;
+}
+
+template <int DTM, int TT, int NA>
+__global__ __launch_bounds__(kThreads) void fgemm_kernel(const FusedGemmArgs A) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int r = lane & 15;
+    const bool swiglu = A.epilogue == kEpiSwiglu;
+    const int rows_out = swiglu ? 8 * TT : 16 * TT;  // output rows of one group
+    const int nsb = A.K / 256;
+    const int M = A.rows;
+    const ActLayout L0(M, NA, min(A.chunk_sb, nsb), nsb, A.norm != nullptr);
+    const bool one_chunk = A.chunk_sb >= nsb;  // activations stay in LDS across groups
+    float *inv_rms = reinterpret_cast<float *>(lds + L0.total);
+    float *red = reinterpret_cast<float *>(lds + L0.total + 64);
+    if constexpr (DTM != 0) {
+        if (one_chunk) {
+            stream_groups<DTM, TT, NA>(A, lds, inv_rms, red, rows_out, swiglu);
+            return;
+        }
     }
-#else
-    (void)t_start; (void)t_pro; (void)t_loop; (void)t_end;
-#endif
+    uint64_t t_pro = 0, t_wait = 0;
+    for (int grp = blockIdx.x; grp < A.groups; grp += gridDim.x) {
+        const GroupRows<TT> G(A, grp, rows_out, swiglu, r);
+        float acc[TT][NA][4];
+#pragma unroll
+        for (int t = 0; t < TT; t++)
+#pragma unroll
+            for (int a = 0; a < NA; a++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[t][a][i] = 0.0f;
+        const bool first = grp == (int)blockIdx.x;
+        for (int c0 = 0; c0 < nsb; c0 += A.chunk_sb) {
+            const ActLayout L(M, NA, min(A.chunk_sb, nsb), nsb, A.norm != nullptr, min(A.chunk_sb, nsb - c0));
+            const bool pro = first || !one_chunk;
+            if (c0 && pro) __syncthreads();  // previous chunk's LDS reads are done
+            if constexpr (DTM != 0) chunk_pass<DTM, TT, NA>(A, L, lds, c0, nsb, G.rs, G.row_off, acc, pro, t_pro, t_wait);
+            else if (G.dt == kQ4K) chunk_pass<kQ4K, TT, NA>(A, L, lds, c0, nsb, G.rs, G.row_off, acc, pro, t_pro, t_wait);
+            else chunk_pass<kQ6K, TT, NA>(A, L, lds, c0, nsb, G.rs, G.row_off, acc, pro, t_pro, t_wait);
+        }
+        if (first) {
+            __syncthreads();
+            compute_inv_rms(A, L0, lds, inv_rms, nsb);
+        }
+        group_epilogue<TT, NA>(A, red, inv_rms, acc, G.n0, G.N, G.s, rows_out, swiglu);
+    }
+    (void)t_pro;
+    (void)t_wait;
 }
 
 }  // namespace
 
-uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt) {
+uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt, bool norm) {
     const int na = rows <= 8 ? 1 : 2;
     const int nsb = K / 256;
-    const ActLayout L(rows, na, std::min(chunk_sb, nsb), nsb);
+    const ActLayout L(rows, na, std::min(chunk_sb, nsb), nsb, norm);
     return L.total + 64 + (uint32_t)kWaves * tt * na * 4 * 64 * 4;
 }
 
-int fused_gemm_chunk_sb(int rows, int K, int tt) {
+int fused_gemm_chunk_sb(int rows, int K, int tt, bool norm) {
     const int nsb = K / 256;
     for (int c = nsb; c >= 1; c--)
-        if (fused_gemm_lds_bytes(rows, K, c, tt) <= kFusedLds) return c;
+        if (fused_gemm_lds_bytes(rows, K, c, tt, norm) <= kFusedLds) return c;
     return 0;
+}
+
+// Workgroups that are resident at once: a persistent grid never exceeds it,
+// so no group waits for a second round.
+static unsigned resident_wgs(const void *fn, uint32_t lds) {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 1;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, lds) != hipSuccess || per_cu <= 0)
+        per_cu = 1;
+    return (unsigned)(per_cu * cus);
 }
 
 template <int DTM, int TT, int NA>
@@ -621,7 +823,19 @@ static hipError_t launch_tt(const FusedGemmArgs &a, unsigned grid, uint32_t lds,
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr = true;
     }
-    k<<<grid, kThreads, lds, s>>>(a);
+    const unsigned res = resident_wgs(reinterpret_cast<const void *>(k), lds);
+    FusedGemmArgs b = a;
+    b.wk = kWaves;
+    if (DTM != 0 && b.chunk_sb >= b.K / 256) {
+        // streaming path: as many row groups per workgroup as keep every
+        // resident workgroup busy, the rest of the waves split K
+        int wr = 1;
+        while (wr < kWaves && (unsigned)b.groups >= res * (unsigned)wr * 2u) wr *= 2;
+        b.wk = kWaves / wr;
+        grid = (unsigned)((b.groups + wr - 1) / wr);
+    }
+    grid = std::min(grid, res);
+    k<<<grid, kThreads, lds, s>>>(b);
     return hipGetLastError();
 }
 
@@ -652,11 +866,11 @@ hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s) {
     }
     b.groups = (int)grid;
     const int nsb = b.K / 256;
-    // One-chunk launches run persistent group loops: the activations are
-    // quantized once per workgroup, then every further group only streams
-    // weights.
-    if (b.chunk_sb >= nsb && grid > (unsigned)kFusedMaxGrid) grid = kFusedMaxGrid;
-    const uint32_t lds = fused_gemm_lds_bytes(b.rows, b.K, b.chunk_sb, tt);
+    // Launches run persistent group loops over at most the resident
+    // workgroups: when the activations fit LDS in one chunk they are
+    // quantized once per workgroup, then further groups only stream weights.
+    (void)nsb;
+    const uint32_t lds = fused_gemm_lds_bytes(b.rows, b.K, b.chunk_sb, tt, b.norm != nullptr);
     bool mixed = false;
     for (int i = 1; i < b.nseg; i++) mixed |= b.seg[i].dtype != b.seg[0].dtype;
     if (mixed) return launch_dt<0>(b, tt, grid, lds, s);

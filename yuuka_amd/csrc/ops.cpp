@@ -87,16 +87,13 @@ static int fused_segments(const yuuka_op &op) {
 // Tiles per workgroup: the largest of 4, 2, 1 that still gives every CU
 // work (about 2 workgroups per CU); Q6_K holds more staging registers and
 // stops at 2. YUUKA_FGEMM_TT overrides (tuning).
+// 16-row tiles per group: one (the persistent group loop supplies the
+// parallelism and keeps registers within one workgroup of eight waves per
+// CU); SwiGLU needs a gate and an up tile. YUUKA_FGEMM_TT overrides (tuning).
 static int fused_tiles(const yuuka_op &op, int nseg) {
-    uint64_t tiles = 0;
     bool q6 = false;
-    for (int i = 0; i < nseg; i++) {
-        tiles += (op.n[2 + i] + 15) / 16;
-        q6 |= ((op.u[0] >> (8 * i)) & 0xff) == YUUKA_DTYPE_Q6_K;
-    }
+    for (int i = 0; i < nseg; i++) q6 |= ((op.u[0] >> (8 * i)) & 0xff) == YUUKA_DTYPE_Q6_K;
     int tt = 1;
-    if (!q6 && tiles >= 4 * 1024) tt = 4;
-    else if (tiles >= 2 * 256) tt = 2;
     if (const char *e = getenv("YUUKA_FGEMM_TT")) {
         const int v = atoi(e);
         if (v == 1 || v == 2 || v == 4) tt = v;
@@ -347,7 +344,7 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         }
         if (epi == kEpiSwiglu && (op.n[2] != op.n[3] || (op.u[0] & 0xff) != ((op.u[0] >> 8) & 0xff)))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED SwiGLU: gate and up must match");
-        if (fused_gemm_chunk_sb((int)rows, (int)K, fused_tiles(op, nseg)) < 1)
+        if (fused_gemm_chunk_sb((int)rows, (int)K, fused_tiles(op, nseg), op.buf[1] != nullptr) < 1)
             return fail(YUUKA_ERR_UNSUPPORTED, "GEMM_FUSED: activations do not fit LDS");
         return YUUKA_OK;
     }
@@ -472,7 +469,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
     case YUUKA_EXT_OP_GEMM_FUSED: {
         FusedGemmArgs a = fused_args(op);
         const int tt = fused_tiles(op, a.nseg);
-        a.chunk_sb = fused_gemm_chunk_sb(a.rows, a.K, tt);
+        a.chunk_sb = fused_gemm_chunk_sb(a.rows, a.K, tt, a.norm != nullptr);
         err = launch_fused_gemm(a, tt, s);
         break;
     }
