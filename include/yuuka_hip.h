@@ -385,6 +385,14 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
  *               0 out = y W^T, 1 out = y W^T + residual, 2 SwiGLU
  *               out_0 = SiLU(y W_0^T) * (y W_1^T) (two segments, same shape).
  *               rows <= 16. One launch, no workspace.
+ *               Optional gated head norm of x (Gated DeltaNet output,
+ *               recurrent.go:39-50): buf14 FP32 gate [rows][n_in] (SiLU
+ *               already applied), buf15 FP32 head norm weight [128]; y =
+ *               RMSNorm over each 128-element head * weight * gate (eps f0);
+ *               excludes buf1. u2 bits 4i..4i+3: output map of segment i
+ *               (epilogue 0 only): 0 none, 1 SiLU, 2 sigmoid, 3 Gated
+ *               DeltaNet decay exp(softplus(v + dt[n]) * a[n]) with buf10+i
+ *               holding {dt[N_i], a[N_i]} (recurrent.go:66-70).
  *   ROPE_TABLE: buf0 FP32 {cos, sin} [rows][rot_dim/2] of positions
  *               position + n2 + row; n={rows, rot_dim, displacement};
  *               f0 base (float64 angles as forward.go:495-514).
@@ -409,6 +417,13 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
 #define YUUKA_EXT_OP_ROPE_TABLE 70u
 #define YUUKA_EXT_OP_ATTN_VERIFY 71u
 #define YUUKA_EXT_FLAG_DEFER 0x100u
+/* With YUUKA_EXT_FLAG_DEFER: buf10 receives the raw per-head scan outputs;
+ * the gated RMSNorm is left to the consumer (GEMM_FUSED gated head norm). */
+#define YUUKA_EXT_FLAG_RAW_OUT 0x200u
+/* On RECURRENT_CHUNK and GDN_COMMIT: the alpha buffer holds the decay
+ * exp(softplus(alpha + dt) * a) and the beta buffer sigmoid(beta) (the
+ * GEMM_FUSED output maps 3 and 2 produce them). */
+#define YUUKA_EXT_FLAG_GDN_COEF 0x400u
 
 /* Timing events (extension): an event created with timing enabled, recorded
  * on a stream, and the elapsed milliseconds between two recorded events. */

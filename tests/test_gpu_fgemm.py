@@ -134,3 +134,60 @@ def test_fused_gemm_rejects_bad_ops(dev):
     with pytest.raises(hip.HipError):   # residual epilogue without residual
         hip.gemm_fused_op(plan, xb, 2560, 5, [(wb, O.Q4_K, 64, ob, None)], hip.EPI_RESIDUAL)
     plan.destroy()
+
+
+def _gated_head_norm(x, z, w, eps):
+    """recurrent.go:39-50 per 128-element head: x * (scale * w) * silu(z),
+    scale = 1/sqrt(mean(x^2) + eps) with a float64 sum (oracle silu)."""
+    rows, k = x.shape
+    out = np.empty_like(x)
+    for r in range(rows):
+        for h in range(k // 128):
+            seg = x[r, h * 128:(h + 1) * 128]
+            mean = np.float32(np.sum(seg.astype(np.float64) ** 2) / 128.0)
+            scale = np.float32(1.0 / np.sqrt(np.float64(mean + np.float32(eps))))
+            y = seg * (scale * w).astype(np.float32)
+            out[r, h * 128:(h + 1) * 128] = y * O.silu_mul(z[r, h * 128:(h + 1) * 128], np.ones(128, np.float32))
+    return out.astype(np.float32)
+
+
+def test_fused_gemm_gated_head_norm_prologue(dev, stream):
+    """Gated DeltaNet output projection: the prologue applies the per-head
+    gated RMSNorm (gate = SiLU(z) supplied by its producer) before the GEMM."""
+    rng = np.random.default_rng(21)
+    k, n, rows, eps = 2048, 700, 5, 1e-6
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    z = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    w = rng.normal(1, 0.1, 128).astype(np.float32)
+    gate = O.silu_mul(z, np.ones_like(z))
+    wq = synth.quant_matrix(rng, O.Q4_K, n, k)
+    plan = hip.Plan(dev)
+    xb, gb, wb = dev.upload(x), dev.upload(gate), dev.upload(w)
+    ob, wqb = dev.alloc(rows * n * 4), dev.upload(wq)
+    bufs = [None] * 16
+    bufs[0], bufs[2], bufs[6], bufs[14], bufs[15] = xb, wqb, ob, gb, wb
+    plan.add(hip.OP["GEMM_FUSED"], bufs, n=[k, rows, n, 0, 0, 0], u=[O.Q4_K, 0], f=[eps])
+    plan.execute(stream)
+    stream.sync()
+    got = ob.read(np.float32).reshape(rows, n)
+    plan.destroy()
+    y = _gated_head_norm(x, z, w, eps)
+    _check(got, _want(O.Q4_K, wq, n, k, y))
+
+
+def test_fused_gemm_silu_store(dev, stream):
+    rng = np.random.default_rng(22)
+    k, n, rows = 2560, 300, 5
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    wq = synth.quant_matrix(rng, O.Q4_K, n, k)
+    plan = hip.Plan(dev)
+    xb, wqb, ob = dev.upload(x), dev.upload(wq), dev.alloc(rows * n * 4)
+    bufs = [None] * 14
+    bufs[0], bufs[2], bufs[6] = xb, wqb, ob
+    plan.add(hip.OP["GEMM_FUSED"], bufs, n=[k, rows, n, 0, 0, 0], u=[O.Q4_K, 0, 1], f=[1e-6])
+    plan.execute(stream)
+    stream.sync()
+    got = ob.read(np.float32).reshape(rows, n)
+    plan.destroy()
+    prod = _want(O.Q4_K, wq, n, k, x)
+    _check(got, O.silu_mul(prod, np.ones_like(prod)), budget=1e-3)

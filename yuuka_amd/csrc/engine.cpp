@@ -45,6 +45,7 @@ struct Layer {
     Tensor qkv, gate, out, beta, alpha, q, k, v, o, ffn_gate, ffn_up, ffn_down;
     yuuka_buffer *conv = nullptr, *dt = nullptr, *a = nullptr, *ssm_norm = nullptr, *q_norm = nullptr,
                  *k_norm = nullptr;
+    yuuka_buffer *dt_a = nullptr;  // {dt[rank], a[rank]}: decay parameters of the projection epilogue
     // per-request state
     yuuka_buffer *conv_state = nullptr, *mat_state = nullptr, *kpool = nullptr, *vpool = nullptr;
     // per-step saved inputs of the recurrent block (read by GDN_COMMIT)
@@ -154,12 +155,16 @@ struct Builder {
     // One GEMM_FUSED op: every segment reads the same activation rows x
     // (optionally RMS-normalised with `norm`).
     void fused(yuuka_buffer *x, yuuka_buffer *norm, float eps, uint64_t rows, std::initializer_list<Seg> segs,
-               uint32_t epilogue) {
+               uint32_t epilogue, uint32_t silu_mask = 0, yuuka_buffer *gate = nullptr,
+               yuuka_buffer *head_norm = nullptr) {
         if (st != YUUKA_OK) return;
         yuuka_op op{};
         op.code = YUUKA_EXT_OP_GEMM_FUSED;
         op.buf[0] = x;
         op.buf[1] = norm;
+        op.buf[14] = gate;
+        op.buf[15] = head_norm;
+        op.u[2] = silu_mask;
         op.n[1] = rows;
         op.u[1] = epilogue;
         op.f[0] = eps;
@@ -205,13 +210,13 @@ yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
           {H, R, yk::row_bytes(q->embedding.dtype, H), (uint64_t)c.vocab}, {q->embedding.dtype});
     const bool fused = use_fused(q);
     const float qscale = (float)(1.0 / std::sqrt((double)c.state_size));
-    auto recurrent_chunk = [&](Layer &L) {
+    auto recurrent_chunk = [&](Layer &L, uint32_t extra_flags) {
         b.add(YUUKA_OP_RECURRENT_CHUNK,
               {L.conv_state, L.mat_state, L.qkv_rows, q->z, L.alpha_rows, L.beta_rows, L.conv, L.dt, L.a, L.ssm_norm,
                q->gdn_out, L.conv_rows},
               {R, (uint64_t)c.groups, (uint64_t)c.rank, (uint64_t)c.state_size, (uint64_t)q->conv_dim,
                (uint64_t)c.inner},
-              {(uint32_t)c.conv_kernel}, {c.eps, qscale}, YUUKA_EXT_FLAG_DEFER);
+              {(uint32_t)c.conv_kernel}, {c.eps, qscale}, YUUKA_EXT_FLAG_DEFER | extra_flags);
     };
     // YUUKA_Q35_ATTN=0 selects the separate norm / RoPE / KV-write /
     // attention ops (comparison); by default one ATTN_VERIFY op per layer.
@@ -246,12 +251,17 @@ yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
         Layer &L = q->layers[i];
         if (fused) {
             if (L.recurrent) {  // plan.go:806-913
+                // z is stored as SiLU(z); the scan writes raw per-head outputs
+                // and the out projection applies the gated RMSNorm in its
+                // prologue (recurrent.go:39-50)
+                // beta is stored as sigmoid(beta), alpha as the decay
+                // exp(softplus(alpha + dt) * a) (recurrent.go:66-70)
                 b.fused(q->x, L.attn_norm, c.eps, R,
                         {{&L.qkv, L.qkv_rows, nullptr}, {&L.gate, q->z, nullptr}, {&L.beta, L.beta_rows, nullptr},
-                         {&L.alpha, L.alpha_rows, nullptr}},
-                        0);
-                recurrent_chunk(L);
-                b.fused(q->gdn_out, nullptr, 0.0f, R, {{&L.out, q->x, q->x}}, 1);
+                         {&L.alpha, L.alpha_rows, L.dt_a}},
+                        0, (1u << 4) | (2u << 8) | (3u << 12));
+                recurrent_chunk(L, YUUKA_EXT_FLAG_RAW_OUT | YUUKA_EXT_FLAG_GDN_COEF);
+                b.fused(q->gdn_out, nullptr, c.eps, R, {{&L.out, q->x, q->x}}, 1, 0, q->z, L.ssm_norm);
             } else {  // plan.go:684-804
                 b.fused(q->x, L.attn_norm, c.eps, R,
                         {{&L.q, q->q, nullptr}, {&L.k, q->k, nullptr}, {&L.v, q->v, nullptr}}, 0);
@@ -270,7 +280,7 @@ yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
             b.gemm(L.gate, q->xq, q->z, R);
             b.gemm(L.beta, q->xq, L.beta_rows, R);
             b.gemm(L.alpha, q->xq, L.alpha_rows, R);
-            recurrent_chunk(L);
+            recurrent_chunk(L, 0);
             b.quant(q->gdn_out, (uint64_t)c.inner, R, q->xq);
             b.gemm(L.out, q->xq, q->x, R, q->x);
         } else {
@@ -311,7 +321,7 @@ yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
               {L.conv_state, L.mat_state, L.qkv_rows, L.conv_rows, L.alpha_rows, L.beta_rows, L.dt, L.a, q->result},
               {R, (uint64_t)c.groups, (uint64_t)c.rank, (uint64_t)c.state_size, (uint64_t)q->conv_dim,
                (uint64_t)c.inner},
-              {(uint32_t)c.conv_kernel});
+              {(uint32_t)c.conv_kernel}, {}, fused ? YUUKA_EXT_FLAG_GDN_COEF : 0u);
     }
     b.add(YUUKA_EXT_OP_ADVANCE, {q->dyn, q->result, q->step}, {R});
     if (b.st != YUUKA_OK) {
@@ -480,6 +490,12 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
                 CHK(upload_vec(q.get(), lw.conv, cd * c.conv_kernel, "ssm_conv1d", &L.conv));
                 CHK(upload_vec(q.get(), lw.dt, c.rank, "ssm_dt", &L.dt));
                 CHK(upload_vec(q.get(), lw.a, c.rank, "ssm_a", &L.a));
+                {
+                    std::vector<float> da(2 * (size_t)c.rank);
+                    std::memcpy(da.data(), lw.dt, (size_t)c.rank * 4);
+                    std::memcpy(da.data() + c.rank, lw.a, (size_t)c.rank * 4);
+                    CHK(upload(q.get(), da.data(), da.size() * 4, &L.dt_a));
+                }
                 CHK(upload_vec(q.get(), lw.ssm_norm, c.state_size, "ssm_norm", &L.ssm_norm));
                 CHK(alloc(q.get(), (uint64_t)(c.conv_kernel - 1) * cd * 4, &L.conv_state));
                 CHK(alloc(q.get(), (uint64_t)c.rank * c.state_size * c.state_size * 4, &L.mat_state));

@@ -28,11 +28,19 @@ struct FusedSeg {
     float *out;          // [rows][n]
     const float *res;    // [rows][n] (kEpiResidual)
     int wg_begin;        // first workgroup (set by the launcher)
+    int act;             // kEpiStore output map: 0 none, 1 SiLU, 2 sigmoid, 3 Gated DeltaNet decay
+                         // exp(softplus(v + p0[n]) * p1[n]) (recurrent.go:66-70)
+    const float *p0, *p1;  // per-row parameters of act 3 (dt, a)
 };
 
 struct FusedGemmArgs {
     const float *x;     // [rows][K] activations
     const float *norm;  // optional RMSNorm weight [K]
+    // Optional gated head norm (Gated DeltaNet output, recurrent.go:39-50):
+    // y = RMSNorm_head(x) * head_norm * gate over heads of 128 elements, with
+    // gate = SiLU(z) already applied by its producer. Excludes `norm`.
+    const float *gate;       // [rows][K]
+    const float *head_norm;  // [128]
     float eps;
     int K, rows;
     int chunk_sb;       // super-blocks of K quantized into LDS at a time
@@ -45,8 +53,8 @@ struct FusedGemmArgs {
 
 // Largest K chunk (in 256-element super-blocks) whose activations fit LDS
 // next to the partial-sum area of a tt-tile launch (0 if none fits).
-int fused_gemm_chunk_sb(int rows, int K, int tt, bool norm);
-uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt, bool norm);
+int fused_gemm_chunk_sb(int rows, int K, int tt, bool norm, bool gated = false);
+uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt, bool norm, bool gated = false);
 // tt: 16-row tiles per workgroup (1, 2 or 4; even for kEpiSwiglu).
 hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s);
 

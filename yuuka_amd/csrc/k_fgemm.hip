@@ -133,6 +133,20 @@ __device__ __forceinline__ float row_sum(float v) {
     v += dppf<0x124>(v);
     return v + dppf<0x128>(v);
 }
+// float64 sum over each 16-lane row, in every lane of the row.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t b = __double_as_longlong(v);
+    const int lo = dpp<CTRL>((int)(uint32_t)b), hi = dpp<CTRL>((int)(uint32_t)(b >> 32));
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+__device__ __forceinline__ double row_sum_d(double v) {
+    v += dpp_d<0xb1>(v);
+    v += dpp_d<0x4e>(v);
+    v += dpp_d<0x124>(v);
+    return v + dpp_d<0x128>(v);
+}
+
 // Sum over each quad, in every lane of the quad.
 __device__ __forceinline__ int quad_sum(int v) {
     v += dpp<0xb1>(v);
@@ -143,6 +157,7 @@ __device__ __forceinline__ int quad_sum(int v) {
 // 0..rows-1, l plane rows rows..2rows-1), RHOP = 16 * NA:
 //   raw    [cap][rows][256] float    (the chunk's x, copied straight from HBM)
 //   graw   [cap][256] float          (the chunk's norm weights)
+//   zraw   [cap][rows][256] float    (the chunk's gate values, gated mode)
 //   planes [cap * 8 sub-blocks][4 slices][RHO][8 B]
 //   sums   [cap][RHOP][8] int16      (sub-block sums of each plane row)
 //   xs     [cap][RHOP] float         (activation scale of each plane row)
@@ -152,12 +167,13 @@ __device__ __forceinline__ int quad_sum(int v) {
 // live in the current chunk.
 struct ActLayout {
     int rho, rhop, cap, cnt;
-    uint32_t raw, graw, planes, sums, xs, nsq, junk, total;
-    __host__ __device__ ActLayout(int rows, int na, int cap_, int nsb, bool norm, int cnt_ = -1)
+    uint32_t raw, graw, zraw, planes, sums, xs, nsq, junk, total;
+    __host__ __device__ ActLayout(int rows, int na, int cap_, int nsb, bool norm, int cnt_ = -1, bool gated = false)
         : rho(2 * rows), rhop(16 * na), cap(cap_), cnt(cnt_ < 0 ? cap_ : cnt_) {
         raw = 0;
         graw = raw + (uint32_t)cap * rows * 1024;
-        planes = graw + (norm ? (uint32_t)cap * 1024 : 0u);
+        zraw = graw + (norm ? (uint32_t)cap * 1024 : 0u);
+        planes = zraw + (gated ? (uint32_t)cap * rows * 1024 : 0u);
         sums = planes + (uint32_t)cap * 8 * 4 * rho * 8;
         xs = sums + (uint32_t)cap * rhop * 16;
         nsq = xs + (uint32_t)cap * rhop * 4;
@@ -174,14 +190,19 @@ __device__ __forceinline__ void act_fetch(const FusedGemmArgs &A, const ActLayou
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int M = A.rows;
-    const int xunits = M * L.cnt, gunits = A.norm ? L.cnt : 0;
-    for (int u = wave; u < xunits + gunits; u += kWaves) {
+    const int xunits = M * L.cnt, gunits = A.norm ? L.cnt : 0, zunits = A.gate ? xunits : 0;
+    for (int u = wave; u < xunits + gunits + zunits; u += kWaves) {
         const float *src;
         uint32_t dst;
         if (u < xunits) {
             const int m = u / L.cnt, sbl = u - m * L.cnt;
             src = A.x + (size_t)m * A.K + (size_t)(c0 + sbl) * 256 + lane * 4;
             dst = L.raw + (uint32_t)(sbl * M + m) * 1024;
+        } else if (u >= xunits + gunits) {
+            const int uz = u - xunits - gunits;
+            const int m = uz / L.cnt, sbl = uz - m * L.cnt;
+            src = A.gate + (size_t)m * A.K + (size_t)(c0 + sbl) * 256 + lane * 4;
+            dst = L.zraw + (uint32_t)(sbl * M + m) * 1024;
         } else {
             const int sbl = u - xunits;
             src = A.norm + (size_t)(c0 + sbl) * 256 + lane * 4;
@@ -213,6 +234,14 @@ __device__ __forceinline__ void act_prologue(const FusedGemmArgs &A, const ActLa
     const float *raw = reinterpret_cast<const float *>(lds + L.raw);
     const float *graw = reinterpret_cast<const float *>(lds + L.graw);
     const int jl = s >> 2, g = s & 3;
+    // head-norm weights of this lane's 8 elements (position (s % 16) * 8 in its head)
+    float hw[8];
+    if (A.gate) {
+        const float4 h0 = *reinterpret_cast<const float4 *>(A.head_norm + (s & 15) * 8);
+        const float4 h1 = *reinterpret_cast<const float4 *>(A.head_norm + (s & 15) * 8 + 4);
+        hw[0] = h0.x; hw[1] = h0.y; hw[2] = h0.z; hw[3] = h0.w;
+        hw[4] = h1.x; hw[5] = h1.y; hw[6] = h1.z; hw[7] = h1.w;
+    }
     // unit index -> (row, super-block): row-major over the chunk, u = m * cnt + sbl
     for (int q0 = 0; q0 < units; q0 += 2 * kPairs) {
         float4 xa[kPairs], xb[kPairs], ga[kPairs], gb[kPairs];
@@ -250,6 +279,21 @@ __device__ __forceinline__ void act_prologue(const FusedGemmArgs &A, const ActLa
                 const float gg[8] = {ga[p].x, ga[p].y, ga[p].z, ga[p].w, gb[p].x, gb[p].y, gb[p].z, gb[p].w};
 #pragma unroll
                 for (int i = 0; i < 8; i++) v[i] = __fmul_rn(v[i], gg[i]);
+            }
+            if (A.gate) {
+                // gated head norm: a 16-lane DPP row holds one 128-element head
+                const float *zsrc = reinterpret_cast<const float *>(lds + L.zraw) + (sbl * M + m) * 256 + s * 8;
+                const float4 za = *reinterpret_cast<const float4 *>(zsrc), zb = *reinterpret_cast<const float4 *>(zsrc + 4);
+                const float zz[8] = {za.x, za.y, za.z, za.w, zb.x, zb.y, zb.z, zb.w};
+                double ss = 0.0;
+#pragma unroll
+                for (int i = 0; i < 8; i++) ss += (double)v[i] * (double)v[i];
+                ss = row_sum_d(ss);
+                const float mean = (float)(ss / 128.0);
+                const float scale = (float)(1.0 / sqrt((double)(mean + A.eps)));
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    v[i] = __fmul_rn(__fmul_rn(v[i], __fmul_rn(scale, hw[i])), zz[i]);
             }
             float a = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
                             fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
@@ -525,6 +569,16 @@ __device__ __forceinline__ void chunk_pass(const FusedGemmArgs &A, const ActLayo
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return __fmul_rn(__fmul_rn(g, sigmoid_ref(g)), u); }
 
+// Output map of a store epilogue (FusedSeg::act) for output row n.
+__device__ __forceinline__ float out_map(const FusedSeg &S, float v, int n) {
+    switch (S.act) {
+    case 1: return silu_ref(v);
+    case 2: return sigmoid_ref(v);
+    case 3: return (float)exp((double)__fmul_rn(softplus_ref(__fadd_rn(v, S.p0[n])), S.p1[n]));
+    default: return v;
+    }
+}
+
 // TT: 16-row tiles per group (for SwiGLU, TT/2 gate tiles then TT/2 up tiles
 // over the same rows). NA: 16-row A tiles (rows <= 8: 1, <= 16: 2).
 // DTM: kQ4K or kQ6K for single-dtype launches, 0 for a per-segment switch.
@@ -607,6 +661,7 @@ __device__ __forceinline__ void group_epilogue(const FusedGemmArgs &A, float *re
         } else {
             float v = value(t, m, col);
             if (A.epilogue == kEpiResidual) v += A.seg[s].res[o];
+            else v = out_map(A.seg[s], v, n);
             A.seg[s].out[o] = v;
         }
     }
@@ -632,7 +687,7 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
     const int nsb = A.K / 256;
     const int wk = A.wk, wr = kWaves / wk;
     const int rg = wave / wk, kg = wave - rg * wk;
-    const ActLayout L(A.rows, NA, nsb, nsb, A.norm != nullptr);
+    const ActLayout L(A.rows, NA, nsb, nsb, A.norm != nullptr, -1, A.gate != nullptr);
     const int mine = kg < nsb ? (nsb - kg + wk - 1) / wk : 0;  // super-blocks per tile
     const int per_iter = (int)gridDim.x * wr;                   // row tiles per grid iteration
     const int niter = (A.groups - (int)blockIdx.x * wr + per_iter - 1) / per_iter;
@@ -730,6 +785,7 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
             } else {
                 float v = value(t, m, col);
                 if (A.epilogue == kEpiResidual) v += A.seg[G.s].res[o];
+                else v = out_map(A.seg[G.s], v, n);
                 A.seg[G.s].out[o] = v;
             }
         }
@@ -745,7 +801,7 @@ __global__ __launch_bounds__(kThreads) void fgemm_kernel(const FusedGemmArgs A) 
     const int rows_out = swiglu ? 8 * TT : 16 * TT;  // output rows of one group
     const int nsb = A.K / 256;
     const int M = A.rows;
-    const ActLayout L0(M, NA, min(A.chunk_sb, nsb), nsb, A.norm != nullptr);
+    const ActLayout L0(M, NA, min(A.chunk_sb, nsb), nsb, A.norm != nullptr, -1, A.gate != nullptr);
     const bool one_chunk = A.chunk_sb >= nsb;  // activations stay in LDS across groups
     float *inv_rms = reinterpret_cast<float *>(lds + L0.total);
     float *red = reinterpret_cast<float *>(lds + L0.total + 64);
@@ -767,7 +823,8 @@ __global__ __launch_bounds__(kThreads) void fgemm_kernel(const FusedGemmArgs A) 
                 for (int i = 0; i < 4; i++) acc[t][a][i] = 0.0f;
         const bool first = grp == (int)blockIdx.x;
         for (int c0 = 0; c0 < nsb; c0 += A.chunk_sb) {
-            const ActLayout L(M, NA, min(A.chunk_sb, nsb), nsb, A.norm != nullptr, min(A.chunk_sb, nsb - c0));
+            const ActLayout L(M, NA, min(A.chunk_sb, nsb), nsb, A.norm != nullptr, min(A.chunk_sb, nsb - c0),
+                              A.gate != nullptr);
             const bool pro = first || !one_chunk;
             if (c0 && pro) __syncthreads();  // previous chunk's LDS reads are done
             if constexpr (DTM != 0) chunk_pass<DTM, TT, NA>(A, L, lds, c0, nsb, G.rs, G.row_off, acc, pro, t_pro, t_wait);
@@ -786,17 +843,17 @@ __global__ __launch_bounds__(kThreads) void fgemm_kernel(const FusedGemmArgs A) 
 
 }  // namespace
 
-uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt, bool norm) {
+uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt, bool norm, bool gated) {
     const int na = rows <= 8 ? 1 : 2;
     const int nsb = K / 256;
-    const ActLayout L(rows, na, std::min(chunk_sb, nsb), nsb, norm);
+    const ActLayout L(rows, na, std::min(chunk_sb, nsb), nsb, norm, -1, gated);
     return L.total + 64 + (uint32_t)kWaves * tt * na * 4 * 64 * 4;
 }
 
-int fused_gemm_chunk_sb(int rows, int K, int tt, bool norm) {
+int fused_gemm_chunk_sb(int rows, int K, int tt, bool norm, bool gated) {
     const int nsb = K / 256;
     for (int c = nsb; c >= 1; c--)
-        if (fused_gemm_lds_bytes(rows, K, c, tt, norm) <= kFusedLds) return c;
+        if (fused_gemm_lds_bytes(rows, K, c, tt, norm, gated) <= kFusedLds) return c;
     return 0;
 }
 
@@ -870,7 +927,7 @@ hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s) {
     // workgroups: when the activations fit LDS in one chunk they are
     // quantized once per workgroup, then further groups only stream weights.
     (void)nsb;
-    const uint32_t lds = fused_gemm_lds_bytes(b.rows, b.K, b.chunk_sb, tt, b.norm != nullptr);
+    const uint32_t lds = fused_gemm_lds_bytes(b.rows, b.K, b.chunk_sb, tt, b.norm != nullptr, b.gate != nullptr);
     bool mixed = false;
     for (int i = 1; i < b.nseg; i++) mixed |= b.seg[i].dtype != b.seg[0].dtype;
     if (mixed) return launch_dt<0>(b, tt, grid, lds, s);

@@ -1,0 +1,467 @@
+// k_gdn.hip — Gated DeltaNet block of the verify step, one workgroup per
+// value head.
+//
+// Verify (model/qwen35/recurrent.go:56-105 and forward.go:248-268, 484-493,
+// recurrent.go:39-50 in one kernel): for head h the workgroup
+//  * runs the causal depthwise conv over [conv state, verify rows] for the
+//    head's q, k (group h % groups) and v channels, SiLU, and the L2 norm of
+//    q (times 1/sqrt(state)) and k;
+//  * keeps the 128 x 128 state in registers (thread = state column j and a
+//    quarter of the state rows) and runs the delta rule over the rows;
+//  * applies the gated RMSNorm (x * scale * w * silu(z)) to each row's
+//    outputs.
+// The state and the conv state are left untouched (verify mode); the conv
+// outputs are saved for the commit.
+//
+// Commit: replays the accepted rows (acceptance result[0] + 1) through the
+// state and writes it back, and moves the conv state window forward — the
+// scan and the conv-state update of one head in one workgroup.
+//
+// Arithmetic is the reference's: float32 with separately rounded products
+// and sums in the reference's order per element, float64 where the
+// reference converts (norm sums, exp, log1p). Cross-thread sums add partials
+// of 32 state rows in a fixed order.
+#include <hip/hip_runtime.h>
+
+#include "model_kernels.h"
+#include "refmath.h"
+
+namespace yk {
+namespace {
+
+constexpr int kGdnThreads = 512;
+constexpr int kS = 128;  // state size (validated by the op)
+
+__device__ __forceinline__ double wave_sum_dd(double v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// Sum over the 4 lanes of a quad (quad_perm [1,0,3,2] then [2,3,0,1]), in
+// every lane: (p0 + p1) + (p2 + p3).
+__device__ __forceinline__ float quad_sum_f(float v) {
+    v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, true)));
+    return __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, true)));
+}
+
+// Causal conv + SiLU of one channel over the rows: every input is requested
+// before the first use (one memory round trip).
+__device__ __forceinline__ void conv_channel(const float *conv_state, const float *qkv, const float *conv_w,
+                                             const GdnArgs &g, int c, float *dst, int dst_stride) {
+    const int R = g.rows, K = g.kernel;
+    float w[8], st[8], x[16];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        w[i] = i < K ? conv_w[(uint64_t)c * K + i] : 0.0f;
+        st[i] = i < K - 1 ? conv_state[(uint64_t)c * (K - 1) + i] : 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) x[r] = r < R ? qkv[(uint64_t)r * g.conv_dim + c] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        if (r >= R) break;
+        float sum = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 7; tt++) {
+            if (tt >= K - 1) break;
+            const int idx = r + tt - (K - 1);
+            // idx < 0 reads the conv state slot K - 1 + idx
+            float xv = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++)
+                if (q == idx) xv = x[q];
+#pragma unroll
+            for (int q = 0; q < 7; q++)
+                if (q == K - 1 + idx && idx < 0) xv = st[q];
+            sum = __fadd_rn(sum, __fmul_rn(w[tt], xv));
+        }
+        float wl = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            if (q == K - 1) wl = w[q];
+        sum = __fadd_rn(sum, __fmul_rn(wl, x[r]));
+        dst[r * dst_stride] = silu_ref(sum);
+    }
+}
+
+// Sum over each aligned group of 8 lanes, in every lane of the group:
+// quad_perm [1,0,3,2], [2,3,0,1], then row_half_mirror (lane i <-> 7 - i).
+__device__ __forceinline__ float group8_sum_f(float v) {
+    v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, true)));
+    v = __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, true)));
+    return __fadd_rn(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, true)));
+}
+
+__device__ __forceinline__ float gdn_decay(const GdnArgs &g, const float *alpha_raw, const float *dt,
+                                           const float *a_log, int r, int h) {
+    if (g.coef) return alpha_raw[(uint64_t)r * g.rank + h];
+    const float act = __fmul_rn(softplus_ref(__fadd_rn(alpha_raw[(uint64_t)r * g.rank + h], dt[h])), a_log[h]);
+    return (float)exp((double)act);
+}
+
+// LDS: cv [rows][3][128] conv outputs (q, k, v of this head), raw [rows][128]
+// scan outputs.
+__global__ __launch_bounds__(kGdnThreads) void gdn_verify_kernel(
+    const float *__restrict__ conv_state, const float *__restrict__ state, const float *__restrict__ qkv,
+    const float *__restrict__ z, const float *__restrict__ alpha_raw, const float *__restrict__ beta_raw,
+    const float *__restrict__ conv_w, const float *__restrict__ dt, const float *__restrict__ a_log,
+    const float *__restrict__ norm_w, float *__restrict__ out, float *__restrict__ conv_out, GdnArgs g) {
+    extern __shared__ float sm[];
+    const int h = blockIdx.x;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int R = g.rows, K = g.kernel;
+    const int key_dim = g.groups * kS;
+    const int kh = h % g.groups;
+    const bool owns_qk = h < g.groups;  // writes the shared q/k conv outputs once
+    float *cv = sm;                    // [R][3][128]
+    float *raw = cv + R * 3 * kS;      // [R][128]
+
+    // ---- state registers (issued first; used after the conv). Lane l of
+    // wave w holds column j = 16 w + l / 4, state rows 32 (l % 4) .. +31: a
+    // column's four row quarters sit in one quad.
+    const int rq = lane & 3, j = wave * 16 + (lane >> 2);
+    const float *mat = state + (uint64_t)h * kS * kS;
+    float s_reg[32];
+#pragma unroll
+    for (int ii = 0; ii < 32; ii++) s_reg[ii] = mat[(uint64_t)(rq * 32 + ii) * kS + j];
+
+    // ---- causal conv + SiLU of the head's 384 channels (forward.go:248-268)
+    if (t < 3 * kS) {
+        const int part_i = t >> 7, cc = t & (kS - 1);
+        const int c = part_i == 0 ? kh * kS + cc : part_i == 1 ? key_dim + kh * kS + cc : 2 * key_dim + h * kS + cc;
+        conv_channel(conv_state, qkv, conv_w, g, c, cv + part_i * kS + cc, 3 * kS);
+    }
+    __syncthreads();
+    // ---- L2 norm of q and k per row (forward.go:484-493); save conv outputs
+    for (int vec = wave; vec < 2 * R; vec += kGdnThreads / 64) {
+        const int r = vec >> 1, which = vec & 1;
+        float *x = cv + (r * 3 + which) * kS;
+        const float a0 = x[lane], a1 = x[lane + 64];
+        double sq = (double)a0 * (double)a0 + (double)a1 * (double)a1;
+        sq = wave_sum_dd(sq);
+        const float extra = which == 0 ? g.q_scale : 1.0f;
+        const float scale = __fmul_rn((float)(1.0 / sqrt(sq + (double)g.eps)), extra);
+        const float y0 = __fmul_rn(a0, scale), y1 = __fmul_rn(a1, scale);
+        x[lane] = y0;
+        x[lane + 64] = y1;
+        if (owns_qk) {
+            float *dst = conv_out + (uint64_t)r * g.conv_dim + (which == 0 ? 0 : key_dim) + kh * kS;
+            dst[lane] = y0;
+            dst[lane + 64] = y1;
+        }
+    }
+    for (int idx = t; idx < R * kS; idx += kGdnThreads) {
+        const int r = idx / kS, cc = idx % kS;
+        conv_out[(uint64_t)r * g.conv_dim + 2 * key_dim + h * kS + cc] = cv[(r * 3 + 2) * kS + cc];
+    }
+    __syncthreads();
+
+    // ---- delta rule over the rows (recurrent.go:56-105), state untouched;
+    // column sums over the quad, no barrier per row
+    for (int r = 0; r < R; r++) {
+        const float *q = cv + (r * 3 + 0) * kS, *k = cv + (r * 3 + 1) * kS, *v = cv + (r * 3 + 2) * kS;
+        const float decay = gdn_decay(g, alpha_raw, dt, a_log, r, h);
+        const float beta = g.coef ? beta_raw[(uint64_t)r * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)r * g.rank + h]);
+        float sk = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < 32; ii++) {
+            s_reg[ii] = __fmul_rn(s_reg[ii], decay);
+            sk = __fadd_rn(sk, __fmul_rn(s_reg[ii], k[rq * 32 + ii]));
+        }
+        sk = quad_sum_f(sk);
+        const float d = __fmul_rn(__fsub_rn(v[j], sk), beta);
+        float o = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < 32; ii++) {
+            s_reg[ii] = __fadd_rn(s_reg[ii], __fmul_rn(k[rq * 32 + ii], d));
+            o = __fadd_rn(o, __fmul_rn(s_reg[ii], q[rq * 32 + ii]));
+        }
+        o = quad_sum_f(o);
+        if (rq == 0) raw[r * kS + j] = o;
+    }
+    __syncthreads();
+    // ---- gated RMSNorm per row (recurrent.go:39-50)
+    for (int r = wave; r < R; r += kGdnThreads / 64) {
+        const float x0 = raw[r * kS + lane], x1 = raw[r * kS + lane + 64];
+        double s = (double)x0 * (double)x0 + (double)x1 * (double)x1;
+        s = wave_sum_dd(s);
+        const float mean = (float)(s / (double)kS);
+        const float scale = (float)(1.0 / sqrt((double)(mean + g.eps)));
+        const uint64_t base = ((uint64_t)r * g.rank + h) * kS;
+        const float y0 = __fmul_rn(x0, __fmul_rn(scale, norm_w[lane]));
+        const float y1 = __fmul_rn(x1, __fmul_rn(scale, norm_w[lane + 64]));
+        out[base + lane] = __fmul_rn(y0, silu_ref(z[base + lane]));
+        out[base + lane + 64] = __fmul_rn(y1, silu_ref(z[base + lane + 64]));
+    }
+}
+
+// Commit of one layer: state replay of the accepted rows and the conv-state
+// window (forward.go:259-264); head h owns its v channels and, for
+// h < groups, its q/k group's channels.
+__global__ __launch_bounds__(kGdnThreads) void gdn_commit_kernel(
+    float *__restrict__ conv_state, float *__restrict__ state, const float *__restrict__ qkv,
+    const float *__restrict__ conv, const float *__restrict__ alpha_raw, const float *__restrict__ beta_raw,
+    const float *__restrict__ dt, const float *__restrict__ a_log, GdnArgs g,
+    const int32_t *__restrict__ accept_result) {
+    const int h = blockIdx.x;
+    const int t = threadIdx.x;
+    const int K = g.kernel;
+    const int key_dim = g.groups * kS;
+    const int kh = h % g.groups;
+    const int n = accept_result ? min(accept_result[0] + 1, g.rows) : g.rows;
+    // conv-state window: the last K-1 inputs of [old state, raw rows 0..n-1]
+    if (t < 3 * kS) {
+        const int part_i = t >> 7, cc = t & (kS - 1);
+        const bool owner = part_i == 2 || h < g.groups;
+        if (owner) {
+            const int c = part_i == 0 ? kh * kS + cc : part_i == 1 ? key_dim + kh * kS + cc : 2 * key_dim + h * kS + cc;
+            // new slot tt holds sequence index n + tt (relative to row 0);
+            // all reads complete before any write (same thread, same channel)
+            float win[8];
+#pragma unroll
+            for (int tt = 0; tt < 7; tt++) {
+                const int idx = n + tt - (K - 1);
+                win[tt] = tt >= K - 1 ? 0.0f
+                          : idx < 0   ? conv_state[(uint64_t)c * (K - 1) + (K - 1 + idx)]
+                                      : qkv[(uint64_t)idx * g.conv_dim + c];
+            }
+#pragma unroll
+            for (int tt = 0; tt < 7; tt++)
+                if (tt < K - 1) conv_state[(uint64_t)c * (K - 1) + tt] = win[tt];
+        }
+    }
+    const int wave = t >> 6, lane = t & 63;
+    const int rq = lane & 3, j = wave * 16 + (lane >> 2);
+    float *mat = state + (uint64_t)h * kS * kS;
+    float s_reg[32];
+#pragma unroll
+    for (int ii = 0; ii < 32; ii++) s_reg[ii] = mat[(uint64_t)(rq * 32 + ii) * kS + j];
+    for (int r = 0; r < n; r++) {
+        const float *row = conv + (uint64_t)r * g.conv_dim;
+        const float *k = row + key_dim + kh * kS;
+        const float decay = gdn_decay(g, alpha_raw, dt, a_log, r, h);
+        const float beta = g.coef ? beta_raw[(uint64_t)r * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)r * g.rank + h]);
+        float kr[32];
+#pragma unroll
+        for (int ii = 0; ii < 32; ii++) kr[ii] = k[rq * 32 + ii];
+        const float vj = row[2 * key_dim + h * kS + j];
+        float sk = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < 32; ii++) {
+            s_reg[ii] = __fmul_rn(s_reg[ii], decay);
+            sk = __fadd_rn(sk, __fmul_rn(s_reg[ii], kr[ii]));
+        }
+        sk = quad_sum_f(sk);
+        const float d = __fmul_rn(__fsub_rn(vj, sk), beta);
+#pragma unroll
+        for (int ii = 0; ii < 32; ii++) s_reg[ii] = __fadd_rn(s_reg[ii], __fmul_rn(kr[ii], d));
+    }
+#pragma unroll
+    for (int ii = 0; ii < 32; ii++) mat[(uint64_t)(rq * 32 + ii) * kS + j] = s_reg[ii];
+}
+
+
+// ---- column-split variants: workgroup (head h, block of kCols state
+// columns). Lane l of wave w holds column j = kCols * blockIdx.y + 8 w + l / 8
+// and state rows 16 (l % 8) .. +15; a column's eight row parts form an
+// aligned 8-lane group, so column sums need no barrier.
+constexpr int kCols = 32;
+constexpr int kColThreads = 256;
+
+// Verify: conv + SiLU + L2 norm of the head's q / k channels and this
+// block's v channels, then the delta rule over the rows for this block's
+// columns. Writes the raw outputs (the gated norm runs in the consumer) and
+// the conv outputs for the commit; the states are left untouched.
+__global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
+    const float *__restrict__ conv_state, const float *__restrict__ state, const float *__restrict__ qkv,
+    const float *__restrict__ alpha_raw, const float *__restrict__ beta_raw, const float *__restrict__ conv_w,
+    const float *__restrict__ dt, const float *__restrict__ a_log, float *__restrict__ raw_out,
+    float *__restrict__ conv_out, GdnArgs g) {
+    extern __shared__ float sm[];
+    const int h = blockIdx.x, cb = blockIdx.y;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int R = g.rows;
+    const int key_dim = g.groups * kS;
+    const int kh = h % g.groups;
+    float *qk = sm;                 // [R][2][128] q, k
+    float *vv = qk + R * 2 * kS;    // [R][kCols]
+    const int p = lane & 7, j = cb * kCols + wave * 8 + (lane >> 3);
+    const float *mat = state + (uint64_t)h * kS * kS;
+    float s_reg[16];
+#pragma unroll
+    for (int ii = 0; ii < 16; ii++) s_reg[ii] = mat[(uint64_t)(p * 16 + ii) * kS + j];
+    // conv of 256 q/k channels + kCols v channels
+    for (int ch = t; ch < 2 * kS + kCols; ch += kColThreads) {
+        int c;
+        float *dst;
+        int stride;
+        if (ch < 2 * kS) {
+            const int which = ch >> 7, cc = ch & (kS - 1);
+            c = (which == 0 ? 0 : key_dim) + kh * kS + cc;
+            dst = qk + which * kS + cc;
+            stride = 2 * kS;
+        } else {
+            const int cc = ch - 2 * kS;
+            c = 2 * key_dim + h * kS + cb * kCols + cc;
+            dst = vv + cc;
+            stride = kCols;
+        }
+        conv_channel(conv_state, qkv, conv_w, g, c, dst, stride);
+    }
+    __syncthreads();
+    const bool owns_qk = cb == 0 && h < g.groups;
+    for (int vec = wave; vec < 2 * R; vec += kColThreads / 64) {
+        const int r = vec >> 1, which = vec & 1;
+        float *x = qk + (r * 2 + which) * kS;
+        const float a0 = x[lane], a1 = x[lane + 64];
+        double sq = (double)a0 * (double)a0 + (double)a1 * (double)a1;
+        sq = wave_sum_dd(sq);
+        const float extra = which == 0 ? g.q_scale : 1.0f;
+        const float scale = __fmul_rn((float)(1.0 / sqrt(sq + (double)g.eps)), extra);
+        const float y0 = __fmul_rn(a0, scale), y1 = __fmul_rn(a1, scale);
+        x[lane] = y0;
+        x[lane + 64] = y1;
+        if (owns_qk) {
+            float *dst = conv_out + (uint64_t)r * g.conv_dim + (which == 0 ? 0 : key_dim) + kh * kS;
+            dst[lane] = y0;
+            dst[lane + 64] = y1;
+        }
+    }
+    for (int idx = t; idx < R * kCols; idx += kColThreads) {
+        const int r = idx / kCols, cc = idx % kCols;
+        conv_out[(uint64_t)r * g.conv_dim + 2 * key_dim + h * kS + cb * kCols + cc] = vv[r * kCols + cc];
+    }
+    __syncthreads();
+    const int jl = j - cb * kCols;
+    for (int r = 0; r < R; r++) {
+        const float *q = qk + (r * 2 + 0) * kS, *k = qk + (r * 2 + 1) * kS;
+        const float decay = gdn_decay(g, alpha_raw, dt, a_log, r, h);
+        const float beta = g.coef ? beta_raw[(uint64_t)r * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)r * g.rank + h]);
+        float sk = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < 16; ii++) {
+            s_reg[ii] = __fmul_rn(s_reg[ii], decay);
+            sk = __fadd_rn(sk, __fmul_rn(s_reg[ii], k[p * 16 + ii]));
+        }
+        sk = group8_sum_f(sk);
+        const float d = __fmul_rn(__fsub_rn(vv[r * kCols + jl], sk), beta);
+        float o = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < 16; ii++) {
+            s_reg[ii] = __fadd_rn(s_reg[ii], __fmul_rn(k[p * 16 + ii], d));
+            o = __fadd_rn(o, __fmul_rn(s_reg[ii], q[p * 16 + ii]));
+        }
+        o = group8_sum_f(o);
+        if (p == 0) raw_out[((uint64_t)r * g.rank + h) * kS + j] = o;
+    }
+}
+
+// Commit: replay of the accepted rows for this block's columns, state
+// written back; this block's v channels and (cb == 0, h < groups) the q/k
+// group's channels move their conv window forward.
+__global__ __launch_bounds__(kColThreads) void gdn_commit_cols_kernel(
+    float *__restrict__ conv_state, float *__restrict__ state, const float *__restrict__ qkv,
+    const float *__restrict__ conv, const float *__restrict__ alpha_raw, const float *__restrict__ beta_raw,
+    const float *__restrict__ dt, const float *__restrict__ a_log, GdnArgs g,
+    const int32_t *__restrict__ accept_result) {
+    const int h = blockIdx.x, cb = blockIdx.y;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int K = g.kernel;
+    const int key_dim = g.groups * kS;
+    const int kh = h % g.groups;
+    const int n = accept_result ? min(accept_result[0] + 1, g.rows) : g.rows;
+    {
+        const bool qk_owner = cb == 0 && h < g.groups;
+        const int nch = kCols + (qk_owner ? 2 * kS : 0);
+        for (int ch = t; ch < nch; ch += kColThreads) {
+            const int c = ch < kCols ? 2 * key_dim + h * kS + cb * kCols + ch
+                                     : ((ch - kCols) < kS ? kh * kS + (ch - kCols) : key_dim + kh * kS + (ch - kCols - kS));
+            float win[8];
+#pragma unroll
+            for (int tt = 0; tt < 7; tt++) {
+                const int idx = n + tt - (K - 1);
+                win[tt] = tt >= K - 1 ? 0.0f
+                          : idx < 0   ? conv_state[(uint64_t)c * (K - 1) + (K - 1 + idx)]
+                                      : qkv[(uint64_t)idx * g.conv_dim + c];
+            }
+#pragma unroll
+            for (int tt = 0; tt < 7; tt++)
+                if (tt < K - 1) conv_state[(uint64_t)c * (K - 1) + tt] = win[tt];
+        }
+    }
+    const int p = lane & 7, j = cb * kCols + wave * 8 + (lane >> 3);
+    float *mat = state + (uint64_t)h * kS * kS;
+    float s_reg[16];
+#pragma unroll
+    for (int ii = 0; ii < 16; ii++) s_reg[ii] = mat[(uint64_t)(p * 16 + ii) * kS + j];
+    for (int r = 0; r < n; r++) {
+        const float *row = conv + (uint64_t)r * g.conv_dim;
+        const float *k = row + key_dim + kh * kS;
+        const float decay = gdn_decay(g, alpha_raw, dt, a_log, r, h);
+        const float beta = g.coef ? beta_raw[(uint64_t)r * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)r * g.rank + h]);
+        float kr[16];
+#pragma unroll
+        for (int ii = 0; ii < 16; ii++) kr[ii] = k[p * 16 + ii];
+        const float vj = row[2 * key_dim + h * kS + j];
+        float sk = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < 16; ii++) {
+            s_reg[ii] = __fmul_rn(s_reg[ii], decay);
+            sk = __fadd_rn(sk, __fmul_rn(s_reg[ii], kr[ii]));
+        }
+        sk = group8_sum_f(sk);
+        const float d = __fmul_rn(__fsub_rn(vj, sk), beta);
+#pragma unroll
+        for (int ii = 0; ii < 16; ii++) s_reg[ii] = __fadd_rn(s_reg[ii], __fmul_rn(kr[ii], d));
+    }
+#pragma unroll
+    for (int ii = 0; ii < 16; ii++) mat[(uint64_t)(p * 16 + ii) * kS + j] = s_reg[ii];
+}
+
+}  // namespace
+
+uint32_t gdn_verify_cols_lds_bytes(const GdnArgs &g) { return (uint32_t)(g.rows * 2 * kS + g.rows * kCols) * 4; }
+
+hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, const float *qkv,
+                                  const float *alpha_raw, const float *beta_raw, const float *conv_w, const float *dt,
+                                  const float *a_log, float *raw_out, float *conv_out, const GdnArgs &g,
+                                  hipStream_t s) {
+    gdn_verify_cols_kernel<<<dim3((unsigned)g.rank, kS / kCols), kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
+        conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_commit_cols(float *conv_state, float *state, const float *qkv, const float *conv,
+                                  const float *alpha_raw, const float *beta_raw, const float *dt, const float *a_log,
+                                  const GdnArgs &g, const int32_t *accept_result, hipStream_t s) {
+    gdn_commit_cols_kernel<<<dim3((unsigned)g.rank, kS / kCols), kColThreads, 0, s>>>(
+        conv_state, state, qkv, conv, alpha_raw, beta_raw, dt, a_log, g, accept_result);
+    return hipGetLastError();
+}
+
+uint32_t gdn_verify_lds_bytes(const GdnArgs &g) { return (uint32_t)(g.rows * 3 * kS + g.rows * kS) * 4; }
+
+hipError_t launch_gdn_verify(const float *conv_state, const float *state, const float *qkv, const float *z,
+                             const float *alpha_raw, const float *beta_raw, const float *conv_w, const float *dt,
+                             const float *a_log, const float *norm_w, float *out, float *conv_out, const GdnArgs &g,
+                             hipStream_t s) {
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(gdn_verify_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr = true;
+    }
+    gdn_verify_kernel<<<(unsigned)g.rank, kGdnThreads, gdn_verify_lds_bytes(g), s>>>(
+        conv_state, state, qkv, z, alpha_raw, beta_raw, conv_w, dt, a_log, norm_w, out, conv_out, g);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_commit(float *conv_state, float *state, const float *qkv, const float *conv,
+                             const float *alpha_raw, const float *beta_raw, const float *dt, const float *a_log,
+                             const GdnArgs &g, const int32_t *accept_result, hipStream_t s) {
+    gdn_commit_kernel<<<(unsigned)g.rank, kGdnThreads, 0, s>>>(conv_state, state, qkv, conv, alpha_raw, beta_raw, dt,
+                                                               a_log, g, accept_result);
+    return hipGetLastError();
+}
+
+}  // namespace yk

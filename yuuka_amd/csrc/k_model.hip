@@ -340,9 +340,14 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(float *__restrict__ state
         if (threadIdx.x < 128) kq[0][threadIdx.x] = row[key_dim + kh * S + threadIdx.x];
         else kq[1][threadIdx.x - 128] = row[kh * S + threadIdx.x - 128];
         if (threadIdx.x == 0) {
-            const float act = __fmul_rn(softplus_ref(__fadd_rn(alpha_raw[(uint64_t)r * g.rank + h], dt[h])), a_log[h]);
-            coef[0] = (float)exp((double)act);
-            coef[1] = sigmoid_ref(beta_raw[(uint64_t)r * g.rank + h]);
+            if (g.coef) {  // decay and sigmoid(beta) precomputed by the projection
+                coef[0] = alpha_raw[(uint64_t)r * g.rank + h];
+                coef[1] = beta_raw[(uint64_t)r * g.rank + h];
+            } else {
+                const float act = __fmul_rn(softplus_ref(__fadd_rn(alpha_raw[(uint64_t)r * g.rank + h], dt[h])), a_log[h]);
+                coef[0] = (float)exp((double)act);
+                coef[1] = sigmoid_ref(beta_raw[(uint64_t)r * g.rank + h]);
+            }
         }
         __syncthreads();
         const float decay = coef[0], beta = coef[1];

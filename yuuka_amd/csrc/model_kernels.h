@@ -36,6 +36,7 @@ struct AttnVArgs {
 struct GdnArgs {
     int rows, groups, rank, state, conv_dim, inner, kernel;
     float eps, q_scale;
+    int coef;  // 1: alpha / beta buffers hold the decay and sigmoid(beta)
 };
 
 hipError_t launch_embedding(const void *table, uint32_t dtype, uint64_t row_bytes, const int32_t *tokens, int vocab,
@@ -60,6 +61,22 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
                               const int32_t *table, const float *q_norm, const float *k_norm, const float2 *rope,
                               float *out, const AttnVArgs &a, void *scratch, const ModelDyn &dyn, int max_pos_hint,
                               hipStream_t s);
+uint32_t gdn_verify_lds_bytes(const GdnArgs &g);
+hipError_t launch_gdn_verify(const float *conv_state, const float *state, const float *qkv, const float *z,
+                             const float *alpha_raw, const float *beta_raw, const float *conv_w, const float *dt,
+                             const float *a_log, const float *norm_w, float *out, float *conv_out, const GdnArgs &g,
+                             hipStream_t s);
+hipError_t launch_gdn_commit(float *conv_state, float *state, const float *qkv, const float *conv,
+                             const float *alpha_raw, const float *beta_raw, const float *dt, const float *a_log,
+                             const GdnArgs &g, const int32_t *accept_result, hipStream_t s);
+uint32_t gdn_verify_cols_lds_bytes(const GdnArgs &g);
+hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, const float *qkv,
+                                  const float *alpha_raw, const float *beta_raw, const float *conv_w, const float *dt,
+                                  const float *a_log, float *raw_out, float *conv_out, const GdnArgs &g,
+                                  hipStream_t s);
+hipError_t launch_gdn_commit_cols(float *conv_state, float *state, const float *qkv, const float *conv,
+                                  const float *alpha_raw, const float *beta_raw, const float *dt, const float *a_log,
+                                  const GdnArgs &g, const int32_t *accept_result, hipStream_t s);
 hipError_t launch_attention(const float *q, const void *kpool, const void *vpool, const int32_t *table, float *out,
                             const AttnArgs &a, void *scratch, const ModelDyn &dyn, int max_pos_hint, hipStream_t s);
 hipError_t launch_gdn_conv(const float *conv_state, const float *qkv, const float *w, float *out, const GdnArgs &g,

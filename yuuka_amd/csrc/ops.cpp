@@ -74,6 +74,7 @@ static GdnArgs gdn_args(const yuuka_op &op) {
     g.kernel = (int)op.u[0];
     g.eps = op.f[0];
     g.q_scale = op.f[1];
+    g.coef = (op.flags & YUUKA_EXT_FLAG_GDN_COEF) ? 1 : 0;
     return g;
 }
 
@@ -107,6 +108,8 @@ static FusedGemmArgs fused_args(const yuuka_op &op) {
     FusedGemmArgs a{};
     a.x = at<const float>(op, 0);
     a.norm = at<const float>(op, 1);
+    a.gate = at<const float>(op, 14);
+    a.head_norm = at<const float>(op, 15);
     a.eps = op.f[0];
     a.K = (int)op.n[0];
     a.rows = (int)op.n[1];
@@ -122,6 +125,13 @@ static FusedGemmArgs fused_args(const yuuka_op &op) {
         g.w_bytes = (uint32_t)(g.row_bytes * (uint64_t)g.n);
         g.out = at<float>(op, 6 + i);
         g.res = at<const float>(op, 10 + i);
+        g.act = (int)((op.u[2] >> (4 * i)) & 0xfu);
+        g.p0 = g.p1 = nullptr;
+        if (g.act == 3) {  // the (unused) residual slot carries {dt[n], a[n]}
+            g.p0 = g.res;
+            g.p1 = g.res + g.n;
+            g.res = nullptr;
+        }
     }
     return a;
 }
@@ -344,7 +354,18 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         }
         if (epi == kEpiSwiglu && (op.n[2] != op.n[3] || (op.u[0] & 0xff) != ((op.u[0] >> 8) & 0xff)))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED SwiGLU: gate and up must match");
-        if (fused_gemm_chunk_sb((int)rows, (int)K, fused_tiles(op, nseg), op.buf[1] != nullptr) < 1)
+        if (op.buf[14] && (op.buf[1] || !buf_ok(op.buf[14], op.off[14], K * rows * 4) ||
+                           !buf_ok(op.buf[15], op.off[15], 128 * 4) || K % 128 || op.off[14] % 16 || op.off[15] % 16))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED gated head norm: buffers (and no RMSNorm weight)");
+        if (op.u[2] && epi != kEpiStore)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED: output maps need the store epilogue");
+        for (int i = 0; i < nseg; i++) {
+            const uint32_t act = (op.u[2] >> (4 * i)) & 0xfu;
+            if (act > 3) return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED segment %d: output map %u", i, act);
+            if (act == 3 && !buf_ok(op.buf[10 + i], op.off[10 + i], 2 * op.n[2 + i] * 4))
+                return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED segment %d: decay parameters {dt, a}", i);
+        }
+        if (fused_gemm_chunk_sb((int)rows, (int)K, fused_tiles(op, nseg), op.buf[1] != nullptr, op.buf[14] != nullptr) < 1)
             return fail(YUUKA_ERR_UNSUPPORTED, "GEMM_FUSED: activations do not fit LDS");
         return YUUKA_OK;
     }
@@ -447,6 +468,19 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
         const bool defer = (op.flags & YUUKA_EXT_FLAG_DEFER) != 0;
         float *conv = at<float>(op, 11);
         float *raw = static_cast<float *>(ctx.ws);
+        if (defer && (op.flags & YUUKA_EXT_FLAG_RAW_OUT) && g.rows <= 16) {  // column-split scan (k_gdn.hip)
+            err = launch_gdn_verify_cols(at<const float>(op, 0), at<const float>(op, 1), at<const float>(op, 2),
+                                         at<const float>(op, 4), at<const float>(op, 5), at<const float>(op, 6),
+                                         at<const float>(op, 7), at<const float>(op, 8), at<float>(op, 10), conv, g, s);
+            break;
+        }
+        if (defer && g.rows <= 16 && !getenv("YUUKA_GDN_SPLIT")) {  // one fused kernel per layer (k_gdn.hip)
+            err = launch_gdn_verify(at<const float>(op, 0), at<const float>(op, 1), at<const float>(op, 2),
+                                    at<const float>(op, 3), at<const float>(op, 4), at<const float>(op, 5),
+                                    at<const float>(op, 6), at<const float>(op, 7), at<const float>(op, 8),
+                                    at<const float>(op, 9), at<float>(op, 10), conv, g, s);
+            break;
+        }
         err = launch_gdn_conv(at<const float>(op, 0), at<const float>(op, 2), at<const float>(op, 6), conv, g, s);
         if (err == hipSuccess)
             err = launch_gdn_scan(at<float>(op, 1), conv, at<const float>(op, 4), at<const float>(op, 5),
@@ -469,7 +503,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
     case YUUKA_EXT_OP_GEMM_FUSED: {
         FusedGemmArgs a = fused_args(op);
         const int tt = fused_tiles(op, a.nseg);
-        a.chunk_sb = fused_gemm_chunk_sb(a.rows, a.K, tt, a.norm != nullptr);
+        a.chunk_sb = fused_gemm_chunk_sb(a.rows, a.K, tt, a.norm != nullptr, a.gate != nullptr);
         err = launch_fused_gemm(a, tt, s);
         break;
     }
@@ -493,6 +527,12 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
     case YUUKA_EXT_OP_GDN_COMMIT: {
         const GdnArgs g = gdn_args(op);
         const int32_t *res = at<const int32_t>(op, 8);
+        if (!getenv("YUUKA_GDN_SPLIT")) {  // scan replay + conv window, column-split (k_gdn.hip)
+            err = launch_gdn_commit_cols(at<float>(op, 0), at<float>(op, 1), at<const float>(op, 2), at<const float>(op, 3),
+                                    at<const float>(op, 4), at<const float>(op, 5), at<const float>(op, 6),
+                                    at<const float>(op, 7), g, res, s);
+            break;
+        }
         err = launch_gdn_scan(at<float>(op, 1), at<const float>(op, 3), at<const float>(op, 4), at<const float>(op, 5),
                               at<const float>(op, 6), at<const float>(op, 7), nullptr, g, 1, res, s);
         if (err == hipSuccess) err = launch_gdn_conv_commit(at<float>(op, 0), at<const float>(op, 2), g, res, s);
