@@ -44,6 +44,8 @@ def parse():
     ap.add_argument("--drafts", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="time only the dominant kernel, then one 256 MiB copy (profiling calibration)")
     return ap.parse_args()
 
 
@@ -190,6 +192,82 @@ def lookup_draft(history, max_draft, min_match=2):
     return []
 
 
+def read_traffic(name):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel
+    calibration), or None when the summary is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
+    try:
+        with open(path) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_launch:"):
+                    return float(ln.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def dominant_kernel(dev, cfg, rows, rng):
+    from yuuka_amd import hip, synth
+    # Dominant kernel: the fused FFN gate/up verify GEMM (RMSNorm + activation
+    # quantization prologue, two Q4_K 9216x2560 weight streams, SwiGLU
+    # epilogue), the largest weight stream of every layer, launched exactly as
+    # the engine launches it (one GEMM_FUSED op), timed live with HIP events
+    # on the stream it runs on. One plan holds `copies` ops over distinct
+    # weight buffers (>= 512 MB in all) so that no launch finds its weights
+    # in the Infinity Cache.
+    N, K = cfg.ffn, cfg.hidden
+    wq = synth.quant_matrix(rng, synth.Q4_K, N, K)
+    copies = max(1, -(-512 * 2**20 // (2 * wq.nbytes)))
+    wg = [dev.upload(wq) for _ in range(copies)]
+    wu = [dev.upload(wq) for _ in range(copies)]
+    st = hip.Stream(dev)
+    xb = dev.upload(rng.normal(0, 1, (rows, K)).astype(np.float32))
+    nb = dev.upload((1.0 + 0.1 * rng.normal(0, 1, K)).astype(np.float32))
+    ob = dev.alloc(rows * N * 4)
+    plan = hip.Plan(dev)
+    for i in range(copies):
+        hip.gemm_fused_op(plan, xb, K, rows, [(wg[i], synth.Q4_K, N, ob, None), (wu[i], synth.Q4_K, N, None, None)],
+                          epilogue=hip.EPI_SWIGLU, norm=nb, eps=cfg.eps)
+    for _ in range(2):
+        plan.execute(st)
+    st.sync()
+    e0, e1 = hip.Event(dev, timed=True), hip.Event(dev, timed=True)
+    reps = max(1, 200 // copies)
+    e0.record(st)
+    for _ in range(reps):
+        plan.execute(st)
+    e1.record(st)
+    st.sync()
+    gemm_us = e1.elapsed_ms(e0) * 1e3 / (reps * copies)
+    gemm_bytes = 2 * wq.nbytes + rows * K * 4 + K * 4 + rows * N * 4
+    gemm_ach = gemm_bytes / (gemm_us * 1e-6) / 1e9
+    plan.destroy()
+    for b in wg + wu:
+        b.free()
+    return {"bound": "hbm", "achieved": gemm_ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": gemm_ach / HBM_PEAK_GBS, "traffic": read_traffic("fgemm_ffn_swiglu_pmc.md"),
+            "kernel": f"fgemm_kernel<12,2,1> (GEMM_FUSED SwiGLU) 2x{N}x{K} Q4_K M={rows}",
+            "alg_bytes_per_launch": gemm_bytes, "avg_us": gemm_us, "launches": reps * copies}
+
+
+def kernel_only(args):
+    """--kernel-only: the dominant-kernel measurement alone, followed by one
+    plain 256 MiB device-to-device copy (the calibration kernel for the
+    FETCH_SIZE/WRITE_SIZE counters). Used for the rocprofv3 --pmc passes."""
+    from yuuka_amd import hip, model as Mdl
+    dev = hip.Device(0)
+    rng = np.random.default_rng(2)
+    dk = dominant_kernel(dev, Mdl.QWEN35_4B_LIKE, args.drafts + 1, rng)
+    nbytes = 256 * 2**20
+    src, dst = dev.alloc(nbytes), dev.alloc(nbytes)
+    st = hip.Stream(dev)
+    hip.check(hip.lib().yuuka_buffer_copy(st.ptr, dst.ptr, 0, src.ptr, 0, nbytes, None), "buffer_copy")
+    st.sync()
+    return {"kernel_only": dk, "copy_calibration_bytes": nbytes}
+
+
+
 def bench_config2(args):
     """full verify step on the Qwen3.5-4B-like hybrid
     decoder (random init, Q4_K_M mix), 512-token prompt in paged F16 KV,
@@ -247,30 +325,7 @@ def bench_config2(args):
     step_bytes = wbytes + kv_bytes + state_bytes + logit_bytes
     step_ach = step_bytes / (step_gpu_ms * 1e-3) / 1e9
 
-    # Dominant kernel (Q4_K verify GEMM at the FFN gate/up shape, the most
-    # frequent weight stream of the step), timed live on one stream.
-    N, K = cfg.ffn, cfg.hidden
-    wq = synth.quant_matrix(rng, synth.Q4_K, N, K)
-    copies = max(1, -(-512 * 2**20 // wq.nbytes))
-    wbufs = [dev.upload(wq)] + [dev.upload(synth.quant_matrix(rng, synth.Q4_K, N, K)) for _ in range(copies - 1)]
-    st = hip.Stream(dev)
-    xb = dev.upload(rng.normal(0, 1, (rows, K)).astype(np.float32))
-    xq = dev.alloc(hip.quantized_bytes(K, rows))
-    ob = dev.alloc(rows * N * 4)
-    hip.quantize_activations(st, xq, xb, K, rows)
-    for i in range(10):
-        hip.gemm_quantized(st, ob, xq, wbufs[i % copies], K, N, rows, synth.Q4_K)
-    st.sync()
-    e0, e1 = hip.Event(dev, timed=True), hip.Event(dev, timed=True)
-    reps = 200
-    e0.record(st)
-    for i in range(reps):
-        hip.gemm_quantized(st, ob, xq, wbufs[i % copies], K, N, rows, synth.Q4_K)
-    e1.record(st)
-    st.sync()
-    gemm_us = e1.elapsed_ms(e0) * 1e3 / reps
-    gemm_bytes = wq.nbytes + rows * K * 4 + rows * N * 4
-    gemm_ach = gemm_bytes / (gemm_us * 1e-6) / 1e9
+    dk = dominant_kernel(dev, cfg, rows, rng)
 
     line = {
         "metric": "accepted tokens/s on 1 MI355X; verify-step HBM GB/s vs peak",
@@ -296,10 +351,7 @@ def bench_config2(args):
         "step_roofline": {"bound": "hbm", "achieved": step_ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": step_ach / HBM_PEAK_GBS, "alg_bytes_per_step": step_bytes,
                           "weights": wbytes, "kv": kv_bytes, "gdn_state": state_bytes, "logits": logit_bytes},
-        "roofline": {"bound": "hbm", "achieved": gemm_ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": gemm_ach / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": f"gemm_q4k_kernel<1> {N}x{K} M={rows}", "alg_bytes_per_launch": gemm_bytes,
-                     "avg_us": gemm_us},
+        "roofline": dk,
         "context_end": ctx,
         "prefill_s": prefill_s,
         "weight_gen_s": gen_s,
@@ -356,7 +408,9 @@ def main():
                                    "(multi-GPU sharding is a design note, not implemented)"}))
         sys.exit(2)
     ensure_built()
-    if args.config == 1:
+    if args.kernel_only:
+        line = kernel_only(args)
+    elif args.config == 1:
         args.steps = args.steps or 200
         args.warmup = args.warmup if args.warmup is not None else 20
         line = bench_config1(args)
