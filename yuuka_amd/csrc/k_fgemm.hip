@@ -56,14 +56,13 @@ constexpr int kQ6K = YUUKA_DTYPE_Q6_K;
 constexpr int kQMax = 32639;  // |q| bound that keeps the high plane in int8
 constexpr int kWaves = kFusedWaves;
 constexpr int kThreads = 64 * kWaves;
+// 1/rms of the rows: 16 floats per wave
+constexpr uint32_t kInvBytes = kWaves * 16 * 4;
 
 // Keeps one ring stage's activation reads from being hoisted into the
 // previous stage (that multiplies live registers).
 #ifndef YK_FG_STAGE_FENCE
 #define YK_FG_STAGE_FENCE() __builtin_amdgcn_sched_barrier(0)
-#endif
-#ifndef YK_FG_PAIRS
-#define YK_FG_PAIRS 4
 #endif
 #ifndef YK_FG_DEPTH1
 #define YK_FG_DEPTH1 2
@@ -77,6 +76,17 @@ __device__ uint64_t *yk_fg_dbg;
 #else
 #define YK_FG_STAMP(v) (void)0
 #endif
+
+// Workgroup barrier that orders LDS only. __syncthreads() also fences
+// global memory, which makes every wave wait for all of its outstanding
+// weight loads at the barrier; the kernels here share data between waves
+// through LDS alone (activation copies into LDS are waited for by the wave
+// that issued them before it reaches a barrier).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 __device__ __forceinline__ i32x4 mfma_i8(int64_t a, int64_t b) {
     const i32x4 zero = {0, 0, 0, 0};
@@ -162,7 +172,7 @@ __device__ __forceinline__ int quad_sum(int v) {
 //   sums   [cap][RHOP][8] int16      (sub-block sums of each plane row)
 //   xs     [cap][RHOP] float         (activation scale of each plane row)
 //   nsq    [rows][nsb] float         (per super-block sums of x^2, norm)
-//   junk   16 B                      (stores of units past the end)
+//   junk   8 B per lane              (stores of units past the end)
 // The tables hold `cap` super-blocks (the chunk capacity); `cnt` of them are
 // live in the current chunk.
 struct ActLayout {
@@ -178,11 +188,24 @@ struct ActLayout {
         xs = sums + (uint32_t)cap * rhop * 16;
         nsq = xs + (uint32_t)cap * rhop * 4;
         junk = nsq + (uint32_t)rows * nsb * 4;
-        total = (junk + 16 + 15) & ~15u;
+        total = (junk + 512 + 15) & ~15u;
     }
 };
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+// One wave-wide 16-byte-per-lane copy from global memory straight into LDS
+// (lane l writes [dst + 16 l, +16)). Written as inline assembly so that the
+// compiler's wait-count tracking does not see it: otherwise it waits for
+// every outstanding vector load (the weight stream) before any later LDS
+// access, as it cannot tell which loads target LDS. Callers wait for the
+// copy themselves (s_waitcnt vmcnt) before reading it; the copies are
+// issued before the weight loads, so the compiler's own counts for those
+// stay exact (loads it does not know of only make its waits longer).
+__device__ __forceinline__ void lds_copy16(const float *src, uint8_t *lds, uint32_t dst) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds + dst));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(base) : "memory", "m0");
+}
 
 // Issues the chunk's activation (and norm weight) copies into LDS: one
 // 1 KB wave load per (row, super-block), no registers held.
@@ -208,138 +231,139 @@ __device__ __forceinline__ void act_fetch(const FusedGemmArgs &A, const ActLayou
             src = A.norm + (size_t)(c0 + sbl) * 256 + lane * 4;
             dst = L.graw + (uint32_t)sbl * 1024;
         }
-        __builtin_amdgcn_global_load_lds((const void *)src, (lds_ptr_t)(lds + dst), 16, 0, 0);
+        lds_copy16(src, lds, dst);
     }
 }
 
+// Row reductions (every lane of each 16-lane DPP row receives the row's
+// result) for the prologue: unsigned maximum, FP32 and FP64 sums.
+__device__ __forceinline__ uint32_t row_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)dpp<0xb1>((int)v));
+    v = max(v, (uint32_t)dpp<0x4e>((int)v));
+    v = max(v, (uint32_t)dpp<0x124>((int)v));
+    return max(v, (uint32_t)dpp<0x128>((int)v));
+}
+// Sum over each group of 8 lanes (quad sums, then the mirrored half row).
+__device__ __forceinline__ int oct_sum(int v) {
+    v += dpp<0xb1>(v);
+    v += dpp<0x4e>(v);
+    return v + dpp<0x141>(v);
+}
+__device__ __forceinline__ uint32_t rl_u(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
+__device__ __forceinline__ double rl_d(double v, int l) {
+    const uint64_t b = __double_as_longlong(v);
+    const uint32_t lo = rl_u((uint32_t)b, l), hi = rl_u((uint32_t)(b >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// x * inv rounded to the nearest integer q and offset by 128 sits in the low
+// bits of this FP32 sum: bits = 0x4B400000 + q + 128 for |q| < 2^22, so byte 1
+// is the high plane h = (q + 128) >> 8 and byte 0 XOR 0x80 the low plane
+// l = q - 256 h (one fused multiply-add per element, round to nearest even).
+constexpr float kRoundMagic = 12582912.0f + 128.0f;
+
 // Quantizes super-blocks [c0, c0 + cnt) of every row from the LDS copy made
-// by act_fetch. Wave w owns the chunk's super-blocks w, w + kWaves, ...; its
-// (row, super-block) units are taken two at a time, one per half wave, where
-// lane s of the half quantizes elements [8s, 8s + 8) (sub-block s/4, MFMA
-// slice s%4). Stores are branch-free (a unit past the end writes to a
-// scratch slot).
-__device__ __forceinline__ void act_prologue(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, int c0,
-                                             int nsb) {
+// by act_fetch. A (row, super-block) unit is one wave's work: lane s holds
+// elements [4s, 4s + 4), i.e. sub-block s / 8, MFMA slice (s / 2) % 4, bytes
+// 4 (s % 2) .. +4 of that slice. Reductions stay inside DPP rows; the four row
+// results combine through readlane into scalars. Wave w owns units w, w + 8,
+// ... (row-major over the chunk). The loop body is straight-line code over
+// kUnits units at once (independent dependency chains interleave); units
+// past the end are computed on a clamped index and their stores go to a
+// per-lane scratch slot. MODE: 0 y = x, 1 y = x * g (RMSNorm weight, sums of
+// x^2 recorded), 2 gated head norm.
+template <int MODE>
+__device__ __forceinline__ void act_prologue_m(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, int c0,
+                                               int nsb, float4 hw) {
+    constexpr int kUnits = 4;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int half = lane >> 5, s = lane & 31;
     const int M = A.rows;
-    const int total = M * L.cnt;                              // (row, super-block) units of the chunk
-    const int units = wave < total ? (total - wave + kWaves - 1) / kWaves : 0;  // mine: wave + kWaves*i
-    constexpr int kPairs = YK_FG_PAIRS;  // unit pairs per batch
-    float *nsq = reinterpret_cast<float *>(lds + L.nsq);
-    float *xsv = reinterpret_cast<float *>(lds + L.xs);
-    int16_t *sums = reinterpret_cast<int16_t *>(lds + L.sums);
-    uint8_t *junk = lds + L.junk;
+    const int total = M * L.cnt;
+    const int j = lane >> 3, g = (lane >> 1) & 3, hf = lane & 1;
+    const uint32_t junk = L.junk + (uint32_t)lane * 8;
     const float *raw = reinterpret_cast<const float *>(lds + L.raw);
     const float *graw = reinterpret_cast<const float *>(lds + L.graw);
-    const int jl = s >> 2, g = s & 3;
-    // head-norm weights of this lane's 8 elements (position (s % 16) * 8 in its head)
-    float hw[8];
-    if (A.gate) {
-        const float4 h0 = *reinterpret_cast<const float4 *>(A.head_norm + (s & 15) * 8);
-        const float4 h1 = *reinterpret_cast<const float4 *>(A.head_norm + (s & 15) * 8 + 4);
-        hw[0] = h0.x; hw[1] = h0.y; hw[2] = h0.z; hw[3] = h0.w;
-        hw[4] = h1.x; hw[5] = h1.y; hw[6] = h1.z; hw[7] = h1.w;
-    }
-    // unit index -> (row, super-block): row-major over the chunk, u = m * cnt + sbl
-    for (int q0 = 0; q0 < units; q0 += 2 * kPairs) {
-        float4 xa[kPairs], xb[kPairs], ga[kPairs], gb[kPairs];
-        int mq[kPairs], sq[kPairs];
+    const float *zraw = reinterpret_cast<const float *>(lds + L.zraw);
+    for (int u0 = wave; u0 < total; u0 += kWaves * kUnits) {
+        float v[kUnits][4], sq[kUnits];
+        int m[kUnits], sbl[kUnits];
+        bool live[kUnits];
 #pragma unroll
-        for (int p = 0; p < kPairs; p++) {
-            // this half's unit, from wave-uniform pieces (no per-lane array index)
-            const int ua = min(wave + kWaves * (q0 + 2 * p), total - 1);
-            const int ub = min(wave + kWaves * (q0 + 2 * p + 1), total - 1);
-            const int ma = ua / L.cnt, mb = ub / L.cnt;
-            const int sa = ua - ma * L.cnt, sbb = ub - mb * L.cnt;
-            mq[p] = ma + half * (mb - ma);
-            sq[p] = sa + half * (sbb - sa);
-            const float *src = raw + (sq[p] * M + mq[p]) * 256 + s * 8;
-            xa[p] = *reinterpret_cast<const float4 *>(src);
-            xb[p] = *reinterpret_cast<const float4 *>(src + 4);
-            if (A.norm) {
-                ga[p] = *reinterpret_cast<const float4 *>(graw + sq[p] * 256 + s * 8);
-                gb[p] = *reinterpret_cast<const float4 *>(graw + sq[p] * 256 + s * 8 + 4);
+        for (int k = 0; k < kUnits; k++) {
+            const int u = min(u0 + kWaves * k, total - 1);
+            live[k] = u0 + kWaves * k < total;
+            m[k] = u / L.cnt;
+            sbl[k] = u - m[k] * L.cnt;
+            const float4 x = *reinterpret_cast<const float4 *>(raw + (sbl[k] * M + m[k]) * 256 + lane * 4);
+            v[k][0] = x.x; v[k][1] = x.y; v[k][2] = x.z; v[k][3] = x.w;
+            sq[k] = 0.0f;
+            if constexpr (MODE == 1) {
+                const float4 w = *reinterpret_cast<const float4 *>(graw + sbl[k] * 256 + lane * 4);
+                sq[k] = fmaf(v[k][3], v[k][3], fmaf(v[k][2], v[k][2], fmaf(v[k][1], v[k][1], v[k][0] * v[k][0])));
+                v[k][0] = __fmul_rn(v[k][0], w.x); v[k][1] = __fmul_rn(v[k][1], w.y);
+                v[k][2] = __fmul_rn(v[k][2], w.z); v[k][3] = __fmul_rn(v[k][3], w.w);
+            }
+            if constexpr (MODE == 2) {
+                // gated head norm: lanes [32h, 32h + 32) hold head h (two DPP rows)
+                const float4 z = *reinterpret_cast<const float4 *>(zraw + (sbl[k] * M + m[k]) * 256 + lane * 4);
+                double ss = 0.0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) ss += (double)v[k][i] * (double)v[k][i];
+                ss = row_sum_d(ss);
+                const double h0 = rl_d(ss, 15) + rl_d(ss, 31), h1 = rl_d(ss, 47) + rl_d(ss, 63);
+                const double hs = lane < 32 ? h0 : h1;
+                const float mean = (float)(hs / 128.0);
+                const float scale = (float)(1.0 / sqrt((double)(mean + A.eps)));
+                v[k][0] = __fmul_rn(__fmul_rn(v[k][0], __fmul_rn(scale, hw.x)), z.x);
+                v[k][1] = __fmul_rn(__fmul_rn(v[k][1], __fmul_rn(scale, hw.y)), z.y);
+                v[k][2] = __fmul_rn(__fmul_rn(v[k][2], __fmul_rn(scale, hw.z)), z.z);
+                v[k][3] = __fmul_rn(__fmul_rn(v[k][3], __fmul_rn(scale, hw.w)), z.w);
             }
         }
 #pragma unroll
-        for (int p = 0; p < kPairs; p++) {
-            const bool valid = q0 + 2 * p + half < units;
-            const int m = mq[p], sbl = sq[p];
-            float v[8] = {xa[p].x, xa[p].y, xa[p].z, xa[p].w, xb[p].x, xb[p].y, xb[p].z, xb[p].w};
-            if (A.norm) {
-                float t = 0.0f;
-#pragma unroll
-                for (int i = 0; i < 8; i++) t = fmaf(v[i], v[i], t);
-                t = row_sum(t);
-                const float tot = half ? rdl(t, 32) + rdl(t, 48) : rdl(t, 0) + rdl(t, 16);
-                float *dst = valid ? nsq + m * nsb + c0 + sbl : reinterpret_cast<float *>(junk);
-                *dst = tot;
-                const float gg[8] = {ga[p].x, ga[p].y, ga[p].z, ga[p].w, gb[p].x, gb[p].y, gb[p].z, gb[p].w};
-#pragma unroll
-                for (int i = 0; i < 8; i++) v[i] = __fmul_rn(v[i], gg[i]);
-            }
-            if (A.gate) {
-                // gated head norm: a 16-lane DPP row holds one 128-element head
-                const float *zsrc = reinterpret_cast<const float *>(lds + L.zraw) + (sbl * M + m) * 256 + s * 8;
-                const float4 za = *reinterpret_cast<const float4 *>(zsrc), zb = *reinterpret_cast<const float4 *>(zsrc + 4);
-                const float zz[8] = {za.x, za.y, za.z, za.w, zb.x, zb.y, zb.z, zb.w};
-                double ss = 0.0;
-#pragma unroll
-                for (int i = 0; i < 8; i++) ss += (double)v[i] * (double)v[i];
-                ss = row_sum_d(ss);
-                const float mean = (float)(ss / 128.0);
-                const float scale = (float)(1.0 / sqrt((double)(mean + A.eps)));
-#pragma unroll
-                for (int i = 0; i < 8; i++)
-                    v[i] = __fmul_rn(__fmul_rn(v[i], __fmul_rn(scale, hw[i])), zz[i]);
-            }
-            float a = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))),
-                            fmaxf(fmaxf(fabsf(v[4]), fabsf(v[5])), fmaxf(fabsf(v[6]), fabsf(v[7]))));
-            a = row_max(a);
-            const float amax = half ? fmaxf(rdl(a, 32), rdl(a, 48)) : fmaxf(rdl(a, 0), rdl(a, 16));
+        for (int k = 0; k < kUnits; k++) {
+            // max |v| over the unit (non-negative floats order as integers)
+            const uint32_t a = max(max(__float_as_uint(v[k][0]) & 0x7fffffffu, __float_as_uint(v[k][1]) & 0x7fffffffu),
+                                   max(__float_as_uint(v[k][2]) & 0x7fffffffu, __float_as_uint(v[k][3]) & 0x7fffffffu));
+            const uint32_t ar = row_max_u32(a);
+            const float amax = __uint_as_float(max(max(rl_u(ar, 15), rl_u(ar, 31)), max(rl_u(ar, 47), rl_u(ar, 63))));
             // xs * inv ~ 1 keeps every value exact to the quantization step;
             // the reciprocal keeps |v * inv| <= kQMax + 2^-10, so no clamp.
             const float xs = amax * (1.0f / (float)kQMax);
             const float inv = amax > 0.0f ? (float)kQMax * __builtin_amdgcn_rcpf(amax) : 0.0f;
-            int q[8], hsum = 0, qsum = 0;
-            uint32_t hb[8];
+            uint32_t t[4];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                q[i] = (int)rintf(v[i] * inv);
-                hb[i] = (uint32_t)(q[i] + 128);  // high plane h = (q + 128) >> 8 sits in byte 1
-                hsum += (int)hb[i] >> 8;
-                qsum += q[i];
+            for (int i = 0; i < 4; i++) t[i] = __float_as_uint(fmaf(v[k][i], inv, kRoundMagic));
+            const uint32_t hp = __builtin_amdgcn_perm(t[1], t[0], 0x0c0c0501u) | __builtin_amdgcn_perm(t[3], t[2], 0x05010c0cu);
+            const uint32_t lp = (__builtin_amdgcn_perm(t[1], t[0], 0x0c0c0400u) | __builtin_amdgcn_perm(t[3], t[2], 0x04000c0cu)) ^
+                                0x80808080u;
+            const uint32_t slot = L.planes + ((uint32_t)((sbl[k] * 8 + j) * 4 + g) * L.rho + m[k]) * 8 + 4 * hf;
+            *reinterpret_cast<uint32_t *>(lds + (live[k] ? slot : junk)) = hp;
+            *reinterpret_cast<uint32_t *>(lds + (live[k] ? slot + (uint32_t)M * 8 : junk + 4)) = lp;
+            // exact int16 sums of both planes per 32-element sub-block
+            const int hs = oct_sum(__builtin_amdgcn_sdot4((int)hp, 0x01010101, 0, false));
+            const int ls = oct_sum(__builtin_amdgcn_sdot4((int)lp, 0x01010101, 0, false));
+            const bool lead = live[k] && (lane & 7) == 0;
+            const uint32_t sh = L.sums + (((uint32_t)sbl[k] * L.rhop + m[k]) * 8 + j) * 2;
+            const uint32_t sl = L.sums + (((uint32_t)sbl[k] * L.rhop + M + m[k]) * 8 + j) * 2;
+            *reinterpret_cast<int16_t *>(lds + (lead ? sh : junk)) = (int16_t)hs;
+            *reinterpret_cast<int16_t *>(lds + (lead ? sl : junk + 2)) = (int16_t)ls;
+            const bool first = live[k] && lane == 0;
+            const uint32_t xh = L.xs + ((uint32_t)sbl[k] * L.rhop + m[k]) * 4;
+            const uint32_t xl = L.xs + ((uint32_t)sbl[k] * L.rhop + M + m[k]) * 4;
+            *reinterpret_cast<float *>(lds + (first ? xh : junk)) = xs;
+            *reinterpret_cast<float *>(lds + (first ? xl : junk + 4)) = xs;
+            if constexpr (MODE == 1) {
+                const float r = row_sum(sq[k]);
+                const float tot = (rdl(r, 15) + rdl(r, 31)) + (rdl(r, 47) + rdl(r, 63));
+                const uint32_t nq = L.nsq + (uint32_t)(m[k] * nsb + c0 + sbl[k]) * 4;
+                *reinterpret_cast<float *>(lds + (first ? nq : junk)) = tot;
             }
-            // l = q - 256 h has the low byte of q; h the second byte of q + 128
-            const uint32_t l0 = __builtin_amdgcn_perm((uint32_t)q[1], (uint32_t)q[0], 0x0c0c0400u) |
-                                (__builtin_amdgcn_perm((uint32_t)q[3], (uint32_t)q[2], 0x0c0c0400u) << 16);
-            const uint32_t l1 = __builtin_amdgcn_perm((uint32_t)q[5], (uint32_t)q[4], 0x0c0c0400u) |
-                                (__builtin_amdgcn_perm((uint32_t)q[7], (uint32_t)q[6], 0x0c0c0400u) << 16);
-            const uint32_t h0 = __builtin_amdgcn_perm(hb[1], hb[0], 0x0c0c0501u) |
-                                (__builtin_amdgcn_perm(hb[3], hb[2], 0x0c0c0501u) << 16);
-            const uint32_t h1 = __builtin_amdgcn_perm(hb[5], hb[4], 0x0c0c0501u) |
-                                (__builtin_amdgcn_perm(hb[7], hb[6], 0x0c0c0501u) << 16);
-            const int j = sbl * 8 + jl;
-            uint8_t *hp = valid ? lds + L.planes + ((uint32_t)(j * 4 + g) * L.rho + m) * 8 : junk;
-            uint8_t *lp = valid ? lds + L.planes + ((uint32_t)(j * 4 + g) * L.rho + M + m) * 8 : junk;
-            *reinterpret_cast<uint2 *>(hp) = make_uint2(h0, h1);
-            *reinterpret_cast<uint2 *>(lp) = make_uint2(l0, l1);
-            // sub-block (4 lanes) sums of both planes: sum l = sum q - 256 sum h
-            hsum = quad_sum(hsum);
-            qsum = quad_sum(qsum);
-            int16_t *sh = valid ? sums + ((uint32_t)sbl * L.rhop + m) * 8 + jl : reinterpret_cast<int16_t *>(junk);
-            int16_t *sl = valid ? sums + ((uint32_t)sbl * L.rhop + M + m) * 8 + jl : reinterpret_cast<int16_t *>(junk);
-            *sh = (int16_t)hsum;
-            *sl = (int16_t)(qsum - 256 * hsum);
-            float *xh = valid ? xsv + (uint32_t)sbl * L.rhop + m : reinterpret_cast<float *>(junk);
-            float *xl = valid ? xsv + (uint32_t)sbl * L.rhop + M + m : reinterpret_cast<float *>(junk);
-            *xh = xs;
-            *xl = xs;
         }
     }
     // rows past 2M of the padded tables read as zero
+    float *xsv = reinterpret_cast<float *>(lds + L.xs);
     for (int idx = threadIdx.x; idx < L.cnt * L.rhop; idx += kThreads) {
         const int rho = idx % L.rhop;
         if (rho >= L.rho) {
@@ -347,6 +371,21 @@ __device__ __forceinline__ void act_prologue(const FusedGemmArgs &A, const ActLa
             *reinterpret_cast<uint4 *>(lds + L.sums + (uint32_t)idx * 16) = make_uint4(0, 0, 0, 0);
         }
     }
+}
+
+// Head-norm weights of this lane's 4 prologue elements (position 4 (s % 32)
+// in its head), gated mode only. Loaded at kernel start, before the weight
+// stream, so that waiting for them does not wait for the weights.
+__device__ __forceinline__ float4 head_norm_lane(const FusedGemmArgs &A) {
+    if (!A.gate) return make_float4(0.f, 0.f, 0.f, 0.f);
+    return *reinterpret_cast<const float4 *>(A.head_norm + (threadIdx.x & 31) * 4);
+}
+
+__device__ __forceinline__ void act_prologue(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, int c0,
+                                             int nsb, float4 hw) {
+    if (A.gate) act_prologue_m<2>(A, L, lds, c0, nsb, hw);
+    else if (A.norm) act_prologue_m<1>(A, L, lds, c0, nsb, hw);
+    else act_prologue_m<0>(A, L, lds, c0, nsb, hw);
 }
 
 // Staged weight bytes of one 16-row tile for one super-block.
@@ -536,10 +575,10 @@ __device__ __forceinline__ void chunk_pass(const FusedGemmArgs &A, const ActLayo
         // the LDS copies (issued before the weights) are complete once the
         // counter drains; the weights are already in flight behind them
         __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        lds_barrier();
         YK_FG_STAMP(t_wait);
-        act_prologue(A, L, lds, c0, nsb);
-        __syncthreads();
+        act_prologue(A, L, lds, c0, nsb, head_norm_lane(A));
+        lds_barrier();
         YK_FG_STAMP(t_pro);
     }
     for (int base = 0; base < mine; base += D) {
@@ -629,14 +668,14 @@ __device__ __forceinline__ void group_epilogue(const FusedGemmArgs &A, float *re
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int M = A.rows;
-    __syncthreads();  // the previous group's partials are consumed
+    lds_barrier();  // the previous group's partials are consumed
 #pragma unroll
     for (int t = 0; t < TT; t++)
 #pragma unroll
         for (int a = 0; a < NA; a++)
 #pragma unroll
             for (int i = 0; i < 4; i++) red[(((wave * TT + t) * NA + a) * 4 + i) * 64 + lane] = acc[t][a][i];
-    __syncthreads();
+    lds_barrier();
     auto partial = [&](int t, int rho, int col) {
         const int a = rho >> 4, g = (rho & 15) >> 2, i = rho & 3;
         float v = 0.0f;
@@ -667,20 +706,144 @@ __device__ __forceinline__ void group_epilogue(const FusedGemmArgs &A, float *re
     }
 }
 
-// Single-dtype launch whose activations fit LDS in one piece. The eight
-// waves form A.wr row groups x A.wk K groups: a workgroup iteration covers
-// wr row tiles (16*TT rows each); wave (rg, kg) owns tile rg of the
-// iteration and super-blocks kg, kg + wk, ... of K. A wave's work is one
-// sequence of (iteration, super-block) items; its two register stages run
-// across iterations, so the next tile's weights are in flight while the
-// current one is stored. With wk = 1 (large launches such as the LM head) a
-// wave owns whole rows: no barrier after the prologue, each wave stores its
-// own results.
+// Vector-memory loads one weight stage issues per 16-row tile.
+template <int DT> struct StageLoads { static constexpr int value = DT == kQ4K ? 5 : 8; };
+
+// s_waitcnt for "at most N vector-memory loads outstanding" (export and LDS
+// counters left alone).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// 1 / rms of row `lane` (lanes < rows) from the per super-block sums of
+// squares (float64 sum in super-block order, the reference's formula).
+__device__ __forceinline__ float lane_inv_rms(const FusedGemmArgs &A, const float *nsq, int nsb) {
+    const int lane = threadIdx.x & 63;
+    float inv = 1.0f;
+    if (A.norm && lane < A.rows) {
+        double sum = 0.0;
+        for (int sb = 0; sb < nsb; sb++) sum += (double)nsq[lane * nsb + sb];
+        const float mean = (float)(sum / (double)A.K);
+        inv = (float)(1.0 / sqrt((double)(mean + A.eps)));
+    }
+    return inv;
+}
+
+#ifndef YK_FG_DEEP
+#define YK_FG_DEEP 0
+#endif
+// Weight items a wave requests together with its activation copy.
+#ifndef YK_FG_EARLY
+#define YK_FG_EARLY 2
+#endif
+// Activation prologue of the streaming kernel, then each wave's own copy of
+// the rows' 1/rms (no extra barrier).
+__device__ __forceinline__ void stream_prologue(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, float *my_inv,
+                                                int nsb, float4 hw) {
+    lds_barrier();
+    act_prologue(A, L, lds, 0, nsb, hw);
+    lds_barrier();
+    const float v = lane_inv_rms(A, reinterpret_cast<const float *>(lds + L.nsq), nsb);
+    if ((threadIdx.x & 63) < 16) my_inv[threadIdx.x & 63] = v;
+}
+
+// Fixed-order sum of a row group's wk waves through LDS, then the stores
+// (shared by the wk waves).
+template <int TT, int NA>
+__device__ __forceinline__ void stream_epilogue(const FusedGemmArgs &A, float *red, const float *my_inv,
+                                                const float (&acc)[TT][NA][4], bool live, int tile, int rows_out,
+                                                bool swiglu, int rg, int kg, int wk) {
+    const int lane = threadIdx.x & 63;
+    const int M = A.rows;
+    const GroupRows<TT> Gr(A, tile, rows_out, swiglu, lane & 15);
+    float *myred = red + (size_t)rg * wk * TT * NA * 4 * 64;
+    if (wk > 1) lds_barrier();  // previous iteration's partials are consumed
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+#pragma unroll
+        for (int a = 0; a < NA; a++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) myred[(((kg * TT + t) * NA + a) * 4 + e) * 64 + lane] = acc[t][a][e];
+    if (wk > 1) lds_barrier();
+    if (!live) return;
+    for (int idx = kg * 64 + lane; idx < rows_out * M; idx += wk * 64) {
+        const int m = idx / rows_out, rr = idx % rows_out;
+        const int n = Gr.n0 + rr;
+        const float ir = my_inv[m];
+        if (n >= Gr.N) continue;
+        const int t = rr >> 4, col = rr & 15;
+        float val[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int tt = t + h * (TT / 2);
+            float ph = 0.0f, pl = 0.0f;
+            const int ah = m >> 4, gh = (m & 15) >> 2, eh = m & 3;
+            const int rl = M + m, al = rl >> 4, gl = (rl & 15) >> 2, el = rl & 3;
+            for (int w = 0; w < wk; w++) {
+                ph += myred[(((w * TT + tt) * NA + ah) * 4 + eh) * 64 + gh * 16 + col];
+                pl += myred[(((w * TT + tt) * NA + al) * 4 + el) * 64 + gl * 16 + col];
+            }
+            float v = 256.0f * ph + pl;
+            if (A.norm) v *= ir;
+            val[h] = v;
+            if (!swiglu) break;
+        }
+        const size_t o = (size_t)m * Gr.N + n;
+        if (swiglu) {
+            A.seg[0].out[o] = silu_mul(val[0], val[1]);
+        } else {
+            float v = val[0];
+            if (A.epilogue == kEpiResidual) v += A.seg[Gr.s].res[o];
+            else v = out_map(A.seg[Gr.s], v, n);
+            A.seg[Gr.s].out[o] = v;
+        }
+    }
+}
+
+// Items (super-blocks of one tile) a wave may hold in registers at once in
+// the deep path.
+template <int TT, int NA> struct DeepItems { static constexpr int value = NA > 1 ? 2 : (TT == 1 ? 6 : (TT == 2 ? 5 : 2)); };
+
+// "At most n * PER vector-memory loads outstanding" for a runtime n in
+// [0, N] (s_waitcnt takes an immediate; counts above 63 clamp, which only
+// waits longer).
+template <int PER, int N>
+__device__ __forceinline__ void wait_vm_n(int n) {
+    if constexpr (N > 0) {
+        if (n == N) {
+            wait_vm<(N * PER > 63 ? 63 : N * PER)>();
+            return;
+        }
+        wait_vm_n<PER, N - 1>(n);
+    } else {
+        wait_vm<0>();
+    }
+}
+
+// Single-dtype launch whose activations fit LDS in one piece. Workgroup b
+// owns the contiguous row tiles [b G / R, (b + 1) G / R) of the G tiles (R
+// workgroups), so tile counts differ by at most one. Its eight waves form
+// A.wr row groups x A.wk K groups: row group rg takes the workgroup's tiles
+// rg, rg + wr, ...; wave (rg, kg) owns super-blocks kg, kg + wk, ... of each.
+//  * Deep path (each row group has at most one tile and a wave at most
+//    DeepItems super-blocks, the common verify shape): every weight load of
+//    the wave is issued before the activation prologue, so the whole weight
+//    stream is in flight while the activations are quantized.
+//  * Ring path (larger launches such as the LM head): a wave's (tile,
+//    super-block) items stream through two register stages across tiles,
+//    so the next tile's weights are in flight while the current one is
+//    stored; the first stages are requested before the prologue.
+// With wk = 1 a wave owns whole rows: no barrier after the prologue, each
+// wave stores its own results.
 template <int DT, int TT, int NA>
-__device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *lds, float *inv_rms, float *red,
+__device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *lds, float *inv_w, float *red,
                                               int rows_out, bool swiglu) {
     using Stage = typename StageOf<DT>::T;
     constexpr uint32_t blk = DT == kQ4K ? 144u : 210u;
+    constexpr int kDeep = DeepItems<TT, NA>::value;
+    constexpr int kPer = TT * StageLoads<DT>::value;  // loads per item
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
@@ -689,107 +852,179 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
     const int rg = wave / wk, kg = wave - rg * wk;
     const ActLayout L(A.rows, NA, nsb, nsb, A.norm != nullptr, -1, A.gate != nullptr);
     const int mine = kg < nsb ? (nsb - kg + wk - 1) / wk : 0;  // super-blocks per tile
-    const int per_iter = (int)gridDim.x * wr;                   // row tiles per grid iteration
-    const int niter = (A.groups - (int)blockIdx.x * wr + per_iter - 1) / per_iter;
-    auto tile_of = [&](int k) { return ((int)blockIdx.x + k * (int)gridDim.x) * wr + rg; };
-    // my items: iterations whose tile exists, times my super-blocks
-    int ntile = 0;
-    for (int k = 0; k < niter; k++) ntile += tile_of(k) < A.groups ? 1 : 0;
+    const int G = A.groups, R = (int)gridDim.x, b = (int)blockIdx.x;
+    const int t0 = (int)((int64_t)b * G / R), t1 = (int)((int64_t)(b + 1) * G / R);
+    const int niter = (t1 - t0 + wr - 1) / wr;
+    auto tile_of = [&](int k) __attribute__((always_inline)) { return t0 + k * wr + rg; };
+    const int ntile = rg < t1 - t0 ? (t1 - t0 - rg + wr - 1) / wr : 0;
     const int total = ntile * mine;
-    int kq = 0, jq = 0;  // issue cursor (iteration, super-block index)
-    auto issue_next = [&](Stage (&S)[TT]) {
-        const GroupRows<TT> G(A, tile_of(kq), rows_out, swiglu, r);
-#pragma unroll
-        for (int t = 0; t < TT; t++) issue(S[t], G.rs[t], G.row_off[t] + (uint32_t)(kg + wk * jq) * blk, g);
-        if (++jq == mine) {
-            jq = 0;
-            ++kq;
-        }
-    };
-    Stage st[2][TT];
-    act_fetch(A, L, lds, 0);
-    if (total > 0) issue_next(st[0]);
-    if (total > 1) issue_next(st[1]);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    act_prologue(A, L, lds, 0, nsb);
-    __syncthreads();
-    compute_inv_rms(A, L, lds, inv_rms, nsb);
-    __syncthreads();
-    int i = 0;
-    for (int k = 0; k < niter; k++) {
-        const int tile = tile_of(k);
-        const bool live = tile < A.groups;
-        float acc[TT][NA][4];
+    float *my_inv = inv_w + wave * 16;
+    const int M = A.rows;
+    const float4 hw = head_norm_lane(A);
+
+    auto zero = [&](float (&acc)[TT][NA][4]) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < TT; t++)
 #pragma unroll
             for (int a = 0; a < NA; a++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) acc[t][a][e] = 0.0f;
-        for (int j = 0; live && j < mine; j++, i++) {
-            int64_t xa[NA][8];
-            uint32_t sxp[NA][4][4];
-            float xsr[NA][4];
-            load_act<NA>(lds, L, kg + wk * j, r, g, xa, sxp, xsr, DT == kQ4K);
-            if ((i & 1) == 0) {
+    };
+    auto compute_item = [&](const Stage (&S)[TT], int sb, float (&acc)[TT][NA][4]) __attribute__((always_inline)) {
+        int64_t xa[NA][8];
+        uint32_t sxp[NA][4][4];
+        float xsr[NA][4];
+        load_act<NA>(lds, L, sb, r, g, xa, sxp, xsr, DT == kQ4K);
 #pragma unroll
-                for (int t = 0; t < TT; t++) {
-                    if constexpr (DT == kQ4K) compute<NA>(st[0][t], xa, sxp, xsr, acc[t]);
-                    else compute<NA>(st[0][t], xa, sxp, xsr, acc[t], g);
-                }
+        for (int t = 0; t < TT; t++) {
+            if constexpr (DT == kQ4K) compute<NA>(S[t], xa, sxp, xsr, acc[t]);
+            else compute<NA>(S[t], xa, sxp, xsr, acc[t], g);
+        }
+    };
+    if (YK_FG_DEEP && niter <= 1 && (nsb + wk - 1) / wk <= kDeep) {
+        // ---- deep path: one tile per row group, all items in flight
+        Stage st[kDeep][TT];
+#ifdef YK_FG_TIMING
+        uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        YK_FG_STAMP(ts[0]);
+#endif
+        const int tile = tile_of(0);
+        const bool live = ntile > 0;
+        const GroupRows<TT> Gr(A, live ? tile : t0, rows_out, swiglu, r);
+        act_fetch(A, L, lds, 0);
+        __builtin_amdgcn_sched_barrier(0);  // the LDS copies are the oldest loads
+        // two items go out with the activation copy; the rest only once the
+        // copy has landed, so that it does not queue behind the whole weight
+        // stream, and they stream while the activations are quantized
+        const int n_in = live ? mine : 0;
+        constexpr int kEarly = YK_FG_EARLY;
+#pragma unroll
+        for (int d = 0; d < kEarly; d++)
+            if (d < n_in) {
+#pragma unroll
+                for (int t = 0; t < TT; t++) issue(st[d][t], Gr.rs[t], Gr.row_off[t] + (uint32_t)(kg + wk * d) * blk, g);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (kEarly > 0) wait_vm_n<kPer, kEarly>(min(n_in, kEarly));  // activations in LDS
+        else wait_vm<0>();
+        // the rest of the weights once every wave's copy has landed (the
+        // memory pipeline returns in order: earlier they would delay the
+        // slower waves' copies)
+        lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = kEarly; d < kDeep; d++)
+            if (d < n_in) {
+#pragma unroll
+                for (int t = 0; t < TT; t++) issue(st[d][t], Gr.rs[t], Gr.row_off[t] + (uint32_t)(kg + wk * d) * blk, g);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+#ifdef YK_FG_TIMING
+        YK_FG_STAMP(ts[1]);
+#endif
+        stream_prologue(A, L, lds, my_inv, nsb, hw);
+#ifdef YK_FG_TIMING
+        YK_FG_STAMP(ts[3]);
+        ts[2] = ts[3];
+        ts[4] = ts[3];
+#endif
+        float acc[TT][NA][4];
+        zero(acc);
+#pragma unroll
+        for (int d = 0; d < kDeep; d++)
+            if (d < n_in) compute_item(st[d], kg + wk * d, acc);
+#ifdef YK_FG_TIMING
+        YK_FG_STAMP(ts[5]);
+#endif
+        stream_epilogue<TT, NA>(A, red, my_inv, acc, live, live ? tile : t0, rows_out, swiglu, rg, kg, wk);
+#ifdef YK_FG_TIMING
+        YK_FG_STAMP(ts[7]);
+        if (yk_fg_dbg && lane == 0) {
+            uint64_t *o = yk_fg_dbg + ((size_t)blockIdx.x * kWaves + wave) * 8;
+            for (int e = 0; e < 8; e++) o[e] = ts[e];
+        }
+#endif
+        return;
+    }
+
+    // ---- ring path
+    int kq = 0, jq = 0;  // issue cursor (iteration, super-block index)
+    auto issue_next = [&](Stage (&S)[TT]) __attribute__((always_inline)) {
+        const GroupRows<TT> Gr(A, tile_of(kq), rows_out, swiglu, r);
+#pragma unroll
+        for (int t = 0; t < TT; t++) issue(S[t], Gr.rs[t], Gr.row_off[t] + (uint32_t)(kg + wk * jq) * blk, g);
+        if (++jq == mine) {
+            jq = 0;
+            ++kq;
+        }
+    };
+    Stage st[2][TT];
+#ifdef YK_FG_TIMING
+    uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    YK_FG_STAMP(ts[0]);
+#endif
+    act_fetch(A, L, lds, 0);
+    __builtin_amdgcn_sched_barrier(0);  // the LDS copies are the oldest loads
+    if (total > 1) {
+        issue_next(st[0]);
+        issue_next(st[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm<2 * kPer>();  // activations in LDS, weights still in flight
+    } else {
+        if (total > 0) issue_next(st[0]);
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+#ifdef YK_FG_TIMING
+    YK_FG_STAMP(ts[1]);
+#endif
+    stream_prologue(A, L, lds, my_inv, nsb, hw);
+#ifdef YK_FG_TIMING
+    YK_FG_STAMP(ts[3]);
+    ts[2] = ts[3];
+    ts[4] = ts[3];
+#endif
+    int i = 0;
+    for (int k = 0; k < niter; k++) {
+        const int tile = tile_of(k);
+        const bool live = tile < t1;
+        float acc[TT][NA][4];
+        zero(acc);
+        for (int j = 0; live && j < mine; j++, i++) {
+            if ((i & 1) == 0) {
+                compute_item(st[0], kg + wk * j, acc);
                 if (i + 2 < total) issue_next(st[0]);
             } else {
-#pragma unroll
-                for (int t = 0; t < TT; t++) {
-                    if constexpr (DT == kQ4K) compute<NA>(st[1][t], xa, sxp, xsr, acc[t]);
-                    else compute<NA>(st[1][t], xa, sxp, xsr, acc[t], g);
-                }
+                compute_item(st[1], kg + wk * j, acc);
                 if (i + 2 < total) issue_next(st[1]);
             }
         }
-        // ---- epilogue: sum the wk waves of this row group in a fixed order
-        const GroupRows<TT> G(A, live ? tile : 0, rows_out, swiglu, r);
-        float *myred = red + (size_t)rg * wk * TT * NA * 4 * 64;  // this row group's partials
-        if (wk > 1) __syncthreads();  // previous iteration's partials are consumed
-#pragma unroll
-        for (int t = 0; t < TT; t++)
-#pragma unroll
-            for (int a = 0; a < NA; a++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) myred[(((kg * TT + t) * NA + a) * 4 + e) * 64 + lane] = acc[t][a][e];
-        if (wk > 1) __syncthreads();
-        if (!live) continue;
-        const int M = A.rows;
-        auto partial = [&](int t, int rho, int col) {
-            const int a = rho >> 4, gg = (rho & 15) >> 2, e = rho & 3;
-            float v = 0.0f;
-            for (int w = 0; w < wk; w++) v += myred[(((w * TT + t) * NA + a) * 4 + e) * 64 + gg * 16 + col];
-            return v;
-        };
-        auto value = [&](int t, int m, int col) {
-            float v = 256.0f * partial(t, m, col) + partial(t, M + m, col);
-            if (A.norm) v *= inv_rms[m];
-            return v;
-        };
-        // the row group's wk waves share the stores
-        for (int idx = kg * 64 + lane; idx < rows_out * M; idx += wk * 64) {
-            const int m = idx / rows_out, rr = idx % rows_out;
-            const int n = G.n0 + rr;
-            if (n >= G.N) continue;
-            const int t = rr >> 4, col = rr & 15;
-            const size_t o = (size_t)m * G.N + n;
-            if (swiglu) {
-                const float gv = value(t, m, col), uv = value(t + TT / 2, m, col);
-                A.seg[0].out[o] = silu_mul(gv, uv);
-            } else {
-                float v = value(t, m, col);
-                if (A.epilogue == kEpiResidual) v += A.seg[G.s].res[o];
-                else v = out_map(A.seg[G.s], v, n);
-                A.seg[G.s].out[o] = v;
-            }
-        }
+#ifdef YK_FG_TIMING
+        if (k == 0) YK_FG_STAMP(ts[5]);
+#endif
+        stream_epilogue<TT, NA>(A, red, my_inv, acc, live, live ? tile : t0, rows_out, swiglu, rg, kg, wk);
     }
+#ifdef YK_FG_TIMING
+    YK_FG_STAMP(ts[7]);
+    if (yk_fg_dbg && lane == 0) {
+        uint64_t *o = yk_fg_dbg + ((size_t)blockIdx.x * kWaves + wave) * 8;
+        for (int e = 0; e < 8; e++) o[e] = ts[e];
+    }
+#endif
+}
+
+// Streaming kernel (single dtype, activations in LDS in one piece): a
+// separate instantiation so that it carries none of the chunked path's
+// registers or scratch.
+template <int DT, int TT, int NA>
+__global__ __launch_bounds__(kThreads) void fgemm_stream_kernel(const FusedGemmArgs A) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const bool swiglu = A.epilogue == kEpiSwiglu;
+    const int rows_out = swiglu ? 8 * TT : 16 * TT;
+    const int nsb = A.K / 256;
+    const ActLayout L0(A.rows, NA, nsb, nsb, A.norm != nullptr, -1, A.gate != nullptr);
+    float *inv_w = reinterpret_cast<float *>(lds + L0.total);
+    float *red = reinterpret_cast<float *>(lds + L0.total + kInvBytes);
+    stream_groups<DT, TT, NA>(A, lds, inv_w, red, rows_out, swiglu);
 }
 
 template <int DTM, int TT, int NA>
@@ -804,13 +1039,7 @@ __global__ __launch_bounds__(kThreads) void fgemm_kernel(const FusedGemmArgs A) 
     const ActLayout L0(M, NA, min(A.chunk_sb, nsb), nsb, A.norm != nullptr, -1, A.gate != nullptr);
     const bool one_chunk = A.chunk_sb >= nsb;  // activations stay in LDS across groups
     float *inv_rms = reinterpret_cast<float *>(lds + L0.total);
-    float *red = reinterpret_cast<float *>(lds + L0.total + 64);
-    if constexpr (DTM != 0) {
-        if (one_chunk) {
-            stream_groups<DTM, TT, NA>(A, lds, inv_rms, red, rows_out, swiglu);
-            return;
-        }
-    }
+    float *red = reinterpret_cast<float *>(lds + L0.total + kInvBytes);
     uint64_t t_pro = 0, t_wait = 0;
     for (int grp = blockIdx.x; grp < A.groups; grp += gridDim.x) {
         const GroupRows<TT> G(A, grp, rows_out, swiglu, r);
@@ -826,13 +1055,13 @@ __global__ __launch_bounds__(kThreads) void fgemm_kernel(const FusedGemmArgs A) 
             const ActLayout L(M, NA, min(A.chunk_sb, nsb), nsb, A.norm != nullptr, min(A.chunk_sb, nsb - c0),
                               A.gate != nullptr);
             const bool pro = first || !one_chunk;
-            if (c0 && pro) __syncthreads();  // previous chunk's LDS reads are done
+            if (c0 && pro) lds_barrier();  // previous chunk's LDS reads are done
             if constexpr (DTM != 0) chunk_pass<DTM, TT, NA>(A, L, lds, c0, nsb, G.rs, G.row_off, acc, pro, t_pro, t_wait);
             else if (G.dt == kQ4K) chunk_pass<kQ4K, TT, NA>(A, L, lds, c0, nsb, G.rs, G.row_off, acc, pro, t_pro, t_wait);
             else chunk_pass<kQ6K, TT, NA>(A, L, lds, c0, nsb, G.rs, G.row_off, acc, pro, t_pro, t_wait);
         }
         if (first) {
-            __syncthreads();
+            lds_barrier();
             compute_inv_rms(A, L0, lds, inv_rms, nsb);
         }
         group_epilogue<TT, NA>(A, red, inv_rms, acc, G.n0, G.N, G.s, rows_out, swiglu);
@@ -847,7 +1076,7 @@ uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt, bool norm, 
     const int na = rows <= 8 ? 1 : 2;
     const int nsb = K / 256;
     const ActLayout L(rows, na, std::min(chunk_sb, nsb), nsb, norm, -1, gated);
-    return L.total + 64 + (uint32_t)kWaves * tt * na * 4 * 64 * 4;
+    return L.total + kInvBytes + (uint32_t)kWaves * tt * na * 4 * 64 * 4;
 }
 
 int fused_gemm_chunk_sb(int rows, int K, int tt, bool norm, bool gated) {
@@ -874,6 +1103,38 @@ static unsigned resident_wgs(const void *fn, uint32_t lds) {
 
 template <int DTM, int TT, int NA>
 static hipError_t launch_tt(const FusedGemmArgs &a, unsigned grid, uint32_t lds, hipStream_t s) {
+    FusedGemmArgs b = a;
+    b.wk = kWaves;
+    if constexpr (DTM != 0) {
+        if (b.chunk_sb >= b.K / 256) {
+            auto k = fgemm_stream_kernel<DTM, TT, NA>;
+            static bool attr = false;
+            if (!attr) {
+                (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          160 * 1024);
+                attr = true;
+            }
+            const unsigned res = resident_wgs(reinterpret_cast<const void *>(k), lds);
+            // every resident workgroup gets floor or ceil of G / R row tiles;
+            // the waves split into the row-group x K-group shape that
+            // minimizes the largest per-wave item count (ties: more row
+            // groups, fewer barriers)
+            const int nsb = b.K / 256;
+            const unsigned R = std::min((unsigned)b.groups, res);
+            const int per_wg = (int)((b.groups + R - 1) / R);
+            int best = 1 << 30;
+            for (int wr = 1; wr <= kWaves; wr *= 2) {
+                const int wk = kWaves / wr;
+                const int items = ((per_wg + wr - 1) / wr) * ((nsb + wk - 1) / wk);
+                if (items <= best) {
+                    best = items;
+                    b.wk = wk;
+                }
+            }
+            k<<<R, kThreads, lds, s>>>(b);
+            return hipGetLastError();
+        }
+    }
     auto k = fgemm_kernel<DTM, TT, NA>;
     static bool attr = false;
     if (!attr) {
@@ -881,16 +1142,6 @@ static hipError_t launch_tt(const FusedGemmArgs &a, unsigned grid, uint32_t lds,
         attr = true;
     }
     const unsigned res = resident_wgs(reinterpret_cast<const void *>(k), lds);
-    FusedGemmArgs b = a;
-    b.wk = kWaves;
-    if (DTM != 0 && b.chunk_sb >= b.K / 256) {
-        // streaming path: as many row groups per workgroup as keep every
-        // resident workgroup busy, the rest of the waves split K
-        int wr = 1;
-        while (wr < kWaves && (unsigned)b.groups >= res * (unsigned)wr * 2u) wr *= 2;
-        b.wk = kWaves / wr;
-        grid = (unsigned)((b.groups + wr - 1) / wr);
-    }
     grid = std::min(grid, res);
     k<<<grid, kThreads, lds, s>>>(b);
     return hipGetLastError();
