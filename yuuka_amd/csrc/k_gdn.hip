@@ -266,6 +266,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_commit_kernel(
 // and state rows 16 (l % 8) .. +15; a column's eight row parts form an
 // aligned 8-lane group, so column sums need no barrier.
 constexpr int kCols = 32;
+constexpr int kMaxRows = 16;  // verify rows of one step
 constexpr int kColThreads = 256;
 
 // Verify: conv + SiLU + L2 norm of the head's q / k channels and this
@@ -285,6 +286,11 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
     const int kh = h % g.groups;
     float *qk = sm;                 // [R][2][128] q, k
     float *vv = qk + R * 2 * kS;    // [R][kCols]
+    float *cf = vv + R * kCols;     // [2][R] decay, beta of every row
+    if (t < R) {
+        cf[t] = gdn_decay(g, alpha_raw, dt, a_log, t, h);
+        cf[R + t] = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
+    }
     const int p = lane & 7, j = cb * kCols + wave * 8 + (lane >> 3);
     const float *mat = state + (uint64_t)h * kS * kS;
     float s_reg[16];
@@ -335,8 +341,7 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
     const int jl = j - cb * kCols;
     for (int r = 0; r < R; r++) {
         const float *q = qk + (r * 2 + 0) * kS, *k = qk + (r * 2 + 1) * kS;
-        const float decay = gdn_decay(g, alpha_raw, dt, a_log, r, h);
-        const float beta = g.coef ? beta_raw[(uint64_t)r * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)r * g.rank + h]);
+        const float decay = cf[r], beta = cf[R + r];
         float sk = 0.0f;
 #pragma unroll
         for (int ii = 0; ii < 16; ii++) {
@@ -356,20 +361,19 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
     }
 }
 
-// Commit: replay of the accepted rows for this block's columns, state
-// written back; this block's v channels and (cb == 0, h < groups) the q/k
-// group's channels move their conv window forward.
-__global__ __launch_bounds__(kColThreads) void gdn_commit_cols_kernel(
-    float *__restrict__ conv_state, float *__restrict__ state, const float *__restrict__ qkv,
-    const float *__restrict__ conv, const float *__restrict__ alpha_raw, const float *__restrict__ beta_raw,
-    const float *__restrict__ dt, const float *__restrict__ a_log, GdnArgs g,
-    const int32_t *__restrict__ accept_result) {
+// Commit of one layer: replay of the accepted rows for this block's
+// columns, state written back; this block's v channels and (cb == 0,
+// h < groups) the q/k group's channels move their conv window forward.
+__device__ __forceinline__ void gdn_commit_cols_body(float *__restrict__ conv_state, float *__restrict__ state,
+                                                     const float *__restrict__ qkv, const float *__restrict__ conv,
+                                                     const float *__restrict__ alpha_raw,
+                                                     const float *__restrict__ beta_raw, const float *__restrict__ dt,
+                                                     const float *__restrict__ a_log, const GdnArgs &g, int n) {
     const int h = blockIdx.x, cb = blockIdx.y;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int K = g.kernel;
     const int key_dim = g.groups * kS;
     const int kh = h % g.groups;
-    const int n = accept_result ? min(accept_result[0] + 1, g.rows) : g.rows;
     {
         const bool qk_owner = cb == 0 && h < g.groups;
         const int nch = kCols + (qk_owner ? 2 * kS : 0);
@@ -394,15 +398,27 @@ __global__ __launch_bounds__(kColThreads) void gdn_commit_cols_kernel(
     float s_reg[16];
 #pragma unroll
     for (int ii = 0; ii < 16; ii++) s_reg[ii] = mat[(uint64_t)(p * 16 + ii) * kS + j];
-    for (int r = 0; r < n; r++) {
+    // the accepted rows' k, v (this block's columns), decay and beta, staged
+    // once so that the serial row loop reads LDS only
+    __shared__ float sk_rows[kMaxRows][kS], sv_rows[kMaxRows][kCols], scf[2][kMaxRows];
+    for (int idx = t; idx < n * (kS + kCols); idx += kColThreads) {
+        const int r = idx / (kS + kCols), c = idx - r * (kS + kCols);
         const float *row = conv + (uint64_t)r * g.conv_dim;
-        const float *k = row + key_dim + kh * kS;
-        const float decay = gdn_decay(g, alpha_raw, dt, a_log, r, h);
-        const float beta = g.coef ? beta_raw[(uint64_t)r * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)r * g.rank + h]);
+        if (c < kS) sk_rows[r][c] = row[key_dim + kh * kS + c];
+        else sv_rows[r][c - kS] = row[2 * key_dim + h * kS + cb * kCols + (c - kS)];
+    }
+    if (t < n) {
+        scf[0][t] = gdn_decay(g, alpha_raw, dt, a_log, t, h);
+        scf[1][t] = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
+    }
+    __syncthreads();
+    for (int r = 0; r < n; r++) {
+        const float *k = sk_rows[r];
+        const float decay = scf[0][r], beta = scf[1][r];
         float kr[16];
 #pragma unroll
         for (int ii = 0; ii < 16; ii++) kr[ii] = k[p * 16 + ii];
-        const float vj = row[2 * key_dim + h * kS + j];
+        const float vj = sv_rows[r][j - cb * kCols];
         float sk = 0.0f;
 #pragma unroll
         for (int ii = 0; ii < 16; ii++) {
@@ -418,9 +434,27 @@ __global__ __launch_bounds__(kColThreads) void gdn_commit_cols_kernel(
     for (int ii = 0; ii < 16; ii++) mat[(uint64_t)(p * 16 + ii) * kS + j] = s_reg[ii];
 }
 
+__global__ __launch_bounds__(kColThreads) void gdn_commit_cols_kernel(
+    float *__restrict__ conv_state, float *__restrict__ state, const float *__restrict__ qkv,
+    const float *__restrict__ conv, const float *__restrict__ alpha_raw, const float *__restrict__ beta_raw,
+    const float *__restrict__ dt, const float *__restrict__ a_log, GdnArgs g,
+    const int32_t *__restrict__ accept_result) {
+    const int n = accept_result ? min(accept_result[0] + 1, g.rows) : g.rows;
+    gdn_commit_cols_body(conv_state, state, qkv, conv, alpha_raw, beta_raw, dt, a_log, g, n);
+}
+
+// Every recurrent layer's commit in one launch (blockIdx.z = layer): the
+// layers are independent once the acceptance result is known.
+__global__ __launch_bounds__(kColThreads) void gdn_commit_cols_multi_kernel(const GdnCommitSet set, GdnArgs g,
+                                                                            const int32_t *__restrict__ accept_result) {
+    const GdnCommitLayer &L = set.layer[blockIdx.z];
+    const int n = accept_result ? min(accept_result[0] + 1, g.rows) : g.rows;
+    gdn_commit_cols_body(L.conv_state, L.state, L.qkv, L.conv, L.alpha, L.beta, L.dt, L.a_log, g, n);
+}
+
 }  // namespace
 
-uint32_t gdn_verify_cols_lds_bytes(const GdnArgs &g) { return (uint32_t)(g.rows * 2 * kS + g.rows * kCols) * 4; }
+uint32_t gdn_verify_cols_lds_bytes(const GdnArgs &g) { return (uint32_t)(g.rows * 2 * kS + g.rows * kCols + 2 * g.rows) * 4; }
 
 hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, const float *qkv,
                                   const float *alpha_raw, const float *beta_raw, const float *conv_w, const float *dt,
@@ -436,6 +470,14 @@ hipError_t launch_gdn_commit_cols(float *conv_state, float *state, const float *
                                   const GdnArgs &g, const int32_t *accept_result, hipStream_t s) {
     gdn_commit_cols_kernel<<<dim3((unsigned)g.rank, kS / kCols), kColThreads, 0, s>>>(
         conv_state, state, qkv, conv, alpha_raw, beta_raw, dt, a_log, g, accept_result);
+    return hipGetLastError();
+}
+
+hipError_t launch_gdn_commit_cols_multi(const GdnCommitSet &set, int layers, const GdnArgs &g,
+                                        const int32_t *accept_result, hipStream_t s) {
+    if (layers < 1 || layers > kGdnCommitMaxLayers) return hipErrorInvalidValue;
+    gdn_commit_cols_multi_kernel<<<dim3((unsigned)g.rank, kS / kCols, (unsigned)layers), kColThreads, 0, s>>>(
+        set, g, accept_result);
     return hipGetLastError();
 }
 

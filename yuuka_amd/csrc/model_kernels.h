@@ -74,6 +74,18 @@ hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, c
                                   const float *alpha_raw, const float *beta_raw, const float *conv_w, const float *dt,
                                   const float *a_log, float *raw_out, float *conv_out, const GdnArgs &g,
                                   hipStream_t s);
+// Per-layer buffers of a multi-layer GDN commit (one launch for a run of
+// GDN_COMMIT ops that share shape and acceptance result).
+struct GdnCommitLayer {
+    float *conv_state, *state;
+    const float *qkv, *conv, *alpha, *beta, *dt, *a_log;
+};
+constexpr int kGdnCommitMaxLayers = 48;
+struct GdnCommitSet {
+    GdnCommitLayer layer[kGdnCommitMaxLayers];
+};
+hipError_t launch_gdn_commit_cols_multi(const GdnCommitSet &set, int layers, const GdnArgs &g,
+                                        const int32_t *accept_result, hipStream_t s);
 hipError_t launch_gdn_commit_cols(float *conv_state, float *state, const float *qkv, const float *conv,
                                   const float *alpha_raw, const float *beta_raw, const float *dt, const float *a_log,
                                   const GdnArgs &g, const int32_t *accept_result, hipStream_t s);

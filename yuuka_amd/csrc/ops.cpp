@@ -407,6 +407,36 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
     }
 }
 
+int gdn_commit_run(const yuuka_op *ops, int count) {
+    if (count < 2 || ops[0].code != YUUKA_EXT_OP_GDN_COMMIT || getenv("YUUKA_GDN_SPLIT")) return 1;
+    const GdnArgs g0 = gdn_args(ops[0]);
+    if (g0.rows > 16) return 1;
+    int n = 1;
+    while (n < count && n < kGdnCommitMaxLayers && ops[n].code == YUUKA_EXT_OP_GDN_COMMIT &&
+           ops[n].flags == ops[0].flags && ops[n].buf[8] == ops[0].buf[8] && ops[n].off[8] == ops[0].off[8]) {
+        const GdnArgs g = gdn_args(ops[n]);
+        if (g.rows != g0.rows || g.groups != g0.groups || g.rank != g0.rank || g.state != g0.state ||
+            g.conv_dim != g0.conv_dim || g.inner != g0.inner || g.kernel != g0.kernel || g.coef != g0.coef)
+            break;
+        n++;
+    }
+    return n;
+}
+
+yuuka_status execute_gdn_commit_run(const yuuka_op *ops, int count, const ExecCtx &ctx) {
+    const GdnArgs g = gdn_args(ops[0]);
+    GdnCommitSet set{};
+    for (int i = 0; i < count; i++) {
+        const yuuka_op &op = ops[i];
+        set.layer[i] = GdnCommitLayer{at<float>(op, 0),       at<float>(op, 1),       at<const float>(op, 2),
+                                      at<const float>(op, 3), at<const float>(op, 4), at<const float>(op, 5),
+                                      at<const float>(op, 6), at<const float>(op, 7)};
+    }
+    const hipError_t err = launch_gdn_commit_cols_multi(set, count, g, at<const int32_t>(ops[0], 8), ctx.stream);
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "GDN commit launch: %s", hip_error(err));
+    return YUUKA_OK;
+}
+
 yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
     hipError_t err = hipSuccess;
     const hipStream_t s = ctx.stream;
@@ -527,7 +557,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
     case YUUKA_EXT_OP_GDN_COMMIT: {
         const GdnArgs g = gdn_args(op);
         const int32_t *res = at<const int32_t>(op, 8);
-        if (!getenv("YUUKA_GDN_SPLIT")) {  // scan replay + conv window, column-split (k_gdn.hip)
+        if (!getenv("YUUKA_GDN_SPLIT") && g.rows <= 16) {  // scan replay + conv window, column-split (k_gdn.hip)
             err = launch_gdn_commit_cols(at<float>(op, 0), at<float>(op, 1), at<const float>(op, 2), at<const float>(op, 3),
                                     at<const float>(op, 4), at<const float>(op, 5), at<const float>(op, 6),
                                     at<const float>(op, 7), g, res, s);

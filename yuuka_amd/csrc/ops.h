@@ -15,6 +15,11 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx);
 // True when the op reads the execution position (graph capture then needs
 // the dynamic-parameter buffer).
 bool op_uses_position(const yuuka_op &op);
+// Length of the run of consecutive GDN_COMMIT ops starting at ops[0] that
+// one multi-layer launch can serve (same shape, flags and acceptance
+// result), 1 when there is none to merge.
+int gdn_commit_run(const yuuka_op *ops, int count);
+yuuka_status execute_gdn_commit_run(const yuuka_op *ops, int count, const ExecCtx &ctx);
 
 // Elementwise launchers (k_ops.hip).
 hipError_t launch_copy_f32(float *dst, const float *src, uint64_t n, hipStream_t stream);

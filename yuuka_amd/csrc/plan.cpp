@@ -113,8 +113,28 @@ static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token,
             return fail(YUUKA_ERR_DEVICE, "profiling events");
     }
     yuuka_status st = YUUKA_OK;
-    for (const yuuka_op &op : plan->ops) {
+    const int nops = (int)plan->ops.size();
+    for (int oi = 0; oi < nops; oi++) {
+        const yuuka_op &op = plan->ops[oi];
         if ((op.flags & YUUKA_OP_FLAG_TAIL) && !run_tail) continue;
+        if (!times && op.code == YUUKA_EXT_OP_GDN_COMMIT) {
+            // consecutive per-layer commits go out as one launch
+            int run = gdn_commit_run(&plan->ops[oi], nops - oi);
+            for (int k = 1; k < run; k++)
+                if ((plan->ops[oi + k].flags & YUUKA_OP_FLAG_TAIL) && !run_tail) run = k;
+            for (int k = 0; k < run && st == YUUKA_OK; k++)
+                for (int i = 0; i < 16; i++)
+                    if (plan->ops[oi + k].buf[i] && !plan->ops[oi + k].buf[i]->ptr)
+                        st = fail(YUUKA_ERR_INVALID_ARGUMENT, "plan op %u has a freed buffer", op.code);
+            if (st != YUUKA_OK) break;
+            if (run > 1) {
+                st = execute_gdn_commit_run(&plan->ops[oi], run, ctx);
+                if (st != YUUKA_OK) break;
+                n += run;
+                oi += run - 1;
+                continue;
+            }
+        }
         for (int i = 0; i < 16; i++)
             if (op.buf[i] && !op.buf[i]->ptr) {
                 st = fail(YUUKA_ERR_INVALID_ARGUMENT, "plan op %u has a freed buffer", op.code);
