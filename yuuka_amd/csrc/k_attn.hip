@@ -22,12 +22,21 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "model_kernels.h"
 #include "refmath.h"
 
 namespace yk {
 namespace {
+
+#ifdef YK_AT_TIMING
+// Phase timestamps per wave (probe builds only; s_memrealtime, 100 MHz).
+__device__ uint64_t *yk_at_dbg;
+#define YK_AT_STAMP(i) ts[i] = __builtin_amdgcn_s_memrealtime()
+#else
+#define YK_AT_STAMP(i) (void)0
+#endif
 
 __device__ __forceinline__ int cur_pos_a(const ModelDyn &dyn) { return dyn.pos_dev ? *dyn.pos_dev : dyn.pos; }
 
@@ -138,6 +147,10 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
     const int last = p0 + R - 1;
     const int key0 = chunk * CK;
     if (key0 > last) return;  // no row sees this chunk; the merge skips it
+#ifdef YK_AT_TIMING
+    uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#endif
+    YK_AT_STAMP(0);
     const int half = a.rope_dim / 2;
     const int qstride = a.gated ? 2 * D : D;
     const int ks = D + PAD;  // LDS row stride of K and V (elements)
@@ -179,6 +192,7 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
         norm_rope_wave(q + ((int64_t)r * a.heads + head) * qstride, q_norm, Qs + vec * D, D, a.eps,
                        rope + r * half, half);
     }
+    YK_AT_STAMP(1);
     float *kbuf = S;  // scratch for one new key row per wave (S is free until the scores)
     for (int r = wave; r < R; r += 4) {
         const int p = p0 + r;
@@ -196,7 +210,9 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
             vpool[slot * a.kv_dim + (int64_t)kvh * D + d] = vq;
         }
     }
+    YK_AT_STAMP(2);
     __syncthreads();
+    YK_AT_STAMP(3);
 
     // ---- scores: thread = (key kk, query group), full D, 8 queries a pass
     {
@@ -231,6 +247,7 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
         }
     }
     __syncthreads();
+    YK_AT_STAMP(4);
     // ---- softmax partials: one wave per query row of the chunk
     for (int j = wave; j < nq; j += 4) {
         const float sc = lane < CK ? S[j * CK + lane] : -INFINITY;
@@ -246,6 +263,7 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
         }
     }
     __syncthreads();
+    YK_AT_STAMP(5);
     // ---- value product: thread = dimension d, 16 query rows a pass
     for (int d = threadIdx.x; d < D; d += 256) {
         for (int j0 = 0; j0 < nq; j0 += 16) {
@@ -275,32 +293,383 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
             }
         }
     }
+    YK_AT_STAMP(6);
+#ifdef YK_AT_TIMING
+    if (yk_at_dbg && lane == 0) {
+        uint64_t *o = yk_at_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave) * 8;
+        for (int e = 0; e < 8; e++) o[e] = ts[e];
+    }
+#endif
+}
+
+// ---- MFMA path (F16 KV, head_dim 256, rope_dim 64, at most 32 query rows
+// per kv head): scores and the value product run on v_mfma_f32_16x16x32_f16.
+// K and V are exact in F16; query rows and probabilities are split into an
+// F16 high part and an F16 remainder (two MFMAs), which keeps every product
+// to ~2^-22 relative with FP32 accumulation.
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMD = 256;            // head dim
+constexpr int kMK = 64;             // keys per workgroup
+constexpr int kMQ = 32;             // query rows (two 16-row MFMA tiles)
+constexpr int kVt = kMK + 8;        // halves per transposed V row (bank spread)
+constexpr uint32_t kOffK = 0;                               // [64][256] f16, 16-B blocks XOR (key & 15)
+constexpr uint32_t kOffVt = kOffK + kMK * kMD * 2;          // [256][72] f16 (V transposed)
+constexpr uint32_t kOffQh = kOffVt + kMD * kVt * 2;         // [32][256] f16, blocks XOR (row & 15)
+constexpr uint32_t kOffQl = kOffQh + kMQ * kMD * 2;
+constexpr uint32_t kOffS = kOffQl + kMQ * kMD * 2;          // [32][64] f32
+constexpr uint32_t kOffPh = kOffS + kMQ * kMK * 4;          // [32][64] f16, blocks XOR (row & 7)
+constexpr uint32_t kOffPl = kOffPh + kMQ * kMK * 2;
+constexpr uint32_t kMfmaLds = kOffPl + kMQ * kMK * 2;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xf, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xf, 0xf, true);
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+__device__ __forceinline__ float rl_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
+__device__ __forceinline__ double rl_dd(double v, int l) {
+    const uint64_t b = __double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// wave-wide sum / max (DPP inside 16-lane rows, then the four row results)
+__device__ __forceinline__ double wave_sum_dpp_d(double v) {
+    v += dpp_d<0xb1>(v);
+    v += dpp_d<0x4e>(v);
+    v += dpp_d<0x124>(v);
+    v += dpp_d<0x128>(v);
+    return (rl_dd(v, 15) + rl_dd(v, 31)) + (rl_dd(v, 47) + rl_dd(v, 63));
+}
+__device__ __forceinline__ float wave_sum_dpp_f(float v) {
+    v += dpp_f<0xb1>(v);
+    v += dpp_f<0x4e>(v);
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x128>(v);
+    return (rl_f(v, 15) + rl_f(v, 31)) + (rl_f(v, 47) + rl_f(v, 63));
+}
+__device__ __forceinline__ float wave_max_dpp_f(float v) {
+    v = fmaxf(v, dpp_f<0xb1>(v));
+    v = fmaxf(v, dpp_f<0x4e>(v));
+    v = fmaxf(v, dpp_f<0x124>(v));
+    v = fmaxf(v, dpp_f<0x128>(v));
+    return fmaxf(fmaxf(rl_f(v, 15), rl_f(v, 31)), fmaxf(rl_f(v, 47), rl_f(v, 63)));
+}
+
+// Per-head RMSNorm and RoPE (rope_dim 64) of one 256-vector by one wave; lane
+// l holds elements 4l .. 4l + 3, so rotation pair (i, i + 32) sits in lanes
+// (l, l + 8) of the first DPP row and one row rotation exchanges them.
+__device__ __forceinline__ void norm_rope4(const float *__restrict__ src, const float *__restrict__ w, float eps,
+                                           const float2 *__restrict__ cs, float (&y)[4]) {
+    const int lane = threadIdx.x & 63;
+    const float4 x = *reinterpret_cast<const float4 *>(src + 4 * lane);
+    const float4 w4 = *reinterpret_cast<const float4 *>(w + 4 * lane);
+    double ss = (double)x.x * (double)x.x;
+    ss += (double)x.y * (double)x.y;
+    ss += (double)x.z * (double)x.z;
+    ss += (double)x.w * (double)x.w;
+    ss = wave_sum_dpp_d(ss);
+    const float mean = (float)(ss / (double)kMD);
+    const float scale = (float)(1.0 / sqrt((double)(mean + eps)));
+    y[0] = __fmul_rn(x.x, __fmul_rn(scale, w4.x));
+    y[1] = __fmul_rn(x.y, __fmul_rn(scale, w4.y));
+    y[2] = __fmul_rn(x.z, __fmul_rn(scale, w4.z));
+    y[3] = __fmul_rn(x.w, __fmul_rn(scale, w4.w));
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pr[i] = dpp_f<0x128>(y[i]);  // partner lane (l + 8) % 16 of the row
+    if (lane < 16) {
+        const bool first = lane < 8;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = 4 * lane + i, pi = first ? e : e - 32;
+            const float c = cs[pi].x, sn = cs[pi].y;
+            // first half: y0 c - y1 s; second half: y0 s + y1 c (y0 = element pi)
+            y[i] = first ? __fsub_rn(__fmul_rn(y[i], c), __fmul_rn(pr[i], sn))
+                         : __fadd_rn(__fmul_rn(pr[i], sn), __fmul_rn(y[i], c));
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// 16-byte global -> LDS copy of one lane (lane l writes [m0 + 16 l, +16)),
+// issued as inline assembly so the compiler does not wait on it (the kernel
+// waits with s_waitcnt vmcnt(0) before its first barrier).
+__device__ __forceinline__ void lds_copy16_at(const void *src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+
+__device__ __forceinline__ void lds_only_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__restrict__ q, const float *__restrict__ k,
+                                                               const float *__restrict__ v, uint16_t *kpool,
+                                                               uint16_t *vpool, const int32_t *__restrict__ table,
+                                                               const float *__restrict__ q_norm,
+                                                               const float *__restrict__ k_norm,
+                                                               const float2 *__restrict__ rope, AttnVArgs a,
+                                                               float *__restrict__ part, ModelDyn dyn) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int kvh = blockIdx.y, chunk = blockIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const int R = a.rows;
+    const int G = a.heads / a.kv_heads, nq = G * R;
+    const int p0 = cur_pos_a(dyn) + a.displacement;  // position of verify row 0
+    const int last = p0 + R - 1;
+    const int key0 = chunk * kMK;
+    if (key0 > last) return;  // no row sees this chunk; the merge skips it
+#ifdef YK_AT_TIMING
+    uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#endif
+    YK_AT_STAMP(0);
+    const int half = a.rope_dim / 2;
+    const int qstride = a.gated ? 2 * kMD : kMD;
+    const uint32_t base = (uint32_t)(uintptr_t)lds;
+
+    // ---- cached keys: DMA into LDS, wave w copies keys [16w, 16w + 16), two a
+    //      wave instruction; lane (key, block b) fetches block b ^ (key & 15)
+    {
+        const int kk0 = wave * 16;
+#pragma unroll 1
+        for (int i = 0; i < 8; i++) {
+            const int kk = kk0 + 2 * i + (lane >> 5), blk = lane & 31;
+            const int p = key0 + kk;
+            if (p < p0) {
+                const int64_t slot = (int64_t)table[p / a.block_size] * a.block_size + p % a.block_size;
+                const uint16_t *src = kpool + slot * a.kv_dim + (int64_t)kvh * kMD + (blk ^ (kk & 15)) * 8;
+                lds_copy16_at(src, base + kOffK + (uint32_t)(kk0 + 2 * i) * kMD * 2);
+            }
+        }
+    }
+    // ---- cached values: wave w loads dims [64w, 64w + 64) of every key
+    //      (lane = key) and stores them transposed
+    uint4 vreg[8];
+    const int vkey = lane, vp = key0 + vkey;
+    {
+        if (vp < p0) {
+            const int64_t slot = (int64_t)table[vp / a.block_size] * a.block_size + vp % a.block_size;
+            const uint4 *src = reinterpret_cast<const uint4 *>(vpool + slot * a.kv_dim + (int64_t)kvh * kMD + wave * 64);
+#pragma unroll
+            for (int e = 0; e < 8; e++) vreg[e] = src[e];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) vreg[e] = make_uint4(0, 0, 0, 0);
+        }
+    }
+    // ---- query rows: normalised, rotated, split into F16 high + remainder
+    for (int vec = wave; vec < nq; vec += 4) {
+        const int gq = vec / R, r = vec % R;
+        float y[4];
+        norm_rope4(q + ((int64_t)r * a.heads + kvh * G + gq) * qstride, q_norm, a.eps, rope + r * half, y);
+        _Float16 hi[4], lo[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            hi[i] = (_Float16)y[i];
+            lo[i] = (_Float16)(y[i] - (float)hi[i]);
+        }
+        const uint32_t off = (uint32_t)vec * kMD * 2 + (uint32_t)(((lane >> 1) ^ (vec & 15)) * 16 + (lane & 1) * 8);
+        *reinterpret_cast<uint2 *>(lds + kOffQh + off) = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
+        *reinterpret_cast<uint2 *>(lds + kOffQl + off) = make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
+    }
+    // ---- values of this chunk, transposed (keys past the verify rows: zero)
+    {
+        uint16_t *vt = reinterpret_cast<uint16_t *>(lds + kOffVt);
+        if (vp < p0 || vp > last) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const uint32_t w4[4] = {vreg[e].x, vreg[e].y, vreg[e].z, vreg[e].w};
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    vt[(wave * 64 + e * 8 + i) * kVt + vkey] = (uint16_t)(w4[i >> 1] >> (16 * (i & 1)));
+            }
+        }
+    }
+    YK_AT_STAMP(1);
+    // ---- the verify rows' own keys and values (rows whose position falls in
+    //      this chunk): rounded as the pool stores them, into LDS and the pool
+    for (int r = wave; r < R; r += 4) {
+        const int p = p0 + r;
+        if (p < key0 || p >= key0 + kMK) continue;
+        const int kk = p - key0;
+        const int64_t slot = (int64_t)table[p / a.block_size] * a.block_size + p % a.block_size;
+        float y[4];
+        norm_rope4(k + (int64_t)r * a.kv_dim + (int64_t)kvh * kMD, k_norm, a.eps, rope + r * half, y);
+        uint16_t kq[4], vq[4];
+        const float4 vv = *reinterpret_cast<const float4 *>(v + (int64_t)r * a.kv_dim + (int64_t)kvh * kMD + 4 * lane);
+        const float vf[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            kq[i] = ref_f32_to_f16(y[i]);
+            vq[i] = ref_f32_to_f16(vf[i]);
+        }
+        const uint2 kw = make_uint2((uint32_t)kq[0] | ((uint32_t)kq[1] << 16), (uint32_t)kq[2] | ((uint32_t)kq[3] << 16));
+        const uint2 vw = make_uint2((uint32_t)vq[0] | ((uint32_t)vq[1] << 16), (uint32_t)vq[2] | ((uint32_t)vq[3] << 16));
+        *reinterpret_cast<uint2 *>(kpool + slot * a.kv_dim + (int64_t)kvh * kMD + 4 * lane) = kw;
+        *reinterpret_cast<uint2 *>(vpool + slot * a.kv_dim + (int64_t)kvh * kMD + 4 * lane) = vw;
+        *reinterpret_cast<uint2 *>(lds + kOffK + (uint32_t)kk * kMD * 2 + (uint32_t)(((lane >> 1) ^ (kk & 15)) * 16 + (lane & 1) * 8)) = kw;
+        uint16_t *vt = reinterpret_cast<uint16_t *>(lds + kOffVt);
+#pragma unroll
+        for (int i = 0; i < 4; i++) vt[(4 * lane + i) * kVt + kk] = vq[i];
+    }
+    YK_AT_STAMP(2);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's key copies have landed
+    lds_only_barrier();
+    YK_AT_STAMP(3);
+
+    // ---- scores: wave w owns keys [16w, 16w + 16) for both row tiles
+    {
+        f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        const int kk = wave * 16 + r16;
+        const bool two = nq > 16;
+#pragma unroll
+        for (int ks = 0; ks < kMD / 32; ks++) {
+            const int blk = ks * 4 + g4;
+            const half8 b = *reinterpret_cast<const half8 *>(lds + kOffK + (uint32_t)kk * kMD * 2 + (uint32_t)((blk ^ r16) * 16));
+            const uint32_t qo = (uint32_t)r16 * kMD * 2 + (uint32_t)((blk ^ r16) * 16);
+            const half8 ah0 = *reinterpret_cast<const half8 *>(lds + kOffQh + qo);
+            const half8 al0 = *reinterpret_cast<const half8 *>(lds + kOffQl + qo);
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah0, b, acc[0], 0, 0, 0);
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al0, b, acc[0], 0, 0, 0);
+            if (two) {
+                const half8 ah1 = *reinterpret_cast<const half8 *>(lds + kOffQh + 16 * kMD * 2 + qo);
+                const half8 al1 = *reinterpret_cast<const half8 *>(lds + kOffQl + 16 * kMD * 2 + qo);
+                acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah1, b, acc[1], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al1, b, acc[1], 0, 0, 0);
+            }
+        }
+        float *S = reinterpret_cast<float *>(lds + kOffS);
+        const int p = key0 + kk;
+#pragma unroll
+        for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int qi = rt * 16 + g4 * 4 + e;
+                if (qi < nq) S[qi * kMK + kk] = p <= p0 + qi % R ? acc[rt][e] * a.scale : -INFINITY;
+            }
+    }
+    lds_only_barrier();
+    YK_AT_STAMP(4);
+    // ---- softmax partials: one wave per query row, lane = key
+    {
+        const float *S = reinterpret_cast<const float *>(lds + kOffS);
+        for (int qi = wave; qi < nq; qi += 4) {
+            const float sc = S[qi * kMK + lane];
+            const float m = wave_max_dpp_f(sc);
+            const float e = (sc == -INFINITY) ? 0.0f : (float)exp((double)(sc - m));
+            const float l = wave_sum_dpp_f(e);
+            const _Float16 hi = (_Float16)e, lo = (_Float16)(e - (float)hi);
+            const uint32_t off = (uint32_t)qi * kMK * 2 + (uint32_t)((((lane >> 3) ^ (qi & 7)) * 16) + (lane & 7) * 2);
+            *reinterpret_cast<_Float16 *>(lds + kOffPh + off) = hi;
+            *reinterpret_cast<_Float16 *>(lds + kOffPl + off) = lo;
+            if (lane == 0) {
+                const int gq = qi / R, r = qi % R;
+                float *rec = part + (((int64_t)chunk * R + r) * a.heads + kvh * G + gq) * (kMD + 2);
+                rec[kMD] = m;
+                rec[kMD + 1] = l;
+            }
+        }
+    }
+    lds_only_barrier();
+    YK_AT_STAMP(5);
+    // ---- value product: wave w owns dims [64w, 64w + 64) (four 16-wide tiles)
+    {
+        f32x4 o[4][2];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++) o[j][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const bool two = nq > 16;
+#pragma unroll
+        for (int ks = 0; ks < kMK / 32; ks++) {
+            const int blk = ks * 4 + g4;
+            half8 ah[2], al[2];
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++) {
+                const uint32_t po = (uint32_t)(rt * 16 + r16) * kMK * 2 + (uint32_t)((blk ^ (r16 & 7)) * 16);
+                ah[rt] = *reinterpret_cast<const half8 *>(lds + kOffPh + po);
+                al[rt] = *reinterpret_cast<const half8 *>(lds + kOffPl + po);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int dcol = wave * 64 + j * 16 + r16;
+                const half8 b = *reinterpret_cast<const half8 *>(lds + kOffVt + (uint32_t)dcol * kVt * 2 + (uint32_t)(ks * 32 + g4 * 8) * 2);
+                o[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[0], b, o[j][0], 0, 0, 0);
+                o[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[0], b, o[j][0], 0, 0, 0);
+                if (two) {
+                    o[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[1], b, o[j][1], 0, 0, 0);
+                    o[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[1], b, o[j][1], 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int qi = rt * 16 + g4 * 4 + e;
+                    if (qi < nq) {
+                        const int gq = qi / R, r = qi % R, d = wave * 64 + j * 16 + r16;
+                        part[(((int64_t)chunk * R + r) * a.heads + kvh * G + gq) * (kMD + 2) + d] = o[j][rt][e];
+                    }
+                }
+    }
+    YK_AT_STAMP(6);
+#ifdef YK_AT_TIMING
+    if (yk_at_dbg && lane == 0) {
+        uint64_t *o = yk_at_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave) * 8;
+        for (int e = 0; e < 8; e++) o[e] = ts[e];
+    }
+#endif
 }
 
 // Merges the chunk partials of one (query head, row) and applies the output
-// gate sigmoid(gate) (forward.go:452-456).
+// gate sigmoid(gate) (forward.go:452-456). The chunk weights exp(m_c - max)
+// are computed once per workgroup into LDS.
 __global__ __launch_bounds__(256) void attn_merge_v_kernel(const float *__restrict__ q, const float *__restrict__ part,
                                                            AttnVArgs a, int ck, int chunks, float *__restrict__ out,
                                                            ModelDyn dyn) {
+    extern __shared__ float wsh[];  // [chunks] weights
+    __shared__ float red[4];
     const int r = blockIdx.y, h = blockIdx.x;
     const int D = a.head_dim;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int p0 = cur_pos_a(dyn) + a.displacement;
     const int nchunk = min((p0 + r) / ck + 1, chunks);
+    auto rec_of = [&](int c) { return part + (((int64_t)c * a.rows + r) * a.heads + h) * (D + 2); };
     float mx = -INFINITY;
-    for (int c = 0; c < nchunk; c++) mx = fmaxf(mx, part[(((int64_t)c * a.rows + r) * a.heads + h) * (D + 2) + D]);
-    float lsum = 0.0f;
-    for (int c = 0; c < nchunk; c++) {
-        const float *rec = part + (((int64_t)c * a.rows + r) * a.heads + h) * (D + 2);
-        if (rec[D] != -INFINITY) lsum += rec[D + 1] * (float)exp((double)(rec[D] - mx));
+    for (int c = threadIdx.x; c < nchunk; c += 256) mx = fmaxf(mx, rec_of(c)[D]);
+    mx = wave_max_f(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int c = threadIdx.x; c < nchunk; c += 256) {
+        const float mc = rec_of(c)[D];
+        wsh[c] = mc == -INFINITY ? 0.0f : (float)exp((double)(mc - mx));
     }
+    __syncthreads();
+    float lsum = 0.0f;
+    for (int c = 0; c < nchunk; c++) lsum += rec_of(c)[D + 1] * wsh[c];
     const float inv = 1.0f / lsum;
     const int qstride = a.gated ? 2 * D : D;
     for (int d = threadIdx.x; d < D; d += 256) {
         float acc = 0.0f;
-        for (int c = 0; c < nchunk; c++) {
-            const float *rec = part + (((int64_t)c * a.rows + r) * a.heads + h) * (D + 2);
-            if (rec[D] != -INFINITY) acc += rec[d] * (float)exp((double)(rec[D] - mx));
-        }
+        for (int c = 0; c < nchunk; c++) acc += rec_of(c)[d] * wsh[c];
         float o = acc * inv;
         if (a.gated) o *= sigmoid_ref(q[((int64_t)r * a.heads + h) * qstride + D + d]);
         out[((int64_t)r * a.heads + h) * D + d] = o;
@@ -333,17 +702,32 @@ hipError_t launch_rope_table(float2 *tab, int rows, int rot_dim, double base, co
     return hipGetLastError();
 }
 
+static bool use_mfma_path(const AttnVArgs &a) {
+    return a.fmt == 1 && a.head_dim == kMD && a.rope_dim == 64 && a.heads / a.kv_heads * a.rows <= kMQ &&
+           a.kv_dim % 8 == 0 && !getenv("YUUKA_ATTN_FMA");
+}
+
 hipError_t launch_attn_verify(const float *q, const float *k, const float *v, void *kpool, void *vpool,
                               const int32_t *table, const float *q_norm, const float *k_norm, const float2 *rope,
                               float *out, const AttnVArgs &a, void *scratch, const ModelDyn &dyn, int max_pos_hint,
                               hipStream_t s) {
-    const int ck = attn_verify_chunk(a.fmt);
+    const bool mfma = use_mfma_path(a);
+    const int ck = mfma ? kMK : attn_verify_chunk(a.fmt);
     const int chunks = (a.capacity + ck - 1) / ck;
     const int launch_chunks = max_pos_hint >= 0 ? std::min(chunks, max_pos_hint / ck + 1) : chunks;
-    const uint32_t lds = attn_verify_lds_bytes(a);
     auto *part = static_cast<float *>(scratch);
-    static bool attr0 = false, attr1 = false;
-    if (a.fmt == 1) {
+    static bool attr0 = false, attr1 = false, attr2 = false;
+    if (mfma) {
+        if (!attr2) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_mfma_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            attr2 = true;
+        }
+        attn_verify_mfma_kernel<<<dim3((unsigned)launch_chunks, (unsigned)a.kv_heads), 256, kMfmaLds, s>>>(
+            q, k, v, static_cast<uint16_t *>(kpool), static_cast<uint16_t *>(vpool), table, q_norm, k_norm, rope, a,
+            part, dyn);
+    } else if (a.fmt == 1) {
+        const uint32_t lds = attn_verify_lds_bytes(a);
         if (!attr1) {
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_kernel<1>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -353,6 +737,7 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
             q, k, v, static_cast<uint8_t *>(kpool), static_cast<uint8_t *>(vpool), table, q_norm, k_norm, rope, a,
             part, dyn);
     } else {
+        const uint32_t lds = attn_verify_lds_bytes(a);
         if (!attr0) {
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_kernel<0>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -362,8 +747,8 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
             q, k, v, static_cast<uint8_t *>(kpool), static_cast<uint8_t *>(vpool), table, q_norm, k_norm, rope, a,
             part, dyn);
     }
-    attn_merge_v_kernel<<<dim3((unsigned)a.heads, (unsigned)a.rows), 256, 0, s>>>(q, part, a, ck, launch_chunks, out,
-                                                                                  dyn);
+    attn_merge_v_kernel<<<dim3((unsigned)a.heads, (unsigned)a.rows), 256, (size_t)launch_chunks * 4, s>>>(
+        q, part, a, ck, launch_chunks, out, dyn);
     return hipGetLastError();
 }
 
