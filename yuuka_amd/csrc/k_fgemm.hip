@@ -41,6 +41,7 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "fgemm.h"
 #include "refmath.h"
@@ -178,12 +179,15 @@ __device__ __forceinline__ int quad_sum(int v) {
 struct ActLayout {
     int rho, rhop, cap, cnt;
     uint32_t raw, graw, zraw, planes, sums, xs, nsq, junk, total;
-    __host__ __device__ ActLayout(int rows, int na, int cap_, int nsb, bool norm, int cnt_ = -1, bool gated = false)
+    // staged: the raw copies of x (and g, z) live in LDS (act_fetch); the
+    // streaming kernel keeps them in registers instead.
+    __host__ __device__ ActLayout(int rows, int na, int cap_, int nsb, bool norm, int cnt_ = -1, bool gated = false,
+                                  bool staged = true)
         : rho(2 * rows), rhop(16 * na), cap(cap_), cnt(cnt_ < 0 ? cap_ : cnt_) {
         raw = 0;
-        graw = raw + (uint32_t)cap * rows * 1024;
-        zraw = graw + (norm ? (uint32_t)cap * 1024 : 0u);
-        planes = zraw + (gated ? (uint32_t)cap * rows * 1024 : 0u);
+        graw = raw + (staged ? (uint32_t)cap * rows * 1024 : 0u);
+        zraw = graw + (staged && norm ? (uint32_t)cap * 1024 : 0u);
+        planes = zraw + (staged && gated ? (uint32_t)cap * rows * 1024 : 0u);
         sums = planes + (uint32_t)cap * 8 * 4 * rho * 8;
         xs = sums + (uint32_t)cap * rhop * 16;
         nsq = xs + (uint32_t)cap * rhop * 4;
@@ -386,6 +390,97 @@ __device__ __forceinline__ void act_prologue(const FusedGemmArgs &A, const ActLa
     if (A.gate) act_prologue_m<2>(A, L, lds, c0, nsb, hw);
     else if (A.norm) act_prologue_m<1>(A, L, lds, c0, nsb, hw);
     else act_prologue_m<0>(A, L, lds, c0, nsb, hw);
+}
+
+// Quantization of the streaming kernel's units from registers: wave w's
+// units are w, w + 8, ... (k-th in slot k of xr / gr / zr, loaded at kernel
+// start, before the weight stream). Same arithmetic and LDS tables as
+// act_prologue_m; four units at a time, branch-free (units past the end
+// store to the per-lane scratch slot).
+template <int MODE, int KU>
+__device__ __forceinline__ void act_prologue_regs(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, int nsb,
+                                                  const float4 (&xr)[KU], const float4 (&gr)[KU], const float4 (&zr)[KU],
+                                                  float4 hw) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int M = A.rows;
+    const int total = M * nsb;
+    const int j = lane >> 3, g = (lane >> 1) & 3, hf = lane & 1;
+    const uint32_t junk = L.junk + (uint32_t)lane * 8;
+#pragma unroll
+    for (int k0 = 0; k0 < KU; k0 += 4) {
+        if (wave + kWaves * k0 >= total) break;  // wave-uniform
+#pragma unroll
+        for (int k = k0; k < k0 + 4; k++) {
+            const int uu = wave + kWaves * k;
+            const bool live = uu < total;
+            const int u = min(uu, total - 1);
+            const int m = u / nsb, sbl = u - m * nsb;
+            float v[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
+            float sq = 0.0f;
+            if constexpr (MODE == 1) {
+                sq = fmaf(v[3], v[3], fmaf(v[2], v[2], fmaf(v[1], v[1], v[0] * v[0])));
+                v[0] = __fmul_rn(v[0], gr[k].x); v[1] = __fmul_rn(v[1], gr[k].y);
+                v[2] = __fmul_rn(v[2], gr[k].z); v[3] = __fmul_rn(v[3], gr[k].w);
+            }
+            if constexpr (MODE == 2) {
+                double ss = 0.0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) ss += (double)v[i] * (double)v[i];
+                ss = row_sum_d(ss);
+                const double h0 = rl_d(ss, 15) + rl_d(ss, 31), h1 = rl_d(ss, 47) + rl_d(ss, 63);
+                const double hs = lane < 32 ? h0 : h1;
+                const float mean = (float)(hs / 128.0);
+                const float scale = (float)(1.0 / sqrt((double)(mean + A.eps)));
+                v[0] = __fmul_rn(__fmul_rn(v[0], __fmul_rn(scale, hw.x)), zr[k].x);
+                v[1] = __fmul_rn(__fmul_rn(v[1], __fmul_rn(scale, hw.y)), zr[k].y);
+                v[2] = __fmul_rn(__fmul_rn(v[2], __fmul_rn(scale, hw.z)), zr[k].z);
+                v[3] = __fmul_rn(__fmul_rn(v[3], __fmul_rn(scale, hw.w)), zr[k].w);
+            }
+            const uint32_t a = max(max(__float_as_uint(v[0]) & 0x7fffffffu, __float_as_uint(v[1]) & 0x7fffffffu),
+                                   max(__float_as_uint(v[2]) & 0x7fffffffu, __float_as_uint(v[3]) & 0x7fffffffu));
+            const uint32_t ar = row_max_u32(a);
+            const float amax = __uint_as_float(max(max(rl_u(ar, 15), rl_u(ar, 31)), max(rl_u(ar, 47), rl_u(ar, 63))));
+            const float xs = amax * (1.0f / (float)kQMax);
+            const float inv = amax > 0.0f ? (float)kQMax * __builtin_amdgcn_rcpf(amax) : 0.0f;
+            uint32_t t[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) t[i] = __float_as_uint(fmaf(v[i], inv, kRoundMagic));
+            const uint32_t hp = __builtin_amdgcn_perm(t[1], t[0], 0x0c0c0501u) | __builtin_amdgcn_perm(t[3], t[2], 0x05010c0cu);
+            const uint32_t lp = (__builtin_amdgcn_perm(t[1], t[0], 0x0c0c0400u) | __builtin_amdgcn_perm(t[3], t[2], 0x04000c0cu)) ^
+                                0x80808080u;
+            const uint32_t slot = L.planes + ((uint32_t)((sbl * 8 + j) * 4 + g) * L.rho + m) * 8 + 4 * hf;
+            *reinterpret_cast<uint32_t *>(lds + (live ? slot : junk)) = hp;
+            *reinterpret_cast<uint32_t *>(lds + (live ? slot + (uint32_t)M * 8 : junk + 4)) = lp;
+            const int hs = oct_sum(__builtin_amdgcn_sdot4((int)hp, 0x01010101, 0, false));
+            const int ls = oct_sum(__builtin_amdgcn_sdot4((int)lp, 0x01010101, 0, false));
+            const bool lead = live && (lane & 7) == 0;
+            const uint32_t sh = L.sums + (((uint32_t)sbl * L.rhop + m) * 8 + j) * 2;
+            const uint32_t sl = L.sums + (((uint32_t)sbl * L.rhop + M + m) * 8 + j) * 2;
+            *reinterpret_cast<int16_t *>(lds + (lead ? sh : junk)) = (int16_t)hs;
+            *reinterpret_cast<int16_t *>(lds + (lead ? sl : junk + 2)) = (int16_t)ls;
+            const bool first = live && lane == 0;
+            const uint32_t xh = L.xs + ((uint32_t)sbl * L.rhop + m) * 4;
+            const uint32_t xl = L.xs + ((uint32_t)sbl * L.rhop + M + m) * 4;
+            *reinterpret_cast<float *>(lds + (first ? xh : junk)) = xs;
+            *reinterpret_cast<float *>(lds + (first ? xl : junk + 4)) = xs;
+            if constexpr (MODE == 1) {
+                const float rsum = row_sum(sq);
+                const float tot = (rdl(rsum, 15) + rdl(rsum, 31)) + (rdl(rsum, 47) + rdl(rsum, 63));
+                const uint32_t nq = L.nsq + (uint32_t)(m * nsb + sbl) * 4;
+                *reinterpret_cast<float *>(lds + (first ? nq : junk)) = tot;
+            }
+        }
+    }
+    // rows past 2M of the padded tables read as zero
+    float *xsv = reinterpret_cast<float *>(lds + L.xs);
+    for (int idx = threadIdx.x; idx < nsb * L.rhop; idx += kThreads) {
+        const int rho = idx % L.rhop;
+        if (rho >= L.rho) {
+            xsv[idx] = 0.0f;
+            *reinterpret_cast<uint4 *>(lds + L.sums + (uint32_t)idx * 16) = make_uint4(0, 0, 0, 0);
+        }
+    }
 }
 
 // Staged weight bytes of one 16-row tile for one super-block.
@@ -731,24 +826,6 @@ __device__ __forceinline__ float lane_inv_rms(const FusedGemmArgs &A, const floa
     return inv;
 }
 
-#ifndef YK_FG_DEEP
-#define YK_FG_DEEP 0
-#endif
-// Weight items a wave requests together with its activation copy.
-#ifndef YK_FG_EARLY
-#define YK_FG_EARLY 2
-#endif
-// Activation prologue of the streaming kernel, then each wave's own copy of
-// the rows' 1/rms (no extra barrier).
-__device__ __forceinline__ void stream_prologue(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, float *my_inv,
-                                                int nsb, float4 hw) {
-    lds_barrier();
-    act_prologue(A, L, lds, 0, nsb, hw);
-    lds_barrier();
-    const float v = lane_inv_rms(A, reinterpret_cast<const float *>(lds + L.nsq), nsb);
-    if ((threadIdx.x & 63) < 16) my_inv[threadIdx.x & 63] = v;
-}
-
 // Fixed-order sum of a row group's wk waves through LDS, then the stores
 // (shared by the wk waves).
 template <int TT, int NA>
@@ -802,55 +879,32 @@ __device__ __forceinline__ void stream_epilogue(const FusedGemmArgs &A, float *r
     }
 }
 
-// Items (super-blocks of one tile) a wave may hold in registers at once in
-// the deep path.
-template <int TT, int NA> struct DeepItems { static constexpr int value = NA > 1 ? 2 : (TT == 1 ? 6 : (TT == 2 ? 5 : 2)); };
-
-// "At most n * PER vector-memory loads outstanding" for a runtime n in
-// [0, N] (s_waitcnt takes an immediate; counts above 63 clamp, which only
-// waits longer).
-template <int PER, int N>
-__device__ __forceinline__ void wait_vm_n(int n) {
-    if constexpr (N > 0) {
-        if (n == N) {
-            wait_vm<(N * PER > 63 ? 63 : N * PER)>();
-            return;
-        }
-        wait_vm_n<PER, N - 1>(n);
-    } else {
-        wait_vm<0>();
-    }
-}
-
-// Single-dtype launch whose activations fit LDS in one piece. Workgroup b
-// owns the contiguous row tiles [b G / R, (b + 1) G / R) of the G tiles (R
-// workgroups), so tile counts differ by at most one. Its eight waves form
-// A.wr row groups x A.wk K groups: row group rg takes the workgroup's tiles
-// rg, rg + wr, ...; wave (rg, kg) owns super-blocks kg, kg + wk, ... of each.
-//  * Deep path (each row group has at most one tile and a wave at most
-//    DeepItems super-blocks, the common verify shape): every weight load of
-//    the wave is issued before the activation prologue, so the whole weight
-//    stream is in flight while the activations are quantized.
-//  * Ring path (larger launches such as the LM head): a wave's (tile,
-//    super-block) items stream through two register stages across tiles,
-//    so the next tile's weights are in flight while the current one is
-//    stored; the first stages are requested before the prologue.
-// With wk = 1 a wave owns whole rows: no barrier after the prologue, each
-// wave stores its own results.
-template <int DT, int TT, int NA>
+// Single-dtype launch (rows <= 8) whose quantized activations fit LDS in one
+// piece. Workgroup b owns the contiguous row tiles [b G / R, (b + 1) G / R) of
+// the G tiles (R workgroups), so tile counts differ by at most one. Its eight
+// waves form A.wr row groups x A.wk K groups: row group rg takes the
+// workgroup's tiles rg, rg + wr, ...; wave (rg, kg) owns super-blocks kg,
+// kg + wk, ... of each. Each wave first loads its own activation units
+// (rows x super-blocks, at most KU) into registers, then requests its first
+// two weight stages, and quantizes its units while the weights are in
+// flight (the compiler waits for the activation loads only: they are older).
+// After one barrier the (tile, super-block) items stream through the two
+// register stages across tiles, so the next tile's weights are in flight
+// while the current one is stored. With wk = 1 (large launches such as the
+// LM head) a wave owns whole rows and stores its own results.
+template <int DT, int TT, int KU, int MODE>
 __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *lds, float *inv_w, float *red,
                                               int rows_out, bool swiglu) {
+    constexpr int NA = 1;
     using Stage = typename StageOf<DT>::T;
     constexpr uint32_t blk = DT == kQ4K ? 144u : 210u;
-    constexpr int kDeep = DeepItems<TT, NA>::value;
-    constexpr int kPer = TT * StageLoads<DT>::value;  // loads per item
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
     const int nsb = A.K / 256;
     const int wk = A.wk, wr = kWaves / wk;
     const int rg = wave / wk, kg = wave - rg * wk;
-    const ActLayout L(A.rows, NA, nsb, nsb, A.norm != nullptr, -1, A.gate != nullptr);
+    const ActLayout L(A.rows, NA, nsb, nsb, MODE == 1, -1, MODE == 2, false);
     const int mine = kg < nsb ? (nsb - kg + wk - 1) / wk : 0;  // super-blocks per tile
     const int G = A.groups, R = (int)gridDim.x, b = (int)blockIdx.x;
     const int t0 = (int)((int64_t)b * G / R), t1 = (int)((int64_t)(b + 1) * G / R);
@@ -859,8 +913,22 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
     const int ntile = rg < t1 - t0 ? (t1 - t0 - rg + wr - 1) / wr : 0;
     const int total = ntile * mine;
     float *my_inv = inv_w + wave * 16;
-    const int M = A.rows;
-    const float4 hw = head_norm_lane(A);
+    const float4 hw = MODE == 2 ? head_norm_lane(A) : make_float4(0.f, 0.f, 0.f, 0.f);
+
+    // ---- this wave's activation units (clamped indices past the end)
+    float4 xr[KU], gr[KU], zr[KU];
+    {
+        const int units = A.rows * nsb;
+#pragma unroll
+        for (int k = 0; k < KU; k++) {
+            const int u = min(wave + kWaves * k, units - 1);
+            const int m = u / nsb, sb = u - m * nsb;
+            xr[k] = *reinterpret_cast<const float4 *>(A.x + (size_t)m * A.K + sb * 256 + 4 * lane);
+            if constexpr (MODE == 1) gr[k] = *reinterpret_cast<const float4 *>(A.norm + sb * 256 + 4 * lane);
+            if constexpr (MODE == 2) zr[k] = *reinterpret_cast<const float4 *>(A.gate + (size_t)m * A.K + sb * 256 + 4 * lane);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
     auto zero = [&](float (&acc)[TT][NA][4]) __attribute__((always_inline)) {
 #pragma unroll
@@ -881,73 +949,6 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
             else compute<NA>(S[t], xa, sxp, xsr, acc[t], g);
         }
     };
-    if (YK_FG_DEEP && niter <= 1 && (nsb + wk - 1) / wk <= kDeep) {
-        // ---- deep path: one tile per row group, all items in flight
-        Stage st[kDeep][TT];
-#ifdef YK_FG_TIMING
-        uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        YK_FG_STAMP(ts[0]);
-#endif
-        const int tile = tile_of(0);
-        const bool live = ntile > 0;
-        const GroupRows<TT> Gr(A, live ? tile : t0, rows_out, swiglu, r);
-        act_fetch(A, L, lds, 0);
-        __builtin_amdgcn_sched_barrier(0);  // the LDS copies are the oldest loads
-        // two items go out with the activation copy; the rest only once the
-        // copy has landed, so that it does not queue behind the whole weight
-        // stream, and they stream while the activations are quantized
-        const int n_in = live ? mine : 0;
-        constexpr int kEarly = YK_FG_EARLY;
-#pragma unroll
-        for (int d = 0; d < kEarly; d++)
-            if (d < n_in) {
-#pragma unroll
-                for (int t = 0; t < TT; t++) issue(st[d][t], Gr.rs[t], Gr.row_off[t] + (uint32_t)(kg + wk * d) * blk, g);
-            }
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (kEarly > 0) wait_vm_n<kPer, kEarly>(min(n_in, kEarly));  // activations in LDS
-        else wait_vm<0>();
-        // the rest of the weights once every wave's copy has landed (the
-        // memory pipeline returns in order: earlier they would delay the
-        // slower waves' copies)
-        lds_barrier();
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int d = kEarly; d < kDeep; d++)
-            if (d < n_in) {
-#pragma unroll
-                for (int t = 0; t < TT; t++) issue(st[d][t], Gr.rs[t], Gr.row_off[t] + (uint32_t)(kg + wk * d) * blk, g);
-            }
-        __builtin_amdgcn_sched_barrier(0);
-#ifdef YK_FG_TIMING
-        YK_FG_STAMP(ts[1]);
-#endif
-        stream_prologue(A, L, lds, my_inv, nsb, hw);
-#ifdef YK_FG_TIMING
-        YK_FG_STAMP(ts[3]);
-        ts[2] = ts[3];
-        ts[4] = ts[3];
-#endif
-        float acc[TT][NA][4];
-        zero(acc);
-#pragma unroll
-        for (int d = 0; d < kDeep; d++)
-            if (d < n_in) compute_item(st[d], kg + wk * d, acc);
-#ifdef YK_FG_TIMING
-        YK_FG_STAMP(ts[5]);
-#endif
-        stream_epilogue<TT, NA>(A, red, my_inv, acc, live, live ? tile : t0, rows_out, swiglu, rg, kg, wk);
-#ifdef YK_FG_TIMING
-        YK_FG_STAMP(ts[7]);
-        if (yk_fg_dbg && lane == 0) {
-            uint64_t *o = yk_fg_dbg + ((size_t)blockIdx.x * kWaves + wave) * 8;
-            for (int e = 0; e < 8; e++) o[e] = ts[e];
-        }
-#endif
-        return;
-    }
-
-    // ---- ring path
     int kq = 0, jq = 0;  // issue cursor (iteration, super-block index)
     auto issue_next = [&](Stage (&S)[TT]) __attribute__((always_inline)) {
         const GroupRows<TT> Gr(A, tile_of(kq), rows_out, swiglu, r);
@@ -963,21 +964,18 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
     uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     YK_FG_STAMP(ts[0]);
 #endif
-    act_fetch(A, L, lds, 0);
-    __builtin_amdgcn_sched_barrier(0);  // the LDS copies are the oldest loads
-    if (total > 1) {
-        issue_next(st[0]);
-        issue_next(st[1]);
-        __builtin_amdgcn_sched_barrier(0);
-        wait_vm<2 * kPer>();  // activations in LDS, weights still in flight
-    } else {
-        if (total > 0) issue_next(st[0]);
-        __builtin_amdgcn_s_waitcnt(0);
-    }
+    if (total > 0) issue_next(st[0]);
+    if (total > 1) issue_next(st[1]);
+    __builtin_amdgcn_sched_barrier(0);
 #ifdef YK_FG_TIMING
     YK_FG_STAMP(ts[1]);
 #endif
-    stream_prologue(A, L, lds, my_inv, nsb, hw);
+    act_prologue_regs<MODE, KU>(A, L, lds, nsb, xr, gr, zr, hw);
+    lds_barrier();
+    {
+        const float v = lane_inv_rms(A, reinterpret_cast<const float *>(lds + L.nsq), nsb);
+        if (lane < 16) my_inv[lane] = v;
+    }
 #ifdef YK_FG_TIMING
     YK_FG_STAMP(ts[3]);
     ts[2] = ts[3];
@@ -1012,19 +1010,19 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
 #endif
 }
 
-// Streaming kernel (single dtype, activations in LDS in one piece): a
-// separate instantiation so that it carries none of the chunked path's
-// registers or scratch.
-template <int DT, int TT, int NA>
+// Streaming kernel: a separate instantiation per (dtype, tiles, activation
+// units per wave, prologue mode) so that it carries none of the chunked
+// path's registers or scratch.
+template <int DT, int TT, int KU, int MODE>
 __global__ __launch_bounds__(kThreads) void fgemm_stream_kernel(const FusedGemmArgs A) {
     extern __shared__ __align__(16) uint8_t lds[];
     const bool swiglu = A.epilogue == kEpiSwiglu;
     const int rows_out = swiglu ? 8 * TT : 16 * TT;
     const int nsb = A.K / 256;
-    const ActLayout L0(A.rows, NA, nsb, nsb, A.norm != nullptr, -1, A.gate != nullptr);
+    const ActLayout L0(A.rows, 1, nsb, nsb, MODE == 1, -1, MODE == 2, false);
     float *inv_w = reinterpret_cast<float *>(lds + L0.total);
     float *red = reinterpret_cast<float *>(lds + L0.total + kInvBytes);
-    stream_groups<DT, TT, NA>(A, lds, inv_w, red, rows_out, swiglu);
+    stream_groups<DT, TT, KU, MODE>(A, lds, inv_w, red, rows_out, swiglu);
 }
 
 template <int DTM, int TT, int NA>
@@ -1101,40 +1099,64 @@ static unsigned resident_wgs(const void *fn, uint32_t lds) {
     return (unsigned)(per_cu * cus);
 }
 
+// Streaming launch: every resident workgroup gets floor or ceil of G / R row
+// tiles; the waves split into the row-group x K-group shape that minimizes
+// the largest per-wave item count (ties: more row groups, fewer barriers).
+template <int DT, int TT, int KU, int MODE>
+static hipError_t launch_stream(const FusedGemmArgs &a, uint32_t lds, hipStream_t s) {
+    auto k = fgemm_stream_kernel<DT, TT, KU, MODE>;
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        attr = true;
+    }
+    FusedGemmArgs b = a;
+    const unsigned res = resident_wgs(reinterpret_cast<const void *>(k), lds);
+    const int nsb = b.K / 256;
+    const unsigned R = std::min((unsigned)b.groups, res);
+    const int per_wg = (int)((b.groups + R - 1) / R);
+    int best = 1 << 30;
+    b.wk = kWaves;
+    for (int wr = 1; wr <= kWaves; wr *= 2) {
+        const int wk = kWaves / wr;
+        const int items = ((per_wg + wr - 1) / wr) * ((nsb + wk - 1) / wk);
+        if (items <= best) {
+            best = items;
+            b.wk = wk;
+        }
+    }
+    k<<<R, kThreads, lds, s>>>(b);
+    return hipGetLastError();
+}
+
+template <int DT, int TT>
+static hipError_t launch_stream_ku(const FusedGemmArgs &a, int ku, int mode, uint32_t lds, hipStream_t s) {
+    if (mode == 2) return launch_stream<DT, TT, 8, 2>(a, lds, s);
+    if (mode == 1) return ku <= 8 ? launch_stream<DT, TT, 8, 1>(a, lds, s) : launch_stream<DT, TT, 16, 1>(a, lds, s);
+    if (ku <= 8) return launch_stream<DT, TT, 8, 0>(a, lds, s);
+    if (ku <= 16) return launch_stream<DT, TT, 16, 0>(a, lds, s);
+    return launch_stream<DT, TT, 24, 0>(a, lds, s);
+}
+
+// Streaming-kernel shape of a launch, or false when it takes the chunked path:
+// one dtype, rows <= 8, 1 or 2 tiles, activation units per wave within the
+// register bucket of the prologue mode, quantized activations in LDS.
+static bool stream_shape(const FusedGemmArgs &a, int tt, bool mixed, int *ku, int *mode, uint32_t *lds) {
+    if (mixed || a.rows > 8 || (tt != 1 && tt != 2) || (a.seg[0].dtype == kQ6K && tt != 1)) return false;
+    const int nsb = a.K / 256;
+    *mode = a.gate ? 2 : (a.norm ? 1 : 0);
+    *ku = (a.rows * nsb + kWaves - 1) / kWaves;
+    const int cap = *mode == 2 ? 8 : (*mode == 1 ? 16 : 24);
+    if (*ku > cap) return false;
+    const ActLayout L(a.rows, 1, nsb, nsb, *mode == 1, -1, *mode == 2, false);
+    *lds = L.total + kInvBytes + (uint32_t)kWaves * tt * 4 * 64 * 4;
+    return *lds <= kFusedLds;
+}
+
 template <int DTM, int TT, int NA>
 static hipError_t launch_tt(const FusedGemmArgs &a, unsigned grid, uint32_t lds, hipStream_t s) {
     FusedGemmArgs b = a;
     b.wk = kWaves;
-    if constexpr (DTM != 0) {
-        if (b.chunk_sb >= b.K / 256) {
-            auto k = fgemm_stream_kernel<DTM, TT, NA>;
-            static bool attr = false;
-            if (!attr) {
-                (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          160 * 1024);
-                attr = true;
-            }
-            const unsigned res = resident_wgs(reinterpret_cast<const void *>(k), lds);
-            // every resident workgroup gets floor or ceil of G / R row tiles;
-            // the waves split into the row-group x K-group shape that
-            // minimizes the largest per-wave item count (ties: more row
-            // groups, fewer barriers)
-            const int nsb = b.K / 256;
-            const unsigned R = std::min((unsigned)b.groups, res);
-            const int per_wg = (int)((b.groups + R - 1) / R);
-            int best = 1 << 30;
-            for (int wr = 1; wr <= kWaves; wr *= 2) {
-                const int wk = kWaves / wr;
-                const int items = ((per_wg + wr - 1) / wr) * ((nsb + wk - 1) / wk);
-                if (items <= best) {
-                    best = items;
-                    b.wk = wk;
-                }
-            }
-            k<<<R, kThreads, lds, s>>>(b);
-            return hipGetLastError();
-        }
-    }
     auto k = fgemm_kernel<DTM, TT, NA>;
     static bool attr = false;
     if (!attr) {
@@ -1173,14 +1195,18 @@ hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s) {
         grid += (unsigned)((b.seg[i].n + rows_out - 1) / rows_out);
     }
     b.groups = (int)grid;
-    const int nsb = b.K / 256;
     // Launches run persistent group loops over at most the resident
-    // workgroups: when the activations fit LDS in one chunk they are
-    // quantized once per workgroup, then further groups only stream weights.
-    (void)nsb;
-    const uint32_t lds = fused_gemm_lds_bytes(b.rows, b.K, b.chunk_sb, tt, b.norm != nullptr, b.gate != nullptr);
+    // workgroups; each workgroup quantizes the activations once.
     bool mixed = false;
     for (int i = 1; i < b.nseg; i++) mixed |= b.seg[i].dtype != b.seg[0].dtype;
+    int ku = 0, mode = 0;
+    uint32_t slds = 0;
+    if (!getenv("YUUKA_FGEMM_CHUNKED") && stream_shape(b, tt, mixed, &ku, &mode, &slds)) {
+        if (b.seg[0].dtype == kQ4K)
+            return tt == 1 ? launch_stream_ku<kQ4K, 1>(b, ku, mode, slds, s) : launch_stream_ku<kQ4K, 2>(b, ku, mode, slds, s);
+        return launch_stream_ku<kQ6K, 1>(b, ku, mode, slds, s);
+    }
+    const uint32_t lds = fused_gemm_lds_bytes(b.rows, b.K, b.chunk_sb, tt, b.norm != nullptr, b.gate != nullptr);
     if (mixed) return launch_dt<0>(b, tt, grid, lds, s);
     if (b.seg[0].dtype == kQ4K) return launch_dt<kQ4K>(b, tt, grid, lds, s);
     return launch_dt<kQ6K>(b, tt, grid, lds, s);
