@@ -889,13 +889,26 @@ __device__ __forceinline__ void stream_epilogue(const FusedGemmArgs &A, float *r
 // two weight stages, and quantizes its units while the weights are in
 // flight (the compiler waits for the activation loads only: they are older).
 // After one barrier the (tile, super-block) items stream through the two
-// register stages across tiles, so the next tile's weights are in flight
-// while the current one is stored. With wk = 1 (large launches such as the
+// register stages (kRing) across tiles, so the next tile's weights are in
+// flight while the current one is stored. With wk = 1 (large launches such as the
 // LM head) a wave owns whole rows and stores its own results.
+// Register stages of the weight ring (items in flight per wave).
+#ifndef YK_FG_RING_Q6
+#define YK_FG_RING_Q6 2
+#endif
+#ifndef YK_FG_RING_Q4
+#define YK_FG_RING_Q4 2
+#endif
+template <int DT, int TT> struct RingDepth {
+    static constexpr int value = TT > 1 ? 2 : (DT == kQ6K ? YK_FG_RING_Q6 : YK_FG_RING_Q4);
+};
+
 template <int DT, int TT, int KU, int MODE>
 __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *lds, float *inv_w, float *red,
                                               int rows_out, bool swiglu) {
     constexpr int NA = 1;
+    constexpr int kRing = RingDepth<DT, TT>::value;
+    static_assert(kRing >= 2 && kRing <= 4, "ring depth");
     using Stage = typename StageOf<DT>::T;
     constexpr uint32_t blk = DT == kQ4K ? 144u : 210u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -959,13 +972,14 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
             ++kq;
         }
     };
-    Stage st[2][TT];
+    Stage st[kRing][TT];
 #ifdef YK_FG_TIMING
     uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     YK_FG_STAMP(ts[0]);
 #endif
-    if (total > 0) issue_next(st[0]);
-    if (total > 1) issue_next(st[1]);
+#pragma unroll
+    for (int d = 0; d < kRing; d++)
+        if (total > d) issue_next(st[d]);
     __builtin_amdgcn_sched_barrier(0);
 #ifdef YK_FG_TIMING
     YK_FG_STAMP(ts[1]);
@@ -988,12 +1002,20 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
         float acc[TT][NA][4];
         zero(acc);
         for (int j = 0; live && j < mine; j++, i++) {
-            if ((i & 1) == 0) {
-                compute_item(st[0], kg + wk * j, acc);
-                if (i + 2 < total) issue_next(st[0]);
-            } else {
-                compute_item(st[1], kg + wk * j, acc);
-                if (i + 2 < total) issue_next(st[1]);
+            // stage i % kRing holds item i; it is refilled with item i + kRing
+            switch (i % kRing) {
+#define YK_FG_RING_CASE(c)                                                                                         \
+    case c:                                                                                                        \
+        if constexpr (c < kRing) {                                                                                 \
+            compute_item(st[c], kg + wk * j, acc);                                                                 \
+            if (i + kRing < total) issue_next(st[c]);                                                              \
+        }                                                                                                          \
+        break;
+                YK_FG_RING_CASE(0)
+                YK_FG_RING_CASE(1)
+                YK_FG_RING_CASE(2)
+                YK_FG_RING_CASE(3)
+#undef YK_FG_RING_CASE
             }
         }
 #ifdef YK_FG_TIMING

@@ -261,10 +261,89 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_commit_kernel(
 }
 
 
+// float64 sum over the wave on the DPP path (16-lane row trees, then the four
+// row results through readlane), in every lane.
+template <int CTRL>
+__device__ __forceinline__ double dpp_dd(double v) {
+    const uint64_t b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xf, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xf, 0xf, true);
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+__device__ __forceinline__ double rl_dd(double v, int l) {
+    const uint64_t b = __double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double wave_sum_dpp(double v) {
+    v += dpp_dd<0xb1>(v);
+    v += dpp_dd<0x4e>(v);
+    v += dpp_dd<0x124>(v);
+    v += dpp_dd<0x128>(v);
+    return (rl_dd(v, 15) + rl_dd(v, 31)) + (rl_dd(v, 47) + rl_dd(v, 63));
+}
+
+// Causal conv + SiLU of two channels (c1 < 0: one) with every input load
+// issued before either is computed.
+__device__ __forceinline__ void conv_channel2(const float *conv_state, const float *qkv, const float *conv_w,
+                                              const GdnArgs &g, int c0, float *dst0, int stride0, int c1, float *dst1,
+                                              int stride1) {
+    const int R = g.rows, K = g.kernel;
+    const int cc[2] = {c0, c1 < 0 ? c0 : c1};
+    float w[2][8], st[2][8], x[2][16];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            w[u][i] = i < K ? conv_w[(uint64_t)cc[u] * K + i] : 0.0f;
+            st[u][i] = i < K - 1 ? conv_state[(uint64_t)cc[u] * (K - 1) + i] : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) x[u][r] = r < R ? qkv[(uint64_t)r * g.conv_dim + cc[u]] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        if (u == 1 && c1 < 0) break;
+        float *dst = u == 0 ? dst0 : dst1;
+        const int stride = u == 0 ? stride0 : stride1;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            if (r >= R) break;
+            float sum = 0.0f;
+#pragma unroll
+            for (int tt = 0; tt < 7; tt++) {
+                if (tt >= K - 1) break;
+                const int idx = r + tt - (K - 1);
+                float xv = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 16; q++)
+                    if (q == idx) xv = x[u][q];
+#pragma unroll
+                for (int q = 0; q < 7; q++)
+                    if (q == K - 1 + idx && idx < 0) xv = st[u][q];
+                sum = __fadd_rn(sum, __fmul_rn(w[u][tt], xv));
+            }
+            float wl = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (q == K - 1) wl = w[u][q];
+            sum = __fadd_rn(sum, __fmul_rn(wl, x[u][r]));
+            dst[r * stride] = silu_ref(sum);
+        }
+    }
+}
+
 // ---- column-split variants: workgroup (head h, block of kCols state
 // columns). Lane l of wave w holds column j = kCols * blockIdx.y + 8 w + l / 8
 // and state rows 16 (l % 8) .. +15; a column's eight row parts form an
 // aligned 8-lane group, so column sums need no barrier.
+#ifdef YK_GD_TIMING
+__device__ uint64_t *yk_gd_dbg;
+#define YK_GD_STAMP(i) ts[i] = __builtin_amdgcn_s_memrealtime()
+#else
+#define YK_GD_STAMP(i) (void)0
+#endif
 constexpr int kCols = 32;
 constexpr int kMaxRows = 16;  // verify rows of one step
 constexpr int kColThreads = 256;
@@ -291,37 +370,34 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
         cf[t] = gdn_decay(g, alpha_raw, dt, a_log, t, h);
         cf[R + t] = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
     }
+#ifdef YK_GD_TIMING
+    uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#endif
+    YK_GD_STAMP(0);
     const int p = lane & 7, j = cb * kCols + wave * 8 + (lane >> 3);
     const float *mat = state + (uint64_t)h * kS * kS;
     float s_reg[16];
 #pragma unroll
     for (int ii = 0; ii < 16; ii++) s_reg[ii] = mat[(uint64_t)(p * 16 + ii) * kS + j];
-    // conv of 256 q/k channels + kCols v channels
-    for (int ch = t; ch < 2 * kS + kCols; ch += kColThreads) {
-        int c;
-        float *dst;
-        int stride;
-        if (ch < 2 * kS) {
-            const int which = ch >> 7, cc = ch & (kS - 1);
-            c = (which == 0 ? 0 : key_dim) + kh * kS + cc;
-            dst = qk + which * kS + cc;
-            stride = 2 * kS;
-        } else {
-            const int cc = ch - 2 * kS;
-            c = 2 * key_dim + h * kS + cb * kCols + cc;
-            dst = vv + cc;
-            stride = kCols;
-        }
-        conv_channel(conv_state, qkv, conv_w, g, c, dst, stride);
+    // conv of 256 q/k channels (thread t: channel t) + kCols v channels
+    // (threads 0 .. kCols - 1, loaded together with their first channel)
+    {
+        static_assert(2 * kS == kColThreads, "one q/k channel per thread");
+        const int which = t >> 7, cc = t & (kS - 1);
+        const int c0 = (which == 0 ? 0 : key_dim) + kh * kS + cc;
+        const int c1 = t < kCols ? 2 * key_dim + h * kS + cb * kCols + t : -1;
+        conv_channel2(conv_state, qkv, conv_w, g, c0, qk + which * kS + cc, 2 * kS, c1, vv + t, kCols);
     }
+    YK_GD_STAMP(1);
     __syncthreads();
+    YK_GD_STAMP(2);
     const bool owns_qk = cb == 0 && h < g.groups;
     for (int vec = wave; vec < 2 * R; vec += kColThreads / 64) {
         const int r = vec >> 1, which = vec & 1;
         float *x = qk + (r * 2 + which) * kS;
         const float a0 = x[lane], a1 = x[lane + 64];
         double sq = (double)a0 * (double)a0 + (double)a1 * (double)a1;
-        sq = wave_sum_dd(sq);
+        sq = wave_sum_dpp(sq);
         const float extra = which == 0 ? g.q_scale : 1.0f;
         const float scale = __fmul_rn((float)(1.0 / sqrt(sq + (double)g.eps)), extra);
         const float y0 = __fmul_rn(a0, scale), y1 = __fmul_rn(a1, scale);
@@ -337,7 +413,9 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
         const int r = idx / kCols, cc = idx % kCols;
         conv_out[(uint64_t)r * g.conv_dim + 2 * key_dim + h * kS + cb * kCols + cc] = vv[r * kCols + cc];
     }
+    YK_GD_STAMP(3);
     __syncthreads();
+    YK_GD_STAMP(4);
     const int jl = j - cb * kCols;
     for (int r = 0; r < R; r++) {
         const float *q = qk + (r * 2 + 0) * kS, *k = qk + (r * 2 + 1) * kS;
@@ -359,6 +437,13 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
         o = group8_sum_f(o);
         if (p == 0) raw_out[((uint64_t)r * g.rank + h) * kS + j] = o;
     }
+    YK_GD_STAMP(5);
+#ifdef YK_GD_TIMING
+    if (yk_gd_dbg && lane == 0) {
+        uint64_t *o = yk_gd_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave) * 8;
+        for (int e = 0; e < 8; e++) o[e] = ts[e];
+    }
+#endif
 }
 
 // Commit of one layer: replay of the accepted rows for this block's
