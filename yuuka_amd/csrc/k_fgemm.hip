@@ -392,84 +392,116 @@ __device__ __forceinline__ void act_prologue(const FusedGemmArgs &A, const ActLa
     else act_prologue_m<0>(A, L, lds, c0, nsb, hw);
 }
 
-// Quantization of the streaming kernel's units from registers: wave w's
-// units are w, w + 8, ... (k-th in slot k of xr / gr / zr, loaded at kernel
-// start, before the weight stream). Same arithmetic and LDS tables as
-// act_prologue_m; four units at a time, branch-free (units past the end
-// store to the per-lane scratch slot).
-template <int MODE, int KU>
+// Quantization of the streaming kernel's units from registers. A unit (row
+// m, super-block sb: 256 elements) belongs to one 16-lane DPP row: lane s of
+// the row holds elements [16 s, 16 s + 16), i.e. sub-block s / 2 and MFMA
+// slices 2 (s % 2) and 2 (s % 2) + 1. Every reduction stays inside the row
+// (no cross-row exchange). Unit-step k of wave w covers units 4 (w + 8 k) +
+// row; xr[k][0..3] hold the lane's 16 values (gr: norm weights, zr: gate),
+// loaded at kernel start before the weight stream. Units past the end
+// compute on a clamped index and store to the per-lane scratch slot.
+template <int MODE, int KS>
 __device__ __forceinline__ void act_prologue_regs(const FusedGemmArgs &A, const ActLayout &L, uint8_t *lds, int nsb,
-                                                  const float4 (&xr)[KU], const float4 (&gr)[KU], const float4 (&zr)[KU],
-                                                  float4 hw) {
+                                                  const float4 (&xr)[KS][4], const float4 (&gr)[KS][4],
+                                                  const float4 (&zr)[KS][4], const float4 (&hw)[4]) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
+    const int s16 = lane & 15, row = lane >> 4;
     const int M = A.rows;
     const int total = M * nsb;
-    const int j = lane >> 3, g = (lane >> 1) & 3, hf = lane & 1;
+    const int j = s16 >> 1, g0 = (s16 & 1) * 2;
     const uint32_t junk = L.junk + (uint32_t)lane * 8;
 #pragma unroll
-    for (int k0 = 0; k0 < KU; k0 += 4) {
-        if (wave + kWaves * k0 >= total) break;  // wave-uniform
+    for (int k = 0; k < KS; k++) {
+        if (4 * (wave + kWaves * k) >= total) break;  // wave-uniform
+        const int uu = 4 * (wave + kWaves * k) + row;
+        const bool live = uu < total;
+        const int u = min(uu, total - 1);
+        const int m = u / nsb, sbl = u - m * nsb;
+        float v[16];
 #pragma unroll
-        for (int k = k0; k < k0 + 4; k++) {
-            const int uu = wave + kWaves * k;
-            const bool live = uu < total;
-            const int u = min(uu, total - 1);
-            const int m = u / nsb, sbl = u - m * nsb;
-            float v[4] = {xr[k].x, xr[k].y, xr[k].z, xr[k].w};
-            float sq = 0.0f;
-            if constexpr (MODE == 1) {
-                sq = fmaf(v[3], v[3], fmaf(v[2], v[2], fmaf(v[1], v[1], v[0] * v[0])));
-                v[0] = __fmul_rn(v[0], gr[k].x); v[1] = __fmul_rn(v[1], gr[k].y);
-                v[2] = __fmul_rn(v[2], gr[k].z); v[3] = __fmul_rn(v[3], gr[k].w);
-            }
-            if constexpr (MODE == 2) {
-                double ss = 0.0;
+        for (int q = 0; q < 4; q++) {
+            v[4 * q + 0] = xr[k][q].x; v[4 * q + 1] = xr[k][q].y;
+            v[4 * q + 2] = xr[k][q].z; v[4 * q + 3] = xr[k][q].w;
+        }
+        float sq = 0.0f;
+        if constexpr (MODE == 1) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) ss += (double)v[i] * (double)v[i];
-                ss = row_sum_d(ss);
-                const double h0 = rl_d(ss, 15) + rl_d(ss, 31), h1 = rl_d(ss, 47) + rl_d(ss, 63);
-                const double hs = lane < 32 ? h0 : h1;
-                const float mean = (float)(hs / 128.0);
-                const float scale = (float)(1.0 / sqrt((double)(mean + A.eps)));
-                v[0] = __fmul_rn(__fmul_rn(v[0], __fmul_rn(scale, hw.x)), zr[k].x);
-                v[1] = __fmul_rn(__fmul_rn(v[1], __fmul_rn(scale, hw.y)), zr[k].y);
-                v[2] = __fmul_rn(__fmul_rn(v[2], __fmul_rn(scale, hw.z)), zr[k].z);
-                v[3] = __fmul_rn(__fmul_rn(v[3], __fmul_rn(scale, hw.w)), zr[k].w);
-            }
-            const uint32_t a = max(max(__float_as_uint(v[0]) & 0x7fffffffu, __float_as_uint(v[1]) & 0x7fffffffu),
-                                   max(__float_as_uint(v[2]) & 0x7fffffffu, __float_as_uint(v[3]) & 0x7fffffffu));
-            const uint32_t ar = row_max_u32(a);
-            const float amax = __uint_as_float(max(max(rl_u(ar, 15), rl_u(ar, 31)), max(rl_u(ar, 47), rl_u(ar, 63))));
-            const float xs = amax * (1.0f / (float)kQMax);
-            const float inv = amax > 0.0f ? (float)kQMax * __builtin_amdgcn_rcpf(amax) : 0.0f;
-            uint32_t t[4];
+            for (int i = 0; i < 16; i++) sq = fmaf(v[i], v[i], sq);
 #pragma unroll
-            for (int i = 0; i < 4; i++) t[i] = __float_as_uint(fmaf(v[i], inv, kRoundMagic));
-            const uint32_t hp = __builtin_amdgcn_perm(t[1], t[0], 0x0c0c0501u) | __builtin_amdgcn_perm(t[3], t[2], 0x05010c0cu);
-            const uint32_t lp = (__builtin_amdgcn_perm(t[1], t[0], 0x0c0c0400u) | __builtin_amdgcn_perm(t[3], t[2], 0x04000c0cu)) ^
-                                0x80808080u;
-            const uint32_t slot = L.planes + ((uint32_t)((sbl * 8 + j) * 4 + g) * L.rho + m) * 8 + 4 * hf;
-            *reinterpret_cast<uint32_t *>(lds + (live ? slot : junk)) = hp;
-            *reinterpret_cast<uint32_t *>(lds + (live ? slot + (uint32_t)M * 8 : junk + 4)) = lp;
-            const int hs = oct_sum(__builtin_amdgcn_sdot4((int)hp, 0x01010101, 0, false));
-            const int ls = oct_sum(__builtin_amdgcn_sdot4((int)lp, 0x01010101, 0, false));
-            const bool lead = live && (lane & 7) == 0;
-            const uint32_t sh = L.sums + (((uint32_t)sbl * L.rhop + m) * 8 + j) * 2;
-            const uint32_t sl = L.sums + (((uint32_t)sbl * L.rhop + M + m) * 8 + j) * 2;
-            *reinterpret_cast<int16_t *>(lds + (lead ? sh : junk)) = (int16_t)hs;
-            *reinterpret_cast<int16_t *>(lds + (lead ? sl : junk + 2)) = (int16_t)ls;
-            const bool first = live && lane == 0;
-            const uint32_t xh = L.xs + ((uint32_t)sbl * L.rhop + m) * 4;
-            const uint32_t xl = L.xs + ((uint32_t)sbl * L.rhop + M + m) * 4;
-            *reinterpret_cast<float *>(lds + (first ? xh : junk)) = xs;
-            *reinterpret_cast<float *>(lds + (first ? xl : junk + 4)) = xs;
-            if constexpr (MODE == 1) {
-                const float rsum = row_sum(sq);
-                const float tot = (rdl(rsum, 15) + rdl(rsum, 31)) + (rdl(rsum, 47) + rdl(rsum, 63));
-                const uint32_t nq = L.nsq + (uint32_t)(m * nsb + sbl) * 4;
-                *reinterpret_cast<float *>(lds + (first ? nq : junk)) = tot;
+            for (int q = 0; q < 4; q++) {
+                v[4 * q + 0] = __fmul_rn(v[4 * q + 0], gr[k][q].x); v[4 * q + 1] = __fmul_rn(v[4 * q + 1], gr[k][q].y);
+                v[4 * q + 2] = __fmul_rn(v[4 * q + 2], gr[k][q].z); v[4 * q + 3] = __fmul_rn(v[4 * q + 3], gr[k][q].w);
             }
+        }
+        if constexpr (MODE == 2) {
+            // gated head norm: a 128-element head is 8 lanes
+            double ss = 0.0;
+#pragma unroll
+            for (int i = 0; i < 16; i++) ss += (double)v[i] * (double)v[i];
+            ss += dpp_d<0xb1>(ss);
+            ss += dpp_d<0x4e>(ss);
+            ss += dpp_d<0x141>(ss);
+            const float mean = (float)(ss / 128.0);
+            const float scale = (float)(1.0 / sqrt((double)(mean + A.eps)));
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                v[4 * q + 0] = __fmul_rn(__fmul_rn(v[4 * q + 0], __fmul_rn(scale, hw[q].x)), zr[k][q].x);
+                v[4 * q + 1] = __fmul_rn(__fmul_rn(v[4 * q + 1], __fmul_rn(scale, hw[q].y)), zr[k][q].y);
+                v[4 * q + 2] = __fmul_rn(__fmul_rn(v[4 * q + 2], __fmul_rn(scale, hw[q].z)), zr[k][q].z);
+                v[4 * q + 3] = __fmul_rn(__fmul_rn(v[4 * q + 3], __fmul_rn(scale, hw[q].w)), zr[k][q].w);
+            }
+        }
+        uint32_t a = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i++) a = max(a, __float_as_uint(v[i]) & 0x7fffffffu);
+        const float amax = __uint_as_float(row_max_u32(a));
+        // xs * inv ~ 1 keeps every value exact to the quantization step;
+        // the reciprocal keeps |v * inv| <= kQMax + 2^-10, so no clamp.
+        const float xs = amax * (1.0f / (float)kQMax);
+        const float inv = amax > 0.0f ? (float)kQMax * __builtin_amdgcn_rcpf(amax) : 0.0f;
+        uint32_t t[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) t[i] = __float_as_uint(fmaf(v[i], inv, kRoundMagic));
+        uint32_t hp[4], lp[4];
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            hp[d] = __builtin_amdgcn_perm(t[4 * d + 1], t[4 * d], 0x0c0c0501u) |
+                    __builtin_amdgcn_perm(t[4 * d + 3], t[4 * d + 2], 0x05010c0cu);
+            lp[d] = (__builtin_amdgcn_perm(t[4 * d + 1], t[4 * d], 0x0c0c0400u) |
+                     __builtin_amdgcn_perm(t[4 * d + 3], t[4 * d + 2], 0x04000c0cu)) ^
+                    0x80808080u;
+        }
+        // slices g0 (elements 0..7 of the lane) and g0 + 1 (8..15)
+        const uint32_t s0 = L.planes + ((uint32_t)((sbl * 8 + j) * 4 + g0) * L.rho + m) * 8;
+        const uint32_t s1 = s0 + (uint32_t)L.rho * 8;
+        *reinterpret_cast<uint2 *>(lds + (live ? s0 : junk)) = make_uint2(hp[0], hp[1]);
+        *reinterpret_cast<uint2 *>(lds + (live ? s1 : junk)) = make_uint2(hp[2], hp[3]);
+        *reinterpret_cast<uint2 *>(lds + (live ? s0 + (uint32_t)M * 8 : junk)) = make_uint2(lp[0], lp[1]);
+        *reinterpret_cast<uint2 *>(lds + (live ? s1 + (uint32_t)M * 8 : junk)) = make_uint2(lp[2], lp[3]);
+        // exact int16 sums of both planes per 32-element sub-block (2 lanes)
+        int hs = 0, ls = 0;
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            hs = __builtin_amdgcn_sdot4((int)hp[d], 0x01010101, hs, false);
+            ls = __builtin_amdgcn_sdot4((int)lp[d], 0x01010101, ls, false);
+        }
+        hs += dpp<0xb1>(hs);
+        ls += dpp<0xb1>(ls);
+        const bool lead = live && (s16 & 1) == 0;
+        const uint32_t sh = L.sums + (((uint32_t)sbl * L.rhop + m) * 8 + j) * 2;
+        const uint32_t sl = L.sums + (((uint32_t)sbl * L.rhop + M + m) * 8 + j) * 2;
+        *reinterpret_cast<int16_t *>(lds + (lead ? sh : junk)) = (int16_t)hs;
+        *reinterpret_cast<int16_t *>(lds + (lead ? sl : junk + 2)) = (int16_t)ls;
+        const bool first = live && s16 == 0;
+        const uint32_t xh = L.xs + ((uint32_t)sbl * L.rhop + m) * 4;
+        const uint32_t xl = L.xs + ((uint32_t)sbl * L.rhop + M + m) * 4;
+        *reinterpret_cast<float *>(lds + (first ? xh : junk)) = xs;
+        *reinterpret_cast<float *>(lds + (first ? xl : junk + 4)) = xs;
+        if constexpr (MODE == 1) {
+            const float tot = row_sum(sq);
+            const uint32_t nq = L.nsq + (uint32_t)(m * nsb + sbl) * 4;
+            *reinterpret_cast<float *>(lds + (first ? nq : junk)) = tot;
         }
     }
     // rows past 2M of the padded tables read as zero
@@ -926,19 +958,28 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
     const int ntile = rg < t1 - t0 ? (t1 - t0 - rg + wr - 1) / wr : 0;
     const int total = ntile * mine;
     float *my_inv = inv_w + wave * 16;
-    const float4 hw = MODE == 2 ? head_norm_lane(A) : make_float4(0.f, 0.f, 0.f, 0.f);
-
-    // ---- this wave's activation units (clamped indices past the end)
-    float4 xr[KU], gr[KU], zr[KU];
+    // ---- this wave's activation units: unit-step k, DPP row `row` holds unit
+    //      4 (wave + 8 k) + row, lane s16 its elements [16 s16, +16)
+    constexpr int KS = KU / 4;
+    float4 xr[KS][4], gr[KS][4], zr[KS][4], hw[4];
     {
         const int units = A.rows * nsb;
+        const int s16 = lane & 15, row = lane >> 4;
+        if constexpr (MODE == 2) {
 #pragma unroll
-        for (int k = 0; k < KU; k++) {
-            const int u = min(wave + kWaves * k, units - 1);
+            for (int q = 0; q < 4; q++) hw[q] = *reinterpret_cast<const float4 *>(A.head_norm + (s16 & 7) * 16 + 4 * q);
+        }
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            const int u = min(4 * (wave + kWaves * k) + row, units - 1);
             const int m = u / nsb, sb = u - m * nsb;
-            xr[k] = *reinterpret_cast<const float4 *>(A.x + (size_t)m * A.K + sb * 256 + 4 * lane);
-            if constexpr (MODE == 1) gr[k] = *reinterpret_cast<const float4 *>(A.norm + sb * 256 + 4 * lane);
-            if constexpr (MODE == 2) zr[k] = *reinterpret_cast<const float4 *>(A.gate + (size_t)m * A.K + sb * 256 + 4 * lane);
+            const size_t off = (size_t)m * A.K + sb * 256 + 16 * s16;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                xr[k][q] = *reinterpret_cast<const float4 *>(A.x + off + 4 * q);
+                if constexpr (MODE == 1) gr[k][q] = *reinterpret_cast<const float4 *>(A.norm + sb * 256 + 16 * s16 + 4 * q);
+                if constexpr (MODE == 2) zr[k][q] = *reinterpret_cast<const float4 *>(A.gate + off + 4 * q);
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -984,7 +1025,7 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
 #ifdef YK_FG_TIMING
     YK_FG_STAMP(ts[1]);
 #endif
-    act_prologue_regs<MODE, KU>(A, L, lds, nsb, xr, gr, zr, hw);
+    act_prologue_regs<MODE, KS>(A, L, lds, nsb, xr, gr, zr, hw);
     lds_barrier();
     {
         const float v = lane_inv_rms(A, reinterpret_cast<const float *>(lds + L.nsq), nsb);
