@@ -47,7 +47,7 @@ struct FusedGemmArgs {
     int epilogue;       // FusedEpilogue
     int nseg;
     int groups;         // row tiles (16*tt rows) over all segments (set by the launcher)
-    int wk;             // waves splitting K in the streaming path (1, 2, 4 or 8; set by the launcher)
+    int wk;             // streaming path: waves splitting K (1, 2, 4 or 8), 0 = items dealt to waves one by one (set by the launcher)
     FusedSeg seg[kFusedMaxSeg];
 };
 

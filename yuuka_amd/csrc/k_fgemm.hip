@@ -59,6 +59,9 @@ constexpr int kWaves = kFusedWaves;
 constexpr int kThreads = 64 * kWaves;
 // 1/rms of the rows: 16 floats per wave
 constexpr uint32_t kInvBytes = kWaves * 16 * 4;
+// Tiles per workgroup up to which the streaming kernel deals items to waves
+// one by one (balanced mode, wk = 0).
+constexpr int kBalMax = 4;
 
 // Keeps one ring stage's activation reads from being hoisted into the
 // previous stage (that multiplies live registers).
@@ -935,7 +938,7 @@ template <int DT, int TT> struct RingDepth {
     static constexpr int value = TT > 1 ? 2 : (DT == kQ6K ? YK_FG_RING_Q6 : YK_FG_RING_Q4);
 };
 
-template <int DT, int TT, int KU, int MODE>
+template <int DT, int TT, int KU, int MODE, bool BAL>
 __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *lds, float *inv_w, float *red,
                                               int rows_out, bool swiglu) {
     constexpr int NA = 1;
@@ -947,7 +950,9 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
     const int lane = threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
     const int nsb = A.K / 256;
-    const int wk = A.wk, wr = kWaves / wk;
+    // A.wk == 0 selects balanced mode; the row-group x K-group shape below is
+    // only used by the ring path (the guard keeps the divisions defined)
+    const int wk = BAL || A.wk < 1 ? 1 : A.wk, wr = kWaves / wk;
     const int rg = wave / wk, kg = wave - rg * wk;
     const ActLayout L(A.rows, NA, nsb, nsb, MODE == 1, -1, MODE == 2, false);
     const int mine = kg < nsb ? (nsb - kg + wk - 1) / wk : 0;  // super-blocks per tile
@@ -1013,6 +1018,102 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
             ++kq;
         }
     };
+    if constexpr (BAL) {
+        // ---- balanced mode (at most kBalMax tiles per workgroup): the
+        //      workgroup's (tile, super-block) items, tile-major, are dealt
+        //      round-robin to the eight waves; each wave keeps one partial per
+        //      tile in LDS, and every tile's outputs sum the eight partials in
+        //      wave order after one barrier.
+        const int cnt = t1 - t0, I = cnt * nsb;
+        const int nmine = wave < I ? (I - wave + kWaves - 1) / kWaves : 0;
+        auto issue_item = [&](Stage (&S)[TT], int ii) __attribute__((always_inline)) {
+            const int c = ii / nsb, sb = ii - c * nsb;
+            const GroupRows<TT> Gr(A, t0 + c, rows_out, swiglu, r);
+#pragma unroll
+            for (int t = 0; t < TT; t++) issue(S[t], Gr.rs[t], Gr.row_off[t] + (uint32_t)sb * blk, g);
+        };
+        constexpr int kSlot = TT * NA * 256;  // floats of one wave's partial of one tile
+        float *myr = red + (size_t)wave * kBalMax * kSlot;
+        Stage sb2[2][TT];
+        if (nmine > 0) issue_item(sb2[0], wave);
+        if (nmine > 1) issue_item(sb2[1], wave + kWaves);
+        __builtin_amdgcn_sched_barrier(0);
+        for (int idx = lane; idx < cnt * kSlot / 4; idx += 64)
+            reinterpret_cast<float4 *>(myr)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
+        act_prologue_regs<MODE, KS>(A, L, lds, nsb, xr, gr, zr, hw);
+        lds_barrier();
+        {
+            const float v = lane_inv_rms(A, reinterpret_cast<const float *>(lds + L.nsq), nsb);
+            if (lane < 16) my_inv[lane] = v;
+        }
+        float acc[TT][NA][4];
+        zero(acc);
+        auto flush = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int a = 0; a < NA; a++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) myr[c * kSlot + ((t * NA + a) * 4 + e) * 64 + lane] = acc[t][a][e];
+        };
+        int cur = nmine > 0 ? wave / nsb : 0;
+        for (int q = 0; q < nmine; q++) {
+            const int ii = wave + kWaves * q, c = ii / nsb, sbi = ii - c * nsb;
+            if (c != cur) {
+                flush(cur);
+                zero(acc);
+                cur = c;
+            }
+            if ((q & 1) == 0) {
+                compute_item(sb2[0], sbi, acc);
+                if (q + 2 < nmine) issue_item(sb2[0], ii + 2 * kWaves);
+            } else {
+                compute_item(sb2[1], sbi, acc);
+                if (q + 2 < nmine) issue_item(sb2[1], ii + 2 * kWaves);
+            }
+        }
+        if (nmine > 0) flush(cur);
+        lds_barrier();
+        const int M = A.rows, per_tile = rows_out * M;
+        for (int idx = threadIdx.x; idx < cnt * per_tile; idx += kThreads) {
+            const int c = idx / per_tile, rem = idx - c * per_tile;
+            const int m = rem / rows_out, rr = rem - m * rows_out;
+            const GroupRows<TT> Gr(A, t0 + c, rows_out, swiglu, 0);
+            const int n = Gr.n0 + rr;
+            if (n >= Gr.N) continue;
+            const int t = rr >> 4, col = rr & 15;
+            const float ir = my_inv[m];
+            float val[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int tt = t + h * (TT / 2);
+                const int ah = m >> 4, gh = (m & 15) >> 2, eh = m & 3;
+                const int rl = M + m, al = rl >> 4, gl = (rl & 15) >> 2, el = rl & 3;
+                float ph = 0.0f, pl = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kWaves; w++) {
+                    const float *wr_ = red + ((size_t)w * kBalMax + c) * kSlot;
+                    ph += wr_[((tt * NA + ah) * 4 + eh) * 64 + gh * 16 + col];
+                    pl += wr_[((tt * NA + al) * 4 + el) * 64 + gl * 16 + col];
+                }
+                float v = 256.0f * ph + pl;
+                if (A.norm) v *= ir;
+                val[h] = v;
+                if (!swiglu) break;
+            }
+            const size_t o = (size_t)m * Gr.N + n;
+            if (swiglu) {
+                A.seg[0].out[o] = silu_mul(val[0], val[1]);
+            } else {
+                float v = val[0];
+                if (A.epilogue == kEpiResidual) v += A.seg[Gr.s].res[o];
+                else v = out_map(A.seg[Gr.s], v, n);
+                A.seg[Gr.s].out[o] = v;
+            }
+        }
+        return;
+    }
+
     Stage st[kRing][TT];
 #ifdef YK_FG_TIMING
     uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -1076,7 +1177,7 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
 // Streaming kernel: a separate instantiation per (dtype, tiles, activation
 // units per wave, prologue mode) so that it carries none of the chunked
 // path's registers or scratch.
-template <int DT, int TT, int KU, int MODE>
+template <int DT, int TT, int KU, int MODE, bool BAL>
 __global__ __launch_bounds__(kThreads) void fgemm_stream_kernel(const FusedGemmArgs A) {
     extern __shared__ __align__(16) uint8_t lds[];
     const bool swiglu = A.epilogue == kEpiSwiglu;
@@ -1085,7 +1186,7 @@ __global__ __launch_bounds__(kThreads) void fgemm_stream_kernel(const FusedGemmA
     const ActLayout L0(A.rows, 1, nsb, nsb, MODE == 1, -1, MODE == 2, false);
     float *inv_w = reinterpret_cast<float *>(lds + L0.total);
     float *red = reinterpret_cast<float *>(lds + L0.total + kInvBytes);
-    stream_groups<DT, TT, KU, MODE>(A, lds, inv_w, red, rows_out, swiglu);
+    stream_groups<DT, TT, KU, MODE, BAL>(A, lds, inv_w, red, rows_out, swiglu);
 }
 
 template <int DTM, int TT, int NA>
@@ -1149,13 +1250,9 @@ int fused_gemm_chunk_sb(int rows, int K, int tt, bool norm, bool gated) {
 
 // Workgroups that are resident at once: a persistent grid never exceeds it,
 // so no group waits for a second round.
+static int device_cus();
 static unsigned resident_wgs(const void *fn, uint32_t lds) {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0;
-        (void)hipGetDevice(&dev);
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 1;
-    }
+    const int cus = device_cus();
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, lds) != hipSuccess || per_cu <= 0)
         per_cu = 1;
@@ -1165,16 +1262,19 @@ static unsigned resident_wgs(const void *fn, uint32_t lds) {
 // Streaming launch: every resident workgroup gets floor or ceil of G / R row
 // tiles; the waves split into the row-group x K-group shape that minimizes
 // the largest per-wave item count (ties: more row groups, fewer barriers).
-template <int DT, int TT, int KU, int MODE>
-static hipError_t launch_stream(const FusedGemmArgs &a, uint32_t lds, hipStream_t s) {
-    auto k = fgemm_stream_kernel<DT, TT, KU, MODE>;
+template <int DT, int TT, int KU, int MODE, bool BAL>
+static hipError_t launch_stream1(const FusedGemmArgs &a, uint32_t lds, hipStream_t s) {
+    constexpr bool balanced = BAL;
+    auto k = fgemm_stream_kernel<DT, TT, KU, MODE, BAL>;
     static bool attr = false;
     if (!attr) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(k), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         attr = true;
     }
     FusedGemmArgs b = a;
-    const unsigned res = resident_wgs(reinterpret_cast<const void *>(k), lds);
+    // one workgroup per CU: a second one would quantize the same activations
+    // again on the same CU
+    const unsigned res = std::min(resident_wgs(reinterpret_cast<const void *>(k), lds), (unsigned)device_cus());
     const int nsb = b.K / 256;
     const unsigned R = std::min((unsigned)b.groups, res);
     const int per_wg = (int)((b.groups + R - 1) / R);
@@ -1188,23 +1288,45 @@ static hipError_t launch_stream(const FusedGemmArgs &a, uint32_t lds, hipStream_
             b.wk = wk;
         }
     }
+    if (balanced) b.wk = 0;
     k<<<R, kThreads, lds, s>>>(b);
     return hipGetLastError();
 }
 
+template <int DT, int TT, int KU, int MODE>
+static hipError_t launch_stream(const FusedGemmArgs &a, uint32_t lds, bool balanced, hipStream_t s) {
+    return balanced ? launch_stream1<DT, TT, KU, MODE, true>(a, lds, s) : launch_stream1<DT, TT, KU, MODE, false>(a, lds, s);
+}
+
 template <int DT, int TT>
-static hipError_t launch_stream_ku(const FusedGemmArgs &a, int ku, int mode, uint32_t lds, hipStream_t s) {
-    if (mode == 2) return launch_stream<DT, TT, 8, 2>(a, lds, s);
-    if (mode == 1) return ku <= 8 ? launch_stream<DT, TT, 8, 1>(a, lds, s) : launch_stream<DT, TT, 16, 1>(a, lds, s);
-    if (ku <= 8) return launch_stream<DT, TT, 8, 0>(a, lds, s);
-    if (ku <= 16) return launch_stream<DT, TT, 16, 0>(a, lds, s);
-    return launch_stream<DT, TT, 24, 0>(a, lds, s);
+static hipError_t launch_stream_ku(const FusedGemmArgs &a, int ku, int mode, uint32_t lds, bool bal, hipStream_t s) {
+    if (mode == 2) return launch_stream<DT, TT, 8, 2>(a, lds, bal, s);
+    if (mode == 1) return ku <= 8 ? launch_stream<DT, TT, 8, 1>(a, lds, bal, s) : launch_stream<DT, TT, 16, 1>(a, lds, bal, s);
+    if (ku <= 8) return launch_stream<DT, TT, 8, 0>(a, lds, bal, s);
+    if (ku <= 16) return launch_stream<DT, TT, 16, 0>(a, lds, bal, s);
+    return launch_stream<DT, TT, 24, 0>(a, lds, bal, s);
 }
 
 // Streaming-kernel shape of a launch, or false when it takes the chunked path:
 // one dtype, rows <= 8, 1 or 2 tiles, activation units per wave within the
 // register bucket of the prologue mode, quantized activations in LDS.
-static bool stream_shape(const FusedGemmArgs &a, int tt, bool mixed, int *ku, int *mode, uint32_t *lds) {
+static int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 1;
+    }
+    return cus;
+}
+
+// Streaming-kernel shape of a launch, or false when it takes the chunked path:
+// one dtype, rows <= 8, 1 or 2 tiles, activation units per wave within the
+// register bucket of the prologue mode, quantized activations in LDS.
+// *balanced: at most kBalMax row tiles per workgroup (one workgroup per CU:
+// 512 threads at more than 128 VGPRs).
+static bool stream_shape(const FusedGemmArgs &a, int tt, bool mixed, int *ku, int *mode, uint32_t *lds,
+                         bool *balanced) {
     if (mixed || a.rows > 8 || (tt != 1 && tt != 2) || (a.seg[0].dtype == kQ6K && tt != 1)) return false;
     const int nsb = a.K / 256;
     *mode = a.gate ? 2 : (a.norm ? 1 : 0);
@@ -1212,7 +1334,9 @@ static bool stream_shape(const FusedGemmArgs &a, int tt, bool mixed, int *ku, in
     const int cap = *mode == 2 ? 8 : (*mode == 1 ? 16 : 24);
     if (*ku > cap) return false;
     const ActLayout L(a.rows, 1, nsb, nsb, *mode == 1, -1, *mode == 2, false);
-    *lds = L.total + kInvBytes + (uint32_t)kWaves * tt * 4 * 64 * 4;
+    const int R = std::min(a.groups, device_cus());
+    *balanced = (a.groups + R - 1) / R <= kBalMax && !getenv("YUUKA_FGEMM_UNBALANCED");
+    *lds = L.total + kInvBytes + (uint32_t)kWaves * (*balanced ? kBalMax : 1) * tt * 4 * 64 * 4;
     return *lds <= kFusedLds;
 }
 
@@ -1264,10 +1388,12 @@ hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s) {
     for (int i = 1; i < b.nseg; i++) mixed |= b.seg[i].dtype != b.seg[0].dtype;
     int ku = 0, mode = 0;
     uint32_t slds = 0;
-    if (!getenv("YUUKA_FGEMM_CHUNKED") && stream_shape(b, tt, mixed, &ku, &mode, &slds)) {
+    bool bal = false;
+    if (!getenv("YUUKA_FGEMM_CHUNKED") && stream_shape(b, tt, mixed, &ku, &mode, &slds, &bal)) {
         if (b.seg[0].dtype == kQ4K)
-            return tt == 1 ? launch_stream_ku<kQ4K, 1>(b, ku, mode, slds, s) : launch_stream_ku<kQ4K, 2>(b, ku, mode, slds, s);
-        return launch_stream_ku<kQ6K, 1>(b, ku, mode, slds, s);
+            return tt == 1 ? launch_stream_ku<kQ4K, 1>(b, ku, mode, slds, bal, s)
+                           : launch_stream_ku<kQ4K, 2>(b, ku, mode, slds, bal, s);
+        return launch_stream_ku<kQ6K, 1>(b, ku, mode, slds, bal, s);
     }
     const uint32_t lds = fused_gemm_lds_bytes(b.rows, b.K, b.chunk_sb, tt, b.norm != nullptr, b.gate != nullptr);
     if (mixed) return launch_dt<0>(b, tt, grid, lds, s);
