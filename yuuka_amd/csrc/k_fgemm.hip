@@ -530,9 +530,17 @@ struct Q6Stage {
     uint32_t d;     // f16 bits
 };
 
+// Stage of a launch whose segments mix Q4_K and Q6_K (dtype uniform per tile).
+struct MixStage {
+    Q4Stage q4;
+    Q6Stage q6;
+    int dt;
+};
+
 template <int DT> struct StageOf;
 template <> struct StageOf<kQ4K> { using T = Q4Stage; };
 template <> struct StageOf<kQ6K> { using T = Q6Stage; };
+template <> struct StageOf<0> { using T = MixStage; };
 
 __device__ __forceinline__ void issue(Q4Stage &S, __amdgpu_buffer_rsrc_t rs, uint32_t row_off, int g) {
     S.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, row_off, 0, 0);
@@ -641,6 +649,37 @@ __device__ __forceinline__ void compute(const Q6Stage &S, const int64_t (&xa)[NA
     for (int a = 0; a < NA; a++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[a][i] += xsr[a][i] * (d * (float)acci[a][i]);
+}
+
+// Super-block sb of the 16-row tile whose row 0 of this lane starts at
+// row_off, in the stage's format.
+__device__ __forceinline__ void issue_any(Q4Stage &S, __amdgpu_buffer_rsrc_t rs, uint32_t row_off, uint32_t sb, int g, int) {
+    issue(S, rs, row_off + sb * 144u, g);
+}
+__device__ __forceinline__ void issue_any(Q6Stage &S, __amdgpu_buffer_rsrc_t rs, uint32_t row_off, uint32_t sb, int g, int) {
+    issue(S, rs, row_off + sb * 210u, g);
+}
+__device__ __forceinline__ void issue_any(MixStage &S, __amdgpu_buffer_rsrc_t rs, uint32_t row_off, uint32_t sb, int g,
+                                          int dt) {
+    S.dt = dt;
+    if (dt == kQ4K) issue(S.q4, rs, row_off + sb * 144u, g);
+    else issue(S.q6, rs, row_off + sb * 210u, g);
+}
+template <int NA>
+__device__ __forceinline__ void compute_any(const Q4Stage &S, const int64_t (&xa)[NA][8], const uint32_t (&sxp)[NA][4][4],
+                                            const float (&xsr)[NA][4], float (&acc)[NA][4], int) {
+    compute<NA>(S, xa, sxp, xsr, acc);
+}
+template <int NA>
+__device__ __forceinline__ void compute_any(const Q6Stage &S, const int64_t (&xa)[NA][8], const uint32_t (&sxp)[NA][4][4],
+                                            const float (&xsr)[NA][4], float (&acc)[NA][4], int g) {
+    compute<NA>(S, xa, sxp, xsr, acc, g);
+}
+template <int NA>
+__device__ __forceinline__ void compute_any(const MixStage &S, const int64_t (&xa)[NA][8], const uint32_t (&sxp)[NA][4][4],
+                                            const float (&xsr)[NA][4], float (&acc)[NA][4], int g) {
+    if (S.dt == kQ4K) compute<NA>(S.q4, xa, sxp, xsr, acc);
+    else compute<NA>(S.q6, xa, sxp, xsr, acc, g);
 }
 
 template <int NA>
@@ -945,7 +984,6 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
     constexpr int kRing = RingDepth<DT, TT>::value;
     static_assert(kRing >= 2 && kRing <= 4, "ring depth");
     using Stage = typename StageOf<DT>::T;
-    constexpr uint32_t blk = DT == kQ4K ? 144u : 210u;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int r = lane & 15, g = lane >> 4;
@@ -1001,18 +1039,15 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
         int64_t xa[NA][8];
         uint32_t sxp[NA][4][4];
         float xsr[NA][4];
-        load_act<NA>(lds, L, sb, r, g, xa, sxp, xsr, DT == kQ4K);
+        load_act<NA>(lds, L, sb, r, g, xa, sxp, xsr, DT != kQ6K);
 #pragma unroll
-        for (int t = 0; t < TT; t++) {
-            if constexpr (DT == kQ4K) compute<NA>(S[t], xa, sxp, xsr, acc[t]);
-            else compute<NA>(S[t], xa, sxp, xsr, acc[t], g);
-        }
+        for (int t = 0; t < TT; t++) compute_any<NA>(S[t], xa, sxp, xsr, acc[t], g);
     };
     int kq = 0, jq = 0;  // issue cursor (iteration, super-block index)
     auto issue_next = [&](Stage (&S)[TT]) __attribute__((always_inline)) {
         const GroupRows<TT> Gr(A, tile_of(kq), rows_out, swiglu, r);
 #pragma unroll
-        for (int t = 0; t < TT; t++) issue(S[t], Gr.rs[t], Gr.row_off[t] + (uint32_t)(kg + wk * jq) * blk, g);
+        for (int t = 0; t < TT; t++) issue_any(S[t], Gr.rs[t], Gr.row_off[t], (uint32_t)(kg + wk * jq), g, Gr.dt);
         if (++jq == mine) {
             jq = 0;
             ++kq;
@@ -1030,7 +1065,7 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
             const int c = ii / nsb, sb = ii - c * nsb;
             const GroupRows<TT> Gr(A, t0 + c, rows_out, swiglu, r);
 #pragma unroll
-            for (int t = 0; t < TT; t++) issue(S[t], Gr.rs[t], Gr.row_off[t] + (uint32_t)sb * blk, g);
+            for (int t = 0; t < TT; t++) issue_any(S[t], Gr.rs[t], Gr.row_off[t], (uint32_t)sb, g, Gr.dt);
         };
         constexpr int kSlot = TT * NA * 256;  // floats of one wave's partial of one tile
         float *myr = red + (size_t)wave * kBalMax * kSlot;
@@ -1327,7 +1362,7 @@ static int device_cus() {
 // 512 threads at more than 128 VGPRs).
 static bool stream_shape(const FusedGemmArgs &a, int tt, bool mixed, int *ku, int *mode, uint32_t *lds,
                          bool *balanced) {
-    if (mixed || a.rows > 8 || (tt != 1 && tt != 2) || (a.seg[0].dtype == kQ6K && tt != 1)) return false;
+    if (a.rows > 8 || (tt != 1 && tt != 2) || ((mixed || a.seg[0].dtype == kQ6K) && tt != 1)) return false;
     const int nsb = a.K / 256;
     *mode = a.gate ? 2 : (a.norm ? 1 : 0);
     *ku = (a.rows * nsb + kWaves - 1) / kWaves;
@@ -1390,6 +1425,7 @@ hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s) {
     uint32_t slds = 0;
     bool bal = false;
     if (!getenv("YUUKA_FGEMM_CHUNKED") && stream_shape(b, tt, mixed, &ku, &mode, &slds, &bal)) {
+        if (mixed) return launch_stream_ku<0, 1>(b, ku, mode, slds, bal, s);
         if (b.seg[0].dtype == kQ4K)
             return tt == 1 ? launch_stream_ku<kQ4K, 1>(b, ku, mode, slds, bal, s)
                            : launch_stream_ku<kQ4K, 2>(b, ku, mode, slds, bal, s);
