@@ -247,7 +247,7 @@ def dominant_kernel(dev, cfg, rows, rng):
         b.free()
     return {"bound": "hbm", "achieved": gemm_ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": gemm_ach / HBM_PEAK_GBS, "traffic": read_traffic("fgemm_ffn_swiglu_pmc.md"),
-            "kernel": f"fgemm_kernel<12,2,1> (GEMM_FUSED SwiGLU) 2x{N}x{K} Q4_K M={rows}",
+            "kernel": f"fgemm_stream_kernel<12,2,8,1,true> (GEMM_FUSED SwiGLU) 2x{N}x{K} Q4_K M={rows}",
             "alg_bytes_per_launch": gemm_bytes, "avg_us": gemm_us, "launches": reps * copies}
 
 
