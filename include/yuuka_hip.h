@@ -343,12 +343,14 @@ typedef struct yuuka_accept_params {
  * Greedy: accept draft i iff argmax(row i) == draft i (lowest index among
  * equal maxima; a NaN at index 0 wins, later NaNs never do); next = argmax
  * of the first rejected row, or of row k when every draft is accepted.
- * Stochastic: target p = softmax(logit/T) over finite logits (float64 sums);
- * draft i is accepted iff u_i < p(d_i) with u_i = Philox(seed; step, i,
- * request, 0); on the first rejection next is drawn from p with d_i removed,
- * and after full acceptance from row k, by inverse CDF in index order with
- * u = Philox(seed; step, i, request, 1).
- * top_k > 1 or top_p < 1 currently returns YUUKA_ERR_UNSUPPORTED. */
+ * Stochastic: the target p is the sampler's distribution
+ * (engine/sampling.go:60-119): drop NaN and -Inf, order by (logit desc, id
+ * asc), keep the first top_k (0 = all), weights exp(float64(logit-max)/T),
+ * then keep the smallest prefix whose share reaches top_p (0 or >= 1 = all);
+ * sums in float64. Draft i is accepted iff u_i < p(d_i) with
+ * u_i = Philox(seed; step, i, request, 0); on the first rejection next is
+ * drawn from p with d_i removed, and after full acceptance from row k, by
+ * inverse CDF in index order with u = Philox(seed; step, i, request, 1). */
 YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
                         const yuuka_buffer * logits, uint64_t logits_offset,
                         const yuuka_buffer * drafts, uint64_t drafts_offset,

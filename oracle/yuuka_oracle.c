@@ -391,6 +391,7 @@ int64_t orc_target_weights(const float *logits, int64_t n, float temperature, in
         *total = 1.0;
         return 1;
     }
+    if (top_p == 0.0f) top_p = 1.0f; /* NewSampler: 0 means off (sampling.go:46-48) */
     cand *c = (cand *)malloc((size_t)n * sizeof(cand));
     int64_t m = 0;
     for (int64_t i = 0; i < n; i++) {

@@ -113,8 +113,89 @@ def test_stochastic_zero_temperature_is_greedy(dev, stream):
     assert (res[0, 0], res[0, 1]) == (a, nxt)
 
 
-def test_top_p_is_reported_unsupported(dev, stream):
-    c = synth.config1(0)
-    p = hip.accept_params(hip.ACCEPT_STOCHASTIC, 1, c["k"], c["V"], temperature=0.7, top_p=0.9)
-    with pytest.raises(hip.Unsupported):
-        _run(dev, stream, c["logits"], c["drafts"], p)
+def _check_truncated(dev, stream, logits, drafts, T, top_k, top_p, seed, step):
+    """Device vs oracle for one request under top-k / top-p: the kept set must
+    match (row totals agree to 1e-12), so must p(draft) and every decision,
+    except at a near-tie of u and p(draft)."""
+    k = len(drafts)
+    V = logits.shape[-1]
+    p = hip.accept_params(hip.ACCEPT_STOCHASTIC, 1, k, V, temperature=T, top_k=top_k, top_p=top_p,
+                          seed=seed, step=step)
+    res, dbg = _run(dev, stream, logits, drafts, p)
+    a, nxt, pd, ua = O.accept_stochastic(logits, drafts, T, seed, step, 0, top_k, top_p)
+    last = min(a, int(res[0, 0]))
+    for i in range(last + 1):
+        _, w, total, _ = O.target_weights(logits[i], T, top_k, top_p)
+        assert abs(dbg[0, i, 2] - total) <= 1e-12 * total, (i, dbg[0, i, 2], total)
+        if i < k:
+            assert dbg[0, i, 1] == ua[i]
+            assert abs(dbg[0, i, 0] - pd[i]) <= 1e-9 * max(pd[i], 1e-300) + 1e-15
+    if (int(res[0, 0]), int(res[0, 1])) != (a, nxt):
+        assert last < k and abs(ua[last] - pd[last]) < 1e-9, (res[0], a, nxt)
+        return 1
+    return 0
+
+
+@pytest.mark.parametrize("top_k,top_p,T", [(0, 0.9, 0.7), (50, 1.0, 0.8), (400, 0.9, 0.7), (0, 0.5, 1.3)])
+def test_stochastic_top_k_top_p_matches_oracle(dev, stream, top_k, top_p, T):
+    """The config-3 sampler settings (T = 0.7, top-p 0.9) and top-k alone or
+    combined, on N(0, 3) logits over the full vocabulary."""
+    rng = np.random.default_rng(31 + top_k)
+    k, V = 8, 151936
+    mism = 0
+    for trial in range(6):
+        logits = rng.normal(0, 3, (k + 1, V)).astype(np.float32)
+        drafts = rng.integers(0, V, k).astype(np.int32)
+        order = np.argsort(-logits, axis=1, kind="stable")
+        for i in range(k):  # drafts from the head of the distribution, so rows get accepted
+            if rng.random() < 0.8:
+                drafts[i] = order[i, int(rng.integers(0, 3))]
+        mism += _check_truncated(dev, stream, logits, drafts, T, top_k, top_p, 77, trial)
+    assert mism <= 1
+
+
+def test_truncation_cut_inside_tie_groups(dev, stream):
+    """Integer-valued logits make the top-k and top-p boundaries fall inside
+    large groups of equal logits: the kept members are the lowest ids
+    (sampling.go:84-92); -0 and +0 rank as equal."""
+    rng = np.random.default_rng(5)
+    k, V = 3, 5000
+    for top_k, top_p in [(37, 1.0), (0, 0.3), (700, 0.6), (5, 0.99)]:
+        logits = rng.integers(0, 8, (k + 1, V)).astype(np.float32)
+        logits[:, ::7] = 0.0
+        logits[:, 3::7] = -0.0
+        logits[:, 11] = np.nan
+        logits[:, 12] = -np.inf
+        drafts = []
+        for i in range(k):
+            ties = np.flatnonzero(logits[i] == 7.0)
+            drafts.append(int(ties[min(len(ties) - 1, (i + 1) * 9)]))
+        for step in range(3):
+            assert _check_truncated(dev, stream, logits, np.array(drafts, np.int32), 1.0, top_k, top_p, 3,
+                                    step) == 0
+
+
+def test_truncation_zero_and_negative_keys(dev, stream):
+    """A cut among zero and negative logits, where the order key of -0 must
+    equal that of +0."""
+    k, V = 2, 3000
+    logits = np.full((k + 1, V), -1.0, np.float32)
+    logits[:, 100:200] = -0.0
+    logits[:, 150:250] = 0.0
+    logits[:, 5] = 2.0
+    drafts = np.array([180, 240], np.int32)
+    for top_k in (30, 120, 190, 260):
+        assert _check_truncated(dev, stream, logits, drafts, 0.5, top_k, 1.0, 9, top_k) == 0
+
+
+def test_truncated_acceptance_is_reproducible(dev, stream):
+    """The radix-selection histograms are combined in a fixed order: two runs
+    give bit-identical probabilities and decisions."""
+    rng = np.random.default_rng(12)
+    k, V = 8, 151936
+    logits = rng.normal(0, 3, (k + 1, V)).astype(np.float32)
+    drafts = np.argsort(-logits, axis=1)[:k, 1].astype(np.int32)
+    p = hip.accept_params(hip.ACCEPT_STOCHASTIC, 1, k, V, temperature=0.7, top_p=0.9, seed=4, step=2)
+    r1, d1 = _run(dev, stream, logits, drafts, p)
+    r2, d2 = _run(dev, stream, logits, drafts, p)
+    assert (r1 == r2).all() and np.array_equal(d1, d2)

@@ -313,6 +313,21 @@ def test_sampler_top_p_smallest_prefix():
     assert kept == 3 and w[3] == 0
 
 
+def test_sampler_top_p_zero_is_off_and_ties_keep_lowest_ids():
+    """NewSampler maps top-p 0 to 1 (sampling.go:46-48); equal logits are
+    ordered by id (sampling.go:84-89), so a cut inside a tie keeps the lowest
+    ids, and -0 ties with +0."""
+    logits = np.log(np.array([0.5, 0.3, 0.15, 0.05], np.float64)).astype(np.float32)
+    kept, w, _, _ = O.target_weights(logits, 1.0, 0, 0.0)
+    assert kept == 4 and (w > 0).all()
+    flat = np.zeros(10, np.float32)
+    flat[[1, 4, 6]] = -0.0
+    kept, w, _, _ = O.target_weights(flat, 1.0, 3, 1.0)
+    assert kept == 3 and np.flatnonzero(w).tolist() == [0, 1, 2]
+    kept, w, _, _ = O.target_weights(flat, 1.0, 0, 0.25)  # 3 of 10 equal weights reach 0.25
+    assert kept == 3 and np.flatnonzero(w).tolist() == [0, 1, 2]
+
+
 # ------------------------------------------------------------ acceptance
 
 def test_accept_greedy_onehot_reduces_to_string_compare():

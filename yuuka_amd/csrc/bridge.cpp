@@ -485,9 +485,6 @@ yuuka_status yuuka_verify_accept(yuuka_stream *stream, const yuuka_buffer *logit
         if (p.batch == 0 || p.vocab == 0 || p.vocab > (1u << 30) || p.drafts > 255)
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid batch %u, drafts %u or vocab %u", p.batch,
                         p.drafts, p.vocab);
-        if (p.mode == YUUKA_ACCEPT_STOCHASTIC && p.temperature > 0.0f && p.top_k != 1 &&
-            (p.top_k > 1 || p.top_p < 1.0f))
-            return fail(YUUKA_ERR_UNSUPPORTED, "top-k/top-p truncation is not implemented");
         if (p.mode == YUUKA_ACCEPT_STOCHASTIC && !(p.top_p >= 0.0f && p.top_p <= 1.0f) && p.top_p != 0.0f)
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "top-p must be in (0,1]");
         const uint64_t stride = p.row_stride ? p.row_stride : p.vocab;

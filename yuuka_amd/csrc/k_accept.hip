@@ -5,15 +5,18 @@
 // argmaxLogit (:263-271): draft i is accepted iff the first maximum of row i
 // equals it. Stochastic mode is speculative sampling with a one-hot draft
 // (no reference counterpart): accept iff u < p(d), else resample from p with
-// d removed; the target p follows engine/sampling.go:94-100 (weights
-// exp(float64(logit - max) / T) over finite logits).
+// d removed; the target p follows engine/sampling.go:60-119 (drop NaN/-Inf,
+// top-k in (logit desc, id asc) order, weights exp(float64(logit - max) / T),
+// top-p smallest prefix).
 //
-// Three kernels (the two passes over a row are separate launches so that the
-// exact row maximum is known before any exponential is taken):
+// Kernels (the passes over a row are separate launches so that the exact row
+// maximum is known before any exponential is taken):
 //   1. stats:    per (request, row, chunk): maximum and its first index.
-//   2. weights:  (stochastic) per chunk: float64 sum of the weights with the
-//                draft removed, and the draft's own weight.
-//   3. finalize: one workgroup per request walks the rows in order, decides,
+//   2. select:   (top-k / top-p only) one workgroup per row finds the row's
+//                cut by radix selection over the order key of the logits.
+//   3. weights:  (stochastic) per chunk: float64 sum of the kept weights with
+//                the draft removed, and the draft's own weight.
+//   4. finalize: one workgroup per request walks the rows in order, decides,
 //                and for a rejection or the bonus row draws by inverse CDF
 //                in index order (chunk prefix, then a scan inside the chunk).
 #include <hip/hip_runtime.h>
@@ -79,15 +82,48 @@ __global__ __launch_bounds__(256) void accept_stats_kernel(const float *__restri
     }
 }
 
-__device__ __forceinline__ double weight_of(float l, float mx, double inv_t) {
-    if (!(l == l) || l == -INFINITY) return 0.0;  // NaN and -Inf are dropped
-    return exp((double)(l - mx) * inv_t);
+// Truncation cut of one row (top-k / top-p): an element is kept iff its
+// order key is above `key`, or equal to it with an id of at most `id`. The
+// default {0, INT_MAX} keeps every valid logit.
+struct Cut {
+    uint32_t key;
+    int32_t id;
+};
+
+// Monotone map of a float onto uint32 (larger logit, larger key). -0 maps
+// with +0, since the sampler's sort compares values (sampling.go:84-89).
+__device__ __forceinline__ uint32_t order_key(float l) {
+    uint32_t u = __float_as_uint(l);
+    if ((u << 1) == 0u) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float key_value(uint32_t key) {
+    return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+// NaN and -Inf are dropped (sampling.go:75-80).
+__device__ __forceinline__ bool valid_logit(float l) { return l == l && l != -INFINITY; }
+
+__device__ __forceinline__ bool in_cut(uint32_t key, int j, const Cut &c) {
+    return key > c.key || (key == c.key && j <= c.id);
+}
+
+// exp(float64(logit - max) / T) (sampling.go:97), zero outside the cut.
+__device__ __forceinline__ double weight_of(float l, int j, float mx, double t, const Cut &c) {
+    if (!valid_logit(l) || !in_cut(order_key(l), j, c)) return 0.0;
+    return exp((double)(l - mx) / t);
+}
+
+__device__ __forceinline__ Cut row_cut(const Cut *cuts, const Geo &g, int b, int row) {
+    return cuts ? cuts[(uint64_t)b * g.R + row] : Cut{0u, INT_MAX};
 }
 
 __global__ __launch_bounds__(256) void accept_weights_kernel(const float *__restrict__ logits, Geo g,
                                                              const int32_t *__restrict__ drafts,
                                                              const Stat *__restrict__ stats,
-                                                             double inv_t, double *__restrict__ sums,
+                                                             const Cut *__restrict__ cuts, double t,
+                                                             double *__restrict__ sums,
                                                              double *__restrict__ wdraft) {
     const int c = blockIdx.x, row = blockIdx.y, b = blockIdx.z;
     const float *p = row_ptr(logits, g, b, row);
@@ -107,12 +143,13 @@ __global__ __launch_bounds__(256) void accept_weights_kernel(const float *__rest
     }
     __syncthreads();
     const float mx = mx_s;
+    const Cut cut = row_cut(cuts, g, b, row);
     const int d = row < g.k ? drafts[(uint64_t)b * g.k + row] : -1;
     const int begin = c * g.L;
     const int end = min(begin + g.L, g.V);
     double acc = 0.0;
     for (int j = begin + threadIdx.x; j < end; j += 256) {
-        const double w = weight_of(p[j], mx, inv_t);
+        const double w = weight_of(p[j], j, mx, t, cut);
         if (j == d)
             wdraft[(uint64_t)b * g.R + row] = w;
         else
@@ -123,6 +160,252 @@ __global__ __launch_bounds__(256) void accept_weights_kernel(const float *__rest
     if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = acc;
     __syncthreads();
     if (threadIdx.x == 0) sums[((uint64_t)b * g.R + row) * g.C + c] = ws[0] + ws[1] + ws[2] + ws[3];
+}
+
+// ---------------------------------------------------------------- truncation
+// Per-row cut for top-k / top-p (sampling.go:84-113) without sorting: radix
+// selection over the 32-bit order key, one workgroup per row, histograms in
+// LDS. Each wave fills its own histogram and the waves are combined in wave
+// order, so weight sums do not depend on wave scheduling.
+constexpr int kSelWaves = 16;
+
+struct SelShared {
+    uint32_t cnt[kSelWaves][256];
+    double wsum[kSelWaves][256];
+    uint32_t tc[256];
+    double tw[256];
+    uint32_t prefix;    // digits chosen so far
+    int bucket;         // bucket chosen by the last scan (-1: none)
+    uint32_t before_c;  // count of the buckets ahead of it in scan order
+    double before_w;    // their weight
+    double total_w;     // all weight of the first pass
+    uint32_t total_c;
+    int id;             // result of an id selection
+    float mx;
+};
+
+template <bool W, class Sel, class Dig>
+__device__ __forceinline__ void hist_pass(const float *__restrict__ p, int V, float mx, double t, SelShared &s,
+                                          Sel sel, Dig dig) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int b = lane; b < 256; b += 64) {
+        s.cnt[wave][b] = 0u;
+        if (W) s.wsum[wave][b] = 0.0;
+    }
+    __syncthreads();
+    constexpr int kStride = kSelWaves * 64;
+    for (int j0 = threadIdx.x; j0 < V; j0 += 4 * kStride) {
+        float l[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) l[u] = j0 + u * kStride < V ? p[j0 + u * kStride] : NAN;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int j = j0 + u * kStride;
+            if (!valid_logit(l[u]) || !sel(l[u], j)) continue;
+            const int b = dig(l[u], j);
+            atomicAdd(&s.cnt[wave][b], 1u);
+            if (W) unsafeAtomicAdd(&s.wsum[wave][b], exp((double)(l[u] - mx) / t));
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 256) {
+        uint32_t c = 0u;
+        double w = 0.0;
+        for (int q = 0; q < kSelWaves; q++) {
+            c += s.cnt[q][threadIdx.x];
+            if (W) w += s.wsum[q][threadIdx.x];
+        }
+        s.tc[threadIdx.x] = c;
+        s.tw[threadIdx.x] = w;
+    }
+    __syncthreads();
+}
+
+// Thread 0: walk the buckets in scan order (descending keys, or ascending for
+// ids) to the first non-empty one where the running count reaches need_c (or
+// the running weight reaches need_w); append its digit to the prefix.
+__device__ __forceinline__ void scan_buckets(SelShared &s, bool descending, bool by_weight, uint32_t need_c,
+                                             double need_w, int shift) {
+    uint32_t c = s.before_c;
+    double w = s.before_w;
+    int pick = -1;
+    for (int q = 0; q < 256; q++) {
+        const int b = descending ? 255 - q : q;
+        const uint32_t bc = s.tc[b];
+        if (!bc) continue;
+        if (by_weight ? (w + s.tw[b] >= need_w) : (c + bc >= need_c)) {
+            pick = b;
+            break;
+        }
+        c += bc;
+        w += s.tw[b];
+    }
+    s.bucket = pick;
+    if (pick >= 0) {
+        s.before_c = c;
+        s.before_w = w;
+        s.prefix |= (uint32_t)pick << shift;
+    }
+}
+
+// The need-th smallest id (1-based) among the elements with order key `key`
+// that lie inside `cut`.
+__device__ int select_id(const float *p, int V, SelShared &s, uint32_t key, Cut cut, uint32_t need) {
+    if (threadIdx.x == 0) {
+        s.prefix = 0u;
+        s.before_c = 0u;
+        s.before_w = 0.0;
+    }
+    __syncthreads();
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 24 - 8 * pass;
+        const uint32_t mask = pass ? ~0u << (shift + 8) : 0u;
+        const uint32_t pre = s.prefix;
+        hist_pass<false>(
+            p, V, 0.f, 1.0, s,
+            [=](float l, int j) {
+                const uint32_t k = order_key(l);
+                return k == key && in_cut(k, j, cut) && ((uint32_t)j & mask) == pre;
+            },
+            [=](float, int j) { return ((uint32_t)j >> shift) & 255u; });
+        if (threadIdx.x == 0) scan_buckets(s, false, false, need, 0.0, shift);
+        __syncthreads();
+    }
+    const int id = (int)s.prefix;
+    __syncthreads();  // every thread has read the result before the state is reused
+    return id;
+}
+
+__global__ __launch_bounds__(1024) void accept_select_kernel(const float *__restrict__ logits, Geo g,
+                                                             const Stat *__restrict__ stats, int top_k,
+                                                             float top_p, double t, Cut *__restrict__ cuts) {
+    const int row = blockIdx.x, b = blockIdx.y;
+    const float *p = row_ptr(logits, g, b, row);
+    __shared__ SelShared s;
+    if (threadIdx.x < 64) {  // the row maximum from the per-chunk statistics
+        const Stat *st = stats + ((uint64_t)b * g.R + row) * g.C;
+        float bv = -INFINITY;
+        int bi = INT_MAX;
+        for (int cc = threadIdx.x; cc < g.C; cc += 64)
+            if (beats(st[cc].v, st[cc].i, bv, bi)) { bv = st[cc].v; bi = st[cc].i; }
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+        }
+        if (threadIdx.x == 0) s.mx = bv;
+    }
+    __syncthreads();
+    const float mx = s.mx;
+    Cut cut{0u, INT_MAX};
+
+    // top-k: the top_k-th element in (logit desc, id asc) order (sampling.go:90-92).
+    if (top_k > 0) {
+        if (threadIdx.x == 0) {
+            s.prefix = 0u;
+            s.before_c = 0u;
+            s.before_w = 0.0;
+        }
+        __syncthreads();
+        bool all = false;
+        for (int pass = 0; pass < 4; pass++) {
+            const int shift = 24 - 8 * pass;
+            const uint32_t mask = pass ? ~0u << (shift + 8) : 0u;
+            const uint32_t pre = s.prefix;
+            hist_pass<false>(
+                p, g.V, mx, t, s, [=](float l, int) { return (order_key(l) & mask) == pre; },
+                [=](float l, int) { return (order_key(l) >> shift) & 255u; });
+            if (threadIdx.x == 0) {
+                if (pass == 0) {
+                    uint32_t m = 0u;
+                    for (int q = 0; q < 256; q++) m += s.tc[q];
+                    s.total_c = m;
+                }
+                if (s.total_c > (uint32_t)top_k) scan_buckets(s, true, false, (uint32_t)top_k, 0.0, shift);
+            }
+            __syncthreads();
+            if (s.total_c <= (uint32_t)top_k) {
+                all = true;
+                break;
+            }
+        }
+        if (!all) {
+            const uint32_t key = s.prefix;
+            const uint32_t need = (uint32_t)top_k - s.before_c;
+            const uint32_t ties = s.tc[s.bucket];
+            __syncthreads();
+            cut.key = key;
+            cut.id = need < ties ? select_id(p, g.V, s, key, Cut{0u, INT_MAX}, need) : INT_MAX;
+        }
+    }
+
+    // top-p: the smallest prefix whose cumulative share reaches top_p
+    // (sampling.go:104-113), within the top-k set.
+    if (top_p > 0.0f && top_p < 1.0f) {
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            s.prefix = 0u;
+            s.before_c = 0u;
+            s.before_w = 0.0;
+        }
+        __syncthreads();
+        bool found = true;
+        for (int pass = 0; pass < 4 && found; pass++) {
+            const int shift = 24 - 8 * pass;
+            const uint32_t mask = pass ? ~0u << (shift + 8) : 0u;
+            const uint32_t pre = s.prefix;
+            const Cut ck = cut;
+            hist_pass<true>(
+                p, g.V, mx, t, s,
+                [=](float l, int j) {
+                    const uint32_t k = order_key(l);
+                    return in_cut(k, j, ck) && (k & mask) == pre;
+                },
+                [=](float l, int) { return (order_key(l) >> shift) & 255u; });
+            if (threadIdx.x == 0) {
+                if (pass == 0) {
+                    double w = 0.0;
+                    for (int q = 0; q < 256; q++) w += s.tw[q];
+                    s.total_w = w;
+                }
+                const double tot = s.total_w;
+                if (tot > 0.0 && !isinf(tot))
+                    scan_buckets(s, true, true, 0u, (double)top_p * tot, shift);
+                else
+                    s.bucket = -1;
+            }
+            __syncthreads();
+            found = s.bucket >= 0;
+        }
+        if (found) {
+            // The tie group at the boundary: add its members one by one as the
+            // sampler's running sum does.
+            if (threadIdx.x == 0) {
+                const uint32_t key = s.prefix;
+                const uint32_t ties = s.tc[s.bucket];
+                const double tot = s.total_w;
+                const double wt = exp((double)(key_value(key) - mx) / t);
+                double cum = s.before_w / tot;
+                uint32_t m = ties;
+                for (uint32_t i = 1; i <= ties; i++) {
+                    cum += wt / tot;
+                    if (cum >= (double)top_p) {
+                        m = i;
+                        break;
+                    }
+                }
+                s.before_c = m;  // kept members of the tie group
+                s.total_c = ties;
+            }
+            __syncthreads();
+            const uint32_t key = s.prefix, m = s.before_c, ties = s.total_c;
+            __syncthreads();
+            Cut nc{key, key == cut.key ? cut.id : INT_MAX};
+            if (m < ties) nc.id = select_id(p, g.V, s, key, cut, m);
+            cut = nc;
+        }
+    }
+    if (threadIdx.x == 0) cuts[(uint64_t)b * g.R + row] = cut;
 }
 
 // Philox4x32-10 (Salmon et al., SC'11).
@@ -152,7 +435,7 @@ __device__ __forceinline__ double draw(uint64_t seed, uint64_t step, uint32_t ro
 // weight > 0) whose running weight sum exceeds `target`. Returns -1 when the
 // target lies beyond the chunk's own sum (rounding), with *last the last
 // positive-weight index of the chunk.
-__device__ int scan_chunk(const float *p, const Geo &g, int c, int d, float mx, double inv_t,
+__device__ int scan_chunk(const float *p, const Geo &g, int c, int d, float mx, double t, const Cut &cut,
                           double target, double *shared_prefix, int *shared_pick) {
     const int begin = c * g.L;
     const int end = min(begin + g.L, g.V);
@@ -162,7 +445,7 @@ __device__ int scan_chunk(const float *p, const Geo &g, int c, int d, float mx, 
     const int hi = min(lo + per, end);
     double local = 0.0;
     for (int j = lo; j < hi; j++)
-        if (j != d) local += weight_of(p[j], mx, inv_t);
+        if (j != d) local += weight_of(p[j], j, mx, t, cut);
     shared_prefix[threadIdx.x] = local;
     if (threadIdx.x == 0) *shared_pick = -1;
     __syncthreads();
@@ -179,7 +462,7 @@ __device__ int scan_chunk(const float *p, const Geo &g, int c, int d, float mx, 
     if (run <= target && target < run + local) {
         for (int j = lo; j < hi; j++) {
             if (j == d) continue;
-            const double w = weight_of(p[j], mx, inv_t);
+            const double w = weight_of(p[j], j, mx, t, cut);
             if (w <= 0.0) continue;
             run += w;
             if (target < run) {
@@ -189,7 +472,7 @@ __device__ int scan_chunk(const float *p, const Geo &g, int c, int d, float mx, 
         }
         if (*shared_pick < 0) {  // rounding at the boundary: last positive weight
             for (int j = hi - 1; j >= lo; j--)
-                if (j != d && weight_of(p[j], mx, inv_t) > 0.0) {
+                if (j != d && weight_of(p[j], j, mx, t, cut) > 0.0) {
                     *shared_pick = j;
                     break;
                 }
@@ -202,7 +485,8 @@ __device__ int scan_chunk(const float *p, const Geo &g, int c, int d, float mx, 
 __global__ __launch_bounds__(256) void accept_finalize_kernel(
     const float *__restrict__ logits, Geo g, const int32_t *__restrict__ drafts,
     const Stat *__restrict__ stats, const double *__restrict__ sums,
-    const double *__restrict__ wdraft, int stochastic, double inv_t, uint64_t seed, uint64_t step,
+    const double *__restrict__ wdraft, const Cut *__restrict__ cuts, int stochastic, double t, uint64_t seed,
+    uint64_t step,
     uint32_t request_base, int32_t *__restrict__ result, double *__restrict__ debug,
     const uint64_t *__restrict__ step_dev) {
     const int b = blockIdx.x;
@@ -265,6 +549,11 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
                     decided_next = best.i;
                 }
             } else {
+                // The sampler's first candidate: the maximum over valid logits;
+                // with none valid, argmaxLogit's answer (sampling.go:83-89).
+                Stat sb = row_best_s[row];
+                if (sb.v == -INFINITY) sb = best;
+                best_s = sb;
                 const double *cs = sums + ((uint64_t)b * g.R + row) * g.C;
                 const double rest = row_rest_s[row];
                 const double wd = (row < g.k && d >= 0 && d < g.V) ? wdraft[(uint64_t)b * g.R + row] : 0.0;
@@ -272,14 +561,14 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
                 const bool onehot = !(total > 0.0) || isinf(total);
                 dbg[2] = total;
                 if (row < g.k) {
-                    const double pd = onehot ? (d == best.i ? 1.0 : 0.0) : wd / total;
+                    const double pd = onehot ? (d == sb.i ? 1.0 : 0.0) : wd / total;
                     const double u = draw(seed, step, (uint32_t)row, request, 0);
                     dbg[0] = pd;
                     dbg[1] = u;
                     if (u < pd) {
                         action = 0;
                     } else if (onehot || !(rest > 0.0)) {
-                        decided_next = best.i;
+                        decided_next = sb.i;
                     } else {
                         const double u2 = draw(seed, step, (uint32_t)row, request, 1);
                         const double target = u2 * rest;
@@ -291,12 +580,12 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
                         }
                         target_s = target - run;
                         cstar = c;
-                        mx_s = best.v;
+                        mx_s = sb.v;
                         action = 2;
                     }
                 } else {
                     if (onehot) {
-                        decided_next = best.i;
+                        decided_next = sb.i;
                     } else {
                         const double u2 = draw(seed, step, (uint32_t)row, request, 1);
                         const double target = u2 * total;
@@ -308,7 +597,7 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
                         }
                         target_s = target - run;
                         cstar = c;
-                        mx_s = best.v;
+                        mx_s = sb.v;
                         action = 2;
                     }
                 }
@@ -326,7 +615,7 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
         }
         if (action == 2) {
             const int d = row < g.k ? drafts[(uint64_t)b * g.k + row] : -1;
-            const int j = scan_chunk(p, g, cstar, d, mx_s, inv_t, target_s, prefix, &pick);
+            const int j = scan_chunk(p, g, cstar, d, mx_s, t, row_cut(cuts, g, b, row), target_s, prefix, &pick);
             if (threadIdx.x == 0) decided_next = j >= 0 ? j : best_s.i;
         }
         break;
@@ -362,7 +651,7 @@ Geo make_geo(const yuuka_accept_params &p) {
 uint64_t accept_scratch_bytes(const yuuka_accept_params &p) {
     const Geo g = make_geo(p);
     const uint64_t n = (uint64_t)g.B * g.R * g.C;
-    return n * sizeof(Stat) + n * sizeof(double) + (uint64_t)g.B * g.R * sizeof(double) + 256;
+    return n * sizeof(Stat) + n * sizeof(double) + (uint64_t)g.B * g.R * (sizeof(double) + sizeof(Cut)) + 256;
 }
 
 hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int32_t *result,
@@ -374,14 +663,23 @@ hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int3
     Stat *stats = reinterpret_cast<Stat *>(base);
     double *sums = reinterpret_cast<double *>(base + ((n * sizeof(Stat) + 255) & ~255ull));
     double *wdraft = sums + n;
+    Cut *cuts = reinterpret_cast<Cut *>(wdraft + (uint64_t)g.B * g.R);
     const bool stochastic = p.mode == YUUKA_ACCEPT_STOCHASTIC && p.temperature > 0.0f && p.top_k != 1;
-    const double inv_t = stochastic ? 1.0 / (double)p.temperature : 0.0;
+    const double t = stochastic ? (double)p.temperature : 1.0;
+    // top_p 0 means off (sampling.go:46-48); top_k at or above the vocabulary keeps everything.
+    const bool top_k_on = p.top_k > 1 && p.top_k < p.vocab;
+    const bool top_p_on = p.top_p > 0.0f && p.top_p < 1.0f;
+    const bool truncate = stochastic && (top_k_on || top_p_on);
     const dim3 grid((unsigned)g.C, (unsigned)g.R, (unsigned)g.B);
     accept_stats_kernel<<<grid, 256, 0, stream>>>(logits, g, stats);
+    if (truncate)
+        accept_select_kernel<<<dim3((unsigned)g.R, (unsigned)g.B), kSelWaves * 64, 0, stream>>>(
+            logits, g, stats, top_k_on ? (int)p.top_k : 0, top_p_on ? p.top_p : 1.0f, t, cuts);
+    const Cut *cut_arg = truncate ? cuts : nullptr;
     if (stochastic)
-        accept_weights_kernel<<<grid, 256, 0, stream>>>(logits, g, drafts, stats, inv_t, sums, wdraft);
-    accept_finalize_kernel<<<(unsigned)g.B, 256, 0, stream>>>(logits, g, drafts, stats, sums, wdraft,
-                                                             stochastic ? 1 : 0, inv_t, p.seed, p.step,
+        accept_weights_kernel<<<grid, 256, 0, stream>>>(logits, g, drafts, stats, cut_arg, t, sums, wdraft);
+    accept_finalize_kernel<<<(unsigned)g.B, 256, 0, stream>>>(logits, g, drafts, stats, sums, wdraft, cut_arg,
+                                                             stochastic ? 1 : 0, t, p.seed, p.step,
                                                              p.request_base, result, debug, step_dev);
     return hipGetLastError();
 }

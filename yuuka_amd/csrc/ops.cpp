@@ -379,8 +379,8 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         if ((p.mode != YUUKA_ACCEPT_GREEDY && p.mode != YUUKA_ACCEPT_STOCHASTIC) || !p.batch || !p.vocab ||
             p.drafts > 255)
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid ACCEPT parameters");
-        if (p.mode == YUUKA_ACCEPT_STOCHASTIC && op.f[0] > 0.0f && op.u[1] != 1 && (op.u[1] > 1 || op.f[1] < 1.0f))
-            return fail(YUUKA_ERR_UNSUPPORTED, "top-k/top-p truncation is not implemented");
+        if (p.mode == YUUKA_ACCEPT_STOCHASTIC && !(op.f[1] >= 0.0f && op.f[1] <= 1.0f))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "ACCEPT: top-p must be in [0,1]");
         const uint64_t stride = p.row_stride ? p.row_stride : p.vocab;
         const uint64_t rows = (uint64_t)p.batch * (p.drafts + 1);
         if (!buf_ok(op.buf[0], op.off[0], ((rows - 1) * stride + p.vocab) * 4) ||
