@@ -270,7 +270,8 @@ YUUKA_API yuuka_status yuuka_gemv_batch(yuuka_stream * stream, yuuka_buffer * ou
 /* Plan and graph API (reference :477-496). Supported op codes: LM_HEAD,
  * GEMV_BATCH (Q4_K/Q6_K), RMSNORM_BATCH, RMSNORM_HEADS_BATCH, ROPE_BATCH,
  * EMBEDDING_BATCH, KV_WRITE_BATCH_PAGED, ATTENTION_PREFILL_PAGED,
- * RECURRENT_CHUNK, ADD, SILU_MUL, COPY, plus the YUUKA_EXT_OP_* codes. The
+ * RECURRENT_CHUNK, ADD, SILU_MUL, COPY, MOE_ROUTE, MOE_GATE_UP, MOE_DOWN,
+ * MOE_REDUCE_ADD (experts in Q4_K), plus the YUUKA_EXT_OP_* codes. The
  * v10 buffer layouts of the reference header (:336-476) are honoured.
  * Other codes are rejected with YUUKA_ERR_UNSUPPORTED and not appended. */
 YUUKA_API yuuka_status yuuka_graph_create(yuuka_plan * plan, yuuka_stream * stream,
@@ -408,6 +409,22 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
  *               rows, displacement}; u={block_size, capacity, kv dtype (F32 or
  *               F16), rot_dim}; f={scale, eps}. Writes the rows' K/V to the
  *               pool at position + displacement + row.
+ *   MOE_ROUTER: FP32 router of the MoE FFN (ffn_gate_inp, forward.go:328):
+ *               buf0 FP32 y [rows][hidden], buf1 FP32 router weight
+ *               [experts][hidden], buf2 FP32 logits [rows][experts];
+ *               optional buf3 FP32 shared-expert gate vector [hidden]
+ *               (ffn_gate_inp_shexp) with buf4 FP32 [rows] receiving its
+ *               dot product (before the sigmoid); n={hidden, experts, rows}.
+ *   MOE_COMBINE: MOE_REDUCE_ADD plus the shared expert (forward.go:336-388):
+ *               buf0 x [rows][hidden] += sum_slot w * expert_out +
+ *               sigmoid(buf4[row]) * buf3[row]; buf1 expert_out
+ *               [rows*used][hidden], buf2 weights [rows][used], optional
+ *               buf3 shared expert output [rows][hidden] and buf4 its gate
+ *               logit [rows]; n={hidden, rows, used}.
+ * The v10 MoE ops (MOE_ROUTE, MOE_GATE_UP, MOE_DOWN, MOE_REDUCE_ADD) keep
+ * the layouts above; experts are served in Q4_K. The route op fills the
+ * assignment bins in (row, slot) order and writes every count, so it needs
+ * no memset and is deterministic.
  * YUUKA_EXT_FLAG_DEFER on RECURRENT_CHUNK: compute the outputs of every row
  * but leave both states untouched (verify mode; see GDN_COMMIT). */
 #define YUUKA_EXT_OP_QUANTIZE_X 64u
@@ -418,6 +435,8 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
 #define YUUKA_EXT_OP_GEMM_FUSED 69u
 #define YUUKA_EXT_OP_ROPE_TABLE 70u
 #define YUUKA_EXT_OP_ATTN_VERIFY 71u
+#define YUUKA_EXT_OP_MOE_ROUTER 72u
+#define YUUKA_EXT_OP_MOE_COMBINE 73u
 #define YUUKA_EXT_FLAG_DEFER 0x100u
 /* With YUUKA_EXT_FLAG_DEFER: buf10 receives the raw per-head scan outputs;
  * the gated RMSNorm is left to the consumer (GEMM_FUSED gated head norm). */
@@ -426,6 +445,9 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
  * exp(softplus(alpha + dt) * a) and the beta buffer sigmoid(beta) (the
  * GEMM_FUSED output maps 3 and 2 produce them). */
 #define YUUKA_EXT_FLAG_GDN_COEF 0x400u
+/* On MOE_GATE_UP: buf6 receives SiLU(gate) * up (forward.go:348-351) and
+ * buf7 is not written (may be null). */
+#define YUUKA_EXT_FLAG_MOE_SWIGLU 0x800u
 
 /* Timing events (extension): an event created with timing enabled, recorded
  * on a stream, and the elapsed milliseconds between two recorded events. */

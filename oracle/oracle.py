@@ -120,6 +120,15 @@ def silu_mul(g: np.ndarray, u: np.ndarray) -> np.ndarray:
     return np.array([f(float(a)) for a in g.ravel()], np.float32).reshape(g.shape) * u.astype(np.float32)
 
 
+def select_experts(logits: np.ndarray, used: int):
+    """forward.go:393-439 selectExperts: (ids, float32 weights)."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    ids = np.zeros(used, np.int32)
+    w = np.zeros(used, np.float32)
+    lib().orc_select_experts(_ptr(logits), logits.size, used, _ptr(ids), _ptr(w))
+    return ids, w
+
+
 def argmax(logits: np.ndarray) -> int:
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     return int(lib().orc_argmax(_ptr(logits), logits.size))

@@ -417,3 +417,31 @@ def test_rmsnorm_and_rope_closed_forms():
     assert np.array_equal(v[:, 8:], v0[:, 8:])  # beyond rot_dim untouched
     assert abs(O.lib().orc_softplus(0.0) - math.log(2)) < 1e-7
     assert O.lib().orc_softplus(25.0) == 25.0
+
+
+# ------------------------------------------------------------ MoE routing
+
+def test_select_experts_against_sorting():
+    """forward.go:393-439: the repeated strict-greater scan equals a stable
+    sort by descending logit (lower index first on ties); the weights are the
+    softmax over the selected logits."""
+    rng = np.random.default_rng(4)
+    for trial in range(50):
+        E, used = int(rng.integers(1, 40)), 0
+        used = int(rng.integers(1, E + 1))
+        logits = rng.integers(-3, 4, E).astype(np.float32) if trial % 2 else rng.normal(0, 1, E).astype(np.float32)
+        ids, w = O.select_experts(logits, used)
+        order = np.lexsort((np.arange(E), -logits.astype(np.float64)))[:used]
+        assert ids.tolist() == order.tolist()
+        sel = logits[order].astype(np.float64)
+        p = np.exp(sel - sel.max())
+        np.testing.assert_allclose(w, p / p.sum(), rtol=1e-6)
+        assert abs(float(w.sum()) - 1.0) < 1e-5
+
+
+def test_select_experts_nan_and_more_slots_than_experts():
+    logits = np.array([np.nan, 1.0, 2.0, np.nan], np.float32)
+    ids, _ = O.select_experts(logits, 2)
+    assert ids.tolist() == [0, 2]          # a NaN first candidate is never replaced
+    ids, _ = O.select_experts(np.array([1.0, 3.0], np.float32), 2)
+    assert ids.tolist() == [1, 0]

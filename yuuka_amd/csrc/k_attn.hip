@@ -120,9 +120,10 @@ __device__ __forceinline__ void norm_rope_wave(const float *__restrict__ src, co
         y1 = dst[lane + half];
     }
     if (lane < half) {
+#pragma clang fp contract(off)  // float32 products and sums rounded separately, as the reference
         const float c = cs[lane].x, s = cs[lane].y;
-        dst[lane] = __fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, s));
-        dst[lane + half] = __fadd_rn(__fmul_rn(y0, s), __fmul_rn(y1, c));
+        dst[lane] = y0 * c - y1 * s;
+        dst[lane + half] = y0 * s + y1 * c;
     }
 }
 
@@ -387,14 +388,14 @@ __device__ __forceinline__ void norm_rope4(const float *__restrict__ src, const 
 #pragma unroll
     for (int i = 0; i < 4; i++) pr[i] = dpp_f<0x128>(y[i]);  // partner lane (l + 8) % 16 of the row
     if (lane < 16) {
+#pragma clang fp contract(off)  // float32 products and sums rounded separately, as the reference
         const bool first = lane < 8;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int e = 4 * lane + i, pi = first ? e : e - 32;
             const float c = cs[pi].x, sn = cs[pi].y;
             // first half: y0 c - y1 s; second half: y0 s + y1 c (y0 = element pi)
-            y[i] = first ? __fsub_rn(__fmul_rn(y[i], c), __fmul_rn(pr[i], sn))
-                         : __fadd_rn(__fmul_rn(pr[i], sn), __fmul_rn(y[i], c));
+            y[i] = first ? y[i] * c - pr[i] * sn : pr[i] * sn + y[i] * c;
         }
     }
 }

@@ -17,8 +17,9 @@
 // state and writes it back, and moves the conv state window forward — the
 // scan and the conv-state update of one head in one workgroup.
 //
-// Arithmetic is the reference's: float32 with separately rounded products
-// and sums in the reference's order per element, float64 where the
+// Arithmetic follows the reference's order per element in float32 (the
+// compiler may fuse a product into the following sum as one FMA, which
+// rounds once where the reference rounds twice), float64 where the
 // reference converts (norm sums, exp, log1p). Cross-thread sums add partials
 // of 32 state rows in a fixed order.
 #include <hip/hip_runtime.h>

@@ -104,4 +104,25 @@ hipError_t launch_gdn_conv_commit(float *conv_state, const float *qkv, const Gdn
 hipError_t launch_advance(const ModelDyn &dyn, const int32_t *accept_result, int rows, uint64_t *step,
                           hipStream_t s);
 
+// Mixture of experts (k_moe.hip). Assignment layout of the reference's MoE
+// plan ops: counts [E], assignment arrays [E][rows*used] in (row, slot) order.
+struct MoeGemm {
+    const float *x;           // activations [.][K]
+    const void *w0, *w1;      // expert-stacked Q4_K matrices [E*N rows of K]; w1 optional
+    uint64_t row_bytes;
+    const int32_t *counts, *arows, *aslots;
+    int rows, used, experts, K, N;
+    int by_slot;              // activation row = row*used + slot (down), else row (gate/up)
+    int swiglu;               // out0 = SiLU(W0 y) * (W1 y)
+    float *out0, *out1;       // [rows*used][N]
+};
+uint32_t moe_gemm_lds(int K);
+hipError_t launch_moe_router(const float *y, int H, int rows, const float *w, int E, float *logits, const float *sv,
+                             float *extra, hipStream_t s);
+hipError_t launch_moe_route(const float *logits, int rows, int E, int used, int32_t *ids, float *weights,
+                            int32_t *counts, int32_t *arows, int32_t *aslots, float *aweights, hipStream_t s);
+hipError_t launch_moe_gemm(const MoeGemm &g, hipStream_t s);
+hipError_t launch_moe_combine(float *x, const float *eo, const float *w, int rows, int used, int H, const float *so,
+                              const float *sg, hipStream_t s);
+
 }  // namespace yk

@@ -398,6 +398,72 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
             if (!op.buf[i]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "GDN commit buffer %d is null", i);
         return YUUKA_OK;
     }
+    case YUUKA_OP_MOE_ROUTE: {  // hip.go:1585-1608: n={rows, experts, used}
+        const uint64_t rows = op.n[0], E = op.n[1], used = op.n[2];
+        if (!rows || !E || !used || used > E || E > (1u << 20) || rows * used > 8192)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid MoE route dimensions");
+        const uint64_t a = E * rows * used * 4;
+        if (!buf_ok(op.buf[0], op.off[0], rows * E * 4) || !buf_ok(op.buf[1], op.off[1], rows * used * 4) ||
+            !buf_ok(op.buf[2], op.off[2], rows * used * 4) || !buf_ok(op.buf[3], op.off[3], E * 4) ||
+            !buf_ok(op.buf[4], op.off[4], a) || !buf_ok(op.buf[5], op.off[5], a) || !buf_ok(op.buf[6], op.off[6], a))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE route buffers too small");
+        for (int i = 0; i < 7; i++)
+            if (op.off[i] % 4) return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE route buffer %d misaligned", i);
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_MOE_GATE_UP:    // hip.go:1610-1642: n={hidden, ffn, rows, experts, used}
+    case YUUKA_OP_MOE_DOWN: {     // hip.go:1644-1670: n={ffn, hidden, rows, experts, used}
+        const bool gu = op.code == YUUKA_OP_MOE_GATE_UP;
+        const uint64_t K = op.n[0], N = op.n[1], rows = op.n[2], E = op.n[3], used = op.n[4];
+        if (!K || !N || !rows || !E || !used || used > E)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid MoE %s dimensions", gu ? "gate/up" : "down");
+        if (op.u[0] != YUUKA_DTYPE_Q4_K)
+            return fail(YUUKA_ERR_UNSUPPORTED, "MoE expert dtype %u (Q4_K is served)", op.u[0]);
+        if (K % 256 || N % 16 || K > 8192)
+            return fail(YUUKA_ERR_UNSUPPORTED, "MoE expert shape %llu x %llu", (unsigned long long)N,
+                        (unsigned long long)K);
+        const uint64_t rb = row_bytes(op.u[0], K), wb = E * N * rb, a = E * rows * used * 4;
+        const uint64_t x_rows = gu ? rows : rows * used;
+        const bool swiglu = gu && (op.flags & YUUKA_EXT_FLAG_MOE_SWIGLU);
+        const int ib = gu ? 3 : 2;  // counts, assign_rows, assign_slots, out...
+        bool ok = buf_ok(op.buf[0], op.off[0], x_rows * K * 4) && buf_ok(op.buf[1], op.off[1], wb) &&
+                  (!gu || buf_ok(op.buf[2], op.off[2], wb)) && buf_ok(op.buf[ib], op.off[ib], E * 4) &&
+                  buf_ok(op.buf[ib + 1], op.off[ib + 1], a) && buf_ok(op.buf[ib + 2], op.off[ib + 2], a) &&
+                  buf_ok(op.buf[ib + 3], op.off[ib + 3], rows * used * N * 4) &&
+                  (!gu || swiglu || buf_ok(op.buf[ib + 4], op.off[ib + 4], rows * used * N * 4));
+        if (!ok) return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE %s buffers too small", gu ? "gate/up" : "down");
+        if (op.off[0] % 16 || op.off[1] % 16 || (gu && op.off[2] % 16))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE activations and weights must be 16-byte aligned");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_MOE_REDUCE_ADD: {  // hip.go:1672-1690: n={hidden, rows, used}
+        const uint64_t H = op.n[0], rows = op.n[1], used = op.n[2];
+        if (!H || !rows || !used) return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid MoE reduce dimensions");
+        if (!buf_ok(op.buf[0], op.off[0], rows * H * 4) || !buf_ok(op.buf[1], op.off[1], rows * used * H * 4) ||
+            !buf_ok(op.buf[2], op.off[2], rows * used * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE reduce buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_EXT_OP_MOE_ROUTER: {
+        const uint64_t H = op.n[0], E = op.n[1], rows = op.n[2];
+        if (!H || !E || !rows || H % 4) return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid MoE router dimensions");
+        if (!buf_ok(op.buf[0], op.off[0], rows * H * 4) || !buf_ok(op.buf[1], op.off[1], E * H * 4) ||
+            !buf_ok(op.buf[2], op.off[2], rows * E * 4) ||
+            (op.buf[3] && (!buf_ok(op.buf[3], op.off[3], H * 4) || !buf_ok(op.buf[4], op.off[4], rows * 4))))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE router buffers too small");
+        if (op.off[0] % 16 || op.off[1] % 16 || (op.buf[3] && op.off[3] % 16))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE router inputs must be 16-byte aligned");
+        return YUUKA_OK;
+    }
+    case YUUKA_EXT_OP_MOE_COMBINE: {
+        const uint64_t H = op.n[0], rows = op.n[1], used = op.n[2];
+        if (!H || !rows || !used) return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid MoE combine dimensions");
+        if (!buf_ok(op.buf[0], op.off[0], rows * H * 4) || !buf_ok(op.buf[1], op.off[1], rows * used * H * 4) ||
+            !buf_ok(op.buf[2], op.off[2], rows * used * 4) ||
+            (op.buf[3] && (!buf_ok(op.buf[3], op.off[3], rows * H * 4) || !buf_ok(op.buf[4], op.off[4], rows * 4))))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE combine buffers too small");
+        return YUUKA_OK;
+    }
     case YUUKA_EXT_OP_ADVANCE:
         if (!op.buf[0] || op.buf[0]->bytes < 8 || !op.buf[1] || op.n[0] == 0)
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid ADVANCE buffers");
@@ -568,6 +634,47 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
         if (err == hipSuccess) err = launch_gdn_conv_commit(at<float>(op, 0), at<const float>(op, 2), g, res, s);
         break;
     }
+    case YUUKA_OP_MOE_ROUTE:
+        err = launch_moe_route(at<const float>(op, 0), (int)op.n[0], (int)op.n[1], (int)op.n[2], at<int32_t>(op, 1),
+                               at<float>(op, 2), at<int32_t>(op, 3), at<int32_t>(op, 4), at<int32_t>(op, 5),
+                               at<float>(op, 6), s);
+        break;
+    case YUUKA_OP_MOE_GATE_UP:
+    case YUUKA_OP_MOE_DOWN: {
+        const bool gu = op.code == YUUKA_OP_MOE_GATE_UP;
+        const int ib = gu ? 3 : 2;
+        MoeGemm g{};
+        g.x = at<const float>(op, 0);
+        g.w0 = at<const void>(op, 1);
+        g.w1 = gu ? at<const void>(op, 2) : nullptr;
+        g.row_bytes = row_bytes(op.u[0], op.n[0]);
+        g.counts = at<const int32_t>(op, ib);
+        g.arows = at<const int32_t>(op, ib + 1);
+        g.aslots = at<const int32_t>(op, ib + 2);
+        g.K = (int)op.n[0];
+        g.N = (int)op.n[1];
+        g.rows = (int)op.n[2];
+        g.experts = (int)op.n[3];
+        g.used = (int)op.n[4];
+        g.by_slot = gu ? 0 : 1;
+        g.swiglu = gu && (op.flags & YUUKA_EXT_FLAG_MOE_SWIGLU) ? 1 : 0;
+        g.out0 = at<float>(op, ib + 3);
+        g.out1 = gu ? at<float>(op, ib + 4) : nullptr;
+        err = launch_moe_gemm(g, s);
+        break;
+    }
+    case YUUKA_OP_MOE_REDUCE_ADD:
+        err = launch_moe_combine(at<float>(op, 0), at<const float>(op, 1), at<const float>(op, 2), (int)op.n[1],
+                                 (int)op.n[2], (int)op.n[0], nullptr, nullptr, s);
+        break;
+    case YUUKA_EXT_OP_MOE_ROUTER:
+        err = launch_moe_router(at<const float>(op, 0), (int)op.n[0], (int)op.n[2], at<const float>(op, 1),
+                                (int)op.n[1], at<float>(op, 2), at<const float>(op, 3), at<float>(op, 4), s);
+        break;
+    case YUUKA_EXT_OP_MOE_COMBINE:
+        err = launch_moe_combine(at<float>(op, 0), at<const float>(op, 1), at<const float>(op, 2), (int)op.n[1],
+                                 (int)op.n[2], (int)op.n[0], at<const float>(op, 3), at<const float>(op, 4), s);
+        break;
     case YUUKA_EXT_OP_ADVANCE: {
         ModelDyn d{static_cast<int32_t *>(op.buf[0]->ptr) + 1, 0};
         err = launch_advance(d, at<const int32_t>(op, 1), (int)op.n[0], at<uint64_t>(op, 2), s);

@@ -25,8 +25,10 @@ F32, F16, Q4_0, Q5_0, Q8_0, Q4_K, Q5_K, Q6_K = 0, 1, 2, 6, 8, 12, 13, 14
 OP = dict(
     SILU_MUL=9, ADD=10, COPY=11, GEMV_BATCH=17, RMSNORM_BATCH=18, RMSNORM_HEADS_BATCH=19,
     ROPE_BATCH=20, RECURRENT_CHUNK=23, EMBEDDING_BATCH=24, KV_WRITE_BATCH_PAGED=28,
-    ATTENTION_PREFILL_PAGED=29, LM_HEAD=37, GEMM_FUSED=69,
+    ATTENTION_PREFILL_PAGED=29, MOE_ROUTE=30, MOE_GATE_UP=31, MOE_DOWN=32, MOE_REDUCE_ADD=33, LM_HEAD=37,
+    GEMM_FUSED=69, MOE_ROUTER=72, MOE_COMBINE=73,
 )
+FLAG_MOE_SWIGLU = 0x800
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
 FLAG_TAIL = 0x1
 
