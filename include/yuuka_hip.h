@@ -368,8 +368,13 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
  *   ACCEPT:     buf0 logits, buf1 int32 drafts, buf2 int32 result [batch][4],
  *               optional buf3 FP64 debug, optional buf4 uint64 step counter
  *               (else n[5] is the step); n={batch, drafts, vocab, row_stride,
- *               seed, step}; u0 mode, u1 top_k, u2 request_base;
- *               f0 temperature, f1 top_p (yuuka_verify_accept semantics)
+ *               seed, step}; u0 mode, u1 top_k, u2 request_base, u3 drafts
+ *               row stride in int32 (0 = drafts); f0 temperature, f1 top_p
+ *               (yuuka_verify_accept semantics). Optional buf5 int32 [batch]
+ *               forced acceptance lengths (benchmark configurations that
+ *               prescribe the accept length): draft i of request b is
+ *               accepted iff i < buf5[b], and next is the mode's token at
+ *               the first rejected row (or row k).
  *   GDN_COMMIT: buf0 conv_state, buf1 matrix state, buf2 raw qkv rows,
  *               buf3 conv outputs (RECURRENT_CHUNK buf11), buf4 alpha,
  *               buf5 beta, buf6 dt, buf7 a, buf8 int32 acceptance result;
@@ -445,6 +450,10 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
  * exp(softplus(alpha + dt) * a) and the beta buffer sigmoid(beta) (the
  * GEMM_FUSED output maps 3 and 2 produce them). */
 #define YUUKA_EXT_FLAG_GDN_COEF 0x400u
+/* On ROPE_TABLE and ATTN_VERIFY: buf15 holds the op's own {token,
+ * position} int32 pair (a request of a batched plan) instead of the plan's
+ * dynamic buffer. */
+#define YUUKA_EXT_FLAG_OWN_POS 0x1000u
 /* On MOE_GATE_UP: buf6 receives SiLU(gate) * up (forward.go:348-351) and
  * buf7 is not written (may be null). */
 #define YUUKA_EXT_FLAG_MOE_SWIGLU 0x800u
@@ -486,10 +495,15 @@ typedef struct yuuka_q35_config {
     int32_t conv_kernel, state_size, groups, rank, inner, full_interval;
     double rope_base;
     float eps;
-    int32_t capacity;    /* tokens of context */
+    int32_t capacity;    /* tokens of context per request */
     int32_t block_size;  /* paged KV block (16) */
     uint32_t kv_dtype;   /* YUUKA_DTYPE_F16 (reference default) or F32 */
-    int32_t max_rows;    /* largest row block of one step (<= 16) */
+    int32_t max_rows;    /* largest row block of one request in one step (<= 32) */
+    int32_t batch;       /* concurrent requests (0 means 1) */
+    int32_t kv_blocks;   /* blocks of the KV pool the requests share (0: every
+                            request can hold its whole capacity) */
+    /* qwen35moe FFN (config.go MoE fields; n_experts 0 = dense FFN) */
+    int32_t n_experts, n_experts_used, expert_ffn, shared_ffn;
 } yuuka_q35_config;
 
 typedef struct yuuka_q35_tensor {
@@ -512,6 +526,13 @@ typedef struct yuuka_q35_layer_weights {
     const float * q_norm;
     const float * k_norm;
     yuuka_q35_tensor ffn_gate, ffn_up, ffn_down;
+    /* MoE FFN (load.go ffn_gate_inp, ffn_gate_inp_shexp, *_shexp, *_exps):
+     * router [experts][hidden] FP32, shared-expert gate vector [hidden],
+     * shared expert SwiGLU, experts stacked by rows ([experts*ffn][hidden]
+     * for gate/up, [experts*hidden][ffn] for down), Q4_K. */
+    yuuka_q35_tensor router;
+    const float * shared_gate_vec;
+    yuuka_q35_tensor shared_gate, shared_up, shared_down, gate_exps, up_exps, down_exps;
 } yuuka_q35_layer_weights;
 
 typedef struct yuuka_q35_weights {
@@ -553,6 +574,33 @@ YUUKA_API yuuka_status yuuka_q35_logits(yuuka_q35 * q, float * out, int32_t rows
 YUUKA_API uint64_t yuuka_q35_snapshot_bytes(const yuuka_q35 * q);
 YUUKA_API yuuka_status yuuka_q35_snapshot(yuuka_q35 * q, void * out, int32_t * position);
 YUUKA_API yuuka_status yuuka_q35_restore(yuuka_q35 * q, const void * data, uint64_t bytes, int32_t position);
+
+/* Batched engine (cfg.batch requests). Each request has its own position,
+ * recurrent state and KV block table over a shared pool with reference
+ * counts (memory/memory.go Table, memory/prefix.go sharing). The functions
+ * above act on request 0. */
+YUUKA_API int32_t yuuka_q35_request_position(const yuuka_q35 * q, int32_t request);
+/* Clears one request's recurrent state and position and returns its KV
+ * blocks to the pool (a block is reused once no table references it). */
+YUUKA_API yuuka_status yuuka_q35_reset_request(yuuka_q35 * q, int32_t request);
+/* Prefill of one request (yuuka_q35_prefill semantics). */
+YUUKA_API yuuka_status yuuka_q35_prefill_request(yuuka_q35 * q, int32_t request, const int32_t * tokens,
+                                                 int32_t n, float * last_logits);
+/* Prefix sharing: request dst takes request src's prefix (its position,
+ * recurrent state and the KV blocks of its full blocks, shared by
+ * reference; a partial last block is copied). dst is reset first. */
+YUUKA_API yuuka_status yuuka_q35_fork(yuuka_q35 * q, int32_t src, int32_t dst);
+/* One step over requests 0..n_req-1 with `rows` tokens each (tokens
+ * [n_req][rows]). mode 0: verify (k = rows-1 drafts per request, fused
+ * acceptance per request with Philox request index = request, commit of
+ * each request's accepted prefix); forced (may be NULL) gives per-request
+ * acceptance lengths that replace the accept test (benchmark settings).
+ * mode 1: prefill (every row committed). result [n_req][4] as
+ * yuuka_q35_verify (mode 1: {rows-1, -1, argmax of the last row... } is
+ * not defined; pass NULL). */
+YUUKA_API yuuka_status yuuka_q35_step_batch(yuuka_q35 * q, int32_t n_req, const int32_t * tokens, int32_t rows,
+                                            int32_t mode, const yuuka_q35_accept * accept,
+                                            const int32_t * forced, int32_t * result);
 
 /* engine/speculative.go:13-34 options and :48-49 counters. */
 typedef struct yuuka_q35_generate_opts {

@@ -267,6 +267,8 @@ class Q35:
         for n in ("n_layers", "hidden", "ffn", "heads", "kv_heads", "head_dim", "rope_dim", "vocab",
                   "conv_kernel", "state_size", "groups", "rank", "full_interval"):
             setattr(c, n, getattr(cfg, n))
+        for n in ("n_experts", "n_experts_used", "expert_ffn", "shared_ffn"):
+            setattr(c, n, getattr(cfg, n, 0))
         c.inner = cfg.inner
         c.rope_base = cfg.rope_base
         c.eps = cfg.eps
@@ -276,9 +278,10 @@ class Q35:
             s = self.layers[i]
             s.attn_norm = Lw["attn_norm"].ctypes.data_as(_FP)
             s.post_norm = Lw["post_norm"].ctypes.data_as(_FP)
-            for n in ("qkv", "gate", "out", "beta", "alpha", "q", "k", "v", "o", "ffn_gate", "ffn_up", "ffn_down"):
+            for n in ("qkv", "gate", "out", "beta", "alpha", "q", "k", "v", "o", "ffn_gate", "ffn_up", "ffn_down",
+                      "router", "shared_gate", "shared_up", "shared_down", "gate_exps", "up_exps", "down_exps"):
                 setattr(s, n, _mat(Lw.get(n)))
-            for n in ("conv", "dt", "a", "ssm_norm", "q_norm", "k_norm"):
+            for n in ("conv", "dt", "a", "ssm_norm", "q_norm", "k_norm", "shared_gate_vec"):
                 if n in Lw:
                     setattr(s, n, Lw[n].ctypes.data_as(_FP))
         self.model = orc_q35_model(c, _mat(weights["embedding"]), _mat(weights["output"]),

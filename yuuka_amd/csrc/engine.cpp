@@ -1,17 +1,24 @@
-// engine.cpp — qwen35 verify engine: the host side of the speculative verify
-// path, in C++ over this library's own plan API.
+// engine.cpp — qwen35 / qwen35moe verify engine: the host side of the
+// speculative verify path, in C++ over this library's own plan API.
 //
 // Counterparts in the reference: engine/gpu/runtime.go + session.go (weights
 // and per-request state on the device, PrefillLogits, Snapshot/Restore),
-// engine/gpu/plan.go:569-988 (buildPrefillPlan and the per-layer blocks) and
-// engine/speculative.go:68-261 (generateSpeculative). Differences by design:
-//  * the verify plan covers k+1 rows {pending token, d1..dk}, ends with the
-//    fused acceptance and commits only the accepted prefix of the recurrent
-//    state on the device (GDN_COMMIT), then advances the device position, so
-//    no snapshot / restore / replay crosses PCIe per step;
-//  * every plan is captured once per row count into a HIP graph.
+// engine/gpu/plan.go:569-988 (buildPrefillPlan and the per-layer blocks),
+// model/qwen35/forward.go:320-439 (the MoE FFN), memory/memory.go and
+// memory/prefix.go (paged KV tables over a shared pool, prefix sharing by
+// reference count) and engine/speculative.go:68-261 (generateSpeculative).
+// Differences by design:
+//  * a step covers the k+1 rows {pending token, d1..dk} of every active
+//    request; the dense projections run over all rows at once, attention and
+//    the recurrent scan per request (own position, block table and state);
+//  * the step ends with the fused acceptance of every request and commits
+//    only each request's accepted prefix of the recurrent state on the
+//    device (GDN_COMMIT), then advances the device positions, so no
+//    snapshot / restore / replay crosses PCIe per step;
+//  * every plan is captured once per (requests, rows, mode) into a HIP graph.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstring>
@@ -19,6 +26,7 @@
 #include <memory>
 #include <new>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "internal.h"
@@ -28,10 +36,8 @@ namespace {
 
 using yk::fail;
 
-struct DevBuf {
-    yuuka_buffer *b = nullptr;
-    ~DevBuf() { yuuka_buffer_free(b); }
-};
+constexpr int kRowBlock = 16;   // rows of one fused GEMM launch
+constexpr int kAttnRows = 8;    // query rows of one verify-attention launch (MFMA path)
 
 struct Tensor {
     yuuka_buffer *b = nullptr;
@@ -41,20 +47,31 @@ struct Tensor {
 
 struct Layer {
     bool recurrent = false;
+    bool moe = false;
     yuuka_buffer *attn_norm = nullptr, *post_norm = nullptr;
     Tensor qkv, gate, out, beta, alpha, q, k, v, o, ffn_gate, ffn_up, ffn_down;
+    Tensor router, shared_gate, shared_up, shared_down, gate_exps, up_exps, down_exps;
+    yuuka_buffer *shared_gate_vec = nullptr;
     yuuka_buffer *conv = nullptr, *dt = nullptr, *a = nullptr, *ssm_norm = nullptr, *q_norm = nullptr,
                  *k_norm = nullptr;
     yuuka_buffer *dt_a = nullptr;  // {dt[rank], a[rank]}: decay parameters of the projection epilogue
-    // per-request state
-    yuuka_buffer *conv_state = nullptr, *mat_state = nullptr, *kpool = nullptr, *vpool = nullptr;
-    // per-step saved inputs of the recurrent block (read by GDN_COMMIT)
+    // per-request state, request-major: [batch][...]
+    yuuka_buffer *conv_state = nullptr, *mat_state = nullptr;
+    uint64_t conv_bytes = 0, mat_bytes = 0;  // one request's slice
+    // KV pool shared by the requests (attention layers)
+    yuuka_buffer *kpool = nullptr, *vpool = nullptr;
+    // per-step saved inputs of the recurrent block (read by GDN_COMMIT), [rows][...]
     yuuka_buffer *qkv_rows = nullptr, *conv_rows = nullptr, *alpha_rows = nullptr, *beta_rows = nullptr;
 };
 
 struct Graphs {
     yuuka_plan *plan = nullptr;
     yuuka_graph *graph = nullptr;
+};
+
+struct Request {
+    std::vector<int32_t> blocks;  // table entries in use
+    int32_t pos = 0;              // host mirror of the device position
 };
 
 }  // namespace
@@ -64,27 +81,45 @@ struct yuuka_q35 {
     yuuka_stream *stream = nullptr;
     yuuka_q35_config cfg{};
     int conv_dim = 0;
+    int B = 1;           // requests
+    int MR = 16;         // rows per request
+    int M = 16;          // B * MR rows of the activation buffers
+    int max_blocks = 0;  // table entries per request
     std::vector<yuuka_buffer *> owned;
     std::vector<Layer> layers;
     Tensor embedding, output;
     yuuka_buffer *output_norm = nullptr;
-    // activations [max_rows][...]
+    // activations [M][...]
     yuuka_buffer *x = nullptr, *xn = nullptr, *xq = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
                  *attn = nullptr, *z = nullptr, *gdn_out = nullptr, *fg = nullptr, *fu = nullptr, *logits = nullptr,
-                 *tokens = nullptr, *result = nullptr, *dyn = nullptr, *step = nullptr, *table = nullptr,
                  *rope = nullptr;
-    int32_t *pinned = nullptr;  // tokens staging {tokens[16], result[4]}
+    // MoE scratch
+    yuuka_buffer *moe_logits = nullptr, *moe_sg = nullptr, *moe_ids = nullptr, *moe_w = nullptr,
+                 *moe_counts = nullptr, *moe_arows = nullptr, *moe_aslots = nullptr, *moe_aw = nullptr,
+                 *moe_act = nullptr, *moe_eo = nullptr, *moe_sfg = nullptr, *moe_so = nullptr;
+    // step I/O and per-request device state
+    yuuka_buffer *tokens = nullptr, *result = nullptr, *dyn = nullptr, *step = nullptr, *table = nullptr,
+                 *forced = nullptr;
+    int32_t *pinned = nullptr;  // staging {tokens[M], result[4B], forced[B]}
     hipEvent_t ev0 = nullptr, ev1 = nullptr;  // around the last graph replay
     bool eager = false;  // YUUKA_Q35_EAGER=1: launch plans op by op (profilers), no graphs
     float last_ms = 0.0f;
-    // plans keyed by (rows, mode): mode 0 verify greedy/stochastic, 1 commit-all
-    std::map<std::pair<int, int>, Graphs> plans;
+    // plans keyed by (first request, requests, rows, mode, forced)
+    std::map<std::tuple<int, int, int, int, int>, Graphs> plans;
     yuuka_q35_accept accept_cfg{};
     bool accept_set = false;
-    int last_rows = 0;
+    int last_rows = 0, last_first = 0, last_nreq = 1;
+    // KV block pool
+    std::vector<int32_t> refs;
+    std::vector<int32_t> free_blocks;
+    std::vector<Request> req;
 };
 
 namespace {
+
+int32_t *pin_tokens(yuuka_q35 *q) { return q->pinned; }
+int32_t *pin_result(yuuka_q35 *q) { return q->pinned + q->M; }
+int32_t *pin_forced(yuuka_q35 *q) { return q->pinned + q->M + 4 * q->B; }
 
 yuuka_status alloc(yuuka_q35 *q, uint64_t bytes, yuuka_buffer **out) {
     yuuka_status st = yuuka_buffer_alloc(q->dev, bytes ? bytes : 4, out);
@@ -125,7 +160,7 @@ struct Builder {
     yuuka_status st = YUUKA_OK;
     void add(uint32_t code, std::initializer_list<yuuka_buffer *> bufs, std::initializer_list<uint64_t> n,
              std::initializer_list<uint32_t> u = {}, std::initializer_list<float> f = {}, uint32_t flags = 0,
-             std::initializer_list<uint64_t> offs = {}) {
+             std::initializer_list<uint64_t> offs = {}, yuuka_buffer *own_pos = nullptr, uint64_t own_off = 0) {
         if (st != YUUKA_OK) return;
         yuuka_op op{};
         op.code = code;
@@ -140,99 +175,137 @@ struct Builder {
         for (auto v : f) op.f[i++] = v;
         i = 0;
         for (auto v : offs) op.off[i++] = v;
+        if (own_pos) {
+            op.flags |= YUUKA_EXT_FLAG_OWN_POS;
+            op.buf[15] = own_pos;
+            op.off[15] = own_off;
+        }
         st = yuuka_plan_add(plan, &op);
-    }
-    void gemm(const Tensor &w, yuuka_buffer *xq, yuuka_buffer *out, uint64_t rows, yuuka_buffer *residual = nullptr) {
-        add(YUUKA_EXT_OP_GEMM_Q, {w.b, xq, out, residual}, {w.cols, w.rows, rows}, {w.dtype});
-    }
-    void quant(yuuka_buffer *x, uint64_t K, uint64_t rows, yuuka_buffer *xq) {
-        add(YUUKA_EXT_OP_QUANTIZE_X, {x, xq}, {K, rows});
     }
     struct Seg {
         const Tensor *w;
         yuuka_buffer *out, *res;
     };
-    // One GEMM_FUSED op: every segment reads the same activation rows x
-    // (optionally RMS-normalised with `norm`).
+    // GEMM_FUSED ops over `rows` activation rows of x (optionally
+    // RMS-normalised with `norm`), in launches of at most kRowBlock rows:
+    // every segment reads the same rows, outputs are [rows][N_i].
     void fused(yuuka_buffer *x, yuuka_buffer *norm, float eps, uint64_t rows, std::initializer_list<Seg> segs,
-               uint32_t epilogue, uint32_t silu_mask = 0, yuuka_buffer *gate = nullptr,
+               uint32_t epilogue, uint32_t out_map = 0, yuuka_buffer *gate = nullptr,
                yuuka_buffer *head_norm = nullptr) {
-        if (st != YUUKA_OK) return;
-        yuuka_op op{};
-        op.code = YUUKA_EXT_OP_GEMM_FUSED;
-        op.buf[0] = x;
-        op.buf[1] = norm;
-        op.buf[14] = gate;
-        op.buf[15] = head_norm;
-        op.u[2] = silu_mask;
-        op.n[1] = rows;
-        op.u[1] = epilogue;
-        op.f[0] = eps;
-        int i = 0;
-        for (const Seg &g : segs) {
-            op.buf[2 + i] = g.w->b;
-            op.buf[6 + i] = g.out;
-            op.buf[10 + i] = g.res;
-            op.n[0] = g.w->cols;
-            op.n[2 + i] = g.w->rows;
-            op.u[0] |= g.w->dtype << (8 * i);
-            i++;
+        const uint64_t blocks = (rows + kRowBlock - 1) / kRowBlock;
+        for (uint64_t bi = 0; bi < blocks && st == YUUKA_OK; bi++) {
+            // equal blocks (rows 40 -> 14, 13, 13), so no launch is nearly empty
+            const uint64_t r0 = rows * bi / blocks, r1 = rows * (bi + 1) / blocks;
+            yuuka_op op{};
+            op.code = YUUKA_EXT_OP_GEMM_FUSED;
+            op.buf[1] = norm;
+            op.buf[15] = head_norm;
+            op.u[2] = out_map;
+            op.n[1] = r1 - r0;
+            op.u[1] = epilogue;
+            op.f[0] = eps;
+            int i = 0;
+            uint64_t K = 0;
+            for (const Seg &g : segs) {
+                K = g.w->cols;
+                op.buf[2 + i] = g.w->b;
+                op.buf[6 + i] = g.out;
+                op.off[6 + i] = g.out ? r0 * g.w->rows * 4 : 0;
+                op.buf[10 + i] = g.res;
+                // residual rows (epilogue 1) follow the output rows; the decay
+                // parameters of output map 3 are per column, not per row
+                op.off[10 + i] = g.res && epilogue == 1 ? r0 * g.w->rows * 4 : 0;
+                op.n[2 + i] = g.w->rows;
+                op.u[0] |= g.w->dtype << (8 * i);
+                i++;
+            }
+            op.n[0] = K;
+            op.buf[0] = x;
+            op.off[0] = r0 * K * 4;
+            op.buf[14] = gate;
+            op.off[14] = gate ? r0 * K * 4 : 0;
+            st = yuuka_plan_add(plan, &op);
         }
-        st = yuuka_plan_add(plan, &op);
+    }
+    // Split path: quantize + GEMM per block of kRowBlock rows.
+    void split_gemm(const Tensor &w, yuuka_buffer *x, yuuka_buffer *xq, yuuka_buffer *out, uint64_t rows,
+                    yuuka_buffer *residual = nullptr) {
+        for (uint64_t r0 = 0; r0 < rows && st == YUUKA_OK; r0 += kRowBlock) {
+            const uint64_t n = std::min<uint64_t>(kRowBlock, rows - r0);
+            add(YUUKA_EXT_OP_QUANTIZE_X, {x, xq}, {w.cols, n}, {}, {}, 0, {r0 * w.cols * 4, 0});
+            add(YUUKA_EXT_OP_GEMM_Q, {w.b, xq, out, residual}, {w.cols, w.rows, n}, {w.dtype}, {}, 0,
+                {0, 0, r0 * w.rows * 4, residual ? r0 * w.rows * 4 : 0});
+        }
     }
 };
 
 // Fused projections need Q4_K / Q6_K weights; YUUKA_Q35_FUSED=0 selects the
-// separate quantize / GEMM / reduce ops (comparison and fallback).
+// separate quantize / GEMM ops (comparison and fallback; dense model only).
 bool use_fused(const yuuka_q35 *q) {
     if (const char *e = getenv("YUUKA_Q35_FUSED"))
-        if (e[0] == '0') return false;
-    auto ok = [](const Tensor &t) { return !t.b || t.dtype == YUUKA_DTYPE_Q4_K || t.dtype == YUUKA_DTYPE_Q6_K; };
-    if (!ok(q->output)) return false;
-    for (const Layer &L : q->layers)
-        for (const Tensor *t : {&L.qkv, &L.gate, &L.beta, &L.alpha, &L.out, &L.q, &L.k, &L.v, &L.o, &L.ffn_gate,
-                                &L.ffn_up, &L.ffn_down})
-            if (!ok(*t)) return false;
+        if (e[0] == '0' && q->cfg.n_experts == 0) return false;
     return true;
 }
 
+struct PlanKey {
+    int first, nreq, rows, mode, forced;
+};
+
 // mode 0: verify (acceptance on device), mode 1: commit every row (prefill).
-yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
+yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
     const yuuka_q35_config &c = q->cfg;
     yuuka_plan *plan = nullptr;
     yuuka_status st = yuuka_plan_create(q->dev, &plan);
     if (st != YUUKA_OK) return st;
     Builder b{plan};
-    const uint64_t R = (uint64_t)rows, H = (uint64_t)c.hidden, hd = (uint64_t)c.head_dim;
+    const int first = key.first, nreq = key.nreq, mode = key.mode;
+    const uint64_t R1 = (uint64_t)key.rows, R = (uint64_t)nreq * R1;
+    const uint64_t H = (uint64_t)c.hidden, hd = (uint64_t)c.head_dim;
     const uint64_t qdim = (uint64_t)c.heads * hd * 2, kvdim = (uint64_t)c.kv_heads * hd, odim = (uint64_t)c.heads * hd;
+    const uint64_t cd = (uint64_t)q->conv_dim, half = (uint64_t)(c.rope_dim / 2);
     // plan.go:585-588 EMBEDDING_BATCH
     b.add(YUUKA_OP_EMBEDDING_BATCH, {q->embedding.b, q->x, q->tokens},
           {H, R, yk::row_bytes(q->embedding.dtype, H), (uint64_t)c.vocab}, {q->embedding.dtype});
     const bool fused = use_fused(q);
     const float qscale = (float)(1.0 / std::sqrt((double)c.state_size));
-    auto recurrent_chunk = [&](Layer &L, uint32_t extra_flags) {
-        b.add(YUUKA_OP_RECURRENT_CHUNK,
-              {L.conv_state, L.mat_state, L.qkv_rows, q->z, L.alpha_rows, L.beta_rows, L.conv, L.dt, L.a, L.ssm_norm,
-               q->gdn_out, L.conv_rows},
-              {R, (uint64_t)c.groups, (uint64_t)c.rank, (uint64_t)c.state_size, (uint64_t)q->conv_dim,
-               (uint64_t)c.inner},
-              {(uint32_t)c.conv_kernel}, {c.eps, qscale}, YUUKA_EXT_FLAG_DEFER | extra_flags);
-    };
+    auto dyn_off = [&](int j) { return (uint64_t)(first + j) * 8; };
     // YUUKA_Q35_ATTN=0 selects the separate norm / RoPE / KV-write /
-    // attention ops (comparison); by default one ATTN_VERIFY op per layer.
+    // attention ops (comparison; one request at request 0 only); by default
+    // ATTN_VERIFY ops with their own position per request.
     const char *attn_env = getenv("YUUKA_Q35_ATTN");
-    const bool attn_fused = !(attn_env && attn_env[0] == '0');
+    const bool attn_fused = !(attn_env && attn_env[0] == '0' && nreq == 1 && first == 0);
     bool any_attn = false;
     for (const Layer &L : q->layers) any_attn |= !L.recurrent;
     if (attn_fused && any_attn)
-        b.add(YUUKA_EXT_OP_ROPE_TABLE, {q->rope}, {R, (uint64_t)c.rope_dim, 0}, {}, {(float)c.rope_base});
+        for (int j = 0; j < nreq; j++)
+            b.add(YUUKA_EXT_OP_ROPE_TABLE, {q->rope}, {R1, (uint64_t)c.rope_dim, 0}, {}, {(float)c.rope_base}, 0,
+                  {(uint64_t)j * R1 * half * 8}, q->dyn, dyn_off(j));
+    auto recurrent = [&](Layer &L, uint32_t extra_flags) {
+        for (int j = 0; j < nreq; j++) {
+            const uint64_t r0 = (uint64_t)j * R1, rq = (uint64_t)(first + j);
+            b.add(YUUKA_OP_RECURRENT_CHUNK,
+                  {L.conv_state, L.mat_state, L.qkv_rows, q->z, L.alpha_rows, L.beta_rows, L.conv, L.dt, L.a,
+                   L.ssm_norm, q->gdn_out, L.conv_rows},
+                  {R1, (uint64_t)c.groups, (uint64_t)c.rank, (uint64_t)c.state_size, cd, (uint64_t)c.inner},
+                  {(uint32_t)c.conv_kernel}, {c.eps, qscale}, YUUKA_EXT_FLAG_DEFER | extra_flags,
+                  {rq * L.conv_bytes, rq * L.mat_bytes, r0 * cd * 4, r0 * c.inner * 4, r0 * c.rank * 4,
+                   r0 * c.rank * 4, 0, 0, 0, 0, r0 * c.inner * 4, r0 * cd * 4});
+        }
+    };
     auto attention = [&](Layer &L) {
         if (attn_fused) {
-            b.add(YUUKA_EXT_OP_ATTN_VERIFY,
-                  {q->q, q->k, q->v, L.kpool, L.vpool, q->attn, q->table, L.q_norm, L.k_norm, q->rope},
-                  {(uint64_t)c.kv_heads, (uint64_t)c.heads, hd, kvdim, R, 0},
-                  {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype, (uint32_t)c.rope_dim},
-                  {(float)(1.0 / std::sqrt((double)hd)), c.eps});
+            for (int j = 0; j < nreq; j++)
+                for (uint64_t c0 = 0; c0 < R1; c0 += kAttnRows) {
+                    const uint64_t n = std::min<uint64_t>(kAttnRows, R1 - c0), r0 = (uint64_t)j * R1 + c0;
+                    b.add(YUUKA_EXT_OP_ATTN_VERIFY,
+                          {q->q, q->k, q->v, L.kpool, L.vpool, q->attn, q->table, L.q_norm, L.k_norm, q->rope},
+                          {(uint64_t)c.kv_heads, (uint64_t)c.heads, hd, kvdim, n, c0},
+                          {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype, (uint32_t)c.rope_dim},
+                          {(float)(1.0 / std::sqrt((double)hd)), c.eps}, 0,
+                          {r0 * qdim * 4, r0 * kvdim * 4, r0 * kvdim * 4, 0, 0, r0 * odim * 4,
+                           (uint64_t)(first + j) * q->max_blocks * 4, 0, 0, r0 * half * 8},
+                          q->dyn, dyn_off(j));
+                }
             return;
         }
         b.add(YUUKA_OP_RMSNORM_HEADS_BATCH, {q->k, L.k_norm, q->k}, {hd, (uint64_t)c.kv_heads, hd, R}, {}, {c.eps});
@@ -247,6 +320,25 @@ yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
               {(uint64_t)c.kv_heads, (uint64_t)c.heads, hd, kvdim, R, 0},
               {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype, 0}, {(float)(1.0 / std::sqrt((double)hd))});
     };
+    // forward.go:320-389 forwardMoEFFN over all rows: router, top-k binning,
+    // grouped expert SwiGLU and down projections, shared expert, weighted sum.
+    auto moe_ffn = [&](Layer &L) {
+        const uint64_t E = (uint64_t)c.n_experts, used = (uint64_t)c.n_experts_used;
+        const uint64_t ef = (uint64_t)c.expert_ffn;
+        b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, L.post_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
+        b.add(YUUKA_EXT_OP_MOE_ROUTER, {q->xn, L.router.b, q->moe_logits, L.shared_gate_vec, q->moe_sg}, {H, E, R});
+        b.add(YUUKA_OP_MOE_ROUTE,
+              {q->moe_logits, q->moe_ids, q->moe_w, q->moe_counts, q->moe_arows, q->moe_aslots, q->moe_aw},
+              {R, E, used});
+        b.add(YUUKA_OP_MOE_GATE_UP,
+              {q->xn, L.gate_exps.b, L.up_exps.b, q->moe_counts, q->moe_arows, q->moe_aslots, q->moe_act, nullptr},
+              {H, ef, R, E, used}, {L.gate_exps.dtype}, {}, YUUKA_EXT_FLAG_MOE_SWIGLU);
+        b.add(YUUKA_OP_MOE_DOWN, {q->moe_act, L.down_exps.b, q->moe_counts, q->moe_arows, q->moe_aslots, q->moe_eo},
+              {ef, H, R, E, used}, {L.down_exps.dtype});
+        b.fused(q->xn, nullptr, 0.0f, R, {{&L.shared_gate, q->moe_sfg, nullptr}, {&L.shared_up, nullptr, nullptr}}, 2);
+        b.fused(q->moe_sfg, nullptr, 0.0f, R, {{&L.shared_down, q->moe_so, nullptr}}, 0);
+        b.add(YUUKA_EXT_OP_MOE_COMBINE, {q->x, q->moe_eo, q->moe_w, q->moe_so, q->moe_sg}, {H, R, used});
+    };
     for (int i = 0; i < c.n_layers; i++) {
         Layer &L = q->layers[i];
         if (fused) {
@@ -260,7 +352,7 @@ yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
                         {{&L.qkv, L.qkv_rows, nullptr}, {&L.gate, q->z, nullptr}, {&L.beta, L.beta_rows, nullptr},
                          {&L.alpha, L.alpha_rows, L.dt_a}},
                         0, (1u << 4) | (2u << 8) | (3u << 12));
-                recurrent_chunk(L, YUUKA_EXT_FLAG_RAW_OUT | YUUKA_EXT_FLAG_GDN_COEF);
+                recurrent(L, YUUKA_EXT_FLAG_RAW_OUT | YUUKA_EXT_FLAG_GDN_COEF);
                 b.fused(q->gdn_out, nullptr, c.eps, R, {{&L.out, q->x, q->x}}, 1, 0, q->z, L.ssm_norm);
             } else {  // plan.go:684-804
                 b.fused(q->x, L.attn_norm, c.eps, R,
@@ -268,62 +360,73 @@ yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
                 attention(L);
                 b.fused(q->attn, nullptr, 0.0f, R, {{&L.o, q->x, q->x}}, 1);
             }
-            // plan.go:915-988 FFN: norm + gate/up + SwiGLU in one op, down + residual
-            b.fused(q->x, L.post_norm, c.eps, R, {{&L.ffn_gate, q->fg, nullptr}, {&L.ffn_up, nullptr, nullptr}}, 2);
-            b.fused(q->fg, nullptr, 0.0f, R, {{&L.ffn_down, q->x, q->x}}, 1);
+            if (L.moe) {
+                moe_ffn(L);
+            } else {
+                // plan.go:915-988 FFN: norm + gate/up + SwiGLU in one op, down + residual
+                b.fused(q->x, L.post_norm, c.eps, R, {{&L.ffn_gate, q->fg, nullptr}, {&L.ffn_up, nullptr, nullptr}},
+                        2);
+                b.fused(q->fg, nullptr, 0.0f, R, {{&L.ffn_down, q->x, q->x}}, 1);
+            }
             continue;
         }
         b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, L.attn_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
-        b.quant(q->xn, H, R, q->xq);
         if (L.recurrent) {
-            b.gemm(L.qkv, q->xq, L.qkv_rows, R);
-            b.gemm(L.gate, q->xq, q->z, R);
-            b.gemm(L.beta, q->xq, L.beta_rows, R);
-            b.gemm(L.alpha, q->xq, L.alpha_rows, R);
-            recurrent_chunk(L, 0);
-            b.quant(q->gdn_out, (uint64_t)c.inner, R, q->xq);
-            b.gemm(L.out, q->xq, q->x, R, q->x);
+            b.split_gemm(L.qkv, q->xn, q->xq, L.qkv_rows, R);
+            b.split_gemm(L.gate, q->xn, q->xq, q->z, R);
+            b.split_gemm(L.beta, q->xn, q->xq, L.beta_rows, R);
+            b.split_gemm(L.alpha, q->xn, q->xq, L.alpha_rows, R);
+            recurrent(L, 0);
+            b.split_gemm(L.out, q->gdn_out, q->xq, q->x, R, q->x);
         } else {
-            b.gemm(L.q, q->xq, q->q, R);
-            b.gemm(L.k, q->xq, q->k, R);
-            b.gemm(L.v, q->xq, q->v, R);
+            b.split_gemm(L.q, q->xn, q->xq, q->q, R);
+            b.split_gemm(L.k, q->xn, q->xq, q->k, R);
+            b.split_gemm(L.v, q->xn, q->xq, q->v, R);
             attention(L);
-            b.quant(q->attn, odim, R, q->xq);
-            b.gemm(L.o, q->xq, q->x, R, q->x);
+            b.split_gemm(L.o, q->attn, q->xq, q->x, R, q->x);
         }
         b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, L.post_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
-        b.quant(q->xn, H, R, q->xq);
-        b.gemm(L.ffn_gate, q->xq, q->fg, R);
-        b.gemm(L.ffn_up, q->xq, q->fu, R);
+        b.split_gemm(L.ffn_gate, q->xn, q->xq, q->fg, R);
+        b.split_gemm(L.ffn_up, q->xn, q->xq, q->fu, R);
         b.add(YUUKA_OP_SILU_MUL, {q->fg, q->fu, q->fg}, {R * (uint64_t)c.ffn});
-        b.quant(q->fg, (uint64_t)c.ffn, R, q->xq);
-        b.gemm(L.ffn_down, q->xq, q->x, R, q->x);
+        b.split_gemm(L.ffn_down, q->fg, q->xq, q->x, R, q->x);
     }
     // plan.go:635-662 all-logits tail
     if (fused) {
         b.fused(q->x, q->output_norm, c.eps, R, {{&q->output, q->logits, nullptr}}, 0);
     } else {
         b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, q->output_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
-        b.quant(q->xn, H, R, q->xq);
-        b.gemm(q->output, q->xq, q->logits, R);
+        b.split_gemm(q->output, q->xn, q->xq, q->logits, R);
     }
     if (mode == 0) {
         const yuuka_q35_accept &a = q->accept_cfg;
-        // drafts are tokens[1..k]
-        b.add(YUUKA_EXT_OP_ACCEPT, {q->logits, q->tokens, q->result, nullptr, q->step},
-              {1, R - 1, (uint64_t)c.vocab, 0, a.seed, 0}, {a.mode, a.top_k, 0}, {a.temperature, a.top_p}, 0,
-              {0, 4, 0, 0, 0});
+        // drafts are tokens[j][1..k]; request index j of this plan is
+        // request first + j (its Philox stream and result slot)
+        b.add(YUUKA_EXT_OP_ACCEPT,
+              {q->logits, q->tokens, q->result, nullptr, q->step, key.forced ? q->forced : nullptr},
+              {(uint64_t)nreq, R1 - 1, (uint64_t)c.vocab, 0, a.seed, 0},
+              {a.mode, a.top_k, (uint32_t)first, (uint32_t)R1}, {a.temperature, a.top_p}, 0,
+              {0, 4, (uint64_t)first * 16, 0, 0, (uint64_t)first * 4});
     }
-    for (int i = 0; i < c.n_layers; i++) {
-        Layer &L = q->layers[i];
-        if (!L.recurrent) continue;
-        b.add(YUUKA_EXT_OP_GDN_COMMIT,
-              {L.conv_state, L.mat_state, L.qkv_rows, L.conv_rows, L.alpha_rows, L.beta_rows, L.dt, L.a, q->result},
-              {R, (uint64_t)c.groups, (uint64_t)c.rank, (uint64_t)c.state_size, (uint64_t)q->conv_dim,
-               (uint64_t)c.inner},
-              {(uint32_t)c.conv_kernel}, {}, fused ? YUUKA_EXT_FLAG_GDN_COEF : 0u);
+    for (int j = 0; j < nreq; j++) {
+        const uint64_t r0 = (uint64_t)j * R1, rq = (uint64_t)(first + j);
+        for (int i = 0; i < c.n_layers; i++) {
+            Layer &L = q->layers[i];
+            if (!L.recurrent) continue;
+            b.add(YUUKA_EXT_OP_GDN_COMMIT,
+                  {L.conv_state, L.mat_state, L.qkv_rows, L.conv_rows, L.alpha_rows, L.beta_rows, L.dt, L.a,
+                   q->result},
+                  {R1, (uint64_t)c.groups, (uint64_t)c.rank, (uint64_t)c.state_size, cd, (uint64_t)c.inner},
+                  {(uint32_t)c.conv_kernel}, {}, fused ? YUUKA_EXT_FLAG_GDN_COEF : 0u,
+                  {rq * L.conv_bytes, rq * L.mat_bytes, r0 * cd * 4, r0 * cd * 4, r0 * c.rank * 4, r0 * c.rank * 4, 0,
+                   0, rq * 16});
+        }
     }
-    b.add(YUUKA_EXT_OP_ADVANCE, {q->dyn, q->result, q->step}, {R});
+    for (int j = 0; j < nreq; j++) {
+        // the step counter (Philox) advances once per step
+        b.add(YUUKA_EXT_OP_ADVANCE, {q->dyn, q->result, j == 0 ? q->step : nullptr}, {R1}, {}, {}, 0,
+              {dyn_off(j), (uint64_t)(first + j) * 16, 0});
+    }
     if (b.st != YUUKA_OK) {
         yuuka_plan_destroy(plan);
         return b.st;
@@ -332,12 +435,12 @@ yuuka_status build_plan(yuuka_q35 *q, int rows, int mode, yuuka_plan **out) {
     return YUUKA_OK;
 }
 
-yuuka_status get_graph(yuuka_q35 *q, int rows, int mode, Graphs **out) {
-    auto key = std::make_pair(rows, mode);
+yuuka_status get_graph(yuuka_q35 *q, const PlanKey &k, Graphs **out) {
+    auto key = std::make_tuple(k.first, k.nreq, k.rows, k.mode, k.forced);
     auto it = q->plans.find(key);
     if (it == q->plans.end()) {
         Graphs g;
-        yuuka_status st = build_plan(q, rows, mode, &g.plan);
+        yuuka_status st = build_plan(q, k, &g.plan);
         if (st != YUUKA_OK) return st;
         if (!q->eager) st = yuuka_graph_create(g.plan, q->stream, q->dyn, 1, &g.graph);
         if (st != YUUKA_OK) {
@@ -350,28 +453,82 @@ yuuka_status get_graph(yuuka_q35 *q, int rows, int mode, Graphs **out) {
     return YUUKA_OK;
 }
 
-void drop_graphs(yuuka_q35 *q) {
-    for (auto &kv : q->plans) {
-        yuuka_graph_destroy(kv.second.graph);
-        yuuka_plan_destroy(kv.second.plan);
+void drop_graphs(yuuka_q35 *q, bool verify_only) {
+    for (auto it = q->plans.begin(); it != q->plans.end();) {
+        if (verify_only && std::get<3>(it->first) != 0) {
+            ++it;
+            continue;
+        }
+        yuuka_graph_destroy(it->second.graph);
+        yuuka_plan_destroy(it->second.plan);
+        it = q->plans.erase(it);
     }
-    q->plans.clear();
 }
 
-// Runs one step over `rows` tokens (already in q->pinned). mode 1 presets
-// result[0] = rows - 1 so the commit keeps every row.
-yuuka_status run_step(yuuka_q35 *q, int rows, int mode, int32_t *result_out) {
+// ------------------------------------------------------------ KV blocks
+
+void release_blocks(yuuka_q35 *q, int r) {
+    for (int32_t blk : q->req[r].blocks)
+        if (--q->refs[blk] == 0) q->free_blocks.push_back(blk);
+    q->req[r].blocks.clear();
+}
+
+yuuka_status upload_table(yuuka_q35 *q, int r) {
+    std::vector<int32_t> t(q->max_blocks, 0);
+    std::copy(q->req[r].blocks.begin(), q->req[r].blocks.end(), t.begin());
+    hipError_t err = hipMemcpy(static_cast<uint8_t *>(q->table->ptr) + (uint64_t)r * q->max_blocks * 4, t.data(),
+                               (size_t)q->max_blocks * 4, hipMemcpyHostToDevice);
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "block table upload: %s", yk::hip_error(err));
+    return YUUKA_OK;
+}
+
+// Makes request r's table cover positions [0, upto).
+yuuka_status ensure_blocks(yuuka_q35 *q, int r, int upto) {
+    const int need = (upto + q->cfg.block_size - 1) / q->cfg.block_size;
+    if (need > q->max_blocks) return fail(YUUKA_ERR_INVALID_ARGUMENT, "request %d exceeds its context capacity", r);
+    bool grew = false;
+    while ((int)q->req[r].blocks.size() < need) {
+        if (q->free_blocks.empty()) return fail(YUUKA_ERR_ALLOCATION, "KV pool exhausted (%zu blocks)", q->refs.size());
+        const int32_t blk = q->free_blocks.back();
+        q->free_blocks.pop_back();
+        q->refs[blk] = 1;
+        q->req[r].blocks.push_back(blk);
+        grew = true;
+    }
+    return grew ? upload_table(q, r) : YUUKA_OK;
+}
+
+// ------------------------------------------------------------ stepping
+
+// Runs one step of `key.rows` tokens for requests first..first+nreq-1
+// (tokens already in the pinned staging). mode 1 presets result[0] =
+// rows - 1 so the commit keeps every row.
+yuuka_status run_step(yuuka_q35 *q, const PlanKey &key, int32_t *result_out) {
+    for (int j = 0; j < key.nreq; j++) {
+        yuuka_status st = ensure_blocks(q, key.first + j, q->req[key.first + j].pos + key.rows);
+        if (st != YUUKA_OK) return st;
+    }
     Graphs *g = nullptr;
-    yuuka_status st = get_graph(q, rows, mode, &g);
+    yuuka_status st = get_graph(q, key, &g);
     if (st != YUUKA_OK) return st;
     hipStream_t s = q->stream->stream;
-    hipError_t err = hipMemcpyAsync(q->tokens->ptr, q->pinned, (size_t)rows * 4, hipMemcpyHostToDevice, s);
-    if (err == hipSuccess && mode == 1) {
-        q->pinned[16] = rows - 1;
-        q->pinned[17] = -1;
-        err = hipMemcpyAsync(q->result->ptr, q->pinned + 16, 8, hipMemcpyHostToDevice, s);
+    const size_t nt = (size_t)key.nreq * key.rows;
+    hipError_t err = hipMemcpyAsync(q->tokens->ptr, pin_tokens(q), nt * 4, hipMemcpyHostToDevice, s);
+    int32_t *pr = pin_result(q) + 4 * key.first;
+    if (err == hipSuccess && key.mode == 1) {
+        for (int j = 0; j < key.nreq; j++) {
+            pr[4 * j] = key.rows - 1;
+            pr[4 * j + 1] = -1;
+            pr[4 * j + 2] = -1;
+            pr[4 * j + 3] = 0;
+        }
+        err = hipMemcpyAsync(static_cast<uint8_t *>(q->result->ptr) + (uint64_t)key.first * 16, pr,
+                             (size_t)key.nreq * 16, hipMemcpyHostToDevice, s);
     }
-    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "token upload: %s", yk::hip_error(err));
+    if (err == hipSuccess && key.forced)
+        err = hipMemcpyAsync(static_cast<uint8_t *>(q->forced->ptr) + (uint64_t)key.first * 4,
+                             pin_forced(q) + key.first, (size_t)key.nreq * 4, hipMemcpyHostToDevice, s);
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "step upload: %s", yk::hip_error(err));
     (void)hipEventRecord(q->ev0, s);
     if (g->graph)
         st = yuuka_graph_replay(g->graph, q->stream, nullptr);
@@ -379,18 +536,22 @@ yuuka_status run_step(yuuka_q35 *q, int rows, int mode, int32_t *result_out) {
         st = yk::plan_run_dynamic(g->plan, s, static_cast<const int32_t *>(q->dyn->ptr));
     if (st != YUUKA_OK) return st;
     (void)hipEventRecord(q->ev1, s);
-    err = hipMemcpyAsync(q->pinned + 16, q->result->ptr, 16, hipMemcpyDeviceToHost, s);
+    err = hipMemcpyAsync(pr, static_cast<uint8_t *>(q->result->ptr) + (uint64_t)key.first * 16,
+                         (size_t)key.nreq * 16, hipMemcpyDeviceToHost, s);
     if (err == hipSuccess) err = hipStreamSynchronize(s);
     if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "verify step: %s", yk::hip_error(err));
     (void)hipEventElapsedTime(&q->last_ms, q->ev0, q->ev1);
-    q->last_rows = rows;
-    if (result_out) std::memcpy(result_out, q->pinned + 16, 16);
+    q->last_rows = key.rows;
+    q->last_first = key.first;
+    q->last_nreq = key.nreq;
+    for (int j = 0; j < key.nreq; j++) q->req[key.first + j].pos += pr[4 * j] + 1;
+    if (result_out) std::memcpy(result_out, pr, (size_t)key.nreq * 16);
     return YUUKA_OK;
 }
 
-int32_t read_pos(yuuka_q35 *q) {
+int32_t read_pos(const yuuka_q35 *q, int r) {
     int32_t d[2] = {0, 0};
-    (void)hipMemcpy(d, q->dyn->ptr, 8, hipMemcpyDeviceToHost);
+    (void)hipMemcpy(d, static_cast<const uint8_t *>(q->dyn->ptr) + (uint64_t)r * 8, 8, hipMemcpyDeviceToHost);
     return d[1];
 }
 
@@ -410,6 +571,58 @@ yuuka_status guard(const char *what, F &&f) {
 bool same_accept(const yuuka_q35_accept &a, const yuuka_q35_accept &b) {
     return a.mode == b.mode && a.temperature == b.temperature && a.top_k == b.top_k && a.top_p == b.top_p &&
            a.seed == b.seed;
+}
+
+void set_accept(yuuka_q35 *q, const yuuka_q35_accept &a) {
+    if (q->accept_set && same_accept(a, q->accept_cfg)) return;
+    drop_graphs(q, true);  // acceptance settings are baked into the captured graphs
+    q->accept_cfg = a;
+    q->accept_set = true;
+}
+
+yuuka_status check_tokens(const yuuka_q35 *q, const int32_t *t, size_t n) {
+    for (size_t i = 0; i < n; i++)
+        if (t[i] < 0 || t[i] >= q->cfg.vocab) return fail(YUUKA_ERR_INVALID_ARGUMENT, "token id %d is out of range", t[i]);
+    return YUUKA_OK;
+}
+
+yuuka_status reset_request(yuuka_q35 *q, int r) {
+    hipStream_t s = q->stream->stream;
+    for (auto &L : q->layers) {
+        if (!L.recurrent) continue;
+        (void)hipMemsetAsync(static_cast<uint8_t *>(L.conv_state->ptr) + (uint64_t)r * L.conv_bytes, 0, L.conv_bytes, s);
+        (void)hipMemsetAsync(static_cast<uint8_t *>(L.mat_state->ptr) + (uint64_t)r * L.mat_bytes, 0, L.mat_bytes, s);
+    }
+    (void)hipMemsetAsync(static_cast<uint8_t *>(q->dyn->ptr) + (uint64_t)r * 8, 0, 8, s);
+    hipError_t err = hipStreamSynchronize(s);
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "reset: %s", yk::hip_error(err));
+    release_blocks(q, r);
+    q->req[r].pos = 0;
+    return upload_table(q, r);
+}
+
+yuuka_status prefill_request(yuuka_q35 *q, int r, const int32_t *tokens, int32_t n, float *last_logits) {
+    if (!tokens || n <= 0) return fail(YUUKA_ERR_INVALID_ARGUMENT, "empty token sequence");
+    if (q->req[r].pos + n > q->cfg.capacity)
+        return fail(YUUKA_ERR_INVALID_ARGUMENT, "token sequence of %d exceeds remaining context %d", n,
+                    q->cfg.capacity - q->req[r].pos);
+    yuuka_status st = check_tokens(q, tokens, (size_t)n);
+    if (st != YUUKA_OK) return st;
+    int done = 0;
+    while (done < n) {
+        const int rows = std::min(n - done, q->MR);
+        std::memcpy(pin_tokens(q), tokens + done, (size_t)rows * 4);
+        st = run_step(q, PlanKey{r, 1, rows, 1, 0}, nullptr);
+        if (st != YUUKA_OK) return st;
+        done += rows;
+    }
+    if (last_logits) {
+        hipError_t err = hipMemcpy(last_logits,
+                                   static_cast<float *>(q->logits->ptr) + (uint64_t)(q->last_rows - 1) * q->cfg.vocab,
+                                   (size_t)q->cfg.vocab * 4, hipMemcpyDeviceToHost);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "logits copy: %s", yk::hip_error(err));
+    }
+    return YUUKA_OK;
 }
 
 // engine/speculative.go:39-66 lookupDraft.
@@ -440,45 +653,60 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
     return guard("q35_create", [&]() -> yuuka_status {
         if (!dev || !cfg || !w || !out || !w->layers) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
         *out = nullptr;
-        const yuuka_q35_config &c = *cfg;
-        if (c.n_layers <= 0 || c.hidden <= 0 || c.ffn <= 0 || c.heads <= 0 || c.kv_heads <= 0 ||
+        yuuka_q35_config c = *cfg;
+        if (c.batch <= 0) c.batch = 1;
+        if (c.n_layers <= 0 || c.hidden <= 0 || c.ffn < 0 || c.heads <= 0 || c.kv_heads <= 0 ||
             c.heads % c.kv_heads || c.vocab <= 0 || c.full_interval <= 0 || c.capacity <= 0 || c.block_size <= 0 ||
-            c.max_rows < 1 || c.max_rows > 16 || c.conv_kernel < 2 || c.inner != c.rank * c.state_size)
+            c.max_rows < 1 || c.max_rows > 32 || c.conv_kernel < 2 || c.inner != c.rank * c.state_size ||
+            c.batch > 256 || c.kv_blocks < 0)
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid qwen35 configuration");
+        const bool moe = c.n_experts > 0;
+        if (moe && (c.n_experts_used <= 0 || c.n_experts_used > c.n_experts || c.expert_ffn <= 0 || c.shared_ffn <= 0))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid MoE configuration");
+        if (!moe && c.ffn <= 0) return fail(YUUKA_ERR_INVALID_ARGUMENT, "dense FFN size must be positive");
         if (c.kv_dtype != YUUKA_DTYPE_F16 && c.kv_dtype != YUUKA_DTYPE_F32)
             return fail(YUUKA_ERR_UNSUPPORTED, "KV dtype %u", c.kv_dtype);
         std::unique_ptr<yuuka_q35> q(new yuuka_q35());
         q->dev = dev;
         q->cfg = c;
+        q->B = c.batch;
+        q->MR = c.max_rows;
+        q->M = q->B * q->MR;
+        q->max_blocks = (c.capacity + c.block_size - 1) / c.block_size;
         q->conv_dim = 2 * c.groups * c.state_size + c.inner;
+        q->req.resize(q->B);
+        const int pool_blocks = c.kv_blocks > 0 ? c.kv_blocks : q->B * q->max_blocks;
+        q->refs.assign(pool_blocks, 0);
+        for (int i = pool_blocks - 1; i >= 0; i--) q->free_blocks.push_back(i);
         yuuka_status st = yuuka_stream_create(dev, &q->stream);
         if (st != YUUKA_OK) return st;
-        hipError_t err = hipHostMalloc(reinterpret_cast<void **>(&q->pinned), 32 * 4, hipHostMallocDefault);
+        hipError_t err = hipHostMalloc(reinterpret_cast<void **>(&q->pinned), (size_t)(q->M + 5 * q->B + 16) * 4,
+                                       hipHostMallocDefault);
         if (err != hipSuccess) return fail(YUUKA_ERR_ALLOCATION, "pinned staging: %s", yk::hip_error(err));
         q->eager = getenv("YUUKA_Q35_EAGER") && getenv("YUUKA_Q35_EAGER")[0] == '1';
         if (hipEventCreate(&q->ev0) != hipSuccess || hipEventCreate(&q->ev1) != hipSuccess)
             return fail(YUUKA_ERR_DEVICE, "timing events");
-        const uint64_t H = c.hidden, M = c.max_rows, hd = c.head_dim;
+        const uint64_t H = c.hidden, M = (uint64_t)q->M, hd = c.head_dim, Bq = (uint64_t)q->B;
         const uint64_t qdim = (uint64_t)c.heads * hd * 2, kvdim = (uint64_t)c.kv_heads * hd;
         const uint64_t cd = (uint64_t)q->conv_dim;
-#define CHK(x)                           \
-    do {                                 \
-        yuuka_status s_ = (x);           \
-        if (s_ != YUUKA_OK) {            \
+#define CHK(x)                              \
+    do {                                    \
+        yuuka_status s_ = (x);              \
+        if (s_ != YUUKA_OK) {               \
             yuuka_q35_destroy(q.release()); \
-            return s_;                   \
-        }                                \
+            return s_;                      \
+        }                                   \
     } while (0)
         CHK(upload_tensor(q.get(), w->embedding, c.vocab, H, "token_embd", &q->embedding));
         CHK(upload_tensor(q.get(), w->output, c.vocab, H, "output", &q->output));
         CHK(upload_vec(q.get(), w->output_norm, H, "output_norm", &q->output_norm));
         q->layers.resize(c.n_layers);
-        const int blocks = (c.capacity + c.block_size - 1) / c.block_size;
-        const uint64_t kv_bytes = (uint64_t)blocks * c.block_size * kvdim * (c.kv_dtype == YUUKA_DTYPE_F16 ? 2 : 4);
+        const uint64_t kv_bytes = (uint64_t)pool_blocks * c.block_size * kvdim * (c.kv_dtype == YUUKA_DTYPE_F16 ? 2 : 4);
         for (int i = 0; i < c.n_layers; i++) {
             const yuuka_q35_layer_weights &lw = w->layers[i];
             Layer &L = q->layers[i];
             L.recurrent = (i + 1) % c.full_interval != 0;  // config.go:280-282
+            L.moe = moe;
             CHK(upload_vec(q.get(), lw.attn_norm, H, "attn_norm", &L.attn_norm));
             CHK(upload_vec(q.get(), lw.post_norm, H, "post_attention_norm", &L.post_norm));
             if (L.recurrent) {
@@ -497,8 +725,10 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
                     CHK(upload(q.get(), da.data(), da.size() * 4, &L.dt_a));
                 }
                 CHK(upload_vec(q.get(), lw.ssm_norm, c.state_size, "ssm_norm", &L.ssm_norm));
-                CHK(alloc(q.get(), (uint64_t)(c.conv_kernel - 1) * cd * 4, &L.conv_state));
-                CHK(alloc(q.get(), (uint64_t)c.rank * c.state_size * c.state_size * 4, &L.mat_state));
+                L.conv_bytes = (uint64_t)(c.conv_kernel - 1) * cd * 4;
+                L.mat_bytes = (uint64_t)c.rank * c.state_size * c.state_size * 4;
+                CHK(alloc(q.get(), Bq * L.conv_bytes, &L.conv_state));
+                CHK(alloc(q.get(), Bq * L.mat_bytes, &L.mat_state));
                 CHK(alloc(q.get(), M * cd * 4, &L.qkv_rows));
                 CHK(alloc(q.get(), M * cd * 4, &L.conv_rows));
                 CHK(alloc(q.get(), M * c.rank * 4, &L.alpha_rows));
@@ -513,14 +743,30 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
                 CHK(alloc(q.get(), kv_bytes, &L.kpool));
                 CHK(alloc(q.get(), kv_bytes, &L.vpool));
             }
-            CHK(upload_tensor(q.get(), lw.ffn_gate, c.ffn, H, "ffn_gate", &L.ffn_gate));
-            CHK(upload_tensor(q.get(), lw.ffn_up, c.ffn, H, "ffn_up", &L.ffn_up));
-            CHK(upload_tensor(q.get(), lw.ffn_down, H, c.ffn, "ffn_down", &L.ffn_down));
+            if (moe) {
+                const uint64_t E = c.n_experts, ef = c.expert_ffn, sf = c.shared_ffn;
+                if (lw.router.dtype != YUUKA_DTYPE_F32 || lw.gate_exps.dtype != YUUKA_DTYPE_Q4_K ||
+                    lw.up_exps.dtype != YUUKA_DTYPE_Q4_K || lw.down_exps.dtype != YUUKA_DTYPE_Q4_K)
+                    CHK(fail(YUUKA_ERR_UNSUPPORTED, "MoE layer %d: router F32 and Q4_K experts are served", i));
+                CHK(upload_tensor(q.get(), lw.router, E, H, "ffn_gate_inp", &L.router));
+                CHK(upload_vec(q.get(), lw.shared_gate_vec, H, "ffn_gate_inp_shexp", &L.shared_gate_vec));
+                CHK(upload_tensor(q.get(), lw.shared_gate, sf, H, "ffn_gate_shexp", &L.shared_gate));
+                CHK(upload_tensor(q.get(), lw.shared_up, sf, H, "ffn_up_shexp", &L.shared_up));
+                CHK(upload_tensor(q.get(), lw.shared_down, H, sf, "ffn_down_shexp", &L.shared_down));
+                CHK(upload_tensor(q.get(), lw.gate_exps, E * ef, H, "ffn_gate_exps", &L.gate_exps));
+                CHK(upload_tensor(q.get(), lw.up_exps, E * ef, H, "ffn_up_exps", &L.up_exps));
+                CHK(upload_tensor(q.get(), lw.down_exps, E * H, ef, "ffn_down_exps", &L.down_exps));
+            } else {
+                CHK(upload_tensor(q.get(), lw.ffn_gate, c.ffn, H, "ffn_gate", &L.ffn_gate));
+                CHK(upload_tensor(q.get(), lw.ffn_up, c.ffn, H, "ffn_up", &L.ffn_up));
+                CHK(upload_tensor(q.get(), lw.ffn_down, H, c.ffn, "ffn_down", &L.ffn_down));
+            }
         }
-        const uint64_t kmax = std::max<uint64_t>({H, (uint64_t)c.ffn, (uint64_t)c.inner, (uint64_t)c.heads * hd});
+        const uint64_t ffn_w = moe ? (uint64_t)c.shared_ffn : (uint64_t)c.ffn;
+        const uint64_t kmax = std::max<uint64_t>({H, ffn_w, (uint64_t)c.inner, (uint64_t)c.heads * hd});
         CHK(alloc(q.get(), M * H * 4, &q->x));
         CHK(alloc(q.get(), M * H * 4, &q->xn));
-        CHK(alloc(q.get(), yk::gemm_plan(kmax, 1, M, YUUKA_DTYPE_Q4_K).xq_bytes + 256, &q->xq));
+        CHK(alloc(q.get(), yk::gemm_plan(kmax, 1, kRowBlock, YUUKA_DTYPE_Q4_K).xq_bytes + 256, &q->xq));
         CHK(alloc(q.get(), M * qdim * 4, &q->q));
         CHK(alloc(q.get(), M * kvdim * 4, &q->k));
         CHK(alloc(q.get(), M * kvdim * 4, &q->v));
@@ -528,17 +774,30 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
         CHK(alloc(q.get(), M * (uint64_t)(c.rope_dim / 2) * 8, &q->rope));
         CHK(alloc(q.get(), M * c.inner * 4, &q->z));
         CHK(alloc(q.get(), M * c.inner * 4, &q->gdn_out));
-        CHK(alloc(q.get(), M * c.ffn * 4, &q->fg));
-        CHK(alloc(q.get(), M * c.ffn * 4, &q->fu));
+        CHK(alloc(q.get(), M * ffn_w * 4, &q->fg));
+        CHK(alloc(q.get(), M * ffn_w * 4, &q->fu));
         CHK(alloc(q.get(), M * (uint64_t)c.vocab * 4, &q->logits));
-        CHK(alloc(q.get(), 64 * 4, &q->tokens));
-        CHK(alloc(q.get(), 16, &q->result));
-        CHK(alloc(q.get(), 16, &q->dyn));
+        if (moe) {
+            const uint64_t E = c.n_experts, used = c.n_experts_used;
+            CHK(alloc(q.get(), M * E * 4, &q->moe_logits));
+            CHK(alloc(q.get(), M * 4, &q->moe_sg));
+            CHK(alloc(q.get(), M * used * 4, &q->moe_ids));
+            CHK(alloc(q.get(), M * used * 4, &q->moe_w));
+            CHK(alloc(q.get(), E * 4, &q->moe_counts));
+            CHK(alloc(q.get(), E * M * used * 4, &q->moe_arows));
+            CHK(alloc(q.get(), E * M * used * 4, &q->moe_aslots));
+            CHK(alloc(q.get(), E * M * used * 4, &q->moe_aw));
+            CHK(alloc(q.get(), M * used * c.expert_ffn * 4, &q->moe_act));
+            CHK(alloc(q.get(), M * used * H * 4, &q->moe_eo));
+            CHK(alloc(q.get(), M * c.shared_ffn * 4, &q->moe_sfg));
+            CHK(alloc(q.get(), M * H * 4, &q->moe_so));
+        }
+        CHK(alloc(q.get(), (M + 64) * 4, &q->tokens));
+        CHK(alloc(q.get(), Bq * 16, &q->result));
+        CHK(alloc(q.get(), Bq * 8, &q->dyn));
         CHK(alloc(q.get(), 8, &q->step));
-        // identity block table (memory/memory.go Table over a private pool)
-        std::vector<int32_t> table(blocks);
-        for (int i = 0; i < blocks; i++) table[i] = i;
-        CHK(upload(q.get(), table.data(), (uint64_t)blocks * 4, &q->table));
+        CHK(alloc(q.get(), Bq * 4, &q->forced));
+        CHK(alloc(q.get(), Bq * q->max_blocks * 4, &q->table));
         *out = q.release();
         return yuuka_q35_reset(*out);
 #undef CHK
@@ -548,7 +807,7 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
 void yuuka_q35_destroy(yuuka_q35 *q) {
     if (!q) return;
     if (q->stream) (void)hipStreamSynchronize(q->stream->stream);
-    drop_graphs(q);
+    drop_graphs(q, false);
     for (auto *b : q->owned) yuuka_buffer_free(b);
     if (q->pinned) (void)hipHostFree(q->pinned);
     if (q->ev0) (void)hipEventDestroy(q->ev0);
@@ -560,49 +819,93 @@ void yuuka_q35_destroy(yuuka_q35 *q) {
 yuuka_status yuuka_q35_reset(yuuka_q35 *q) {
     return guard("q35_reset", [&]() -> yuuka_status {
         if (!q) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null engine");
-        hipStream_t s = q->stream->stream;
-        for (auto &L : q->layers) {
-            if (!L.recurrent) continue;
-            (void)hipMemsetAsync(L.conv_state->ptr, 0, L.conv_state->bytes, s);
-            (void)hipMemsetAsync(L.mat_state->ptr, 0, L.mat_state->bytes, s);
+        for (int r = 0; r < q->B; r++) {
+            yuuka_status st = reset_request(q, r);
+            if (st != YUUKA_OK) return st;
         }
-        (void)hipMemsetAsync(q->dyn->ptr, 0, q->dyn->bytes, s);
-        (void)hipMemsetAsync(q->step->ptr, 0, 8, s);
-        hipError_t err = hipStreamSynchronize(s);
+        (void)hipMemsetAsync(q->step->ptr, 0, 8, q->stream->stream);
+        hipError_t err = hipStreamSynchronize(q->stream->stream);
         if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "reset: %s", yk::hip_error(err));
         return YUUKA_OK;
     });
 }
 
+yuuka_status yuuka_q35_reset_request(yuuka_q35 *q, int32_t request) {
+    return guard("q35_reset_request", [&]() -> yuuka_status {
+        if (!q || request < 0 || request >= q->B) return fail(YUUKA_ERR_INVALID_ARGUMENT, "bad request index");
+        return reset_request(q, request);
+    });
+}
+
 float yuuka_q35_last_step_ms(const yuuka_q35 *q) { return q ? q->last_ms : 0.0f; }
 
-int32_t yuuka_q35_position(const yuuka_q35 *q) { return q ? read_pos(const_cast<yuuka_q35 *>(q)) : -1; }
+int32_t yuuka_q35_position(const yuuka_q35 *q) { return q ? read_pos(q, 0) : -1; }
+
+int32_t yuuka_q35_request_position(const yuuka_q35 *q, int32_t request) {
+    return q && request >= 0 && request < q->B ? read_pos(q, request) : -1;
+}
 
 yuuka_status yuuka_q35_prefill(yuuka_q35 *q, const int32_t *tokens, int32_t n, float *last_logits) {
     return guard("q35_prefill", [&]() -> yuuka_status {
         if (!q || (!tokens && n)) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
-        if (n <= 0) return fail(YUUKA_ERR_INVALID_ARGUMENT, "empty token sequence");
-        const int32_t pos = read_pos(q);
-        if (pos + n > q->cfg.capacity)
-            return fail(YUUKA_ERR_INVALID_ARGUMENT, "token sequence of %d exceeds remaining context %d", n,
-                        q->cfg.capacity - pos);
-        for (int i = 0; i < n; i++)
-            if (tokens[i] < 0 || tokens[i] >= q->cfg.vocab)
-                return fail(YUUKA_ERR_INVALID_ARGUMENT, "token id %d is out of range", tokens[i]);
-        int done = 0;
-        while (done < n) {
-            const int rows = std::min(n - done, q->cfg.max_rows);
-            std::memcpy(q->pinned, tokens + done, (size_t)rows * 4);
-            yuuka_status st = run_step(q, rows, 1, nullptr);
+        return prefill_request(q, 0, tokens, n, last_logits);
+    });
+}
+
+yuuka_status yuuka_q35_prefill_request(yuuka_q35 *q, int32_t request, const int32_t *tokens, int32_t n,
+                                       float *last_logits) {
+    return guard("q35_prefill_request", [&]() -> yuuka_status {
+        if (!q || (!tokens && n)) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        if (request < 0 || request >= q->B) return fail(YUUKA_ERR_INVALID_ARGUMENT, "bad request index");
+        return prefill_request(q, request, tokens, n, last_logits);
+    });
+}
+
+yuuka_status yuuka_q35_fork(yuuka_q35 *q, int32_t src, int32_t dst) {
+    return guard("q35_fork", [&]() -> yuuka_status {
+        if (!q || src < 0 || dst < 0 || src >= q->B || dst >= q->B || src == dst)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "bad request indices");
+        yuuka_status st = reset_request(q, dst);
+        if (st != YUUKA_OK) return st;
+        const int32_t pos = q->req[src].pos, bs = q->cfg.block_size;
+        const int full = pos / bs;
+        hipStream_t s = q->stream->stream;
+        Request &d = q->req[dst];
+        for (int i = 0; i < full; i++) {  // memory/prefix.go: shared blocks, one more reference each
+            const int32_t blk = q->req[src].blocks[i];
+            q->refs[blk]++;
+            d.blocks.push_back(blk);
+        }
+        if (pos % bs) {  // the partial last block is copied: both requests write past it
+            st = ensure_blocks(q, dst, pos);
             if (st != YUUKA_OK) return st;
-            done += rows;
+            const int32_t from = q->req[src].blocks[full], to = d.blocks[full];
+            const uint64_t kvdim = (uint64_t)q->cfg.kv_heads * q->cfg.head_dim;
+            const uint64_t blk_bytes = (uint64_t)bs * kvdim * (q->cfg.kv_dtype == YUUKA_DTYPE_F16 ? 2 : 4);
+            for (auto &L : q->layers) {
+                if (L.recurrent) continue;
+                for (yuuka_buffer *pool : {L.kpool, L.vpool}) {
+                    uint8_t *base = static_cast<uint8_t *>(pool->ptr);
+                    (void)hipMemcpyAsync(base + (uint64_t)to * blk_bytes, base + (uint64_t)from * blk_bytes, blk_bytes,
+                                         hipMemcpyDeviceToDevice, s);
+                }
+            }
         }
-        if (last_logits) {
-            hipError_t err = hipMemcpy(last_logits,
-                                       static_cast<float *>(q->logits->ptr) + (uint64_t)(q->last_rows - 1) * q->cfg.vocab,
-                                       (size_t)q->cfg.vocab * 4, hipMemcpyDeviceToHost);
-            if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "logits copy: %s", yk::hip_error(err));
+        st = upload_table(q, dst);
+        if (st != YUUKA_OK) return st;
+        for (auto &L : q->layers) {
+            if (!L.recurrent) continue;
+            uint8_t *cs = static_cast<uint8_t *>(L.conv_state->ptr), *ms = static_cast<uint8_t *>(L.mat_state->ptr);
+            (void)hipMemcpyAsync(cs + (uint64_t)dst * L.conv_bytes, cs + (uint64_t)src * L.conv_bytes, L.conv_bytes,
+                                 hipMemcpyDeviceToDevice, s);
+            (void)hipMemcpyAsync(ms + (uint64_t)dst * L.mat_bytes, ms + (uint64_t)src * L.mat_bytes, L.mat_bytes,
+                                 hipMemcpyDeviceToDevice, s);
         }
+        uint8_t *dy = static_cast<uint8_t *>(q->dyn->ptr);
+        (void)hipMemcpyAsync(dy + (uint64_t)dst * 8, dy + (uint64_t)src * 8, 8, hipMemcpyDeviceToDevice, s);
+        hipError_t err = hipStreamSynchronize(s);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "fork: %s", yk::hip_error(err));
+        d.pos = pos;
         return YUUKA_OK;
     });
 }
@@ -611,34 +914,42 @@ yuuka_status yuuka_q35_verify(yuuka_q35 *q, const int32_t *tokens, int32_t rows,
                               int32_t *result) {
     return guard("q35_verify", [&]() -> yuuka_status {
         if (!q || !tokens || !accept) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
-        if (rows < 1 || rows > q->cfg.max_rows)
-            return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify rows %d outside 1..%d", rows, q->cfg.max_rows);
-        for (int i = 0; i < rows; i++)
-            if (tokens[i] < 0 || tokens[i] >= q->cfg.vocab)
-                return fail(YUUKA_ERR_INVALID_ARGUMENT, "token id %d is out of range", tokens[i]);
-        if (read_pos(q) + rows > q->cfg.capacity) return fail(YUUKA_ERR_INVALID_ARGUMENT, "context capacity exhausted");
-        if (!q->accept_set || !same_accept(*accept, q->accept_cfg)) {
-            // acceptance settings are baked into the captured graphs
-            for (auto it = q->plans.begin(); it != q->plans.end();) {
-                if (it->first.second == 0) {
-                    yuuka_graph_destroy(it->second.graph);
-                    yuuka_plan_destroy(it->second.plan);
-                    it = q->plans.erase(it);
-                } else {
-                    ++it;
-                }
-            }
-            q->accept_cfg = *accept;
-            q->accept_set = true;
-        }
-        std::memcpy(q->pinned, tokens, (size_t)rows * 4);
-        return run_step(q, rows, 0, result);
+        if (rows < 1 || rows > q->MR)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify rows %d outside 1..%d", rows, q->MR);
+        yuuka_status st = check_tokens(q, tokens, (size_t)rows);
+        if (st != YUUKA_OK) return st;
+        if (q->req[0].pos + rows > q->cfg.capacity)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "context capacity exhausted");
+        set_accept(q, *accept);
+        std::memcpy(pin_tokens(q), tokens, (size_t)rows * 4);
+        return run_step(q, PlanKey{0, 1, rows, 0, 0}, result);
+    });
+}
+
+yuuka_status yuuka_q35_step_batch(yuuka_q35 *q, int32_t n_req, const int32_t *tokens, int32_t rows, int32_t mode,
+                                  const yuuka_q35_accept *accept, const int32_t *forced, int32_t *result) {
+    return guard("q35_step_batch", [&]() -> yuuka_status {
+        if (!q || !tokens) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        if (n_req < 1 || n_req > q->B) return fail(YUUKA_ERR_INVALID_ARGUMENT, "requests %d outside 1..%d", n_req, q->B);
+        if (rows < 1 || rows > q->MR) return fail(YUUKA_ERR_INVALID_ARGUMENT, "rows %d outside 1..%d", rows, q->MR);
+        if (mode != 0 && mode != 1) return fail(YUUKA_ERR_INVALID_ARGUMENT, "mode %d", mode);
+        if (mode == 0 && !accept) return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify needs acceptance settings");
+        yuuka_status st = check_tokens(q, tokens, (size_t)n_req * rows);
+        if (st != YUUKA_OK) return st;
+        for (int r = 0; r < n_req; r++)
+            if (q->req[r].pos + rows > q->cfg.capacity)
+                return fail(YUUKA_ERR_INVALID_ARGUMENT, "request %d: context capacity exhausted", r);
+        if (mode == 0) set_accept(q, *accept);
+        std::memcpy(pin_tokens(q), tokens, (size_t)n_req * rows * 4);
+        const bool use_forced = mode == 0 && forced != nullptr;
+        if (use_forced) std::memcpy(pin_forced(q), forced, (size_t)n_req * 4);
+        return run_step(q, PlanKey{0, n_req, rows, mode, use_forced ? 1 : 0}, result);
     });
 }
 
 yuuka_status yuuka_q35_logits(yuuka_q35 *q, float *out, int32_t rows) {
     return guard("q35_logits", [&]() -> yuuka_status {
-        if (!q || !out || rows < 1 || rows > q->cfg.max_rows) return fail(YUUKA_ERR_INVALID_ARGUMENT, "bad arguments");
+        if (!q || !out || rows < 1 || rows > q->M) return fail(YUUKA_ERR_INVALID_ARGUMENT, "bad arguments");
         hipError_t err = hipMemcpy(out, q->logits->ptr, (size_t)rows * q->cfg.vocab * 4, hipMemcpyDeviceToHost);
         if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "logits copy: %s", yk::hip_error(err));
         return YUUKA_OK;
@@ -649,7 +960,7 @@ uint64_t yuuka_q35_snapshot_bytes(const yuuka_q35 *q) {
     if (!q) return 0;
     uint64_t n = 0;
     for (auto &L : q->layers)
-        if (L.recurrent) n += L.conv_state->bytes + L.mat_state->bytes;
+        if (L.recurrent) n += L.conv_bytes + L.mat_bytes;
     return n;
 }
 
@@ -659,14 +970,13 @@ yuuka_status yuuka_q35_snapshot(yuuka_q35 *q, void *out, int32_t *position) {
         uint8_t *p = static_cast<uint8_t *>(out);
         for (auto &L : q->layers) {
             if (!L.recurrent) continue;
-            yuuka_status st = yuuka_memcpy_d2h(p, L.conv_state, L.conv_state->bytes);
-            if (st != YUUKA_OK) return st;
-            p += L.conv_state->bytes;
-            st = yuuka_memcpy_d2h(p, L.mat_state, L.mat_state->bytes);
-            if (st != YUUKA_OK) return st;
-            p += L.mat_state->bytes;
+            hipError_t err = hipMemcpy(p, L.conv_state->ptr, L.conv_bytes, hipMemcpyDeviceToHost);
+            p += L.conv_bytes;
+            if (err == hipSuccess) err = hipMemcpy(p, L.mat_state->ptr, L.mat_bytes, hipMemcpyDeviceToHost);
+            p += L.mat_bytes;
+            if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "snapshot: %s", yk::hip_error(err));
         }
-        if (position) *position = read_pos(q);
+        if (position) *position = read_pos(q, 0);
         return YUUKA_OK;
     });
 }
@@ -682,15 +992,21 @@ yuuka_status yuuka_q35_restore(yuuka_q35 *q, const void *data, uint64_t bytes, i
         const uint8_t *p = static_cast<const uint8_t *>(data);
         for (auto &L : q->layers) {
             if (!L.recurrent) continue;
-            yuuka_status st = yuuka_memcpy_h2d(L.conv_state, p, L.conv_state->bytes);
-            if (st != YUUKA_OK) return st;
-            p += L.conv_state->bytes;
-            st = yuuka_memcpy_h2d(L.mat_state, p, L.mat_state->bytes);
-            if (st != YUUKA_OK) return st;
-            p += L.mat_state->bytes;
+            hipError_t err = hipMemcpy(L.conv_state->ptr, p, L.conv_bytes, hipMemcpyHostToDevice);
+            p += L.conv_bytes;
+            if (err == hipSuccess) err = hipMemcpy(L.mat_state->ptr, p, L.mat_bytes, hipMemcpyHostToDevice);
+            p += L.mat_bytes;
+            if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "restore: %s", yk::hip_error(err));
         }
+        // the KV rows up to `position` stay where they are (state.go:230-263
+        // restores the recurrent state only; the KV cache is position-indexed)
+        yuuka_status st = ensure_blocks(q, 0, position);
+        if (st != YUUKA_OK) return st;
+        q->req[0].pos = position;
         int32_t d[2] = {0, position};
-        return yuuka_memcpy_h2d(q->dyn, d, 8);
+        hipError_t err = hipMemcpy(q->dyn->ptr, d, 8, hipMemcpyHostToDevice);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "restore: %s", yk::hip_error(err));
+        return YUUKA_OK;
     });
 }
 
@@ -706,16 +1022,19 @@ yuuka_status yuuka_q35_generate(yuuka_q35 *q, const int32_t *prompt, int32_t n_p
                         q->cfg.capacity);
         // speculative.go:21-34 normalize, capped by the engine's row block
         int k = o->max_draft <= 0 ? 4 : std::min(o->max_draft, 16);
-        k = std::min(k, q->cfg.max_rows - 1);
+        k = std::min(k, q->MR - 1);
         int min_match = o->min_match <= 0 ? 2 : std::min(o->min_match, 8);
         int max_tokens = std::min(o->max_tokens, q->cfg.capacity - n_prompt);
         if (max_tokens <= 0) return fail(YUUKA_ERR_INVALID_ARGUMENT, "no context space remains");
         yuuka_q35_generate_stats st_local{};
-        yuuka_status st = yuuka_q35_reset(q);
+        yuuka_status st = reset_request(q, 0);
         if (st != YUUKA_OK) return st;
+        // a generation starts its Philox step counter at 0
+        hipError_t err0 = hipMemset(q->step->ptr, 0, 8);
+        if (err0 != hipSuccess) return fail(YUUKA_ERR_DEVICE, "step counter: %s", yk::hip_error(err0));
         auto t0 = std::chrono::steady_clock::now();
         if (n_prompt > 1) {
-            st = yuuka_q35_prefill(q, prompt, n_prompt - 1, nullptr);
+            st = prefill_request(q, 0, prompt, n_prompt - 1, nullptr);
             if (st != YUUKA_OK) return st;
         }
         auto t1 = std::chrono::steady_clock::now();
@@ -723,13 +1042,13 @@ yuuka_status yuuka_q35_generate(yuuka_q35 *q, const int32_t *prompt, int32_t n_p
         int32_t pending = prompt[n_prompt - 1];
         int emitted = 0;
         bool stop = false;
-        std::vector<int32_t> rows_tok(17);
+        std::vector<int32_t> rows_tok(33);
         while (emitted < max_tokens && !stop) {
-            const int32_t pos = read_pos(q);
+            const int32_t pos = q->req[0].pos;
             int limit = std::min(k, max_tokens - emitted);
             limit = std::min(limit, q->cfg.capacity - pos - 1);
             if (limit < 0) break;
-            int32_t draft[16];
+            int32_t draft[32];
             int nd = lookup_draft(history, limit, min_match, draft);
             for (int i = nd; i < limit; i++) draft[i] = pending;  // padding guess
             rows_tok[0] = pending;

@@ -83,7 +83,8 @@ hipError_t launch_cast_f16(const float *src, uint16_t *dst, uint64_t n, hipStrea
 uint64_t accept_scratch_bytes(const yuuka_accept_params &p);
 hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int32_t *result,
                                 double *debug, const yuuka_accept_params &p, void *scratch,
-                                hipStream_t stream, const uint64_t *step_dev = nullptr);
+                                hipStream_t stream, const uint64_t *step_dev = nullptr, uint32_t draft_stride = 0,
+                                const int32_t *forced = nullptr);
 
 // ----------------------------------------------------------- small ops
 hipError_t launch_add_f32(float *dst, const float *a, const float *b, uint64_t n,

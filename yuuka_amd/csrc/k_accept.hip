@@ -41,6 +41,7 @@ __device__ __forceinline__ bool beats(float av, int ai, float bv, int bi) {
 struct Geo {
     int B, R, k, V, C, L;
     uint64_t stride;
+    int ds;  // int32 elements between consecutive requests' drafts
 };
 
 __device__ __forceinline__ const float *row_ptr(const float *logits, const Geo &g, int b, int row) {
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(256) void accept_weights_kernel(const float *__rest
     __syncthreads();
     const float mx = mx_s;
     const Cut cut = row_cut(cuts, g, b, row);
-    const int d = row < g.k ? drafts[(uint64_t)b * g.k + row] : -1;
+    const int d = row < g.k ? drafts[(uint64_t)b * g.ds + row] : -1;
     const int begin = c * g.L;
     const int end = min(begin + g.L, g.V);
     double acc = 0.0;
@@ -488,7 +489,7 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
     const double *__restrict__ wdraft, const Cut *__restrict__ cuts, int stochastic, double t, uint64_t seed,
     uint64_t step,
     uint32_t request_base, int32_t *__restrict__ result, double *__restrict__ debug,
-    const uint64_t *__restrict__ step_dev) {
+    const uint64_t *__restrict__ step_dev, const int32_t *__restrict__ forced) {
     const int b = blockIdx.x;
     if (step_dev) step = *step_dev;
     const uint32_t request = request_base + (uint32_t)b;
@@ -539,11 +540,14 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
             if (p[0] != p[0]) best = Stat{p[0], 0};  // argmaxLogit keeps a NaN at index 0
             best_s = best;
             if (row == 0) argmax0 = best.i;
-            const int d = row < g.k ? drafts[(uint64_t)b * g.k + row] : -1;
+            const int d = row < g.k ? drafts[(uint64_t)b * g.ds + row] : -1;
             double dbg[4] = {0.0, 0.0, 0.0, (double)best.v};
             action = 1;
+            // forced: a prescribed acceptance length replaces the accept test;
+            // the token at the first rejected row is still the mode's choice
+            const int flen = forced ? forced[b] : -1;
             if (!stochastic) {
-                if (row < g.k && best.i == d) {
+                if (row < g.k && (forced ? row < flen : best.i == d)) {
                     action = 0;
                 } else {
                     decided_next = best.i;
@@ -565,7 +569,7 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
                     const double u = draw(seed, step, (uint32_t)row, request, 0);
                     dbg[0] = pd;
                     dbg[1] = u;
-                    if (u < pd) {
+                    if (forced ? row < flen : u < pd) {
                         action = 0;
                     } else if (onehot || !(rest > 0.0)) {
                         decided_next = sb.i;
@@ -614,7 +618,7 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
             continue;
         }
         if (action == 2) {
-            const int d = row < g.k ? drafts[(uint64_t)b * g.k + row] : -1;
+            const int d = row < g.k ? drafts[(uint64_t)b * g.ds + row] : -1;
             const int j = scan_chunk(p, g, cstar, d, mx_s, t, row_cut(cuts, g, b, row), target_s, prefix, &pick);
             if (threadIdx.x == 0) decided_next = j >= 0 ? j : best_s.i;
         }
@@ -637,6 +641,7 @@ Geo make_geo(const yuuka_accept_params &p) {
     g.R = g.k + 1;
     g.V = (int)p.vocab;
     g.stride = p.row_stride ? p.row_stride : p.vocab;
+    g.ds = g.k;
     int c = (2048 + g.B * g.R - 1) / (g.B * g.R);
     c = c < 1 ? 1 : (c > 256 ? 256 : c);
     int L = (g.V + c - 1) / c;
@@ -656,8 +661,10 @@ uint64_t accept_scratch_bytes(const yuuka_accept_params &p) {
 
 hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int32_t *result,
                                 double *debug, const yuuka_accept_params &p, void *scratch,
-                                hipStream_t stream, const uint64_t *step_dev) {
-    const Geo g = make_geo(p);
+                                hipStream_t stream, const uint64_t *step_dev, uint32_t draft_stride,
+                                const int32_t *forced) {
+    Geo g = make_geo(p);
+    if (draft_stride) g.ds = (int)draft_stride;
     const uint64_t n = (uint64_t)g.B * g.R * g.C;
     auto *base = static_cast<uint8_t *>(scratch);
     Stat *stats = reinterpret_cast<Stat *>(base);
@@ -680,7 +687,7 @@ hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int3
         accept_weights_kernel<<<grid, 256, 0, stream>>>(logits, g, drafts, stats, cut_arg, t, sums, wdraft);
     accept_finalize_kernel<<<(unsigned)g.B, 256, 0, stream>>>(logits, g, drafts, stats, sums, wdraft, cut_arg,
                                                              stochastic ? 1 : 0, t, p.seed, p.step,
-                                                             p.request_base, result, debug, step_dev);
+                                                             p.request_base, result, debug, step_dev, forced);
     return hipGetLastError();
 }
 

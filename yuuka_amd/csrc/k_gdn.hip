@@ -287,12 +287,13 @@ __device__ __forceinline__ double wave_sum_dpp(double v) {
 
 // Causal conv + SiLU of two channels (c1 < 0: one) with every input load
 // issued before either is computed.
+template <int RC>  // row capacity: rows <= RC
 __device__ __forceinline__ void conv_channel2(const float *conv_state, const float *qkv, const float *conv_w,
                                               const GdnArgs &g, int c0, float *dst0, int stride0, int c1, float *dst1,
                                               int stride1) {
     const int R = g.rows, K = g.kernel;
     const int cc[2] = {c0, c1 < 0 ? c0 : c1};
-    float w[2][8], st[2][8], x[2][16];
+    float w[2][8], st[2][8], x[2][RC];
 #pragma unroll
     for (int u = 0; u < 2; u++) {
 #pragma unroll
@@ -301,7 +302,7 @@ __device__ __forceinline__ void conv_channel2(const float *conv_state, const flo
             st[u][i] = i < K - 1 ? conv_state[(uint64_t)cc[u] * (K - 1) + i] : 0.0f;
         }
 #pragma unroll
-        for (int r = 0; r < 16; r++) x[u][r] = r < R ? qkv[(uint64_t)r * g.conv_dim + cc[u]] : 0.0f;
+        for (int r = 0; r < RC; r++) x[u][r] = r < R ? qkv[(uint64_t)r * g.conv_dim + cc[u]] : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < 2; u++) {
@@ -309,7 +310,7 @@ __device__ __forceinline__ void conv_channel2(const float *conv_state, const flo
         float *dst = u == 0 ? dst0 : dst1;
         const int stride = u == 0 ? stride0 : stride1;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
+        for (int r = 0; r < RC; r++) {
             if (r >= R) break;
             float sum = 0.0f;
 #pragma unroll
@@ -318,7 +319,7 @@ __device__ __forceinline__ void conv_channel2(const float *conv_state, const flo
                 const int idx = r + tt - (K - 1);
                 float xv = 0.0f;
 #pragma unroll
-                for (int q = 0; q < 16; q++)
+                for (int q = 0; q < RC; q++)
                     if (q == idx) xv = x[u][q];
 #pragma unroll
                 for (int q = 0; q < 7; q++)
@@ -346,13 +347,14 @@ __device__ uint64_t *yk_gd_dbg;
 #define YK_GD_STAMP(i) (void)0
 #endif
 constexpr int kCols = 32;
-constexpr int kMaxRows = 16;  // verify rows of one step
+constexpr int kMaxRows = 32;  // verify rows of one step (k <= 31 drafts)
 constexpr int kColThreads = 256;
 
 // Verify: conv + SiLU + L2 norm of the head's q / k channels and this
 // block's v channels, then the delta rule over the rows for this block's
 // columns. Writes the raw outputs (the gated norm runs in the consumer) and
 // the conv outputs for the commit; the states are left untouched.
+template <int RC>
 __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
     const float *__restrict__ conv_state, const float *__restrict__ state, const float *__restrict__ qkv,
     const float *__restrict__ alpha_raw, const float *__restrict__ beta_raw, const float *__restrict__ conv_w,
@@ -387,7 +389,7 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
         const int which = t >> 7, cc = t & (kS - 1);
         const int c0 = (which == 0 ? 0 : key_dim) + kh * kS + cc;
         const int c1 = t < kCols ? 2 * key_dim + h * kS + cb * kCols + t : -1;
-        conv_channel2(conv_state, qkv, conv_w, g, c0, qk + which * kS + cc, 2 * kS, c1, vv + t, kCols);
+        conv_channel2<RC>(conv_state, qkv, conv_w, g, c0, qk + which * kS + cc, 2 * kS, c1, vv + t, kCols);
     }
     YK_GD_STAMP(1);
     __syncthreads();
@@ -546,8 +548,13 @@ hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, c
                                   const float *alpha_raw, const float *beta_raw, const float *conv_w, const float *dt,
                                   const float *a_log, float *raw_out, float *conv_out, const GdnArgs &g,
                                   hipStream_t s) {
-    gdn_verify_cols_kernel<<<dim3((unsigned)g.rank, kS / kCols), kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
-        conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
+    const dim3 grid((unsigned)g.rank, kS / kCols);
+    if (g.rows <= 16)
+        gdn_verify_cols_kernel<16><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
+            conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
+    else
+        gdn_verify_cols_kernel<kMaxRows><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
+            conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
     return hipGetLastError();
 }
 

@@ -22,6 +22,13 @@ static ModelDyn dyn_of(const ExecCtx &ctx) {
     return ModelDyn{ctx.dyn ? const_cast<int32_t *>(ctx.dyn) + 1 : nullptr, (int32_t)ctx.position};
 }
 
+// YUUKA_EXT_FLAG_OWN_POS: the op reads its position from its own {token,
+// position} buffer in buf15 (one request of a batched plan).
+static ModelDyn dyn_of(const ExecCtx &ctx, const yuuka_op &op) {
+    if ((op.flags & YUUKA_EXT_FLAG_OWN_POS) && op.buf[15]) return ModelDyn{at<int32_t>(op, 15) + 1, 0};
+    return dyn_of(ctx);
+}
+
 static uint32_t kv_fmt(uint32_t dtype, bool *ok) {
     *ok = dtype == YUUKA_DTYPE_F32 || dtype == YUUKA_DTYPE_F16;
     return dtype == YUUKA_DTYPE_F16 ? 1u : 0u;
@@ -153,7 +160,7 @@ bool op_uses_position(const yuuka_op &op) {
     case YUUKA_OP_ATTENTION_PREFILL_PAGED:
     case YUUKA_EXT_OP_ROPE_TABLE:
     case YUUKA_EXT_OP_ATTN_VERIFY:
-        return true;
+        return !(op.flags & YUUKA_EXT_FLAG_OWN_POS);
     default:
         return false;
     }
@@ -257,6 +264,8 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         return YUUKA_OK;
     }
     case YUUKA_EXT_OP_ROPE_TABLE: {
+        if ((op.flags & YUUKA_EXT_FLAG_OWN_POS) && (!buf_ok(op.buf[15], op.off[15], 8) || op.off[15] % 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "ROPE_TABLE: own position buffer");
         const uint64_t rows = op.n[0], rot = op.n[1];
         if (!rows || rows > 4096 || !rot || rot % 2 || rot > 128 || op.off[0] % 8 ||
             !buf_ok(op.buf[0], op.off[0], rows * (rot / 2) * 8))
@@ -264,6 +273,8 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         return YUUKA_OK;
     }
     case YUUKA_EXT_OP_ATTN_VERIFY: {
+        if ((op.flags & YUUKA_EXT_FLAG_OWN_POS) && (!buf_ok(op.buf[15], op.off[15], 8) || op.off[15] % 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "ATTN_VERIFY: own position buffer");
         const AttnVArgs a = attnv_args(op);
         bool ok;
         kv_fmt(op.u[2], &ok);
@@ -306,6 +317,8 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
             !buf_ok(op.buf[4], op.off[4], R * g.rank * 4) || !buf_ok(op.buf[5], op.off[5], R * g.rank * 4) ||
             !buf_ok(op.buf[10], op.off[10], R * g.inner * 4) || !buf_ok(op.buf[11], op.off[11], R * g.conv_dim * 4))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "recurrent chunk buffers too small");
+        if ((op.flags & YUUKA_EXT_FLAG_RAW_OUT) && (!(op.flags & YUUKA_EXT_FLAG_DEFER) || R > 32))
+            return fail(YUUKA_ERR_UNSUPPORTED, "recurrent chunk: raw outputs need the deferred mode and <= 32 rows");
         *ws = R * g.inner * 4;  // raw per-head outputs before the gated norm
         return YUUKA_OK;
     }
@@ -377,14 +390,17 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         p.vocab = (uint32_t)op.n[2];
         p.row_stride = op.n[3];
         if ((p.mode != YUUKA_ACCEPT_GREEDY && p.mode != YUUKA_ACCEPT_STOCHASTIC) || !p.batch || !p.vocab ||
-            p.drafts > 255)
+            p.drafts > 255 || (op.u[3] && op.u[3] < p.drafts))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid ACCEPT parameters");
+        const uint64_t dstride = op.u[3] ? op.u[3] : p.drafts;
+        if (op.buf[5] && !buf_ok(op.buf[5], op.off[5], (uint64_t)p.batch * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "ACCEPT forced lengths buffer too small");
         if (p.mode == YUUKA_ACCEPT_STOCHASTIC && !(op.f[1] >= 0.0f && op.f[1] <= 1.0f))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "ACCEPT: top-p must be in [0,1]");
         const uint64_t stride = p.row_stride ? p.row_stride : p.vocab;
         const uint64_t rows = (uint64_t)p.batch * (p.drafts + 1);
         if (!buf_ok(op.buf[0], op.off[0], ((rows - 1) * stride + p.vocab) * 4) ||
-            (p.drafts && !buf_ok(op.buf[1], op.off[1], (uint64_t)p.batch * p.drafts * 4)) ||
+            (p.drafts && !buf_ok(op.buf[1], op.off[1], ((uint64_t)p.batch - 1) * dstride * 4 + p.drafts * 4)) ||
             !buf_ok(op.buf[2], op.off[2], (uint64_t)p.batch * 16))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "ACCEPT buffers too small");
         *ws = accept_scratch_bytes(p);
@@ -465,7 +481,8 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         return YUUKA_OK;
     }
     case YUUKA_EXT_OP_ADVANCE:
-        if (!op.buf[0] || op.buf[0]->bytes < 8 || !op.buf[1] || op.n[0] == 0)
+        if (!buf_ok(op.buf[0], op.off[0], 8) || op.off[0] % 4 || !buf_ok(op.buf[1], op.off[1], 8) || op.n[0] == 0 ||
+            (op.buf[2] && !buf_ok(op.buf[2], op.off[2], 8)))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid ADVANCE buffers");
         return YUUKA_OK;
     default:
@@ -476,7 +493,7 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
 int gdn_commit_run(const yuuka_op *ops, int count) {
     if (count < 2 || ops[0].code != YUUKA_EXT_OP_GDN_COMMIT || getenv("YUUKA_GDN_SPLIT")) return 1;
     const GdnArgs g0 = gdn_args(ops[0]);
-    if (g0.rows > 16) return 1;
+    if (g0.rows > 32) return 1;
     int n = 1;
     while (n < count && n < kGdnCommitMaxLayers && ops[n].code == YUUKA_EXT_OP_GDN_COMMIT &&
            ops[n].flags == ops[0].flags && ops[n].buf[8] == ops[0].buf[8] && ops[n].off[8] == ops[0].off[8]) {
@@ -541,22 +558,24 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
     }
     case YUUKA_OP_ATTENTION_PREFILL_PAGED: {
         const AttnArgs a = attn_args(op);
-        const int hint = ctx.dyn ? -1 : (int)ctx.position + a.displacement + a.rows - 1;
+        const bool own = (op.flags & YUUKA_EXT_FLAG_OWN_POS) != 0;
+        const int hint = ctx.dyn || own ? -1 : (int)ctx.position + a.displacement + a.rows - 1;
         err = launch_attention(at<const float>(op, 0), at<const uint8_t>(op, 1), at<const uint8_t>(op, 2),
                                at<const int32_t>(op, 4), at<float>(op, 3), a, ctx.ws, dyn_of(ctx), hint, s);
         break;
     }
     case YUUKA_EXT_OP_ROPE_TABLE:
-        err = launch_rope_table(at<float2>(op, 0), (int)op.n[0], (int)op.n[1], (double)op.f[0], dyn_of(ctx),
+        err = launch_rope_table(at<float2>(op, 0), (int)op.n[0], (int)op.n[1], (double)op.f[0], dyn_of(ctx, op),
                                 (int)op.n[2], s);
         break;
     case YUUKA_EXT_OP_ATTN_VERIFY: {
         const AttnVArgs a = attnv_args(op);
-        const int hint = ctx.dyn ? -1 : (int)ctx.position + a.displacement + a.rows - 1;
+        const bool own = (op.flags & YUUKA_EXT_FLAG_OWN_POS) != 0;
+        const int hint = ctx.dyn || own ? -1 : (int)ctx.position + a.displacement + a.rows - 1;
         err = launch_attn_verify(at<const float>(op, 0), at<const float>(op, 1), at<const float>(op, 2),
                                  at<uint8_t>(op, 3), at<uint8_t>(op, 4), at<const int32_t>(op, 6),
                                  at<const float>(op, 7), at<const float>(op, 8), at<const float2>(op, 9),
-                                 at<float>(op, 5), a, ctx.ws, dyn_of(ctx), hint, s);
+                                 at<float>(op, 5), a, ctx.ws, dyn_of(ctx, op), hint, s);
         break;
     }
     case YUUKA_OP_RECURRENT_CHUNK: {
@@ -564,7 +583,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
         const bool defer = (op.flags & YUUKA_EXT_FLAG_DEFER) != 0;
         float *conv = at<float>(op, 11);
         float *raw = static_cast<float *>(ctx.ws);
-        if (defer && (op.flags & YUUKA_EXT_FLAG_RAW_OUT) && g.rows <= 16) {  // column-split scan (k_gdn.hip)
+        if (defer && (op.flags & YUUKA_EXT_FLAG_RAW_OUT) && g.rows <= 32) {  // column-split scan (k_gdn.hip)
             err = launch_gdn_verify_cols(at<const float>(op, 0), at<const float>(op, 1), at<const float>(op, 2),
                                          at<const float>(op, 4), at<const float>(op, 5), at<const float>(op, 6),
                                          at<const float>(op, 7), at<const float>(op, 8), at<float>(op, 10), conv, g, s);
@@ -617,13 +636,14 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
         p.temperature = op.f[0];
         p.top_p = op.f[1];
         err = launch_verify_accept(at<const float>(op, 0), at<const int32_t>(op, 1), at<int32_t>(op, 2),
-                                   at<double>(op, 3), p, ctx.ws, s, at<const uint64_t>(op, 4));
+                                   at<double>(op, 3), p, ctx.ws, s, at<const uint64_t>(op, 4), op.u[3],
+                                   at<const int32_t>(op, 5));
         break;
     }
     case YUUKA_EXT_OP_GDN_COMMIT: {
         const GdnArgs g = gdn_args(op);
         const int32_t *res = at<const int32_t>(op, 8);
-        if (!getenv("YUUKA_GDN_SPLIT") && g.rows <= 16) {  // scan replay + conv window, column-split (k_gdn.hip)
+        if (!getenv("YUUKA_GDN_SPLIT") && g.rows <= 32) {  // scan replay + conv window, column-split (k_gdn.hip)
             err = launch_gdn_commit_cols(at<float>(op, 0), at<float>(op, 1), at<const float>(op, 2), at<const float>(op, 3),
                                     at<const float>(op, 4), at<const float>(op, 5), at<const float>(op, 6),
                                     at<const float>(op, 7), g, res, s);
@@ -676,7 +696,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
                                  (int)op.n[2], (int)op.n[0], at<const float>(op, 3), at<const float>(op, 4), s);
         break;
     case YUUKA_EXT_OP_ADVANCE: {
-        ModelDyn d{static_cast<int32_t *>(op.buf[0]->ptr) + 1, 0};
+        ModelDyn d{at<int32_t>(op, 0) + 1, 0};
         err = launch_advance(d, at<const int32_t>(op, 1), (int)op.n[0], at<uint64_t>(op, 2), s);
         break;
     }

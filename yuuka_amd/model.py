@@ -38,6 +38,12 @@ class Q35Config:
     block_size: int = 16
     kv_dtype: int = F16
     max_rows: int = 16
+    batch: int = 1
+    kv_blocks: int = 0
+    n_experts: int = 0
+    n_experts_used: int = 0
+    expert_ffn: int = 0
+    shared_ffn: int = 0
 
     @property
     def inner(self) -> int:
@@ -56,18 +62,35 @@ class Q35Config:
 QWEN35_4B_LIKE = Q35Config(n_layers=32, hidden=2560, ffn=9216, heads=16, kv_heads=4, head_dim=256,
                            rope_dim=64, vocab=151936, groups=16, rank=16, capacity=1024)
 
+# Qwen3.5-9B-like hybrid decoder (hidden 4096, FFN
+# 12288, 16 Q / 4 KV heads of 256; GDN with 16 heads of 128).
+QWEN35_9B_LIKE = Q35Config(n_layers=32, hidden=4096, ffn=12288, heads=16, kv_heads=4, head_dim=256,
+                           rope_dim=64, vocab=151936, groups=16, rank=16, capacity=16384 + 64)
+
+# Qwen3.5-MoE-like decoder (hidden 2048, 40 layers,
+# 256 experts, top-8, expert FFN 512, one shared expert of 512).
+QWEN35_MOE_LIKE = Q35Config(n_layers=40, hidden=2048, ffn=0, heads=16, kv_heads=4, head_dim=256, rope_dim=64,
+                            vocab=151936, groups=16, rank=16, capacity=2048 + 64, n_experts=256,
+                            n_experts_used=8, expert_ffn=512, shared_ffn=512)
+
 # Small geometry for parity tests (every matrix width a multiple of 256).
 TINY = Q35Config(n_layers=4, hidden=256, ffn=512, heads=2, kv_heads=1, head_dim=256, rope_dim=64,
                  vocab=1024, groups=1, rank=2, capacity=256)
+TINY_MOE = replace(TINY, ffn=0, n_experts=16, n_experts_used=4, expert_ffn=256, shared_ffn=256)
 
 
-def make_weights(cfg: Q35Config, seed: int = 0, q6_output: bool = True, q6_v: bool = True) -> dict:
+def make_weights(cfg: Q35Config, seed: int = 0, q6_output: bool = True, q6_v: bool = True,
+                 share_experts: bool = False) -> dict:
     """Seeded random-init weights: every 2-D matrix packed as Q4_K (Q6_K for
     the output head and attn_v, the Q4_K_M mix), dequantized std ~0.02;
     norm vectors near 1, conv weights and GDN dt/a chosen so the decay
-    exp(softplus(alpha + dt) * a) stays inside (0, 1)."""
+    exp(softplus(alpha + dt) * a) stays inside (0, 1). MoE layers: FP32
+    router scaled so router logits are ~N(0, 1), Q4_K experts and shared
+    expert. share_experts: every layer holds the same expert bytes (one host
+    copy; the engine still uploads one device copy per layer)."""
     rng = np.random.default_rng(seed)
     H, cd = cfg.hidden, cfg.conv_dim
+    shared = {}
 
     def mat(rows, cols, dtype=Q4_K):
         return dict(data=synth.quant_matrix(rng, dtype, rows, cols, model_scale=True), rows=rows, cols=cols,
@@ -92,7 +115,21 @@ def make_weights(cfg: Q35Config, seed: int = 0, q6_output: bool = True, q6_v: bo
             L.update(q=mat(cfg.heads * hd * 2, H), k=mat(cfg.kv_heads * hd, H),
                      v=mat(cfg.kv_heads * hd, H, Q6_K if q6_v else Q4_K), o=mat(H, cfg.heads * hd),
                      q_norm=norm(hd), k_norm=norm(hd))
-        L.update(ffn_gate=mat(cfg.ffn, H), ffn_up=mat(cfg.ffn, H), ffn_down=mat(H, cfg.ffn))
+        if cfg.n_experts:
+            E, ef, sf = cfg.n_experts, cfg.expert_ffn, cfg.shared_ffn
+            if share_experts and shared:
+                L.update(shared)
+            else:
+                ex = dict(gate_exps=mat(E * ef, H), up_exps=mat(E * ef, H), down_exps=mat(E * H, ef))
+                if share_experts:
+                    shared.update(ex)
+                L.update(ex)
+            L.update(router=dict(data=rng.normal(0, 1 / np.sqrt(H), (E, H)).astype(np.float32).view(np.uint8).ravel(),
+                                 rows=E, cols=H, dtype=F32),
+                     shared_gate_vec=rng.normal(0, 1 / np.sqrt(H), H).astype(np.float32),
+                     shared_gate=mat(sf, H), shared_up=mat(sf, H), shared_down=mat(H, sf))
+        else:
+            L.update(ffn_gate=mat(cfg.ffn, H), ffn_up=mat(cfg.ffn, H), ffn_down=mat(H, cfg.ffn))
         w["layers"].append(L)
     return w
 
@@ -114,7 +151,8 @@ class yuuka_q35_config(C.Structure):
                                          "rope_dim", "vocab", "conv_kernel", "state_size", "groups", "rank",
                                          "inner", "full_interval")] + [
         ("rope_base", C.c_double), ("eps", C.c_float), ("capacity", C.c_int32), ("block_size", C.c_int32),
-        ("kv_dtype", C.c_uint32), ("max_rows", C.c_int32)]
+        ("kv_dtype", C.c_uint32), ("max_rows", C.c_int32)] + [
+        (n, C.c_int32) for n in ("batch", "kv_blocks", "n_experts", "n_experts_used", "expert_ffn", "shared_ffn")]
 
 
 class yuuka_q35_tensor(C.Structure):
@@ -131,7 +169,10 @@ class yuuka_q35_layer_weights(C.Structure):
         [(n, _FP) for n in ("conv", "dt", "a", "ssm_norm")] + \
         [(n, yuuka_q35_tensor) for n in ("q", "k", "v", "o")] + \
         [("q_norm", _FP), ("k_norm", _FP)] + \
-        [(n, yuuka_q35_tensor) for n in ("ffn_gate", "ffn_up", "ffn_down")]
+        [(n, yuuka_q35_tensor) for n in ("ffn_gate", "ffn_up", "ffn_down", "router")] + \
+        [("shared_gate_vec", _FP)] + \
+        [(n, yuuka_q35_tensor) for n in ("shared_gate", "shared_up", "shared_down", "gate_exps", "up_exps",
+                                         "down_exps")]
 
 
 class yuuka_q35_weights(C.Structure):
@@ -178,9 +219,10 @@ def weights_struct(cfg: Q35Config, w: dict):
     for i, L in enumerate(w["layers"]):
         s = layers[i]
         s.attn_norm, s.post_norm = _ptr(L["attn_norm"]), _ptr(L["post_norm"])
-        for n in ("qkv", "gate", "out", "beta", "alpha", "q", "k", "v", "o", "ffn_gate", "ffn_up", "ffn_down"):
+        for n in ("qkv", "gate", "out", "beta", "alpha", "q", "k", "v", "o", "ffn_gate", "ffn_up", "ffn_down",
+                  "router", "shared_gate", "shared_up", "shared_down", "gate_exps", "up_exps", "down_exps"):
             setattr(s, n, _tensor(L.get(n)))
-        for n in ("conv", "dt", "a", "ssm_norm", "q_norm", "k_norm"):
+        for n in ("conv", "dt", "a", "ssm_norm", "q_norm", "k_norm", "shared_gate_vec"):
             if n in L:
                 setattr(s, n, _ptr(L[n]))
     ws = yuuka_q35_weights(_tensor(w["embedding"]), _tensor(w["output"]), _ptr(w["output_norm"]), layers)
@@ -204,6 +246,12 @@ def _declare(L):
         "yuuka_q35_restore": (C.c_int, [vp, vp, C.c_uint64, C.c_int32]),
         "yuuka_q35_generate": (C.c_int, [vp, vp, C.c_int32, C.POINTER(yuuka_q35_generate_opts), vp,
                                          C.POINTER(yuuka_q35_generate_stats)]),
+        "yuuka_q35_request_position": (C.c_int32, [vp, C.c_int32]),
+        "yuuka_q35_reset_request": (C.c_int, [vp, C.c_int32]),
+        "yuuka_q35_prefill_request": (C.c_int, [vp, C.c_int32, vp, C.c_int32, vp]),
+        "yuuka_q35_fork": (C.c_int, [vp, C.c_int32, C.c_int32]),
+        "yuuka_q35_step_batch": (C.c_int, [vp, C.c_int32, vp, C.c_int32, C.c_int32, C.POINTER(yuuka_q35_accept),
+                                           vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -256,6 +304,35 @@ class Engine:
         acc = accept or accept_struct()
         hip.check(hip.lib().yuuka_q35_verify(self.ptr, t.ctypes.data_as(C.c_void_p), t.size, C.byref(acc),
                                              res.ctypes.data_as(C.c_void_p)), "q35_verify")
+        return res
+
+    def request_position(self, r: int) -> int:
+        return int(hip.lib().yuuka_q35_request_position(self.ptr, r))
+
+    def reset_request(self, r: int):
+        hip.check(hip.lib().yuuka_q35_reset_request(self.ptr, r), "q35_reset_request")
+
+    def prefill_request(self, r: int, tokens, want_logits=False):
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.zeros(self.cfg.vocab, np.float32) if want_logits else None
+        hip.check(hip.lib().yuuka_q35_prefill_request(self.ptr, r, t.ctypes.data_as(C.c_void_p), t.size,
+                                                      None if out is None else out.ctypes.data_as(C.c_void_p)),
+                  "q35_prefill_request")
+        return out
+
+    def fork(self, src: int, dst: int):
+        hip.check(hip.lib().yuuka_q35_fork(self.ptr, src, dst), "q35_fork")
+
+    def step_batch(self, tokens, mode: int = 0, accept=None, forced=None):
+        """tokens [n_req][rows]; returns result [n_req][4] (mode 0)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        n_req, rows = t.shape
+        res = np.zeros((n_req, 4), np.int32)
+        acc = accept or accept_struct()
+        f = None if forced is None else np.ascontiguousarray(forced, np.int32)
+        hip.check(hip.lib().yuuka_q35_step_batch(self.ptr, n_req, t.ctypes.data_as(C.c_void_p), rows, mode,
+                                                 C.byref(acc), None if f is None else f.ctypes.data_as(C.c_void_p),
+                                                 res.ctypes.data_as(C.c_void_p)), "q35_step_batch")
         return res
 
     def logits(self, rows):
