@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the speculative verify path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|4|5]
 
 A step is one pass of the hot path over one synthetic batch, with every input
 already resident in HBM:
@@ -11,6 +11,9 @@ already resident in HBM:
             151936 tokens, fused greedy acceptance, on-device commit of the
             accepted prefix — as one captured HIP graph; drafts from prompt
             lookup over the history (engine/speculative.go lookupDraft).
+  config 3-5 (configs[2..4]): batched verify steps of the batched engine
+            (4B-like 16 x k=8 stochastic top-p with a shared prefix; 9B-like
+            4 x k=16 greedy at 16K context; MoE-like 8 x k=4 stochastic).
   config 1: activation quantization + one Q4_K
             9216x2560 verify GEMM (M = 5) + fused greedy acceptance over
             5 x 151936 logits.
@@ -44,6 +47,8 @@ def parse():
     ap.add_argument("--drafts", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prompt", type=int, default=None,
+                    help="configs 3-5: prompt length override (short traces for profiling)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="time only the dominant kernel, then one 256 MiB copy (profiling calibration)")
     return ap.parse_args()
@@ -401,6 +406,211 @@ def cpu_baseline_config2(cfg, w, k, budget_s):
             "ms_per_step": el * 1e3 / n}
 
 
+BATCHED = {
+    # 4B-like, 16 requests x 4096-token prompts
+    # sharing a 1024-token prefix, k = 8, stochastic T = 0.7 / top-p 0.9,
+    # forced accept length uniform 0..8.
+    3: dict(model="QWEN35_4B_LIKE", batch=16, prompt=4096, shared=1024, k=8, accept="stochastic",
+            temperature=0.7, top_p=0.9, forced="uniform"),
+    # 9B-like, 4 requests x 16384-token context, k = 16, greedy;
+    # drafts equal the argmax with probability 0.7 (geometric accept length).
+    4: dict(model="QWEN35_9B_LIKE", batch=4, prompt=16384, shared=0, k=16, accept="greedy", forced="geometric"),
+    # MoE-like, 8 requests x 2048-token context, k = 4, T = 0.8.
+    5: dict(model="QWEN35_MOE_LIKE", batch=8, prompt=2048, shared=0, k=4, accept="stochastic", temperature=0.8,
+            top_p=1.0, forced=None),
+}
+
+
+def bench_batched(args, which):
+    """BASELINE configs[2..4]: batched verify steps of the batched engine
+    (every request's k+1 rows in one captured graph, acceptance and commit
+    per request on the device)."""
+    from yuuka_amd import hip, model as Mdl
+
+    spec = BATCHED[which]
+    k, B, P = spec["k"], spec["batch"], args.prompt or spec["prompt"]
+    steps, warmup = args.steps or 32, args.warmup if args.warmup is not None else 4
+    base = getattr(Mdl, spec["model"])
+    cap = P + (steps + warmup + 2) * (k + 1) + 16
+    cfg = Mdl.replace(base, batch=B, max_rows=max(16, k + 1), capacity=cap)
+    t0 = time.perf_counter()
+    w = Mdl.make_weights(cfg, seed=0, share_experts=True)
+    gen_s = time.perf_counter() - t0
+    wbytes = Mdl.weight_bytes(w)
+    dev = hip.Device(0)
+    info = dev.info()
+    eng = Mdl.Engine(dev, cfg, w)
+    rng = np.random.default_rng(which)
+    t0 = time.perf_counter()
+    prompts = rng.integers(0, cfg.vocab, (B, P)).astype(np.int32)
+    S = min(spec["shared"], P // 4)
+    done = 0
+    if S:
+        prompts[:, :S] = prompts[0, :S]
+        eng.prefill_request(0, prompts[0, :S])
+        for r in range(1, B):
+            eng.fork(0, r)   # shared prefix blocks, reference-counted
+        done = S
+    rows = 16
+    while done < P - 1:
+        n = min(rows, P - 1 - done)
+        eng.step_batch(prompts[:, done:done + n], mode=1)
+        done += n
+    prefill_s = time.perf_counter() - t0
+    if spec["accept"] == "greedy":
+        acc = Mdl.accept_struct()
+    else:
+        acc = Mdl.accept_struct(mode=1, temperature=spec["temperature"], seed=1234, top_p=spec["top_p"])
+    pending = prompts[:, -1].copy()
+    histories = [list(prompts[r]) for r in range(B)]
+
+    def forced_lengths():
+        if spec["forced"] == "uniform":
+            return rng.integers(0, k + 1, B).astype(np.int32)
+        if spec["forced"] == "geometric":
+            # leading drafts that equal the argmax, each with probability 0.7
+            hit = rng.random((B, k)) < 0.7
+            return np.where(hit.all(axis=1), k, np.argmin(hit, axis=1)).astype(np.int32)
+        return None
+
+    def step():
+        toks = np.zeros((B, k + 1), np.int32)
+        toks[:, 0] = pending
+        for r in range(B):
+            d = lookup_draft(histories[r], k)
+            d = d + list(rng.integers(0, cfg.vocab, k - len(d)))
+            toks[r, 1:] = d
+        forced = forced_lengths()
+        res = eng.step_batch(toks, 0, acc, forced)
+        n = 0
+        for r in range(B):
+            a = int(res[r, 0])
+            emitted = list(toks[r, 1:1 + a]) + [int(res[r, 1])]
+            histories[r].extend(emitted)
+            pending[r] = res[r, 1]
+            n += len(emitted)
+        return n, eng.last_step_ms
+
+    for _ in range(warmup):
+        step()
+    tokens, gpu_ms = 0, []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        n, ms = step()
+        tokens += n
+        gpu_ms.append(ms)
+    wall = time.perf_counter() - t0
+    step_gpu_ms = float(np.median(gpu_ms))
+    ctx = [eng.request_position(r) for r in range(B)]
+    R1 = k + 1
+    kvdim = cfg.kv_heads * cfg.head_dim
+    n_attn = sum(1 for i in range(cfg.n_layers) if not cfg.is_recurrent(i))
+    n_rec = cfg.n_layers - n_attn
+    # unique KV rows read: the shared prefix once, every request's own rows once
+    kv_rows = (S + sum(c - S for c in ctx)) if S else sum(ctx)
+    kv_bytes = n_attn * kv_rows * kvdim * 2 * 2
+    state_bytes = B * 2 * n_rec * (cfg.rank * cfg.state_size ** 2 + 3 * cfg.conv_dim) * 4
+    logit_bytes = 2 * B * R1 * cfg.vocab * 4
+    step_w = wbytes
+    moe_note = None
+    if cfg.n_experts:
+        # expert bytes actually streamed: the distinct experts the B*(k+1)
+        # routed rows touch, in expectation under uniform routing
+        E, used, ef, H = cfg.n_experts, cfg.n_experts_used, cfg.expert_ffn, cfg.hidden
+        distinct = E * (1 - (1 - used / E) ** (B * R1))
+        per_expert = 3 * ef * H // 256 * 144
+        step_w = wbytes - cfg.n_layers * E * per_expert + cfg.n_layers * int(distinct * per_expert)
+        moe_note = f"expert bytes for {distinct:.1f} of {E} experts per layer (expected distinct under uniform routing)"
+    step_bytes = step_w + kv_bytes + state_bytes + logit_bytes
+    step_ach = step_bytes / (step_gpu_ms * 1e-3) / 1e9
+    line = {
+        "metric": "accepted tokens/s on 1 MI355X; verify-step HBM GB/s vs peak",
+        "value": tokens / wall,
+        "unit": "accepted tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": wall * 1e3 / steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k/q6_k weights x int16-split activations (int32 MFMA), fp32 norms/attention/GDN",
+        "data": "synthetic: random-init Q4_K_M-mix weights, random prompts; drafts from prompt lookup, padded "
+                "with random ids" + ("; prescribed accept lengths (" + spec["forced"] + ")" if spec["forced"] else ""),
+        "config": {"workload": f"config{which}: {spec['model']} batched verify, {B} requests, k={k}",
+                   "requests": B, "prompt": P, "shared_prefix": S, "drafts": k, "rows": B * R1,
+                   "acceptance": spec["accept"] + (f" T={spec['temperature']} top-p={spec['top_p']}"
+                                                   if spec["accept"] != "greedy" else ""),
+                   "hidden": cfg.hidden, "layers": cfg.n_layers, "experts": cfg.n_experts,
+                   "parallelism": "single GPU"},
+        "verify_step_gpu_us": step_gpu_ms * 1e3,
+        "accepted_tokens_per_step": tokens / steps,
+        "step_roofline": {"bound": "hbm", "achieved": step_ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": step_ach / HBM_PEAK_GBS, "alg_bytes_per_step": step_bytes, "weights": step_w,
+                          "kv": kv_bytes, "gdn_state": state_bytes, "logits": logit_bytes, "note": moe_note},
+        "context_end": ctx,
+        "prefill_s": prefill_s,
+        "weight_gen_s": gen_s,
+        "device": info,
+    }
+    eng.close()
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline_batched(cfg, w, spec, args.cpu_seconds)
+    return line
+
+
+def cpu_baseline_batched(cfg, w, spec, budget_s):
+    """The oracle decoder running verify steps of ONE request of the same
+    model (the reference serves requests one after another): k+1 rows of
+    PrefillLogits per step, the acceptance rule of the configuration, and the
+    reference rollback (snapshot, restore, replay of the accepted rows)."""
+    from oracle import oracle as O
+    cores = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    k = spec["k"]
+    cfg1 = Mdl_replace(cfg, batch=1)
+    orc = O.Q35(cfg1, w, kv_format=1, workers=cores)
+    rng = np.random.default_rng(3)
+    prompt = rng.integers(0, cfg.vocab, 4).astype(np.int32).tolist()
+    orc.forward(prompt[:-1])
+    pending = prompt[-1]
+    n, tokens = 0, 0
+    t0 = time.perf_counter()
+    while True:
+        d = list(rng.integers(0, cfg.vocab, k))
+        rows = [pending] + d
+        snap, pos = orc.snapshot()
+        logits = orc.forward(rows, all_logits=True)
+        if spec["forced"] == "uniform":
+            a = int(rng.integers(0, k + 1))
+        elif spec["forced"] == "geometric":
+            hit = rng.random(k) < 0.7
+            a = k if hit.all() else int(np.argmin(hit))
+        elif spec["accept"] == "greedy":
+            a = O.accept_greedy(logits, d)[0]
+        else:
+            a = O.accept_stochastic(logits, d, spec["temperature"], 1234, n, 0, 0, spec["top_p"])[0]
+        nxt = O.argmax(logits[a])
+        if a < k:
+            orc.restore(snap, pos)
+            orc.forward(rows[:a + 1])
+        pending = nxt
+        tokens += a + 1
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 1000:
+            break
+    orc.close()
+    return {"value": tokens / el, "unit": "accepted tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{n} verify steps of one request (k={k}, {k + 1} rows of the full model each, "
+                      f"same acceptance rule, snapshot/replay rollback) after a 4-token prompt, {el:.1f} s",
+            "ms_per_step": el * 1e3 / n}
+
+
+def Mdl_replace(cfg, **kw):
+    from yuuka_amd import model as Mdl
+    return Mdl.replace(cfg, **kw)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -416,6 +626,8 @@ def main():
         line = bench_config1(args)
     elif args.config == 2:
         line = bench_config2(args)
+    elif args.config in BATCHED:
+        line = bench_batched(args, args.config)
     else:
         print(json.dumps({"error": f"config {args.config} not available yet"}))
         sys.exit(2)

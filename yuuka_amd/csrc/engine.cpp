@@ -29,6 +29,7 @@
 #include <tuple>
 #include <vector>
 
+#include "fgemm.h"
 #include "internal.h"
 #include "plan.h"
 
@@ -36,7 +37,7 @@ namespace {
 
 using yk::fail;
 
-constexpr int kRowBlock = 16;   // rows of one fused GEMM launch
+constexpr int kRowBlock = 16;   // rows of one GEMM launch (split path; fused path upper bound)
 constexpr int kAttnRows = 8;    // query rows of one verify-attention launch (MFMA path)
 
 struct Tensor {
@@ -192,9 +193,14 @@ struct Builder {
     void fused(yuuka_buffer *x, yuuka_buffer *norm, float eps, uint64_t rows, std::initializer_list<Seg> segs,
                uint32_t epilogue, uint32_t out_map = 0, yuuka_buffer *gate = nullptr,
                yuuka_buffer *head_norm = nullptr) {
-        const uint64_t blocks = (rows + kRowBlock - 1) / kRowBlock;
+        // rows per launch: what the streaming kernel serves for this K and
+        // prologue (it reads the weights at verify shapes fastest), else 16
+        const uint64_t K0 = segs.begin()->w->cols;
+        int per = yk::fused_gemm_stream_rows((int)K0, norm != nullptr, gate != nullptr);
+        if (per < 1) per = kRowBlock;
+        const uint64_t blocks = (rows + per - 1) / per;
         for (uint64_t bi = 0; bi < blocks && st == YUUKA_OK; bi++) {
-            // equal blocks (rows 40 -> 14, 13, 13), so no launch is nearly empty
+            // equal blocks (rows 40 -> 8 x 5), so no launch is nearly empty
             const uint64_t r0 = rows * bi / blocks, r1 = rows * (bi + 1) / blocks;
             yuuka_op op{};
             op.code = YUUKA_EXT_OP_GEMM_FUSED;

@@ -55,6 +55,10 @@ struct FusedGemmArgs {
 // next to the partial-sum area of a tt-tile launch (0 if none fits).
 int fused_gemm_chunk_sb(int rows, int K, int tt, bool norm, bool gated = false);
 uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt, bool norm, bool gated = false);
+// Largest row count the streaming kernel (one launch per layer projection
+// at verify shapes) serves for this K; larger row counts take the chunked
+// kernel. 0 when K has no super-block.
+int fused_gemm_stream_rows(int K, bool norm, bool gated);
 // tt: 16-row tiles per workgroup (1, 2 or 4; even for kEpiSwiglu).
 hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s);
 

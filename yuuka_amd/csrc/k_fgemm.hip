@@ -1360,6 +1360,15 @@ static int device_cus() {
 // register bucket of the prologue mode, quantized activations in LDS.
 // *balanced: at most kBalMax row tiles per workgroup (one workgroup per CU:
 // 512 threads at more than 128 VGPRs).
+// Largest row count the streaming kernel serves for this K and prologue
+// (its activation units per wave stay within the register budget).
+int fused_gemm_stream_rows(int K, bool norm, bool gated) {
+    const int nsb = K / 256;
+    if (nsb < 1) return 0;
+    const int cap = gated ? 8 : (norm ? 16 : 24);
+    return std::min(8, cap * kWaves / nsb);
+}
+
 static bool stream_shape(const FusedGemmArgs &a, int tt, bool mixed, int *ku, int *mode, uint32_t *lds,
                          bool *balanced) {
     if (a.rows > 8 || (tt != 1 && tt != 2) || ((mixed || a.seg[0].dtype == kQ6K) && tt != 1)) return false;

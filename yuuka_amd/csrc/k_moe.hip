@@ -24,6 +24,7 @@
 //              order of float32 operations.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 
 #include "model_kernels.h"
@@ -46,128 +47,265 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // ---------------------------------------------------------------- router
 // logits[r][e] = W[e] . y[r] (FP32 weights, ffn_gate_inp) and, when `sv` is
-// given, extra[r] = sv . y[r] (ffn_gate_inp_shexp, forward.go:385).
-__global__ __launch_bounds__(kMoeThreads) void moe_router_kernel(const float *__restrict__ y, int H, int rows,
-                                                                 const float *__restrict__ w, int E,
-                                                                 float *__restrict__ logits,
-                                                                 const float *__restrict__ sv,
-                                                                 float *__restrict__ extra) {
+// given, extra[r] = sv . y[r] (ffn_gate_inp_shexp, forward.go:385). One
+// workgroup per expert row (the shared gate vector is row E); its four waves
+// take the rows in turn, two rows per pass so that their loads overlap.
+constexpr int kRouterWaves = 4;
+
+__global__ __launch_bounds__(64 * kRouterWaves) void moe_router_kernel(const float *__restrict__ y, int H, int rows,
+                                                                       const float *__restrict__ w, int E,
+                                                                       float *__restrict__ logits,
+                                                                       const float *__restrict__ sv,
+                                                                       float *__restrict__ extra) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int e = blockIdx.x * kMoeWaves + wave;
-    if (e > E || (e == E && !sv)) return;
+    const int e = blockIdx.x;
     const float *wr = e < E ? w + (uint64_t)e * H : sv;
-    for (int r = 0; r < rows; r++) {
-        const float *yr = y + (uint64_t)r * H;
-        float acc = 0.f;
+    for (int r = wave; r < rows; r += 2 * kRouterWaves) {
+        const int r2 = r + kRouterWaves;
+        const bool two = r2 < rows;
+        const float *y0 = y + (uint64_t)r * H, *y1 = y + (uint64_t)(two ? r2 : r) * H;
+        float a0 = 0.f, a1 = 0.f;
         for (int k = 4 * lane; k < H; k += 256) {
-            const float4 a = *reinterpret_cast<const float4 *>(wr + k);
-            const float4 b = *reinterpret_cast<const float4 *>(yr + k);
-            acc += a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+            const float4 wv = *reinterpret_cast<const float4 *>(wr + k);
+            const float4 b0 = *reinterpret_cast<const float4 *>(y0 + k);
+            const float4 b1 = *reinterpret_cast<const float4 *>(y1 + k);
+            a0 += wv.x * b0.x + wv.y * b0.y + wv.z * b0.z + wv.w * b0.w;
+            a1 += wv.x * b1.x + wv.y * b1.y + wv.z * b1.z + wv.w * b1.w;
         }
-        acc = wave_sum(acc);
+        a0 = wave_sum(a0);
+        a1 = wave_sum(a1);
         if (lane == 0) {
-            if (e < E)
-                logits[(uint64_t)r * E + e] = acc;
-            else
-                extra[r] = acc;
+            if (e < E) {
+                logits[(uint64_t)r * E + e] = a0;
+                if (two) logits[(uint64_t)r2 * E + e] = a1;
+            } else {
+                extra[r] = a0;
+                if (two) extra[r2] = a1;
+            }
         }
     }
 }
 
 // ---------------------------------------------------------------- route
-// forward.go:393-439 selectExperts for every row, then binning by expert
-// (the reference's assignment layout, yuuka_hip.h:457-460: bucket capacity
-// rows*used). LDS: ids [rows*used].
+// forward.go:393-439 selectExperts for every row (one wave per row, the
+// row's logits held in registers, a taken mask per lane), then binning by
+// expert (the reference's assignment layout, yuuka_hip.h:457-460: bucket
+// capacity rows*used). An assignment's place in its bin is the number of
+// earlier (row, slot) assignments to the same expert, so the bins are in
+// (row, slot) order. LDS: ids, weights and picked logits [rows*used].
+constexpr int kRouteMaxPerLane = 16;  // experts <= 1024
+
+// Monotone uint32 image of a float (larger value, larger key); -0 keys as +0
+// because the reference compares values.
+__device__ __forceinline__ uint32_t route_key(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u << 1) == 0u) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+
+// Maxima / minima over the wave: DPP inside each 16-lane row, then the four
+// rows' results through readlane (wave-uniform).
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+#define YK_STEP(C)                                                                   \
+    {                                                                                \
+        const uint64_t o = ((uint64_t)dpp_u32<C>((uint32_t)(k >> 32)) << 32) |       \
+                           dpp_u32<C>((uint32_t)k);                                  \
+        k = o > k ? o : k;                                                           \
+    }
+    YK_STEP(0xb1) YK_STEP(0x4e) YK_STEP(0x124) YK_STEP(0x128)
+#undef YK_STEP
+    uint64_t best = 0;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(k >> 32), 16 * r) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 16 * r);
+        best = o > best ? o : best;
+    }
+    return best;
+}
+
+__device__ __forceinline__ int wave_min_i32(int v) {
+    v = min(v, (int)dpp_u32<0xb1>((uint32_t)v));
+    v = min(v, (int)dpp_u32<0x4e>((uint32_t)v));
+    v = min(v, (int)dpp_u32<0x124>((uint32_t)v));
+    v = min(v, (int)dpp_u32<0x128>((uint32_t)v));
+    int best = INT_MAX;
+#pragma unroll
+    for (int r = 0; r < 4; r++) best = min(best, __builtin_amdgcn_readlane(v, 16 * r));
+    return best;
+}
+
+// The logit of expert e (wave-uniform) from its owner lane's registers.
+__device__ __forceinline__ float pick_lane_value(const float (&v)[kRouteMaxPerLane], int e) {
+    const int idx = e >> 6;
+    float mine = 0.f;
+#pragma unroll
+    for (int i = 0; i < kRouteMaxPerLane; i++)
+        if (i == idx) mine = v[i];
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), e & 63));
+}
+
 __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ logits, int rows, int E,
                                                          int used, int32_t *__restrict__ ids,
                                                          float *__restrict__ weights, int32_t *__restrict__ counts,
                                                          int32_t *__restrict__ arows, int32_t *__restrict__ aslots,
                                                          float *__restrict__ aweights) {
-    extern __shared__ int32_t sid[];  // ids [rows*used], then weights [rows*used]
-    float *sw = reinterpret_cast<float *>(sid + rows * used);
+    extern __shared__ int32_t sid[];
+    float *sw = reinterpret_cast<float *>(sid + ((rows * used + 3) & ~3));
+    float *spv = sw + rows * used;  // picked logits
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
     for (int r = wave; r < rows; r += nw) {
         const float *l = logits + (uint64_t)r * E;
-        int32_t *rid = sid + r * used;
+        float v[kRouteMaxPerLane];
+#pragma unroll
+        for (int i = 0; i < kRouteMaxPerLane; i++) v[i] = lane + 64 * i < E ? l[lane + 64 * i] : 0.f;
+        uint32_t taken = 0;
         for (int slot = 0; slot < used; slot++) {
             // Reference scan: the first untaken expert starts as best and a
             // later one replaces it only when strictly greater. So a NaN
             // start keeps the slot, NaN elsewhere never wins, and equal
-            // maxima resolve to the lowest index.
-            int first = INT_MAX, bi = INT_MAX;
-            float bv = 0.f;
-            for (int e = lane; e < E; e += 64) {
-                bool taken = false;
-                for (int p = 0; p < slot; p++) taken |= rid[p] == e;
-                if (taken) continue;
+            // maxima resolve to the lowest index: the largest key
+            // (order key of the logit, then the complemented index) over
+            // untaken non-NaN experts.
+            uint64_t key = 0;
+            int first = INT_MAX;
+#pragma unroll
+            for (int i = 0; i < kRouteMaxPerLane; i++) {
+                const int e = lane + 64 * i;
+                if (e >= E || (taken >> i & 1u)) continue;
                 first = min(first, e);
-                const float v = l[e];
-                if (v == v && (bi == INT_MAX || v > bv)) {
-                    bv = v;
-                    bi = e;
+                if (v[i] == v[i]) {
+                    const uint64_t k = ((uint64_t)route_key(v[i]) << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+                    key = k > key ? k : key;
                 }
             }
-            for (int off = 32; off > 0; off >>= 1) {
-                first = min(first, __shfl_xor(first, off));
-                const float ov = __shfl_xor(bv, off);
-                const int oi = __shfl_xor(bi, off);
-                if (oi != INT_MAX && (bi == INT_MAX || ov > bv || (ov == bv && oi < bi))) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
+            key = wave_max_u64(key);
+            first = wave_min_i32(first);
             int pick;
-            if (first == INT_MAX)
+            if (first == INT_MAX) {
                 pick = 0;  // more slots than experts (forward.go:413-417)
-            else if (!(l[first] == l[first]) || bi == INT_MAX)
-                pick = first;
-            else
-                pick = bi;
-            if (lane == 0) rid[slot] = pick;
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-        }
-        if (lane == 0) {
-            // weights: float32(exp(float64(l - max))), float32 total in slot
-            // order, then each divided by the total (forward.go:424-438).
-            float mx = l[rid[0]];
-            for (int s = 1; s < used; s++)
-                if (l[rid[s]] > mx) mx = l[rid[s]];
-            float total = 0.f;
-            for (int s = 0; s < used; s++) total = __fadd_rn(total, (float)exp((double)__fsub_rn(l[rid[s]], mx)));
-            for (int s = 0; s < used; s++) {
-                const float wt = (float)exp((double)__fsub_rn(l[rid[s]], mx));
-                const float v = total > 0.f ? __fdiv_rn(wt, total) : wt;
-                sw[r * used + s] = v;
-                ids[(uint64_t)r * used + s] = rid[s];
-                weights[(uint64_t)r * used + s] = v;
+            } else {
+                const float fv = pick_lane_value(v, first);
+                pick = (!(fv == fv) || key == 0) ? first : (int)(0xffffffffu - (uint32_t)key);
+                if ((pick & 63) == lane) taken |= 1u << (pick >> 6);
             }
+            const float pvv = pick_lane_value(v, pick);
+            if (lane == 0) {
+                sid[r * used + slot] = pick;
+                spv[r * used + slot] = pvv;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // weights: float32(exp(float64(l - max))), float32 total in slot
+        // order, then each divided by the total (forward.go:424-438); lane s
+        // computes slot s's exponential, lane 0 the ordered total.
+        const float *pv = spv + r * used;
+        float mx = pv[0];
+        for (int sl = 1; sl < used; sl++)
+            if (pv[sl] > mx) mx = pv[sl];
+        const float mine = lane < used ? pv[lane] : 0.f;
+        const float wt = lane < used ? (float)exp((double)__fsub_rn(mine, mx)) : 0.f;
+        float total = 0.f;
+        for (int sl = 0; sl < used; sl++)
+            total = __fadd_rn(total, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wt), sl)));
+        if (lane < used) {
+            const float val = total > 0.f ? __fdiv_rn(wt, total) : wt;
+            sw[r * used + lane] = val;
+            ids[(uint64_t)r * used + lane] = sid[r * used + lane];
+            weights[(uint64_t)r * used + lane] = val;
         }
     }
-    __syncthreads();
     const int cap = rows * used;
+    for (int a = cap + threadIdx.x; a < ((cap + 3) & ~3); a += blockDim.x) sid[a] = -1;  // pad to int4
+    __syncthreads();
+    // thread e fills bin e in (row, slot) order and writes its count
+    const int4 *sid4 = reinterpret_cast<const int4 *>(sid);
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
         int n = 0;
-        for (int a = 0; a < cap; a++) {
-            if (sid[a] != e) continue;
-            const uint64_t o = (uint64_t)e * cap + n;
-            arows[o] = a / used;
-            aslots[o] = a % used;
-            aweights[o] = sw[a];
-            n++;
+        for (int a4 = 0; a4 < (cap + 3) / 4; a4++) {
+            const int4 v = sid4[a4];
+            const int vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                if (vv[t] != e) continue;
+                const int a = 4 * a4 + t;
+                const uint64_t o = (uint64_t)e * cap + n;
+                arows[o] = a / used;
+                aslots[o] = a % used;
+                aweights[o] = sw[a];
+                n++;
+            }
         }
         counts[e] = n;
     }
 }
 
 // ---------------------------------------------------------------- grouped GEMM
+// Activation rows quantized once per launch into scratch (moe_quant_kernel):
+//   planes [rows][K/32 sub-blocks][2: high, low][32 B]
+//   sums   [rows][K/32]   int32 sums of q per sub-block (Q4_K min term)
+//   scales [rows][K/256]  float (x ~= scale * q, q = 256 h + l)
+struct MoeQuant {
+    int8_t *planes;
+    int32_t *sums;
+    float *scales;
+};
+
+__host__ __device__ inline MoeQuant moe_quant_view(void *ws, int rows, int K) {
+    uint8_t *p = static_cast<uint8_t *>(ws);
+    MoeQuant q;
+    q.planes = reinterpret_cast<int8_t *>(p);
+    q.sums = reinterpret_cast<int32_t *>(p + (uint64_t)rows * K * 2);
+    q.scales = reinterpret_cast<float *>(p + (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 32) * 4);
+    return q;
+}
+
+// One wave per (row, super-block): lane l holds elements 4l .. 4l+3.
+__global__ __launch_bounds__(256) void moe_quant_kernel(const float *__restrict__ x, int rows, int K, MoeQuant q) {
+    const int nsb = K / 256;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (u >= rows * nsb) return;
+    const int row = u / nsb, sb = u % nsb;
+    const float4 v = *reinterpret_cast<const float4 *>(x + (uint64_t)row * K + sb * 256 + 4 * lane);
+    float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float inv = m > 0.f ? (float)kQMax / m : 0.f;
+    const int qv[4] = {(int)rintf(v.x * inv), (int)rintf(v.y * inv), (int)rintf(v.z * inv), (int)rintf(v.w * inv)};
+    uint32_t hp = 0, lp = 0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int h = (qv[t] + 128) >> 8;
+        const int l = qv[t] - 256 * h;
+        hp |= (uint32_t)(h & 0xff) << (8 * t);
+        lp |= (uint32_t)(l & 0xff) << (8 * t);
+    }
+    const int j = lane >> 3, o = 4 * (lane & 7);
+    int8_t *dst = q.planes + (uint64_t)row * K * 2 + (uint64_t)(sb * 8 + j) * 64 + o;
+    *reinterpret_cast<uint32_t *>(dst) = hp;
+    *reinterpret_cast<uint32_t *>(dst + 32) = lp;
+    int sum = qv[0] + qv[1] + qv[2] + qv[3];
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    if ((lane & 7) == 0) q.sums[(uint64_t)row * (K / 32) + sb * 8 + j] = sum;
+    if (lane == 0) q.scales[(uint64_t)row * nsb + sb] = m > 0.f ? m / (float)kQMax : 0.f;
+}
+
 struct MoeGemmArgs {
-    const float *x;       // activation rows [.][K]
     const uint8_t *w0;    // expert-stacked Q4_K rows: expert e, output n at row e*N + n
     const uint8_t *w1;    // second matrix of a gate/up pair (or null)
     uint64_t row_bytes;   // bytes of one packed row (K/256 * 144)
     const int32_t *counts, *arows, *aslots;
-    int rows, used, E, K, N, parts;
+    MoeQuant xq;
+    int rows, used, E, K, N;
+    int tpw;              // 16-channel tiles per workgroup
     int by_slot;          // activation row = row*used + slot (down projection), else row
     int swiglu;           // out0 = SiLU(W0 y) * (W1 y)
     float *out0, *out1;   // [rows*used][N]
@@ -178,48 +316,53 @@ __device__ __forceinline__ i32x4 mfma_i8(int64_t a, int64_t b) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero, 0, 0, 0);
 }
 
-// tensor/quant.go:96-103 getScaleMinK4 for the eight sub-blocks of a Q4_K
-// block whose scale bytes are s[0..11].
-__device__ __forceinline__ void scales_k4(const uint8_t *s, int sc[8], int mn[8]) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        sc[j] = s[j] & 63;
-        mn[j] = s[j + 4] & 63;
-        sc[j + 4] = (s[j + 8] & 0xF) | ((s[j] >> 6) << 4);
-        mn[j + 4] = (s[j + 8] >> 4) | ((s[j + 4] >> 6) << 4);
+// tensor/quant.go:96-103 getScaleMinK4 for sub-block j of a Q4_K block
+// whose scale bytes 0..11 are the words s1, s2, s3 (block bytes 4..15).
+__device__ __forceinline__ void scale_min_k4(int j, uint32_t s1, uint32_t s2, uint32_t s3, int *sc, int *mn) {
+    if (j < 4) {
+        *sc = (s1 >> (8 * j)) & 63;
+        *mn = (s2 >> (8 * j)) & 63;
+    } else {
+        const int k = j - 4;
+        const uint32_t a = (s1 >> (8 * k)) & 0xff, b = (s2 >> (8 * k)) & 0xff, cc = (s3 >> (8 * k)) & 0xff;
+        *sc = (int)((cc & 0xF) | ((a >> 6) << 4));
+        *mn = (int)((cc >> 4) | ((b >> 6) << 4));
     }
 }
 
-// LDS layout of one chunk of activations:
-//   xa   [K/32 sub-blocks][4 g][16 r][8 B]  r < 8: high plane of row r,
-//                                           r >= 8: low plane of row r - 8
-//   sums [K/32][8]  int32 sub-block sums of q per row
-//   xs   [K/256][8] float scales
-__host__ __device__ constexpr uint32_t moe_lds_bytes(int K) {
-    return (uint32_t)K * 16 + (uint32_t)(K / 32) * 8 * 4 + (uint32_t)(K / 256) * 8 * 4;
-}
-
-__global__ __launch_bounds__(kMoeThreads) void moe_gemm_kernel(MoeGemmArgs A) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    const int e = blockIdx.x, part = blockIdx.y;
+// Workgroup (expert e, part): tiles [t0, t0 + tpw) of 16 output channels.
+// Per chunk of up to eight assignments, the (tile, super-block) items are
+// dealt to the waves; each item's partial sums go to LDS and are added in
+// super-block order at the end (deterministic). Lane (c, g) of an item
+// loads channel c's Q4_K bytes straight into MFMA B order and the
+// activation planes of assignment c & 7 (high plane for c < 8) into A order.
+__global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))) void moe_gemm_kernel(MoeGemmArgs A) {
+    // LDS: partial sums [tpw][nsb][mats][8 rows][16 ch] floats, then the
+    // chunk's activations: planes [K/32][16 r][32 B] (r < 8 high plane of
+    // assignment r, r >= 8 low plane of assignment r - 8), sub-block sums
+    // [K/32][8] int32, scales [K/256][8] float.
+    extern __shared__ __attribute__((aligned(16))) float part[];
+    const int e = blockIdx.x;
     const int count = A.counts[e];
     if (count <= 0) return;
     const int nsb = A.K / 256, nsub = A.K / 32;
-    uint8_t *xa = lds;
-    int32_t *sums = reinterpret_cast<int32_t *>(lds + (uint32_t)A.K * 16);
-    float *xs = reinterpret_cast<float *>(lds + (uint32_t)A.K * 16 + (uint32_t)nsub * 32);
-    __shared__ int s_row[kChunk], s_out[kChunk];
-
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int tiles = A.N / 16;
-    const int t_begin = (int)((int64_t)tiles * part / A.parts);
-    const int t_end = (int)((int64_t)tiles * (part + 1) / A.parts);
-    const uint64_t cap = (uint64_t)A.rows * A.used;
+    const int t0 = blockIdx.y * A.tpw;
+    if (t0 >= tiles) return;
+    const int ntl = min(A.tpw, tiles - t0);
     const bool dual = A.w1 != nullptr;
+    const int mats = dual ? 2 : 1;
+    __shared__ int s_row[kChunk], s_out[kChunk];
+    uint8_t *la = reinterpret_cast<uint8_t *>(part + (uint64_t)A.tpw * nsb * mats * 128);
+    int32_t *lsum = reinterpret_cast<int32_t *>(la + (uint64_t)nsub * 16 * 32);
+    float *lxs = reinterpret_cast<float *>(lsum + nsub * 8);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = lane & 15, g = lane >> 4;
+    const uint64_t cap = (uint64_t)A.rows * A.used;
 
     for (int c0 = 0; c0 < count; c0 += kChunk) {
         const int nr = min(kChunk, count - c0);
-        __syncthreads();  // the previous chunk's readers are done with LDS
+        __syncthreads();
         if (threadIdx.x < kChunk) {
             const int i = threadIdx.x;
             if (i < nr) {
@@ -227,112 +370,92 @@ __global__ __launch_bounds__(kMoeThreads) void moe_gemm_kernel(MoeGemmArgs A) {
                 const int row = A.arows[o], slot = A.aslots[o];
                 s_out[i] = row * A.used + slot;
                 s_row[i] = A.by_slot ? row * A.used + slot : row;
-            } else {
+            } else {  // padding rows read assignment 0 and are never stored
+                const uint64_t o = (uint64_t)e * cap + c0;
+                const int row = A.arows[o], slot = A.aslots[o];
                 s_out[i] = -1;
-                s_row[i] = -1;
+                s_row[i] = A.by_slot ? row * A.used + slot : row;
             }
         }
         __syncthreads();
-        // Quantize: wave per (row, super-block) unit; lane holds 4 elements.
-        for (int u = wave; u < kChunk * nsb; u += kMoeWaves) {
-            const int i = u / nsb, sb = u % nsb;
-            const int j = lane >> 3, g = (lane >> 1) & 3, e0 = (lane & 1) * 4;
-            int q[4] = {0, 0, 0, 0};
-            float scale = 0.f;
-            if (i < nr) {
-                const float4 v = *reinterpret_cast<const float4 *>(A.x + (uint64_t)s_row[i] * A.K + sb * 256 + 4 * lane);
-                float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-                for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-                const float inv = m > 0.f ? (float)kQMax / m : 0.f;
-                scale = m > 0.f ? m / (float)kQMax : 0.f;
-                q[0] = (int)rintf(v.x * inv);
-                q[1] = (int)rintf(v.y * inv);
-                q[2] = (int)rintf(v.z * inv);
-                q[3] = (int)rintf(v.w * inv);
-            }
-            uint32_t hp = 0, lp = 0;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int h = (q[t] + 128) >> 8;
-                const int l = q[t] - 256 * h;
-                hp |= (uint32_t)(h & 0xff) << (8 * t);
-                lp |= (uint32_t)(l & 0xff) << (8 * t);
-            }
-            uint8_t *dst = xa + ((uint32_t)((sb * 8 + j) * 4 + g)) * 128 + e0;
-            *reinterpret_cast<uint32_t *>(dst + i * 8) = hp;
-            *reinterpret_cast<uint32_t *>(dst + (8 + i) * 8) = lp;
-            int s = q[0] + q[1] + q[2] + q[3];
-            s += __shfl_xor(s, 1);
-            s += __shfl_xor(s, 2);
-            s += __shfl_xor(s, 4);
-            if ((lane & 7) == 0) sums[(sb * 8 + j) * 8 + i] = s;
-            if (lane == 0) xs[sb * 8 + i] = scale;
+        for (int idx = threadIdx.x; idx < nsub * 32; idx += kMoeThreads) {  // 16 B pieces of the planes
+            const int j = idx >> 5, r = (idx >> 1) & 15, half = idx & 1;
+            const int8_t *src = A.xq.planes + (uint64_t)s_row[r & 7] * A.K * 2 + (uint64_t)j * 64 + (r >= 8 ? 32 : 0) +
+                                16 * half;
+            *reinterpret_cast<uint4 *>(la + ((uint64_t)j * 16 + r) * 32 + 16 * half) =
+                *reinterpret_cast<const uint4 *>(src);
         }
+        for (int idx = threadIdx.x; idx < nsub * 8; idx += kMoeThreads)
+            lsum[idx] = A.xq.sums[(uint64_t)s_row[idx & 7] * nsub + (idx >> 3)];
+        for (int idx = threadIdx.x; idx < nsb * 8; idx += kMoeThreads)
+            lxs[idx] = A.xq.scales[(uint64_t)s_row[idx & 7] * nsb + (idx >> 3)];
         __syncthreads();
-
-        const int c = lane & 15, g = lane >> 4;
-        for (int t = t_begin + wave; t < t_end; t += kMoeWaves) {
-            const int n0 = t * 16;
-            float y[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-            for (int sb = 0; sb < nsb; sb++) {
+        // items (tile, matrix, super-block), two per wave per pass: both
+        // items' weight loads are issued before either is multiplied
+        const int items = ntl * mats * nsb;
+        for (int it0 = 2 * wave; it0 < items; it0 += 2 * kMoeWaves) {
+            uint4 hdr[2];
+            uint64_t qv[2][4];
+            int sbs[2], slot[2];
 #pragma unroll
-                for (int m = 0; m < 2; m++) {
-                    if (m == 1 && !dual) break;
-                    const uint8_t *blk =
-                        (m ? A.w1 : A.w0) + ((uint64_t)e * A.N + n0 + c) * A.row_bytes + (uint64_t)sb * 144;
-                    const uint4 hdr = *reinterpret_cast<const uint4 *>(blk);
-                    uint64_t qv[4];
+            for (int u = 0; u < 2; u++) {
+                const int it = min(it0 + u, items - 1);
+                const int sb = it % nsb, tm = it / nsb, m = tm % mats, tl = tm / mats;
+                sbs[u] = sb;
+                slot[u] = (tl * nsb + sb) * mats + m;
+                const uint8_t *blk = (m ? A.w1 : A.w0) + ((uint64_t)e * A.N + (t0 + tl) * 16 + c) * A.row_bytes +
+                                     (uint64_t)sb * 144;
+                hdr[u] = *reinterpret_cast<const uint4 *>(blk);
 #pragma unroll
-                    for (int p = 0; p < 4; p++) qv[p] = *reinterpret_cast<const uint64_t *>(blk + 16 + 32 * p + 8 * g);
-                    int sc[8], mn[8];
-                    {
-                        uint8_t sb12[12];
+                for (int p = 0; p < 4; p++) qv[u][p] = *reinterpret_cast<const uint64_t *>(blk + 16 + 32 * p + 8 * g);
+            }
+            const int rbase = 4 * (g & 1);
 #pragma unroll
-                        for (int p = 0; p < 4; p++) {
-                            sb12[p] = (hdr.y >> (8 * p)) & 0xff;
-                            sb12[4 + p] = (hdr.z >> (8 * p)) & 0xff;
-                            sb12[8 + p] = (hdr.w >> (8 * p)) & 0xff;
-                        }
-                        scales_k4(sb12, sc, mn);
-                    }
-                    int acc[4] = {0, 0, 0, 0}, ms[4] = {0, 0, 0, 0};
+            for (int u = 0; u < 2; u++) {
+                if (it0 + u >= items) break;
+                const int sb = sbs[u];
+                const float4 xs4 = *reinterpret_cast<const float4 *>(lxs + sb * 8 + rbase);
+                const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+                int acc[4] = {0, 0, 0, 0}, ms[4] = {0, 0, 0, 0};
 #pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const uint64_t raw = qv[j >> 1];
-                        const uint64_t b = (j & 1) ? (raw >> 4) & 0x0F0F0F0F0F0F0F0Full : raw & 0x0F0F0F0F0F0F0F0Full;
-                        const int64_t a =
-                            *reinterpret_cast<const int64_t *>(xa + ((uint32_t)((sb * 8 + j) * 4 + g)) * 128 + c * 8);
-                        const i32x4 r = mfma_i8(a, (int64_t)b);
-                        const int4 sm = *reinterpret_cast<const int4 *>(sums + (sb * 8 + j) * 8 + 4 * (g & 1));
+                for (int j = 0; j < 8; j++) {
+                    int scj, mnj;
+                    scale_min_k4(j, hdr[u].y, hdr[u].z, hdr[u].w, &scj, &mnj);
+                    const uint64_t raw = qv[u][j >> 1];
+                    const uint64_t bq = (j & 1) ? (raw >> 4) & 0x0F0F0F0F0F0F0F0Full : raw & 0x0F0F0F0F0F0F0F0Full;
+                    const int64_t av = *reinterpret_cast<const int64_t *>(la + ((uint64_t)(sb * 8 + j) * 16 + c) * 32 + 8 * g);
+                    const i32x4 r = mfma_i8(av, (int64_t)bq);
+                    const int4 sm = *reinterpret_cast<const int4 *>(lsum + (sb * 8 + j) * 8 + rbase);
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[i] += r[i] * sc[j];
-                        ms[0] += mn[j] * sm.x;
-                        ms[1] += mn[j] * sm.y;
-                        ms[2] += mn[j] * sm.z;
-                        ms[3] += mn[j] * sm.w;
-                    }
-                    const float d = h2f((uint16_t)(hdr.x & 0xffffu)), dmin = h2f((uint16_t)(hdr.x >> 16));
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int lo = __shfl_xor(acc[i], 32);
-                        const float v = d * (256.f * (float)acc[i] + (float)lo) - dmin * (float)ms[i];
-                        y[m][i] += xs[sb * 8 + ((4 * g + i) & 7)] * v;
-                    }
+                    for (int i = 0; i < 4; i++) acc[i] += r[i] * scj;
+                    ms[0] += mnj * sm.x;
+                    ms[1] += mnj * sm.y;
+                    ms[2] += mnj * sm.z;
+                    ms[3] += mnj * sm.w;
                 }
-            }
-            if (g < 2) {
+                const float d = h2f((uint16_t)(hdr[u].x & 0xffffu)), dmin = h2f((uint16_t)(hdr[u].x >> 16));
+                float *dst = part + (uint64_t)slot[u] * 128;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int rr = 4 * g + i;
-                    if (rr >= nr) continue;
-                    const uint64_t o = (uint64_t)s_out[rr] * A.N + n0 + c;
-                    if (A.swiglu) {
-                        A.out0[o] = __fmul_rn(silu_ref(y[0][i]), y[1][i]);
-                    } else {
-                        A.out0[o] = y[0][i];
-                        if (dual) A.out1[o] = y[1][i];
-                    }
+                    const int lo = __shfl_xor(acc[i], 32);
+                    if (g < 2) dst[(4 * g + i) * 16 + c] = xs[i] * (d * (256.f * (float)acc[i] + (float)lo) -
+                                                                    dmin * (float)ms[i]);
                 }
+            }
+        }
+        __syncthreads();
+        // sum the super-blocks in order, then the epilogue
+        for (int o = threadIdx.x; o < ntl * nr * 16; o += kMoeThreads) {
+            const int tl = o / (nr * 16), rem = o % (nr * 16), i = rem / 16, cc = rem % 16;
+            float y[2] = {0.f, 0.f};
+            for (int m = 0; m < mats; m++)
+                for (int sb = 0; sb < nsb; sb++) y[m] += part[((uint64_t)(tl * nsb + sb) * mats + m) * 128 + i * 16 + cc];
+            const uint64_t dst = (uint64_t)s_out[i] * A.N + (t0 + tl) * 16 + cc;
+            if (A.swiglu) {
+                A.out0[dst] = __fmul_rn(silu_ref(y[0]), y[1]);
+            } else {
+                A.out0[dst] = y[0];
+                if (dual) A.out1[dst] = y[1];
             }
         }
     }
@@ -363,31 +486,34 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ x,
 
 }  // namespace
 
-uint32_t moe_gemm_lds(int K) { return moe_lds_bytes(K); }
+uint64_t moe_gemm_ws(int act_rows, int K) { return (uint64_t)act_rows * K * 2 + (uint64_t)act_rows * (K / 32) * 4 +
+                                                      (uint64_t)act_rows * (K / 256) * 4 + 256; }
 
 hipError_t launch_moe_router(const float *y, int H, int rows, const float *w, int E, float *logits, const float *sv,
                              float *extra, hipStream_t s) {
     const int n = E + (sv ? 1 : 0);
-    moe_router_kernel<<<(n + kMoeWaves - 1) / kMoeWaves, kMoeThreads, 0, s>>>(y, H, rows, w, E, logits, sv, extra);
+    moe_router_kernel<<<n, 64 * kRouterWaves, 0, s>>>(y, H, rows, w, E, logits, sv, extra);
     return hipGetLastError();
 }
 
 hipError_t launch_moe_route(const float *logits, int rows, int E, int used, int32_t *ids, float *weights,
                             int32_t *counts, int32_t *arows, int32_t *aslots, float *aweights, hipStream_t s) {
-    const uint32_t lds = (uint32_t)rows * used * 8;
+    if (E > 64 * kRouteMaxPerLane) return hipErrorInvalidValue;
+    const uint32_t lds = (uint32_t)rows * used * 12 + 16;
     moe_route_kernel<<<1, 1024, lds, s>>>(logits, rows, E, used, ids, weights, counts, arows, aslots, aweights);
     return hipGetLastError();
 }
 
-hipError_t launch_moe_gemm(const MoeGemm &g, hipStream_t s) {
+hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
+    const int act_rows = g.by_slot ? g.rows * g.used : g.rows;
     MoeGemmArgs a{};
-    a.x = g.x;
     a.w0 = static_cast<const uint8_t *>(g.w0);
     a.w1 = static_cast<const uint8_t *>(g.w1);
     a.row_bytes = g.row_bytes;
     a.counts = g.counts;
     a.arows = g.arows;
     a.aslots = g.aslots;
+    a.xq = moe_quant_view(ws, act_rows, g.K);
     a.rows = g.rows;
     a.used = g.used;
     a.E = g.experts;
@@ -397,13 +523,16 @@ hipError_t launch_moe_gemm(const MoeGemm &g, hipStream_t s) {
     a.swiglu = g.swiglu;
     a.out0 = g.out0;
     a.out1 = g.out1;
-    const int tiles = g.N / 16;
-    // Enough workgroups per expert that the active experts cover the chip,
-    // at least two tiles per wave.
-    int parts = tiles / (2 * kMoeWaves);
-    parts = parts < 1 ? 1 : (parts > 16 ? 16 : parts);
-    a.parts = parts;
-    moe_gemm_kernel<<<dim3((unsigned)g.experts, (unsigned)parts), kMoeThreads, moe_lds_bytes(g.K), s>>>(a);
+    const int nsb = g.K / 256, mats = g.w1 ? 2 : 1, tiles = g.N / 16;
+    // partial sums of one chunk: tpw * nsb * mats * 512 B within 32 KB
+    int tpw = (32 * 1024) / (nsb * mats * 512);
+    tpw = std::max(1, std::min(tpw, 16));
+    tpw = std::min(tpw, tiles);
+    a.tpw = tpw;
+    const uint32_t lds = (uint32_t)tpw * nsb * mats * 512 + (uint32_t)(g.K / 32) * (16 * 32 + 32) + (uint32_t)nsb * 32;
+    const int units = act_rows * nsb;
+    moe_quant_kernel<<<(units + 3) / 4, 256, 0, s>>>(g.x, act_rows, g.K, a.xq);
+    moe_gemm_kernel<<<dim3((unsigned)g.experts, (unsigned)((tiles + tpw - 1) / tpw)), kMoeThreads, lds, s>>>(a);
     return hipGetLastError();
 }
 

@@ -116,12 +116,13 @@ struct MoeGemm {
     int swiglu;               // out0 = SiLU(W0 y) * (W1 y)
     float *out0, *out1;       // [rows*used][N]
 };
-uint32_t moe_gemm_lds(int K);
+// Workspace of launch_moe_gemm: the quantized activation rows.
+uint64_t moe_gemm_ws(int act_rows, int K);
 hipError_t launch_moe_router(const float *y, int H, int rows, const float *w, int E, float *logits, const float *sv,
                              float *extra, hipStream_t s);
 hipError_t launch_moe_route(const float *logits, int rows, int E, int used, int32_t *ids, float *weights,
                             int32_t *counts, int32_t *arows, int32_t *aslots, float *aweights, hipStream_t s);
-hipError_t launch_moe_gemm(const MoeGemm &g, hipStream_t s);
+hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s);
 hipError_t launch_moe_combine(float *x, const float *eo, const float *w, int rows, int used, int H, const float *so,
                               const float *sg, hipStream_t s);
 

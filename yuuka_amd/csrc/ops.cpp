@@ -416,8 +416,12 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
     }
     case YUUKA_OP_MOE_ROUTE: {  // hip.go:1585-1608: n={rows, experts, used}
         const uint64_t rows = op.n[0], E = op.n[1], used = op.n[2];
-        if (!rows || !E || !used || used > E || E > (1u << 20) || rows * used > 8192)
+        if (!rows || !E || !used || used > E)
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid MoE route dimensions");
+        if (E > 1024 || used > 64 || rows * used > 4096)
+            return fail(YUUKA_ERR_UNSUPPORTED, "MoE route: %llu experts, %llu used, %llu rows (<= 1024, 64, 4096 "
+                        "assignments are served)", (unsigned long long)E, (unsigned long long)used,
+                        (unsigned long long)rows);
         const uint64_t a = E * rows * used * 4;
         if (!buf_ok(op.buf[0], op.off[0], rows * E * 4) || !buf_ok(op.buf[1], op.off[1], rows * used * 4) ||
             !buf_ok(op.buf[2], op.off[2], rows * used * 4) || !buf_ok(op.buf[3], op.off[3], E * 4) ||
@@ -450,6 +454,7 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         if (!ok) return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE %s buffers too small", gu ? "gate/up" : "down");
         if (op.off[0] % 16 || op.off[1] % 16 || (gu && op.off[2] % 16))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE activations and weights must be 16-byte aligned");
+        *ws = moe_gemm_ws((int)x_rows, (int)K);
         return YUUKA_OK;
     }
     case YUUKA_OP_MOE_REDUCE_ADD: {  // hip.go:1672-1690: n={hidden, rows, used}
@@ -680,7 +685,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
         g.swiglu = gu && (op.flags & YUUKA_EXT_FLAG_MOE_SWIGLU) ? 1 : 0;
         g.out0 = at<float>(op, ib + 3);
         g.out1 = gu ? at<float>(op, ib + 4) : nullptr;
-        err = launch_moe_gemm(g, s);
+        err = launch_moe_gemm(g, ctx.ws, s);
         break;
     }
     case YUUKA_OP_MOE_REDUCE_ADD:
