@@ -392,7 +392,9 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
  *               out_i); n={n_in, rows, N_0, N_1, N_2, N_3}; u1 epilogue:
  *               0 out = y W^T, 1 out = y W^T + residual, 2 SwiGLU
  *               out_0 = SiLU(y W_0^T) * (y W_1^T) (two segments, same shape).
- *               rows <= 16. One launch, no workspace.
+ *               rows <= 512: up to 8 rows one launch without workspace;
+ *               more rows (batched requests) read each weight once per 64
+ *               rows and use plan workspace for the quantized rows.
  *               Optional gated head norm of x (Gated DeltaNet output,
  *               recurrent.go:39-50): buf14 FP32 gate [rows][n_in] (SiLU
  *               already applied), buf15 FP32 head norm weight [128]; y =

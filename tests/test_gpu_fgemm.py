@@ -125,8 +125,8 @@ def test_fused_gemm_rejects_bad_ops(dev):
     ob = dev.alloc(5 * 64 * 4)
     with pytest.raises(hip.HipError):   # K not a multiple of 256
         hip.gemm_fused_op(plan, xb, 2500, 5, [(wb, O.Q4_K, 64, ob, None)])
-    with pytest.raises(hip.HipError):   # 17 rows
-        hip.gemm_fused_op(plan, xb, 2560, 17, [(wb, O.Q4_K, 64, ob, None)])
+    with pytest.raises(hip.HipError):   # 513 rows
+        hip.gemm_fused_op(plan, xb, 2560, 513, [(wb, O.Q4_K, 64, ob, None)])
     with pytest.raises(hip.HipError):   # weight buffer too small for 65 rows
         hip.gemm_fused_op(plan, xb, 2560, 5, [(wb, O.Q4_K, 65, ob, None)])
     with pytest.raises(hip.HipError):   # Q8_0 weights
@@ -190,4 +190,59 @@ def test_fused_gemm_silu_store(dev, stream):
     got = ob.read(np.float32).reshape(rows, n)
     plan.destroy()
     prod = _want(O.Q4_K, wq, n, k, x)
+    _check(got, O.silu_mul(prod, np.ones_like(prod)), budget=1e-3)
+
+
+# Many rows (batched requests): one launch reads every weight once per 64 rows.
+MANY = [
+    ([(O.Q4_K, 1000)], 2560, 9, True),
+    ([(O.Q4_K, 8192), (O.Q4_K, 1024), (O.Q6_K, 1024)], 2560, 40, True),   # attention q/k/v, 8 requests x 5
+    ([(O.Q6_K, 3001)], 2560, 64, True),                                   # LM head shape
+    ([(O.Q4_K, 2560)], 9216, 65, False),                                  # FFN down, two row blocks
+    ([(O.Q4_K, 700), (O.Q4_K, 130), (O.Q4_K, 16), (O.Q4_K, 16)], 4096, 144, True),  # 16 requests x 9
+    ([(O.Q6_K, 520)], 12288, 17, False),
+]
+
+
+@pytest.mark.parametrize("segs,k,rows,norm", MANY)
+def test_fused_gemm_many_rows(dev, stream, segs, k, rows, norm):
+    rng = np.random.default_rng(k * 3 + rows + len(segs))
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    g = rng.normal(1, 0.1, k).astype(np.float32) if norm else None
+    ws = [synth.quant_matrix(rng, dt, n, k) for dt, n in segs]
+    got = _run(dev, stream, x, [(dt, w, n) for (dt, n), w in zip(segs, ws)], k, rows, norm=g)
+    y = O.rmsnorm_rows(x, g, 1e-6) if norm else x
+    for (dt, n), w, gv in zip(segs, ws, got):
+        _check(gv, _want(dt, w, n, k, y))
+
+
+def test_fused_gemm_many_rows_epilogues(dev, stream):
+    """SwiGLU, residual, output maps and the gated head norm at 37 rows."""
+    rng = np.random.default_rng(31)
+    k, n, rows = 2048, 520, 37
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    g = rng.normal(1, 0.1, k).astype(np.float32)
+    wg = synth.quant_matrix(rng, O.Q4_K, n, k)
+    wu = synth.quant_matrix(rng, O.Q4_K, n, k)
+    y = O.rmsnorm_rows(x, g, 1e-6)
+    got = _run(dev, stream, x, [(O.Q4_K, wg, n), (O.Q4_K, wu, n)], k, rows, hip.EPI_SWIGLU, norm=g)[0]
+    _check(got, O.silu_mul(_want(O.Q4_K, wg, n, k, y), _want(O.Q4_K, wu, n, k, y)), budget=1e-3)
+    res = rng.normal(0, 3, (rows, n)).astype(np.float32)
+    got = _run(dev, stream, x, [(O.Q4_K, wg, n)], k, rows, hip.EPI_RESIDUAL, residuals=[res])[0]
+    _check(got - res, _want(O.Q4_K, wg, n, k, x))
+    # gated head norm prologue + SiLU output map
+    z = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    w = rng.normal(1, 0.1, 128).astype(np.float32)
+    gate = O.silu_mul(z, np.ones_like(z))
+    plan = hip.Plan(dev)
+    xb, gb, wb = dev.upload(x), dev.upload(gate), dev.upload(w)
+    ob, wqb = dev.alloc(rows * n * 4), dev.upload(wg)
+    bufs = [None] * 16
+    bufs[0], bufs[2], bufs[6], bufs[14], bufs[15] = xb, wqb, ob, gb, wb
+    plan.add(hip.OP["GEMM_FUSED"], bufs, n=[k, rows, n, 0, 0, 0], u=[O.Q4_K, 0, 1], f=[1e-6])
+    plan.execute(stream)
+    stream.sync()
+    got = ob.read(np.float32).reshape(rows, n)
+    plan.destroy()
+    prod = _want(O.Q4_K, wg, n, k, _gated_head_norm(x, z, w, 1e-6))
     _check(got, O.silu_mul(prod, np.ones_like(prod)), budget=1e-3)

@@ -198,6 +198,10 @@ struct Builder {
         const uint64_t K0 = segs.begin()->w->cols;
         int per = yk::fused_gemm_stream_rows((int)K0, norm != nullptr, gate != nullptr);
         if (per < 1) per = kRowBlock;
+        // more than 8 rows: one launch of the many-row kernel (every weight
+        // read once per 64 rows) unless YUUKA_Q35_ROWBLOCKS=1 asks for blocks
+        const char *rbk = getenv("YUUKA_Q35_ROWBLOCKS");
+        if (rows > 8 && !(rbk && rbk[0] == '1')) per = (int)rows;
         const uint64_t blocks = (rows + per - 1) / per;
         for (uint64_t bi = 0; bi < blocks && st == YUUKA_OK; bi++) {
             // equal blocks (rows 40 -> 8 x 5), so no launch is nearly empty

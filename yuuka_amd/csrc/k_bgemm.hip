@@ -1,0 +1,464 @@
+// k_bgemm.hip — verify GEMM for many rows (batched requests, 9..512 rows):
+//
+//   out_s[m, n] = epi( sum_k y[m, k] * dequant(W_s)[n, k] )
+//
+// with the prologues and epilogues of the fused verify GEMM (fgemm.h:
+// RMSNorm or gated head norm of x, store / residual / SwiGLU, output maps).
+// At a few rows the fused streaming kernel reads every weight once per
+// launch; a batch of B requests x (k+1) rows would read them once per 8-row
+// block. Here each weight super-block is read once per 64 rows:
+//
+//  * prologue (one workgroup per row): y = prologue(x) computed as the
+//    reference computes it (forward.go:460-482 rmsNorm, recurrent.go:39-50
+//    gated norm), then quantized per 256-element super-block into an int16
+//    split into two int8 planes (q = 256 h + l, |q| <= 32639), one scale per
+//    (row, super-block) and the exact int32 sums of every 32-element
+//    sub-block (Q4_K min term) — a workspace of rows * (2K + K/8 + K/64) B.
+//  * GEMM (workgroup = 64 rows x 8 tiles of 16 output channels, one tile per
+//    wave): per super-block the workgroup stages the 64 rows' planes in LDS
+//    in MFMA operand order; each wave decodes its tile's weights straight
+//    from HBM into MFMA B operands (Q4_K: one v_mfma_i32_16x16x32_i8 per
+//    32-element sub-block; Q6_K: two, one per 16-element scale group) while
+//    the next super-block's weights are in flight, and multiplies them with
+//    the eight 8-row A tiles (high planes in MFMA rows 0..7, low planes in
+//    8..15). Sub-block scales are applied in int32 (exact), d / dmin and the
+//    activation scale per super-block in FP32.
+//
+// Replaces, for batched verify shapes, the reference's per-matrix GEMV
+// launches over all rows (kernels/hip/gemm/lm_head.hip:61-173 with MaxRows 16,
+// engine/gpu/plan.go); no reference kernel serves more than 16 rows.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <type_traits>
+
+#include "fgemm.h"
+#include "refmath.h"
+
+namespace yk {
+namespace {
+
+typedef __attribute__((ext_vector_type(4))) int i32x4;
+
+constexpr int kQ4K = YUUKA_DTYPE_Q4_K;
+constexpr int kQ6K = YUUKA_DTYPE_Q6_K;
+constexpr int kQMax = 32639;
+constexpr int kBgWaves = 8;
+constexpr int kBgThreads = 64 * kBgWaves;
+constexpr int kBgRows = 64;  // rows per workgroup: 8 A tiles of 8 rows
+// LDS of the GEMM: A planes [8 t][8 j][4 g][16 r][8 B] + sums [8 t][8 j][8]
+// int32 + scales [8 t][8] float; the SwiGLU epilogue reuses the A region.
+constexpr uint32_t kBgLdsA = 8 * 8 * 4 * 16 * 8;
+constexpr uint32_t kBgLds = kBgLdsA + 8 * 8 * 8 * 4 + 8 * 8 * 4;
+
+struct BgQuant {
+    int8_t *planes;  // [rows][K/32][2: high, low][32 B]
+    int32_t *sums;   // [rows][K/32]
+    float *scales;   // [rows][K/256]
+};
+
+__host__ __device__ inline BgQuant bg_view(void *ws, int rows, int K) {
+    uint8_t *p = static_cast<uint8_t *>(ws);
+    BgQuant q;
+    q.planes = reinterpret_cast<int8_t *>(p);
+    q.sums = reinterpret_cast<int32_t *>(p + (uint64_t)rows * K * 2);
+    q.scales = reinterpret_cast<float *>(p + (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 32) * 4);
+    return q;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// ---------------------------------------------------------------- prologue
+__global__ __launch_bounds__(256) void bg_prologue_kernel(const FusedGemmArgs A, BgQuant q) {
+    extern __shared__ float ys[];  // [K]
+    __shared__ double red[4];
+    const int row = blockIdx.x, K = A.K;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const float *x = A.x + (uint64_t)row * K;
+    if (A.gate) {
+        // gated head norm over heads of 128: x * (scale * w) * gate
+        const float *z = A.gate + (uint64_t)row * K;
+        for (int h = wave; h < K / 128; h += 4) {
+            const float a0 = x[h * 128 + lane], a1 = x[h * 128 + 64 + lane];
+            double ss = (double)a0 * (double)a0 + (double)a1 * (double)a1;
+            ss = wave_sum_d(ss);
+            const float mean = (float)(ss / 128.0);
+            const float scale = (float)(1.0 / sqrt((double)(mean + A.eps)));
+            ys[h * 128 + lane] = __fmul_rn(__fmul_rn(a0, __fmul_rn(scale, A.head_norm[lane])), z[h * 128 + lane]);
+            ys[h * 128 + 64 + lane] =
+                __fmul_rn(__fmul_rn(a1, __fmul_rn(scale, A.head_norm[64 + lane])), z[h * 128 + 64 + lane]);
+        }
+    } else if (A.norm) {
+        // forward.go:460-470 rmsNorm: float64 sum of squares, x * scale * w
+        double s = 0.0;
+        for (int c = t; c < K; c += 256) s += (double)x[c] * (double)x[c];
+        s = wave_sum_d(s);
+        if (lane == 0) red[wave] = s;
+        __syncthreads();
+        s = red[0] + red[1] + red[2] + red[3];
+        const float mean = (float)(s / (double)K);
+        const float scale = (float)(1.0 / sqrt((double)(mean + A.eps)));
+        for (int c = t; c < K; c += 256) ys[c] = __fmul_rn(__fmul_rn(x[c], scale), A.norm[c]);
+    } else {
+        for (int c = t; c < K; c += 256) ys[c] = x[c];
+    }
+    __syncthreads();
+    const int nsb = K / 256;
+    for (int sb = wave; sb < nsb; sb += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(ys + sb * 256 + 4 * lane);
+        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        const float inv = m > 0.f ? (float)kQMax / m : 0.f;
+        const int qv[4] = {(int)rintf(v.x * inv), (int)rintf(v.y * inv), (int)rintf(v.z * inv),
+                           (int)rintf(v.w * inv)};
+        uint32_t hp = 0, lp = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int h = (qv[i] + 128) >> 8;
+            const int l = qv[i] - 256 * h;
+            hp |= (uint32_t)(h & 0xff) << (8 * i);
+            lp |= (uint32_t)(l & 0xff) << (8 * i);
+        }
+        const int j = lane >> 3, o = 4 * (lane & 7);
+        int8_t *dst = q.planes + (uint64_t)row * K * 2 + (uint64_t)(sb * 8 + j) * 64 + o;
+        *reinterpret_cast<uint32_t *>(dst) = hp;
+        *reinterpret_cast<uint32_t *>(dst + 32) = lp;
+        int sum = qv[0] + qv[1] + qv[2] + qv[3];
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        sum += __shfl_xor(sum, 4);
+        if ((lane & 7) == 0) q.sums[(uint64_t)row * (K / 32) + sb * 8 + j] = sum;
+        if (lane == 0) q.scales[(uint64_t)row * nsb + sb] = m > 0.f ? m / (float)kQMax : 0.f;
+    }
+}
+
+// ---------------------------------------------------------------- GEMM
+struct BgArgs {
+    FusedGemmArgs f;
+    BgQuant q;
+    int tiles[kFusedMaxSeg + 1];  // prefix counts of workgroups (8 tiles of 16 channels) per segment
+    int swiglu;
+};
+
+__device__ __forceinline__ i32x4 mfma_i8(int64_t a, int64_t b) {
+    const i32x4 zero = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero, 0, 0, 0);
+}
+
+// 8 bytes at an even byte address (Q6_K blocks are 210 B): two dword-aligned
+// loads and a byte shift.
+__device__ __forceinline__ uint64_t load8_even(const uint8_t *p) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
+    const uint32_t sh = (uint32_t)(a & 3);
+    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+    const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
+    const uint32_t hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
+    return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
+// Signed q - 32 for eight packed unsigned 6-bit values (one per byte).
+__device__ __forceinline__ uint64_t q6_to_i8(uint64_t q6) {
+    const uint64_t t = q6 ^ 0x2020202020202020ull;
+    const uint64_t s = t & 0x2020202020202020ull;
+    return t | (s << 1) | (s << 2);
+}
+
+// One super-block of one channel, as lane (c, g) needs it.
+struct WQ4 {
+    uint4 hdr;       // d, dmin, 12 scale bytes
+    uint64_t q[4];   // bytes [32 p + 8 g, +8) of the 128 quant bytes
+};
+struct WQ6 {
+    uint64_t ql[4];  // ql bytes [64 half + 32 p + 8 g, +8), index 2 half + p
+    uint64_t qh[2];  // qh bytes [32 half + 8 g, +8)
+    uint4 sc;        // 16 int8 scales
+    uint32_t d;      // fp16 d in the low half
+};
+
+__device__ __forceinline__ void load_q4(WQ4 &w, const uint8_t *blk, int g) {
+    w.hdr = *reinterpret_cast<const uint4 *>(blk);
+#pragma unroll
+    for (int p = 0; p < 4; p++) w.q[p] = *reinterpret_cast<const uint64_t *>(blk + 16 + 32 * p + 8 * g);
+}
+
+__device__ __forceinline__ void load_q6(WQ6 &w, const uint8_t *blk, int g) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) w.ql[i] = load8_even(blk + 64 * (i >> 1) + 32 * (i & 1) + 8 * g);
+#pragma unroll
+    for (int h = 0; h < 2; h++) w.qh[h] = load8_even(blk + 128 + 32 * h + 8 * g);
+    // the block's last 18 bytes by 2-byte loads: nothing past byte 210 is read
+    const uint64_t s01 = load8_even(blk + 192);
+    const uint16_t *t = reinterpret_cast<const uint16_t *>(blk + 200);
+    w.sc.x = (uint32_t)s01;
+    w.sc.y = (uint32_t)(s01 >> 32);
+    w.sc.z = (uint32_t)t[0] | ((uint32_t)t[1] << 16);
+    w.sc.w = (uint32_t)t[2] | ((uint32_t)t[3] << 16);
+    w.d = t[4];
+}
+
+__device__ __forceinline__ int sbyte(const uint4 &v, int i) {
+    const uint32_t w = i < 4 ? v.x : (i < 8 ? v.y : (i < 12 ? v.z : v.w));
+    return (int)(int8_t)((w >> (8 * (i & 3))) & 0xff);
+}
+
+// tensor/quant.go:96-103 getScaleMinK4 for sub-block j (scale bytes in
+// words s1, s2, s3 = block bytes 4..15).
+__device__ __forceinline__ void scale_min_k4(int j, uint32_t s1, uint32_t s2, uint32_t s3, int *sc, int *mn) {
+    if (j < 4) {
+        *sc = (s1 >> (8 * j)) & 63;
+        *mn = (s2 >> (8 * j)) & 63;
+    } else {
+        const int k = j - 4;
+        const uint32_t a = (s1 >> (8 * k)) & 0xff, b = (s2 >> (8 * k)) & 0xff, cc = (s3 >> (8 * k)) & 0xff;
+        *sc = (int)((cc & 0xF) | ((a >> 6) << 4));
+        *mn = (int)((cc >> 4) | ((b >> 6) << 4));
+    }
+}
+
+__device__ __forceinline__ int seg_of(const BgArgs &A, int tile) {
+    int s = 0;
+#pragma unroll
+    for (int i = 1; i < kFusedMaxSeg; i++)
+        if (i < A.f.nseg && tile >= A.tiles[i]) s = i;
+    return s;
+}
+
+__device__ __forceinline__ float out_map(const FusedSeg &S, int n, float v) {
+    switch (S.act) {
+    case 1: return silu_ref(v);
+    case 2: return sigmoid_ref(v);
+    case 3: return (float)exp((double)__fmul_rn(softplus_ref(__fadd_rn(v, S.p0[n])), S.p1[n]));
+    default: return v;
+    }
+}
+
+// Stages super-block sb of the workgroup's rows (planes, sums, scales) in LDS.
+__device__ __forceinline__ void stage_rows(const BgArgs &A, uint8_t *la, int32_t *lsum, float *lxs, int m0, int mrows,
+                                           int sb) {
+    const int K = A.f.K, nsb = K / 256, nsub = K / 32;
+    // thread piece = (row, sub-block, plane, 16-byte half)
+    for (int idx = threadIdx.x; idx < kBgRows * 8 * 4; idx += kBgThreads) {
+        const int r = idx >> 5, j = (idx >> 2) & 7, p = (idx >> 1) & 1, half = idx & 1;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (r < mrows)
+            v = *reinterpret_cast<const uint4 *>(A.q.planes + (uint64_t)(m0 + r) * K * 2 + (uint64_t)(sb * 8 + j) * 64 +
+                                                 32 * p + 16 * half);
+        const int t = r >> 3, rr = (r & 7) + 8 * p;
+        uint8_t *d0 = la + ((uint32_t)((t * 8 + j) * 4 + 2 * half) * 16 + rr) * 8;
+        *reinterpret_cast<uint2 *>(d0) = make_uint2(v.x, v.y);
+        *reinterpret_cast<uint2 *>(d0 + 16 * 8) = make_uint2(v.z, v.w);
+    }
+    for (int idx = threadIdx.x; idx < kBgRows * 8; idx += kBgThreads) {
+        const int r = idx >> 3, j = idx & 7;
+        lsum[((r >> 3) * 8 + j) * 8 + (r & 7)] = r < mrows ? A.q.sums[(uint64_t)(m0 + r) * nsub + sb * 8 + j] : 0;
+    }
+    if (threadIdx.x < kBgRows) {
+        const int r = threadIdx.x;
+        lxs[r] = r < mrows ? A.q.scales[(uint64_t)(m0 + r) * nsb + sb] : 0.f;
+    }
+}
+
+// The main loop of one wave over the super-blocks (weights of dtype DT).
+template <int DT>
+__device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *la, int32_t *lsum, float *lxs, int m0, int mrows,
+                                        bool live, const uint8_t *wrow, float (&y)[8][4]) {
+    const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+    const int nsb = A.f.K / 256;
+    const int rb = 4 * (g & 1);
+    typedef typename std::conditional<DT == kQ4K, WQ4, WQ6>::type W;
+    constexpr int blk = DT == kQ4K ? 144 : 210;
+    W w{};
+    if (live) {
+        if constexpr (DT == kQ4K) load_q4(w, wrow, g);
+        else load_q6(w, wrow, g);
+    }
+    for (int sb = 0; sb < nsb; sb++) {
+        __syncthreads();  // the previous super-block's readers are done with LDS
+        stage_rows(A, la, lsum, lxs, m0, mrows, sb);
+        const W cur = w;  // this super-block; the next one's loads go out now
+        if (live && sb + 1 < nsb) {
+            if constexpr (DT == kQ4K) load_q4(w, wrow + (uint64_t)(sb + 1) * blk, g);
+            else load_q6(w, wrow + (uint64_t)(sb + 1) * blk, g);
+        }
+        __syncthreads();
+        if (!live) continue;
+        if constexpr (DT == kQ4K) {
+            const float d = h2f((uint16_t)(cur.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(cur.hdr.x >> 16));
+#pragma unroll
+            for (int t = 0; t < 8; t++) {  // all 8 tiles: rows past the end are zero in LDS
+                int acc[4] = {0, 0, 0, 0}, ms[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const uint64_t raw = cur.q[j >> 1];
+                    const int64_t bq = (int64_t)((j & 1) ? (raw >> 4) & 0x0F0F0F0F0F0F0F0Full : raw & 0x0F0F0F0F0F0F0F0Full);
+                    int sc, mn;
+                    scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sc, &mn);
+                    const int64_t a = *reinterpret_cast<const int64_t *>(la + ((uint32_t)((t * 8 + j) * 4 + g) * 16 + c) * 8);
+                    const i32x4 r = mfma_i8(a, bq);
+                    const int4 sm = *reinterpret_cast<const int4 *>(lsum + (t * 8 + j) * 8 + rb);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[i] += r[i] * sc;
+                    ms[0] += mn * sm.x;
+                    ms[1] += mn * sm.y;
+                    ms[2] += mn * sm.z;
+                    ms[3] += mn * sm.w;
+                }
+                const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
+                const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int lo = __shfl_xor(acc[i], 32);
+                    y[t][i] += xsv[i] * (d * (256.f * (float)acc[i] + (float)lo) - dmin * (float)ms[i]);
+                }
+                __builtin_amdgcn_sched_barrier(0);  // one A tile at a time (register pressure)
+            }
+        } else {
+            const float d = h2f((uint16_t)cur.d);
+            int64_t bq[8];
+            int sc2[8];  // scale of elements 0..15 (low half) and 16..31 (high half) of sub-block j
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int half = j >> 2, qd = j & 3;
+                const uint64_t lo4 = (cur.ql[2 * half + (qd & 1)] >> (4 * (qd >> 1))) & 0x0F0F0F0F0F0F0F0Full;
+                const uint64_t hi2 = ((cur.qh[half] >> (2 * qd)) & 0x0303030303030303ull) << 4;
+                bq[j] = (int64_t)q6_to_i8(lo4 | hi2);
+                sc2[j] = (sbyte(cur.sc, 8 * half + 2 * qd) & 0xffff) | (sbyte(cur.sc, 8 * half + 2 * qd + 1) << 16);
+            }
+#pragma unroll
+            for (int t = 0; t < 8; t++) {  // all 8 tiles: rows past the end are zero in LDS
+                int acc[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int64_t a = *reinterpret_cast<const int64_t *>(la + ((uint32_t)((t * 8 + j) * 4 + g) * 16 + c) * 8);
+                    // lanes g < 2 hold elements 0..15 (first scale group)
+                    const i32x4 r0 = mfma_i8(a, g < 2 ? bq[j] : 0);
+                    const i32x4 r1 = mfma_i8(a, g < 2 ? 0 : bq[j]);
+                    const int s0 = (int)(int16_t)(sc2[j] & 0xffff), s1 = sc2[j] >> 16;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) acc[i] += r0[i] * s0 + r1[i] * s1;
+                }
+                const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
+                const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int lo = __shfl_xor(acc[i], 32);
+                    y[t][i] += xsv[i] * (d * (256.f * (float)acc[i] + (float)lo));
+                }
+                __builtin_amdgcn_sched_barrier(0);  // one A tile at a time (register pressure)
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBgThreads) void bg_gemm_kernel(const BgArgs A) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    uint8_t *la = lds;
+    int32_t *lsum = reinterpret_cast<int32_t *>(lds + kBgLdsA);
+    float *lxs = reinterpret_cast<float *>(lds + kBgLdsA + 8 * 8 * 8 * 4);
+    const FusedGemmArgs &F = A.f;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = lane & 15, g = lane >> 4;
+    const int m0 = blockIdx.y * kBgRows;
+    const int mrows = min(kBgRows, F.rows - m0);
+
+    // this wave's tile: the workgroup's segment (segments start on whole
+    // workgroups, so a workgroup has one weight type) and tile 8 w + wave, or
+    // (SwiGLU) waves 0..3 gate tiles and 4..7 the same up tiles
+    int tile, seg;
+    if (A.swiglu) {
+        tile = blockIdx.x * 4 + (wave & 3);
+        seg = wave >> 2;
+    } else {
+        seg = seg_of(A, blockIdx.x);
+        tile = (blockIdx.x - A.tiles[seg]) * kBgWaves + wave;
+    }
+    const FusedSeg &S = F.seg[seg];
+    const int n0 = tile * 16;
+    const bool live = n0 < S.n;
+    const int n = min(n0 + c, S.n - 1);  // clamped channel for the loads
+    const uint8_t *wrow = static_cast<const uint8_t *>(S.w) + (uint64_t)n * S.row_bytes;
+
+    float y[8][4];
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) y[t][i] = 0.f;
+    if (S.dtype == kQ6K)
+        bg_main<kQ6K>(A, la, lsum, lxs, m0, mrows, live, wrow, y);
+    else
+        bg_main<kQ4K>(A, la, lsum, lxs, m0, mrows, live, wrow, y);
+
+    // epilogue: lanes g < 2 hold rows 8 t + 4 g + i of channel n0 + c
+    if (A.swiglu) {
+        __syncthreads();
+        float *up = reinterpret_cast<float *>(lds);  // [4 tiles][64 rows][16]
+        if (wave >= 4 && g < 2) {
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) up[((wave - 4) * kBgRows + 8 * t + 4 * g + i) * 16 + c] = y[t][i];
+        }
+        __syncthreads();
+        if (wave < 4 && g < 2 && live && n0 + c < S.n) {
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 8 * t + 4 * g + i;
+                    if (r >= mrows) continue;
+                    const float u = up[(wave * kBgRows + r) * 16 + c];
+                    S.out[(uint64_t)(m0 + r) * S.n + n0 + c] = __fmul_rn(silu_ref(y[t][i]), u);
+                }
+        }
+        return;
+    }
+    if (!live || g >= 2 || n0 + c >= S.n) return;
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 8 * t + 4 * g + i;
+            if (r >= mrows) continue;
+            const uint64_t o = (uint64_t)(m0 + r) * S.n + n0 + c;
+            float v = y[t][i];
+            if (F.epilogue == kEpiResidual) v = __fadd_rn(v, S.res[o]);
+            else v = out_map(S, n0 + c, v);
+            S.out[o] = v;
+        }
+}
+
+}  // namespace
+
+uint64_t fused_gemm_rows_ws(int rows, int K) {
+    return (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 32) * 4 + (uint64_t)rows * (K / 256) * 4 + 256;
+}
+
+hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t s) {
+    BgArgs A{};
+    A.f = a;
+    A.q = bg_view(ws, a.rows, a.K);
+    A.swiglu = a.epilogue == kEpiSwiglu ? 1 : 0;
+    // segment prefix in workgroups of 8 tiles (a workgroup never straddles two segments)
+    A.tiles[0] = 0;
+    for (int i = 0; i < a.nseg; i++) A.tiles[i + 1] = A.tiles[i] + (a.seg[i].n + 16 * kBgWaves - 1) / (16 * kBgWaves);
+    for (int i = a.nseg + 1; i <= kFusedMaxSeg; i++) A.tiles[i] = A.tiles[a.nseg];
+    const uint32_t plds = (uint32_t)a.K * 4;
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(bg_prologue_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+        attr = true;
+    }
+    bg_prologue_kernel<<<(unsigned)a.rows, 256, plds, s>>>(a, A.q);
+    const unsigned gx = A.swiglu ? (unsigned)((a.seg[0].n + 63) / 64) : (unsigned)A.tiles[a.nseg];
+    const unsigned gy = (unsigned)((a.rows + kBgRows - 1) / kBgRows);
+    bg_gemm_kernel<<<dim3(gx, gy), kBgThreads, kBgLds, s>>>(A);
+    return hipGetLastError();
+}
+
+}  // namespace yk

@@ -111,6 +111,13 @@ static int fused_tiles(const yuuka_op &op, int nseg) {
     return tt;
 }
 
+// Rows beyond what one fused launch serves from LDS go to the many-row
+// kernel (YUUKA_FGEMM_CHUNKED keeps 9..16 rows on the chunked kernel).
+static bool fused_many_rows(const yuuka_op &op) {
+    if (op.n[1] > 16) return true;
+    return op.n[1] > 8 && !getenv("YUUKA_FGEMM_CHUNKED");
+}
+
 static FusedGemmArgs fused_args(const yuuka_op &op) {
     FusedGemmArgs a{};
     a.x = at<const float>(op, 0);
@@ -346,7 +353,7 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         const uint64_t K = op.n[0], rows = op.n[1];
         const int nseg = fused_segments(op);
         const uint32_t epi = op.u[1];
-        if (!K || K % 256 || K > 65536 || rows < 1 || rows > 16 || nseg == 0 || epi > kEpiSwiglu ||
+        if (!K || K % 256 || K > 65536 || rows < 1 || rows > 512 || nseg == 0 || epi > kEpiSwiglu ||
             (epi == kEpiSwiglu && nseg != 2) || op.off[0] % 16 || op.off[1] % 16 ||
             !buf_ok(op.buf[0], op.off[0], K * rows * 4) || (op.buf[1] && !buf_ok(op.buf[1], op.off[1], K * 4)))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid GEMM_FUSED shape or activation buffers");
@@ -377,6 +384,12 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
             if (act > 3) return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED segment %d: output map %u", i, act);
             if (act == 3 && !buf_ok(op.buf[10 + i], op.off[10 + i], 2 * op.n[2 + i] * 4))
                 return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_FUSED segment %d: decay parameters {dt, a}", i);
+        }
+        if (fused_many_rows(op)) {  // k_bgemm.hip: quantized rows in the workspace
+            if (K > 16384) return fail(YUUKA_ERR_UNSUPPORTED, "GEMM_FUSED: K %llu over 16384 rows > 8",
+                                       (unsigned long long)K);
+            *ws = fused_gemm_rows_ws((int)rows, (int)K);
+            return YUUKA_OK;
         }
         if (fused_gemm_chunk_sb((int)rows, (int)K, fused_tiles(op, nseg), op.buf[1] != nullptr, op.buf[14] != nullptr) < 1)
             return fail(YUUKA_ERR_UNSUPPORTED, "GEMM_FUSED: activations do not fit LDS");
@@ -622,6 +635,10 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
     }
     case YUUKA_EXT_OP_GEMM_FUSED: {
         FusedGemmArgs a = fused_args(op);
+        if (fused_many_rows(op)) {
+            err = launch_fused_gemm_rows(a, ctx.ws, s);
+            break;
+        }
         const int tt = fused_tiles(op, a.nseg);
         a.chunk_sb = fused_gemm_chunk_sb(a.rows, a.K, tt, a.norm != nullptr, a.gate != nullptr);
         err = launch_fused_gemm(a, tt, s);
