@@ -381,6 +381,9 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
  *               n={rows, groups, heads, state, conv_dim, inner}; u0 kernel.
  *               Advances both states by result[0] + 1 rows (the accepted
  *               prefix of a RECURRENT_CHUNK run with YUUKA_EXT_FLAG_DEFER).
+ *               u1 = requests (0 or 1: one): states, rows and the [u1][4]
+ *               results request-major; the same u1 on RECURRENT_CHUNK
+ *               (with DEFER and RAW_OUT) scans every request in one launch.
  *   ADVANCE:    buf0 dynamic buffer {token, position}, buf1 int32 result,
  *               optional buf2 uint64 step counter; n0 = rows. position +=
  *               result[0] + 1; step += 1.

@@ -290,14 +290,18 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
         for (int j = 0; j < nreq; j++)
             b.add(YUUKA_EXT_OP_ROPE_TABLE, {q->rope}, {R1, (uint64_t)c.rope_dim, 0}, {}, {(float)c.rope_base}, 0,
                   {(uint64_t)j * R1 * half * 8}, q->dyn, dyn_off(j));
+    // the recurrent scan of every request in one op (requests in grid z;
+    // states and rows request-major); the split path goes request by request
     auto recurrent = [&](Layer &L, uint32_t extra_flags) {
-        for (int j = 0; j < nreq; j++) {
+        const bool together = (extra_flags & YUUKA_EXT_FLAG_RAW_OUT) && R1 <= 32;
+        for (int j = 0; j < nreq; j += together ? nreq : 1) {
             const uint64_t r0 = (uint64_t)j * R1, rq = (uint64_t)(first + j);
             b.add(YUUKA_OP_RECURRENT_CHUNK,
                   {L.conv_state, L.mat_state, L.qkv_rows, q->z, L.alpha_rows, L.beta_rows, L.conv, L.dt, L.a,
                    L.ssm_norm, q->gdn_out, L.conv_rows},
                   {R1, (uint64_t)c.groups, (uint64_t)c.rank, (uint64_t)c.state_size, cd, (uint64_t)c.inner},
-                  {(uint32_t)c.conv_kernel}, {c.eps, qscale}, YUUKA_EXT_FLAG_DEFER | extra_flags,
+                  {(uint32_t)c.conv_kernel, together ? (uint32_t)nreq : 1u}, {c.eps, qscale},
+                  YUUKA_EXT_FLAG_DEFER | extra_flags,
                   {rq * L.conv_bytes, rq * L.mat_bytes, r0 * cd * 4, r0 * c.inner * 4, r0 * c.rank * 4,
                    r0 * c.rank * 4, 0, 0, 0, 0, r0 * c.inner * 4, r0 * cd * 4});
         }
@@ -418,7 +422,10 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
               {a.mode, a.top_k, (uint32_t)first, (uint32_t)R1}, {a.temperature, a.top_p}, 0,
               {0, 4, (uint64_t)first * 16, 0, 0, (uint64_t)first * 4});
     }
-    for (int j = 0; j < nreq; j++) {
+    // commit of every request's accepted prefix: one op per layer covering
+    // all requests (consecutive layers merge into one launch)
+    const bool commit_together = R1 <= 32;
+    for (int j = 0; j < nreq; j += commit_together ? nreq : 1) {
         const uint64_t r0 = (uint64_t)j * R1, rq = (uint64_t)(first + j);
         for (int i = 0; i < c.n_layers; i++) {
             Layer &L = q->layers[i];
@@ -427,7 +434,8 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
                   {L.conv_state, L.mat_state, L.qkv_rows, L.conv_rows, L.alpha_rows, L.beta_rows, L.dt, L.a,
                    q->result},
                   {R1, (uint64_t)c.groups, (uint64_t)c.rank, (uint64_t)c.state_size, cd, (uint64_t)c.inner},
-                  {(uint32_t)c.conv_kernel}, {}, fused ? YUUKA_EXT_FLAG_GDN_COEF : 0u,
+                  {(uint32_t)c.conv_kernel, commit_together ? (uint32_t)nreq : 1u}, {},
+                  fused ? YUUKA_EXT_FLAG_GDN_COEF : 0u,
                   {rq * L.conv_bytes, rq * L.mat_bytes, r0 * cd * 4, r0 * cd * 4, r0 * c.rank * 4, r0 * c.rank * 4, 0,
                    0, rq * 16});
         }

@@ -364,6 +364,16 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
     const int h = blockIdx.x, cb = blockIdx.y;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int R = g.rows;
+    {  // request blockIdx.z: states and rows are request-major
+        const uint64_t rq = blockIdx.z;
+        conv_state += rq * (uint64_t)(g.kernel - 1) * g.conv_dim;
+        state += rq * (uint64_t)g.rank * kS * kS;
+        qkv += rq * (uint64_t)R * g.conv_dim;
+        alpha_raw += rq * (uint64_t)R * g.rank;
+        beta_raw += rq * (uint64_t)R * g.rank;
+        raw_out += rq * (uint64_t)R * g.rank * kS;
+        conv_out += rq * (uint64_t)R * g.conv_dim;
+    }
     const int key_dim = g.groups * kS;
     const int kh = h % g.groups;
     float *qk = sm;                 // [R][2][128] q, k
@@ -522,22 +532,36 @@ __device__ __forceinline__ void gdn_commit_cols_body(float *__restrict__ conv_st
     for (int ii = 0; ii < 16; ii++) mat[(uint64_t)(p * 16 + ii) * kS + j] = s_reg[ii];
 }
 
+// Request rq of a request-major launch: its state, rows and result.
+__device__ __forceinline__ void gdn_commit_request(float *conv_state, float *state, const float *qkv,
+                                                   const float *conv, const float *alpha_raw, const float *beta_raw,
+                                                   const float *dt, const float *a_log, const GdnArgs &g,
+                                                   const int32_t *accept_result, uint64_t rq) {
+    const uint64_t R = (uint64_t)g.rows;
+    const int32_t *res = accept_result ? accept_result + 4 * rq : nullptr;
+    const int n = res ? min(res[0] + 1, g.rows) : g.rows;
+    gdn_commit_cols_body(conv_state + rq * (uint64_t)(g.kernel - 1) * g.conv_dim,
+                         state + rq * (uint64_t)g.rank * kS * kS, qkv + rq * R * g.conv_dim,
+                         conv + rq * R * g.conv_dim, alpha_raw + rq * R * g.rank, beta_raw + rq * R * g.rank, dt,
+                         a_log, g, n);
+}
+
 __global__ __launch_bounds__(kColThreads) void gdn_commit_cols_kernel(
     float *__restrict__ conv_state, float *__restrict__ state, const float *__restrict__ qkv,
     const float *__restrict__ conv, const float *__restrict__ alpha_raw, const float *__restrict__ beta_raw,
     const float *__restrict__ dt, const float *__restrict__ a_log, GdnArgs g,
     const int32_t *__restrict__ accept_result) {
-    const int n = accept_result ? min(accept_result[0] + 1, g.rows) : g.rows;
-    gdn_commit_cols_body(conv_state, state, qkv, conv, alpha_raw, beta_raw, dt, a_log, g, n);
+    gdn_commit_request(conv_state, state, qkv, conv, alpha_raw, beta_raw, dt, a_log, g, accept_result, blockIdx.z);
 }
 
-// Every recurrent layer's commit in one launch (blockIdx.z = layer): the
-// layers are independent once the acceptance result is known.
+// Every recurrent layer's commit in one launch (blockIdx.z = layer * nreq +
+// request): the layers are independent once the acceptance result is known.
 __global__ __launch_bounds__(kColThreads) void gdn_commit_cols_multi_kernel(const GdnCommitSet set, GdnArgs g,
                                                                             const int32_t *__restrict__ accept_result) {
-    const GdnCommitLayer &L = set.layer[blockIdx.z];
-    const int n = accept_result ? min(accept_result[0] + 1, g.rows) : g.rows;
-    gdn_commit_cols_body(L.conv_state, L.state, L.qkv, L.conv, L.alpha, L.beta, L.dt, L.a_log, g, n);
+    const int nq = g.nreq > 0 ? g.nreq : 1;
+    const GdnCommitLayer &L = set.layer[blockIdx.z / nq];
+    gdn_commit_request(L.conv_state, L.state, L.qkv, L.conv, L.alpha, L.beta, L.dt, L.a_log, g, accept_result,
+                       blockIdx.z % nq);
 }
 
 }  // namespace
@@ -548,7 +572,7 @@ hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, c
                                   const float *alpha_raw, const float *beta_raw, const float *conv_w, const float *dt,
                                   const float *a_log, float *raw_out, float *conv_out, const GdnArgs &g,
                                   hipStream_t s) {
-    const dim3 grid((unsigned)g.rank, kS / kCols);
+    const dim3 grid((unsigned)g.rank, kS / kCols, (unsigned)(g.nreq > 0 ? g.nreq : 1));
     if (g.rows <= 16)
         gdn_verify_cols_kernel<16><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
             conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
@@ -561,7 +585,7 @@ hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, c
 hipError_t launch_gdn_commit_cols(float *conv_state, float *state, const float *qkv, const float *conv,
                                   const float *alpha_raw, const float *beta_raw, const float *dt, const float *a_log,
                                   const GdnArgs &g, const int32_t *accept_result, hipStream_t s) {
-    gdn_commit_cols_kernel<<<dim3((unsigned)g.rank, kS / kCols), kColThreads, 0, s>>>(
+    gdn_commit_cols_kernel<<<dim3((unsigned)g.rank, kS / kCols, (unsigned)(g.nreq > 0 ? g.nreq : 1)), kColThreads, 0, s>>>(
         conv_state, state, qkv, conv, alpha_raw, beta_raw, dt, a_log, g, accept_result);
     return hipGetLastError();
 }
@@ -569,7 +593,8 @@ hipError_t launch_gdn_commit_cols(float *conv_state, float *state, const float *
 hipError_t launch_gdn_commit_cols_multi(const GdnCommitSet &set, int layers, const GdnArgs &g,
                                         const int32_t *accept_result, hipStream_t s) {
     if (layers < 1 || layers > kGdnCommitMaxLayers) return hipErrorInvalidValue;
-    gdn_commit_cols_multi_kernel<<<dim3((unsigned)g.rank, kS / kCols, (unsigned)layers), kColThreads, 0, s>>>(
+    gdn_commit_cols_multi_kernel<<<dim3((unsigned)g.rank, kS / kCols, (unsigned)(layers * (g.nreq > 0 ? g.nreq : 1))),
+                                   kColThreads, 0, s>>>(
         set, g, accept_result);
     return hipGetLastError();
 }

@@ -37,6 +37,7 @@ struct GdnArgs {
     int rows, groups, rank, state, conv_dim, inner, kernel;
     float eps, q_scale;
     int coef;  // 1: alpha / beta buffers hold the decay and sigmoid(beta)
+    int nreq;  // requests in one launch (column-split kernels): states and rows request-major
 };
 
 hipError_t launch_embedding(const void *table, uint32_t dtype, uint64_t row_bytes, const int32_t *tokens, int vocab,

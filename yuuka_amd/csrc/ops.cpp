@@ -82,6 +82,7 @@ static GdnArgs gdn_args(const yuuka_op &op) {
     g.eps = op.f[0];
     g.q_scale = op.f[1];
     g.coef = (op.flags & YUUKA_EXT_FLAG_GDN_COEF) ? 1 : 0;
+    g.nreq = op.u[1] ? (int)op.u[1] : 1;
     return g;
 }
 
@@ -317,14 +318,16 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         if (st != YUUKA_OK) return st;
         for (int i = 0; i < 12; i++)
             if (!op.buf[i]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "recurrent chunk buffer %d is null", i);
-        const uint64_t R = (uint64_t)g.rows;
-        if (!buf_ok(op.buf[0], op.off[0], (uint64_t)(g.kernel - 1) * g.conv_dim * 4) ||
-            !buf_ok(op.buf[1], op.off[1], (uint64_t)g.rank * g.state * g.state * 4) ||
+        const uint64_t R = (uint64_t)g.rows * g.nreq, nq = (uint64_t)g.nreq;
+        if (g.nreq > 1 && (!(op.flags & YUUKA_EXT_FLAG_DEFER) || !(op.flags & YUUKA_EXT_FLAG_RAW_OUT) || g.rows > 32))
+            return fail(YUUKA_ERR_UNSUPPORTED, "recurrent chunk: several requests need deferred raw outputs, <= 32 rows");
+        if (!buf_ok(op.buf[0], op.off[0], nq * (g.kernel - 1) * g.conv_dim * 4) ||
+            !buf_ok(op.buf[1], op.off[1], nq * g.rank * g.state * g.state * 4) ||
             !buf_ok(op.buf[2], op.off[2], R * g.conv_dim * 4) || !buf_ok(op.buf[3], op.off[3], R * g.inner * 4) ||
             !buf_ok(op.buf[4], op.off[4], R * g.rank * 4) || !buf_ok(op.buf[5], op.off[5], R * g.rank * 4) ||
             !buf_ok(op.buf[10], op.off[10], R * g.inner * 4) || !buf_ok(op.buf[11], op.off[11], R * g.conv_dim * 4))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "recurrent chunk buffers too small");
-        if ((op.flags & YUUKA_EXT_FLAG_RAW_OUT) && (!(op.flags & YUUKA_EXT_FLAG_DEFER) || R > 32))
+        if ((op.flags & YUUKA_EXT_FLAG_RAW_OUT) && (!(op.flags & YUUKA_EXT_FLAG_DEFER) || g.rows > 32))
             return fail(YUUKA_ERR_UNSUPPORTED, "recurrent chunk: raw outputs need the deferred mode and <= 32 rows");
         *ws = R * g.inner * 4;  // raw per-head outputs before the gated norm
         return YUUKA_OK;
@@ -425,6 +428,15 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         if (st != YUUKA_OK) return st;
         for (int i = 0; i < 9; i++)
             if (!op.buf[i]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "GDN commit buffer %d is null", i);
+        if (g.nreq > 1 && g.rows > 32)
+            return fail(YUUKA_ERR_UNSUPPORTED, "GDN commit: several requests need <= 32 rows");
+        const uint64_t nq = (uint64_t)g.nreq, R = nq * g.rows;
+        if (!buf_ok(op.buf[0], op.off[0], nq * (g.kernel - 1) * g.conv_dim * 4) ||
+            !buf_ok(op.buf[1], op.off[1], nq * g.rank * g.state * g.state * 4) ||
+            !buf_ok(op.buf[2], op.off[2], R * g.conv_dim * 4) || !buf_ok(op.buf[3], op.off[3], R * g.conv_dim * 4) ||
+            !buf_ok(op.buf[4], op.off[4], R * g.rank * 4) || !buf_ok(op.buf[5], op.off[5], R * g.rank * 4) ||
+            !buf_ok(op.buf[8], op.off[8], nq * 16))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "GDN commit buffers too small");
         return YUUKA_OK;
     }
     case YUUKA_OP_MOE_ROUTE: {  // hip.go:1585-1608: n={rows, experts, used}
@@ -516,7 +528,7 @@ int gdn_commit_run(const yuuka_op *ops, int count) {
     while (n < count && n < kGdnCommitMaxLayers && ops[n].code == YUUKA_EXT_OP_GDN_COMMIT &&
            ops[n].flags == ops[0].flags && ops[n].buf[8] == ops[0].buf[8] && ops[n].off[8] == ops[0].off[8]) {
         const GdnArgs g = gdn_args(ops[n]);
-        if (g.rows != g0.rows || g.groups != g0.groups || g.rank != g0.rank || g.state != g0.state ||
+        if (g.rows != g0.rows || g.nreq != g0.nreq || g.groups != g0.groups || g.rank != g0.rank || g.state != g0.state ||
             g.conv_dim != g0.conv_dim || g.inner != g0.inner || g.kernel != g0.kernel || g.coef != g0.coef)
             break;
         n++;
@@ -665,7 +677,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
     case YUUKA_EXT_OP_GDN_COMMIT: {
         const GdnArgs g = gdn_args(op);
         const int32_t *res = at<const int32_t>(op, 8);
-        if (!getenv("YUUKA_GDN_SPLIT") && g.rows <= 32) {  // scan replay + conv window, column-split (k_gdn.hip)
+        if ((!getenv("YUUKA_GDN_SPLIT") || g.nreq > 1) && g.rows <= 32) {  // scan replay + conv window, column-split (k_gdn.hip)
             err = launch_gdn_commit_cols(at<float>(op, 0), at<float>(op, 1), at<const float>(op, 2), at<const float>(op, 3),
                                     at<const float>(op, 4), at<const float>(op, 5), at<const float>(op, 6),
                                     at<const float>(op, 7), g, res, s);
