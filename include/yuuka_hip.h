@@ -407,7 +407,8 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
  *               DeltaNet decay exp(softplus(v + dt[n]) * a[n]) with buf10+i
  *               holding {dt[N_i], a[N_i]} (recurrent.go:66-70).
  *   ROPE_TABLE: buf0 FP32 {cos, sin} [rows][rot_dim/2] of positions
- *               position + n2 + row; n={rows, rot_dim, displacement};
+ *               position + n2 + row; n={rows, rot_dim, displacement,
+ *               requests (0: one), rows between requests (OWN_POS pairs)};
  *               f0 base (float64 angles as forward.go:495-514).
  *   ATTN_VERIFY: gated paged attention of the verify rows with the per-head
  *               q/k RMSNorm, RoPE and the KV write folded in: buf0 FP32 raw
@@ -417,8 +418,12 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
  *               table, buf7 q_norm [head_dim], buf8 k_norm [head_dim],
  *               buf9 ROPE_TABLE output; n={kv_heads, heads, head_dim, kv_dim,
  *               rows, displacement}; u={block_size, capacity, kv dtype (F32 or
- *               F16), rot_dim}; f={scale, eps}. Writes the rows' K/V to the
- *               pool at position + displacement + row.
+ *               F16), rot_dim | requests << 8 | request_rows << 20};
+ *               f={scale, eps}. Writes the rows' K/V to the pool at position
+ *               + displacement + row. With requests > 1 (and OWN_POS) request
+ *               j's rows start request_rows rows after request j-1's, its
+ *               block table ceil(capacity / block_size) entries later and its
+ *               {token, position} pair 8 bytes later (one launch).
  *   MOE_ROUTER: FP32 router of the MoE FFN (ffn_gate_inp, forward.go:328):
  *               buf0 FP32 y [rows][hidden], buf1 FP32 router weight
  *               [experts][hidden], buf2 FP32 logits [rows][experts];

@@ -286,10 +286,9 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
     const bool attn_fused = !(attn_env && attn_env[0] == '0' && nreq == 1 && first == 0);
     bool any_attn = false;
     for (const Layer &L : q->layers) any_attn |= !L.recurrent;
-    if (attn_fused && any_attn)
-        for (int j = 0; j < nreq; j++)
-            b.add(YUUKA_EXT_OP_ROPE_TABLE, {q->rope}, {R1, (uint64_t)c.rope_dim, 0}, {}, {(float)c.rope_base}, 0,
-                  {(uint64_t)j * R1 * half * 8}, q->dyn, dyn_off(j));
+    if (attn_fused && any_attn)  // every request's rotation table in one op (request rows R1 apart)
+        b.add(YUUKA_EXT_OP_ROPE_TABLE, {q->rope}, {R1, (uint64_t)c.rope_dim, 0, (uint64_t)nreq, R1}, {},
+              {(float)c.rope_base}, 0, {0}, q->dyn, dyn_off(0));
     // the recurrent scan of every request in one op (requests in grid z;
     // states and rows request-major); the split path goes request by request
     auto recurrent = [&](Layer &L, uint32_t extra_flags) {
@@ -308,18 +307,20 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
     };
     auto attention = [&](Layer &L) {
         if (attn_fused) {
-            for (int j = 0; j < nreq; j++)
-                for (uint64_t c0 = 0; c0 < R1; c0 += kAttnRows) {
-                    const uint64_t n = std::min<uint64_t>(kAttnRows, R1 - c0), r0 = (uint64_t)j * R1 + c0;
-                    b.add(YUUKA_EXT_OP_ATTN_VERIFY,
-                          {q->q, q->k, q->v, L.kpool, L.vpool, q->attn, q->table, L.q_norm, L.k_norm, q->rope},
-                          {(uint64_t)c.kv_heads, (uint64_t)c.heads, hd, kvdim, n, c0},
-                          {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype, (uint32_t)c.rope_dim},
-                          {(float)(1.0 / std::sqrt((double)hd)), c.eps}, 0,
-                          {r0 * qdim * 4, r0 * kvdim * 4, r0 * kvdim * 4, 0, 0, r0 * odim * 4,
-                           (uint64_t)(first + j) * q->max_blocks * 4, 0, 0, r0 * half * 8},
-                          q->dyn, dyn_off(j));
-                }
+            // one op per block of kAttnRows query rows, every request in it
+            // (grid z; request rows R1 apart, tables max_blocks apart)
+            const uint32_t packed = (uint32_t)c.rope_dim | ((uint32_t)nreq << 8) | ((uint32_t)R1 << 20);
+            for (uint64_t c0 = 0; c0 < R1; c0 += kAttnRows) {
+                const uint64_t n = std::min<uint64_t>(kAttnRows, R1 - c0), r0 = c0;
+                b.add(YUUKA_EXT_OP_ATTN_VERIFY,
+                      {q->q, q->k, q->v, L.kpool, L.vpool, q->attn, q->table, L.q_norm, L.k_norm, q->rope},
+                      {(uint64_t)c.kv_heads, (uint64_t)c.heads, hd, kvdim, n, c0},
+                      {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype, packed},
+                      {(float)(1.0 / std::sqrt((double)hd)), c.eps}, 0,
+                      {r0 * qdim * 4, r0 * kvdim * 4, r0 * kvdim * 4, 0, 0, r0 * odim * 4,
+                       (uint64_t)first * q->max_blocks * 4, 0, 0, r0 * half * 8},
+                      q->dyn, dyn_off(0));
+            }
             return;
         }
         b.add(YUUKA_OP_RMSNORM_HEADS_BATCH, {q->k, L.k_norm, q->k}, {hd, (uint64_t)c.kv_heads, hd, R}, {}, {c.eps});

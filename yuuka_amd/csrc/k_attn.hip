@@ -55,15 +55,52 @@ __device__ __forceinline__ float wave_sum_f(float v) {
 
 // cos / sin of every (row, rotation pair): theta = pos * base^(-2i/rot).
 __global__ void rope_table_kernel(float2 *__restrict__ tab, int rows, int rot_dim, double base, ModelDyn dyn,
-                                  int displacement) {
+                                  int displacement, int rq_rows) {
     const int half = rot_dim / 2;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= rows * half) return;
+    if (blockIdx.y) {  // request blockIdx.y: its rows and {token, position} pair
+        tab += (uint64_t)blockIdx.y * rq_rows * half;
+        if (dyn.pos_dev) dyn.pos_dev += 2 * blockIdx.y;
+    }
     const int r = idx / half, i = idx % half;
     const int pos = cur_pos_a(dyn) + displacement + r;
     const double theta = (double)pos * pow(base, -2.0 * (double)i / (double)rot_dim);
     tab[idx] = make_float2((float)cos(theta), (float)sin(theta));
 }
+
+// Request blockIdx.z of a batched launch: offsets of its query rows (q),
+// key / value rows (kv), block table, rope rows, partial-result slab and
+// {token, position} pair.
+struct AttnReqOff {
+    uint64_t q, kv, table, rope, part;
+    int pos;
+};
+
+__device__ __forceinline__ AttnReqOff attn_request(const AttnVArgs &a, int ck) {
+    const uint64_t rq = blockIdx.z;
+    const uint64_t rows = rq * a.rq_rows;
+    AttnReqOff o;
+    o.q = rows * a.heads * (a.gated ? 2 * a.head_dim : a.head_dim);
+    o.kv = rows * a.kv_dim;
+    o.table = rq * (uint64_t)((a.capacity + a.block_size - 1) / a.block_size);
+    o.rope = rows * (a.rope_dim / 2);
+    o.part = rq * (uint64_t)((a.capacity + ck - 1) / ck) * a.rows * a.heads * (a.head_dim + 2);
+    o.pos = 2 * (int)rq;
+    return o;
+}
+
+#define YK_ATTN_REQUEST(CK)                                  \
+    {                                                        \
+        const AttnReqOff ro_ = attn_request(a, CK);          \
+        q += ro_.q;                                          \
+        k += ro_.kv;                                         \
+        v += ro_.kv;                                         \
+        table += ro_.table;                                  \
+        rope += ro_.rope;                                    \
+        part += ro_.part;                                    \
+        if (dyn.pos_dev) dyn.pos_dev += ro_.pos;             \
+    }
 
 template <int FMT> struct KvT;
 // CK keys per workgroup; rows of K / V in LDS are padded by PAD elements
@@ -140,6 +177,7 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
     extern __shared__ __align__(16) uint8_t lds[];
     T *kpool = reinterpret_cast<T *>(kpool_b);
     T *vpool = reinterpret_cast<T *>(vpool_b);
+    YK_ATTN_REQUEST(CK);
     const int kvh = blockIdx.y, chunk = blockIdx.x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int D = a.head_dim, R = a.rows;
@@ -425,6 +463,7 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
                                                                const float2 *__restrict__ rope, AttnVArgs a,
                                                                float *__restrict__ part, ModelDyn dyn) {
     extern __shared__ __align__(16) uint8_t lds[];
+    YK_ATTN_REQUEST(kMK);
     const int kvh = blockIdx.y, chunk = blockIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int r16 = lane & 15, g4 = lane >> 4;
@@ -642,11 +681,20 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
 // Merges the chunk partials of one (query head, row) and applies the output
 // gate sigmoid(gate) (forward.go:452-456). The chunk weights exp(m_c - max)
 // are computed once per workgroup into LDS.
+__device__ __forceinline__ int chunks_total(const AttnVArgs &a, int ck) { return (a.capacity + ck - 1) / ck; }
+
 __global__ __launch_bounds__(256) void attn_merge_v_kernel(const float *__restrict__ q, const float *__restrict__ part,
                                                            AttnVArgs a, int ck, int chunks, float *__restrict__ out,
                                                            ModelDyn dyn) {
     extern __shared__ float wsh[];  // [chunks] weights
     __shared__ float red[4];
+    if (blockIdx.z) {  // request blockIdx.z
+        const uint64_t rq = blockIdx.z, rows = rq * a.rq_rows;
+        q += rows * a.heads * (a.gated ? 2 * a.head_dim : a.head_dim);
+        out += rows * a.heads * a.head_dim;
+        part += rq * (uint64_t)chunks_total(a, ck) * a.rows * a.heads * (a.head_dim + 2);
+        if (dyn.pos_dev) dyn.pos_dev += 2 * rq;
+    }
     const int r = blockIdx.y, h = blockIdx.x;
     const int D = a.head_dim;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -697,9 +745,10 @@ uint32_t attn_verify_lds_bytes(const AttnVArgs &a) {
 }
 
 hipError_t launch_rope_table(float2 *tab, int rows, int rot_dim, double base, const ModelDyn &dyn, int displacement,
-                             hipStream_t s) {
+                             hipStream_t s, int nreq, int rq_rows) {
     const int n = rows * (rot_dim / 2);
-    rope_table_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(tab, rows, rot_dim, base, dyn, displacement);
+    rope_table_kernel<<<dim3((unsigned)((n + 255) / 256), (unsigned)(nreq > 0 ? nreq : 1)), 256, 0, s>>>(
+        tab, rows, rot_dim, base, dyn, displacement, rq_rows > rows ? rq_rows : rows);
     return hipGetLastError();
 }
 
@@ -717,6 +766,7 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
     const int chunks = (a.capacity + ck - 1) / ck;
     const int launch_chunks = max_pos_hint >= 0 ? std::min(chunks, max_pos_hint / ck + 1) : chunks;
     auto *part = static_cast<float *>(scratch);
+    const unsigned nz = (unsigned)(a.nreq > 0 ? a.nreq : 1);
     static bool attr0 = false, attr1 = false, attr2 = false;
     if (mfma) {
         if (!attr2) {
@@ -724,7 +774,7 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
             attr2 = true;
         }
-        attn_verify_mfma_kernel<<<dim3((unsigned)launch_chunks, (unsigned)a.kv_heads), 256, kMfmaLds, s>>>(
+        attn_verify_mfma_kernel<<<dim3((unsigned)launch_chunks, (unsigned)a.kv_heads, nz), 256, kMfmaLds, s>>>(
             q, k, v, static_cast<uint16_t *>(kpool), static_cast<uint16_t *>(vpool), table, q_norm, k_norm, rope, a,
             part, dyn);
     } else if (a.fmt == 1) {
@@ -734,7 +784,7 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
             attr1 = true;
         }
-        attn_verify_kernel<1><<<dim3((unsigned)launch_chunks, (unsigned)a.kv_heads), 256, lds, s>>>(
+        attn_verify_kernel<1><<<dim3((unsigned)launch_chunks, (unsigned)a.kv_heads, nz), 256, lds, s>>>(
             q, k, v, static_cast<uint8_t *>(kpool), static_cast<uint8_t *>(vpool), table, q_norm, k_norm, rope, a,
             part, dyn);
     } else {
@@ -744,11 +794,11 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
             attr0 = true;
         }
-        attn_verify_kernel<0><<<dim3((unsigned)launch_chunks, (unsigned)a.kv_heads), 256, lds, s>>>(
+        attn_verify_kernel<0><<<dim3((unsigned)launch_chunks, (unsigned)a.kv_heads, nz), 256, lds, s>>>(
             q, k, v, static_cast<uint8_t *>(kpool), static_cast<uint8_t *>(vpool), table, q_norm, k_norm, rope, a,
             part, dyn);
     }
-    attn_merge_v_kernel<<<dim3((unsigned)a.heads, (unsigned)a.rows), 256, (size_t)launch_chunks * 4, s>>>(
+    attn_merge_v_kernel<<<dim3((unsigned)a.heads, (unsigned)a.rows, nz), 256, (size_t)launch_chunks * 4, s>>>(
         q, part, a, ck, launch_chunks, out, dyn);
     return hipGetLastError();
 }

@@ -31,6 +31,10 @@ struct AttnVArgs {
     int gated;     // 1: query rows hold [q | gate] per head (qwen35)
     int rope_dim;  // rotated dimensions per head (pairs i, i + rope_dim/2)
     float scale, eps;
+    // requests of one launch (grid z): request j's rows start rq_rows rows
+    // after request j-1's, its block table ceil(capacity / block_size)
+    // entries after, its {token, position} pair two int32 after
+    int nreq, rq_rows;
 };
 
 struct GdnArgs {
@@ -57,7 +61,7 @@ int attn_verify_chunk(uint32_t fmt);
 uint64_t attn_verify_scratch_bytes(const AttnVArgs &a);
 uint32_t attn_verify_lds_bytes(const AttnVArgs &a);
 hipError_t launch_rope_table(float2 *tab, int rows, int rot_dim, double base, const ModelDyn &dyn, int displacement,
-                             hipStream_t s);
+                             hipStream_t s, int nreq = 1, int rq_rows = 0);
 hipError_t launch_attn_verify(const float *q, const float *k, const float *v, void *kpool, void *vpool,
                               const int32_t *table, const float *q_norm, const float *k_norm, const float2 *rope,
                               float *out, const AttnVArgs &a, void *scratch, const ModelDyn &dyn, int max_pos_hint,

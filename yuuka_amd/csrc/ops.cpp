@@ -64,7 +64,11 @@ static AttnVArgs attnv_args(const yuuka_op &op) {
     bool ok;
     a.fmt = kv_fmt(op.u[2], &ok);
     a.gated = 1;
-    a.rope_dim = (int)op.u[3];
+    a.rope_dim = (int)(op.u[3] & 0xffu);
+    a.nreq = (int)((op.u[3] >> 8) & 0xfffu);
+    if (a.nreq < 1) a.nreq = 1;
+    a.rq_rows = (int)(op.u[3] >> 20);
+    if (a.rq_rows < a.rows) a.rq_rows = a.rows;
     a.scale = op.f[0];
     a.eps = op.f[1];
     return a;
@@ -274,16 +278,22 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
     case YUUKA_EXT_OP_ROPE_TABLE: {
         if ((op.flags & YUUKA_EXT_FLAG_OWN_POS) && (!buf_ok(op.buf[15], op.off[15], 8) || op.off[15] % 4))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "ROPE_TABLE: own position buffer");
-        const uint64_t rows = op.n[0], rot = op.n[1];
-        if (!rows || rows > 4096 || !rot || rot % 2 || rot > 128 || op.off[0] % 8 ||
-            !buf_ok(op.buf[0], op.off[0], rows * (rot / 2) * 8))
+        const uint64_t rows = op.n[0], rot = op.n[1], nq = op.n[3] ? op.n[3] : 1;
+        const uint64_t rqr = op.n[4] > rows ? op.n[4] : rows;
+        if (!rows || rows > 4096 || !rot || rot % 2 || rot > 128 || op.off[0] % 8 || nq > 4096 ||
+            !buf_ok(op.buf[0], op.off[0], ((nq - 1) * rqr + rows) * (rot / 2) * 8))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid ROPE_TABLE shape or buffer");
+        if (nq > 1 && (!(op.flags & YUUKA_EXT_FLAG_OWN_POS) || !buf_ok(op.buf[15], op.off[15], 8 * nq)))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "ROPE_TABLE: several requests need their own positions");
         return YUUKA_OK;
     }
     case YUUKA_EXT_OP_ATTN_VERIFY: {
-        if ((op.flags & YUUKA_EXT_FLAG_OWN_POS) && (!buf_ok(op.buf[15], op.off[15], 8) || op.off[15] % 4))
-            return fail(YUUKA_ERR_INVALID_ARGUMENT, "ATTN_VERIFY: own position buffer");
         const AttnVArgs a = attnv_args(op);
+        if ((op.flags & YUUKA_EXT_FLAG_OWN_POS) &&
+            (!buf_ok(op.buf[15], op.off[15], 8ull * a.nreq) || op.off[15] % 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "ATTN_VERIFY: own position buffer");
+        if (a.nreq > 1 && !(op.flags & YUUKA_EXT_FLAG_OWN_POS))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "ATTN_VERIFY: several requests need their own positions");
         bool ok;
         kv_fmt(op.u[2], &ok);
         if (!ok) return fail(YUUKA_ERR_UNSUPPORTED, "KV pool dtype %u (F32 and F16 are served)", op.u[2]);
@@ -297,11 +307,13 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
             return fail(YUUKA_ERR_UNSUPPORTED, "verify attention: %d query rows per kv head do not fit LDS",
                         a.rows * a.heads / a.kv_heads);
         const uint64_t blocks = ((uint64_t)a.capacity + a.block_size - 1) / a.block_size;
-        const uint64_t R = (uint64_t)a.rows;
+        // rows spanned by the requests, and block table entries
+        const uint64_t R = (uint64_t)(a.nreq - 1) * a.rq_rows + a.rows;
+        const uint64_t tbl = (uint64_t)a.nreq * blocks;
         if (!buf_ok(op.buf[0], op.off[0], R * a.heads * 2 * a.head_dim * 4) ||
             !buf_ok(op.buf[1], op.off[1], R * a.kv_dim * 4) || !buf_ok(op.buf[2], op.off[2], R * a.kv_dim * 4) ||
             !op.buf[3] || !op.buf[4] || !buf_ok(op.buf[5], op.off[5], R * a.heads * a.head_dim * 4) ||
-            !buf_ok(op.buf[6], op.off[6], blocks * 4) || !buf_ok(op.buf[7], op.off[7], (uint64_t)a.head_dim * 4) ||
+            !buf_ok(op.buf[6], op.off[6], tbl * 4) || !buf_ok(op.buf[7], op.off[7], (uint64_t)a.head_dim * 4) ||
             !buf_ok(op.buf[8], op.off[8], (uint64_t)a.head_dim * 4) ||
             !buf_ok(op.buf[9], op.off[9], R * (a.rope_dim / 2) * 8))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify attention buffers too small");
@@ -309,7 +321,7 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         const uint64_t pool = (uint64_t)blocks * a.block_size * a.kv_dim * esz;
         if (op.buf[3]->bytes < pool || op.buf[4]->bytes < pool)
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify attention: KV pool smaller than capacity");
-        *ws = attn_verify_scratch_bytes(a);
+        *ws = attn_verify_scratch_bytes(a) * (uint64_t)a.nreq;
         return YUUKA_OK;
     }
     case YUUKA_OP_RECURRENT_CHUNK: {  // hip.go:1874-1934
@@ -596,7 +608,8 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
     }
     case YUUKA_EXT_OP_ROPE_TABLE:
         err = launch_rope_table(at<float2>(op, 0), (int)op.n[0], (int)op.n[1], (double)op.f[0], dyn_of(ctx, op),
-                                (int)op.n[2], s);
+                                (int)op.n[2], s, op.n[3] ? (int)op.n[3] : 1,
+                                (int)(op.n[4] > op.n[0] ? op.n[4] : op.n[0]));
         break;
     case YUUKA_EXT_OP_ATTN_VERIFY: {
         const AttnVArgs a = attnv_args(op);
