@@ -47,10 +47,12 @@ constexpr int kQMax = 32639;
 constexpr int kBgWaves = 8;
 constexpr int kBgThreads = 64 * kBgWaves;
 constexpr int kBgRows = 64;  // rows per workgroup: 8 A tiles of 8 rows
-// LDS of the GEMM: A planes [8 t][8 j][4 g][16 r][8 B] + sums [8 t][8 j][8]
-// int32 + scales [8 t][8] float; the SwiGLU epilogue reuses the A region.
+// LDS of the GEMM, per stage: A planes [8 t][8 j][4 g][16 r][8 B] + sums
+// [8 t][8 j][8] int32 + scales [8 t][8] float; two stages. The SwiGLU
+// epilogue reuses the first.
 constexpr uint32_t kBgLdsA = 8 * 8 * 4 * 16 * 8;
-constexpr uint32_t kBgLds = kBgLdsA + 8 * 8 * 8 * 4 + 8 * 8 * 4;
+constexpr uint32_t kBgStage = kBgLdsA + 8 * 8 * 8 * 4 + 8 * 8 * 4;  // one stage (double-buffered)
+constexpr uint32_t kBgLds = 2 * kBgStage;
 
 struct BgQuant {
     int8_t *planes;  // [rows][K/32][2: high, low][32 B]
@@ -237,36 +239,53 @@ __device__ __forceinline__ float out_map(const FusedSeg &S, int n, float v) {
     }
 }
 
-// Stages super-block sb of the workgroup's rows (planes, sums, scales) in LDS.
-__device__ __forceinline__ void stage_rows(const BgArgs &A, uint8_t *la, int32_t *lsum, float *lxs, int m0, int mrows,
-                                           int sb) {
+// Super-block sb of the workgroup's rows (planes, sums, scales): loaded by
+// every thread into registers, then written to one of two LDS buffers.
+struct Staged {
+    uint4 v[4];
+    int32_t sum;
+    float xs;
+};
+
+__device__ __forceinline__ void stage_load(const BgArgs &A, Staged &st, int m0, int mrows, int sb) {
     const int K = A.f.K, nsb = K / 256, nsub = K / 32;
-    // thread piece = (row, sub-block, plane, 16-byte half)
-    for (int idx = threadIdx.x; idx < kBgRows * 8 * 4; idx += kBgThreads) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {  // piece = (row, sub-block, plane, 16-byte half)
+        const int idx = threadIdx.x + u * kBgThreads;
         const int r = idx >> 5, j = (idx >> 2) & 7, p = (idx >> 1) & 1, half = idx & 1;
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (r < mrows)
-            v = *reinterpret_cast<const uint4 *>(A.q.planes + (uint64_t)(m0 + r) * K * 2 + (uint64_t)(sb * 8 + j) * 64 +
-                                                 32 * p + 16 * half);
+        st.v[u] = r < mrows ? *reinterpret_cast<const uint4 *>(A.q.planes + (uint64_t)(m0 + r) * K * 2 +
+                                                               (uint64_t)(sb * 8 + j) * 64 + 32 * p + 16 * half)
+                            : make_uint4(0u, 0u, 0u, 0u);
+    }
+    {
+        const int r = threadIdx.x >> 3, j = threadIdx.x & 7;
+        st.sum = r < mrows ? A.q.sums[(uint64_t)(m0 + r) * nsub + sb * 8 + j] : 0;
+    }
+    st.xs = threadIdx.x < mrows ? A.q.scales[(uint64_t)(m0 + threadIdx.x) * nsb + sb] : 0.f;
+}
+
+__device__ __forceinline__ void stage_store(const Staged &st, uint8_t *la, int32_t *lsum, float *lxs) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int idx = threadIdx.x + u * kBgThreads;
+        const int r = idx >> 5, j = (idx >> 2) & 7, p = (idx >> 1) & 1, half = idx & 1;
         const int t = r >> 3, rr = (r & 7) + 8 * p;
         uint8_t *d0 = la + ((uint32_t)((t * 8 + j) * 4 + 2 * half) * 16 + rr) * 8;
-        *reinterpret_cast<uint2 *>(d0) = make_uint2(v.x, v.y);
-        *reinterpret_cast<uint2 *>(d0 + 16 * 8) = make_uint2(v.z, v.w);
+        *reinterpret_cast<uint2 *>(d0) = make_uint2(st.v[u].x, st.v[u].y);
+        *reinterpret_cast<uint2 *>(d0 + 16 * 8) = make_uint2(st.v[u].z, st.v[u].w);
     }
-    for (int idx = threadIdx.x; idx < kBgRows * 8; idx += kBgThreads) {
-        const int r = idx >> 3, j = idx & 7;
-        lsum[((r >> 3) * 8 + j) * 8 + (r & 7)] = r < mrows ? A.q.sums[(uint64_t)(m0 + r) * nsub + sb * 8 + j] : 0;
+    {
+        const int r = threadIdx.x >> 3, j = threadIdx.x & 7;
+        lsum[((r >> 3) * 8 + j) * 8 + (r & 7)] = st.sum;
     }
-    if (threadIdx.x < kBgRows) {
-        const int r = threadIdx.x;
-        lxs[r] = r < mrows ? A.q.scales[(uint64_t)(m0 + r) * nsb + sb] : 0.f;
-    }
+    if (threadIdx.x < kBgRows) lxs[threadIdx.x] = st.xs;
 }
 
 // The main loop of one wave over the super-blocks (weights of dtype DT).
+// LDS holds two stages; stage sb + 1 is loaded while sb is multiplied.
 template <int DT>
-__device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *la, int32_t *lsum, float *lxs, int m0, int mrows,
-                                        bool live, const uint8_t *wrow, float (&y)[8][4]) {
+__device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, int mrows, bool live,
+                                        const uint8_t *wrow, float (&y)[8][4]) {
     const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
     const int nsb = A.f.K / 256;
     const int rb = 4 * (g & 1);
@@ -277,89 +296,102 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *la, int32_t *l
         if constexpr (DT == kQ4K) load_q4(w, wrow, g);
         else load_q6(w, wrow, g);
     }
+    Staged st;
+    stage_load(A, st, m0, mrows, 0);
+    stage_store(st, lds, reinterpret_cast<int32_t *>(lds + kBgLdsA), reinterpret_cast<float *>(lds + kBgLdsA + 2048));
+    __syncthreads();
     for (int sb = 0; sb < nsb; sb++) {
-        __syncthreads();  // the previous super-block's readers are done with LDS
-        stage_rows(A, la, lsum, lxs, m0, mrows, sb);
+        uint8_t *cur_l = lds + (uint32_t)(sb & 1) * kBgStage;
+        uint8_t *nxt_l = lds + (uint32_t)((sb + 1) & 1) * kBgStage;
+        const uint8_t *la = cur_l;
+        const int32_t *lsum = reinterpret_cast<const int32_t *>(cur_l + kBgLdsA);
+        const float *lxs = reinterpret_cast<const float *>(cur_l + kBgLdsA + 2048);
+        const bool more = sb + 1 < nsb;
+        if (more) stage_load(A, st, m0, mrows, sb + 1);
         const W cur = w;  // this super-block; the next one's loads go out now
-        if (live && sb + 1 < nsb) {
+        if (live && more) {
             if constexpr (DT == kQ4K) load_q4(w, wrow + (uint64_t)(sb + 1) * blk, g);
             else load_q6(w, wrow + (uint64_t)(sb + 1) * blk, g);
         }
-        __syncthreads();
-        if (!live) continue;
-        if constexpr (DT == kQ4K) {
-            const float d = h2f((uint16_t)(cur.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(cur.hdr.x >> 16));
+        if (live) {
+            if constexpr (DT == kQ4K) {
+                const float d = h2f((uint16_t)(cur.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(cur.hdr.x >> 16));
 #pragma unroll
-            for (int t = 0; t < 8; t++) {  // all 8 tiles: rows past the end are zero in LDS
-                int acc[4] = {0, 0, 0, 0}, ms[4] = {0, 0, 0, 0};
+                for (int t = 0; t < 8; t++) {  // all 8 tiles: rows past the end are zero in LDS
+                    int acc[4] = {0, 0, 0, 0}, ms[4] = {0, 0, 0, 0};
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const uint64_t raw = cur.q[j >> 1];
+                        const int64_t bq = (int64_t)((j & 1) ? (raw >> 4) & 0x0F0F0F0F0F0F0F0Full
+                                                             : raw & 0x0F0F0F0F0F0F0F0Full);
+                        int sc, mn;
+                        scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sc, &mn);
+                        const int64_t a =
+                            *reinterpret_cast<const int64_t *>(la + ((uint32_t)((t * 8 + j) * 4 + g) * 16 + c) * 8);
+                        const i32x4 r = mfma_i8(a, bq);
+                        const int4 sm = *reinterpret_cast<const int4 *>(lsum + (t * 8 + j) * 8 + rb);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[i] += r[i] * sc;
+                        ms[0] += mn * sm.x;
+                        ms[1] += mn * sm.y;
+                        ms[2] += mn * sm.z;
+                        ms[3] += mn * sm.w;
+                    }
+                    const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
+                    const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int lo = __shfl_xor(acc[i], 32);
+                        y[t][i] += xsv[i] * (d * (256.f * (float)acc[i] + (float)lo) - dmin * (float)ms[i]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);  // one A tile at a time (register pressure)
+                }
+            } else {
+                const float d = h2f((uint16_t)cur.d);
+                int64_t bq[8];
+                int sc2[8];  // scales of elements 0..15 (low half) and 16..31 (high half) of sub-block j
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const uint64_t raw = cur.q[j >> 1];
-                    const int64_t bq = (int64_t)((j & 1) ? (raw >> 4) & 0x0F0F0F0F0F0F0F0Full : raw & 0x0F0F0F0F0F0F0F0Full);
-                    int sc, mn;
-                    scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sc, &mn);
-                    const int64_t a = *reinterpret_cast<const int64_t *>(la + ((uint32_t)((t * 8 + j) * 4 + g) * 16 + c) * 8);
-                    const i32x4 r = mfma_i8(a, bq);
-                    const int4 sm = *reinterpret_cast<const int4 *>(lsum + (t * 8 + j) * 8 + rb);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) acc[i] += r[i] * sc;
-                    ms[0] += mn * sm.x;
-                    ms[1] += mn * sm.y;
-                    ms[2] += mn * sm.z;
-                    ms[3] += mn * sm.w;
+                    const int half = j >> 2, qd = j & 3;
+                    const uint64_t lo4 = (cur.ql[2 * half + (qd & 1)] >> (4 * (qd >> 1))) & 0x0F0F0F0F0F0F0F0Full;
+                    const uint64_t hi2 = ((cur.qh[half] >> (2 * qd)) & 0x0303030303030303ull) << 4;
+                    bq[j] = (int64_t)q6_to_i8(lo4 | hi2);
+                    sc2[j] = (sbyte(cur.sc, 8 * half + 2 * qd) & 0xffff) | (sbyte(cur.sc, 8 * half + 2 * qd + 1) << 16);
                 }
-                const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
-                const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int lo = __shfl_xor(acc[i], 32);
-                    y[t][i] += xsv[i] * (d * (256.f * (float)acc[i] + (float)lo) - dmin * (float)ms[i]);
+                for (int t = 0; t < 8; t++) {  // all 8 tiles: rows past the end are zero in LDS
+                    int acc[4] = {0, 0, 0, 0};
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const int64_t a =
+                            *reinterpret_cast<const int64_t *>(la + ((uint32_t)((t * 8 + j) * 4 + g) * 16 + c) * 8);
+                        // lanes g < 2 hold elements 0..15 (first scale group)
+                        const i32x4 r0 = mfma_i8(a, g < 2 ? bq[j] : 0);
+                        const i32x4 r1 = mfma_i8(a, g < 2 ? 0 : bq[j]);
+                        const int s0 = (int)(int16_t)(sc2[j] & 0xffff), s1 = sc2[j] >> 16;
+#pragma unroll
+                        for (int i = 0; i < 4; i++) acc[i] += r0[i] * s0 + r1[i] * s1;
+                    }
+                    const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
+                    const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int lo = __shfl_xor(acc[i], 32);
+                        y[t][i] += xsv[i] * (d * (256.f * (float)acc[i] + (float)lo));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);  // one A tile at a time (register pressure)
                 }
-                __builtin_amdgcn_sched_barrier(0);  // one A tile at a time (register pressure)
-            }
-        } else {
-            const float d = h2f((uint16_t)cur.d);
-            int64_t bq[8];
-            int sc2[8];  // scale of elements 0..15 (low half) and 16..31 (high half) of sub-block j
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int half = j >> 2, qd = j & 3;
-                const uint64_t lo4 = (cur.ql[2 * half + (qd & 1)] >> (4 * (qd >> 1))) & 0x0F0F0F0F0F0F0F0Full;
-                const uint64_t hi2 = ((cur.qh[half] >> (2 * qd)) & 0x0303030303030303ull) << 4;
-                bq[j] = (int64_t)q6_to_i8(lo4 | hi2);
-                sc2[j] = (sbyte(cur.sc, 8 * half + 2 * qd) & 0xffff) | (sbyte(cur.sc, 8 * half + 2 * qd + 1) << 16);
-            }
-#pragma unroll
-            for (int t = 0; t < 8; t++) {  // all 8 tiles: rows past the end are zero in LDS
-                int acc[4] = {0, 0, 0, 0};
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const int64_t a = *reinterpret_cast<const int64_t *>(la + ((uint32_t)((t * 8 + j) * 4 + g) * 16 + c) * 8);
-                    // lanes g < 2 hold elements 0..15 (first scale group)
-                    const i32x4 r0 = mfma_i8(a, g < 2 ? bq[j] : 0);
-                    const i32x4 r1 = mfma_i8(a, g < 2 ? 0 : bq[j]);
-                    const int s0 = (int)(int16_t)(sc2[j] & 0xffff), s1 = sc2[j] >> 16;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) acc[i] += r0[i] * s0 + r1[i] * s1;
-                }
-                const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
-                const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int lo = __shfl_xor(acc[i], 32);
-                    y[t][i] += xsv[i] * (d * (256.f * (float)acc[i] + (float)lo));
-                }
-                __builtin_amdgcn_sched_barrier(0);  // one A tile at a time (register pressure)
             }
         }
+        if (more)
+            stage_store(st, nxt_l, reinterpret_cast<int32_t *>(nxt_l + kBgLdsA),
+                        reinterpret_cast<float *>(nxt_l + kBgLdsA + 2048));
+        __syncthreads();  // stage sb + 1 written; stage sb read by every wave
     }
 }
 
 __global__ __launch_bounds__(kBgThreads) void bg_gemm_kernel(const BgArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    uint8_t *la = lds;
-    int32_t *lsum = reinterpret_cast<int32_t *>(lds + kBgLdsA);
-    float *lxs = reinterpret_cast<float *>(lds + kBgLdsA + 8 * 8 * 8 * 4);
     const FusedGemmArgs &F = A.f;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = lane & 15, g = lane >> 4;
@@ -389,9 +421,9 @@ __global__ __launch_bounds__(kBgThreads) void bg_gemm_kernel(const BgArgs A) {
 #pragma unroll
         for (int i = 0; i < 4; i++) y[t][i] = 0.f;
     if (S.dtype == kQ6K)
-        bg_main<kQ6K>(A, la, lsum, lxs, m0, mrows, live, wrow, y);
+        bg_main<kQ6K>(A, lds, m0, mrows, live, wrow, y);
     else
-        bg_main<kQ4K>(A, la, lsum, lxs, m0, mrows, live, wrow, y);
+        bg_main<kQ4K>(A, lds, m0, mrows, live, wrow, y);
 
     // epilogue: lanes g < 2 hold rows 8 t + 4 g + i of channel n0 + c
     if (A.swiglu) {
@@ -452,6 +484,8 @@ hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t 
     if (!attr) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(bg_prologue_kernel),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(bg_gemm_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kBgLds);
         attr = true;
     }
     bg_prologue_kernel<<<(unsigned)a.rows, 256, plds, s>>>(a, A.q);
