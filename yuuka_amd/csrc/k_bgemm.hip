@@ -31,6 +31,7 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "fgemm.h"
@@ -143,7 +144,10 @@ struct BgArgs {
     FusedGemmArgs f;
     BgQuant q;
     int tiles[kFusedMaxSeg + 1];  // prefix counts of workgroups (8 tiles of 16 channels) per segment
+    int cols[kFusedMaxSeg + 1];   // prefix counts of output channels per segment
     int swiglu;
+    int splits;                   // K split over grid z; > 1: partial sums to `part`, then bg_reduce_kernel
+    float *part;                  // [splits][rows][cols[nseg]]
 };
 
 __device__ __forceinline__ i32x4 mfma_i8(int64_t a, int64_t b) {
@@ -287,7 +291,11 @@ template <int DT>
 __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, int mrows, bool live,
                                         const uint8_t *wrow, float (&y)[8][4]) {
     const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
-    const int nsb = A.f.K / 256;
+    // this split's super-blocks [sb_lo, nsb)
+    const int nsb_all = A.f.K / 256;
+    const int sb_lo = (int)((int64_t)nsb_all * blockIdx.z / A.splits);
+    const int nsb = (int)((int64_t)nsb_all * (blockIdx.z + 1) / A.splits);
+    wrow += (uint64_t)sb_lo * (DT == kQ4K ? 144 : 210);
     const int rb = 4 * (g & 1);
     typedef typename std::conditional<DT == kQ4K, WQ4, WQ6>::type W;
     constexpr int blk = DT == kQ4K ? 144 : 210;
@@ -297,12 +305,12 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
         else load_q6(w, wrow, g);
     }
     Staged st;
-    stage_load(A, st, m0, mrows, 0);
+    stage_load(A, st, m0, mrows, sb_lo);
     stage_store(st, lds, reinterpret_cast<int32_t *>(lds + kBgLdsA), reinterpret_cast<float *>(lds + kBgLdsA + 2048));
     __syncthreads();
-    for (int sb = 0; sb < nsb; sb++) {
-        uint8_t *cur_l = lds + (uint32_t)(sb & 1) * kBgStage;
-        uint8_t *nxt_l = lds + (uint32_t)((sb + 1) & 1) * kBgStage;
+    for (int sb = sb_lo; sb < nsb; sb++) {
+        uint8_t *cur_l = lds + (uint32_t)((sb - sb_lo) & 1) * kBgStage;
+        uint8_t *nxt_l = lds + (uint32_t)((sb - sb_lo + 1) & 1) * kBgStage;
         const uint8_t *la = cur_l;
         const int32_t *lsum = reinterpret_cast<const int32_t *>(cur_l + kBgLdsA);
         const float *lxs = reinterpret_cast<const float *>(cur_l + kBgLdsA + 2048);
@@ -310,8 +318,8 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
         if (more) stage_load(A, st, m0, mrows, sb + 1);
         const W cur = w;  // this super-block; the next one's loads go out now
         if (live && more) {
-            if constexpr (DT == kQ4K) load_q4(w, wrow + (uint64_t)(sb + 1) * blk, g);
-            else load_q6(w, wrow + (uint64_t)(sb + 1) * blk, g);
+            if constexpr (DT == kQ4K) load_q4(w, wrow + (uint64_t)(sb + 1 - sb_lo) * blk, g);
+            else load_q6(w, wrow + (uint64_t)(sb + 1 - sb_lo) * blk, g);
         }
         if (live) {
             if constexpr (DT == kQ4K) {
@@ -426,6 +434,19 @@ __global__ __launch_bounds__(kBgThreads) void bg_gemm_kernel(const BgArgs A) {
         bg_main<kQ4K>(A, lds, m0, mrows, live, wrow, y);
 
     // epilogue: lanes g < 2 hold rows 8 t + 4 g + i of channel n0 + c
+    if (A.splits > 1) {  // partial sums of this split; bg_reduce_kernel finishes
+        if (!live || g >= 2 || n0 + c >= S.n) return;
+        const int ncol = A.cols[F.nseg];
+        float *pp = A.part + (uint64_t)blockIdx.z * F.rows * ncol + A.cols[seg] + n0 + c;
+#pragma unroll
+        for (int t = 0; t < 8; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int r = 8 * t + 4 * g + i;
+                if (r < mrows) pp[(uint64_t)(m0 + r) * ncol] = y[t][i];
+            }
+        return;
+    }
     if (A.swiglu) {
         __syncthreads();
         float *up = reinterpret_cast<float *>(lds);  // [4 tiles][64 rows][16]
@@ -464,10 +485,70 @@ __global__ __launch_bounds__(kBgThreads) void bg_gemm_kernel(const BgArgs A) {
         }
 }
 
+// Sum of the splits in split order, then the epilogue (one thread per output).
+__global__ __launch_bounds__(256) void bg_reduce_kernel(const BgArgs A) {
+    const FusedGemmArgs &F = A.f;
+    const int ncol = A.cols[F.nseg];
+    const int nout = A.swiglu ? F.seg[0].n : ncol;
+    const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (uint64_t)F.rows * nout) return;
+    const int m = (int)(idx / nout), col = (int)(idx % nout);
+    auto sum = [&](int cc) {
+        float v = 0.f;
+        for (int sp = 0; sp < A.splits; sp++) v += A.part[((uint64_t)sp * F.rows + m) * ncol + cc];
+        return v;
+    };
+    if (A.swiglu) {
+        const float gsum = sum(col), usum = sum(A.cols[1] + col);
+        F.seg[0].out[(uint64_t)m * F.seg[0].n + col] = __fmul_rn(silu_ref(gsum), usum);
+        return;
+    }
+    int seg = 0;
+    for (int i = 1; i < F.nseg; i++)
+        if (col >= A.cols[i]) seg = i;
+    const FusedSeg &S = F.seg[seg];
+    const int n = col - A.cols[seg];
+    const uint64_t o = (uint64_t)m * S.n + n;
+    float v = sum(col);
+    if (F.epilogue == kEpiResidual) v = __fadd_rn(v, S.res[o]);
+    else v = out_map(S, n, v);
+    S.out[o] = v;
+}
+
+// K splits that bring a small launch near two workgroups per CU.
+int bg_splits(int wgs, int nsb) {
+    int sp = (512 + wgs - 1) / wgs;
+    sp = std::min(sp, std::max(1, nsb / 2));
+    return std::max(1, std::min(sp, 16));
+}
+
+uint64_t bg_quant_bytes(int rows, int K) {
+    return (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 32) * 4 + (uint64_t)rows * (K / 256) * 4;
+}
+
 }  // namespace
 
-uint64_t fused_gemm_rows_ws(int rows, int K) {
-    return (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 32) * 4 + (uint64_t)rows * (K / 256) * 4 + 256;
+// Grid of one launch: x workgroups of 8 tiles (SwiGLU: 4 channel tiles of
+// both matrices), y row blocks, z K splits.
+static void bg_grid(const int *n, int nseg, bool swiglu, int rows, int K, unsigned *gx, unsigned *gy, int *splits) {
+    unsigned x = 0;
+    if (swiglu)
+        x = (unsigned)((n[0] + 63) / 64);
+    else
+        for (int i = 0; i < nseg; i++) x += (unsigned)((n[i] + 16 * kBgWaves - 1) / (16 * kBgWaves));
+    *gx = x;
+    *gy = (unsigned)((rows + kBgRows - 1) / kBgRows);
+    *splits = getenv("YUUKA_BG_NOSPLIT") ? 1 : bg_splits((int)(x * *gy), K / 256);
+}
+
+uint64_t fused_gemm_rows_ws(int rows, int K, const int *n, int nseg, bool swiglu) {
+    unsigned gx, gy;
+    int splits;
+    bg_grid(n, nseg, swiglu, rows, K, &gx, &gy, &splits);
+    int ncol = 0;
+    for (int i = 0; i < nseg; i++) ncol += n[i];
+    const uint64_t part = splits > 1 ? (uint64_t)splits * rows * ncol * 4 : 0;
+    return ((bg_quant_bytes(rows, K) + 255) & ~255ull) + part + 256;
 }
 
 hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t s) {
@@ -489,9 +570,19 @@ hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t 
         attr = true;
     }
     bg_prologue_kernel<<<(unsigned)a.rows, 256, plds, s>>>(a, A.q);
-    const unsigned gx = A.swiglu ? (unsigned)((a.seg[0].n + 63) / 64) : (unsigned)A.tiles[a.nseg];
-    const unsigned gy = (unsigned)((a.rows + kBgRows - 1) / kBgRows);
-    bg_gemm_kernel<<<dim3(gx, gy), kBgThreads, kBgLds, s>>>(A);
+    int nn[kFusedMaxSeg];
+    for (int i = 0; i < a.nseg; i++) nn[i] = a.seg[i].n;
+    unsigned gx, gy;
+    bg_grid(nn, a.nseg, A.swiglu != 0, a.rows, a.K, &gx, &gy, &A.splits);
+    A.cols[0] = 0;
+    for (int i = 0; i < a.nseg; i++) A.cols[i + 1] = A.cols[i] + a.seg[i].n;
+    for (int i = a.nseg + 1; i <= kFusedMaxSeg; i++) A.cols[i] = A.cols[a.nseg];
+    A.part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + ((bg_quant_bytes(a.rows, a.K) + 255) & ~255ull));
+    bg_gemm_kernel<<<dim3(gx, gy, (unsigned)A.splits), kBgThreads, kBgLds, s>>>(A);
+    if (A.splits > 1) {
+        const uint64_t nout = (uint64_t)a.rows * (A.swiglu ? a.seg[0].n : A.cols[a.nseg]);
+        bg_reduce_kernel<<<(unsigned)((nout + 255) / 256), 256, 0, s>>>(A);
+    }
     return hipGetLastError();
 }
 

@@ -403,7 +403,9 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         if (fused_many_rows(op)) {  // k_bgemm.hip: quantized rows in the workspace
             if (K > 16384) return fail(YUUKA_ERR_UNSUPPORTED, "GEMM_FUSED: K %llu over 16384 rows > 8",
                                        (unsigned long long)K);
-            *ws = fused_gemm_rows_ws((int)rows, (int)K);
+            int nn[kFusedMaxSeg] = {0, 0, 0, 0};
+            for (int i = 0; i < nseg; i++) nn[i] = (int)op.n[2 + i];
+            *ws = fused_gemm_rows_ws((int)rows, (int)K, nn, nseg, epi == kEpiSwiglu);
             return YUUKA_OK;
         }
         if (fused_gemm_chunk_sb((int)rows, (int)K, fused_tiles(op, nseg), op.buf[1] != nullptr, op.buf[14] != nullptr) < 1)
