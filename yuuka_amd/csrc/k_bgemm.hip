@@ -150,6 +150,11 @@ struct BgArgs {
     float *part;                  // [splits][rows][cols[nseg]]
 };
 
+// 24-bit multiply-add (full rate; a 32-bit multiply is quarter rate). Every
+// product here fits: MFMA sub-block results |r| < 2^17, scales <= 63,
+// sub-block sums |S| < 2^21.
+__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+
 __device__ __forceinline__ i32x4 mfma_i8(int64_t a, int64_t b) {
     const i32x4 zero = {0, 0, 0, 0};
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero, 0, 0, 0);
@@ -323,36 +328,57 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
         }
         if (live) {
             if constexpr (DT == kQ4K) {
+                // Scale and min term on the MFMA accumulators: with sc = 8 sc_hi
+                // + sc_lo (3-bit digits), q * sc_lo and q * sc_hi (<= 105) are
+                // exact int8 B operands, and the sub-block min m (<= 63)
+                // broadcast over the sub-block gives the min term directly.
+                // Three chained MFMAs per sub-block and 8-row tile, no VALU
+                // multiply-adds. Two passes of four A tiles bound the registers.
                 const float d = h2f((uint16_t)(cur.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(cur.hdr.x >> 16));
 #pragma unroll
-                for (int t = 0; t < 8; t++) {  // all 8 tiles: rows past the end are zero in LDS
-                    int acc[4] = {0, 0, 0, 0}, ms[4] = {0, 0, 0, 0};
+                for (int th = 0; th < 2; th++) {
+                    i32x4 alo[4], ahi[4], amn[4];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        alo[u] = i32x4{0, 0, 0, 0};
+                        ahi[u] = i32x4{0, 0, 0, 0};
+                        amn[u] = i32x4{0, 0, 0, 0};
+                    }
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
                         const uint64_t raw = cur.q[j >> 1];
-                        const int64_t bq = (int64_t)((j & 1) ? (raw >> 4) & 0x0F0F0F0F0F0F0F0Full
-                                                             : raw & 0x0F0F0F0F0F0F0F0Full);
+                        const uint64_t qb = (j & 1) ? (raw >> 4) & 0x0F0F0F0F0F0F0F0Full : raw & 0x0F0F0F0F0F0F0F0Full;
                         int sc, mn;
                         scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sc, &mn);
-                        const int64_t a =
-                            *reinterpret_cast<const int64_t *>(la + ((uint32_t)((t * 8 + j) * 4 + g) * 16 + c) * 8);
-                        const i32x4 r = mfma_i8(a, bq);
-                        const int4 sm = *reinterpret_cast<const int4 *>(lsum + (t * 8 + j) * 8 + rb);
+                        // per-byte products stay below 256: no carries between bytes
+                        const uint32_t q0 = (uint32_t)qb, q1 = (uint32_t)(qb >> 32);
+                        const uint32_t lo = (uint32_t)(sc & 7), hi = (uint32_t)(sc >> 3);
+                        const int64_t b_lo = (int64_t)((uint64_t)(q0 * lo) | ((uint64_t)(q1 * lo) << 32));
+                        const int64_t b_hi = (int64_t)((uint64_t)(q0 * hi) | ((uint64_t)(q1 * hi) << 32));
+                        const int64_t b_mn = (int64_t)((uint64_t)(uint32_t)mn * 0x0101010101010101ull);
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[i] += r[i] * sc;
-                        ms[0] += mn * sm.x;
-                        ms[1] += mn * sm.y;
-                        ms[2] += mn * sm.z;
-                        ms[3] += mn * sm.w;
+                        for (int u = 0; u < 4; u++) {
+                            const int t = 4 * th + u;
+                            const int64_t av =
+                                *reinterpret_cast<const int64_t *>(la + ((uint32_t)((t * 8 + j) * 4 + g) * 16 + c) * 8);
+                            alo[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_lo, alo[u], 0, 0, 0);
+                            ahi[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_hi, ahi[u], 0, 0, 0);
+                            amn[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_mn, amn[u], 0, 0, 0);
+                        }
                     }
-                    const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
-                    const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int lo = __shfl_xor(acc[i], 32);
-                        y[t][i] += xsv[i] * (d * (256.f * (float)acc[i] + (float)lo) - dmin * (float)ms[i]);
+                    for (int u = 0; u < 4; u++) {
+                        const int t = 4 * th + u;
+                        const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
+                        const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            // this lane's plane (rows 0..7 high, 8..15 low), then both
+                            const float v = d * (float)(alo[u][i] + 8 * ahi[u][i]) - dmin * (float)amn[u][i];
+                            const float other = __shfl_xor(v, 32);
+                            y[t][i] += xsv[i] * (256.f * v + other);
+                        }
                     }
-                    __builtin_amdgcn_sched_barrier(0);  // one A tile at a time (register pressure)
                 }
             } else {
                 const float d = h2f((uint16_t)cur.d);
@@ -378,7 +404,7 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                         const i32x4 r1 = mfma_i8(a, g < 2 ? 0 : bq[j]);
                         const int s0 = (int)(int16_t)(sc2[j] & 0xffff), s1 = sc2[j] >> 16;
 #pragma unroll
-                        for (int i = 0; i < 4; i++) acc[i] += r0[i] * s0 + r1[i] * s1;
+                        for (int i = 0; i < 4; i++) acc[i] = mad24(r1[i], s1, mad24(r0[i], s0, acc[i]));
                     }
                     const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
                     const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};

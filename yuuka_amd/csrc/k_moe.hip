@@ -311,6 +311,11 @@ struct MoeGemmArgs {
     float *out0, *out1;   // [rows*used][N]
 };
 
+// 24-bit multiply-add (full rate; a 32-bit multiply is quarter rate). Every
+// product here fits: MFMA sub-block results |r| < 2^17, scales <= 63,
+// sub-block sums |S| < 2^21.
+__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+
 __device__ __forceinline__ i32x4 mfma_i8(int64_t a, int64_t b) {
     const i32x4 zero = {0, 0, 0, 0};
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero, 0, 0, 0);
@@ -427,11 +432,11 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
                     const i32x4 r = mfma_i8(av, (int64_t)bq);
                     const int4 sm = *reinterpret_cast<const int4 *>(lsum + (sb * 8 + j) * 8 + rbase);
 #pragma unroll
-                    for (int i = 0; i < 4; i++) acc[i] += r[i] * scj;
-                    ms[0] += mnj * sm.x;
-                    ms[1] += mnj * sm.y;
-                    ms[2] += mnj * sm.z;
-                    ms[3] += mnj * sm.w;
+                    for (int i = 0; i < 4; i++) acc[i] = mad24(r[i], scj, acc[i]);
+                    ms[0] = mad24(mnj, sm.x, ms[0]);
+                    ms[1] = mad24(mnj, sm.y, ms[1]);
+                    ms[2] = mad24(mnj, sm.z, ms[2]);
+                    ms[3] = mad24(mnj, sm.w, ms[3]);
                 }
                 const float d = h2f((uint16_t)(hdr[u].x & 0xffffu)), dmin = h2f((uint16_t)(hdr[u].x >> 16));
                 float *dst = part + (uint64_t)slot[u] * 128;
