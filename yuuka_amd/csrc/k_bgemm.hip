@@ -273,15 +273,22 @@ __device__ __forceinline__ void stage_load(const BgArgs &A, Staged &st, int m0, 
     st.xs = threadIdx.x < mrows ? A.q.scales[(uint64_t)(m0 + threadIdx.x) * nsb + sb] : 0.f;
 }
 
+// LDS byte offset of the 8 A bytes of tile t (8 rows, two planes), sub-block
+// j, lane group gg, MFMA row rr: sub-blocks 2 jp and 2 jp + 1 sit side by side,
+// so one 16-byte read gives a lane both halves of a K = 64 operand.
+__device__ __forceinline__ uint32_t la_off(int t, int j, int gg, int rr) {
+    return ((uint32_t)(((t * 4 + (j >> 1)) * 4 + gg) * 16 + rr) * 2 + (j & 1)) * 8;
+}
+
 __device__ __forceinline__ void stage_store(const Staged &st, uint8_t *la, int32_t *lsum, float *lxs) {
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int idx = threadIdx.x + u * kBgThreads;
         const int r = idx >> 5, j = (idx >> 2) & 7, p = (idx >> 1) & 1, half = idx & 1;
         const int t = r >> 3, rr = (r & 7) + 8 * p;
-        uint8_t *d0 = la + ((uint32_t)((t * 8 + j) * 4 + 2 * half) * 16 + rr) * 8;
+        uint8_t *d0 = la + la_off(t, j, 2 * half, rr);
         *reinterpret_cast<uint2 *>(d0) = make_uint2(st.v[u].x, st.v[u].y);
-        *reinterpret_cast<uint2 *>(d0 + 16 * 8) = make_uint2(st.v[u].z, st.v[u].w);
+        *reinterpret_cast<uint2 *>(d0 + 256) = make_uint2(st.v[u].z, st.v[u].w);
     }
     {
         const int r = threadIdx.x >> 3, j = threadIdx.x & 7;
@@ -331,9 +338,11 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                 // Scale and min term on the MFMA accumulators: with sc = 8 sc_hi
                 // + sc_lo (3-bit digits), q * sc_lo and q * sc_hi (<= 105) are
                 // exact int8 B operands, and the sub-block min m (<= 63)
-                // broadcast over the sub-block gives the min term directly.
-                // Three chained MFMAs per sub-block and 8-row tile, no VALU
-                // multiply-adds. Two passes of four A tiles bound the registers.
+                // broadcast over the sub-block gives the min term directly. A
+                // K = 64 MFMA covers sub-blocks 2 jp and 2 jp + 1 (low and high
+                // nibbles of the same quant bytes): three chained MFMAs per
+                // sub-block pair and 8-row tile, no VALU multiply-adds. Two
+                // passes of four A tiles bound the registers.
                 const float d = h2f((uint16_t)(cur.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(cur.hdr.x >> 16));
 #pragma unroll
                 for (int th = 0; th < 2; th++) {
@@ -345,25 +354,27 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                         amn[u] = i32x4{0, 0, 0, 0};
                     }
 #pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const uint64_t raw = cur.q[j >> 1];
-                        const uint64_t qb = (j & 1) ? (raw >> 4) & 0x0F0F0F0F0F0F0F0Full : raw & 0x0F0F0F0F0F0F0F0Full;
-                        int sc, mn;
-                        scale_min_k4(j, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sc, &mn);
+                    for (int jp = 0; jp < 4; jp++) {
+                        const uint64_t raw = cur.q[jp];
+                        const uint64_t qe = raw & 0x0F0F0F0F0F0F0F0Full, qo = (raw >> 4) & 0x0F0F0F0F0F0F0F0Full;
+                        int sce, mne, sco, mno;
+                        scale_min_k4(2 * jp, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sce, &mne);
+                        scale_min_k4(2 * jp + 1, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sco, &mno);
                         // per-byte products stay below 256: no carries between bytes
-                        const uint32_t q0 = (uint32_t)qb, q1 = (uint32_t)(qb >> 32);
-                        const uint32_t lo = (uint32_t)(sc & 7), hi = (uint32_t)(sc >> 3);
-                        const int64_t b_lo = (int64_t)((uint64_t)(q0 * lo) | ((uint64_t)(q1 * lo) << 32));
-                        const int64_t b_hi = (int64_t)((uint64_t)(q0 * hi) | ((uint64_t)(q1 * hi) << 32));
-                        const int64_t b_mn = (int64_t)((uint64_t)(uint32_t)mn * 0x0101010101010101ull);
+                        const uint32_t q[4] = {(uint32_t)qe, (uint32_t)(qe >> 32), (uint32_t)qo, (uint32_t)(qo >> 32)};
+                        const uint32_t lo[2] = {(uint32_t)(sce & 7), (uint32_t)(sco & 7)};
+                        const uint32_t hi[2] = {(uint32_t)(sce >> 3), (uint32_t)(sco >> 3)};
+                        const i32x4 b_lo = {(int)(q[0] * lo[0]), (int)(q[1] * lo[0]), (int)(q[2] * lo[1]), (int)(q[3] * lo[1])};
+                        const i32x4 b_hi = {(int)(q[0] * hi[0]), (int)(q[1] * hi[0]), (int)(q[2] * hi[1]), (int)(q[3] * hi[1])};
+                        const int me = (int)((uint32_t)mne * 0x01010101u), mo = (int)((uint32_t)mno * 0x01010101u);
+                        const i32x4 b_mn = {me, me, mo, mo};
 #pragma unroll
                         for (int u = 0; u < 4; u++) {
                             const int t = 4 * th + u;
-                            const int64_t av =
-                                *reinterpret_cast<const int64_t *>(la + ((uint32_t)((t * 8 + j) * 4 + g) * 16 + c) * 8);
-                            alo[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_lo, alo[u], 0, 0, 0);
-                            ahi[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_hi, ahi[u], 0, 0, 0);
-                            amn[u] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b_mn, amn[u], 0, 0, 0);
+                            const i32x4 av = *reinterpret_cast<const i32x4 *>(la + la_off(t, 2 * jp, g, c));
+                            alo[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_lo, alo[u], 0, 0, 0);
+                            ahi[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_hi, ahi[u], 0, 0, 0);
+                            amn[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_mn, amn[u], 0, 0, 0);
                         }
                     }
 #pragma unroll
@@ -397,8 +408,7 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                     int acc[4] = {0, 0, 0, 0};
 #pragma unroll
                     for (int j = 0; j < 8; j++) {
-                        const int64_t a =
-                            *reinterpret_cast<const int64_t *>(la + ((uint32_t)((t * 8 + j) * 4 + g) * 16 + c) * 8);
+                        const int64_t a = *reinterpret_cast<const int64_t *>(la + la_off(t, j, g, c));
                         // lanes g < 2 hold elements 0..15 (first scale group)
                         const i32x4 r0 = mfma_i8(a, g < 2 ? bq[j] : 0);
                         const i32x4 r1 = mfma_i8(a, g < 2 ? 0 : bq[j]);
