@@ -11,18 +11,19 @@
 //  * prologue (one workgroup per row): y = prologue(x) computed as the
 //    reference computes it (forward.go:460-482 rmsNorm, recurrent.go:39-50
 //    gated norm), then quantized per 256-element super-block into an int16
-//    split into two int8 planes (q = 256 h + l, |q| <= 32639), one scale per
-//    (row, super-block) and the exact int32 sums of every 32-element
-//    sub-block (Q4_K min term) — a workspace of rows * (2K + K/8 + K/64) B.
+//    split into two int8 planes (q = 256 h + l, |q| <= 32639) and one scale
+//    per (row, super-block) — a workspace of rows * (2K + K/64) B.
 //  * GEMM (workgroup = 64 rows x 8 tiles of 16 output channels, one tile per
 //    wave): per super-block the workgroup stages the 64 rows' planes in LDS
 //    in MFMA operand order; each wave decodes its tile's weights straight
-//    from HBM into MFMA B operands (Q4_K: one v_mfma_i32_16x16x32_i8 per
-//    32-element sub-block; Q6_K: two, one per 16-element scale group) while
-//    the next super-block's weights are in flight, and multiplies them with
-//    the eight 8-row A tiles (high planes in MFMA rows 0..7, low planes in
-//    8..15). Sub-block scales are applied in int32 (exact), d / dmin and the
-//    activation scale per super-block in FP32.
+//    from HBM into MFMA B operands while the next super-block's weights are
+//    in flight, and multiplies them with the eight 8-row A tiles (high planes
+//    in MFMA rows 0..7, low planes in 8..15). Q4_K: the 6-bit sub-block scale
+//    and min ride in the B operands (three v_mfma_i32_16x16x64_i8 per pair of
+//    sub-blocks); Q6_K: two v_mfma_i32_16x16x32_i8 per sub-block (one per
+//    16-element scale group), scales applied in int32. Everything up to the
+//    super-block is exact integer; d / dmin and the activation scale are
+//    applied per super-block in FP32.
 //
 // Replaces, for batched verify shapes, the reference's per-matrix GEMV
 // launches over all rows (kernels/hip/gemm/lm_head.hip:61-173 with MaxRows 16,
@@ -48,16 +49,14 @@ constexpr int kQMax = 32639;
 constexpr int kBgWaves = 8;
 constexpr int kBgThreads = 64 * kBgWaves;
 constexpr int kBgRows = 64;  // rows per workgroup: 8 A tiles of 8 rows
-// LDS of the GEMM, per stage: A planes [8 t][8 j][4 g][16 r][8 B] + sums
-// [8 t][8 j][8] int32 + scales [8 t][8] float; two stages. The SwiGLU
-// epilogue reuses the first.
+// LDS of the GEMM, per stage: A planes [8 t][4 jp][4 g][16 r][2][8 B] +
+// scales [8 t][8] float; two stages. The SwiGLU epilogue reuses the first.
 constexpr uint32_t kBgLdsA = 8 * 8 * 4 * 16 * 8;
-constexpr uint32_t kBgStage = kBgLdsA + 8 * 8 * 8 * 4 + 8 * 8 * 4;  // one stage (double-buffered)
+constexpr uint32_t kBgStage = kBgLdsA + 8 * 8 * 4;  // one stage (double-buffered)
 constexpr uint32_t kBgLds = 2 * kBgStage;
 
 struct BgQuant {
     int8_t *planes;  // [rows][K/32][2: high, low][32 B]
-    int32_t *sums;   // [rows][K/32]
     float *scales;   // [rows][K/256]
 };
 
@@ -65,8 +64,7 @@ __host__ __device__ inline BgQuant bg_view(void *ws, int rows, int K) {
     uint8_t *p = static_cast<uint8_t *>(ws);
     BgQuant q;
     q.planes = reinterpret_cast<int8_t *>(p);
-    q.sums = reinterpret_cast<int32_t *>(p + (uint64_t)rows * K * 2);
-    q.scales = reinterpret_cast<float *>(p + (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 32) * 4);
+    q.scales = reinterpret_cast<float *>(p + (uint64_t)rows * K * 2);
     return q;
 }
 
@@ -76,43 +74,64 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 }
 
 // ---------------------------------------------------------------- prologue
-__global__ __launch_bounds__(256) void bg_prologue_kernel(const FusedGemmArgs A, BgQuant q) {
-    extern __shared__ float ys[];  // [K]
-    __shared__ double red[4];
+constexpr int kPrThreads = 512;
+
+__global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemmArgs A, BgQuant q) {
+    extern __shared__ float ys[];  // [K]: x, then y
+    __shared__ double red[kPrThreads / 64];
     const int row = blockIdx.x, K = A.K;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const float *x = A.x + (uint64_t)row * K;
-    if (A.gate) {
-        // gated head norm over heads of 128: x * (scale * w) * gate
-        const float *z = A.gate + (uint64_t)row * K;
-        for (int h = wave; h < K / 128; h += 4) {
-            const float a0 = x[h * 128 + lane], a1 = x[h * 128 + 64 + lane];
-            double ss = (double)a0 * (double)a0 + (double)a1 * (double)a1;
-            ss = wave_sum_d(ss);
-            const float mean = (float)(ss / 128.0);
-            const float scale = (float)(1.0 / sqrt((double)(mean + A.eps)));
-            ys[h * 128 + lane] = __fmul_rn(__fmul_rn(a0, __fmul_rn(scale, A.head_norm[lane])), z[h * 128 + lane]);
-            ys[h * 128 + 64 + lane] =
-                __fmul_rn(__fmul_rn(a1, __fmul_rn(scale, A.head_norm[64 + lane])), z[h * 128 + 64 + lane]);
-        }
-    } else if (A.norm) {
+    // x into LDS with independent 16-byte loads (the float64 sum of squares
+    // for RMSNorm on the way)
+    const float4 *x4 = reinterpret_cast<const float4 *>(A.x + (uint64_t)row * K);
+    double ss = 0.0;
+#pragma unroll 4
+    for (int c = t; c < K / 4; c += kPrThreads) {
+        const float4 v = x4[c];
+        *reinterpret_cast<float4 *>(ys + 4 * c) = v;
+        ss += (double)v.x * (double)v.x + (double)v.y * (double)v.y + (double)v.z * (double)v.z +
+              (double)v.w * (double)v.w;
+    }
+    float nscale = 1.f;
+    if (A.norm) {
         // forward.go:460-470 rmsNorm: float64 sum of squares, x * scale * w
-        double s = 0.0;
-        for (int c = t; c < K; c += 256) s += (double)x[c] * (double)x[c];
-        s = wave_sum_d(s);
-        if (lane == 0) red[wave] = s;
-        __syncthreads();
-        s = red[0] + red[1] + red[2] + red[3];
-        const float mean = (float)(s / (double)K);
-        const float scale = (float)(1.0 / sqrt((double)(mean + A.eps)));
-        for (int c = t; c < K; c += 256) ys[c] = __fmul_rn(__fmul_rn(x[c], scale), A.norm[c]);
-    } else {
-        for (int c = t; c < K; c += 256) ys[c] = x[c];
+        ss = wave_sum_d(ss);
+        if (lane == 0) red[wave] = ss;
     }
     __syncthreads();
+    if (A.norm) {
+        double s = 0.0;
+#pragma unroll
+        for (int w = 0; w < kPrThreads / 64; w++) s += red[w];
+        const float mean = (float)(s / (double)K);
+        nscale = (float)(1.0 / sqrt((double)(mean + A.eps)));
+    }
     const int nsb = K / 256;
-    for (int sb = wave; sb < nsb; sb += 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(ys + sb * 256 + 4 * lane);
+#pragma unroll 2
+    for (int sb = wave; sb < nsb; sb += kPrThreads / 64) {
+        const int e = sb * 256 + 4 * lane;
+        float4 v = *reinterpret_cast<const float4 *>(ys + e);
+        if (A.gate) {
+            // recurrent.go:39-50 gated head norm over heads of 128 (lanes 0..31
+            // and 32..63 hold one head each): x * (scale * w) * gate
+            const float4 z = *reinterpret_cast<const float4 *>(A.gate + (uint64_t)row * K + e);
+            const float4 w = *reinterpret_cast<const float4 *>(A.head_norm + (e & 127));
+            double hs = (double)v.x * (double)v.x + (double)v.y * (double)v.y + (double)v.z * (double)v.z +
+                        (double)v.w * (double)v.w;
+            for (int off = 16; off > 0; off >>= 1) hs += __shfl_xor(hs, off);
+            const float mean = (float)(hs / 128.0);
+            const float hsc = (float)(1.0 / sqrt((double)(mean + A.eps)));
+            v.x = __fmul_rn(__fmul_rn(v.x, __fmul_rn(hsc, w.x)), z.x);
+            v.y = __fmul_rn(__fmul_rn(v.y, __fmul_rn(hsc, w.y)), z.y);
+            v.z = __fmul_rn(__fmul_rn(v.z, __fmul_rn(hsc, w.z)), z.z);
+            v.w = __fmul_rn(__fmul_rn(v.w, __fmul_rn(hsc, w.w)), z.w);
+        } else if (A.norm) {
+            const float4 w = *reinterpret_cast<const float4 *>(A.norm + e);
+            v.x = __fmul_rn(__fmul_rn(v.x, nscale), w.x);
+            v.y = __fmul_rn(__fmul_rn(v.y, nscale), w.y);
+            v.z = __fmul_rn(__fmul_rn(v.z, nscale), w.z);
+            v.w = __fmul_rn(__fmul_rn(v.w, nscale), w.w);
+        }
         float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
         for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
         const float inv = m > 0.f ? (float)kQMax / m : 0.f;
@@ -130,11 +149,6 @@ __global__ __launch_bounds__(256) void bg_prologue_kernel(const FusedGemmArgs A,
         int8_t *dst = q.planes + (uint64_t)row * K * 2 + (uint64_t)(sb * 8 + j) * 64 + o;
         *reinterpret_cast<uint32_t *>(dst) = hp;
         *reinterpret_cast<uint32_t *>(dst + 32) = lp;
-        int sum = qv[0] + qv[1] + qv[2] + qv[3];
-        sum += __shfl_xor(sum, 1);
-        sum += __shfl_xor(sum, 2);
-        sum += __shfl_xor(sum, 4);
-        if ((lane & 7) == 0) q.sums[(uint64_t)row * (K / 32) + sb * 8 + j] = sum;
         if (lane == 0) q.scales[(uint64_t)row * nsb + sb] = m > 0.f ? m / (float)kQMax : 0.f;
     }
 }
@@ -154,6 +168,15 @@ struct BgArgs {
 // product here fits: MFMA sub-block results |r| < 2^17, scales <= 63,
 // sub-block sums |S| < 2^21.
 __device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+
+typedef __attribute__((ext_vector_type(2))) unsigned short u16x2;
+
+// Every byte of q times k, for byte products below 256: one packed 16-bit
+// multiply (b0 + 256 b1) k = b0 k + 256 b1 k per half, no carry between bytes.
+__device__ __forceinline__ uint32_t bytes_times(uint32_t q, uint32_t k) {
+    const u16x2 b = {(unsigned short)k, (unsigned short)k};
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q) * b);
+}
 
 __device__ __forceinline__ i32x4 mfma_i8(int64_t a, int64_t b) {
     const i32x4 zero = {0, 0, 0, 0};
@@ -248,16 +271,15 @@ __device__ __forceinline__ float out_map(const FusedSeg &S, int n, float v) {
     }
 }
 
-// Super-block sb of the workgroup's rows (planes, sums, scales): loaded by
+// Super-block sb of the workgroup's rows (planes, scales): loaded by
 // every thread into registers, then written to one of two LDS buffers.
 struct Staged {
     uint4 v[4];
-    int32_t sum;
     float xs;
 };
 
 __device__ __forceinline__ void stage_load(const BgArgs &A, Staged &st, int m0, int mrows, int sb) {
-    const int K = A.f.K, nsb = K / 256, nsub = K / 32;
+    const int K = A.f.K, nsb = K / 256;
 #pragma unroll
     for (int u = 0; u < 4; u++) {  // piece = (row, sub-block, plane, 16-byte half)
         const int idx = threadIdx.x + u * kBgThreads;
@@ -265,10 +287,6 @@ __device__ __forceinline__ void stage_load(const BgArgs &A, Staged &st, int m0, 
         st.v[u] = r < mrows ? *reinterpret_cast<const uint4 *>(A.q.planes + (uint64_t)(m0 + r) * K * 2 +
                                                                (uint64_t)(sb * 8 + j) * 64 + 32 * p + 16 * half)
                             : make_uint4(0u, 0u, 0u, 0u);
-    }
-    {
-        const int r = threadIdx.x >> 3, j = threadIdx.x & 7;
-        st.sum = r < mrows ? A.q.sums[(uint64_t)(m0 + r) * nsub + sb * 8 + j] : 0;
     }
     st.xs = threadIdx.x < mrows ? A.q.scales[(uint64_t)(m0 + threadIdx.x) * nsb + sb] : 0.f;
 }
@@ -280,7 +298,7 @@ __device__ __forceinline__ uint32_t la_off(int t, int j, int gg, int rr) {
     return ((uint32_t)(((t * 4 + (j >> 1)) * 4 + gg) * 16 + rr) * 2 + (j & 1)) * 8;
 }
 
-__device__ __forceinline__ void stage_store(const Staged &st, uint8_t *la, int32_t *lsum, float *lxs) {
+__device__ __forceinline__ void stage_store(const Staged &st, uint8_t *la, float *lxs) {
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int idx = threadIdx.x + u * kBgThreads;
@@ -292,7 +310,6 @@ __device__ __forceinline__ void stage_store(const Staged &st, uint8_t *la, int32
     }
     {
         const int r = threadIdx.x >> 3, j = threadIdx.x & 7;
-        lsum[((r >> 3) * 8 + j) * 8 + (r & 7)] = st.sum;
     }
     if (threadIdx.x < kBgRows) lxs[threadIdx.x] = st.xs;
 }
@@ -318,14 +335,13 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
     }
     Staged st;
     stage_load(A, st, m0, mrows, sb_lo);
-    stage_store(st, lds, reinterpret_cast<int32_t *>(lds + kBgLdsA), reinterpret_cast<float *>(lds + kBgLdsA + 2048));
+    stage_store(st, lds, reinterpret_cast<float *>(lds + kBgLdsA));
     __syncthreads();
     for (int sb = sb_lo; sb < nsb; sb++) {
         uint8_t *cur_l = lds + (uint32_t)((sb - sb_lo) & 1) * kBgStage;
         uint8_t *nxt_l = lds + (uint32_t)((sb - sb_lo + 1) & 1) * kBgStage;
         const uint8_t *la = cur_l;
-        const int32_t *lsum = reinterpret_cast<const int32_t *>(cur_l + kBgLdsA);
-        const float *lxs = reinterpret_cast<const float *>(cur_l + kBgLdsA + 2048);
+        const float *lxs = reinterpret_cast<const float *>(cur_l + kBgLdsA);
         const bool more = sb + 1 < nsb;
         if (more) stage_load(A, st, m0, mrows, sb + 1);
         const W cur = w;  // this super-block; the next one's loads go out now
@@ -364,9 +380,13 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                         const uint32_t q[4] = {(uint32_t)qe, (uint32_t)(qe >> 32), (uint32_t)qo, (uint32_t)(qo >> 32)};
                         const uint32_t lo[2] = {(uint32_t)(sce & 7), (uint32_t)(sco & 7)};
                         const uint32_t hi[2] = {(uint32_t)(sce >> 3), (uint32_t)(sco >> 3)};
-                        const i32x4 b_lo = {(int)(q[0] * lo[0]), (int)(q[1] * lo[0]), (int)(q[2] * lo[1]), (int)(q[3] * lo[1])};
-                        const i32x4 b_hi = {(int)(q[0] * hi[0]), (int)(q[1] * hi[0]), (int)(q[2] * hi[1]), (int)(q[3] * hi[1])};
-                        const int me = (int)((uint32_t)mne * 0x01010101u), mo = (int)((uint32_t)mno * 0x01010101u);
+                        const i32x4 b_lo = {(int)bytes_times(q[0], lo[0]), (int)bytes_times(q[1], lo[0]),
+                                            (int)bytes_times(q[2], lo[1]), (int)bytes_times(q[3], lo[1])};
+                        const i32x4 b_hi = {(int)bytes_times(q[0], hi[0]), (int)bytes_times(q[1], hi[0]),
+                                            (int)bytes_times(q[2], hi[1]), (int)bytes_times(q[3], hi[1])};
+                        // byte 0 in all four bytes (v_perm; a multiply by 0x01010101 is quarter rate)
+                        const int me = (int)__builtin_amdgcn_perm((uint32_t)mne, (uint32_t)mne, 0u);
+                        const int mo = (int)__builtin_amdgcn_perm((uint32_t)mno, (uint32_t)mno, 0u);
                         const i32x4 b_mn = {me, me, mo, mo};
 #pragma unroll
                         for (int u = 0; u < 4; u++) {
@@ -384,52 +404,98 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                         const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
-                            // this lane's plane (rows 0..7 high, 8..15 low), then both
+                            // this lane's plane (rows 0..7 high, 8..15 low)
                             const float v = d * (float)(alo[u][i] + 8 * ahi[u][i]) - dmin * (float)amn[u][i];
-                            const float other = __shfl_xor(v, 32);
-                            y[t][i] += xsv[i] * (256.f * v + other);
+                            y[t][i] += xsv[i] * v;
                         }
                     }
                 }
             } else {
+                // Q6_K: q = ql | qh << 4 - 32 in [-32, 31] and a signed 8-bit
+                // scale per 16 elements, written in balanced base 7
+                // (s = e0 + 7 e1 + 49 e2, e in [-3, 3]): every q * e (|.| <= 96)
+                // is an exact int8 B operand, so three K = 64 MFMAs per pair of
+                // sub-blocks and 8-row tile replace the int32 scaling. A lane's
+                // eight bytes of sub-block j lie in one 16-element scale group.
                 const float d = h2f((uint16_t)cur.d);
-                int64_t bq[8];
-                int sc2[8];  // scales of elements 0..15 (low half) and 16..31 (high half) of sub-block j
+                uint32_t qw[8][2];  // q + 32 (0..63) of sub-block j, bytes 0..3 and 4..7
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const int half = j >> 2, qd = j & 3;
                     const uint64_t lo4 = (cur.ql[2 * half + (qd & 1)] >> (4 * (qd >> 1))) & 0x0F0F0F0F0F0F0F0Full;
                     const uint64_t hi2 = ((cur.qh[half] >> (2 * qd)) & 0x0303030303030303ull) << 4;
-                    bq[j] = (int64_t)q6_to_i8(lo4 | hi2);
-                    sc2[j] = (sbyte(cur.sc, 8 * half + 2 * qd) & 0xffff) | (sbyte(cur.sc, 8 * half + 2 * qd + 1) << 16);
+                    qw[j][0] = (uint32_t)(lo4 | hi2);
+                    qw[j][1] = (uint32_t)((lo4 | hi2) >> 32);
+                }
+                // the three digits of this lane's scale for every sub-block,
+                // each as (e, -32 e) in both 16-bit halves
+                uint32_t dm[8][3], dc[8][3];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    uint32_t u = (uint32_t)(sbyte(cur.sc, 2 * j + (g >> 1)) + 171);  // 43..298
+#pragma unroll
+                    for (int k = 0; k < 3; k++) {
+                        const uint32_t nq = k < 2 ? (u * 9363u) >> 16 : 0u;  // u / 7 for u < 13107
+                        const int e = (int)(k < 2 ? u - 7 * nq : u) - 3;
+                        // low 16 bits in both halves
+                        dm[j][k] = __builtin_amdgcn_perm((uint32_t)e, (uint32_t)e, 0x01000100u);
+                        dc[j][k] = __builtin_amdgcn_perm((uint32_t)(-32 * e), (uint32_t)(-32 * e), 0x01000100u);
+                        u = nq;
+                    }
                 }
 #pragma unroll
-                for (int t = 0; t < 8; t++) {  // all 8 tiles: rows past the end are zero in LDS
-                    int acc[4] = {0, 0, 0, 0};
+                for (int th = 0; th < 2; th++) {
+                    i32x4 a0[4], a1[4], a2[4];
 #pragma unroll
-                    for (int j = 0; j < 8; j++) {
-                        const int64_t a = *reinterpret_cast<const int64_t *>(la + la_off(t, j, g, c));
-                        // lanes g < 2 hold elements 0..15 (first scale group)
-                        const i32x4 r0 = mfma_i8(a, g < 2 ? bq[j] : 0);
-                        const i32x4 r1 = mfma_i8(a, g < 2 ? 0 : bq[j]);
-                        const int s0 = (int)(int16_t)(sc2[j] & 0xffff), s1 = sc2[j] >> 16;
-#pragma unroll
-                        for (int i = 0; i < 4; i++) acc[i] = mad24(r1[i], s1, mad24(r0[i], s0, acc[i]));
+                    for (int u = 0; u < 4; u++) {
+                        a0[u] = i32x4{0, 0, 0, 0};
+                        a1[u] = i32x4{0, 0, 0, 0};
+                        a2[u] = i32x4{0, 0, 0, 0};
                     }
-                    const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
-                    const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int lo = __shfl_xor(acc[i], 32);
-                        y[t][i] += xsv[i] * (d * (256.f * (float)acc[i] + (float)lo));
+                    for (int jp = 0; jp < 4; jp++) {
+                        i32x4 bk[3];
+#pragma unroll
+                        for (int w = 0; w < 4; w++) {
+                            const int j = 2 * jp + (w >> 1);
+                            const uint32_t qv = qw[j][w & 1];
+                            // bytes 0, 2 and 1, 3 in 16-bit halves: (q + 32) e - 32 e
+                            const u16x2 ev = __builtin_bit_cast(u16x2, qv & 0x00FF00FFu);
+                            const u16x2 ov = __builtin_bit_cast(u16x2, (qv >> 8) & 0x00FF00FFu);
+#pragma unroll
+                            for (int k = 0; k < 3; k++) {
+                                const u16x2 m = __builtin_bit_cast(u16x2, dm[j][k]);
+                                const u16x2 cc = __builtin_bit_cast(u16x2, dc[j][k]);
+                                const uint32_t pe = __builtin_bit_cast(uint32_t, ev * m + cc);
+                                const uint32_t po = __builtin_bit_cast(uint32_t, ov * m + cc);
+                                bk[k][w] = (int)__builtin_amdgcn_perm(po, pe, 0x06020400u);
+                            }
+                        }
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            const int t = 4 * th + u;
+                            const i32x4 av = *reinterpret_cast<const i32x4 *>(la + la_off(t, 2 * jp, g, c));
+                            a0[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bk[0], a0[u], 0, 0, 0);
+                            a1[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bk[1], a1[u], 0, 0, 0);
+                            a2[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bk[2], a2[u], 0, 0, 0);
+                        }
                     }
-                    __builtin_amdgcn_sched_barrier(0);  // one A tile at a time (register pressure)
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const int t = 4 * th + u;
+                        const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
+                        const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const int acc = mad24(49, a2[u][i], mad24(7, a1[u][i], a0[u][i]));
+                            y[t][i] += xsv[i] * (d * (float)acc);
+                        }
+                    }
                 }
             }
         }
         if (more)
-            stage_store(st, nxt_l, reinterpret_cast<int32_t *>(nxt_l + kBgLdsA),
-                        reinterpret_cast<float *>(nxt_l + kBgLdsA + 2048));
+            stage_store(st, nxt_l, reinterpret_cast<float *>(nxt_l + kBgLdsA));
         __syncthreads();  // stage sb + 1 written; stage sb read by every wave
     }
 }
@@ -468,6 +534,11 @@ __global__ __launch_bounds__(kBgThreads) void bg_gemm_kernel(const BgArgs A) {
         bg_main<kQ6K>(A, lds, m0, mrows, live, wrow, y);
     else
         bg_main<kQ4K>(A, lds, m0, mrows, live, wrow, y);
+    // y holds the plane sums: high on lanes g < 2, low on g >= 2 (same rows)
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) y[t][i] = fmaf(256.f, y[t][i], __shfl_xor(y[t][i], 32));
 
     // epilogue: lanes g < 2 hold rows 8 t + 4 g + i of channel n0 + c
     if (A.splits > 1) {  // partial sums of this split; bg_reduce_kernel finishes
@@ -559,7 +630,7 @@ int bg_splits(int wgs, int nsb) {
 }
 
 uint64_t bg_quant_bytes(int rows, int K) {
-    return (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 32) * 4 + (uint64_t)rows * (K / 256) * 4;
+    return (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 256) * 4;
 }
 
 }  // namespace
@@ -605,7 +676,7 @@ hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t 
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)kBgLds);
         attr = true;
     }
-    bg_prologue_kernel<<<(unsigned)a.rows, 256, plds, s>>>(a, A.q);
+    bg_prologue_kernel<<<(unsigned)a.rows, kPrThreads, plds, s>>>(a, A.q);
     int nn[kFusedMaxSeg];
     for (int i = 0; i < a.nseg; i++) nn[i] = a.seg[i].n;
     unsigned gx, gy;
