@@ -316,7 +316,7 @@ __device__ __forceinline__ void stage_store(const Staged &st, uint8_t *la, float
 
 // The main loop of one wave over the super-blocks (weights of dtype DT).
 // LDS holds two stages; stage sb + 1 is loaded while sb is multiplied.
-template <int DT>
+template <int DT, int TH>
 __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, int mrows, bool live,
                                         const uint8_t *wrow, float (&y)[8][4]) {
     const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
@@ -361,7 +361,7 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                 // passes of four A tiles bound the registers.
                 const float d = h2f((uint16_t)(cur.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(cur.hdr.x >> 16));
 #pragma unroll
-                for (int th = 0; th < 2; th++) {
+                for (int th = 0; th < TH; th++) {  // TH = 1: rows in tiles 0..3 only
                     i32x4 alo[4], ahi[4], amn[4];
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
@@ -444,7 +444,7 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                     }
                 }
 #pragma unroll
-                for (int th = 0; th < 2; th++) {
+                for (int th = 0; th < TH; th++) {  // TH = 1: rows in tiles 0..3 only
                     i32x4 a0[4], a1[4], a2[4];
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
@@ -530,10 +530,14 @@ __global__ __launch_bounds__(kBgThreads) void bg_gemm_kernel(const BgArgs A) {
     for (int t = 0; t < 8; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) y[t][i] = 0.f;
-    if (S.dtype == kQ6K)
-        bg_main<kQ6K>(A, lds, m0, mrows, live, wrow, y);
-    else
-        bg_main<kQ4K>(A, lds, m0, mrows, live, wrow, y);
+    // a block of at most 32 rows multiplies only the first four 8-row tiles
+    if (S.dtype == kQ6K) {
+        if (mrows > 32) bg_main<kQ6K, 2>(A, lds, m0, mrows, live, wrow, y);
+        else bg_main<kQ6K, 1>(A, lds, m0, mrows, live, wrow, y);
+    } else {
+        if (mrows > 32) bg_main<kQ4K, 2>(A, lds, m0, mrows, live, wrow, y);
+        else bg_main<kQ4K, 1>(A, lds, m0, mrows, live, wrow, y);
+    }
     // y holds the plane sums: high on lanes g < 2, low on g >= 2 (same rows)
 #pragma unroll
     for (int t = 0; t < 8; t++)
