@@ -254,7 +254,6 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict
 //   scales [rows][K/256]  float (x ~= scale * q, q = 256 h + l)
 struct MoeQuant {
     int8_t *planes;
-    int32_t *sums;
     float *scales;
 };
 
@@ -262,8 +261,7 @@ __host__ __device__ inline MoeQuant moe_quant_view(void *ws, int rows, int K) {
     uint8_t *p = static_cast<uint8_t *>(ws);
     MoeQuant q;
     q.planes = reinterpret_cast<int8_t *>(p);
-    q.sums = reinterpret_cast<int32_t *>(p + (uint64_t)rows * K * 2);
-    q.scales = reinterpret_cast<float *>(p + (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 32) * 4);
+    q.scales = reinterpret_cast<float *>(p + (uint64_t)rows * K * 2);
     return q;
 }
 
@@ -290,11 +288,6 @@ __global__ __launch_bounds__(256) void moe_quant_kernel(const float *__restrict_
     int8_t *dst = q.planes + (uint64_t)row * K * 2 + (uint64_t)(sb * 8 + j) * 64 + o;
     *reinterpret_cast<uint32_t *>(dst) = hp;
     *reinterpret_cast<uint32_t *>(dst + 32) = lp;
-    int sum = qv[0] + qv[1] + qv[2] + qv[3];
-    sum += __shfl_xor(sum, 1);
-    sum += __shfl_xor(sum, 2);
-    sum += __shfl_xor(sum, 4);
-    if ((lane & 7) == 0) q.sums[(uint64_t)row * (K / 32) + sb * 8 + j] = sum;
     if (lane == 0) q.scales[(uint64_t)row * nsb + sb] = m > 0.f ? m / (float)kQMax : 0.f;
 }
 
@@ -311,14 +304,20 @@ struct MoeGemmArgs {
     float *out0, *out1;   // [rows*used][N]
 };
 
-// 24-bit multiply-add (full rate; a 32-bit multiply is quarter rate). Every
-// product here fits: MFMA sub-block results |r| < 2^17, scales <= 63,
-// sub-block sums |S| < 2^21.
-__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
+typedef __attribute__((ext_vector_type(2))) unsigned short u16x2;
 
-__device__ __forceinline__ i32x4 mfma_i8(int64_t a, int64_t b) {
-    const i32x4 zero = {0, 0, 0, 0};
-    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero, 0, 0, 0);
+// Every byte of q times k, for byte products below 256: one packed 16-bit
+// multiply (b0 + 256 b1) k = b0 k + 256 b1 k per half, no carry between bytes.
+__device__ __forceinline__ uint32_t bytes_times(uint32_t q, uint32_t k) {
+    const u16x2 b = {(unsigned short)k, (unsigned short)k};
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q) * b);
+}
+
+// LDS byte offset of the 8 activation bytes of sub-block j, MFMA row r (high
+// plane of assignment r for r < 8, low plane of r - 8), lane group gg:
+// sub-blocks 2 jp and 2 jp + 1 side by side (one 16-byte read per K = 64).
+__device__ __forceinline__ uint32_t moe_la_off(int j, int r, int gg) {
+    return ((uint32_t)((((j >> 1) * 16 + r) * 4 + gg) * 2 + (j & 1))) * 8;
 }
 
 // tensor/quant.go:96-103 getScaleMinK4 for sub-block j of a Q4_K block
@@ -343,9 +342,9 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s1, uint32_t s2, ui
 // activation planes of assignment c & 7 (high plane for c < 8) into A order.
 __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))) void moe_gemm_kernel(MoeGemmArgs A) {
     // LDS: partial sums [tpw][nsb][mats][8 rows][16 ch] floats, then the
-    // chunk's activations: planes [K/32][16 r][32 B] (r < 8 high plane of
-    // assignment r, r >= 8 low plane of assignment r - 8), sub-block sums
-    // [K/32][8] int32, scales [K/256][8] float.
+    // chunk's activations: planes [K/64][16 r][4 g][2][8 B] (r < 8 high
+    // plane of assignment r, r >= 8 low plane of assignment r - 8), scales
+    // [K/256][8] float.
     extern __shared__ __attribute__((aligned(16))) float part[];
     const int e = blockIdx.x;
     const int count = A.counts[e];
@@ -359,8 +358,7 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
     const int mats = dual ? 2 : 1;
     __shared__ int s_row[kChunk], s_out[kChunk];
     uint8_t *la = reinterpret_cast<uint8_t *>(part + (uint64_t)A.tpw * nsb * mats * 128);
-    int32_t *lsum = reinterpret_cast<int32_t *>(la + (uint64_t)nsub * 16 * 32);
-    float *lxs = reinterpret_cast<float *>(lsum + nsub * 8);
+    float *lxs = reinterpret_cast<float *>(la + (uint64_t)nsub * 16 * 32);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = lane & 15, g = lane >> 4;
     const uint64_t cap = (uint64_t)A.rows * A.used;
@@ -387,11 +385,12 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
             const int j = idx >> 5, r = (idx >> 1) & 15, half = idx & 1;
             const int8_t *src = A.xq.planes + (uint64_t)s_row[r & 7] * A.K * 2 + (uint64_t)j * 64 + (r >= 8 ? 32 : 0) +
                                 16 * half;
-            *reinterpret_cast<uint4 *>(la + ((uint64_t)j * 16 + r) * 32 + 16 * half) =
-                *reinterpret_cast<const uint4 *>(src);
+            const uint4 v = *reinterpret_cast<const uint4 *>(src);
+            // lane groups 2 half and 2 half + 1; sub-blocks 2 jp, 2 jp + 1 side by side
+            uint8_t *d0 = la + moe_la_off(j, r, 2 * half);
+            *reinterpret_cast<uint2 *>(d0) = make_uint2(v.x, v.y);
+            *reinterpret_cast<uint2 *>(d0 + 16) = make_uint2(v.z, v.w);
         }
-        for (int idx = threadIdx.x; idx < nsub * 8; idx += kMoeThreads)
-            lsum[idx] = A.xq.sums[(uint64_t)s_row[idx & 7] * nsub + (idx >> 3)];
         for (int idx = threadIdx.x; idx < nsb * 8; idx += kMoeThreads)
             lxs[idx] = A.xq.scales[(uint64_t)s_row[idx & 7] * nsb + (idx >> 3)];
         __syncthreads();
@@ -421,30 +420,39 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
                 const int sb = sbs[u];
                 const float4 xs4 = *reinterpret_cast<const float4 *>(lxs + sb * 8 + rbase);
                 const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
-                int acc[4] = {0, 0, 0, 0}, ms[4] = {0, 0, 0, 0};
+                // sub-block scale (two 3-bit digits) and min in the B operands
+                // of three K = 64 MFMAs per pair of sub-blocks: exact int32
+                i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    int scj, mnj;
-                    scale_min_k4(j, hdr[u].y, hdr[u].z, hdr[u].w, &scj, &mnj);
-                    const uint64_t raw = qv[u][j >> 1];
-                    const uint64_t bq = (j & 1) ? (raw >> 4) & 0x0F0F0F0F0F0F0F0Full : raw & 0x0F0F0F0F0F0F0F0Full;
-                    const int64_t av = *reinterpret_cast<const int64_t *>(la + ((uint64_t)(sb * 8 + j) * 16 + c) * 32 + 8 * g);
-                    const i32x4 r = mfma_i8(av, (int64_t)bq);
-                    const int4 sm = *reinterpret_cast<const int4 *>(lsum + (sb * 8 + j) * 8 + rbase);
-#pragma unroll
-                    for (int i = 0; i < 4; i++) acc[i] = mad24(r[i], scj, acc[i]);
-                    ms[0] = mad24(mnj, sm.x, ms[0]);
-                    ms[1] = mad24(mnj, sm.y, ms[1]);
-                    ms[2] = mad24(mnj, sm.z, ms[2]);
-                    ms[3] = mad24(mnj, sm.w, ms[3]);
+                for (int jp = 0; jp < 4; jp++) {
+                    const uint64_t raw = qv[u][jp];
+                    const uint64_t qe = raw & 0x0F0F0F0F0F0F0F0Full, qo = (raw >> 4) & 0x0F0F0F0F0F0F0F0Full;
+                    int sce, mne, sco, mno;
+                    scale_min_k4(2 * jp, hdr[u].y, hdr[u].z, hdr[u].w, &sce, &mne);
+                    scale_min_k4(2 * jp + 1, hdr[u].y, hdr[u].z, hdr[u].w, &sco, &mno);
+                    const uint32_t q[4] = {(uint32_t)qe, (uint32_t)(qe >> 32), (uint32_t)qo, (uint32_t)(qo >> 32)};
+                    const uint32_t lo[2] = {(uint32_t)(sce & 7), (uint32_t)(sco & 7)};
+                    const uint32_t hi[2] = {(uint32_t)(sce >> 3), (uint32_t)(sco >> 3)};
+                    const i32x4 b_lo = {(int)bytes_times(q[0], lo[0]), (int)bytes_times(q[1], lo[0]),
+                                        (int)bytes_times(q[2], lo[1]), (int)bytes_times(q[3], lo[1])};
+                    const i32x4 b_hi = {(int)bytes_times(q[0], hi[0]), (int)bytes_times(q[1], hi[0]),
+                                        (int)bytes_times(q[2], hi[1]), (int)bytes_times(q[3], hi[1])};
+                    const int me = (int)__builtin_amdgcn_perm((uint32_t)mne, (uint32_t)mne, 0u);
+                    const int mo = (int)__builtin_amdgcn_perm((uint32_t)mno, (uint32_t)mno, 0u);
+                    const i32x4 b_mn = {me, me, mo, mo};
+                    const i32x4 av = *reinterpret_cast<const i32x4 *>(la + moe_la_off(sb * 8 + 2 * jp, c, g));
+                    alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_lo, alo, 0, 0, 0);
+                    ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_hi, ahi, 0, 0, 0);
+                    amn = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_mn, amn, 0, 0, 0);
                 }
                 const float d = h2f((uint16_t)(hdr[u].x & 0xffffu)), dmin = h2f((uint16_t)(hdr[u].x >> 16));
                 float *dst = part + (uint64_t)slot[u] * 128;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int lo = __shfl_xor(acc[i], 32);
-                    if (g < 2) dst[(4 * g + i) * 16 + c] = xs[i] * (d * (256.f * (float)acc[i] + (float)lo) -
-                                                                    dmin * (float)ms[i]);
+                    // this lane's plane (rows 0..7 high, 8..15 low), then both
+                    const float v = d * (float)(alo[i] + 8 * ahi[i]) - dmin * (float)amn[i];
+                    const float lo = __shfl_xor(v, 32);
+                    if (g < 2) dst[(4 * g + i) * 16 + c] = xs[i] * (256.f * v + lo);
                 }
             }
         }
@@ -491,8 +499,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ x,
 
 }  // namespace
 
-uint64_t moe_gemm_ws(int act_rows, int K) { return (uint64_t)act_rows * K * 2 + (uint64_t)act_rows * (K / 32) * 4 +
-                                                      (uint64_t)act_rows * (K / 256) * 4 + 256; }
+uint64_t moe_gemm_ws(int act_rows, int K) { return (uint64_t)act_rows * K * 2 + (uint64_t)act_rows * (K / 256) * 4 + 256; }
 
 hipError_t launch_moe_router(const float *y, int H, int rows, const float *w, int E, float *logits, const float *sv,
                              float *extra, hipStream_t s) {
@@ -534,7 +541,7 @@ hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
     tpw = std::max(1, std::min(tpw, 16));
     tpw = std::min(tpw, tiles);
     a.tpw = tpw;
-    const uint32_t lds = (uint32_t)tpw * nsb * mats * 512 + (uint32_t)(g.K / 32) * (16 * 32 + 32) + (uint32_t)nsb * 32;
+    const uint32_t lds = (uint32_t)tpw * nsb * mats * 512 + (uint32_t)(g.K / 32) * (16 * 32) + (uint32_t)nsb * 32;
     const int units = act_rows * nsb;
     moe_quant_kernel<<<(units + 3) / 4, 256, 0, s>>>(g.x, act_rows, g.K, a.xq);
     moe_gemm_kernel<<<dim3((unsigned)g.experts, (unsigned)((tiles + tpw - 1) / tpw)), kMoeThreads, lds, s>>>(a);
