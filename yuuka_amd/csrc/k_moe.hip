@@ -89,10 +89,10 @@ __global__ __launch_bounds__(64 * kRouterWaves) void moe_router_kernel(const flo
 // ---------------------------------------------------------------- route
 // forward.go:393-439 selectExperts for every row (one wave per row, the
 // row's logits held in registers, a taken mask per lane), then binning by
-// expert (the reference's assignment layout, yuuka_hip.h:457-460: bucket
-// capacity rows*used). An assignment's place in its bin is the number of
-// earlier (row, slot) assignments to the same expert, so the bins are in
-// (row, slot) order. LDS: ids, weights and picked logits [rows*used].
+// expert in a second launch (the reference's assignment layout,
+// yuuka_hip.h:457-460: bucket capacity rows*used). An assignment's place in
+// its bin is the number of earlier (row, slot) assignments to the same
+// expert, so the bins are in (row, slot) order.
 constexpr int kRouteMaxPerLane = 16;  // experts <= 1024
 
 // Monotone uint32 image of a float (larger value, larger key); -0 keys as +0
@@ -150,101 +150,105 @@ __device__ __forceinline__ float pick_lane_value(const float (&v)[kRouteMaxPerLa
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), e & 63));
 }
 
-__global__ __launch_bounds__(1024) void moe_route_kernel(const float *__restrict__ logits, int rows, int E,
-                                                         int used, int32_t *__restrict__ ids,
-                                                         float *__restrict__ weights, int32_t *__restrict__ counts,
-                                                         int32_t *__restrict__ arows, int32_t *__restrict__ aslots,
-                                                         float *__restrict__ aweights) {
-    extern __shared__ int32_t sid[];
-    float *sw = reinterpret_cast<float *>(sid + ((rows * used + 3) & ~3));
-    float *spv = sw + rows * used;  // picked logits
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-    for (int r = wave; r < rows; r += nw) {
-        const float *l = logits + (uint64_t)r * E;
-        float v[kRouteMaxPerLane];
+// One wave per row (PL = experts per lane / 64, rounded up): the slots'
+// picks and weights, kept by lane `slot`.
+template <int PL>
+__global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ logits, int rows, int E, int used,
+                                                        int32_t *__restrict__ ids, float *__restrict__ weights) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float *l = logits + (uint64_t)r * E;
+    float v[kRouteMaxPerLane];
 #pragma unroll
-        for (int i = 0; i < kRouteMaxPerLane; i++) v[i] = lane + 64 * i < E ? l[lane + 64 * i] : 0.f;
-        uint32_t taken = 0;
-        for (int slot = 0; slot < used; slot++) {
-            // Reference scan: the first untaken expert starts as best and a
-            // later one replaces it only when strictly greater. So a NaN
-            // start keeps the slot, NaN elsewhere never wins, and equal
-            // maxima resolve to the lowest index: the largest key
-            // (order key of the logit, then the complemented index) over
-            // untaken non-NaN experts.
-            uint64_t key = 0;
-            int first = INT_MAX;
+    for (int i = 0; i < kRouteMaxPerLane; i++) v[i] = i < PL && lane + 64 * i < E ? l[lane + 64 * i] : 0.f;
+    uint32_t taken = 0;
+    int my_id = 0;
+    float my_pv = 0.f;
+    for (int slot = 0; slot < used; slot++) {
+        // Reference scan: the first untaken expert starts as best and a
+        // later one replaces it only when strictly greater. So a NaN start
+        // keeps the slot, NaN elsewhere never wins, and equal maxima resolve
+        // to the lowest index: the largest key (order key of the logit, then
+        // the complemented index) over untaken non-NaN experts.
+        uint64_t key = 0;
+        int first = INT_MAX;
 #pragma unroll
-            for (int i = 0; i < kRouteMaxPerLane; i++) {
-                const int e = lane + 64 * i;
-                if (e >= E || (taken >> i & 1u)) continue;
-                first = min(first, e);
-                if (v[i] == v[i]) {
-                    const uint64_t k = ((uint64_t)route_key(v[i]) << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
-                    key = k > key ? k : key;
-                }
-            }
-            key = wave_max_u64(key);
-            first = wave_min_i32(first);
-            int pick;
-            if (first == INT_MAX) {
-                pick = 0;  // more slots than experts (forward.go:413-417)
-            } else {
-                const float fv = pick_lane_value(v, first);
-                pick = (!(fv == fv) || key == 0) ? first : (int)(0xffffffffu - (uint32_t)key);
-                if ((pick & 63) == lane) taken |= 1u << (pick >> 6);
-            }
-            const float pvv = pick_lane_value(v, pick);
-            if (lane == 0) {
-                sid[r * used + slot] = pick;
-                spv[r * used + slot] = pvv;
+        for (int i = 0; i < PL; i++) {
+            const int e = lane + 64 * i;
+            if (e >= E || (taken >> i & 1u)) continue;
+            first = min(first, e);
+            if (v[i] == v[i]) {
+                const uint64_t k = ((uint64_t)route_key(v[i]) << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
+                key = k > key ? k : key;
             }
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // weights: float32(exp(float64(l - max))), float32 total in slot
-        // order, then each divided by the total (forward.go:424-438); lane s
-        // computes slot s's exponential, lane 0 the ordered total.
-        const float *pv = spv + r * used;
-        float mx = pv[0];
-        for (int sl = 1; sl < used; sl++)
-            if (pv[sl] > mx) mx = pv[sl];
-        const float mine = lane < used ? pv[lane] : 0.f;
-        const float wt = lane < used ? (float)exp((double)__fsub_rn(mine, mx)) : 0.f;
-        float total = 0.f;
-        for (int sl = 0; sl < used; sl++)
-            total = __fadd_rn(total, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wt), sl)));
-        if (lane < used) {
-            const float val = total > 0.f ? __fdiv_rn(wt, total) : wt;
-            sw[r * used + lane] = val;
-            ids[(uint64_t)r * used + lane] = sid[r * used + lane];
-            weights[(uint64_t)r * used + lane] = val;
+        key = wave_max_u64(key);
+        first = wave_min_i32(first);
+        int pick;
+        if (first == INT_MAX) {
+            pick = 0;  // more slots than experts (forward.go:413-417)
+        } else {
+            const float fv = pick_lane_value(v, first);
+            pick = (!(fv == fv) || key == 0) ? first : (int)(0xffffffffu - (uint32_t)key);
+            if ((pick & 63) == lane) taken |= 1u << (pick >> 6);
+        }
+        const float pvv = pick_lane_value(v, pick);
+        if (lane == slot) {
+            my_id = pick;
+            my_pv = pvv;
         }
     }
-    const int cap = rows * used;
-    for (int a = cap + threadIdx.x; a < ((cap + 3) & ~3); a += blockDim.x) sid[a] = -1;  // pad to int4
-    __syncthreads();
-    // thread e fills bin e in (row, slot) order and writes its count
-    const int4 *sid4 = reinterpret_cast<const int4 *>(sid);
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        int n = 0;
-        for (int a4 = 0; a4 < (cap + 3) / 4; a4++) {
-            const int4 v = sid4[a4];
-            const int vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                if (vv[t] != e) continue;
-                const int a = 4 * a4 + t;
-                const uint64_t o = (uint64_t)e * cap + n;
-                arows[o] = a / used;
-                aslots[o] = a % used;
-                aweights[o] = sw[a];
-                n++;
-            }
-        }
-        counts[e] = n;
+    // weights: float32(exp(float64(l - max))), float32 total in slot order,
+    // then each divided by the total (forward.go:424-438); lane s computes
+    // slot s's exponential, every lane the ordered total.
+    float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_pv), 0));
+    for (int sl = 1; sl < used; sl++) {
+        const float o = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_pv), sl));
+        if (o > mx) mx = o;
     }
+    const float wt = lane < used ? (float)exp((double)__fsub_rn(my_pv, mx)) : 0.f;
+    float total = 0.f;
+    for (int sl = 0; sl < used; sl++)
+        total = __fadd_rn(total, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wt), sl)));
+    if (lane < used) {
+        ids[(uint64_t)r * used + lane] = my_id;
+        weights[(uint64_t)r * used + lane] = total > 0.f ? __fdiv_rn(wt, total) : wt;
+    }
+}
+
+// Workgroup e: expert e's assignments in (row, slot) order. Each pass tests
+// 256 assignments; positions from a ballot prefix inside each wave plus the
+// earlier waves' counts. Every count is written (no clearing needed).
+__global__ __launch_bounds__(256) void moe_bin_kernel(const int32_t *__restrict__ ids,
+                                                      const float *__restrict__ weights, int cap, int used,
+                                                      int32_t *__restrict__ counts, int32_t *__restrict__ arows,
+                                                      int32_t *__restrict__ aslots, float *__restrict__ aweights) {
+    __shared__ int wcnt[2][4];
+    const int e = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint64_t below = (1ull << lane) - 1ull;
+    int base = 0, ph = 0;
+    for (int a0 = 0; a0 < cap; a0 += 256, ph ^= 1) {
+        const int a = a0 + (int)threadIdx.x;
+        const bool hit = a < cap && ids[a] == e;
+        const uint64_t b = __ballot(hit);
+        if (lane == 0) wcnt[ph][wave] = __popcll(b);
+        __syncthreads();  // alternating count buffers: one barrier per pass
+        int off = base, tot = 0;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            off += w < wave ? wcnt[ph][w] : 0;
+            tot += wcnt[ph][w];
+        }
+        if (hit) {
+            const uint64_t o = (uint64_t)e * cap + off + __popcll(b & below);
+            arows[o] = a / used;
+            aslots[o] = a % used;
+            aweights[o] = weights[a];
+        }
+        base += tot;
+    }
+    if (threadIdx.x == 0) counts[e] = base;
 }
 
 // ---------------------------------------------------------------- grouped GEMM
@@ -510,9 +514,12 @@ hipError_t launch_moe_router(const float *y, int H, int rows, const float *w, in
 
 hipError_t launch_moe_route(const float *logits, int rows, int E, int used, int32_t *ids, float *weights,
                             int32_t *counts, int32_t *arows, int32_t *aslots, float *aweights, hipStream_t s) {
-    if (E > 64 * kRouteMaxPerLane) return hipErrorInvalidValue;
-    const uint32_t lds = (uint32_t)rows * used * 12 + 16;
-    moe_route_kernel<<<1, 1024, lds, s>>>(logits, rows, E, used, ids, weights, counts, arows, aslots, aweights);
+    if (E > 64 * kRouteMaxPerLane || used > 64) return hipErrorInvalidValue;
+    const unsigned g = (unsigned)((rows + 3) / 4);
+    if (E <= 256) moe_route_kernel<4><<<g, 256, 0, s>>>(logits, rows, E, used, ids, weights);
+    else if (E <= 512) moe_route_kernel<8><<<g, 256, 0, s>>>(logits, rows, E, used, ids, weights);
+    else moe_route_kernel<16><<<g, 256, 0, s>>>(logits, rows, E, used, ids, weights);
+    moe_bin_kernel<<<(unsigned)E, 256, 0, s>>>(ids, weights, rows * used, used, counts, arows, aslots, aweights);
     return hipGetLastError();
 }
 
