@@ -86,11 +86,13 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float *__restri
     __shared__ double red[4];
     const float *x = src + blockIdx.x * src_stride;
     double s = 0.0;
+#pragma unroll 8
     for (int c = threadIdx.x; c < cols; c += 256) s += (double)x[c] * (double)x[c];
     s = block_sum256(s, red);
     const float mean = (float)(s / (double)cols);
     const float scale = (float)(1.0 / sqrt((double)(mean + eps)));
     float *y = dst + blockIdx.x * dst_stride;
+#pragma unroll 8
     for (int c = threadIdx.x; c < cols; c += 256) y[c] = __fmul_rn(__fmul_rn(x[c], scale), w[c]);
 }
 

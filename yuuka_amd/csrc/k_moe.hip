@@ -48,8 +48,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 // ---------------------------------------------------------------- router
 // logits[r][e] = W[e] . y[r] (FP32 weights, ffn_gate_inp) and, when `sv` is
 // given, extra[r] = sv . y[r] (ffn_gate_inp_shexp, forward.go:385). One
-// workgroup per expert row (the shared gate vector is row E); its four waves
-// take the rows in turn, two rows per pass so that their loads overlap.
+// workgroup per (expert row, block of 8 rows) (the shared gate vector is
+// row E); each of its four waves takes two rows so that their loads overlap.
 constexpr int kRouterWaves = 4;
 
 __global__ __launch_bounds__(64 * kRouterWaves) void moe_router_kernel(const float *__restrict__ y, int H, int rows,
@@ -60,11 +60,13 @@ __global__ __launch_bounds__(64 * kRouterWaves) void moe_router_kernel(const flo
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int e = blockIdx.x;
     const float *wr = e < E ? w + (uint64_t)e * H : sv;
-    for (int r = wave; r < rows; r += 2 * kRouterWaves) {
-        const int r2 = r + kRouterWaves;
+    {
+        const int r = blockIdx.y * 2 * kRouterWaves + wave, r2 = r + kRouterWaves;
+        if (r >= rows) return;
         const bool two = r2 < rows;
         const float *y0 = y + (uint64_t)r * H, *y1 = y + (uint64_t)(two ? r2 : r) * H;
         float a0 = 0.f, a1 = 0.f;
+#pragma unroll 4
         for (int k = 4 * lane; k < H; k += 256) {
             const float4 wv = *reinterpret_cast<const float4 *>(wr + k);
             const float4 b0 = *reinterpret_cast<const float4 *>(y0 + k);
@@ -493,8 +495,10 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ x,
     const float *er = eo + (uint64_t)r * used * H;
     const float *wr = w + (uint64_t)r * used;
     const float gate = so ? sigmoid_ref(sg[r]) : 0.f;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+    const int i = blockIdx.y * blockDim.x + threadIdx.x;  // grid (rows, H / 256): one element per thread
+    if (i < H) {
         float t = 0.f;
+#pragma unroll 8
         for (int s = 0; s < used; s++) t = t + wr[s] * er[(uint64_t)s * H + i];
         if (so) t = t + gate * so[(uint64_t)r * H + i];
         x[(uint64_t)r * H + i] = x[(uint64_t)r * H + i] + t;
@@ -508,7 +512,8 @@ uint64_t moe_gemm_ws(int act_rows, int K) { return (uint64_t)act_rows * K * 2 + 
 hipError_t launch_moe_router(const float *y, int H, int rows, const float *w, int E, float *logits, const float *sv,
                              float *extra, hipStream_t s) {
     const int n = E + (sv ? 1 : 0);
-    moe_router_kernel<<<n, 64 * kRouterWaves, 0, s>>>(y, H, rows, w, E, logits, sv, extra);
+    moe_router_kernel<<<dim3((unsigned)n, (unsigned)((rows + 2 * kRouterWaves - 1) / (2 * kRouterWaves))),
+                        64 * kRouterWaves, 0, s>>>(y, H, rows, w, E, logits, sv, extra);
     return hipGetLastError();
 }
 
@@ -557,7 +562,7 @@ hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
 
 hipError_t launch_moe_combine(float *x, const float *eo, const float *w, int rows, int used, int H, const float *so,
                               const float *sg, hipStream_t s) {
-    moe_combine_kernel<<<rows, 256, 0, s>>>(x, eo, w, rows, used, H, so, sg);
+    moe_combine_kernel<<<dim3((unsigned)rows, (unsigned)((H + 255) / 256)), 256, 0, s>>>(x, eo, w, rows, used, H, so, sg);
     return hipGetLastError();
 }
 
