@@ -604,9 +604,12 @@ __global__ __launch_bounds__(256) void bg_reduce_kernel(const BgArgs A) {
     const uint64_t idx = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (uint64_t)F.rows * nout) return;
     const int m = (int)(idx / nout), col = (int)(idx % nout);
+    const uint64_t sstride = (uint64_t)F.rows * ncol;
     auto sum = [&](int cc) {
+        const float *p = A.part + (uint64_t)m * ncol + cc;
         float v = 0.f;
-        for (int sp = 0; sp < A.splits; sp++) v += A.part[((uint64_t)sp * F.rows + m) * ncol + cc];
+#pragma unroll 4
+        for (int sp = 0; sp < A.splits; sp++) v += p[sp * sstride];  // split order
         return v;
     };
     if (A.swiglu) {
@@ -626,11 +629,31 @@ __global__ __launch_bounds__(256) void bg_reduce_kernel(const BgArgs A) {
     S.out[o] = v;
 }
 
-// K splits that bring a small launch near two workgroups per CU.
+// K splits for a launch of `wgs` workgroups (one resident per CU: 8 waves
+// of ~250 VGPRs): the split count with the fewest estimated super-block
+// times, rounds of workgroups x (super-blocks per split + one for staging
+// and the epilogue), plus a small cost per split for the reduction.
 int bg_splits(int wgs, int nsb) {
-    int sp = (512 + wgs - 1) / wgs;
-    sp = std::min(sp, std::max(1, nsb / 2));
-    return std::max(1, std::min(sp, 16));
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    int best = 1;
+    double best_t = 1e30;
+    for (int sp = 1; sp <= std::min(16, std::max(1, nsb / 2)); sp++) {
+        const double rounds = (double)((wgs * sp + cus - 1) / cus);
+        const double t = rounds * ((nsb + sp - 1) / sp + 1) + (sp > 1 ? 0.25 * sp : 0.0);
+        if (t < best_t - 1e-9) {
+            best_t = t;
+            best = sp;
+        }
+    }
+    return best;
 }
 
 uint64_t bg_quant_bytes(int rows, int K) {
