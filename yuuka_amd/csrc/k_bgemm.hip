@@ -278,19 +278,6 @@ struct Staged {
     float xs;
 };
 
-__device__ __forceinline__ void stage_load(const BgArgs &A, Staged &st, int m0, int mrows, int sb) {
-    const int K = A.f.K, nsb = K / 256;
-#pragma unroll
-    for (int u = 0; u < 4; u++) {  // piece = (row, sub-block, plane, 16-byte half)
-        const int idx = threadIdx.x + u * kBgThreads;
-        const int r = idx >> 5, j = (idx >> 2) & 7, p = (idx >> 1) & 1, half = idx & 1;
-        st.v[u] = r < mrows ? *reinterpret_cast<const uint4 *>(A.q.planes + (uint64_t)(m0 + r) * K * 2 +
-                                                               (uint64_t)(sb * 8 + j) * 64 + 32 * p + 16 * half)
-                            : make_uint4(0u, 0u, 0u, 0u);
-    }
-    st.xs = threadIdx.x < mrows ? A.q.scales[(uint64_t)(m0 + threadIdx.x) * nsb + sb] : 0.f;
-}
-
 // LDS byte offset of the 8 A bytes of tile t (8 rows, two planes), sub-block
 // j, lane group gg, MFMA row rr: sub-blocks 2 jp and 2 jp + 1 sit side by side,
 // so one 16-byte read gives a lane both halves of a K = 64 operand.
@@ -298,18 +285,33 @@ __device__ __forceinline__ uint32_t la_off(int t, int j, int gg, int rr) {
     return ((uint32_t)(((t * 4 + (j >> 1)) * 4 + gg) * 16 + rr) * 2 + (j & 1)) * 8;
 }
 
+// Thread piece u = ((t * 8 + j) * 2 + half) * 16 + rr (four per thread):
+// bytes [16 half, 16 half + 16) of plane rr >> 3 of row 8 t + (rr & 7),
+// sub-block j: one 16-byte global load (a row's 128 bytes come from 8
+// lanes) and two 8-byte LDS writes for lane groups 2 half and 2 half + 1
+// that cover every bank.
+__device__ __forceinline__ void stage_load(const BgArgs &A, Staged &st, int m0, int mrows, int sb) {
+    const int K = A.f.K, nsb = K / 256;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int u = threadIdx.x + k * kBgThreads;
+        const int rr = u & 15, half = (u >> 4) & 1, j = (u >> 5) & 7, t = u >> 8;
+        const int r = 8 * t + (rr & 7);
+        st.v[k] = r < mrows ? *reinterpret_cast<const uint4 *>(A.q.planes + (uint64_t)(m0 + r) * K * 2 +
+                                                               (uint64_t)(sb * 8 + j) * 64 + 32 * (rr >> 3) + 16 * half)
+                            : make_uint4(0u, 0u, 0u, 0u);
+    }
+    st.xs = threadIdx.x < mrows ? A.q.scales[(uint64_t)(m0 + threadIdx.x) * nsb + sb] : 0.f;
+}
+
 __device__ __forceinline__ void stage_store(const Staged &st, uint8_t *la, float *lxs) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int idx = threadIdx.x + u * kBgThreads;
-        const int r = idx >> 5, j = (idx >> 2) & 7, p = (idx >> 1) & 1, half = idx & 1;
-        const int t = r >> 3, rr = (r & 7) + 8 * p;
+    for (int k = 0; k < 4; k++) {
+        const int u = threadIdx.x + k * kBgThreads;
+        const int rr = u & 15, half = (u >> 4) & 1, j = (u >> 5) & 7, t = u >> 8;
         uint8_t *d0 = la + la_off(t, j, 2 * half, rr);
-        *reinterpret_cast<uint2 *>(d0) = make_uint2(st.v[u].x, st.v[u].y);
-        *reinterpret_cast<uint2 *>(d0 + 256) = make_uint2(st.v[u].z, st.v[u].w);
-    }
-    {
-        const int r = threadIdx.x >> 3, j = threadIdx.x & 7;
+        *reinterpret_cast<uint2 *>(d0) = make_uint2(st.v[k].x, st.v[k].y);
+        *reinterpret_cast<uint2 *>(d0 + 256) = make_uint2(st.v[k].z, st.v[k].w);
     }
     if (threadIdx.x < kBgRows) lxs[threadIdx.x] = st.xs;
 }
