@@ -1069,9 +1069,17 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
         };
         constexpr int kSlot = TT * NA * 256;  // floats of one wave's partial of one tile
         float *myr = red + (size_t)wave * kBalMax * kSlot;
-        Stage sb2[2][TT];
-        if (nmine > 0) issue_item(sb2[0], wave);
-        if (nmine > 1) issue_item(sb2[1], wave + kWaves);
+        // two items in flight per wave (four measured slower: the early
+        // weight traffic delays the activation fetch)
+        constexpr int kD = 2;
+        Stage sbr[kD][TT];
+#ifdef YK_FG_TIMING
+        uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        YK_FG_STAMP(ts[0]);
+#endif
+#pragma unroll
+        for (int d = 0; d < kD; d++)
+            if (nmine > d) issue_item(sbr[d], wave + d * kWaves);
         __builtin_amdgcn_sched_barrier(0);
         for (int idx = lane; idx < cnt * kSlot / 4; idx += 64)
             reinterpret_cast<float4 *>(myr)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1081,6 +1089,9 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
             const float v = lane_inv_rms(A, reinterpret_cast<const float *>(lds + L.nsq), nsb);
             if (lane < 16) my_inv[lane] = v;
         }
+#ifdef YK_FG_TIMING
+        YK_FG_STAMP(ts[1]);
+#endif
         float acc[TT][NA][4];
         zero(acc);
         auto flush = [&](int c) __attribute__((always_inline)) {
@@ -1099,16 +1110,30 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
                 zero(acc);
                 cur = c;
             }
-            if ((q & 1) == 0) {
-                compute_item(sb2[0], sbi, acc);
-                if (q + 2 < nmine) issue_item(sb2[0], ii + 2 * kWaves);
-            } else {
-                compute_item(sb2[1], sbi, acc);
-                if (q + 2 < nmine) issue_item(sb2[1], ii + 2 * kWaves);
+            // stage q % kD holds item q; it is refilled with item q + kD
+            switch (q % kD) {
+#define YK_FG_BAL_CASE(cs)                                                                                         \
+    case cs:                                                                                                       \
+        if constexpr (cs < kD) {                                                                                   \
+            compute_item(sbr[cs], sbi, acc);                                                                       \
+            if (q + kD < nmine) issue_item(sbr[cs], ii + kD * kWaves);                                             \
+        }                                                                                                          \
+        break;
+                YK_FG_BAL_CASE(0)
+                YK_FG_BAL_CASE(1)
+                YK_FG_BAL_CASE(2)
+                YK_FG_BAL_CASE(3)
+#undef YK_FG_BAL_CASE
             }
         }
         if (nmine > 0) flush(cur);
+#ifdef YK_FG_TIMING
+        YK_FG_STAMP(ts[2]);
+#endif
         lds_barrier();
+#ifdef YK_FG_TIMING
+        YK_FG_STAMP(ts[3]);
+#endif
         const int M = A.rows, per_tile = rows_out * M;
         for (int idx = threadIdx.x; idx < cnt * per_tile; idx += kThreads) {
             const int c = idx / per_tile, rem = idx - c * per_tile;
@@ -1146,6 +1171,13 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
                 A.seg[Gr.s].out[o] = v;
             }
         }
+#ifdef YK_FG_TIMING
+        YK_FG_STAMP(ts[4]);
+        if (yk_fg_dbg && lane == 0) {
+            uint64_t *o = yk_fg_dbg + ((size_t)blockIdx.x * kWaves + wave) * 8;
+            for (int e = 0; e < 8; e++) o[e] = ts[e];
+        }
+#endif
         return;
     }
 
