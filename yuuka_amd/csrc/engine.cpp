@@ -31,6 +31,7 @@
 
 #include "fgemm.h"
 #include "internal.h"
+#include "model_kernels.h"
 #include "plan.h"
 
 namespace {
@@ -38,7 +39,7 @@ namespace {
 using yk::fail;
 
 constexpr int kRowBlock = 16;   // rows of one GEMM launch (split path; fused path upper bound)
-constexpr int kAttnRows = 8;    // query rows of one verify-attention launch (MFMA path)
+constexpr int kAttnRows = 8;    // query rows of one verify-attention launch (non-MFMA path)
 
 struct Tensor {
     yuuka_buffer *b = nullptr;
@@ -310,8 +311,14 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
             // one op per block of kAttnRows query rows, every request in it
             // (grid z; request rows R1 apart, tables max_blocks apart)
             const uint32_t packed = (uint32_t)c.rope_dim | ((uint32_t)nreq << 8) | ((uint32_t)R1 << 20);
-            for (uint64_t c0 = 0; c0 < R1; c0 += kAttnRows) {
-                const uint64_t n = std::min<uint64_t>(kAttnRows, R1 - c0), r0 = c0;
+            // the MFMA kernel walks up to 32 rows in one launch (the key chunk
+            // read once); the other kernel takes kAttnRows at a time
+            const uint64_t per = yk::attn_verify_mfma(c.kv_dtype == YUUKA_DTYPE_F16 ? 1 : 0, c.heads, c.kv_heads,
+                                                      (int)hd, c.rope_dim, (int)kvdim)
+                                     ? 32
+                                     : kAttnRows;
+            for (uint64_t c0 = 0; c0 < R1; c0 += per) {
+                const uint64_t n = std::min<uint64_t>(per, R1 - c0), r0 = c0;
                 b.add(YUUKA_EXT_OP_ATTN_VERIFY,
                       {q->q, q->k, q->v, L.kpool, L.vpool, q->attn, q->table, L.q_norm, L.k_norm, q->rope},
                       {(uint64_t)c.kv_heads, (uint64_t)c.heads, hd, kvdim, n, c0},

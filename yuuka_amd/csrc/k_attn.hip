@@ -438,6 +438,36 @@ __device__ __forceinline__ void norm_rope4(const float *__restrict__ src, const 
     }
 }
 
+// norm_rope4 on operands already in registers: x = elements 4l .. 4l + 3,
+// w4 the norm weights, cs the rotation pairs lane l < 16 uses.
+__device__ __forceinline__ void norm_rope_regs(const float4 x, const float4 w4, float eps, const float2 (&cs)[4],
+                                               float (&y)[4]) {
+    const int lane = threadIdx.x & 63;
+    double ss = (double)x.x * (double)x.x;
+    ss += (double)x.y * (double)x.y;
+    ss += (double)x.z * (double)x.z;
+    ss += (double)x.w * (double)x.w;
+    ss = wave_sum_dpp_d(ss);
+    const float mean = (float)(ss / (double)kMD);
+    const float scale = (float)(1.0 / sqrt((double)(mean + eps)));
+    y[0] = __fmul_rn(x.x, __fmul_rn(scale, w4.x));
+    y[1] = __fmul_rn(x.y, __fmul_rn(scale, w4.y));
+    y[2] = __fmul_rn(x.z, __fmul_rn(scale, w4.z));
+    y[3] = __fmul_rn(x.w, __fmul_rn(scale, w4.w));
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) pr[i] = dpp_f<0x128>(y[i]);  // partner lane (l + 8) % 16 of the row
+    if (lane < 16) {
+#pragma clang fp contract(off)  // float32 products and sums rounded separately, as the reference
+        const bool first = lane < 8;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float c = cs[i].x, sn = cs[i].y;
+            y[i] = first ? y[i] * c - pr[i] * sn : pr[i] * sn + y[i] * c;
+        }
+    }
+}
+
 __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
     return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
@@ -468,7 +498,7 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int r16 = lane & 15, g4 = lane >> 4;
     const int R = a.rows;
-    const int G = a.heads / a.kv_heads, nq = G * R;
+    const int G = a.heads / a.kv_heads;
     const int p0 = cur_pos_a(dyn) + a.displacement;  // position of verify row 0
     const int last = p0 + R - 1;
     const int key0 = chunk * kMK;
@@ -511,21 +541,49 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
             for (int e = 0; e < 8; e++) vreg[e] = make_uint4(0, 0, 0, 0);
         }
     }
-    // ---- query rows: normalised, rotated, split into F16 high + remainder
-    for (int vec = wave; vec < nq; vec += 4) {
-        const int gq = vec / R, r = vec % R;
-        float y[4];
-        norm_rope4(q + ((int64_t)r * a.heads + kvh * G + gq) * qstride, q_norm, a.eps, rope + r * half, y);
-        _Float16 hi[4], lo[4];
+    // ---- query rows in blocks of RB verify rows (G * RB <= kMQ MFMA rows):
+    //      normalised, rotated, split into F16 high + remainder. A wave's
+    //      rows are loaded first, then computed (no load waits in the loop).
+    const int RB = kMQ / G;
+    auto prep_q = [&](int r0, int Rb) __attribute__((always_inline)) {
+        constexpr int kQV = kMQ / 4;
+        const int nqb = G * Rb;
+        const float4 w4 = *reinterpret_cast<const float4 *>(q_norm + 4 * lane);
+        float4 xq[kQV];
+        float2 cq[kQV][4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            hi[i] = (_Float16)y[i];
-            lo[i] = (_Float16)(y[i] - (float)hi[i]);
+        for (int t = 0; t < kQV; t++) {
+            const int vec = wave + 4 * t;
+            if (vec < nqb) {
+                const int gq = vec / Rb, r = r0 + vec % Rb;
+                xq[t] = *reinterpret_cast<const float4 *>(q + ((int64_t)r * a.heads + kvh * G + gq) * qstride + 4 * lane);
+                if (lane < 16) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int e = 4 * lane + i;
+                        cq[t][i] = rope[r * half + (lane < 8 ? e : e - 32)];
+                    }
+                }
+            }
         }
-        const uint32_t off = (uint32_t)vec * kMD * 2 + (uint32_t)(((lane >> 1) ^ (vec & 15)) * 16 + (lane & 1) * 8);
-        *reinterpret_cast<uint2 *>(lds + kOffQh + off) = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
-        *reinterpret_cast<uint2 *>(lds + kOffQl + off) = make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
-    }
+#pragma unroll
+        for (int t = 0; t < kQV; t++) {
+            const int vec = wave + 4 * t;
+            if (vec >= nqb) break;
+            float y[4];
+            norm_rope_regs(xq[t], w4, a.eps, cq[t], y);
+            _Float16 hi[4], lo[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                hi[i] = (_Float16)y[i];
+                lo[i] = (_Float16)(y[i] - (float)hi[i]);
+            }
+            const uint32_t off = (uint32_t)vec * kMD * 2 + (uint32_t)(((lane >> 1) ^ (vec & 15)) * 16 + (lane & 1) * 8);
+            *reinterpret_cast<uint2 *>(lds + kOffQh + off) = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
+            *reinterpret_cast<uint2 *>(lds + kOffQl + off) = make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
+        }
+    };
+    prep_q(0, min(RB, R));
     // ---- values of this chunk, transposed (keys past the verify rows: zero)
     {
         uint16_t *vt = reinterpret_cast<uint16_t *>(lds + kOffVt);
@@ -571,6 +629,13 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
     lds_only_barrier();
     YK_AT_STAMP(3);
 
+    for (int r0 = 0; r0 < R; r0 += RB) {
+    const int Rb = min(RB, R - r0), nq = G * Rb;  // this block's verify rows and MFMA rows
+    if (r0) {  // every wave is past the previous block's scores and softmax
+        lds_only_barrier();
+        prep_q(r0, Rb);
+        lds_only_barrier();
+    }
     // ---- scores: wave w owns keys [16w, 16w + 16) for both row tiles
     {
         f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -599,7 +664,7 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int qi = rt * 16 + g4 * 4 + e;
-                if (qi < nq) S[qi * kMK + kk] = p <= p0 + qi % R ? acc[rt][e] * a.scale : -INFINITY;
+                if (qi < nq) S[qi * kMK + kk] = p <= p0 + r0 + qi % Rb ? acc[rt][e] * a.scale : -INFINITY;
             }
     }
     lds_only_barrier();
@@ -617,7 +682,7 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
             *reinterpret_cast<_Float16 *>(lds + kOffPh + off) = hi;
             *reinterpret_cast<_Float16 *>(lds + kOffPl + off) = lo;
             if (lane == 0) {
-                const int gq = qi / R, r = qi % R;
+                const int gq = qi / Rb, r = r0 + qi % Rb;
                 float *rec = part + (((int64_t)chunk * R + r) * a.heads + kvh * G + gq) * (kMD + 2);
                 rec[kMD] = m;
                 rec[kMD + 1] = l;
@@ -664,10 +729,11 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
                 for (int e = 0; e < 4; e++) {
                     const int qi = rt * 16 + g4 * 4 + e;
                     if (qi < nq) {
-                        const int gq = qi / R, r = qi % R, d = wave * 64 + j * 16 + r16;
+                        const int gq = qi / Rb, r = r0 + qi % Rb, d = wave * 64 + j * 16 + r16;
                         part[(((int64_t)chunk * R + r) * a.heads + kvh * G + gq) * (kMD + 2) + d] = o[j][rt][e];
                     }
                 }
+    }
     }
     YK_AT_STAMP(6);
 #ifdef YK_AT_TIMING
@@ -752,9 +818,19 @@ hipError_t launch_rope_table(float2 *tab, int rows, int rot_dim, double base, co
     return hipGetLastError();
 }
 
+// The MFMA kernel serves F16 pools with 256-dim heads and 64-dim rotation;
+// it walks the verify rows in blocks of kMQ / G, so up to 32 rows a launch.
+bool attn_verify_mfma(int fmt, int heads, int kv_heads, int head_dim, int rope_dim, int kv_dim) {
+    return fmt == 1 && head_dim == kMD && rope_dim == 64 && kv_heads > 0 && heads / kv_heads <= kMQ &&
+           kv_dim % 8 == 0 && !getenv("YUUKA_ATTN_FMA");
+}
+
+int attn_verify_max_rows(const AttnVArgs &a) {
+    return attn_verify_mfma((int)a.fmt, a.heads, a.kv_heads, a.head_dim, a.rope_dim, a.kv_dim) ? 32 : 16;
+}
+
 static bool use_mfma_path(const AttnVArgs &a) {
-    return a.fmt == 1 && a.head_dim == kMD && a.rope_dim == 64 && a.heads / a.kv_heads * a.rows <= kMQ &&
-           a.kv_dim % 8 == 0 && !getenv("YUUKA_ATTN_FMA");
+    return attn_verify_mfma((int)a.fmt, a.heads, a.kv_heads, a.head_dim, a.rope_dim, a.kv_dim) && a.rows <= 32;
 }
 
 hipError_t launch_attn_verify(const float *q, const float *k, const float *v, void *kpool, void *vpool,

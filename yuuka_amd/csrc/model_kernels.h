@@ -60,6 +60,10 @@ uint64_t attention_scratch_bytes(const AttnArgs &a);
 int attn_verify_chunk(uint32_t fmt);
 uint64_t attn_verify_scratch_bytes(const AttnVArgs &a);
 uint32_t attn_verify_lds_bytes(const AttnVArgs &a);
+// The MFMA verify-attention kernel applies (F16 pool, 256-dim heads, 64-dim
+// rotation); it serves up to attn_verify_max_rows rows in one launch.
+bool attn_verify_mfma(int fmt, int heads, int kv_heads, int head_dim, int rope_dim, int kv_dim);
+int attn_verify_max_rows(const AttnVArgs &a);
 hipError_t launch_rope_table(float2 *tab, int rows, int rot_dim, double base, const ModelDyn &dyn, int displacement,
                              hipStream_t s, int nreq = 1, int rq_rows = 0);
 hipError_t launch_attn_verify(const float *q, const float *k, const float *v, void *kpool, void *vpool,

@@ -297,13 +297,17 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         bool ok;
         kv_fmt(op.u[2], &ok);
         if (!ok) return fail(YUUKA_ERR_UNSUPPORTED, "KV pool dtype %u (F32 and F16 are served)", op.u[2]);
-        if (a.rows <= 0 || a.rows > 16 || a.heads <= 0 || a.kv_heads <= 0 || a.heads % a.kv_heads ||
+        if (a.rows <= 0 || a.heads <= 0 || a.kv_heads <= 0 || a.heads % a.kv_heads ||
             a.kv_dim != a.kv_heads * a.head_dim || a.block_size <= 0 || a.capacity < a.rows)
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid verify attention dimensions");
+        if (a.rows > attn_verify_max_rows(a))
+            return fail(YUUKA_ERR_UNSUPPORTED, "verify attention: %d rows in one op (at most %d)", a.rows,
+                        attn_verify_max_rows(a));
         if (a.head_dim % 64 || a.head_dim > 256 || a.rope_dim <= 0 || a.rope_dim % 2 || a.rope_dim > a.head_dim ||
             a.rope_dim > 128)
             return fail(YUUKA_ERR_UNSUPPORTED, "attention head dimension %d / rotation %d", a.head_dim, a.rope_dim);
-        if (attn_verify_lds_bytes(a) > 160 * 1024)
+        if (!attn_verify_mfma((int)a.fmt, a.heads, a.kv_heads, a.head_dim, a.rope_dim, a.kv_dim) &&
+            attn_verify_lds_bytes(a) > 160 * 1024)
             return fail(YUUKA_ERR_UNSUPPORTED, "verify attention: %d query rows per kv head do not fit LDS",
                         a.rows * a.heads / a.kv_heads);
         const uint64_t blocks = ((uint64_t)a.capacity + a.block_size - 1) / a.block_size;
