@@ -352,6 +352,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMD = 256;            // head dim
 constexpr int kMK = 64;             // keys per workgroup
 constexpr int kMQ = 32;             // query rows (two 16-row MFMA tiles)
+constexpr int kAW = 8;              // waves of the MFMA kernel
 constexpr int kVt = kMK + 8;        // halves per transposed V row (bank spread)
 constexpr uint32_t kOffK = 0;                               // [64][256] f16, 16-B blocks XOR (key & 15)
 constexpr uint32_t kOffVt = kOffK + kMK * kMD * 2;          // [256][72] f16 (V transposed)
@@ -485,7 +486,7 @@ __device__ __forceinline__ void lds_only_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-__global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__restrict__ q, const float *__restrict__ k,
+__global__ __launch_bounds__(64 * kAW) void attn_verify_mfma_kernel(const float *__restrict__ q, const float *__restrict__ k,
                                                                const float *__restrict__ v, uint16_t *kpool,
                                                                uint16_t *vpool, const int32_t *__restrict__ table,
                                                                const float *__restrict__ q_norm,
@@ -511,12 +512,12 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
     const int qstride = a.gated ? 2 * kMD : kMD;
     const uint32_t base = (uint32_t)(uintptr_t)lds;
 
-    // ---- cached keys: DMA into LDS, wave w copies keys [16w, 16w + 16), two a
+    // ---- cached keys: DMA into LDS, wave w copies keys [8w, 8w + 8), two a
     //      wave instruction; lane (key, block b) fetches block b ^ (key & 15)
     {
-        const int kk0 = wave * 16;
+        const int kk0 = wave * (kMK / kAW);
 #pragma unroll 1
-        for (int i = 0; i < 8; i++) {
+        for (int i = 0; i < kMK / kAW / 2; i++) {
             const int kk = kk0 + 2 * i + (lane >> 5), blk = lane & 31;
             const int p = key0 + kk;
             if (p < p0) {
@@ -526,19 +527,21 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
             }
         }
     }
-    // ---- cached values: wave w loads dims [64w, 64w + 64) of every key
+    // ---- cached values: wave w loads dims [32w, 32w + 32) of every key
     //      (lane = key) and stores them transposed
-    uint4 vreg[8];
+    constexpr int kVE = kMD / kAW / 8;  // 16-byte pieces per lane
+    uint4 vreg[kVE];
     const int vkey = lane, vp = key0 + vkey;
     {
         if (vp < p0) {
             const int64_t slot = (int64_t)table[vp / a.block_size] * a.block_size + vp % a.block_size;
-            const uint4 *src = reinterpret_cast<const uint4 *>(vpool + slot * a.kv_dim + (int64_t)kvh * kMD + wave * 64);
+            const uint4 *src =
+                reinterpret_cast<const uint4 *>(vpool + slot * a.kv_dim + (int64_t)kvh * kMD + wave * (kMD / kAW));
 #pragma unroll
-            for (int e = 0; e < 8; e++) vreg[e] = src[e];
+            for (int e = 0; e < kVE; e++) vreg[e] = src[e];
         } else {
 #pragma unroll
-            for (int e = 0; e < 8; e++) vreg[e] = make_uint4(0, 0, 0, 0);
+            for (int e = 0; e < kVE; e++) vreg[e] = make_uint4(0, 0, 0, 0);
         }
     }
     // ---- query rows in blocks of RB verify rows (G * RB <= kMQ MFMA rows):
@@ -546,14 +549,14 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
     //      rows are loaded first, then computed (no load waits in the loop).
     const int RB = kMQ / G;
     auto prep_q = [&](int r0, int Rb) __attribute__((always_inline)) {
-        constexpr int kQV = kMQ / 4;
+        constexpr int kQV = kMQ / kAW;
         const int nqb = G * Rb;
         const float4 w4 = *reinterpret_cast<const float4 *>(q_norm + 4 * lane);
         float4 xq[kQV];
         float2 cq[kQV][4];
 #pragma unroll
         for (int t = 0; t < kQV; t++) {
-            const int vec = wave + 4 * t;
+            const int vec = wave + kAW * t;
             if (vec < nqb) {
                 const int gq = vec / Rb, r = r0 + vec % Rb;
                 xq[t] = *reinterpret_cast<const float4 *>(q + ((int64_t)r * a.heads + kvh * G + gq) * qstride + 4 * lane);
@@ -568,7 +571,7 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
         }
 #pragma unroll
         for (int t = 0; t < kQV; t++) {
-            const int vec = wave + 4 * t;
+            const int vec = wave + kAW * t;
             if (vec >= nqb) break;
             float y[4];
             norm_rope_regs(xq[t], w4, a.eps, cq[t], y);
@@ -589,18 +592,18 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
         uint16_t *vt = reinterpret_cast<uint16_t *>(lds + kOffVt);
         if (vp < p0 || vp > last) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
+            for (int e = 0; e < kVE; e++) {
                 const uint32_t w4[4] = {vreg[e].x, vreg[e].y, vreg[e].z, vreg[e].w};
 #pragma unroll
                 for (int i = 0; i < 8; i++)
-                    vt[(wave * 64 + e * 8 + i) * kVt + vkey] = (uint16_t)(w4[i >> 1] >> (16 * (i & 1)));
+                    vt[(wave * (kMD / kAW) + e * 8 + i) * kVt + vkey] = (uint16_t)(w4[i >> 1] >> (16 * (i & 1)));
             }
         }
     }
     YK_AT_STAMP(1);
     // ---- the verify rows' own keys and values (rows whose position falls in
     //      this chunk): rounded as the pool stores them, into LDS and the pool
-    for (int r = wave; r < R; r += 4) {
+    for (int r = wave; r < R; r += kAW) {
         const int p = p0 + r;
         if (p < key0 || p >= key0 + kMK) continue;
         const int kk = p - key0;
@@ -636,43 +639,35 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
         prep_q(r0, Rb);
         lds_only_barrier();
     }
-    // ---- scores: wave w owns keys [16w, 16w + 16) for both row tiles
-    {
-        f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        const int kk = wave * 16 + r16;
-        const bool two = nq > 16;
+    // ---- scores: wave w owns keys [16 (w & 3), +16) of row tile w >> 2
+    if (16 * (wave >> 2) < nq) {
+        const int rt = wave >> 2;
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const int kk = (wave & 3) * 16 + r16;
 #pragma unroll
         for (int ks = 0; ks < kMD / 32; ks++) {
             const int blk = ks * 4 + g4;
             const half8 b = *reinterpret_cast<const half8 *>(lds + kOffK + (uint32_t)kk * kMD * 2 + (uint32_t)((blk ^ r16) * 16));
-            const uint32_t qo = (uint32_t)r16 * kMD * 2 + (uint32_t)((blk ^ r16) * 16);
-            const half8 ah0 = *reinterpret_cast<const half8 *>(lds + kOffQh + qo);
-            const half8 al0 = *reinterpret_cast<const half8 *>(lds + kOffQl + qo);
-            acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah0, b, acc[0], 0, 0, 0);
-            acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al0, b, acc[0], 0, 0, 0);
-            if (two) {
-                const half8 ah1 = *reinterpret_cast<const half8 *>(lds + kOffQh + 16 * kMD * 2 + qo);
-                const half8 al1 = *reinterpret_cast<const half8 *>(lds + kOffQl + 16 * kMD * 2 + qo);
-                acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah1, b, acc[1], 0, 0, 0);
-                acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al1, b, acc[1], 0, 0, 0);
-            }
+            const uint32_t qo = (uint32_t)(rt * 16 + r16) * kMD * 2 + (uint32_t)((blk ^ r16) * 16);
+            const half8 ah = *reinterpret_cast<const half8 *>(lds + kOffQh + qo);
+            const half8 al = *reinterpret_cast<const half8 *>(lds + kOffQl + qo);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, acc, 0, 0, 0);
         }
         float *S = reinterpret_cast<float *>(lds + kOffS);
         const int p = key0 + kk;
 #pragma unroll
-        for (int rt = 0; rt < 2; rt++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int qi = rt * 16 + g4 * 4 + e;
-                if (qi < nq) S[qi * kMK + kk] = p <= p0 + r0 + qi % Rb ? acc[rt][e] * a.scale : -INFINITY;
-            }
+        for (int e = 0; e < 4; e++) {
+            const int qi = rt * 16 + g4 * 4 + e;
+            if (qi < nq) S[qi * kMK + kk] = p <= p0 + r0 + qi % Rb ? acc[e] * a.scale : -INFINITY;
+        }
     }
     lds_only_barrier();
     YK_AT_STAMP(4);
     // ---- softmax partials: one wave per query row, lane = key
     {
         const float *S = reinterpret_cast<const float *>(lds + kOffS);
-        for (int qi = wave; qi < nq; qi += 4) {
+        for (int qi = wave; qi < nq; qi += kAW) {
             const float sc = S[qi * kMK + lane];
             const float m = wave_max_dpp_f(sc);
             const float e = (sc == -INFINITY) ? 0.0f : (float)exp((double)(sc - m));
@@ -691,11 +686,12 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
     }
     lds_only_barrier();
     YK_AT_STAMP(5);
-    // ---- value product: wave w owns dims [64w, 64w + 64) (four 16-wide tiles)
+    // ---- value product: wave w owns dims [32w, 32w + 32) (two 16-wide tiles)
     {
-        f32x4 o[4][2];
+        constexpr int kJ = kMD / kAW / 16;
+        f32x4 o[kJ][2];
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < kJ; j++)
 #pragma unroll
             for (int rt = 0; rt < 2; rt++) o[j][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
         const bool two = nq > 16;
@@ -710,8 +706,8 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
                 al[rt] = *reinterpret_cast<const half8 *>(lds + kOffPl + po);
             }
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int dcol = wave * 64 + j * 16 + r16;
+            for (int j = 0; j < kJ; j++) {
+                const int dcol = wave * (kMD / kAW) + j * 16 + r16;
                 const half8 b = *reinterpret_cast<const half8 *>(lds + kOffVt + (uint32_t)dcol * kVt * 2 + (uint32_t)(ks * 32 + g4 * 8) * 2);
                 o[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[0], b, o[j][0], 0, 0, 0);
                 o[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[0], b, o[j][0], 0, 0, 0);
@@ -722,14 +718,14 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
             }
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < kJ; j++)
 #pragma unroll
             for (int rt = 0; rt < 2; rt++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int qi = rt * 16 + g4 * 4 + e;
                     if (qi < nq) {
-                        const int gq = qi / Rb, r = r0 + qi % Rb, d = wave * 64 + j * 16 + r16;
+                        const int gq = qi / Rb, r = r0 + qi % Rb, d = wave * (kMD / kAW) + j * 16 + r16;
                         part[(((int64_t)chunk * R + r) * a.heads + kvh * G + gq) * (kMD + 2) + d] = o[j][rt][e];
                     }
                 }
@@ -738,7 +734,7 @@ __global__ __launch_bounds__(256) void attn_verify_mfma_kernel(const float *__re
     YK_AT_STAMP(6);
 #ifdef YK_AT_TIMING
     if (yk_at_dbg && lane == 0) {
-        uint64_t *o = yk_at_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave) * 8;
+        uint64_t *o = yk_at_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * kAW + wave) * 8;
         for (int e = 0; e < 8; e++) o[e] = ts[e];
     }
 #endif
@@ -850,7 +846,7 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
             attr2 = true;
         }
-        attn_verify_mfma_kernel<<<dim3((unsigned)launch_chunks, (unsigned)a.kv_heads, nz), 256, kMfmaLds, s>>>(
+        attn_verify_mfma_kernel<<<dim3((unsigned)launch_chunks, (unsigned)a.kv_heads, nz), 64 * kAW, kMfmaLds, s>>>(
             q, k, v, static_cast<uint16_t *>(kpool), static_cast<uint16_t *>(vpool), table, q_norm, k_norm, rope, a,
             part, dyn);
     } else if (a.fmt == 1) {
