@@ -354,14 +354,12 @@ constexpr int kMK = 64;             // keys per workgroup
 constexpr int kMQ = 32;             // query rows (two 16-row MFMA tiles)
 constexpr int kAW = 8;              // waves of the MFMA kernel
 constexpr int kVt = kMK + 8;        // halves per transposed V row (bank spread)
-constexpr uint32_t kOffK = 0;                               // [64][256] f16, 16-B blocks XOR (key & 15)
-constexpr uint32_t kOffVt = kOffK + kMK * kMD * 2;          // [256][72] f16 (V transposed)
+constexpr uint32_t kOffVt = 0;                              // [256][72] f16 (V transposed)
 constexpr uint32_t kOffQh = kOffVt + kMD * kVt * 2;         // [32][256] f16, blocks XOR (row & 15)
 constexpr uint32_t kOffQl = kOffQh + kMQ * kMD * 2;
-constexpr uint32_t kOffS = kOffQl + kMQ * kMD * 2;          // [32][64] f32
-constexpr uint32_t kOffPh = kOffS + kMQ * kMK * 4;          // [32][64] f16, blocks XOR (row & 7)
-constexpr uint32_t kOffPl = kOffPh + kMQ * kMK * 2;
-constexpr uint32_t kMfmaLds = kOffPl + kMQ * kMK * 2;
+constexpr uint32_t kOffS = kOffQl + kMQ * kMD * 2;          // [32][64] f32 scores, then P in place:
+                                                            // [32][2: high, low][64] f16, blocks XOR (row & 7)
+constexpr uint32_t kMfmaLds = kOffS + kMQ * kMK * 4;        // 76 KB: two workgroups per CU
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
@@ -486,7 +484,7 @@ __device__ __forceinline__ void lds_only_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-__global__ __launch_bounds__(64 * kAW) void attn_verify_mfma_kernel(const float *__restrict__ q, const float *__restrict__ k,
+__global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) void attn_verify_mfma_kernel(const float *__restrict__ q, const float *__restrict__ k,
                                                                const float *__restrict__ v, uint16_t *kpool,
                                                                uint16_t *vpool, const int32_t *__restrict__ table,
                                                                const float *__restrict__ q_norm,
@@ -512,21 +510,27 @@ __global__ __launch_bounds__(64 * kAW) void attn_verify_mfma_kernel(const float 
     const int qstride = a.gated ? 2 * kMD : kMD;
     const uint32_t base = (uint32_t)(uintptr_t)lds;
 
-    // ---- cached keys: DMA into LDS, wave w copies keys [8w, 8w + 8), two a
-    //      wave instruction; lane (key, block b) fetches block b ^ (key & 15)
-    {
-        const int kk0 = wave * (kMK / kAW);
-#pragma unroll 1
-        for (int i = 0; i < kMK / kAW / 2; i++) {
-            const int kk = kk0 + 2 * i + (lane >> 5), blk = lane & 31;
-            const int p = key0 + kk;
-            if (p < p0) {
-                const int64_t slot = (int64_t)table[p / a.block_size] * a.block_size + p % a.block_size;
-                const uint16_t *src = kpool + slot * a.kv_dim + (int64_t)kvh * kMD + (blk ^ (kk & 15)) * 8;
-                lds_copy16_at(src, base + kOffK + (uint32_t)(kk0 + 2 * i) * kMD * 2);
-            }
+    // ---- cached keys straight into MFMA B order: the scores lane (key kk,
+    //      group g4) holds dims [32 ks + 8 g4, +8) of key kk for every ks.
+    //      Keys at or past p0 (this step's rows) are read after they are
+    //      written below.
+    const int kk_s = (wave & 3) * 16 + r16;
+    const bool scorer = 16 * (wave >> 2) < G * min(kMQ / G, R);  // row tile of this wave in use
+    half8 kreg[kMD / 32];
+    auto load_keys = [&](bool fresh) __attribute__((always_inline)) {
+        const int p = key0 + kk_s;
+        const bool want = scorer && (fresh ? (p >= p0 && p <= last) : p < p0);
+        if (want) {
+            const int64_t slot = (int64_t)table[p / a.block_size] * a.block_size + p % a.block_size;
+            const half8 *src = reinterpret_cast<const half8 *>(kpool + slot * a.kv_dim + (int64_t)kvh * kMD + g4 * 8);
+#pragma unroll
+            for (int ks = 0; ks < kMD / 32; ks++) kreg[ks] = src[4 * ks];
+        } else if (!fresh) {
+#pragma unroll
+            for (int ks = 0; ks < kMD / 32; ks++) kreg[ks] = half8{};
         }
-    }
+    };
+    load_keys(false);
     // ---- cached values: wave w loads dims [32w, 32w + 32) of every key
     //      (lane = key) and stores them transposed
     constexpr int kVE = kMD / kAW / 8;  // 16-byte pieces per lane
@@ -553,28 +557,29 @@ __global__ __launch_bounds__(64 * kAW) void attn_verify_mfma_kernel(const float 
         const int nqb = G * Rb;
         const float4 w4 = *reinterpret_cast<const float4 *>(q_norm + 4 * lane);
         float4 xq[kQV];
-        float2 cq[kQV][4];
 #pragma unroll
         for (int t = 0; t < kQV; t++) {
             const int vec = wave + kAW * t;
             if (vec < nqb) {
                 const int gq = vec / Rb, r = r0 + vec % Rb;
                 xq[t] = *reinterpret_cast<const float4 *>(q + ((int64_t)r * a.heads + kvh * G + gq) * qstride + 4 * lane);
-                if (lane < 16) {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const int e = 4 * lane + i;
-                        cq[t][i] = rope[r * half + (lane < 8 ? e : e - 32)];
-                    }
-                }
             }
         }
 #pragma unroll
         for (int t = 0; t < kQV; t++) {
             const int vec = wave + kAW * t;
             if (vec >= nqb) break;
+            const int r = r0 + vec % Rb;
+            float2 cq[4] = {};
+            if (lane < 16) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int e = 4 * lane + i;
+                    cq[i] = rope[r * half + (lane < 8 ? e : e - 32)];
+                }
+            }
             float y[4];
-            norm_rope_regs(xq[t], w4, a.eps, cq[t], y);
+            norm_rope_regs(xq[t], w4, a.eps, cq, y);
             _Float16 hi[4], lo[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -586,7 +591,6 @@ __global__ __launch_bounds__(64 * kAW) void attn_verify_mfma_kernel(const float 
             *reinterpret_cast<uint2 *>(lds + kOffQl + off) = make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
         }
     };
-    prep_q(0, min(RB, R));
     // ---- values of this chunk, transposed (keys past the verify rows: zero)
     {
         uint16_t *vt = reinterpret_cast<uint16_t *>(lds + kOffVt);
@@ -600,9 +604,11 @@ __global__ __launch_bounds__(64 * kAW) void attn_verify_mfma_kernel(const float 
             }
         }
     }
+    prep_q(0, min(RB, R));
     YK_AT_STAMP(1);
     // ---- the verify rows' own keys and values (rows whose position falls in
-    //      this chunk): rounded as the pool stores them, into LDS and the pool
+    //      this chunk): rounded as the pool stores them, into the pool (keys)
+    //      and LDS (values)
     for (int r = wave; r < R; r += kAW) {
         const int p = p0 + r;
         if (p < key0 || p >= key0 + kMK) continue;
@@ -622,14 +628,17 @@ __global__ __launch_bounds__(64 * kAW) void attn_verify_mfma_kernel(const float 
         const uint2 vw = make_uint2((uint32_t)vq[0] | ((uint32_t)vq[1] << 16), (uint32_t)vq[2] | ((uint32_t)vq[3] << 16));
         *reinterpret_cast<uint2 *>(kpool + slot * a.kv_dim + (int64_t)kvh * kMD + 4 * lane) = kw;
         *reinterpret_cast<uint2 *>(vpool + slot * a.kv_dim + (int64_t)kvh * kMD + 4 * lane) = vw;
-        *reinterpret_cast<uint2 *>(lds + kOffK + (uint32_t)kk * kMD * 2 + (uint32_t)(((lane >> 1) ^ (kk & 15)) * 16 + (lane & 1) * 8)) = kw;
         uint16_t *vt = reinterpret_cast<uint16_t *>(lds + kOffVt);
 #pragma unroll
         for (int i = 0; i < 4; i++) vt[(4 * lane + i) * kVt + kk] = vq[i];
     }
     YK_AT_STAMP(2);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's key copies have landed
-    lds_only_barrier();
+    if (key0 + kMK - 1 >= p0) {
+        __syncthreads();  // the new keys are in the pool (global and LDS fence)
+        load_keys(true);
+    } else {
+        lds_only_barrier();
+    }
     YK_AT_STAMP(3);
 
     for (int r0 = 0; r0 < R; r0 += RB) {
@@ -647,7 +656,7 @@ __global__ __launch_bounds__(64 * kAW) void attn_verify_mfma_kernel(const float 
 #pragma unroll
         for (int ks = 0; ks < kMD / 32; ks++) {
             const int blk = ks * 4 + g4;
-            const half8 b = *reinterpret_cast<const half8 *>(lds + kOffK + (uint32_t)kk * kMD * 2 + (uint32_t)((blk ^ r16) * 16));
+            const half8 b = kreg[ks];
             const uint32_t qo = (uint32_t)(rt * 16 + r16) * kMD * 2 + (uint32_t)((blk ^ r16) * 16);
             const half8 ah = *reinterpret_cast<const half8 *>(lds + kOffQh + qo);
             const half8 al = *reinterpret_cast<const half8 *>(lds + kOffQl + qo);
@@ -673,9 +682,10 @@ __global__ __launch_bounds__(64 * kAW) void attn_verify_mfma_kernel(const float 
             const float e = (sc == -INFINITY) ? 0.0f : (float)exp((double)(sc - m));
             const float l = wave_sum_dpp_f(e);
             const _Float16 hi = (_Float16)e, lo = (_Float16)(e - (float)hi);
-            const uint32_t off = (uint32_t)qi * kMK * 2 + (uint32_t)((((lane >> 3) ^ (qi & 7)) * 16) + (lane & 7) * 2);
-            *reinterpret_cast<_Float16 *>(lds + kOffPh + off) = hi;
-            *reinterpret_cast<_Float16 *>(lds + kOffPl + off) = lo;
+            // P replaces the row's scores: high halves in bytes [0, 128), low in [128, 256)
+            const uint32_t off = (uint32_t)qi * kMK * 4 + (uint32_t)((((lane >> 3) ^ (qi & 7)) * 16) + (lane & 7) * 2);
+            *reinterpret_cast<_Float16 *>(lds + kOffS + off) = hi;
+            *reinterpret_cast<_Float16 *>(lds + kOffS + kMK * 2 + off) = lo;
             if (lane == 0) {
                 const int gq = qi / Rb, r = r0 + qi % Rb;
                 float *rec = part + (((int64_t)chunk * R + r) * a.heads + kvh * G + gq) * (kMD + 2);
@@ -701,9 +711,9 @@ __global__ __launch_bounds__(64 * kAW) void attn_verify_mfma_kernel(const float 
             half8 ah[2], al[2];
 #pragma unroll
             for (int rt = 0; rt < 2; rt++) {
-                const uint32_t po = (uint32_t)(rt * 16 + r16) * kMK * 2 + (uint32_t)((blk ^ (r16 & 7)) * 16);
-                ah[rt] = *reinterpret_cast<const half8 *>(lds + kOffPh + po);
-                al[rt] = *reinterpret_cast<const half8 *>(lds + kOffPl + po);
+                const uint32_t po = (uint32_t)(rt * 16 + r16) * kMK * 4 + (uint32_t)((blk ^ (r16 & 7)) * 16);
+                ah[rt] = *reinterpret_cast<const half8 *>(lds + kOffS + po);
+                al[rt] = *reinterpret_cast<const half8 *>(lds + kOffS + kMK * 2 + po);
             }
 #pragma unroll
             for (int j = 0; j < kJ; j++) {
@@ -775,11 +785,13 @@ __global__ __launch_bounds__(256) void attn_merge_v_kernel(const float *__restri
     }
     __syncthreads();
     float lsum = 0.0f;
+#pragma unroll 8
     for (int c = 0; c < nchunk; c++) lsum += rec_of(c)[D + 1] * wsh[c];
     const float inv = 1.0f / lsum;
     const int qstride = a.gated ? 2 * D : D;
     for (int d = threadIdx.x; d < D; d += 256) {
         float acc = 0.0f;
+#pragma unroll 8
         for (int c = 0; c < nchunk; c++) acc += rec_of(c)[d] * wsh[c];
         float o = acc * inv;
         if (a.gated) o *= sigmoid_ref(q[((int64_t)r * a.heads + h) * qstride + D + d]);
