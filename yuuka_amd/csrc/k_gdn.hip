@@ -304,6 +304,28 @@ __device__ __forceinline__ void conv_channel2(const float *conv_state, const flo
 #pragma unroll
         for (int r = 0; r < RC; r++) x[u][r] = r < R ? qkv[(uint64_t)r * g.conv_dim + cc[u]] : 0.0f;
     }
+    if (K == 4) {  // the models' conv width: every index below is a compile-time constant
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            if (u == 1 && c1 < 0) break;
+            float *dst = u == 0 ? dst0 : dst1;
+            const int stride = u == 0 ? stride0 : stride1;
+#pragma unroll
+            for (int r = 0; r < RC; r++) {
+                if (r >= R) break;
+                float sum = 0.0f;
+#pragma unroll
+                for (int tt = 0; tt < 3; tt++) {
+                    const int idx = r + tt - 3;
+                    const float xv = idx >= 0 ? x[u][idx >= 0 ? idx : 0] : st[u][idx >= 0 ? 0 : 3 + idx];
+                    sum = __fadd_rn(sum, __fmul_rn(w[u][tt], xv));
+                }
+                sum = __fadd_rn(sum, __fmul_rn(w[u][3], x[u][r]));
+                dst[r * stride] = silu_ref(sum);
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         if (u == 1 && c1 < 0) break;
