@@ -164,9 +164,8 @@ struct BgArgs {
     float *part;                  // [splits][rows][cols[nseg]]
 };
 
-// 24-bit multiply-add (full rate; a 32-bit multiply is quarter rate). Every
-// product here fits: MFMA sub-block results |r| < 2^17, scales <= 63,
-// sub-block sums |S| < 2^21.
+// 24-bit multiply-add (full rate; a 32-bit multiply is quarter rate). Used
+// for the Q6_K digit recombination 49 a2 + 7 a1 + a0, where |a| < 2^22.
 __device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
 
 typedef __attribute__((ext_vector_type(2))) unsigned short u16x2;

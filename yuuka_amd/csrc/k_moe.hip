@@ -3,22 +3,23 @@
 // reference's MoE plan ops (backend/hip/bridge/yuuka_hip.h:457-470).
 //
 //  * router:   FP32 router logits (and the shared-expert gate logit) of the
-//              verify rows, one wave per expert row.
+//              verify rows, one workgroup per (expert row, 8 rows).
 //  * route:    top-`used` experts per row by repeated argmax (lower index
-//              wins ties), softmax over the selected logits, and binning of
-//              the (row, slot) assignments by expert. One workgroup; the
-//              bins are filled in (row, slot) order by one thread per
-//              expert, so they are deterministic and every count is written
-//              (no memset, graph-safe).
+//              wins ties) and softmax over the selected logits, one wave per
+//              row; then binning of the (row, slot) assignments by expert,
+//              one workgroup per expert, in (row, slot) order, so the bins
+//              are deterministic and every count is written (no memset,
+//              graph-safe).
 //  * grouped GEMM: one launch over every expert's assigned rows. Workgroups
 //              are (expert, part); a workgroup with no assignments exits.
-//              The assigned rows are quantized into LDS once per workgroup
-//              (int16 split into two int8 planes, one scale per row and
-//              256-element super-block, exact sub-block sums for the Q4_K
-//              min term) and multiplied with v_mfma_i32_16x16x32_i8 against
-//              Q4_K weights decoded from HBM straight into MFMA operand
-//              order. Eight assignments fill the high-plane half of one MFMA
-//              tile and their low planes the other half.
+//              The activation rows are quantized once per launch (int16
+//              split into two int8 planes, one scale per row and
+//              256-element super-block), staged in LDS per chunk of eight
+//              assignments, and multiplied with v_mfma_i32_16x16x64_i8
+//              against Q4_K weights decoded from HBM straight into MFMA
+//              operand order, the sub-block scale and min in the B operands.
+//              Eight assignments fill the high-plane half of one MFMA tile
+//              and their low planes the other half.
 //  * reduce / combine: weighted sum of the slots (and the sigmoid-gated
 //              shared expert) into the residual stream, in the reference's
 //              order of float32 operations.
@@ -256,7 +257,6 @@ __global__ __launch_bounds__(256) void moe_bin_kernel(const int32_t *__restrict_
 // ---------------------------------------------------------------- grouped GEMM
 // Activation rows quantized once per launch into scratch (moe_quant_kernel):
 //   planes [rows][K/32 sub-blocks][2: high, low][32 B]
-//   sums   [rows][K/32]   int32 sums of q per sub-block (Q4_K min term)
 //   scales [rows][K/256]  float (x ~= scale * q, q = 256 h + l)
 struct MoeQuant {
     int8_t *planes;
