@@ -277,9 +277,69 @@ __device__ int select_id(const float *p, int V, SelShared &s, uint32_t key, Cut 
     return id;
 }
 
+// First top-p digit of one chunk of a row: counts and weights of the
+// elements inside the top-k cut by the top byte of their order key. One
+// workgroup per (chunk, row, request), so the float64 exponentials of the
+// whole vocabulary spread over the GPU; the select kernel adds the chunks in
+// chunk order (deterministic).
+struct Hist0 {
+    uint32_t c[256];
+    double w[256];
+};
+
+__global__ __launch_bounds__(256) void accept_hist_kernel(const float *__restrict__ logits, Geo g,
+                                                          const Stat *__restrict__ stats,
+                                                          const Cut *__restrict__ cuts, double t,
+                                                          Hist0 *__restrict__ out) {
+    const int c = blockIdx.x, row = blockIdx.y, b = blockIdx.z;
+    const int wave = threadIdx.x >> 6;
+    const float *p = row_ptr(logits, g, b, row);
+    __shared__ float mx_s;
+    __shared__ uint32_t cnt[4][256];
+    __shared__ double ws[4][256];
+    for (int i = threadIdx.x; i < 4 * 256; i += 256) {
+        (&cnt[0][0])[i] = 0u;
+        (&ws[0][0])[i] = 0.0;
+    }
+    if (threadIdx.x < 64) {  // wave 0 reduces the row's chunk maxima
+        const Stat *st = stats + ((uint64_t)b * g.R + row) * g.C;
+        float bv = -INFINITY;
+        int bi = INT_MAX;
+        for (int cc = threadIdx.x; cc < g.C; cc += 64)
+            if (beats(st[cc].v, st[cc].i, bv, bi)) { bv = st[cc].v; bi = st[cc].i; }
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+        }
+        if (threadIdx.x == 0) mx_s = bv;
+    }
+    __syncthreads();
+    const float mx = mx_s;
+    const Cut cut = row_cut(cuts, g, b, row);
+    const int begin = c * g.L, end = min(begin + g.L, g.V);
+    for (int j = begin + threadIdx.x; j < end; j += 256) {
+        const float l = p[j];
+        if (!valid_logit(l)) continue;
+        const uint32_t k = order_key(l);
+        if (!in_cut(k, j, cut)) continue;
+        atomicAdd(&cnt[wave][k >> 24], 1u);
+        unsafeAtomicAdd(&ws[wave][k >> 24], exp((double)(l - mx) / t));
+    }
+    __syncthreads();
+    Hist0 &o = out[((uint64_t)b * g.R + row) * g.C + c];
+    const int q = threadIdx.x;
+    o.c[q] = cnt[0][q] + cnt[1][q] + cnt[2][q] + cnt[3][q];
+    o.w[q] = ((ws[0][q] + ws[1][q]) + ws[2][q]) + ws[3][q];
+}
+
+// mode 0: top-k then top-p in one launch; 1: top-k only; 2: top-p only, the
+// top-k cut (top_k > 0) read from `cuts` and the first digit's histogram
+// summed from accept_hist_kernel's chunks.
 __global__ __launch_bounds__(1024) void accept_select_kernel(const float *__restrict__ logits, Geo g,
                                                              const Stat *__restrict__ stats, int top_k,
-                                                             float top_p, double t, Cut *__restrict__ cuts) {
+                                                             float top_p, double t, Cut *__restrict__ cuts,
+                                                             int mode, const Hist0 *__restrict__ h0) {
     const int row = blockIdx.x, b = blockIdx.y;
     const float *p = row_ptr(logits, g, b, row);
     __shared__ SelShared s;
@@ -299,9 +359,10 @@ __global__ __launch_bounds__(1024) void accept_select_kernel(const float *__rest
     __syncthreads();
     const float mx = s.mx;
     Cut cut{0u, INT_MAX};
+    if (mode == 2 && top_k > 0) cut = cuts[(uint64_t)b * g.R + row];
 
     // top-k: the top_k-th element in (logit desc, id asc) order (sampling.go:90-92).
-    if (top_k > 0) {
+    if (top_k > 0 && mode != 2) {
         if (threadIdx.x == 0) {
             s.prefix = 0u;
             s.before_c = 0u;
@@ -342,7 +403,7 @@ __global__ __launch_bounds__(1024) void accept_select_kernel(const float *__rest
 
     // top-p: the smallest prefix whose cumulative share reaches top_p
     // (sampling.go:104-113), within the top-k set.
-    if (top_p > 0.0f && top_p < 1.0f) {
+    if (top_p > 0.0f && top_p < 1.0f && mode != 1) {
         __syncthreads();
         if (threadIdx.x == 0) {
             s.prefix = 0u;
@@ -356,13 +417,28 @@ __global__ __launch_bounds__(1024) void accept_select_kernel(const float *__rest
             const uint32_t mask = pass ? ~0u << (shift + 8) : 0u;
             const uint32_t pre = s.prefix;
             const Cut ck = cut;
-            hist_pass<true>(
-                p, g.V, mx, t, s,
-                [=](float l, int j) {
-                    const uint32_t k = order_key(l);
-                    return in_cut(k, j, ck) && (k & mask) == pre;
-                },
-                [=](float l, int) { return (order_key(l) >> shift) & 255u; });
+            if (pass == 0 && h0) {  // chunk histograms, added in chunk order
+                if (threadIdx.x < 256) {
+                    const Hist0 *hr = h0 + ((uint64_t)b * g.R + row) * g.C;
+                    uint32_t cc = 0u;
+                    double w = 0.0;
+                    for (int ch = 0; ch < g.C; ch++) {
+                        cc += hr[ch].c[threadIdx.x];
+                        w += hr[ch].w[threadIdx.x];
+                    }
+                    s.tc[threadIdx.x] = cc;
+                    s.tw[threadIdx.x] = w;
+                }
+                __syncthreads();
+            } else {
+                hist_pass<true>(
+                    p, g.V, mx, t, s,
+                    [=](float l, int j) {
+                        const uint32_t k = order_key(l);
+                        return in_cut(k, j, ck) && (k & mask) == pre;
+                    },
+                    [=](float l, int) { return (order_key(l) >> shift) & 255u; });
+            }
             if (threadIdx.x == 0) {
                 if (pass == 0) {
                     double w = 0.0;
@@ -656,7 +732,8 @@ Geo make_geo(const yuuka_accept_params &p) {
 uint64_t accept_scratch_bytes(const yuuka_accept_params &p) {
     const Geo g = make_geo(p);
     const uint64_t n = (uint64_t)g.B * g.R * g.C;
-    return n * sizeof(Stat) + n * sizeof(double) + (uint64_t)g.B * g.R * (sizeof(double) + sizeof(Cut)) + 256;
+    return ((n * sizeof(Stat) + 255) & ~255ull) + n * sizeof(double) +
+           (uint64_t)g.B * g.R * (sizeof(double) + sizeof(Cut)) + 256 + n * sizeof(Hist0);
 }
 
 hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int32_t *result,
@@ -671,6 +748,8 @@ hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int3
     double *sums = reinterpret_cast<double *>(base + ((n * sizeof(Stat) + 255) & ~255ull));
     double *wdraft = sums + n;
     Cut *cuts = reinterpret_cast<Cut *>(wdraft + (uint64_t)g.B * g.R);
+    Hist0 *h0 = reinterpret_cast<Hist0 *>(
+        (reinterpret_cast<uintptr_t>(cuts + (uint64_t)g.B * g.R) + 255) & ~(uintptr_t)255);
     const bool stochastic = p.mode == YUUKA_ACCEPT_STOCHASTIC && p.temperature > 0.0f && p.top_k != 1;
     const double t = stochastic ? (double)p.temperature : 1.0;
     // top_p 0 means off (sampling.go:46-48); top_k at or above the vocabulary keeps everything.
@@ -679,9 +758,18 @@ hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int3
     const bool truncate = stochastic && (top_k_on || top_p_on);
     const dim3 grid((unsigned)g.C, (unsigned)g.R, (unsigned)g.B);
     accept_stats_kernel<<<grid, 256, 0, stream>>>(logits, g, stats);
-    if (truncate)
-        accept_select_kernel<<<dim3((unsigned)g.R, (unsigned)g.B), kSelWaves * 64, 0, stream>>>(
-            logits, g, stats, top_k_on ? (int)p.top_k : 0, top_p_on ? p.top_p : 1.0f, t, cuts);
+    const dim3 sel((unsigned)g.R, (unsigned)g.B);
+    const int tk = top_k_on ? (int)p.top_k : 0;
+    if (truncate && !top_p_on) {
+        accept_select_kernel<<<sel, kSelWaves * 64, 0, stream>>>(logits, g, stats, tk, 1.0f, t, cuts, 0, nullptr);
+    } else if (truncate) {
+        // top-k cut, then the first top-p digit over all chunks in parallel,
+        // then the remaining top-p digits per row
+        if (top_k_on)
+            accept_select_kernel<<<sel, kSelWaves * 64, 0, stream>>>(logits, g, stats, tk, 1.0f, t, cuts, 1, nullptr);
+        accept_hist_kernel<<<grid, 256, 0, stream>>>(logits, g, stats, top_k_on ? cuts : nullptr, t, h0);
+        accept_select_kernel<<<sel, kSelWaves * 64, 0, stream>>>(logits, g, stats, tk, p.top_p, t, cuts, 2, h0);
+    }
     const Cut *cut_arg = truncate ? cuts : nullptr;
     if (stochastic)
         accept_weights_kernel<<<grid, 256, 0, stream>>>(logits, g, drafts, stats, cut_arg, t, sums, wdraft);
