@@ -341,13 +341,14 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s1, uint32_t s2, ui
 }
 
 // Workgroup (expert e, part): tiles [t0, t0 + tpw) of 16 output channels.
-// Per chunk of up to eight assignments, the (tile, super-block) items are
-// dealt to the waves; each item's partial sums go to LDS and are added in
-// super-block order at the end (deterministic). Lane (c, g) of an item
-// loads channel c's Q4_K bytes straight into MFMA B order and the
-// activation planes of assignment c & 7 (high plane for c < 8) into A order.
+// Per chunk of up to eight assignments, each wave walks its (tile, matrix)
+// pairs through the super-blocks in order (sums in registers, the next
+// item's weights in flight; deterministic), one result per pair to LDS for
+// the epilogue. Lane (c, g) of an item loads channel c's Q4_K bytes straight
+// into MFMA B order and the activation planes of assignment c & 7 (high
+// plane for c < 8) into A order.
 __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))) void moe_gemm_kernel(MoeGemmArgs A) {
-    // LDS: partial sums [tpw][nsb][mats][8 rows][16 ch] floats, then the
+    // LDS: results [tpw][mats][8 rows][16 ch] floats, then the
     // chunk's activations: planes [K/64][16 r][4 g][2][8 B] (r < 8 high
     // plane of assignment r, r >= 8 low plane of assignment r - 8), scales
     // [K/256][8] float.
@@ -363,7 +364,7 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
     const bool dual = A.w1 != nullptr;
     const int mats = dual ? 2 : 1;
     __shared__ int s_row[kChunk], s_out[kChunk];
-    uint8_t *la = reinterpret_cast<uint8_t *>(part + (uint64_t)A.tpw * nsb * mats * 128);
+    uint8_t *la = reinterpret_cast<uint8_t *>(part + (uint64_t)A.tpw * mats * 128);
     float *lxs = reinterpret_cast<float *>(la + (uint64_t)nsub * 16 * 32);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = lane & 15, g = lane >> 4;
@@ -400,75 +401,88 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
         for (int idx = threadIdx.x; idx < nsb * 8; idx += kMoeThreads)
             lxs[idx] = A.xq.scales[(uint64_t)s_row[idx & 7] * nsb + (idx >> 3)];
         __syncthreads();
-        // items (tile, matrix, super-block), two per wave per pass: both
-        // items' weight loads are issued before either is multiplied
-        const int items = ntl * mats * nsb;
-        for (int it0 = 2 * wave; it0 < items; it0 += 2 * kMoeWaves) {
-            uint4 hdr[2];
-            uint64_t qv[2][4];
-            int sbs[2], slot[2];
+        // items (tile, matrix, super-block): wave w walks the pairs (tile,
+        // matrix) w, w + 8, ... through their super-blocks in order with the
+        // next item's weights in flight, sums in registers in super-block
+        // order, one result per pair to LDS
+        const int pairs = ntl * mats;
+        const int npw = wave < pairs ? (pairs - wave + kMoeWaves - 1) / kMoeWaves : 0;
+        const int total = npw * nsb;
+        const int rbase = 4 * (g & 1);
+        auto load_item = [&](int q, uint4 &H, uint64_t (&Q)[4]) __attribute__((always_inline)) {
+            const int tm = wave + kMoeWaves * (q / nsb), sb = q % nsb, m = tm % mats, tl = tm / mats;
+            const uint8_t *blk = (m ? A.w1 : A.w0) + ((uint64_t)e * A.N + (t0 + tl) * 16 + c) * A.row_bytes +
+                                 (uint64_t)sb * 144;
+            H = *reinterpret_cast<const uint4 *>(blk);
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const int it = min(it0 + u, items - 1);
-                const int sb = it % nsb, tm = it / nsb, m = tm % mats, tl = tm / mats;
-                sbs[u] = sb;
-                slot[u] = (tl * nsb + sb) * mats + m;
-                const uint8_t *blk = (m ? A.w1 : A.w0) + ((uint64_t)e * A.N + (t0 + tl) * 16 + c) * A.row_bytes +
-                                     (uint64_t)sb * 144;
-                hdr[u] = *reinterpret_cast<const uint4 *>(blk);
+            for (int p = 0; p < 4; p++) Q[p] = *reinterpret_cast<const uint64_t *>(blk + 16 + 32 * p + 8 * g);
+        };
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        auto compute_item = [&](int q, const uint4 &H, const uint64_t (&Q)[4]) __attribute__((always_inline)) {
+            const int sb = q % nsb;
+            const float4 xs4 = *reinterpret_cast<const float4 *>(lxs + sb * 8 + rbase);
+            const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+            // sub-block scale (two 3-bit digits) and min in the B operands
+            // of three K = 64 MFMAs per pair of sub-blocks: exact int32
+            i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
 #pragma unroll
-                for (int p = 0; p < 4; p++) qv[u][p] = *reinterpret_cast<const uint64_t *>(blk + 16 + 32 * p + 8 * g);
+            for (int jp = 0; jp < 4; jp++) {
+                const uint64_t raw = Q[jp];
+                const uint64_t qe = raw & 0x0F0F0F0F0F0F0F0Full, qo = (raw >> 4) & 0x0F0F0F0F0F0F0F0Full;
+                int sce, mne, sco, mno;
+                scale_min_k4(2 * jp, H.y, H.z, H.w, &sce, &mne);
+                scale_min_k4(2 * jp + 1, H.y, H.z, H.w, &sco, &mno);
+                const uint32_t qw[4] = {(uint32_t)qe, (uint32_t)(qe >> 32), (uint32_t)qo, (uint32_t)(qo >> 32)};
+                const uint32_t lo[2] = {(uint32_t)(sce & 7), (uint32_t)(sco & 7)};
+                const uint32_t hi[2] = {(uint32_t)(sce >> 3), (uint32_t)(sco >> 3)};
+                const i32x4 b_lo = {(int)bytes_times(qw[0], lo[0]), (int)bytes_times(qw[1], lo[0]),
+                                    (int)bytes_times(qw[2], lo[1]), (int)bytes_times(qw[3], lo[1])};
+                const i32x4 b_hi = {(int)bytes_times(qw[0], hi[0]), (int)bytes_times(qw[1], hi[0]),
+                                    (int)bytes_times(qw[2], hi[1]), (int)bytes_times(qw[3], hi[1])};
+                const int me = (int)__builtin_amdgcn_perm((uint32_t)mne, (uint32_t)mne, 0u);
+                const int mo = (int)__builtin_amdgcn_perm((uint32_t)mno, (uint32_t)mno, 0u);
+                const i32x4 b_mn = {me, me, mo, mo};
+                const i32x4 av = *reinterpret_cast<const i32x4 *>(la + moe_la_off(sb * 8 + 2 * jp, c, g));
+                alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_lo, alo, 0, 0, 0);
+                ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_hi, ahi, 0, 0, 0);
+                amn = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_mn, amn, 0, 0, 0);
             }
-            const int rbase = 4 * (g & 1);
+            const float d = h2f((uint16_t)(H.x & 0xffffu)), dmin = h2f((uint16_t)(H.x >> 16));
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                if (it0 + u >= items) break;
-                const int sb = sbs[u];
-                const float4 xs4 = *reinterpret_cast<const float4 *>(lxs + sb * 8 + rbase);
-                const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
-                // sub-block scale (two 3-bit digits) and min in the B operands
-                // of three K = 64 MFMAs per pair of sub-blocks: exact int32
-                i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
-#pragma unroll
-                for (int jp = 0; jp < 4; jp++) {
-                    const uint64_t raw = qv[u][jp];
-                    const uint64_t qe = raw & 0x0F0F0F0F0F0F0F0Full, qo = (raw >> 4) & 0x0F0F0F0F0F0F0F0Full;
-                    int sce, mne, sco, mno;
-                    scale_min_k4(2 * jp, hdr[u].y, hdr[u].z, hdr[u].w, &sce, &mne);
-                    scale_min_k4(2 * jp + 1, hdr[u].y, hdr[u].z, hdr[u].w, &sco, &mno);
-                    const uint32_t q[4] = {(uint32_t)qe, (uint32_t)(qe >> 32), (uint32_t)qo, (uint32_t)(qo >> 32)};
-                    const uint32_t lo[2] = {(uint32_t)(sce & 7), (uint32_t)(sco & 7)};
-                    const uint32_t hi[2] = {(uint32_t)(sce >> 3), (uint32_t)(sco >> 3)};
-                    const i32x4 b_lo = {(int)bytes_times(q[0], lo[0]), (int)bytes_times(q[1], lo[0]),
-                                        (int)bytes_times(q[2], lo[1]), (int)bytes_times(q[3], lo[1])};
-                    const i32x4 b_hi = {(int)bytes_times(q[0], hi[0]), (int)bytes_times(q[1], hi[0]),
-                                        (int)bytes_times(q[2], hi[1]), (int)bytes_times(q[3], hi[1])};
-                    const int me = (int)__builtin_amdgcn_perm((uint32_t)mne, (uint32_t)mne, 0u);
-                    const int mo = (int)__builtin_amdgcn_perm((uint32_t)mno, (uint32_t)mno, 0u);
-                    const i32x4 b_mn = {me, me, mo, mo};
-                    const i32x4 av = *reinterpret_cast<const i32x4 *>(la + moe_la_off(sb * 8 + 2 * jp, c, g));
-                    alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_lo, alo, 0, 0, 0);
-                    ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_hi, ahi, 0, 0, 0);
-                    amn = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_mn, amn, 0, 0, 0);
-                }
-                const float d = h2f((uint16_t)(hdr[u].x & 0xffffu)), dmin = h2f((uint16_t)(hdr[u].x >> 16));
-                float *dst = part + (uint64_t)slot[u] * 128;
+            for (int i = 0; i < 4; i++) {
+                // this lane's plane (rows 0..7 high, 8..15 low), then both
+                const float v = d * (float)(alo[i] + 8 * ahi[i]) - dmin * (float)amn[i];
+                const float lo = __shfl_xor(v, 32);
+                acc[i] += xs[i] * (256.f * v + lo);
+            }
+            if (sb == nsb - 1) {  // the pair's last super-block: its result to LDS
+                const int tm = wave + kMoeWaves * (q / nsb);
+                float *dst = part + (uint64_t)tm * 128;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    // this lane's plane (rows 0..7 high, 8..15 low), then both
-                    const float v = d * (float)(alo[i] + 8 * ahi[i]) - dmin * (float)amn[i];
-                    const float lo = __shfl_xor(v, 32);
-                    if (g < 2) dst[(4 * g + i) * 16 + c] = xs[i] * (256.f * v + lo);
+                    if (g < 2) dst[(4 * g + i) * 16 + c] = acc[i];
+                    acc[i] = 0.f;
                 }
+            }
+        };
+        uint4 h0, h1;
+        uint64_t q0[4], q1[4];
+        if (total > 0) load_item(0, h0, q0);
+        if (total > 1) load_item(1, h1, q1);
+        for (int q = 0; q < total; q += 2) {
+            compute_item(q, h0, q0);
+            if (q + 2 < total) load_item(q + 2, h0, q0);
+            if (q + 1 < total) {
+                compute_item(q + 1, h1, q1);
+                if (q + 3 < total) load_item(q + 3, h1, q1);
             }
         }
         __syncthreads();
-        // sum the super-blocks in order, then the epilogue
+        // the epilogue
         for (int o = threadIdx.x; o < ntl * nr * 16; o += kMoeThreads) {
             const int tl = o / (nr * 16), rem = o % (nr * 16), i = rem / 16, cc = rem % 16;
             float y[2] = {0.f, 0.f};
-            for (int m = 0; m < mats; m++)
-                for (int sb = 0; sb < nsb; sb++) y[m] += part[((uint64_t)(tl * nsb + sb) * mats + m) * 128 + i * 16 + cc];
+            for (int m = 0; m < mats; m++) y[m] = part[(uint64_t)(tl * mats + m) * 128 + i * 16 + cc];
             const uint64_t dst = (uint64_t)s_out[i] * A.N + (t0 + tl) * 16 + cc;
             if (A.swiglu) {
                 A.out0[dst] = __fmul_rn(silu_ref(y[0]), y[1]);
@@ -548,12 +562,13 @@ hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
     a.out0 = g.out0;
     a.out1 = g.out1;
     const int nsb = g.K / 256, mats = g.w1 ? 2 : 1, tiles = g.N / 16;
-    // partial sums of one chunk: tpw * nsb * mats * 512 B within 32 KB
+    // tiles per workgroup: as many as keep nsb * mats * tpw items near 64
+    // (enough workgroups in flight; each wave walks a few pairs)
     int tpw = (32 * 1024) / (nsb * mats * 512);
     tpw = std::max(1, std::min(tpw, 16));
     tpw = std::min(tpw, tiles);
     a.tpw = tpw;
-    const uint32_t lds = (uint32_t)tpw * nsb * mats * 512 + (uint32_t)(g.K / 32) * (16 * 32) + (uint32_t)nsb * 32;
+    const uint32_t lds = (uint32_t)tpw * mats * 512 + (uint32_t)(g.K / 32) * (16 * 32) + (uint32_t)nsb * 32;
     const int units = act_rows * nsb;
     moe_quant_kernel<<<(units + 3) / 4, 256, 0, s>>>(g.x, act_rows, g.K, a.xq);
     moe_gemm_kernel<<<dim3((unsigned)g.experts, (unsigned)((tiles + tpw - 1) / tpw)), kMoeThreads, lds, s>>>(a);
