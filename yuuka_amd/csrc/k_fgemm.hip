@@ -1077,9 +1077,11 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
         uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         YK_FG_STAMP(ts[0]);
 #endif
+        // issued unconditionally (item index clamped; the buffer resources
+        // bound every access): under a branch the compiler's wait counts
+        // lose track and the prologue would wait for these weights too
 #pragma unroll
-        for (int d = 0; d < kD; d++)
-            if (nmine > d) issue_item(sbr[d], wave + d * kWaves);
+        for (int d = 0; d < kD; d++) issue_item(sbr[d], min(wave + d * kWaves, max(I - 1, 0)));
         __builtin_amdgcn_sched_barrier(0);
         for (int idx = lane; idx < cnt * kSlot / 4; idx += 64)
             reinterpret_cast<float4 *>(myr)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
