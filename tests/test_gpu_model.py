@@ -74,6 +74,31 @@ def test_verify_rows_match_prefill_logits(dev, tiny, kv):
     orc.close()
 
 
+@pytest.mark.parametrize("cpw", [1, 2, 3])
+@pytest.mark.parametrize("k", [4, 16])
+def test_verify_over_chunk_groups_matches_oracle(dev, tiny, monkeypatch, cpw, k):
+    """A 200-token context spans four 64-key chunks: one verify-attention
+    workgroup walks `cpw` of them with a running softmax (cpw = 1: one chunk
+    per workgroup), then the groups are merged. Logits of k + 1 verify rows
+    against the oracle."""
+    monkeypatch.setenv("YUUKA_ATTN_CPW", str(cpw))
+    cfg, w = tiny
+    cfg = replace(cfg, max_rows=max(cfg.max_rows, k + 1))
+    eng = Mdl.Engine(dev, cfg, w)
+    orc = O.Q35(cfg, w, kv_format=1)
+    rng = np.random.default_rng(7)
+    prompt = rng.integers(0, cfg.vocab, 200).astype(np.int32)
+    eng.prefill(prompt[:-1])
+    orc.forward(prompt[:-1])
+    rows = np.concatenate([prompt[-1:], rng.integers(0, cfg.vocab, k)]).astype(np.int32)
+    eng.verify(rows)
+    got = eng.logits(k + 1)
+    want = orc.forward(rows, all_logits=True)
+    _close(got, want, f"verify cpw={cpw} k={k}")
+    eng.close()
+    orc.close()
+
+
 def test_partial_acceptance_commits_exact_prefix(dev, tiny):
     """Drafts chosen so that exactly two are accepted: the device commit must
     leave the state the oracle has after the accepted prefix, and the next

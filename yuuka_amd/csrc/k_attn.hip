@@ -359,7 +359,8 @@ constexpr uint32_t kOffQh = kOffVt + kMD * kVt * 2;         // [32][256] f16, bl
 constexpr uint32_t kOffQl = kOffQh + kMQ * kMD * 2;
 constexpr uint32_t kOffS = kOffQl + kMQ * kMD * 2;          // [32][64] f32 scores, then P in place:
                                                             // [32][2: high, low][64] f16, blocks XOR (row & 7)
-constexpr uint32_t kMfmaLds = kOffS + kMQ * kMK * 4;        // 76 KB: two workgroups per CU
+constexpr uint32_t kOffML = kOffS + kMQ * kMK * 4;         // [3][32] f32: running max, sum, rescale
+constexpr uint32_t kMfmaLds = kOffML + 3 * kMQ * 4;         // 76 KB: two workgroups per CU
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
@@ -484,6 +485,10 @@ __device__ __forceinline__ void lds_only_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// One workgroup per (64-key chunk, KV head, request): launches of at most
+// ~1024 chunk workgroups (short contexts). The chunk's keys and values load
+// while the queries are prepared; the verify rows walk the LDS-resident
+// chunk in blocks of kMQ / G rows.
 __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) void attn_verify_mfma_kernel(const float *__restrict__ q, const float *__restrict__ k,
                                                                const float *__restrict__ v, uint16_t *kpool,
                                                                uint16_t *vpool, const int32_t *__restrict__ table,
@@ -750,6 +755,285 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
 #endif
 }
 
+// One workgroup per (group of `cpw` 64-key chunks, KV head, request). The
+// verify rows' own keys and values in the group's range go to the pool
+// first; then, per block of kMQ / G verify rows, the group's chunks are
+// walked in order with an online softmax (running max m, sum l and the
+// rescale of the P.V accumulators in registers). One partial record
+// (o, m, l) per (group, row, head) for the merge.
+__global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) void attn_verify_mfma_group_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, uint16_t *kpool,
+    uint16_t *vpool, const int32_t *__restrict__ table, const float *__restrict__ q_norm,
+    const float *__restrict__ k_norm, const float2 *__restrict__ rope, AttnVArgs a, float *__restrict__ part,
+    ModelDyn dyn, int cpw) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    YK_ATTN_REQUEST(kMK * cpw);
+    const int kvh = blockIdx.y, grp = blockIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int r16 = lane & 15, g4 = lane >> 4;
+    const int R = a.rows;
+    const int G = a.heads / a.kv_heads;
+    const int p0 = cur_pos_a(dyn) + a.displacement;  // position of verify row 0
+    const int last = p0 + R - 1;
+    const int c_lo = grp * cpw;
+    if (c_lo * kMK > last) return;  // no row sees this group; the merge skips it
+    const int c_hi = min(c_lo + cpw, last / kMK + 1);
+#ifdef YK_AT_TIMING
+    uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#endif
+    YK_AT_STAMP(0);
+    const int half = a.rope_dim / 2;
+    const int qstride = a.gated ? 2 * kMD : kMD;
+    float *Mrow = reinterpret_cast<float *>(lds + kOffML);  // running max per MFMA row
+    float *Lrow = Mrow + kMQ;                               // running sum
+    float *Arow = Lrow + kMQ;                               // this chunk's rescale of the accumulators
+
+    // ---- the verify rows' own keys and values (rows whose position falls in
+    //      this group): rounded as the pool stores them, into the pool
+    for (int r = wave; r < R; r += kAW) {
+        const int p = p0 + r;
+        if (p < c_lo * kMK || p >= c_hi * kMK) continue;
+        const int64_t slot = (int64_t)table[p / a.block_size] * a.block_size + p % a.block_size;
+        float y[4];
+        norm_rope4(k + (int64_t)r * a.kv_dim + (int64_t)kvh * kMD, k_norm, a.eps, rope + r * half, y);
+        uint16_t kq[4], vq[4];
+        const float4 vv = *reinterpret_cast<const float4 *>(v + (int64_t)r * a.kv_dim + (int64_t)kvh * kMD + 4 * lane);
+        const float vf[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            kq[i] = ref_f32_to_f16(y[i]);
+            vq[i] = ref_f32_to_f16(vf[i]);
+        }
+        const uint2 kw = make_uint2((uint32_t)kq[0] | ((uint32_t)kq[1] << 16), (uint32_t)kq[2] | ((uint32_t)kq[3] << 16));
+        const uint2 vw = make_uint2((uint32_t)vq[0] | ((uint32_t)vq[1] << 16), (uint32_t)vq[2] | ((uint32_t)vq[3] << 16));
+        *reinterpret_cast<uint2 *>(kpool + slot * a.kv_dim + (int64_t)kvh * kMD + 4 * lane) = kw;
+        *reinterpret_cast<uint2 *>(vpool + slot * a.kv_dim + (int64_t)kvh * kMD + 4 * lane) = vw;
+    }
+    if (p0 < c_hi * kMK) __syncthreads();  // the new rows are in the pool (global fence)
+    YK_AT_STAMP(1);
+
+    // keys straight into MFMA B order: the scores lane (key kk, group g4)
+    // holds dims [32 ks + 8 g4, +8) of key kk for every ks
+    const int kk_s = (wave & 3) * 16 + r16;
+    const bool scorer = 16 * (wave >> 2) < G * min(kMQ / G, R);  // row tile of this wave in use
+    constexpr int kVE = kMD / kAW / 8;                          // 16-byte V pieces per lane
+    constexpr int kJ = kMD / kAW / 16;                          // 16-wide output tiles per wave
+    const int RB = kMQ / G;
+    // ---- query rows of one block: normalised, rotated, split into F16 high +
+    //      remainder. A wave's rows are loaded first, then computed.
+    auto prep_q = [&](int r0, int Rb) __attribute__((always_inline)) {
+        constexpr int kQV = kMQ / kAW;
+        const int nqb = G * Rb;
+        const float4 w4 = *reinterpret_cast<const float4 *>(q_norm + 4 * lane);
+        float4 xq[kQV];
+#pragma unroll
+        for (int t = 0; t < kQV; t++) {
+            const int vec = wave + kAW * t;
+            if (vec < nqb) {
+                const int gq = vec / Rb, r = r0 + vec % Rb;
+                xq[t] = *reinterpret_cast<const float4 *>(q + ((int64_t)r * a.heads + kvh * G + gq) * qstride + 4 * lane);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < kQV; t++) {
+            const int vec = wave + kAW * t;
+            if (vec >= nqb) break;
+            const int r = r0 + vec % Rb;
+            float2 cq[4] = {};
+            if (lane < 16) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int e = 4 * lane + i;
+                    cq[i] = rope[r * half + (lane < 8 ? e : e - 32)];
+                }
+            }
+            float y[4];
+            norm_rope_regs(xq[t], w4, a.eps, cq, y);
+            _Float16 hi[4], lo[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                hi[i] = (_Float16)y[i];
+                lo[i] = (_Float16)(y[i] - (float)hi[i]);
+            }
+            const uint32_t off = (uint32_t)vec * kMD * 2 + (uint32_t)(((lane >> 1) ^ (vec & 15)) * 16 + (lane & 1) * 8);
+            *reinterpret_cast<uint2 *>(lds + kOffQh + off) = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
+            *reinterpret_cast<uint2 *>(lds + kOffQl + off) = make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
+        }
+    };
+
+    // keys (scorer waves) and values (wave w: dims [32w, +32) of key `lane`)
+    // of chunk ci, from clamped positions; keys / values past the verify rows
+    // count as zero where they are used
+    half8 kreg[kMD / 32];
+    uint4 vreg[kVE];
+    bool kval = false, vval = false;
+    auto load_k = [&](int ci) __attribute__((always_inline)) {
+        const int key0 = ci * kMK;
+        const int p = min(key0 + kk_s, last);
+        kval = scorer && key0 + kk_s <= last;
+        const int64_t ks_ = (int64_t)table[p / a.block_size] * a.block_size + p % a.block_size;
+        const half8 *ksrc = reinterpret_cast<const half8 *>(kpool + ks_ * a.kv_dim + (int64_t)kvh * kMD + g4 * 8);
+#pragma unroll
+        for (int ks = 0; ks < kMD / 32; ks++) kreg[ks] = ksrc[4 * ks];
+    };
+    auto load_v = [&](int ci) __attribute__((always_inline)) {
+        const int key0 = ci * kMK;
+        const int vp = min(key0 + lane, last);
+        vval = key0 + lane <= last;
+        const int64_t vs_ = (int64_t)table[vp / a.block_size] * a.block_size + vp % a.block_size;
+        const uint4 *vsrc =
+            reinterpret_cast<const uint4 *>(vpool + vs_ * a.kv_dim + (int64_t)kvh * kMD + wave * (kMD / kAW));
+#pragma unroll
+        for (int e = 0; e < kVE; e++) vreg[e] = vsrc[e];
+    };
+
+    for (int r0 = 0; r0 < R; r0 += RB) {
+        const int Rb = min(RB, R - r0), nq = G * Rb;  // this block's verify rows and MFMA rows
+        if (r0) lds_only_barrier();                   // the previous block's reads of Q, M, L are done
+        prep_q(r0, Rb);
+        if (threadIdx.x < kMQ) {
+            Mrow[threadIdx.x] = -INFINITY;
+            Lrow[threadIdx.x] = 0.0f;
+        }
+        f32x4 o[kJ][2];
+#pragma unroll
+        for (int j = 0; j < kJ; j++)
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++) o[j][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const bool two = nq > 16;
+        YK_AT_STAMP(2);
+        for (int ci = c_lo; ci < c_hi; ci++) {
+            const int key0 = ci * kMK;
+            load_k(ci);
+            load_v(ci);
+            lds_only_barrier();  // the previous chunk's P.V reads of Vt are done; Q, M, L are written
+            {
+                uint16_t *vt = reinterpret_cast<uint16_t *>(lds + kOffVt);
+#pragma unroll
+                for (int e = 0; e < kVE; e++) {
+                    const uint4 vv = vval ? vreg[e] : make_uint4(0, 0, 0, 0);
+                    const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+                    for (int i = 0; i < 8; i++)
+                        vt[(wave * (kMD / kAW) + e * 8 + i) * kVt + lane] = (uint16_t)(w4[i >> 1] >> (16 * (i & 1)));
+                }
+            }
+            // ---- scores: wave w owns keys [16 (w & 3), +16) of row tile w >> 2
+            if (16 * (wave >> 2) < nq) {
+                const int rt = wave >> 2;
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < kMD / 32; ks++) {
+                    const int blk = ks * 4 + g4;
+                    const uint32_t qo = (uint32_t)(rt * 16 + r16) * kMD * 2 + (uint32_t)((blk ^ r16) * 16);
+                    const half8 ah = *reinterpret_cast<const half8 *>(lds + kOffQh + qo);
+                    const half8 al = *reinterpret_cast<const half8 *>(lds + kOffQl + qo);
+                    const half8 kb = kval ? kreg[ks] : half8{};
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, kb, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, kb, acc, 0, 0, 0);
+                }
+                float *S = reinterpret_cast<float *>(lds + kOffS);
+                const int p = key0 + kk_s;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int qi = rt * 16 + g4 * 4 + e;
+                    if (qi < nq) S[qi * kMK + kk_s] = p <= p0 + r0 + qi % Rb ? acc[e] * a.scale : -INFINITY;
+                }
+            }
+            lds_only_barrier();
+            YK_AT_STAMP(3);
+            // ---- online softmax: one wave per query row, lane = key
+            {
+                const float *S = reinterpret_cast<const float *>(lds + kOffS);
+                for (int qi = wave; qi < nq; qi += kAW) {
+                    const float sc = S[qi * kMK + lane];
+                    const float mc = wave_max_dpp_f(sc);
+                    const float m_old = Mrow[qi];
+                    const float m_new = fmaxf(m_old, mc);
+                    float e = 0.0f, alpha = 1.0f;
+                    if (m_new != -INFINITY) {
+                        e = (sc == -INFINITY) ? 0.0f : (float)exp((double)(sc - m_new));
+                        alpha = m_old == -INFINITY ? 0.0f : (float)exp((double)(m_old - m_new));
+                    }
+                    const float lc = wave_sum_dpp_f(e);
+                    const _Float16 hi = (_Float16)e, lo = (_Float16)(e - (float)hi);
+                    // P replaces the row's scores: high halves in bytes [0, 128), low in [128, 256)
+                    const uint32_t off = (uint32_t)qi * kMK * 4 + (uint32_t)((((lane >> 3) ^ (qi & 7)) * 16) + (lane & 7) * 2);
+                    *reinterpret_cast<_Float16 *>(lds + kOffS + off) = hi;
+                    *reinterpret_cast<_Float16 *>(lds + kOffS + kMK * 2 + off) = lo;
+                    if (lane == 0) {
+                        Lrow[qi] = Lrow[qi] * alpha + lc;
+                        Mrow[qi] = m_new;
+                        Arow[qi] = alpha;
+                    }
+                }
+            }
+            lds_only_barrier();
+            YK_AT_STAMP(4);
+            // ---- value product: wave w owns dims [32w, 32w + 32); the running
+            //      accumulators are rescaled by this chunk's alpha first
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int qi = rt * 16 + g4 * 4 + e;
+                    const float al = qi < nq ? Arow[qi] : 1.0f;
+#pragma unroll
+                    for (int j = 0; j < kJ; j++) o[j][rt][e] *= al;
+                }
+#pragma unroll
+            for (int ks = 0; ks < kMK / 32; ks++) {
+                const int blk = ks * 4 + g4;
+                half8 ah[2], al[2];
+#pragma unroll
+                for (int rt = 0; rt < 2; rt++) {
+                    const uint32_t po = (uint32_t)(rt * 16 + r16) * kMK * 4 + (uint32_t)((blk ^ (r16 & 7)) * 16);
+                    ah[rt] = *reinterpret_cast<const half8 *>(lds + kOffS + po);
+                    al[rt] = *reinterpret_cast<const half8 *>(lds + kOffS + kMK * 2 + po);
+                }
+#pragma unroll
+                for (int j = 0; j < kJ; j++) {
+                    const int dcol = wave * (kMD / kAW) + j * 16 + r16;
+                    const half8 b = *reinterpret_cast<const half8 *>(lds + kOffVt + (uint32_t)dcol * kVt * 2 +
+                                                                    (uint32_t)(ks * 32 + g4 * 8) * 2);
+                    o[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[0], b, o[j][0], 0, 0, 0);
+                    o[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[0], b, o[j][0], 0, 0, 0);
+                    if (two) {
+                        o[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[1], b, o[j][1], 0, 0, 0);
+                        o[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[1], b, o[j][1], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        // ---- this block's partial records: o, and (m, l) of every row
+#pragma unroll
+        for (int j = 0; j < kJ; j++)
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int qi = rt * 16 + g4 * 4 + e;
+                    if (qi < nq) {
+                        const int gq = qi / Rb, r = r0 + qi % Rb, d = wave * (kMD / kAW) + j * 16 + r16;
+                        part[(((int64_t)grp * R + r) * a.heads + kvh * G + gq) * (kMD + 2) + d] = o[j][rt][e];
+                    }
+                }
+        if (threadIdx.x < nq) {
+            const int qi = threadIdx.x, gq = qi / Rb, r = r0 + qi % Rb;
+            float *rec = part + (((int64_t)grp * R + r) * a.heads + kvh * G + gq) * (kMD + 2);
+            rec[kMD] = Mrow[qi];
+            rec[kMD + 1] = Lrow[qi];
+        }
+    }
+    YK_AT_STAMP(6);
+#ifdef YK_AT_TIMING
+    if (yk_at_dbg && lane == 0) {
+        uint64_t *o = yk_at_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * kAW + wave) * 8;
+        for (int e = 0; e < 8; e++) o[e] = ts[e];
+    }
+#endif
+}
+
 // Merges the chunk partials of one (query head, row) and applies the output
 // gate sigmoid(gate) (forward.go:452-456). The chunk weights exp(m_c - max)
 // are computed once per workgroup into LDS.
@@ -846,21 +1130,43 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
                               float *out, const AttnVArgs &a, void *scratch, const ModelDyn &dyn, int max_pos_hint,
                               hipStream_t s) {
     const bool mfma = use_mfma_path(a);
-    const int ck = mfma ? kMK : attn_verify_chunk(a.fmt);
+    const unsigned nz = (unsigned)(a.nreq > 0 ? a.nreq : 1);
+    // MFMA kernel: groups of cpw chunks per workgroup once a launch has more
+    // than ~1024 chunk workgroups (fewer partial records, query preparation
+    // amortized); short contexts keep one chunk per workgroup
+    int cpw = 1;
+    if (mfma) {
+        const int c1 = (a.capacity + kMK - 1) / kMK;
+        const int l1 = max_pos_hint >= 0 ? std::min(c1, max_pos_hint / kMK + 1) : c1;
+        const int64_t wgs = (int64_t)l1 * a.kv_heads * nz;
+        cpw = (int)std::max<int64_t>(1, std::min<int64_t>(8, wgs / 1024));
+        if (const char *e = getenv("YUUKA_ATTN_CPW")) {  // tests and tuning: a fixed group size
+            const int v = atoi(e);
+            if (v >= 1 && v <= 8) cpw = v;
+        }
+    }
+    const int ck = mfma ? kMK * cpw : attn_verify_chunk(a.fmt);
     const int chunks = (a.capacity + ck - 1) / ck;
     const int launch_chunks = max_pos_hint >= 0 ? std::min(chunks, max_pos_hint / ck + 1) : chunks;
     auto *part = static_cast<float *>(scratch);
-    const unsigned nz = (unsigned)(a.nreq > 0 ? a.nreq : 1);
     static bool attr0 = false, attr1 = false, attr2 = false;
     if (mfma) {
         if (!attr2) {
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_mfma_kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_mfma_group_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
             attr2 = true;
         }
-        attn_verify_mfma_kernel<<<dim3((unsigned)launch_chunks, (unsigned)a.kv_heads, nz), 64 * kAW, kMfmaLds, s>>>(
-            q, k, v, static_cast<uint16_t *>(kpool), static_cast<uint16_t *>(vpool), table, q_norm, k_norm, rope, a,
-            part, dyn);
+        const dim3 grid((unsigned)launch_chunks, (unsigned)a.kv_heads, nz);
+        if (cpw == 1)
+            attn_verify_mfma_kernel<<<grid, 64 * kAW, kMfmaLds, s>>>(q, k, v, static_cast<uint16_t *>(kpool),
+                                                                      static_cast<uint16_t *>(vpool), table, q_norm,
+                                                                      k_norm, rope, a, part, dyn);
+        else
+            attn_verify_mfma_group_kernel<<<grid, 64 * kAW, kMfmaLds, s>>>(q, k, v, static_cast<uint16_t *>(kpool),
+                                                                            static_cast<uint16_t *>(vpool), table,
+                                                                            q_norm, k_norm, rope, a, part, dyn, cpw);
     } else if (a.fmt == 1) {
         const uint32_t lds = attn_verify_lds_bytes(a);
         if (!attr1) {
