@@ -294,15 +294,23 @@ __device__ __forceinline__ void conv_channel2(const float *conv_state, const flo
     const int R = g.rows, K = g.kernel;
     const int cc[2] = {c0, c1 < 0 ? c0 : c1};
     float w[2][8], st[2][8], x[2][RC];
+    // every load unconditional from a clamped index (out-of-range values are
+    // zeroed after the load): loads under branches make the compiler's wait
+    // counts conservative and serialize them
 #pragma unroll
     for (int u = 0; u < 2; u++) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            w[u][i] = i < K ? conv_w[(uint64_t)cc[u] * K + i] : 0.0f;
-            st[u][i] = i < K - 1 ? conv_state[(uint64_t)cc[u] * (K - 1) + i] : 0.0f;
+            const float wv = conv_w[(uint64_t)cc[u] * K + min(i, K - 1)];
+            const float sv = conv_state[(uint64_t)cc[u] * (K - 1) + min(i, K - 2)];
+            w[u][i] = i < K ? wv : 0.0f;
+            st[u][i] = i < K - 1 ? sv : 0.0f;
         }
 #pragma unroll
-        for (int r = 0; r < RC; r++) x[u][r] = r < R ? qkv[(uint64_t)r * g.conv_dim + cc[u]] : 0.0f;
+        for (int r = 0; r < RC; r++) {
+            const float xv = qkv[(uint64_t)min(r, R - 1) * g.conv_dim + cc[u]];
+            x[u][r] = r < R ? xv : 0.0f;
+        }
     }
     if (K == 4) {  // the models' conv width: every index below is a compile-time constant
 #pragma unroll
@@ -595,7 +603,11 @@ hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, c
                                   const float *a_log, float *raw_out, float *conv_out, const GdnArgs &g,
                                   hipStream_t s) {
     const dim3 grid((unsigned)g.rank, kS / kCols, (unsigned)(g.nreq > 0 ? g.nreq : 1));
-    if (g.rows <= 16)
+    // row capacity of the conv registers: the smallest instantiation that holds the rows
+    if (g.rows <= 8)
+        gdn_verify_cols_kernel<8><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
+            conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
+    else if (g.rows <= 16)
         gdn_verify_cols_kernel<16><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
             conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
     else
