@@ -68,9 +68,43 @@ __host__ __device__ inline BgQuant bg_view(void *ws, int rows, int K) {
     return q;
 }
 
+// Reductions on the DPP path (a __shfl_xor is an LDS permute): within each
+// 16-lane row (lane pairs, quads, half rows, rows), then the rows' results
+// through readlane.
+template <int C>
+__device__ __forceinline__ double dpp_d(double v) {
+    const uint64_t b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, C, 0xf, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), C, 0xf, 0xf, true);
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+__device__ __forceinline__ double rl_d(double v, int l) {
+    const uint64_t b = __double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double row16_sum_d(double v) {  // every lane: its 16-lane row's sum
+    v += dpp_d<0xb1>(v);
+    v += dpp_d<0x4e>(v);
+    v += dpp_d<0x141>(v);
+    return v + dpp_d<0x140>(v);
+}
 __device__ __forceinline__ double wave_sum_d(double v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
+    v = row16_sum_d(v);
+    return (rl_d(v, 0) + rl_d(v, 16)) + (rl_d(v, 32) + rl_d(v, 48));
+}
+// Maximum of non-negative values over the wave.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, true)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, true)));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 // ---------------------------------------------------------------- prologue
@@ -118,7 +152,8 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
             const float4 w = *reinterpret_cast<const float4 *>(A.head_norm + (e & 127));
             double hs = (double)v.x * (double)v.x + (double)v.y * (double)v.y + (double)v.z * (double)v.z +
                         (double)v.w * (double)v.w;
-            for (int off = 16; off > 0; off >>= 1) hs += __shfl_xor(hs, off);
+            hs = row16_sum_d(hs);  // each 128-element head is two 16-lane rows
+            hs = lane < 32 ? rl_d(hs, 0) + rl_d(hs, 16) : rl_d(hs, 32) + rl_d(hs, 48);
             const float mean = (float)(hs / 128.0);
             const float hsc = (float)(1.0 / sqrt((double)(mean + A.eps)));
             v.x = __fmul_rn(__fmul_rn(v.x, __fmul_rn(hsc, w.x)), z.x);
@@ -133,7 +168,7 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
             v.w = __fmul_rn(__fmul_rn(v.w, nscale), w.w);
         }
         float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        m = wave_max_nonneg(m);
         const float inv = m > 0.f ? (float)kQMax / m : 0.f;
         const int qv[4] = {(int)rintf(v.x * inv), (int)rintf(v.y * inv), (int)rintf(v.z * inv),
                            (int)rintf(v.w * inv)};
