@@ -41,9 +41,27 @@ constexpr int kMoeWaves = 8;
 constexpr int kMoeThreads = 64 * kMoeWaves;
 constexpr int kChunk = 8;        // assignments per MFMA tile (high planes in rows 0..7)
 
+// Wave reductions on the DPP path (a __shfl_xor is an LDS permute): within
+// each 16-lane row (pairs, quads, half rows, rows), then the four rows'
+// results through readlane (every lane gets the result).
+template <int C>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), C, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float rl_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
 __device__ __forceinline__ float wave_sum(float v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
+    v += dpp_f<0xb1>(v);
+    v += dpp_f<0x4e>(v);
+    v += dpp_f<0x141>(v);
+    v += dpp_f<0x140>(v);
+    return (rl_f(v, 0) + rl_f(v, 16)) + (rl_f(v, 32) + rl_f(v, 48));
+}
+__device__ __forceinline__ float wave_max_nonneg(float v) {  // values >= 0
+    v = fmaxf(v, dpp_f<0xb1>(v));
+    v = fmaxf(v, dpp_f<0x4e>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return fmaxf(fmaxf(rl_f(v, 0), rl_f(v, 16)), fmaxf(rl_f(v, 32), rl_f(v, 48)));
 }
 
 // ---------------------------------------------------------------- router
@@ -279,7 +297,7 @@ __global__ __launch_bounds__(256) void moe_quant_kernel(const float *__restrict_
     const int row = u / nsb, sb = u % nsb;
     const float4 v = *reinterpret_cast<const float4 *>(x + (uint64_t)row * K + sb * 256 + 4 * lane);
     float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    m = wave_max_nonneg(m);
     const float inv = m > 0.f ? (float)kQMax / m : 0.f;
     const int qv[4] = {(int)rintf(v.x * inv), (int)rintf(v.y * inv), (int)rintf(v.z * inv), (int)rintf(v.w * inv)};
     uint32_t hp = 0, lp = 0;
@@ -450,17 +468,18 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
             const float d = h2f((uint16_t)(H.x & 0xffffu)), dmin = h2f((uint16_t)(H.x >> 16));
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                // this lane's plane (rows 0..7 high, 8..15 low), then both
+                // this lane's plane (rows 0..7 high, 8..15 low); the planes
+                // are combined once per pair
                 const float v = d * (float)(alo[i] + 8 * ahi[i]) - dmin * (float)amn[i];
-                const float lo = __shfl_xor(v, 32);
-                acc[i] += xs[i] * (256.f * v + lo);
+                acc[i] += xs[i] * v;
             }
             if (sb == nsb - 1) {  // the pair's last super-block: its result to LDS
                 const int tm = wave + kMoeWaves * (q / nsb);
                 float *dst = part + (uint64_t)tm * 128;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    if (g < 2) dst[(4 * g + i) * 16 + c] = acc[i];
+                    const float lo = __shfl_xor(acc[i], 32);
+                    if (g < 2) dst[(4 * g + i) * 16 + c] = fmaf(256.f, acc[i], lo);
                     acc[i] = 0.f;
                 }
             }
