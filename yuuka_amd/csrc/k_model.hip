@@ -21,9 +21,37 @@ namespace {
 
 __device__ __forceinline__ int cur_pos(const ModelDyn &dyn) { return dyn.pos_dev ? *dyn.pos_dev : dyn.pos; }
 
+// Wave sums on the DPP path (a __shfl_xor is an LDS permute): pairs, quads,
+// half rows and rows of 16 lanes, then the four rows through readlane.
+template <int C>
+__device__ __forceinline__ double dpp_sum_step(double v) {
+    const uint64_t b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, C, 0xf, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), C, 0xf, 0xf, true);
+    return v + __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+__device__ __forceinline__ double rl_dbl(double v, int l) {
+    const uint64_t b = __double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double wave_sum_dpp(double v) {
+    v = dpp_sum_step<0x140>(dpp_sum_step<0x141>(dpp_sum_step<0x4e>(dpp_sum_step<0xb1>(v))));
+    return (rl_dbl(v, 0) + rl_dbl(v, 16)) + (rl_dbl(v, 32) + rl_dbl(v, 48));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xf, 0xf, true));
+    const auto rl = [](float x, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
+    return (rl(v, 0) + rl(v, 16)) + (rl(v, 32) + rl(v, 48));
+}
+
 template <typename T>
 __device__ __forceinline__ T block_sum256(T v, T *red) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    v = wave_sum_dpp(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
     T s = red[0];
