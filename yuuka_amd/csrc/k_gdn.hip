@@ -285,34 +285,32 @@ __device__ __forceinline__ double wave_sum_dpp(double v) {
     return (rl_dd(v, 15) + rl_dd(v, 31)) + (rl_dd(v, 47) + rl_dd(v, 63));
 }
 
-// Causal conv + SiLU of two channels (c1 < 0: one) with every input load
-// issued before either is computed.
+// Causal conv + SiLU of two channels (c1 < 0: one). Width 4 (the models'
+// conv) issues every input load of both channels before either is computed;
+// other widths take the channels one after the other.
 template <int RC>  // row capacity: rows <= RC
 __device__ __forceinline__ void conv_channel2(const float *conv_state, const float *qkv, const float *conv_w,
                                               const GdnArgs &g, int c0, float *dst0, int stride0, int c1, float *dst1,
                                               int stride1) {
     const int R = g.rows, K = g.kernel;
     const int cc[2] = {c0, c1 < 0 ? c0 : c1};
-    float w[2][8], st[2][8], x[2][RC];
     // every load unconditional from a clamped index (out-of-range values are
     // zeroed after the load): loads under branches make the compiler's wait
     // counts conservative and serialize them
+    if (K == 4) {  // every index below is a compile-time constant
+        float w[2][4], st[2][3], x[2][RC];
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
+        for (int u = 0; u < 2; u++) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float wv = conv_w[(uint64_t)cc[u] * K + min(i, K - 1)];
-            const float sv = conv_state[(uint64_t)cc[u] * (K - 1) + min(i, K - 2)];
-            w[u][i] = i < K ? wv : 0.0f;
-            st[u][i] = i < K - 1 ? sv : 0.0f;
+            for (int i = 0; i < 4; i++) w[u][i] = conv_w[(uint64_t)cc[u] * 4 + i];
+#pragma unroll
+            for (int i = 0; i < 3; i++) st[u][i] = conv_state[(uint64_t)cc[u] * 3 + i];
+#pragma unroll
+            for (int r = 0; r < RC; r++) {
+                const float xv = qkv[(uint64_t)min(r, R - 1) * g.conv_dim + cc[u]];
+                x[u][r] = r < R ? xv : 0.0f;
+            }
         }
-#pragma unroll
-        for (int r = 0; r < RC; r++) {
-            const float xv = qkv[(uint64_t)min(r, R - 1) * g.conv_dim + cc[u]];
-            x[u][r] = r < R ? xv : 0.0f;
-        }
-    }
-    if (K == 4) {  // the models' conv width: every index below is a compile-time constant
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             if (u == 1 && c1 < 0) break;
@@ -337,6 +335,19 @@ __device__ __forceinline__ void conv_channel2(const float *conv_state, const flo
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         if (u == 1 && c1 < 0) break;
+        float w[8], st[8], x[RC];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float wv = conv_w[(uint64_t)cc[u] * K + min(i, K - 1)];
+            const float sv = conv_state[(uint64_t)cc[u] * (K - 1) + min(i, K - 2)];
+            w[i] = i < K ? wv : 0.0f;
+            st[i] = i < K - 1 ? sv : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < RC; r++) {
+            const float xv = qkv[(uint64_t)min(r, R - 1) * g.conv_dim + cc[u]];
+            x[r] = r < R ? xv : 0.0f;
+        }
         float *dst = u == 0 ? dst0 : dst1;
         const int stride = u == 0 ? stride0 : stride1;
 #pragma unroll
@@ -350,17 +361,17 @@ __device__ __forceinline__ void conv_channel2(const float *conv_state, const flo
                 float xv = 0.0f;
 #pragma unroll
                 for (int q = 0; q < RC; q++)
-                    if (q == idx) xv = x[u][q];
+                    if (q == idx) xv = x[q];
 #pragma unroll
                 for (int q = 0; q < 7; q++)
-                    if (q == K - 1 + idx && idx < 0) xv = st[u][q];
-                sum = __fadd_rn(sum, __fmul_rn(w[u][tt], xv));
+                    if (q == K - 1 + idx && idx < 0) xv = st[q];
+                sum = __fadd_rn(sum, __fmul_rn(w[tt], xv));
             }
             float wl = 0.0f;
 #pragma unroll
             for (int q = 0; q < 8; q++)
-                if (q == K - 1) wl = w[u][q];
-            sum = __fadd_rn(sum, __fmul_rn(wl, x[u][r]));
+                if (q == K - 1) wl = w[q];
+            sum = __fadd_rn(sum, __fmul_rn(wl, x[r]));
             dst[r * stride] = silu_ref(sum);
         }
     }
@@ -483,7 +494,7 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
     YK_GD_STAMP(5);
 #ifdef YK_GD_TIMING
     if (yk_gd_dbg && lane == 0) {
-        uint64_t *o = yk_gd_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave) * 8;
+        uint64_t *o = yk_gd_dbg + ((((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 4 + wave) * 8;
         for (int e = 0; e < 8; e++) o[e] = ts[e];
     }
 #endif
@@ -606,6 +617,9 @@ hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, c
     // row capacity of the conv registers: the smallest instantiation that holds the rows
     if (g.rows <= 8)
         gdn_verify_cols_kernel<8><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
+            conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
+    else if (g.rows <= 12)
+        gdn_verify_cols_kernel<12><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
             conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
     else if (g.rows <= 16)
         gdn_verify_cols_kernel<16><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
