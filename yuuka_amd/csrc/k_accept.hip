@@ -252,27 +252,49 @@ __device__ __forceinline__ void scan_buckets(SelShared &s, bool descending, bool
 // The need-th smallest id (1-based) among the elements with order key `key`
 // that lie inside `cut`.
 __device__ int select_id(const float *p, int V, SelShared &s, uint32_t key, Cut cut, uint32_t need) {
-    if (threadIdx.x == 0) {
-        s.prefix = 0u;
-        s.before_c = 0u;
-        s.before_w = 0.0;
+    // One ordered sweep: 8 slices of kSelWaves * 64 consecutive ids per
+    // step, the matches of each wave counted by ballot, and the step where
+    // the running count reaches `need` resolved by rank.
+    constexpr int kT = kSelWaves * 64, kU = 8;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (threadIdx.x == 0) s.id = INT_MAX;
+    uint32_t before = 0u;
+    for (int base = 0; base < V; base += kU * kT) {
+        float l[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int j = base + u * kT + threadIdx.x;
+            l[u] = p[min(j, V - 1)];
+        }
+        bool m[kU];
+        uint64_t bal[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int j = base + u * kT + threadIdx.x;
+            m[u] = j < V && valid_logit(l[u]) && order_key(l[u]) == key && in_cut(key, j, cut);
+            bal[u] = __ballot(m[u]);
+            if (lane == 0) s.cnt[u][wave] = (uint32_t)__popcll(bal[u]);
+        }
+        __syncthreads();
+        uint32_t tot = 0u;
+        for (int q = 0; q < kU * kSelWaves; q++) tot += s.cnt[q / kSelWaves][q % kSelWaves];
+        if (before + tot >= need) {
+            uint32_t r = before;
+#pragma unroll
+            for (int u = 0; u < kU; u++) {
+                uint32_t pw = 0u;
+                for (int q = 0; q < kSelWaves; q++) pw += q < wave ? s.cnt[u][q] : 0u;
+                const uint32_t rank = r + pw + (uint32_t)__popcll(bal[u] & ((1ull << lane) - 1ull)) + 1u;
+                if (m[u] && rank == need) s.id = base + u * kT + threadIdx.x;
+                for (int q = 0; q < kSelWaves; q++) r += s.cnt[u][q];
+            }
+            break;
+        }
+        before += tot;
+        __syncthreads();  // the counts are read before the next step overwrites them
     }
     __syncthreads();
-    for (int pass = 0; pass < 4; pass++) {
-        const int shift = 24 - 8 * pass;
-        const uint32_t mask = pass ? ~0u << (shift + 8) : 0u;
-        const uint32_t pre = s.prefix;
-        hist_pass<false>(
-            p, V, 0.f, 1.0, s,
-            [=](float l, int j) {
-                const uint32_t k = order_key(l);
-                return k == key && in_cut(k, j, cut) && ((uint32_t)j & mask) == pre;
-            },
-            [=](float, int j) { return ((uint32_t)j >> shift) & 255u; });
-        if (threadIdx.x == 0) scan_buckets(s, false, false, need, 0.0, shift);
-        __syncthreads();
-    }
-    const int id = (int)s.prefix;
+    const int id = s.id;
     __syncthreads();  // every thread has read the result before the state is reused
     return id;
 }
