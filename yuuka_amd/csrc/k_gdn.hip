@@ -618,9 +618,6 @@ hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, c
     if (g.rows <= 8)
         gdn_verify_cols_kernel<8><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
             conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
-    else if (g.rows <= 12)
-        gdn_verify_cols_kernel<12><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
-            conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
     else if (g.rows <= 16)
         gdn_verify_cols_kernel<16><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
             conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
