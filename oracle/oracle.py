@@ -241,6 +241,7 @@ def _declare_q35(L):
         "orc_q35_snapshot": (None, [vp, vp]),
         "orc_q35_restore": (C.c_int, [vp, vp, C.c_uint64]),
         "orc_q35_forward": (C.c_int, [C.POINTER(orc_q35_model), vp, vp, i32, i32, vp, vp]),
+        "orc_q35_forward_residual": (C.c_int, [C.POINTER(orc_q35_model), vp, vp, i32, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -309,6 +310,25 @@ class Q35:
         if rc != 0:
             raise RuntimeError(f"orc_q35_forward failed ({rc})")
         return out if all_logits else out[0]
+
+    def forward_residual(self, tokens) -> np.ndarray:
+        """The residual stream after the last layer, one row per token."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.zeros((t.size, self.cfg.hidden), np.float32)
+        rc = lib().orc_q35_forward_residual(C.byref(self.model), self.state, _ptr(t), t.size, _ptr(out))
+        if rc != 0:
+            raise RuntimeError(f"orc_q35_forward_residual failed ({rc})")
+        return out
+
+    def forward_hidden(self, tokens) -> tuple[np.ndarray, np.ndarray]:
+        """PrefillLogits plus the normalized hidden rows: (logits, hidden)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = np.zeros((t.size, self.cfg.vocab), np.float32)
+        hid = np.zeros((t.size, self.cfg.hidden), np.float32)
+        rc = lib().orc_q35_forward(C.byref(self.model), self.state, _ptr(t), t.size, 1, _ptr(out), _ptr(hid))
+        if rc != 0:
+            raise RuntimeError(f"orc_q35_forward failed ({rc})")
+        return out, hid
 
     def snapshot(self):
         n = lib().orc_q35_snapshot_bytes(self.state)

@@ -585,7 +585,7 @@ static int forward_recurrent(const orc_q35_model *m, int32_t index, const orc_q3
 
 /* forward.go:116-155 */
 static int forward_one(const orc_q35_model *m, orc_q35_state *s, int32_t token, int want_logits,
-                       float *logits, float *hidden_out) {
+                       float *logits, float *hidden_out, float *residual_out) {
     const orc_q35_config *c = &m->cfg;
     if (s->pos >= s->capacity) return -4;
     uint64_t rb = orc_row_bytes(m->embedding.dtype, (uint64_t)c->hidden);
@@ -597,6 +597,7 @@ static int forward_one(const orc_q35_model *m, orc_q35_state *s, int32_t token, 
                                     : forward_full(m, i, &m->layers[i], s);
         if (rc) return rc;
     }
+    if (residual_out) memcpy(residual_out, s->x, (size_t)c->hidden * 4);
     orc_rmsnorm(s->norm, s->x, m->output_norm, c->hidden, c->eps);
     if (hidden_out) memcpy(hidden_out, s->norm, (size_t)c->hidden * 4);
     if (want_logits && matvec(m, &m->output, logits, s->norm)) return -1;
@@ -613,7 +614,22 @@ int orc_q35_forward(const orc_q35_model *m, orc_q35_state *s, const int32_t *tok
         int want = all_logits || i == n - 1;
         float *dst = all_logits ? logits + (int64_t)i * m->cfg.vocab : logits;
         float *hid = hidden_out ? hidden_out + (int64_t)(all_logits ? i : 0) * m->cfg.hidden : NULL;
-        int rc = forward_one(m, s, tokens[i], want, dst, hid);
+        int rc = forward_one(m, s, tokens[i], want, dst, hid, NULL);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+/* forward.go:116-155 without the output head: the residual stream after the
+ * last layer, [n, hidden] (test hook for closed-form layer checks). */
+int orc_q35_forward_residual(const orc_q35_model *m, orc_q35_state *s, const int32_t *tokens,
+                             int32_t n, float *residual_out) {
+    if (n <= 0) return -6;
+    if (s->pos + n > s->capacity) return -7;
+    for (int32_t i = 0; i < n; i++) {
+        if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab) return -8;
+        int rc = forward_one(m, s, tokens[i], 0, NULL, NULL,
+                             residual_out + (int64_t)i * m->cfg.hidden);
         if (rc) return rc;
     }
     return 0;

@@ -117,6 +117,11 @@ int orc_q35_restore(orc_q35_state *st, const uint8_t *data, uint64_t bytes);
 int orc_q35_forward(const orc_q35_model *m, orc_q35_state *st, const int32_t *tokens, int32_t n,
                     int32_t all_logits, float *logits, float *hidden_out);
 
+/* The residual stream after the last layer for each of n tokens, [n, hidden]
+ * (forward.go:116-155 up to the output norm); no logits are computed. */
+int orc_q35_forward_residual(const orc_q35_model *m, orc_q35_state *st, const int32_t *tokens,
+                             int32_t n, float *residual_out);
+
 /* Pieces exposed for kernel-level parity tests. */
 void orc_rmsnorm(float *dst, const float *src, const float *weight, int32_t n, float eps);
 void orc_rmsnorm_inplace(float *x, const float *weight, int32_t n, float eps);

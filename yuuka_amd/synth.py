@@ -71,3 +71,25 @@ def config1(seed: int = 0):
     logits = rng.normal(0.0, 3.0, size=(k + 1, V)).astype(np.float32)
     drafts = rng.integers(0, V, size=k, dtype=np.int32)
     return dict(N=N, K=K, M=M, V=V, k=k, w=w, x=x, logits=logits, drafts=drafts)
+
+
+def q4k_from_int(w: np.ndarray, d: float = 1.0) -> np.ndarray:
+    """Packs an integer matrix with entries in [-8, 7] as Q4_K so that it
+    dequantizes to exactly d * w (tensor/quant.go:96-125 layout): fp16 d and
+    dmin = d, every 6-bit sub-block scale 1 and min 8, nibble = w + 8. d must
+    be representable in fp16. Used to build models whose layers reduce to
+    closed forms."""
+    w = np.asarray(w)
+    rows, cols = w.shape
+    assert cols % 256 == 0 and w.min() >= -8 and w.max() <= 7
+    q = (w + 8).astype(np.uint8).reshape(rows * cols // 256, 4, 2, 32)
+    nb = q.shape[0]
+    b = np.zeros((nb, 144), np.uint8)
+    hd = _f16_bits(np.full(nb, d, np.float32)).view(np.uint8).reshape(nb, 2)
+    b[:, 0:2] = hd
+    b[:, 2:4] = hd
+    b[:, 4:8] = 1            # sub-block scales 0..3 (high bits of 4..7 zero)
+    b[:, 8:12] = 8           # sub-block mins 0..3
+    b[:, 12:16] = 0x81       # scale 1 | min 8 << 4 for sub-blocks 4..7
+    b[:, 16:144] = (q[:, :, 0, :] | (q[:, :, 1, :] << 4)).reshape(nb, 128)
+    return b.reshape(-1)
