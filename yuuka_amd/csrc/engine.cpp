@@ -449,8 +449,9 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
         }
     }
     for (int j = 0; j < nreq; j++) {
-        // the step counter (Philox) advances once per step
-        b.add(YUUKA_EXT_OP_ADVANCE, {q->dyn, q->result, j == 0 ? q->step : nullptr}, {R1}, {}, {}, 0,
+        // the step counter (Philox) advances once per verify step; prefill
+        // chunks leave it alone
+        b.add(YUUKA_EXT_OP_ADVANCE, {q->dyn, q->result, mode == 0 && j == 0 ? q->step : nullptr}, {R1}, {}, {}, 0,
               {dyn_off(j), (uint64_t)(first + j) * 16, 0});
     }
     if (b.st != YUUKA_OK) {
