@@ -56,14 +56,14 @@ def parse():
 
 def ensure_built():
     from yuuka_amd import build as b
-    if not b.LIB.exists():
-        b.build()
-    oracle_so = os.path.join(os.path.dirname(os.path.abspath(__file__)), "oracle", "liboracle.so")
-    if not os.path.exists(oracle_so):
-        b.build_oracle()
+    b.ensure_built()
 
 
 def bench_config1(args):
+    """the v10 LM_HEAD op (the verify GEMM as the Go
+    engine submits it, backend/hip/hip.go:1187-1235) over one Q4_K 9216x2560
+    matrix at M = 5, then the fused greedy acceptance over 5 x 151936 logits,
+    as one plan captured in a HIP graph per weight copy."""
     from yuuka_amd import hip, synth
 
     c = synth.config1(0)
@@ -78,17 +78,28 @@ def bench_config1(args):
     for _ in range(copies - 1):
         ws.append(dev.upload(synth.quant_matrix(rng, synth.Q4_K, N, K)))
     xb = dev.upload(c["x"])
-    xq = dev.alloc(hip.quantized_bytes(K, M))
     out = dev.alloc(M * N * 4)
     lb = dev.upload(c["logits"])
     db = dev.upload(c["drafts"])
     rb = dev.alloc(16)
-    params = hip.accept_params(hip.ACCEPT_GREEDY, 1, k, V)
+    rb2 = dev.alloc(16)
+
+    def lm_head_op(plan, w):
+        plan.add(hip.OP["LM_HEAD"], [w, xb, out], n=[K, N, M], u=[synth.Q4_K])
+
+    def accept_op(plan, mode, res, temperature=0.0):
+        plan.add(hip.OP["ACCEPT"], [lb, db, res], n=[1, k, V, 0, 0, 0], u=[mode, 0, 0, 0], f=[temperature, 1.0])
+
+    plans, graphs = [], []
+    for i in range(copies):
+        p = hip.Plan(dev)
+        lm_head_op(p, ws[i])
+        accept_op(p, hip.ACCEPT_GREEDY, rb)
+        plans.append(p)
+        graphs.append(hip.Graph(p, stream, None))
 
     def step(i):
-        hip.quantize_activations(stream, xq, xb, K, M)
-        hip.gemm_quantized(stream, out, xq, ws[i % copies], K, N, M, synth.Q4_K)
-        hip.verify_accept(stream, lb, db, rb, params)
+        graphs[i % copies].replay(stream)
 
     for i in range(args.warmup):
         step(i)
@@ -106,28 +117,45 @@ def bench_config1(args):
     tokens_per_step = int(res[0]) + 1
     ms_per_step = ms_total / args.steps
 
-    # Dominant kernel alone: the verify GEMM, back-to-back launches.
-    reps = max(50, args.steps)
-    e0.record(stream)
-    for i in range(reps):
-        hip.gemm_quantized(stream, out, xq, ws[i % copies], K, N, M, synth.Q4_K)
-    e1.record(stream)
-    stream.sync()
-    gemm_us = e1.elapsed_ms(e0) * 1e3 / reps
+    def timed_graph(build, reps, launches):
+        p = hip.Plan(dev)
+        for j in range(launches):
+            build(p, j)
+        g = hip.Graph(p, stream, None)
+        g.replay(stream)
+        stream.sync()
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay(stream)
+        e1.record(stream)
+        stream.sync()
+        us = e1.elapsed_ms(e0) * 1e3 / (reps * launches)
+        g.destroy()
+        p.destroy()
+        return us
+
+    # Dominant kernel: LM_HEAD launches back to back in one graph, rotating
+    # the weight copies (each launch streams its matrix from HBM).
+    launches = 4 * copies
+    gemm_us = timed_graph(lambda p, j: lm_head_op(p, ws[j % copies]), 20, launches)
     alg_bytes = wbytes + M * K * 4 + M * N * 4  # W + X + Y (fp32 activations in/out)
     achieved = alg_bytes / (gemm_us * 1e-6) / 1e9
-
-    e0.record(stream)
-    for i in range(reps):
-        hip.verify_accept(stream, lb, db, rb, params)
-    e1.record(stream)
-    stream.sync()
-    accept_us = e1.elapsed_ms(e0) * 1e3 / reps
+    accept_us = timed_graph(lambda p, j: accept_op(p, hip.ACCEPT_GREEDY, rb2), 20, 16)
+    accept_t08_us = timed_graph(lambda p, j: accept_op(p, hip.ACCEPT_STOCHASTIC, rb2, 0.8), 20, 16)
 
     # Correctness of the timed configuration against the oracle.
     from oracle import oracle as O
+    hip.lm_head(stream, out, xb, ws[0], K, N, M, synth.Q4_K)
+    stream.sync()
+    want = O.matmul(O.Q4_K, c["w"], c["x"], N, K)
+    got = out.read(np.float32).reshape(M, N)
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
     a_ref, nxt_ref, _ = O.accept_greedy(c["logits"], c["drafts"])
-    parity = bool(res[0] == a_ref and res[1] == nxt_ref)
+    graphs[0].replay(stream)
+    stream.sync()
+    res0 = rb.read(np.int32)
+    parity = bool(res0[0] == a_ref and res0[1] == nxt_ref and np.max(np.abs(got - want)) <= 1e-3 * rms)
+    traffic = read_traffic("fgemm_config1_lm_head_pmc.md")
 
     line = {
         "metric": "accepted tokens/s on 1 MI355X; verify-step HBM GB/s vs peak",
@@ -143,17 +171,20 @@ def bench_config1(args):
         "dtype": "q4_k weights x int16-split activations, int32/fp32 accumulate",
         "data": "synthetic (seeded, BASELINE configs[0]; weights rotated over %d copies = %.0f MB)"
                 % (copies, copies * wbytes / 2**20),
-        "config": {"workload": "config1: Q4_K 9216x2560 verify GEMM (M=5) + greedy accept V=151936",
+        "config": {"workload": "config1: v10 LM_HEAD Q4_K 9216x2560 verify GEMM (M=5) + greedy accept V=151936",
                    "N": N, "K": K, "rows": M, "drafts": k, "vocab": V, "parallelism": "single GPU"},
         "verify_step_us": ms_per_step * 1e3,
+        "accepted_tokens_per_step": tokens_per_step,
         "gemm_us": gemm_us,
         "accept_us": accept_us,
+        "accept_t0.8_us": accept_t08_us,
         "accept_parity": parity,
         "device": info,
         "wall_s": wall,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "gemm_kq_kernel<Q4_K,1>", "alg_bytes_per_launch": alg_bytes},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel": "fgemm_stream_kernel<12,1,...> (LM_HEAD) Q4_K 9216x2560 M=5",
+                     "alg_bytes_per_launch": alg_bytes, "avg_us": gemm_us},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_config1(c, args.cpu_seconds)

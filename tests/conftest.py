@@ -18,10 +18,7 @@ def pytest_configure(config):
 
 def _ensure_built():
     from yuuka_amd import build as b
-    if not b.LIB.exists():
-        b.build()
-    if not (ROOT / "oracle" / "liboracle.so").exists():
-        b.build_oracle()
+    b.ensure_built()
 
 
 _ensure_built()

@@ -181,3 +181,19 @@ def test_stochastic_generate_is_deterministic(dev, tiny):
     c, _ = eng.generate(prompt, 24, accept=Mdl.accept_struct(mode=1, temperature=0.8, seed=12))
     assert len(c) == 24
     eng.close()
+
+
+def test_eager_plan_execution_equals_graph_replay(dev, tiny, monkeypatch):
+    """YUUKA_Q35_EAGER=1 (profiling) runs the same plans op by op instead
+    of replaying captured graphs: the logits and results are bit-identical."""
+    cfg, w = tiny
+    out = []
+    for eager in ("0", "1"):
+        monkeypatch.setenv("YUUKA_Q35_EAGER", eager)
+        eng = Mdl.Engine(dev, cfg, w)
+        eng.prefill(np.arange(3, 40, dtype=np.int32))
+        res = eng.verify(np.array([4, 5, 6, 7, 8], np.int32))
+        out.append((res.copy(), eng.logits(5)))
+        eng.close()
+    assert np.array_equal(out[0][0], out[1][0])
+    assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))

@@ -77,6 +77,24 @@ def build_oracle(verbose: bool = False) -> Path:
     return oracle / "liboracle.so"
 
 
+def _stale(target: Path, srcs) -> bool:
+    if not target.exists():
+        return True
+    t = target.stat().st_mtime
+    return any(p.stat().st_mtime > t for p in srcs)
+
+
+def ensure_built() -> None:
+    """Builds the library (and the oracle) when missing or older than any of
+    its sources, so that a stale build never runs silently."""
+    hdr = PKG.parent / "include"
+    if _stale(LIB, [*sources(), *CSRC.glob("*.h"), *hdr.glob("*.h")]):
+        build()
+    oracle = PKG.parent / "oracle"
+    if _stale(oracle / "liboracle.so", [*oracle.glob("*.c"), *oracle.glob("*.h"), oracle / "Makefile"]):
+        build_oracle()
+
+
 if __name__ == "__main__":
     build(verbose=True)
     if "--no-oracle" not in sys.argv:

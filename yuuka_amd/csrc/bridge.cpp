@@ -376,13 +376,24 @@ static yuuka_status direct_gemm(const char *what, yuuka_stream *stream, yuuka_bu
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s input buffer is too small", what);
         if (!range_ok(out, 0, n_out * rows * 4))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s output buffer is too small", what);
-        st = ensure_scratch(stream, &stream->scratch, verify_gemm_ws_bytes(n_in, n_out, rows, dtype));
+        yuuka_op op{};
+        op.code = YUUKA_OP_LM_HEAD;
+        op.buf[0] = const_cast<yuuka_buffer *>(w);
+        op.buf[1] = const_cast<yuuka_buffer *>(x);
+        op.buf[2] = out;
+        op.n[0] = n_in;
+        op.n[1] = n_out;
+        op.n[2] = rows;
+        op.u[0] = dtype;
+        uint64_t ws = 0;
+        uint32_t tickets = 0;
+        st = verify_gemm_op_needs(op, &ws, &tickets);
         if (st != YUUKA_OK) return st;
-        st = ensure_scratch(stream, &stream->tickets, (uint64_t)verify_gemm_tickets(n_in, n_out, rows, dtype) * 4 + 4);
+        st = ensure_scratch(stream, &stream->scratch, ws + 256);
         if (st != YUUKA_OK) return st;
-        st = run_verify_gemm(stream->stream, w->ptr, dtype, static_cast<const float *>(x->ptr),
-                             static_cast<float *>(out->ptr), n_in, n_out, rows, stream->scratch.ptr,
-                             static_cast<uint32_t *>(stream->tickets.ptr));
+        st = ensure_scratch(stream, &stream->tickets, (uint64_t)tickets * 4 + 4);
+        if (st != YUUKA_OK) return st;
+        st = run_verify_gemm_op(op, stream->stream, stream->scratch.ptr, static_cast<uint32_t *>(stream->tickets.ptr));
         if (st != YUUKA_OK) return st;
         return record(stream, completion);
     });

@@ -38,7 +38,7 @@ namespace {
 
 using yk::fail;
 
-constexpr int kRowBlock = 16;   // rows of one GEMM launch (split path; fused path upper bound)
+constexpr int kRowBlock = 16;   // rows of one streaming GEMM launch at most
 constexpr int kAttnRows = 8;    // query rows of one verify-attention launch (non-MFMA path)
 
 struct Tensor {
@@ -92,7 +92,7 @@ struct yuuka_q35 {
     Tensor embedding, output;
     yuuka_buffer *output_norm = nullptr;
     // activations [M][...]
-    yuuka_buffer *x = nullptr, *xn = nullptr, *xq = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
+    yuuka_buffer *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr,
                  *attn = nullptr, *z = nullptr, *gdn_out = nullptr, *fg = nullptr, *fu = nullptr, *logits = nullptr,
                  *rope = nullptr;
     // MoE scratch
@@ -200,9 +200,8 @@ struct Builder {
         int per = yk::fused_gemm_stream_rows((int)K0, norm != nullptr, gate != nullptr);
         if (per < 1) per = kRowBlock;
         // more than 8 rows: one launch of the many-row kernel (every weight
-        // read once per 64 rows) unless YUUKA_Q35_ROWBLOCKS=1 asks for blocks
-        const char *rbk = getenv("YUUKA_Q35_ROWBLOCKS");
-        if (rows > 8 && !(rbk && rbk[0] == '1')) per = (int)rows;
+        // read once per 64 rows)
+        if (rows > 8) per = (int)rows;
         const uint64_t blocks = (rows + per - 1) / per;
         for (uint64_t bi = 0; bi < blocks && st == YUUKA_OK; bi++) {
             // equal blocks (rows 40 -> 8 x 5), so no launch is nearly empty
@@ -238,25 +237,7 @@ struct Builder {
             st = yuuka_plan_add(plan, &op);
         }
     }
-    // Split path: quantize + GEMM per block of kRowBlock rows.
-    void split_gemm(const Tensor &w, yuuka_buffer *x, yuuka_buffer *xq, yuuka_buffer *out, uint64_t rows,
-                    yuuka_buffer *residual = nullptr) {
-        for (uint64_t r0 = 0; r0 < rows && st == YUUKA_OK; r0 += kRowBlock) {
-            const uint64_t n = std::min<uint64_t>(kRowBlock, rows - r0);
-            add(YUUKA_EXT_OP_QUANTIZE_X, {x, xq}, {w.cols, n}, {}, {}, 0, {r0 * w.cols * 4, 0});
-            add(YUUKA_EXT_OP_GEMM_Q, {w.b, xq, out, residual}, {w.cols, w.rows, n}, {w.dtype}, {}, 0,
-                {0, 0, r0 * w.rows * 4, residual ? r0 * w.rows * 4 : 0});
-        }
-    }
 };
-
-// Fused projections need Q4_K / Q6_K weights; YUUKA_Q35_FUSED=0 selects the
-// separate quantize / GEMM ops (comparison and fallback; dense model only).
-bool use_fused(const yuuka_q35 *q) {
-    if (const char *e = getenv("YUUKA_Q35_FUSED"))
-        if (e[0] == '0' && q->cfg.n_experts == 0) return false;
-    return true;
-}
 
 struct PlanKey {
     int first, nreq, rows, mode, forced;
@@ -277,17 +258,12 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
     // plan.go:585-588 EMBEDDING_BATCH
     b.add(YUUKA_OP_EMBEDDING_BATCH, {q->embedding.b, q->x, q->tokens},
           {H, R, yk::row_bytes(q->embedding.dtype, H), (uint64_t)c.vocab}, {q->embedding.dtype});
-    const bool fused = use_fused(q);
     const float qscale = (float)(1.0 / std::sqrt((double)c.state_size));
     auto dyn_off = [&](int j) { return (uint64_t)(first + j) * 8; };
-    // YUUKA_Q35_ATTN=0 selects the separate norm / RoPE / KV-write /
-    // attention ops (comparison; one request at request 0 only); by default
-    // ATTN_VERIFY ops with their own position per request.
-    const char *attn_env = getenv("YUUKA_Q35_ATTN");
-    const bool attn_fused = !(attn_env && attn_env[0] == '0' && nreq == 1 && first == 0);
+    // attention: ATTN_VERIFY ops with their own position per request
     bool any_attn = false;
     for (const Layer &L : q->layers) any_attn |= !L.recurrent;
-    if (attn_fused && any_attn)  // every request's rotation table in one op (request rows R1 apart)
+    if (any_attn)  // every request's rotation table in one op (request rows R1 apart)
         b.add(YUUKA_EXT_OP_ROPE_TABLE, {q->rope}, {R1, (uint64_t)c.rope_dim, 0, (uint64_t)nreq, R1}, {},
               {(float)c.rope_base}, 0, {0}, q->dyn, dyn_off(0));
     // the recurrent scan of every request in one op (requests in grid z;
@@ -307,7 +283,7 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
         }
     };
     auto attention = [&](Layer &L) {
-        if (attn_fused) {
+        {
             // one op per block of kAttnRows query rows, every request in it
             // (grid z; request rows R1 apart, tables max_blocks apart)
             const uint32_t packed = (uint32_t)c.rope_dim | ((uint32_t)nreq << 8) | ((uint32_t)R1 << 20);
@@ -328,19 +304,7 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
                        (uint64_t)first * q->max_blocks * 4, 0, 0, r0 * half * 8},
                       q->dyn, dyn_off(0));
             }
-            return;
         }
-        b.add(YUUKA_OP_RMSNORM_HEADS_BATCH, {q->k, L.k_norm, q->k}, {hd, (uint64_t)c.kv_heads, hd, R}, {}, {c.eps});
-        b.add(YUUKA_OP_ROPE_BATCH, {q->k}, {(uint64_t)c.kv_heads, hd, hd, (uint64_t)c.rope_dim, R, kvdim}, {0},
-              {(float)c.rope_base});
-        b.add(YUUKA_OP_KV_WRITE_BATCH_PAGED, {q->k, q->v, L.kpool, L.vpool, q->table}, {kvdim, R},
-              {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype});
-        b.add(YUUKA_OP_RMSNORM_HEADS_BATCH, {q->q, L.q_norm, q->q}, {hd, (uint64_t)c.heads, 2 * hd, R}, {}, {c.eps});
-        b.add(YUUKA_OP_ROPE_BATCH, {q->q}, {(uint64_t)c.heads, 2 * hd, hd, (uint64_t)c.rope_dim, R, qdim}, {0},
-              {(float)c.rope_base});
-        b.add(YUUKA_OP_ATTENTION_PREFILL_PAGED, {q->q, L.kpool, L.vpool, q->attn, q->table},
-              {(uint64_t)c.kv_heads, (uint64_t)c.heads, hd, kvdim, R, 0},
-              {(uint32_t)c.block_size, (uint32_t)c.capacity, c.kv_dtype, 0}, {(float)(1.0 / std::sqrt((double)hd))});
     };
     // forward.go:320-389 forwardMoEFFN over all rows: router, top-k binning,
     // grouped expert SwiGLU and down projections, shared expert, weighted sum.
@@ -363,63 +327,35 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
     };
     for (int i = 0; i < c.n_layers; i++) {
         Layer &L = q->layers[i];
-        if (fused) {
-            if (L.recurrent) {  // plan.go:806-913
-                // z is stored as SiLU(z); the scan writes raw per-head outputs
-                // and the out projection applies the gated RMSNorm in its
-                // prologue (recurrent.go:39-50)
-                // beta is stored as sigmoid(beta), alpha as the decay
-                // exp(softplus(alpha + dt) * a) (recurrent.go:66-70)
-                b.fused(q->x, L.attn_norm, c.eps, R,
-                        {{&L.qkv, L.qkv_rows, nullptr}, {&L.gate, q->z, nullptr}, {&L.beta, L.beta_rows, nullptr},
-                         {&L.alpha, L.alpha_rows, L.dt_a}},
-                        0, (1u << 4) | (2u << 8) | (3u << 12));
-                recurrent(L, YUUKA_EXT_FLAG_RAW_OUT | YUUKA_EXT_FLAG_GDN_COEF);
-                b.fused(q->gdn_out, nullptr, c.eps, R, {{&L.out, q->x, q->x}}, 1, 0, q->z, L.ssm_norm);
-            } else {  // plan.go:684-804
-                b.fused(q->x, L.attn_norm, c.eps, R,
-                        {{&L.q, q->q, nullptr}, {&L.k, q->k, nullptr}, {&L.v, q->v, nullptr}}, 0);
-                attention(L);
-                b.fused(q->attn, nullptr, 0.0f, R, {{&L.o, q->x, q->x}}, 1);
-            }
-            if (L.moe) {
-                moe_ffn(L);
-            } else {
-                // plan.go:915-988 FFN: norm + gate/up + SwiGLU in one op, down + residual
-                b.fused(q->x, L.post_norm, c.eps, R, {{&L.ffn_gate, q->fg, nullptr}, {&L.ffn_up, nullptr, nullptr}},
-                        2);
-                b.fused(q->fg, nullptr, 0.0f, R, {{&L.ffn_down, q->x, q->x}}, 1);
-            }
-            continue;
-        }
-        b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, L.attn_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
-        if (L.recurrent) {
-            b.split_gemm(L.qkv, q->xn, q->xq, L.qkv_rows, R);
-            b.split_gemm(L.gate, q->xn, q->xq, q->z, R);
-            b.split_gemm(L.beta, q->xn, q->xq, L.beta_rows, R);
-            b.split_gemm(L.alpha, q->xn, q->xq, L.alpha_rows, R);
-            recurrent(L, 0);
-            b.split_gemm(L.out, q->gdn_out, q->xq, q->x, R, q->x);
-        } else {
-            b.split_gemm(L.q, q->xn, q->xq, q->q, R);
-            b.split_gemm(L.k, q->xn, q->xq, q->k, R);
-            b.split_gemm(L.v, q->xn, q->xq, q->v, R);
+        if (L.recurrent) {  // plan.go:806-913
+            // z is stored as SiLU(z); the scan writes raw per-head outputs
+            // and the out projection applies the gated RMSNorm in its
+            // prologue (recurrent.go:39-50)
+            // beta is stored as sigmoid(beta), alpha as the decay
+            // exp(softplus(alpha + dt) * a) (recurrent.go:66-70)
+            b.fused(q->x, L.attn_norm, c.eps, R,
+                    {{&L.qkv, L.qkv_rows, nullptr}, {&L.gate, q->z, nullptr}, {&L.beta, L.beta_rows, nullptr},
+                     {&L.alpha, L.alpha_rows, L.dt_a}},
+                    0, (1u << 4) | (2u << 8) | (3u << 12));
+            recurrent(L, YUUKA_EXT_FLAG_RAW_OUT | YUUKA_EXT_FLAG_GDN_COEF);
+            b.fused(q->gdn_out, nullptr, c.eps, R, {{&L.out, q->x, q->x}}, 1, 0, q->z, L.ssm_norm);
+        } else {  // plan.go:684-804
+            b.fused(q->x, L.attn_norm, c.eps, R,
+                    {{&L.q, q->q, nullptr}, {&L.k, q->k, nullptr}, {&L.v, q->v, nullptr}}, 0);
             attention(L);
-            b.split_gemm(L.o, q->attn, q->xq, q->x, R, q->x);
+            b.fused(q->attn, nullptr, 0.0f, R, {{&L.o, q->x, q->x}}, 1);
         }
-        b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, L.post_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
-        b.split_gemm(L.ffn_gate, q->xn, q->xq, q->fg, R);
-        b.split_gemm(L.ffn_up, q->xn, q->xq, q->fu, R);
-        b.add(YUUKA_OP_SILU_MUL, {q->fg, q->fu, q->fg}, {R * (uint64_t)c.ffn});
-        b.split_gemm(L.ffn_down, q->fg, q->xq, q->x, R, q->x);
+        if (L.moe) {
+            moe_ffn(L);
+        } else {
+            // plan.go:915-988 FFN: norm + gate/up + SwiGLU in one op, down + residual
+            b.fused(q->x, L.post_norm, c.eps, R, {{&L.ffn_gate, q->fg, nullptr}, {&L.ffn_up, nullptr, nullptr}},
+                    2);
+            b.fused(q->fg, nullptr, 0.0f, R, {{&L.ffn_down, q->x, q->x}}, 1);
+        }
     }
     // plan.go:635-662 all-logits tail
-    if (fused) {
-        b.fused(q->x, q->output_norm, c.eps, R, {{&q->output, q->logits, nullptr}}, 0);
-    } else {
-        b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, q->output_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
-        b.split_gemm(q->output, q->xn, q->xq, q->logits, R);
-    }
+    b.fused(q->x, q->output_norm, c.eps, R, {{&q->output, q->logits, nullptr}}, 0);
     if (mode == 0) {
         const yuuka_q35_accept &a = q->accept_cfg;
         // drafts are tokens[j][1..k]; request index j of this plan is
@@ -443,7 +379,7 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
                    q->result},
                   {R1, (uint64_t)c.groups, (uint64_t)c.rank, (uint64_t)c.state_size, cd, (uint64_t)c.inner},
                   {(uint32_t)c.conv_kernel, commit_together ? (uint32_t)nreq : 1u}, {},
-                  fused ? YUUKA_EXT_FLAG_GDN_COEF : 0u,
+                  YUUKA_EXT_FLAG_GDN_COEF,
                   {rq * L.conv_bytes, rq * L.mat_bytes, r0 * cd * 4, r0 * cd * 4, r0 * c.rank * 4, r0 * c.rank * 4, 0,
                    0, rq * 16});
         }
@@ -790,10 +726,8 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
             }
         }
         const uint64_t ffn_w = moe ? (uint64_t)c.shared_ffn : (uint64_t)c.ffn;
-        const uint64_t kmax = std::max<uint64_t>({H, ffn_w, (uint64_t)c.inner, (uint64_t)c.heads * hd});
         CHK(alloc(q.get(), M * H * 4, &q->x));
         CHK(alloc(q.get(), M * H * 4, &q->xn));
-        CHK(alloc(q.get(), yk::gemm_plan(kmax, 1, kRowBlock, YUUKA_DTYPE_Q4_K).xq_bytes + 256, &q->xq));
         CHK(alloc(q.get(), M * qdim * 4, &q->q));
         CHK(alloc(q.get(), M * kvdim * 4, &q->k));
         CHK(alloc(q.get(), M * kvdim * 4, &q->v));

@@ -1114,7 +1114,7 @@ hipError_t launch_rope_table(float2 *tab, int rows, int rot_dim, double base, co
 // it walks the verify rows in blocks of kMQ / G, so up to 32 rows a launch.
 bool attn_verify_mfma(int fmt, int heads, int kv_heads, int head_dim, int rope_dim, int kv_dim) {
     return fmt == 1 && head_dim == kMD && rope_dim == 64 && kv_heads > 0 && heads / kv_heads <= kMQ &&
-           kv_dim % 8 == 0 && !getenv("YUUKA_ATTN_FMA");
+           kv_dim % 8 == 0;
 }
 
 int attn_verify_max_rows(const AttnVArgs &a) {

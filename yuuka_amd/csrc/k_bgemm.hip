@@ -708,7 +708,7 @@ static void bg_grid(const int *n, int nseg, bool swiglu, int rows, int K, unsign
         for (int i = 0; i < nseg; i++) x += (unsigned)((n[i] + 16 * kBgWaves - 1) / (16 * kBgWaves));
     *gx = x;
     *gy = (unsigned)((rows + kBgRows - 1) / kBgRows);
-    *splits = getenv("YUUKA_BG_NOSPLIT") ? 1 : bg_splits((int)(x * *gy), K / 256);
+    *splits = bg_splits((int)(x * *gy), K / 256);
 }
 
 uint64_t fused_gemm_rows_ws(int rows, int K, const int *n, int nseg, bool swiglu) {

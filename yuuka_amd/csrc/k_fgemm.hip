@@ -1413,7 +1413,7 @@ static bool stream_shape(const FusedGemmArgs &a, int tt, bool mixed, int *ku, in
     if (*ku > cap) return false;
     const ActLayout L(a.rows, 1, nsb, nsb, *mode == 1, -1, *mode == 2, false);
     const int R = std::min(a.groups, device_cus());
-    *balanced = (a.groups + R - 1) / R <= kBalMax && !getenv("YUUKA_FGEMM_UNBALANCED");
+    *balanced = (a.groups + R - 1) / R <= kBalMax;
     *lds = L.total + kInvBytes + (uint32_t)kWaves * (*balanced ? kBalMax : 1) * tt * 4 * 64 * 4;
     return *lds <= kFusedLds;
 }
@@ -1467,7 +1467,7 @@ hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s) {
     int ku = 0, mode = 0;
     uint32_t slds = 0;
     bool bal = false;
-    if (!getenv("YUUKA_FGEMM_CHUNKED") && stream_shape(b, tt, mixed, &ku, &mode, &slds, &bal)) {
+    if (stream_shape(b, tt, mixed, &ku, &mode, &slds, &bal)) {
         if (mixed) return launch_stream_ku<0, 1>(b, ku, mode, slds, bal, s);
         if (b.seg[0].dtype == kQ4K)
             return tt == 1 ? launch_stream_ku<kQ4K, 1>(b, ku, mode, slds, bal, s)

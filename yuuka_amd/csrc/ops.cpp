@@ -97,30 +97,16 @@ static int fused_segments(const yuuka_op &op) {
     return n;
 }
 
-// Tiles per workgroup: the largest of 4, 2, 1 that still gives every CU
-// work (about 2 workgroups per CU); Q6_K holds more staging registers and
-// stops at 2. YUUKA_FGEMM_TT overrides (tuning).
 // 16-row tiles per group: one (the persistent group loop supplies the
 // parallelism and keeps registers within one workgroup of eight waves per
-// CU); SwiGLU needs a gate and an up tile. YUUKA_FGEMM_TT overrides (tuning).
-static int fused_tiles(const yuuka_op &op, int nseg) {
-    bool q6 = false;
-    for (int i = 0; i < nseg; i++) q6 |= ((op.u[0] >> (8 * i)) & 0xff) == YUUKA_DTYPE_Q6_K;
-    int tt = 1;
-    if (const char *e = getenv("YUUKA_FGEMM_TT")) {
-        const int v = atoi(e);
-        if (v == 1 || v == 2 || v == 4) tt = v;
-    }
-    if (q6 && tt > 2) tt = 2;
-    if (op.u[1] == kEpiSwiglu && tt < 2) tt = 2;
-    return tt;
+// CU); SwiGLU needs a gate and an up tile.
+static int fused_tiles(const yuuka_op &op, int) {
+    return op.u[1] == kEpiSwiglu ? 2 : 1;
 }
 
-// Rows beyond what one fused launch serves from LDS go to the many-row
-// kernel (YUUKA_FGEMM_CHUNKED keeps 9..16 rows on the chunked kernel).
+// More than 8 rows go to the many-row kernel (k_bgemm.hip).
 static bool fused_many_rows(const yuuka_op &op) {
-    if (op.n[1] > 16) return true;
-    return op.n[1] > 8 && !getenv("YUUKA_FGEMM_CHUNKED");
+    return op.n[1] > 8;
 }
 
 static FusedGemmArgs fused_args(const yuuka_op &op) {
@@ -539,7 +525,7 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
 }
 
 int gdn_commit_run(const yuuka_op *ops, int count) {
-    if (count < 2 || ops[0].code != YUUKA_EXT_OP_GDN_COMMIT || getenv("YUUKA_GDN_SPLIT")) return 1;
+    if (count < 2 || ops[0].code != YUUKA_EXT_OP_GDN_COMMIT) return 1;
     const GdnArgs g0 = gdn_args(ops[0]);
     if (g0.rows > 32) return 1;
     int n = 1;
@@ -638,7 +624,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
                                          at<const float>(op, 7), at<const float>(op, 8), at<float>(op, 10), conv, g, s);
             break;
         }
-        if (defer && g.rows <= 16 && !getenv("YUUKA_GDN_SPLIT")) {  // one fused kernel per layer (k_gdn.hip)
+        if (defer && g.rows <= 16) {  // one fused kernel per layer (k_gdn.hip)
             err = launch_gdn_verify(at<const float>(op, 0), at<const float>(op, 1), at<const float>(op, 2),
                                     at<const float>(op, 3), at<const float>(op, 4), at<const float>(op, 5),
                                     at<const float>(op, 6), at<const float>(op, 7), at<const float>(op, 8),
@@ -696,7 +682,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
     case YUUKA_EXT_OP_GDN_COMMIT: {
         const GdnArgs g = gdn_args(op);
         const int32_t *res = at<const int32_t>(op, 8);
-        if ((!getenv("YUUKA_GDN_SPLIT") || g.nreq > 1) && g.rows <= 32) {  // scan replay + conv window, column-split (k_gdn.hip)
+        if (g.rows <= 32) {  // scan replay + conv window, column-split (k_gdn.hip)
             err = launch_gdn_commit_cols(at<float>(op, 0), at<float>(op, 1), at<const float>(op, 2), at<const float>(op, 3),
                                     at<const float>(op, 4), at<const float>(op, 5), at<const float>(op, 6),
                                     at<const float>(op, 7), g, res, s);

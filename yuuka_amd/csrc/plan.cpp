@@ -28,6 +28,50 @@ struct Need {
     uint32_t tickets = 0;
 };
 
+// LM_HEAD / GEMV_BATCH as the fused verify GEMM (GEMM_FUSED with one
+// segment and the store epilogue, no norm): the streaming kernel for up to 8
+// rows, the many-row kernel beyond. True when that op serves the shape (its
+// workspace in *ws); otherwise the split quantize + GEMM kernels run it.
+static bool fused_form(const yuuka_op &op, yuuka_op *f, uint64_t *ws) {
+    *f = yuuka_op{};
+    f->code = YUUKA_EXT_OP_GEMM_FUSED;
+    if (op.code == YUUKA_OP_GEMM_SWIGLU) {
+        // hip.go:1149-1176: buf0 gate W, buf1 up W, buf2 x, buf3 out;
+        // n = {K, N, rows}; out = SiLU(x gate^T) * (x up^T)
+        f->buf[0] = op.buf[2];
+        f->off[0] = op.off[2];
+        f->buf[2] = op.buf[0];
+        f->off[2] = op.off[0];
+        f->buf[3] = op.buf[1];
+        f->off[3] = op.off[1];
+        f->buf[6] = op.buf[3];
+        f->off[6] = op.off[3];
+        f->n[0] = op.n[0];
+        f->n[1] = op.n[2];
+        f->n[2] = f->n[3] = op.n[1];
+        f->u[0] = op.u[0] | (op.u[0] << 8);
+        f->u[1] = 2;  // SwiGLU epilogue
+        uint64_t need = 0;
+        if (validate_model_op(*f, &need) != YUUKA_OK) return false;
+        *ws = need;
+        return true;
+    }
+    f->buf[0] = op.buf[1];
+    f->off[0] = op.off[1];
+    f->buf[2] = op.buf[0];
+    f->off[2] = op.off[0];
+    f->buf[6] = op.buf[2];
+    f->off[6] = op.off[2];
+    f->n[0] = op.n[0];
+    f->n[1] = op.n[2];
+    f->n[2] = op.n[1];
+    f->u[0] = op.u[0];
+    uint64_t need = 0;
+    if (validate_model_op(*f, &need) != YUUKA_OK) return false;
+    *ws = need;
+    return true;
+}
+
 static yuuka_status validate(const yuuka_op &op, Need *need) {
     switch (op.code) {
     case YUUKA_OP_LM_HEAD:
@@ -47,8 +91,36 @@ static yuuka_status validate(const yuuka_op &op, Need *need) {
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify GEMM input buffer is too small");
         if (!buf_ok(op.buf[2], op.off[2], N * rows * 4))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify GEMM output buffer is too small");
+        yuuka_op f;
+        if (fused_form(op, &f, &need->ws)) return YUUKA_OK;
         need->ws = verify_gemm_ws_bytes(K, N, rows, op.u[0]);
         need->tickets = verify_gemm_tickets(K, N, rows, op.u[0]);
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_GEMM_SWIGLU: {
+        for (int i = 0; i < 4; i++)
+            if (!op.buf[i]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM_SWIGLU buffer %d is null", i);
+        yuuka_status st = check_verify_gemm(op.n[0], op.n[1], op.n[2], op.u[0], 512);
+        if (st != YUUKA_OK) return st;
+        yuuka_op f;
+        if (!fused_form(op, &f, &need->ws))
+            return fail(YUUKA_ERR_UNSUPPORTED, "GEMM_SWIGLU shape %llux%llu at %llu rows is not served",
+                        (unsigned long long)op.n[1], (unsigned long long)op.n[0], (unsigned long long)op.n[2]);
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_GEMM: {
+        // hip.go:966-997 AddGemmPathAt (the WMMA route SelectPrefillPath
+        // picks for 8..127 rows with few outputs): served for Q4_K / Q6_K
+        // weights by the fused verify GEMM; F32/F16 weights are not.
+        for (int i = 0; i < 3; i++)
+            if (!op.buf[i]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "GEMM buffer %d is null", i);
+        const uint64_t K = op.n[0], N = op.n[1], rows = op.n[2];
+        yuuka_status st = check_verify_gemm(K, N, rows, op.u[0], 512);
+        if (st != YUUKA_OK) return st;
+        yuuka_op f;
+        if (!fused_form(op, &f, &need->ws))
+            return fail(YUUKA_ERR_UNSUPPORTED, "GEMM shape %llux%llu at %llu rows is not served",
+                        (unsigned long long)N, (unsigned long long)K, (unsigned long long)rows);
         return YUUKA_OK;
     }
     default:
@@ -58,10 +130,21 @@ static yuuka_status validate(const yuuka_op &op, Need *need) {
 
 static yuuka_status execute(const yuuka_op &op, const ExecCtx &ctx) {
     switch (op.code) {
+    case YUUKA_OP_GEMM_SWIGLU:
+    case YUUKA_OP_GEMM: {
+        yuuka_op f;
+        uint64_t ws = 0;
+        if (!fused_form(op, &f, &ws)) return fail(YUUKA_ERR_INTERNAL, "GEMM op changed after validation");
+        return execute_model_op(f, ctx);
+    }
     case YUUKA_OP_LM_HEAD:
-    case YUUKA_OP_GEMV_BATCH:
+    case YUUKA_OP_GEMV_BATCH: {
+        yuuka_op f;
+        uint64_t ws = 0;
+        if (fused_form(op, &f, &ws)) return execute_model_op(f, ctx);
         return run_verify_gemm(ctx.stream, at<const uint8_t>(op, 0), op.u[0], at<const float>(op, 1),
                                at<float>(op, 2), op.n[0], op.n[1], op.n[2], ctx.ws, ctx.tickets);
+    }
     default:
         return execute_model_op(op, ctx);
     }
@@ -169,6 +252,19 @@ static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token,
 using namespace yk;
 
 namespace yk {
+yuuka_status verify_gemm_op_needs(const yuuka_op &op, uint64_t *ws, uint32_t *tickets) {
+    Need need;
+    yuuka_status st = validate(op, &need);
+    *ws = need.ws;
+    *tickets = need.tickets;
+    return st;
+}
+
+yuuka_status run_verify_gemm_op(const yuuka_op &op, hipStream_t stream, void *ws, uint32_t *tickets) {
+    ExecCtx ctx{stream, 0, 0, nullptr, ws, tickets};
+    return execute(op, ctx);
+}
+
 yuuka_status plan_run_dynamic(yuuka_plan *plan, hipStream_t stream, const int32_t *dyn) {
     yuuka_status st = prepare(plan);
     if (st != YUUKA_OK) return st;

@@ -31,6 +31,12 @@ yuuka_status run_verify_gemm(hipStream_t stream, const void *w, uint32_t dtype, 
 uint64_t verify_gemm_ws_bytes(uint64_t n_in, uint64_t n_out, uint64_t rows, uint32_t dtype);
 uint32_t verify_gemm_tickets(uint64_t n_in, uint64_t n_out, uint64_t rows, uint32_t dtype);
 
+// An LM_HEAD / GEMV_BATCH op outside a plan (yuuka_lm_head, yuuka_gemv*):
+// validation with its workspace and ticket needs, then execution on `stream`
+// (the fused verify GEMM where it serves the shape).
+yuuka_status verify_gemm_op_needs(const yuuka_op &op, uint64_t *ws, uint32_t *tickets);
+yuuka_status run_verify_gemm_op(const yuuka_op &op, hipStream_t stream, void *ws, uint32_t *tickets);
+
 // Runs the plan's ops directly on `stream` (no graph), reading {token,
 // position} from the device buffer `dyn` exactly as a captured graph would.
 yuuka_status plan_run_dynamic(yuuka_plan *plan, hipStream_t stream, const int32_t *dyn);

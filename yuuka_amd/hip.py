@@ -26,7 +26,8 @@ OP = dict(
     SILU_MUL=9, ADD=10, COPY=11, GEMV_BATCH=17, RMSNORM_BATCH=18, RMSNORM_HEADS_BATCH=19,
     ROPE_BATCH=20, RECURRENT_CHUNK=23, EMBEDDING_BATCH=24, KV_WRITE_BATCH_PAGED=28,
     ATTENTION_PREFILL_PAGED=29, MOE_ROUTE=30, MOE_GATE_UP=31, MOE_DOWN=32, MOE_REDUCE_ADD=33, LM_HEAD=37,
-    GEMM_FUSED=69, MOE_ROUTER=72, MOE_COMBINE=73,
+    ACCEPT=66, GDN_COMMIT=67, ADVANCE=68, GEMM_FUSED=69, ROPE_TABLE=70, ATTN_VERIFY=71, MOE_ROUTER=72,
+    MOE_COMBINE=73,
 )
 FLAG_MOE_SWIGLU = 0x800
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
