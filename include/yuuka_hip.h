@@ -359,6 +359,25 @@ YUUKA_API yuuka_status yuuka_verify_accept(yuuka_stream * stream,
                         yuuka_buffer * debug, const yuuka_accept_params * params,
                         yuuka_event * completion);
 
+/* yuuka_verify_accept without any allocation. No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments (no debug buffer) and results as yuuka_verify_accept; its
+ * partial results live in one fixed device array per GPU of
+ * YUUKA_NOALLOC_SCRATCH_BYTES, set up by yuuka_device_open. Calls whose
+ * partials exceed it (yuuka_noalloc_accept_bytes) fail with
+ * YUUKA_ERR_INVALID_ARGUMENT before anything is launched: at V = 151936 that
+ * is above about 2048 rows (batch x (drafts + 1)). Every call on one GPU
+ * shares the array: calls that overlap on one GPU (several streams) race;
+ * calls on one stream are ordered. Nothing in the array needs clearing. */
+#define YUUKA_NOALLOC_SCRATCH_BYTES (8u << 20)
+YUUKA_API uint64_t yuuka_noalloc_accept_bytes(const yuuka_accept_params * params);
+YUUKA_API yuuka_status yuuka_verify_accept_noalloc(yuuka_stream * stream,
+                        const yuuka_buffer * logits, uint64_t logits_offset,
+                        const yuuka_buffer * drafts, uint64_t drafts_offset,
+                        yuuka_buffer * result, uint64_t result_offset,
+                        const yuuka_accept_params * params, yuuka_event * completion);
+
 /* Extension plan ops (codes >= 64; layouts below).
  *   QUANTIZE_X: buf0 FP32 x, buf1 quantized block (yuuka_quantized_bytes);
  *               n={n_in, rows}

@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <exception>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -142,6 +143,34 @@ uint32_t yuuka_abi_version(void) { return YUUKA_HIP_ABI_VERSION; }
 uint32_t yuuka_ext_version(void) { return YUUKA_EXT_VERSION; }
 const char *yuuka_last_error(void) { return g_last_error.c_str(); }
 
+// Fixed scratch of yuuka_verify_accept_noalloc. Each GPU the library runs
+// on holds its own copy until the process ends. In host code `scratch` only
+// names the symbol: its device address (per GPU) comes from
+// hipGetSymbolAddress, called once per device with that device current.
+static __device__ __align__(256) uint8_t scratch[YUUKA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's scratch array; the device must be current.
+yuuka_status noalloc_scratch_address(int index, void **out) {
+    if (index < 0 || index >= kMaxDevices)
+        return fail(YUUKA_ERR_UNSUPPORTED, "device index %d beyond the no-allocation table", index);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[index]) {
+        void *p = nullptr;
+        hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !p)
+            return fail(YUUKA_ERR_DEVICE, "scratch symbol address: %s", hip_error(err));
+        g_scratch_ptr[index] = p;
+    }
+    *out = g_scratch_ptr[index];
+    return YUUKA_OK;
+}
+}  // namespace
+
 yuuka_status yuuka_device_open(int32_t index, yuuka_device **out) {
     return guard("device_open", [&]() -> yuuka_status {
         if (!out) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null output handle");
@@ -159,6 +188,11 @@ yuuka_status yuuka_device_open(int32_t index, yuuka_device **out) {
         if (err != hipSuccess) {
             delete dev;
             return fail(YUUKA_ERR_DEVICE, "device properties: %s", hip_error(err));
+        }
+        yuuka_status st = noalloc_scratch_address(index, &dev->noalloc_scratch);
+        if (st != YUUKA_OK) {
+            delete dev;
+            return st;
         }
         *out = dev;
         return YUUKA_OK;
@@ -482,6 +516,32 @@ yuuka_status yuuka_cast_f32_to_f16(yuuka_stream *stream, yuuka_buffer *dst, cons
     });
 }
 
+// Shared argument checks of the acceptance entry points.
+static yuuka_status check_accept(const yuuka_accept_params &p, const yuuka_buffer *logits, uint64_t logits_offset,
+                                 const yuuka_buffer *drafts, uint64_t drafts_offset, const yuuka_buffer *result,
+                                 uint64_t result_offset, const yuuka_buffer *debug) {
+    if (p.mode != YUUKA_ACCEPT_GREEDY && p.mode != YUUKA_ACCEPT_STOCHASTIC)
+        return fail(YUUKA_ERR_INVALID_ARGUMENT, "unknown accept mode %u", p.mode);
+    if (p.batch == 0 || p.vocab == 0 || p.vocab > (1u << 30) || p.drafts > 255)
+        return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid batch %u, drafts %u or vocab %u", p.batch,
+                    p.drafts, p.vocab);
+    if (p.mode == YUUKA_ACCEPT_STOCHASTIC && !(p.top_p >= 0.0f && p.top_p <= 1.0f) && p.top_p != 0.0f)
+        return fail(YUUKA_ERR_INVALID_ARGUMENT, "top-p must be in (0,1]");
+    const uint64_t stride = p.row_stride ? p.row_stride : p.vocab;
+    if (stride < p.vocab) return fail(YUUKA_ERR_INVALID_ARGUMENT, "row stride below vocab");
+    const uint64_t rows = (uint64_t)p.batch * (p.drafts + 1);
+    if (logits_offset % 4 || !range_ok(logits, logits_offset, ((rows - 1) * stride + p.vocab) * 4))
+        return fail(YUUKA_ERR_INVALID_ARGUMENT, "logits buffer too small or misaligned");
+    if (p.drafts > 0 && (!drafts || drafts_offset % 4 ||
+                         !range_ok(drafts, drafts_offset, (uint64_t)p.batch * p.drafts * 4)))
+        return fail(YUUKA_ERR_INVALID_ARGUMENT, "drafts buffer too small or misaligned");
+    if (result_offset % 4 || !range_ok(result, result_offset, (uint64_t)p.batch * 16))
+        return fail(YUUKA_ERR_INVALID_ARGUMENT, "result buffer too small or misaligned");
+    if (debug && !range_ok(debug, 0, rows * 32))
+        return fail(YUUKA_ERR_INVALID_ARGUMENT, "debug buffer too small");
+    return YUUKA_OK;
+}
+
 yuuka_status yuuka_verify_accept(yuuka_stream *stream, const yuuka_buffer *logits,
                                  uint64_t logits_offset, const yuuka_buffer *drafts,
                                  uint64_t drafts_offset, yuuka_buffer *result,
@@ -491,26 +551,10 @@ yuuka_status yuuka_verify_accept(yuuka_stream *stream, const yuuka_buffer *logit
         if (!stream || !logits || !result || !params)
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
         const yuuka_accept_params &p = *params;
-        if (p.mode != YUUKA_ACCEPT_GREEDY && p.mode != YUUKA_ACCEPT_STOCHASTIC)
-            return fail(YUUKA_ERR_INVALID_ARGUMENT, "unknown accept mode %u", p.mode);
-        if (p.batch == 0 || p.vocab == 0 || p.vocab > (1u << 30) || p.drafts > 255)
-            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid batch %u, drafts %u or vocab %u", p.batch,
-                        p.drafts, p.vocab);
-        if (p.mode == YUUKA_ACCEPT_STOCHASTIC && !(p.top_p >= 0.0f && p.top_p <= 1.0f) && p.top_p != 0.0f)
-            return fail(YUUKA_ERR_INVALID_ARGUMENT, "top-p must be in (0,1]");
-        const uint64_t stride = p.row_stride ? p.row_stride : p.vocab;
-        if (stride < p.vocab) return fail(YUUKA_ERR_INVALID_ARGUMENT, "row stride below vocab");
-        const uint64_t rows = (uint64_t)p.batch * (p.drafts + 1);
-        if (logits_offset % 4 || !range_ok(logits, logits_offset, ((rows - 1) * stride + p.vocab) * 4))
-            return fail(YUUKA_ERR_INVALID_ARGUMENT, "logits buffer too small or misaligned");
-        if (p.drafts > 0 && (!drafts || drafts_offset % 4 ||
-                             !range_ok(drafts, drafts_offset, (uint64_t)p.batch * p.drafts * 4)))
-            return fail(YUUKA_ERR_INVALID_ARGUMENT, "drafts buffer too small or misaligned");
-        if (result_offset % 4 || !range_ok(result, result_offset, (uint64_t)p.batch * 16))
-            return fail(YUUKA_ERR_INVALID_ARGUMENT, "result buffer too small or misaligned");
-        if (debug && !range_ok(debug, 0, rows * 32))
-            return fail(YUUKA_ERR_INVALID_ARGUMENT, "debug buffer too small");
-        yuuka_status st = ensure_scratch(stream, &stream->scratch, accept_scratch_bytes(p));
+        yuuka_status st = check_accept(p, logits, logits_offset, drafts, drafts_offset, result, result_offset,
+                                       debug);
+        if (st != YUUKA_OK) return st;
+        st = ensure_scratch(stream, &stream->scratch, accept_scratch_bytes(p));
         if (st != YUUKA_OK) return st;
         const int32_t *dp = p.drafts > 0
                                 ? reinterpret_cast<const int32_t *>(static_cast<const uint8_t *>(drafts->ptr) + drafts_offset)
@@ -519,6 +563,41 @@ yuuka_status yuuka_verify_accept(yuuka_stream *stream, const yuuka_buffer *logit
             reinterpret_cast<const float *>(static_cast<const uint8_t *>(logits->ptr) + logits_offset), dp,
             reinterpret_cast<int32_t *>(static_cast<uint8_t *>(result->ptr) + result_offset),
             debug ? static_cast<double *>(debug->ptr) : nullptr, p, stream->scratch.ptr, stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "accept launch: %s", hip_error(err));
+        return record(stream, completion);
+    });
+}
+
+
+uint64_t yuuka_noalloc_accept_bytes(const yuuka_accept_params *params) {
+    return params ? accept_scratch_bytes(*params) : 0;
+}
+
+yuuka_status yuuka_verify_accept_noalloc(yuuka_stream *stream, const yuuka_buffer *logits,
+                                         uint64_t logits_offset, const yuuka_buffer *drafts,
+                                         uint64_t drafts_offset, yuuka_buffer *result,
+                                         uint64_t result_offset, const yuuka_accept_params *params,
+                                         yuuka_event *completion) {
+    return guard("verify_accept_noalloc", [&]() -> yuuka_status {
+        if (!stream || !stream->dev || !logits || !result || !params)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        const yuuka_accept_params &p = *params;
+        yuuka_status st = check_accept(p, logits, logits_offset, drafts, drafts_offset, result, result_offset,
+                                       nullptr);
+        if (st != YUUKA_OK) return st;
+        const uint64_t need = accept_scratch_bytes(p);
+        if (need > YUUKA_NOALLOC_SCRATCH_BYTES)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT,
+                        "acceptance partials of %llu bytes exceed the fixed scratch of %u bytes",
+                        (unsigned long long)need, (unsigned)YUUKA_NOALLOC_SCRATCH_BYTES);
+        if (!stream->dev->noalloc_scratch) return fail(YUUKA_ERR_DEVICE, "no scratch address for this device");
+        const int32_t *dp = p.drafts > 0
+                                ? reinterpret_cast<const int32_t *>(static_cast<const uint8_t *>(drafts->ptr) + drafts_offset)
+                                : nullptr;
+        hipError_t err = launch_verify_accept(
+            reinterpret_cast<const float *>(static_cast<const uint8_t *>(logits->ptr) + logits_offset), dp,
+            reinterpret_cast<int32_t *>(static_cast<uint8_t *>(result->ptr) + result_offset), nullptr, p,
+            stream->dev->noalloc_scratch, stream->stream);
         if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "accept launch: %s", hip_error(err));
         return record(stream, completion);
     });

@@ -15,6 +15,7 @@
 struct yuuka_device {
     int index = 0;
     hipDeviceProp_t props{};
+    void *noalloc_scratch = nullptr;  // this GPU's copy of the fixed accept scratch array
 };
 
 struct yuuka_buffer {

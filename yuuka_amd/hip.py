@@ -136,6 +136,9 @@ def _declare(L: C.CDLL) -> None:
         "yuuka_dequant_f16": (C.c_int, [vp, vp, vp, u64, u64, u32, vp]),
         "yuuka_verify_accept": (C.c_int, [vp, vp, u64, vp, u64, vp, u64, vp,
                                           C.POINTER(yuuka_accept_params), vp]),
+        "yuuka_verify_accept_noalloc": (C.c_int, [vp, vp, u64, vp, u64, vp, u64, C.POINTER(yuuka_accept_params),
+                                                  vp]),
+        "yuuka_noalloc_accept_bytes": (u64, [C.POINTER(yuuka_accept_params)]),
         "yuuka_event_create_timed": (C.c_int, [vp, C.POINTER(vp)]),
         "yuuka_event_record": (C.c_int, [vp, vp]),
         "yuuka_event_elapsed_ms": (C.c_int, [vp, vp, C.POINTER(C.c_float)]),
