@@ -199,3 +199,22 @@ def test_truncated_acceptance_is_reproducible(dev, stream):
     r1, d1 = _run(dev, stream, logits, drafts, p)
     r2, d2 = _run(dev, stream, logits, drafts, p)
     assert (r1 == r2).all() and np.array_equal(d1, d2)
+
+
+def test_truncation_tie_group_spanning_late_id_steps(dev, stream):
+    """Full vocabulary: a top tie group of 300 equal logits, 40 of them below
+    id 8192 and the rest spread up to the last id, so the top-k / top-p cut
+    falls on a member the kept-id sweep reaches only in a later 8192-id step.
+    The kept set (lowest ids of the group) and every decision match the
+    oracle's."""
+    rng = np.random.default_rng(17)
+    k, V = 4, 151936
+    logits = rng.normal(0, 1, (k + 1, V)).astype(np.float32)
+    ties = np.concatenate([rng.choice(8192, 40, replace=False),
+                           8192 + rng.choice(V - 8192, 260, replace=False)])
+    ties.sort()
+    logits[:, ties] = 10.0
+    drafts = np.array([ties[150], ties[20], ties[299], ties[90]], np.int32)
+    for top_k, top_p in [(120, 1.0), (0, 0.5), (250, 0.3), (41, 1.0)]:
+        for step in range(2):
+            assert _check_truncated(dev, stream, logits, drafts, 1.0, top_k, top_p, 21, step) == 0

@@ -514,7 +514,9 @@ yuuka_status run_step(yuuka_q35 *q, const PlanKey &key, int32_t *result_out) {
 
 int32_t read_pos(const yuuka_q35 *q, int r) {
     int32_t d[2] = {0, 0};
-    (void)hipMemcpy(d, static_cast<const uint8_t *>(q->dyn->ptr) + (uint64_t)r * 8, 8, hipMemcpyDeviceToHost);
+    if (hipMemcpy(d, static_cast<const uint8_t *>(q->dyn->ptr) + (uint64_t)r * 8, 8, hipMemcpyDeviceToHost) !=
+        hipSuccess)
+        return -1;  // reported as an invalid position
     return d[1];
 }
 
@@ -551,13 +553,16 @@ yuuka_status check_tokens(const yuuka_q35 *q, const int32_t *t, size_t n) {
 
 yuuka_status reset_request(yuuka_q35 *q, int r) {
     hipStream_t s = q->stream->stream;
+    hipError_t eq = hipSuccess;  // first enqueue failure
+    auto enq = [&](hipError_t e) { if (eq == hipSuccess) eq = e; };
     for (auto &L : q->layers) {
         if (!L.recurrent) continue;
-        (void)hipMemsetAsync(static_cast<uint8_t *>(L.conv_state->ptr) + (uint64_t)r * L.conv_bytes, 0, L.conv_bytes, s);
-        (void)hipMemsetAsync(static_cast<uint8_t *>(L.mat_state->ptr) + (uint64_t)r * L.mat_bytes, 0, L.mat_bytes, s);
+        enq(hipMemsetAsync(static_cast<uint8_t *>(L.conv_state->ptr) + (uint64_t)r * L.conv_bytes, 0, L.conv_bytes, s));
+        enq(hipMemsetAsync(static_cast<uint8_t *>(L.mat_state->ptr) + (uint64_t)r * L.mat_bytes, 0, L.mat_bytes, s));
     }
-    (void)hipMemsetAsync(static_cast<uint8_t *>(q->dyn->ptr) + (uint64_t)r * 8, 0, 8, s);
+    enq(hipMemsetAsync(static_cast<uint8_t *>(q->dyn->ptr) + (uint64_t)r * 8, 0, 8, s));
     hipError_t err = hipStreamSynchronize(s);
+    if (eq != hipSuccess) return fail(YUUKA_ERR_DEVICE, "reset enqueue: %s", yk::hip_error(eq));
     if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "reset: %s", yk::hip_error(err));
     release_blocks(q, r);
     q->req[r].pos = 0;
@@ -784,8 +789,9 @@ yuuka_status yuuka_q35_reset(yuuka_q35 *q) {
             yuuka_status st = reset_request(q, r);
             if (st != YUUKA_OK) return st;
         }
-        (void)hipMemsetAsync(q->step->ptr, 0, 8, q->stream->stream);
+        hipError_t eq = hipMemsetAsync(q->step->ptr, 0, 8, q->stream->stream);
         hipError_t err = hipStreamSynchronize(q->stream->stream);
+        if (eq != hipSuccess) return fail(YUUKA_ERR_DEVICE, "reset enqueue: %s", yk::hip_error(eq));
         if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "reset: %s", yk::hip_error(err));
         return YUUKA_OK;
     });
@@ -831,6 +837,8 @@ yuuka_status yuuka_q35_fork(yuuka_q35 *q, int32_t src, int32_t dst) {
         const int32_t pos = q->req[src].pos, bs = q->cfg.block_size;
         const int full = pos / bs;
         hipStream_t s = q->stream->stream;
+        hipError_t eq = hipSuccess;  // first enqueue failure
+        auto enq = [&](hipError_t e) { if (eq == hipSuccess) eq = e; };
         Request &d = q->req[dst];
         for (int i = 0; i < full; i++) {  // memory/prefix.go: shared blocks, one more reference each
             const int32_t blk = q->req[src].blocks[i];
@@ -847,8 +855,8 @@ yuuka_status yuuka_q35_fork(yuuka_q35 *q, int32_t src, int32_t dst) {
                 if (L.recurrent) continue;
                 for (yuuka_buffer *pool : {L.kpool, L.vpool}) {
                     uint8_t *base = static_cast<uint8_t *>(pool->ptr);
-                    (void)hipMemcpyAsync(base + (uint64_t)to * blk_bytes, base + (uint64_t)from * blk_bytes, blk_bytes,
-                                         hipMemcpyDeviceToDevice, s);
+                    enq(hipMemcpyAsync(base + (uint64_t)to * blk_bytes, base + (uint64_t)from * blk_bytes, blk_bytes,
+                                       hipMemcpyDeviceToDevice, s));
                 }
             }
         }
@@ -857,14 +865,15 @@ yuuka_status yuuka_q35_fork(yuuka_q35 *q, int32_t src, int32_t dst) {
         for (auto &L : q->layers) {
             if (!L.recurrent) continue;
             uint8_t *cs = static_cast<uint8_t *>(L.conv_state->ptr), *ms = static_cast<uint8_t *>(L.mat_state->ptr);
-            (void)hipMemcpyAsync(cs + (uint64_t)dst * L.conv_bytes, cs + (uint64_t)src * L.conv_bytes, L.conv_bytes,
-                                 hipMemcpyDeviceToDevice, s);
-            (void)hipMemcpyAsync(ms + (uint64_t)dst * L.mat_bytes, ms + (uint64_t)src * L.mat_bytes, L.mat_bytes,
-                                 hipMemcpyDeviceToDevice, s);
+            enq(hipMemcpyAsync(cs + (uint64_t)dst * L.conv_bytes, cs + (uint64_t)src * L.conv_bytes, L.conv_bytes,
+                               hipMemcpyDeviceToDevice, s));
+            enq(hipMemcpyAsync(ms + (uint64_t)dst * L.mat_bytes, ms + (uint64_t)src * L.mat_bytes, L.mat_bytes,
+                               hipMemcpyDeviceToDevice, s));
         }
         uint8_t *dy = static_cast<uint8_t *>(q->dyn->ptr);
-        (void)hipMemcpyAsync(dy + (uint64_t)dst * 8, dy + (uint64_t)src * 8, 8, hipMemcpyDeviceToDevice, s);
+        enq(hipMemcpyAsync(dy + (uint64_t)dst * 8, dy + (uint64_t)src * 8, 8, hipMemcpyDeviceToDevice, s));
         hipError_t err = hipStreamSynchronize(s);
+        if (eq != hipSuccess) return fail(YUUKA_ERR_DEVICE, "fork enqueue: %s", yk::hip_error(eq));
         if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "fork: %s", yk::hip_error(err));
         d.pos = pos;
         return YUUKA_OK;
