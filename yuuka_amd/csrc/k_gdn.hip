@@ -377,6 +377,47 @@ __device__ __forceinline__ void conv_channel2(const float *conv_state, const flo
     }
 }
 
+// Width-4 causal conv + SiLU of N channels (cc[u] < 0: none) with every
+// input requested before the first use: one memory round trip for all of
+// the thread's channels.
+template <int RC, int N>
+__device__ __forceinline__ void conv_channels4(const float *conv_state, const float *qkv, const float *conv_w,
+                                               const GdnArgs &g, const int (&cc)[N], float *const (&dst)[N],
+                                               const int (&stride)[N]) {
+    const int R = g.rows;
+    float w[N][4], st[N][3], x[N][RC];
+#pragma unroll
+    for (int u = 0; u < N; u++) {
+        const int c = cc[u] < 0 ? cc[0] : cc[u];
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[u][i] = conv_w[(uint64_t)c * 4 + i];
+#pragma unroll
+        for (int i = 0; i < 3; i++) st[u][i] = conv_state[(uint64_t)c * 3 + i];
+#pragma unroll
+        for (int r = 0; r < RC; r++) {
+            const float xv = qkv[(uint64_t)min(r, R - 1) * g.conv_dim + c];
+            x[u][r] = r < R ? xv : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < N; u++) {
+        if (cc[u] < 0) continue;
+#pragma unroll
+        for (int r = 0; r < RC; r++) {
+            if (r >= R) break;
+            float sum = 0.0f;
+#pragma unroll
+            for (int tt = 0; tt < 3; tt++) {
+                const int idx = r + tt - 3;
+                const float xv = idx >= 0 ? x[u][idx >= 0 ? idx : 0] : st[u][idx >= 0 ? 0 : 3 + idx];
+                sum = __fadd_rn(sum, __fmul_rn(w[u][tt], xv));
+            }
+            sum = __fadd_rn(sum, __fmul_rn(w[u][3], x[u][r]));
+            dst[u][r * stride[u]] = silu_ref(sum);
+        }
+    }
+}
+
 // ---- column-split variants: workgroup (head h, block of kCols state
 // columns). Lane l of wave w holds column j = kCols * blockIdx.y + 8 w + l / 8
 // and state rows 16 (l % 8) .. +15; a column's eight row parts form an
@@ -394,13 +435,16 @@ constexpr int kColThreads = 256;
 // Verify: conv + SiLU + L2 norm of the head's q / k channels and this
 // block's v channels, then the delta rule over the rows for this block's
 // columns. Writes the raw outputs (the gated norm runs in the consumer) and
-// the conv outputs for the commit; the states are left untouched.
-template <int RC>
-__global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
+// the conv outputs for the commit; the states are left untouched. COLS state
+// columns per workgroup (8 per wave): smaller blocks spread one request's
+// heads over more CUs; every block of a head repeats the head's q / k conv.
+template <int RC, int COLS>
+__global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
     const float *__restrict__ conv_state, const float *__restrict__ state, const float *__restrict__ qkv,
     const float *__restrict__ alpha_raw, const float *__restrict__ beta_raw, const float *__restrict__ conv_w,
     const float *__restrict__ dt, const float *__restrict__ a_log, float *__restrict__ raw_out,
     float *__restrict__ conv_out, GdnArgs g) {
+    constexpr int kThr = 8 * COLS;
     extern __shared__ float sm[];
     const int h = blockIdx.x, cb = blockIdx.y;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
@@ -418,8 +462,8 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
     const int key_dim = g.groups * kS;
     const int kh = h % g.groups;
     float *qk = sm;                 // [R][2][128] q, k
-    float *vv = qk + R * 2 * kS;    // [R][kCols]
-    float *cf = vv + R * kCols;     // [2][R] decay, beta of every row
+    float *vv = qk + R * 2 * kS;    // [R][COLS]
+    float *cf = vv + R * COLS;      // [2][R] decay, beta of every row
     if (t < R) {
         cf[t] = gdn_decay(g, alpha_raw, dt, a_log, t, h);
         cf[R + t] = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
@@ -428,25 +472,43 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
     uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #endif
     YK_GD_STAMP(0);
-    const int p = lane & 7, j = cb * kCols + wave * 8 + (lane >> 3);
+    const int p = lane & 7, j = cb * COLS + wave * 8 + (lane >> 3);
     const float *mat = state + (uint64_t)h * kS * kS;
     float s_reg[16];
 #pragma unroll
     for (int ii = 0; ii < 16; ii++) s_reg[ii] = mat[(uint64_t)(p * 16 + ii) * kS + j];
-    // conv of 256 q/k channels (thread t: channel t) + kCols v channels
-    // (threads 0 .. kCols - 1, loaded together with their first channel)
-    {
-        static_assert(2 * kS == kColThreads, "one q/k channel per thread");
-        const int which = t >> 7, cc = t & (kS - 1);
-        const int c0 = (which == 0 ? 0 : key_dim) + kh * kS + cc;
-        const int c1 = t < kCols ? 2 * key_dim + h * kS + cb * kCols + t : -1;
-        conv_channel2<RC>(conv_state, qkv, conv_w, g, c0, qk + which * kS + cc, 2 * kS, c1, vv + t, kCols);
+    // conv of the 256 q/k channels (thread t: channels t, t + kThr, ...) and
+    // of this block's COLS v channels (threads 0 .. COLS - 1, loaded with
+    // their first q/k channel)
+    if (g.kernel == 4) {
+        constexpr int NQ = 2 * kS / kThr, N = NQ + 1;
+        int cc[N], stride[N];
+        float *dst[N];
+#pragma unroll
+        for (int u = 0; u < NQ; u++) {
+            const int ch = u * kThr + t, which = ch >> 7, c = ch & (kS - 1);
+            cc[u] = (which == 0 ? 0 : key_dim) + kh * kS + c;
+            dst[u] = qk + which * kS + c;
+            stride[u] = 2 * kS;
+        }
+        cc[NQ] = t < COLS ? 2 * key_dim + h * kS + cb * COLS + t : -1;
+        dst[NQ] = vv + t;
+        stride[NQ] = COLS;
+        conv_channels4<RC, N>(conv_state, qkv, conv_w, g, cc, dst, stride);
+    } else {
+#pragma unroll
+        for (int base = 0; base < 2 * kS; base += kThr) {
+            const int ch = base + t, which = ch >> 7, cc = ch & (kS - 1);
+            const int c0 = (which == 0 ? 0 : key_dim) + kh * kS + cc;
+            const int c1 = base == 0 && t < COLS ? 2 * key_dim + h * kS + cb * COLS + t : -1;
+            conv_channel2<RC>(conv_state, qkv, conv_w, g, c0, qk + which * kS + cc, 2 * kS, c1, vv + t, COLS);
+        }
     }
     YK_GD_STAMP(1);
     __syncthreads();
     YK_GD_STAMP(2);
     const bool owns_qk = cb == 0 && h < g.groups;
-    for (int vec = wave; vec < 2 * R; vec += kColThreads / 64) {
+    for (int vec = wave; vec < 2 * R; vec += kThr / 64) {
         const int r = vec >> 1, which = vec & 1;
         float *x = qk + (r * 2 + which) * kS;
         const float a0 = x[lane], a1 = x[lane + 64];
@@ -463,14 +525,14 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
             dst[lane + 64] = y1;
         }
     }
-    for (int idx = t; idx < R * kCols; idx += kColThreads) {
-        const int r = idx / kCols, cc = idx % kCols;
-        conv_out[(uint64_t)r * g.conv_dim + 2 * key_dim + h * kS + cb * kCols + cc] = vv[r * kCols + cc];
+    for (int idx = t; idx < R * COLS; idx += kThr) {
+        const int r = idx / COLS, cc = idx % COLS;
+        conv_out[(uint64_t)r * g.conv_dim + 2 * key_dim + h * kS + cb * COLS + cc] = vv[r * COLS + cc];
     }
     YK_GD_STAMP(3);
     __syncthreads();
     YK_GD_STAMP(4);
-    const int jl = j - cb * kCols;
+    const int jl = j - cb * COLS;
     for (int r = 0; r < R; r++) {
         const float *q = qk + (r * 2 + 0) * kS, *k = qk + (r * 2 + 1) * kS;
         const float decay = cf[r], beta = cf[R + r];
@@ -481,7 +543,7 @@ __global__ __launch_bounds__(kColThreads) void gdn_verify_cols_kernel(
             sk = __fadd_rn(sk, __fmul_rn(s_reg[ii], k[p * 16 + ii]));
         }
         sk = group8_sum_f(sk);
-        const float d = __fmul_rn(__fsub_rn(vv[r * kCols + jl], sk), beta);
+        const float d = __fmul_rn(__fsub_rn(vv[r * COLS + jl], sk), beta);
         float o = 0.0f;
 #pragma unroll
         for (int ii = 0; ii < 16; ii++) {
@@ -607,23 +669,50 @@ __global__ __launch_bounds__(kColThreads) void gdn_commit_cols_multi_kernel(cons
 
 }  // namespace
 
-uint32_t gdn_verify_cols_lds_bytes(const GdnArgs &g) { return (uint32_t)(g.rows * 2 * kS + g.rows * kCols + 2 * g.rows) * 4; }
+// State columns per verify workgroup: the widest block that still gives
+// about two workgroups per CU (one request: 8 columns, 256 workgroups at
+// rank 16; many requests: 32).
+// Columns of the state per workgroup. Measured per launch at the 27B
+// geometry (32 heads, 128-wide state): one request with 5 rows, 7.9 us at 16
+// columns against 8.3 us at 32 and 10.1 us at 8; four requests of 17 rows,
+// 22.4 us at 32 against 37.9 us at 16. Narrow workgroups pay once the grid
+// would otherwise leave CUs idle, wide ones amortise the row loads otherwise.
+static int verify_cols(const GdnArgs &g) {
+    const int64_t heads = (int64_t)g.rank * (g.nreq > 0 ? g.nreq : 1);
+    return heads >= 128 ? 32 : 16;
+}
+
+uint32_t gdn_verify_cols_lds_bytes(const GdnArgs &g) {
+    return (uint32_t)(g.rows * 2 * kS + g.rows * verify_cols(g) + 2 * g.rows) * 4;
+}
+
+template <int COLS>
+static void launch_verify_cols(const float *conv_state, const float *state, const float *qkv, const float *alpha_raw,
+                               const float *beta_raw, const float *conv_w, const float *dt, const float *a_log,
+                               float *raw_out, float *conv_out, const GdnArgs &g, hipStream_t s) {
+    const dim3 grid((unsigned)g.rank, kS / COLS, (unsigned)(g.nreq > 0 ? g.nreq : 1));
+    const uint32_t lds = gdn_verify_cols_lds_bytes(g);
+    // row capacity of the conv registers: the smallest instantiation that holds the rows
+    if (g.rows <= 8)
+        gdn_verify_cols_kernel<8, COLS><<<grid, 8 * COLS, lds, s>>>(conv_state, state, qkv, alpha_raw, beta_raw,
+                                                                    conv_w, dt, a_log, raw_out, conv_out, g);
+    else if (g.rows <= 16)
+        gdn_verify_cols_kernel<16, COLS><<<grid, 8 * COLS, lds, s>>>(conv_state, state, qkv, alpha_raw, beta_raw,
+                                                                     conv_w, dt, a_log, raw_out, conv_out, g);
+    else
+        gdn_verify_cols_kernel<kMaxRows, COLS><<<grid, 8 * COLS, lds, s>>>(conv_state, state, qkv, alpha_raw,
+                                                                           beta_raw, conv_w, dt, a_log, raw_out,
+                                                                           conv_out, g);
+}
 
 hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, const float *qkv,
                                   const float *alpha_raw, const float *beta_raw, const float *conv_w, const float *dt,
                                   const float *a_log, float *raw_out, float *conv_out, const GdnArgs &g,
                                   hipStream_t s) {
-    const dim3 grid((unsigned)g.rank, kS / kCols, (unsigned)(g.nreq > 0 ? g.nreq : 1));
-    // row capacity of the conv registers: the smallest instantiation that holds the rows
-    if (g.rows <= 8)
-        gdn_verify_cols_kernel<8><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
-            conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
-    else if (g.rows <= 16)
-        gdn_verify_cols_kernel<16><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
-            conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
+    if (verify_cols(g) == 16)
+        launch_verify_cols<16>(conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g, s);
     else
-        gdn_verify_cols_kernel<kMaxRows><<<grid, kColThreads, gdn_verify_cols_lds_bytes(g), s>>>(
-            conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g);
+        launch_verify_cols<32>(conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g, s);
     return hipGetLastError();
 }
 
