@@ -287,6 +287,38 @@ def dominant_kernel(dev, cfg, rows, rng):
             "alg_bytes_per_launch": gemm_bytes, "avg_us": gemm_us, "launches": reps * copies}
 
 
+def lm_head_only(dev):
+    """Config 1's dominant kernel alone: the v10 LM_HEAD op over the Q4_K
+    9216x2560 matrix at M = 5, 4 x copies launches per graph replay (weight
+    copies rotated, 512 MB in all), 20 replays after one warm-up replay."""
+    from yuuka_amd import hip, synth
+    c = synth.config1(0)
+    N, K, M = c["N"], c["K"], c["M"]
+    wbytes = c["w"].nbytes
+    copies = max(1, -(-512 * 2**20 // wbytes))
+    rng = np.random.default_rng(1)
+    ws = [dev.upload(c["w"])] + [dev.upload(synth.quant_matrix(rng, synth.Q4_K, N, K)) for _ in range(copies - 1)]
+    xb = dev.upload(c["x"])
+    out = dev.alloc(M * N * 4)
+    stream = hip.Stream(dev)
+    p = hip.Plan(dev)
+    launches = 4 * copies
+    for j in range(launches):
+        p.add(hip.OP["LM_HEAD"], [ws[j % copies], xb, out], n=[K, N, M], u=[synth.Q4_K])
+    g = hip.Graph(p, stream, None)
+    g.replay(stream)
+    stream.sync()
+    e0, e1 = hip.Event(dev, timed=True), hip.Event(dev, timed=True)
+    reps = 20
+    e0.record(stream)
+    for _ in range(reps):
+        g.replay(stream)
+    e1.record(stream)
+    stream.sync()
+    us = e1.elapsed_ms(e0) * 1e3 / (reps * launches)
+    return {"kernel": "LM_HEAD Q4_K 9216x2560 M=5", "avg_us": us, "launches": (reps + 1) * launches}
+
+
 def kernel_only(args):
     """--kernel-only: the dominant-kernel measurement alone, followed by one
     plain 256 MiB device-to-device copy (the calibration kernel for the
@@ -294,7 +326,10 @@ def kernel_only(args):
     from yuuka_amd import hip, model as Mdl
     dev = hip.Device(0)
     rng = np.random.default_rng(2)
-    dk = dominant_kernel(dev, Mdl.QWEN35_4B_LIKE, args.drafts + 1, rng)
+    if args.config == 1:
+        dk = lm_head_only(dev)
+    else:
+        dk = dominant_kernel(dev, Mdl.QWEN35_4B_LIKE, args.drafts + 1, rng)
     nbytes = 256 * 2**20
     src, dst = dev.alloc(nbytes), dev.alloc(nbytes)
     st = hip.Stream(dev)

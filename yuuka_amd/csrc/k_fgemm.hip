@@ -518,6 +518,10 @@ __device__ __forceinline__ void act_prologue_regs(const FusedGemmArgs &A, const 
     }
 }
 
+// Buffer offset past every weight range: loads there return zero and make
+// no memory request.
+constexpr uint32_t kOutOfRange = 0xC0000000u;
+
 // Staged weight bytes of one 16-row tile for one super-block.
 struct Q4Stage {
     i32x4 hdr;      // d | dmin, 12 scale bytes
@@ -1067,21 +1071,34 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
 #pragma unroll
             for (int t = 0; t < TT; t++) issue_any(S[t], Gr.rs[t], Gr.row_off[t], (uint32_t)sb, g, Gr.dt);
         };
+        // A ring slot past the wave's last item still issues its loads (a
+        // fixed load count keeps the compiler's wait counts exact), at an
+        // offset beyond the buffer's range: they return zero without a
+        // memory request instead of re-reading a live item.
+        auto issue_slot = [&](Stage (&S)[TT], int q) __attribute__((always_inline)) {
+            const bool live = q < nmine;
+            const int ii = live ? wave + q * kWaves : 0;
+            const int c = ii / nsb, sb = ii - c * nsb;
+            const GroupRows<TT> Gr(A, t0 + c, rows_out, swiglu, r);
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+                issue_any(S[t], Gr.rs[t], live ? Gr.row_off[t] : kOutOfRange, live ? (uint32_t)sb : 0u, g, Gr.dt);
+        };
         constexpr int kSlot = TT * NA * 256;  // floats of one wave's partial of one tile
         float *myr = red + (size_t)wave * kBalMax * kSlot;
-        // two items in flight per wave (four measured slower: the early
-        // weight traffic delays the activation fetch)
+        // two items in flight per wave (deeper rings, issued before or after
+        // the activations land, measured slower: the loop is bound by
+        // instruction issue, not by outstanding loads)
         constexpr int kD = 2;
         Stage sbr[kD][TT];
 #ifdef YK_FG_TIMING
         uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         YK_FG_STAMP(ts[0]);
 #endif
-        // issued unconditionally (item index clamped; the buffer resources
-        // bound every access): under a branch the compiler's wait counts
-        // lose track and the prologue would wait for these weights too
+        // issued unconditionally (under a branch the compiler's wait counts
+        // lose track and the prologue would wait for these weights too)
 #pragma unroll
-        for (int d = 0; d < kD; d++) issue_item(sbr[d], min(wave + d * kWaves, max(I - 1, 0)));
+        for (int d = 0; d < kD; d++) issue_slot(sbr[d], d);
         __builtin_amdgcn_sched_barrier(0);
         for (int idx = lane; idx < cnt * kSlot / 4; idx += 64)
             reinterpret_cast<float4 *>(myr)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);

@@ -669,17 +669,15 @@ __global__ __launch_bounds__(kColThreads) void gdn_commit_cols_multi_kernel(cons
 
 }  // namespace
 
-// State columns per verify workgroup: the widest block that still gives
-// about two workgroups per CU (one request: 8 columns, 256 workgroups at
-// rank 16; many requests: 32).
-// Columns of the state per workgroup. Measured per launch at the 27B
-// geometry (32 heads, 128-wide state): one request with 5 rows, 7.9 us at 16
-// columns against 8.3 us at 32 and 10.1 us at 8; four requests of 17 rows,
-// 22.4 us at 32 against 37.9 us at 16. Narrow workgroups pay once the grid
-// would otherwise leave CUs idle, wide ones amortise the row loads otherwise.
+// Columns of the state per workgroup. Measured per launch with 16 heads
+// of 128-wide state: one request of 5 rows, 7.9 us at 16 columns against
+// 8.3 us at 32 and 10.1 us at 8; four requests of 17 rows, 22.4 us at 32
+// against 37.9 us at 16; sixteen requests of 9 rows, 27.5 us at 32 against
+// 40.8 us at 16. Narrow blocks pay only while the grid would otherwise leave
+// CUs idle; wide ones share the q / k conv and norm over more columns.
 static int verify_cols(const GdnArgs &g) {
     const int64_t heads = (int64_t)g.rank * (g.nreq > 0 ? g.nreq : 1);
-    return heads >= 128 ? 32 : 16;
+    return heads >= 32 ? 32 : 16;
 }
 
 uint32_t gdn_verify_cols_lds_bytes(const GdnArgs &g) {
