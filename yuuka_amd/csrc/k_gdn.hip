@@ -436,8 +436,8 @@ constexpr int kColThreads = 256;
 // block's v channels, then the delta rule over the rows for this block's
 // columns. Writes the raw outputs (the gated norm runs in the consumer) and
 // the conv outputs for the commit; the states are left untouched. COLS state
-// columns per workgroup (8 per wave): smaller blocks spread one request's
-// heads over more CUs; every block of a head repeats the head's q / k conv.
+// columns per workgroup (8 per wave); every block of a head repeats the
+// head's q / k conv and norm.
 template <int RC, int COLS>
 __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
     const float *__restrict__ conv_state, const float *__restrict__ state, const float *__restrict__ qkv,
@@ -507,22 +507,56 @@ __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
     YK_GD_STAMP(1);
     __syncthreads();
     YK_GD_STAMP(2);
+    // L2 norm of the 2R q / k vectors. One 16-lane DPP row per vector (lane
+    // s of the row holds elements [8 s, 8 s + 8)), two vectors per row at a
+    // time: the float64 sums of every vector reduce side by side instead of
+    // one wave-wide reduction after another.
     const bool owns_qk = cb == 0 && h < g.groups;
-    for (int vec = wave; vec < 2 * R; vec += kThr / 64) {
-        const int r = vec >> 1, which = vec & 1;
-        float *x = qk + (r * 2 + which) * kS;
-        const float a0 = x[lane], a1 = x[lane + 64];
-        double sq = (double)a0 * (double)a0 + (double)a1 * (double)a1;
-        sq = wave_sum_dpp(sq);
-        const float extra = which == 0 ? g.q_scale : 1.0f;
-        const float scale = __fmul_rn((float)(1.0 / sqrt(sq + (double)g.eps)), extra);
-        const float y0 = __fmul_rn(a0, scale), y1 = __fmul_rn(a1, scale);
-        x[lane] = y0;
-        x[lane + 64] = y1;
-        if (owns_qk) {
-            float *dst = conv_out + (uint64_t)r * g.conv_dim + (which == 0 ? 0 : key_dim) + kh * kS;
-            dst[lane] = y0;
-            dst[lane + 64] = y1;
+    {
+        constexpr int kGroups = kThr / 16;  // DPP rows of the workgroup
+        const int s16 = lane & 15, grp = t >> 4;
+        for (int v0 = 0; v0 < 2 * R; v0 += 2 * kGroups) {
+            float e[2][8];
+            double sq[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int vc = min(v0 + u * kGroups + grp, 2 * R - 1);
+                const float4 *x = reinterpret_cast<const float4 *>(qk + vc * kS + 8 * s16);
+                const float4 x0 = x[0], x1 = x[1];
+                e[u][0] = x0.x; e[u][1] = x0.y; e[u][2] = x0.z; e[u][3] = x0.w;
+                e[u][4] = x1.x; e[u][5] = x1.y; e[u][6] = x1.z; e[u][7] = x1.w;
+                double acc = 0.0;
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc += (double)e[u][i] * (double)e[u][i];
+                sq[u] = acc;
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++) sq[u] += dpp_dd<0xb1>(sq[u]);
+#pragma unroll
+            for (int u = 0; u < 2; u++) sq[u] += dpp_dd<0x4e>(sq[u]);
+#pragma unroll
+            for (int u = 0; u < 2; u++) sq[u] += dpp_dd<0x124>(sq[u]);
+#pragma unroll
+            for (int u = 0; u < 2; u++) sq[u] += dpp_dd<0x128>(sq[u]);
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int vec = v0 + u * kGroups + grp;
+                if (vec >= 2 * R) continue;
+                const int r = vec >> 1, which = vec & 1;
+                const float extra = which == 0 ? g.q_scale : 1.0f;
+                const float scale = __fmul_rn((float)(1.0 / sqrt(sq[u] + (double)g.eps)), extra);
+                float y[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) y[i] = __fmul_rn(e[u][i], scale);
+                float4 *x = reinterpret_cast<float4 *>(qk + vec * kS + 8 * s16);
+                x[0] = make_float4(y[0], y[1], y[2], y[3]);
+                x[1] = make_float4(y[4], y[5], y[6], y[7]);
+                if (owns_qk) {
+                    float *dst = conv_out + (uint64_t)r * g.conv_dim + (which == 0 ? 0 : key_dim) + kh * kS + 8 * s16;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) dst[i] = y[i];
+                }
+            }
         }
     }
     for (int idx = t; idx < R * COLS; idx += kThr) {
@@ -533,25 +567,56 @@ __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
     __syncthreads();
     YK_GD_STAMP(4);
     const int jl = j - cb * COLS;
-    for (int r = 0; r < R; r++) {
-        const float *q = qk + (r * 2 + 0) * kS, *k = qk + (r * 2 + 1) * kS;
-        const float decay = cf[r], beta = cf[R + r];
-        float sk = 0.0f;
+    // Row r's k, q slices, v and coefficients are read from LDS while row
+    // r - 1 is computed (two register sets, alternating).
+    struct RowIn {
+        float k[16], q[16], v, decay, beta;
+    };
+    auto fetch = [&](RowIn &in, int r) __attribute__((always_inline)) {
+        const float4 *kp = reinterpret_cast<const float4 *>(qk + (r * 2 + 1) * kS + p * 16);
+        const float4 *qp = reinterpret_cast<const float4 *>(qk + (r * 2 + 0) * kS + p * 16);
 #pragma unroll
-        for (int ii = 0; ii < 16; ii++) {
-            s_reg[ii] = __fmul_rn(s_reg[ii], decay);
-            sk = __fadd_rn(sk, __fmul_rn(s_reg[ii], k[p * 16 + ii]));
+        for (int c = 0; c < 4; c++) {
+            const float4 kv = kp[c], qv = qp[c];
+            in.k[4 * c] = kv.x; in.k[4 * c + 1] = kv.y; in.k[4 * c + 2] = kv.z; in.k[4 * c + 3] = kv.w;
+            in.q[4 * c] = qv.x; in.q[4 * c + 1] = qv.y; in.q[4 * c + 2] = qv.z; in.q[4 * c + 3] = qv.w;
         }
-        sk = group8_sum_f(sk);
-        const float d = __fmul_rn(__fsub_rn(vv[r * COLS + jl], sk), beta);
-        float o = 0.0f;
+        in.v = vv[r * COLS + jl];
+        in.decay = cf[r];
+        in.beta = cf[R + r];
+    };
+    // Column sums over the lane's 16 rows as two interleaved chains (even
+    // and odd rows), then the 8-lane group.
+    auto step = [&](const RowIn &in, int r) __attribute__((always_inline)) {
+        float sk0 = 0.0f, sk1 = 0.0f;
 #pragma unroll
-        for (int ii = 0; ii < 16; ii++) {
-            s_reg[ii] = __fadd_rn(s_reg[ii], __fmul_rn(k[p * 16 + ii], d));
-            o = __fadd_rn(o, __fmul_rn(s_reg[ii], q[p * 16 + ii]));
+        for (int ii = 0; ii < 16; ii += 2) {
+            s_reg[ii] = __fmul_rn(s_reg[ii], in.decay);
+            s_reg[ii + 1] = __fmul_rn(s_reg[ii + 1], in.decay);
+            sk0 = __fadd_rn(sk0, __fmul_rn(s_reg[ii], in.k[ii]));
+            sk1 = __fadd_rn(sk1, __fmul_rn(s_reg[ii + 1], in.k[ii + 1]));
         }
-        o = group8_sum_f(o);
+        const float sk = group8_sum_f(__fadd_rn(sk0, sk1));
+        const float d = __fmul_rn(__fsub_rn(in.v, sk), in.beta);
+        float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < 16; ii += 2) {
+            s_reg[ii] = __fadd_rn(s_reg[ii], __fmul_rn(in.k[ii], d));
+            s_reg[ii + 1] = __fadd_rn(s_reg[ii + 1], __fmul_rn(in.k[ii + 1], d));
+            o0 = __fadd_rn(o0, __fmul_rn(s_reg[ii], in.q[ii]));
+            o1 = __fadd_rn(o1, __fmul_rn(s_reg[ii + 1], in.q[ii + 1]));
+        }
+        const float o = group8_sum_f(__fadd_rn(o0, o1));
         if (p == 0) raw_out[((uint64_t)r * g.rank + h) * kS + j] = o;
+    };
+    RowIn ra, rb;
+    fetch(ra, 0);
+    for (int r = 0; r < R; r += 2) {
+        if (r + 1 < R) fetch(rb, r + 1);
+        step(ra, r);
+        if (r + 1 >= R) break;
+        if (r + 2 < R) fetch(ra, r + 2);
+        step(rb, r + 1);
     }
     YK_GD_STAMP(5);
 #ifdef YK_GD_TIMING
@@ -669,19 +734,15 @@ __global__ __launch_bounds__(kColThreads) void gdn_commit_cols_multi_kernel(cons
 
 }  // namespace
 
-// Columns of the state per workgroup. Measured per launch with 16 heads
-// of 128-wide state: one request of 5 rows, 7.9 us at 16 columns against
-// 8.3 us at 32 and 10.1 us at 8; four requests of 17 rows, 22.4 us at 32
-// against 37.9 us at 16; sixteen requests of 9 rows, 27.5 us at 32 against
-// 40.8 us at 16. Narrow blocks pay only while the grid would otherwise leave
-// CUs idle; wide ones share the q / k conv and norm over more columns.
-static int verify_cols(const GdnArgs &g) {
-    const int64_t heads = (int64_t)g.rank * (g.nreq > 0 ? g.nreq : 1);
-    return heads >= 32 ? 32 : 16;
-}
+// Columns of the state per verify workgroup. Measured per launch with 16
+// heads of 128-wide state, 16 / 32 columns: one request of 5 rows 6.97 /
+// 6.82 us; sixteen requests of 9 rows 34.5 / 19.3 us; four requests of 17
+// rows 33.1 / 18.4 us. Wider blocks share the q / k conv and norm over more
+// columns, which outweighs the smaller grid even at one request.
+constexpr int kVerifyCols = 32;
 
 uint32_t gdn_verify_cols_lds_bytes(const GdnArgs &g) {
-    return (uint32_t)(g.rows * 2 * kS + g.rows * verify_cols(g) + 2 * g.rows) * 4;
+    return (uint32_t)(g.rows * 2 * kS + g.rows * kVerifyCols + 2 * g.rows) * 4;
 }
 
 template <int COLS>
@@ -707,10 +768,8 @@ hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, c
                                   const float *alpha_raw, const float *beta_raw, const float *conv_w, const float *dt,
                                   const float *a_log, float *raw_out, float *conv_out, const GdnArgs &g,
                                   hipStream_t s) {
-    if (verify_cols(g) == 16)
-        launch_verify_cols<16>(conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g, s);
-    else
-        launch_verify_cols<32>(conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g, s);
+    launch_verify_cols<kVerifyCols>(conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g,
+                                    s);
     return hipGetLastError();
 }
 
