@@ -34,8 +34,13 @@ namespace {
 // Phase timestamps per wave (probe builds only; s_memrealtime, 100 MHz).
 __device__ uint64_t *yk_at_dbg;
 #define YK_AT_STAMP(i) ts[i] = __builtin_amdgcn_s_memrealtime()
+// adds the time since the last YK_AT_MARK to slot i
+#define YK_AT_MARK() t_mark = __builtin_amdgcn_s_memrealtime()
+#define YK_AT_ACC(i) { const uint64_t t_ = __builtin_amdgcn_s_memrealtime(); ts[i] += t_ - t_mark; t_mark = t_; }
 #else
 #define YK_AT_STAMP(i) (void)0
+#define YK_AT_MARK() (void)0
+#define YK_AT_ACC(i) (void)0
 #endif
 
 __device__ __forceinline__ int cur_pos_a(const ModelDyn &dyn) { return dyn.pos_dev ? *dyn.pos_dev : dyn.pos; }
@@ -755,13 +760,35 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
 #endif
 }
 
+// LDS layout of the grouped kernel with NT 16-row query tiles: the
+// transposed V chunk, the query tiles (F16 high, remainder), the scores /
+// probabilities and the running (max, sum, rescale) of every query row.
+template <int NT> struct GroupLds {
+    static constexpr int kQ = 16 * NT;
+    static constexpr uint32_t Vt = 0;
+    static constexpr uint32_t Qh = Vt + kMD * kVt * 2;
+    static constexpr uint32_t Ql = Qh + kQ * kMD * 2;
+    static constexpr uint32_t S = Ql + kQ * kMD * 2;
+    static constexpr uint32_t ML = S + kQ * kMK * 4;
+    static constexpr uint32_t total = ML + 3 * kQ * 4;
+};
+static_assert(GroupLds<2>::total == kMfmaLds, "two-tile layout");
+static_assert(GroupLds<6>::total <= 160 * 1024, "six-tile layout fits LDS");
+
 // One workgroup per (group of `cpw` 64-key chunks, KV head, request). The
 // verify rows' own keys and values in the group's range go to the pool
-// first; then, per block of kMQ / G verify rows, the group's chunks are
+// first; then, per block of 16 NT / G verify rows, the group's chunks are
 // walked in order with an online softmax (running max m, sum l and the
 // rescale of the P.V accumulators in registers). One partial record
 // (o, m, l) per (group, row, head) for the merge.
-__global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) void attn_verify_mfma_group_kernel(
+// NT = 2: 76 KB of LDS and at most 128 VGPRs, two workgroups per CU.
+// NT = 6: up to 96 MFMA rows in one block (all 68 rows of 4 heads x 17 verify
+// rows, so each chunk is read once per step), 157 KB of LDS and one
+// workgroup per CU; with the register budget of two waves per SIMD the next
+// chunk's keys and values load into a second register set while the current
+// chunk is computed (PF).
+template <int NT, bool PF>
+__global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2 ? 2 : 4))) void attn_verify_mfma_group_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, uint16_t *kpool,
     uint16_t *vpool, const int32_t *__restrict__ table, const float *__restrict__ q_norm,
     const float *__restrict__ k_norm, const float2 *__restrict__ rope, AttnVArgs a, float *__restrict__ part,
@@ -779,14 +806,17 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
     if (c_lo * kMK > last) return;  // no row sees this group; the merge skips it
     const int c_hi = min(c_lo + cpw, last / kMK + 1);
 #ifdef YK_AT_TIMING
-    uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint64_t ts[12] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    uint64_t t_mark = 0;
 #endif
     YK_AT_STAMP(0);
     const int half = a.rope_dim / 2;
     const int qstride = a.gated ? 2 * kMD : kMD;
-    float *Mrow = reinterpret_cast<float *>(lds + kOffML);  // running max per MFMA row
-    float *Lrow = Mrow + kMQ;                               // running sum
-    float *Arow = Lrow + kMQ;                               // this chunk's rescale of the accumulators
+    using LY = GroupLds<NT>;
+    constexpr int kQ = LY::kQ;
+    float *Mrow = reinterpret_cast<float *>(lds + LY::ML);  // running max per MFMA row
+    float *Lrow = Mrow + kQ;                                // running sum
+    float *Arow = Lrow + kQ;                                // this chunk's rescale of the accumulators
 
     // ---- the verify rows' own keys and values (rows whose position falls in
     //      this group): rounded as the pool stores them, into the pool
@@ -815,23 +845,26 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
     // keys straight into MFMA B order: the scores lane (key kk, group g4)
     // holds dims [32 ks + 8 g4, +8) of key kk for every ks
     const int kk_s = (wave & 3) * 16 + r16;
-    const bool scorer = 16 * (wave >> 2) < G * min(kMQ / G, R);  // row tile of this wave in use
+    const bool scorer = 16 * (wave >> 2) < G * min(kQ / G, R);  // a row tile of this wave is in use
     constexpr int kVE = kMD / kAW / 8;                          // 16-byte V pieces per lane
     constexpr int kJ = kMD / kAW / 16;                          // 16-wide output tiles per wave
-    const int RB = kMQ / G;
+    const int RB = kQ / G;
     // ---- query rows of one block: normalised, rotated, split into F16 high +
     //      remainder. A wave's rows are loaded first, then computed.
     auto prep_q = [&](int r0, int Rb) __attribute__((always_inline)) {
-        constexpr int kQV = kMQ / kAW;
+        int oz;  // opaque zero: keeps the per-vector offsets below from being hoisted and spilled
+        asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+        const int plane = lane + oz;
+        constexpr int kQV = kQ / kAW;
         const int nqb = G * Rb;
-        const float4 w4 = *reinterpret_cast<const float4 *>(q_norm + 4 * lane);
+        const float4 w4 = *reinterpret_cast<const float4 *>(q_norm + 4 * plane);
         float4 xq[kQV];
 #pragma unroll
         for (int t = 0; t < kQV; t++) {
             const int vec = wave + kAW * t;
             if (vec < nqb) {
                 const int gq = vec / Rb, r = r0 + vec % Rb;
-                xq[t] = *reinterpret_cast<const float4 *>(q + ((int64_t)r * a.heads + kvh * G + gq) * qstride + 4 * lane);
+                xq[t] = *reinterpret_cast<const float4 *>(q + ((int64_t)r * a.heads + kvh * G + gq) * qstride + 4 * plane);
             }
         }
 #pragma unroll
@@ -840,11 +873,11 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
             if (vec >= nqb) break;
             const int r = r0 + vec % Rb;
             float2 cq[4] = {};
-            if (lane < 16) {
+            if (plane < 16) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int e = 4 * lane + i;
-                    cq[i] = rope[r * half + (lane < 8 ? e : e - 32)];
+                    const int e = 4 * plane + i;
+                    cq[i] = rope[r * half + (plane < 8 ? e : e - 32)];
                 }
             }
             float y[4];
@@ -855,166 +888,255 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
                 hi[i] = (_Float16)y[i];
                 lo[i] = (_Float16)(y[i] - (float)hi[i]);
             }
-            const uint32_t off = (uint32_t)vec * kMD * 2 + (uint32_t)(((lane >> 1) ^ (vec & 15)) * 16 + (lane & 1) * 8);
-            *reinterpret_cast<uint2 *>(lds + kOffQh + off) = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
-            *reinterpret_cast<uint2 *>(lds + kOffQl + off) = make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
+            const uint32_t off = (uint32_t)vec * kMD * 2 + (uint32_t)(((plane >> 1) ^ (vec & 15)) * 16 + (plane & 1) * 8);
+            *reinterpret_cast<uint2 *>(lds + LY::Qh + off) = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
+            *reinterpret_cast<uint2 *>(lds + LY::Ql + off) = make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
         }
     };
 
-    // keys (scorer waves) and values (wave w: dims [32w, +32) of key `lane`)
+    // keys (scorer waves) and values (wave w: dims [32w, +32) of key `plane`)
     // of chunk ci, from clamped positions; keys / values past the verify rows
     // count as zero where they are used
-    half8 kreg[kMD / 32];
-    uint4 vreg[kVE];
-    bool kval = false, vval = false;
-    auto load_k = [&](int ci) __attribute__((always_inline)) {
+    struct KvRegs {
+        half8 k[kMD / 32];
+        uint4 v[kVE];
+        bool kval, vval;
+    };
+    // Page-table entries of this lane's key (scores) and value row of chunk
+    // ci, then the chunk's loads from them. The entries are requested one
+    // chunk ahead of the loads that use them: waiting for them then also
+    // waits only for loads that are due anyway.
+    struct Pages {
+        int32_t k, v;
+    };
+    auto fetch_pages = [&](Pages &P, int ci) __attribute__((always_inline)) {
+        const int key0 = ci * kMK;
+        P.k = table[min(key0 + kk_s, last) / a.block_size];
+        P.v = table[min(key0 + lane, last) / a.block_size];
+    };
+    auto load_kv = [&](KvRegs &X, const Pages &P, int ci) __attribute__((always_inline)) {
         const int key0 = ci * kMK;
         const int p = min(key0 + kk_s, last);
-        kval = scorer && key0 + kk_s <= last;
-        const int64_t ks_ = (int64_t)table[p / a.block_size] * a.block_size + p % a.block_size;
+        X.kval = scorer && key0 + kk_s <= last;
+        const int64_t ks_ = (int64_t)P.k * a.block_size + p % a.block_size;
         const half8 *ksrc = reinterpret_cast<const half8 *>(kpool + ks_ * a.kv_dim + (int64_t)kvh * kMD + g4 * 8);
 #pragma unroll
-        for (int ks = 0; ks < kMD / 32; ks++) kreg[ks] = ksrc[4 * ks];
-    };
-    auto load_v = [&](int ci) __attribute__((always_inline)) {
-        const int key0 = ci * kMK;
+        for (int ks = 0; ks < kMD / 32; ks++) X.k[ks] = ksrc[4 * ks];
         const int vp = min(key0 + lane, last);
-        vval = key0 + lane <= last;
-        const int64_t vs_ = (int64_t)table[vp / a.block_size] * a.block_size + vp % a.block_size;
+        X.vval = key0 + lane <= last;
+        const int64_t vs_ = (int64_t)P.v * a.block_size + vp % a.block_size;
         const uint4 *vsrc =
             reinterpret_cast<const uint4 *>(vpool + vs_ * a.kv_dim + (int64_t)kvh * kMD + wave * (kMD / kAW));
 #pragma unroll
-        for (int e = 0; e < kVE; e++) vreg[e] = vsrc[e];
+        for (int e = 0; e < kVE; e++) X.v[e] = vsrc[e];
     };
 
     for (int r0 = 0; r0 < R; r0 += RB) {
         const int Rb = min(RB, R - r0), nq = G * Rb;  // this block's verify rows and MFMA rows
+        const int ntl = (nq + 15) / 16;               // row tiles in use
         if (r0) lds_only_barrier();                   // the previous block's reads of Q, M, L are done
         prep_q(r0, Rb);
-        if (threadIdx.x < kMQ) {
+        YK_AT_STAMP(8);
+        if (threadIdx.x < kQ) {
             Mrow[threadIdx.x] = -INFINITY;
             Lrow[threadIdx.x] = 0.0f;
         }
-        f32x4 o[kJ][2];
+        f32x4 o[kJ][NT];
 #pragma unroll
         for (int j = 0; j < kJ; j++)
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++) o[j][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const bool two = nq > 16;
-        YK_AT_STAMP(2);
-        for (int ci = c_lo; ci < c_hi; ci++) {
+            for (int rt = 0; rt < NT; rt++) o[j][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // one chunk of the group from the registers X
+        auto chunk = [&](const KvRegs &X, int ci) __attribute__((always_inline)) {
             const int key0 = ci * kMK;
-            load_k(ci);
-            load_v(ci);
+            // Lane constants re-derived per chunk from an opaque zero: hoisted
+            // out of the chunk loop, the per-tile offsets they feed would be
+            // spilled for the whole loop.
+            int oz;
+            asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+            const int lr16 = r16 + oz, lg4 = g4 + oz, lkk = kk_s + oz, llane = lane + oz;
+            YK_AT_MARK();
             lds_only_barrier();  // the previous chunk's P.V reads of Vt are done; Q, M, L are written
+            YK_AT_ACC(2);
             {
-                uint16_t *vt = reinterpret_cast<uint16_t *>(lds + kOffVt);
+                uint16_t *vt = reinterpret_cast<uint16_t *>(lds + LY::Vt);
 #pragma unroll
                 for (int e = 0; e < kVE; e++) {
-                    const uint4 vv = vval ? vreg[e] : make_uint4(0, 0, 0, 0);
+                    const uint4 vv = X.vval ? X.v[e] : make_uint4(0, 0, 0, 0);
                     const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
                     for (int i = 0; i < 8; i++)
-                        vt[(wave * (kMD / kAW) + e * 8 + i) * kVt + lane] = (uint16_t)(w4[i >> 1] >> (16 * (i & 1)));
+                        vt[(wave * (kMD / kAW) + e * 8 + i) * kVt + llane] = (uint16_t)(w4[i >> 1] >> (16 * (i & 1)));
                 }
             }
-            // ---- scores: wave w owns keys [16 (w & 3), +16) of row tile w >> 2
-            if (16 * (wave >> 2) < nq) {
-                const int rt = wave >> 2;
+            // ---- scores: wave w owns keys [16 (w & 3), +16) of row tiles
+            //      w >> 2, (w >> 2) + 2, ...
+#pragma unroll
+            for (int rt = 0; rt < NT; rt++) {
+                if (rt % 2 != (wave >> 2) || rt >= ntl) continue;
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < kMD / 32; ks++) {
-                    const int blk = ks * 4 + g4;
-                    const uint32_t qo = (uint32_t)(rt * 16 + r16) * kMD * 2 + (uint32_t)((blk ^ r16) * 16);
-                    const half8 ah = *reinterpret_cast<const half8 *>(lds + kOffQh + qo);
-                    const half8 al = *reinterpret_cast<const half8 *>(lds + kOffQl + qo);
-                    const half8 kb = kval ? kreg[ks] : half8{};
+                    const int blk = ks * 4 + lg4;
+                    const uint32_t qo = (uint32_t)(rt * 16 + lr16) * kMD * 2 + (uint32_t)((blk ^ lr16) * 16);
+                    const half8 ah = *reinterpret_cast<const half8 *>(lds + LY::Qh + qo);
+                    const half8 al = *reinterpret_cast<const half8 *>(lds + LY::Ql + qo);
+                    const half8 kb = X.kval ? X.k[ks] : half8{};
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, kb, acc, 0, 0, 0);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, kb, acc, 0, 0, 0);
                 }
-                float *S = reinterpret_cast<float *>(lds + kOffS);
-                const int p = key0 + kk_s;
+                float *S = reinterpret_cast<float *>(lds + LY::S);
+                const int p = key0 + lkk;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const int qi = rt * 16 + g4 * 4 + e;
-                    if (qi < nq) S[qi * kMK + kk_s] = p <= p0 + r0 + qi % Rb ? acc[e] * a.scale : -INFINITY;
+                    const int qi = rt * 16 + lg4 * 4 + e;
+                    if (qi < nq) S[qi * kMK + lkk] = p <= p0 + r0 + qi % Rb ? acc[e] * a.scale : -INFINITY;
                 }
             }
+            YK_AT_ACC(3);
             lds_only_barrier();
-            YK_AT_STAMP(3);
-            // ---- online softmax: one wave per query row, lane = key
+            YK_AT_ACC(4);
+            // ---- online softmax: four query rows per wave at a time, one
+            //      16-lane DPP row per query row, lane s holding keys
+            //      [4 s, 4 s + 4) (the row's reductions never leave the DPP
+            //      row, and the four exponentials of a lane overlap)
             {
-                const float *S = reinterpret_cast<const float *>(lds + kOffS);
-                for (int qi = wave; qi < nq; qi += kAW) {
-                    const float sc = S[qi * kMK + lane];
-                    const float mc = wave_max_dpp_f(sc);
-                    const float m_old = Mrow[qi];
+                const float *S = reinterpret_cast<const float *>(lds + LY::S);
+                const int sub = llane >> 4, s16 = llane & 15;
+                for (int q0 = 4 * wave; q0 < nq; q0 += 4 * kAW) {
+                    const int qi = q0 + sub;
+                    const bool live = qi < nq;
+                    const int qc = live ? qi : q0;
+                    const float4 sv = *reinterpret_cast<const float4 *>(S + qc * kMK + 4 * s16);
+                    const float sc[4] = {sv.x, sv.y, sv.z, sv.w};
+                    float mc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+                    mc = fmaxf(mc, dpp_f<0xb1>(mc));
+                    mc = fmaxf(mc, dpp_f<0x4e>(mc));
+                    mc = fmaxf(mc, dpp_f<0x124>(mc));
+                    mc = fmaxf(mc, dpp_f<0x128>(mc));
+                    const float m_old = Mrow[qc];
                     const float m_new = fmaxf(m_old, mc);
-                    float e = 0.0f, alpha = 1.0f;
+                    float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    float alpha = 1.0f;
                     if (m_new != -INFINITY) {
-                        e = (sc == -INFINITY) ? 0.0f : (float)exp((double)(sc - m_new));
+#pragma unroll
+                        for (int i = 0; i < 4; i++) e[i] = (sc[i] == -INFINITY) ? 0.0f : (float)exp((double)(sc[i] - m_new));
                         alpha = m_old == -INFINITY ? 0.0f : (float)exp((double)(m_old - m_new));
                     }
-                    const float lc = wave_sum_dpp_f(e);
-                    const _Float16 hi = (_Float16)e, lo = (_Float16)(e - (float)hi);
-                    // P replaces the row's scores: high halves in bytes [0, 128), low in [128, 256)
-                    const uint32_t off = (uint32_t)qi * kMK * 4 + (uint32_t)((((lane >> 3) ^ (qi & 7)) * 16) + (lane & 7) * 2);
-                    *reinterpret_cast<_Float16 *>(lds + kOffS + off) = hi;
-                    *reinterpret_cast<_Float16 *>(lds + kOffS + kMK * 2 + off) = lo;
-                    if (lane == 0) {
-                        Lrow[qi] = Lrow[qi] * alpha + lc;
-                        Mrow[qi] = m_new;
-                        Arow[qi] = alpha;
+                    float lc = (e[0] + e[1]) + (e[2] + e[3]);
+                    lc += dpp_f<0xb1>(lc);
+                    lc += dpp_f<0x4e>(lc);
+                    lc += dpp_f<0x124>(lc);
+                    lc += dpp_f<0x128>(lc);
+                    _Float16 hi[4], lo[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        hi[i] = (_Float16)e[i];
+                        lo[i] = (_Float16)(e[i] - (float)hi[i]);
+                    }
+                    if (live) {
+                        // P replaces the row's scores: high halves in bytes [0, 128), low in
+                        // [128, 256); keys 4 s16 .. + 3 sit in one 8-key block
+                        const int key = 4 * s16;
+                        const uint32_t off = (uint32_t)qi * kMK * 4 + (uint32_t)((((key >> 3) ^ (qi & 7)) * 16) + (key & 7) * 2);
+                        *reinterpret_cast<uint2 *>(lds + LY::S + off) = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
+                        *reinterpret_cast<uint2 *>(lds + LY::S + kMK * 2 + off) =
+                            make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
+                        if (s16 == 0) {
+                            Lrow[qi] = Lrow[qi] * alpha + lc;
+                            Mrow[qi] = m_new;
+                            Arow[qi] = alpha;
+                        }
                     }
                 }
             }
+            YK_AT_ACC(5);
             lds_only_barrier();
-            YK_AT_STAMP(4);
+            YK_AT_ACC(4);
             // ---- value product: wave w owns dims [32w, 32w + 32); the running
             //      accumulators are rescaled by this chunk's alpha first
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++)
+            for (int rt = 0; rt < NT; rt++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const int qi = rt * 16 + g4 * 4 + e;
+                    const int qi = rt * 16 + lg4 * 4 + e;
                     const float al = qi < nq ? Arow[qi] : 1.0f;
 #pragma unroll
                     for (int j = 0; j < kJ; j++) o[j][rt][e] *= al;
                 }
+            // this wave's V operands for both key halves, then one row tile
+            // at a time (its probabilities, 2 x kJ x 2 MFMAs)
+            half8 vb[kMK / 32][kJ];
 #pragma unroll
-            for (int ks = 0; ks < kMK / 32; ks++) {
-                const int blk = ks * 4 + g4;
-                half8 ah[2], al[2];
-#pragma unroll
-                for (int rt = 0; rt < 2; rt++) {
-                    const uint32_t po = (uint32_t)(rt * 16 + r16) * kMK * 4 + (uint32_t)((blk ^ (r16 & 7)) * 16);
-                    ah[rt] = *reinterpret_cast<const half8 *>(lds + kOffS + po);
-                    al[rt] = *reinterpret_cast<const half8 *>(lds + kOffS + kMK * 2 + po);
-                }
+            for (int ks = 0; ks < kMK / 32; ks++)
 #pragma unroll
                 for (int j = 0; j < kJ; j++) {
-                    const int dcol = wave * (kMD / kAW) + j * 16 + r16;
-                    const half8 b = *reinterpret_cast<const half8 *>(lds + kOffVt + (uint32_t)dcol * kVt * 2 +
-                                                                    (uint32_t)(ks * 32 + g4 * 8) * 2);
-                    o[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[0], b, o[j][0], 0, 0, 0);
-                    o[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[0], b, o[j][0], 0, 0, 0);
-                    if (two) {
-                        o[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[1], b, o[j][1], 0, 0, 0);
-                        o[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[1], b, o[j][1], 0, 0, 0);
+                    const int dcol = wave * (kMD / kAW) + j * 16 + lr16;
+                    vb[ks][j] = *reinterpret_cast<const half8 *>(lds + LY::Vt + (uint32_t)dcol * kVt * 2 +
+                                                                 (uint32_t)(ks * 32 + lg4 * 8) * 2);
+                }
+#pragma unroll
+            for (int rt = 0; rt < NT; rt++) {
+                if (rt >= ntl) continue;
+#pragma unroll
+                for (int ks = 0; ks < kMK / 32; ks++) {
+                    const int blk = ks * 4 + lg4;
+                    const uint32_t po = (uint32_t)(rt * 16 + lr16) * kMK * 4 + (uint32_t)((blk ^ (lr16 & 7)) * 16);
+                    const half8 ah = *reinterpret_cast<const half8 *>(lds + LY::S + po);
+                    const half8 al = *reinterpret_cast<const half8 *>(lds + LY::S + kMK * 2 + po);
+#pragma unroll
+                    for (int j = 0; j < kJ; j++) {
+                        o[j][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, vb[ks][j], o[j][rt], 0, 0, 0);
+                        o[j][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, vb[ks][j], o[j][rt], 0, 0, 0);
                     }
                 }
             }
+            YK_AT_ACC(7);
+        };
+        if constexpr (PF) {
+            // two register sets: chunk ci + 1 loads while chunk ci is computed,
+            // and the page entries of chunk ci + 2 are requested meanwhile.
+            // Every load is issued unconditionally (indices clamped to the last
+            // chunk): under a branch the compiler's wait counts merge
+            // conservatively and the current chunk would wait for the next
+            // one's loads.
+            KvRegs XA, XB;
+            Pages PA, PB;
+            fetch_pages(PA, c_lo);
+            load_kv(XA, PA, c_lo);
+            fetch_pages(PB, min(c_lo + 1, c_hi - 1));
+            for (int ci = c_lo; ci < c_hi; ci += 2) {
+                load_kv(XB, PB, min(ci + 1, c_hi - 1));
+                fetch_pages(PA, min(ci + 2, c_hi - 1));
+                chunk(XA, ci);
+                if (ci + 1 >= c_hi) break;
+                load_kv(XA, PA, min(ci + 2, c_hi - 1));
+                fetch_pages(PB, min(ci + 3, c_hi - 1));
+                chunk(XB, ci + 1);
+            }
+        } else {
+            KvRegs X;
+            Pages P;
+            for (int ci = c_lo; ci < c_hi; ci++) {
+                fetch_pages(P, ci);
+                load_kv(X, P, ci);
+                chunk(X, ci);
+            }
         }
+        YK_AT_STAMP(9);
         // ---- this block's partial records: o, and (m, l) of every row
+        int oz;  // opaque zero: the per-row indices below stay inside the block loop
+        asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+        const int rg4 = g4 + oz, rr16 = r16 + oz;
 #pragma unroll
         for (int j = 0; j < kJ; j++)
 #pragma unroll
-            for (int rt = 0; rt < 2; rt++)
+            for (int rt = 0; rt < NT; rt++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const int qi = rt * 16 + g4 * 4 + e;
+                    const int qi = rt * 16 + rg4 * 4 + e;
                     if (qi < nq) {
-                        const int gq = qi / Rb, r = r0 + qi % Rb, d = wave * (kMD / kAW) + j * 16 + r16;
+                        const int gq = qi / Rb, r = r0 + qi % Rb, d = wave * (kMD / kAW) + j * 16 + rr16;
                         part[(((int64_t)grp * R + r) * a.heads + kvh * G + gq) * (kMD + 2) + d] = o[j][rt][e];
                     }
                 }
@@ -1028,8 +1150,8 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
     YK_AT_STAMP(6);
 #ifdef YK_AT_TIMING
     if (yk_at_dbg && lane == 0) {
-        uint64_t *o = yk_at_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * kAW + wave) * 8;
-        for (int e = 0; e < 8; e++) o[e] = ts[e];
+        uint64_t *o = yk_at_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * kAW + wave) * 12;
+        for (int e = 0; e < 12; e++) o[e] = ts[e];
     }
 #endif
 }
@@ -1121,6 +1243,16 @@ int attn_verify_max_rows(const AttnVArgs &a) {
     return attn_verify_mfma((int)a.fmt, a.heads, a.kv_heads, a.head_dim, a.rope_dim, a.kv_dim) ? 32 : 16;
 }
 
+static int64_t attn_device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 1;
+    }
+    return cus;
+}
+
 static bool use_mfma_path(const AttnVArgs &a) {
     return attn_verify_mfma((int)a.fmt, a.heads, a.kv_heads, a.head_dim, a.rope_dim, a.kv_dim) && a.rows <= 32;
 }
@@ -1134,15 +1266,24 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
     // MFMA kernel: groups of cpw chunks per workgroup once a launch has more
     // than ~1024 chunk workgroups (fewer partial records, query preparation
     // amortized); short contexts keep one chunk per workgroup
+    // Blocks of more than 32 MFMA rows (G x rows) take the six-tile grouped
+    // kernel: one workgroup per CU, so its groups are sized for about one
+    // round of workgroups over the CUs.
+    const bool wide = mfma && (a.heads / a.kv_heads) * a.rows > 32;
     int cpw = 1;
     if (mfma) {
         const int c1 = (a.capacity + kMK - 1) / kMK;
         const int l1 = max_pos_hint >= 0 ? std::min(c1, max_pos_hint / kMK + 1) : c1;
         const int64_t wgs = (int64_t)l1 * a.kv_heads * nz;
         cpw = (int)std::max<int64_t>(1, std::min<int64_t>(8, wgs / 1024));
+        if (wide && cpw > 1) {
+            // groups per (KV head, request) that fit one workgroup per CU
+            const int64_t per = std::max<int64_t>(1, attn_device_cus() / ((int64_t)a.kv_heads * nz));
+            cpw = (int)std::max<int64_t>(2, std::min<int64_t>(32, (l1 + per - 1) / per));
+        }
         if (const char *e = getenv("YUUKA_ATTN_CPW")) {  // tests and tuning: a fixed group size
             const int v = atoi(e);
-            if (v >= 1 && v <= 8) cpw = v;
+            if (v >= 1 && v <= 32) cpw = v;
         }
     }
     const int ck = mfma ? kMK * cpw : attn_verify_chunk(a.fmt);
@@ -1154,7 +1295,9 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
         if (!attr2) {
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_mfma_kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_mfma_group_kernel),
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_mfma_group_kernel<2, false>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_mfma_group_kernel<6, true>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
             attr2 = true;
         }
@@ -1163,10 +1306,14 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
             attn_verify_mfma_kernel<<<grid, 64 * kAW, kMfmaLds, s>>>(q, k, v, static_cast<uint16_t *>(kpool),
                                                                       static_cast<uint16_t *>(vpool), table, q_norm,
                                                                       k_norm, rope, a, part, dyn);
+        else if (wide)
+            attn_verify_mfma_group_kernel<6, true><<<grid, 64 * kAW, GroupLds<6>::total, s>>>(
+                q, k, v, static_cast<uint16_t *>(kpool), static_cast<uint16_t *>(vpool), table, q_norm, k_norm, rope,
+                a, part, dyn, cpw);
         else
-            attn_verify_mfma_group_kernel<<<grid, 64 * kAW, kMfmaLds, s>>>(q, k, v, static_cast<uint16_t *>(kpool),
-                                                                            static_cast<uint16_t *>(vpool), table,
-                                                                            q_norm, k_norm, rope, a, part, dyn, cpw);
+            attn_verify_mfma_group_kernel<2, false><<<grid, 64 * kAW, kMfmaLds, s>>>(
+                q, k, v, static_cast<uint16_t *>(kpool), static_cast<uint16_t *>(vpool), table, q_norm, k_norm, rope,
+                a, part, dyn, cpw);
     } else if (a.fmt == 1) {
         const uint32_t lds = attn_verify_lds_bytes(a);
         if (!attr1) {
