@@ -563,16 +563,19 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
     //      rows are loaded first, then computed (no load waits in the loop).
     const int RB = kMQ / G;
     auto prep_q = [&](int r0, int Rb) __attribute__((always_inline)) {
+        int oz;  // opaque zero: keeps the per-vector offsets below from being hoisted and spilled
+        asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+        const int plane = lane + oz;
         constexpr int kQV = kMQ / kAW;
         const int nqb = G * Rb;
-        const float4 w4 = *reinterpret_cast<const float4 *>(q_norm + 4 * lane);
+        const float4 w4 = *reinterpret_cast<const float4 *>(q_norm + 4 * plane);
         float4 xq[kQV];
 #pragma unroll
         for (int t = 0; t < kQV; t++) {
             const int vec = wave + kAW * t;
             if (vec < nqb) {
                 const int gq = vec / Rb, r = r0 + vec % Rb;
-                xq[t] = *reinterpret_cast<const float4 *>(q + ((int64_t)r * a.heads + kvh * G + gq) * qstride + 4 * lane);
+                xq[t] = *reinterpret_cast<const float4 *>(q + ((int64_t)r * a.heads + kvh * G + gq) * qstride + 4 * plane);
             }
         }
 #pragma unroll
@@ -581,11 +584,11 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
             if (vec >= nqb) break;
             const int r = r0 + vec % Rb;
             float2 cq[4] = {};
-            if (lane < 16) {
+            if (plane < 16) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int e = 4 * lane + i;
-                    cq[i] = rope[r * half + (lane < 8 ? e : e - 32)];
+                    const int e = 4 * plane + i;
+                    cq[i] = rope[r * half + (plane < 8 ? e : e - 32)];
                 }
             }
             float y[4];
@@ -596,7 +599,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
                 hi[i] = (_Float16)y[i];
                 lo[i] = (_Float16)(y[i] - (float)hi[i]);
             }
-            const uint32_t off = (uint32_t)vec * kMD * 2 + (uint32_t)(((lane >> 1) ^ (vec & 15)) * 16 + (lane & 1) * 8);
+            const uint32_t off = (uint32_t)vec * kMD * 2 + (uint32_t)(((plane >> 1) ^ (vec & 15)) * 16 + (plane & 1) * 8);
             *reinterpret_cast<uint2 *>(lds + kOffQh + off) = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
             *reinterpret_cast<uint2 *>(lds + kOffQl + off) = make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
         }
@@ -683,24 +686,50 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
     }
     lds_only_barrier();
     YK_AT_STAMP(4);
-    // ---- softmax partials: one wave per query row, lane = key
+    // ---- softmax partials: four query rows per wave at a time, one 16-lane
+    //      DPP row per query row, lane s holding keys [4 s, 4 s + 4)
     {
         const float *S = reinterpret_cast<const float *>(lds + kOffS);
-        for (int qi = wave; qi < nq; qi += kAW) {
-            const float sc = S[qi * kMK + lane];
-            const float m = wave_max_dpp_f(sc);
-            const float e = (sc == -INFINITY) ? 0.0f : (float)exp((double)(sc - m));
-            const float l = wave_sum_dpp_f(e);
-            const _Float16 hi = (_Float16)e, lo = (_Float16)(e - (float)hi);
-            // P replaces the row's scores: high halves in bytes [0, 128), low in [128, 256)
-            const uint32_t off = (uint32_t)qi * kMK * 4 + (uint32_t)((((lane >> 3) ^ (qi & 7)) * 16) + (lane & 7) * 2);
-            *reinterpret_cast<_Float16 *>(lds + kOffS + off) = hi;
-            *reinterpret_cast<_Float16 *>(lds + kOffS + kMK * 2 + off) = lo;
-            if (lane == 0) {
-                const int gq = qi / Rb, r = r0 + qi % Rb;
-                float *rec = part + (((int64_t)chunk * R + r) * a.heads + kvh * G + gq) * (kMD + 2);
-                rec[kMD] = m;
-                rec[kMD + 1] = l;
+        const int sub = lane >> 4, s16 = lane & 15;
+        for (int q0 = 4 * wave; q0 < nq; q0 += 4 * kAW) {
+            const int qi = q0 + sub;
+            const bool live = qi < nq;
+            const int qc = live ? qi : q0;
+            const float4 sv = *reinterpret_cast<const float4 *>(S + qc * kMK + 4 * s16);
+            const float sc[4] = {sv.x, sv.y, sv.z, sv.w};
+            float m = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+            m = fmaxf(m, dpp_f<0xb1>(m));
+            m = fmaxf(m, dpp_f<0x4e>(m));
+            m = fmaxf(m, dpp_f<0x124>(m));
+            m = fmaxf(m, dpp_f<0x128>(m));
+            float e[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) e[i] = (sc[i] == -INFINITY) ? 0.0f : (float)exp((double)(sc[i] - m));
+            float l = (e[0] + e[1]) + (e[2] + e[3]);
+            l += dpp_f<0xb1>(l);
+            l += dpp_f<0x4e>(l);
+            l += dpp_f<0x124>(l);
+            l += dpp_f<0x128>(l);
+            _Float16 hi[4], lo[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                hi[i] = (_Float16)e[i];
+                lo[i] = (_Float16)(e[i] - (float)hi[i]);
+            }
+            if (live) {
+                // P replaces the row's scores: high halves in bytes [0, 128), low in [128, 256);
+                // keys 4 s16 .. + 3 sit in one 8-key block
+                const int key = 4 * s16;
+                const uint32_t off = (uint32_t)qi * kMK * 4 + (uint32_t)((((key >> 3) ^ (qi & 7)) * 16) + (key & 7) * 2);
+                *reinterpret_cast<uint2 *>(lds + kOffS + off) = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
+                *reinterpret_cast<uint2 *>(lds + kOffS + kMK * 2 + off) =
+                    make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
+                if (s16 == 0) {
+                    const int gq = qi / Rb, r = r0 + qi % Rb;
+                    float *rec = part + (((int64_t)chunk * R + r) * a.heads + kvh * G + gq) * (kMD + 2);
+                    rec[kMD] = m;
+                    rec[kMD + 1] = l;
+                }
             }
         }
     }
