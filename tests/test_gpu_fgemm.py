@@ -22,6 +22,17 @@ def _check(got, want, budget=5e-4):
     assert np.all(err <= 1e-2 * (np.abs(want) + rms))
 
 
+# Launches of more than 8 rows take the many-row kernel. Its MFMA operands
+# are FP16, as in the reference's own many-row GEMM
+# (kernels/hip/gemm/wmma_gemm.hip load_a_tile / load_b_tile): the activations
+# round to FP16 (at most 2^-12 relative per element) and the Q6_K scale x
+# quant products above 2048 to even integers, with FP32 accumulation. The
+# largest error over a launch's outputs is then about 1e-3 of their rms
+# (SwiGLU products about twice that); MANY_BUDGET bounds it, and the
+# per-element 1e-2 bound of the verify logits is checked as everywhere.
+MANY_BUDGET = 3e-3
+
+
 def _run(dev, stream, x, segs, k, rows, epilogue=hip.EPI_STORE, norm=None, eps=1e-6, residuals=None):
     """segs: [(dtype, w_bytes_array, n_out)] -> list of outputs."""
     plan = hip.Plan(dev)
@@ -73,7 +84,7 @@ def test_fused_gemm_matches_oracle(dev, stream, segs, k, rows, norm):
     got = _run(dev, stream, x, [(dt, w, n) for (dt, n), w in zip(segs, ws)], k, rows, norm=g)
     y = O.rmsnorm_rows(x, g, 1e-6) if norm else x
     for (dt, n), w, gv in zip(segs, ws, got):
-        _check(gv, _want(dt, w, n, k, y))
+        _check(gv, _want(dt, w, n, k, y), budget=MANY_BUDGET if rows > 8 else 5e-4)
 
 
 def test_fused_gemm_residual_epilogue(dev, stream):
@@ -213,7 +224,7 @@ def test_fused_gemm_many_rows(dev, stream, segs, k, rows, norm):
     got = _run(dev, stream, x, [(dt, w, n) for (dt, n), w in zip(segs, ws)], k, rows, norm=g)
     y = O.rmsnorm_rows(x, g, 1e-6) if norm else x
     for (dt, n), w, gv in zip(segs, ws, got):
-        _check(gv, _want(dt, w, n, k, y))
+        _check(gv, _want(dt, w, n, k, y), budget=MANY_BUDGET)
 
 
 def test_fused_gemm_many_rows_epilogues(dev, stream):
@@ -226,10 +237,10 @@ def test_fused_gemm_many_rows_epilogues(dev, stream):
     wu = synth.quant_matrix(rng, O.Q4_K, n, k)
     y = O.rmsnorm_rows(x, g, 1e-6)
     got = _run(dev, stream, x, [(O.Q4_K, wg, n), (O.Q4_K, wu, n)], k, rows, hip.EPI_SWIGLU, norm=g)[0]
-    _check(got, O.silu_mul(_want(O.Q4_K, wg, n, k, y), _want(O.Q4_K, wu, n, k, y)), budget=1e-3)
+    _check(got, O.silu_mul(_want(O.Q4_K, wg, n, k, y), _want(O.Q4_K, wu, n, k, y)), budget=2 * MANY_BUDGET)
     res = rng.normal(0, 3, (rows, n)).astype(np.float32)
     got = _run(dev, stream, x, [(O.Q4_K, wg, n)], k, rows, hip.EPI_RESIDUAL, residuals=[res])[0]
-    _check(got - res, _want(O.Q4_K, wg, n, k, x))
+    _check(got - res, _want(O.Q4_K, wg, n, k, x), budget=MANY_BUDGET)
     # gated head norm prologue + SiLU output map
     z = rng.normal(0, 1, (rows, k)).astype(np.float32)
     w = rng.normal(1, 0.1, 128).astype(np.float32)
@@ -245,4 +256,4 @@ def test_fused_gemm_many_rows_epilogues(dev, stream):
     got = ob.read(np.float32).reshape(rows, n)
     plan.destroy()
     prod = _want(O.Q4_K, wg, n, k, _gated_head_norm(x, z, w, 1e-6))
-    _check(got, O.silu_mul(prod, np.ones_like(prod)), budget=1e-3)
+    _check(got, O.silu_mul(prod, np.ones_like(prod)), budget=2 * MANY_BUDGET)

@@ -50,6 +50,13 @@ def _gemm(dev, stream, dtype, w, x, n, k, m):
     return ob.read(np.float32).reshape(m, n)
 
 
+# Launches of more than 8 rows take the many-row kernel, whose MFMA operands
+# are FP16 as in the reference's own many-row GEMM
+# (kernels/hip/gemm/wmma_gemm.hip): activations rounded to FP16, at most
+# 2^-12 relative per element, the largest output error about 1e-3 of the rms.
+MANY_ROWS_BUDGET = 3e-3
+
+
 def _check(got, want, budget=5e-4):
     # `budget`: error budget of the 16-bit per-row activation quantization
     # relative to the output rms (observed ~2.5e-4 at configuration 1). The
@@ -83,7 +90,7 @@ def test_verify_gemm_matches_oracle(dev, stream, dtype, n, k, m):
     x = rng.normal(0, 1, (m, k)).astype(np.float32)
     got = _gemm(dev, stream, dtype, w, x, n, k, m)
     want = O.matmul(dtype, w, x, n, k)
-    _check(got, want)
+    _check(got, want, budget=MANY_ROWS_BUDGET if m > 8 else 5e-4)
 
 
 def test_verify_gemm_is_bitwise_repeatable(dev, stream):

@@ -6,28 +6,39 @@
 // RMSNorm or gated head norm of x, store / residual / SwiGLU, output maps).
 // At a few rows the fused streaming kernel reads every weight once per
 // launch; a batch of B requests x (k+1) rows would read them once per 8-row
-// block. Here each weight super-block is read once per 64 rows:
+// block. Here each weight super-block is read once per 64 rows, and the
+// products run on v_mfma_f32_16x16x32_f16:
 //
 //  * prologue (one workgroup per row): y = prologue(x) computed as the
 //    reference computes it (forward.go:460-482 rmsNorm, recurrent.go:39-50
-//    gated norm), then quantized per 256-element super-block into an int16
-//    split into two int8 planes (q = 256 h + l, |q| <= 32639) and one scale
-//    per (row, super-block) — a workspace of rows * (2K + K/64) B.
+//    gated norm), then per 256-element super-block scaled into [-256, 256]
+//    (one FP32 scale per row and super-block) and rounded to FP16, with the
+//    FP32 sum of every 32-element sub-block of those FP16 values stored as an
+//    FP16 high part and its FP16 remainder — a workspace of
+//    rows * (2 K + K / 8 + K / 64) B.
 //  * GEMM (workgroup = 64 rows x 8 tiles of 16 output channels, one tile per
-//    wave): per super-block the workgroup stages the 64 rows' planes in LDS
-//    in MFMA operand order; each wave decodes its tile's weights straight
-//    from HBM into MFMA B operands while the next super-block's weights are
-//    in flight, and multiplies them with the eight 8-row A tiles (high planes
-//    in MFMA rows 0..7, low planes in 8..15). Q4_K: the 6-bit sub-block scale
-//    and min ride in the B operands (three v_mfma_i32_16x16x64_i8 per pair of
-//    sub-blocks); Q6_K: two v_mfma_i32_16x16x32_i8 per sub-block (one per
-//    16-element scale group), scales applied in int32. Everything up to the
-//    super-block is exact integer; d / dmin and the activation scale are
-//    applied per super-block in FP32.
+//    wave): per super-block the workgroup stages the 64 rows' FP16 values and
+//    sub-block sums in LDS, double-buffered; each wave decodes its tile's
+//    weights straight from HBM into MFMA B operands while the next
+//    super-block's weights are in flight.
+//    - Q4_K: the 6-bit sub-block scale is folded into the operand, B = sc q
+//      (at most 945, exact in FP16), so the eight K = 32 MFMAs of a
+//      super-block chain into one FP32 accumulator; the min term
+//      sum_j m_j sum_k y_k is one more MFMA of the sub-block sums (high and
+//      remainder in K slots 0..7 and 8..15) against the 6-bit mins. Then
+//      acc * d - mins * dmin, times the row scale, per super-block in FP32.
+//    - Q6_K: B = sc q with the signed 8-bit scale of the lane's 16-element
+//      group (|sc q| <= 4064, rounded to FP16 above 2048, as the reference's
+//      FP16 dequantization rounds d sc q), times d and the row scale.
+//    The weights are the reference's FP16 dequantized values up to the FP32
+//    factors d and dmin, and the activations FP16 as in the reference's own
+//    FP16 GEMM (kernels/hip/gemm/wmma_gemm.hip load_a_tile / load_b_tile);
+//    products and sums are exact in the MFMA's FP32 accumulation.
 //
 // Replaces, for batched verify shapes, the reference's per-matrix GEMV
 // launches over all rows (kernels/hip/gemm/lm_head.hip:61-173 with MaxRows 16,
-// engine/gpu/plan.go); no reference kernel serves more than 16 rows.
+// engine/gpu/plan.go); no reference kernel on the verify path serves more
+// than 16 rows.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -42,29 +53,37 @@ namespace yk {
 namespace {
 
 typedef __attribute__((ext_vector_type(4))) int i32x4;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 constexpr int kQ4K = YUUKA_DTYPE_Q4_K;
 constexpr int kQ6K = YUUKA_DTYPE_Q6_K;
-constexpr int kQMax = 32639;
 constexpr int kBgWaves = 8;
 constexpr int kBgThreads = 64 * kBgWaves;
-constexpr int kBgRows = 64;  // rows per workgroup: 8 A tiles of 8 rows
-// LDS of the GEMM, per stage: A planes [8 t][4 jp][4 g][16 r][2][8 B] +
-// scales [8 t][8] float; two stages. The SwiGLU epilogue reuses the first.
-constexpr uint32_t kBgLdsA = 8 * 8 * 4 * 16 * 8;
-constexpr uint32_t kBgStage = kBgLdsA + 8 * 8 * 4;  // one stage (double-buffered)
+constexpr int kBgRows = 64;  // rows per workgroup: four 16-row MFMA tiles
+// LDS of the GEMM, per stage: A [64 rows][32 blocks of 8 FP16] with block b
+// of row r at b ^ (r & 15) (a tile's 16 rows read one block each without
+// bank conflicts), sums [64 rows][16 FP16], row scales [64] float; two
+// stages. The SwiGLU epilogue reuses the first.
+constexpr uint32_t kBgLdsA = kBgRows * 512;
+constexpr uint32_t kBgLdsSum = kBgRows * 32;
+constexpr uint32_t kBgStage = kBgLdsA + kBgLdsSum + kBgRows * 4;
 constexpr uint32_t kBgLds = 2 * kBgStage;
+constexpr float kBgRange = 256.0f;  // |y / scale| <= kBgRange
 
 struct BgQuant {
-    int8_t *planes;  // [rows][K/32][2: high, low][32 B]
+    _Float16 *h;     // [rows][K]: y / scale
+    _Float16 *sums;  // [rows][K/256][16]: sub-block sums of h, high parts (8) then remainders (8)
     float *scales;   // [rows][K/256]
 };
 
 __host__ __device__ inline BgQuant bg_view(void *ws, int rows, int K) {
     uint8_t *p = static_cast<uint8_t *>(ws);
     BgQuant q;
-    q.planes = reinterpret_cast<int8_t *>(p);
-    q.scales = reinterpret_cast<float *>(p + (uint64_t)rows * K * 2);
+    q.h = reinterpret_cast<_Float16 *>(p);
+    q.sums = reinterpret_cast<_Float16 *>(p + (uint64_t)rows * K * 2);
+    q.scales = reinterpret_cast<float *>(p + (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 256) * 32);
     return q;
 }
 
@@ -105,6 +124,16 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {
     const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
     const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+// Sum over each aligned group of 8 lanes, in every lane of the group.
+__device__ __forceinline__ float group8_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xb1, 0xf, 0xf, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4e, 0xf, 0xf, true));
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, true));
+}
+
+__device__ __forceinline__ uint32_t h2bits(_Float16 a, _Float16 b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
 // ---------------------------------------------------------------- prologue
@@ -169,22 +198,19 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
         }
         float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
         m = wave_max_nonneg(m);
-        const float inv = m > 0.f ? (float)kQMax / m : 0.f;
-        const int qv[4] = {(int)rintf(v.x * inv), (int)rintf(v.y * inv), (int)rintf(v.z * inv),
-                           (int)rintf(v.w * inv)};
-        uint32_t hp = 0, lp = 0;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int h = (qv[i] + 128) >> 8;
-            const int l = qv[i] - 256 * h;
-            hp |= (uint32_t)(h & 0xff) << (8 * i);
-            lp |= (uint32_t)(l & 0xff) << (8 * i);
+        const float inv = m > 0.f ? kBgRange / m : 0.f;
+        const _Float16 h0 = (_Float16)(v.x * inv), h1 = (_Float16)(v.y * inv), h2 = (_Float16)(v.z * inv),
+                       h3 = (_Float16)(v.w * inv);
+        *reinterpret_cast<uint2 *>(q.h + (uint64_t)row * K + e) = make_uint2(h2bits(h0, h1), h2bits(h2, h3));
+        // sub-block lane >> 3: eight lanes of four values
+        const float s = group8_sum(((float)h0 + (float)h1) + ((float)h2 + (float)h3));
+        if ((lane & 7) == 0) {
+            const _Float16 shi = (_Float16)s, slo = (_Float16)(s - (float)shi);
+            _Float16 *sd = q.sums + ((uint64_t)row * nsb + sb) * 16 + (lane >> 3);
+            sd[0] = shi;
+            sd[8] = slo;
         }
-        const int j = lane >> 3, o = 4 * (lane & 7);
-        int8_t *dst = q.planes + (uint64_t)row * K * 2 + (uint64_t)(sb * 8 + j) * 64 + o;
-        *reinterpret_cast<uint32_t *>(dst) = hp;
-        *reinterpret_cast<uint32_t *>(dst + 32) = lp;
-        if (lane == 0) q.scales[(uint64_t)row * nsb + sb] = m > 0.f ? m / (float)kQMax : 0.f;
+        if (lane == 0) q.scales[(uint64_t)row * nsb + sb] = m > 0.f ? m / kBgRange : 0.f;
     }
 }
 
@@ -199,24 +225,6 @@ struct BgArgs {
     float *part;                  // [splits][rows][cols[nseg]]
 };
 
-// 24-bit multiply-add (full rate; a 32-bit multiply is quarter rate). Used
-// for the Q6_K digit recombination 49 a2 + 7 a1 + a0, where |a| < 2^22.
-__device__ __forceinline__ int mad24(int a, int b, int c) { return __mul24(a, b) + c; }
-
-typedef __attribute__((ext_vector_type(2))) unsigned short u16x2;
-
-// Every byte of q times k, for byte products below 256: one packed 16-bit
-// multiply (b0 + 256 b1) k = b0 k + 256 b1 k per half, no carry between bytes.
-__device__ __forceinline__ uint32_t bytes_times(uint32_t q, uint32_t k) {
-    const u16x2 b = {(unsigned short)k, (unsigned short)k};
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, q) * b);
-}
-
-__device__ __forceinline__ i32x4 mfma_i8(int64_t a, int64_t b) {
-    const i32x4 zero = {0, 0, 0, 0};
-    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, zero, 0, 0, 0);
-}
-
 // 8 bytes at an even byte address (Q6_K blocks are 210 B): two dword-aligned
 // loads and a byte shift.
 __device__ __forceinline__ uint64_t load8_even(const uint8_t *p) {
@@ -227,13 +235,6 @@ __device__ __forceinline__ uint64_t load8_even(const uint8_t *p) {
     const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
     const uint32_t hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
     return (uint64_t)lo | ((uint64_t)hi << 32);
-}
-
-// Signed q - 32 for eight packed unsigned 6-bit values (one per byte).
-__device__ __forceinline__ uint64_t q6_to_i8(uint64_t q6) {
-    const uint64_t t = q6 ^ 0x2020202020202020ull;
-    const uint64_t s = t & 0x2020202020202020ull;
-    return t | (s << 1) | (s << 2);
 }
 
 // One super-block of one channel, as lane (c, g) needs it.
@@ -305,63 +306,78 @@ __device__ __forceinline__ float out_map(const FusedSeg &S, int n, float v) {
     }
 }
 
-// Super-block sb of the workgroup's rows (planes, scales): loaded by
-// every thread into registers, then written to one of two LDS buffers.
+// FP16 pairs from byte pairs: (x & mask) | 0x6400 in each 16-bit half is
+// 1024 + x as FP16 (x < 1024).
+__device__ __forceinline__ half2v magic_pair(uint32_t w, uint32_t mask) {
+    return __builtin_bit_cast(half2v, (w & mask) | 0x64006400u);
+}
+__device__ __forceinline__ half2v splat_h(float v) {
+    const _Float16 h = (_Float16)v;
+    return half2v{h, h};
+}
+// Operand of one K = 32 MFMA as four FP16 pairs.
+__device__ __forceinline__ half8 pack8(half2v a, half2v b, half2v c, half2v d) {
+    return half8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Super-block sb of the workgroup's rows: loaded into registers by every
+// thread, then written to one of two LDS stages.
 struct Staged {
-    uint4 v[4];
-    float xs;
+    uint4 v[4];  // FP16 values: piece u = threadIdx.x + 512 k is row u >> 5, block u & 31
+    uint4 s;     // sums: threads < 128, row t >> 1, half t & 1
+    float xs;    // row scale: threads < 64
 };
 
-// LDS byte offset of the 8 A bytes of tile t (8 rows, two planes), sub-block
-// j, lane group gg, MFMA row rr: sub-blocks 2 jp and 2 jp + 1 sit side by side,
-// so one 16-byte read gives a lane both halves of a K = 64 operand.
-__device__ __forceinline__ uint32_t la_off(int t, int j, int gg, int rr) {
-    return ((uint32_t)(((t * 4 + (j >> 1)) * 4 + gg) * 16 + rr) * 2 + (j & 1)) * 8;
-}
-
-// Thread piece u = ((t * 8 + j) * 2 + half) * 16 + rr (four per thread):
-// bytes [16 half, 16 half + 16) of plane rr >> 3 of row 8 t + (rr & 7),
-// sub-block j: one 16-byte global load (a row's 128 bytes come from 8
-// lanes) and two 8-byte LDS writes for lane groups 2 half and 2 half + 1
-// that cover every bank.
 __device__ __forceinline__ void stage_load(const BgArgs &A, Staged &st, int m0, int mrows, int sb) {
     const int K = A.f.K, nsb = K / 256;
+    int oz;  // opaque zero: the thread's addresses are recomputed per call, not held (and spilled) across the loop
+    asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+    const int tid = (int)threadIdx.x + oz;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        const int u = threadIdx.x + k * kBgThreads;
-        const int rr = u & 15, half = (u >> 4) & 1, j = (u >> 5) & 7, t = u >> 8;
-        const int r = 8 * t + (rr & 7);
-        st.v[k] = r < mrows ? *reinterpret_cast<const uint4 *>(A.q.planes + (uint64_t)(m0 + r) * K * 2 +
-                                                               (uint64_t)(sb * 8 + j) * 64 + 32 * (rr >> 3) + 16 * half)
+        const int u = tid + k * kBgThreads;
+        const int r = u >> 5, b = u & 31;
+        st.v[k] = r < mrows ? *reinterpret_cast<const uint4 *>(A.q.h + (uint64_t)(m0 + r) * K + sb * 256 + b * 8)
                             : make_uint4(0u, 0u, 0u, 0u);
     }
-    st.xs = threadIdx.x < mrows ? A.q.scales[(uint64_t)(m0 + threadIdx.x) * nsb + sb] : 0.f;
+    {
+        const int r = (tid >> 1) & 63, hf = tid & 1;
+        st.s = tid < 128 && r < mrows
+                   ? *reinterpret_cast<const uint4 *>(A.q.sums + ((uint64_t)(m0 + r) * nsb + sb) * 16 + hf * 8)
+                   : make_uint4(0u, 0u, 0u, 0u);
+    }
+    st.xs = tid < mrows ? A.q.scales[(uint64_t)(m0 + tid) * nsb + sb] : 0.f;
 }
 
-__device__ __forceinline__ void stage_store(const Staged &st, uint8_t *la, float *lxs) {
+__device__ __forceinline__ void stage_store(const Staged &st, uint8_t *stage) {
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const int u = threadIdx.x + k * kBgThreads;
-        const int rr = u & 15, half = (u >> 4) & 1, j = (u >> 5) & 7, t = u >> 8;
-        uint8_t *d0 = la + la_off(t, j, 2 * half, rr);
-        *reinterpret_cast<uint2 *>(d0) = make_uint2(st.v[k].x, st.v[k].y);
-        *reinterpret_cast<uint2 *>(d0 + 256) = make_uint2(st.v[k].z, st.v[k].w);
+        const int r = u >> 5, b = u & 31;
+        *reinterpret_cast<uint4 *>(stage + (uint32_t)r * 512 + (uint32_t)((b ^ (r & 15)) * 16)) = st.v[k];
     }
-    if (threadIdx.x < kBgRows) lxs[threadIdx.x] = st.xs;
+    if (threadIdx.x < 128) *reinterpret_cast<uint4 *>(stage + kBgLdsA + threadIdx.x * 16) = st.s;
+    if (threadIdx.x < kBgRows) reinterpret_cast<float *>(stage + kBgLdsA + kBgLdsSum)[threadIdx.x] = st.xs;
 }
 
-// The main loop of one wave over the super-blocks (weights of dtype DT).
-// LDS holds two stages; stage sb + 1 is loaded while sb is multiplied.
-template <int DT, int TH>
+// A operand of row tile t, sub-block j for lane (row c, group g).
+__device__ __forceinline__ half8 a_op(const uint8_t *stage, int t, int j, int c, int g) {
+    const int r = 16 * t + c, b = 4 * j + g;
+    return *reinterpret_cast<const half8 *>(stage + (uint32_t)r * 512 + (uint32_t)((b ^ c) * 16));
+}
+
+// The main loop of one wave over the super-blocks (weights of dtype DT), NT
+// row tiles of 16. LDS holds two stages; stage sb + 1 is loaded while sb is
+// multiplied.
+template <int DT, int NT>
 __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, int mrows, bool live,
-                                        const uint8_t *wrow, float (&y)[8][4]) {
+                                        const uint8_t *wrow, float (&y)[4][4]) {
     const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
     // this split's super-blocks [sb_lo, nsb)
     const int nsb_all = A.f.K / 256;
     const int sb_lo = (int)((int64_t)nsb_all * blockIdx.z / A.splits);
     const int nsb = (int)((int64_t)nsb_all * (blockIdx.z + 1) / A.splits);
     wrow += (uint64_t)sb_lo * (DT == kQ4K ? 144 : 210);
-    const int rb = 4 * (g & 1);
     typedef typename std::conditional<DT == kQ4K, WQ4, WQ6>::type W;
     constexpr int blk = DT == kQ4K ? 144 : 210;
     W w{};
@@ -371,13 +387,12 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
     }
     Staged st;
     stage_load(A, st, m0, mrows, sb_lo);
-    stage_store(st, lds, reinterpret_cast<float *>(lds + kBgLdsA));
+    stage_store(st, lds);
     __syncthreads();
     for (int sb = sb_lo; sb < nsb; sb++) {
-        uint8_t *cur_l = lds + (uint32_t)((sb - sb_lo) & 1) * kBgStage;
+        const uint8_t *cur_l = lds + (uint32_t)((sb - sb_lo) & 1) * kBgStage;
         uint8_t *nxt_l = lds + (uint32_t)((sb - sb_lo + 1) & 1) * kBgStage;
-        const uint8_t *la = cur_l;
-        const float *lxs = reinterpret_cast<const float *>(cur_l + kBgLdsA);
+        const float *lxs = reinterpret_cast<const float *>(cur_l + kBgLdsA + kBgLdsSum);
         const bool more = sb + 1 < nsb;
         if (more) stage_load(A, st, m0, mrows, sb + 1);
         const W cur = w;  // this super-block; the next one's loads go out now
@@ -386,157 +401,102 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
             else load_q6(w, wrow + (uint64_t)(sb + 1 - sb_lo) * blk, g);
         }
         if (live) {
+            // lane constants re-derived per super-block from an opaque zero:
+            // hoisted out of the loop, the per-tile LDS offsets they feed
+            // would be spilled
+            int oz;
+            asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+            const int lc = c + oz, lg = g + oz;
+            // sub-block pairs outer, row tiles inner: two B operands live at a
+            // time, one FP32 accumulator per row tile
+            f32x4 acc[NT];
+#pragma unroll
+            for (int t = 0; t < NT; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            float d, dmin = 0.f;
             if constexpr (DT == kQ4K) {
-                // Scale and min term on the MFMA accumulators: with sc = 8 sc_hi
-                // + sc_lo (3-bit digits), q * sc_lo and q * sc_hi (<= 105) are
-                // exact int8 B operands, and the sub-block min m (<= 63)
-                // broadcast over the sub-block gives the min term directly. A
-                // K = 64 MFMA covers sub-blocks 2 jp and 2 jp + 1 (low and high
-                // nibbles of the same quant bytes): three chained MFMAs per
-                // sub-block pair and 8-row tile, no VALU multiply-adds. Two
-                // passes of four A tiles bound the registers.
-                const float d = h2f((uint16_t)(cur.hdr.x & 0xffffu)), dmin = h2f((uint16_t)(cur.hdr.x >> 16));
+                d = h2f((uint16_t)(cur.hdr.x & 0xffffu));
+                dmin = h2f((uint16_t)(cur.hdr.x >> 16));
+                _Float16 mins[8];
 #pragma unroll
-                for (int th = 0; th < TH; th++) {  // TH = 1: rows in tiles 0..3 only
-                    i32x4 alo[4], ahi[4], amn[4];
+                for (int jp = 0; jp < 4; jp++) {
+                    int sce, mne, sco, mno;
+                    scale_min_k4(2 * jp, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sce, &mne);
+                    scale_min_k4(2 * jp + 1, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sco, &mno);
+                    mins[2 * jp] = (_Float16)mne;
+                    mins[2 * jp + 1] = (_Float16)mno;
+                    // bytes b0..b7 of the lane: low nibbles are sub-block 2 jp,
+                    // high nibbles 2 jp + 1; (1024 + q) sc - 1024 sc = q sc exactly
+                    const uint32_t w0 = (uint32_t)cur.q[jp], w1 = (uint32_t)(cur.q[jp] >> 32);
+                    const uint32_t p01 = __builtin_amdgcn_perm(0u, w0, 0x0c010c00u), p23 = __builtin_amdgcn_perm(0u, w0, 0x0c030c02u);
+                    const uint32_t p45 = __builtin_amdgcn_perm(0u, w1, 0x0c010c00u), p67 = __builtin_amdgcn_perm(0u, w1, 0x0c030c02u);
+                    const half2v se = splat_h((float)sce), so = splat_h((float)sco);
+                    const half2v ce = splat_h(-1024.f * (float)sce), co = splat_h(-1024.f * (float)sco);
+                    const half8 be = pack8(__builtin_elementwise_fma(magic_pair(p01, 0x000F000Fu), se, ce),
+                                           __builtin_elementwise_fma(magic_pair(p23, 0x000F000Fu), se, ce),
+                                           __builtin_elementwise_fma(magic_pair(p45, 0x000F000Fu), se, ce),
+                                           __builtin_elementwise_fma(magic_pair(p67, 0x000F000Fu), se, ce));
+                    const half8 bo = pack8(__builtin_elementwise_fma(magic_pair(p01 >> 4, 0x000F000Fu), so, co),
+                                           __builtin_elementwise_fma(magic_pair(p23 >> 4, 0x000F000Fu), so, co),
+                                           __builtin_elementwise_fma(magic_pair(p45 >> 4, 0x000F000Fu), so, co),
+                                           __builtin_elementwise_fma(magic_pair(p67 >> 4, 0x000F000Fu), so, co));
 #pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        alo[u] = i32x4{0, 0, 0, 0};
-                        ahi[u] = i32x4{0, 0, 0, 0};
-                        amn[u] = i32x4{0, 0, 0, 0};
-                    }
-#pragma unroll
-                    for (int jp = 0; jp < 4; jp++) {
-                        const uint64_t raw = cur.q[jp];
-                        const uint64_t qe = raw & 0x0F0F0F0F0F0F0F0Full, qo = (raw >> 4) & 0x0F0F0F0F0F0F0F0Full;
-                        int sce, mne, sco, mno;
-                        scale_min_k4(2 * jp, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sce, &mne);
-                        scale_min_k4(2 * jp + 1, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sco, &mno);
-                        // per-byte products stay below 256: no carries between bytes
-                        const uint32_t q[4] = {(uint32_t)qe, (uint32_t)(qe >> 32), (uint32_t)qo, (uint32_t)(qo >> 32)};
-                        const uint32_t lo[2] = {(uint32_t)(sce & 7), (uint32_t)(sco & 7)};
-                        const uint32_t hi[2] = {(uint32_t)(sce >> 3), (uint32_t)(sco >> 3)};
-                        const i32x4 b_lo = {(int)bytes_times(q[0], lo[0]), (int)bytes_times(q[1], lo[0]),
-                                            (int)bytes_times(q[2], lo[1]), (int)bytes_times(q[3], lo[1])};
-                        const i32x4 b_hi = {(int)bytes_times(q[0], hi[0]), (int)bytes_times(q[1], hi[0]),
-                                            (int)bytes_times(q[2], hi[1]), (int)bytes_times(q[3], hi[1])};
-                        // byte 0 in all four bytes (v_perm; a multiply by 0x01010101 is quarter rate)
-                        const int me = (int)__builtin_amdgcn_perm((uint32_t)mne, (uint32_t)mne, 0u);
-                        const int mo = (int)__builtin_amdgcn_perm((uint32_t)mno, (uint32_t)mno, 0u);
-                        const i32x4 b_mn = {me, me, mo, mo};
-#pragma unroll
-                        for (int u = 0; u < 4; u++) {
-                            const int t = 4 * th + u;
-                            const i32x4 av = *reinterpret_cast<const i32x4 *>(la + la_off(t, 2 * jp, g, c));
-                            alo[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_lo, alo[u], 0, 0, 0);
-                            ahi[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_hi, ahi[u], 0, 0, 0);
-                            amn[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_mn, amn[u], 0, 0, 0);
-                        }
-                    }
-#pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        const int t = 4 * th + u;
-                        const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
-                        const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            // this lane's plane (rows 0..7 high, 8..15 low)
-                            const float v = d * (float)(alo[u][i] + 8 * ahi[u][i]) - dmin * (float)amn[u][i];
-                            y[t][i] += xsv[i] * v;
-                        }
+                    for (int t = 0; t < NT; t++) {
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op(cur_l, t, 2 * jp, lc, lg), be, acc[t], 0, 0, 0);
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op(cur_l, t, 2 * jp + 1, lc, lg), bo, acc[t], 0, 0, 0);
                     }
                 }
+                // min term: K slots 0..7 (lanes g = 0) and 8..15 (g = 1) hold the
+                // mins against the sums' high parts and remainders
+                const half8 bmin = g < 2 ? half8{mins[0], mins[1], mins[2], mins[3], mins[4], mins[5], mins[6], mins[7]}
+                                         : half8{};
+                const uint8_t *lsum = cur_l + kBgLdsA;
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    const half8 as = g < 2 ? *reinterpret_cast<const half8 *>(lsum + (uint32_t)(16 * t + lc) * 32 + lg * 16)
+                                           : half8{};
+                    const f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bmin, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    const float4 xs = *reinterpret_cast<const float4 *>(lxs + 16 * t + 4 * lg);
+                    const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) y[t][i] += xsv[i] * (d * acc[t][i] - dmin * mn[i]);
+                }
             } else {
-                // Q6_K: q = ql | qh << 4 - 32 in [-32, 31] and a signed 8-bit
-                // scale per 16 elements, written in balanced base 7
-                // (s = e0 + 7 e1 + 49 e2, e in [-3, 3]): every q * e (|.| <= 96)
-                // is an exact int8 B operand, so three K = 64 MFMAs per pair of
-                // sub-blocks and 8-row tile replace the int32 scaling. A lane's
-                // eight bytes of sub-block j lie in one 16-element scale group.
-                const float d = h2f((uint16_t)cur.d);
-                uint32_t qw[8][2];  // q + 32 (0..63) of sub-block j, bytes 0..3 and 4..7
+                // Q6_K: q = (ql | qh << 4) - 32, scale byte 2 j + (g >> 1) for
+                // the lane's eight elements of sub-block j
+                d = h2f((uint16_t)cur.d);
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     const int half = j >> 2, qd = j & 3;
                     const uint64_t lo4 = (cur.ql[2 * half + (qd & 1)] >> (4 * (qd >> 1))) & 0x0F0F0F0F0F0F0F0Full;
                     const uint64_t hi2 = ((cur.qh[half] >> (2 * qd)) & 0x0303030303030303ull) << 4;
-                    qw[j][0] = (uint32_t)(lo4 | hi2);
-                    qw[j][1] = (uint32_t)((lo4 | hi2) >> 32);
-                }
-                // the three digits of this lane's scale for every sub-block,
-                // each as (e, -32 e) in both 16-bit halves
-                uint32_t dm[8][3], dc[8][3];
+                    const uint64_t u = lo4 | hi2;  // q + 32 per byte
+                    const uint32_t w0 = (uint32_t)u, w1 = (uint32_t)(u >> 32);
+                    const half2v s2 = splat_h((float)sbyte(cur.sc, 2 * j + (g >> 1)));
+                    const half2v off = splat_h(-1056.f);
+                    auto one = [&](uint32_t pq) __attribute__((always_inline)) {
+                        return (magic_pair(pq, 0x003F003Fu) + off) * s2;  // (1024 + q + 32) - 1056 = q, times sc
+                    };
+                    const half8 bj = pack8(one(__builtin_amdgcn_perm(0u, w0, 0x0c010c00u)), one(__builtin_amdgcn_perm(0u, w0, 0x0c030c02u)),
+                                           one(__builtin_amdgcn_perm(0u, w1, 0x0c010c00u)), one(__builtin_amdgcn_perm(0u, w1, 0x0c030c02u)));
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    uint32_t u = (uint32_t)(sbyte(cur.sc, 2 * j + (g >> 1)) + 171);  // 43..298
-#pragma unroll
-                    for (int k = 0; k < 3; k++) {
-                        const uint32_t nq = k < 2 ? (u * 9363u) >> 16 : 0u;  // u / 7 for u < 13107
-                        const int e = (int)(k < 2 ? u - 7 * nq : u) - 3;
-                        // low 16 bits in both halves
-                        dm[j][k] = __builtin_amdgcn_perm((uint32_t)e, (uint32_t)e, 0x01000100u);
-                        dc[j][k] = __builtin_amdgcn_perm((uint32_t)(-32 * e), (uint32_t)(-32 * e), 0x01000100u);
-                        u = nq;
-                    }
+                    for (int t = 0; t < NT; t++)
+                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op(cur_l, t, j, lc, lg), bj, acc[t], 0, 0, 0);
                 }
 #pragma unroll
-                for (int th = 0; th < TH; th++) {  // TH = 1: rows in tiles 0..3 only
-                    i32x4 a0[4], a1[4], a2[4];
+                for (int t = 0; t < NT; t++) {
+                    const float4 xs = *reinterpret_cast<const float4 *>(lxs + 16 * t + 4 * lg);
+                    const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
 #pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        a0[u] = i32x4{0, 0, 0, 0};
-                        a1[u] = i32x4{0, 0, 0, 0};
-                        a2[u] = i32x4{0, 0, 0, 0};
-                    }
-#pragma unroll
-                    for (int jp = 0; jp < 4; jp++) {
-                        i32x4 bk[3];
-#pragma unroll
-                        for (int w = 0; w < 4; w++) {
-                            const int j = 2 * jp + (w >> 1);
-                            const uint32_t qv = qw[j][w & 1];
-                            // bytes 0, 2 and 1, 3 in 16-bit halves: (q + 32) e - 32 e
-                            const u16x2 ev = __builtin_bit_cast(u16x2, qv & 0x00FF00FFu);
-                            const u16x2 ov = __builtin_bit_cast(u16x2, (qv >> 8) & 0x00FF00FFu);
-#pragma unroll
-                            for (int k = 0; k < 3; k++) {
-                                const u16x2 m = __builtin_bit_cast(u16x2, dm[j][k]);
-                                const u16x2 cc = __builtin_bit_cast(u16x2, dc[j][k]);
-                                const uint32_t pe = __builtin_bit_cast(uint32_t, ev * m + cc);
-                                const uint32_t po = __builtin_bit_cast(uint32_t, ov * m + cc);
-                                bk[k][w] = (int)__builtin_amdgcn_perm(po, pe, 0x06020400u);
-                            }
-                        }
-#pragma unroll
-                        for (int u = 0; u < 4; u++) {
-                            const int t = 4 * th + u;
-                            const i32x4 av = *reinterpret_cast<const i32x4 *>(la + la_off(t, 2 * jp, g, c));
-                            a0[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bk[0], a0[u], 0, 0, 0);
-                            a1[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bk[1], a1[u], 0, 0, 0);
-                            a2[u] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bk[2], a2[u], 0, 0, 0);
-                        }
-                    }
-#pragma unroll
-                    for (int u = 0; u < 4; u++) {
-                        const int t = 4 * th + u;
-                        const float4 xs = *reinterpret_cast<const float4 *>(lxs + t * 8 + rb);
-                        const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const int acc = mad24(49, a2[u][i], mad24(7, a1[u][i], a0[u][i]));
-                            y[t][i] += xsv[i] * (d * (float)acc);
-                        }
-                    }
+                    for (int i = 0; i < 4; i++) y[t][i] += xsv[i] * (d * acc[t][i]);
                 }
             }
         }
-        if (more)
-            stage_store(st, nxt_l, reinterpret_cast<float *>(nxt_l + kBgLdsA));
+        if (more) stage_store(st, nxt_l);
         __syncthreads();  // stage sb + 1 written; stage sb read by every wave
     }
 }
 
-__global__ __launch_bounds__(kBgThreads) void bg_gemm_kernel(const BgArgs A) {
+__global__ __launch_bounds__(kBgThreads) __attribute__((amdgpu_waves_per_eu(4))) void bg_gemm_kernel(const BgArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const FusedGemmArgs &F = A.f;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -561,35 +521,33 @@ __global__ __launch_bounds__(kBgThreads) void bg_gemm_kernel(const BgArgs A) {
     const int n = min(n0 + c, S.n - 1);  // clamped channel for the loads
     const uint8_t *wrow = static_cast<const uint8_t *>(S.w) + (uint64_t)n * S.row_bytes;
 
-    float y[8][4];
+    float y[4][4];
 #pragma unroll
-    for (int t = 0; t < 8; t++)
+    for (int t = 0; t < 4; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) y[t][i] = 0.f;
-    // a block of at most 32 rows multiplies only the first four 8-row tiles
+    // blocks of at most 16 / 32 rows multiply only their first one / two tiles
+    const int nt = (mrows + 15) / 16;
     if (S.dtype == kQ6K) {
-        if (mrows > 32) bg_main<kQ6K, 2>(A, lds, m0, mrows, live, wrow, y);
+        if (nt > 2) bg_main<kQ6K, 4>(A, lds, m0, mrows, live, wrow, y);
+        else if (nt == 2) bg_main<kQ6K, 2>(A, lds, m0, mrows, live, wrow, y);
         else bg_main<kQ6K, 1>(A, lds, m0, mrows, live, wrow, y);
     } else {
-        if (mrows > 32) bg_main<kQ4K, 2>(A, lds, m0, mrows, live, wrow, y);
+        if (nt > 2) bg_main<kQ4K, 4>(A, lds, m0, mrows, live, wrow, y);
+        else if (nt == 2) bg_main<kQ4K, 2>(A, lds, m0, mrows, live, wrow, y);
         else bg_main<kQ4K, 1>(A, lds, m0, mrows, live, wrow, y);
     }
-    // y holds the plane sums: high on lanes g < 2, low on g >= 2 (same rows)
-#pragma unroll
-    for (int t = 0; t < 8; t++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) y[t][i] = fmaf(256.f, y[t][i], __shfl_xor(y[t][i], 32));
 
-    // epilogue: lanes g < 2 hold rows 8 t + 4 g + i of channel n0 + c
+    // epilogue: lane (c, g) holds rows 16 t + 4 g + i of channel n0 + c
     if (A.splits > 1) {  // partial sums of this split; bg_reduce_kernel finishes
-        if (!live || g >= 2 || n0 + c >= S.n) return;
+        if (!live || n0 + c >= S.n) return;
         const int ncol = A.cols[F.nseg];
         float *pp = A.part + (uint64_t)blockIdx.z * F.rows * ncol + A.cols[seg] + n0 + c;
 #pragma unroll
-        for (int t = 0; t < 8; t++)
+        for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int r = 8 * t + 4 * g + i;
+                const int r = 16 * t + 4 * g + i;
                 if (r < mrows) pp[(uint64_t)(m0 + r) * ncol] = y[t][i];
             }
         return;
@@ -597,19 +555,19 @@ __global__ __launch_bounds__(kBgThreads) void bg_gemm_kernel(const BgArgs A) {
     if (A.swiglu) {
         __syncthreads();
         float *up = reinterpret_cast<float *>(lds);  // [4 tiles][64 rows][16]
-        if (wave >= 4 && g < 2) {
+        if (wave >= 4) {
 #pragma unroll
-            for (int t = 0; t < 8; t++)
+            for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) up[((wave - 4) * kBgRows + 8 * t + 4 * g + i) * 16 + c] = y[t][i];
+                for (int i = 0; i < 4; i++) up[((wave - 4) * kBgRows + 16 * t + 4 * g + i) * 16 + c] = y[t][i];
         }
         __syncthreads();
-        if (wave < 4 && g < 2 && live && n0 + c < S.n) {
+        if (wave < 4 && live && n0 + c < S.n) {
 #pragma unroll
-            for (int t = 0; t < 8; t++)
+            for (int t = 0; t < 4; t++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const int r = 8 * t + 4 * g + i;
+                    const int r = 16 * t + 4 * g + i;
                     if (r >= mrows) continue;
                     const float u = up[(wave * kBgRows + r) * 16 + c];
                     S.out[(uint64_t)(m0 + r) * S.n + n0 + c] = __fmul_rn(silu_ref(y[t][i]), u);
@@ -617,12 +575,12 @@ __global__ __launch_bounds__(kBgThreads) void bg_gemm_kernel(const BgArgs A) {
         }
         return;
     }
-    if (!live || g >= 2 || n0 + c >= S.n) return;
+    if (!live || n0 + c >= S.n) return;
 #pragma unroll
-    for (int t = 0; t < 8; t++)
+    for (int t = 0; t < 4; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int r = 8 * t + 4 * g + i;
+            const int r = 16 * t + 4 * g + i;
             if (r >= mrows) continue;
             const uint64_t o = (uint64_t)(m0 + r) * S.n + n0 + c;
             float v = y[t][i];
@@ -665,20 +623,24 @@ __global__ __launch_bounds__(256) void bg_reduce_kernel(const BgArgs A) {
     S.out[o] = v;
 }
 
-// K splits for a launch of `wgs` workgroups (one resident per CU: 8 waves
-// of ~250 VGPRs): the split count with the fewest estimated super-block
-// times, rounds of workgroups x (super-blocks per split + one for staging
-// and the epilogue), plus a small cost per split for the reduction.
+// K splits for a launch of `wgs` workgroups: the split count with the
+// fewest estimated super-block times, rounds of resident workgroups x
+// (super-blocks per split + one for staging and the epilogue), plus a small
+// cost per split for the reduction.
 int bg_splits(int wgs, int nsb) {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-            cus = n;
-        else
-            cus = 256;
+    static int resident = 0;
+    if (!resident) {
+        int dev = 0, n = 0, per = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void *>(bg_gemm_kernel),
+                                                         kBgThreads, kBgLds) != hipSuccess ||
+            per <= 0)
+            per = 1;
+        resident = n * per;
     }
+    const int cus = resident;
     int best = 1;
     double best_t = 1e30;
     for (int sp = 1; sp <= std::min(16, std::max(1, nsb / 2)); sp++) {
@@ -693,7 +655,7 @@ int bg_splits(int wgs, int nsb) {
 }
 
 uint64_t bg_quant_bytes(int rows, int K) {
-    return (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 256) * 4;
+    return (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 256) * 32 + (uint64_t)rows * (K / 256) * 4;
 }
 
 }  // namespace
