@@ -6,8 +6,8 @@
 // RMSNorm or gated head norm of x, store / residual / SwiGLU, output maps).
 // At a few rows the fused streaming kernel reads every weight once per
 // launch; a batch of B requests x (k+1) rows would read them once per 8-row
-// block. Here each weight super-block is read once per 64 rows, and the
-// products run on v_mfma_f32_16x16x32_f16:
+// block. Here each weight super-block is read once per block of 48 rows (80
+// for 49..80 rows), and the products run on v_mfma_f32_16x16x32_f16:
 //
 //  * prologue (one workgroup per row): y = prologue(x) computed as the
 //    reference computes it (forward.go:460-482 rmsNorm, recurrent.go:39-50
@@ -16,9 +16,10 @@
 //    FP32 sum of every 32-element sub-block of those FP16 values stored as an
 //    FP16 high part and its FP16 remainder — a workspace of
 //    rows * (2 K + K / 8 + K / 64) B.
-//  * GEMM (workgroup = 64 rows x 8 tiles of 16 output channels, one tile per
-//    wave): per super-block the workgroup stages the 64 rows' FP16 values and
-//    sub-block sums in LDS, double-buffered; each wave decodes its tile's
+//  * GEMM (workgroup = a block of 16-row tiles x 8 tiles of 16 output
+//    channels, one channel tile per wave): per super-block the block's FP16
+//    values and sub-block sums are copied straight into LDS
+//    (global_load_lds), double-buffered; each wave decodes its tile's
 //    weights straight from HBM into MFMA B operands while the next
 //    super-block's weights are in flight.
 //    - Q4_K: the 6-bit sub-block scale is folded into the operand, B = sc q
@@ -33,7 +34,7 @@
 //    The weights are the reference's FP16 dequantized values up to the FP32
 //    factors d and dmin, and the activations FP16 as in the reference's own
 //    FP16 GEMM (kernels/hip/gemm/wmma_gemm.hip load_a_tile / load_b_tile);
-//    products and sums are exact in the MFMA's FP32 accumulation.
+//    the products are exact and accumulate in FP32.
 //
 // Replaces, for batched verify shapes, the reference's per-matrix GEMV
 // launches over all rows (kernels/hip/gemm/lm_head.hip:61-173 with MaxRows 16,
@@ -61,15 +62,6 @@ constexpr int kQ4K = YUUKA_DTYPE_Q4_K;
 constexpr int kQ6K = YUUKA_DTYPE_Q6_K;
 constexpr int kBgWaves = 8;
 constexpr int kBgThreads = 64 * kBgWaves;
-constexpr int kBgRows = 64;  // rows per workgroup: four 16-row MFMA tiles
-// LDS of the GEMM, per stage: A [64 rows][32 blocks of 8 FP16] with block b
-// of row r at b ^ (r & 15) (a tile's 16 rows read one block each without
-// bank conflicts), sums [64 rows][16 FP16], row scales [64] float; two
-// stages. The SwiGLU epilogue reuses the first.
-constexpr uint32_t kBgLdsA = kBgRows * 512;
-constexpr uint32_t kBgLdsSum = kBgRows * 32;
-constexpr uint32_t kBgStage = kBgLdsA + kBgLdsSum + kBgRows * 4;
-constexpr uint32_t kBgLds = 2 * kBgStage;
 constexpr float kBgRange = 256.0f;  // |y / scale| <= kBgRange
 
 struct BgQuant {
@@ -320,44 +312,55 @@ __device__ __forceinline__ half8 pack8(half2v a, half2v b, half2v c, half2v d) {
     return half8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
-// Super-block sb of the workgroup's rows: loaded into registers by every
-// thread, then written to one of two LDS stages.
-struct Staged {
-    uint4 v[4];  // FP16 values: piece u = threadIdx.x + 512 k is row u >> 5, block u & 31
-    uint4 s;     // sums: threads < 128, row t >> 1, half t & 1
-    float xs;    // row scale: threads < 64
+// LDS of one stage for NT row tiles: A [16 NT rows][32 blocks of 8 FP16]
+// with block b of row r at b ^ (r & 15) (a tile's 16 rows read one block
+// each without bank conflicts), sub-block sums [rows][16 FP16] padded to
+// whole 1 KB copies, row scales [rows] float. Two stages; the SwiGLU
+// epilogue reuses the first.
+template <int NT> struct BgLds {
+    static constexpr int kRows = 16 * NT;
+    static constexpr uint32_t A = 0;
+    static constexpr uint32_t S = A + kRows * 512;
+    static constexpr uint32_t X = S + ((kRows + 31) / 32) * 1024;
+    static constexpr uint32_t stage = X + kRows * 4;
+    static constexpr uint32_t total = 2 * stage;
 };
+static_assert(BgLds<5>::total <= 160 * 1024, "five tiles fit LDS");
 
-__device__ __forceinline__ void stage_load(const BgArgs &A, Staged &st, int m0, int mrows, int sb) {
-    const int K = A.f.K, nsb = K / 256;
-    int oz;  // opaque zero: the thread's addresses are recomputed per call, not held (and spilled) across the loop
-    asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
-    const int tid = (int)threadIdx.x + oz;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int u = tid + k * kBgThreads;
-        const int r = u >> 5, b = u & 31;
-        st.v[k] = r < mrows ? *reinterpret_cast<const uint4 *>(A.q.h + (uint64_t)(m0 + r) * K + sb * 256 + b * 8)
-                            : make_uint4(0u, 0u, 0u, 0u);
-    }
-    {
-        const int r = (tid >> 1) & 63, hf = tid & 1;
-        st.s = tid < 128 && r < mrows
-                   ? *reinterpret_cast<const uint4 *>(A.q.sums + ((uint64_t)(m0 + r) * nsb + sb) * 16 + hf * 8)
-                   : make_uint4(0u, 0u, 0u, 0u);
-    }
-    st.xs = tid < mrows ? A.q.scales[(uint64_t)(m0 + tid) * nsb + sb] : 0.f;
+// 16-byte global -> LDS copy of one lane (lane l writes [m0 + 16 l, +16)),
+// as inline assembly so that the compiler's wait counts do not see it (it
+// would otherwise wait for the weight loads before every LDS read). The
+// main loop waits for the copies itself (vmcnt(0) before its barrier).
+__device__ __forceinline__ void lds_copy16(const void *src, const uint8_t *lds_dst) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_dst);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
 }
 
-__device__ __forceinline__ void stage_store(const Staged &st, uint8_t *stage) {
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int u = threadIdx.x + k * kBgThreads;
-        const int r = u >> 5, b = u & 31;
-        *reinterpret_cast<uint4 *>(stage + (uint32_t)r * 512 + (uint32_t)((b ^ (r & 15)) * 16)) = st.v[k];
+// Issues the copies of super-block sb of the block's rows into a stage
+// (rows past the block's end repeat its last row; their outputs are never
+// stored) and returns this thread's row scale (threads < 16 NT).
+template <int NT>
+__device__ __forceinline__ float stage_issue(const BgArgs &A, uint8_t *stage, int m0, int mrows, int sb) {
+    using LY = BgLds<NT>;
+    const int K = A.f.K, nsb = K / 256;
+    int oz;  // opaque zero: the copy addresses are recomputed per call, not held (and spilled) across the loop
+    asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = (threadIdx.x & 63) + oz;
+    // A: copy i covers rows 2 i, 2 i + 1 (lane l: row 2 i + l / 32, LDS block l % 32)
+#pragma unroll 1
+    for (int i = wave; i < LY::kRows / 2; i += kBgWaves) {
+        const int r = 2 * i + (lane >> 5), pb = lane & 31;
+        const int rr = min(r, mrows - 1);
+        lds_copy16(A.q.h + (uint64_t)(m0 + rr) * K + sb * 256 + (pb ^ (r & 15)) * 8, stage + LY::A + (uint32_t)i * 1024);
     }
-    if (threadIdx.x < 128) *reinterpret_cast<uint4 *>(stage + kBgLdsA + threadIdx.x * 16) = st.s;
-    if (threadIdx.x < kBgRows) reinterpret_cast<float *>(stage + kBgLdsA + kBgLdsSum)[threadIdx.x] = st.xs;
+    // sums: copy i covers rows 32 i .. 32 i + 31 (lane l: row 32 i + l / 2, half l % 2)
+#pragma unroll 1
+    for (int i = wave; i < (LY::kRows + 31) / 32; i += kBgWaves) {
+        const int r = min(32 * i + (lane >> 1), mrows - 1);
+        lds_copy16(A.q.sums + ((uint64_t)(m0 + r) * nsb + sb) * 16 + (lane & 1) * 8, stage + LY::S + (uint32_t)i * 1024);
+    }
+    const int t = (int)threadIdx.x + oz;
+    return t < LY::kRows ? A.q.scales[(uint64_t)(m0 + min(t, mrows - 1)) * nsb + sb] : 0.f;
 }
 
 // A operand of row tile t, sub-block j for lane (row c, group g).
@@ -366,12 +369,16 @@ __device__ __forceinline__ half8 a_op(const uint8_t *stage, int t, int j, int c,
     return *reinterpret_cast<const half8 *>(stage + (uint32_t)r * 512 + (uint32_t)((b ^ c) * 16));
 }
 
-// The main loop of one wave over the super-blocks (weights of dtype DT), NT
-// row tiles of 16. LDS holds two stages; stage sb + 1 is loaded while sb is
-// multiplied.
+// The main loop of one wave over the super-blocks (weights of dtype DT): its
+// tile's B operands are built once per super-block and multiplied with all
+// NT row tiles (rows past the block's end are copies of its last row; a
+// branch per tile would keep the scheduler from issuing the tiles' LDS reads
+// ahead of their MFMAs). LDS holds two stages; stage sb + 1 is copied in
+// while sb is multiplied.
 template <int DT, int NT>
 __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, int mrows, bool live,
-                                        const uint8_t *wrow, float (&y)[4][4]) {
+                                        const uint8_t *wrow, float (&y)[NT][4]) {
+    using LY = BgLds<NT>;
     const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
     // this split's super-blocks [sb_lo, nsb)
     const int nsb_all = A.f.K / 256;
@@ -385,16 +392,17 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
         if constexpr (DT == kQ4K) load_q4(w, wrow, g);
         else load_q6(w, wrow, g);
     }
-    Staged st;
-    stage_load(A, st, m0, mrows, sb_lo);
-    stage_store(st, lds);
+    float xs_next = stage_issue<NT>(A, lds, m0, mrows, sb_lo);
+    __builtin_amdgcn_s_waitcnt(0);
+    if (threadIdx.x < LY::kRows) reinterpret_cast<float *>(lds + LY::X)[threadIdx.x] = xs_next;
     __syncthreads();
+#pragma unroll 1  // one super-block per iteration: unrolled, the live registers double
     for (int sb = sb_lo; sb < nsb; sb++) {
-        const uint8_t *cur_l = lds + (uint32_t)((sb - sb_lo) & 1) * kBgStage;
-        uint8_t *nxt_l = lds + (uint32_t)((sb - sb_lo + 1) & 1) * kBgStage;
-        const float *lxs = reinterpret_cast<const float *>(cur_l + kBgLdsA + kBgLdsSum);
+        const uint8_t *cur_l = lds + (uint32_t)((sb - sb_lo) & 1) * LY::stage;
+        uint8_t *nxt_l = lds + (uint32_t)((sb - sb_lo + 1) & 1) * LY::stage;
+        const float *lxs = reinterpret_cast<const float *>(cur_l + LY::X);
         const bool more = sb + 1 < nsb;
-        if (more) stage_load(A, st, m0, mrows, sb + 1);
+        if (more) xs_next = stage_issue<NT>(A, nxt_l, m0, mrows, sb + 1);
         const W cur = w;  // this super-block; the next one's loads go out now
         if (live && more) {
             if constexpr (DT == kQ4K) load_q4(w, wrow + (uint64_t)(sb + 1 - sb_lo) * blk, g);
@@ -449,7 +457,7 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                 // mins against the sums' high parts and remainders
                 const half8 bmin = g < 2 ? half8{mins[0], mins[1], mins[2], mins[3], mins[4], mins[5], mins[6], mins[7]}
                                          : half8{};
-                const uint8_t *lsum = cur_l + kBgLdsA;
+                const uint8_t *lsum = cur_l + LY::S;
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
                     const half8 as = g < 2 ? *reinterpret_cast<const half8 *>(lsum + (uint32_t)(16 * t + lc) * 32 + lg * 16)
@@ -479,8 +487,9 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                     const half8 bj = pack8(one(__builtin_amdgcn_perm(0u, w0, 0x0c010c00u)), one(__builtin_amdgcn_perm(0u, w0, 0x0c030c02u)),
                                            one(__builtin_amdgcn_perm(0u, w1, 0x0c010c00u)), one(__builtin_amdgcn_perm(0u, w1, 0x0c030c02u)));
 #pragma unroll
-                    for (int t = 0; t < NT; t++)
+                    for (int t = 0; t < NT; t++) {
                         acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op(cur_l, t, j, lc, lg), bj, acc[t], 0, 0, 0);
+                    }
                 }
 #pragma unroll
                 for (int t = 0; t < NT; t++) {
@@ -491,18 +500,24 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                 }
             }
         }
-        if (more) stage_store(st, nxt_l);
-        __syncthreads();  // stage sb + 1 written; stage sb read by every wave
+        if (more) {
+            __builtin_amdgcn_s_waitcnt(0);  // the copies into stage sb + 1 (and this thread's row scale)
+            if (threadIdx.x < LY::kRows) reinterpret_cast<float *>(nxt_l + LY::X)[threadIdx.x] = xs_next;
+        }
+        __syncthreads();  // stage sb + 1 complete; stage sb read by every wave
     }
 }
 
-__global__ __launch_bounds__(kBgThreads) __attribute__((amdgpu_waves_per_eu(4))) void bg_gemm_kernel(const BgArgs A) {
+template <int NT>
+__global__ __launch_bounds__(kBgThreads) __attribute__((amdgpu_waves_per_eu(NT > 4 ? 2 : 4))) void bg_gemm_kernel(
+    const BgArgs A) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    constexpr int kRowsB = 16 * NT;
     const FusedGemmArgs &F = A.f;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = lane & 15, g = lane >> 4;
-    const int m0 = blockIdx.y * kBgRows;
-    const int mrows = min(kBgRows, F.rows - m0);
+    const int m0 = blockIdx.y * kRowsB;
+    const int mrows = min(kRowsB, F.rows - m0);
 
     // this wave's tile: the workgroup's segment (segments start on whole
     // workgroups, so a workgroup has one weight type) and tile 8 w + wave, or
@@ -521,22 +536,13 @@ __global__ __launch_bounds__(kBgThreads) __attribute__((amdgpu_waves_per_eu(4)))
     const int n = min(n0 + c, S.n - 1);  // clamped channel for the loads
     const uint8_t *wrow = static_cast<const uint8_t *>(S.w) + (uint64_t)n * S.row_bytes;
 
-    float y[4][4];
+    float y[NT][4];
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) y[t][i] = 0.f;
-    // blocks of at most 16 / 32 rows multiply only their first one / two tiles
-    const int nt = (mrows + 15) / 16;
-    if (S.dtype == kQ6K) {
-        if (nt > 2) bg_main<kQ6K, 4>(A, lds, m0, mrows, live, wrow, y);
-        else if (nt == 2) bg_main<kQ6K, 2>(A, lds, m0, mrows, live, wrow, y);
-        else bg_main<kQ6K, 1>(A, lds, m0, mrows, live, wrow, y);
-    } else {
-        if (nt > 2) bg_main<kQ4K, 4>(A, lds, m0, mrows, live, wrow, y);
-        else if (nt == 2) bg_main<kQ4K, 2>(A, lds, m0, mrows, live, wrow, y);
-        else bg_main<kQ4K, 1>(A, lds, m0, mrows, live, wrow, y);
-    }
+    if (S.dtype == kQ6K) bg_main<kQ6K, NT>(A, lds, m0, mrows, live, wrow, y);
+    else bg_main<kQ4K, NT>(A, lds, m0, mrows, live, wrow, y);
 
     // epilogue: lane (c, g) holds rows 16 t + 4 g + i of channel n0 + c
     if (A.splits > 1) {  // partial sums of this split; bg_reduce_kernel finishes
@@ -544,7 +550,7 @@ __global__ __launch_bounds__(kBgThreads) __attribute__((amdgpu_waves_per_eu(4)))
         const int ncol = A.cols[F.nseg];
         float *pp = A.part + (uint64_t)blockIdx.z * F.rows * ncol + A.cols[seg] + n0 + c;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = 0; t < NT; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int r = 16 * t + 4 * g + i;
@@ -554,22 +560,22 @@ __global__ __launch_bounds__(kBgThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
     if (A.swiglu) {
         __syncthreads();
-        float *up = reinterpret_cast<float *>(lds);  // [4 tiles][64 rows][16]
+        float *up = reinterpret_cast<float *>(lds);  // [4 tiles][rows][16]
         if (wave >= 4) {
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+            for (int t = 0; t < NT; t++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) up[((wave - 4) * kBgRows + 16 * t + 4 * g + i) * 16 + c] = y[t][i];
+                for (int i = 0; i < 4; i++) up[((wave - 4) * kRowsB + 16 * t + 4 * g + i) * 16 + c] = y[t][i];
         }
         __syncthreads();
         if (wave < 4 && live && n0 + c < S.n) {
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+            for (int t = 0; t < NT; t++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int r = 16 * t + 4 * g + i;
                     if (r >= mrows) continue;
-                    const float u = up[(wave * kBgRows + r) * 16 + c];
+                    const float u = up[(wave * kRowsB + r) * 16 + c];
                     S.out[(uint64_t)(m0 + r) * S.n + n0 + c] = __fmul_rn(silu_ref(y[t][i]), u);
                 }
         }
@@ -577,7 +583,7 @@ __global__ __launch_bounds__(kBgThreads) __attribute__((amdgpu_waves_per_eu(4)))
     }
     if (!live || n0 + c >= S.n) return;
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int r = 16 * t + 4 * g + i;
@@ -623,24 +629,39 @@ __global__ __launch_bounds__(256) void bg_reduce_kernel(const BgArgs A) {
     S.out[o] = v;
 }
 
-// K splits for a launch of `wgs` workgroups: the split count with the
-// fewest estimated super-block times, rounds of resident workgroups x
-// (super-blocks per split + one for staging and the epilogue), plus a small
-// cost per split for the reduction.
-int bg_splits(int wgs, int nsb) {
-    static int resident = 0;
-    if (!resident) {
+// Row tiles per workgroup for a launch of `rows` rows (measured at config
+// shapes, prologue + GEMM per launch: 144 rows gate/up 50.1 / 54.7 / 64.2 /
+// 60.7 us at 3 / 4 / 5 / 9 tiles; 68 rows 44.1 / 47.2 / 41.4 / 49.4 us;
+// 40 rows 30.0 / 31.4 / 37.2 / 45.3 us). Five tiles (80 rows, one
+// workgroup per CU) serve 49..80 rows in one block; otherwise blocks of 48
+// rows (three tiles, two workgroups per CU).
+int bg_tiles(int rows) { return rows > 48 && rows <= 80 ? 5 : 3; }
+
+template <int NT> const void *bg_kernel_ptr() { return reinterpret_cast<const void *>(bg_gemm_kernel<NT>); }
+
+// Resident workgroups of the NT-tile kernel on the device (cached).
+int bg_resident(int nt) {
+    static int res[10] = {0};  // by tile count
+    if (!res[nt]) {
         int dev = 0, n = 0, per = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
             n = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void *>(bg_gemm_kernel),
-                                                         kBgThreads, kBgLds) != hipSuccess ||
-            per <= 0)
-            per = 1;
-        resident = n * per;
+        const void *k = nt == 5 ? bg_kernel_ptr<5>() : bg_kernel_ptr<3>();
+        const uint32_t lds = nt == 5 ? BgLds<5>::total : BgLds<3>::total;
+        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, kBgThreads, lds) != hipSuccess || per <= 0) per = 1;
+        res[nt] = n * per;
     }
-    const int cus = resident;
+    return res[nt];
+}
+
+// K splits for a launch of `wgs` workgroups: the split count with the
+// fewest estimated super-block times, rounds of resident workgroups x
+// (super-blocks per split + one for staging and the epilogue), plus a small
+// cost per split for the reduction.
+int bg_splits(int wgs, int nsb, int nt) {
+    const int cus = bg_resident(nt);
     int best = 1;
     double best_t = 1e30;
     for (int sp = 1; sp <= std::min(16, std::max(1, nsb / 2)); sp++) {
@@ -669,8 +690,9 @@ static void bg_grid(const int *n, int nseg, bool swiglu, int rows, int K, unsign
     else
         for (int i = 0; i < nseg; i++) x += (unsigned)((n[i] + 16 * kBgWaves - 1) / (16 * kBgWaves));
     *gx = x;
-    *gy = (unsigned)((rows + kBgRows - 1) / kBgRows);
-    *splits = bg_splits((int)(x * *gy), K / 256);
+    const int nt = bg_tiles(rows);
+    *gy = (unsigned)((rows + 16 * nt - 1) / (16 * nt));
+    *splits = bg_splits((int)(x * *gy), K / 256, nt);
 }
 
 uint64_t fused_gemm_rows_ws(int rows, int K, const int *n, int nseg, bool swiglu) {
@@ -697,8 +719,6 @@ hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t 
     if (!attr) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(bg_prologue_kernel),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(bg_gemm_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kBgLds);
         attr = true;
     }
     bg_prologue_kernel<<<(unsigned)a.rows, kPrThreads, plds, s>>>(a, A.q);
@@ -710,7 +730,10 @@ hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t 
     for (int i = 0; i < a.nseg; i++) A.cols[i + 1] = A.cols[i] + a.seg[i].n;
     for (int i = a.nseg + 1; i <= kFusedMaxSeg; i++) A.cols[i] = A.cols[a.nseg];
     A.part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + ((bg_quant_bytes(a.rows, a.K) + 255) & ~255ull));
-    bg_gemm_kernel<<<dim3(gx, gy, (unsigned)A.splits), kBgThreads, kBgLds, s>>>(A);
+    const dim3 grid(gx, gy, (unsigned)A.splits);
+    // (bg_grid's bg_resident call has set the kernel's LDS attribute)
+    if (bg_tiles(a.rows) == 5) bg_gemm_kernel<5><<<grid, kBgThreads, BgLds<5>::total, s>>>(A);
+    else bg_gemm_kernel<3><<<grid, kBgThreads, BgLds<3>::total, s>>>(A);
     if (A.splits > 1) {
         const uint64_t nout = (uint64_t)a.rows * (A.swiglu ? a.seg[0].n : A.cols[a.nseg]);
         bg_reduce_kernel<<<(unsigned)((nout + 255) / 256), 256, 0, s>>>(A);
