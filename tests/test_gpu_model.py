@@ -197,3 +197,36 @@ def test_eager_plan_execution_equals_graph_replay(dev, tiny, monkeypatch):
         eng.close()
     assert np.array_equal(out[0][0], out[1][0])
     assert np.array_equal(out[0][1].view(np.uint32), out[1][1].view(np.uint32))
+
+
+
+@pytest.mark.parametrize("which", ["dense", "moe"])
+def test_engine_from_gguf_equals_engine_from_weights(dev, tiny, tmp_path, which):
+    """A model written to GGUF and loaded back (yuuka_amd.gguf: the reader,
+    LoadConfig and Load of model/qwen35) gives the engine the same bytes:
+    prefill, verify result and verify logits bit-identical to the engine
+    built from the in-memory weights."""
+    from yuuka_amd import gguf as G
+    if which == "dense":
+        cfg, w = tiny
+    else:
+        cfg = Mdl.TINY_MOE
+        w = Mdl.make_weights(cfg, seed=11)
+    path = str(tmp_path / f"{which}.gguf")
+    G.write_q35(path, cfg, w)
+    session = dict(capacity=cfg.capacity, block_size=cfg.block_size, kv_dtype=cfg.kv_dtype,
+                   max_rows=cfg.max_rows, batch=cfg.batch, kv_blocks=cfg.kv_blocks)
+    out = []
+    with G.Reader(path) as r:
+        cfg2 = G.load_config(r, **session)
+        assert cfg2.n_experts == cfg.n_experts and cfg2.vocab == cfg.vocab
+        w2 = G.load_weights(r, cfg2)
+        for c, ws in ((cfg, w), (cfg2, w2)):
+            eng = Mdl.Engine(dev, c, ws)
+            first = eng.prefill(np.arange(5, 30, dtype=np.int32) % c.vocab)
+            res = eng.verify(np.array([9, 10, 11, 12, 13], np.int32))
+            out.append((first, res.copy(), eng.logits(5)))
+            eng.close()
+        del w2
+    for a, b in zip(out[0], out[1]):
+        assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
