@@ -692,13 +692,13 @@ __device__ __forceinline__ void load_act(const uint8_t *lds, const ActLayout &L,
                                          bool want_sums) {
 #pragma unroll
     for (int a = 0; a < NA; a++) {
-        const int rho = 16 * a + r;
+        // rows past 2M read the last plane row: MFMA output row i depends on
+        // A row i only, and the outputs of those rows are never read (integer
+        // products, so no NaN either); a branch per lane would cost moves
+        const int rho = min(16 * a + r, L.rho - 1);
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            int64_t v = 0;
-            if (rho < L.rho) v = *reinterpret_cast<const int64_t *>(lds + L.planes + ((uint32_t)((sbl * 8 + j) * 4 + g) * L.rho + rho) * 8);
-            xa[a][j] = v;
-        }
+        for (int j = 0; j < 8; j++)
+            xa[a][j] = *reinterpret_cast<const int64_t *>(lds + L.planes + ((uint32_t)((sbl * 8 + j) * 4 + g) * L.rho + rho) * 8);
         const float4 xv = *reinterpret_cast<const float4 *>(lds + L.xs + ((uint32_t)sbl * L.rhop + 16 * a + 4 * g) * 4);
         xsr[a][0] = xv.x;
         xsr[a][1] = xv.y;
