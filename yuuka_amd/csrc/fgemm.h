@@ -60,9 +60,9 @@ uint32_t fused_gemm_lds_bytes(int rows, int K, int chunk_sb, int tt, bool norm, 
 // kernel. 0 when K has no super-block.
 int fused_gemm_stream_rows(int K, bool norm, bool gated);
 // Verify GEMM over many rows (k_bgemm.hip): same arguments and results for
-// rows 9..512 (K <= 16384), reading every weight once per 64 rows; `ws`
-// holds fused_gemm_rows_ws(rows, K, total output channels) bytes (the
-// quantized activations and split-K partial sums).
+// rows 9..512 (K <= 16384), reading every weight once per block of 48 or 80
+// rows; `ws` holds fused_gemm_rows_ws(rows, K, total output channels) bytes
+// (the quantized activations and split-K partial sums).
 uint64_t fused_gemm_rows_ws(int rows, int K, const int *n, int nseg, bool swiglu);
 hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t s);
 // tt: 16-row tiles per workgroup (1, 2 or 4; even for kEpiSwiglu).

@@ -301,7 +301,9 @@ __device__ __forceinline__ float out_map(const FusedSeg &S, int n, float v) {
 // FP16 pairs from byte pairs: (x & mask) | 0x6400 in each 16-bit half is
 // 1024 + x as FP16 (x < 1024).
 __device__ __forceinline__ half2v magic_pair(uint32_t w, uint32_t mask) {
-    return __builtin_bit_cast(half2v, (w & mask) | 0x64006400u);
+    uint32_t r;  // one v_and_or_b32 (written out: the compiler splits it when the and is shared)
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(mask), "v"(0x64006400u));
+    return __builtin_bit_cast(half2v, r);
 }
 __device__ __forceinline__ half2v splat_h(float v) {
     const _Float16 h = (_Float16)v;
@@ -433,20 +435,22 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, i
                     mins[2 * jp] = (_Float16)mne;
                     mins[2 * jp + 1] = (_Float16)mno;
                     // bytes b0..b7 of the lane: low nibbles are sub-block 2 jp,
-                    // high nibbles 2 jp + 1; (1024 + q) sc - 1024 sc = q sc exactly
+                    // high nibbles 2 jp + 1. Low: (1024 + q) sc - 1024 sc; high,
+                    // masked in place: (1024 + 16 q) (sc / 16) - 64 sc. Both are
+                    // q sc exactly (one rounding of an exact value below 2048).
                     const uint32_t w0 = (uint32_t)cur.q[jp], w1 = (uint32_t)(cur.q[jp] >> 32);
                     const uint32_t p01 = __builtin_amdgcn_perm(0u, w0, 0x0c010c00u), p23 = __builtin_amdgcn_perm(0u, w0, 0x0c030c02u);
                     const uint32_t p45 = __builtin_amdgcn_perm(0u, w1, 0x0c010c00u), p67 = __builtin_amdgcn_perm(0u, w1, 0x0c030c02u);
-                    const half2v se = splat_h((float)sce), so = splat_h((float)sco);
-                    const half2v ce = splat_h(-1024.f * (float)sce), co = splat_h(-1024.f * (float)sco);
+                    const half2v se = splat_h((float)sce), so = splat_h(0.0625f * (float)sco);
+                    const half2v ce = splat_h(-1024.f * (float)sce), co = splat_h(-64.f * (float)sco);
                     const half8 be = pack8(__builtin_elementwise_fma(magic_pair(p01, 0x000F000Fu), se, ce),
                                            __builtin_elementwise_fma(magic_pair(p23, 0x000F000Fu), se, ce),
                                            __builtin_elementwise_fma(magic_pair(p45, 0x000F000Fu), se, ce),
                                            __builtin_elementwise_fma(magic_pair(p67, 0x000F000Fu), se, ce));
-                    const half8 bo = pack8(__builtin_elementwise_fma(magic_pair(p01 >> 4, 0x000F000Fu), so, co),
-                                           __builtin_elementwise_fma(magic_pair(p23 >> 4, 0x000F000Fu), so, co),
-                                           __builtin_elementwise_fma(magic_pair(p45 >> 4, 0x000F000Fu), so, co),
-                                           __builtin_elementwise_fma(magic_pair(p67 >> 4, 0x000F000Fu), so, co));
+                    const half8 bo = pack8(__builtin_elementwise_fma(magic_pair(p01, 0x00F000F0u), so, co),
+                                           __builtin_elementwise_fma(magic_pair(p23, 0x00F000F0u), so, co),
+                                           __builtin_elementwise_fma(magic_pair(p45, 0x00F000F0u), so, co),
+                                           __builtin_elementwise_fma(magic_pair(p67, 0x00F000F0u), so, co));
 #pragma unroll
                     for (int t = 0; t < NT; t++) {
                         acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op(cur_l, t, 2 * jp, lc, lg), be, acc[t], 0, 0, 0);
@@ -656,17 +660,30 @@ int bg_resident(int nt) {
     return res[nt];
 }
 
-// K splits for a launch of `wgs` workgroups: the split count with the
-// fewest estimated super-block times, rounds of resident workgroups x
-// (super-blocks per split + one for staging and the epilogue), plus a small
-// cost per split for the reduction.
+// K splits for a launch of `wgs` workgroups over `nsb` super-blocks: the
+// split count with the least estimated time, in super-block steps,
+//   ceil(wgs * splits / CUs) * (ceil(nsb / splits) + 1) + 0.1 splits,
+// i.e. the workgroups the busiest CU runs (one at a time: a CU's issue
+// saturates with one workgroup) times each one's steps, the + 1 being its
+// staging and epilogue and the last term the reduction. Fitted to a sweep
+// of 1..12 splits over the config shapes at 40, 68 and 144 rows: the chosen
+// splits cost 0.5 % more than the best of each shape (2.6 % for a count of
+// resident-workgroup rounds).
 int bg_splits(int wgs, int nsb, int nt) {
-    const int cus = bg_resident(nt);
+    (void)bg_resident(nt);  // sets the kernel's LDS attribute
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cus = n;
+    }
     int best = 1;
     double best_t = 1e30;
     for (int sp = 1; sp <= std::min(16, std::max(1, nsb / 2)); sp++) {
-        const double rounds = (double)((wgs * sp + cus - 1) / cus);
-        const double t = rounds * ((nsb + sp - 1) / sp + 1) + (sp > 1 ? 0.25 * sp : 0.0);
+        const double k = (double)((wgs * sp + cus - 1) / cus);
+        const double t = k * (double)((nsb + sp - 1) / sp + 1) + (sp > 1 ? 0.1 * sp : 0.0);
         if (t < best_t - 1e-9) {
             best_t = t;
             best = sp;
