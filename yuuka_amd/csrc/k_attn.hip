@@ -45,6 +45,22 @@ __device__ uint64_t *yk_at_dbg;
 
 __device__ __forceinline__ int cur_pos_a(const ModelDyn &dyn) { return dyn.pos_dev ? *dyn.pos_dev : dyn.pos; }
 
+// exp(x) for finite x <= 0 (a score minus its row's running maximum), in
+// float32 as the reference's GPU attention kernels compute it
+// (kernels/hip/attention: expf of score - max). 2^(x log2 e) on the hardware
+// exp2 (v_exp_f32), with the rounding error of the product x * L1 (an FMA
+// residual) and the low part L2 of log2 e carried as a factor 2^r ~ 1 + r ln 2
+// (|r| < 2^-17, so r^2 is below float precision): relative error ~1e-7
+// against the float64 exp, instead of ~|x| 2^-24 for exp2(x * log2 e).
+__device__ __forceinline__ float exp_nonpos(float x) {
+    constexpr float L1 = 1.44269502162933349609375f;  // log2(e) rounded to float
+    constexpr float L2 = 1.92596298909e-8f;            // log2(e) - L1
+    x = fmaxf(x, -128.0f);  // exp(-128) is 0 in float; keeps x * L1 and its residual finite
+    const float p = x * L1;
+    const float r = fmaf(x, L1, -p) + x * L2;
+    return __builtin_amdgcn_exp2f(p) * fmaf(r, 0.693147180559945309f, 1.0f);
+}
+
 __device__ __forceinline__ double wave_sum_d(double v) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
     return v;
@@ -296,7 +312,7 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
     for (int j = wave; j < nq; j += 4) {
         const float sc = lane < CK ? S[j * CK + lane] : -INFINITY;
         const float m = wave_max_f(sc);
-        const float e = (sc == -INFINITY) ? 0.0f : (float)exp((double)(sc - m));
+        const float e = (sc == -INFINITY) ? 0.0f : exp_nonpos(sc - m);
         const float l = wave_sum_f(e);
         if (lane < CK) S[j * CK + lane] = e;
         if (lane == 0) {
@@ -704,7 +720,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
             m = fmaxf(m, dpp_f<0x128>(m));
             float e[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) e[i] = (sc[i] == -INFINITY) ? 0.0f : (float)exp((double)(sc[i] - m));
+            for (int i = 0; i < 4; i++) e[i] = (sc[i] == -INFINITY) ? 0.0f : exp_nonpos(sc[i] - m);
             float l = (e[0] + e[1]) + (e[2] + e[3]);
             l += dpp_f<0xb1>(l);
             l += dpp_f<0x4e>(l);
@@ -1049,8 +1065,8 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                     float alpha = 1.0f;
                     if (m_new != -INFINITY) {
 #pragma unroll
-                        for (int i = 0; i < 4; i++) e[i] = (sc[i] == -INFINITY) ? 0.0f : (float)exp((double)(sc[i] - m_new));
-                        alpha = m_old == -INFINITY ? 0.0f : (float)exp((double)(m_old - m_new));
+                        for (int i = 0; i < 4; i++) e[i] = (sc[i] == -INFINITY) ? 0.0f : exp_nonpos(sc[i] - m_new);
+                        alpha = m_old == -INFINITY ? 0.0f : exp_nonpos(m_old - m_new);
                     }
                     float lc = (e[0] + e[1]) + (e[2] + e[3]);
                     lc += dpp_f<0xb1>(lc);
@@ -1216,7 +1232,7 @@ __global__ __launch_bounds__(256) void attn_merge_v_kernel(const float *__restri
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     for (int c = threadIdx.x; c < nchunk; c += 256) {
         const float mc = rec_of(c)[D];
-        wsh[c] = mc == -INFINITY ? 0.0f : (float)exp((double)(mc - mx));
+        wsh[c] = mc == -INFINITY ? 0.0f : exp_nonpos(mc - mx);
     }
     __syncthreads();
     float lsum = 0.0f;
