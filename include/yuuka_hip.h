@@ -404,8 +404,9 @@ YUUKA_API yuuka_status yuuka_verify_accept_noalloc(yuuka_stream * stream,
  *               results request-major; the same u1 on RECURRENT_CHUNK
  *               (with DEFER and RAW_OUT) scans every request in one launch.
  *   ADVANCE:    buf0 dynamic buffer {token, position}, buf1 int32 result,
- *               optional buf2 uint64 step counter; n0 = rows. position +=
- *               result[0] + 1; step += 1.
+ *               optional buf2 uint64 step counter; n0 = rows, u0 = requests
+ *               (0 means 1). Request j: position (buf0 + 8 j) += min(result
+ *               (buf1 + 16 j)[0] + 1, rows); step += 1 once.
  *   GEMM_FUSED: buf0 FP32 x [rows][n_in], optional buf1 FP32 RMSNorm weight
  *               [n_in] (y = RMSNorm(x) * w, eps f0; else y = x); segments
  *               i = 0..3 (the leading non-null weights): buf2+i packed W_i

@@ -384,12 +384,10 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
                    0, rq * 16});
         }
     }
-    for (int j = 0; j < nreq; j++) {
-        // the step counter (Philox) advances once per verify step; prefill
-        // chunks leave it alone
-        b.add(YUUKA_EXT_OP_ADVANCE, {q->dyn, q->result, mode == 0 && j == 0 ? q->step : nullptr}, {R1}, {}, {}, 0,
-              {dyn_off(j), (uint64_t)(first + j) * 16, 0});
-    }
+    // every request's position in one launch; the step counter (Philox)
+    // advances once per verify step, prefill chunks leave it alone
+    b.add(YUUKA_EXT_OP_ADVANCE, {q->dyn, q->result, mode == 0 ? q->step : nullptr}, {R1}, {(uint32_t)nreq}, {}, 0,
+          {dyn_off(0), (uint64_t)first * 16, 0});
     if (b.st != YUUKA_OK) {
         yuuka_plan_destroy(plan);
         return b.st;

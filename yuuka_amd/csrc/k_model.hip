@@ -450,11 +450,10 @@ __global__ __launch_bounds__(256) void gdn_conv_commit_kernel(float *__restrict_
 }
 
 __global__ void advance_kernel(ModelDyn dyn, const int32_t *__restrict__ accept_result, int rows,
-                               uint64_t *__restrict__ step) {
-    if (threadIdx.x == 0) {
-        if (dyn.pos_dev) *dyn.pos_dev += min(accept_result[0] + 1, rows);
-        if (step) *step += 1;
-    }
+                               uint64_t *__restrict__ step, int nreq) {
+    for (int j = threadIdx.x; j < nreq; j += blockDim.x)
+        if (dyn.pos_dev) dyn.pos_dev[2 * j] += min(accept_result[4 * j] + 1, rows);
+    if (threadIdx.x == 0 && step) *step += 1;
 }
 
 }  // namespace
@@ -539,9 +538,9 @@ hipError_t launch_gdn_conv_commit(float *conv_state, const float *qkv, const Gdn
     return hipGetLastError();
 }
 
-hipError_t launch_advance(const ModelDyn &dyn, const int32_t *accept_result, int rows, uint64_t *step,
+hipError_t launch_advance(const ModelDyn &dyn, const int32_t *accept_result, int rows, uint64_t *step, int nreq,
                           hipStream_t s) {
-    advance_kernel<<<1, 64, 0, s>>>(dyn, accept_result, rows, step);
+    advance_kernel<<<1, 256, 0, s>>>(dyn, accept_result, rows, step, nreq);
     return hipGetLastError();
 }
 

@@ -110,7 +110,9 @@ hipError_t launch_gdn_norm_gate(const float *raw, const float *z, const float *n
                                 hipStream_t s);
 hipError_t launch_gdn_conv_commit(float *conv_state, const float *qkv, const GdnArgs &g, const int32_t *accept_result,
                                   hipStream_t s);
-hipError_t launch_advance(const ModelDyn &dyn, const int32_t *accept_result, int rows, uint64_t *step,
+// nreq requests: request j's position is dyn.pos_dev[2 j], its result
+// accept_result[4 j .. 4 j + 3]; the step counter advances once.
+hipError_t launch_advance(const ModelDyn &dyn, const int32_t *accept_result, int rows, uint64_t *step, int nreq,
                           hipStream_t s);
 
 // Mixture of experts (k_moe.hip). Assignment layout of the reference's MoE

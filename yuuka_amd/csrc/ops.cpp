@@ -514,11 +514,14 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE combine buffers too small");
         return YUUKA_OK;
     }
-    case YUUKA_EXT_OP_ADVANCE:
-        if (!buf_ok(op.buf[0], op.off[0], 8) || op.off[0] % 4 || !buf_ok(op.buf[1], op.off[1], 8) || op.n[0] == 0 ||
+    case YUUKA_EXT_OP_ADVANCE: {
+        const uint64_t nq = op.u[0] ? op.u[0] : 1;
+        if (nq > 1024 || !buf_ok(op.buf[0], op.off[0], 8 * nq) || op.off[0] % 4 ||
+            !buf_ok(op.buf[1], op.off[1], 16 * (nq - 1) + 8) || op.n[0] == 0 ||
             (op.buf[2] && !buf_ok(op.buf[2], op.off[2], 8)))
-            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid ADVANCE buffers");
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid ADVANCE buffers or request count");
         return YUUKA_OK;
+    }
     default:
         return fail(YUUKA_ERR_UNSUPPORTED, "plan op code %u is not served by this library", op.code);
     }
@@ -736,7 +739,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
         break;
     case YUUKA_EXT_OP_ADVANCE: {
         ModelDyn d{at<int32_t>(op, 0) + 1, 0};
-        err = launch_advance(d, at<const int32_t>(op, 1), (int)op.n[0], at<uint64_t>(op, 2), s);
+        err = launch_advance(d, at<const int32_t>(op, 1), (int)op.n[0], at<uint64_t>(op, 2), op.u[0] ? (int)op.u[0] : 1, s);
         break;
     }
     default:
