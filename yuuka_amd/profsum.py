@@ -1,12 +1,13 @@
 """Summarise a rocprofv3 CSV output directory (``--kernel-trace`` and/or
 ``--pmc`` with ``--output-format csv``) as a Markdown table per kernel.
 
-    python3 -m yuuka_amd.profsum DIR [--steps N] [--by-grid] [--counters]
+    python3 -m yuuka_amd.profsum DIR [--steps N] [--by-grid] [--templates] [--counters]
 
 ``--steps N`` keeps the dispatches of the last N verify steps: those after
 the (N+1)-th-from-last ``accept_finalize_kernel`` up to the last one (every
 verify step ends with exactly one). Kernel names are shown without namespace
-or template arguments; ``--by-grid`` splits a kernel's rows by grid size.
+or template arguments; ``--by-grid`` splits a kernel's rows by grid size and
+``--templates`` by template arguments.
 With ``--counters`` the per-dispatch average of every collected counter is
 appended. Reads the CSV files only; writes to stdout."""
 from __future__ import annotations
@@ -19,11 +20,14 @@ import os
 import re
 
 
-def base_name(name: str) -> str:
-    """`void yk::(anonymous namespace)::foo<...>(...)` -> `foo`."""
+def base_name(name: str, templates: bool = False) -> str:
+    """`void yk::(anonymous namespace)::foo<1, 2>(...)` -> `foo` (or `foo<1, 2>`)."""
     n = name.replace("(anonymous namespace)", "anon")
-    m = re.search(r"(\w+)\s*[<(]", n)
-    return m.group(1) if m else n.strip()
+    m = re.search(r"(\w+)\s*(<[^()]*>)?\s*\(", n) or re.search(r"(\w+)\s*[<(]", n)
+    if not m:
+        return n.strip()
+    args = m.group(2) if m.re.groups >= 2 else None
+    return m.group(1) + (args if templates and args else "")
 
 
 def load(directory: str) -> dict:
@@ -44,7 +48,8 @@ def load(directory: str) -> dict:
     return disp
 
 
-def summarise(disp: dict, steps: int = 0, by_grid: bool = False, counters: bool = False) -> str:
+def summarise(disp: dict, steps: int = 0, by_grid: bool = False, counters: bool = False,
+              templates: bool = False) -> str:
     ids = sorted(disp)
     if steps:
         acc = [i for i in ids if base_name(disp[i]["name"]) == "accept_finalize_kernel"]
@@ -55,7 +60,7 @@ def summarise(disp: dict, steps: int = 0, by_grid: bool = False, counters: bool 
     agg: dict[str, dict] = collections.OrderedDict()
     for i in ids:
         e = disp[i]
-        k = base_name(e["name"]) + (f" grid={e['grid']}" if by_grid else "")
+        k = base_name(e["name"], templates) + (f" grid={e['grid']}" if by_grid else "")
         g = agg.setdefault(k, {"n": 0, "dur": 0.0, "c": collections.Counter()})
         g["n"] += 1
         g["dur"] += (e["end"] - e["start"]) / 1e3
@@ -81,9 +86,10 @@ def main(argv=None) -> None:
     ap.add_argument("dir")
     ap.add_argument("--steps", type=int, default=0)
     ap.add_argument("--by-grid", action="store_true")
+    ap.add_argument("--templates", action="store_true")
     ap.add_argument("--counters", action="store_true")
     a = ap.parse_args(argv)
-    print(summarise(load(a.dir), a.steps, a.by_grid, a.counters))
+    print(summarise(load(a.dir), a.steps, a.by_grid, a.counters, a.templates))
 
 
 if __name__ == "__main__":
