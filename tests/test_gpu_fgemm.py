@@ -257,3 +257,48 @@ def test_fused_gemm_many_rows_epilogues(dev, stream):
     plan.destroy()
     prod = _want(O.Q4_K, wg, n, k, _gated_head_norm(x, z, w, 1e-6))
     _check(got, O.silu_mul(prod, np.ones_like(prod)), budget=2 * MANY_BUDGET)
+
+
+@pytest.mark.parametrize("k_a", [9216, 2048])
+def test_many_rows_pair_reduce_and_prologue_in_one_launch(dev, stream, k_a):
+    """A split-K residual GEMM followed by a GEMM that normalises its output
+    (the FFN down -> next in-projection and out-projection -> FFN gate/up
+    pairs of a batched step) runs with the split reduction and the second
+    prologue in one kernel. Executed that way (plan.execute) and op by op
+    (execute_profiled, which pairs nothing), every output is bit-identical,
+    and both match the oracle. With k_a = 2048 the second GEMM's quantized
+    rows do not fit before the first one's partial sums, so its workspace
+    moves behind them (a leading K = 9216 launch makes the plan's workspace
+    large enough, as the down projection does in the engine's plans)."""
+    rng = np.random.default_rng(77 + k_a)
+    rows, h, f = 144, 2560, 1536
+    x_a = rng.normal(0, 1, (rows, k_a)).astype(np.float32)
+    res0 = rng.normal(0, 2, (rows, h)).astype(np.float32)
+    g = rng.normal(1, 0.1, h).astype(np.float32)
+    w_a = synth.quant_matrix(rng, O.Q4_K, h, k_a)
+    w_g = synth.quant_matrix(rng, O.Q4_K, f, h)
+    w_u = synth.quant_matrix(rng, O.Q6_K, f, h)
+    x_big = rng.normal(0, 1, (rows, 9216)).astype(np.float32)
+    w_big = synth.quant_matrix(rng, O.Q4_K, 512, 9216)
+    plan = hip.Plan(dev)
+    xa, xb, gb = dev.upload(x_a), dev.upload(x_big), dev.upload(g)
+    hbuf = dev.alloc(rows * h * 4)
+    ob, og, ou = dev.alloc(rows * 512 * 4), dev.alloc(rows * f * 4), dev.alloc(rows * f * 4)
+    wa, wg, wu, wbig = dev.upload(w_a), dev.upload(w_g), dev.upload(w_u), dev.upload(w_big)
+    hip.gemm_fused_op(plan, xb, 9216, rows, [(wbig, O.Q4_K, 512, ob, None)])  # sizes the workspace
+    hip.gemm_fused_op(plan, xa, k_a, rows, [(wa, O.Q4_K, h, hbuf, hbuf)], hip.EPI_RESIDUAL)
+    hip.gemm_fused_op(plan, hbuf, h, rows, [(wg, O.Q4_K, f, og, None), (wu, O.Q6_K, f, ou, None)], norm=gb)
+    outs = []
+    for run in (plan.execute, plan.execute_profiled):
+        hbuf.write(res0)
+        run(stream)
+        stream.sync()
+        outs.append([b.read(np.float32).copy() for b in (hbuf, og, ou)])
+    plan.destroy()
+    for a, b in zip(*outs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    hh = outs[0][0].reshape(rows, h)
+    _check(hh - res0, _want(O.Q4_K, w_a, h, k_a, x_a), budget=MANY_BUDGET)
+    y = O.rmsnorm_rows(hh, g, 1e-6)
+    _check(outs[0][1].reshape(rows, f), _want(O.Q4_K, w_g, f, h, y), budget=MANY_BUDGET)
+    _check(outs[0][2].reshape(rows, f), _want(O.Q6_K, w_u, f, h, y), budget=MANY_BUDGET)

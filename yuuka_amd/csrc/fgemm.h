@@ -65,6 +65,14 @@ int fused_gemm_stream_rows(int K, bool norm, bool gated);
 // (the quantized activations and split-K partial sums).
 uint64_t fused_gemm_rows_ws(int rows, int K, const int *n, int nseg, bool swiglu);
 hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t s);
+// Two consecutive many-row launches where b normalises a's residual output
+// (b.x == a's single output, b.K == its width): a's split reduction and b's
+// prologue run as one kernel (one workgroup per row sums the splits, adds
+// the residual, stores x and quantizes it for b). *fused is false, and
+// nothing is launched, when the pair does not qualify or the workspace
+// (ws_bytes) cannot hold both layouts; the caller then runs a and b apart.
+hipError_t launch_fused_gemm_rows_pair(const FusedGemmArgs &a, const FusedGemmArgs &b, void *ws, uint64_t ws_bytes,
+                                       hipStream_t s, bool *fused);
 // tt: 16-row tiles per workgroup (1, 2 or 4; even for kEpiSwiglu).
 hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s);
 

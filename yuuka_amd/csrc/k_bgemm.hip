@@ -131,7 +131,18 @@ __device__ __forceinline__ uint32_t h2bits(_Float16 a, _Float16 b) {
 // ---------------------------------------------------------------- prologue
 constexpr int kPrThreads = 512;
 
-__global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemmArgs A, BgQuant q) {
+// Where the prologue's x comes from: A.x, or (part != null) the split
+// partial sums of the previous many-row GEMM, which the prologue finishes as
+// bg_reduce_kernel would (sum in split order, + residual) and stores to out.
+struct BgSrc {
+    const float *part;  // [splits][rows][K]
+    const float *res;   // [rows][K] residual of the previous GEMM (may alias out)
+    float *out;         // [rows][K] the previous GEMM's output
+    uint64_t sstride;   // floats between splits (rows * K)
+    int splits;
+};
+
+__global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemmArgs A, BgQuant q, const BgSrc src) {
     extern __shared__ float ys[];  // [K]: x, then y
     __shared__ double red[kPrThreads / 64];
     const int row = blockIdx.x, K = A.K;
@@ -142,7 +153,34 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
     double ss = 0.0;
 #pragma unroll 4
     for (int c = t; c < K / 4; c += kPrThreads) {
-        const float4 v = x4[c];
+        float4 v;
+        if (src.part) {
+            const float4 *p4 = reinterpret_cast<const float4 *>(src.part + (uint64_t)row * K) + c;
+            v = make_float4(0.f, 0.f, 0.f, 0.f);
+            // eight splits' loads in flight at a time, added in split order
+            for (int s0 = 0; s0 < src.splits; s0 += 8) {
+                float4 w[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    if (s0 + i < src.splits) w[i] = p4[(uint64_t)(s0 + i) * (src.sstride / 4)];
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    if (s0 + i < src.splits) {
+                        v.x += w[i].x;
+                        v.y += w[i].y;
+                        v.z += w[i].z;
+                        v.w += w[i].w;
+                    }
+            }
+            const float4 r = reinterpret_cast<const float4 *>(src.res + (uint64_t)row * K)[c];
+            v.x = __fadd_rn(v.x, r.x);
+            v.y = __fadd_rn(v.y, r.y);
+            v.z = __fadd_rn(v.z, r.z);
+            v.w = __fadd_rn(v.w, r.w);
+            reinterpret_cast<float4 *>(src.out + (uint64_t)row * K)[c] = v;
+        } else {
+            v = x4[c];
+        }
         *reinterpret_cast<float4 *>(ys + 4 * c) = v;
         ss += (double)v.x * (double)v.x + (double)v.y * (double)v.y + (double)v.z * (double)v.z +
               (double)v.w * (double)v.w;
@@ -722,8 +760,9 @@ uint64_t fused_gemm_rows_ws(int rows, int K, const int *n, int nseg, bool swiglu
     return ((bg_quant_bytes(rows, K) + 255) & ~255ull) + part + 256;
 }
 
-hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t s) {
-    BgArgs A{};
+// The arguments, grid and workspace view of one many-row launch.
+static void bg_setup(const FusedGemmArgs &a, void *ws, BgArgs &A, unsigned &gx, unsigned &gy) {
+    A = BgArgs{};
     A.f = a;
     A.q = bg_view(ws, a.rows, a.K);
     A.swiglu = a.epilogue == kEpiSwiglu ? 1 : 0;
@@ -731,31 +770,77 @@ hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t 
     A.tiles[0] = 0;
     for (int i = 0; i < a.nseg; i++) A.tiles[i + 1] = A.tiles[i] + (a.seg[i].n + 16 * kBgWaves - 1) / (16 * kBgWaves);
     for (int i = a.nseg + 1; i <= kFusedMaxSeg; i++) A.tiles[i] = A.tiles[a.nseg];
-    const uint32_t plds = (uint32_t)a.K * 4;
+    int nn[kFusedMaxSeg];
+    for (int i = 0; i < a.nseg; i++) nn[i] = a.seg[i].n;
+    bg_grid(nn, a.nseg, A.swiglu != 0, a.rows, a.K, &gx, &gy, &A.splits);
+    A.cols[0] = 0;
+    for (int i = 0; i < a.nseg; i++) A.cols[i + 1] = A.cols[i] + a.seg[i].n;
+    for (int i = a.nseg + 1; i <= kFusedMaxSeg; i++) A.cols[i] = A.cols[a.nseg];
+    A.part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + ((bg_quant_bytes(a.rows, a.K) + 255) & ~255ull));
+}
+
+static hipError_t bg_launch_prologue(const FusedGemmArgs &a, const BgQuant &q, const BgSrc &src, hipStream_t s) {
     static bool attr = false;
     if (!attr) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void *>(bg_prologue_kernel),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
         attr = true;
     }
-    bg_prologue_kernel<<<(unsigned)a.rows, kPrThreads, plds, s>>>(a, A.q);
-    int nn[kFusedMaxSeg];
-    for (int i = 0; i < a.nseg; i++) nn[i] = a.seg[i].n;
-    unsigned gx, gy;
-    bg_grid(nn, a.nseg, A.swiglu != 0, a.rows, a.K, &gx, &gy, &A.splits);
-    A.cols[0] = 0;
-    for (int i = 0; i < a.nseg; i++) A.cols[i + 1] = A.cols[i] + a.seg[i].n;
-    for (int i = a.nseg + 1; i <= kFusedMaxSeg; i++) A.cols[i] = A.cols[a.nseg];
-    A.part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + ((bg_quant_bytes(a.rows, a.K) + 255) & ~255ull));
+    bg_prologue_kernel<<<(unsigned)a.rows, kPrThreads, (uint32_t)a.K * 4, s>>>(a, q, src);
+    return hipGetLastError();
+}
+
+// The GEMM, then (reduce and more than one split) the split reduction.
+static hipError_t bg_launch_gemm(const BgArgs &A, unsigned gx, unsigned gy, bool reduce, hipStream_t s) {
+    const FusedGemmArgs &a = A.f;
     const dim3 grid(gx, gy, (unsigned)A.splits);
     // (bg_grid's bg_resident call has set the kernel's LDS attribute)
     if (bg_tiles(a.rows) == 5) bg_gemm_kernel<5><<<grid, kBgThreads, BgLds<5>::total, s>>>(A);
     else bg_gemm_kernel<3><<<grid, kBgThreads, BgLds<3>::total, s>>>(A);
-    if (A.splits > 1) {
+    if (reduce && A.splits > 1) {
         const uint64_t nout = (uint64_t)a.rows * (A.swiglu ? a.seg[0].n : A.cols[a.nseg]);
         bg_reduce_kernel<<<(unsigned)((nout + 255) / 256), 256, 0, s>>>(A);
     }
     return hipGetLastError();
+}
+
+hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t s) {
+    BgArgs A;
+    unsigned gx, gy;
+    bg_setup(a, ws, A, gx, gy);
+    hipError_t err = bg_launch_prologue(a, A.q, BgSrc{}, s);
+    if (err == hipSuccess) err = bg_launch_gemm(A, gx, gy, true, s);
+    return err;
+}
+
+hipError_t launch_fused_gemm_rows_pair(const FusedGemmArgs &a, const FusedGemmArgs &b, void *ws, uint64_t ws_bytes,
+                                       hipStream_t s, bool *fused) {
+    *fused = false;
+    if (a.epilogue != kEpiResidual || a.nseg != 1 || a.seg[0].res == nullptr || b.rows != a.rows ||
+        b.K != a.seg[0].n || b.x != a.seg[0].out || b.norm == nullptr || b.gate != nullptr || b.K % 256)
+        return hipSuccess;
+    BgArgs A;
+    unsigned gx, gy;
+    bg_setup(a, ws, A, gx, gy);
+    if (A.splits < 2) return hipSuccess;
+    // b's workspace: from the start when its quantized rows end before a's
+    // partial sums, else after them
+    const uint64_t part_off = (bg_quant_bytes(a.rows, a.K) + 255) & ~255ull;
+    const uint64_t part_bytes = (uint64_t)A.splits * a.rows * a.seg[0].n * 4;
+    const uint64_t b_off = bg_quant_bytes(b.rows, b.K) <= part_off ? 0 : (part_off + part_bytes + 255) & ~255ull;
+    int nb[kFusedMaxSeg];
+    for (int i = 0; i < b.nseg; i++) nb[i] = b.seg[i].n;
+    if (b_off + fused_gemm_rows_ws(b.rows, b.K, nb, b.nseg, b.epilogue == kEpiSwiglu) > ws_bytes) return hipSuccess;
+    BgArgs B;
+    unsigned bx, by;
+    bg_setup(b, static_cast<uint8_t *>(ws) + b_off, B, bx, by);
+    *fused = true;
+    const BgSrc src{A.part, a.seg[0].res, a.seg[0].out, (uint64_t)a.rows * a.seg[0].n, A.splits};
+    hipError_t err = bg_launch_prologue(a, A.q, BgSrc{}, s);
+    if (err == hipSuccess) err = bg_launch_gemm(A, gx, gy, false, s);
+    if (err == hipSuccess) err = bg_launch_prologue(b, B.q, src, s);
+    if (err == hipSuccess) err = bg_launch_gemm(B, bx, by, true, s);
+    return err;
 }
 
 }  // namespace yk

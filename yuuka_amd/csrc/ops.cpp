@@ -527,6 +527,17 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
     }
 }
 
+yuuka_status execute_gemm_pair(const yuuka_op &a, const yuuka_op &b, const ExecCtx &ctx, bool *done) {
+    *done = false;
+    if (a.code != YUUKA_EXT_OP_GEMM_FUSED || b.code != YUUKA_EXT_OP_GEMM_FUSED || !fused_many_rows(a) ||
+        !fused_many_rows(b) || !ctx.ws_bytes)
+        return YUUKA_OK;
+    const FusedGemmArgs fa = fused_args(a), fb = fused_args(b);
+    const hipError_t err = launch_fused_gemm_rows_pair(fa, fb, ctx.ws, ctx.ws_bytes, ctx.stream, done);
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "GEMM_FUSED pair launch: %s", hip_error(err));
+    return YUUKA_OK;
+}
+
 int gdn_commit_run(const yuuka_op *ops, int count) {
     if (count < 2 || ops[0].code != YUUKA_EXT_OP_GDN_COMMIT) return 1;
     const GdnArgs g0 = gdn_args(ops[0]);

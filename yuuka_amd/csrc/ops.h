@@ -20,6 +20,10 @@ bool op_uses_position(const yuuka_op &op);
 // result), 1 when there is none to merge.
 int gdn_commit_run(const yuuka_op *ops, int count);
 yuuka_status execute_gdn_commit_run(const yuuka_op *ops, int count, const ExecCtx &ctx);
+// Two consecutive GEMM_FUSED ops over more than 8 rows where b normalises a's
+// residual output run with a's split reduction and b's prologue in one
+// launch; *done is false when they do not qualify (nothing was launched).
+yuuka_status execute_gemm_pair(const yuuka_op &a, const yuuka_op &b, const ExecCtx &ctx, bool *done);
 
 // Elementwise launchers (k_ops.hip).
 hipError_t launch_copy_f32(float *dst, const float *src, uint64_t n, hipStream_t stream);

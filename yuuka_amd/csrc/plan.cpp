@@ -188,7 +188,7 @@ static yuuka_status guard(F &&f) {
 static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token, uint32_t position,
                             const int32_t *dyn, int run_tail, uint32_t *codes, uint64_t *times,
                             uint64_t capacity, uint64_t *count) {
-    ExecCtx ctx{stream, token, position, dyn, plan->ws, plan->tickets};
+    ExecCtx ctx{stream, token, position, dyn, plan->ws, plan->tickets, plan->ws_bytes};
     uint64_t n = 0;
     hipEvent_t a = nullptr, b = nullptr;
     if (times) {
@@ -224,6 +224,22 @@ static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token,
                 break;
             }
         if (st != YUUKA_OK) break;
+        if (!times && op.code == YUUKA_EXT_OP_GEMM_FUSED && oi + 1 < nops &&
+            !((plan->ops[oi + 1].flags & YUUKA_OP_FLAG_TAIL) && !run_tail)) {
+            // a many-row GEMM whose residual output the next one normalises:
+            // the split reduction and the next prologue in one launch
+            const yuuka_op &nx = plan->ops[oi + 1];
+            bool live = true;
+            for (int i = 0; i < 16; i++) live = live && (!nx.buf[i] || nx.buf[i]->ptr);
+            bool done = false;
+            if (live) st = execute_gemm_pair(op, nx, ctx, &done);
+            if (st != YUUKA_OK) break;
+            if (done) {
+                n += 2;
+                oi += 1;
+                continue;
+            }
+        }
         if (times) (void)hipEventRecord(a, stream);
         st = execute(op, ctx);
         if (st != YUUKA_OK) break;

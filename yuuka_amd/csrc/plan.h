@@ -49,6 +49,7 @@ struct ExecCtx {
     const int32_t *dyn;  // device {token, position} for graph replay, or null
     void *ws;
     uint32_t *tickets;
+    uint64_t ws_bytes = 0;  // size of ws (0: unknown, no op pairs fused)
 };
 
 }  // namespace yk
