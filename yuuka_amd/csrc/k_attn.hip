@@ -808,6 +808,9 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
 // LDS layout of the grouped kernel with NT 16-row query tiles: the
 // transposed V chunk, the query tiles (F16 high, remainder), the scores /
 // probabilities and the running (max, sum, rescale) of every query row.
+// Page-table entries of a group's keys held in LDS by the six-tile kernel
+// (its launcher caps the group so that they fit).
+constexpr int kPtCap = 256;
 template <int NT> struct GroupLds {
     static constexpr int kQ = 16 * NT;
     static constexpr uint32_t Vt = 0;
@@ -815,7 +818,8 @@ template <int NT> struct GroupLds {
     static constexpr uint32_t Ql = Qh + kQ * kMD * 2;
     static constexpr uint32_t S = Ql + kQ * kMD * 2;
     static constexpr uint32_t ML = S + kQ * kMK * 4;
-    static constexpr uint32_t total = ML + 3 * kQ * 4;
+    static constexpr uint32_t PT = ML + 3 * kQ * 4;
+    static constexpr uint32_t total = PT + (NT > 2 ? kPtCap * 4 : 0);
 };
 static_assert(GroupLds<2>::total == kMfmaLds, "two-tile layout");
 static_assert(GroupLds<6>::total <= 160 * 1024, "six-tile layout fits LDS");
@@ -954,8 +958,23 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
     struct Pages {
         int32_t k, v;
     };
+    // PF: the group's page-table entries sit in LDS (loaded once below), so
+    // waiting for an entry never waits for the vector loads issued before it
+    const int pg0 = (c_lo * kMK) / a.block_size;
+    if constexpr (PF) {
+        int *pt = reinterpret_cast<int *>(lds + LY::PT);
+        const int pg1 = min(c_hi * kMK - 1, last) / a.block_size;
+        for (int i = (int)threadIdx.x; i <= pg1 - pg0; i += (int)blockDim.x) pt[i] = table[pg0 + i];
+        __syncthreads();
+    }
     auto fetch_pages = [&](Pages &P, int ci) __attribute__((always_inline)) {
         const int key0 = ci * kMK;
+        if constexpr (PF) {
+            const int *pt = reinterpret_cast<const int *>(lds + LY::PT);
+            P.k = pt[min(key0 + kk_s, last) / a.block_size - pg0];
+            P.v = pt[min(key0 + lane, last) / a.block_size - pg0];
+            return;
+        }
         P.k = table[min(key0 + kk_s, last) / a.block_size];
         P.v = table[min(key0 + lane, last) / a.block_size];
     };
@@ -1330,6 +1349,8 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
             const int v = atoi(e);
             if (v >= 1 && v <= 32) cpw = v;
         }
+        // the six-tile kernel keeps the group's page entries in LDS
+        if (wide) cpw = std::max(1, std::min(cpw, (kPtCap - 2) * std::max(1, a.block_size) / kMK));
     }
     const int ck = mfma ? kMK * cpw : attn_verify_chunk(a.fmt);
     const int chunks = (a.capacity + ck - 1) / ck;
