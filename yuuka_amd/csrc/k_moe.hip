@@ -365,7 +365,17 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s1, uint32_t s2, ui
 // the epilogue. Lane (c, g) of an item loads channel c's Q4_K bytes straight
 // into MFMA B order and the activation planes of assignment c & 7 (high
 // plane for c < 8) into A order.
+#ifdef YK_MOE_TIMING
+__device__ uint64_t *yk_moe_dbg;  // per wave: start, rows known, staged, items done, end
+#define YK_MOE_STAMP(i) ts[i] = __builtin_amdgcn_s_memrealtime()
+#else
+#define YK_MOE_STAMP(i) (void)0
+#endif
 __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))) void moe_gemm_kernel(MoeGemmArgs A) {
+#ifdef YK_MOE_TIMING
+    uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    YK_MOE_STAMP(0);
+#endif
     // LDS: results [tpw][mats][8 rows][16 ch] floats, then the
     // chunk's activations: planes [K/64][16 r][4 g][2][8 B] (r < 8 high
     // plane of assignment r, r >= 8 low plane of assignment r - 8), scales
@@ -406,6 +416,7 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
             }
         }
         __syncthreads();
+        YK_MOE_STAMP(1);
         for (int idx = threadIdx.x; idx < nsub * 32; idx += kMoeThreads) {  // 16 B pieces of the planes
             const int j = idx >> 5, r = (idx >> 1) & 15, half = idx & 1;
             const int8_t *src = A.xq.planes + (uint64_t)s_row[r & 7] * A.K * 2 + (uint64_t)j * 64 + (r >= 8 ? 32 : 0) +
@@ -419,6 +430,7 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
         for (int idx = threadIdx.x; idx < nsb * 8; idx += kMoeThreads)
             lxs[idx] = A.xq.scales[(uint64_t)s_row[idx & 7] * nsb + (idx >> 3)];
         __syncthreads();
+        YK_MOE_STAMP(2);
         // items (tile, matrix, super-block): wave w walks the pairs (tile,
         // matrix) w, w + 8, ... through their super-blocks in order with the
         // next item's weights in flight, sums in registers in super-block
@@ -427,29 +439,55 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
         const int npw = wave < pairs ? (pairs - wave + kMoeWaves - 1) / kMoeWaves : 0;
         const int total = npw * nsb;
         const int rbase = 4 * (g & 1);
-        auto load_item = [&](int q, uint4 &H, uint64_t (&Q)[4]) __attribute__((always_inline)) {
+        // quant bytes of an item: lane (c, g) loads 16 contiguous bytes per
+        // half of the block, [32 jp + 16 (g & 1), +16) with jp = 2 qq + (g >> 1),
+        // so each load covers 64 contiguous bytes of every channel; the
+        // activation operands below follow the same (sub-block, element)
+        // assignment (the MFMA sums over K in any order)
+        auto load_item = [&](int q, uint4 &H, uint4 (&Q)[2]) __attribute__((always_inline)) {
+            int oz;  // opaque zero: the lane's row address is rebuilt per item, not held (and spilled)
+            asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+            const int lc = c + oz, lg = g + oz;
             const int tm = wave + kMoeWaves * (q / nsb), sb = q % nsb, m = tm % mats, tl = tm / mats;
-            const uint8_t *blk = (m ? A.w1 : A.w0) + ((uint64_t)e * A.N + (t0 + tl) * 16 + c) * A.row_bytes +
+            const uint8_t *blk = (m ? A.w1 : A.w0) + ((uint64_t)e * A.N + (t0 + tl) * 16 + lc) * A.row_bytes +
                                  (uint64_t)sb * 144;
             H = *reinterpret_cast<const uint4 *>(blk);
 #pragma unroll
-            for (int p = 0; p < 4; p++) Q[p] = *reinterpret_cast<const uint64_t *>(blk + 16 + 32 * p + 8 * g);
+            for (int qq = 0; qq < 2; qq++)
+                Q[qq] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * (2 * qq + (lg >> 1)) + 16 * (lg & 1));
         };
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        auto compute_item = [&](int q, const uint4 &H, const uint64_t (&Q)[4]) __attribute__((always_inline)) {
+        auto compute_item = [&](int q, const uint4 &H, const uint4 (&Q)[2]) __attribute__((always_inline)) {
             const int sb = q % nsb;
             const float4 xs4 = *reinterpret_cast<const float4 *>(lxs + sb * 8 + rbase);
             const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
             // sub-block scale (two 3-bit digits) and min in the B operands
             // of three K = 64 MFMAs per pair of sub-blocks: exact int32
             i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
+            // this lane's scale bytes: sub-blocks 2 jp, 2 jp + 1 of jp = 2 qq + b
+            // sit in bytes 2 b, 2 b + 1 of each scale word (getScaleMinK4 layout)
+            int oz;  // opaque zero: lane-derived offsets are rebuilt per item
+            asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+            const int lc = c + oz, lg = g + oz, b = lg >> 1;
+            const uint32_t y1 = H.y >> (16 * b), z1 = H.z >> (16 * b), w1 = H.w >> (16 * b);
 #pragma unroll
-            for (int jp = 0; jp < 4; jp++) {
-                const uint64_t raw = Q[jp];
+            for (int mi = 0; mi < 4; mi++) {
+                const int qq = mi >> 1, hh = mi & 1, jp = 2 * qq + b;
+                const uint64_t raw = hh ? ((uint64_t)Q[qq].z | ((uint64_t)Q[qq].w << 32))
+                                        : ((uint64_t)Q[qq].x | ((uint64_t)Q[qq].y << 32));
                 const uint64_t qe = raw & 0x0F0F0F0F0F0F0F0Full, qo = (raw >> 4) & 0x0F0F0F0F0F0F0F0Full;
                 int sce, mne, sco, mno;
-                scale_min_k4(2 * jp, H.y, H.z, H.w, &sce, &mne);
-                scale_min_k4(2 * jp + 1, H.y, H.z, H.w, &sco, &mno);
+                if (qq == 0) {  // sub-blocks 0..3: low six bits of scale / min bytes
+                    sce = (int)(y1 & 63);
+                    sco = (int)((y1 >> 8) & 63);
+                    mne = (int)(z1 & 63);
+                    mno = (int)((z1 >> 8) & 63);
+                } else {  // sub-blocks 4..7: nibbles of bytes 8..11, high bits of 0..7
+                    sce = (int)((w1 & 0xF) | (((y1 >> 6) & 3) << 4));
+                    sco = (int)(((w1 >> 8) & 0xF) | (((y1 >> 14) & 3) << 4));
+                    mne = (int)(((w1 >> 4) & 0xF) | (((z1 >> 6) & 3) << 4));
+                    mno = (int)(((w1 >> 12) & 0xF) | (((z1 >> 14) & 3) << 4));
+                }
                 const uint32_t qw[4] = {(uint32_t)qe, (uint32_t)(qe >> 32), (uint32_t)qo, (uint32_t)(qo >> 32)};
                 const uint32_t lo[2] = {(uint32_t)(sce & 7), (uint32_t)(sco & 7)};
                 const uint32_t hi[2] = {(uint32_t)(sce >> 3), (uint32_t)(sco >> 3)};
@@ -460,7 +498,7 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
                 const int me = (int)__builtin_amdgcn_perm((uint32_t)mne, (uint32_t)mne, 0u);
                 const int mo = (int)__builtin_amdgcn_perm((uint32_t)mno, (uint32_t)mno, 0u);
                 const i32x4 b_mn = {me, me, mo, mo};
-                const i32x4 av = *reinterpret_cast<const i32x4 *>(la + moe_la_off(sb * 8 + 2 * jp, c, g));
+                const i32x4 av = *reinterpret_cast<const i32x4 *>(la + moe_la_off(sb * 8 + 2 * jp, lc, 2 * (lg & 1) + hh));
                 alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_lo, alo, 0, 0, 0);
                 ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_hi, ahi, 0, 0, 0);
                 amn = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_mn, amn, 0, 0, 0);
@@ -485,7 +523,7 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
             }
         };
         uint4 h0, h1;
-        uint64_t q0[4], q1[4];
+        uint4 q0[2], q1[2];
         if (total > 0) load_item(0, h0, q0);
         if (total > 1) load_item(1, h1, q1);
         for (int q = 0; q < total; q += 2) {
@@ -496,6 +534,7 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
                 if (q + 3 < total) load_item(q + 3, h1, q1);
             }
         }
+        YK_MOE_STAMP(3);
         __syncthreads();
         // the epilogue
         for (int o = threadIdx.x; o < ntl * nr * 16; o += kMoeThreads) {
@@ -511,6 +550,13 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
             }
         }
     }
+#ifdef YK_MOE_TIMING
+    YK_MOE_STAMP(4);
+    if (yk_moe_dbg && (threadIdx.x & 63) == 0) {
+        uint64_t *o = yk_moe_dbg + (((uint64_t)blockIdx.y * gridDim.x + blockIdx.x) * kMoeWaves + (threadIdx.x >> 6)) * 8;
+        for (int i = 0; i < 8; i++) o[i] = ts[i];
+    }
+#endif
 }
 
 // ---------------------------------------------------------------- reduce
