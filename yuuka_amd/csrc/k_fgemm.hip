@@ -523,9 +523,16 @@ __device__ __forceinline__ void act_prologue_regs(const FusedGemmArgs &A, const 
 constexpr uint32_t kOutOfRange = 0xC0000000u;
 
 // Staged weight bytes of one 16-row tile for one super-block.
+// K order of the weight and activation operands: MFMA lane group g holds
+// the 8-byte chunk kperm(g) of each 32-element sub-block (0, 2, 1, 3). The
+// product sums over K, so any order is exact as long as both operands
+// follow it; this one lets a Q4_K lane load its quant bytes as 16-byte
+// pieces (64 contiguous bytes of every channel per load).
+__device__ __forceinline__ int kperm(int g) { return ((g & 1) << 1) | (g >> 1); }
+
 struct Q4Stage {
     i32x4 hdr;      // d | dmin, 12 scale bytes
-    uint64_t qs[4]; // bytes [16 + 32p + 8g, +8) for p = 0..3
+    uint4 q16[2];   // bytes [16 + 32 (2 h + (g >> 1)) + 16 (g & 1), +16) for h = 0, 1
 };
 struct Q6Stage {
     uint64_t ql[4]; // [n][half]: bytes n*64 + half*32 + 8g
@@ -549,16 +556,30 @@ template <> struct StageOf<0> { using T = MixStage; };
 __device__ __forceinline__ void issue(Q4Stage &S, __amdgpu_buffer_rsrc_t rs, uint32_t row_off, int g) {
     S.hdr = __builtin_amdgcn_raw_buffer_load_b128(rs, row_off, 0, 0);
 #pragma unroll
-    for (int p = 0; p < 4; p++)
-        S.qs[p] = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(rs, row_off + 16 + 32 * p + 8 * g, 0, 0));
+    for (int h = 0; h < 2; h++)
+        S.q16[h] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, row_off + 16 + 32 * (2 * h + (g >> 1)) + 16 * (g & 1), 0, 0));
+}
+
+// The four 8-byte quant pieces of p-blocks 0..3 in the kperm order: lanes
+// 0..31 loaded p-block 2 h, lanes 32..63 p-block 2 h + 1 (16 bytes each);
+// one lane-half swap of each dword gives every lane its chunk of both.
+__device__ __forceinline__ void q4_pieces(const Q4Stage &S, uint64_t (&qs)[4]) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const auto lo = __builtin_amdgcn_permlane32_swap(S.q16[h].x, S.q16[h].z, true, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap(S.q16[h].y, S.q16[h].w, true, false);
+        qs[2 * h] = (uint64_t)lo[0] | ((uint64_t)hi[0] << 32);
+        qs[2 * h + 1] = (uint64_t)lo[1] | ((uint64_t)hi[1] << 32);
+    }
 }
 
 __device__ __forceinline__ void issue(Q6Stage &S, __amdgpu_buffer_rsrc_t rs, uint32_t row_off, int g) {
 #pragma unroll
     for (int n = 0; n < 2; n++) {
-        S.ql[2 * n] = load8_a2(rs, row_off + n * 64 + 8 * g);
-        S.ql[2 * n + 1] = load8_a2(rs, row_off + n * 64 + 32 + 8 * g);
-        S.qh[n] = load8_a2(rs, row_off + 128 + n * 32 + 8 * g);
+        S.ql[2 * n] = load8_a2(rs, row_off + n * 64 + 8 * kperm(g));
+        S.ql[2 * n + 1] = load8_a2(rs, row_off + n * 64 + 32 + 8 * kperm(g));
+        S.qh[n] = load8_a2(rs, row_off + 128 + n * 32 + 8 * kperm(g));
     }
     const uint32_t a = row_off + 192;
     typedef __attribute__((ext_vector_type(4))) int v4;
@@ -583,6 +604,8 @@ __device__ __forceinline__ void compute(const Q4Stage &S, const int64_t (&xa)[NA
                                         const float (&xsr)[NA][4], float (&acc)[NA][4]) {
     const uint32_t h0 = (uint32_t)S.hdr[0], q0 = (uint32_t)S.hdr[1], q1 = (uint32_t)S.hdr[2], q2 = (uint32_t)S.hdr[3];
     const float d = half_lo(h0), dmin = half_lo(h0 >> 16);
+    uint64_t qs[4];
+    q4_pieces(S, qs);
     // getScaleMinK4 (tensor/quant.go:96-103) for all eight sub-blocks
     const uint32_t sc_lo = q0 & 0x3f3f3f3fu;
     const uint32_t sc_hi = (q2 & 0x0f0f0f0fu) | ((q0 >> 2) & 0x30303030u);
@@ -597,8 +620,8 @@ __device__ __forceinline__ void compute(const Q4Stage &S, const int64_t (&xa)[NA
         for (int i = 0; i < 4; i++) acci[a][i] = 0;
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-        const int64_t blo = (int64_t)(S.qs[p] & 0x0f0f0f0f0f0f0f0full);
-        const int64_t bhi = (int64_t)((S.qs[p] >> 4) & 0x0f0f0f0f0f0f0f0full);
+        const int64_t blo = (int64_t)(qs[p] & 0x0f0f0f0f0f0f0f0full);
+        const int64_t bhi = (int64_t)((qs[p] >> 4) & 0x0f0f0f0f0f0f0f0full);
         const uint32_t scw = p < 2 ? sc_lo : sc_hi;
         const int s0 = (int)__builtin_amdgcn_ubfe(scw, 16 * (p & 1), 8);
         const int s1 = (int)__builtin_amdgcn_ubfe(scw, 16 * (p & 1) + 8, 8);
@@ -630,7 +653,7 @@ __device__ __forceinline__ void compute(const Q6Stage &S, const int64_t (&xa)[NA
     for (int a = 0; a < NA; a++)
 #pragma unroll
         for (int i = 0; i < 4; i++) acci[a][i] = 0;
-    const bool first = g < 2;  // lanes holding elements 0..15 of each 32
+    const bool first = kperm(g) < 2;  // lanes holding elements 0..15 of each 32
 #pragma unroll
     for (int c = 0; c < 8; c++) {
         const int n = c >> 2, qd = c & 3;
@@ -695,10 +718,10 @@ __device__ __forceinline__ void load_act(const uint8_t *lds, const ActLayout &L,
         // rows past 2M read the last plane row: MFMA output row i depends on
         // A row i only, and the outputs of those rows are never read (integer
         // products, so no NaN either); a branch per lane would cost moves
-        const int rho = min(16 * a + r, L.rho - 1);
+        const int rho = min(16 * a + r, L.rho - 1), gk = kperm(g);  // the weights' K order
 #pragma unroll
         for (int j = 0; j < 8; j++)
-            xa[a][j] = *reinterpret_cast<const int64_t *>(lds + L.planes + ((uint32_t)((sbl * 8 + j) * 4 + g) * L.rho + rho) * 8);
+            xa[a][j] = *reinterpret_cast<const int64_t *>(lds + L.planes + ((uint32_t)((sbl * 8 + j) * 4 + gk) * L.rho + rho) * 8);
         const float4 xv = *reinterpret_cast<const float4 *>(lds + L.xs + ((uint32_t)sbl * L.rhop + 16 * a + 4 * g) * 4);
         xsr[a][0] = xv.x;
         xsr[a][1] = xv.y;
