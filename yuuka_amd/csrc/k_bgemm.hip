@@ -142,96 +142,121 @@ struct BgSrc {
     int splits;
 };
 
+// One row per workgroup. Wave w owns super-blocks w, w + 8, ... (at most P
+// of them) and lane l elements [4 l, +4) of each: x (or the split sums), the
+// norm weights and the gate are loaded into registers in one round trip; the
+// row's float64 sum of squares is the only exchange between waves.
+template <int P>
 __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemmArgs A, BgQuant q, const BgSrc src) {
-    extern __shared__ float ys[];  // [K]: x, then y
-    __shared__ double red[kPrThreads / 64];
-    const int row = blockIdx.x, K = A.K;
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    // x into LDS with independent 16-byte loads (the float64 sum of squares
-    // for RMSNorm on the way)
-    const float4 *x4 = reinterpret_cast<const float4 *>(A.x + (uint64_t)row * K);
-    double ss = 0.0;
-#pragma unroll 4
-    for (int c = t; c < K / 4; c += kPrThreads) {
-        float4 v;
-        if (src.part) {
-            const float4 *p4 = reinterpret_cast<const float4 *>(src.part + (uint64_t)row * K) + c;
-            v = make_float4(0.f, 0.f, 0.f, 0.f);
-            // eight splits' loads in flight at a time, added in split order
-            for (int s0 = 0; s0 < src.splits; s0 += 8) {
-                float4 w[8];
+    constexpr int W = kPrThreads / 64;
+    __shared__ double red[W];
+    const int row = blockIdx.x, K = A.K, nsb = K / 256;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const uint64_t rbase = (uint64_t)row * K;
+    auto elem = [&](int i) { return (wave + W * i) * 256 + 4 * lane; };
+    auto live = [&](int i) { return wave + W * i < nsb; };
+    auto add4 = [](float4 &v, const float4 &w) {
+        v.x += w.x;
+        v.y += w.y;
+        v.z += w.z;
+        v.w += w.w;
+    };
+    float4 v[P], nw[P], z[P];
+    if (src.part) {
+        // the previous GEMM's split partial sums, added in split order, then
+        // its residual; 16 loads in flight at a time
+        constexpr int SG = P >= 8 ? 2 : 16 / P;
 #pragma unroll
-                for (int i = 0; i < 8; i++)
-                    if (s0 + i < src.splits) w[i] = p4[(uint64_t)(s0 + i) * (src.sstride / 4)];
+        for (int i = 0; i < P; i++) v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s0 = 0; s0 < src.splits; s0 += SG) {
+            float4 t[SG][P];
 #pragma unroll
-                for (int i = 0; i < 8; i++)
-                    if (s0 + i < src.splits) {
-                        v.x += w[i].x;
-                        v.y += w[i].y;
-                        v.z += w[i].z;
-                        v.w += w[i].w;
-                    }
-            }
-            const float4 r = reinterpret_cast<const float4 *>(src.res + (uint64_t)row * K)[c];
-            v.x = __fadd_rn(v.x, r.x);
-            v.y = __fadd_rn(v.y, r.y);
-            v.z = __fadd_rn(v.z, r.z);
-            v.w = __fadd_rn(v.w, r.w);
-            reinterpret_cast<float4 *>(src.out + (uint64_t)row * K)[c] = v;
-        } else {
-            v = x4[c];
+            for (int j = 0; j < SG; j++)
+#pragma unroll
+                for (int i = 0; i < P; i++)
+                    if (s0 + j < src.splits && live(i))
+                        t[j][i] = *reinterpret_cast<const float4 *>(src.part + (uint64_t)(s0 + j) * src.sstride + rbase +
+                                                                    elem(i));
+#pragma unroll
+            for (int j = 0; j < SG; j++)
+#pragma unroll
+                for (int i = 0; i < P; i++)
+                    if (s0 + j < src.splits && live(i)) add4(v[i], t[j][i]);
         }
-        *reinterpret_cast<float4 *>(ys + 4 * c) = v;
-        ss += (double)v.x * (double)v.x + (double)v.y * (double)v.y + (double)v.z * (double)v.z +
-              (double)v.w * (double)v.w;
+#pragma unroll
+        for (int i = 0; i < P; i++)
+            if (live(i)) {
+                const float4 r = *reinterpret_cast<const float4 *>(src.res + rbase + elem(i));
+                v[i].x = __fadd_rn(v[i].x, r.x);
+                v[i].y = __fadd_rn(v[i].y, r.y);
+                v[i].z = __fadd_rn(v[i].z, r.z);
+                v[i].w = __fadd_rn(v[i].w, r.w);
+                *reinterpret_cast<float4 *>(src.out + rbase + elem(i)) = v[i];
+            }
+    } else {
+#pragma unroll
+        for (int i = 0; i < P; i++)
+            if (live(i)) v[i] = *reinterpret_cast<const float4 *>(A.x + rbase + elem(i));
+    }
+    float4 hw = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (A.gate) {
+        hw = *reinterpret_cast<const float4 *>(A.head_norm + ((4 * lane) & 127));
+#pragma unroll
+        for (int i = 0; i < P; i++)
+            if (live(i)) z[i] = *reinterpret_cast<const float4 *>(A.gate + rbase + elem(i));
+    } else if (A.norm) {
+#pragma unroll
+        for (int i = 0; i < P; i++)
+            if (live(i)) nw[i] = *reinterpret_cast<const float4 *>(A.norm + elem(i));
     }
     float nscale = 1.f;
-    if (A.norm) {
+    if (A.norm && !A.gate) {
         // forward.go:460-470 rmsNorm: float64 sum of squares, x * scale * w
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < P; i++)
+            if (live(i))
+                ss += (double)v[i].x * (double)v[i].x + (double)v[i].y * (double)v[i].y +
+                      (double)v[i].z * (double)v[i].z + (double)v[i].w * (double)v[i].w;
         ss = wave_sum_d(ss);
         if (lane == 0) red[wave] = ss;
-    }
-    __syncthreads();
-    if (A.norm) {
-        double s = 0.0;
+        __syncthreads();
+        double t = 0.0;
 #pragma unroll
-        for (int w = 0; w < kPrThreads / 64; w++) s += red[w];
-        const float mean = (float)(s / (double)K);
+        for (int w = 0; w < W; w++) t += red[w];
+        const float mean = (float)(t / (double)K);
         nscale = (float)(1.0 / sqrt((double)(mean + A.eps)));
     }
-    const int nsb = K / 256;
-#pragma unroll 2
-    for (int sb = wave; sb < nsb; sb += kPrThreads / 64) {
-        const int e = sb * 256 + 4 * lane;
-        float4 v = *reinterpret_cast<const float4 *>(ys + e);
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+        if (!live(i)) break;  // wave-uniform
+        const int sb = wave + W * i, e = elem(i);
+        float4 y = v[i];
         if (A.gate) {
             // recurrent.go:39-50 gated head norm over heads of 128 (lanes 0..31
             // and 32..63 hold one head each): x * (scale * w) * gate
-            const float4 z = *reinterpret_cast<const float4 *>(A.gate + (uint64_t)row * K + e);
-            const float4 w = *reinterpret_cast<const float4 *>(A.head_norm + (e & 127));
-            double hs = (double)v.x * (double)v.x + (double)v.y * (double)v.y + (double)v.z * (double)v.z +
-                        (double)v.w * (double)v.w;
+            double hs = (double)y.x * (double)y.x + (double)y.y * (double)y.y + (double)y.z * (double)y.z +
+                        (double)y.w * (double)y.w;
             hs = row16_sum_d(hs);  // each 128-element head is two 16-lane rows
             hs = lane < 32 ? rl_d(hs, 0) + rl_d(hs, 16) : rl_d(hs, 32) + rl_d(hs, 48);
             const float mean = (float)(hs / 128.0);
             const float hsc = (float)(1.0 / sqrt((double)(mean + A.eps)));
-            v.x = __fmul_rn(__fmul_rn(v.x, __fmul_rn(hsc, w.x)), z.x);
-            v.y = __fmul_rn(__fmul_rn(v.y, __fmul_rn(hsc, w.y)), z.y);
-            v.z = __fmul_rn(__fmul_rn(v.z, __fmul_rn(hsc, w.z)), z.z);
-            v.w = __fmul_rn(__fmul_rn(v.w, __fmul_rn(hsc, w.w)), z.w);
+            y.x = __fmul_rn(__fmul_rn(y.x, __fmul_rn(hsc, hw.x)), z[i].x);
+            y.y = __fmul_rn(__fmul_rn(y.y, __fmul_rn(hsc, hw.y)), z[i].y);
+            y.z = __fmul_rn(__fmul_rn(y.z, __fmul_rn(hsc, hw.z)), z[i].z);
+            y.w = __fmul_rn(__fmul_rn(y.w, __fmul_rn(hsc, hw.w)), z[i].w);
         } else if (A.norm) {
-            const float4 w = *reinterpret_cast<const float4 *>(A.norm + e);
-            v.x = __fmul_rn(__fmul_rn(v.x, nscale), w.x);
-            v.y = __fmul_rn(__fmul_rn(v.y, nscale), w.y);
-            v.z = __fmul_rn(__fmul_rn(v.z, nscale), w.z);
-            v.w = __fmul_rn(__fmul_rn(v.w, nscale), w.w);
+            y.x = __fmul_rn(__fmul_rn(y.x, nscale), nw[i].x);
+            y.y = __fmul_rn(__fmul_rn(y.y, nscale), nw[i].y);
+            y.z = __fmul_rn(__fmul_rn(y.z, nscale), nw[i].z);
+            y.w = __fmul_rn(__fmul_rn(y.w, nscale), nw[i].w);
         }
-        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        float m = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
         m = wave_max_nonneg(m);
         const float inv = m > 0.f ? kBgRange / m : 0.f;
-        const _Float16 h0 = (_Float16)(v.x * inv), h1 = (_Float16)(v.y * inv), h2 = (_Float16)(v.z * inv),
-                       h3 = (_Float16)(v.w * inv);
-        *reinterpret_cast<uint2 *>(q.h + (uint64_t)row * K + e) = make_uint2(h2bits(h0, h1), h2bits(h2, h3));
+        const _Float16 h0 = (_Float16)(y.x * inv), h1 = (_Float16)(y.y * inv), h2 = (_Float16)(y.z * inv),
+                       h3 = (_Float16)(y.w * inv);
+        *reinterpret_cast<uint2 *>(q.h + rbase + e) = make_uint2(h2bits(h0, h1), h2bits(h2, h3));
         // sub-block lane >> 3: eight lanes of four values
         const float s = group8_sum(((float)h0 + (float)h1) + ((float)h2 + (float)h3));
         if ((lane & 7) == 0) {
@@ -780,13 +805,20 @@ static void bg_setup(const FusedGemmArgs &a, void *ws, BgArgs &A, unsigned &gx, 
 }
 
 static hipError_t bg_launch_prologue(const FusedGemmArgs &a, const BgQuant &q, const BgSrc &src, hipStream_t s) {
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void *>(bg_prologue_kernel),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024);
-        attr = true;
+    // super-blocks per wave, rounded up to an instantiated register count
+    const int per = (a.K / 256 + kPrThreads / 64 - 1) / (kPrThreads / 64);
+    const dim3 grid((unsigned)a.rows);
+    switch (per) {
+    case 1: bg_prologue_kernel<1><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
+    case 2: bg_prologue_kernel<2><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
+    case 3: bg_prologue_kernel<3><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
+    case 4: bg_prologue_kernel<4><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
+    case 5:
+    case 6: bg_prologue_kernel<6><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
+    case 7:
+    case 8: bg_prologue_kernel<8><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
+    default: return hipErrorInvalidValue;  // K over 16384
     }
-    bg_prologue_kernel<<<(unsigned)a.rows, kPrThreads, (uint32_t)a.K * 4, s>>>(a, q, src);
     return hipGetLastError();
 }
 
