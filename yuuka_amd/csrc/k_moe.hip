@@ -40,6 +40,7 @@ constexpr int kQMax = 32639;     // |q| bound that keeps the high plane in int8
 constexpr int kMoeWaves = 8;
 constexpr int kMoeThreads = 64 * kMoeWaves;
 constexpr int kChunk = 8;        // assignments per MFMA tile (high planes in rows 0..7)
+constexpr int kMoeMaxExperts = 1024;
 
 // Wave reductions on the DPP path (a __shfl_xor is an LDS permute): within
 // each 16-lane row (pairs, quads, half rows, rows), then the four rows'
@@ -381,172 +382,194 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
     // plane of assignment r, r >= 8 low plane of assignment r - 8), scales
     // [K/256][8] float.
     extern __shared__ __attribute__((aligned(16))) float part[];
-    const int e = blockIdx.x;
-    const int count = A.counts[e];
-    if (count <= 0) return;
     const int nsb = A.K / 256, nsub = A.K / 32;
     const int tiles = A.N / 16;
-    const int t0 = blockIdx.y * A.tpw;
-    if (t0 >= tiles) return;
-    const int ntl = min(A.tpw, tiles - t0);
+    const int parts = (tiles + A.tpw - 1) / A.tpw;
     const bool dual = A.w1 != nullptr;
     const int mats = dual ? 2 : 1;
     __shared__ int s_row[kChunk], s_out[kChunk];
+    __shared__ int s_act[kMoeMaxExperts], s_wtot[kMoeWaves];
     uint8_t *la = reinterpret_cast<uint8_t *>(part + (uint64_t)A.tpw * mats * 128);
     float *lxs = reinterpret_cast<float *>(la + (uint64_t)nsub * 16 * 32);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = lane & 15, g = lane >> 4;
     const uint64_t cap = (uint64_t)A.rows * A.used;
 
-    for (int c0 = 0; c0 < count; c0 += kChunk) {
-        const int nr = min(kChunk, count - c0);
+    // The experts some row selected, in expert order (ballot prefix counts
+    // per 64 experts, wave totals added in wave order): the work items are
+    // (active expert, tile part) pairs dealt round-robin over the grid, so
+    // every workgroup gets an equal share wherever the active experts fall.
+    int nact = 0;
+    for (int b0 = 0; b0 < A.E; b0 += kMoeThreads) {
+        const int ex = b0 + (int)threadIdx.x;
+        const bool on = ex < A.E && A.counts[ex] > 0;
+        const uint64_t m = __ballot(on);
+        const int below = __popcll(m & ((1ull << lane) - 1ull));
+        if (lane == 0) s_wtot[wave] = __popcll(m);
         __syncthreads();
-        if (threadIdx.x < kChunk) {
-            const int i = threadIdx.x;
-            if (i < nr) {
-                const uint64_t o = (uint64_t)e * cap + c0 + i;
-                const int row = A.arows[o], slot = A.aslots[o];
-                s_out[i] = row * A.used + slot;
-                s_row[i] = A.by_slot ? row * A.used + slot : row;
-            } else {  // padding rows read assignment 0 and are never stored
-                const uint64_t o = (uint64_t)e * cap + c0;
-                const int row = A.arows[o], slot = A.aslots[o];
-                s_out[i] = -1;
-                s_row[i] = A.by_slot ? row * A.used + slot : row;
-            }
-        }
+        int base = nact;
+        for (int w = 0; w < wave; w++) base += s_wtot[w];
+        if (on) s_act[base + below] = ex;
+        for (int w = 0; w < kMoeWaves; w++) nact += s_wtot[w];
         __syncthreads();
-        YK_MOE_STAMP(1);
-        for (int idx = threadIdx.x; idx < nsub * 32; idx += kMoeThreads) {  // 16 B pieces of the planes
-            const int j = idx >> 5, r = (idx >> 1) & 15, half = idx & 1;
-            const int8_t *src = A.xq.planes + (uint64_t)s_row[r & 7] * A.K * 2 + (uint64_t)j * 64 + (r >= 8 ? 32 : 0) +
-                                16 * half;
-            const uint4 v = *reinterpret_cast<const uint4 *>(src);
-            // lane groups 2 half and 2 half + 1; sub-blocks 2 jp, 2 jp + 1 side by side
-            uint8_t *d0 = la + moe_la_off(j, r, 2 * half);
-            *reinterpret_cast<uint2 *>(d0) = make_uint2(v.x, v.y);
-            *reinterpret_cast<uint2 *>(d0 + 16) = make_uint2(v.z, v.w);
-        }
-        for (int idx = threadIdx.x; idx < nsb * 8; idx += kMoeThreads)
-            lxs[idx] = A.xq.scales[(uint64_t)s_row[idx & 7] * nsb + (idx >> 3)];
-        __syncthreads();
-        YK_MOE_STAMP(2);
-        // items (tile, matrix, super-block): wave w walks the pairs (tile,
-        // matrix) w, w + 8, ... through their super-blocks in order with the
-        // next item's weights in flight, sums in registers in super-block
-        // order, one result per pair to LDS
-        const int pairs = ntl * mats;
-        const int npw = wave < pairs ? (pairs - wave + kMoeWaves - 1) / kMoeWaves : 0;
-        const int total = npw * nsb;
-        const int rbase = 4 * (g & 1);
-        // quant bytes of an item: lane (c, g) loads 16 contiguous bytes per
-        // half of the block, [32 jp + 16 (g & 1), +16) with jp = 2 qq + (g >> 1),
-        // so each load covers 64 contiguous bytes of every channel; the
-        // activation operands below follow the same (sub-block, element)
-        // assignment (the MFMA sums over K in any order)
-        auto load_item = [&](int q, uint4 &H, uint4 (&Q)[2]) __attribute__((always_inline)) {
-            int oz;  // opaque zero: the lane's row address is rebuilt per item, not held (and spilled)
-            asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
-            const int lc = c + oz, lg = g + oz;
-            const int tm = wave + kMoeWaves * (q / nsb), sb = q % nsb, m = tm % mats, tl = tm / mats;
-            const uint8_t *blk = (m ? A.w1 : A.w0) + ((uint64_t)e * A.N + (t0 + tl) * 16 + lc) * A.row_bytes +
-                                 (uint64_t)sb * 144;
-            H = *reinterpret_cast<const uint4 *>(blk);
-#pragma unroll
-            for (int qq = 0; qq < 2; qq++)
-                Q[qq] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * (2 * qq + (lg >> 1)) + 16 * (lg & 1));
-        };
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        auto compute_item = [&](int q, const uint4 &H, const uint4 (&Q)[2]) __attribute__((always_inline)) {
-            const int sb = q % nsb;
-            const float4 xs4 = *reinterpret_cast<const float4 *>(lxs + sb * 8 + rbase);
-            const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
-            // sub-block scale (two 3-bit digits) and min in the B operands
-            // of three K = 64 MFMAs per pair of sub-blocks: exact int32
-            i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
-            // this lane's scale bytes: sub-blocks 2 jp, 2 jp + 1 of jp = 2 qq + b
-            // sit in bytes 2 b, 2 b + 1 of each scale word (getScaleMinK4 layout)
-            int oz;  // opaque zero: lane-derived offsets are rebuilt per item
-            asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
-            const int lc = c + oz, lg = g + oz, b = lg >> 1;
-            const uint32_t y1 = H.y >> (16 * b), z1 = H.z >> (16 * b), w1 = H.w >> (16 * b);
-#pragma unroll
-            for (int mi = 0; mi < 4; mi++) {
-                const int qq = mi >> 1, hh = mi & 1, jp = 2 * qq + b;
-                const uint64_t raw = hh ? ((uint64_t)Q[qq].z | ((uint64_t)Q[qq].w << 32))
-                                        : ((uint64_t)Q[qq].x | ((uint64_t)Q[qq].y << 32));
-                const uint64_t qe = raw & 0x0F0F0F0F0F0F0F0Full, qo = (raw >> 4) & 0x0F0F0F0F0F0F0F0Full;
-                int sce, mne, sco, mno;
-                if (qq == 0) {  // sub-blocks 0..3: low six bits of scale / min bytes
-                    sce = (int)(y1 & 63);
-                    sco = (int)((y1 >> 8) & 63);
-                    mne = (int)(z1 & 63);
-                    mno = (int)((z1 >> 8) & 63);
-                } else {  // sub-blocks 4..7: nibbles of bytes 8..11, high bits of 0..7
-                    sce = (int)((w1 & 0xF) | (((y1 >> 6) & 3) << 4));
-                    sco = (int)(((w1 >> 8) & 0xF) | (((y1 >> 14) & 3) << 4));
-                    mne = (int)(((w1 >> 4) & 0xF) | (((z1 >> 6) & 3) << 4));
-                    mno = (int)(((w1 >> 12) & 0xF) | (((z1 >> 14) & 3) << 4));
+    }
+    const int items = nact * parts;
+    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+        const int e = s_act[it / parts];
+        const int count = A.counts[e];
+        const int t0 = (it % parts) * A.tpw;
+        const int ntl = min(A.tpw, tiles - t0);
+        for (int c0 = 0; c0 < count; c0 += kChunk) {
+            const int nr = min(kChunk, count - c0);
+            __syncthreads();
+            if (threadIdx.x < kChunk) {
+                const int i = threadIdx.x;
+                if (i < nr) {
+                    const uint64_t o = (uint64_t)e * cap + c0 + i;
+                    const int row = A.arows[o], slot = A.aslots[o];
+                    s_out[i] = row * A.used + slot;
+                    s_row[i] = A.by_slot ? row * A.used + slot : row;
+                } else {  // padding rows read assignment 0 and are never stored
+                    const uint64_t o = (uint64_t)e * cap + c0;
+                    const int row = A.arows[o], slot = A.aslots[o];
+                    s_out[i] = -1;
+                    s_row[i] = A.by_slot ? row * A.used + slot : row;
                 }
-                const uint32_t qw[4] = {(uint32_t)qe, (uint32_t)(qe >> 32), (uint32_t)qo, (uint32_t)(qo >> 32)};
-                const uint32_t lo[2] = {(uint32_t)(sce & 7), (uint32_t)(sco & 7)};
-                const uint32_t hi[2] = {(uint32_t)(sce >> 3), (uint32_t)(sco >> 3)};
-                const i32x4 b_lo = {(int)bytes_times(qw[0], lo[0]), (int)bytes_times(qw[1], lo[0]),
-                                    (int)bytes_times(qw[2], lo[1]), (int)bytes_times(qw[3], lo[1])};
-                const i32x4 b_hi = {(int)bytes_times(qw[0], hi[0]), (int)bytes_times(qw[1], hi[0]),
-                                    (int)bytes_times(qw[2], hi[1]), (int)bytes_times(qw[3], hi[1])};
-                const int me = (int)__builtin_amdgcn_perm((uint32_t)mne, (uint32_t)mne, 0u);
-                const int mo = (int)__builtin_amdgcn_perm((uint32_t)mno, (uint32_t)mno, 0u);
-                const i32x4 b_mn = {me, me, mo, mo};
-                const i32x4 av = *reinterpret_cast<const i32x4 *>(la + moe_la_off(sb * 8 + 2 * jp, lc, 2 * (lg & 1) + hh));
-                alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_lo, alo, 0, 0, 0);
-                ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_hi, ahi, 0, 0, 0);
-                amn = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_mn, amn, 0, 0, 0);
             }
-            const float d = h2f((uint16_t)(H.x & 0xffffu)), dmin = h2f((uint16_t)(H.x >> 16));
+            __syncthreads();
+            YK_MOE_STAMP(1);
+            for (int idx = threadIdx.x; idx < nsub * 32; idx += kMoeThreads) {  // 16 B pieces of the planes
+                const int j = idx >> 5, r = (idx >> 1) & 15, half = idx & 1;
+                const int8_t *src = A.xq.planes + (uint64_t)s_row[r & 7] * A.K * 2 + (uint64_t)j * 64 +
+                                    (r >= 8 ? 32 : 0) + 16 * half;
+                const uint4 v = *reinterpret_cast<const uint4 *>(src);
+                // lane groups 2 half and 2 half + 1; sub-blocks 2 jp, 2 jp + 1 side by side
+                uint8_t *d0 = la + moe_la_off(j, r, 2 * half);
+                *reinterpret_cast<uint2 *>(d0) = make_uint2(v.x, v.y);
+                *reinterpret_cast<uint2 *>(d0 + 16) = make_uint2(v.z, v.w);
+            }
+            for (int idx = threadIdx.x; idx < nsb * 8; idx += kMoeThreads)
+                lxs[idx] = A.xq.scales[(uint64_t)s_row[idx & 7] * nsb + (idx >> 3)];
+            __syncthreads();
+            YK_MOE_STAMP(2);
+            // items (tile, matrix, super-block): wave w walks the pairs (tile,
+            // matrix) w, w + 8, ... through their super-blocks in order with the
+            // next item's weights in flight, sums in registers in super-block
+            // order, one result per pair to LDS
+            const int pairs = ntl * mats;
+            const int npw = wave < pairs ? (pairs - wave + kMoeWaves - 1) / kMoeWaves : 0;
+            const int total = npw * nsb;
+            const int rbase = 4 * (g & 1);
+            // quant bytes of an item: lane (c, g) loads 16 contiguous bytes per
+            // half of the block, [32 jp + 16 (g & 1), +16) with jp = 2 qq + (g >> 1),
+            // so each load covers 64 contiguous bytes of every channel; the
+            // activation operands below follow the same (sub-block, element)
+            // assignment (the MFMA sums over K in any order)
+            auto load_item = [&](int q, uint4 &H, uint4 (&Q)[2]) __attribute__((always_inline)) {
+                int oz;  // opaque zero: the lane's row address is rebuilt per item, not held (and spilled)
+                asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+                const int lc = c + oz, lg = g + oz;
+                const int tm = wave + kMoeWaves * (q / nsb), sb = q % nsb, m = tm % mats, tl = tm / mats;
+                const uint8_t *blk = (m ? A.w1 : A.w0) + ((uint64_t)e * A.N + (t0 + tl) * 16 + lc) * A.row_bytes +
+                                     (uint64_t)sb * 144;
+                H = *reinterpret_cast<const uint4 *>(blk);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                // this lane's plane (rows 0..7 high, 8..15 low); the planes
-                // are combined once per pair
-                const float v = d * (float)(alo[i] + 8 * ahi[i]) - dmin * (float)amn[i];
-                acc[i] += xs[i] * v;
-            }
-            if (sb == nsb - 1) {  // the pair's last super-block: its result to LDS
-                const int tm = wave + kMoeWaves * (q / nsb);
-                float *dst = part + (uint64_t)tm * 128;
+                for (int qq = 0; qq < 2; qq++)
+                    Q[qq] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * (2 * qq + (lg >> 1)) + 16 * (lg & 1));
+            };
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+            auto compute_item = [&](int q, const uint4 &H, const uint4 (&Q)[2]) __attribute__((always_inline)) {
+                const int sb = q % nsb;
+                const float4 xs4 = *reinterpret_cast<const float4 *>(lxs + sb * 8 + rbase);
+                const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+                // sub-block scale (two 3-bit digits) and min in the B operands
+                // of three K = 64 MFMAs per pair of sub-blocks: exact int32
+                i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
+                // this lane's scale bytes: sub-blocks 2 jp, 2 jp + 1 of jp = 2 qq + b
+                // sit in bytes 2 b, 2 b + 1 of each scale word (getScaleMinK4 layout)
+                int oz;  // opaque zero: lane-derived offsets are rebuilt per item
+                asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+                const int lc = c + oz, lg = g + oz, b = lg >> 1;
+                const uint32_t y1 = H.y >> (16 * b), z1 = H.z >> (16 * b), w1 = H.w >> (16 * b);
+#pragma unroll
+                for (int mi = 0; mi < 4; mi++) {
+                    const int qq = mi >> 1, hh = mi & 1, jp = 2 * qq + b;
+                    const uint64_t raw = hh ? ((uint64_t)Q[qq].z | ((uint64_t)Q[qq].w << 32))
+                                            : ((uint64_t)Q[qq].x | ((uint64_t)Q[qq].y << 32));
+                    const uint64_t qe = raw & 0x0F0F0F0F0F0F0F0Full, qo = (raw >> 4) & 0x0F0F0F0F0F0F0F0Full;
+                    int sce, mne, sco, mno;
+                    if (qq == 0) {  // sub-blocks 0..3: low six bits of scale / min bytes
+                        sce = (int)(y1 & 63);
+                        sco = (int)((y1 >> 8) & 63);
+                        mne = (int)(z1 & 63);
+                        mno = (int)((z1 >> 8) & 63);
+                    } else {  // sub-blocks 4..7: nibbles of bytes 8..11, high bits of 0..7
+                        sce = (int)((w1 & 0xF) | (((y1 >> 6) & 3) << 4));
+                        sco = (int)(((w1 >> 8) & 0xF) | (((y1 >> 14) & 3) << 4));
+                        mne = (int)(((w1 >> 4) & 0xF) | (((z1 >> 6) & 3) << 4));
+                        mno = (int)(((w1 >> 12) & 0xF) | (((z1 >> 14) & 3) << 4));
+                    }
+                    const uint32_t qw[4] = {(uint32_t)qe, (uint32_t)(qe >> 32), (uint32_t)qo, (uint32_t)(qo >> 32)};
+                    const uint32_t lo[2] = {(uint32_t)(sce & 7), (uint32_t)(sco & 7)};
+                    const uint32_t hi[2] = {(uint32_t)(sce >> 3), (uint32_t)(sco >> 3)};
+                    const i32x4 b_lo = {(int)bytes_times(qw[0], lo[0]), (int)bytes_times(qw[1], lo[0]),
+                                        (int)bytes_times(qw[2], lo[1]), (int)bytes_times(qw[3], lo[1])};
+                    const i32x4 b_hi = {(int)bytes_times(qw[0], hi[0]), (int)bytes_times(qw[1], hi[0]),
+                                        (int)bytes_times(qw[2], hi[1]), (int)bytes_times(qw[3], hi[1])};
+                    const int me = (int)__builtin_amdgcn_perm((uint32_t)mne, (uint32_t)mne, 0u);
+                    const int mo = (int)__builtin_amdgcn_perm((uint32_t)mno, (uint32_t)mno, 0u);
+                    const i32x4 b_mn = {me, me, mo, mo};
+                    const i32x4 av =
+                        *reinterpret_cast<const i32x4 *>(la + moe_la_off(sb * 8 + 2 * jp, lc, 2 * (lg & 1) + hh));
+                    alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_lo, alo, 0, 0, 0);
+                    ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_hi, ahi, 0, 0, 0);
+                    amn = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_mn, amn, 0, 0, 0);
+                }
+                const float d = h2f((uint16_t)(H.x & 0xffffu)), dmin = h2f((uint16_t)(H.x >> 16));
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const float lo = __shfl_xor(acc[i], 32);
-                    if (g < 2) dst[(4 * g + i) * 16 + c] = fmaf(256.f, acc[i], lo);
-                    acc[i] = 0.f;
+                    // this lane's plane (rows 0..7 high, 8..15 low); the planes
+                    // are combined once per pair
+                    const float v = d * (float)(alo[i] + 8 * ahi[i]) - dmin * (float)amn[i];
+                    acc[i] += xs[i] * v;
+                }
+                if (sb == nsb - 1) {  // the pair's last super-block: its result to LDS
+                    const int tm = wave + kMoeWaves * (q / nsb);
+                    float *dst = part + (uint64_t)tm * 128;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float lo = __shfl_xor(acc[i], 32);
+                        if (g < 2) dst[(4 * g + i) * 16 + c] = fmaf(256.f, acc[i], lo);
+                        acc[i] = 0.f;
+                    }
+                }
+            };
+            uint4 h0, h1;
+            uint4 q0[2], q1[2];
+            if (total > 0) load_item(0, h0, q0);
+            if (total > 1) load_item(1, h1, q1);
+            for (int q = 0; q < total; q += 2) {
+                compute_item(q, h0, q0);
+                if (q + 2 < total) load_item(q + 2, h0, q0);
+                if (q + 1 < total) {
+                    compute_item(q + 1, h1, q1);
+                    if (q + 3 < total) load_item(q + 3, h1, q1);
                 }
             }
-        };
-        uint4 h0, h1;
-        uint4 q0[2], q1[2];
-        if (total > 0) load_item(0, h0, q0);
-        if (total > 1) load_item(1, h1, q1);
-        for (int q = 0; q < total; q += 2) {
-            compute_item(q, h0, q0);
-            if (q + 2 < total) load_item(q + 2, h0, q0);
-            if (q + 1 < total) {
-                compute_item(q + 1, h1, q1);
-                if (q + 3 < total) load_item(q + 3, h1, q1);
-            }
-        }
-        YK_MOE_STAMP(3);
-        __syncthreads();
-        // the epilogue
-        for (int o = threadIdx.x; o < ntl * nr * 16; o += kMoeThreads) {
-            const int tl = o / (nr * 16), rem = o % (nr * 16), i = rem / 16, cc = rem % 16;
-            float y[2] = {0.f, 0.f};
-            for (int m = 0; m < mats; m++) y[m] = part[(uint64_t)(tl * mats + m) * 128 + i * 16 + cc];
-            const uint64_t dst = (uint64_t)s_out[i] * A.N + (t0 + tl) * 16 + cc;
-            if (A.swiglu) {
-                A.out0[dst] = __fmul_rn(silu_ref(y[0]), y[1]);
-            } else {
-                A.out0[dst] = y[0];
-                if (dual) A.out1[dst] = y[1];
+            YK_MOE_STAMP(3);
+            __syncthreads();
+            // the epilogue
+            for (int o = threadIdx.x; o < ntl * nr * 16; o += kMoeThreads) {
+                const int tl = o / (nr * 16), rem = o % (nr * 16), i = rem / 16, cc = rem % 16;
+                float y[2] = {0.f, 0.f};
+                for (int m = 0; m < mats; m++) y[m] = part[(uint64_t)(tl * mats + m) * 128 + i * 16 + cc];
+                const uint64_t dst = (uint64_t)s_out[i] * A.N + (t0 + tl) * 16 + cc;
+                if (A.swiglu) {
+                    A.out0[dst] = __fmul_rn(silu_ref(y[0]), y[1]);
+                } else {
+                    A.out0[dst] = y[0];
+                    if (dual) A.out1[dst] = y[1];
+                }
             }
         }
     }
@@ -626,6 +649,7 @@ hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
     a.swiglu = g.swiglu;
     a.out0 = g.out0;
     a.out1 = g.out1;
+    if (g.experts > kMoeMaxExperts) return hipErrorInvalidValue;
     const int nsb = g.K / 256, mats = g.w1 ? 2 : 1, tiles = g.N / 16;
     // tiles per workgroup: as many as keep nsb * mats * tpw items near 64
     // (enough workgroups in flight; each wave walks a few pairs)
@@ -636,7 +660,23 @@ hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
     const uint32_t lds = (uint32_t)tpw * mats * 512 + (uint32_t)(g.K / 32) * (16 * 32) + (uint32_t)nsb * 32;
     const int units = act_rows * nsb;
     moe_quant_kernel<<<(units + 3) / 4, 256, 0, s>>>(g.x, act_rows, g.K, a.xq);
-    moe_gemm_kernel<<<dim3((unsigned)g.experts, (unsigned)((tiles + tpw - 1) / tpw)), kMoeThreads, lds, s>>>(a);
+    // a persistent grid of the resident workgroups (the kernel deals the
+    // active experts' items over it)
+    static int per_cu = 0, cus = 0;
+    static uint32_t per_cu_lds = ~0u;
+    if (per_cu_lds != lds) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 1;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(moe_gemm_kernel),
+                                                         kMoeThreads, lds) != hipSuccess || per_cu <= 0)
+            per_cu = 1;
+        per_cu_lds = lds;
+    }
+    const int parts = (tiles + tpw - 1) / tpw;
+    const unsigned grid = (unsigned)std::min<int64_t>((int64_t)g.experts * parts, (int64_t)per_cu * cus);
+    moe_gemm_kernel<<<grid, kMoeThreads, lds, s>>>(a);
     return hipGetLastError();
 }
 
