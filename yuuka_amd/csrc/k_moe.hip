@@ -275,7 +275,7 @@ __global__ __launch_bounds__(256) void moe_bin_kernel(const int32_t *__restrict_
 
 // ---------------------------------------------------------------- grouped GEMM
 // Activation rows quantized once per launch into scratch (moe_quant_kernel):
-//   planes [rows][K/32 sub-blocks][2: high, low][32 B]
+//   planes [rows][2: high, low][K/64][4][16 B] (moe_quant_kernel's order)
 //   scales [rows][K/256]  float (x ~= scale * q, q = 256 h + l)
 struct MoeQuant {
     int8_t *planes;
@@ -309,10 +309,13 @@ __global__ __launch_bounds__(256) void moe_quant_kernel(const float *__restrict_
         hp |= (uint32_t)(h & 0xff) << (8 * t);
         lp |= (uint32_t)(l & 0xff) << (8 * t);
     }
-    const int j = lane >> 3, o = 4 * (lane & 7);
-    int8_t *dst = q.planes + (uint64_t)row * K * 2 + (uint64_t)(sb * 8 + j) * 64 + o;
+    // row layout: [plane][K/64 groups J][lane group gg][16 B], the 16 bytes
+    // being bytes [8 gg, +8) of sub-blocks 2 J and 2 J + 1: the grouped
+    // GEMM's LDS tile order, so it stages whole 16-byte pieces
+    const int js = sb * 8 + (lane >> 3), o = 4 * (lane & 7);
+    int8_t *dst = q.planes + (uint64_t)row * K * 2 + (uint64_t)(js >> 1) * 64 + (o >> 3) * 16 + (js & 1) * 8 + (o & 7);
     *reinterpret_cast<uint32_t *>(dst) = hp;
-    *reinterpret_cast<uint32_t *>(dst + 32) = lp;
+    *reinterpret_cast<uint32_t *>(dst + K) = lp;
     if (lane == 0) q.scales[(uint64_t)row * nsb + sb] = m > 0.f ? m / (float)kQMax : 0.f;
 }
 
@@ -359,7 +362,21 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s1, uint32_t s2, ui
     }
 }
 
-// Workgroup (expert e, part): tiles [t0, t0 + tpw) of 16 output channels.
+// Global -> LDS copies of one lane (lane l writes [m0 + 16 l, +16) or
+// [m0 + 4 l, +4)), as inline assembly so that the compiler's wait counts
+// do not see them (they would make every weight wait also wait for the
+// copies); the kernel waits for them itself before a barrier.
+__device__ __forceinline__ void lds_copy16(const void *src, const void *lds_dst) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_dst);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4(const void *src, const void *lds_dst) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_dst);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void vmem_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Item (expert e, part): tiles [t0, t0 + tpw) of 16 output channels.
 // Per chunk of up to eight assignments, each wave walks its (tile, matrix)
 // pairs through the super-blocks in order (sums in registers, the next
 // item's weights in flight; deterministic), one result per pair to LDS for
@@ -382,15 +399,18 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
     // plane of assignment r, r >= 8 low plane of assignment r - 8), scales
     // [K/256][8] float.
     extern __shared__ __attribute__((aligned(16))) float part[];
-    const int nsb = A.K / 256, nsub = A.K / 32;
+    const int nsb = A.K / 256;
     const int tiles = A.N / 16;
     const int parts = (tiles + A.tpw - 1) / A.tpw;
     const bool dual = A.w1 != nullptr;
     const int mats = dual ? 2 : 1;
-    __shared__ int s_row[kChunk], s_out[kChunk];
     __shared__ int s_act[kMoeMaxExperts], s_wtot[kMoeWaves];
+    // assignment metadata of three tasks (current, next, the one after):
+    // [0, 8) rows, [8, 16) slots, [16] the expert's count
+    __shared__ __attribute__((aligned(16))) int s_meta[3][32];
+    const uint32_t la_bytes = (uint32_t)A.K * 16;  // one task's planes: K/64 groups of 1 KB
     uint8_t *la = reinterpret_cast<uint8_t *>(part + (uint64_t)A.tpw * mats * 128);
-    float *lxs = reinterpret_cast<float *>(la + (uint64_t)nsub * 16 * 32);
+    float *lxs = reinterpret_cast<float *>(la + 2 * (uint64_t)la_bytes);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = lane & 15, g = lane >> 4;
     const uint64_t cap = (uint64_t)A.rows * A.used;
@@ -414,164 +434,209 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
         __syncthreads();
     }
     const int items = nact * parts;
-    for (int it = blockIdx.x; it < items; it += gridDim.x) {
-        const int e = s_act[it / parts];
-        const int count = A.counts[e];
-        const int t0 = (it % parts) * A.tpw;
-        const int ntl = min(A.tpw, tiles - t0);
-        for (int c0 = 0; c0 < count; c0 += kChunk) {
-            const int nr = min(kChunk, count - c0);
-            __syncthreads();
-            if (threadIdx.x < kChunk) {
-                const int i = threadIdx.x;
-                if (i < nr) {
-                    const uint64_t o = (uint64_t)e * cap + c0 + i;
-                    const int row = A.arows[o], slot = A.aslots[o];
-                    s_out[i] = row * A.used + slot;
-                    s_row[i] = A.by_slot ? row * A.used + slot : row;
-                } else {  // padding rows read assignment 0 and are never stored
-                    const uint64_t o = (uint64_t)e * cap + c0;
-                    const int row = A.arows[o], slot = A.aslots[o];
-                    s_out[i] = -1;
-                    s_row[i] = A.by_slot ? row * A.used + slot : row;
-                }
-            }
-            __syncthreads();
-            YK_MOE_STAMP(1);
-            for (int idx = threadIdx.x; idx < nsub * 32; idx += kMoeThreads) {  // 16 B pieces of the planes
-                const int j = idx >> 5, r = (idx >> 1) & 15, half = idx & 1;
-                const int8_t *src = A.xq.planes + (uint64_t)s_row[r & 7] * A.K * 2 + (uint64_t)j * 64 +
-                                    (r >= 8 ? 32 : 0) + 16 * half;
-                const uint4 v = *reinterpret_cast<const uint4 *>(src);
-                // lane groups 2 half and 2 half + 1; sub-blocks 2 jp, 2 jp + 1 side by side
-                uint8_t *d0 = la + moe_la_off(j, r, 2 * half);
-                *reinterpret_cast<uint2 *>(d0) = make_uint2(v.x, v.y);
-                *reinterpret_cast<uint2 *>(d0 + 16) = make_uint2(v.z, v.w);
-            }
-            for (int idx = threadIdx.x; idx < nsb * 8; idx += kMoeThreads)
-                lxs[idx] = A.xq.scales[(uint64_t)s_row[idx & 7] * nsb + (idx >> 3)];
-            __syncthreads();
-            YK_MOE_STAMP(2);
-            // items (tile, matrix, super-block): wave w walks the pairs (tile,
-            // matrix) w, w + 8, ... through their super-blocks in order with the
-            // next item's weights in flight, sums in registers in super-block
-            // order, one result per pair to LDS
-            const int pairs = ntl * mats;
-            const int npw = wave < pairs ? (pairs - wave + kMoeWaves - 1) / kMoeWaves : 0;
-            const int total = npw * nsb;
-            const int rbase = 4 * (g & 1);
-            // quant bytes of an item: lane (c, g) loads 16 contiguous bytes per
-            // half of the block, [32 jp + 16 (g & 1), +16) with jp = 2 qq + (g >> 1),
-            // so each load covers 64 contiguous bytes of every channel; the
-            // activation operands below follow the same (sub-block, element)
-            // assignment (the MFMA sums over K in any order)
-            auto load_item = [&](int q, uint4 &H, uint4 (&Q)[2]) __attribute__((always_inline)) {
-                int oz;  // opaque zero: the lane's row address is rebuilt per item, not held (and spilled)
-                asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
-                const int lc = c + oz, lg = g + oz;
-                const int tm = wave + kMoeWaves * (q / nsb), sb = q % nsb, m = tm % mats, tl = tm / mats;
-                const uint8_t *blk = (m ? A.w1 : A.w0) + ((uint64_t)e * A.N + (t0 + tl) * 16 + lc) * A.row_bytes +
-                                     (uint64_t)sb * 144;
-                H = *reinterpret_cast<const uint4 *>(blk);
+    if ((int)blockIdx.x >= items) return;  // workgroup-uniform
+
+    // A task is one chunk (up to kChunk assignments) of one of this
+    // workgroup's items: item k is blockIdx.x + k * gridDim.x. Task t's
+    // planes and scales sit in LDS buffer t & 1, its metadata in slot t % 3;
+    // task t + 1's planes and task t + 2's metadata are copied into LDS
+    // (global_load_lds, outside the compiler's wait counts) while task t
+    // streams its weights, and every wave waits for its own copies (vmcnt 0)
+    // before the barrier that ends task t.
+    auto item_of = [&](int k) { return (int)blockIdx.x + k * (int)gridDim.x; };
+    auto expert_of = [&](int k) { return s_act[item_of(k) / parts]; };
+    auto meta_issue = [&](int k, int c0, int slot) __attribute__((always_inline)) {
+        if (wave == 0 && lane < 17) {
+            const int e = expert_of(k);
+            const uint64_t b = (uint64_t)e * cap;
+            const int32_t *src = lane < 8    ? A.arows + b + min((uint64_t)(c0 + lane), cap - 1)
+                                 : lane < 16 ? A.aslots + b + min((uint64_t)(c0 + lane - 8), cap - 1)
+                                             : A.counts + e;
+            lds_copy4(src, &s_meta[slot][0]);
+        }
+    };
+    // activation row of assignment i of a task (padding rows repeat the
+    // chunk's first assignment and are never stored)
+    auto act_row = [&](const int *mt, int c0, int i) __attribute__((always_inline)) {
+        const int j = c0 + i < mt[16] ? i : 0;
+        return A.by_slot ? mt[j] * A.used + mt[8 + j] : mt[j];
+    };
+    auto stage_issue = [&](int c0, int slot, int buf) __attribute__((always_inline)) {
+        const int *mt = s_meta[slot];
+        uint8_t *dst = la + (uint64_t)buf * la_bytes;
+        {   // planes: lane l of group J copies MFMA row l >> 2, lane group l & 3
+            const int r = lane >> 2, gg = lane & 3;
+            const int8_t *src = A.xq.planes + (uint64_t)act_row(mt, c0, r & 7) * A.K * 2 + (r >= 8 ? A.K : 0) + gg * 16;
+            for (int J = wave; J < A.K / 64; J += kMoeWaves) lds_copy16(src + J * 64, dst + J * 1024);
+        }
+        float *xd = lxs + (uint64_t)buf * nsb * 8;  // scales [K/256][8]
+        for (int b = wave; b * 64 < nsb * 8; b += kMoeWaves) {
+            const int idx = b * 64 + lane;
+            if (idx < nsb * 8) lds_copy4(A.xq.scales + (uint64_t)act_row(mt, c0, idx & 7) * nsb + (idx >> 3), xd + b * 64);
+        }
+    };
+    auto next_task = [&](int k, int c0, int count, int &nk, int &nc0) __attribute__((always_inline)) {
+        if (c0 + kChunk < count) {
+            nk = k;
+            nc0 = c0 + kChunk;
+        } else {
+            nk = k + 1;
+            nc0 = 0;
+        }
+    };
+
+    // task 0: metadata, then its planes with task 1's metadata
+    int k = 0, c0 = 0;
+    meta_issue(0, 0, 0);
+    vmem_wait_all();
+    __syncthreads();
+    int k1, c1;
+    next_task(0, 0, s_meta[0][16], k1, c1);
+    if (item_of(k1) < items) meta_issue(k1, c1, 1);
+    stage_issue(0, 0, 0);
+    vmem_wait_all();
+    __syncthreads();
+    for (int t = 0;; t++) {
+        YK_MOE_STAMP(1);
+        const int slot = t % 3, buf = t & 1;
+        const int *mt = s_meta[slot];
+        const int count = mt[16], nr = min(kChunk, count - c0);
+        const int e = expert_of(k), t0 = (item_of(k) % parts) * A.tpw, ntl = min(A.tpw, tiles - t0);
+        // the next task's planes, and the metadata of the one after it
+        if (item_of(k1) < items) {
+            int k2, c2;
+            stage_issue(c1, (t + 1) % 3, buf ^ 1);
+            next_task(k1, c1, s_meta[(t + 1) % 3][16], k2, c2);
+            if (item_of(k2) < items) meta_issue(k2, c2, (t + 2) % 3);
+        }
+        const uint8_t *lat = la + (uint64_t)buf * la_bytes;
+        const float *lxt = lxs + (uint64_t)buf * nsb * 8;
+        YK_MOE_STAMP(2);
+        // items (tile, matrix, super-block): wave w walks the pairs (tile,
+        // matrix) w, w + 8, ... through their super-blocks in order with the
+        // next item's weights in flight, sums in registers in super-block
+        // order, one result per pair to LDS
+        const int pairs = ntl * mats;
+        const int npw = wave < pairs ? (pairs - wave + kMoeWaves - 1) / kMoeWaves : 0;
+        const int total = npw * nsb;
+        const int rbase = 4 * (g & 1);
+        // quant bytes of an item: lane (c, g) loads 16 contiguous bytes per
+        // half of the block, [32 jp + 16 (g & 1), +16) with jp = 2 qq + (g >> 1),
+        // so each load covers 64 contiguous bytes of every channel; the
+        // activation operands below follow the same (sub-block, element)
+        // assignment (the MFMA sums over K in any order)
+        auto load_item = [&](int q, uint4 &H, uint4 (&Q)[2]) __attribute__((always_inline)) {
+            int oz;  // opaque zero: the lane's row address is rebuilt per item, not held (and spilled)
+            asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+            const int lc = c + oz, lg = g + oz;
+            const int tm = wave + kMoeWaves * (q / nsb), sb = q % nsb, m = tm % mats, tl = tm / mats;
+            const uint8_t *blk = (m ? A.w1 : A.w0) + ((uint64_t)e * A.N + (t0 + tl) * 16 + lc) * A.row_bytes +
+                                 (uint64_t)sb * 144;
+            H = *reinterpret_cast<const uint4 *>(blk);
 #pragma unroll
-                for (int qq = 0; qq < 2; qq++)
-                    Q[qq] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * (2 * qq + (lg >> 1)) + 16 * (lg & 1));
-            };
-            float acc[4] = {0.f, 0.f, 0.f, 0.f};
-            auto compute_item = [&](int q, const uint4 &H, const uint4 (&Q)[2]) __attribute__((always_inline)) {
-                const int sb = q % nsb;
-                const float4 xs4 = *reinterpret_cast<const float4 *>(lxs + sb * 8 + rbase);
-                const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
-                // sub-block scale (two 3-bit digits) and min in the B operands
-                // of three K = 64 MFMAs per pair of sub-blocks: exact int32
-                i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
-                // this lane's scale bytes: sub-blocks 2 jp, 2 jp + 1 of jp = 2 qq + b
-                // sit in bytes 2 b, 2 b + 1 of each scale word (getScaleMinK4 layout)
-                int oz;  // opaque zero: lane-derived offsets are rebuilt per item
-                asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
-                const int lc = c + oz, lg = g + oz, b = lg >> 1;
-                const uint32_t y1 = H.y >> (16 * b), z1 = H.z >> (16 * b), w1 = H.w >> (16 * b);
+            for (int qq = 0; qq < 2; qq++)
+                Q[qq] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * (2 * qq + (lg >> 1)) + 16 * (lg & 1));
+        };
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        auto compute_item = [&](int q, const uint4 &H, const uint4 (&Q)[2]) __attribute__((always_inline)) {
+            const int sb = q % nsb;
+            const float4 xs4 = *reinterpret_cast<const float4 *>(lxt + sb * 8 + rbase);
+            const float xs[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+            // sub-block scale (two 3-bit digits) and min in the B operands
+            // of three K = 64 MFMAs per pair of sub-blocks: exact int32
+            i32x4 alo = {0, 0, 0, 0}, ahi = {0, 0, 0, 0}, amn = {0, 0, 0, 0};
+            // this lane's scale bytes: sub-blocks 2 jp, 2 jp + 1 of jp = 2 qq + b
+            // sit in bytes 2 b, 2 b + 1 of each scale word (getScaleMinK4 layout)
+            int oz;  // opaque zero: lane-derived offsets are rebuilt per item
+            asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
+            const int lc = c + oz, lg = g + oz, b = lg >> 1;
+            const uint32_t y1 = H.y >> (16 * b), z1 = H.z >> (16 * b), w1 = H.w >> (16 * b);
 #pragma unroll
-                for (int mi = 0; mi < 4; mi++) {
-                    const int qq = mi >> 1, hh = mi & 1, jp = 2 * qq + b;
-                    const uint64_t raw = hh ? ((uint64_t)Q[qq].z | ((uint64_t)Q[qq].w << 32))
-                                            : ((uint64_t)Q[qq].x | ((uint64_t)Q[qq].y << 32));
-                    const uint64_t qe = raw & 0x0F0F0F0F0F0F0F0Full, qo = (raw >> 4) & 0x0F0F0F0F0F0F0F0Full;
-                    int sce, mne, sco, mno;
-                    if (qq == 0) {  // sub-blocks 0..3: low six bits of scale / min bytes
-                        sce = (int)(y1 & 63);
-                        sco = (int)((y1 >> 8) & 63);
-                        mne = (int)(z1 & 63);
-                        mno = (int)((z1 >> 8) & 63);
-                    } else {  // sub-blocks 4..7: nibbles of bytes 8..11, high bits of 0..7
-                        sce = (int)((w1 & 0xF) | (((y1 >> 6) & 3) << 4));
-                        sco = (int)(((w1 >> 8) & 0xF) | (((y1 >> 14) & 3) << 4));
-                        mne = (int)(((w1 >> 4) & 0xF) | (((z1 >> 6) & 3) << 4));
-                        mno = (int)(((w1 >> 12) & 0xF) | (((z1 >> 14) & 3) << 4));
-                    }
-                    const uint32_t qw[4] = {(uint32_t)qe, (uint32_t)(qe >> 32), (uint32_t)qo, (uint32_t)(qo >> 32)};
-                    const uint32_t lo[2] = {(uint32_t)(sce & 7), (uint32_t)(sco & 7)};
-                    const uint32_t hi[2] = {(uint32_t)(sce >> 3), (uint32_t)(sco >> 3)};
-                    const i32x4 b_lo = {(int)bytes_times(qw[0], lo[0]), (int)bytes_times(qw[1], lo[0]),
-                                        (int)bytes_times(qw[2], lo[1]), (int)bytes_times(qw[3], lo[1])};
-                    const i32x4 b_hi = {(int)bytes_times(qw[0], hi[0]), (int)bytes_times(qw[1], hi[0]),
-                                        (int)bytes_times(qw[2], hi[1]), (int)bytes_times(qw[3], hi[1])};
-                    const int me = (int)__builtin_amdgcn_perm((uint32_t)mne, (uint32_t)mne, 0u);
-                    const int mo = (int)__builtin_amdgcn_perm((uint32_t)mno, (uint32_t)mno, 0u);
-                    const i32x4 b_mn = {me, me, mo, mo};
-                    const i32x4 av =
-                        *reinterpret_cast<const i32x4 *>(la + moe_la_off(sb * 8 + 2 * jp, lc, 2 * (lg & 1) + hh));
-                    alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_lo, alo, 0, 0, 0);
-                    ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_hi, ahi, 0, 0, 0);
-                    amn = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_mn, amn, 0, 0, 0);
+            for (int mi = 0; mi < 4; mi++) {
+                const int qq = mi >> 1, hh = mi & 1, jp = 2 * qq + b;
+                const uint64_t raw = hh ? ((uint64_t)Q[qq].z | ((uint64_t)Q[qq].w << 32))
+                                        : ((uint64_t)Q[qq].x | ((uint64_t)Q[qq].y << 32));
+                const uint64_t qe = raw & 0x0F0F0F0F0F0F0F0Full, qo = (raw >> 4) & 0x0F0F0F0F0F0F0F0Full;
+                int sce, mne, sco, mno;
+                if (qq == 0) {  // sub-blocks 0..3: low six bits of scale / min bytes
+                    sce = (int)(y1 & 63);
+                    sco = (int)((y1 >> 8) & 63);
+                    mne = (int)(z1 & 63);
+                    mno = (int)((z1 >> 8) & 63);
+                } else {  // sub-blocks 4..7: nibbles of bytes 8..11, high bits of 0..7
+                    sce = (int)((w1 & 0xF) | (((y1 >> 6) & 3) << 4));
+                    sco = (int)(((w1 >> 8) & 0xF) | (((y1 >> 14) & 3) << 4));
+                    mne = (int)(((w1 >> 4) & 0xF) | (((z1 >> 6) & 3) << 4));
+                    mno = (int)(((w1 >> 12) & 0xF) | (((z1 >> 14) & 3) << 4));
                 }
-                const float d = h2f((uint16_t)(H.x & 0xffffu)), dmin = h2f((uint16_t)(H.x >> 16));
+                const uint32_t qw[4] = {(uint32_t)qe, (uint32_t)(qe >> 32), (uint32_t)qo, (uint32_t)(qo >> 32)};
+                const uint32_t lo[2] = {(uint32_t)(sce & 7), (uint32_t)(sco & 7)};
+                const uint32_t hi[2] = {(uint32_t)(sce >> 3), (uint32_t)(sco >> 3)};
+                const i32x4 b_lo = {(int)bytes_times(qw[0], lo[0]), (int)bytes_times(qw[1], lo[0]),
+                                    (int)bytes_times(qw[2], lo[1]), (int)bytes_times(qw[3], lo[1])};
+                const i32x4 b_hi = {(int)bytes_times(qw[0], hi[0]), (int)bytes_times(qw[1], hi[0]),
+                                    (int)bytes_times(qw[2], hi[1]), (int)bytes_times(qw[3], hi[1])};
+                const int me = (int)__builtin_amdgcn_perm((uint32_t)mne, (uint32_t)mne, 0u);
+                const int mo = (int)__builtin_amdgcn_perm((uint32_t)mno, (uint32_t)mno, 0u);
+                const i32x4 b_mn = {me, me, mo, mo};
+                const i32x4 av =
+                    *reinterpret_cast<const i32x4 *>(lat + moe_la_off(sb * 8 + 2 * jp, lc, 2 * (lg & 1) + hh));
+                alo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_lo, alo, 0, 0, 0);
+                ahi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_hi, ahi, 0, 0, 0);
+                amn = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, b_mn, amn, 0, 0, 0);
+            }
+            const float d = h2f((uint16_t)(H.x & 0xffffu)), dmin = h2f((uint16_t)(H.x >> 16));
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                // this lane's plane (rows 0..7 high, 8..15 low); the planes
+                // are combined once per pair
+                const float v = d * (float)(alo[i] + 8 * ahi[i]) - dmin * (float)amn[i];
+                acc[i] += xs[i] * v;
+            }
+            if (sb == nsb - 1) {  // the pair's last super-block: its result to LDS
+                const int tm = wave + kMoeWaves * (q / nsb);
+                float *dst = part + (uint64_t)tm * 128;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    // this lane's plane (rows 0..7 high, 8..15 low); the planes
-                    // are combined once per pair
-                    const float v = d * (float)(alo[i] + 8 * ahi[i]) - dmin * (float)amn[i];
-                    acc[i] += xs[i] * v;
-                }
-                if (sb == nsb - 1) {  // the pair's last super-block: its result to LDS
-                    const int tm = wave + kMoeWaves * (q / nsb);
-                    float *dst = part + (uint64_t)tm * 128;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float lo = __shfl_xor(acc[i], 32);
-                        if (g < 2) dst[(4 * g + i) * 16 + c] = fmaf(256.f, acc[i], lo);
-                        acc[i] = 0.f;
-                    }
-                }
-            };
-            uint4 h0, h1;
-            uint4 q0[2], q1[2];
-            if (total > 0) load_item(0, h0, q0);
-            if (total > 1) load_item(1, h1, q1);
-            for (int q = 0; q < total; q += 2) {
-                compute_item(q, h0, q0);
-                if (q + 2 < total) load_item(q + 2, h0, q0);
-                if (q + 1 < total) {
-                    compute_item(q + 1, h1, q1);
-                    if (q + 3 < total) load_item(q + 3, h1, q1);
+                    const float lo = __shfl_xor(acc[i], 32);
+                    if (g < 2) dst[(4 * g + i) * 16 + c] = fmaf(256.f, acc[i], lo);
+                    acc[i] = 0.f;
                 }
             }
-            YK_MOE_STAMP(3);
-            __syncthreads();
-            // the epilogue
-            for (int o = threadIdx.x; o < ntl * nr * 16; o += kMoeThreads) {
-                const int tl = o / (nr * 16), rem = o % (nr * 16), i = rem / 16, cc = rem % 16;
-                float y[2] = {0.f, 0.f};
-                for (int m = 0; m < mats; m++) y[m] = part[(uint64_t)(tl * mats + m) * 128 + i * 16 + cc];
-                const uint64_t dst = (uint64_t)s_out[i] * A.N + (t0 + tl) * 16 + cc;
-                if (A.swiglu) {
-                    A.out0[dst] = __fmul_rn(silu_ref(y[0]), y[1]);
-                } else {
-                    A.out0[dst] = y[0];
-                    if (dual) A.out1[dst] = y[1];
-                }
+        };
+        uint4 h0, h1;
+        uint4 q0[2], q1[2];
+        if (total > 0) load_item(0, h0, q0);
+        if (total > 1) load_item(1, h1, q1);
+        for (int q = 0; q < total; q += 2) {
+            compute_item(q, h0, q0);
+            if (q + 2 < total) load_item(q + 2, h0, q0);
+            if (q + 1 < total) {
+                compute_item(q + 1, h1, q1);
+                if (q + 3 < total) load_item(q + 3, h1, q1);
             }
         }
+        YK_MOE_STAMP(3);
+        __syncthreads();
+        // the epilogue
+        for (int o = threadIdx.x; o < ntl * nr * 16; o += kMoeThreads) {
+            const int tl = o / (nr * 16), rem = o % (nr * 16), i = rem / 16, cc = rem % 16;
+            float y[2] = {0.f, 0.f};
+            for (int m = 0; m < mats; m++) y[m] = part[(uint64_t)(tl * mats + m) * 128 + i * 16 + cc];
+            const uint64_t dst = (uint64_t)(mt[i] * A.used + mt[8 + i]) * A.N + (t0 + tl) * 16 + cc;
+            if (A.swiglu) {
+                A.out0[dst] = __fmul_rn(silu_ref(y[0]), y[1]);
+            } else {
+                A.out0[dst] = y[0];
+                if (dual) A.out1[dst] = y[1];
+            }
+        }
+        vmem_wait_all();
+        __syncthreads();
+        if (item_of(k1) >= items) break;
+        k = k1;
+        c0 = c1;
+        next_task(k, c0, s_meta[(t + 1) % 3][16], k1, c1);
     }
 #ifdef YK_MOE_TIMING
     YK_MOE_STAMP(4);
@@ -657,7 +722,8 @@ hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
     tpw = std::max(1, std::min(tpw, 16));
     tpw = std::min(tpw, tiles);
     a.tpw = tpw;
-    const uint32_t lds = (uint32_t)tpw * mats * 512 + (uint32_t)(g.K / 32) * (16 * 32) + (uint32_t)nsb * 32;
+    // results, two buffers of planes (K/64 groups of 1 KB) and of scales
+    const uint32_t lds = (uint32_t)tpw * mats * 512 + 2 * (uint32_t)g.K * 16 + 2 * (uint32_t)nsb * 32;
     const int units = act_rows * nsb;
     moe_quant_kernel<<<(units + 3) / 4, 256, 0, s>>>(g.x, act_rows, g.K, a.xq);
     // a persistent grid of the resident workgroups (the kernel deals the
