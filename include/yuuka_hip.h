@@ -487,6 +487,20 @@ YUUKA_API yuuka_status yuuka_verify_accept_noalloc(yuuka_stream * stream,
 /* On MOE_GATE_UP: buf6 receives SiLU(gate) * up (forward.go:348-351) and
  * buf7 is not written (may be null). */
 #define YUUKA_EXT_FLAG_MOE_SWIGLU 0x800u
+/* On MOE_GATE_UP and MOE_DOWN: the expert matrices are in the packed layout
+ * that yuuka_moe_pack_q4k writes (same byte count as the v10 layout). */
+#define YUUKA_EXT_FLAG_MOE_PACKED 0x2000u
+
+/* Rewrites expert-stacked Q4_K matrices (the v10 MoE layout, rows of n_in
+ * columns, rows % 16 == 0, n_in % 256 == 0) into the packed layout of
+ * YUUKA_EXT_FLAG_MOE_PACKED: per 16-row tile and 256-column super-block,
+ * 2304 contiguous bytes holding the grouped GEMM's per-lane 16-byte quant
+ * pieces and the 16 rows' block headers, so that its weight loads are
+ * contiguous. dst and src hold rows * n_in / 256 * 144 bytes each and must
+ * not overlap. No counterpart in the reference (its MoE kernels read the
+ * GGUF rows directly). */
+YUUKA_API yuuka_status yuuka_moe_pack_q4k(yuuka_stream * stream, yuuka_buffer * dst, const yuuka_buffer * src,
+                        uint64_t rows, uint64_t n_in, yuuka_event * completion);
 
 /* Timing events (extension): an event created with timing enabled, recorded
  * on a stream, and the elapsed milliseconds between two recorded events. */

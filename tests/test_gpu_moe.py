@@ -158,6 +158,30 @@ def test_grouped_gate_up_down_reduce(dev, stream, rows, E, used, H, F):
         want[r] = (want[r] + t).astype(np.float32)
     np.testing.assert_array_equal(xb.read(np.float32).reshape(rows, H), want)
 
+    # the same ops on packed copies of the experts (yuuka_moe_pack_q4k,
+    # FLAG_MOE_PACKED): every output bit-identical
+    def packed(w, nrows, ncols):
+        dst = dev.alloc(len(w))
+        hip.moe_pack_q4k(stream, dst, dev.upload(w), nrows, ncols)
+        return dst
+    gp, up_, dp = packed(gate_w, E * F, H), packed(up_w, E * F, H), packed(down_w, E * H, F)
+    go2, uo2, act2, eo2 = (dev.alloc(rows * used * F * 4), dev.alloc(rows * used * F * 4),
+                           dev.alloc(rows * used * F * 4), dev.alloc(rows * used * H * 4))
+    plan = hip.Plan(dev)
+    plan.add(hip.OP["MOE_GATE_UP"], [nb, gp, up_, cnt, ar, asl, go2, uo2], n=[H, F, rows, E, used], u=[O.Q4_K],
+             flags=hip.FLAG_MOE_PACKED)
+    plan.add(hip.OP["MOE_GATE_UP"], [nb, gp, up_, cnt, ar, asl, act2, None], n=[H, F, rows, E, used], u=[O.Q4_K],
+             flags=hip.FLAG_MOE_SWIGLU | hip.FLAG_MOE_PACKED)
+    plan.add(hip.OP["MOE_DOWN"], [act2, dp, cnt, ar, asl, eo2], n=[F, H, rows, E, used], u=[O.Q4_K],
+             flags=hip.FLAG_MOE_PACKED)
+    plan.execute(stream)
+    stream.sync()
+    plan.destroy()
+    np.testing.assert_array_equal(go2.read(np.float32).reshape(rows, used, F), g)
+    np.testing.assert_array_equal(uo2.read(np.float32).reshape(rows, used, F), u)
+    np.testing.assert_array_equal(act2.read(np.float32).reshape(rows, used, F), a)
+    np.testing.assert_array_equal(eo2.read(np.float32).reshape(rows, used, H), out)
+
 
 def test_router_and_combine_extension_ops(dev, stream):
     rng = np.random.default_rng(3)
@@ -196,6 +220,18 @@ def test_router_and_combine_extension_ops(dev, stream):
         t = (t + (sgm * so[r]).astype(np.float32)).astype(np.float32)
         want[r] = (want[r] + t).astype(np.float32)
     np.testing.assert_array_equal(xb.read(np.float32).reshape(rows, H), want)
+
+
+def test_moe_pack_rejects_bad_arguments(dev, stream):
+    """Row counts off the 16-row tile, columns off the super-block, buffers
+    too small or overlapping are refused before any launch."""
+    b = dev.alloc(64 * 1024 * 144 // 256 * 4)
+    c = dev.alloc(64 * 1024 * 144 // 256 * 4)
+    for rows, n_in, dst, src in [(15, 256, c, b), (16, 200, c, b), (4096, 1024, c, b), (16, 256, b, b)]:
+        with pytest.raises(hip.HipError):
+            hip.moe_pack_q4k(stream, dst, src, rows, n_in)
+    hip.moe_pack_q4k(stream, c, b, 64, 1024)
+    stream.sync()
 
 
 def test_moe_ops_reject_bad_arguments(dev):

@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "internal.h"
+#include "model_kernels.h"
 #include "plan.h"
 
 namespace yk {
@@ -512,6 +513,24 @@ yuuka_status yuuka_cast_f32_to_f16(yuuka_stream *stream, yuuka_buffer *dst, cons
         hipError_t err = launch_cast_f16(static_cast<const float *>(src->ptr),
                                          static_cast<uint16_t *>(dst->ptr), n, stream->stream);
         if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "cast launch: %s", hip_error(err));
+        return record(stream, completion);
+    });
+}
+
+yuuka_status yuuka_moe_pack_q4k(yuuka_stream *stream, yuuka_buffer *dst, const yuuka_buffer *src, uint64_t rows,
+                                uint64_t n_in, yuuka_event *completion) {
+    return guard("moe_pack_q4k", [&]() -> yuuka_status {
+        if (!stream || !dst || !src) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        if (rows == 0 || rows % 16 || n_in == 0 || n_in % 256 || n_in > (1u << 30))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE pack: %llu rows of %llu columns (rows %% 16, columns %% 256)",
+                        (unsigned long long)rows, (unsigned long long)n_in);
+        const uint64_t bytes = rows * (n_in / 256) * 144;
+        if (!range_ok(src, 0, bytes) || !range_ok(dst, 0, bytes))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE pack exceeds a buffer");
+        const uintptr_t d = reinterpret_cast<uintptr_t>(dst->ptr), r = reinterpret_cast<uintptr_t>(src->ptr);
+        if (d < r + bytes && r < d + bytes) return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE pack buffers overlap");
+        hipError_t err = launch_moe_pack_q4k(src->ptr, dst->ptr, rows, (int)n_in, stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "MoE pack launch: %s", hip_error(err));
         return record(stream, completion);
     });
 }

@@ -150,6 +150,24 @@ yuuka_status upload_tensor(yuuka_q35 *q, const yuuka_q35_tensor &t, uint64_t row
     return upload(q, t.data, rb * rows, &out->b);
 }
 
+// Expert matrices in the grouped GEMM's packed layout (yuuka_moe_pack_q4k,
+// the same bytes rearranged): the v10 layout goes to a staging buffer that
+// is rewritten on the device and freed.
+yuuka_status upload_experts(yuuka_q35 *q, const yuuka_q35_tensor &t, uint64_t rows, uint64_t cols, const char *what,
+                            Tensor *out) {
+    Tensor staged;
+    yuuka_status st = upload_tensor(q, t, rows, cols, what, &staged);
+    if (st != YUUKA_OK) return st;
+    *out = staged;
+    st = alloc(q, yk::row_bytes(t.dtype, cols) * rows, &out->b);
+    if (st == YUUKA_OK) st = yuuka_moe_pack_q4k(q->stream, out->b, staged.b, rows, cols, nullptr);
+    if (st == YUUKA_OK && hipStreamSynchronize(q->stream->stream) != hipSuccess)
+        st = fail(YUUKA_ERR_DEVICE, "%s: packing the experts failed", what);
+    q->owned.erase(std::find(q->owned.begin(), q->owned.end(), staged.b));
+    yuuka_buffer_free(staged.b);
+    return st;
+}
+
 yuuka_status upload_vec(yuuka_q35 *q, const float *v, uint64_t n, const char *what, yuuka_buffer **out) {
     if (!v) return fail(YUUKA_ERR_INVALID_ARGUMENT, "%s: missing data", what);
     return upload(q, v, n * 4, out);
@@ -318,9 +336,9 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
               {R, E, used});
         b.add(YUUKA_OP_MOE_GATE_UP,
               {q->xn, L.gate_exps.b, L.up_exps.b, q->moe_counts, q->moe_arows, q->moe_aslots, q->moe_act, nullptr},
-              {H, ef, R, E, used}, {L.gate_exps.dtype}, {}, YUUKA_EXT_FLAG_MOE_SWIGLU);
+              {H, ef, R, E, used}, {L.gate_exps.dtype}, {}, YUUKA_EXT_FLAG_MOE_SWIGLU | YUUKA_EXT_FLAG_MOE_PACKED);
         b.add(YUUKA_OP_MOE_DOWN, {q->moe_act, L.down_exps.b, q->moe_counts, q->moe_arows, q->moe_aslots, q->moe_eo},
-              {ef, H, R, E, used}, {L.down_exps.dtype});
+              {ef, H, R, E, used}, {L.down_exps.dtype}, {}, YUUKA_EXT_FLAG_MOE_PACKED);
         b.fused(q->xn, nullptr, 0.0f, R, {{&L.shared_gate, q->moe_sfg, nullptr}, {&L.shared_up, nullptr, nullptr}}, 2);
         b.fused(q->moe_sfg, nullptr, 0.0f, R, {{&L.shared_down, q->moe_so, nullptr}}, 0);
         b.add(YUUKA_EXT_OP_MOE_COMBINE, {q->x, q->moe_eo, q->moe_w, q->moe_so, q->moe_sg}, {H, R, used});
@@ -719,9 +737,9 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
                 CHK(upload_tensor(q.get(), lw.shared_gate, sf, H, "ffn_gate_shexp", &L.shared_gate));
                 CHK(upload_tensor(q.get(), lw.shared_up, sf, H, "ffn_up_shexp", &L.shared_up));
                 CHK(upload_tensor(q.get(), lw.shared_down, H, sf, "ffn_down_shexp", &L.shared_down));
-                CHK(upload_tensor(q.get(), lw.gate_exps, E * ef, H, "ffn_gate_exps", &L.gate_exps));
-                CHK(upload_tensor(q.get(), lw.up_exps, E * ef, H, "ffn_up_exps", &L.up_exps));
-                CHK(upload_tensor(q.get(), lw.down_exps, E * H, ef, "ffn_down_exps", &L.down_exps));
+                CHK(upload_experts(q.get(), lw.gate_exps, E * ef, H, "ffn_gate_exps", &L.gate_exps));
+                CHK(upload_experts(q.get(), lw.up_exps, E * ef, H, "ffn_up_exps", &L.up_exps));
+                CHK(upload_experts(q.get(), lw.down_exps, E * H, ef, "ffn_down_exps", &L.down_exps));
             } else {
                 CHK(upload_tensor(q.get(), lw.ffn_gate, c.ffn, H, "ffn_gate", &L.ffn_gate));
                 CHK(upload_tensor(q.get(), lw.ffn_up, c.ffn, H, "ffn_up", &L.ffn_up));

@@ -329,8 +329,41 @@ struct MoeGemmArgs {
     int tpw;              // 16-channel tiles per workgroup
     int by_slot;          // activation row = row*used + slot (down projection), else row
     int swiglu;           // out0 = SiLU(W0 y) * (W1 y)
+    int packed;           // w0 / w1 packed (moe_pack_q4k_kernel)
     float *out0, *out1;   // [rows*used][N]
 };
+
+// Packed expert layout (launch_moe_pack_q4k): per (16-row tile T, super-block
+// sb) 2304 contiguous bytes at (T * K/256 + sb) * 2304 — the grouped GEMM's
+// 64 lanes' first 16-byte quant pieces (1 KB), their second pieces (1 KB),
+// then the 16 rows' 16-byte headers (d, dmin, scales) — so that each of an
+// item's three loads is one contiguous 1 KB (or 256 B) wave access.
+constexpr int kPackItem = 2304;
+// quant-byte offset in the Q4_K block of lane (c, g)'s piece qq (0, 1)
+__host__ __device__ inline int moe_piece_off(int g, int qq) { return 16 + 32 * (2 * qq + (g >> 1)) + 16 * (g & 1); }
+
+__global__ __launch_bounds__(256) void moe_pack_q4k_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                           uint64_t rows, int K) {
+    // one thread per 16-byte piece: 144 pieces per (tile, super-block)
+    const int nsb = K / 256;
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x, n = rows / 16 * nsb * (kPackItem / 16);
+    if (i >= n) return;
+    const uint64_t item = i / (kPackItem / 16);
+    const int p = (int)(i % (kPackItem / 16));
+    const uint64_t T = item / nsb;
+    const int sb = (int)(item % nsb);
+    int row, off;
+    if (p < 128) {  // quant pieces: lane l = p & 63 (c = l & 15, g = l >> 4), piece p >> 6
+        const int l = p & 63;
+        row = l & 15;
+        off = moe_piece_off(l >> 4, p >> 6);
+    } else {  // header of row p - 128
+        row = p - 128;
+        off = 0;
+    }
+    const uint8_t *s = src + ((T * 16 + row) * nsb + sb) * 144 + off;
+    *reinterpret_cast<uint4 *>(dst + item * kPackItem + 16 * p) = *reinterpret_cast<const uint4 *>(s);
+}
 
 typedef __attribute__((ext_vector_type(2))) unsigned short u16x2;
 
@@ -389,6 +422,7 @@ __device__ uint64_t *yk_moe_dbg;  // per wave: start, rows known, staged, items 
 #else
 #define YK_MOE_STAMP(i) (void)0
 #endif
+template <bool PACKED>
 __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))) void moe_gemm_kernel(MoeGemmArgs A) {
 #ifdef YK_MOE_TIMING
     uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -530,12 +564,18 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
             asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
             const int lc = c + oz, lg = g + oz;
             const int tm = wave + kMoeWaves * (q / nsb), sb = q % nsb, m = tm % mats, tl = tm / mats;
-            const uint8_t *blk = (m ? A.w1 : A.w0) + ((uint64_t)e * A.N + (t0 + tl) * 16 + lc) * A.row_bytes +
-                                 (uint64_t)sb * 144;
-            H = *reinterpret_cast<const uint4 *>(blk);
+            const uint8_t *w = m ? A.w1 : A.w0;
+            if constexpr (PACKED) {
+                const uint8_t *it = w + ((uint64_t)(e * (A.N / 16) + t0 + tl) * nsb + sb) * kPackItem;
+                Q[0] = *reinterpret_cast<const uint4 *>(it + 16 * (lc + 16 * lg));
+                Q[1] = *reinterpret_cast<const uint4 *>(it + 1024 + 16 * (lc + 16 * lg));
+                H = *reinterpret_cast<const uint4 *>(it + 2048 + 16 * lc);
+            } else {
+                const uint8_t *blk = w + ((uint64_t)e * A.N + (t0 + tl) * 16 + lc) * A.row_bytes + (uint64_t)sb * 144;
+                H = *reinterpret_cast<const uint4 *>(blk);
 #pragma unroll
-            for (int qq = 0; qq < 2; qq++)
-                Q[qq] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * (2 * qq + (lg >> 1)) + 16 * (lg & 1));
+                for (int qq = 0; qq < 2; qq++) Q[qq] = *reinterpret_cast<const uint4 *>(blk + moe_piece_off(lg, qq));
+            }
         };
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
         auto compute_item = [&](int q, const uint4 &H, const uint4 (&Q)[2]) __attribute__((always_inline)) {
@@ -712,6 +752,7 @@ hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
     a.N = g.N;
     a.by_slot = g.by_slot;
     a.swiglu = g.swiglu;
+    a.packed = g.packed;
     a.out0 = g.out0;
     a.out1 = g.out1;
     if (g.experts > kMoeMaxExperts) return hipErrorInvalidValue;
@@ -735,14 +776,24 @@ hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 1;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(moe_gemm_kernel),
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(moe_gemm_kernel<false>),
                                                          kMoeThreads, lds) != hipSuccess || per_cu <= 0)
             per_cu = 1;
         per_cu_lds = lds;
     }
     const int parts = (tiles + tpw - 1) / tpw;
     const unsigned grid = (unsigned)std::min<int64_t>((int64_t)g.experts * parts, (int64_t)per_cu * cus);
-    moe_gemm_kernel<<<grid, kMoeThreads, lds, s>>>(a);
+    if (g.packed) moe_gemm_kernel<true><<<grid, kMoeThreads, lds, s>>>(a);
+    else moe_gemm_kernel<false><<<grid, kMoeThreads, lds, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_pack_q4k(const void *src, void *dst, uint64_t rows, int K, hipStream_t s) {
+    if (rows % 16 || K % 256 || K <= 0) return hipErrorInvalidValue;
+    const uint64_t n = rows / 16 * (uint64_t)(K / 256) * (kPackItem / 16);
+    if (n == 0) return hipSuccess;
+    moe_pack_q4k_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(static_cast<const uint8_t *>(src),
+                                                                     static_cast<uint8_t *>(dst), rows, K);
     return hipGetLastError();
 }
 

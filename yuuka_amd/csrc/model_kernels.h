@@ -126,7 +126,11 @@ struct MoeGemm {
     int by_slot;              // activation row = row*used + slot (down), else row (gate/up)
     int swiglu;               // out0 = SiLU(W0 y) * (W1 y)
     float *out0, *out1;       // [rows*used][N]
+    int packed = 0;           // w0 / w1 in launch_moe_pack_q4k's layout
 };
+// Rewrites expert-stacked Q4_K matrices [rows][K] (rows % 16 == 0) into the
+// grouped GEMM's packed layout (same byte count) in dst.
+hipError_t launch_moe_pack_q4k(const void *src, void *dst, uint64_t rows, int K, hipStream_t s);
 // Workspace of launch_moe_gemm: the quantized activation rows.
 uint64_t moe_gemm_ws(int act_rows, int K);
 hipError_t launch_moe_router(const float *y, int H, int rows, const float *w, int E, float *logits, const float *sv,

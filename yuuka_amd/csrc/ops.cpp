@@ -731,6 +731,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
         g.used = (int)op.n[4];
         g.by_slot = gu ? 0 : 1;
         g.swiglu = gu && (op.flags & YUUKA_EXT_FLAG_MOE_SWIGLU) ? 1 : 0;
+        g.packed = (op.flags & YUUKA_EXT_FLAG_MOE_PACKED) ? 1 : 0;
         g.out0 = at<float>(op, ib + 3);
         g.out1 = gu ? at<float>(op, ib + 4) : nullptr;
         err = launch_moe_gemm(g, ctx.ws, s);

@@ -30,6 +30,7 @@ OP = dict(
     MOE_COMBINE=73,
 )
 FLAG_MOE_SWIGLU = 0x800
+FLAG_MOE_PACKED = 0x2000
 EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU = 0, 1, 2
 FLAG_TAIL = 0x1
 
@@ -133,6 +134,7 @@ def _declare(L: C.CDLL) -> None:
         "yuuka_gemv": (C.c_int, [vp, vp, vp, vp, u64, u64, u32, vp]),
         "yuuka_gemv_batch": (C.c_int, [vp, vp, vp, vp, u64, u64, u64, u32, vp]),
         "yuuka_dequant_f32": (C.c_int, [vp, vp, vp, u64, u64, u32, vp]),
+        "yuuka_moe_pack_q4k": (C.c_int, [vp, vp, vp, u64, u64, vp]),
         "yuuka_dequant_f16": (C.c_int, [vp, vp, vp, u64, u64, u32, vp]),
         "yuuka_verify_accept": (C.c_int, [vp, vp, u64, vp, u64, vp, u64, vp,
                                           C.POINTER(yuuka_accept_params), vp]),
@@ -304,6 +306,11 @@ def gemm_quantized(stream: Stream, out: Buffer, xq: Buffer, w: Buffer, n_in: int
 
 def dequant_f32(stream: Stream, dst: Buffer, src: Buffer, n_in: int, n_out: int, dtype: int) -> None:
     check(lib().yuuka_dequant_f32(stream.ptr, dst.ptr, src.ptr, n_in, n_out, dtype, None), "dequant_f32")
+
+
+def moe_pack_q4k(stream: Stream, dst: Buffer, src: Buffer, rows: int, n_in: int) -> None:
+    """Expert-stacked Q4_K rows into the packed layout of FLAG_MOE_PACKED."""
+    check(lib().yuuka_moe_pack_q4k(stream.ptr, dst.ptr, src.ptr, rows, n_in, None), "moe_pack_q4k")
 
 
 def verify_accept(stream: Stream, logits: Buffer, drafts: Buffer | None, result: Buffer,
