@@ -463,6 +463,7 @@ def bench_config2(args):
                           "weights": wbytes, "kv": kv_bytes, "gdn_state": state_bytes, "logits": logit_bytes},
         "roofline": dk,
         "context_end": ctx,
+        **({"moe_routing": routing} if routing else {}),
         "prefill_s": prefill_s,
         "weight_gen_s": gen_s,
         "device": info,
@@ -605,6 +606,19 @@ def bench_batched(args, which):
         gpu_ms.append(ms)
     wall = time.perf_counter() - t0
     step_gpu_ms = float(np.median(gpu_ms))
+    routing = None
+    if cfg.n_experts:
+        # the experts the verify rows actually selected, per layer, over a few
+        # more (untimed) steps: the expert matrices a step streams
+        distinct, top = [], []
+        for _ in range(4):
+            step()
+            for li in range(cfg.n_layers):
+                cnt = eng.moe_counts(li)
+                distinct.append(int((cnt > 0).sum()))
+                top.append(int(cnt.max()))
+        routing = {"distinct_experts_per_layer": float(np.mean(distinct)), "max_rows_per_expert": max(top),
+                   "sample": f"4 steps after the timed ones, all {cfg.n_layers} layers"}
     ctx = [eng.request_position(r) for r in range(B)]
     R1 = k + 1
     kvdim = cfg.kv_heads * cfg.head_dim
@@ -618,13 +632,16 @@ def bench_batched(args, which):
     step_w = wbytes
     moe_note = None
     if cfg.n_experts:
-        # expert bytes actually streamed: the distinct experts the B*(k+1)
-        # routed rows touch, in expectation under uniform routing
+        # expert bytes actually streamed: the distinct experts the verify rows
+        # selected (measured above); uniform routing would touch
+        # E (1 - (1 - used / E)^rows) of them
         E, used, ef, H = cfg.n_experts, cfg.n_experts_used, cfg.expert_ffn, cfg.hidden
-        distinct = E * (1 - (1 - used / E) ** (B * R1))
+        distinct = routing["distinct_experts_per_layer"]
+        uniform = E * (1 - (1 - used / E) ** (B * R1))
         per_expert = 3 * ef * H // 256 * 144
         step_w = wbytes - cfg.n_layers * E * per_expert + cfg.n_layers * int(distinct * per_expert)
-        moe_note = f"expert bytes for {distinct:.1f} of {E} experts per layer (expected distinct under uniform routing)"
+        moe_note = (f"expert bytes for the {distinct:.1f} of {E} experts per layer the rows selected "
+                    f"(uniform routing would touch {uniform:.1f})")
     step_bytes = step_w + kv_bytes + state_bytes + logit_bytes
     step_ach = step_bytes / (step_gpu_ms * 1e-3) / 1e9
     line = {
@@ -654,6 +671,7 @@ def bench_batched(args, which):
                           "frac": step_ach / HBM_PEAK_GBS, "alg_bytes_per_step": step_bytes, "weights": step_w,
                           "kv": kv_bytes, "gdn_state": state_bytes, "logits": logit_bytes, "note": moe_note},
         "context_end": ctx,
+        **({"moe_routing": routing} if routing else {}),
         "prefill_s": prefill_s,
         "weight_gen_s": gen_s,
         "device": info,

@@ -490,6 +490,12 @@ YUUKA_API yuuka_status yuuka_verify_accept_noalloc(yuuka_stream * stream,
 /* On MOE_GATE_UP and MOE_DOWN: the expert matrices are in the packed layout
  * that yuuka_moe_pack_q4k writes (same byte count as the v10 layout). */
 #define YUUKA_EXT_FLAG_MOE_PACKED 0x2000u
+/* On MOE_GATE_UP and MOE_DOWN: expert index `experts` (the weights hold
+ * experts + 1 matrices) is the shared expert, applied to every row as slot
+ * `used`: the activation rows of MOE_DOWN and the output rows of both have
+ * used + 1 slots. On MOE_COMBINE: the shared expert's output is slot `used`
+ * of buf1 (rows of used + 1 slots; buf3 null, buf4 its gate logit). */
+#define YUUKA_EXT_FLAG_MOE_SHARED 0x4000u
 
 /* Rewrites expert-stacked Q4_K matrices (the v10 MoE layout, rows of n_in
  * columns, rows % 16 == 0, n_in % 256 == 0) into the packed layout of
@@ -613,6 +619,12 @@ YUUKA_API yuuka_status yuuka_q35_verify(yuuka_q35 * q, const int32_t * tokens, i
                                         const yuuka_q35_accept * accept, int32_t * result);
 /* Copies the logits rows of the last verify or prefill step [rows][vocab]. */
 YUUKA_API yuuka_status yuuka_q35_logits(yuuka_q35 * q, float * out, int32_t rows);
+/* Per expert of MoE layer `layer`: how many rows of the last step selected
+ * it (of the last block of 512 rows when the step had more); counts holds
+ * n >= n_experts entries. Every layer's routing is kept, so a caller can
+ * tell which expert matrices a step streamed (benchmark accounting; no
+ * counterpart in the reference). */
+YUUKA_API yuuka_status yuuka_q35_moe_counts(yuuka_q35 * q, int32_t layer, int32_t * counts, int32_t n);
 /* state.go:211-263 Snapshot/Restore: all recurrent state (conv then matrix,
  * per recurrent layer, little-endian FP32) and the position. */
 YUUKA_API uint64_t yuuka_q35_snapshot_bytes(const yuuka_q35 * q);

@@ -190,8 +190,12 @@ def test_long_draft_seventeen_rows(dev):
         o.close()
 
 
-def test_moe_single_request_prefill_and_verify(dev):
-    cfg = Mdl.TINY_MOE
+@pytest.mark.parametrize("shared_ffn", [256, 512])
+def test_moe_single_request_prefill_and_verify(dev, shared_ffn):
+    """A shared expert as wide as the routed ones runs inside the grouped
+    GEMMs (expert index n_experts); a wider one as its own GEMMs. Both
+    against the oracle."""
+    cfg = replace(Mdl.TINY_MOE, shared_ffn=shared_ffn)
     w = Mdl.make_weights(cfg, seed=9)
     eng = Mdl.Engine(dev, cfg, w)
     orc = O.Q35(cfg, w)
@@ -200,5 +204,8 @@ def test_moe_single_request_prefill_and_verify(dev):
     rows = np.array([3, 1, 4, 1, 5], np.int32)
     eng.verify(rows)
     _close(eng.logits(5), _all_rows(orc, rows), "moe verify")
+    for li in range(cfg.n_layers):  # every layer's routing of the step: rows x used selections
+        cnt = eng.moe_counts(li)
+        assert cnt.sum() == len(rows) * cfg.n_experts_used and 0 <= cnt.min() and cnt.max() <= len(rows), (li, cnt)
     eng.close()
     orc.close()

@@ -241,6 +241,8 @@ def test_moe_ops_reject_bad_arguments(dev):
         plan.add(hip.OP["MOE_ROUTE"], [b] * 7, n=[4, 8, 9])          # used > experts
     with pytest.raises(hip.Unsupported):
         plan.add(hip.OP["MOE_GATE_UP"], [b] * 8, n=[256, 16, 1, 1, 1], u=[O.Q6_K])
+    with pytest.raises(hip.Unsupported):  # more rows than one grouped GEMM takes
+        plan.add(hip.OP["MOE_GATE_UP"], [b] * 8, n=[256, 16, 513, 8, 2], u=[O.Q4_K])
     with pytest.raises(hip.HipError):
         plan.add(hip.OP["MOE_REDUCE_ADD"], [b, b, b], n=[1 << 20, 64, 8])  # overflow of the buffers
     plan.destroy()

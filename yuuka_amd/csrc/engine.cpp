@@ -99,6 +99,9 @@ struct yuuka_q35 {
     yuuka_buffer *moe_logits = nullptr, *moe_sg = nullptr, *moe_ids = nullptr, *moe_w = nullptr,
                  *moe_counts = nullptr, *moe_arows = nullptr, *moe_aslots = nullptr, *moe_aw = nullptr,
                  *moe_act = nullptr, *moe_eo = nullptr, *moe_sfg = nullptr, *moe_so = nullptr;
+    // the shared expert runs inside the grouped GEMMs as expert n_experts
+    // (its width equals the experts'): output slot n_experts_used of every row
+    bool moe_shared = false;
     // step I/O and per-request device state
     yuuka_buffer *tokens = nullptr, *result = nullptr, *dyn = nullptr, *step = nullptr, *table = nullptr,
                  *forced = nullptr;
@@ -153,18 +156,38 @@ yuuka_status upload_tensor(yuuka_q35 *q, const yuuka_q35_tensor &t, uint64_t row
 // Expert matrices in the grouped GEMM's packed layout (yuuka_moe_pack_q4k,
 // the same bytes rearranged): the v10 layout goes to a staging buffer that
 // is rewritten on the device and freed.
+// With `extra` (the shared expert, extra_rows rows) that matrix is packed
+// after the experts, as expert index rows / expert rows.
 yuuka_status upload_experts(yuuka_q35 *q, const yuuka_q35_tensor &t, uint64_t rows, uint64_t cols, const char *what,
-                            Tensor *out) {
-    Tensor staged;
+                            Tensor *out, const yuuka_q35_tensor *extra = nullptr, uint64_t extra_rows = 0,
+                            const char *extra_what = nullptr) {
+    const uint64_t rb = yk::row_bytes(t.dtype, cols);
+    Tensor staged, staged_x;
     yuuka_status st = upload_tensor(q, t, rows, cols, what, &staged);
+    if (st == YUUKA_OK && extra) {
+        if (extra->dtype != t.dtype) return fail(YUUKA_ERR_UNSUPPORTED, "%s: dtype %u", extra_what, extra->dtype);
+        st = upload_tensor(q, *extra, extra_rows, cols, extra_what, &staged_x);
+    }
     if (st != YUUKA_OK) return st;
     *out = staged;
-    st = alloc(q, yk::row_bytes(t.dtype, cols) * rows, &out->b);
+    out->rows = rows + extra_rows;
+    st = alloc(q, rb * (rows + extra_rows), &out->b);
     if (st == YUUKA_OK) st = yuuka_moe_pack_q4k(q->stream, out->b, staged.b, rows, cols, nullptr);
+    if (st == YUUKA_OK && extra) {
+        // the packed layout is tile-major: the extra matrix's tiles follow at
+        // the same byte offset as its rows would
+        yuuka_buffer view = *out->b;
+        view.ptr = static_cast<uint8_t *>(out->b->ptr) + rb * rows;
+        view.bytes = rb * extra_rows;
+        st = yuuka_moe_pack_q4k(q->stream, &view, staged_x.b, extra_rows, cols, nullptr);
+    }
     if (st == YUUKA_OK && hipStreamSynchronize(q->stream->stream) != hipSuccess)
         st = fail(YUUKA_ERR_DEVICE, "%s: packing the experts failed", what);
-    q->owned.erase(std::find(q->owned.begin(), q->owned.end(), staged.b));
-    yuuka_buffer_free(staged.b);
+    for (yuuka_buffer *b : {staged.b, staged_x.b}) {
+        if (!b) continue;
+        q->owned.erase(std::find(q->owned.begin(), q->owned.end(), b));
+        yuuka_buffer_free(b);
+    }
     return st;
 }
 
@@ -174,6 +197,8 @@ yuuka_status upload_vec(yuuka_q35 *q, const float *v, uint64_t n, const char *wh
 }
 
 // ------------------------------------------------------------ plan build
+
+constexpr uint64_t kMoeRows = 512;  // rows of one grouped-GEMM launch
 
 struct Builder {
     yuuka_plan *plan;
@@ -326,22 +351,35 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
     };
     // forward.go:320-389 forwardMoEFFN over all rows: router, top-k binning,
     // grouped expert SwiGLU and down projections, shared expert, weighted sum.
-    auto moe_ffn = [&](Layer &L) {
+    auto moe_ffn = [&](Layer &L, uint64_t li) {
         const uint64_t E = (uint64_t)c.n_experts, used = (uint64_t)c.n_experts_used;
         const uint64_t ef = (uint64_t)c.expert_ffn;
+        const bool sh = q->moe_shared;
+        const uint32_t mf = YUUKA_EXT_FLAG_MOE_PACKED | (sh ? YUUKA_EXT_FLAG_MOE_SHARED : 0u);
         b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, L.post_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
         b.add(YUUKA_EXT_OP_MOE_ROUTER, {q->xn, L.router.b, q->moe_logits, L.shared_gate_vec, q->moe_sg}, {H, E, R});
-        b.add(YUUKA_OP_MOE_ROUTE,
-              {q->moe_logits, q->moe_ids, q->moe_w, q->moe_counts, q->moe_arows, q->moe_aslots, q->moe_aw},
-              {R, E, used});
-        b.add(YUUKA_OP_MOE_GATE_UP,
-              {q->xn, L.gate_exps.b, L.up_exps.b, q->moe_counts, q->moe_arows, q->moe_aslots, q->moe_act, nullptr},
-              {H, ef, R, E, used}, {L.gate_exps.dtype}, {}, YUUKA_EXT_FLAG_MOE_SWIGLU | YUUKA_EXT_FLAG_MOE_PACKED);
-        b.add(YUUKA_OP_MOE_DOWN, {q->moe_act, L.down_exps.b, q->moe_counts, q->moe_arows, q->moe_aslots, q->moe_eo},
-              {ef, H, R, E, used}, {L.down_exps.dtype}, {}, YUUKA_EXT_FLAG_MOE_PACKED);
-        b.fused(q->xn, nullptr, 0.0f, R, {{&L.shared_gate, q->moe_sfg, nullptr}, {&L.shared_up, nullptr, nullptr}}, 2);
-        b.fused(q->moe_sfg, nullptr, 0.0f, R, {{&L.shared_down, q->moe_so, nullptr}}, 0);
-        b.add(YUUKA_EXT_OP_MOE_COMBINE, {q->x, q->moe_eo, q->moe_w, q->moe_so, q->moe_sg}, {H, R, used});
+        if (!sh) {  // the shared expert as its own GEMMs (its width differs from the experts')
+            b.fused(q->xn, nullptr, 0.0f, R, {{&L.shared_gate, q->moe_sfg, nullptr}, {&L.shared_up, nullptr, nullptr}},
+                    2);
+            b.fused(q->moe_sfg, nullptr, 0.0f, R, {{&L.shared_down, q->moe_so, nullptr}}, 0);
+        }
+        // the grouped GEMMs take at most kMoeRows rows: row blocks (MoE rows are
+        // independent), the bins and expert buffers reused by each block in turn
+        for (uint64_t r0 = 0; r0 < R; r0 += kMoeRows) {
+            const uint64_t n = std::min<uint64_t>(kMoeRows, R - r0);
+            // each layer's expert counts stay in their own slice (yuuka_q35_moe_counts)
+            const uint64_t co = li * E * 4;
+            b.add(YUUKA_OP_MOE_ROUTE,
+                  {q->moe_logits, q->moe_ids, q->moe_w, q->moe_counts, q->moe_arows, q->moe_aslots, q->moe_aw},
+                  {n, E, used}, {}, {}, 0, {r0 * E * 4, 0, 0, co});
+            b.add(YUUKA_OP_MOE_GATE_UP,
+                  {q->xn, L.gate_exps.b, L.up_exps.b, q->moe_counts, q->moe_arows, q->moe_aslots, q->moe_act, nullptr},
+                  {H, ef, n, E, used}, {L.gate_exps.dtype}, {}, YUUKA_EXT_FLAG_MOE_SWIGLU | mf, {r0 * H * 4, 0, 0, co});
+            b.add(YUUKA_OP_MOE_DOWN, {q->moe_act, L.down_exps.b, q->moe_counts, q->moe_arows, q->moe_aslots, q->moe_eo},
+                  {ef, H, n, E, used}, {L.down_exps.dtype}, {}, mf, {0, 0, co});
+            b.add(YUUKA_EXT_OP_MOE_COMBINE, {q->x, q->moe_eo, q->moe_w, sh ? nullptr : q->moe_so, q->moe_sg},
+                  {H, n, used}, {}, {}, sh ? YUUKA_EXT_FLAG_MOE_SHARED : 0u, {r0 * H * 4, 0, 0, sh ? 0 : r0 * H * 4, r0 * 4});
+        }
     };
     for (int i = 0; i < c.n_layers; i++) {
         Layer &L = q->layers[i];
@@ -364,7 +402,7 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
             b.fused(q->attn, nullptr, 0.0f, R, {{&L.o, q->x, q->x}}, 1);
         }
         if (L.moe) {
-            moe_ffn(L);
+            moe_ffn(L, (uint64_t)i);
         } else {
             // plan.go:915-988 FFN: norm + gate/up + SwiGLU in one op, down + residual
             b.fused(q->x, L.post_norm, c.eps, R, {{&L.ffn_gate, q->fg, nullptr}, {&L.ffn_up, nullptr, nullptr}},
@@ -656,6 +694,7 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
         q->B = c.batch;
         q->MR = c.max_rows;
         q->M = q->B * q->MR;
+        q->moe_shared = moe && c.shared_ffn == c.expert_ffn;
         q->max_blocks = (c.capacity + c.block_size - 1) / c.block_size;
         q->conv_dim = 2 * c.groups * c.state_size + c.inner;
         q->req.resize(q->B);
@@ -734,12 +773,21 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
                     CHK(fail(YUUKA_ERR_UNSUPPORTED, "MoE layer %d: router F32 and Q4_K experts are served", i));
                 CHK(upload_tensor(q.get(), lw.router, E, H, "ffn_gate_inp", &L.router));
                 CHK(upload_vec(q.get(), lw.shared_gate_vec, H, "ffn_gate_inp_shexp", &L.shared_gate_vec));
-                CHK(upload_tensor(q.get(), lw.shared_gate, sf, H, "ffn_gate_shexp", &L.shared_gate));
-                CHK(upload_tensor(q.get(), lw.shared_up, sf, H, "ffn_up_shexp", &L.shared_up));
-                CHK(upload_tensor(q.get(), lw.shared_down, H, sf, "ffn_down_shexp", &L.shared_down));
-                CHK(upload_experts(q.get(), lw.gate_exps, E * ef, H, "ffn_gate_exps", &L.gate_exps));
-                CHK(upload_experts(q.get(), lw.up_exps, E * ef, H, "ffn_up_exps", &L.up_exps));
-                CHK(upload_experts(q.get(), lw.down_exps, E * H, ef, "ffn_down_exps", &L.down_exps));
+                if (q->moe_shared) {
+                    CHK(upload_experts(q.get(), lw.gate_exps, E * ef, H, "ffn_gate_exps", &L.gate_exps, &lw.shared_gate,
+                                       sf, "ffn_gate_shexp"));
+                    CHK(upload_experts(q.get(), lw.up_exps, E * ef, H, "ffn_up_exps", &L.up_exps, &lw.shared_up, sf,
+                                       "ffn_up_shexp"));
+                    CHK(upload_experts(q.get(), lw.down_exps, E * H, ef, "ffn_down_exps", &L.down_exps, &lw.shared_down,
+                                       H, "ffn_down_shexp"));
+                } else {
+                    CHK(upload_tensor(q.get(), lw.shared_gate, sf, H, "ffn_gate_shexp", &L.shared_gate));
+                    CHK(upload_tensor(q.get(), lw.shared_up, sf, H, "ffn_up_shexp", &L.shared_up));
+                    CHK(upload_tensor(q.get(), lw.shared_down, H, sf, "ffn_down_shexp", &L.shared_down));
+                    CHK(upload_experts(q.get(), lw.gate_exps, E * ef, H, "ffn_gate_exps", &L.gate_exps));
+                    CHK(upload_experts(q.get(), lw.up_exps, E * ef, H, "ffn_up_exps", &L.up_exps));
+                    CHK(upload_experts(q.get(), lw.down_exps, E * H, ef, "ffn_down_exps", &L.down_exps));
+                }
             } else {
                 CHK(upload_tensor(q.get(), lw.ffn_gate, c.ffn, H, "ffn_gate", &L.ffn_gate));
                 CHK(upload_tensor(q.get(), lw.ffn_up, c.ffn, H, "ffn_up", &L.ffn_up));
@@ -765,14 +813,18 @@ yuuka_status yuuka_q35_create(yuuka_device *dev, const yuuka_q35_config *cfg, co
             CHK(alloc(q.get(), M * 4, &q->moe_sg));
             CHK(alloc(q.get(), M * used * 4, &q->moe_ids));
             CHK(alloc(q.get(), M * used * 4, &q->moe_w));
-            CHK(alloc(q.get(), E * 4, &q->moe_counts));
+            CHK(alloc(q.get(), E * (uint64_t)c.n_layers * 4, &q->moe_counts));
             CHK(alloc(q.get(), E * M * used * 4, &q->moe_arows));
             CHK(alloc(q.get(), E * M * used * 4, &q->moe_aslots));
             CHK(alloc(q.get(), E * M * used * 4, &q->moe_aw));
-            CHK(alloc(q.get(), M * used * c.expert_ffn * 4, &q->moe_act));
-            CHK(alloc(q.get(), M * used * H * 4, &q->moe_eo));
-            CHK(alloc(q.get(), M * c.shared_ffn * 4, &q->moe_sfg));
-            CHK(alloc(q.get(), M * H * 4, &q->moe_so));
+            // with the shared expert fused, one more output slot per row
+            const uint64_t os = used + (q->moe_shared ? 1 : 0), mb = std::min<uint64_t>(M, kMoeRows);
+            CHK(alloc(q.get(), mb * os * c.expert_ffn * 4, &q->moe_act));
+            CHK(alloc(q.get(), mb * os * H * 4, &q->moe_eo));
+            if (!q->moe_shared) {
+                CHK(alloc(q.get(), M * c.shared_ffn * 4, &q->moe_sfg));
+                CHK(alloc(q.get(), M * H * 4, &q->moe_so));
+            }
         }
         CHK(alloc(q.get(), (M + 64) * 4, &q->tokens));
         CHK(alloc(q.get(), Bq * 16, &q->result));
@@ -938,6 +990,20 @@ yuuka_status yuuka_q35_logits(yuuka_q35 *q, float *out, int32_t rows) {
         if (!q || !out || rows < 1 || rows > q->M) return fail(YUUKA_ERR_INVALID_ARGUMENT, "bad arguments");
         hipError_t err = hipMemcpy(out, q->logits->ptr, (size_t)rows * q->cfg.vocab * 4, hipMemcpyDeviceToHost);
         if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "logits copy: %s", yk::hip_error(err));
+        return YUUKA_OK;
+    });
+}
+
+yuuka_status yuuka_q35_moe_counts(yuuka_q35 *q, int32_t layer, int32_t *counts, int32_t n) {
+    return guard("q35_moe_counts", [&]() -> yuuka_status {
+        if (!q || !counts || layer < 0 || layer >= q->cfg.n_layers || q->cfg.n_experts <= 0 || n < q->cfg.n_experts)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "bad arguments");
+        const uint64_t E = (uint64_t)q->cfg.n_experts;
+        hipError_t err = hipStreamSynchronize(q->stream->stream);
+        if (err == hipSuccess)
+            err = hipMemcpy(counts, static_cast<const uint8_t *>(q->moe_counts->ptr) + (uint64_t)layer * E * 4, E * 4,
+                            hipMemcpyDeviceToHost);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "MoE counts copy: %s", yk::hip_error(err));
         return YUUKA_OK;
     });
 }

@@ -41,6 +41,8 @@ constexpr int kMoeWaves = 8;
 constexpr int kMoeThreads = 64 * kMoeWaves;
 constexpr int kChunk = 8;        // assignments per MFMA tile (high planes in rows 0..7)
 constexpr int kMoeMaxExperts = 1024;
+constexpr int kMoeMaxRows = 512;     // rows of a grouped GEMM (an expert's chunks stay below 64)
+constexpr int kMoeMaxList = 2048;    // work-list entries: experts + chunks past their first
 
 // Wave reductions on the DPP path (a __shfl_xor is an LDS permute): within
 // each 16-lane row (pairs, quads, half rows, rows), then the four rows'
@@ -330,6 +332,8 @@ struct MoeGemmArgs {
     int by_slot;          // activation row = row*used + slot (down projection), else row
     int swiglu;           // out0 = SiLU(W0 y) * (W1 y)
     int packed;           // w0 / w1 packed (moe_pack_q4k_kernel)
+    int shared;           // expert E is the shared expert: every row, output slot `used`
+    int ostride;          // slots per row of the activation (down) and output rows: used + shared
     float *out0, *out1;   // [rows*used][N]
 };
 
@@ -438,7 +442,8 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
     const int parts = (tiles + A.tpw - 1) / A.tpw;
     const bool dual = A.w1 != nullptr;
     const int mats = dual ? 2 : 1;
-    __shared__ int s_act[kMoeMaxExperts], s_wtot[kMoeWaves];
+    __shared__ uint16_t s_list[kMoeMaxList];
+    __shared__ int s_wtot[kMoeWaves];
     // assignment metadata of three tasks (current, next, the one after):
     // [0, 8) rows, [8, 16) slots, [16] the expert's count
     __shared__ __attribute__((aligned(16))) int s_meta[3][32];
@@ -449,51 +454,63 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
     const int c = lane & 15, g = lane >> 4;
     const uint64_t cap = (uint64_t)A.rows * A.used;
 
-    // The experts some row selected, in expert order (ballot prefix counts
-    // per 64 experts, wave totals added in wave order): the work items are
-    // (active expert, tile part) pairs dealt round-robin over the grid, so
-    // every workgroup gets an equal share wherever the active experts fall.
-    int nact = 0;
-    for (int b0 = 0; b0 < A.E; b0 += kMoeThreads) {
+    // The work list: one entry (expert | chunk << 10) per chunk of up to
+    // kChunk assignments of every expert some row selected, in expert and
+    // chunk order (wave prefix sums of the chunk counts, wave totals added in
+    // wave order); with A.shared, expert E is the shared expert and holds
+    // every row. The work items are (entry, tile part) pairs dealt
+    // round-robin over the grid, so every workgroup gets an equal share
+    // wherever the assignments fall.
+    const int nexp = A.E + (A.shared ? 1 : 0);
+    int nlist = 0;
+    for (int b0 = 0; b0 < nexp; b0 += kMoeThreads) {
         const int ex = b0 + (int)threadIdx.x;
-        const bool on = ex < A.E && A.counts[ex] > 0;
-        const uint64_t m = __ballot(on);
-        const int below = __popcll(m & ((1ull << lane) - 1ull));
-        if (lane == 0) s_wtot[wave] = __popcll(m);
+        const int cnt = ex < A.E ? A.counts[ex] : (ex < nexp ? A.rows : 0);
+        const int nch = (max(cnt, 0) + kChunk - 1) / kChunk;
+        int incl = nch;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int o = __shfl_up(incl, d);
+            if (lane >= d) incl += o;
+        }
+        if (lane == 63) s_wtot[wave] = incl;
         __syncthreads();
-        int base = nact;
+        int base = nlist + incl - nch;
         for (int w = 0; w < wave; w++) base += s_wtot[w];
-        if (on) s_act[base + below] = ex;
-        for (int w = 0; w < kMoeWaves; w++) nact += s_wtot[w];
+        for (int j = 0; j < nch; j++) s_list[base + j] = (uint16_t)(ex | (j << 10));
+        for (int w = 0; w < kMoeWaves; w++) nlist += s_wtot[w];
         __syncthreads();
     }
-    const int items = nact * parts;
+    const int items = nlist * parts;
     if ((int)blockIdx.x >= items) return;  // workgroup-uniform
 
-    // A task is one chunk (up to kChunk assignments) of one of this
-    // workgroup's items: item k is blockIdx.x + k * gridDim.x. Task t's
-    // planes and scales sit in LDS buffer t & 1, its metadata in slot t % 3;
-    // task t + 1's planes and task t + 2's metadata are copied into LDS
-    // (global_load_lds, outside the compiler's wait counts) while task t
+    // Task k is this workgroup's item k, blockIdx.x + k * gridDim.x. Task
+    // k's planes and scales sit in LDS buffer k & 1, its metadata in slot
+    // k % 3; task k + 1's planes and task k + 2's metadata are copied into
+    // LDS (global_load_lds, outside the compiler's wait counts) while task k
     // streams its weights, and every wave waits for its own copies (vmcnt 0)
-    // before the barrier that ends task t.
+    // before the barrier that ends task k.
     auto item_of = [&](int k) { return (int)blockIdx.x + k * (int)gridDim.x; };
-    auto expert_of = [&](int k) { return s_act[item_of(k) / parts]; };
-    auto meta_issue = [&](int k, int c0, int slot) __attribute__((always_inline)) {
+    auto entry_of = [&](int k) { return (int)s_list[item_of(k) / parts]; };
+    auto meta_issue = [&](int k, int slot) __attribute__((always_inline)) {
+        const int en = entry_of(k), e = en & 1023, c0 = (en >> 10) * kChunk;
         if (wave == 0 && lane < 17) {
-            const int e = expert_of(k);
-            const uint64_t b = (uint64_t)e * cap;
-            const int32_t *src = lane < 8    ? A.arows + b + min((uint64_t)(c0 + lane), cap - 1)
-                                 : lane < 16 ? A.aslots + b + min((uint64_t)(c0 + lane - 8), cap - 1)
-                                             : A.counts + e;
-            lds_copy4(src, &s_meta[slot][0]);
+            if (e == A.E) {  // the shared expert: rows c0.., slot `used`, count rows
+                s_meta[slot][lane] = lane < 8 ? min(c0 + lane, A.rows - 1) : lane < 16 ? A.used : A.rows;
+            } else {
+                const uint64_t b = (uint64_t)e * cap;
+                const int32_t *src = lane < 8    ? A.arows + b + min((uint64_t)(c0 + lane), cap - 1)
+                                     : lane < 16 ? A.aslots + b + min((uint64_t)(c0 + lane - 8), cap - 1)
+                                                 : A.counts + e;
+                lds_copy4(src, &s_meta[slot][0]);
+            }
         }
     };
     // activation row of assignment i of a task (padding rows repeat the
     // chunk's first assignment and are never stored)
     auto act_row = [&](const int *mt, int c0, int i) __attribute__((always_inline)) {
         const int j = c0 + i < mt[16] ? i : 0;
-        return A.by_slot ? mt[j] * A.used + mt[8 + j] : mt[j];
+        return A.by_slot ? mt[j] * A.ostride + mt[8 + j] : mt[j];
     };
     auto stage_issue = [&](int c0, int slot, int buf) __attribute__((always_inline)) {
         const int *mt = s_meta[slot];
@@ -509,39 +526,26 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
             if (idx < nsb * 8) lds_copy4(A.xq.scales + (uint64_t)act_row(mt, c0, idx & 7) * nsb + (idx >> 3), xd + b * 64);
         }
     };
-    auto next_task = [&](int k, int c0, int count, int &nk, int &nc0) __attribute__((always_inline)) {
-        if (c0 + kChunk < count) {
-            nk = k;
-            nc0 = c0 + kChunk;
-        } else {
-            nk = k + 1;
-            nc0 = 0;
-        }
-    };
 
     // task 0: metadata, then its planes with task 1's metadata
-    int k = 0, c0 = 0;
-    meta_issue(0, 0, 0);
+    meta_issue(0, 0);
     vmem_wait_all();
     __syncthreads();
-    int k1, c1;
-    next_task(0, 0, s_meta[0][16], k1, c1);
-    if (item_of(k1) < items) meta_issue(k1, c1, 1);
-    stage_issue(0, 0, 0);
+    if (item_of(1) < items) meta_issue(1, 1);
+    stage_issue((entry_of(0) >> 10) * kChunk, 0, 0);
     vmem_wait_all();
     __syncthreads();
-    for (int t = 0;; t++) {
+    for (int k = 0;; k++) {
         YK_MOE_STAMP(1);
-        const int slot = t % 3, buf = t & 1;
+        const int slot = k % 3, buf = k & 1;
         const int *mt = s_meta[slot];
+        const int en = entry_of(k), e = en & 1023, c0 = (en >> 10) * kChunk;
         const int count = mt[16], nr = min(kChunk, count - c0);
-        const int e = expert_of(k), t0 = (item_of(k) % parts) * A.tpw, ntl = min(A.tpw, tiles - t0);
+        const int t0 = (item_of(k) % parts) * A.tpw, ntl = min(A.tpw, tiles - t0);
         // the next task's planes, and the metadata of the one after it
-        if (item_of(k1) < items) {
-            int k2, c2;
-            stage_issue(c1, (t + 1) % 3, buf ^ 1);
-            next_task(k1, c1, s_meta[(t + 1) % 3][16], k2, c2);
-            if (item_of(k2) < items) meta_issue(k2, c2, (t + 2) % 3);
+        if (item_of(k + 1) < items) {
+            stage_issue((entry_of(k + 1) >> 10) * kChunk, (k + 1) % 3, buf ^ 1);
+            if (item_of(k + 2) < items) meta_issue(k + 2, (k + 2) % 3);
         }
         const uint8_t *lat = la + (uint64_t)buf * la_bytes;
         const float *lxt = lxs + (uint64_t)buf * nsb * 8;
@@ -663,7 +667,7 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
             const int tl = o / (nr * 16), rem = o % (nr * 16), i = rem / 16, cc = rem % 16;
             float y[2] = {0.f, 0.f};
             for (int m = 0; m < mats; m++) y[m] = part[(uint64_t)(tl * mats + m) * 128 + i * 16 + cc];
-            const uint64_t dst = (uint64_t)(mt[i] * A.used + mt[8 + i]) * A.N + (t0 + tl) * 16 + cc;
+            const uint64_t dst = (uint64_t)(mt[i] * A.ostride + mt[8 + i]) * A.N + (t0 + tl) * 16 + cc;
             if (A.swiglu) {
                 A.out0[dst] = __fmul_rn(silu_ref(y[0]), y[1]);
             } else {
@@ -673,10 +677,7 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
         }
         vmem_wait_all();
         __syncthreads();
-        if (item_of(k1) >= items) break;
-        k = k1;
-        c0 = c1;
-        next_task(k, c0, s_meta[(t + 1) % 3][16], k1, c1);
+        if (item_of(k + 1) >= items) break;
     }
 #ifdef YK_MOE_TIMING
     YK_MOE_STAMP(4);
@@ -693,21 +694,25 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
 // operations in the reference's order, no contraction (written as plain
 // operators under the pragma: the __fmul_rn / __fadd_rn helpers are defined
 // in a contractable context and would still be fused after inlining).
+// With `shared_slot` the shared expert's output is slot `used` of eo (rows
+// of used + 1 slots) instead of `so`.
 __global__ __launch_bounds__(256) void moe_combine_kernel(float *__restrict__ x, const float *__restrict__ eo,
                                                           const float *__restrict__ w, int rows, int used, int H,
                                                           const float *__restrict__ so,
-                                                          const float *__restrict__ sg) {
+                                                          const float *__restrict__ sg, int shared_slot) {
 #pragma clang fp contract(off)  // the reference rounds every product and sum
     const int r = blockIdx.x;
-    const float *er = eo + (uint64_t)r * used * H;
+    const int ostride = used + (shared_slot ? 1 : 0);
+    const float *er = eo + (uint64_t)r * ostride * H;
     const float *wr = w + (uint64_t)r * used;
-    const float gate = so ? sigmoid_ref(sg[r]) : 0.f;
+    const float *sr = shared_slot ? er + (uint64_t)used * H : (so ? so + (uint64_t)r * H : nullptr);
+    const float gate = sr ? sigmoid_ref(sg[r]) : 0.f;
     const int i = blockIdx.y * blockDim.x + threadIdx.x;  // grid (rows, H / 256): one element per thread
     if (i < H) {
         float t = 0.f;
 #pragma unroll 8
         for (int s = 0; s < used; s++) t = t + wr[s] * er[(uint64_t)s * H + i];
-        if (so) t = t + gate * so[(uint64_t)r * H + i];
+        if (sr) t = t + gate * sr[i];
         x[(uint64_t)r * H + i] = x[(uint64_t)r * H + i] + t;
     }
 }
@@ -736,7 +741,12 @@ hipError_t launch_moe_route(const float *logits, int rows, int E, int used, int3
 }
 
 hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
-    const int act_rows = g.by_slot ? g.rows * g.used : g.rows;
+    const int ostride = g.used + (g.shared ? 1 : 0);
+    const int act_rows = g.by_slot ? g.rows * ostride : g.rows;
+    // work-list bounds: expert | chunk << 10 in 16 bits, at most kMoeMaxList entries
+    if (g.experts + (g.shared ? 1 : 0) > kMoeMaxExperts || g.rows > kMoeMaxRows ||
+        g.experts + 1 + (g.rows * ostride) / kChunk > kMoeMaxList)
+        return hipErrorInvalidValue;
     MoeGemmArgs a{};
     a.w0 = static_cast<const uint8_t *>(g.w0);
     a.w1 = static_cast<const uint8_t *>(g.w1);
@@ -753,9 +763,10 @@ hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
     a.by_slot = g.by_slot;
     a.swiglu = g.swiglu;
     a.packed = g.packed;
+    a.shared = g.shared ? 1 : 0;
+    a.ostride = ostride;
     a.out0 = g.out0;
     a.out1 = g.out1;
-    if (g.experts > kMoeMaxExperts) return hipErrorInvalidValue;
     const int nsb = g.K / 256, mats = g.w1 ? 2 : 1, tiles = g.N / 16;
     // tiles per workgroup: as many as keep nsb * mats * tpw items near 64
     // (enough workgroups in flight; each wave walks a few pairs)
@@ -798,8 +809,9 @@ hipError_t launch_moe_pack_q4k(const void *src, void *dst, uint64_t rows, int K,
 }
 
 hipError_t launch_moe_combine(float *x, const float *eo, const float *w, int rows, int used, int H, const float *so,
-                              const float *sg, hipStream_t s) {
-    moe_combine_kernel<<<dim3((unsigned)rows, (unsigned)((H + 255) / 256)), 256, 0, s>>>(x, eo, w, rows, used, H, so, sg);
+                              const float *sg, hipStream_t s, bool shared_slot) {
+    moe_combine_kernel<<<dim3((unsigned)rows, (unsigned)((H + 255) / 256)), 256, 0, s>>>(x, eo, w, rows, used, H, so, sg,
+                                                                                         shared_slot ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -127,6 +127,8 @@ struct MoeGemm {
     int swiglu;               // out0 = SiLU(W0 y) * (W1 y)
     float *out0, *out1;       // [rows*used][N]
     int packed = 0;           // w0 / w1 in launch_moe_pack_q4k's layout
+    int shared = 0;           // expert `experts` is the shared expert: every row, output slot `used`
+                              // (activation / output rows of used + 1 slots)
 };
 // Rewrites expert-stacked Q4_K matrices [rows][K] (rows % 16 == 0) into the
 // grouped GEMM's packed layout (same byte count) in dst.
@@ -139,6 +141,6 @@ hipError_t launch_moe_route(const float *logits, int rows, int E, int used, int3
                             int32_t *counts, int32_t *arows, int32_t *aslots, float *aweights, hipStream_t s);
 hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s);
 hipError_t launch_moe_combine(float *x, const float *eo, const float *w, int rows, int used, int H, const float *so,
-                              const float *sg, hipStream_t s);
+                              const float *sg, hipStream_t s, bool shared_slot = false);
 
 }  // namespace yk

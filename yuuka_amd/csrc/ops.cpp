@@ -471,15 +471,21 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         if (K % 256 || N % 16 || K > 8192)
             return fail(YUUKA_ERR_UNSUPPORTED, "MoE expert shape %llu x %llu", (unsigned long long)N,
                         (unsigned long long)K);
-        const uint64_t rb = row_bytes(op.u[0], K), wb = E * N * rb, a = E * rows * used * 4;
-        const uint64_t x_rows = gu ? rows : rows * used;
+        // shared: expert E is the shared expert (weights of E + 1 experts), and
+        // the activation (down) and output rows have used + 1 slots
+        const uint64_t sh = (op.flags & YUUKA_EXT_FLAG_MOE_SHARED) ? 1 : 0, os = used + sh;
+        if (rows > 512 || E + sh > 1024 || E + 1 + rows * os / 8 > 2048)
+            return fail(YUUKA_ERR_UNSUPPORTED, "MoE %s: %llu rows of %llu experts (at most 512 rows, 1024 experts)",
+                        gu ? "gate/up" : "down", (unsigned long long)rows, (unsigned long long)E);
+        const uint64_t rb = row_bytes(op.u[0], K), wb = (E + sh) * N * rb, a = E * rows * used * 4;
+        const uint64_t x_rows = gu ? rows : rows * os;
         const bool swiglu = gu && (op.flags & YUUKA_EXT_FLAG_MOE_SWIGLU);
         const int ib = gu ? 3 : 2;  // counts, assign_rows, assign_slots, out...
         bool ok = buf_ok(op.buf[0], op.off[0], x_rows * K * 4) && buf_ok(op.buf[1], op.off[1], wb) &&
                   (!gu || buf_ok(op.buf[2], op.off[2], wb)) && buf_ok(op.buf[ib], op.off[ib], E * 4) &&
                   buf_ok(op.buf[ib + 1], op.off[ib + 1], a) && buf_ok(op.buf[ib + 2], op.off[ib + 2], a) &&
-                  buf_ok(op.buf[ib + 3], op.off[ib + 3], rows * used * N * 4) &&
-                  (!gu || swiglu || buf_ok(op.buf[ib + 4], op.off[ib + 4], rows * used * N * 4));
+                  buf_ok(op.buf[ib + 3], op.off[ib + 3], rows * os * N * 4) &&
+                  (!gu || swiglu || buf_ok(op.buf[ib + 4], op.off[ib + 4], rows * os * N * 4));
         if (!ok) return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE %s buffers too small", gu ? "gate/up" : "down");
         if (op.off[0] % 16 || op.off[1] % 16 || (gu && op.off[2] % 16))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE activations and weights must be 16-byte aligned");
@@ -508,10 +514,13 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
     case YUUKA_EXT_OP_MOE_COMBINE: {
         const uint64_t H = op.n[0], rows = op.n[1], used = op.n[2];
         if (!H || !rows || !used) return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid MoE combine dimensions");
-        if (!buf_ok(op.buf[0], op.off[0], rows * H * 4) || !buf_ok(op.buf[1], op.off[1], rows * used * H * 4) ||
+        const bool sh = (op.flags & YUUKA_EXT_FLAG_MOE_SHARED) != 0;  // shared output in eo slot `used`
+        if (!buf_ok(op.buf[0], op.off[0], rows * H * 4) || !buf_ok(op.buf[1], op.off[1], rows * (used + sh) * H * 4) ||
             !buf_ok(op.buf[2], op.off[2], rows * used * 4) ||
-            (op.buf[3] && (!buf_ok(op.buf[3], op.off[3], rows * H * 4) || !buf_ok(op.buf[4], op.off[4], rows * 4))))
+            (op.buf[3] && !buf_ok(op.buf[3], op.off[3], rows * H * 4)) ||
+            ((op.buf[3] || sh) && !buf_ok(op.buf[4], op.off[4], rows * 4)))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE combine buffers too small");
+        if (sh && op.buf[3]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "MoE combine: shared output in eo and buf3");
         return YUUKA_OK;
     }
     case YUUKA_EXT_OP_ADVANCE: {
@@ -732,6 +741,7 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
         g.by_slot = gu ? 0 : 1;
         g.swiglu = gu && (op.flags & YUUKA_EXT_FLAG_MOE_SWIGLU) ? 1 : 0;
         g.packed = (op.flags & YUUKA_EXT_FLAG_MOE_PACKED) ? 1 : 0;
+        g.shared = (op.flags & YUUKA_EXT_FLAG_MOE_SHARED) ? 1 : 0;
         g.out0 = at<float>(op, ib + 3);
         g.out1 = gu ? at<float>(op, ib + 4) : nullptr;
         err = launch_moe_gemm(g, ctx.ws, s);
@@ -747,7 +757,8 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
         break;
     case YUUKA_EXT_OP_MOE_COMBINE:
         err = launch_moe_combine(at<float>(op, 0), at<const float>(op, 1), at<const float>(op, 2), (int)op.n[1],
-                                 (int)op.n[2], (int)op.n[0], at<const float>(op, 3), at<const float>(op, 4), s);
+                                 (int)op.n[2], (int)op.n[0], at<const float>(op, 3), at<const float>(op, 4), s,
+                                 (op.flags & YUUKA_EXT_FLAG_MOE_SHARED) != 0);
         break;
     case YUUKA_EXT_OP_ADVANCE: {
         ModelDyn d{at<int32_t>(op, 0) + 1, 0};

@@ -241,6 +241,7 @@ def _declare(L):
         "yuuka_q35_prefill": (C.c_int, [vp, vp, C.c_int32, vp]),
         "yuuka_q35_verify": (C.c_int, [vp, vp, C.c_int32, C.POINTER(yuuka_q35_accept), vp]),
         "yuuka_q35_logits": (C.c_int, [vp, vp, C.c_int32]),
+        "yuuka_q35_moe_counts": (C.c_int, [vp, C.c_int32, vp, C.c_int32]),
         "yuuka_q35_snapshot_bytes": (C.c_uint64, [vp]),
         "yuuka_q35_snapshot": (C.c_int, [vp, vp, C.POINTER(C.c_int32)]),
         "yuuka_q35_restore": (C.c_int, [vp, vp, C.c_uint64, C.c_int32]),
@@ -285,6 +286,13 @@ class Engine:
     @property
     def position(self) -> int:
         return int(hip.lib().yuuka_q35_position(self.ptr))
+
+    def moe_counts(self, layer: int) -> np.ndarray:
+        """Rows of the last step per expert of MoE layer `layer`."""
+        out = np.zeros(self.cfg.n_experts, np.int32)
+        hip.check(hip.lib().yuuka_q35_moe_counts(self.ptr, layer, out.ctypes.data_as(C.c_void_p), len(out)),
+                  "q35_moe_counts")
+        return out
 
     @property
     def last_step_ms(self) -> float:
