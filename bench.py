@@ -597,6 +597,19 @@ def bench_batched(args, which):
 
     for _ in range(warmup):
         step()
+    routing = None
+    if cfg.n_experts:
+        # the experts the verify rows actually select, per layer, over a few
+        # untimed steps before the timed ones: the expert matrices a step streams
+        distinct, top = [], []
+        for _ in range(4):
+            step()
+            for li in range(cfg.n_layers):
+                cnt = eng.moe_counts(li)
+                distinct.append(int((cnt > 0).sum()))
+                top.append(int(cnt.max()))
+        routing = {"distinct_experts_per_layer": float(np.mean(distinct)), "max_rows_per_expert": max(top),
+                   "sample": f"4 untimed steps before the timed ones, all {cfg.n_layers} layers"}
     tokens, accepted, gpu_ms = 0, 0, []
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -606,19 +619,6 @@ def bench_batched(args, which):
         gpu_ms.append(ms)
     wall = time.perf_counter() - t0
     step_gpu_ms = float(np.median(gpu_ms))
-    routing = None
-    if cfg.n_experts:
-        # the experts the verify rows actually selected, per layer, over a few
-        # more (untimed) steps: the expert matrices a step streams
-        distinct, top = [], []
-        for _ in range(4):
-            step()
-            for li in range(cfg.n_layers):
-                cnt = eng.moe_counts(li)
-                distinct.append(int((cnt > 0).sum()))
-                top.append(int(cnt.max()))
-        routing = {"distinct_experts_per_layer": float(np.mean(distinct)), "max_rows_per_expert": max(top),
-                   "sample": f"4 steps after the timed ones, all {cfg.n_layers} layers"}
     ctx = [eng.request_position(r) for r in range(B)]
     R1 = k + 1
     kvdim = cfg.kv_heads * cfg.head_dim

@@ -302,3 +302,37 @@ def test_many_rows_pair_reduce_and_prologue_in_one_launch(dev, stream, k_a):
     y = O.rmsnorm_rows(hh, g, 1e-6)
     _check(outs[0][1].reshape(rows, f), _want(O.Q4_K, w_g, f, h, y), budget=MANY_BUDGET)
     _check(outs[0][2].reshape(rows, f), _want(O.Q6_K, w_u, f, h, y), budget=MANY_BUDGET)
+
+
+def test_many_rows_reduce_and_rmsnorm_in_one_launch(dev, stream):
+    """A split-K residual GEMM whose output the next RMSNORM_BATCH normalises
+    (out-projection -> the MoE FFN's norm) runs with the split reduction and
+    the RMSNorm in one kernel. Executed that way (plan.execute) and op by op
+    (execute_profiled, which pairs nothing), both outputs are bit-identical,
+    and they match the oracle. A narrow output (8 workgroups of channels)
+    over a deep K makes the launch split K."""
+    rng = np.random.default_rng(91)
+    rows, h, k = 40, 1024, 8192
+    x = rng.normal(0, 1, (rows, k)).astype(np.float32)
+    res0 = rng.normal(0, 2, (rows, h)).astype(np.float32)
+    g = rng.normal(1, 0.1, h).astype(np.float32)
+    w = synth.quant_matrix(rng, O.Q4_K, h, k)
+    plan = hip.Plan(dev)
+    xb, gb, wb = dev.upload(x), dev.upload(g), dev.upload(w)
+    hbuf, yb = dev.alloc(rows * h * 4), dev.alloc(rows * h * 4)
+    hip.gemm_fused_op(plan, xb, k, rows, [(wb, O.Q4_K, h, hbuf, hbuf)], hip.EPI_RESIDUAL)
+    plan.add(hip.OP["RMSNORM_BATCH"], [hbuf, gb, yb], n=[h, rows, h, h], f=[1e-6])
+    outs = []
+    for run in (plan.execute, plan.execute_profiled):
+        hbuf.write(res0)
+        run(stream)
+        stream.sync()
+        outs.append([b.read(np.float32).copy() for b in (hbuf, yb)])
+    plan.destroy()
+    for a, b in zip(*outs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    hh = outs[0][0].reshape(rows, h)
+    _check(hh - res0, _want(O.Q4_K, w, h, k, x), budget=MANY_BUDGET)
+    # the float64 sum of squares is added in a different order from the
+    # oracle's sequential one: at most a last-bit difference of the scale
+    np.testing.assert_allclose(outs[0][1].reshape(rows, h), O.rmsnorm_rows(hh, g, 1e-6), rtol=1e-6, atol=0)

@@ -71,6 +71,11 @@ hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t 
 // the residual, stores x and quantizes it for b). *fused is false, and
 // nothing is launched, when the pair does not qualify or the workspace
 // (ws_bytes) cannot hold both layouts; the caller then runs a and b apart.
+// A residual many-row GEMM (one segment) with split K: its prologue and GEMM
+// only (*split = true), the partial sums [splits][rows][n] left at *part for
+// the caller's reduction; *split = false (nothing launched) without a split.
+hipError_t launch_fused_gemm_rows_split(const FusedGemmArgs &a, void *ws, hipStream_t s, bool *split,
+                                        const float **part, uint64_t *sstride, int *splits);
 hipError_t launch_fused_gemm_rows_pair(const FusedGemmArgs &a, const FusedGemmArgs &b, void *ws, uint64_t ws_bytes,
                                        hipStream_t s, bool *fused);
 // tt: 16-row tiles per workgroup (1, 2 or 4; even for kEpiSwiglu).

@@ -845,6 +845,23 @@ hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t 
     return err;
 }
 
+hipError_t launch_fused_gemm_rows_split(const FusedGemmArgs &a, void *ws, hipStream_t s, bool *split,
+                                        const float **part, uint64_t *sstride, int *splits) {
+    *split = false;
+    if (a.epilogue != kEpiResidual || a.nseg != 1 || a.seg[0].res == nullptr) return hipSuccess;
+    BgArgs A;
+    unsigned gx, gy;
+    bg_setup(a, ws, A, gx, gy);
+    if (A.splits < 2) return hipSuccess;
+    *split = true;
+    *part = A.part;
+    *sstride = (uint64_t)a.rows * a.seg[0].n;
+    *splits = A.splits;
+    hipError_t err = bg_launch_prologue(a, A.q, BgSrc{}, s);
+    if (err == hipSuccess) err = bg_launch_gemm(A, gx, gy, false, s);
+    return err;
+}
+
 hipError_t launch_fused_gemm_rows_pair(const FusedGemmArgs &a, const FusedGemmArgs &b, void *ws, uint64_t ws_bytes,
                                        hipStream_t s, bool *fused) {
     *fused = false;

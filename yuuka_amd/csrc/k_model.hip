@@ -124,6 +124,57 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float *__restri
     for (int c = threadIdx.x; c < cols; c += 256) y[c] = __fmul_rn(__fmul_rn(x[c], scale), w[c]);
 }
 
+// A split-K residual GEMM's reduction (partials summed in split order, then
+// + residual, stored to out: bg_reduce_kernel's arithmetic) and the RMSNorm
+// of the result (rmsnorm_rows_kernel's arithmetic and summation order) in
+// one launch, bit-identical to the two kernels in turn.
+template <int P>
+__global__ __launch_bounds__(256) void reduce_rmsnorm_rows_kernel(const float *__restrict__ part, uint64_t sstride,
+                                                                  int splits, const float *res, float *out,
+                                                                  const float *__restrict__ w, float *__restrict__ dst,
+                                                                  int cols, uint64_t dst_stride, float eps) {
+    // thread t holds elements t + 256 i (i < P, cols = 256 P) in registers;
+    // each element sums its partials in split order, SG splits' loads in
+    // flight at a time, and the squares add in element order as
+    // rmsnorm_rows_kernel adds them
+    constexpr int SG = P >= 16 ? 2 : 32 / P;
+    __shared__ double red[4];
+    const uint64_t r = blockIdx.x, base = r * (uint64_t)cols;
+    float v[P];
+#pragma unroll
+    for (int i = 0; i < P; i++) v[i] = 0.f;
+    for (int s0 = 0; s0 < splits; s0 += SG) {
+        float t[SG][P];
+#pragma unroll
+        for (int j = 0; j < SG; j++)
+#pragma unroll
+            for (int i = 0; i < P; i++)
+                if (s0 + j < splits) t[j][i] = part[(uint64_t)(s0 + j) * sstride + base + threadIdx.x + 256 * i];
+#pragma unroll
+        for (int j = 0; j < SG; j++)
+#pragma unroll
+            for (int i = 0; i < P; i++)
+                if (s0 + j < splits) v[i] += t[j][i];
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+        const uint64_t o = base + threadIdx.x + 256 * i;
+        v[i] = __fadd_rn(v[i], res[o]);
+        out[o] = v[i];
+        s += (double)v[i] * (double)v[i];
+    }
+    s = block_sum256(s, red);
+    const float mean = (float)(s / (double)cols);
+    const float scale = (float)(1.0 / sqrt((double)(mean + eps)));
+    float *y = dst + r * dst_stride;
+#pragma unroll
+    for (int i = 0; i < P; i++) {
+        const int c = threadIdx.x + 256 * i;
+        y[c] = __fmul_rn(__fmul_rn(v[i], scale), w[c]);
+    }
+}
+
 // forward.go:472-482 per head: x *= scale * weight.
 __global__ __launch_bounds__(256) void rmsnorm_heads_kernel(const float *__restrict__ src, const float *__restrict__ w,
                                                             float *__restrict__ dst, int size, int heads, int stride,
@@ -468,6 +519,18 @@ hipError_t launch_embedding(const void *table, uint32_t dtype, uint64_t row_byte
 hipError_t launch_rmsnorm_rows(const float *src, const float *w, float *dst, int cols, int rows, uint64_t src_stride,
                                uint64_t dst_stride, float eps, hipStream_t s) {
     rmsnorm_rows_kernel<<<(unsigned)rows, 256, 0, s>>>(src, w, dst, cols, src_stride, dst_stride, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_reduce_rmsnorm_rows(const float *part, uint64_t sstride, int splits, const float *res, float *out,
+                                      const float *w, float *dst, int cols, int rows, uint64_t dst_stride, float eps,
+                                      hipStream_t s) {
+    auto k = cols == 1024   ? reduce_rmsnorm_rows_kernel<4>
+             : cols == 2048 ? reduce_rmsnorm_rows_kernel<8>
+             : cols == 4096 ? reduce_rmsnorm_rows_kernel<16>
+                            : nullptr;
+    if (!k) return hipErrorInvalidValue;  // the caller keeps the two kernels for other widths
+    k<<<(unsigned)rows, 256, 0, s>>>(part, sstride, splits, res, out, w, dst, cols, dst_stride, eps);
     return hipGetLastError();
 }
 

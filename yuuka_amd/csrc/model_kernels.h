@@ -48,6 +48,12 @@ hipError_t launch_embedding(const void *table, uint32_t dtype, uint64_t row_byte
                             int cols, int rows, float *out, hipStream_t s);
 hipError_t launch_rmsnorm_rows(const float *src, const float *w, float *dst, int cols, int rows, uint64_t src_stride,
                                uint64_t dst_stride, float eps, hipStream_t s);
+// bg_reduce_kernel then rmsnorm_rows_kernel in one launch: out = sum of the
+// split partials [splits][rows][cols] (split order) + res; dst = RMSNorm(out) * w.
+// cols 1024, 2048 or 4096.
+hipError_t launch_reduce_rmsnorm_rows(const float *part, uint64_t sstride, int splits, const float *res, float *out,
+                                      const float *w, float *dst, int cols, int rows, uint64_t dst_stride, float eps,
+                                      hipStream_t s);
 hipError_t launch_rmsnorm_heads(const float *src, const float *w, float *dst, int size, int heads, int stride, int rows,
                                 float eps, hipStream_t s);
 hipError_t launch_rope(float *data, int heads, int stride, int rot_dim, int rows, uint64_t row_stride, double base,

@@ -538,6 +538,27 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
 
 yuuka_status execute_gemm_pair(const yuuka_op &a, const yuuka_op &b, const ExecCtx &ctx, bool *done) {
     *done = false;
+    if (a.code == YUUKA_EXT_OP_GEMM_FUSED && b.code == YUUKA_OP_RMSNORM_BATCH && fused_many_rows(a)) {
+        // a split-K residual GEMM whose output the next op normalises (the
+        // MoE FFN's RMSNorm): the split reduction and the RMSNorm in one launch
+        const FusedGemmArgs fa = fused_args(a);
+        const uint64_t cols = b.n[0], rows = b.n[1];
+        if (fa.nseg != 1 || fa.epilogue != kEpiResidual || b.buf[0] != a.buf[6] ||
+            b.off[0] != a.off[6] || cols != (uint64_t)fa.seg[0].n || rows != (uint64_t)fa.rows ||
+            b.n[2] != cols || (cols != 1024 && cols != 2048 && cols != 4096))
+            return YUUKA_OK;
+        bool split = false;
+        const float *part = nullptr;
+        uint64_t sstride = 0;
+        int splits = 0;
+        hipError_t err = launch_fused_gemm_rows_split(fa, ctx.ws, ctx.stream, &split, &part, &sstride, &splits);
+        if (err == hipSuccess && split)
+            err = launch_reduce_rmsnorm_rows(part, sstride, splits, fa.seg[0].res, fa.seg[0].out, at<const float>(b, 1),
+                                             at<float>(b, 2), (int)cols, (int)rows, b.n[3], b.f[0], ctx.stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "GEMM_FUSED + RMSNorm launch: %s", hip_error(err));
+        *done = split;
+        return YUUKA_OK;
+    }
     if (a.code != YUUKA_EXT_OP_GEMM_FUSED || b.code != YUUKA_EXT_OP_GEMM_FUSED || !fused_many_rows(a) ||
         !fused_many_rows(b) || !ctx.ws_bytes)
         return YUUKA_OK;
