@@ -463,7 +463,6 @@ def bench_config2(args):
                           "weights": wbytes, "kv": kv_bytes, "gdn_state": state_bytes, "logits": logit_bytes},
         "roofline": dk,
         "context_end": ctx,
-        **({"moe_routing": routing} if routing else {}),
         "prefill_s": prefill_s,
         "weight_gen_s": gen_s,
         "device": info,
