@@ -336,3 +336,39 @@ def test_many_rows_reduce_and_rmsnorm_in_one_launch(dev, stream):
     # the float64 sum of squares is added in a different order from the
     # oracle's sequential one: at most a last-bit difference of the scale
     np.testing.assert_allclose(outs[0][1].reshape(rows, h), O.rmsnorm_rows(hh, g, 1e-6), rtol=1e-6, atol=0)
+
+
+def test_many_rows_swiglu_pair_reduce_and_prologue_in_one_launch(dev, stream):
+    """A split-K SwiGLU GEMM (FFN gate/up) followed by the GEMM that reads its
+    output (FFN down): the split reduction with SiLU(gate) * up and the down
+    prologue run as one kernel. Executed that way (plan.execute) and op by op
+    (execute_profiled), every output is bit-identical, and both match the
+    oracle. 68 rows (one block of five row tiles) split the gate/up launch."""
+    rng = np.random.default_rng(93)
+    rows, h, f = 68, 2048, 4096
+    x = rng.normal(0, 1, (rows, h)).astype(np.float32)
+    res0 = rng.normal(0, 2, (rows, h)).astype(np.float32)
+    g = rng.normal(1, 0.1, h).astype(np.float32)
+    w_g, w_u = synth.quant_matrix(rng, O.Q4_K, f, h), synth.quant_matrix(rng, O.Q4_K, f, h)
+    w_d = synth.quant_matrix(rng, O.Q4_K, h, f)
+    plan = hip.Plan(dev)
+    xb, gb = dev.upload(x), dev.upload(g)
+    wg, wu, wd = dev.upload(w_g), dev.upload(w_u), dev.upload(w_d)
+    hb, ob = dev.alloc(rows * f * 4), dev.alloc(rows * h * 4)
+    hip.gemm_fused_op(plan, xb, h, rows, [(wg, O.Q4_K, f, hb, None), (wu, O.Q4_K, f, None, None)], hip.EPI_SWIGLU,
+                      norm=gb)
+    hip.gemm_fused_op(plan, hb, f, rows, [(wd, O.Q4_K, h, ob, ob)], hip.EPI_RESIDUAL)
+    outs = []
+    for run in (plan.execute, plan.execute_profiled):
+        ob.write(res0)
+        run(stream)
+        stream.sync()
+        outs.append([b.read(np.float32).copy() for b in (hb, ob)])
+    plan.destroy()
+    for a, b in zip(*outs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    y = O.rmsnorm_rows(x, g, 1e-6)
+    hh = outs[0][0].reshape(rows, f)
+    want_h = O.silu_mul(_want(O.Q4_K, w_g, f, h, y), _want(O.Q4_K, w_u, f, h, y))
+    _check(hh, want_h, budget=MANY_BUDGET * 4)
+    _check(outs[0][1].reshape(rows, h) - res0, _want(O.Q4_K, w_d, h, f, hh), budget=MANY_BUDGET)

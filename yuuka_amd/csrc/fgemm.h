@@ -65,19 +65,23 @@ int fused_gemm_stream_rows(int K, bool norm, bool gated);
 // (the quantized activations and split-K partial sums).
 uint64_t fused_gemm_rows_ws(int rows, int K, const int *n, int nseg, bool swiglu);
 hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t s);
-// Two consecutive many-row launches where b normalises a's residual output
-// (b.x == a's single output, b.K == its width): a's split reduction and b's
-// prologue run as one kernel (one workgroup per row sums the splits, adds
-// the residual, stores x and quantizes it for b). *fused is false, and
-// nothing is launched, when the pair does not qualify or the workspace
-// (ws_bytes) cannot hold both layouts; the caller then runs a and b apart.
-// A residual many-row GEMM (one segment) with split K: its prologue and GEMM
-// only (*split = true), the partial sums [splits][rows][n] left at *part for
-// the caller's reduction; *split = false (nothing launched) without a split.
-hipError_t launch_fused_gemm_rows_split(const FusedGemmArgs &a, void *ws, hipStream_t s, bool *split,
-                                        const float **part, uint64_t *sstride, int *splits);
-hipError_t launch_fused_gemm_rows_pair(const FusedGemmArgs &a, const FusedGemmArgs &b, void *ws, uint64_t ws_bytes,
-                                       hipStream_t s, bool *fused);
+// A run of many-row GEMMs (rows > 8) launched in turn. Where g[i] splits K
+// and g[i + 1] normalises g[i]'s residual output, or reads g[i]'s SwiGLU
+// output as it is, g[i]'s split reduction runs inside g[i + 1]'s prologue
+// (bit-identical to the separate reduce). Every member's quantized rows sit
+// at the start of ws and its partial sums at part_off (at least the largest
+// member's quantized rows). defer_last: when the last member is a split
+// residual GEMM its reduction is left to the caller (*last).
+struct BgDeferred {
+    bool on;
+    const float *part;  // [splits][rows][n]
+    uint64_t sstride;
+    int splits;
+};
+hipError_t launch_fused_gemm_rows_chain(const FusedGemmArgs *g, int n, void *ws, uint64_t part_off, bool defer_last,
+                                        hipStream_t s, BgDeferred *last);
+// Workspace of launch_fused_gemm_rows in two parts: quantized rows, partial sums.
+void fused_gemm_rows_ws_parts(int rows, int K, const int *n, int nseg, bool swiglu, uint64_t *quant, uint64_t *part);
 // tt: 16-row tiles per workgroup (1, 2 or 4; even for kEpiSwiglu).
 hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s);
 

@@ -135,11 +135,13 @@ constexpr int kPrThreads = 512;
 // partial sums of the previous many-row GEMM, which the prologue finishes as
 // bg_reduce_kernel would (sum in split order, + residual) and stores to out.
 struct BgSrc {
-    const float *part;  // [splits][rows][K]
-    const float *res;   // [rows][K] residual of the previous GEMM (may alias out)
+    const float *part;  // [splits][rows][prow]
+    const float *res;   // [rows][K] residual of the previous GEMM (may alias out), or null
     float *out;         // [rows][K] the previous GEMM's output
-    uint64_t sstride;   // floats between splits (rows * K)
+    uint64_t sstride;   // floats between splits (rows * prow)
     int splits;
+    int swiglu;         // the previous GEMM's SwiGLU: gate columns [0, K), up [K, 2K) of each part row
+    uint64_t prow;      // floats between rows of part (K, or 2K with swiglu)
 };
 
 // One row per workgroup. Wave w owns super-blocks w, w + 8, ... (at most P
@@ -153,8 +155,11 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
     const int row = blockIdx.x, K = A.K, nsb = K / 256;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint64_t rbase = (uint64_t)row * K;
-    auto elem = [&](int i) { return (wave + W * i) * 256 + 4 * lane; };
-    auto live = [&](int i) { return wave + W * i < nsb; };
+    // super-blocks [sb0, sb0 + W P) of the row: all of them when the row's
+    // RMSNorm needs the whole row, else one group per workgroup (grid y)
+    const int sb0 = (int)blockIdx.y * W * P;
+    auto elem = [&](int i) { return (sb0 + wave + W * i) * 256 + 4 * lane; };
+    auto live = [&](int i) { return sb0 + wave + W * i < nsb; };
     auto add4 = [](float4 &v, const float4 &w) {
         v.x += w.x;
         v.y += w.y;
@@ -162,7 +167,44 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
         v.w += w.w;
     };
     float4 v[P], nw[P], z[P];
-    if (src.part) {
+    if (src.part && src.swiglu) {
+        // the previous GEMM's gate and up partial sums, each added in split
+        // order, then SiLU(gate) * up (bg_reduce_kernel's arithmetic)
+        constexpr int SG = P >= 4 ? 1 : 8 / P;
+        float4 u[P];
+        const uint64_t pbase = (uint64_t)row * src.prow;
+#pragma unroll
+        for (int i = 0; i < P; i++) v[i] = u[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int s0 = 0; s0 < src.splits; s0 += SG) {
+            float4 tg[SG][P], tu[SG][P];
+#pragma unroll
+            for (int j = 0; j < SG; j++)
+#pragma unroll
+                for (int i = 0; i < P; i++)
+                    if (s0 + j < src.splits && live(i)) {
+                        const float *q = src.part + (uint64_t)(s0 + j) * src.sstride + pbase + elem(i);
+                        tg[j][i] = *reinterpret_cast<const float4 *>(q);
+                        tu[j][i] = *reinterpret_cast<const float4 *>(q + K);
+                    }
+#pragma unroll
+            for (int j = 0; j < SG; j++)
+#pragma unroll
+                for (int i = 0; i < P; i++)
+                    if (s0 + j < src.splits && live(i)) {
+                        add4(v[i], tg[j][i]);
+                        add4(u[i], tu[j][i]);
+                    }
+        }
+#pragma unroll
+        for (int i = 0; i < P; i++)
+            if (live(i)) {
+                v[i].x = __fmul_rn(silu_ref(v[i].x), u[i].x);
+                v[i].y = __fmul_rn(silu_ref(v[i].y), u[i].y);
+                v[i].z = __fmul_rn(silu_ref(v[i].z), u[i].z);
+                v[i].w = __fmul_rn(silu_ref(v[i].w), u[i].w);
+                *reinterpret_cast<float4 *>(src.out + rbase + elem(i)) = v[i];
+            }
+    } else if (src.part) {
         // the previous GEMM's split partial sums, added in split order, then
         // its residual; 16 loads in flight at a time
         constexpr int SG = P >= 8 ? 2 : 16 / P;
@@ -230,7 +272,7 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
 #pragma unroll
     for (int i = 0; i < P; i++) {
         if (!live(i)) break;  // wave-uniform
-        const int sb = wave + W * i, e = elem(i);
+        const int sb = sb0 + wave + W * i, e = elem(i);
         float4 y = v[i];
         if (A.gate) {
             // recurrent.go:39-50 gated head norm over heads of 128 (lanes 0..31
@@ -775,6 +817,17 @@ static void bg_grid(const int *n, int nseg, bool swiglu, int rows, int K, unsign
     *splits = bg_splits((int)(x * *gy), K / 256, nt);
 }
 
+void fused_gemm_rows_ws_parts(int rows, int K, const int *n, int nseg, bool swiglu, uint64_t *quant,
+                              uint64_t *part) {
+    unsigned gx, gy;
+    int splits;
+    bg_grid(n, nseg, swiglu, rows, K, &gx, &gy, &splits);
+    int ncol = 0;
+    for (int i = 0; i < nseg; i++) ncol += n[i];
+    *quant = bg_quant_bytes(rows, K);
+    *part = splits > 1 ? (uint64_t)splits * rows * ncol * 4 : 0;
+}
+
 uint64_t fused_gemm_rows_ws(int rows, int K, const int *n, int nseg, bool swiglu) {
     unsigned gx, gy;
     int splits;
@@ -786,7 +839,8 @@ uint64_t fused_gemm_rows_ws(int rows, int K, const int *n, int nseg, bool swiglu
 }
 
 // The arguments, grid and workspace view of one many-row launch.
-static void bg_setup(const FusedGemmArgs &a, void *ws, BgArgs &A, unsigned &gx, unsigned &gy) {
+static void bg_setup(const FusedGemmArgs &a, void *ws, BgArgs &A, unsigned &gx, unsigned &gy,
+                     uint64_t part_off = 0) {
     A = BgArgs{};
     A.f = a;
     A.q = bg_view(ws, a.rows, a.K);
@@ -801,13 +855,20 @@ static void bg_setup(const FusedGemmArgs &a, void *ws, BgArgs &A, unsigned &gx, 
     A.cols[0] = 0;
     for (int i = 0; i < a.nseg; i++) A.cols[i + 1] = A.cols[i] + a.seg[i].n;
     for (int i = a.nseg + 1; i <= kFusedMaxSeg; i++) A.cols[i] = A.cols[a.nseg];
-    A.part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) + ((bg_quant_bytes(a.rows, a.K) + 255) & ~255ull));
+    // split partial sums after the quantized rows, or at part_off (a chain's
+    // common offset, past every member's quantized rows)
+    A.part = reinterpret_cast<float *>(static_cast<uint8_t *>(ws) +
+                                       (part_off ? part_off : (bg_quant_bytes(a.rows, a.K) + 255) & ~255ull));
 }
 
 static hipError_t bg_launch_prologue(const FusedGemmArgs &a, const BgQuant &q, const BgSrc &src, hipStream_t s) {
-    // super-blocks per wave, rounded up to an instantiated register count
-    const int per = (a.K / 256 + kPrThreads / 64 - 1) / (kPrThreads / 64);
-    const dim3 grid((unsigned)a.rows);
+    // super-blocks per wave, rounded up to an instantiated register count;
+    // without the row RMSNorm (plain x, or the gated head norm inside each
+    // super-block) a row's super-blocks spread over workgroups, one per wave
+    const int nsb = a.K / 256, W = kPrThreads / 64;
+    const bool whole_row = a.norm != nullptr && a.gate == nullptr;
+    const int per = whole_row ? (nsb + W - 1) / W : 1;
+    const dim3 grid((unsigned)a.rows, whole_row ? 1u : (unsigned)((nsb + W - 1) / W));
     switch (per) {
     case 1: bg_prologue_kernel<1><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
     case 2: bg_prologue_kernel<2><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
@@ -845,51 +906,42 @@ hipError_t launch_fused_gemm_rows(const FusedGemmArgs &a, void *ws, hipStream_t 
     return err;
 }
 
-hipError_t launch_fused_gemm_rows_split(const FusedGemmArgs &a, void *ws, hipStream_t s, bool *split,
-                                        const float **part, uint64_t *sstride, int *splits) {
-    *split = false;
-    if (a.epilogue != kEpiResidual || a.nseg != 1 || a.seg[0].res == nullptr) return hipSuccess;
-    BgArgs A;
-    unsigned gx, gy;
-    bg_setup(a, ws, A, gx, gy);
-    if (A.splits < 2) return hipSuccess;
-    *split = true;
-    *part = A.part;
-    *sstride = (uint64_t)a.rows * a.seg[0].n;
-    *splits = A.splits;
-    hipError_t err = bg_launch_prologue(a, A.q, BgSrc{}, s);
-    if (err == hipSuccess) err = bg_launch_gemm(A, gx, gy, false, s);
-    return err;
+// Whether b's prologue can take a's split partial sums: a residual GEMM
+// whose output b normalises, or a SwiGLU GEMM whose output b reads as it is
+// (FFN gate/up -> down).
+static bool bg_link(const FusedGemmArgs &a, const FusedGemmArgs &b) {
+    const bool res_pair = a.epilogue == kEpiResidual && a.nseg == 1 && a.seg[0].res != nullptr && b.norm != nullptr;
+    const bool glu_pair = a.epilogue == kEpiSwiglu && a.nseg == 2 && b.norm == nullptr;
+    return (res_pair || glu_pair) && b.rows == a.rows && b.K == a.seg[0].n && b.x == a.seg[0].out &&
+           b.gate == nullptr && b.K % 256 == 0;
 }
 
-hipError_t launch_fused_gemm_rows_pair(const FusedGemmArgs &a, const FusedGemmArgs &b, void *ws, uint64_t ws_bytes,
-                                       hipStream_t s, bool *fused) {
-    *fused = false;
-    if (a.epilogue != kEpiResidual || a.nseg != 1 || a.seg[0].res == nullptr || b.rows != a.rows ||
-        b.K != a.seg[0].n || b.x != a.seg[0].out || b.norm == nullptr || b.gate != nullptr || b.K % 256)
-        return hipSuccess;
-    BgArgs A;
-    unsigned gx, gy;
-    bg_setup(a, ws, A, gx, gy);
-    if (A.splits < 2) return hipSuccess;
-    // b's workspace: from the start when its quantized rows end before a's
-    // partial sums, else after them
-    const uint64_t part_off = (bg_quant_bytes(a.rows, a.K) + 255) & ~255ull;
-    const uint64_t part_bytes = (uint64_t)A.splits * a.rows * a.seg[0].n * 4;
-    const uint64_t b_off = bg_quant_bytes(b.rows, b.K) <= part_off ? 0 : (part_off + part_bytes + 255) & ~255ull;
-    int nb[kFusedMaxSeg];
-    for (int i = 0; i < b.nseg; i++) nb[i] = b.seg[i].n;
-    if (b_off + fused_gemm_rows_ws(b.rows, b.K, nb, b.nseg, b.epilogue == kEpiSwiglu) > ws_bytes) return hipSuccess;
-    BgArgs B;
-    unsigned bx, by;
-    bg_setup(b, static_cast<uint8_t *>(ws) + b_off, B, bx, by);
-    *fused = true;
-    const BgSrc src{A.part, a.seg[0].res, a.seg[0].out, (uint64_t)a.rows * a.seg[0].n, A.splits};
-    hipError_t err = bg_launch_prologue(a, A.q, BgSrc{}, s);
-    if (err == hipSuccess) err = bg_launch_gemm(A, gx, gy, false, s);
-    if (err == hipSuccess) err = bg_launch_prologue(b, B.q, src, s);
-    if (err == hipSuccess) err = bg_launch_gemm(B, bx, by, true, s);
-    return err;
+hipError_t launch_fused_gemm_rows_chain(const FusedGemmArgs *g, int n, void *ws, uint64_t part_off, bool defer_last,
+                                        hipStream_t s, BgDeferred *last) {
+    *last = BgDeferred{};
+    BgSrc src{};  // the previous member's partials, when this member's prologue takes them
+    for (int i = 0; i < n; i++) {
+        const FusedGemmArgs &a = g[i];
+        BgArgs A;
+        unsigned gx, gy;
+        bg_setup(a, ws, A, gx, gy, part_off);
+        const bool link = A.splits > 1 && i + 1 < n && bg_link(a, g[i + 1]);
+        const bool defer = A.splits > 1 && i + 1 == n && defer_last && a.epilogue == kEpiResidual && a.nseg == 1 &&
+                           a.seg[0].res != nullptr;
+        hipError_t err = bg_launch_prologue(a, A.q, src, s);
+        if (err == hipSuccess) err = bg_launch_gemm(A, gx, gy, !(link || defer), s);
+        if (err != hipSuccess) return err;
+        src = BgSrc{};
+        if (link) {
+            const bool glu = a.epilogue == kEpiSwiglu;
+            src = BgSrc{A.part,    glu ? nullptr : a.seg[0].res,
+                        a.seg[0].out, (uint64_t)a.rows * A.cols[a.nseg],
+                        A.splits,  glu ? 1 : 0,
+                        (uint64_t)A.cols[a.nseg]};
+        }
+        if (defer) *last = BgDeferred{true, A.part, (uint64_t)a.rows * a.seg[0].n, A.splits};
+    }
+    return hipSuccess;
 }
 
 }  // namespace yk

@@ -536,35 +536,40 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
     }
 }
 
-yuuka_status execute_gemm_pair(const yuuka_op &a, const yuuka_op &b, const ExecCtx &ctx, bool *done) {
-    *done = false;
-    if (a.code == YUUKA_EXT_OP_GEMM_FUSED && b.code == YUUKA_OP_RMSNORM_BATCH && fused_many_rows(a)) {
-        // a split-K residual GEMM whose output the next op normalises (the
-        // MoE FFN's RMSNorm): the split reduction and the RMSNorm in one launch
-        const FusedGemmArgs fa = fused_args(a);
-        const uint64_t cols = b.n[0], rows = b.n[1];
-        if (fa.nseg != 1 || fa.epilogue != kEpiResidual || b.buf[0] != a.buf[6] ||
-            b.off[0] != a.off[6] || cols != (uint64_t)fa.seg[0].n || rows != (uint64_t)fa.rows ||
-            b.n[2] != cols || (cols != 1024 && cols != 2048 && cols != 4096))
-            return YUUKA_OK;
-        bool split = false;
-        const float *part = nullptr;
-        uint64_t sstride = 0;
-        int splits = 0;
-        hipError_t err = launch_fused_gemm_rows_split(fa, ctx.ws, ctx.stream, &split, &part, &sstride, &splits);
-        if (err == hipSuccess && split)
-            err = launch_reduce_rmsnorm_rows(part, sstride, splits, fa.seg[0].res, fa.seg[0].out, at<const float>(b, 1),
-                                             at<float>(b, 2), (int)cols, (int)rows, b.n[3], b.f[0], ctx.stream);
-        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "GEMM_FUSED + RMSNorm launch: %s", hip_error(err));
-        *done = split;
-        return YUUKA_OK;
+bool gemm_chain_member(const yuuka_op &op) { return op.code == YUUKA_EXT_OP_GEMM_FUSED && fused_many_rows(op); }
+
+bool gemm_chain_ws(const yuuka_op &op, uint64_t *quant, uint64_t *part) {
+    if (!gemm_chain_member(op)) return false;
+    const int nseg = fused_segments(op);
+    int nn[kFusedMaxSeg] = {0, 0, 0, 0};
+    for (int i = 0; i < nseg; i++) nn[i] = (int)op.n[2 + i];
+    fused_gemm_rows_ws_parts((int)op.n[1], (int)op.n[0], nn, nseg, op.u[1] == kEpiSwiglu, quant, part);
+    return true;
+}
+
+yuuka_status execute_gemm_chain(const yuuka_op *ops, int n, const yuuka_op *after, const ExecCtx &ctx,
+                                bool *after_done) {
+    *after_done = false;
+    std::vector<FusedGemmArgs> g(n);
+    for (int i = 0; i < n; i++) g[i] = fused_args(ops[i]);
+    // the last member's split reduction inside the next op's RMSNorm of its
+    // output (the MoE FFN norm after the out-projection)
+    const yuuka_op &l = ops[n - 1];
+    const FusedGemmArgs &la = g[n - 1];
+    const bool norm_next = after && after->code == YUUKA_OP_RMSNORM_BATCH && la.nseg == 1 &&
+                           la.epilogue == kEpiResidual && after->buf[0] == l.buf[6] && after->off[0] == l.off[6] &&
+                           after->n[0] == (uint64_t)la.seg[0].n && after->n[1] == (uint64_t)la.rows &&
+                           after->n[2] == after->n[0] &&
+                           (after->n[0] == 1024 || after->n[0] == 2048 || after->n[0] == 4096);
+    BgDeferred last{};
+    hipError_t err = launch_fused_gemm_rows_chain(g.data(), n, ctx.ws, ctx.part_off, norm_next, ctx.stream, &last);
+    if (err == hipSuccess && last.on) {
+        err = launch_reduce_rmsnorm_rows(last.part, last.sstride, last.splits, la.seg[0].res, la.seg[0].out,
+                                         at<const float>(*after, 1), at<float>(*after, 2), (int)after->n[0],
+                                         (int)after->n[1], after->n[3], after->f[0], ctx.stream);
+        *after_done = true;
     }
-    if (a.code != YUUKA_EXT_OP_GEMM_FUSED || b.code != YUUKA_EXT_OP_GEMM_FUSED || !fused_many_rows(a) ||
-        !fused_many_rows(b) || !ctx.ws_bytes)
-        return YUUKA_OK;
-    const FusedGemmArgs fa = fused_args(a), fb = fused_args(b);
-    const hipError_t err = launch_fused_gemm_rows_pair(fa, fb, ctx.ws, ctx.ws_bytes, ctx.stream, done);
-    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "GEMM_FUSED pair launch: %s", hip_error(err));
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "GEMM_FUSED run launch: %s", hip_error(err));
     return YUUKA_OK;
 }
 

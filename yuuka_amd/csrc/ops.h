@@ -20,10 +20,17 @@ bool op_uses_position(const yuuka_op &op);
 // result), 1 when there is none to merge.
 int gdn_commit_run(const yuuka_op *ops, int count);
 yuuka_status execute_gdn_commit_run(const yuuka_op *ops, int count, const ExecCtx &ctx);
-// Two consecutive GEMM_FUSED ops over more than 8 rows where b normalises a's
-// residual output run with a's split reduction and b's prologue in one
-// launch; *done is false when they do not qualify (nothing was launched).
-yuuka_status execute_gemm_pair(const yuuka_op &a, const yuuka_op &b, const ExecCtx &ctx, bool *done);
+// GEMM_FUSED over more than 8 rows (the many-row kernel), and its workspace
+// in two parts (quantized rows, split partial sums).
+bool gemm_chain_member(const yuuka_op &op);
+bool gemm_chain_ws(const yuuka_op &op, uint64_t *quant, uint64_t *part);
+// A run of n consecutive many-row GEMM_FUSED ops (launch_fused_gemm_rows_chain:
+// each split reduction inside the next member's prologue where they link),
+// with ctx.part_off the run's common partial-sum offset. `after` (may be
+// null) is the op that follows the run: an RMSNORM_BATCH of the last
+// member's residual output takes its split reduction too (*after_done).
+yuuka_status execute_gemm_chain(const yuuka_op *ops, int n, const yuuka_op *after, const ExecCtx &ctx,
+                                bool *after_done);
 
 // Elementwise launchers (k_ops.hip).
 hipError_t launch_copy_f32(float *dst, const float *src, uint64_t n, hipStream_t stream);

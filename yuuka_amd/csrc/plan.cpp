@@ -189,6 +189,7 @@ static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token,
                             const int32_t *dyn, int run_tail, uint32_t *codes, uint64_t *times,
                             uint64_t capacity, uint64_t *count) {
     ExecCtx ctx{stream, token, position, dyn, plan->ws, plan->tickets, plan->ws_bytes};
+    ctx.part_off = plan->chain_quant ? (plan->chain_quant + 255) & ~255ull : 0;
     uint64_t n = 0;
     hipEvent_t a = nullptr, b = nullptr;
     if (times) {
@@ -224,19 +225,24 @@ static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token,
                 break;
             }
         if (st != YUUKA_OK) break;
-        if (!times && op.code == YUUKA_EXT_OP_GEMM_FUSED && oi + 1 < nops &&
-            !((plan->ops[oi + 1].flags & YUUKA_OP_FLAG_TAIL) && !run_tail)) {
-            // a many-row GEMM whose residual output the next one normalises:
-            // the split reduction and the next prologue in one launch
-            const yuuka_op &nx = plan->ops[oi + 1];
-            bool live = true;
-            for (int i = 0; i < 16; i++) live = live && (!nx.buf[i] || nx.buf[i]->ptr);
-            bool done = false;
-            if (live) st = execute_gemm_pair(op, nx, ctx, &done);
-            if (st != YUUKA_OK) break;
-            if (done) {
-                n += 2;
-                oi += 1;
+        if (!times && ctx.part_off && gemm_chain_member(op)) {
+            // a run of many-row GEMMs: split reductions inside the next
+            // member's prologue (and a following RMSNorm of the last output)
+            auto usable = [&](int k) {
+                if ((plan->ops[k].flags & YUUKA_OP_FLAG_TAIL) && !run_tail) return false;
+                for (int i = 0; i < 16; i++)
+                    if (plan->ops[k].buf[i] && !plan->ops[k].buf[i]->ptr) return false;
+                return true;
+            };
+            int j = 1;
+            while (oi + j < nops && gemm_chain_member(plan->ops[oi + j]) && usable(oi + j)) j++;
+            const yuuka_op *after = oi + j < nops && usable(oi + j) ? &plan->ops[oi + j] : nullptr;
+            if (j > 1 || (after && after->code == YUUKA_OP_RMSNORM_BATCH)) {
+                bool after_done = false;
+                st = execute_gemm_chain(&plan->ops[oi], j, after, ctx, &after_done);
+                if (st != YUUKA_OK) break;
+                n += j + (after_done ? 1 : 0);
+                oi += j - 1 + (after_done ? 1 : 0);
                 continue;
             }
         }
@@ -316,6 +322,12 @@ yuuka_status yuuka_plan_add(yuuka_plan *plan, const yuuka_op *op) {
         if (st != YUUKA_OK) return st;
         plan->ops.push_back(*op);
         plan->ws_need = std::max(plan->ws_need, need.ws);
+        uint64_t q = 0, p = 0;
+        if (gemm_chain_ws(*op, &q, &p)) {  // runs of them share one layout
+            plan->chain_quant = std::max(plan->chain_quant, q);
+            plan->chain_part = std::max(plan->chain_part, p);
+            plan->ws_need = std::max<uint64_t>(plan->ws_need, ((plan->chain_quant + 255) & ~255ull) + plan->chain_part + 256);
+        }
         plan->ticket_need = std::max(plan->ticket_need, need.tickets);
         return YUUKA_OK;
     });

@@ -9,6 +9,8 @@ struct yuuka_plan {
     yuuka_device *dev = nullptr;
     std::vector<yuuka_op> ops;
     uint64_t ws_need = 0;      // bytes of op workspace (max over ops)
+    uint64_t chain_quant = 0;  // many-row GEMMs: largest quantized-row area
+    uint64_t chain_part = 0;   // and largest split partial-sum area (chained layout)
     uint32_t ticket_need = 0;  // split-K tickets (max over ops)
     void *ws = nullptr;
     uint64_t ws_bytes = 0;
@@ -50,6 +52,7 @@ struct ExecCtx {
     void *ws;
     uint32_t *tickets;
     uint64_t ws_bytes = 0;  // size of ws (0: unknown, no op pairs fused)
+    uint64_t part_off = 0;  // many-row GEMM runs: partial sums at ws + part_off (0: not chained)
 };
 
 }  // namespace yk
