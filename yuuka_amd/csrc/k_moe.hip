@@ -70,9 +70,11 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {  // values >= 0
 // ---------------------------------------------------------------- router
 // logits[r][e] = W[e] . y[r] (FP32 weights, ffn_gate_inp) and, when `sv` is
 // given, extra[r] = sv . y[r] (ffn_gate_inp_shexp, forward.go:385). One
-// workgroup per (expert row, block of 8 rows) (the shared gate vector is
-// row E); each of its four waves takes two rows so that their loads overlap.
+// workgroup per (block of kRouterExperts expert rows, block of 8 rows) (the
+// shared gate vector is row E); each of its four waves takes two rows and
+// reuses their loads for the block's expert rows.
 constexpr int kRouterWaves = 4;
+constexpr int kRouterExperts = 4;
 
 __global__ __launch_bounds__(64 * kRouterWaves) void moe_router_kernel(const float *__restrict__ y, int H, int rows,
                                                                        const float *__restrict__ w, int E,
@@ -80,31 +82,43 @@ __global__ __launch_bounds__(64 * kRouterWaves) void moe_router_kernel(const flo
                                                                        const float *__restrict__ sv,
                                                                        float *__restrict__ extra) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int e = blockIdx.x;
-    const float *wr = e < E ? w + (uint64_t)e * H : sv;
-    {
-        const int r = blockIdx.y * 2 * kRouterWaves + wave, r2 = r + kRouterWaves;
-        if (r >= rows) return;
-        const bool two = r2 < rows;
-        const float *y0 = y + (uint64_t)r * H, *y1 = y + (uint64_t)(two ? r2 : r) * H;
-        float a0 = 0.f, a1 = 0.f;
-#pragma unroll 4
-        for (int k = 4 * lane; k < H; k += 256) {
-            const float4 wv = *reinterpret_cast<const float4 *>(wr + k);
-            const float4 b0 = *reinterpret_cast<const float4 *>(y0 + k);
-            const float4 b1 = *reinterpret_cast<const float4 *>(y1 + k);
-            a0 += wv.x * b0.x + wv.y * b0.y + wv.z * b0.z + wv.w * b0.w;
-            a1 += wv.x * b1.x + wv.y * b1.y + wv.z * b1.z + wv.w * b1.w;
+    const int e0 = blockIdx.x * kRouterExperts, ne = E + (sv ? 1 : 0);
+    const int r = blockIdx.y * 2 * kRouterWaves + wave, r2 = r + kRouterWaves;
+    if (r >= rows) return;
+    const bool two = r2 < rows;
+    const float *y0 = y + (uint64_t)r * H, *y1 = y + (uint64_t)(two ? r2 : r) * H;
+    const float *wr[kRouterExperts];
+#pragma unroll
+    for (int x = 0; x < kRouterExperts; x++) {
+        const int e = min(e0 + x, ne - 1);
+        wr[x] = e < E ? w + (uint64_t)e * H : sv;
+    }
+    float a0[kRouterExperts], a1[kRouterExperts];
+#pragma unroll
+    for (int x = 0; x < kRouterExperts; x++) a0[x] = a1[x] = 0.f;
+#pragma unroll 2
+    for (int k = 4 * lane; k < H; k += 256) {
+        const float4 b0 = *reinterpret_cast<const float4 *>(y0 + k);
+        const float4 b1 = *reinterpret_cast<const float4 *>(y1 + k);
+#pragma unroll
+        for (int x = 0; x < kRouterExperts; x++) {
+            const float4 wv = *reinterpret_cast<const float4 *>(wr[x] + k);
+            a0[x] += wv.x * b0.x + wv.y * b0.y + wv.z * b0.z + wv.w * b0.w;
+            a1[x] += wv.x * b1.x + wv.y * b1.y + wv.z * b1.z + wv.w * b1.w;
         }
-        a0 = wave_sum(a0);
-        a1 = wave_sum(a1);
+    }
+#pragma unroll
+    for (int x = 0; x < kRouterExperts; x++) {
+        const int e = e0 + x;
+        if (e >= ne) break;
+        const float s0 = wave_sum(a0[x]), s1 = wave_sum(a1[x]);
         if (lane == 0) {
             if (e < E) {
-                logits[(uint64_t)r * E + e] = a0;
-                if (two) logits[(uint64_t)r2 * E + e] = a1;
+                logits[(uint64_t)r * E + e] = s0;
+                if (two) logits[(uint64_t)r2 * E + e] = s1;
             } else {
-                extra[r] = a0;
-                if (two) extra[r2] = a1;
+                extra[r] = s0;
+                if (two) extra[r2] = s1;
             }
         }
     }
@@ -724,7 +738,8 @@ uint64_t moe_gemm_ws(int act_rows, int K) { return (uint64_t)act_rows * K * 2 + 
 hipError_t launch_moe_router(const float *y, int H, int rows, const float *w, int E, float *logits, const float *sv,
                              float *extra, hipStream_t s) {
     const int n = E + (sv ? 1 : 0);
-    moe_router_kernel<<<dim3((unsigned)n, (unsigned)((rows + 2 * kRouterWaves - 1) / (2 * kRouterWaves))),
+    moe_router_kernel<<<dim3((unsigned)((n + kRouterExperts - 1) / kRouterExperts),
+                             (unsigned)((rows + 2 * kRouterWaves - 1) / (2 * kRouterWaves))),
                         64 * kRouterWaves, 0, s>>>(y, H, rows, w, E, logits, sv, extra);
     return hipGetLastError();
 }
