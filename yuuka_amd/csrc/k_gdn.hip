@@ -661,9 +661,26 @@ __device__ __forceinline__ void gdn_commit_cols_body(float *__restrict__ conv_st
     }
     const int p = lane & 7, j = cb * kCols + wave * 8 + (lane >> 3);
     float *mat = state + (uint64_t)h * kS * kS;
-    float s_reg[16];
+    // the block's 128 x 32 state tile through LDS: 16-byte loads of whole
+    // 128-byte row pieces (eight rows per wave instruction), then each thread
+    // takes its column's 16 rows
+    __shared__ float tile[kS][kCols + 1];
+    {
+        float4 v4[kS * kCols / 4 / kColThreads];
 #pragma unroll
-    for (int ii = 0; ii < 16; ii++) s_reg[ii] = mat[(uint64_t)(p * 16 + ii) * kS + j];
+        for (int it = 0; it < kS * kCols / 4 / kColThreads; it++) {
+            const int idx = t + kColThreads * it, row = idx >> 3, c4 = idx & 7;
+            v4[it] = *reinterpret_cast<const float4 *>(mat + (uint64_t)row * kS + cb * kCols + 4 * c4);
+        }
+#pragma unroll
+        for (int it = 0; it < kS * kCols / 4 / kColThreads; it++) {
+            const int idx = t + kColThreads * it, row = idx >> 3, c4 = idx & 7;
+            tile[row][4 * c4] = v4[it].x;
+            tile[row][4 * c4 + 1] = v4[it].y;
+            tile[row][4 * c4 + 2] = v4[it].z;
+            tile[row][4 * c4 + 3] = v4[it].w;
+        }
+    }
     // the accepted rows' k, v (this block's columns), decay and beta, staged
     // once so that the serial row loop reads LDS only
     __shared__ float sk_rows[kMaxRows][kS], sv_rows[kMaxRows][kCols], scf[2][kMaxRows];
@@ -678,6 +695,9 @@ __device__ __forceinline__ void gdn_commit_cols_body(float *__restrict__ conv_st
         scf[1][t] = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
     }
     __syncthreads();
+    float s_reg[16];
+#pragma unroll
+    for (int ii = 0; ii < 16; ii++) s_reg[ii] = tile[p * 16 + ii][j - cb * kCols];
     for (int r = 0; r < n; r++) {
         const float *k = sk_rows[r];
         const float decay = scf[0][r], beta = scf[1][r];
@@ -696,8 +716,16 @@ __device__ __forceinline__ void gdn_commit_cols_body(float *__restrict__ conv_st
 #pragma unroll
         for (int ii = 0; ii < 16; ii++) s_reg[ii] = __fadd_rn(s_reg[ii], __fmul_rn(kr[ii], d));
     }
+    __syncthreads();  // every thread has read its column from the tile
 #pragma unroll
-    for (int ii = 0; ii < 16; ii++) mat[(uint64_t)(p * 16 + ii) * kS + j] = s_reg[ii];
+    for (int ii = 0; ii < 16; ii++) tile[p * 16 + ii][j - cb * kCols] = s_reg[ii];
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < kS * kCols / 4 / kColThreads; it++) {
+        const int idx = t + kColThreads * it, row = idx >> 3, c4 = idx & 7;
+        *reinterpret_cast<float4 *>(mat + (uint64_t)row * kS + cb * kCols + 4 * c4) =
+            make_float4(tile[row][4 * c4], tile[row][4 * c4 + 1], tile[row][4 * c4 + 2], tile[row][4 * c4 + 3]);
+    }
 }
 
 // Request rq of a request-major launch: its state, rows and result.
