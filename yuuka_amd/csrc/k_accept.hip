@@ -195,12 +195,15 @@ __device__ __forceinline__ void hist_pass(const float *__restrict__ p, int V, fl
     }
     __syncthreads();
     constexpr int kStride = kSelWaves * 64;
-    for (int j0 = threadIdx.x; j0 < V; j0 += 4 * kStride) {
-        float l[4];
+    // eight loads in flight per thread (the row is read from L2 / the
+    // Infinity Cache once per pass: latency, not bandwidth, bounds the pass)
+    constexpr int kU = 8;
+    for (int j0 = threadIdx.x; j0 < V; j0 += kU * kStride) {
+        float l[kU];
 #pragma unroll
-        for (int u = 0; u < 4; u++) l[u] = j0 + u * kStride < V ? p[j0 + u * kStride] : NAN;
+        for (int u = 0; u < kU; u++) l[u] = j0 + u * kStride < V ? p[j0 + u * kStride] : NAN;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < kU; u++) {
             const int j = j0 + u * kStride;
             if (!valid_logit(l[u]) || !sel(l[u], j)) continue;
             const int b = dig(l[u], j);
@@ -340,13 +343,21 @@ __global__ __launch_bounds__(256) void accept_hist_kernel(const float *__restric
     const float mx = mx_s;
     const Cut cut = row_cut(cuts, g, b, row);
     const int begin = c * g.L, end = min(begin + g.L, g.V);
-    for (int j = begin + threadIdx.x; j < end; j += 256) {
-        const float l = p[j];
-        if (!valid_logit(l)) continue;
-        const uint32_t k = order_key(l);
-        if (!in_cut(k, j, cut)) continue;
-        atomicAdd(&cnt[wave][k >> 24], 1u);
-        unsafeAtomicAdd(&ws[wave][k >> 24], exp((double)(l - mx) / t));
+    constexpr int kU = 8;  // loads in flight per thread
+    for (int j0 = begin + threadIdx.x; j0 < end; j0 += kU * 256) {
+        float lv[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) lv[u] = j0 + 256 * u < end ? p[j0 + 256 * u] : NAN;
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const int j = j0 + 256 * u;
+            const float l = lv[u];
+            if (!valid_logit(l)) continue;
+            const uint32_t k = order_key(l);
+            if (!in_cut(k, j, cut)) continue;
+            atomicAdd(&cnt[wave][k >> 24], 1u);
+            unsafeAtomicAdd(&ws[wave][k >> 24], exp((double)(l - mx) / t));
+        }
     }
     __syncthreads();
     Hist0 &o = out[((uint64_t)b * g.R + row) * g.C + c];
