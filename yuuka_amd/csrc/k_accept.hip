@@ -48,22 +48,47 @@ __device__ __forceinline__ const float *row_ptr(const float *logits, const Geo &
     return logits + ((uint64_t)b * g.R + row) * g.stride;
 }
 
+// Per (request, row, chunk) maximum. A chunk of L (a multiple of 4) logits
+// is read by `wpc` waves (1: four chunks per workgroup, for short chunks;
+// 4: one chunk per workgroup), with 16-byte loads when the rows are 16-byte
+// aligned. The maximum under `beats` does not depend on the order in which
+// elements are visited, so the split does not change the result.
 __global__ __launch_bounds__(256) void accept_stats_kernel(const float *__restrict__ logits, Geo g,
-                                                           Stat *__restrict__ stats) {
-    const int c = blockIdx.x, row = blockIdx.y, b = blockIdx.z;
-    const float *p = row_ptr(logits, g, b, row);
-    const int begin = c * g.L;
-    const int end = min(begin + g.L, g.V);
+                                                           Stat *__restrict__ stats, int vec, int wpc) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = blockIdx.x * (4 / wpc) + wave / wpc, row = blockIdx.y, b = blockIdx.z;
+    const int t = (wave % wpc) * 64 + lane, nt = wpc * 64;
+    const bool live = c < g.C;
     float bv = -INFINITY;
     int bi = INT_MAX;
-    for (int j = begin + threadIdx.x; j < end; j += 256) {
-        const float v = p[j];
-        if (beats(v, j, bv, bi)) {
-            bv = v;
-            bi = j;
+    if (live) {
+        const float *p = row_ptr(logits, g, b, row);
+        const int begin = c * g.L;
+        const int end = min(begin + g.L, g.V);
+        if (vec) {
+            const int end4 = begin + ((end - begin) & ~3);
+            for (int j = begin + t * 4; j < end4; j += nt * 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(p + j);
+                if (beats(v.x, j, bv, bi)) { bv = v.x; bi = j; }
+                if (beats(v.y, j + 1, bv, bi)) { bv = v.y; bi = j + 1; }
+                if (beats(v.z, j + 2, bv, bi)) { bv = v.z; bi = j + 2; }
+                if (beats(v.w, j + 3, bv, bi)) { bv = v.w; bi = j + 3; }
+            }
+            const int j = end4 + t;
+            if (j < end && beats(p[j], j, bv, bi)) {
+                bv = p[j];
+                bi = j;
+            }
+        } else {
+            for (int j = begin + t; j < end; j += nt) {
+                const float v = p[j];
+                if (beats(v, j, bv, bi)) {
+                    bv = v;
+                    bi = j;
+                }
+            }
         }
     }
-    // wave reduction, then across the four waves
     for (int off = 32; off > 0; off >>= 1) {
         const float ov = __shfl_xor(bv, off);
         const int oi = __shfl_xor(bi, off);
@@ -72,10 +97,14 @@ __global__ __launch_bounds__(256) void accept_stats_kernel(const float *__restri
             bi = oi;
         }
     }
+    if (wpc == 1) {
+        if (live && lane == 0) stats[((uint64_t)b * g.R + row) * g.C + c] = Stat{bv, bi};
+        return;
+    }
     __shared__ Stat ws[4];
-    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = Stat{bv, bi};
+    if (lane == 0) ws[wave] = Stat{bv, bi};
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x == 0 && live) {
         Stat s = ws[0];
         for (int w = 1; w < 4; w++)
             if (beats(ws[w].v, ws[w].i, s.v, s.i)) s = ws[w];
@@ -609,6 +638,8 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
     __shared__ int argmax0;
     __shared__ Stat row_best_s[256];
     __shared__ double row_rest_s[256];
+    __shared__ float row_p0_s[256];  // logit 0 of each row
+    __shared__ int row_d_s[256];     // each row's draft (-1 on the bonus row)
     if (threadIdx.x == 0) {
         decided_next = -1;
         accepted_s = 0;
@@ -633,6 +664,8 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
             if (lane == 0) {
                 row_best_s[row] = best;
                 row_rest_s[row] = rest;
+                row_p0_s[row] = row_ptr(logits, g, b, row)[0];
+                row_d_s[row] = row < g.k ? drafts[(uint64_t)b * g.ds + row] : -1;
             }
         }
     }
@@ -646,10 +679,11 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
         __shared__ float mx_s;
         if (threadIdx.x == 0) {
             Stat best = row_best_s[row];
-            if (p[0] != p[0]) best = Stat{p[0], 0};  // argmaxLogit keeps a NaN at index 0
+            const float p0 = row_p0_s[row];
+            if (p0 != p0) best = Stat{p0, 0};  // argmaxLogit keeps a NaN at index 0
             best_s = best;
             if (row == 0) argmax0 = best.i;
-            const int d = row < g.k ? drafts[(uint64_t)b * g.ds + row] : -1;
+            const int d = row_d_s[row];
             double dbg[4] = {0.0, 0.0, 0.0, (double)best.v};
             action = 1;
             // forced: a prescribed acceptance length replaces the accept test;
@@ -790,7 +824,12 @@ hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int3
     const bool top_p_on = p.top_p > 0.0f && p.top_p < 1.0f;
     const bool truncate = stochastic && (top_k_on || top_p_on);
     const dim3 grid((unsigned)g.C, (unsigned)g.R, (unsigned)g.B);
-    accept_stats_kernel<<<grid, 256, 0, stream>>>(logits, g, stats);
+    // 16-byte loads need every row start 16-byte aligned
+    const int vec = (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && (g.stride & 3) == 0;
+    // one wave per chunk up to 8 logits per lane, else a workgroup per chunk
+    const int wpc = g.L <= 512 * 4 ? 1 : 4;
+    const dim3 sgrid((unsigned)((g.C + 4 / wpc - 1) / (4 / wpc)), (unsigned)g.R, (unsigned)g.B);
+    accept_stats_kernel<<<sgrid, 256, 0, stream>>>(logits, g, stats, vec, wpc);
     const dim3 sel((unsigned)g.R, (unsigned)g.B);
     const int tk = top_k_on ? (int)p.top_k : 0;
     if (truncate && !top_p_on) {
