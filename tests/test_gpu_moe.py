@@ -50,7 +50,10 @@ def _bins(ids, used, E):
     return bins
 
 
-@pytest.mark.parametrize("rows,E,used", [(5, 256, 8), (40, 256, 8), (3, 16, 4), (7, 8, 8)])
+# Up to 16 rows route and bin in one workgroup; more rows take the per-row
+# and per-expert launches.
+@pytest.mark.parametrize("rows,E,used", [(5, 256, 8), (40, 256, 8), (3, 16, 4), (7, 8, 8), (16, 1024, 16),
+                                         (64, 512, 8), (33, 1024, 16), (200, 64, 4)])
 def test_route_matches_select_experts(dev, stream, rows, E, used):
     rng = np.random.default_rng(rows * 1000 + E)
     logits = rng.normal(0, 1, (rows, E)).astype(np.float32)

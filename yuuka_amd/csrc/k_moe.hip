@@ -9,7 +9,8 @@
 //              row; then binning of the (row, slot) assignments by expert,
 //              one workgroup per expert, in (row, slot) order, so the bins
 //              are deterministic and every count is written (no memset,
-//              graph-safe).
+//              graph-safe). Up to 16 rows, routing and binning run in one
+//              workgroup (row masks per expert give the bin places).
 //  * grouped GEMM: one launch over every expert's assigned rows. Workgroups
 //              are (expert, part); a workgroup with no assignments exits.
 //              The activation rows are quantized once per launch (int16
@@ -127,7 +128,7 @@ __global__ __launch_bounds__(64 * kRouterWaves) void moe_router_kernel(const flo
 // ---------------------------------------------------------------- route
 // forward.go:393-439 selectExperts for every row (one wave per row, the
 // row's logits held in registers, a taken mask per lane), then binning by
-// expert in a second launch (the reference's assignment layout,
+// expert (in a second launch above 16 rows) (the reference's assignment layout,
 // yuuka_hip.h:457-460: bucket capacity rows*used). An assignment's place in
 // its bin is the number of earlier (row, slot) assignments to the same
 // expert, so the bins are in (row, slot) order.
@@ -146,95 +147,87 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
 
-// Maxima / minima over the wave: DPP inside each 16-lane row, then the four
-// rows' results through readlane (wave-uniform).
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
-#define YK_STEP(C)                                                                   \
-    {                                                                                \
-        const uint64_t o = ((uint64_t)dpp_u32<C>((uint32_t)(k >> 32)) << 32) |       \
-                           dpp_u32<C>((uint32_t)k);                                  \
-        k = o > k ? o : k;                                                           \
-    }
-    YK_STEP(0xb1) YK_STEP(0x4e) YK_STEP(0x124) YK_STEP(0x128)
-#undef YK_STEP
-    uint64_t best = 0;
+// Maximum over the wave: DPP inside each 16-lane row, then the four rows'
+// results through readlane (wave-uniform).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0xb1>(v));
+    v = max(v, dpp_u32<0x4e>(v));
+    v = max(v, dpp_u32<0x124>(v));
+    v = max(v, dpp_u32<0x128>(v));
+    uint32_t best = 0;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const uint64_t o = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(k >> 32), 16 * r) << 32) |
-                           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 16 * r);
-        best = o > best ? o : best;
-    }
+    for (int r = 0; r < 4; r++) best = max(best, (uint32_t)__builtin_amdgcn_readlane((int)v, 16 * r));
     return best;
 }
 
-__device__ __forceinline__ int wave_min_i32(int v) {
-    v = min(v, (int)dpp_u32<0xb1>((uint32_t)v));
-    v = min(v, (int)dpp_u32<0x4e>((uint32_t)v));
-    v = min(v, (int)dpp_u32<0x124>((uint32_t)v));
-    v = min(v, (int)dpp_u32<0x128>((uint32_t)v));
-    int best = INT_MAX;
-#pragma unroll
-    for (int r = 0; r < 4; r++) best = min(best, __builtin_amdgcn_readlane(v, 16 * r));
-    return best;
-}
-
-// The logit of expert e (wave-uniform) from its owner lane's registers.
-__device__ __forceinline__ float pick_lane_value(const float (&v)[kRouteMaxPerLane], int e) {
-    const int idx = e >> 6;
-    float mine = 0.f;
-#pragma unroll
-    for (int i = 0; i < kRouteMaxPerLane; i++)
-        if (i == idx) mine = v[i];
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), e & 63));
-}
-
-// One wave per row (PL = experts per lane / 64, rounded up): the slots'
-// picks and weights, kept by lane `slot`.
+// selectExperts for one row by one wave. Expert e = lane + 64 i sits in
+// lane `lane`, register i, so scanning i then lane visits experts in index
+// order. The reference's scan (forward.go:403-418) starts each slot at the
+// first untaken expert and replaces it only with a strictly greater logit:
+// a NaN start keeps the slot, NaN elsewhere never wins, and equal maxima go
+// to the lowest index. Per slot: the wave maximum of the order keys of the
+// untaken non-NaN logits, then the lowest expert holding it from ballots;
+// the untaken and NaN sets are wave-wide ballot masks.
 template <int PL>
-__global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ logits, int rows, int E, int used,
-                                                        int32_t *__restrict__ ids, float *__restrict__ weights) {
+__device__ __forceinline__ void load_route_row(const float *__restrict__ l, int E, float (&v)[PL]) {
     const int lane = threadIdx.x & 63;
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (r >= rows) return;
-    const float *l = logits + (uint64_t)r * E;
-    float v[kRouteMaxPerLane];
 #pragma unroll
-    for (int i = 0; i < kRouteMaxPerLane; i++) v[i] = i < PL && lane + 64 * i < E ? l[lane + 64 * i] : 0.f;
-    uint32_t taken = 0;
-    int my_id = 0;
+    for (int i = 0; i < PL; i++) v[i] = lane + 64 * i < E ? l[lane + 64 * i] : 0.f;
+}
+
+template <int PL>
+__device__ __forceinline__ void route_row(const float (&v)[PL], int E, int used, int &my_id, float &my_w) {
+    const int lane = threadIdx.x & 63;
+    uint32_t key[PL];  // 0: taken, NaN or past E
+    uint64_t live[PL], nan[PL];
+#pragma unroll
+    for (int i = 0; i < PL; i++) {
+        const bool in = lane + 64 * i < E;
+        key[i] = in && v[i] == v[i] ? route_key(v[i]) : 0u;
+        live[i] = __ballot(in);
+        nan[i] = __ballot(in && !(v[i] == v[i]));
+    }
+    my_id = 0;
     float my_pv = 0.f;
     for (int slot = 0; slot < used; slot++) {
-        // Reference scan: the first untaken expert starts as best and a
-        // later one replaces it only when strictly greater. So a NaN start
-        // keeps the slot, NaN elsewhere never wins, and equal maxima resolve
-        // to the lowest index: the largest key (order key of the logit, then
-        // the complemented index) over untaken non-NaN experts.
-        uint64_t key = 0;
-        int first = INT_MAX;
+        uint32_t m = key[0];
 #pragma unroll
-        for (int i = 0; i < PL; i++) {
-            const int e = lane + 64 * i;
-            if (e >= E || (taken >> i & 1u)) continue;
-            first = min(first, e);
-            if (v[i] == v[i]) {
-                const uint64_t k = ((uint64_t)route_key(v[i]) << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
-                key = k > key ? k : key;
+        for (int i = 1; i < PL; i++) m = max(m, key[i]);
+        const uint32_t K = wave_max_u32(m);
+        int first = -1;
+        bool first_nan = false;
+#pragma unroll
+        for (int i = PL - 1; i >= 0; i--)
+            if (live[i]) {
+                const int bit = __builtin_ctzll(live[i]);
+                first = 64 * i + bit;
+                first_nan = (nan[i] >> bit) & 1ull;
             }
+        int pick = 0;  // more slots than experts (forward.go:413-417)
+        if (first >= 0) {
+            if (K == 0u || first_nan) {
+                pick = first;
+            } else {
+#pragma unroll
+                for (int i = PL - 1; i >= 0; i--) {
+                    const uint64_t hit = __ballot(key[i] == K);
+                    if (hit) pick = 64 * i + __builtin_ctzll(hit);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < PL; i++)
+                if (i == (pick >> 6)) {
+                    live[i] &= ~(1ull << (pick & 63));
+                    if (lane == (pick & 63)) key[i] = 0u;
+                }
         }
-        key = wave_max_u64(key);
-        first = wave_min_i32(first);
-        int pick;
-        if (first == INT_MAX) {
-            pick = 0;  // more slots than experts (forward.go:413-417)
-        } else {
-            const float fv = pick_lane_value(v, first);
-            pick = (!(fv == fv) || key == 0) ? first : (int)(0xffffffffu - (uint32_t)key);
-            if ((pick & 63) == lane) taken |= 1u << (pick >> 6);
-        }
-        const float pvv = pick_lane_value(v, pick);
+        float pv = 0.f;
+#pragma unroll
+        for (int i = 0; i < PL; i++)
+            if (i == (pick >> 6)) pv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[i]), pick & 63));
         if (lane == slot) {
             my_id = pick;
-            my_pv = pvv;
+            my_pv = pv;
         }
     }
     // weights: float32(exp(float64(l - max))), float32 total in slot order,
@@ -249,9 +242,78 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
     float total = 0.f;
     for (int sl = 0; sl < used; sl++)
         total = __fadd_rn(total, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wt), sl)));
+    my_w = total > 0.f ? __fdiv_rn(wt, total) : wt;
+}
+
+// One wave per row (PL = experts per lane / 64, rounded up): the slots'
+// picks and weights, kept by lane `slot`.
+template <int PL>
+__global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ logits, int rows, int E, int used,
+                                                        int32_t *__restrict__ ids, float *__restrict__ weights) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    int id;
+    float w;
+    float v[PL];
+    load_route_row<PL>(logits + (uint64_t)r * E, E, v);
+    route_row<PL>(v, E, used, id, w);
     if (lane < used) {
-        ids[(uint64_t)r * used + lane] = my_id;
-        weights[(uint64_t)r * used + lane] = total > 0.f ? __fdiv_rn(wt, total) : wt;
+        ids[(uint64_t)r * used + lane] = id;
+        weights[(uint64_t)r * used + lane] = w;
+    }
+}
+
+// Routing and binning in one workgroup of 16 waves, for at most 16 rows and
+// used <= E (a row's experts are then distinct): wave w routes row w, and
+// every pick sets its row's bit in its expert's row mask. (Routing a row is
+// a few microseconds of dependent wave reductions, so more rows than waves
+// are faster as one wave per row over many workgroups plus moe_bin_kernel.) An assignment's place in its expert's bin is the number of earlier
+// rows in that mask, the order moe_bin_kernel gives.
+constexpr int kRouteBinWaves = 16;
+constexpr int kRouteBinRows = 16;
+template <int PL>
+__global__ __launch_bounds__(64 * kRouteBinWaves) void moe_route_bin_kernel(
+    const float *__restrict__ logits, int rows, int E, int used, int32_t *__restrict__ ids,
+    float *__restrict__ weights, int cap, int32_t *__restrict__ counts, int32_t *__restrict__ arows,
+    int32_t *__restrict__ aslots, float *__restrict__ aweights) {
+    __shared__ unsigned long long mask[64 * kRouteMaxPerLane];
+    constexpr int kRounds = kRouteBinRows / kRouteBinWaves;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int e = threadIdx.x; e < E; e += 64 * kRouteBinWaves) mask[e] = 0ull;
+    __syncthreads();
+    int id[kRounds];
+    float w[kRounds];
+    float v[kRounds][PL];  // every row's logits requested before the first is routed
+#pragma unroll
+    for (int i = 0; i < kRounds; i++)
+        if (wave + kRouteBinWaves * i < rows)
+            load_route_row<PL>(logits + (uint64_t)(wave + kRouteBinWaves * i) * E, E, v[i]);
+#pragma unroll
+    for (int i = 0; i < kRounds; i++) {
+        const int r = wave + kRouteBinWaves * i;
+        id[i] = 0;
+        w[i] = 0.f;
+        if (r < rows) {
+            route_row<PL>(v[i], E, used, id[i], w[i]);
+            if (lane < used) {
+                ids[(uint64_t)r * used + lane] = id[i];
+                weights[(uint64_t)r * used + lane] = w[i];
+                atomicOr(&mask[id[i]], 1ull << r);
+            }
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += 64 * kRouteBinWaves) counts[e] = __popcll(mask[e]);
+#pragma unroll
+    for (int i = 0; i < kRounds; i++) {
+        const int r = wave + kRouteBinWaves * i;
+        if (r < rows && lane < used) {
+            const uint64_t o = (uint64_t)id[i] * cap + __popcll(mask[id[i]] & ((1ull << r) - 1ull));
+            arows[o] = r;
+            aslots[o] = lane;
+            aweights[o] = w[i];
+        }
     }
 }
 
@@ -747,6 +809,18 @@ hipError_t launch_moe_router(const float *y, int H, int rows, const float *w, in
 hipError_t launch_moe_route(const float *logits, int rows, int E, int used, int32_t *ids, float *weights,
                             int32_t *counts, int32_t *arows, int32_t *aslots, float *aweights, hipStream_t s) {
     if (E > 64 * kRouteMaxPerLane || used > 64) return hipErrorInvalidValue;
+    if (rows <= kRouteBinRows && used <= E) {
+        if (E <= 256)
+            moe_route_bin_kernel<4><<<1, 64 * kRouteBinWaves, 0, s>>>(logits, rows, E, used, ids, weights, rows * used,
+                                                                      counts, arows, aslots, aweights);
+        else if (E <= 512)
+            moe_route_bin_kernel<8><<<1, 64 * kRouteBinWaves, 0, s>>>(logits, rows, E, used, ids, weights, rows * used,
+                                                                      counts, arows, aslots, aweights);
+        else
+            moe_route_bin_kernel<16><<<1, 64 * kRouteBinWaves, 0, s>>>(logits, rows, E, used, ids, weights,
+                                                                       rows * used, counts, arows, aslots, aweights);
+        return hipGetLastError();
+    }
     const unsigned g = (unsigned)((rows + 3) / 4);
     if (E <= 256) moe_route_kernel<4><<<g, 256, 0, s>>>(logits, rows, E, used, ids, weights);
     else if (E <= 512) moe_route_kernel<8><<<g, 256, 0, s>>>(logits, rows, E, used, ids, weights);
