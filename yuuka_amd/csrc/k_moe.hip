@@ -3,7 +3,8 @@
 // reference's MoE plan ops (backend/hip/bridge/yuuka_hip.h:457-470).
 //
 //  * router:   FP32 router logits (and the shared-expert gate logit) of the
-//              verify rows, one workgroup per (expert row, 8 rows).
+//              verify rows, one workgroup per (4 expert rows, 8 rows), K
+//              split over its waves.
 //  * route:    top-`used` experts per row by repeated argmax (lower index
 //              wins ties) and softmax over the selected logits, one wave per
 //              row; then binning of the (row, slot) assignments by expert,
@@ -71,57 +72,72 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {  // values >= 0
 // ---------------------------------------------------------------- router
 // logits[r][e] = W[e] . y[r] (FP32 weights, ffn_gate_inp) and, when `sv` is
 // given, extra[r] = sv . y[r] (ffn_gate_inp_shexp, forward.go:385). One
-// workgroup per (block of kRouterExperts expert rows, block of 8 rows) (the
-// shared gate vector is row E); each of its four waves takes two rows and
-// reuses their loads for the block's expert rows.
+// workgroup per (block of kRouterExperts expert rows, block of kRouterRows
+// rows) (the shared gate vector is row E). Its four waves split K: lane l of
+// wave w takes the float4 groups l + 64 (w + 4 j), so every wave issues its
+// few loads at once; each lane's partial sums of the block's 32 dot products
+// go to LDS, and 8 threads per product add them in a fixed order.
 constexpr int kRouterWaves = 4;
 constexpr int kRouterExperts = 4;
+constexpr int kRouterRows = 8;
+constexpr int kRouterDots = kRouterExperts * kRouterRows;
+constexpr int kRouterPad = 264;  // LDS row stride (floats) of one dot product's 256 partials
 
 __global__ __launch_bounds__(64 * kRouterWaves) void moe_router_kernel(const float *__restrict__ y, int H, int rows,
                                                                        const float *__restrict__ w, int E,
                                                                        float *__restrict__ logits,
                                                                        const float *__restrict__ sv,
                                                                        float *__restrict__ extra) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __shared__ float part[kRouterDots * kRouterPad];
+    const int t = threadIdx.x;
     const int e0 = blockIdx.x * kRouterExperts, ne = E + (sv ? 1 : 0);
-    const int r = blockIdx.y * 2 * kRouterWaves + wave, r2 = r + kRouterWaves;
-    if (r >= rows) return;
-    const bool two = r2 < rows;
-    const float *y0 = y + (uint64_t)r * H, *y1 = y + (uint64_t)(two ? r2 : r) * H;
+    const int r0 = blockIdx.y * kRouterRows;
     const float *wr[kRouterExperts];
+    const float *yr[kRouterRows];
 #pragma unroll
     for (int x = 0; x < kRouterExperts; x++) {
         const int e = min(e0 + x, ne - 1);
         wr[x] = e < E ? w + (uint64_t)e * H : sv;
     }
-    float a0[kRouterExperts], a1[kRouterExperts];
 #pragma unroll
-    for (int x = 0; x < kRouterExperts; x++) a0[x] = a1[x] = 0.f;
+    for (int i = 0; i < kRouterRows; i++) yr[i] = y + (uint64_t)min(r0 + i, rows - 1) * H;
+    float acc[kRouterExperts][kRouterRows];
+#pragma unroll
+    for (int x = 0; x < kRouterExperts; x++)
+#pragma unroll
+        for (int i = 0; i < kRouterRows; i++) acc[x][i] = 0.f;
 #pragma unroll 2
-    for (int k = 4 * lane; k < H; k += 256) {
-        const float4 b0 = *reinterpret_cast<const float4 *>(y0 + k);
-        const float4 b1 = *reinterpret_cast<const float4 *>(y1 + k);
+    for (int k = 4 * t; k < H; k += 4 * 64 * kRouterWaves) {
+        float4 wv[kRouterExperts], yv[kRouterRows];
 #pragma unroll
-        for (int x = 0; x < kRouterExperts; x++) {
-            const float4 wv = *reinterpret_cast<const float4 *>(wr[x] + k);
-            a0[x] += wv.x * b0.x + wv.y * b0.y + wv.z * b0.z + wv.w * b0.w;
-            a1[x] += wv.x * b1.x + wv.y * b1.y + wv.z * b1.z + wv.w * b1.w;
-        }
+        for (int x = 0; x < kRouterExperts; x++) wv[x] = *reinterpret_cast<const float4 *>(wr[x] + k);
+#pragma unroll
+        for (int i = 0; i < kRouterRows; i++) yv[i] = *reinterpret_cast<const float4 *>(yr[i] + k);
+#pragma unroll
+        for (int x = 0; x < kRouterExperts; x++)
+#pragma unroll
+            for (int i = 0; i < kRouterRows; i++)
+                acc[x][i] += wv[x].x * yv[i].x + wv[x].y * yv[i].y + wv[x].z * yv[i].z + wv[x].w * yv[i].w;
     }
 #pragma unroll
-    for (int x = 0; x < kRouterExperts; x++) {
-        const int e = e0 + x;
-        if (e >= ne) break;
-        const float s0 = wave_sum(a0[x]), s1 = wave_sum(a1[x]);
-        if (lane == 0) {
-            if (e < E) {
-                logits[(uint64_t)r * E + e] = s0;
-                if (two) logits[(uint64_t)r2 * E + e] = s1;
-            } else {
-                extra[r] = s0;
-                if (two) extra[r2] = s1;
-            }
-        }
+    for (int x = 0; x < kRouterExperts; x++)
+#pragma unroll
+        for (int i = 0; i < kRouterRows; i++) part[(x * kRouterRows + i) * kRouterPad + t] = acc[x][i];
+    __syncthreads();
+    // dot product d = t / 8; thread part p = t % 8 adds partials p, p + 8, ...
+    const int d = t >> 3, p = t & 7;
+    float s = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < 64 * kRouterWaves / 8; j++) s += part[d * kRouterPad + p + 8 * j];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    const int x = d / kRouterRows, r = r0 + d % kRouterRows, e = e0 + x;
+    if (p == 0 && r < rows && e < ne) {
+        if (e < E)
+            logits[(uint64_t)r * E + e] = s;
+        else
+            extra[r] = s;
     }
 }
 
@@ -801,7 +817,7 @@ hipError_t launch_moe_router(const float *y, int H, int rows, const float *w, in
                              float *extra, hipStream_t s) {
     const int n = E + (sv ? 1 : 0);
     moe_router_kernel<<<dim3((unsigned)((n + kRouterExperts - 1) / kRouterExperts),
-                             (unsigned)((rows + 2 * kRouterWaves - 1) / (2 * kRouterWaves))),
+                             (unsigned)((rows + kRouterRows - 1) / kRouterRows)),
                         64 * kRouterWaves, 0, s>>>(y, H, rows, w, E, logits, sv, extra);
     return hipGetLastError();
 }
