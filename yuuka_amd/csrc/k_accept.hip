@@ -67,17 +67,26 @@ __global__ __launch_bounds__(256) void accept_stats_kernel(const float *__restri
         const int end = min(begin + g.L, g.V);
         if (vec) {
             const int end4 = begin + ((end - begin) & ~3);
-            for (int j = begin + t * 4; j < end4; j += nt * 4) {
-                const float4 v = *reinterpret_cast<const float4 *>(p + j);
+            auto take4 = [&](const float4 v, int j) {
                 if (beats(v.x, j, bv, bi)) { bv = v.x; bi = j; }
                 if (beats(v.y, j + 1, bv, bi)) { bv = v.y; bi = j + 1; }
                 if (beats(v.z, j + 2, bv, bi)) { bv = v.z; bi = j + 2; }
                 if (beats(v.w, j + 3, bv, bi)) { bv = v.w; bi = j + 3; }
+            };
+            int j = begin + t * 4;
+            // four 16-byte loads in flight per thread
+            for (; j + 3 * nt * 4 < end4; j += 4 * nt * 4) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) v[u] = *reinterpret_cast<const float4 *>(p + j + u * nt * 4);
+#pragma unroll
+                for (int u = 0; u < 4; u++) take4(v[u], j + u * nt * 4);
             }
-            const int j = end4 + t;
-            if (j < end && beats(p[j], j, bv, bi)) {
-                bv = p[j];
-                bi = j;
+            for (; j < end4; j += nt * 4) take4(*reinterpret_cast<const float4 *>(p + j), j);
+            const int jt = end4 + t;
+            if (jt < end && beats(p[jt], jt, bv, bi)) {
+                bv = p[jt];
+                bi = jt;
             }
         } else {
             for (int j = begin + t; j < end; j += nt) {
@@ -178,7 +187,23 @@ __global__ __launch_bounds__(256) void accept_weights_kernel(const float *__rest
     const int begin = c * g.L;
     const int end = min(begin + g.L, g.V);
     double acc = 0.0;
-    for (int j = begin + threadIdx.x; j < end; j += 256) {
+    // eight logit loads in flight per thread; the sum keeps index order
+    constexpr int kU = 8;
+    int j = begin + threadIdx.x;
+    for (; j + (kU - 1) * 256 < end; j += kU * 256) {
+        float l[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) l[u] = p[j + u * 256];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            const double w = weight_of(l[u], j + u * 256, mx, t, cut);
+            if (j + u * 256 == d)
+                wdraft[(uint64_t)b * g.R + row] = w;
+            else
+                acc += w;
+        }
+    }
+    for (; j < end; j += 256) {
         const double w = weight_of(p[j], j, mx, t, cut);
         if (j == d)
             wdraft[(uint64_t)b * g.R + row] = w;
