@@ -608,7 +608,16 @@ __device__ int scan_chunk(const float *p, const Geo &g, int c, int d, float mx, 
     const int lo = begin + threadIdx.x * per;
     const int hi = min(lo + per, end);
     double local = 0.0;
-    for (int j = lo; j < hi; j++)
+    int j = lo;
+    for (; j + 7 < hi; j += 8) {  // eight loads in flight, summed in index order
+        float l[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) l[u] = p[j + u];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (j + u != d) local += weight_of(l[u], j + u, mx, t, cut);
+    }
+    for (; j < hi; j++)
         if (j != d) local += weight_of(p[j], j, mx, t, cut);
     shared_prefix[threadIdx.x] = local;
     if (threadIdx.x == 0) *shared_pick = -1;
