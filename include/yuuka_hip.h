@@ -214,7 +214,9 @@ YUUKA_API yuuka_status yuuka_gemv(yuuka_stream * stream, yuuka_buffer * out,
                         yuuka_event * completion);
 
 /* reference :221-224, :235-238, :250-256, :266-270: prefill GEMM routes of
- * the reference (rocBLAS/rocWMMA/MMQ). Out of scope: UNSUPPORTED. */
+ * the reference (rocBLAS/rocWMMA/MMQ). Out of scope: UNSUPPORTED, except
+ * yuuka_quantize_q8_1, the Q8_1 activation format the int8 decode matvec
+ * (YUUKA_OP_GEMV_Q8_1) also reads. */
 YUUKA_API yuuka_status yuuka_gemm(yuuka_stream * stream, yuuka_buffer * out,
                         const yuuka_buffer * x, const yuuka_buffer * w,
                         uint64_t n_in, uint64_t n_out, uint64_t batch,

@@ -18,6 +18,7 @@
 
 #include "internal.h"
 #include "model_kernels.h"
+#include "ops.h"
 #include "plan.h"
 
 namespace yk {
@@ -460,9 +461,22 @@ yuuka_status yuuka_gemm_wmma(yuuka_stream *, yuuka_buffer *, const yuuka_buffer 
                              uint64_t, uint64_t, uint64_t, uint32_t, yuuka_event *) {
     UNSUPPORTED_ENTRY("yuuka_gemm_wmma (rocWMMA prefill GEMM)");
 }
-yuuka_status yuuka_quantize_q8_1(yuuka_stream *, yuuka_buffer *, yuuka_buffer *, const yuuka_buffer *,
-                                 uint64_t, uint64_t, yuuka_event *) {
-    UNSUPPORTED_ENTRY("yuuka_quantize_q8_1 (MMQ prefill route)");
+// Q8_1 activations of the int8 decode matvec (reference mmq_gemm.hip
+// quantize_q8_1_kernel contract): qs[n * batch] int8 digits, ds[n * batch /
+// 32] {d, d * sum} pairs; n a multiple of 128.
+yuuka_status yuuka_quantize_q8_1(yuuka_stream *stream, yuuka_buffer *qs, yuuka_buffer *ds, const yuuka_buffer *x,
+                                 uint64_t n, uint64_t batch, yuuka_event *completion) {
+    return guard("quantize_q8_1", [&]() -> yuuka_status {
+        if (!stream || !qs || !ds || !x) return fail(YUUKA_ERR_INVALID_ARGUMENT, "null argument");
+        if (!n || n % 128 || !batch) return fail(YUUKA_ERR_INVALID_ARGUMENT, "Q8_1 width must be a multiple of 128");
+        const uint64_t total = n * batch;
+        if (!range_ok(x, 0, total * 4) || !range_ok(qs, 0, total) || !range_ok(ds, 0, total / 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "Q8_1 buffers too small");
+        hipError_t err = launch_quant_q8_1(static_cast<const float *>(x->ptr), nullptr, qs->ptr, ds->ptr, total,
+                                           stream->stream);
+        if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "quantize launch: %s", hip_error(err));
+        return record(stream, completion);
+    });
 }
 yuuka_status yuuka_gemm_mmq(yuuka_stream *, yuuka_buffer *, const yuuka_buffer *, const yuuka_buffer *,
                             const yuuka_buffer *, uint64_t, uint64_t, uint64_t, uint32_t, yuuka_event *) {

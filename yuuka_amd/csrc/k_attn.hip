@@ -30,18 +30,6 @@
 namespace yk {
 namespace {
 
-#ifdef YK_AT_TIMING
-// Phase timestamps per wave (probe builds only; s_memrealtime, 100 MHz).
-__device__ uint64_t *yk_at_dbg;
-#define YK_AT_STAMP(i) ts[i] = __builtin_amdgcn_s_memrealtime()
-// adds the time since the last YK_AT_MARK to slot i
-#define YK_AT_MARK() t_mark = __builtin_amdgcn_s_memrealtime()
-#define YK_AT_ACC(i) { const uint64_t t_ = __builtin_amdgcn_s_memrealtime(); ts[i] += t_ - t_mark; t_mark = t_; }
-#else
-#define YK_AT_STAMP(i) (void)0
-#define YK_AT_MARK() (void)0
-#define YK_AT_ACC(i) (void)0
-#endif
 
 __device__ __forceinline__ int cur_pos_a(const ModelDyn &dyn) { return dyn.pos_dev ? *dyn.pos_dev : dyn.pos; }
 
@@ -207,10 +195,6 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
     const int last = p0 + R - 1;
     const int key0 = chunk * CK;
     if (key0 > last) return;  // no row sees this chunk; the merge skips it
-#ifdef YK_AT_TIMING
-    uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#endif
-    YK_AT_STAMP(0);
     const int half = a.rope_dim / 2;
     const int qstride = a.gated ? 2 * D : D;
     const int ks = D + PAD;  // LDS row stride of K and V (elements)
@@ -252,7 +236,6 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
         norm_rope_wave(q + ((int64_t)r * a.heads + head) * qstride, q_norm, Qs + vec * D, D, a.eps,
                        rope + r * half, half);
     }
-    YK_AT_STAMP(1);
     float *kbuf = S;  // scratch for one new key row per wave (S is free until the scores)
     for (int r = wave; r < R; r += 4) {
         const int p = p0 + r;
@@ -270,9 +253,7 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
             vpool[slot * a.kv_dim + (int64_t)kvh * D + d] = vq;
         }
     }
-    YK_AT_STAMP(2);
     __syncthreads();
-    YK_AT_STAMP(3);
 
     // ---- scores: thread = (key kk, query group), full D, 8 queries a pass
     {
@@ -307,7 +288,6 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
         }
     }
     __syncthreads();
-    YK_AT_STAMP(4);
     // ---- softmax partials: one wave per query row of the chunk
     for (int j = wave; j < nq; j += 4) {
         const float sc = lane < CK ? S[j * CK + lane] : -INFINITY;
@@ -323,7 +303,6 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
         }
     }
     __syncthreads();
-    YK_AT_STAMP(5);
     // ---- value product: thread = dimension d, 16 query rows a pass
     for (int d = threadIdx.x; d < D; d += 256) {
         for (int j0 = 0; j0 < nq; j0 += 16) {
@@ -353,13 +332,6 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(const float *__restric
             }
         }
     }
-    YK_AT_STAMP(6);
-#ifdef YK_AT_TIMING
-    if (yk_at_dbg && lane == 0) {
-        uint64_t *o = yk_at_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave) * 8;
-        for (int e = 0; e < 8; e++) o[e] = ts[e];
-    }
-#endif
 }
 
 // ---- MFMA path (F16 KV, head_dim 256, rope_dim 64, at most 32 query rows
@@ -528,10 +500,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
     const int last = p0 + R - 1;
     const int key0 = chunk * kMK;
     if (key0 > last) return;  // no row sees this chunk; the merge skips it
-#ifdef YK_AT_TIMING
-    uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#endif
-    YK_AT_STAMP(0);
     const int half = a.rope_dim / 2;
     const int qstride = a.gated ? 2 * kMD : kMD;
     const uint32_t base = (uint32_t)(uintptr_t)lds;
@@ -634,7 +602,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
         }
     }
     prep_q(0, min(RB, R));
-    YK_AT_STAMP(1);
     // ---- the verify rows' own keys and values (rows whose position falls in
     //      this chunk): rounded as the pool stores them, into the pool (keys)
     //      and LDS (values)
@@ -661,14 +628,12 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
 #pragma unroll
         for (int i = 0; i < 4; i++) vt[(4 * lane + i) * kVt + kk] = vq[i];
     }
-    YK_AT_STAMP(2);
     if (key0 + kMK - 1 >= p0) {
         __syncthreads();  // the new keys are in the pool (global and LDS fence)
         load_keys(true);
     } else {
         lds_only_barrier();
     }
-    YK_AT_STAMP(3);
 
     for (int r0 = 0; r0 < R; r0 += RB) {
     const int Rb = min(RB, R - r0), nq = G * Rb;  // this block's verify rows and MFMA rows
@@ -701,7 +666,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
         }
     }
     lds_only_barrier();
-    YK_AT_STAMP(4);
     // ---- softmax partials: four query rows per wave at a time, one 16-lane
     //      DPP row per query row, lane s holding keys [4 s, 4 s + 4)
     {
@@ -750,7 +714,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
         }
     }
     lds_only_barrier();
-    YK_AT_STAMP(5);
     // ---- value product: wave w owns dims [32w, 32w + 32) (two 16-wide tiles)
     {
         constexpr int kJ = kMD / kAW / 16;
@@ -796,13 +759,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
                 }
     }
     }
-    YK_AT_STAMP(6);
-#ifdef YK_AT_TIMING
-    if (yk_at_dbg && lane == 0) {
-        uint64_t *o = yk_at_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * kAW + wave) * 8;
-        for (int e = 0; e < 8; e++) o[e] = ts[e];
-    }
-#endif
 }
 
 // LDS layout of the grouped kernel with NT 16-row query tiles: the
@@ -854,11 +810,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
     const int c_lo = grp * cpw;
     if (c_lo * kMK > last) return;  // no row sees this group; the merge skips it
     const int c_hi = min(c_lo + cpw, last / kMK + 1);
-#ifdef YK_AT_TIMING
-    uint64_t ts[12] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    uint64_t t_mark = 0;
-#endif
-    YK_AT_STAMP(0);
     const int half = a.rope_dim / 2;
     const int qstride = a.gated ? 2 * kMD : kMD;
     using LY = GroupLds<NT>;
@@ -889,7 +840,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
         *reinterpret_cast<uint2 *>(vpool + slot * a.kv_dim + (int64_t)kvh * kMD + 4 * lane) = vw;
     }
     if (p0 < c_hi * kMK) __syncthreads();  // the new rows are in the pool (global fence)
-    YK_AT_STAMP(1);
 
     // keys straight into MFMA B order: the scores lane (key kk, group g4)
     // holds dims [32 ks + 8 g4, +8) of key kk for every ks
@@ -1000,7 +950,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
         const int ntl = (nq + 15) / 16;               // row tiles in use
         if (r0) lds_only_barrier();                   // the previous block's reads of Q, M, L are done
         prep_q(r0, Rb);
-        YK_AT_STAMP(8);
         if (threadIdx.x < kQ) {
             Mrow[threadIdx.x] = -INFINITY;
             Lrow[threadIdx.x] = 0.0f;
@@ -1019,9 +968,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
             int oz;
             asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
             const int lr16 = r16 + oz, lg4 = g4 + oz, lkk = kk_s + oz, llane = lane + oz;
-            YK_AT_MARK();
             lds_only_barrier();  // the previous chunk's P.V reads of Vt are done; Q, M, L are written
-            YK_AT_ACC(2);
             {
                 uint16_t *vt = reinterpret_cast<uint16_t *>(lds + LY::Vt);
 #pragma unroll
@@ -1057,9 +1004,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                     if (qi < nq) S[qi * kMK + lkk] = p <= p0 + r0 + qi % Rb ? acc[e] * a.scale : -INFINITY;
                 }
             }
-            YK_AT_ACC(3);
             lds_only_barrier();
-            YK_AT_ACC(4);
             // ---- online softmax: four query rows per wave at a time, one
             //      16-lane DPP row per query row, lane s holding keys
             //      [4 s, 4 s + 4) (the row's reductions never leave the DPP
@@ -1114,9 +1059,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                     }
                 }
             }
-            YK_AT_ACC(5);
             lds_only_barrier();
-            YK_AT_ACC(4);
             // ---- value product: wave w owns dims [32w, 32w + 32); the running
             //      accumulators are rescaled by this chunk's alpha first
 #pragma unroll
@@ -1155,7 +1098,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                     }
                 }
             }
-            YK_AT_ACC(7);
         };
         if constexpr (PF) {
             // two register sets: chunk ci + 1 loads while chunk ci is computed,
@@ -1187,7 +1129,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                 chunk(X, ci);
             }
         }
-        YK_AT_STAMP(9);
         // ---- this block's partial records: o, and (m, l) of every row
         int oz;  // opaque zero: the per-row indices below stay inside the block loop
         asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
@@ -1211,13 +1152,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
             rec[kMD + 1] = Lrow[qi];
         }
     }
-    YK_AT_STAMP(6);
-#ifdef YK_AT_TIMING
-    if (yk_at_dbg && lane == 0) {
-        uint64_t *o = yk_at_dbg + (((size_t)blockIdx.y * gridDim.x + blockIdx.x) * kAW + wave) * 12;
-        for (int e = 0; e < 12; e++) o[e] = ts[e];
-    }
-#endif
 }
 
 // Merges the chunk partials of one (query head, row) and applies the output

@@ -422,12 +422,6 @@ __device__ __forceinline__ void conv_channels4(const float *conv_state, const fl
 // columns). Lane l of wave w holds column j = kCols * blockIdx.y + 8 w + l / 8
 // and state rows 16 (l % 8) .. +15; a column's eight row parts form an
 // aligned 8-lane group, so column sums need no barrier.
-#ifdef YK_GD_TIMING
-__device__ uint64_t *yk_gd_dbg;
-#define YK_GD_STAMP(i) ts[i] = __builtin_amdgcn_s_memrealtime()
-#else
-#define YK_GD_STAMP(i) (void)0
-#endif
 constexpr int kCols = 32;
 constexpr int kMaxRows = 32;  // verify rows of one step (k <= 31 drafts)
 constexpr int kColThreads = 256;
@@ -468,10 +462,6 @@ __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
         cf[t] = gdn_decay(g, alpha_raw, dt, a_log, t, h);
         cf[R + t] = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
     }
-#ifdef YK_GD_TIMING
-    uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#endif
-    YK_GD_STAMP(0);
     const int p = lane & 7, j = cb * COLS + wave * 8 + (lane >> 3);
     const float *mat = state + (uint64_t)h * kS * kS;
     float s_reg[16];
@@ -504,9 +494,7 @@ __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
             conv_channel2<RC>(conv_state, qkv, conv_w, g, c0, qk + which * kS + cc, 2 * kS, c1, vv + t, COLS);
         }
     }
-    YK_GD_STAMP(1);
     __syncthreads();
-    YK_GD_STAMP(2);
     // L2 norm of the 2R q / k vectors. One 16-lane DPP row per vector (lane
     // s of the row holds elements [8 s, 8 s + 8)), two vectors per row at a
     // time: the float64 sums of every vector reduce side by side instead of
@@ -563,9 +551,7 @@ __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
         const int r = idx / COLS, cc = idx % COLS;
         conv_out[(uint64_t)r * g.conv_dim + 2 * key_dim + h * kS + cb * COLS + cc] = vv[r * COLS + cc];
     }
-    YK_GD_STAMP(3);
     __syncthreads();
-    YK_GD_STAMP(4);
     const int jl = j - cb * COLS;
     // Row r's k, q slices, v and coefficients are read from LDS while row
     // r - 1 is computed (two register sets, alternating).
@@ -618,13 +604,6 @@ __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
         if (r + 2 < R) fetch(ra, r + 2);
         step(rb, r + 1);
     }
-    YK_GD_STAMP(5);
-#ifdef YK_GD_TIMING
-    if (yk_gd_dbg && lane == 0) {
-        uint64_t *o = yk_gd_dbg + ((((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * 4 + wave) * 8;
-        for (int e = 0; e < 8; e++) o[e] = ts[e];
-    }
-#endif
 }
 
 // Commit of one layer: replay of the accepted rows for this block's

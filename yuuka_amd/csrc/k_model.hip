@@ -97,9 +97,9 @@ __device__ float dequant_one(const uint8_t *row, uint32_t dtype, int col) {
 
 __global__ __launch_bounds__(256) void embedding_kernel(const uint8_t *__restrict__ table, uint32_t dtype,
                                                         uint64_t row_bytes, const int32_t *__restrict__ tokens,
-                                                        int vocab, int cols, float *__restrict__ out) {
+                                                        int host_token, int vocab, int cols, float *__restrict__ out) {
     const int r = blockIdx.y;
-    int tok = tokens[r];
+    int tok = tokens ? tokens[r] : host_token;
     tok = tok < 0 ? 0 : (tok >= vocab ? vocab - 1 : tok);  // ids are validated on the host
     const uint8_t *row = table + (uint64_t)tok * row_bytes;
     for (int c = blockIdx.x * 256 + threadIdx.x; c < cols; c += gridDim.x * 256)
@@ -510,9 +510,9 @@ __global__ void advance_kernel(ModelDyn dyn, const int32_t *__restrict__ accept_
 }  // namespace
 
 hipError_t launch_embedding(const void *table, uint32_t dtype, uint64_t row_bytes, const int32_t *tokens, int vocab,
-                            int cols, int rows, float *out, hipStream_t s) {
+                            int cols, int rows, float *out, hipStream_t s, int host_token) {
     embedding_kernel<<<dim3((unsigned)((cols + 255) / 256), (unsigned)rows), 256, 0, s>>>(
-        static_cast<const uint8_t *>(table), dtype, row_bytes, tokens, vocab, cols, out);
+        static_cast<const uint8_t *>(table), dtype, row_bytes, tokens, host_token, vocab, cols, out);
     return hipGetLastError();
 }
 

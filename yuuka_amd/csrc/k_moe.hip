@@ -512,18 +512,8 @@ __device__ __forceinline__ void vmem_wait_all() { asm volatile("s_waitcnt vmcnt(
 // the epilogue. Lane (c, g) of an item loads channel c's Q4_K bytes straight
 // into MFMA B order and the activation planes of assignment c & 7 (high
 // plane for c < 8) into A order.
-#ifdef YK_MOE_TIMING
-__device__ uint64_t *yk_moe_dbg;  // per wave: start, rows known, staged, items done, end
-#define YK_MOE_STAMP(i) ts[i] = __builtin_amdgcn_s_memrealtime()
-#else
-#define YK_MOE_STAMP(i) (void)0
-#endif
 template <bool PACKED>
 __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))) void moe_gemm_kernel(MoeGemmArgs A) {
-#ifdef YK_MOE_TIMING
-    uint64_t ts[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    YK_MOE_STAMP(0);
-#endif
     // LDS: results [tpw][mats][8 rows][16 ch] floats, then the
     // chunk's activations: planes [K/64][16 r][4 g][2][8 B] (r < 8 high
     // plane of assignment r, r >= 8 low plane of assignment r - 8), scales
@@ -628,7 +618,6 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
     vmem_wait_all();
     __syncthreads();
     for (int k = 0;; k++) {
-        YK_MOE_STAMP(1);
         const int slot = k % 3, buf = k & 1;
         const int *mt = s_meta[slot];
         const int en = entry_of(k), e = en & 1023, c0 = (en >> 10) * kChunk;
@@ -641,7 +630,6 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
         }
         const uint8_t *lat = la + (uint64_t)buf * la_bytes;
         const float *lxt = lxs + (uint64_t)buf * nsb * 8;
-        YK_MOE_STAMP(2);
         // items (tile, matrix, super-block): wave w walks the pairs (tile,
         // matrix) w, w + 8, ... through their super-blocks in order with the
         // next item's weights in flight, sums in registers in super-block
@@ -752,7 +740,6 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
                 if (q + 3 < total) load_item(q + 3, h1, q1);
             }
         }
-        YK_MOE_STAMP(3);
         __syncthreads();
         // the epilogue
         for (int o = threadIdx.x; o < ntl * nr * 16; o += kMoeThreads) {
@@ -771,13 +758,6 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
         __syncthreads();
         if (item_of(k + 1) >= items) break;
     }
-#ifdef YK_MOE_TIMING
-    YK_MOE_STAMP(4);
-    if (yk_moe_dbg && (threadIdx.x & 63) == 0) {
-        uint64_t *o = yk_moe_dbg + (((uint64_t)blockIdx.y * gridDim.x + blockIdx.x) * kMoeWaves + (threadIdx.x >> 6)) * 8;
-        for (int i = 0; i < 8; i++) o[i] = ts[i];
-    }
-#endif
 }
 
 // ---------------------------------------------------------------- reduce

@@ -44,8 +44,9 @@ struct GdnArgs {
     int nreq;  // requests in one launch (column-split kernels): states and rows request-major
 };
 
+// tokens null: every row embeds host_token.
 hipError_t launch_embedding(const void *table, uint32_t dtype, uint64_t row_bytes, const int32_t *tokens, int vocab,
-                            int cols, int rows, float *out, hipStream_t s);
+                            int cols, int rows, float *out, hipStream_t s, int host_token = 0);
 hipError_t launch_rmsnorm_rows(const float *src, const float *w, float *dst, int cols, int rows, uint64_t src_stride,
                                uint64_t dst_stride, float eps, hipStream_t s);
 // bg_reduce_kernel then rmsnorm_rows_kernel in one launch: out = sum of the

@@ -151,6 +151,352 @@ static yuuka_status check_gdn(const GdnArgs &g, const char *what) {
     return YUUKA_OK;
 }
 
+
+// ------------------------------------------------------------------------
+// Single-token decode ops (engine/gpu/plan.go:238-307 buildDecodePlan, layouts
+// backend/hip/hip.go): each runs as the one-row form of a verify kernel.
+
+// RECURRENT_TOKEN / GDN read q, k and v from one row laid out [q groups | k
+// groups | v heads] (plan.go:484-497: offsets 0, keyDim and 2 keyDim of the
+// conv buffer), as the recurrent kernels here do.
+static bool qkv_contiguous(const yuuka_op &op, uint64_t key_dim) {
+    return op.buf[1] && op.buf[1] == op.buf[2] && op.buf[1] == op.buf[3] && op.off[2] == op.off[1] + key_dim * 4 &&
+           op.off[3] == op.off[1] + 2 * key_dim * 4;
+}
+
+// GdnArgs of one decode row: groups q/k groups, heads value heads of
+// `state` columns, conv_dim channels.
+static GdnArgs gdn_row(int groups, int heads, int state, int conv_dim, int kernel, float eps, float q_scale) {
+    GdnArgs g{};
+    g.rows = 1;
+    g.groups = groups;
+    g.rank = heads;
+    g.state = state;
+    g.conv_dim = conv_dim;
+    g.inner = heads * state;
+    g.kernel = kernel;
+    g.eps = eps;
+    g.q_scale = q_scale;
+    g.coef = 0;
+    g.nreq = 1;
+    return g;
+}
+
+static AttnArgs attn_paged_args(const yuuka_op &op) {  // hip.go:1548-1585
+    AttnArgs a{};
+    a.kv_heads = (int)op.n[0];
+    a.heads = (int)op.n[1];
+    a.head_dim = (int)op.n[2];
+    a.kv_dim = (int)op.n[3];
+    a.rows = 1;
+    a.displacement = 0;
+    a.block_size = (int)op.u[0];
+    a.capacity = (int)op.u[1];
+    bool ok;
+    a.fmt = kv_fmt(op.u[2], &ok);
+    a.gated = op.u[3] == 0;
+    a.scale = op.f[0];
+    return a;
+}
+
+static yuuka_status validate_decode_op(const yuuka_op &op, uint64_t *ws, bool *handled) {
+    *handled = true;
+    switch (op.code) {
+    case YUUKA_OP_EMBEDDING: {  // hip.go:895-921: buf0 W, buf1 out; n={cols, row_bytes}; u0 dtype; the plan's token
+        const uint64_t cols = op.n[0], rb = op.n[1];
+        const uint32_t dt = op.u[0];
+        if (dt != YUUKA_DTYPE_F32 && dt != YUUKA_DTYPE_F16 && dt != YUUKA_DTYPE_Q8_0 && dt != YUUKA_DTYPE_Q4_K &&
+            dt != YUUKA_DTYPE_Q6_K)
+            return fail(YUUKA_ERR_UNSUPPORTED, "embedding dtype %u", dt);
+        if (!cols || row_bytes(dt, cols) != rb) return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid embedding shape");
+        if (!buf_ok(op.buf[0], op.off[0], rb) || !buf_ok(op.buf[1], op.off[1], cols * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "embedding buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_RMSNORM: {  // hip.go:541-554: buf0 src, buf1 weight, buf2 dst; n0; f0 eps
+        const uint64_t n = op.n[0];
+        if (!n || !buf_ok(op.buf[0], op.off[0], n * 4) || !buf_ok(op.buf[1], op.off[1], n * 4) ||
+            !buf_ok(op.buf[2], op.off[2], n * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid RMSNorm buffers or width");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_RMSNORM_HEADS: {  // hip.go:593-608: n={size, heads, stride}
+        const uint64_t size = op.n[0], heads = op.n[1], stride = op.n[2];
+        if (!size || !heads || stride < size) return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid head RMSNorm dimensions");
+        const uint64_t span = (heads - 1) * stride + size;
+        if (!buf_ok(op.buf[0], op.off[0], span * 4) || !buf_ok(op.buf[1], op.off[1], size * 4) ||
+            !buf_ok(op.buf[2], op.off[2], span * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "head RMSNorm buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_ROPE: {  // hip.go:610-622: buf0 data; n={heads, stride, head_dim, rot_dim}; f0 base
+        const uint64_t heads = op.n[0], stride = op.n[1], hd = op.n[2], rot = op.n[3];
+        if (!heads || !rot || rot % 2 || rot > hd || stride < hd)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid RoPE dimensions");
+        if (!buf_ok(op.buf[0], op.off[0], ((heads - 1) * stride + hd) * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "RoPE buffer too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_KV_WRITE_PAGED: {  // hip.go:1495-1528 with one row
+        const uint64_t kv_dim = op.n[0];
+        const uint32_t bs = op.u[0], cap = op.u[1];
+        bool ok;
+        kv_fmt(op.u[2], &ok);
+        if (!ok) return fail(YUUKA_ERR_UNSUPPORTED, "KV pool dtype %u (F32 and F16 are served)", op.u[2]);
+        if (!kv_dim || !bs || !cap || bs > cap) return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid paged KV write dimensions");
+        const uint64_t blocks = (cap + bs - 1) / bs;
+        if (!buf_ok(op.buf[0], op.off[0], kv_dim * 4) || !buf_ok(op.buf[1], op.off[1], kv_dim * 4) || !op.buf[2] ||
+            !op.buf[3] || !buf_ok(op.buf[4], op.off[4], blocks * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "paged KV write buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_ATTENTION_PAGED: {  // hip.go:1548-1585: buf0 q, buf1/2 pools, buf3 out, buf4 scores, buf5 table
+        const AttnArgs a = attn_paged_args(op);
+        bool ok;
+        kv_fmt(op.u[2], &ok);
+        if (!ok) return fail(YUUKA_ERR_UNSUPPORTED, "KV pool dtype %u (F32 and F16 are served)", op.u[2]);
+        if (a.heads <= 0 || a.kv_heads <= 0 || a.heads % a.kv_heads || a.kv_dim != a.kv_heads * a.head_dim ||
+            a.block_size <= 0 || a.capacity <= 0 || a.block_size > a.capacity || op.n[4] < (uint64_t)a.capacity)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid paged attention dimensions");
+        if (a.head_dim % 64 || a.head_dim > 256)
+            return fail(YUUKA_ERR_UNSUPPORTED, "attention head dimension %d", a.head_dim);
+        const int qs = a.gated ? 2 * a.head_dim : a.head_dim;
+        const uint64_t blocks = ((uint64_t)a.capacity + a.block_size - 1) / a.block_size;
+        if (!buf_ok(op.buf[0], op.off[0], (uint64_t)a.heads * qs * 4) || !op.buf[1] || !op.buf[2] ||
+            !buf_ok(op.buf[3], op.off[3], (uint64_t)a.heads * a.head_dim * 4) ||
+            !buf_ok(op.buf[5], op.off[5], blocks * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "paged attention buffers too small");
+        *ws = attention_scratch_bytes(a);
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_CONV_L2NORM: {  // hip.go:691-712: n={channels, kernel, qk, q, state}; f={eps, q_scale}
+        const uint64_t ch = op.n[0], K = op.n[1], qk = op.n[2], q = op.n[3], st = op.n[4];
+        if (K < 2 || K > 8 || !ch || ch % 128 || st != 128 || qk != 2 * q || q % st || qk > ch)
+            return fail(YUUKA_ERR_UNSUPPORTED, "conv_l2norm shape (channels %llu, q %llu, k %llu, state %llu)",
+                        (unsigned long long)ch, (unsigned long long)q, (unsigned long long)(qk - q),
+                        (unsigned long long)st);
+        if (!buf_ok(op.buf[0], op.off[0], ch * (K - 1) * 4) || !buf_ok(op.buf[1], op.off[1], ch * K * 4) ||
+            !buf_ok(op.buf[2], op.off[2], ch * 4) || !buf_ok(op.buf[3], op.off[3], ch * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "conv_l2norm buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_CONV1D: {  // hip.go:643-655: n={channels, kernel}
+        const uint64_t ch = op.n[0], K = op.n[1];
+        if (K < 2 || K > 8 || !ch || ch % 128)
+            return fail(YUUKA_ERR_UNSUPPORTED, "conv1d shape (channels %llu, kernel %llu)", (unsigned long long)ch,
+                        (unsigned long long)K);
+        if (!buf_ok(op.buf[0], op.off[0], ch * (K - 1) * 4) || !buf_ok(op.buf[1], op.off[1], ch * K * 4) ||
+            !buf_ok(op.buf[2], op.off[2], ch * 4) || !buf_ok(op.buf[3], op.off[3], ch * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "conv1d buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_RECURRENT_TOKEN:  // hip.go:810-834: n={groups, heads, state}; f0 eps
+    case YUUKA_OP_GDN: {            // hip.go:657-689: n={groups, heads, state}
+        const uint64_t groups = op.n[0], heads = op.n[1], st = op.n[2];
+        const bool token = op.code == YUUKA_OP_RECURRENT_TOKEN;
+        if (st != 128 || !groups || !heads || heads % groups)
+            return fail(YUUKA_ERR_UNSUPPORTED, "recurrent token shape (groups %llu, heads %llu, state %llu)",
+                        (unsigned long long)groups, (unsigned long long)heads, (unsigned long long)st);
+        const uint64_t key_dim = groups * st, inner = heads * st;
+        if (!qkv_contiguous(op, key_dim))
+            return fail(YUUKA_ERR_UNSUPPORTED, "recurrent token: q, k and v must be one [q | k | v] row");
+        for (int i = 0; i < (token ? 11 : 9); i++)
+            if (!op.buf[i]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "recurrent token buffer %d is null", i);
+        if (!buf_ok(op.buf[0], op.off[0], heads * st * st * 4) ||
+            !buf_ok(op.buf[1], op.off[1], (2 * key_dim + inner) * 4) || !buf_ok(op.buf[4], op.off[4], heads * 4) ||
+            !buf_ok(op.buf[5], op.off[5], heads * 4) || !buf_ok(op.buf[6], op.off[6], heads * 4) ||
+            !buf_ok(op.buf[7], op.off[7], heads * 4) || !buf_ok(op.buf[8], op.off[8], inner * 4) ||
+            (token && (!buf_ok(op.buf[9], op.off[9], st * 4) || !buf_ok(op.buf[10], op.off[10], inner * 4))))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "recurrent token buffers too small");
+        *ws = token ? inner * 4 : 0;
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_L2NORM: {  // hip.go:556-575: buf0 src, buf2 dst; n={heads, size, stride}; f={eps, scale}
+        const uint64_t heads = op.n[0], size = op.n[1], stride = op.n[2];
+        if (!heads || !size || stride < size) return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid L2 norm dimensions");
+        const uint64_t span = (heads - 1) * stride + size;
+        if (!buf_ok(op.buf[0], op.off[0], span * 4) || !buf_ok(op.buf[2], op.off[2], span * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "L2 norm buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_GATED_RMSNORM: {  // hip.go:577-591: buf0 src, buf1 w, buf2 gate, buf3 dst; n={size, heads, size}
+        const uint64_t size = op.n[0], heads = op.n[1];
+        if (size != 128 || !heads || op.n[2] != size)
+            return fail(YUUKA_ERR_UNSUPPORTED, "gated RMSNorm over heads of %llu (128 is served)",
+                        (unsigned long long)size);
+        if (!buf_ok(op.buf[0], op.off[0], heads * size * 4) || !buf_ok(op.buf[1], op.off[1], size * 4) ||
+            !buf_ok(op.buf[2], op.off[2], heads * size * 4) || !buf_ok(op.buf[3], op.off[3], heads * size * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "gated RMSNorm buffers too small");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_SCALE: {  // hip.go:884-893: buf0 x; n0; f0 scale
+        if (!op.n[0] || !buf_ok(op.buf[0], op.off[0], op.n[0] * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid SCALE buffer or count");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_QUANT_Q8_1:             // hip.go:1041-1073: buf0 x, buf1 qs, buf2 ds; n={n_in, batch}
+    case YUUKA_OP_SILU_MUL_QUANT_Q8_1: {  // hip.go:1075-1093: buf0 gate, buf1 up, buf2 qs, buf3 ds
+        const bool swiglu = op.code == YUUKA_OP_SILU_MUL_QUANT_Q8_1;
+        const uint64_t n = op.n[0] * (op.n[1] ? op.n[1] : 1);
+        const int q = swiglu ? 2 : 1;
+        if (!op.n[0] || op.n[0] % 128 || !buf_ok(op.buf[0], op.off[0], n * 4) ||
+            (swiglu && !buf_ok(op.buf[1], op.off[1], n * 4)) || !buf_ok(op.buf[q], op.off[q], n) ||
+            !buf_ok(op.buf[q + 1], op.off[q + 1], n / 4) || op.off[q + 1] % 8)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid Q8_1 quantization shape or buffers");
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_GEMV_Q8_1: {  // hip.go:1256-1321: buf0 W, buf1 qs (or x), buf2 ds, buf3 out; n={n_in, n_out}; u0 dtype; u1 fused
+        const uint64_t K = op.n[0], N = op.n[1];
+        const bool fused = op.u[1] != 0;
+        yuuka_status st = check_verify_gemm(K, N, 1, op.u[0], 1);
+        if (st != YUUKA_OK) return st;
+        if (op.off[0] % 16 || !buf_ok(op.buf[0], op.off[0], row_bytes(op.u[0], K) * N) ||
+            !buf_ok(op.buf[1], op.off[1], fused ? K * 4 : K) || (!fused && !buf_ok(op.buf[2], op.off[2], K / 4)) ||
+            (!fused && op.off[2] % 8) || !buf_ok(op.buf[3], op.off[3], N * 4))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "int8 GEMV buffers too small");
+        // the dequantized row (and, fused, its Q8_1 digits and scales)
+        *ws = K * 4 + (fused ? ((K + 255) & ~255ull) + K / 4 : 0);
+        return YUUKA_OK;
+    }
+    default:
+        *handled = false;
+        return YUUKA_OK;
+    }
+}
+
+static yuuka_status execute_decode_op(const yuuka_op &op, const ExecCtx &ctx, bool *handled) {
+    *handled = true;
+    hipError_t err = hipSuccess;
+    const hipStream_t s = ctx.stream;
+    switch (op.code) {
+    case YUUKA_OP_EMBEDDING: {
+        // the token is the plan's dynamic token (device word 0 of the
+        // {token, position} buffer under graph replay, else the host value)
+        const uint64_t rb = op.n[1];
+        const uint64_t vocab = (op.buf[0]->bytes - op.off[0]) / rb;
+        err = launch_embedding(at<const uint8_t>(op, 0), op.u[0], rb, ctx.dyn, (int)std::min<uint64_t>(vocab, INT32_MAX),
+                               (int)op.n[0], 1, at<float>(op, 1), s, ctx.token);
+        break;
+    }
+    case YUUKA_OP_RMSNORM:
+        err = launch_rmsnorm_rows(at<const float>(op, 0), at<const float>(op, 1), at<float>(op, 2), (int)op.n[0], 1,
+                                  op.n[0], op.n[0], op.f[0], s);
+        break;
+    case YUUKA_OP_RMSNORM_HEADS:
+        err = launch_rmsnorm_heads(at<const float>(op, 0), at<const float>(op, 1), at<float>(op, 2), (int)op.n[0],
+                                   (int)op.n[1], (int)op.n[2], 1, op.f[0], s);
+        break;
+    case YUUKA_OP_ROPE:
+        err = launch_rope(at<float>(op, 0), (int)op.n[0], (int)op.n[1], (int)op.n[3], 1, op.n[0] * op.n[1],
+                          (double)op.f[0], dyn_of(ctx), 0, s);
+        break;
+    case YUUKA_OP_KV_WRITE_PAGED: {
+        if (!ctx.dyn && (uint64_t)ctx.position + 1 > op.u[1])
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "paged KV write at %u exceeds capacity %u", ctx.position, op.u[1]);
+        bool ok;
+        err = launch_kv_write(at<const float>(op, 0), at<const float>(op, 1), at<uint8_t>(op, 2), at<uint8_t>(op, 3),
+                              at<const int32_t>(op, 4), (int)op.n[0], 1, (int)op.u[0], kv_fmt(op.u[2], &ok),
+                              dyn_of(ctx), 0, s);
+        break;
+    }
+    case YUUKA_OP_ATTENTION_PAGED: {
+        const AttnArgs a = attn_paged_args(op);
+        if (!ctx.dyn && ctx.position >= (uint32_t)a.capacity)
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "paged attention position %u exceeds capacity %d", ctx.position,
+                        a.capacity);
+        const int hint = ctx.dyn ? -1 : (int)ctx.position;
+        err = launch_attention(at<const float>(op, 0), at<const uint8_t>(op, 1), at<const uint8_t>(op, 2),
+                               at<const int32_t>(op, 5), at<float>(op, 3), a, ctx.ws, dyn_of(ctx), hint, s);
+        break;
+    }
+    case YUUKA_OP_CONV_L2NORM:
+    case YUUKA_OP_CONV1D: {
+        // the convolution of the row against the stored window, SiLU, the q/k
+        // L2 norms (CONV_L2NORM only), then the window advances by the row
+        const bool norm = op.code == YUUKA_OP_CONV_L2NORM;
+        const int st = norm ? (int)op.n[4] : 128;
+        const GdnArgs g = gdn_row(norm ? (int)(op.n[3] / op.n[4]) : 0, 0, st, (int)op.n[0], (int)op.n[1],
+                                  norm ? op.f[0] : 0.0f, norm ? op.f[1] : 1.0f);
+        err = launch_gdn_conv(at<const float>(op, 0), at<const float>(op, 2), at<const float>(op, 1), at<float>(op, 3),
+                              g, s);
+        if (err == hipSuccess) err = launch_gdn_conv_commit(at<float>(op, 0), at<const float>(op, 2), g, nullptr, s);
+        break;
+    }
+    case YUUKA_OP_RECURRENT_TOKEN:
+    case YUUKA_OP_GDN: {
+        // one row of the delta rule on the stored state (decay, S^T k, the
+        // rank-1 update, S^T q); RECURRENT_TOKEN then applies the gated RMSNorm
+        const bool token = op.code == YUUKA_OP_RECURRENT_TOKEN;
+        const int groups = (int)op.n[0], heads = (int)op.n[1], st = (int)op.n[2];
+        const GdnArgs g = gdn_row(groups, heads, st, 2 * groups * st + heads * st, 2, token ? op.f[0] : 0.0f, 1.0f);
+        float *raw = token ? static_cast<float *>(ctx.ws) : at<float>(op, 8);
+        err = launch_gdn_scan(at<float>(op, 0), at<const float>(op, 1), at<const float>(op, 4), at<const float>(op, 5),
+                              at<const float>(op, 6), at<const float>(op, 7), raw, g, 2, nullptr, s);
+        if (err == hipSuccess && token)
+            err = launch_gdn_norm_gate(raw, at<const float>(op, 10), at<const float>(op, 9), at<float>(op, 8), g, s);
+        break;
+    }
+    case YUUKA_OP_L2NORM:
+        err = launch_l2norm_heads(at<const float>(op, 0), at<float>(op, 2), (int)op.n[0], (int)op.n[1], op.n[2],
+                                  op.f[0], op.f[1], s);
+        break;
+    case YUUKA_OP_GATED_RMSNORM: {
+        const GdnArgs g = gdn_row(1, (int)op.n[1], (int)op.n[0], 0, 2, op.f[0], 1.0f);
+        err = launch_gdn_norm_gate(at<const float>(op, 0), at<const float>(op, 2), at<const float>(op, 1),
+                                   at<float>(op, 3), g, s);
+        break;
+    }
+    case YUUKA_OP_SCALE:
+        err = launch_scale_f32(at<float>(op, 0), op.n[0], op.f[0], s);
+        break;
+    case YUUKA_OP_QUANT_Q8_1:
+        err = launch_quant_q8_1(at<const float>(op, 0), nullptr, at<void>(op, 1), at<void>(op, 2),
+                                op.n[0] * (op.n[1] ? op.n[1] : 1), s);
+        break;
+    case YUUKA_OP_SILU_MUL_QUANT_Q8_1:
+        err = launch_quant_q8_1(at<const float>(op, 0), at<const float>(op, 1), at<void>(op, 2), at<void>(op, 3),
+                                op.n[0] * (op.n[1] ? op.n[1] : 1), s);
+        break;
+    case YUUKA_OP_GEMV_Q8_1: {
+        // the matvec over the Q8_1 row's exact values q * d (the digits are
+        // made here from the FP32 row when fused)
+        const uint64_t K = op.n[0];
+        float *x = static_cast<float *>(ctx.ws);
+        const void *qs = at<const void>(op, 1), *ds = at<const void>(op, 2);
+        if (op.u[1]) {
+            uint8_t *q8 = static_cast<uint8_t *>(ctx.ws) + K * 4;
+            uint8_t *d8 = q8 + ((K + 255) & ~255ull);
+            err = launch_quant_q8_1(at<const float>(op, 1), nullptr, q8, d8, K, s);
+            qs = q8;
+            ds = d8;
+        }
+        if (err == hipSuccess) err = launch_dequant_q8_1(qs, ds, x, K, s);
+        if (err != hipSuccess) break;
+        FusedGemmArgs a{};
+        a.x = x;
+        a.K = (int)K;
+        a.rows = 1;
+        a.epilogue = kEpiStore;
+        a.nseg = 1;
+        FusedSeg &g = a.seg[0];
+        g.dtype = (int)op.u[0];
+        g.n = (int)op.n[1];
+        g.row_bytes = (uint32_t)row_bytes(op.u[0], K);
+        g.w = at<const uint8_t>(op, 0);
+        g.w_bytes = (uint32_t)(g.row_bytes * (uint64_t)g.n);
+        g.out = at<float>(op, 3);
+        a.chunk_sb = fused_gemm_chunk_sb(1, (int)K, 1, false, false);
+        err = launch_fused_gemm(a, 1, s);
+        break;
+    }
+    default:
+        *handled = false;
+        return YUUKA_OK;
+    }
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "decode op %u launch: %s", op.code, hip_error(err));
+    return YUUKA_OK;
+}
+
 bool op_uses_position(const yuuka_op &op) {
     switch (op.code) {
     case YUUKA_OP_ROPE_BATCH:
@@ -159,6 +505,11 @@ bool op_uses_position(const yuuka_op &op) {
     case YUUKA_EXT_OP_ROPE_TABLE:
     case YUUKA_EXT_OP_ATTN_VERIFY:
         return !(op.flags & YUUKA_EXT_FLAG_OWN_POS);
+    case YUUKA_OP_EMBEDDING:  // the dynamic token
+    case YUUKA_OP_ROPE:
+    case YUUKA_OP_KV_WRITE_PAGED:
+    case YUUKA_OP_ATTENTION_PAGED:
+        return true;
     default:
         return false;
     }
@@ -166,6 +517,9 @@ bool op_uses_position(const yuuka_op &op) {
 
 yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
     *ws = 0;
+    bool decode = false;
+    const yuuka_status dst = validate_decode_op(op, ws, &decode);
+    if (decode) return dst;
     switch (op.code) {
     case YUUKA_OP_ADD: {  // hip.go:852-861: buf0 x (in/out), buf1 delta; n0
         const uint64_t n = op.n[0];
@@ -538,6 +892,20 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
 
 bool gemm_chain_member(const yuuka_op &op) { return op.code == YUUKA_EXT_OP_GEMM_FUSED && fused_many_rows(op); }
 
+bool stream_chain_stage(const yuuka_op &op, FusedChainStage *st) {
+    if (op.code != YUUKA_EXT_OP_GEMM_FUSED || fused_many_rows(op)) return false;
+    FusedGemmArgs a = fused_args(op);
+    const int tt = fused_tiles(op, a.nseg);
+    a.chunk_sb = fused_gemm_chunk_sb(a.rows, a.K, tt, a.norm != nullptr, a.gate != nullptr);
+    return fused_gemm_chain_stage(a, tt, st);
+}
+
+yuuka_status execute_stream_chain(const FusedChainStage *st, int n, const ExecCtx &ctx) {
+    const hipError_t err = launch_fused_gemm_chain(st, n, ctx.chain_sync, ctx.stream);
+    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "chained GEMM_FUSED launch: %s", hip_error(err));
+    return YUUKA_OK;
+}
+
 bool gemm_chain_ws(const yuuka_op &op, uint64_t *quant, uint64_t *part) {
     if (!gemm_chain_member(op)) return false;
     const int nseg = fused_segments(op);
@@ -604,6 +972,9 @@ yuuka_status execute_gdn_commit_run(const yuuka_op *ops, int count, const ExecCt
 }
 
 yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
+    bool decode = false;
+    const yuuka_status dst = execute_decode_op(op, ctx, &decode);
+    if (decode) return dst;
     hipError_t err = hipSuccess;
     const hipStream_t s = ctx.stream;
     switch (op.code) {

@@ -5,6 +5,7 @@
 #include <cstdlib>
 
 #include "plan.h"
+#include "fgemm.h"
 
 namespace yk {
 
@@ -23,6 +24,11 @@ yuuka_status execute_gdn_commit_run(const yuuka_op *ops, int count, const ExecCt
 // GEMM_FUSED over more than 8 rows (the many-row kernel), and its workspace
 // in two parts (quantized rows, split partial sums).
 bool gemm_chain_member(const yuuka_op &op);
+// A GEMM_FUSED op the streaming kernel serves in a chained form (*st set).
+bool stream_chain_stage(const yuuka_op &op, FusedChainStage *st);
+// Runs ops[0..n) (stream_chain_stage true for each, supported together) as
+// one chained launch.
+yuuka_status execute_stream_chain(const FusedChainStage *st, int n, const ExecCtx &ctx);
 bool gemm_chain_ws(const yuuka_op &op, uint64_t *quant, uint64_t *part);
 // A run of n consecutive many-row GEMM_FUSED ops (launch_fused_gemm_rows_chain:
 // each split reduction inside the next member's prologue where they link),
@@ -34,6 +40,14 @@ yuuka_status execute_gemm_chain(const yuuka_op *ops, int n, const yuuka_op *afte
 
 // Elementwise launchers (k_ops.hip).
 hipError_t launch_copy_f32(float *dst, const float *src, uint64_t n, hipStream_t stream);
+// One-row decode helpers (k_decode.hip).
+hipError_t launch_scale_f32(float *x, uint64_t n, float s, hipStream_t stream);
+hipError_t launch_l2norm_heads(const float *src, float *dst, int heads, int size, uint64_t stride, float eps,
+                               float extra, hipStream_t stream);
+// Q8_1: n values (n % 32 == 0) -> int8 digits qs[n], {d, d * sum} pairs ds[n / 32];
+// with `up`, the values are SiLU(x) * up.
+hipError_t launch_quant_q8_1(const float *x, const float *up, void *qs, void *ds, uint64_t n, hipStream_t stream);
+hipError_t launch_dequant_q8_1(const void *qs, const void *ds, float *x, uint64_t n, hipStream_t stream);
 hipError_t launch_silu_mul(const float *gate, const float *up, float *out, uint64_t n,
                            hipStream_t stream);
 

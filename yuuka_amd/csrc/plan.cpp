@@ -4,6 +4,7 @@
 #include "plan.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <exception>
 #include <new>
@@ -11,6 +12,16 @@
 #include "ops.h"
 
 namespace yk {
+
+// Chained streaming GEMMs (k_fchain.hip) run only with YUUKA_STREAM_CHAIN=1:
+// at the config-2 verify step the chained launch measured slower than one
+// launch per projection (the stage hand-off and the device-scope activation
+// reads cost more than the launch boundaries they remove). Read when a plan
+// is executed or captured.
+static bool stream_chains_enabled() {
+    const char *e = std::getenv("YUUKA_STREAM_CHAIN");
+    return e && e[0] == '1';
+}
 
 static bool buf_ok(const yuuka_buffer *b, uint64_t off, uint64_t bytes) {
     return b != nullptr && off <= b->bytes && bytes <= b->bytes - off;
@@ -56,6 +67,37 @@ static bool fused_form(const yuuka_op &op, yuuka_op *f, uint64_t *ws) {
         *ws = need;
         return true;
     }
+    if (op.code == YUUKA_OP_GEMV_PAIR) {
+        // hip.go:748-783: buf0 A, buf1 B, buf2 x, buf3 outA, buf4 outB;
+        // n = {K, N_A, N_B}; u = {dtype A, dtype B, epilogue}: both rows
+        // written (0) or outA = SiLU(A x) * (B x) (1)
+        f->buf[0] = op.buf[2];
+        f->off[0] = op.off[2];
+        f->buf[2] = op.buf[0];
+        f->off[2] = op.off[0];
+        f->buf[3] = op.buf[1];
+        f->off[3] = op.off[1];
+        f->buf[6] = op.buf[3];
+        f->off[6] = op.off[3];
+        if (op.u[2] == 0) {
+            f->buf[7] = op.buf[4];
+            f->off[7] = op.off[4];
+        } else if (op.u[2] != 1) {
+            return false;
+        }
+        f->n[0] = op.n[0];
+        f->n[1] = 1;
+        f->n[2] = op.n[1];
+        f->n[3] = op.n[2];
+        f->u[0] = (op.u[0] & 0xff) | ((op.u[1] & 0xff) << 8);
+        f->u[1] = op.u[2] == 1 ? 2 : 0;
+        uint64_t need = 0;
+        if (validate_model_op(*f, &need) != YUUKA_OK) return false;
+        *ws = need;
+        return true;
+    }
+    // LM_HEAD / GEMV_BATCH / GEMV (one row) / GEMV_RESIDUAL (hip.go:714-742:
+    // buf3 the residual, out = W x + res)
     f->buf[0] = op.buf[1];
     f->off[0] = op.off[1];
     f->buf[2] = op.buf[0];
@@ -63,9 +105,14 @@ static bool fused_form(const yuuka_op &op, yuuka_op *f, uint64_t *ws) {
     f->buf[6] = op.buf[2];
     f->off[6] = op.off[2];
     f->n[0] = op.n[0];
-    f->n[1] = op.n[2];
+    f->n[1] = op.code == YUUKA_OP_GEMV ? 1 : op.n[2];
     f->n[2] = op.n[1];
     f->u[0] = op.u[0];
+    if (op.code == YUUKA_OP_GEMV_RESIDUAL) {
+        f->buf[10] = op.buf[3];
+        f->off[10] = op.off[3];
+        f->u[1] = 1;  // residual epilogue
+    }
     uint64_t need = 0;
     if (validate_model_op(*f, &need) != YUUKA_OK) return false;
     *ws = need;
@@ -74,13 +121,32 @@ static bool fused_form(const yuuka_op &op, yuuka_op *f, uint64_t *ws) {
 
 static yuuka_status validate(const yuuka_op &op, Need *need) {
     switch (op.code) {
+    case YUUKA_OP_GEMV_RESIDUAL:
+    case YUUKA_OP_GEMV_PAIR: {
+        // the single-token decode plan's fused projections (plan.go:84-149)
+        for (int i = 0; i < 4; i++)
+            if (!op.buf[i]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "decode matvec buffer %d is null", i);
+        if (op.code == YUUKA_OP_GEMV_PAIR && op.u[2] == 0 && !op.buf[4])
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "a matvec pair that writes both rows needs both outputs");
+        const uint64_t rows = op.code == YUUKA_OP_GEMV_RESIDUAL ? op.n[2] : 1;
+        yuuka_status st = check_verify_gemm(op.n[0], op.n[1], rows, op.u[0], 16);
+        if (st == YUUKA_OK && op.code == YUUKA_OP_GEMV_PAIR) st = check_verify_gemm(op.n[0], op.n[2], 1, op.u[1], 1);
+        if (st != YUUKA_OK) return st;
+        yuuka_op f;
+        if (!fused_form(op, &f, &need->ws))
+            return fail(YUUKA_ERR_UNSUPPORTED, "decode matvec %u: shape %llux%llu is not served", op.code,
+                        (unsigned long long)op.n[1], (unsigned long long)op.n[0]);
+        return YUUKA_OK;
+    }
+    case YUUKA_OP_GEMV:
     case YUUKA_OP_LM_HEAD:
     case YUUKA_OP_GEMV_BATCH: {
         // LM_HEAD: buf0 W, buf1 x, buf2 out; n={K,N,rows}; u0 dtype (reference :385-387).
         // GEMV_BATCH (hip.go:492-520): buf0 W, buf1 x, buf2 out; n={K,N,batch}; u0 dtype.
+        // GEMV (hip.go:449-472): the same for one row (n2 unused).
         for (int i = 0; i < 3; i++)
             if (!op.buf[i]) return fail(YUUKA_ERR_INVALID_ARGUMENT, "verify GEMM buffer %d is null", i);
-        const uint64_t K = op.n[0], N = op.n[1], rows = op.n[2];
+        const uint64_t K = op.n[0], N = op.n[1], rows = op.code == YUUKA_OP_GEMV ? 1 : op.n[2];
         yuuka_status st = check_verify_gemm(K, N, rows, op.u[0], 16);
         if (st != YUUKA_OK) return st;
         if (op.off[0] % 16 || op.off[1] % 16 || op.off[2] % 4)
@@ -137,13 +203,22 @@ static yuuka_status execute(const yuuka_op &op, const ExecCtx &ctx) {
         if (!fused_form(op, &f, &ws)) return fail(YUUKA_ERR_INTERNAL, "GEMM op changed after validation");
         return execute_model_op(f, ctx);
     }
+    case YUUKA_OP_GEMV_RESIDUAL:
+    case YUUKA_OP_GEMV_PAIR: {
+        yuuka_op f;
+        uint64_t ws = 0;
+        if (!fused_form(op, &f, &ws)) return fail(YUUKA_ERR_INTERNAL, "decode matvec op changed after validation");
+        return execute_model_op(f, ctx);
+    }
+    case YUUKA_OP_GEMV:
     case YUUKA_OP_LM_HEAD:
     case YUUKA_OP_GEMV_BATCH: {
         yuuka_op f;
         uint64_t ws = 0;
         if (fused_form(op, &f, &ws)) return execute_model_op(f, ctx);
         return run_verify_gemm(ctx.stream, at<const uint8_t>(op, 0), op.u[0], at<const float>(op, 1),
-                               at<float>(op, 2), op.n[0], op.n[1], op.n[2], ctx.ws, ctx.tickets);
+                               at<float>(op, 2), op.n[0], op.n[1], op.code == YUUKA_OP_GEMV ? 1 : op.n[2], ctx.ws,
+                               ctx.tickets);
     }
     default:
         return execute_model_op(op, ctx);
@@ -160,10 +235,11 @@ static yuuka_status prepare(yuuka_plan *plan) {
         if (err != hipSuccess) return fail(YUUKA_ERR_ALLOCATION, "plan workspace: %s", hip_error(err));
         plan->ws_bytes = want;
     }
-    if (plan->tickets_len < plan->ticket_need + 1) {
+    // split-K tickets, then the chained GEMMs' counters in the last words
+    if (plan->tickets_len < plan->ticket_need + 1 + kFusedChainSyncWords) {
         if (plan->tickets) (void)hipFree(plan->tickets);
         plan->tickets = nullptr;
-        const uint32_t want = plan->ticket_need + 64;
+        const uint32_t want = plan->ticket_need + 64 + kFusedChainSyncWords;
         hipError_t err = hipMalloc(reinterpret_cast<void **>(&plan->tickets), (size_t)want * 4);
         if (err == hipSuccess) err = hipMemset(plan->tickets, 0, (size_t)want * 4);
         if (err != hipSuccess) return fail(YUUKA_ERR_ALLOCATION, "plan tickets: %s", hip_error(err));
@@ -190,6 +266,7 @@ static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token,
                             uint64_t capacity, uint64_t *count) {
     ExecCtx ctx{stream, token, position, dyn, plan->ws, plan->tickets, plan->ws_bytes};
     ctx.part_off = plan->chain_quant ? (plan->chain_quant + 255) & ~255ull : 0;
+    if (stream_chains_enabled()) ctx.chain_sync = plan->tickets + (plan->tickets_len - kFusedChainSyncWords);
     uint64_t n = 0;
     hipEvent_t a = nullptr, b = nullptr;
     if (times) {
@@ -225,15 +302,31 @@ static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token,
                 break;
             }
         if (st != YUUKA_OK) break;
+        auto usable = [&](int k) {
+            if ((plan->ops[k].flags & YUUKA_OP_FLAG_TAIL) && !run_tail) return false;
+            for (int i = 0; i < 16; i++)
+                if (plan->ops[k].buf[i] && !plan->ops[k].buf[i]->ptr) return false;
+            return true;
+        };
+        if (!times && ctx.chain_sync) {
+            // a run of dependent streaming GEMMs (a layer's out-projection,
+            // FFN and the next in-projection): one chained launch
+            FusedChainStage cs[kFusedChainMax];
+            int j = 0;
+            while (j < kFusedChainMax && oi + j < nops && usable(oi + j) && stream_chain_stage(plan->ops[oi + j], &cs[j]))
+                j++;
+            while (j >= 2 && !fused_gemm_chain_supported(cs, j)) j--;
+            if (j >= 2) {
+                st = execute_stream_chain(cs, j, ctx);
+                if (st != YUUKA_OK) break;
+                n += j;
+                oi += j - 1;
+                continue;
+            }
+        }
         if (!times && ctx.part_off && gemm_chain_member(op)) {
             // a run of many-row GEMMs: split reductions inside the next
             // member's prologue (and a following RMSNorm of the last output)
-            auto usable = [&](int k) {
-                if ((plan->ops[k].flags & YUUKA_OP_FLAG_TAIL) && !run_tail) return false;
-                for (int i = 0; i < 16; i++)
-                    if (plan->ops[k].buf[i] && !plan->ops[k].buf[i]->ptr) return false;
-                return true;
-            };
             int j = 1;
             while (oi + j < nops && gemm_chain_member(plan->ops[oi + j]) && usable(oi + j)) j++;
             const yuuka_op *after = oi + j < nops && usable(oi + j) ? &plan->ops[oi + j] : nullptr;
