@@ -43,7 +43,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--config", type=int, default=None,
+                    help="one configuration (default: config 2 as the value, configs 1, 3, 4, 5 beside it)")
     ap.add_argument("--drafts", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -281,10 +282,73 @@ def dominant_kernel(dev, cfg, rows, rng):
     plan.destroy()
     for b in wg + wu:
         b.free()
+    if rows <= 8:
+        kernel = f"fgemm_stream_kernel<12,2,8,1,true> (GEMM_FUSED SwiGLU) 2x{N}x{K} Q4_K M={rows}"
+        traffic = read_traffic("fgemm_ffn_swiglu_pmc.md")
+    else:  # many-row GEMM: quantizing prologue + bg_gemm_kernel, timed together
+        kernel = f"bg_prologue_kernel + bg_gemm_kernel (GEMM_FUSED SwiGLU, many-row) 2x{N}x{K} Q4_K M={rows}"
+        traffic = None
     return {"bound": "hbm", "achieved": gemm_ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": gemm_ach / HBM_PEAK_GBS, "traffic": read_traffic("fgemm_ffn_swiglu_pmc.md"),
-            "kernel": f"fgemm_stream_kernel<12,2,8,1,true> (GEMM_FUSED SwiGLU) 2x{N}x{K} Q4_K M={rows}",
+            "frac": gemm_ach / HBM_PEAK_GBS, "traffic": traffic, "kernel": kernel,
             "alg_bytes_per_launch": gemm_bytes, "avg_us": gemm_us, "launches": reps * copies}
+
+
+def moe_dominant(dev, cfg, rows, rng):
+    """Config 5's dominant kernel: the grouped expert gate/up GEMM (MOE_GATE_UP
+    with the SwiGLU epilogue on packed experts, as the engine launches it)
+    over rows routed by i.i.d. N(0,1) logits (the configured routing), timed
+    with HIP events on its stream; weight copies rotate so that >= 512 MB of
+    expert matrices stream per round. Algorithmic bytes: the gate and up
+    matrices of the experts the rows selected, the rows, the outputs."""
+    from yuuka_amd import hip, synth
+    E, used, F, H = cfg.n_experts, cfg.n_experts_used, cfg.expert_ffn, cfg.hidden
+    wq = synth.quant_matrix(rng, synth.Q4_K, E * F, H)
+    copies = max(1, -(-512 * 2**20 // (2 * wq.nbytes)))
+    st = hip.Stream(dev)
+    raw = dev.upload(wq)
+    packed = []
+    for _ in range(2 * copies):
+        b = dev.alloc(wq.nbytes)
+        hip.moe_pack_q4k(st, b, raw, E * F, H)
+        packed.append(b)
+    st.sync()
+    raw.free()
+    lb = dev.upload(rng.normal(0, 1, (rows, E)).astype(np.float32))
+    ids, w = dev.alloc(rows * used * 4), dev.alloc(rows * used * 4)
+    cnt = dev.alloc(E * 4)
+    ar, asl, aw = (dev.alloc(E * rows * used * 4) for _ in range(3))
+    xb = dev.upload(rng.normal(0, 1, (rows, H)).astype(np.float32))
+    act = dev.alloc(rows * used * F * 4)
+    route = hip.Plan(dev)
+    route.add(hip.OP["MOE_ROUTE"], [lb, ids, w, cnt, ar, asl, aw], n=[rows, E, used])
+    route.execute(st)
+    st.sync()
+    distinct = int((cnt.read(np.int32, E) > 0).sum())
+    plan = hip.Plan(dev)
+    for i in range(copies):
+        plan.add(hip.OP["MOE_GATE_UP"], [xb, packed[2 * i], packed[2 * i + 1], cnt, ar, asl, act, None],
+                 n=[H, F, rows, E, used], u=[synth.Q4_K], flags=hip.FLAG_MOE_SWIGLU | hip.FLAG_MOE_PACKED)
+    for _ in range(2):
+        plan.execute(st)
+    st.sync()
+    e0, e1 = hip.Event(dev, timed=True), hip.Event(dev, timed=True)
+    reps = max(1, 200 // copies)
+    e0.record(st)
+    for _ in range(reps):
+        plan.execute(st)
+    e1.record(st)
+    st.sync()
+    us = e1.elapsed_ms(e0) * 1e3 / (reps * copies)
+    nbytes = distinct * 2 * F * (H // 256) * 144 + rows * H * 4 + rows * used * F * 4
+    ach = nbytes / (us * 1e-6) / 1e9
+    plan.destroy()
+    route.destroy()
+    for b in packed + [lb, ids, w, cnt, ar, asl, aw, xb, act]:
+        b.free()
+    return {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": ach / HBM_PEAK_GBS,
+            "traffic": None, "kernel": f"moe_gemm_kernel (MOE_GATE_UP SwiGLU, packed) {E} experts {F}x{H} Q4_K, "
+                                       f"{rows} rows x top-{used}, N(0,1) routing: {distinct} experts",
+            "alg_bytes_per_launch": nbytes, "avg_us": us, "launches": reps * copies, "distinct_experts": distinct}
 
 
 def lm_head_only(dev):
@@ -347,9 +411,9 @@ def bench_config2(args):
 
     k = args.drafts
     steps, warmup = args.steps or 256, args.warmup if args.warmup is not None else 8
-    cfg = Mdl.replace(Mdl.QWEN35_4B_LIKE, capacity=512 + (steps + warmup + 4) * (k + 1))
+    cfg = Mdl.replace(Mdl.QWEN35_4B_LIKE, capacity=512 + (steps + warmup + 4) * (k + 1) + 64 * (k + 1) * 2)
     t0 = time.perf_counter()
-    w = Mdl.make_weights(cfg, seed=0)
+    w = model_weights("QWEN35_4B_LIKE", cfg)
     gen_s = time.perf_counter() - t0
     wbytes = Mdl.weight_bytes(w)
     dev = hip.Device(0)
@@ -385,6 +449,23 @@ def bench_config2(args):
         pending = int(res[0, 1])
         return int(res[0, 0]) + 1, int(res[0, 0]), k, eng.last_step_ms
 
+    lookup_drafts = [0]
+
+    def step_lookup_padded():
+        # the headline step: engine/speculative.go:68-261 with prompt-lookup
+        # drafts (lookupDraft, :39-66) topped up with uniform ids to the
+        # configured k = 4, so every step verifies k + 1 rows; the greedy
+        # decision runs on the device's own argmax (nothing prescribed)
+        nonlocal pending
+        d = lookup_draft(history, k)
+        lookup_drafts[0] += len(d)
+        d = d + drng.integers(0, cfg.vocab, k - len(d)).tolist()
+        res = eng.verify(np.array([pending] + d, np.int32), acc)
+        emitted = d[:res[0]] + [int(res[1])]
+        history.extend(emitted)
+        pending = int(res[1])
+        return len(emitted), int(res[0]), k, eng.last_step_ms
+
     def step_lookup():
         # engine/speculative.go:68-261 with prompt-lookup drafts (lookupDraft,
         # :39-66), unpadded: fewer than k drafts give a shorter verify step,
@@ -411,9 +492,16 @@ def bench_config2(args):
             gpu_ms.append(ms)
         return tokens, accepted, drafted, time.perf_counter() - t0, gpu_ms
 
-    tokens, accepted, drafted, wall, gpu_ms = run(step_argmax07, steps, warmup)
+    tokens, accepted, drafted, wall, gpu_ms = run(step_lookup_padded, steps, warmup)
     ms_per_step = wall * 1e3 / steps
     step_gpu_ms = float(np.median(gpu_ms))
+    lookup_share = lookup_drafts[0] / max(1, k * (steps + warmup))
+    f07 = run(step_argmax07, min(steps, 64), 2)
+    forced07 = {"accepted_tokens_per_s": f07[0] / f07[3], "accepted_tokens_per_step": f07[0] / min(steps, 64),
+                "acceptance_rate": f07[1] / max(1, f07[2]), "steps": min(steps, 64),
+                "verify_step_gpu_us_median": float(np.median(f07[4])) * 1e3,
+                "rule": "k uniform drafts, accept length prescribed: leading argmax hits with probability 0.7 "
+                        "each (the draft rule BASELINE states for configs[3])"}
     lk_steps = min(steps, 64)
     lk = run(step_lookup, lk_steps, 2)
     lookup = {"accepted_tokens_per_s": lk[0] / lk[3], "verify_steps_per_s": lk_steps / lk[3],
@@ -445,9 +533,10 @@ def bench_config2(args):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4_k/q6_k weights x int16-split activations (int32 MFMA), fp32 norms/attention/GDN",
-        "data": "synthetic: random-init Q4_K_M-mix weights (dequantized std ~0.02), random 512-token prompt, "
-                "k drafts per step that match the argmax with probability 0.7 each (accept length prescribed, "
-                "geometric); prompt-lookup drafting reported beside it",
+        "data": "synthetic: random-init Q4_K_M-mix weights (dequantized std ~0.02), random 512-token prompt; "
+                "k = 4 drafts per step from prompt lookup over the history (engine/speculative.go lookupDraft), "
+                "topped up with uniform random ids when lookup finds fewer; greedy decisions on the device's "
+                "argmax, nothing prescribed",
         "config": {"workload": "config2: Qwen3.5-4B-like hybrid decoder verify step, batch 1",
                    "hidden": cfg.hidden, "ffn": cfg.ffn, "layers": cfg.n_layers, "gdn_heads": cfg.rank,
                    "attn_heads": f"{cfg.heads}q/{cfg.kv_heads}kv x {cfg.head_dim}", "vocab": cfg.vocab,
@@ -457,7 +546,9 @@ def bench_config2(args):
         "verify_steps_per_s": steps / wall,
         "accepted_tokens_per_step": tokens / steps,
         "acceptance_rate": accepted / max(1, drafted),
-        "prompt_lookup": lookup,
+        "drafts_from_lookup": lookup_share,
+        "prompt_lookup_unpadded": lookup,
+        "forced_argmax07": forced07,
         "step_roofline": {"bound": "hbm", "achieved": step_ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": step_ach / HBM_PEAK_GBS, "alg_bytes_per_step": step_bytes,
                           "weights": wbytes, "kv": kv_bytes, "gdn_state": state_bytes, "logits": logit_bytes},
@@ -528,7 +619,7 @@ BATCHED = {
     4: dict(model="QWEN35_9B_LIKE", batch=4, prompt=16384, shared=0, k=16, accept="greedy", forced="geometric"),
     # MoE-like, 8 requests x 2048-token context, k = 4, T = 0.8.
     5: dict(model="QWEN35_MOE_LIKE", batch=8, prompt=2048, shared=0, k=4, accept="stochastic", temperature=0.8,
-            top_p=1.0, forced=None),
+            top_p=1.0, forced=None, router_normal=True),
 }
 
 
@@ -543,9 +634,10 @@ def bench_batched(args, which):
     steps, warmup = args.steps or 32, args.warmup if args.warmup is not None else 4
     base = getattr(Mdl, spec["model"])
     cap = P + (steps + warmup + 2) * (k + 1) + 16
-    cfg = Mdl.replace(base, batch=B, max_rows=max(16, k + 1), capacity=cap)
+    cfg = Mdl.replace(base, batch=B, max_rows=max(16, k + 1), capacity=cap,
+                      router_normal_seed=7 if spec.get("router_normal") else 0)
     t0 = time.perf_counter()
-    w = Mdl.make_weights(cfg, seed=0, share_experts=True)
+    w = model_weights(spec["model"], cfg)
     gen_s = time.perf_counter() - t0
     wbytes = Mdl.weight_bytes(w)
     dev = hip.Device(0)
@@ -676,9 +768,57 @@ def bench_batched(args, which):
         "device": info,
     }
     eng.close()
+    if cfg.n_experts:
+        line["roofline"] = moe_dominant(dev, cfg, B * R1, np.random.default_rng(6))
+        if spec.get("router_normal"):
+            line["model_routing"] = moe_model_routing(dev, cfg, w, spec)
+    else:
+        line["roofline"] = dominant_kernel(dev, cfg, B * R1, np.random.default_rng(6))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline_batched(cfg, w, spec, args.cpu_seconds)
     return line
+
+
+def moe_model_routing(dev, cfg, w, spec):
+    """Config 5 with the random-init model's own router (no N(0,1)
+    replacement): a short run beside the configured one, for the step time
+    and the experts the rows select when routing follows the model."""
+    from yuuka_amd import model as Mdl
+    B, k = spec["batch"], spec["k"]
+    c2 = Mdl.replace(cfg, router_normal_seed=0, capacity=512)
+    eng = Mdl.Engine(dev, c2, w)
+    rng = np.random.default_rng(11)
+    prompts = rng.integers(0, c2.vocab, (B, 256)).astype(np.int32)
+    for a in range(0, 255, 16):
+        eng.step_batch(prompts[:, a:min(a + 16, 255)], mode=1)
+    acc = Mdl.accept_struct(mode=1, temperature=spec["temperature"], seed=1234, top_p=spec["top_p"])
+    pending = prompts[:, -1].copy()
+    ms, distinct = [], []
+    for i in range(10):
+        toks = np.empty((B, k + 1), np.int32)
+        toks[:, 0] = pending
+        toks[:, 1:] = rng.integers(0, c2.vocab, (B, k))
+        res = eng.step_batch(toks, 0, acc, None)
+        pending[:] = res[:, 1]
+        if i >= 2:
+            ms.append(eng.last_step_ms)
+            distinct += [int((eng.moe_counts(li) > 0).sum()) for li in range(c2.n_layers)]
+    eng.close()
+    return {"verify_step_gpu_us": float(np.median(ms)) * 1e3, "distinct_experts_per_layer": float(np.mean(distinct)),
+            "sample": "8 timed steps after 2 warm-up steps, 256-token prompts, the model's router"}
+
+
+_WEIGHTS = {}
+
+
+def model_weights(name, cfg):
+    """Seeded random-init weights of a BASELINE model, generated once per run
+    (configs 2 and 3 share the 4B-like model); MoE experts share one host
+    copy across layers."""
+    from yuuka_amd import model as Mdl
+    if name not in _WEIGHTS:
+        _WEIGHTS[name] = Mdl.make_weights(cfg, seed=0, share_experts=True)
+    return _WEIGHTS[name]
 
 
 def cpu_baseline_batched(cfg, w, spec, budget_s):
@@ -733,6 +873,41 @@ def Mdl_replace(cfg, **kw):
     return Mdl.replace(cfg, **kw)
 
 
+SUMMARY_KEYS = ("value", "unit", "steps", "warmup", "ms_per_step", "verify_step_us", "verify_step_gpu_us",
+                "accepted_tokens_per_step", "acceptance_rate", "config", "data", "step_roofline", "roofline",
+                "cpu_baseline", "moe_routing", "model_routing", "accept_parity", "context_end", "prefill_s")
+
+
+def bench_all(args):
+    """The default run: config 2 (the metric's
+    configuration) is the line's value; configs 1, 3, 4 and 5 are measured in
+    the same process and reported under "configs" with their own step time,
+    accepted tokens/s, acceptance, step and kernel rooflines and CPU baseline
+    (a 10 s sample each)."""
+    import copy
+    line = bench_config2(args)
+    configs = {}
+    for which in (1, 3, 4, 5):
+        a = copy.copy(args)
+        a.config, a.steps, a.warmup, a.prompt = which, None, None, None
+        a.cpu_seconds = min(args.cpu_seconds, 10.0)
+        t0 = time.perf_counter()
+        if which == 1:
+            a.steps, a.warmup = 200, 20
+            sub = bench_config1(a)
+        else:
+            sub = bench_batched(a, which)
+        if which == 3:
+            _WEIGHTS.pop("QWEN35_4B_LIKE", None)
+        rec = {k: sub[k] for k in SUMMARY_KEYS if k in sub}
+        rec["wall_s"] = time.perf_counter() - t0
+        configs[str(which)] = rec
+        print(f"config {which}: {rec['value']:.1f} {rec['unit']} in {rec['wall_s']:.1f} s", file=sys.stderr,
+              flush=True)
+    line["configs"] = configs
+    return line
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -742,6 +917,8 @@ def main():
     ensure_built()
     if args.kernel_only:
         line = kernel_only(args)
+    elif args.config is None:
+        line = bench_all(args)
     elif args.config == 1:
         args.steps = args.steps or 200
         args.warmup = args.warmup if args.warmup is not None else 20

@@ -474,6 +474,14 @@ YUUKA_API yuuka_status yuuka_verify_accept_noalloc(yuuka_stream * stream,
 #define YUUKA_EXT_OP_ATTN_VERIFY 71u
 #define YUUKA_EXT_OP_MOE_ROUTER 72u
 #define YUUKA_EXT_OP_MOE_COMBINE 73u
+/*   ROUTER_NORMAL: synthetic router logits (BASELINE configs[4] states
+ *               "router logits N(0,1)"; no counterpart in the reference):
+ *               buf0 FP32 logits [rows][experts] are overwritten with i.i.d.
+ *               standard normal draws (Box-Muller over Philox4x32-10 keyed by
+ *               n2 = seed, counter {step, layer n3, row, pair}); optional buf1
+ *               uint64 step counter (0 when null); n={rows, experts, seed,
+ *               layer}. */
+#define YUUKA_EXT_OP_ROUTER_NORMAL 74u
 #define YUUKA_EXT_FLAG_DEFER 0x100u
 /* With YUUKA_EXT_FLAG_DEFER: buf10 receives the raw per-head scan outputs;
  * the gated RMSNorm is left to the consumer (GEMM_FUSED gated head norm). */
@@ -556,6 +564,10 @@ typedef struct yuuka_q35_config {
                             request can hold its whole capacity) */
     /* qwen35moe FFN (config.go MoE fields; n_experts 0 = dense FFN) */
     int32_t n_experts, n_experts_used, expert_ffn, shared_ffn;
+    /* nonzero: the router logits of every MoE layer are replaced, after the
+     * router, by i.i.d. N(0,1) draws seeded with this value and the step
+     * counter (ROUTER_NORMAL; the routing of BASELINE configs[4]) */
+    uint32_t router_normal_seed;
 } yuuka_q35_config;
 
 typedef struct yuuka_q35_tensor {

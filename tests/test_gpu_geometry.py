@@ -319,3 +319,46 @@ def test_config4_16k_context_chunk_groupings_agree(dev, monkeypatch):
         dev_eng.close()
     assert np.array_equal(out["auto"], out["auto2"])
     _close(out["auto"], out["1"], "cpw auto vs 1", tol=1e-4)
+
+
+def test_config3_rows_long_context_grouped_attention(dev, monkeypatch):
+    """Config 3's attention geometry at real context lengths: 16 Q / 4 KV
+    heads of 256, 9 verify rows per request (36 MFMA rows per KV head, the
+    six-tile grouped kernel attn_verify_mfma_group_kernel<6, true>), three
+    requests at ~450-700 tokens of context, the key chunks walked in groups
+    of 3 and of 5 per workgroup with the running softmax, and the one-chunk
+    kernel; each against the oracle decoder on every request (observed
+    1-2e-3 of the row rms for all three), and the groupings against each
+    other. Narrow non-attention widths (hidden 256,
+    one attention layer, 1024-token vocabulary) keep the oracle's prefill
+    short; the attention shapes are config 3's."""
+    cfg = replace(Mdl.QWEN35_4B_LIKE, hidden=256, ffn=512, n_layers=1, full_interval=1, vocab=1024, batch=3,
+                  max_rows=9, capacity=768)
+    w = Mdl.make_weights(cfg, seed=81)
+    rng = np.random.default_rng(82)
+    prompts = [rng.integers(0, cfg.vocab, n).astype(np.int32) for n in (700, 451, 598)]
+    toks = rng.integers(0, cfg.vocab, (3, 9)).astype(np.int32)
+    want = []
+    for r in range(3):
+        o = O.Q35(replace(cfg, batch=1), w)
+        o.forward(prompts[r][:-1])
+        toks[r, 0] = prompts[r][-1]
+        want.append(o.forward(toks[r], all_logits=True))
+        o.close()
+    out = {}
+    for cpw in ("3", "5", "1"):
+        monkeypatch.setenv("YUUKA_ATTN_CPW", cpw)
+        eng = Mdl.Engine(dev, cfg, w)
+        for r in range(3):
+            eng.prefill_request(r, prompts[r][:-1])
+        eng.step_batch(toks, 0, accept=Mdl.accept_struct(), forced=np.zeros(3, np.int32))
+        got = eng.logits(3 * 9).reshape(3, 9, -1)
+        eng.close()
+        for r in range(3):
+            _close(got[r], want[r], f"cpw {cpw} request {r}")
+        out[cpw] = got
+    # the groupings agree up to float32 reassociation, which the narrow
+    # model's int16 activation quantization turns into ~1e-3 of the logits'
+    # rms (the same spread all three show against the oracle)
+    _close(out["3"], out["1"], "cpw 3 vs 1", tol=5e-3)
+    _close(out["5"], out["1"], "cpw 5 vs 1", tol=5e-3)

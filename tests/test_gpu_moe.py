@@ -249,3 +249,42 @@ def test_moe_ops_reject_bad_arguments(dev):
     with pytest.raises(hip.HipError):
         plan.add(hip.OP["MOE_REDUCE_ADD"], [b, b, b], n=[1 << 20, 64, 8])  # overflow of the buffers
     plan.destroy()
+
+
+def test_router_normal_logits(dev, stream):
+    """ROUTER_NORMAL (router logits N(0,1)): the draws
+    have mean 0 and variance 1, are the same for the same (seed, step, layer)
+    and change with the step counter and the layer; the route op then picks
+    distinct experts as uniform routing does (about E (1 - (1 - used/E)^rows)
+    of them)."""
+    rows, E, used = 40, 256, 8
+    lb = dev.alloc(rows * E * 4)
+    step = dev.upload(np.array([7], np.uint64))
+    outs = []
+    for layer, st in ((3, 7), (3, 7), (3, 8), (4, 7)):
+        step.write(np.array([st], np.uint64))
+        p = hip.Plan(dev)
+        p.add(hip.OP["ROUTER_NORMAL"], [lb, step], n=[rows, E, 99, layer])
+        p.execute(stream)
+        stream.sync()
+        outs.append(lb.read(np.float32, rows * E).reshape(rows, E))
+        p.destroy()
+    a = outs[0].astype(np.float64)
+    assert abs(a.mean()) < 0.05 and abs(a.var() - 1.0) < 0.08, (a.mean(), a.var())
+    assert np.all(np.isfinite(a))
+    assert np.array_equal(outs[0], outs[1])
+    assert not np.array_equal(outs[0], outs[2]) and not np.array_equal(outs[0], outs[3])
+    # tail mass of a standard normal: P(|z| > 2) ~ 0.0455
+    assert abs(np.mean(np.abs(a) > 2.0) - 0.0455) < 0.01
+    ids = dev.alloc(rows * used * 4)
+    w = dev.alloc(rows * used * 4)
+    cnt, ar, asl, aw = dev.alloc(E * 4), dev.alloc(E * rows * used * 4), dev.alloc(E * rows * used * 4), \
+        dev.alloc(E * rows * used * 4)
+    p = hip.Plan(dev)
+    p.add(hip.OP["MOE_ROUTE"], [lb, ids, w, cnt, ar, asl, aw], n=[rows, E, used])
+    p.execute(stream)
+    stream.sync()
+    distinct = int((cnt.read(np.int32, E) > 0).sum())
+    expect = E * (1 - (1 - used / E) ** rows)
+    assert abs(distinct - expect) < 20, (distinct, expect)
+    p.destroy()

@@ -358,6 +358,8 @@ yuuka_status build_plan(yuuka_q35 *q, const PlanKey &key, yuuka_plan **out) {
         const uint32_t mf = YUUKA_EXT_FLAG_MOE_PACKED | (sh ? YUUKA_EXT_FLAG_MOE_SHARED : 0u);
         b.add(YUUKA_OP_RMSNORM_BATCH, {q->x, L.post_norm, q->xn}, {H, R, H, H}, {}, {c.eps});
         b.add(YUUKA_EXT_OP_MOE_ROUTER, {q->xn, L.router.b, q->moe_logits, L.shared_gate_vec, q->moe_sg}, {H, E, R});
+        if (c.router_normal_seed)  // the configured routing: logits N(0,1) per row and expert
+            b.add(YUUKA_EXT_OP_ROUTER_NORMAL, {q->moe_logits, q->step}, {R, E, (uint64_t)c.router_normal_seed, li});
         if (!sh) {  // the shared expert as its own GEMMs (its width differs from the experts')
             b.fused(q->xn, nullptr, 0.0f, R, {{&L.shared_gate, q->moe_sfg, nullptr}, {&L.shared_up, nullptr, nullptr}},
                     2);

@@ -82,6 +82,9 @@ hipError_t launch_cast_f16(const float *src, uint16_t *dst, uint64_t n, hipStrea
 
 // --------------------------------------------------------------- accept
 uint64_t accept_scratch_bytes(const yuuka_accept_params &p);
+// ROUTER_NORMAL: logits [rows][E] <- i.i.d. N(0,1) (k_accept.hip).
+hipError_t launch_router_normal(float *logits, int rows, int E, uint64_t seed, uint32_t layer, const uint64_t *step,
+                                hipStream_t s);
 hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int32_t *result,
                                 double *debug, const yuuka_accept_params &p, void *scratch,
                                 hipStream_t stream, const uint64_t *step_dev = nullptr, uint32_t draft_stride = 0,

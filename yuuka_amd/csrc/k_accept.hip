@@ -595,6 +595,27 @@ __device__ __forceinline__ double draw(uint64_t seed, uint64_t step, uint32_t ro
     return (double)v * (1.0 / 9007199254740992.0);
 }
 
+// Router logits replaced by i.i.d. N(0,1) draws: thread per (row, expert
+// pair), one Philox block per pair, Box-Muller on two 53-bit uniforms (u1 in
+// (0, 1]).
+__global__ __launch_bounds__(256) void router_normal_kernel(float *__restrict__ logits, int rows, int E,
+                                                            uint64_t seed, uint32_t layer,
+                                                            const uint64_t *__restrict__ step_ptr) {
+    const int pairs = (E + 1) / 2;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rows * pairs) return;
+    const int r = idx / pairs, p = idx - r * pairs;
+    const uint64_t step = step_ptr ? *step_ptr : 0;
+    uint32_t c[4] = {(uint32_t)step, (uint32_t)(step >> 32), layer, ((uint32_t)r << 16) | (uint32_t)p};
+    philox(c, (uint32_t)seed, (uint32_t)(seed >> 32));
+    const double u1 = (double)(((((uint64_t)c[0]) << 32 | c[1]) >> 11) + 1) * (1.0 / 9007199254740992.0);
+    const double u2 = (double)((((uint64_t)c[2]) << 32 | c[3]) >> 11) * (1.0 / 9007199254740992.0);
+    const double rad = sqrt(-2.0 * log(u1)), ang = 6.283185307179586 * u2;
+    float *row = logits + (uint64_t)r * E;
+    row[2 * p] = (float)(rad * cos(ang));
+    if (2 * p + 1 < E) row[2 * p + 1] = (float)(rad * sin(ang));
+}
+
 // Block-wide inverse CDF inside chunk `c` of a row: the first index j (j != d,
 // weight > 0) whose running weight sum exceeds `target`. Returns -1 when the
 // target lies beyond the chunk's own sum (rounding), with *last the last
@@ -835,6 +856,13 @@ uint64_t accept_scratch_bytes(const yuuka_accept_params &p) {
     const uint64_t n = (uint64_t)g.B * g.R * g.C;
     return ((n * sizeof(Stat) + 255) & ~255ull) + n * sizeof(double) +
            (uint64_t)g.B * g.R * (sizeof(double) + sizeof(Cut)) + 256 + n * sizeof(Hist0);
+}
+
+hipError_t launch_router_normal(float *logits, int rows, int E, uint64_t seed, uint32_t layer, const uint64_t *step,
+                                hipStream_t s) {
+    const int n = rows * ((E + 1) / 2);
+    if (n > 0) router_normal_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(logits, rows, E, seed, layer, step);
+    return hipGetLastError();
 }
 
 hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int32_t *result,

@@ -43,7 +43,10 @@ __device__ __forceinline__ int cur_pos_a(const ModelDyn &dyn) { return dyn.pos_d
 __device__ __forceinline__ float exp_nonpos(float x) {
     constexpr float L1 = 1.44269502162933349609375f;  // log2(e) rounded to float
     constexpr float L2 = 1.92596298909e-8f;            // log2(e) - L1
-    x = fmaxf(x, -128.0f);  // exp(-128) is 0 in float; keeps x * L1 and its residual finite
+    // exp(-128) is 0 in float; the clamp keeps x * L1 and its residual
+    // finite. A NaN score stays NaN (fmaxf would turn it into -128), as the
+    // reference's expf lets it through to the output.
+    x = x == x ? fmaxf(x, -128.0f) : x;
     const float p = x * L1;
     const float r = fmaf(x, L1, -p) + x * L2;
     return __builtin_amdgcn_exp2f(p) * fmaf(r, 0.693147180559945309f, 1.0f);

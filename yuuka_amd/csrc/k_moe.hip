@@ -29,6 +29,9 @@
 
 #include <algorithm>
 #include <climits>
+#include <map>
+#include <mutex>
+#include <tuple>
 
 #include "model_kernels.h"
 #include "refmath.h"
@@ -825,6 +828,30 @@ hipError_t launch_moe_route(const float *logits, int rows, int E, int used, int3
     return hipGetLastError();
 }
 
+// Resident workgroups of the grouped GEMM variant at this LDS size on the
+// current device: measured once per (device, variant, LDS size) under a lock
+// (gate/up and down launches differ in LDS, so a single cached entry would be
+// recomputed on nearly every launch).
+static unsigned moe_resident_wgs(bool packed, uint32_t lds) {
+    static std::mutex mu;
+    static std::map<std::tuple<int, bool, uint32_t>, unsigned> cache;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_tuple(dev, packed, lds);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 1;
+    const void *fn = packed ? reinterpret_cast<const void *>(moe_gemm_kernel<true>)
+                            : reinterpret_cast<const void *>(moe_gemm_kernel<false>);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kMoeThreads, lds) != hipSuccess || per_cu <= 0)
+        per_cu = 1;
+    const unsigned r = (unsigned)(per_cu * cus);
+    cache.emplace(key, r);
+    return r;
+}
+
 hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
     const int ostride = g.used + (g.shared ? 1 : 0);
     const int act_rows = g.by_slot ? g.rows * ostride : g.rows;
@@ -865,20 +892,8 @@ hipError_t launch_moe_gemm(const MoeGemm &g, void *ws, hipStream_t s) {
     moe_quant_kernel<<<(units + 3) / 4, 256, 0, s>>>(g.x, act_rows, g.K, a.xq);
     // a persistent grid of the resident workgroups (the kernel deals the
     // active experts' items over it)
-    static int per_cu = 0, cus = 0;
-    static uint32_t per_cu_lds = ~0u;
-    if (per_cu_lds != lds) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 1;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(moe_gemm_kernel<false>),
-                                                         kMoeThreads, lds) != hipSuccess || per_cu <= 0)
-            per_cu = 1;
-        per_cu_lds = lds;
-    }
     const int parts = (tiles + tpw - 1) / tpw;
-    const unsigned grid = (unsigned)std::min<int64_t>((int64_t)g.experts * parts, (int64_t)per_cu * cus);
+    const unsigned grid = (unsigned)std::min<int64_t>((int64_t)g.experts * parts, moe_resident_wgs(g.packed != 0, lds));
     if (g.packed) moe_gemm_kernel<true><<<grid, kMoeThreads, lds, s>>>(a);
     else moe_gemm_kernel<false><<<grid, kMoeThreads, lds, s>>>(a);
     return hipGetLastError();

@@ -615,6 +615,13 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
         *ws = attention_scratch_bytes(a);
         return YUUKA_OK;
     }
+    case YUUKA_EXT_OP_ROUTER_NORMAL: {
+        const uint64_t rows = op.n[0], E = op.n[1];
+        if (!rows || !E || E > 65536 || rows > 65536 || !buf_ok(op.buf[0], op.off[0], rows * E * 4) ||
+            (op.buf[1] && (!buf_ok(op.buf[1], op.off[1], 8) || op.off[1] % 8)))
+            return fail(YUUKA_ERR_INVALID_ARGUMENT, "invalid ROUTER_NORMAL shape or buffers");
+        return YUUKA_OK;
+    }
     case YUUKA_EXT_OP_ROPE_TABLE: {
         if ((op.flags & YUUKA_EXT_FLAG_OWN_POS) && (!buf_ok(op.buf[15], op.off[15], 8) || op.off[15] % 4))
             return fail(YUUKA_ERR_INVALID_ARGUMENT, "ROPE_TABLE: own position buffer");
@@ -1018,6 +1025,10 @@ yuuka_status execute_model_op(const yuuka_op &op, const ExecCtx &ctx) {
                                at<const int32_t>(op, 4), at<float>(op, 3), a, ctx.ws, dyn_of(ctx), hint, s);
         break;
     }
+    case YUUKA_EXT_OP_ROUTER_NORMAL:
+        err = launch_router_normal(at<float>(op, 0), (int)op.n[0], (int)op.n[1], op.n[2], (uint32_t)op.n[3],
+                                   at<const uint64_t>(op, 1), s);
+        break;
     case YUUKA_EXT_OP_ROPE_TABLE:
         err = launch_rope_table(at<float2>(op, 0), (int)op.n[0], (int)op.n[1], (double)op.f[0], dyn_of(ctx, op),
                                 (int)op.n[2], s, op.n[3] ? (int)op.n[3] : 1,

@@ -27,7 +27,7 @@ OP = dict(
     ROPE_BATCH=20, RECURRENT_CHUNK=23, EMBEDDING_BATCH=24, KV_WRITE_BATCH_PAGED=28,
     ATTENTION_PREFILL_PAGED=29, MOE_ROUTE=30, MOE_GATE_UP=31, MOE_DOWN=32, MOE_REDUCE_ADD=33, LM_HEAD=37,
     ACCEPT=66, GDN_COMMIT=67, ADVANCE=68, GEMM_FUSED=69, ROPE_TABLE=70, ATTN_VERIFY=71, MOE_ROUTER=72,
-    MOE_COMBINE=73,
+    MOE_COMBINE=73, ROUTER_NORMAL=74,
 )
 FLAG_MOE_SWIGLU = 0x800
 FLAG_MOE_PACKED = 0x2000

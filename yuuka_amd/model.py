@@ -44,6 +44,7 @@ class Q35Config:
     n_experts_used: int = 0
     expert_ffn: int = 0
     shared_ffn: int = 0
+    router_normal_seed: int = 0  # nonzero: MoE router logits replaced by N(0,1) draws
 
     @property
     def inner(self) -> int:
@@ -152,7 +153,8 @@ class yuuka_q35_config(C.Structure):
                                          "inner", "full_interval")] + [
         ("rope_base", C.c_double), ("eps", C.c_float), ("capacity", C.c_int32), ("block_size", C.c_int32),
         ("kv_dtype", C.c_uint32), ("max_rows", C.c_int32)] + [
-        (n, C.c_int32) for n in ("batch", "kv_blocks", "n_experts", "n_experts_used", "expert_ffn", "shared_ffn")]
+        (n, C.c_int32) for n in ("batch", "kv_blocks", "n_experts", "n_experts_used", "expert_ffn", "shared_ffn")] + [
+        ("router_normal_seed", C.c_uint32)]
 
 
 class yuuka_q35_tensor(C.Structure):
