@@ -85,23 +85,4 @@ void fused_gemm_rows_ws_parts(int rows, int K, const int *n, int nseg, bool swig
 // tt: 16-row tiles per workgroup (1, 2 or 4; even for kEpiSwiglu).
 hipError_t launch_fused_gemm(const FusedGemmArgs &a, int tt, hipStream_t s);
 
-// Chained streaming GEMMs: a run of dependent launch_fused_gemm calls (rows
-// <= 8) as one persistent launch, each stage waiting on a device-scope
-// counter for the previous one (bit-identical results).
-constexpr int kFusedChainMax = 4;
-constexpr int kFusedChainSyncWords = kFusedChainMax + 2;  // zero before the first launch
-struct FusedChainStage {
-    FusedGemmArgs a;
-    int variant;
-    uint32_t lds;
-};
-// False when the launch's streaming shape has no chained form; otherwise
-// *out is the stage (launch_fused_gemm's tile count tt).
-bool fused_gemm_chain_stage(const FusedGemmArgs &a, int tt, FusedChainStage *out);
-// True when a chained kernel serves the run st[0..n).
-bool fused_gemm_chain_supported(const FusedChainStage *st, int n);
-// sync: kFusedChainSyncWords words, zero between launches (the launch leaves
-// them so); word kFusedChainMax + 1 becomes 1 if a stage's wait gave up.
-hipError_t launch_fused_gemm_chain(const FusedChainStage *st, int n, uint32_t *sync, hipStream_t s);
-
 }  // namespace yk

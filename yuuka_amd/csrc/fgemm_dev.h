@@ -1,5 +1,5 @@
-// fgemm_dev.h — device code of the streaming verify GEMM, shared by the plain
-// launches (k_fgemm.hip) and the chained launches (k_fchain.hip).
+// fgemm_dev.h — device code of the fused verify GEMM (launched by
+// k_fgemm.hip).
 //
 //   out_s[m, n] = epi( sum_k y[m, k] * dequant(W_s)[n, k] ),  m < rows <= 16
 //
@@ -65,8 +65,6 @@ constexpr uint32_t kInvBytes = kWaves * 16 * 4;
 // Tiles per workgroup up to which the streaming kernel deals items to waves
 // one by one (balanced mode, wk = 0).
 constexpr int kBalMax = 4;
-// Cache-policy bits of a buffer access at device scope (sc1).
-constexpr int kCohere = 16;
 
 
 
@@ -95,17 +93,6 @@ __device__ __forceinline__ int dot2(uint32_t a, uint32_t b, int c) {
 }
 
 __device__ __forceinline__ float half_lo(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)(h & 0xffffu))); }
-
-// 8 bytes at an even byte offset of the buffer (Q6_K blocks are only 2-byte
-// aligned): one dword-aligned 12-byte load, then a byte shift.
-__device__ __forceinline__ uint64_t load8_a2(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
-    typedef __attribute__((ext_vector_type(3))) int i32x3;
-    const i32x3 v = __builtin_bit_cast(i32x3, __builtin_amdgcn_raw_buffer_load_b96(rs, off & ~3u, 0, 0));
-    const uint32_t sh = off & 3u;
-    const uint32_t lo = __builtin_amdgcn_alignbyte((uint32_t)v[1], (uint32_t)v[0], sh);
-    const uint32_t hi = __builtin_amdgcn_alignbyte((uint32_t)v[2], (uint32_t)v[1], sh);
-    return (uint64_t)lo | ((uint64_t)hi << 32);
-}
 
 // Signed q - 32 for eight packed unsigned 6-bit values (one per byte).
 __device__ __forceinline__ uint64_t q6_to_i8(uint64_t q6) {
@@ -523,11 +510,16 @@ struct Q4Stage {
     i32x4 hdr;      // d | dmin, 12 scale bytes
     uint4 q16[2];   // bytes [16 + 32 (2 h + (g >> 1)) + 16 (g & 1), +16) for h = 0, 1
 };
+// Q6_K blocks (210 B) are only 2-byte aligned: a stage holds the raw
+// dword-aligned windows of its pieces as loaded, and the byte shift `sh`
+// (0 or 2, the same for every piece of a lane) is applied when the stage is
+// multiplied, so that issuing a stage never waits for its loads.
 struct Q6Stage {
-    uint64_t ql[4]; // [n][half]: bytes n*64 + half*32 + 8g
-    uint64_t qh[2]; // bytes 128 + n*32 + 8g
-    i32x4 sc;       // 16 int8 scales
-    uint32_t d;     // f16 bits
+    uint32_t ql[4][3];  // [n][half]: window of bytes n*64 + half*32 + 8g
+    uint32_t qh[2][3];  // window of bytes 128 + n*32 + 8g
+    i32x4 sc;           // window of the 16 int8 scales
+    uint32_t w4;        // the dword after it (holds d)
+    uint32_t sh;
 };
 
 // Stage of a launch whose segments mix Q4_K and Q6_K (dtype uniform per tile).
@@ -564,26 +556,30 @@ __device__ __forceinline__ void q4_pieces(const Q4Stage &S, uint64_t (&qs)[4]) {
 }
 
 __device__ __forceinline__ void issue(Q6Stage &S, __amdgpu_buffer_rsrc_t rs, uint32_t row_off, int g) {
+    typedef __attribute__((ext_vector_type(3))) int i32x3;
+    const uint32_t base = row_off & ~3u;
+    auto win = [&](uint32_t (&w)[3], uint32_t off) __attribute__((always_inline)) {
+        const i32x3 v = __builtin_bit_cast(i32x3, __builtin_amdgcn_raw_buffer_load_b96(rs, base + off, 0, 0));
+        w[0] = (uint32_t)v[0];
+        w[1] = (uint32_t)v[1];
+        w[2] = (uint32_t)v[2];
+    };
 #pragma unroll
     for (int n = 0; n < 2; n++) {
-        S.ql[2 * n] = load8_a2(rs, row_off + n * 64 + 8 * kperm(g));
-        S.ql[2 * n + 1] = load8_a2(rs, row_off + n * 64 + 32 + 8 * kperm(g));
-        S.qh[n] = load8_a2(rs, row_off + 128 + n * 32 + 8 * kperm(g));
+        win(S.ql[2 * n], n * 64 + 8 * kperm(g));
+        win(S.ql[2 * n + 1], n * 64 + 32 + 8 * kperm(g));
+        win(S.qh[n], 128 + n * 32 + 8 * kperm(g));
     }
-    const uint32_t a = row_off + 192;
-    typedef __attribute__((ext_vector_type(4))) int v4;
-    if ((a & 3u) == 0) {
-        S.sc = __builtin_amdgcn_raw_buffer_load_b128(rs, a, 0, 0);
-        S.d = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, a + 16, 0, 0) & 0xffffu;
-    } else {  // a = 2 mod 4
-        const v4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, a - 2, 0, 0);
-        const uint32_t w4 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, a + 14, 0, 0);
-        S.sc[0] = (int)__builtin_amdgcn_alignbyte((uint32_t)w[1], (uint32_t)w[0], 2);
-        S.sc[1] = (int)__builtin_amdgcn_alignbyte((uint32_t)w[2], (uint32_t)w[1], 2);
-        S.sc[2] = (int)__builtin_amdgcn_alignbyte((uint32_t)w[3], (uint32_t)w[2], 2);
-        S.sc[3] = (int)__builtin_amdgcn_alignbyte(w4, (uint32_t)w[3], 2);
-        S.d = w4 >> 16;
-    }
+    S.sc = __builtin_amdgcn_raw_buffer_load_b128(rs, base + 192, 0, 0);
+    S.w4 = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(rs, base + 208, 0, 0);
+    S.sh = row_off & 3u;
+}
+
+// The 8 bytes of a piece window at byte shift sh.
+__device__ __forceinline__ uint64_t q6_piece(const uint32_t (&w)[3], uint32_t sh) {
+    const uint32_t lo = __builtin_amdgcn_alignbyte(w[1], w[0], sh);
+    const uint32_t hi = __builtin_amdgcn_alignbyte(w[2], w[1], sh);
+    return (uint64_t)lo | ((uint64_t)hi << 32);
 }
 
 // One tile, one super-block: int32 sums per plane row, then the FP32 update
@@ -636,7 +632,17 @@ __device__ __forceinline__ void compute(const Q4Stage &S, const int64_t (&xa)[NA
 template <int NA>
 __device__ __forceinline__ void compute(const Q6Stage &S, const int64_t (&xa)[NA][8], const uint32_t (&)[NA][4][4],
                                         const float (&xsr)[NA][4], float (&acc)[NA][4], int g) {
-    const float d = half_lo(S.d);
+    uint64_t ql[4], qh[2];
+#pragma unroll
+    for (int i = 0; i < 4; i++) ql[i] = q6_piece(S.ql[i], S.sh);
+#pragma unroll
+    for (int i = 0; i < 2; i++) qh[i] = q6_piece(S.qh[i], S.sh);
+    uint32_t scv[4];
+    scv[0] = __builtin_amdgcn_alignbyte((uint32_t)S.sc[1], (uint32_t)S.sc[0], S.sh);
+    scv[1] = __builtin_amdgcn_alignbyte((uint32_t)S.sc[2], (uint32_t)S.sc[1], S.sh);
+    scv[2] = __builtin_amdgcn_alignbyte((uint32_t)S.sc[3], (uint32_t)S.sc[2], S.sh);
+    scv[3] = __builtin_amdgcn_alignbyte(S.w4, (uint32_t)S.sc[3], S.sh);
+    const float d = half_lo(S.w4 >> (8 * S.sh));
     int acci[NA][4];
 #pragma unroll
     for (int a = 0; a < NA; a++)
@@ -646,11 +652,11 @@ __device__ __forceinline__ void compute(const Q6Stage &S, const int64_t (&xa)[NA
 #pragma unroll
     for (int c = 0; c < 8; c++) {
         const int n = c >> 2, qd = c & 3;
-        const uint64_t lo = (S.ql[2 * n + (qd & 1)] >> (4 * (qd >> 1))) & 0x0f0f0f0f0f0f0f0full;
-        const uint64_t hi = ((S.qh[n] >> (2 * qd)) & 0x0303030303030303ull) << 4;
+        const uint64_t lo = (ql[2 * n + (qd & 1)] >> (4 * (qd >> 1))) & 0x0f0f0f0f0f0f0f0full;
+        const uint64_t hi = ((qh[n] >> (2 * qd)) & 0x0303030303030303ull) << 4;
         const int64_t q = (int64_t)q6_to_i8(lo | hi);
         const int64_t b0 = first ? q : 0, b1 = first ? 0 : q;
-        const uint32_t scw = (uint32_t)S.sc[c >> 1];
+        const uint32_t scw = scv[c >> 1];
         const int s0 = (int)(int8_t)__builtin_amdgcn_ubfe(scw, 16 * (c & 1), 8);
         const int s1 = (int)(int8_t)__builtin_amdgcn_ubfe(scw, 16 * (c & 1) + 8, 8);
 #pragma unroll
@@ -677,9 +683,13 @@ __device__ __forceinline__ void issue_any(Q6Stage &S, __amdgpu_buffer_rsrc_t rs,
 }
 __device__ __forceinline__ void issue_any(MixStage &S, __amdgpu_buffer_rsrc_t rs, uint32_t row_off, uint32_t sb, int g,
                                           int dt) {
+    // both formats' loads are always issued, the other one at offsets past
+    // the buffer (zero, no memory request): no branch around loads, so the
+    // compiler never copies a stage whose loads are in flight
     S.dt = dt;
-    if (dt == kQ4K) issue(S.q4, rs, row_off + sb * 144u, g);
-    else issue(S.q6, rs, row_off + sb * 210u, g);
+    const bool q4 = dt == kQ4K;
+    issue(S.q4, rs, q4 ? row_off + sb * 144u : kOutOfRange, g);
+    issue(S.q6, rs, q4 ? kOutOfRange : row_off + sb * 210u, g);
 }
 template <int NA>
 __device__ __forceinline__ void compute_any(const Q4Stage &S, const int64_t (&xa)[NA][8], const uint32_t (&sxp)[NA][4][4],
@@ -915,93 +925,82 @@ __device__ __forceinline__ float lane_inv_rms(const FusedGemmArgs &A, const floa
     return inv;
 }
 
-// Chained launches (fgemm_chain_kernel) hand activations from one GEMM to
-// the next inside one launch: the producer's workgroups sit on every XCD and
-// the XCDs' L2 caches are not coherent with each other, so every activation,
-// residual and output access of a chain stage is made at device scope (sc1:
-// coherent across the XCDs without writing back or invalidating the L2).
-// CH = 0 is the plain launch, whose inputs a kernel boundary made visible.
-template <int CH>
-__device__ __forceinline__ float ld_act(const float *p) {
-    if constexpr (CH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else return *p;
-}
-template <int CH>
-__device__ __forceinline__ void st_act(float *p, float v) {
-    if constexpr (CH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else *p = v;
-}
-template <int CH>
-__device__ __forceinline__ float4 ld_act4(__amdgpu_buffer_rsrc_t rs, const float *base, uint32_t off_floats) {
-    if constexpr (CH) {
-        return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off_floats * 4u, 0, kCohere));
-    } else {
-        return *reinterpret_cast<const float4 *>(base + off_floats);
-    }
-}
-
-// Wait of a chain stage for the previous stage: its counter reaches the
-// grid size once every workgroup has stored its outputs. The spin is
-// bounded: past kChainSpinLimit polls (seconds) the stage records an error
-// word and proceeds, so no wave can wait forever.
-struct ChainCtl {
-    uint32_t *wait;    // counter of the previous stage (null: first stage)
-    uint32_t target;   // workgroups of the launch
-    uint32_t *err;     // set to 1 when a wait gives up
-};
-constexpr uint32_t kChainSpinLimit = 1u << 22;
-__device__ __forceinline__ void chain_wait(const ChainCtl &C) {
-    if (threadIdx.x == 0 && C.wait) {
-        uint32_t spins = 0;
-        while (__hip_atomic_load(C.wait, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < C.target) {
-            __builtin_amdgcn_s_sleep(1);
-            if (++spins == kChainSpinLimit) {
-                __hip_atomic_store(C.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-        }
-    }
-    // no memory access moves across the wait (the compiler sees a clobber)
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// Fixed-order sum of a row group's wk waves through LDS, then the stores
-// (shared by the wk waves).
-template <int TT, int NA, int CH>
-__device__ __forceinline__ void stream_epilogue(const FusedGemmArgs &A, float *red, const float *my_inv,
-                                                const float (&acc)[TT][NA][4], bool live, int tile, int rows_out,
-                                                bool swiglu, int rg, int kg, int wk) {
-    const int lane = threadIdx.x & 63;
-    const int M = A.rows;
-    const GroupRows<TT> Gr(A, tile, rows_out, swiglu, lane & 15);
-    float *myred = red + (size_t)rg * wk * TT * NA * 4 * 64;
-    if (wk > 1) lds_barrier();  // previous iteration's partials are consumed
-#pragma unroll
-    for (int t = 0; t < TT; t++)
-#pragma unroll
-        for (int a = 0; a < NA; a++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) myred[(((kg * TT + t) * NA + a) * 4 + e) * 64 + lane] = acc[t][a][e];
-    if (wk > 1) lds_barrier();
-    if (!live) return;
-    for (int idx = kg * 64 + lane; idx < rows_out * M; idx += wk * 64) {
-        const int m = idx / rows_out, rr = idx % rows_out;
+// Ring mode's outputs: tile c of the workgroup's [t0, t1) belongs to row
+// group (c - t0) % wr as its (c - t0) / wr-th tile; every output sums the
+// row group's wk K-group partials in K-group order (deterministic), then
+// the epilogue. The partial of (row group rg, K group kg, tile k) sits at
+// red + ((rg wk + kg) niter + k) TT NA 256 floats.
+template <int TT, int NA>
+__device__ __forceinline__ void ring_epilogue(const FusedGemmArgs &A, const float *red, const float *my_inv, int t0,
+                                              int t1, int wr, int wk, int niter, int rows_out, bool swiglu) {
+    constexpr int kSlot = TT * NA * 256;
+    const int M = A.rows, per_tile = rows_out * M;
+    for (int idx = threadIdx.x; idx < (t1 - t0) * per_tile; idx += kThreads) {
+        const int c = idx / per_tile, rem = idx - c * per_tile;
+        const int m = rem / rows_out, rr = rem - m * rows_out;
+        const GroupRows<TT> Gr(A, t0 + c, rows_out, swiglu, 0);
         const int n = Gr.n0 + rr;
-        const float ir = my_inv[m];
         if (n >= Gr.N) continue;
+        const int rg = c % wr, k = c / wr;
         const int t = rr >> 4, col = rr & 15;
         float val[2];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int tt = t + h * (TT / 2);
-            float ph = 0.0f, pl = 0.0f;
             const int ah = m >> 4, gh = (m & 15) >> 2, eh = m & 3;
             const int rl = M + m, al = rl >> 4, gl = (rl & 15) >> 2, el = rl & 3;
-            for (int w = 0; w < wk; w++) {
-                ph += myred[(((w * TT + tt) * NA + ah) * 4 + eh) * 64 + gh * 16 + col];
-                pl += myred[(((w * TT + tt) * NA + al) * 4 + el) * 64 + gl * 16 + col];
+            float ph = 0.0f, pl = 0.0f;
+            for (int kg = 0; kg < wk; kg++) {
+                const float *p = red + ((size_t)(rg * wk + kg) * niter + k) * kSlot;
+                ph += p[((tt * NA + ah) * 4 + eh) * 64 + gh * 16 + col];
+                pl += p[((tt * NA + al) * 4 + el) * 64 + gl * 16 + col];
+            }
+            float v = 256.0f * ph + pl;
+            if (A.norm) v *= my_inv[m];
+            val[h] = v;
+            if (!swiglu) break;
+        }
+        const size_t o = (size_t)m * Gr.N + n;
+        if (swiglu) {
+            A.seg[0].out[o] = silu_mul(val[0], val[1]);
+        } else {
+            float v = val[0];
+            if (A.epilogue == kEpiResidual) v += A.seg[Gr.s].res[o];
+            else v = out_map(A.seg[Gr.s], v, n);
+            A.seg[Gr.s].out[o] = v;
+        }
+    }
+}
+
+// Balanced mode's outputs: every (tile, row, channel) of the workgroup's
+// cnt tiles sums the eight waves' partials in wave order (deterministic),
+// then the epilogue. Wave w's partial of tile c sits at red + (w kBalMax + c)
+// TT NA 256 floats.
+template <int TT, int NA>
+__device__ __forceinline__ void bal_epilogue(const FusedGemmArgs &A, const float *red, const float *my_inv, int t0,
+                                             int cnt, int rows_out, bool swiglu) {
+    constexpr int kSlot = TT * NA * 256;
+    const int M = A.rows, per_tile = rows_out * M;
+    for (int idx = threadIdx.x; idx < cnt * per_tile; idx += kThreads) {
+        const int c = idx / per_tile, rem = idx - c * per_tile;
+        const int m = rem / rows_out, rr = rem - m * rows_out;
+        const GroupRows<TT> Gr(A, t0 + c, rows_out, swiglu, 0);
+        const int n = Gr.n0 + rr;
+        if (n >= Gr.N) continue;
+        const int t = rr >> 4, col = rr & 15;
+        const float ir = my_inv[m];
+        float val[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int tt = t + h * (TT / 2);
+            const int ah = m >> 4, gh = (m & 15) >> 2, eh = m & 3;
+            const int rl = M + m, al = rl >> 4, gl = (rl & 15) >> 2, el = rl & 3;
+            float ph = 0.0f, pl = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kWaves; w++) {
+                const float *wr_ = red + ((size_t)w * kBalMax + c) * kSlot;
+                ph += wr_[((tt * NA + ah) * 4 + eh) * 64 + gh * 16 + col];
+                pl += wr_[((tt * NA + al) * 4 + el) * 64 + gl * 16 + col];
             }
             float v = 256.0f * ph + pl;
             if (A.norm) v *= ir;
@@ -1010,12 +1009,12 @@ __device__ __forceinline__ void stream_epilogue(const FusedGemmArgs &A, float *r
         }
         const size_t o = (size_t)m * Gr.N + n;
         if (swiglu) {
-            st_act<CH>(A.seg[0].out + o, silu_mul(val[0], val[1]));
+            *(A.seg[0].out + o) = silu_mul(val[0], val[1]);
         } else {
             float v = val[0];
-            if (A.epilogue == kEpiResidual) v += ld_act<CH>(A.seg[Gr.s].res + o);
+            if (A.epilogue == kEpiResidual) v += *(A.seg[Gr.s].res + o);
             else v = out_map(A.seg[Gr.s], v, n);
-            st_act<CH>(A.seg[Gr.s].out + o, v);
+            *(A.seg[Gr.s].out + o) = v;
         }
     }
 }
@@ -1038,12 +1037,12 @@ template <int DT, int TT> struct RingDepth {
     static constexpr int value = 2;
 };
 
-template <int DT, int TT, int KU, int MODE, bool BAL, int CH>
+template <int DT, int TT, int KU, int MODE, bool BAL>
 __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *lds, float *inv_w, float *red,
-                                              int rows_out, bool swiglu, const ChainCtl &ctl) {
+                                              int rows_out, bool swiglu) {
     constexpr int NA = 1;
     constexpr int kRing = RingDepth<DT, TT>::value;
-    static_assert(kRing >= 2 && kRing <= 4, "ring depth");
+    static_assert(kRing == 2, "two register stages");
     using Stage = typename StageOf<DT>::T;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -1068,10 +1067,6 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
     float4 xr[KS][4], gr[KS][4], zr[KS][4], hw[4];
     auto load_x = [&]() __attribute__((always_inline)) {
         const int units = A.rows * nsb;
-        const int xbytes = A.rows * A.K * 4;
-        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc((void *)A.x, (short)0, xbytes, 0x00020000);
-        const __amdgpu_buffer_rsrc_t zrs =
-            __builtin_amdgcn_make_buffer_rsrc((void *)(MODE == 2 ? A.gate : A.x), (short)0, xbytes, 0x00020000);
         const int s16 = lane & 15, row = lane >> 4;
         if constexpr (MODE == 2) {
 #pragma unroll
@@ -1084,16 +1079,14 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
             const uint32_t off = (uint32_t)(m * A.K + sb * 256 + 16 * s16);
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                xr[k][q] = ld_act4<CH>(xrs, A.x, off + 4 * q);
+                xr[k][q] = *reinterpret_cast<const float4 *>(A.x + off + 4 * q);
                 if constexpr (MODE == 1) gr[k][q] = *reinterpret_cast<const float4 *>(A.norm + sb * 256 + 16 * s16 + 4 * q);
-                if constexpr (MODE == 2) zr[k][q] = ld_act4<CH>(zrs, A.gate, off + 4 * q);
+                if constexpr (MODE == 2) zr[k][q] = *reinterpret_cast<const float4 *>(A.gate + off + 4 * q);
             }
         }
     };
-    // a chain stage requests its first weights before it waits for the
-    // previous stage (they do not depend on it) and loads the activations
-    // after; a plain launch loads the activations first
-    if constexpr (!CH) load_x();
+    // the activations are requested first, then the first weight stages
+    load_x();
     __builtin_amdgcn_sched_barrier(0);
 
     auto zero = [&](float (&acc)[TT][NA][4]) __attribute__((always_inline)) {
@@ -1112,16 +1105,6 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
 #pragma unroll
         for (int t = 0; t < TT; t++) compute_any<NA>(S[t], xa, sxp, xsr, acc[t], g);
     };
-    int kq = 0, jq = 0;  // issue cursor (iteration, super-block index)
-    auto issue_next = [&](Stage (&S)[TT]) __attribute__((always_inline)) {
-        const GroupRows<TT> Gr(A, tile_of(kq), rows_out, swiglu, r);
-#pragma unroll
-        for (int t = 0; t < TT; t++) issue_any(S[t], Gr.rs[t], Gr.row_off[t], (uint32_t)(kg + wk * jq), g, Gr.dt);
-        if (++jq == mine) {
-            jq = 0;
-            ++kq;
-        }
-    };
     if constexpr (BAL) {
         // ---- balanced mode (at most kBalMax tiles per workgroup): the
         //      workgroup's (tile, super-block) items, tile-major, are dealt
@@ -1130,12 +1113,6 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
         //      wave order after one barrier.
         const int cnt = t1 - t0, I = cnt * nsb;
         const int nmine = wave < I ? (I - wave + kWaves - 1) / kWaves : 0;
-        auto issue_item = [&](Stage (&S)[TT], int ii) __attribute__((always_inline)) {
-            const int c = ii / nsb, sb = ii - c * nsb;
-            const GroupRows<TT> Gr(A, t0 + c, rows_out, swiglu, r);
-#pragma unroll
-            for (int t = 0; t < TT; t++) issue_any(S[t], Gr.rs[t], Gr.row_off[t], (uint32_t)sb, g, Gr.dt);
-        };
         // A ring slot past the wave's last item still issues its loads (a
         // fixed load count keeps the compiler's wait counts exact), at an
         // offset beyond the buffer's range: they return zero without a
@@ -1161,11 +1138,6 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
 #pragma unroll
         for (int d = 0; d < kD; d++) issue_slot(sbr[d], d);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (CH) {
-            chain_wait(ctl);
-            load_x();
-            __builtin_amdgcn_sched_barrier(0);
-        }
         for (int idx = lane; idx < cnt * kSlot / 4; idx += 64)
             reinterpret_cast<float4 *>(myr)[idx] = make_float4(0.f, 0.f, 0.f, 0.f);
         act_prologue_regs<MODE, KS>(A, L, lds, nsb, xr, gr, zr, hw);
@@ -1185,112 +1157,94 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
                     for (int e = 0; e < 4; e++) myr[c * kSlot + ((t * NA + a) * 4 + e) * 64 + lane] = acc[t][a][e];
         };
         int cur = nmine > 0 ? wave / nsb : 0;
-        for (int q = 0; q < nmine; q++) {
-            const int ii = wave + kWaves * q, c = ii / nsb, sbi = ii - c * nsb;
+        // two items per iteration, each stage in its own code path: a loop
+        // over a switch on q % kD lets the compiler merge the cases and
+        // rotate the stages through register copies, each of which waits
+        // for the loads in flight
+        static_assert(kD == 2, "two register stages");
+        auto step = [&](Stage (&S)[TT], int q) __attribute__((always_inline)) {
+            // q == nmine (odd counts): a stage issued past the end, all-zero
+            // weights; it multiplies into the current tile's partial exactly
+            const int qq = q < nmine ? q : q - 1;
+            const int ii = wave + kWaves * qq, c = ii / nsb, sbi = ii - c * nsb;
             if (c != cur) {
                 flush(cur);
                 zero(acc);
                 cur = c;
             }
-            // stage q % kD holds item q; it is refilled with item q + kD
-            switch (q % kD) {
-#define YK_FG_BAL_CASE(cs)                                                                                         \
-    case cs:                                                                                                       \
-        if constexpr (cs < kD) {                                                                                   \
-            compute_item(sbr[cs], sbi, acc);                                                                       \
-            if (q + kD < nmine) issue_item(sbr[cs], ii + kD * kWaves);                                             \
-        }                                                                                                          \
-        break;
-                YK_FG_BAL_CASE(0)
-                YK_FG_BAL_CASE(1)
-                YK_FG_BAL_CASE(2)
-                YK_FG_BAL_CASE(3)
-#undef YK_FG_BAL_CASE
-            }
+            compute_item(S, sbi, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            issue_slot(S, q + kD);
+        };
+        for (int q = 0; q < nmine; q += 2) {
+            step(sbr[0], q);
+            step(sbr[1], q + 1);
         }
         if (nmine > 0) flush(cur);
         lds_barrier();
-        const int M = A.rows, per_tile = rows_out * M;
-        for (int idx = threadIdx.x; idx < cnt * per_tile; idx += kThreads) {
-            const int c = idx / per_tile, rem = idx - c * per_tile;
-            const int m = rem / rows_out, rr = rem - m * rows_out;
-            const GroupRows<TT> Gr(A, t0 + c, rows_out, swiglu, 0);
-            const int n = Gr.n0 + rr;
-            if (n >= Gr.N) continue;
-            const int t = rr >> 4, col = rr & 15;
-            const float ir = my_inv[m];
-            float val[2];
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int tt = t + h * (TT / 2);
-                const int ah = m >> 4, gh = (m & 15) >> 2, eh = m & 3;
-                const int rl = M + m, al = rl >> 4, gl = (rl & 15) >> 2, el = rl & 3;
-                float ph = 0.0f, pl = 0.0f;
-#pragma unroll
-                for (int w = 0; w < kWaves; w++) {
-                    const float *wr_ = red + ((size_t)w * kBalMax + c) * kSlot;
-                    ph += wr_[((tt * NA + ah) * 4 + eh) * 64 + gh * 16 + col];
-                    pl += wr_[((tt * NA + al) * 4 + el) * 64 + gl * 16 + col];
-                }
-                float v = 256.0f * ph + pl;
-                if (A.norm) v *= ir;
-                val[h] = v;
-                if (!swiglu) break;
-            }
-            const size_t o = (size_t)m * Gr.N + n;
-            if (swiglu) {
-                st_act<CH>(A.seg[0].out + o, silu_mul(val[0], val[1]));
-            } else {
-                float v = val[0];
-                if (A.epilogue == kEpiResidual) v += ld_act<CH>(A.seg[Gr.s].res + o);
-                else v = out_map(A.seg[Gr.s], v, n);
-                st_act<CH>(A.seg[Gr.s].out + o, v);
-            }
-        }
+        bal_epilogue<TT, NA>(A, red, my_inv, t0, cnt, rows_out, swiglu);
         return;
     }
 
-    Stage st[kRing][TT];
+    // ring item i of this wave: tile tile_of(i / mine), super-block
+    // kg + wk (i % mine); items past the wave's last are issued at offsets
+    // beyond the buffers (zero, no memory request) so that every issue is
+    // unconditional
+    auto issue_at = [&](Stage (&S)[TT], int i) __attribute__((always_inline)) {
+        const bool live = i < total;
+        const int k = live ? i / mine : 0, j = live ? i - k * mine : 0;
+        const GroupRows<TT> Gr(A, tile_of(k), rows_out, swiglu, r);
 #pragma unroll
-    for (int d = 0; d < kRing; d++)
-        if (total > d) issue_next(st[d]);
+        for (int t = 0; t < TT; t++)
+            issue_any(S[t], Gr.rs[t], live ? Gr.row_off[t] : kOutOfRange, live ? (uint32_t)(kg + wk * j) : 0u, g,
+                      Gr.dt);
+    };
+    Stage st[kRing][TT];
+    issue_at(st[0], 0);
+    issue_at(st[1], 1);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (CH) {
-        chain_wait(ctl);
-        load_x();
-        __builtin_amdgcn_sched_barrier(0);
-    }
     act_prologue_regs<MODE, KS>(A, L, lds, nsb, xr, gr, zr, hw);
     lds_barrier();
     {
         const float v = lane_inv_rms(A, reinterpret_cast<const float *>(lds + L.nsq), nsb);
         if (lane < 16) my_inv[lane] = v;
     }
-    int i = 0;
-    for (int k = 0; k < niter; k++) {
-        const int tile = tile_of(k);
-        const bool live = tile < t1;
-        float acc[TT][NA][4];
-        zero(acc);
-        for (int j = 0; live && j < mine; j++, i++) {
-            // stage i % kRing holds item i; it is refilled with item i + kRing
-            switch (i % kRing) {
-#define YK_FG_RING_CASE(c)                                                                                         \
-    case c:                                                                                                        \
-        if constexpr (c < kRing) {                                                                                 \
-            compute_item(st[c], kg + wk * j, acc);                                                                 \
-            if (i + kRing < total) issue_next(st[c]);                                                              \
-        }                                                                                                          \
-        break;
-                YK_FG_RING_CASE(0)
-                YK_FG_RING_CASE(1)
-                YK_FG_RING_CASE(2)
-                YK_FG_RING_CASE(3)
-#undef YK_FG_RING_CASE
-            }
+    // two items per iteration, each stage in its own code path (see the
+    // balanced mode). A tile's partial goes to LDS after its last item and
+    // every output is formed after the loop: an epilogue inside the loop
+    // (global stores, residual loads) would make the compiler wait for the
+    // weight loads in flight at each tile's end.
+    constexpr int kSlot = TT * NA * 256;  // floats of one wave's partial of one tile
+    float *myr = red + (size_t)(rg * wk + kg) * niter * kSlot;
+    float acc[TT][NA][4];
+    zero(acc);
+    auto step = [&](Stage (&S)[TT], int i) __attribute__((always_inline)) {
+        // an odd count's last pair holds one item past the end: its stage
+        // was issued at offsets beyond the buffers (all-zero weights, so the
+        // multiply adds exact zeros) and it stores no partial
+        const bool live = i < total;
+        const int k = live ? i / mine : 0, j = live ? i - k * mine : 0;
+        compute_item(S, kg + wk * j, acc);
+        // every read of the stage precedes its refill, so the refill can
+        // take the stage's own registers (no copies of loads in flight)
+        __builtin_amdgcn_sched_barrier(0);
+        issue_at(S, i + kRing);
+        if (live && j == mine - 1) {
+#pragma unroll
+            for (int t = 0; t < TT; t++)
+#pragma unroll
+                for (int a = 0; a < NA; a++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) myr[k * kSlot + ((t * NA + a) * 4 + e) * 64 + lane] = acc[t][a][e];
+            zero(acc);
         }
-        stream_epilogue<TT, NA, CH>(A, red, my_inv, acc, live, live ? tile : t0, rows_out, swiglu, rg, kg, wk);
+    };
+    for (int i = 0; i < total; i += 2) {
+        step(st[0], i);
+        step(st[1], i + 1);
     }
+    lds_barrier();
+    ring_epilogue<TT, NA>(A, red, my_inv, t0, t1, wr, wk, niter, rows_out, swiglu);
 }
 }  // namespace
 

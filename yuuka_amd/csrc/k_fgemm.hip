@@ -17,7 +17,7 @@ __global__ __launch_bounds__(kThreads) void fgemm_stream_kernel(const FusedGemmA
     const ActLayout L0(A.rows, 1, nsb, nsb, MODE == 1, -1, MODE == 2, false);
     float *inv_w = reinterpret_cast<float *>(lds + L0.total);
     float *red = reinterpret_cast<float *>(lds + L0.total + kInvBytes);
-    stream_groups<DT, TT, KU, MODE, BAL, 0>(A, lds, inv_w, red, rows_out, swiglu, ChainCtl{nullptr, 0u, nullptr});
+    stream_groups<DT, TT, KU, MODE, BAL>(A, lds, inv_w, red, rows_out, swiglu);
 }
 
 template <int DTM, int TT, int NA>
@@ -78,11 +78,12 @@ int fused_gemm_chunk_sb(int rows, int K, int tt, bool norm, bool gated) {
 
 
 // Streaming launch: every resident workgroup gets floor or ceil of G / R row
-// tiles; the waves split into the row-group x K-group shape that minimizes
-// the largest per-wave item count (ties: more row groups, fewer barriers).
+// tiles. Ring mode: the waves split into the row-group x K-group shape that
+// minimizes the largest per-wave item count (ties: more row groups), among
+// the shapes whose per-tile partials fit LDS (one slot per wave and tile of
+// its row group).
 template <int DT, int TT, int KU, int MODE, bool BAL>
 static hipError_t launch_stream1(const FusedGemmArgs &a, uint32_t lds, hipStream_t s) {
-    constexpr bool balanced = BAL;
     auto k = fgemm_stream_kernel<DT, TT, KU, MODE, BAL>;
     static bool attr = false;
     if (!attr) {
@@ -96,17 +97,26 @@ static hipError_t launch_stream1(const FusedGemmArgs &a, uint32_t lds, hipStream
     const int nsb = b.K / 256;
     const unsigned R = std::min((unsigned)b.groups, res);
     const int per_wg = (int)((b.groups + R - 1) / R);
-    int best = 1 << 30;
-    b.wk = kWaves;
-    for (int wr = 1; wr <= kWaves; wr *= 2) {
-        const int wk = kWaves / wr;
-        const int items = ((per_wg + wr - 1) / wr) * ((nsb + wk - 1) / wk);
-        if (items <= best) {
-            best = items;
-            b.wk = wk;
+    b.wk = 0;
+    if (!BAL) {
+        const uint32_t slot = (uint32_t)kWaves * TT * 4 * 64 * 4;  // one partial per wave
+        const uint32_t base = lds - slot;
+        int best = 1 << 30;
+        uint32_t best_lds = 0;
+        for (int wr = 1; wr <= kWaves; wr *= 2) {
+            const int wk = kWaves / wr;
+            const int niter = (per_wg + wr - 1) / wr;
+            const uint32_t need = base + slot * (uint32_t)niter;
+            const int items = niter * ((nsb + wk - 1) / wk);
+            if (need <= kFusedLds && items <= best) {
+                best = items;
+                b.wk = wk;
+                best_lds = need;
+            }
         }
+        if (!b.wk) return hipErrorInvalidValue;  // no shape fits LDS
+        lds = best_lds;
     }
-    if (balanced) b.wk = 0;
     k<<<R, kThreads, lds, s>>>(b);
     return hipGetLastError();
 }

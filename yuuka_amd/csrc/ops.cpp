@@ -899,19 +899,6 @@ yuuka_status validate_model_op(const yuuka_op &op, uint64_t *ws) {
 
 bool gemm_chain_member(const yuuka_op &op) { return op.code == YUUKA_EXT_OP_GEMM_FUSED && fused_many_rows(op); }
 
-bool stream_chain_stage(const yuuka_op &op, FusedChainStage *st) {
-    if (op.code != YUUKA_EXT_OP_GEMM_FUSED || fused_many_rows(op)) return false;
-    FusedGemmArgs a = fused_args(op);
-    const int tt = fused_tiles(op, a.nseg);
-    a.chunk_sb = fused_gemm_chunk_sb(a.rows, a.K, tt, a.norm != nullptr, a.gate != nullptr);
-    return fused_gemm_chain_stage(a, tt, st);
-}
-
-yuuka_status execute_stream_chain(const FusedChainStage *st, int n, const ExecCtx &ctx) {
-    const hipError_t err = launch_fused_gemm_chain(st, n, ctx.chain_sync, ctx.stream);
-    if (err != hipSuccess) return fail(YUUKA_ERR_DEVICE, "chained GEMM_FUSED launch: %s", hip_error(err));
-    return YUUKA_OK;
-}
 
 bool gemm_chain_ws(const yuuka_op &op, uint64_t *quant, uint64_t *part) {
     if (!gemm_chain_member(op)) return false;

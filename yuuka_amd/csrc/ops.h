@@ -24,11 +24,6 @@ yuuka_status execute_gdn_commit_run(const yuuka_op *ops, int count, const ExecCt
 // GEMM_FUSED over more than 8 rows (the many-row kernel), and its workspace
 // in two parts (quantized rows, split partial sums).
 bool gemm_chain_member(const yuuka_op &op);
-// A GEMM_FUSED op the streaming kernel serves in a chained form (*st set).
-bool stream_chain_stage(const yuuka_op &op, FusedChainStage *st);
-// Runs ops[0..n) (stream_chain_stage true for each, supported together) as
-// one chained launch.
-yuuka_status execute_stream_chain(const FusedChainStage *st, int n, const ExecCtx &ctx);
 bool gemm_chain_ws(const yuuka_op &op, uint64_t *quant, uint64_t *part);
 // A run of n consecutive many-row GEMM_FUSED ops (launch_fused_gemm_rows_chain:
 // each split reduction inside the next member's prologue where they link),

@@ -13,16 +13,6 @@
 
 namespace yk {
 
-// Chained streaming GEMMs (k_fchain.hip) run only with YUUKA_STREAM_CHAIN=1:
-// at the config-2 verify step the chained launch measured slower than one
-// launch per projection (the stage hand-off and the device-scope activation
-// reads cost more than the launch boundaries they remove). Read when a plan
-// is executed or captured.
-static bool stream_chains_enabled() {
-    const char *e = std::getenv("YUUKA_STREAM_CHAIN");
-    return e && e[0] == '1';
-}
-
 static bool buf_ok(const yuuka_buffer *b, uint64_t off, uint64_t bytes) {
     return b != nullptr && off <= b->bytes && bytes <= b->bytes - off;
 }
@@ -236,10 +226,10 @@ static yuuka_status prepare(yuuka_plan *plan) {
         plan->ws_bytes = want;
     }
     // split-K tickets, then the chained GEMMs' counters in the last words
-    if (plan->tickets_len < plan->ticket_need + 1 + kFusedChainSyncWords) {
+    if (plan->tickets_len < plan->ticket_need + 1) {
         if (plan->tickets) (void)hipFree(plan->tickets);
         plan->tickets = nullptr;
-        const uint32_t want = plan->ticket_need + 64 + kFusedChainSyncWords;
+        const uint32_t want = plan->ticket_need + 64;
         hipError_t err = hipMalloc(reinterpret_cast<void **>(&plan->tickets), (size_t)want * 4);
         if (err == hipSuccess) err = hipMemset(plan->tickets, 0, (size_t)want * 4);
         if (err != hipSuccess) return fail(YUUKA_ERR_ALLOCATION, "plan tickets: %s", hip_error(err));
@@ -266,7 +256,6 @@ static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token,
                             uint64_t capacity, uint64_t *count) {
     ExecCtx ctx{stream, token, position, dyn, plan->ws, plan->tickets, plan->ws_bytes};
     ctx.part_off = plan->chain_quant ? (plan->chain_quant + 255) & ~255ull : 0;
-    if (stream_chains_enabled()) ctx.chain_sync = plan->tickets + (plan->tickets_len - kFusedChainSyncWords);
     uint64_t n = 0;
     hipEvent_t a = nullptr, b = nullptr;
     if (times) {
@@ -308,22 +297,6 @@ static yuuka_status run_ops(yuuka_plan *plan, hipStream_t stream, int32_t token,
                 if (plan->ops[k].buf[i] && !plan->ops[k].buf[i]->ptr) return false;
             return true;
         };
-        if (!times && ctx.chain_sync) {
-            // a run of dependent streaming GEMMs (a layer's out-projection,
-            // FFN and the next in-projection): one chained launch
-            FusedChainStage cs[kFusedChainMax];
-            int j = 0;
-            while (j < kFusedChainMax && oi + j < nops && usable(oi + j) && stream_chain_stage(plan->ops[oi + j], &cs[j]))
-                j++;
-            while (j >= 2 && !fused_gemm_chain_supported(cs, j)) j--;
-            if (j >= 2) {
-                st = execute_stream_chain(cs, j, ctx);
-                if (st != YUUKA_OK) break;
-                n += j;
-                oi += j - 1;
-                continue;
-            }
-        }
         if (!times && ctx.part_off && gemm_chain_member(op)) {
             // a run of many-row GEMMs: split reductions inside the next
             // member's prologue (and a following RMSNorm of the last output)

@@ -53,7 +53,6 @@ struct ExecCtx {
     uint32_t *tickets;
     uint64_t ws_bytes = 0;  // size of ws (0: unknown, no op pairs fused)
     uint64_t part_off = 0;  // many-row GEMM runs: partial sums at ws + part_off (0: not chained)
-    uint32_t *chain_sync = nullptr;  // chained streaming GEMMs: kFusedChainSyncWords zeroed words (null: none)
 };
 
 }  // namespace yk
