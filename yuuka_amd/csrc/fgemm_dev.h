@@ -1131,6 +1131,7 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
         // two items in flight per wave (deeper rings, issued before or after
         // the activations land, measured slower: the loop is bound by
         // instruction issue, not by outstanding loads)
+        // two stages: three or four (with this loop) made every launch slower
         constexpr int kD = 2;
         Stage sbr[kD][TT];
         // issued unconditionally (under a branch the compiler's wait counts
@@ -1161,11 +1162,11 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
         // over a switch on q % kD lets the compiler merge the cases and
         // rotate the stages through register copies, each of which waits
         // for the loads in flight
-        static_assert(kD == 2, "two register stages");
         auto step = [&](Stage (&S)[TT], int q) __attribute__((always_inline)) {
-            // q == nmine (odd counts): a stage issued past the end, all-zero
-            // weights; it multiplies into the current tile's partial exactly
-            const int qq = q < nmine ? q : q - 1;
+            // q >= nmine (the last round of a count that kD does not divide):
+            // a stage issued past the end, all-zero weights; it multiplies
+            // into the current tile's partial exactly
+            const int qq = min(q, nmine - 1);
             const int ii = wave + kWaves * qq, c = ii / nsb, sbi = ii - c * nsb;
             if (c != cur) {
                 flush(cur);
@@ -1176,9 +1177,9 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
             __builtin_amdgcn_sched_barrier(0);
             issue_slot(S, q + kD);
         };
-        for (int q = 0; q < nmine; q += 2) {
-            step(sbr[0], q);
-            step(sbr[1], q + 1);
+        for (int q = 0; q < nmine; q += kD) {
+#pragma unroll
+            for (int d = 0; d < kD; d++) step(sbr[d], q + d);
         }
         if (nmine > 0) flush(cur);
         lds_barrier();

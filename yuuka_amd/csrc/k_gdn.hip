@@ -327,7 +327,7 @@ __device__ __forceinline__ void conv_channel2(const float *conv_state, const flo
                     sum = __fadd_rn(sum, __fmul_rn(w[u][tt], xv));
                 }
                 sum = __fadd_rn(sum, __fmul_rn(w[u][3], x[u][r]));
-                dst[r * stride] = silu_ref(sum);
+                dst[r * stride] = silu_f32(sum);
             }
         }
         return;
@@ -372,7 +372,7 @@ __device__ __forceinline__ void conv_channel2(const float *conv_state, const flo
             for (int q = 0; q < 8; q++)
                 if (q == K - 1) wl = w[q];
             sum = __fadd_rn(sum, __fmul_rn(wl, x[r]));
-            dst[r * stride] = silu_ref(sum);
+            dst[r * stride] = silu_f32(sum);
         }
     }
 }
@@ -413,7 +413,7 @@ __device__ __forceinline__ void conv_channels4(const float *conv_state, const fl
                 sum = __fadd_rn(sum, __fmul_rn(w[u][tt], xv));
             }
             sum = __fadd_rn(sum, __fmul_rn(w[u][3], x[u][r]));
-            dst[u][r * stride[u]] = silu_ref(sum);
+            dst[u][r * stride[u]] = silu_f32(sum);
         }
     }
 }

@@ -13,6 +13,10 @@ namespace yk {
 // 1/(1+float32(exp(float64(-x)))) as model/qwen35/forward.go:552-554.
 __device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + (float)exp((double)(-x))); }
 __device__ __forceinline__ float silu_ref(float x) { return __fmul_rn(x, sigmoid_ref(x)); }
+// SiLU with a float32 exp (the device library's expf, within 1 ulp of the
+// rounded float64 exp) where the float64 exp is on a latency-critical path;
+// the sigmoid then differs from sigmoid_ref by at most an ulp or two.
+__device__ __forceinline__ float silu_f32(float x) { return __fmul_rn(x, 1.0f / (1.0f + expf(-x))); }
 __device__ __forceinline__ float softplus_ref(float x) { return x > 20.0f ? x : (float)log1p(exp((double)x)); }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
