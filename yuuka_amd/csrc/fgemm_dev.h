@@ -1128,11 +1128,11 @@ __device__ __forceinline__ void stream_groups(const FusedGemmArgs &A, uint8_t *l
         };
         constexpr int kSlot = TT * NA * 256;  // floats of one wave's partial of one tile
         float *myr = red + (size_t)wave * kBalMax * kSlot;
-        // two items in flight per wave (deeper rings, issued before or after
-        // the activations land, measured slower: the loop is bound by
-        // instruction issue, not by outstanding loads)
-        // two stages: three or four (with this loop) made every launch slower
-        constexpr int kD = 2;
+        // Register stages per wave: more weight requests in flight per CU
+        // lower the stream rate (three or four stages made every launch
+        // slower); two-tile items (FFN gate/up) run best with one stage, the
+        // other launches with two.
+        constexpr int kD = TT == 2 ? 1 : 2;
         Stage sbr[kD][TT];
         // issued unconditionally (under a branch the compiler's wait counts
         // lose track and the prologue would wait for these weights too)
