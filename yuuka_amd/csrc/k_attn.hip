@@ -1162,11 +1162,17 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
 // are computed once per workgroup into LDS.
 __device__ __forceinline__ int chunks_total(const AttnVArgs &a, int ck) { return (a.capacity + ck - 1) / ck; }
 
+// Merge of the chunk records of one (head, verify row): softmax weights
+// exp(m_c - max) of the chunks' maxima, o = sum_c o_c w_c / sum_c l_c w_c in
+// chunk order, times the output gate. Every record field a thread needs is
+// requested before the first is used (the chunk maxima and sums, the gate
+// and up to kMergeBatch values of the thread's column), so the merge waits
+// for one memory round trip instead of one per loop over the chunks.
+constexpr int kMergeBatch = 32;
 __global__ __launch_bounds__(256) void attn_merge_v_kernel(const float *__restrict__ q, const float *__restrict__ part,
                                                            AttnVArgs a, int ck, int chunks, float *__restrict__ out,
                                                            ModelDyn dyn) {
-    extern __shared__ float wsh[];  // [chunks] weights
-    __shared__ float red[4];
+    extern __shared__ float wsh[];  // [3][chunks]: maxima, sums, weights
     if (blockIdx.z) {  // request blockIdx.z
         const uint64_t rq = blockIdx.z, rows = rq * a.rq_rows;
         q += rows * a.heads * (a.gated ? 2 * a.head_dim : a.head_dim);
@@ -1175,35 +1181,44 @@ __global__ __launch_bounds__(256) void attn_merge_v_kernel(const float *__restri
         if (dyn.pos_dev) dyn.pos_dev += 2 * rq;
     }
     const int r = blockIdx.y, h = blockIdx.x;
-    const int D = a.head_dim;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int D = a.head_dim;  // <= 256 (launcher)
     const int p0 = cur_pos_a(dyn) + a.displacement;
     const int nchunk = min((p0 + r) / ck + 1, chunks);
+    float *ms = wsh, *ls = wsh + chunks, *ws = wsh + 2 * chunks;
     auto rec_of = [&](int c) { return part + (((int64_t)c * a.rows + r) * a.heads + h) * (D + 2); };
-    float mx = -INFINITY;
-    for (int c = threadIdx.x; c < nchunk; c += 256) mx = fmaxf(mx, rec_of(c)[D]);
-    mx = wave_max_f(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const int d = min((int)threadIdx.x, D - 1);
+    const int qstride = a.gated ? 2 * D : D;
+    const float gq = a.gated ? q[((int64_t)r * a.heads + h) * qstride + D + d] : 0.0f;
+    float v[kMergeBatch];
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; i++) v[i] = rec_of(min(i, nchunk - 1))[d];
     for (int c = threadIdx.x; c < nchunk; c += 256) {
-        const float mc = rec_of(c)[D];
-        wsh[c] = mc == -INFINITY ? 0.0f : exp_nonpos(mc - mx);
+        const float *rc = rec_of(c);
+        ms[c] = rc[D];
+        ls[c] = rc[D + 1];
     }
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int c = 0; c < nchunk; c++) mx = fmaxf(mx, ms[c]);
+    for (int c = threadIdx.x; c < nchunk; c += 256) ws[c] = ms[c] == -INFINITY ? 0.0f : exp_nonpos(ms[c] - mx);
     __syncthreads();
     float lsum = 0.0f;
-#pragma unroll 8
-    for (int c = 0; c < nchunk; c++) lsum += rec_of(c)[D + 1] * wsh[c];
-    const float inv = 1.0f / lsum;
-    const int qstride = a.gated ? 2 * D : D;
-    for (int d = threadIdx.x; d < D; d += 256) {
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int c = 0; c < nchunk; c++) acc += rec_of(c)[d] * wsh[c];
-        float o = acc * inv;
-        if (a.gated) o *= sigmoid_ref(q[((int64_t)r * a.heads + h) * qstride + D + d]);
-        out[((int64_t)r * a.heads + h) * D + d] = o;
+    for (int c = 0; c < nchunk; c++) lsum += ls[c] * ws[c];
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; i++)
+        if (i < nchunk) acc += v[i] * ws[i];
+    for (int c0 = kMergeBatch; c0 < nchunk; c0 += kMergeBatch) {
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; i++) v[i] = rec_of(min(c0 + i, nchunk - 1))[d];
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; i++)
+            if (c0 + i < nchunk) acc += v[i] * ws[c0 + i];
     }
+    if ((int)threadIdx.x >= D) return;
+    float o = acc * (1.0f / lsum);
+    if (a.gated) o *= sigmoid_ref(gq);
+    out[((int64_t)r * a.heads + h) * D + d] = o;
 }
 
 }  // namespace
@@ -1338,7 +1353,8 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
             q, k, v, static_cast<uint8_t *>(kpool), static_cast<uint8_t *>(vpool), table, q_norm, k_norm, rope, a,
             part, dyn);
     }
-    attn_merge_v_kernel<<<dim3((unsigned)a.heads, (unsigned)a.rows, nz), 256, (size_t)launch_chunks * 4, s>>>(
+    if (a.head_dim > 256) return hipErrorInvalidValue;  // the merge holds one column per thread
+    attn_merge_v_kernel<<<dim3((unsigned)a.heads, (unsigned)a.rows, nz), 256, (size_t)launch_chunks * 12, s>>>(
         q, part, a, ck, launch_chunks, out, dyn);
     return hipGetLastError();
 }
