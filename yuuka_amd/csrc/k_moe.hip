@@ -731,16 +731,24 @@ __global__ __launch_bounds__(kMoeThreads) __attribute__((amdgpu_waves_per_eu(4))
                 }
             }
         };
+        // Every load past the first is issued unconditionally (the item index
+        // clamped to the wave's last item, which is then read again): loads
+        // under a branch make the compiler's wait counts merge conservatively,
+        // and the multiply of one stage would wait for the other stage's
+        // loads too. Each stage keeps its own code path (two items per
+        // iteration).
         uint4 h0, h1;
         uint4 q0[2], q1[2];
-        if (total > 0) load_item(0, h0, q0);
-        if (total > 1) load_item(1, h1, q1);
-        for (int q = 0; q < total; q += 2) {
-            compute_item(q, h0, q0);
-            if (q + 2 < total) load_item(q + 2, h0, q0);
-            if (q + 1 < total) {
-                compute_item(q + 1, h1, q1);
-                if (q + 3 < total) load_item(q + 3, h1, q1);
+        if (total > 0) {  // wave-uniform
+            load_item(0, h0, q0);
+            load_item(min(1, total - 1), h1, q1);
+            for (int q = 0; q < total; q += 2) {
+                compute_item(q, h0, q0);
+                __builtin_amdgcn_sched_barrier(0);
+                load_item(min(q + 2, total - 1), h0, q0);
+                if (q + 1 < total) compute_item(q + 1, h1, q1);
+                __builtin_amdgcn_sched_barrier(0);
+                load_item(min(q + 3, total - 1), h1, q1);
             }
         }
         __syncthreads();
