@@ -1191,18 +1191,23 @@ __global__ __launch_bounds__(256) void attn_merge_v_kernel(const float *__restri
     const float gq = a.gated ? q[((int64_t)r * a.heads + h) * qstride + D + d] : 0.0f;
     float v[kMergeBatch];
 #pragma unroll
-    for (int i = 0; i < kMergeBatch; i++) v[i] = rec_of(min(i, nchunk - 1))[d];
+    for (int i = 0; i < kMergeBatch; i++) v[i] = i < nchunk ? rec_of(i)[d] : 0.0f;  // nchunk: workgroup-uniform
+    float mx = -INFINITY;
     for (int c = threadIdx.x; c < nchunk; c += 256) {
         const float *rc = rec_of(c);
         ms[c] = rc[D];
         ls[c] = rc[D + 1];
+        mx = fmaxf(mx, ms[c]);
     }
+    __shared__ float red[4];
+    mx = wave_max_f(mx);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
     __syncthreads();
-    float mx = -INFINITY;
-    for (int c = 0; c < nchunk; c++) mx = fmaxf(mx, ms[c]);
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     for (int c = threadIdx.x; c < nchunk; c += 256) ws[c] = ms[c] == -INFINITY ? 0.0f : exp_nonpos(ms[c] - mx);
     __syncthreads();
     float lsum = 0.0f;
+#pragma unroll 8
     for (int c = 0; c < nchunk; c++) lsum += ls[c] * ws[c];
     float acc = 0.0f;
 #pragma unroll
@@ -1210,7 +1215,7 @@ __global__ __launch_bounds__(256) void attn_merge_v_kernel(const float *__restri
         if (i < nchunk) acc += v[i] * ws[i];
     for (int c0 = kMergeBatch; c0 < nchunk; c0 += kMergeBatch) {
 #pragma unroll
-        for (int i = 0; i < kMergeBatch; i++) v[i] = rec_of(min(c0 + i, nchunk - 1))[d];
+        for (int i = 0; i < kMergeBatch; i++) v[i] = c0 + i < nchunk ? rec_of(c0 + i)[d] : 0.0f;
 #pragma unroll
         for (int i = 0; i < kMergeBatch; i++)
             if (c0 + i < nchunk) acc += v[i] * ws[c0 + i];
