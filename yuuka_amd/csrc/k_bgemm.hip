@@ -64,18 +64,28 @@ constexpr int kBgWaves = 8;
 constexpr int kBgThreads = 64 * kBgWaves;
 constexpr float kBgRange = 256.0f;  // |y / scale| <= kBgRange
 
+// The prologue's output, in the order the GEMM stages it into LDS: rows
+// padded to whole 16-row tiles (tiles = ceil(rows / 16); the padding rows are
+// zero), super-block major so that one stage of a block of row tiles is one
+// contiguous piece per tile:
+//   h      [sb][tile][sub-block j][group g][row c][8 FP16]  (8 KB per tile)
+//   sums   [sb][tile][row c][16 FP16]                       (512 B per tile)
+//   scales [sb][tile * 16 + c] float
 struct BgQuant {
-    _Float16 *h;     // [rows][K]: y / scale
-    _Float16 *sums;  // [rows][K/256][16]: sub-block sums of h, high parts (8) then remainders (8)
-    float *scales;   // [rows][K/256]
+    _Float16 *h;     // y / scale
+    _Float16 *sums;  // sub-block sums of h: high parts (8) then remainders (8)
+    float *scales;
 };
+
+__host__ __device__ inline int bg_rows16(int rows) { return (rows + 15) & ~15; }
 
 __host__ __device__ inline BgQuant bg_view(void *ws, int rows, int K) {
     uint8_t *p = static_cast<uint8_t *>(ws);
+    const uint64_t r16 = (uint64_t)bg_rows16(rows);
     BgQuant q;
     q.h = reinterpret_cast<_Float16 *>(p);
-    q.sums = reinterpret_cast<_Float16 *>(p + (uint64_t)rows * K * 2);
-    q.scales = reinterpret_cast<float *>(p + (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 256) * 32);
+    q.sums = reinterpret_cast<_Float16 *>(p + r16 * K * 2);
+    q.scales = reinterpret_cast<float *>(p + r16 * K * 2 + r16 * (K / 256) * 32);
     return q;
 }
 
@@ -160,6 +170,29 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
     const int sb0 = (int)blockIdx.y * W * P;
     auto elem = [&](int i) { return (sb0 + wave + W * i) * 256 + 4 * lane; };
     auto live = [&](int i) { return sb0 + wave + W * i < nsb; };
+    // where lane's four values, its sub-block sum and the row scale of
+    // super-block sb go (lane: sub-block lane / 8, group (lane / 2) % 4, half lane % 2)
+    const int tiles = bg_rows16(A.rows) / 16, tile = row >> 4, c = row & 15;
+    auto h_at = [&](int sb) {
+        return q.h + ((uint64_t)sb * tiles + tile) * 4096 + (lane >> 3) * 512 + ((lane >> 1) & 3) * 128 + c * 8 +
+               (lane & 1) * 4;
+    };
+    auto sums_at = [&](int sb) { return q.sums + ((uint64_t)sb * tiles + tile) * 256 + c * 16 + (lane >> 3); };
+    auto scale_at = [&](int sb) { return q.scales + (uint64_t)sb * tiles * 16 + row; };
+    if (row >= A.rows) {  // a padding row of the last tile: zeros
+#pragma unroll
+        for (int i = 0; i < P; i++) {
+            if (!live(i)) break;  // wave-uniform
+            const int sb = sb0 + wave + W * i;
+            *reinterpret_cast<uint2 *>(h_at(sb)) = make_uint2(0u, 0u);
+            if ((lane & 7) == 0) {
+                sums_at(sb)[0] = (_Float16)0.0f;
+                sums_at(sb)[8] = (_Float16)0.0f;
+            }
+            if (lane == 0) *scale_at(sb) = 0.f;
+        }
+        return;
+    }
     auto add4 = [](float4 &v, const float4 &w) {
         v.x += w.x;
         v.y += w.y;
@@ -272,7 +305,7 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
 #pragma unroll
     for (int i = 0; i < P; i++) {
         if (!live(i)) break;  // wave-uniform
-        const int sb = sb0 + wave + W * i, e = elem(i);
+        const int sb = sb0 + wave + W * i;
         float4 y = v[i];
         if (A.gate) {
             // recurrent.go:39-50 gated head norm over heads of 128 (lanes 0..31
@@ -298,16 +331,16 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
         const float inv = m > 0.f ? kBgRange / m : 0.f;
         const _Float16 h0 = (_Float16)(y.x * inv), h1 = (_Float16)(y.y * inv), h2 = (_Float16)(y.z * inv),
                        h3 = (_Float16)(y.w * inv);
-        *reinterpret_cast<uint2 *>(q.h + rbase + e) = make_uint2(h2bits(h0, h1), h2bits(h2, h3));
+        *reinterpret_cast<uint2 *>(h_at(sb)) = make_uint2(h2bits(h0, h1), h2bits(h2, h3));
         // sub-block lane >> 3: eight lanes of four values
         const float s = group8_sum(((float)h0 + (float)h1) + ((float)h2 + (float)h3));
         if ((lane & 7) == 0) {
             const _Float16 shi = (_Float16)s, slo = (_Float16)(s - (float)shi);
-            _Float16 *sd = q.sums + ((uint64_t)row * nsb + sb) * 16 + (lane >> 3);
+            _Float16 *sd = sums_at(sb);
             sd[0] = shi;
             sd[8] = slo;
         }
-        if (lane == 0) q.scales[(uint64_t)row * nsb + sb] = m > 0.f ? m / kBgRange : 0.f;
+        if (lane == 0) *scale_at(sb) = m > 0.f ? m / kBgRange : 0.f;
     }
 }
 
@@ -325,9 +358,8 @@ struct BgArgs {
 // 8 bytes at an even byte address (Q6_K blocks are 210 B): two dword-aligned
 // loads and a byte shift.
 __device__ __forceinline__ uint64_t load8_even(const uint8_t *p) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t *w = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
-    const uint32_t sh = (uint32_t)(a & 3);
+    const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(p) & 3;
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(p - sh);  // pointer arithmetic keeps the global address space
     const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
     const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
     const uint32_t hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
@@ -419,201 +451,220 @@ __device__ __forceinline__ half8 pack8(half2v a, half2v b, half2v c, half2v d) {
     return half8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
-// LDS of one stage for NT row tiles: A [16 NT rows][32 blocks of 8 FP16]
-// with block b of row r at b ^ (r & 15) (a tile's 16 rows read one block
-// each without bank conflicts), sub-block sums [rows][16 FP16] padded to
-// whole 1 KB copies, row scales [rows] float. Two stages; the SwiGLU
-// epilogue reuses the first.
+// LDS of one stage for NT row tiles, in the order of the quantized rows
+// (BgQuant): A [tile][sub-block j][group g][row c][8 FP16], so that lane
+// (c, g) reads the A operand of tile t, sub-block j at g 256 + c 16 + t 8192
+// + j 1024 (16 consecutive lanes read 256 consecutive bytes, and all but the
+// lane's own offset are instruction immediates), sub-block sums [tile][c][16
+// FP16], row scales [16 NT] float. Two stages; the SwiGLU epilogue reuses
+// the first.
 template <int NT> struct BgLds {
     static constexpr int kRows = 16 * NT;
     static constexpr uint32_t A = 0;
-    static constexpr uint32_t S = A + kRows * 512;
-    static constexpr uint32_t X = S + ((kRows + 31) / 32) * 1024;
+    static constexpr uint32_t S = A + NT * 8192;
+    static constexpr uint32_t X = S + NT * 512;
     static constexpr uint32_t stage = X + kRows * 4;
     static constexpr uint32_t total = 2 * stage;
 };
-static_assert(BgLds<5>::total <= 160 * 1024, "five tiles fit LDS");
+static_assert(BgLds<9>::total <= 160 * 1024, "nine tiles fit LDS");
 
-// 16-byte global -> LDS copy of one lane (lane l writes [m0 + 16 l, +16)),
-// as inline assembly so that the compiler's wait counts do not see it (it
-// would otherwise wait for the weight loads before every LDS read). The
-// main loop waits for the copies itself (vmcnt(0) before its barrier).
-__device__ __forceinline__ void lds_copy16(const void *src, const uint8_t *lds_dst) {
+// 16-byte global -> LDS copy of one lane (lane l writes [m0 + 16 l, +16)
+// from base + voff, base uniform), as inline assembly so that the
+// compiler's wait counts do not see it (it would otherwise wait for the
+// weight loads before every LDS read). The main loop waits for the copies
+// itself (vmcnt(0) before its barrier).
+__device__ __forceinline__ void lds_copy16(const uint8_t *base, uint32_t voff, const uint8_t *lds_dst) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_dst);
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+    const uint64_t b = reinterpret_cast<uintptr_t>(base);
+    const uint64_t sb = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b) |
+                        ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)) << 32);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sb), "s"(m0)
+                 : "memory", "m0");
 }
 
-// Issues the copies of super-block sb of the block's rows into a stage
-// (rows past the block's end repeat its last row; their outputs are never
-// stored) and returns this thread's row scale (threads < 16 NT).
+// Issues the copies of super-block sb of the block's tiles [T0, T0 + NT)
+// into a stage — per tile one 8 KB piece, 16 bytes per thread, and the
+// tiles' sums as one piece — and returns this thread's row scale (threads <
+// 16 NT). Tiles past the last one are not copied: their rows' outputs are
+// never stored.
 template <int NT>
-__device__ __forceinline__ float stage_issue(const BgArgs &A, uint8_t *stage, int m0, int mrows, int sb) {
+__device__ __forceinline__ float stage_issue(const BgArgs &A, uint8_t *stage, int T0, int tiles, int sb) {
     using LY = BgLds<NT>;
-    const int K = A.f.K, nsb = K / 256;
-    int oz;  // opaque zero: the copy addresses are recomputed per call, not held (and spilled) across the loop
-    asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
-    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = (threadIdx.x & 63) + oz;
-    // A: copy i covers rows 2 i, 2 i + 1 (lane l: row 2 i + l / 32, LDS block l % 32)
-#pragma unroll 1
-    for (int i = wave; i < LY::kRows / 2; i += kBgWaves) {
-        const int r = 2 * i + (lane >> 5), pb = lane & 31;
-        const int rr = min(r, mrows - 1);
-        lds_copy16(A.q.h + (uint64_t)(m0 + rr) * K + sb * 256 + (pb ^ (r & 15)) * 8, stage + LY::A + (uint32_t)i * 1024);
-    }
-    // sums: copy i covers rows 32 i .. 32 i + 31 (lane l: row 32 i + l / 2, half l % 2)
-#pragma unroll 1
-    for (int i = wave; i < (LY::kRows + 31) / 32; i += kBgWaves) {
-        const int r = min(32 * i + (lane >> 1), mrows - 1);
-        lds_copy16(A.q.sums + ((uint64_t)(m0 + r) * nsb + sb) * 16 + (lane & 1) * 8, stage + LY::S + (uint32_t)i * 1024);
-    }
-    const int t = (int)threadIdx.x + oz;
-    return t < LY::kRows ? A.q.scales[(uint64_t)(m0 + min(t, mrows - 1)) * nsb + sb] : 0.f;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const uint32_t voff = threadIdx.x * 16;
+    const int nt = min(NT, tiles - T0);
+    const uint64_t piece = (uint64_t)sb * tiles + T0;
+    const uint8_t *h = reinterpret_cast<const uint8_t *>(A.q.h) + piece * 8192;
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+        if (t < nt) lds_copy16(h + t * 8192, voff, stage + LY::A + t * 8192 + wave * 1024);
+    if (voff < (uint32_t)nt * 512)
+        lds_copy16(reinterpret_cast<const uint8_t *>(A.q.sums) + piece * 512, voff, stage + LY::S + wave * 1024);
+    const int t = (int)threadIdx.x;
+    return t < 16 * nt ? A.q.scales[piece * 16 + t] : 0.f;
 }
 
-// A operand of row tile t, sub-block j for lane (row c, group g).
-__device__ __forceinline__ half8 a_op(const uint8_t *stage, int t, int j, int c, int g) {
-    const int r = 16 * t + c, b = 4 * j + g;
-    return *reinterpret_cast<const half8 *>(stage + (uint32_t)r * 512 + (uint32_t)((b ^ c) * 16));
-}
-
-// The main loop of one wave over the super-blocks (weights of dtype DT): its
-// tile's B operands are built once per super-block and multiplied with all
-// NT row tiles (rows past the block's end are copies of its last row; a
-// branch per tile would keep the scheduler from issuing the tiles' LDS reads
-// ahead of their MFMAs). LDS holds two stages; stage sb + 1 is copied in
-// while sb is multiplied.
-template <int DT, int NT>
-__device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int m0, int mrows, bool live,
-                                        const uint8_t *wrow, float (&y)[NT][4]) {
+// One super-block of the wave's tile against the NT row tiles of stage st
+// (sub-block pairs outer, row tiles inner: two B operands live at a time,
+// one FP32 accumulator per row tile), added into y. Rows past the block's
+// end are computed like the others (a branch per tile would keep the
+// scheduler from issuing the tiles' LDS reads ahead of their MFMAs).
+template <int NT>
+__device__ __forceinline__ void bg_super_q4(const WQ4 &cur, const uint8_t *st, float (&y)[NT][4]) {
     using LY = BgLds<NT>;
     const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+    const uint8_t *la = st + LY::A + g * 256 + c * 16;
+    f32x4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const float d = h2f((uint16_t)(cur.hdr.x & 0xffffu));
+    const float dmin = h2f((uint16_t)(cur.hdr.x >> 16));
+    _Float16 mins[8];
+#pragma unroll
+    for (int jp = 0; jp < 4; jp++) {
+        int sce, mne, sco, mno;
+        scale_min_k4(2 * jp, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sce, &mne);
+        scale_min_k4(2 * jp + 1, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sco, &mno);
+        mins[2 * jp] = (_Float16)mne;
+        mins[2 * jp + 1] = (_Float16)mno;
+        // bytes b0..b7 of the lane: low nibbles are sub-block 2 jp, high
+        // nibbles 2 jp + 1. Low: (1024 + q) sc - 1024 sc; high, masked in
+        // place: (1024 + 16 q) (sc / 16) - 64 sc. Both are q sc exactly (one
+        // rounding of an exact value below 2048).
+        const uint32_t w0 = (uint32_t)cur.q[jp], w1 = (uint32_t)(cur.q[jp] >> 32);
+        const uint32_t p01 = __builtin_amdgcn_perm(0u, w0, 0x0c010c00u), p23 = __builtin_amdgcn_perm(0u, w0, 0x0c030c02u);
+        const uint32_t p45 = __builtin_amdgcn_perm(0u, w1, 0x0c010c00u), p67 = __builtin_amdgcn_perm(0u, w1, 0x0c030c02u);
+        const half2v se = splat_h((float)sce), so = splat_h(0.0625f * (float)sco);
+        const half2v ce = splat_h(-1024.f * (float)sce), co = splat_h(-64.f * (float)sco);
+        const half8 be = pack8(__builtin_elementwise_fma(magic_pair(p01, 0x000F000Fu), se, ce),
+                               __builtin_elementwise_fma(magic_pair(p23, 0x000F000Fu), se, ce),
+                               __builtin_elementwise_fma(magic_pair(p45, 0x000F000Fu), se, ce),
+                               __builtin_elementwise_fma(magic_pair(p67, 0x000F000Fu), se, ce));
+        const half8 bo = pack8(__builtin_elementwise_fma(magic_pair(p01, 0x00F000F0u), so, co),
+                               __builtin_elementwise_fma(magic_pair(p23, 0x00F000F0u), so, co),
+                               __builtin_elementwise_fma(magic_pair(p45, 0x00F000F0u), so, co),
+                               __builtin_elementwise_fma(magic_pair(p67, 0x00F000F0u), so, co));
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const half8 ae = *reinterpret_cast<const half8 *>(la + t * 8192 + (2 * jp) * 1024);
+            const half8 ao = *reinterpret_cast<const half8 *>(la + t * 8192 + (2 * jp + 1) * 1024);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ae, be, acc[t], 0, 0, 0);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao, bo, acc[t], 0, 0, 0);
+        }
+    }
+    // min term: K slots 0..7 (lanes g = 0) and 8..15 (g = 1) hold the mins
+    // against the sums' high parts and remainders
+    const half8 bmin = g < 2 ? half8{mins[0], mins[1], mins[2], mins[3], mins[4], mins[5], mins[6], mins[7]} : half8{};
+    const uint8_t *ls = st + LY::S + c * 32 + g * 16;
+    const float *lxs = reinterpret_cast<const float *>(st + LY::X) + 4 * g;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const half8 as = g < 2 ? *reinterpret_cast<const half8 *>(ls + t * 512) : half8{};
+        const f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bmin, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        const float4 xs = *reinterpret_cast<const float4 *>(lxs + 16 * t);
+        const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) y[t][i] += xsv[i] * (d * acc[t][i] - dmin * mn[i]);
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void bg_super_q6(const WQ6 &cur, const uint8_t *st, float (&y)[NT][4]) {
+    using LY = BgLds<NT>;
+    const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
+    const uint8_t *la = st + LY::A + g * 256 + c * 16;
+    f32x4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Q6_K: q = (ql | qh << 4) - 32, scale byte 2 j + (g >> 1) for the
+    // lane's eight elements of sub-block j
+    const float d = h2f((uint16_t)cur.d);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int half = j >> 2, qd = j & 3;
+        const uint64_t lo4 = (cur.ql[2 * half + (qd & 1)] >> (4 * (qd >> 1))) & 0x0F0F0F0F0F0F0F0Full;
+        const uint64_t hi2 = ((cur.qh[half] >> (2 * qd)) & 0x0303030303030303ull) << 4;
+        const uint64_t u = lo4 | hi2;  // q + 32 per byte
+        const uint32_t w0 = (uint32_t)u, w1 = (uint32_t)(u >> 32);
+        const half2v s2 = splat_h((float)sbyte(cur.sc, 2 * j + (g >> 1)));
+        const half2v off = splat_h(-1056.f);
+        auto one = [&](uint32_t pq) __attribute__((always_inline)) {
+            return (magic_pair(pq, 0x003F003Fu) + off) * s2;  // (1024 + q + 32) - 1056 = q, times sc
+        };
+        const half8 bj = pack8(one(__builtin_amdgcn_perm(0u, w0, 0x0c010c00u)), one(__builtin_amdgcn_perm(0u, w0, 0x0c030c02u)),
+                               one(__builtin_amdgcn_perm(0u, w1, 0x0c010c00u)), one(__builtin_amdgcn_perm(0u, w1, 0x0c030c02u)));
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const half8 *>(la + t * 8192 + j * 1024), bj,
+                                                            acc[t], 0, 0, 0);
+    }
+    const float *lxs = reinterpret_cast<const float *>(st + LY::X) + 4 * g;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const float4 xs = *reinterpret_cast<const float4 *>(lxs + 16 * t);
+        const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) y[t][i] += xsv[i] * (d * acc[t][i]);
+    }
+}
+
+// The main loop of one wave over the super-blocks (weights of dtype DT) of
+// the block of row tiles [T0, T0 + NT): its tile's B operands are built once
+// per super-block and multiplied with all NT row tiles. Two LDS stages and
+// two weight register sets, unrolled by two so that each is a fixed one:
+// super-block sb + 1 is copied and loaded while sb is multiplied. Every
+// weight load is issued, its index clamped to the last super-block (loads
+// under a branch would make the compiler copy the register sets).
+template <int DT, int NT>
+__device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int T0, bool live, const uint8_t *wrow,
+                                        float (&y)[NT][4]) {
+    using LY = BgLds<NT>;
+    const int g = (threadIdx.x & 63) >> 4;
+    const int tiles = bg_rows16(A.f.rows) / 16;
     // this split's super-blocks [sb_lo, nsb)
     const int nsb_all = A.f.K / 256;
     const int sb_lo = (int)((int64_t)nsb_all * blockIdx.z / A.splits);
     const int nsb = (int)((int64_t)nsb_all * (blockIdx.z + 1) / A.splits);
-    wrow += (uint64_t)sb_lo * (DT == kQ4K ? 144 : 210);
-    typedef typename std::conditional<DT == kQ4K, WQ4, WQ6>::type W;
     constexpr int blk = DT == kQ4K ? 144 : 210;
-    W w{};
-    if (live) {
-        if constexpr (DT == kQ4K) load_q4(w, wrow, g);
-        else load_q6(w, wrow, g);
-    }
-    float xs_next = stage_issue<NT>(A, lds, m0, mrows, sb_lo);
+    typedef typename std::conditional<DT == kQ4K, WQ4, WQ6>::type W;
+    auto loadw = [&](W &w, int sb) __attribute__((always_inline)) {
+        const uint8_t *b = wrow + (uint64_t)sb * blk;
+        if constexpr (DT == kQ4K) load_q4(w, b, g);
+        else load_q6(w, b, g);
+    };
+    auto super = [&](const W &w, const uint8_t *st) __attribute__((always_inline)) {
+        if constexpr (DT == kQ4K) bg_super_q4<NT>(w, st, y);
+        else bg_super_q6<NT>(w, st, y);
+    };
+    float *x0 = reinterpret_cast<float *>(lds + LY::X), *x1 = reinterpret_cast<float *>(lds + LY::stage + LY::X);
+    W wa, wb;
+    loadw(wa, sb_lo);
+    float xs = stage_issue<NT>(A, lds, T0, tiles, sb_lo);
     __builtin_amdgcn_s_waitcnt(0);
-    if (threadIdx.x < LY::kRows) reinterpret_cast<float *>(lds + LY::X)[threadIdx.x] = xs_next;
+    if (threadIdx.x < LY::kRows) x0[threadIdx.x] = xs;
     __syncthreads();
-#pragma unroll 1  // one super-block per iteration: unrolled, the live registers double
-    for (int sb = sb_lo; sb < nsb; sb++) {
-        const uint8_t *cur_l = lds + (uint32_t)((sb - sb_lo) & 1) * LY::stage;
-        uint8_t *nxt_l = lds + (uint32_t)((sb - sb_lo + 1) & 1) * LY::stage;
-        const float *lxs = reinterpret_cast<const float *>(cur_l + LY::X);
-        const bool more = sb + 1 < nsb;
-        if (more) xs_next = stage_issue<NT>(A, nxt_l, m0, mrows, sb + 1);
-        const W cur = w;  // this super-block; the next one's loads go out now
-        if (live && more) {
-            if constexpr (DT == kQ4K) load_q4(w, wrow + (uint64_t)(sb + 1 - sb_lo) * blk, g);
-            else load_q6(w, wrow + (uint64_t)(sb + 1 - sb_lo) * blk, g);
+#pragma unroll 1
+    for (int sb = sb_lo; sb < nsb; sb += 2) {
+        // stage 0 and wa hold sb; stage 1 and wb take sb + 1
+        const bool more1 = sb + 1 < nsb;
+        if (more1) xs = stage_issue<NT>(A, lds + LY::stage, T0, tiles, sb + 1);
+        loadw(wb, min(sb + 1, nsb - 1));
+        if (live) super(wa, lds);
+        if (more1) {
+            __builtin_amdgcn_s_waitcnt(0);  // the copies into stage 1 (and this thread's row scale)
+            if (threadIdx.x < LY::kRows) x1[threadIdx.x] = xs;
         }
-        if (live) {
-            // lane constants re-derived per super-block from an opaque zero:
-            // hoisted out of the loop, the per-tile LDS offsets they feed
-            // would be spilled
-            int oz;
-            asm volatile("s_mov_b32 %0, 0" : "=s"(oz));
-            const int lc = c + oz, lg = g + oz;
-            // sub-block pairs outer, row tiles inner: two B operands live at a
-            // time, one FP32 accumulator per row tile
-            f32x4 acc[NT];
-#pragma unroll
-            for (int t = 0; t < NT; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-            float d, dmin = 0.f;
-            if constexpr (DT == kQ4K) {
-                d = h2f((uint16_t)(cur.hdr.x & 0xffffu));
-                dmin = h2f((uint16_t)(cur.hdr.x >> 16));
-                _Float16 mins[8];
-#pragma unroll
-                for (int jp = 0; jp < 4; jp++) {
-                    int sce, mne, sco, mno;
-                    scale_min_k4(2 * jp, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sce, &mne);
-                    scale_min_k4(2 * jp + 1, cur.hdr.y, cur.hdr.z, cur.hdr.w, &sco, &mno);
-                    mins[2 * jp] = (_Float16)mne;
-                    mins[2 * jp + 1] = (_Float16)mno;
-                    // bytes b0..b7 of the lane: low nibbles are sub-block 2 jp,
-                    // high nibbles 2 jp + 1. Low: (1024 + q) sc - 1024 sc; high,
-                    // masked in place: (1024 + 16 q) (sc / 16) - 64 sc. Both are
-                    // q sc exactly (one rounding of an exact value below 2048).
-                    const uint32_t w0 = (uint32_t)cur.q[jp], w1 = (uint32_t)(cur.q[jp] >> 32);
-                    const uint32_t p01 = __builtin_amdgcn_perm(0u, w0, 0x0c010c00u), p23 = __builtin_amdgcn_perm(0u, w0, 0x0c030c02u);
-                    const uint32_t p45 = __builtin_amdgcn_perm(0u, w1, 0x0c010c00u), p67 = __builtin_amdgcn_perm(0u, w1, 0x0c030c02u);
-                    const half2v se = splat_h((float)sce), so = splat_h(0.0625f * (float)sco);
-                    const half2v ce = splat_h(-1024.f * (float)sce), co = splat_h(-64.f * (float)sco);
-                    const half8 be = pack8(__builtin_elementwise_fma(magic_pair(p01, 0x000F000Fu), se, ce),
-                                           __builtin_elementwise_fma(magic_pair(p23, 0x000F000Fu), se, ce),
-                                           __builtin_elementwise_fma(magic_pair(p45, 0x000F000Fu), se, ce),
-                                           __builtin_elementwise_fma(magic_pair(p67, 0x000F000Fu), se, ce));
-                    const half8 bo = pack8(__builtin_elementwise_fma(magic_pair(p01, 0x00F000F0u), so, co),
-                                           __builtin_elementwise_fma(magic_pair(p23, 0x00F000F0u), so, co),
-                                           __builtin_elementwise_fma(magic_pair(p45, 0x00F000F0u), so, co),
-                                           __builtin_elementwise_fma(magic_pair(p67, 0x00F000F0u), so, co));
-#pragma unroll
-                    for (int t = 0; t < NT; t++) {
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op(cur_l, t, 2 * jp, lc, lg), be, acc[t], 0, 0, 0);
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op(cur_l, t, 2 * jp + 1, lc, lg), bo, acc[t], 0, 0, 0);
-                    }
-                }
-                // min term: K slots 0..7 (lanes g = 0) and 8..15 (g = 1) hold the
-                // mins against the sums' high parts and remainders
-                const half8 bmin = g < 2 ? half8{mins[0], mins[1], mins[2], mins[3], mins[4], mins[5], mins[6], mins[7]}
-                                         : half8{};
-                const uint8_t *lsum = cur_l + LY::S;
-#pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    const half8 as = g < 2 ? *reinterpret_cast<const half8 *>(lsum + (uint32_t)(16 * t + lc) * 32 + lg * 16)
-                                           : half8{};
-                    const f32x4 mn = __builtin_amdgcn_mfma_f32_16x16x32_f16(as, bmin, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    const float4 xs = *reinterpret_cast<const float4 *>(lxs + 16 * t + 4 * lg);
-                    const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
-#pragma unroll
-                    for (int i = 0; i < 4; i++) y[t][i] += xsv[i] * (d * acc[t][i] - dmin * mn[i]);
-                }
-            } else {
-                // Q6_K: q = (ql | qh << 4) - 32, scale byte 2 j + (g >> 1) for
-                // the lane's eight elements of sub-block j
-                d = h2f((uint16_t)cur.d);
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const int half = j >> 2, qd = j & 3;
-                    const uint64_t lo4 = (cur.ql[2 * half + (qd & 1)] >> (4 * (qd >> 1))) & 0x0F0F0F0F0F0F0F0Full;
-                    const uint64_t hi2 = ((cur.qh[half] >> (2 * qd)) & 0x0303030303030303ull) << 4;
-                    const uint64_t u = lo4 | hi2;  // q + 32 per byte
-                    const uint32_t w0 = (uint32_t)u, w1 = (uint32_t)(u >> 32);
-                    const half2v s2 = splat_h((float)sbyte(cur.sc, 2 * j + (g >> 1)));
-                    const half2v off = splat_h(-1056.f);
-                    auto one = [&](uint32_t pq) __attribute__((always_inline)) {
-                        return (magic_pair(pq, 0x003F003Fu) + off) * s2;  // (1024 + q + 32) - 1056 = q, times sc
-                    };
-                    const half8 bj = pack8(one(__builtin_amdgcn_perm(0u, w0, 0x0c010c00u)), one(__builtin_amdgcn_perm(0u, w0, 0x0c030c02u)),
-                                           one(__builtin_amdgcn_perm(0u, w1, 0x0c010c00u)), one(__builtin_amdgcn_perm(0u, w1, 0x0c030c02u)));
-#pragma unroll
-                    for (int t = 0; t < NT; t++) {
-                        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a_op(cur_l, t, j, lc, lg), bj, acc[t], 0, 0, 0);
-                    }
-                }
-#pragma unroll
-                for (int t = 0; t < NT; t++) {
-                    const float4 xs = *reinterpret_cast<const float4 *>(lxs + 16 * t + 4 * lg);
-                    const float xsv[4] = {xs.x, xs.y, xs.z, xs.w};
-#pragma unroll
-                    for (int i = 0; i < 4; i++) y[t][i] += xsv[i] * (d * acc[t][i]);
-                }
-            }
+        __syncthreads();  // stage 1 complete; stage 0 read by every wave
+        if (!more1) break;
+        const bool more2 = sb + 2 < nsb;
+        if (more2) xs = stage_issue<NT>(A, lds, T0, tiles, sb + 2);
+        loadw(wa, min(sb + 2, nsb - 1));
+        if (live) super(wb, lds + LY::stage);
+        if (more2) {
+            __builtin_amdgcn_s_waitcnt(0);
+            if (threadIdx.x < LY::kRows) x0[threadIdx.x] = xs;
         }
-        if (more) {
-            __builtin_amdgcn_s_waitcnt(0);  // the copies into stage sb + 1 (and this thread's row scale)
-            if (threadIdx.x < LY::kRows) reinterpret_cast<float *>(nxt_l + LY::X)[threadIdx.x] = xs_next;
-        }
-        __syncthreads();  // stage sb + 1 complete; stage sb read by every wave
+        __syncthreads();
     }
 }
 
@@ -650,8 +701,8 @@ __global__ __launch_bounds__(kBgThreads) __attribute__((amdgpu_waves_per_eu(NT >
     for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) y[t][i] = 0.f;
-    if (S.dtype == kQ6K) bg_main<kQ6K, NT>(A, lds, m0, mrows, live, wrow, y);
-    else bg_main<kQ4K, NT>(A, lds, m0, mrows, live, wrow, y);
+    if (S.dtype == kQ6K) bg_main<kQ6K, NT>(A, lds, m0 / 16, live, wrow, y);
+    else bg_main<kQ4K, NT>(A, lds, m0 / 16, live, wrow, y);
 
     // epilogue: lane (c, g) holds rows 16 t + 4 g + i of channel n0 + c
     if (A.splits > 1) {  // partial sums of this split; bg_reduce_kernel finishes
@@ -798,7 +849,8 @@ int bg_splits(int wgs, int nsb, int nt) {
 }
 
 uint64_t bg_quant_bytes(int rows, int K) {
-    return (uint64_t)rows * K * 2 + (uint64_t)rows * (K / 256) * 32 + (uint64_t)rows * (K / 256) * 4;
+    const uint64_t r16 = (uint64_t)bg_rows16(rows);
+    return r16 * K * 2 + r16 * (K / 256) * 32 + r16 * (K / 256) * 4;
 }
 
 }  // namespace
@@ -868,7 +920,7 @@ static hipError_t bg_launch_prologue(const FusedGemmArgs &a, const BgQuant &q, c
     const int nsb = a.K / 256, W = kPrThreads / 64;
     const bool whole_row = a.norm != nullptr && a.gate == nullptr;
     const int per = whole_row ? (nsb + W - 1) / W : 1;
-    const dim3 grid((unsigned)a.rows, whole_row ? 1u : (unsigned)((nsb + W - 1) / W));
+    const dim3 grid((unsigned)bg_rows16(a.rows), whole_row ? 1u : (unsigned)((nsb + W - 1) / W));  // + padding rows
     switch (per) {
     case 1: bg_prologue_kernel<1><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
     case 2: bg_prologue_kernel<2><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
