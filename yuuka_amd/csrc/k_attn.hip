@@ -505,7 +505,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
     if (key0 > last) return;  // no row sees this chunk; the merge skips it
     const int half = a.rope_dim / 2;
     const int qstride = a.gated ? 2 * kMD : kMD;
-    const uint32_t base = (uint32_t)(uintptr_t)lds;
 
     // ---- cached keys straight into MFMA B order: the scores lane (key kk,
     //      group g4) holds dims [32 ks + 8 g4, +8) of key kk for every ks.
@@ -847,7 +846,6 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
     // keys straight into MFMA B order: the scores lane (key kk, group g4)
     // holds dims [32 ks + 8 g4, +8) of key kk for every ks
     const int kk_s = (wave & 3) * 16 + r16;
-    const bool scorer = 16 * (wave >> 2) < G * min(kQ / G, R);  // a row tile of this wave is in use
     constexpr int kVE = kMD / kAW / 8;                          // 16-byte V pieces per lane
     constexpr int kJ = kMD / kAW / 16;                          // 16-wide output tiles per wave
     const int RB = kQ / G;
@@ -890,19 +888,20 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                 hi[i] = (_Float16)y[i];
                 lo[i] = (_Float16)(y[i] - (float)hi[i]);
             }
-            const uint32_t off = (uint32_t)vec * kMD * 2 + (uint32_t)(((plane >> 1) ^ (vec & 15)) * 16 + (plane & 1) * 8);
+            // [tile][dims / 32][group of 8 dims][row of the tile][8 FP16]
+            const uint32_t off = (uint32_t)(vec >> 4) * 8192 + (uint32_t)(plane >> 3) * 1024 +
+                                 (uint32_t)((plane >> 1) & 3) * 256 + (uint32_t)(vec & 15) * 16 + (uint32_t)(plane & 1) * 8;
             *reinterpret_cast<uint2 *>(lds + LY::Qh + off) = make_uint2(pack_h2(hi[0], hi[1]), pack_h2(hi[2], hi[3]));
             *reinterpret_cast<uint2 *>(lds + LY::Ql + off) = make_uint2(pack_h2(lo[0], lo[1]), pack_h2(lo[2], lo[3]));
         }
     };
 
     // keys (scorer waves) and values (wave w: dims [32w, +32) of key `plane`)
-    // of chunk ci, from clamped positions; keys / values past the verify rows
-    // count as zero where they are used
+    // of chunk ci, from positions clamped to the last verify row: keys past
+    // it are masked out of the scores, and their values get probability 0
     struct KvRegs {
         half8 k[kMD / 32];
         uint4 v[kVE];
-        bool kval, vval;
     };
     // Page-table entries of this lane's key (scores) and value row of chunk
     // ci, then the chunk's loads from them. The entries are requested one
@@ -913,10 +912,15 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
     };
     // PF: the group's page-table entries sit in LDS (loaded once below), so
     // waiting for an entry never waits for the vector loads issued before it
-    const int pg0 = (c_lo * kMK) / a.block_size;
+    // PF (six tiles): the launcher only takes power-of-two page sizes, so
+    // page and slot of a position are a shift and a mask
+    const int bsh = PF ? __builtin_ctz((unsigned)a.block_size) : 0, bsm = a.block_size - 1;
+    auto page_of = [&](int pos) __attribute__((always_inline)) { return PF ? pos >> bsh : pos / a.block_size; };
+    auto slot_in = [&](int pos) __attribute__((always_inline)) { return PF ? pos & bsm : pos % a.block_size; };
+    const int pg0 = page_of(c_lo * kMK);
     if constexpr (PF) {
         int *pt = reinterpret_cast<int *>(lds + LY::PT);
-        const int pg1 = min(c_hi * kMK - 1, last) / a.block_size;
+        const int pg1 = page_of(min(c_hi * kMK - 1, last));
         for (int i = (int)threadIdx.x; i <= pg1 - pg0; i += (int)blockDim.x) pt[i] = table[pg0 + i];
         __syncthreads();
     }
@@ -924,24 +928,22 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
         const int key0 = ci * kMK;
         if constexpr (PF) {
             const int *pt = reinterpret_cast<const int *>(lds + LY::PT);
-            P.k = pt[min(key0 + kk_s, last) / a.block_size - pg0];
-            P.v = pt[min(key0 + lane, last) / a.block_size - pg0];
+            P.k = pt[page_of(min(key0 + kk_s, last)) - pg0];
+            P.v = pt[page_of(min(key0 + lane, last)) - pg0];
             return;
         }
-        P.k = table[min(key0 + kk_s, last) / a.block_size];
-        P.v = table[min(key0 + lane, last) / a.block_size];
+        P.k = table[page_of(min(key0 + kk_s, last))];
+        P.v = table[page_of(min(key0 + lane, last))];
     };
     auto load_kv = [&](KvRegs &X, const Pages &P, int ci) __attribute__((always_inline)) {
         const int key0 = ci * kMK;
         const int p = min(key0 + kk_s, last);
-        X.kval = scorer && key0 + kk_s <= last;
-        const int64_t ks_ = (int64_t)P.k * a.block_size + p % a.block_size;
+        const int64_t ks_ = (int64_t)P.k * a.block_size + slot_in(p);
         const half8 *ksrc = reinterpret_cast<const half8 *>(kpool + ks_ * a.kv_dim + (int64_t)kvh * kMD + g4 * 8);
 #pragma unroll
         for (int ks = 0; ks < kMD / 32; ks++) X.k[ks] = ksrc[4 * ks];
         const int vp = min(key0 + lane, last);
-        X.vval = key0 + lane <= last;
-        const int64_t vs_ = (int64_t)P.v * a.block_size + vp % a.block_size;
+        const int64_t vs_ = (int64_t)P.v * a.block_size + slot_in(vp);
         const uint4 *vsrc =
             reinterpret_cast<const uint4 *>(vpool + vs_ * a.kv_dim + (int64_t)kvh * kMD + wave * (kMD / kAW));
 #pragma unroll
@@ -956,6 +958,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
         if (threadIdx.x < kQ) {
             Mrow[threadIdx.x] = -INFINITY;
             Lrow[threadIdx.x] = 0.0f;
+            Arow[threadIdx.x] = 1.0f;  // rows past the block's own keep their (unused) accumulators
         }
         f32x4 o[kJ][NT];
 #pragma unroll
@@ -976,7 +979,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                 uint16_t *vt = reinterpret_cast<uint16_t *>(lds + LY::Vt);
 #pragma unroll
                 for (int e = 0; e < kVE; e++) {
-                    const uint4 vv = X.vval ? X.v[e] : make_uint4(0, 0, 0, 0);
+                    const uint4 vv = X.v[e];  // past the last key: the last key's (finite, probability 0)
                     const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
                     for (int i = 0; i < 8; i++)
@@ -988,23 +991,34 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
 #pragma unroll
             for (int rt = 0; rt < NT; rt++) {
                 if (rt % 2 != (wave >> 2) || rt >= ntl) continue;
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+                // A operands at lane base + immediates; two accumulators so
+                // that consecutive MFMAs do not wait for each other
+                const uint8_t *qa = lds + LY::Qh + (uint32_t)rt * 8192 + (uint32_t)lg4 * 256 + (uint32_t)lr16 * 16;
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < kMD / 32; ks++) {
-                    const int blk = ks * 4 + lg4;
-                    const uint32_t qo = (uint32_t)(rt * 16 + lr16) * kMD * 2 + (uint32_t)((blk ^ lr16) * 16);
-                    const half8 ah = *reinterpret_cast<const half8 *>(lds + LY::Qh + qo);
-                    const half8 al = *reinterpret_cast<const half8 *>(lds + LY::Ql + qo);
-                    const half8 kb = X.kval ? X.k[ks] : half8{};
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, kb, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, kb, acc, 0, 0, 0);
+                    const half8 ah = *reinterpret_cast<const half8 *>(qa + ks * 1024);
+                    const half8 al = *reinterpret_cast<const half8 *>(qa + (LY::Ql - LY::Qh) + ks * 1024);
+                    // keys past the last are the last key again (clamped loads):
+                    // finite, and masked below
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, X.k[ks], acc, 0, 0, 0);
+                    acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, X.k[ks], acc2, 0, 0, 0);
                 }
+                acc += acc2;
                 float *S = reinterpret_cast<float *>(lds + LY::S);
                 const int p = key0 + lkk;
+                if (key0 + kMK - 1 <= p0 + r0) {  // every key precedes every row of the block
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int qi = rt * 16 + lg4 * 4 + e;
-                    if (qi < nq) S[qi * kMK + lkk] = p <= p0 + r0 + qi % Rb ? acc[e] * a.scale : -INFINITY;
+                    for (int e = 0; e < 4; e++) {
+                        const int qi = rt * 16 + lg4 * 4 + e;
+                        if (qi < nq) S[qi * kMK + lkk] = acc[e] * a.scale;
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int qi = rt * 16 + lg4 * 4 + e;
+                        if (qi < nq) S[qi * kMK + lkk] = p <= p0 + r0 + qi % Rb ? acc[e] * a.scale : -INFINITY;
+                    }
                 }
             }
             lds_only_barrier();
@@ -1066,14 +1080,17 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
             // ---- value product: wave w owns dims [32w, 32w + 32); the running
             //      accumulators are rescaled by this chunk's alpha first
 #pragma unroll
-            for (int rt = 0; rt < NT; rt++)
+            for (int rt = 0; rt < NT; rt++) {
+                if (rt >= ntl) continue;
+                const float4 al = *reinterpret_cast<const float4 *>(Arow + rt * 16 + lg4 * 4);
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int qi = rt * 16 + lg4 * 4 + e;
-                    const float al = qi < nq ? Arow[qi] : 1.0f;
-#pragma unroll
-                    for (int j = 0; j < kJ; j++) o[j][rt][e] *= al;
+                for (int j = 0; j < kJ; j++) {
+                    o[j][rt][0] *= al.x;
+                    o[j][rt][1] *= al.y;
+                    o[j][rt][2] *= al.z;
+                    o[j][rt][3] *= al.w;
                 }
+            }
             // this wave's V operands for both key halves, then one row tile
             // at a time (its probabilities, 2 x kJ x 2 MFMAs)
             half8 vb[kMK / 32][kJ];
@@ -1290,7 +1307,8 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
     // Blocks of more than 32 MFMA rows (G x rows) take the six-tile grouped
     // kernel: one workgroup per CU, so its groups are sized for about one
     // round of workgroups over the CUs.
-    const bool wide = mfma && (a.heads / a.kv_heads) * a.rows > 32;
+    const bool wide = mfma && (a.heads / a.kv_heads) * a.rows > 32 && a.block_size > 0 &&
+                      (a.block_size & (a.block_size - 1)) == 0;
     int cpw = 1;
     if (mfma) {
         const int c1 = (a.capacity + kMK - 1) / kMK;
