@@ -847,6 +847,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
     // holds dims [32 ks + 8 g4, +8) of key kk for every ks
     const int kk_s = (wave & 3) * 16 + r16;
     constexpr int kVE = kMD / kAW / 8;                          // 16-byte V pieces per lane
+    static_assert(kVE == 4, "four value pieces per lane: two keys x two 8-dim blocks");
     constexpr int kJ = kMD / kAW / 16;                          // 16-wide output tiles per wave
     const int RB = kQ / G;
     // ---- query rows of one block: normalised, rotated, split into F16 high +
@@ -908,7 +909,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
     // chunk ahead of the loads that use them: waiting for them then also
     // waits only for loads that are due anyway.
     struct Pages {
-        int32_t k, v;
+        int32_t k, v0, v1;
     };
     // PF: the group's page-table entries sit in LDS (loaded once below), so
     // waiting for an entry never waits for the vector loads issued before it
@@ -929,11 +930,13 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
         if constexpr (PF) {
             const int *pt = reinterpret_cast<const int *>(lds + LY::PT);
             P.k = pt[page_of(min(key0 + kk_s, last)) - pg0];
-            P.v = pt[page_of(min(key0 + lane, last)) - pg0];
+            P.v0 = pt[page_of(min(key0 + (lane & 31), last)) - pg0];
+            P.v1 = pt[page_of(min(key0 + 32 + (lane & 31), last)) - pg0];
             return;
         }
         P.k = table[page_of(min(key0 + kk_s, last))];
-        P.v = table[page_of(min(key0 + lane, last))];
+        P.v0 = table[page_of(min(key0 + (lane & 31), last))];
+        P.v1 = table[page_of(min(key0 + 32 + (lane & 31), last))];
     };
     auto load_kv = [&](KvRegs &X, const Pages &P, int ci) __attribute__((always_inline)) {
         const int key0 = ci * kMK;
@@ -942,12 +945,17 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
         const half8 *ksrc = reinterpret_cast<const half8 *>(kpool + ks_ * a.kv_dim + (int64_t)kvh * kMD + g4 * 8);
 #pragma unroll
         for (int ks = 0; ks < kMD / 32; ks++) X.k[ks] = ksrc[4 * ks];
-        const int vp = min(key0 + lane, last);
-        const int64_t vs_ = (int64_t)P.v * a.block_size + slot_in(vp);
-        const uint4 *vsrc =
-            reinterpret_cast<const uint4 *>(vpool + vs_ * a.kv_dim + (int64_t)kvh * kMD + wave * (kMD / kAW));
-#pragma unroll
-        for (int e = 0; e < kVE; e++) X.v[e] = vsrc[e];
+        // values: piece e of the lane is key 32 (e & 1) + lane % 32, dims
+        // [32 wave + 8 b, +8) with b = 2 (e >> 1) + lane / 32 — 32 keys x 32
+        // bytes per load instruction
+        const int vp0 = min(key0 + (lane & 31), last), vp1 = min(key0 + 32 + (lane & 31), last);
+        const int64_t vcol = (int64_t)kvh * kMD + wave * (kMD / kAW) + (lane >> 5) * 8;
+        const uint4 *v0 = reinterpret_cast<const uint4 *>(vpool + ((int64_t)P.v0 * a.block_size + slot_in(vp0)) * a.kv_dim + vcol);
+        const uint4 *v1 = reinterpret_cast<const uint4 *>(vpool + ((int64_t)P.v1 * a.block_size + slot_in(vp1)) * a.kv_dim + vcol);
+        X.v[0] = v0[0];
+        X.v[1] = v1[0];
+        X.v[2] = v0[2];
+        X.v[3] = v1[2];
     };
 
     for (int r0 = 0; r0 < R; r0 += RB) {
@@ -981,9 +989,10 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                 for (int e = 0; e < kVE; e++) {
                     const uint4 vv = X.v[e];  // past the last key: the last key's (finite, probability 0)
                     const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
+                    const int key = (e & 1) * 32 + (llane & 31), d0 = wave * (kMD / kAW) + (2 * (e >> 1) + (llane >> 5)) * 8;
+                    // lanes 32..63 write 8 dims further: 32 banks away (kVt = 72)
 #pragma unroll
-                    for (int i = 0; i < 8; i++)
-                        vt[(wave * (kMD / kAW) + e * 8 + i) * kVt + llane] = (uint16_t)(w4[i >> 1] >> (16 * (i & 1)));
+                    for (int i = 0; i < 8; i++) vt[(d0 + i) * kVt + key] = (uint16_t)(w4[i >> 1] >> (16 * (i & 1)));
                 }
             }
             // ---- scores: wave w owns keys [16 (w & 3), +16) of row tiles
