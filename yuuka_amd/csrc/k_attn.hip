@@ -996,10 +996,12 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                 }
             }
             // ---- scores: wave w owns keys [16 (w & 3), +16) of row tiles
-            //      w >> 2, (w >> 2) + 2, ...
-#pragma unroll
-            for (int rt = 0; rt < NT; rt++) {
-                if (rt % 2 != (wave >> 2) || rt >= ntl) continue;
+            //      w >> 2, (w >> 2) + 2, ... Every row of a tile is stored (rows
+            //      past the block's own are never read); the causal mask is the
+            //      softmax's. With every tile in use (one block of rows, the
+            //      usual case) the tiles run without a branch between them, so
+            //      their LDS reads can be issued ahead of the MFMAs.
+            auto score_tile = [&](int rt) __attribute__((always_inline)) {
                 // A operands at lane base + immediates; two accumulators so
                 // that consecutive MFMAs do not wait for each other
                 const uint8_t *qa = lds + LY::Qh + (uint32_t)rt * 8192 + (uint32_t)lg4 * 256 + (uint32_t)lr16 * 16;
@@ -1009,26 +1011,28 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                     const half8 ah = *reinterpret_cast<const half8 *>(qa + ks * 1024);
                     const half8 al = *reinterpret_cast<const half8 *>(qa + (LY::Ql - LY::Qh) + ks * 1024);
                     // keys past the last are the last key again (clamped loads):
-                    // finite, and masked below
+                    // finite, and masked by the softmax
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, X.k[ks], acc, 0, 0, 0);
                     acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, X.k[ks], acc2, 0, 0, 0);
                 }
                 acc += acc2;
-                float *S = reinterpret_cast<float *>(lds + LY::S);
-                const int p = key0 + lkk;
-                if (key0 + kMK - 1 <= p0 + r0) {  // every key precedes every row of the block
+                float *S = reinterpret_cast<float *>(lds + LY::S) + (rt * 16 + lg4 * 4) * kMK + lkk;
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int qi = rt * 16 + lg4 * 4 + e;
-                        if (qi < nq) S[qi * kMK + lkk] = acc[e] * a.scale;
-                    }
+                for (int e = 0; e < 4; e++) S[e * kMK] = acc[e] * a.scale;
+            };
+            const bool odd = (wave >> 2) != 0;
+            if (ntl == NT) {
+                if (odd) {
+#pragma unroll
+                    for (int rt = 1; rt < NT; rt += 2) score_tile(rt);
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int qi = rt * 16 + lg4 * 4 + e;
-                        if (qi < nq) S[qi * kMK + lkk] = p <= p0 + r0 + qi % Rb ? acc[e] * a.scale : -INFINITY;
-                    }
+                    for (int rt = 0; rt < NT; rt += 2) score_tile(rt);
                 }
+            } else {
+#pragma unroll
+                for (int rt = 0; rt < NT; rt++)
+                    if (rt % 2 == (int)odd && rt < ntl) score_tile(rt);
             }
             lds_only_barrier();
             // ---- online softmax: four query rows per wave at a time, one
@@ -1043,7 +1047,13 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                     const bool live = qi < nq;
                     const int qc = live ? qi : q0;
                     const float4 sv = *reinterpret_cast<const float4 *>(S + qc * kMK + 4 * s16);
-                    const float sc[4] = {sv.x, sv.y, sv.z, sv.w};
+                    float sc[4] = {sv.x, sv.y, sv.z, sv.w};
+                    if (key0 + kMK - 1 > p0 + r0) {  // the chunk reaches the block's rows: causal mask
+                        const int rowpos = p0 + r0 + qc % Rb;
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            if (key0 + 4 * s16 + i > rowpos) sc[i] = -INFINITY;
+                    }
                     float mc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
                     mc = fmaxf(mc, dpp_f<0xb1>(mc));
                     mc = fmaxf(mc, dpp_f<0x4e>(mc));
@@ -1086,22 +1096,11 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                 }
             }
             lds_only_barrier();
-            // ---- value product: wave w owns dims [32w, 32w + 32); the running
-            //      accumulators are rescaled by this chunk's alpha first
-#pragma unroll
-            for (int rt = 0; rt < NT; rt++) {
-                if (rt >= ntl) continue;
-                const float4 al = *reinterpret_cast<const float4 *>(Arow + rt * 16 + lg4 * 4);
-#pragma unroll
-                for (int j = 0; j < kJ; j++) {
-                    o[j][rt][0] *= al.x;
-                    o[j][rt][1] *= al.y;
-                    o[j][rt][2] *= al.z;
-                    o[j][rt][3] *= al.w;
-                }
-            }
-            // this wave's V operands for both key halves, then one row tile
-            // at a time (its probabilities, 2 x kJ x 2 MFMAs)
+            // ---- value product: wave w owns dims [32w, 32w + 32). This
+            //      wave's V operands for both key halves, then one row tile at
+            //      a time: its accumulators rescaled by this chunk's alpha, then
+            //      its probabilities (2 x kJ x 2 MFMAs). Without a branch between
+            //      the tiles when every tile is in use.
             half8 vb[kMK / 32][kJ];
 #pragma unroll
             for (int ks = 0; ks < kMK / 32; ks++)
@@ -1111,9 +1110,15 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                     vb[ks][j] = *reinterpret_cast<const half8 *>(lds + LY::Vt + (uint32_t)dcol * kVt * 2 +
                                                                  (uint32_t)(ks * 32 + lg4 * 8) * 2);
                 }
+            auto pv_tile = [&](int rt) __attribute__((always_inline)) {
+                const float4 al = *reinterpret_cast<const float4 *>(Arow + rt * 16 + lg4 * 4);
 #pragma unroll
-            for (int rt = 0; rt < NT; rt++) {
-                if (rt >= ntl) continue;
+                for (int j = 0; j < kJ; j++) {
+                    o[j][rt][0] *= al.x;
+                    o[j][rt][1] *= al.y;
+                    o[j][rt][2] *= al.z;
+                    o[j][rt][3] *= al.w;
+                }
 #pragma unroll
                 for (int ks = 0; ks < kMK / 32; ks++) {
                     const int blk = ks * 4 + lg4;
@@ -1126,6 +1131,14 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                         o[j][rt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, vb[ks][j], o[j][rt], 0, 0, 0);
                     }
                 }
+            };
+            if (ntl == NT) {
+#pragma unroll
+                for (int rt = 0; rt < NT; rt++) pv_tile(rt);
+            } else {
+#pragma unroll
+                for (int rt = 0; rt < NT; rt++)
+                    if (rt < ntl) pv_tile(rt);
             }
         };
         if constexpr (PF) {
@@ -1347,6 +1360,10 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_mfma_group_kernel<2, false>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_mfma_group_kernel<3, true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_mfma_group_kernel<5, true>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(attn_verify_mfma_group_kernel<6, true>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
             attr2 = true;
@@ -1356,10 +1373,22 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
             attn_verify_mfma_kernel<<<grid, 64 * kAW, kMfmaLds, s>>>(q, k, v, static_cast<uint16_t *>(kpool),
                                                                       static_cast<uint16_t *>(vpool), table, q_norm,
                                                                       k_norm, rope, a, part, dyn);
-        else if (wide)
-            attn_verify_mfma_group_kernel<6, true><<<grid, 64 * kAW, GroupLds<6>::total, s>>>(
-                q, k, v, static_cast<uint16_t *>(kpool), static_cast<uint16_t *>(vpool), table, q_norm, k_norm, rope,
-                a, part, dyn, cpw);
+        else if (wide) {
+            // row tiles: the launch's MFMA rows in one block where they fit
+            const int nq = (a.heads / a.kv_heads) * a.rows;
+            if (nq <= 48)
+                attn_verify_mfma_group_kernel<3, true><<<grid, 64 * kAW, GroupLds<3>::total, s>>>(
+                    q, k, v, static_cast<uint16_t *>(kpool), static_cast<uint16_t *>(vpool), table, q_norm, k_norm,
+                    rope, a, part, dyn, cpw);
+            else if (nq <= 80)
+                attn_verify_mfma_group_kernel<5, true><<<grid, 64 * kAW, GroupLds<5>::total, s>>>(
+                    q, k, v, static_cast<uint16_t *>(kpool), static_cast<uint16_t *>(vpool), table, q_norm, k_norm,
+                    rope, a, part, dyn, cpw);
+            else
+                attn_verify_mfma_group_kernel<6, true><<<grid, 64 * kAW, GroupLds<6>::total, s>>>(
+                    q, k, v, static_cast<uint16_t *>(kpool), static_cast<uint16_t *>(vpool), table, q_norm, k_norm,
+                    rope, a, part, dyn, cpw);
+        }
         else
             attn_verify_mfma_group_kernel<2, false><<<grid, 64 * kAW, kMfmaLds, s>>>(
                 q, k, v, static_cast<uint16_t *>(kpool), static_cast<uint16_t *>(vpool), table, q_norm, k_norm, rope,
