@@ -324,7 +324,7 @@ def test_config4_16k_context_chunk_groupings_agree(dev, monkeypatch):
 def test_config3_rows_long_context_grouped_attention(dev, monkeypatch):
     """Config 3's attention geometry at real context lengths: 16 Q / 4 KV
     heads of 256, 9 verify rows per request (36 MFMA rows per KV head, the
-    six-tile grouped kernel attn_verify_mfma_group_kernel<6, true>), three
+    three-tile grouped kernel attn_verify_mfma_group_kernel<3, true>), three
     requests at ~450-700 tokens of context, the key chunks walked in groups
     of 3 and of 5 per workgroup with the running softmax, and the one-chunk
     kernel; each against the oracle decoder on every request (observed
@@ -362,3 +362,35 @@ def test_config3_rows_long_context_grouped_attention(dev, monkeypatch):
     # rms (the same spread all three show against the oracle)
     _close(out["3"], out["1"], "cpw 3 vs 1", tol=5e-3)
     _close(out["5"], out["1"], "cpw 5 vs 1", tol=5e-3)
+
+
+def test_many_rows_long_context_grouped_attention_two_row_blocks(dev, monkeypatch):
+    """25 verify rows per request at 16 Q / 4 KV heads: 100 MFMA rows per KV
+    head, more than the six-tile grouped kernel
+    (attn_verify_mfma_group_kernel<6, true>) holds, so it walks the key
+    chunks twice, for a block of 24 rows (every tile in use) and a block of
+    one row (one tile of six in use). Two requests at ~400-500 tokens, chunk
+    groups of 3 and the one-chunk kernel, each against the oracle decoder."""
+    cfg = replace(Mdl.QWEN35_4B_LIKE, hidden=256, ffn=512, n_layers=1, full_interval=1, vocab=1024, batch=2,
+                  max_rows=25, capacity=640)
+    w = Mdl.make_weights(cfg, seed=91)
+    rng = np.random.default_rng(92)
+    prompts = [rng.integers(0, cfg.vocab, n).astype(np.int32) for n in (517, 388)]
+    toks = rng.integers(0, cfg.vocab, (2, 25)).astype(np.int32)
+    want = []
+    for r in range(2):
+        o = O.Q35(replace(cfg, batch=1), w)
+        o.forward(prompts[r][:-1])
+        toks[r, 0] = prompts[r][-1]
+        want.append(o.forward(toks[r], all_logits=True))
+        o.close()
+    for cpw in ("3", "1"):
+        monkeypatch.setenv("YUUKA_ATTN_CPW", cpw)
+        eng = Mdl.Engine(dev, cfg, w)
+        for r in range(2):
+            eng.prefill_request(r, prompts[r][:-1])
+        eng.step_batch(toks, 0, accept=Mdl.accept_struct(), forced=np.zeros(2, np.int32))
+        got = eng.logits(2 * 25).reshape(2, 25, -1)
+        eng.close()
+        for r in range(2):
+            _close(got[r], want[r], f"cpw {cpw} request {r}")
