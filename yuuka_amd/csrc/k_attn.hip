@@ -974,7 +974,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
 #pragma unroll
             for (int rt = 0; rt < NT; rt++) o[j][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
         // one chunk of the group from the registers X
-        auto chunk = [&](const KvRegs &X, int ci) __attribute__((always_inline)) {
+        auto chunk = [&](const KvRegs &X, int ci, auto &&mid) __attribute__((always_inline)) {
             const int key0 = ci * kMK;
             // Lane constants re-derived per chunk from an opaque zero: hoisted
             // out of the chunk loop, the per-tile offsets they feed would be
@@ -1035,6 +1035,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
                     if (rt % 2 == (int)odd && rt < ntl) score_tile(rt);
             }
             lds_only_barrier();
+            mid();  // the next chunk's loads, issued while the waves are spread over the chunk
             // ---- online softmax: four query rows per wave at a time, one
             //      16-lane DPP row per query row, lane s holding keys
             //      [4 s, 4 s + 4) (the row's reductions never leave the DPP
@@ -1144,6 +1145,10 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
         if constexpr (PF) {
             // two register sets: chunk ci + 1 loads while chunk ci is computed,
             // and the page entries of chunk ci + 2 are requested meanwhile.
+            // The loads go out after chunk ci's scores, when the waves are
+            // spread over the chunk (issued together at the chunk's start,
+            // the eight waves' loads queue behind each other: config 3 100
+            // -> 91 us per layer).
             // Every load is issued unconditionally (indices clamped to the last
             // chunk): under a branch the compiler's wait counts merge
             // conservatively and the current chunk would wait for the next
@@ -1154,13 +1159,15 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
             load_kv(XA, PA, c_lo);
             fetch_pages(PB, min(c_lo + 1, c_hi - 1));
             for (int ci = c_lo; ci < c_hi; ci += 2) {
-                load_kv(XB, PB, min(ci + 1, c_hi - 1));
-                fetch_pages(PA, min(ci + 2, c_hi - 1));
-                chunk(XA, ci);
+                chunk(XA, ci, [&]() __attribute__((always_inline)) {
+                    load_kv(XB, PB, min(ci + 1, c_hi - 1));
+                    fetch_pages(PA, min(ci + 2, c_hi - 1));
+                });
                 if (ci + 1 >= c_hi) break;
-                load_kv(XA, PA, min(ci + 2, c_hi - 1));
-                fetch_pages(PB, min(ci + 3, c_hi - 1));
-                chunk(XB, ci + 1);
+                chunk(XB, ci + 1, [&]() __attribute__((always_inline)) {
+                    load_kv(XA, PA, min(ci + 2, c_hi - 1));
+                    fetch_pages(PB, min(ci + 3, c_hi - 1));
+                });
             }
         } else {
             KvRegs X;
@@ -1168,7 +1175,7 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2
             for (int ci = c_lo; ci < c_hi; ci++) {
                 fetch_pages(P, ci);
                 load_kv(X, P, ci);
-                chunk(X, ci);
+                chunk(X, ci, []() {});
             }
         }
         // ---- this block's partial records: o, and (m, l) of every row
