@@ -766,8 +766,8 @@ __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(4))) v
 // LDS layout of the grouped kernel with NT 16-row query tiles: the
 // transposed V chunk, the query tiles (F16 high, remainder), the scores /
 // probabilities and the running (max, sum, rescale) of every query row.
-// Page-table entries of a group's keys held in LDS by the six-tile kernel
-// (its launcher caps the group so that they fit).
+// Page-table entries of a group's keys held in LDS by the PF kernels
+// (three to six tiles; the launcher caps the group so that they fit).
 constexpr int kPtCap = 256;
 template <int NT> struct GroupLds {
     static constexpr int kQ = 16 * NT;
@@ -781,6 +781,7 @@ template <int NT> struct GroupLds {
 };
 static_assert(GroupLds<2>::total == kMfmaLds, "two-tile layout");
 static_assert(GroupLds<6>::total <= 160 * 1024, "six-tile layout fits LDS");
+static_assert(GroupLds<5>::total <= 160 * 1024 && GroupLds<3>::total <= 160 * 1024, "PF layouts fit LDS");
 
 // One workgroup per (group of `cpw` 64-key chunks, KV head, request). The
 // verify rows' own keys and values in the group's range go to the pool
@@ -789,11 +790,12 @@ static_assert(GroupLds<6>::total <= 160 * 1024, "six-tile layout fits LDS");
 // rescale of the P.V accumulators in registers). One partial record
 // (o, m, l) per (group, row, head) for the merge.
 // NT = 2: 76 KB of LDS and at most 128 VGPRs, two workgroups per CU.
-// NT = 6: up to 96 MFMA rows in one block (all 68 rows of 4 heads x 17 verify
-// rows, so each chunk is read once per step), 157 KB of LDS and one
-// workgroup per CU; with the register budget of two waves per SIMD the next
-// chunk's keys and values load into a second register set while the current
-// chunk is computed (PF).
+// NT = 3, 5, 6 (PF): 48, 80 or 96 MFMA rows in one block (config 3's 36
+// rows of 4 heads x 9 verify rows, config 4's 68 of 4 x 17, so each chunk
+// is read once per step), 99 / 137 / 157 KB of LDS and one workgroup per
+// CU; with the register budget of two waves per SIMD the next chunk's keys
+// and values load into a second register set while the current chunk is
+// computed.
 template <int NT, bool PF>
 __global__ __launch_bounds__(64 * kAW) __attribute__((amdgpu_waves_per_eu(NT > 2 ? 2 : 4))) void attn_verify_mfma_group_kernel(
     const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v, uint16_t *kpool,
@@ -1333,9 +1335,9 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
     // MFMA kernel: groups of cpw chunks per workgroup once a launch has more
     // than ~1024 chunk workgroups (fewer partial records, query preparation
     // amortized); short contexts keep one chunk per workgroup
-    // Blocks of more than 32 MFMA rows (G x rows) take the six-tile grouped
-    // kernel: one workgroup per CU, so its groups are sized for about one
-    // round of workgroups over the CUs.
+    // Blocks of more than 32 MFMA rows (G x rows) take the PF grouped kernel
+    // (3, 5 or 6 row tiles): one workgroup per CU, so its groups are sized
+    // for about one round of workgroups over the CUs.
     const bool wide = mfma && (a.heads / a.kv_heads) * a.rows > 32 && a.block_size > 0 &&
                       (a.block_size & (a.block_size - 1)) == 0;
     int cpw = 1;
@@ -1353,7 +1355,7 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
             const int v = atoi(e);
             if (v >= 1 && v <= 32) cpw = v;
         }
-        // the six-tile kernel keeps the group's page entries in LDS
+        // the PF kernels keep the group's page entries in LDS
         if (wide) cpw = std::max(1, std::min(cpw, (kPtCap - 2) * std::max(1, a.block_size) / kMK));
     }
     const int ck = mfma ? kMK * cpw : attn_verify_chunk(a.fmt);
