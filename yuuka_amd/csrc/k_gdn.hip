@@ -662,28 +662,31 @@ __device__ __forceinline__ void gdn_commit_cols_body(float *__restrict__ conv_st
     }
     // the accepted rows' k, v (this block's columns), decay and beta, staged
     // once so that the serial row loop reads LDS only
-    __shared__ float sk_rows[kMaxRows][kS], sv_rows[kMaxRows][kCols], scf[2][kMaxRows];
+    // (dynamic LDS sized for the launch's rows: gdn_commit_lds_bytes)
+    extern __shared__ float commit_rows[];
+    const int R = g.rows;
+    float *sk_rows = commit_rows, *sv_rows = sk_rows + R * kS, *scf = sv_rows + R * kCols;  // [R][kS], [R][kCols], [2][R]
     for (int idx = t; idx < n * (kS + kCols); idx += kColThreads) {
         const int r = idx / (kS + kCols), c = idx - r * (kS + kCols);
         const float *row = conv + (uint64_t)r * g.conv_dim;
-        if (c < kS) sk_rows[r][c] = row[key_dim + kh * kS + c];
-        else sv_rows[r][c - kS] = row[2 * key_dim + h * kS + cb * kCols + (c - kS)];
+        if (c < kS) sk_rows[r * kS + c] = row[key_dim + kh * kS + c];
+        else sv_rows[r * kCols + c - kS] = row[2 * key_dim + h * kS + cb * kCols + (c - kS)];
     }
     if (t < n) {
-        scf[0][t] = gdn_decay(g, alpha_raw, dt, a_log, t, h);
-        scf[1][t] = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
+        scf[t] = gdn_decay(g, alpha_raw, dt, a_log, t, h);
+        scf[R + t] = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
     }
     __syncthreads();
     float s_reg[16];
 #pragma unroll
     for (int ii = 0; ii < 16; ii++) s_reg[ii] = tile[p * 16 + ii][j - cb * kCols];
     for (int r = 0; r < n; r++) {
-        const float *k = sk_rows[r];
-        const float decay = scf[0][r], beta = scf[1][r];
+        const float *k = sk_rows + r * kS;
+        const float decay = scf[r], beta = scf[R + r];
         float kr[16];
 #pragma unroll
         for (int ii = 0; ii < 16; ii++) kr[ii] = k[p * 16 + ii];
-        const float vj = sv_rows[r][j - cb * kCols];
+        const float vj = sv_rows[r * kCols + j - cb * kCols];
         float sk = 0.0f;
 #pragma unroll
         for (int ii = 0; ii < 16; ii++) {
@@ -780,19 +783,26 @@ hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, c
     return hipGetLastError();
 }
 
+// The commit's staged rows: k [rows][128], this block's v [rows][32], decay
+// and beta [2][rows] (the state tile is static LDS). Sized by the launch's
+// rows, so that more workgroups share a CU at few rows.
+static uint32_t gdn_commit_lds_bytes(const GdnArgs &g) { return (uint32_t)(g.rows * (kS + kCols) + 2 * g.rows) * 4; }
+
 hipError_t launch_gdn_commit_cols(float *conv_state, float *state, const float *qkv, const float *conv,
                                   const float *alpha_raw, const float *beta_raw, const float *dt, const float *a_log,
                                   const GdnArgs &g, const int32_t *accept_result, hipStream_t s) {
-    gdn_commit_cols_kernel<<<dim3((unsigned)g.rank, kS / kCols, (unsigned)(g.nreq > 0 ? g.nreq : 1)), kColThreads, 0, s>>>(
+    if (g.rows < 1 || g.rows > kMaxRows) return hipErrorInvalidValue;
+    gdn_commit_cols_kernel<<<dim3((unsigned)g.rank, kS / kCols, (unsigned)(g.nreq > 0 ? g.nreq : 1)), kColThreads,
+                             gdn_commit_lds_bytes(g), s>>>(
         conv_state, state, qkv, conv, alpha_raw, beta_raw, dt, a_log, g, accept_result);
     return hipGetLastError();
 }
 
 hipError_t launch_gdn_commit_cols_multi(const GdnCommitSet &set, int layers, const GdnArgs &g,
                                         const int32_t *accept_result, hipStream_t s) {
-    if (layers < 1 || layers > kGdnCommitMaxLayers) return hipErrorInvalidValue;
+    if (layers < 1 || layers > kGdnCommitMaxLayers || g.rows < 1 || g.rows > kMaxRows) return hipErrorInvalidValue;
     gdn_commit_cols_multi_kernel<<<dim3((unsigned)g.rank, kS / kCols, (unsigned)(layers * (g.nreq > 0 ? g.nreq : 1))),
-                                   kColThreads, 0, s>>>(
+                                   kColThreads, gdn_commit_lds_bytes(g), s>>>(
         set, g, accept_result);
     return hipGetLastError();
 }
