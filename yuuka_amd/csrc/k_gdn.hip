@@ -388,7 +388,7 @@ __device__ __forceinline__ void conv_channels4(const float *conv_state, const fl
     float w[N][4], st[N][3], x[N][RC];
 #pragma unroll
     for (int u = 0; u < N; u++) {
-        const int c = cc[u] < 0 ? cc[0] : cc[u];
+        const int c = cc[u] < 0 ? 0 : cc[u];  // no channel: loads of channel 0, not used
 #pragma unroll
         for (int i = 0; i < 4; i++) w[u][i] = conv_w[(uint64_t)c * 4 + i];
 #pragma unroll
@@ -471,14 +471,14 @@ __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
     // of this block's COLS v channels (threads 0 .. COLS - 1, loaded with
     // their first q/k channel)
     if (g.kernel == 4) {
-        constexpr int NQ = 2 * kS / kThr, N = NQ + 1;
+        constexpr int NQ = (2 * kS + kThr - 1) / kThr, N = NQ + 1;
         int cc[N], stride[N];
         float *dst[N];
 #pragma unroll
         for (int u = 0; u < NQ; u++) {
             const int ch = u * kThr + t, which = ch >> 7, c = ch & (kS - 1);
-            cc[u] = (which == 0 ? 0 : key_dim) + kh * kS + c;
-            dst[u] = qk + which * kS + c;
+            cc[u] = ch < 2 * kS ? (which == 0 ? 0 : key_dim) + kh * kS + c : -1;
+            dst[u] = qk + (which & 1) * kS + c;
             stride[u] = 2 * kS;
         }
         cc[NQ] = t < COLS ? 2 * key_dim + h * kS + cb * COLS + t : -1;
@@ -489,6 +489,7 @@ __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
 #pragma unroll
         for (int base = 0; base < 2 * kS; base += kThr) {
             const int ch = base + t, which = ch >> 7, cc = ch & (kS - 1);
+            if (ch >= 2 * kS) break;  // wider blocks: threads past the q / k channels (none of them owns a v channel)
             const int c0 = (which == 0 ? 0 : key_dim) + kh * kS + cc;
             const int c1 = base == 0 && t < COLS ? 2 * key_dim + h * kS + cb * COLS + t : -1;
             conv_channel2<RC>(conv_state, qkv, conv_w, g, c0, qk + which * kS + cc, 2 * kS, c1, vv + t, COLS);
@@ -744,23 +745,40 @@ __global__ __launch_bounds__(kColThreads) void gdn_commit_cols_multi_kernel(cons
 
 }  // namespace
 
-// Columns of the state per verify workgroup. Measured per launch with 16
-// heads of 128-wide state, 16 / 32 columns: one request of 5 rows 6.97 /
-// 6.82 us; sixteen requests of 9 rows 34.5 / 19.3 us; four requests of 17
-// rows 33.1 / 18.4 us. Wider blocks share the q / k conv and norm over more
-// columns, which outweighs the smaller grid even at one request.
-constexpr int kVerifyCols = 32;
-
-uint32_t gdn_verify_cols_lds_bytes(const GdnArgs &g) {
-    return (uint32_t)(g.rows * 2 * kS + g.rows * kVerifyCols + 2 * g.rows) * 4;
+// Columns of the state per verify workgroup: the widest of 128 / 64 / 32
+// that still gives every CU a workgroup (heads x 128 / COLS x requests >=
+// CUs), else 32. Wider blocks share the head's q / k conv and norm over more
+// columns; narrower ones spread a small launch over more CUs. Measured per
+// launch (16 heads of 128-wide state, 32 / 64 / 128 columns): sixteen
+// requests of 9 rows 18.6 / 17.5 / 16.7 us; four requests of 17 rows 19.4 /
+// 21.9 / 35.3 us; one request of 5 rows 8.0 / 9.1 / 11.9 us (and 16 columns
+// 6.97 against 6.82 us for 32).
+static int verify_cols(const GdnArgs &g) {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    const int64_t per = (int64_t)g.rank * (g.nreq > 0 ? g.nreq : 1);  // workgroups per column block
+    if (per * 1 >= cus) return 128;
+    if (per * 2 >= cus) return 64;
+    return 32;
 }
+
+static uint32_t verify_cols_lds(const GdnArgs &g, int cols) {
+    return (uint32_t)(g.rows * 2 * kS + g.rows * cols + 2 * g.rows) * 4;
+}
+
+uint32_t gdn_verify_cols_lds_bytes(const GdnArgs &g) { return verify_cols_lds(g, verify_cols(g)); }
 
 template <int COLS>
 static void launch_verify_cols(const float *conv_state, const float *state, const float *qkv, const float *alpha_raw,
                                const float *beta_raw, const float *conv_w, const float *dt, const float *a_log,
                                float *raw_out, float *conv_out, const GdnArgs &g, hipStream_t s) {
     const dim3 grid((unsigned)g.rank, kS / COLS, (unsigned)(g.nreq > 0 ? g.nreq : 1));
-    const uint32_t lds = gdn_verify_cols_lds_bytes(g);
+    const uint32_t lds = verify_cols_lds(g, COLS);
     // row capacity of the conv registers: the smallest instantiation that holds the rows
     if (g.rows <= 8)
         gdn_verify_cols_kernel<8, COLS><<<grid, 8 * COLS, lds, s>>>(conv_state, state, qkv, alpha_raw, beta_raw,
@@ -778,8 +796,16 @@ hipError_t launch_gdn_verify_cols(const float *conv_state, const float *state, c
                                   const float *alpha_raw, const float *beta_raw, const float *conv_w, const float *dt,
                                   const float *a_log, float *raw_out, float *conv_out, const GdnArgs &g,
                                   hipStream_t s) {
-    launch_verify_cols<kVerifyCols>(conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g,
-                                    s);
+    switch (verify_cols(g)) {
+    case 128:
+        launch_verify_cols<128>(conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g, s);
+        break;
+    case 64:
+        launch_verify_cols<64>(conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g, s);
+        break;
+    default:
+        launch_verify_cols<32>(conv_state, state, qkv, alpha_raw, beta_raw, conv_w, dt, a_log, raw_out, conv_out, g, s);
+    }
     return hipGetLastError();
 }
 
