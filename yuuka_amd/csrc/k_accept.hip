@@ -239,9 +239,22 @@ struct SelShared {
     float mx;
 };
 
-template <bool W, class Sel, class Dig>
+// Top-p candidates held in LDS (dynamic shared memory of the select kernel):
+// the elements of the first digit's boundary bucket, collected by the second
+// pass when they fit, so that the third and fourth digits scan them instead
+// of the whole row.
+constexpr int kCandCap = 12288;
+struct Cands {
+    float *l;
+    int *j;
+    uint32_t *n;
+};
+
+// Histogram of the next digit over the row's elements that `sel` admits;
+// with C, the admitted elements are also appended to the candidate list.
+template <bool W, bool C = false, class Sel, class Dig>
 __device__ __forceinline__ void hist_pass(const float *__restrict__ p, int V, float mx, double t, SelShared &s,
-                                          Sel sel, Dig dig) {
+                                          Sel sel, Dig dig, Cands cand = Cands{nullptr, nullptr, nullptr}) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int b = lane; b < 256; b += 64) {
         s.cnt[wave][b] = 0u;
@@ -263,6 +276,13 @@ __device__ __forceinline__ void hist_pass(const float *__restrict__ p, int V, fl
             const int b = dig(l[u], j);
             atomicAdd(&s.cnt[wave][b], 1u);
             if (W) unsafeAtomicAdd(&s.wsum[wave][b], exp((double)(l[u] - mx) / t));
+            if (C) {
+                const uint32_t at = atomicAdd(cand.n, 1u);  // the caller checked the count fits
+                if (at < (uint32_t)kCandCap) {
+                    cand.l[at] = l[u];
+                    cand.j[at] = j;
+                }
+            }
         }
     }
     __syncthreads();
@@ -279,31 +299,116 @@ __device__ __forceinline__ void hist_pass(const float *__restrict__ p, int V, fl
     __syncthreads();
 }
 
-// Thread 0: walk the buckets in scan order (descending keys, or ascending for
+// hist_pass over the candidate list instead of the row.
+template <bool W, class Sel, class Dig>
+__device__ __forceinline__ void hist_cands(const Cands cand, uint32_t n, float mx, double t, SelShared &s, Sel sel,
+                                           Dig dig) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int b = lane; b < 256; b += 64) {
+        s.cnt[wave][b] = 0u;
+        if (W) s.wsum[wave][b] = 0.0;
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < n; i += kSelWaves * 64) {
+        const float l = cand.l[i];
+        const int j = cand.j[i];
+        if (!sel(l, j)) continue;
+        const int b = dig(l, j);
+        atomicAdd(&s.cnt[wave][b], 1u);
+        if (W) unsafeAtomicAdd(&s.wsum[wave][b], exp((double)(l - mx) / t));
+    }
+    __syncthreads();
+    if (threadIdx.x < 256) {
+        uint32_t c = 0u;
+        double w = 0.0;
+        for (int q = 0; q < kSelWaves; q++) {
+            c += s.cnt[q][threadIdx.x];
+            if (W) w += s.wsum[q][threadIdx.x];
+        }
+        s.tc[threadIdx.x] = c;
+        s.tw[threadIdx.x] = w;
+    }
+    __syncthreads();
+}
+
+// Wave 0: walk the buckets in scan order (descending keys, or ascending for
 // ids) to the first non-empty one where the running count reaches need_c (or
-// the running weight reaches need_w); append its digit to the prefix.
+// the running weight reaches need_w); append its digit to the prefix. Lane l
+// takes scan positions [4 l, 4 l + 4): its running start is the
+// lanes-before-it prefix (a fixed shuffle tree, so the sums are the same on
+// every run), then its own buckets in order; the first lane that reaches
+// the need picks. (One thread walking 256 LDS entries took ~16 us a pass.)
 __device__ __forceinline__ void scan_buckets(SelShared &s, bool descending, bool by_weight, uint32_t need_c,
                                              double need_w, int shift) {
-    uint32_t c = s.before_c;
-    double w = s.before_w;
-    int pick = -1;
-    for (int q = 0; q < 256; q++) {
-        const int b = descending ? 255 - q : q;
-        const uint32_t bc = s.tc[b];
-        if (!bc) continue;
-        if (by_weight ? (w + s.tw[b] >= need_w) : (c + bc >= need_c)) {
-            pick = b;
-            break;
-        }
-        c += bc;
-        w += s.tw[b];
+    const int lane = threadIdx.x & 63;
+    uint32_t bc[4], lc = 0u;
+    double bw[4], lw = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int q = 4 * lane + i, b = descending ? 255 - q : q;
+        bc[i] = s.tc[b];
+        bw[i] = s.tw[b];
+        lc += bc[i];
+        lw += bw[i];
     }
-    s.bucket = pick;
-    if (pick >= 0) {
+    uint32_t ic = lc;  // inclusive prefix over lanes
+    double iw = lw;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t tc = __shfl_up(ic, off);
+        const double tw = __shfl_up(iw, off);
+        if (lane >= off) {
+            ic += tc;
+            iw += tw;
+        }
+    }
+    const uint32_t ec = __shfl_up(ic, 1);
+    const double ew = __shfl_up(iw, 1);
+    uint32_t c = s.before_c + (lane ? ec : 0u);
+    double w = s.before_w + (lane ? ew : 0.0);
+    int pick = -1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (pick >= 0 || !bc[i]) continue;
+        if (by_weight ? (w + bw[i] >= need_w) : (c + bc[i] >= need_c)) {
+            pick = 4 * lane + i;
+            continue;
+        }
+        c += bc[i];
+        w += bw[i];
+    }
+    const uint64_t hit = __ballot(pick >= 0);
+    const int first = hit ? __ffsll((unsigned long long)hit) - 1 : -1;
+    if (first < 0) {
+        if (lane == 0) s.bucket = -1;
+        return;
+    }
+    if (lane == first) {
+        const int b = descending ? 255 - pick : pick;
+        s.bucket = b;
         s.before_c = c;
         s.before_w = w;
-        s.prefix |= (uint32_t)pick << shift;
+        s.prefix |= (uint32_t)b << shift;
     }
+}
+
+// Wave 0: the sums of the 256 bucket counts and weights (fixed tree order).
+__device__ __forceinline__ void bucket_totals(const SelShared &s, uint32_t *c_out, double *w_out) {
+    const int lane = threadIdx.x & 63;
+    uint32_t c = 0u;
+    double w = 0.0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        c += s.tc[4 * lane + i];
+        w += s.tw[4 * lane + i];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        c += __shfl_xor(c, off);
+        w += __shfl_xor(w, off);
+    }
+    *c_out = c;
+    *w_out = w;
 }
 
 // The need-th smallest id (1-based) among the elements with order key `key`
@@ -464,13 +569,14 @@ __global__ __launch_bounds__(1024) void accept_select_kernel(const float *__rest
             hist_pass<false>(
                 p, g.V, mx, t, s, [=](float l, int) { return (order_key(l) & mask) == pre; },
                 [=](float l, int) { return (order_key(l) >> shift) & 255u; });
-            if (threadIdx.x == 0) {
+            if (threadIdx.x < 64) {
+                uint32_t tot_c = s.total_c;
                 if (pass == 0) {
-                    uint32_t m = 0u;
-                    for (int q = 0; q < 256; q++) m += s.tc[q];
-                    s.total_c = m;
+                    double unused;
+                    bucket_totals(s, &tot_c, &unused);
+                    if (threadIdx.x == 0) s.total_c = tot_c;
                 }
-                if (s.total_c > (uint32_t)top_k) scan_buckets(s, true, false, (uint32_t)top_k, 0.0, shift);
+                if (tot_c > (uint32_t)top_k) scan_buckets(s, true, false, (uint32_t)top_k, 0.0, shift);
             }
             __syncthreads();
             if (s.total_c <= (uint32_t)top_k) {
@@ -499,11 +605,23 @@ __global__ __launch_bounds__(1024) void accept_select_kernel(const float *__rest
         }
         __syncthreads();
         bool found = true;
+        // mode 2: the second pass keeps the first digit's bucket in LDS when
+        // it fits; the later passes then scan only those elements
+        extern __shared__ uint8_t sel_dyn[];
+        const Cands cand{reinterpret_cast<float *>(sel_dyn), reinterpret_cast<int *>(sel_dyn + kCandCap * 4),
+                         reinterpret_cast<uint32_t *>(sel_dyn + kCandCap * 8)};
+        bool compact = false;
         for (int pass = 0; pass < 4 && found; pass++) {
             const int shift = 24 - 8 * pass;
             const uint32_t mask = pass ? ~0u << (shift + 8) : 0u;
             const uint32_t pre = s.prefix;
             const Cut ck = cut;
+            const auto sel_fn = [=](float l, int j) {
+                const uint32_t k = order_key(l);
+                return in_cut(k, j, ck) && (k & mask) == pre;
+            };
+            const auto dig_fn = [=](float l, int) { return (order_key(l) >> shift) & 255u; };
+            const bool collect = mode == 2 && pass == 1 && s.tc[s.bucket] <= (uint32_t)kCandCap;
             if (pass == 0 && h0) {  // chunk histograms, added in chunk order
                 if (threadIdx.x < 256) {
                     const Hist0 *hr = h0 + ((uint64_t)b * g.R + row) * g.C;
@@ -517,25 +635,27 @@ __global__ __launch_bounds__(1024) void accept_select_kernel(const float *__rest
                     s.tw[threadIdx.x] = w;
                 }
                 __syncthreads();
+            } else if (compact) {
+                hist_cands<true>(cand, *cand.n, mx, t, s, sel_fn, dig_fn);
+            } else if (collect) {
+                __syncthreads();  // every thread has read the first digit's count
+                if (threadIdx.x == 0) *cand.n = 0u;
+                __syncthreads();
+                hist_pass<true, true>(p, g.V, mx, t, s, sel_fn, dig_fn, cand);
+                compact = *cand.n <= (uint32_t)kCandCap;  // (always: the count was the first digit's)
             } else {
-                hist_pass<true>(
-                    p, g.V, mx, t, s,
-                    [=](float l, int j) {
-                        const uint32_t k = order_key(l);
-                        return in_cut(k, j, ck) && (k & mask) == pre;
-                    },
-                    [=](float l, int) { return (order_key(l) >> shift) & 255u; });
+                hist_pass<true>(p, g.V, mx, t, s, sel_fn, dig_fn);
             }
-            if (threadIdx.x == 0) {
+            if (threadIdx.x < 64) {
+                double tot = s.total_w;
                 if (pass == 0) {
-                    double w = 0.0;
-                    for (int q = 0; q < 256; q++) w += s.tw[q];
-                    s.total_w = w;
+                    uint32_t unused;
+                    bucket_totals(s, &unused, &tot);
+                    if (threadIdx.x == 0) s.total_w = tot;
                 }
-                const double tot = s.total_w;
                 if (tot > 0.0 && !isinf(tot))
                     scan_buckets(s, true, true, 0u, (double)top_p * tot, shift);
-                else
+                else if (threadIdx.x == 0)
                     s.bucket = -1;
             }
             __syncthreads();
@@ -643,12 +763,17 @@ __device__ int scan_chunk(const float *p, const Geo &g, int c, int d, float mx, 
     shared_prefix[threadIdx.x] = local;
     if (threadIdx.x == 0) *shared_pick = -1;
     __syncthreads();
-    if (threadIdx.x == 0) {  // exclusive prefix in thread order
+    if (threadIdx.x == 0) {  // exclusive prefix in thread order, 16 reads in flight at a time
         double run = 0.0;
-        for (int t = 0; t < 256; t++) {
-            const double v = shared_prefix[t];
-            shared_prefix[t] = run;
-            run += v;
+        for (int t0 = 0; t0 < 256; t0 += 16) {
+            double v[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = shared_prefix[t0 + i];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                shared_prefix[t0 + i] = run;
+                run += v[i];
+            }
         }
     }
     __syncthreads();
@@ -732,6 +857,10 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
         __shared__ double target_s;
         __shared__ int cstar;
         __shared__ float mx_s;
+        __shared__ double cs_s[256];  // the row's chunk weight sums, for thread 0's walk below
+        if (stochastic)
+            for (int c = threadIdx.x; c < g.C && c < 256; c += 256) cs_s[c] = sums[((uint64_t)b * g.R + row) * g.C + c];
+        __syncthreads();
         if (threadIdx.x == 0) {
             Stat best = row_best_s[row];
             const float p0 = row_p0_s[row];
@@ -756,7 +885,7 @@ __global__ __launch_bounds__(256) void accept_finalize_kernel(
                 Stat sb = row_best_s[row];
                 if (sb.v == -INFINITY) sb = best;
                 best_s = sb;
-                const double *cs = sums + ((uint64_t)b * g.R + row) * g.C;
+                const double *cs = g.C <= 256 ? cs_s : sums + ((uint64_t)b * g.R + row) * g.C;
                 const double rest = row_rest_s[row];
                 const double wd = (row < g.k && d >= 0 && d < g.V) ? wdraft[(uint64_t)b * g.R + row] : 0.0;
                 double total = rest + wd;
@@ -902,7 +1031,14 @@ hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int3
         if (top_k_on)
             accept_select_kernel<<<sel, kSelWaves * 64, 0, stream>>>(logits, g, stats, tk, 1.0f, t, cuts, 1, nullptr);
         accept_hist_kernel<<<grid, 256, 0, stream>>>(logits, g, stats, top_k_on ? cuts : nullptr, t, h0);
-        accept_select_kernel<<<sel, kSelWaves * 64, 0, stream>>>(logits, g, stats, tk, p.top_p, t, cuts, 2, h0);
+        static bool attr = false;
+        constexpr uint32_t cand_lds = kCandCap * 8 + 16;
+        if (!attr) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void *>(accept_select_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)cand_lds);
+            attr = true;
+        }
+        accept_select_kernel<<<sel, kSelWaves * 64, cand_lds, stream>>>(logits, g, stats, tk, p.top_p, t, cuts, 2, h0);
     }
     const Cut *cut_arg = truncate ? cuts : nullptr;
     if (stochastic)
