@@ -240,12 +240,11 @@ struct SelShared {
 };
 
 // Top-p candidates held in LDS (dynamic shared memory of the select kernel):
-// the elements of the first digit's boundary bucket, collected by the second
-// pass when they fit, so that the third and fourth digits scan them instead
-// of the whole row.
-constexpr int kCandCap = 12288;
+// the ids of the first digit's boundary bucket, collected by the second pass
+// when they fit, so that the third and fourth digits read those logits
+// (from L2: the second pass has just read the row) instead of the row.
+constexpr int kCandCap = 24576;
 struct Cands {
-    float *l;
     int *j;
     uint32_t *n;
 };
@@ -254,7 +253,7 @@ struct Cands {
 // with C, the admitted elements are also appended to the candidate list.
 template <bool W, bool C = false, class Sel, class Dig>
 __device__ __forceinline__ void hist_pass(const float *__restrict__ p, int V, float mx, double t, SelShared &s,
-                                          Sel sel, Dig dig, Cands cand = Cands{nullptr, nullptr, nullptr}) {
+                                          Sel sel, Dig dig, Cands cand = Cands{nullptr, nullptr}) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int b = lane; b < 256; b += 64) {
         s.cnt[wave][b] = 0u;
@@ -278,10 +277,7 @@ __device__ __forceinline__ void hist_pass(const float *__restrict__ p, int V, fl
             if (W) unsafeAtomicAdd(&s.wsum[wave][b], exp((double)(l[u] - mx) / t));
             if (C) {
                 const uint32_t at = atomicAdd(cand.n, 1u);  // the caller checked the count fits
-                if (at < (uint32_t)kCandCap) {
-                    cand.l[at] = l[u];
-                    cand.j[at] = j;
-                }
+                if (at < (uint32_t)kCandCap) cand.j[at] = j;
             }
         }
     }
@@ -301,8 +297,8 @@ __device__ __forceinline__ void hist_pass(const float *__restrict__ p, int V, fl
 
 // hist_pass over the candidate list instead of the row.
 template <bool W, class Sel, class Dig>
-__device__ __forceinline__ void hist_cands(const Cands cand, uint32_t n, float mx, double t, SelShared &s, Sel sel,
-                                           Dig dig) {
+__device__ __forceinline__ void hist_cands(const float *__restrict__ p, const Cands cand, uint32_t n, float mx,
+                                           double t, SelShared &s, Sel sel, Dig dig) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int b = lane; b < 256; b += 64) {
         s.cnt[wave][b] = 0u;
@@ -310,8 +306,8 @@ __device__ __forceinline__ void hist_cands(const Cands cand, uint32_t n, float m
     }
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < n; i += kSelWaves * 64) {
-        const float l = cand.l[i];
         const int j = cand.j[i];
+        const float l = p[j];
         if (!sel(l, j)) continue;
         const int b = dig(l, j);
         atomicAdd(&s.cnt[wave][b], 1u);
@@ -608,8 +604,7 @@ __global__ __launch_bounds__(1024) void accept_select_kernel(const float *__rest
         // mode 2: the second pass keeps the first digit's bucket in LDS when
         // it fits; the later passes then scan only those elements
         extern __shared__ uint8_t sel_dyn[];
-        const Cands cand{reinterpret_cast<float *>(sel_dyn), reinterpret_cast<int *>(sel_dyn + kCandCap * 4),
-                         reinterpret_cast<uint32_t *>(sel_dyn + kCandCap * 8)};
+        const Cands cand{reinterpret_cast<int *>(sel_dyn), reinterpret_cast<uint32_t *>(sel_dyn + kCandCap * 4)};
         bool compact = false;
         for (int pass = 0; pass < 4 && found; pass++) {
             const int shift = 24 - 8 * pass;
@@ -636,7 +631,7 @@ __global__ __launch_bounds__(1024) void accept_select_kernel(const float *__rest
                 }
                 __syncthreads();
             } else if (compact) {
-                hist_cands<true>(cand, *cand.n, mx, t, s, sel_fn, dig_fn);
+                hist_cands<true>(p, cand, *cand.n, mx, t, s, sel_fn, dig_fn);
             } else if (collect) {
                 __syncthreads();  // every thread has read the first digit's count
                 if (threadIdx.x == 0) *cand.n = 0u;
@@ -1032,7 +1027,7 @@ hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int3
             accept_select_kernel<<<sel, kSelWaves * 64, 0, stream>>>(logits, g, stats, tk, 1.0f, t, cuts, 1, nullptr);
         accept_hist_kernel<<<grid, 256, 0, stream>>>(logits, g, stats, top_k_on ? cuts : nullptr, t, h0);
         static bool attr = false;
-        constexpr uint32_t cand_lds = kCandCap * 8 + 16;
+        constexpr uint32_t cand_lds = kCandCap * 4 + 16;
         if (!attr) {
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(accept_select_kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)cand_lds);
