@@ -230,3 +230,33 @@ def test_engine_from_gguf_equals_engine_from_weights(dev, tiny, tmp_path, which)
         del w2
     for a, b in zip(out[0], out[1]):
         assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+
+@pytest.mark.parametrize("width", [3, 5])
+@pytest.mark.parametrize("k", [4, 16])
+def test_other_conv_widths_match_oracle(dev, width, k):
+    """GDN causal conv of width 3 or 5 (the models use 4; other widths take
+    the kernels' generic conv path): prefill, k + 1 verify rows and the
+    committed state after a partial accept against the oracle."""
+    cfg = replace(Mdl.TINY, conv_kernel=width, max_rows=max(Mdl.TINY.max_rows, k + 1))
+    w = Mdl.make_weights(cfg, seed=11)
+    eng = Mdl.Engine(dev, cfg, w)
+    orc = O.Q35(cfg, w, kv_format=1)
+    rng = np.random.default_rng(width * 100 + k)
+    prompt = rng.integers(0, cfg.vocab, 30).astype(np.int32)
+    _close(eng.prefill(prompt[:-1]), orc.forward(prompt[:-1]), f"prefill width={width}")
+    rows = np.concatenate([prompt[-1:], rng.integers(0, cfg.vocab, k)]).astype(np.int32)
+    snap, pos = orc.snapshot()
+    res = eng.verify(rows)
+    want = orc.forward(rows, all_logits=True)
+    _close(eng.logits(k + 1), want, f"verify width={width} k={k}")
+    # the device accepted res[0] drafts: the oracle replays the same prefix
+    orc.restore(snap, pos)
+    orc.forward(rows[: res[0] + 1])
+    gs, gp = eng.snapshot()
+    cs, cp = orc.snapshot()
+    assert gp == cp
+    g32, c32 = gs.view(np.float32), cs.view(np.float32)
+    assert np.max(np.abs(g32 - c32)) <= 1e-3 * (np.max(np.abs(c32)) + 1e-6)
+    eng.close()
+    orc.close()

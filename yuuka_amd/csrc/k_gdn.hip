@@ -332,46 +332,24 @@ __device__ __forceinline__ void conv_channel2(const float *conv_state, const flo
         }
         return;
     }
-#pragma unroll
+    // other widths (rare): a row loop reading the window from memory, no
+    // register arrays indexed at run time (those would live in scratch)
+#pragma unroll 1
     for (int u = 0; u < 2; u++) {
         if (u == 1 && c1 < 0) break;
-        float w[8], st[8], x[RC];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float wv = conv_w[(uint64_t)cc[u] * K + min(i, K - 1)];
-            const float sv = conv_state[(uint64_t)cc[u] * (K - 1) + min(i, K - 2)];
-            w[i] = i < K ? wv : 0.0f;
-            st[i] = i < K - 1 ? sv : 0.0f;
-        }
-#pragma unroll
-        for (int r = 0; r < RC; r++) {
-            const float xv = qkv[(uint64_t)min(r, R - 1) * g.conv_dim + cc[u]];
-            x[r] = r < R ? xv : 0.0f;
-        }
+        const uint64_t c = (uint64_t)cc[u];
         float *dst = u == 0 ? dst0 : dst1;
         const int stride = u == 0 ? stride0 : stride1;
-#pragma unroll
-        for (int r = 0; r < RC; r++) {
-            if (r >= R) break;
+#pragma unroll 1
+        for (int r = 0; r < R; r++) {
             float sum = 0.0f;
-#pragma unroll
-            for (int tt = 0; tt < 7; tt++) {
-                if (tt >= K - 1) break;
+#pragma unroll 1
+            for (int tt = 0; tt < K - 1; tt++) {
                 const int idx = r + tt - (K - 1);
-                float xv = 0.0f;
-#pragma unroll
-                for (int q = 0; q < RC; q++)
-                    if (q == idx) xv = x[q];
-#pragma unroll
-                for (int q = 0; q < 7; q++)
-                    if (q == K - 1 + idx && idx < 0) xv = st[q];
-                sum = __fadd_rn(sum, __fmul_rn(w[tt], xv));
+                const float xv = idx < 0 ? conv_state[c * (K - 1) + (K - 1 + idx)] : qkv[(uint64_t)idx * g.conv_dim + c];
+                sum = __fadd_rn(sum, __fmul_rn(conv_w[c * K + tt], xv));
             }
-            float wl = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 8; q++)
-                if (q == K - 1) wl = w[q];
-            sum = __fadd_rn(sum, __fmul_rn(wl, x[r]));
+            sum = __fadd_rn(sum, __fmul_rn(conv_w[c * K + K - 1], qkv[(uint64_t)r * g.conv_dim + c]));
             dst[r * stride] = silu_f32(sum);
         }
     }
@@ -404,7 +382,10 @@ __device__ __forceinline__ void conv_channels4(const float *conv_state, const fl
         if (cc[u] < 0) continue;
 #pragma unroll
         for (int r = 0; r < RC; r++) {
-            if (r >= R) break;
+            // a skip, not a break: the loop keeps one exit and unrolls fully,
+            // so x[u][...] stays in registers (an early exit left it rolled
+            // with x in scratch at 32 rows)
+            if (r >= R) continue;
             float sum = 0.0f;
 #pragma unroll
             for (int tt = 0; tt < 3; tt++) {
