@@ -285,59 +285,18 @@ __device__ __forceinline__ double wave_sum_dpp(double v) {
     return (rl_dd(v, 15) + rl_dd(v, 31)) + (rl_dd(v, 47) + rl_dd(v, 63));
 }
 
-// Causal conv + SiLU of two channels (c1 < 0: one). Width 4 (the models'
-// conv) issues every input load of both channels before either is computed;
-// other widths take the channels one after the other.
-template <int RC>  // row capacity: rows <= RC
+// Causal conv + SiLU of two channels (c1 < 0: one) of a width other than 4
+// (the models' width takes conv_channels4): a row loop reading the window
+// from memory, no register arrays indexed at run time (those would live in
+// scratch).
 __device__ __forceinline__ void conv_channel2(const float *conv_state, const float *qkv, const float *conv_w,
                                               const GdnArgs &g, int c0, float *dst0, int stride0, int c1, float *dst1,
                                               int stride1) {
     const int R = g.rows, K = g.kernel;
-    const int cc[2] = {c0, c1 < 0 ? c0 : c1};
-    // every load unconditional from a clamped index (out-of-range values are
-    // zeroed after the load): loads under branches make the compiler's wait
-    // counts conservative and serialize them
-    if (K == 4) {  // every index below is a compile-time constant
-        float w[2][4], st[2][3], x[2][RC];
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) w[u][i] = conv_w[(uint64_t)cc[u] * 4 + i];
-#pragma unroll
-            for (int i = 0; i < 3; i++) st[u][i] = conv_state[(uint64_t)cc[u] * 3 + i];
-#pragma unroll
-            for (int r = 0; r < RC; r++) {
-                const float xv = qkv[(uint64_t)min(r, R - 1) * g.conv_dim + cc[u]];
-                x[u][r] = r < R ? xv : 0.0f;
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            if (u == 1 && c1 < 0) break;
-            float *dst = u == 0 ? dst0 : dst1;
-            const int stride = u == 0 ? stride0 : stride1;
-#pragma unroll
-            for (int r = 0; r < RC; r++) {
-                if (r >= R) break;
-                float sum = 0.0f;
-#pragma unroll
-                for (int tt = 0; tt < 3; tt++) {
-                    const int idx = r + tt - 3;
-                    const float xv = idx >= 0 ? x[u][idx >= 0 ? idx : 0] : st[u][idx >= 0 ? 0 : 3 + idx];
-                    sum = __fadd_rn(sum, __fmul_rn(w[u][tt], xv));
-                }
-                sum = __fadd_rn(sum, __fmul_rn(w[u][3], x[u][r]));
-                dst[r * stride] = silu_f32(sum);
-            }
-        }
-        return;
-    }
-    // other widths (rare): a row loop reading the window from memory, no
-    // register arrays indexed at run time (those would live in scratch)
 #pragma unroll 1
     for (int u = 0; u < 2; u++) {
         if (u == 1 && c1 < 0) break;
-        const uint64_t c = (uint64_t)cc[u];
+        const uint64_t c = (uint64_t)(u == 0 ? c0 : c1);
         float *dst = u == 0 ? dst0 : dst1;
         const int stride = u == 0 ? stride0 : stride1;
 #pragma unroll 1
@@ -473,7 +432,7 @@ __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
             if (ch >= 2 * kS) break;  // wider blocks: threads past the q / k channels (none of them owns a v channel)
             const int c0 = (which == 0 ? 0 : key_dim) + kh * kS + cc;
             const int c1 = base == 0 && t < COLS ? 2 * key_dim + h * kS + cb * COLS + t : -1;
-            conv_channel2<RC>(conv_state, qkv, conv_w, g, c0, qk + which * kS + cc, 2 * kS, c1, vv + t, COLS);
+            conv_channel2(conv_state, qkv, conv_w, g, c0, qk + which * kS + cc, 2 * kS, c1, vv + t, COLS);
         }
     }
     __syncthreads();
