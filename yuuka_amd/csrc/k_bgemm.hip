@@ -9,13 +9,15 @@
 // block. Here each weight super-block is read once per block of 48 rows (80
 // for 49..80 rows), and the products run on v_mfma_f32_16x16x32_f16:
 //
-//  * prologue (one workgroup per row): y = prologue(x) computed as the
-//    reference computes it (forward.go:460-482 rmsNorm, recurrent.go:39-50
-//    gated norm), then per 256-element super-block scaled into [-256, 256]
-//    (one FP32 scale per row and super-block) and rounded to FP16, with the
-//    FP32 sum of every 32-element sub-block of those FP16 values stored as an
-//    FP16 high part and its FP16 remainder — a workspace of
-//    rows * (2 K + K / 8 + K / 64) B.
+//  * prologue (one workgroup per row and group of 8 super-blocks): y =
+//    prologue(x) computed as the reference computes it (recurrent.go:39-50
+//    gated norm), or for the row RMSNorm (forward.go:460-482) y = x * w with
+//    the group's float64 sum of squares stored, the GEMM scaling each row's
+//    sums by its 1 / rms; then per 256-element super-block scaled into
+//    [-256, 256] (one FP32 scale per row and super-block) and rounded to
+//    FP16, with the FP32 sum of every 32-element sub-block of those FP16
+//    values stored as an FP16 high part and its FP16 remainder — a workspace
+//    of rows * (2 K + K / 8 + K / 64 + 64) B.
 //  * GEMM (workgroup = a block of 16-row tiles x 8 tiles of 16 output
 //    channels, one channel tile per wave): per super-block the block's FP16
 //    values and sub-block sums are copied straight into LDS
@@ -71,10 +73,15 @@ constexpr float kBgRange = 256.0f;  // |y / scale| <= kBgRange
 //   h      [sb][tile][sub-block j][group g][row c][8 FP16]  (8 KB per tile)
 //   sums   [sb][tile][row c][16 FP16]                       (512 B per tile)
 //   scales [sb][tile * 16 + c] float
+//   ss     [row][kBgSsGroups] float64 sums of squares of x over the
+//          prologue workgroups' super-block groups (RMSNorm prologues: the
+//          GEMM applies the row's 1/rms to its sums)
+constexpr int kBgSsGroups = 8;  // groups of 8 super-blocks: K <= 16384
 struct BgQuant {
     _Float16 *h;     // y / scale
     _Float16 *sums;  // sub-block sums of h: high parts (8) then remainders (8)
     float *scales;
+    double *ss;
 };
 
 __host__ __device__ inline int bg_rows16(int rows) { return (rows + 15) & ~15; }
@@ -86,6 +93,7 @@ __host__ __device__ inline BgQuant bg_view(void *ws, int rows, int K) {
     q.h = reinterpret_cast<_Float16 *>(p);
     q.sums = reinterpret_cast<_Float16 *>(p + r16 * K * 2);
     q.scales = reinterpret_cast<float *>(p + r16 * K * 2 + r16 * (K / 256) * 32);
+    q.ss = reinterpret_cast<double *>(p + r16 * K * 2 + r16 * (K / 256) * 36);  // 8-byte aligned: K % 256 == 0
     return q;
 }
 
@@ -154,10 +162,13 @@ struct BgSrc {
     uint64_t prow;      // floats between rows of part (K, or 2K with swiglu)
 };
 
-// One row per workgroup. Wave w owns super-blocks w, w + 8, ... (at most P
-// of them) and lane l elements [4 l, +4) of each: x (or the split sums), the
-// norm weights and the gate are loaded into registers in one round trip; the
-// row's float64 sum of squares is the only exchange between waves.
+// Workgroup (row, group of 8 P super-blocks). Wave w owns super-blocks w,
+// w + 8, ... of the group (at most P of them) and lane l elements [4 l, +4)
+// of each: x (or the split sums), the norm weights and the gate are loaded
+// into registers in one round trip. With the row RMSNorm the group's float64
+// sum of squares goes to q.ss and the values are quantized as x * w: the
+// GEMM multiplies each row's sums by the row's 1 / rms, so no workgroup
+// needs the whole row.
 template <int P>
 __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemmArgs A, BgQuant q, const BgSrc src) {
     constexpr int W = kPrThreads / 64;
@@ -165,8 +176,7 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
     const int row = blockIdx.x, K = A.K, nsb = K / 256;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint64_t rbase = (uint64_t)row * K;
-    // super-blocks [sb0, sb0 + W P) of the row: all of them when the row's
-    // RMSNorm needs the whole row, else one group per workgroup (grid y)
+    // super-blocks [sb0, sb0 + W P) of the row (grid y: the group)
     const int sb0 = (int)blockIdx.y * W * P;
     auto elem = [&](int i) { return (sb0 + wave + W * i) * 256 + 4 * lane; };
     auto live = [&](int i) { return sb0 + wave + W * i < nsb; };
@@ -284,9 +294,9 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
         for (int i = 0; i < P; i++)
             if (live(i)) nw[i] = *reinterpret_cast<const float4 *>(A.norm + elem(i));
     }
-    float nscale = 1.f;
     if (A.norm && !A.gate) {
-        // forward.go:460-470 rmsNorm: float64 sum of squares, x * scale * w
+        // forward.go:460-470 rmsNorm: float64 sum of squares (this group's
+        // part, waves in order; the GEMM adds the groups in order)
         double ss = 0.0;
 #pragma unroll
         for (int i = 0; i < P; i++)
@@ -296,11 +306,12 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
         ss = wave_sum_d(ss);
         if (lane == 0) red[wave] = ss;
         __syncthreads();
-        double t = 0.0;
+        if (threadIdx.x == 0) {
+            double t = 0.0;
 #pragma unroll
-        for (int w = 0; w < W; w++) t += red[w];
-        const float mean = (float)(t / (double)K);
-        nscale = (float)(1.0 / sqrt((double)(mean + A.eps)));
+            for (int w = 0; w < W; w++) t += red[w];
+            q.ss[(uint64_t)row * kBgSsGroups + blockIdx.y] = t;
+        }
     }
 #pragma unroll
     for (int i = 0; i < P; i++) {
@@ -320,11 +331,11 @@ __global__ __launch_bounds__(kPrThreads) void bg_prologue_kernel(const FusedGemm
             y.y = __fmul_rn(__fmul_rn(y.y, __fmul_rn(hsc, hw.y)), z[i].y);
             y.z = __fmul_rn(__fmul_rn(y.z, __fmul_rn(hsc, hw.z)), z[i].z);
             y.w = __fmul_rn(__fmul_rn(y.w, __fmul_rn(hsc, hw.w)), z[i].w);
-        } else if (A.norm) {
-            y.x = __fmul_rn(__fmul_rn(y.x, nscale), nw[i].x);
-            y.y = __fmul_rn(__fmul_rn(y.y, nscale), nw[i].y);
-            y.z = __fmul_rn(__fmul_rn(y.z, nscale), nw[i].z);
-            y.w = __fmul_rn(__fmul_rn(y.w, nscale), nw[i].w);
+        } else if (A.norm) {  // x * w; the row's 1 / rms scales the GEMM's sums
+            y.x = __fmul_rn(y.x, nw[i].x);
+            y.y = __fmul_rn(y.y, nw[i].y);
+            y.z = __fmul_rn(y.z, nw[i].z);
+            y.w = __fmul_rn(y.w, nw[i].w);
         }
         float m = fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w)));
         m = wave_max_nonneg(m);
@@ -466,7 +477,7 @@ template <int NT> struct BgLds {
     static constexpr uint32_t stage = X + kRows * 4;
     static constexpr uint32_t total = 2 * stage;
 };
-static_assert(BgLds<9>::total <= 160 * 1024, "nine tiles fit LDS");
+static_assert(BgLds<9>::total + 16 * 9 * 4 <= 160 * 1024, "nine tiles (and the row norms) fit LDS");
 
 // 16-byte global -> LDS copy of one lane (lane l writes [m0 + 16 l, +16)
 // from base + voff, base uniform), as inline assembly so that the
@@ -615,9 +626,12 @@ __device__ __forceinline__ void bg_super_q6(const WQ6 &cur, const uint8_t *st, f
 // super-block sb + 1 is copied and loaded while sb is multiplied. Every
 // weight load is issued, its index clamped to the last super-block (loads
 // under a branch would make the compiler copy the register sets).
-template <int DT, int NT>
+// `pre` runs after the first super-block's copies and weight loads are
+// issued and before the wait for them (its own loads are the youngest, so
+// waiting for them costs nothing more).
+template <int DT, int NT, class Pre>
 __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int T0, bool live, const uint8_t *wrow,
-                                        float (&y)[NT][4]) {
+                                        float (&y)[NT][4], Pre pre) {
     using LY = BgLds<NT>;
     const int g = (threadIdx.x & 63) >> 4;
     const int tiles = bg_rows16(A.f.rows) / 16;
@@ -640,6 +654,7 @@ __device__ __forceinline__ void bg_main(const BgArgs &A, uint8_t *lds, int T0, b
     W wa, wb;
     loadw(wa, sb_lo);
     float xs = stage_issue<NT>(A, lds, T0, tiles, sb_lo);
+    pre();
     __builtin_amdgcn_s_waitcnt(0);
     if (threadIdx.x < LY::kRows) x0[threadIdx.x] = xs;
     __syncthreads();
@@ -701,8 +716,33 @@ __global__ __launch_bounds__(kBgThreads) __attribute__((amdgpu_waves_per_eu(NT >
     for (int t = 0; t < NT; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) y[t][i] = 0.f;
-    if (S.dtype == kQ6K) bg_main<kQ6K, NT>(A, lds, m0 / 16, live, wrow, y);
-    else bg_main<kQ4K, NT>(A, lds, m0 / 16, live, wrow, y);
+    // RMSNorm prologue: the 1 / rms of the block's rows from the prologue's
+    // group sums (added in group order; forward.go:460-470), published by
+    // the main loop's first barrier
+    __shared__ float row_inv[kRowsB];
+    const bool rnorm = F.norm != nullptr && F.gate == nullptr;
+    auto pre = [&]() __attribute__((always_inline)) {
+        if (!rnorm || threadIdx.x >= kRowsB) return;
+        const int row = min(m0 + (int)threadIdx.x, F.rows - 1), G = (F.K / 256 + 7) / 8;
+        const double *ps = A.q.ss + (uint64_t)row * kBgSsGroups;
+        double v[kBgSsGroups];
+#pragma unroll
+        for (int gi = 0; gi < kBgSsGroups; gi++) v[gi] = ps[min(gi, G - 1)];
+        double t = 0.0;
+#pragma unroll
+        for (int gi = 0; gi < kBgSsGroups; gi++)
+            if (gi < G) t += v[gi];
+        const float mean = (float)(t / (double)F.K);
+        row_inv[threadIdx.x] = (float)(1.0 / sqrt((double)(mean + F.eps)));
+    };
+    if (S.dtype == kQ6K) bg_main<kQ6K, NT>(A, lds, m0 / 16, live, wrow, y, pre);
+    else bg_main<kQ4K, NT>(A, lds, m0 / 16, live, wrow, y, pre);
+    if (rnorm) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) y[t][i] = __fmul_rn(y[t][i], row_inv[16 * t + 4 * g + i]);
+    }
 
     // epilogue: lane (c, g) holds rows 16 t + 4 g + i of channel n0 + c
     if (A.splits > 1) {  // partial sums of this split; bg_reduce_kernel finishes
@@ -809,7 +849,7 @@ int bg_resident(int nt) {
             n = 256;
         const void *k = nt == 5 ? bg_kernel_ptr<5>() : bg_kernel_ptr<3>();
         const uint32_t lds = nt == 5 ? BgLds<5>::total : BgLds<3>::total;
-        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, kBgThreads, lds) != hipSuccess || per <= 0) per = 1;
         res[nt] = n * per;
     }
@@ -850,7 +890,7 @@ int bg_splits(int wgs, int nsb, int nt) {
 
 uint64_t bg_quant_bytes(int rows, int K) {
     const uint64_t r16 = (uint64_t)bg_rows16(rows);
-    return r16 * K * 2 + r16 * (K / 256) * 32 + r16 * (K / 256) * 4;
+    return r16 * K * 2 + r16 * (K / 256) * 32 + r16 * (K / 256) * 4 + r16 * kBgSsGroups * 8;
 }
 
 }  // namespace
@@ -914,24 +954,11 @@ static void bg_setup(const FusedGemmArgs &a, void *ws, BgArgs &A, unsigned &gx, 
 }
 
 static hipError_t bg_launch_prologue(const FusedGemmArgs &a, const BgQuant &q, const BgSrc &src, hipStream_t s) {
-    // super-blocks per wave, rounded up to an instantiated register count;
-    // without the row RMSNorm (plain x, or the gated head norm inside each
-    // super-block) a row's super-blocks spread over workgroups, one per wave
+    // one workgroup per (row, group of 8 super-blocks), + the padding rows
     const int nsb = a.K / 256, W = kPrThreads / 64;
-    const bool whole_row = a.norm != nullptr && a.gate == nullptr;
-    const int per = whole_row ? (nsb + W - 1) / W : 1;
-    const dim3 grid((unsigned)bg_rows16(a.rows), whole_row ? 1u : (unsigned)((nsb + W - 1) / W));  // + padding rows
-    switch (per) {
-    case 1: bg_prologue_kernel<1><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
-    case 2: bg_prologue_kernel<2><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
-    case 3: bg_prologue_kernel<3><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
-    case 4: bg_prologue_kernel<4><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
-    case 5:
-    case 6: bg_prologue_kernel<6><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
-    case 7:
-    case 8: bg_prologue_kernel<8><<<grid, kPrThreads, 0, s>>>(a, q, src); break;
-    default: return hipErrorInvalidValue;  // K over 16384
-    }
+    if (nsb > W * kBgSsGroups) return hipErrorInvalidValue;  // K over 16384
+    const dim3 grid((unsigned)bg_rows16(a.rows), (unsigned)((nsb + W - 1) / W));
+    bg_prologue_kernel<1><<<grid, kPrThreads, 0, s>>>(a, q, src);
     return hipGetLastError();
 }
 
