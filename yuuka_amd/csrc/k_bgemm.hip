@@ -76,7 +76,9 @@ constexpr float kBgRange = 256.0f;  // |y / scale| <= kBgRange
 //   ss     [row][kBgSsGroups] float64 sums of squares of x over the
 //          prologue workgroups' super-block groups (RMSNorm prologues: the
 //          GEMM applies the row's 1/rms to its sums)
-constexpr int kBgSsGroups = 8;  // groups of 8 super-blocks: K <= 16384
+constexpr int kPrThreads = 512;                 // prologue workgroup: one super-block per wave
+constexpr int kPrWaves = kPrThreads / 64;
+constexpr int kBgSsGroups = 64 / kPrWaves;  // groups of kPrWaves super-blocks: K <= 16384
 struct BgQuant {
     _Float16 *h;     // y / scale
     _Float16 *sums;  // sub-block sums of h: high parts (8) then remainders (8)
@@ -147,7 +149,6 @@ __device__ __forceinline__ uint32_t h2bits(_Float16 a, _Float16 b) {
 }
 
 // ---------------------------------------------------------------- prologue
-constexpr int kPrThreads = 512;
 
 // Where the prologue's x comes from: A.x, or (part != null) the split
 // partial sums of the previous many-row GEMM, which the prologue finishes as
@@ -723,7 +724,7 @@ __global__ __launch_bounds__(kBgThreads) __attribute__((amdgpu_waves_per_eu(NT >
     const bool rnorm = F.norm != nullptr && F.gate == nullptr;
     auto pre = [&]() __attribute__((always_inline)) {
         if (!rnorm || threadIdx.x >= kRowsB) return;
-        const int row = min(m0 + (int)threadIdx.x, F.rows - 1), G = (F.K / 256 + 7) / 8;
+        const int row = min(m0 + (int)threadIdx.x, F.rows - 1), G = (F.K / 256 + kPrWaves - 1) / kPrWaves;
         const double *ps = A.q.ss + (uint64_t)row * kBgSsGroups;
         double v[kBgSsGroups];
 #pragma unroll
