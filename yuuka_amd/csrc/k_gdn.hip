@@ -560,7 +560,56 @@ __device__ __forceinline__ void gdn_commit_cols_body(float *__restrict__ conv_st
     const int K = g.kernel;
     const int key_dim = g.groups * kS;
     const int kh = h % g.groups;
-    {
+    const int p = lane & 7, j = cb * kCols + wave * 8 + (lane >> 3);
+    float *mat = state + (uint64_t)h * kS * kS;
+    // Every load is issued before the first wait: the block's 128 x 32 state
+    // tile (16-byte loads of whole 128-byte row pieces, eight rows per wave
+    // instruction), the accepted rows' k, v (this block's columns), decay
+    // and beta, and the conv windows. Then the tile goes through LDS, each
+    // thread taking its column's 16 rows, and the rows are staged in LDS so
+    // that the serial row loop reads LDS only.
+    __shared__ float tile[kS][kCols + 1];
+    constexpr int kTileIt = kS * kCols / 4 / kColThreads;
+    float4 v4[kTileIt];
+#pragma unroll
+    for (int it = 0; it < kTileIt; it++) {
+        const int idx = t + kColThreads * it, row = idx >> 3, c4 = idx & 7;
+        v4[it] = *reinterpret_cast<const float4 *>(mat + (uint64_t)row * kS + cb * kCols + 4 * c4);
+    }
+    // (dynamic LDS sized for the launch's rows: gdn_commit_lds_bytes)
+    extern __shared__ float commit_rows[];
+    const int R = g.rows;
+    float *sk_rows = commit_rows, *sv_rows = sk_rows + R * kS, *scf = sv_rows + R * kCols;  // [R][kS], [R][kCols], [2][R]
+    constexpr int kW = kS + kCols;  // staged floats per row
+    constexpr int kSG = 4;          // staged values in flight per thread
+    const int total = n * kW;
+    float cf0 = 0.0f, cf1 = 0.0f;
+    if (t < n) {
+        cf0 = gdn_decay(g, alpha_raw, dt, a_log, t, h);
+        cf1 = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
+    }
+    float sv[kSG];
+    auto stage_load = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < kSG; u++) {
+            const int idx = min(i0 + t + u * kColThreads, total - 1);
+            const int r = idx / kW, c = idx - r * kW;
+            const float *row = conv + (uint64_t)r * g.conv_dim;
+            sv[u] = row[c < kS ? key_dim + kh * kS + c : 2 * key_dim + h * kS + cb * kCols + (c - kS)];
+        }
+    };
+    auto stage_store = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < kSG; u++) {
+            const int idx = i0 + t + u * kColThreads;
+            if (idx >= total) break;
+            const int r = idx / kW, c = idx - r * kW;
+            if (c < kS) sk_rows[r * kS + c] = sv[u];
+            else sv_rows[r * kCols + c - kS] = sv[u];
+        }
+    };
+    if (total > 0) stage_load(0);
+    {  // conv windows: this block's v channels and (cb == 0, h < groups) the q/k group's channels
         const bool qk_owner = cb == 0 && h < g.groups;
         const int nch = kCols + (qk_owner ? 2 * kS : 0);
         for (int ch = t; ch < nch; ch += kColThreads) {
@@ -579,43 +628,21 @@ __device__ __forceinline__ void gdn_commit_cols_body(float *__restrict__ conv_st
                 if (tt < K - 1) conv_state[(uint64_t)c * (K - 1) + tt] = win[tt];
         }
     }
-    const int p = lane & 7, j = cb * kCols + wave * 8 + (lane >> 3);
-    float *mat = state + (uint64_t)h * kS * kS;
-    // the block's 128 x 32 state tile through LDS: 16-byte loads of whole
-    // 128-byte row pieces (eight rows per wave instruction), then each thread
-    // takes its column's 16 rows
-    __shared__ float tile[kS][kCols + 1];
-    {
-        float4 v4[kS * kCols / 4 / kColThreads];
 #pragma unroll
-        for (int it = 0; it < kS * kCols / 4 / kColThreads; it++) {
-            const int idx = t + kColThreads * it, row = idx >> 3, c4 = idx & 7;
-            v4[it] = *reinterpret_cast<const float4 *>(mat + (uint64_t)row * kS + cb * kCols + 4 * c4);
-        }
-#pragma unroll
-        for (int it = 0; it < kS * kCols / 4 / kColThreads; it++) {
-            const int idx = t + kColThreads * it, row = idx >> 3, c4 = idx & 7;
-            tile[row][4 * c4] = v4[it].x;
-            tile[row][4 * c4 + 1] = v4[it].y;
-            tile[row][4 * c4 + 2] = v4[it].z;
-            tile[row][4 * c4 + 3] = v4[it].w;
-        }
+    for (int it = 0; it < kTileIt; it++) {
+        const int idx = t + kColThreads * it, row = idx >> 3, c4 = idx & 7;
+        tile[row][4 * c4] = v4[it].x;
+        tile[row][4 * c4 + 1] = v4[it].y;
+        tile[row][4 * c4 + 2] = v4[it].z;
+        tile[row][4 * c4 + 3] = v4[it].w;
     }
-    // the accepted rows' k, v (this block's columns), decay and beta, staged
-    // once so that the serial row loop reads LDS only
-    // (dynamic LDS sized for the launch's rows: gdn_commit_lds_bytes)
-    extern __shared__ float commit_rows[];
-    const int R = g.rows;
-    float *sk_rows = commit_rows, *sv_rows = sk_rows + R * kS, *scf = sv_rows + R * kCols;  // [R][kS], [R][kCols], [2][R]
-    for (int idx = t; idx < n * (kS + kCols); idx += kColThreads) {
-        const int r = idx / (kS + kCols), c = idx - r * (kS + kCols);
-        const float *row = conv + (uint64_t)r * g.conv_dim;
-        if (c < kS) sk_rows[r * kS + c] = row[key_dim + kh * kS + c];
-        else sv_rows[r * kCols + c - kS] = row[2 * key_dim + h * kS + cb * kCols + (c - kS)];
+    for (int i0 = 0; i0 < total; i0 += kSG * kColThreads) {
+        if (i0) stage_load(i0);
+        stage_store(i0);
     }
     if (t < n) {
-        scf[t] = gdn_decay(g, alpha_raw, dt, a_log, t, h);
-        scf[R + t] = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
+        scf[t] = cf0;
+        scf[R + t] = cf1;
     }
     __syncthreads();
     float s_reg[16];
