@@ -100,6 +100,28 @@ __device__ __forceinline__ float gdn_decay(const GdnArgs &g, const float *alpha_
     return (float)exp((double)act);
 }
 
+// A row's decay and beta in two steps: the loads (issued early, nothing
+// waits for them), then gdn_decay's and the beta map's arithmetic.
+struct GdnCoefIn {
+    float a, b, dt, al;
+};
+__device__ __forceinline__ GdnCoefIn gdn_coef_load(const GdnArgs &g, const float *alpha_raw, const float *beta_raw,
+                                                   const float *dt, const float *a_log, int r, int h) {
+    GdnCoefIn c;
+    c.a = alpha_raw[(uint64_t)r * g.rank + h];
+    c.b = beta_raw[(uint64_t)r * g.rank + h];
+    c.dt = g.coef ? 0.0f : dt[h];  // (read only without precomputed coefficients)
+    c.al = g.coef ? 0.0f : a_log[h];
+    return c;
+}
+__device__ __forceinline__ float gdn_coef_decay(const GdnArgs &g, const GdnCoefIn &c) {
+    if (g.coef) return c.a;
+    return (float)exp((double)__fmul_rn(softplus_ref(__fadd_rn(c.a, c.dt)), c.al));
+}
+__device__ __forceinline__ float gdn_coef_beta(const GdnArgs &g, const GdnCoefIn &c) {
+    return g.coef ? c.b : sigmoid_ref(c.b);
+}
+
 // LDS: cv [rows][3][128] conv outputs (q, k, v of this head), raw [rows][128]
 // scan outputs.
 __global__ __launch_bounds__(kGdnThreads) void gdn_verify_kernel(
@@ -398,10 +420,9 @@ __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
     float *qk = sm;                 // [R][2][128] q, k
     float *vv = qk + R * 2 * kS;    // [R][COLS]
     float *cf = vv + R * COLS;      // [2][R] decay, beta of every row
-    if (t < R) {
-        cf[t] = gdn_decay(g, alpha_raw, dt, a_log, t, h);
-        cf[R + t] = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
-    }
+    // row t's coefficients: loaded now, computed after the conv (so that no
+    // wave waits for them before issuing its state and conv loads)
+    const GdnCoefIn cin = gdn_coef_load(g, alpha_raw, beta_raw, dt, a_log, min(t, R - 1), h);
     const int p = lane & 7, j = cb * COLS + wave * 8 + (lane >> 3);
     const float *mat = state + (uint64_t)h * kS * kS;
     float s_reg[16];
@@ -434,6 +455,10 @@ __global__ __launch_bounds__(8 * COLS) void gdn_verify_cols_kernel(
             const int c1 = base == 0 && t < COLS ? 2 * key_dim + h * kS + cb * COLS + t : -1;
             conv_channel2(conv_state, qkv, conv_w, g, c0, qk + which * kS + cc, 2 * kS, c1, vv + t, COLS);
         }
+    }
+    if (t < R) {
+        cf[t] = gdn_coef_decay(g, cin);
+        cf[R + t] = gdn_coef_beta(g, cin);
     }
     __syncthreads();
     // L2 norm of the 2R q / k vectors. One 16-lane DPP row per vector (lane
@@ -583,11 +608,7 @@ __device__ __forceinline__ void gdn_commit_cols_body(float *__restrict__ conv_st
     constexpr int kW = kS + kCols;  // staged floats per row
     constexpr int kSG = 4;          // staged values in flight per thread
     const int total = n * kW;
-    float cf0 = 0.0f, cf1 = 0.0f;
-    if (t < n) {
-        cf0 = gdn_decay(g, alpha_raw, dt, a_log, t, h);
-        cf1 = g.coef ? beta_raw[(uint64_t)t * g.rank + h] : sigmoid_ref(beta_raw[(uint64_t)t * g.rank + h]);
-    }
+    const GdnCoefIn cin = gdn_coef_load(g, alpha_raw, beta_raw, dt, a_log, min(t, n - 1), h);
     float sv[kSG];
     auto stage_load = [&](int i0) __attribute__((always_inline)) {
 #pragma unroll
@@ -641,8 +662,8 @@ __device__ __forceinline__ void gdn_commit_cols_body(float *__restrict__ conv_st
         stage_store(i0);
     }
     if (t < n) {
-        scf[t] = cf0;
-        scf[R + t] = cf1;
+        scf[t] = gdn_coef_decay(g, cin);
+        scf[R + t] = gdn_coef_beta(g, cin);
     }
     __syncthreads();
     float s_reg[16];
