@@ -1333,8 +1333,10 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
     const bool mfma = use_mfma_path(a);
     const unsigned nz = (unsigned)(a.nreq > 0 ? a.nreq : 1);
     // MFMA kernel: groups of cpw chunks per workgroup once a launch has more
-    // than ~1024 chunk workgroups (fewer partial records, query preparation
-    // amortized); short contexts keep one chunk per workgroup
+    // than ~512 chunk workgroups (fewer partial records, query preparation
+    // amortized; config 5's 1056 chunk workgroups: attention + merge 581 ->
+    // 464 us per step with pairs, 481 us with fours); short contexts keep
+    // one chunk per workgroup
     // Blocks of more than 32 MFMA rows (G x rows) take the PF grouped kernel
     // (3, 5 or 6 row tiles): one workgroup per CU, so its groups are sized
     // for about one round of workgroups over the CUs.
@@ -1345,7 +1347,7 @@ hipError_t launch_attn_verify(const float *q, const float *k, const float *v, vo
         const int c1 = (a.capacity + kMK - 1) / kMK;
         const int l1 = max_pos_hint >= 0 ? std::min(c1, max_pos_hint / kMK + 1) : c1;
         const int64_t wgs = (int64_t)l1 * a.kv_heads * nz;
-        cpw = (int)std::max<int64_t>(1, std::min<int64_t>(8, wgs / 1024));
+        cpw = (int)std::max<int64_t>(1, std::min<int64_t>(8, wgs / 512));
         if (wide && cpw > 1) {
             // groups per (KV head, request) that fit one workgroup per CU
             const int64_t per = std::max<int64_t>(1, attn_device_cus() / ((int64_t)a.kv_heads * nz));
