@@ -242,11 +242,14 @@ struct SelShared {
 // Top-p candidates held in LDS (dynamic shared memory of the select kernel):
 // the ids of the first digit's boundary bucket, collected by the second pass
 // when they fit, so that the third and fourth digits read those logits
-// (from L2: the second pass has just read the row) instead of the row.
+// (from L2: the second pass has just read the row) instead of the row. Each
+// wave fills its own segment in a fixed order, so the later passes add the
+// same values in the same order on every run.
 constexpr int kCandCap = 24576;
+constexpr int kCandWave = kCandCap / kSelWaves;  // per-wave segment
 struct Cands {
-    int *j;
-    uint32_t *n;
+    int *j;       // [wave][kCandWave]
+    uint32_t *n;  // [wave] candidates found (more than kCandWave: not all stored)
 };
 
 // Histogram of the next digit over the row's elements that `sel` admits;
@@ -264,6 +267,7 @@ __device__ __forceinline__ void hist_pass(const float *__restrict__ p, int V, fl
     // eight loads in flight per thread (the row is read from L2 / the
     // Infinity Cache once per pass: latency, not bandwidth, bounds the pass)
     constexpr int kU = 8;
+    uint32_t wn = 0u;  // candidates of this wave so far
     for (int j0 = threadIdx.x; j0 < V; j0 += kU * kStride) {
         float l[kU];
 #pragma unroll
@@ -271,16 +275,22 @@ __device__ __forceinline__ void hist_pass(const float *__restrict__ p, int V, fl
 #pragma unroll
         for (int u = 0; u < kU; u++) {
             const int j = j0 + u * kStride;
-            if (!valid_logit(l[u]) || !sel(l[u], j)) continue;
+            const bool take = valid_logit(l[u]) && sel(l[u], j);
+            if (C) {
+                // this wave's segment, in (iteration, lane) order: the list is
+                // the same on every run, whatever the waves' timing
+                const uint64_t m = __ballot(take);
+                const uint32_t at = wn + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+                if (take && at < (uint32_t)kCandWave) cand.j[wave * kCandWave + at] = j;
+                wn += (uint32_t)__popcll(m);
+            }
+            if (!take) continue;
             const int b = dig(l[u], j);
             atomicAdd(&s.cnt[wave][b], 1u);
             if (W) unsafeAtomicAdd(&s.wsum[wave][b], exp((double)(l[u] - mx) / t));
-            if (C) {
-                const uint32_t at = atomicAdd(cand.n, 1u);  // the caller checked the count fits
-                if (at < (uint32_t)kCandCap) cand.j[at] = j;
-            }
         }
     }
+    if (C && lane == 0) cand.n[wave] = wn;
     __syncthreads();
     if (threadIdx.x < 256) {
         uint32_t c = 0u;
@@ -297,16 +307,17 @@ __device__ __forceinline__ void hist_pass(const float *__restrict__ p, int V, fl
 
 // hist_pass over the candidate list instead of the row.
 template <bool W, class Sel, class Dig>
-__device__ __forceinline__ void hist_cands(const float *__restrict__ p, const Cands cand, uint32_t n, float mx,
-                                           double t, SelShared &s, Sel sel, Dig dig) {
+__device__ __forceinline__ void hist_cands(const float *__restrict__ p, const Cands cand, float mx, double t,
+                                           SelShared &s, Sel sel, Dig dig) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     for (int b = lane; b < 256; b += 64) {
         s.cnt[wave][b] = 0u;
         if (W) s.wsum[wave][b] = 0.0;
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < n; i += kSelWaves * 64) {
-        const int j = cand.j[i];
+    const uint32_t n = min(cand.n[wave], (uint32_t)kCandWave);  // (the caller checked every segment fits)
+    for (uint32_t i = lane; i < n; i += 64) {  // wave w walks segment w
+        const int j = cand.j[wave * kCandWave + i];
         const float l = p[j];
         if (!sel(l, j)) continue;
         const int b = dig(l, j);
@@ -631,13 +642,12 @@ __global__ __launch_bounds__(1024) void accept_select_kernel(const float *__rest
                 }
                 __syncthreads();
             } else if (compact) {
-                hist_cands<true>(p, cand, *cand.n, mx, t, s, sel_fn, dig_fn);
+                hist_cands<true>(p, cand, mx, t, s, sel_fn, dig_fn);
             } else if (collect) {
-                __syncthreads();  // every thread has read the first digit's count
-                if (threadIdx.x == 0) *cand.n = 0u;
-                __syncthreads();
                 hist_pass<true, true>(p, g.V, mx, t, s, sel_fn, dig_fn, cand);
-                compact = *cand.n <= (uint32_t)kCandCap;  // (always: the count was the first digit's)
+                bool fits = true;
+                for (int w = 0; w < kSelWaves; w++) fits = fits && cand.n[w] <= (uint32_t)kCandWave;
+                compact = fits;  // else the later digits read the row
             } else {
                 hist_pass<true>(p, g.V, mx, t, s, sel_fn, dig_fn);
             }
@@ -1027,7 +1037,7 @@ hipError_t launch_verify_accept(const float *logits, const int32_t *drafts, int3
             accept_select_kernel<<<sel, kSelWaves * 64, 0, stream>>>(logits, g, stats, tk, 1.0f, t, cuts, 1, nullptr);
         accept_hist_kernel<<<grid, 256, 0, stream>>>(logits, g, stats, top_k_on ? cuts : nullptr, t, h0);
         static bool attr = false;
-        constexpr uint32_t cand_lds = kCandCap * 4 + 16;
+        constexpr uint32_t cand_lds = kCandCap * 4 + kSelWaves * 4;
         if (!attr) {
             (void)hipFuncSetAttribute(reinterpret_cast<const void *>(accept_select_kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)cand_lds);
